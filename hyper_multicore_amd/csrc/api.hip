@@ -1,0 +1,295 @@
+// C-ABI entry points that chain the kernels: router projection, grouped GEMM, and the MegaMoE
+// expert forward at EP=1 (dispatch -> [MX quant] -> GMM1+SwiGLU[+MX requant] -> GMM2 -> combine).
+// All launches are enqueued on the caller's stream; nothing synchronises the host.
+#include "common.h"
+#include "gemm.h"
+#include "../../include/mi355moe.h"
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+extern "C" int mi355moe_abi_version(void) { return MI355MOE_ABI_VERSION; }
+
+// ---------------------------------------------------------------------------------------------
+// Router projection
+// ---------------------------------------------------------------------------------------------
+__global__ void mask_to_ids_kernel(const uint8_t* mask, int64_t T, int32_t* ids) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < T) ids[t] = mask[t] ? 1 : 0;
+}
+
+__global__ void single_group_list_kernel(int64_t rows, int64_t* group_list) { group_list[0] = rows; }
+
+extern "C" size_t mi355moe_gate_logits_workspace_size(int64_t num_tokens) {
+  // ids[T] + mapping[T] + gather[T] + group_list[2] + tile_prefix[3] + dispatch workspace
+  return al256((size_t)num_tokens * 4) * 3 + 256 + 256 + mi355moe_dispatch_workspace_size(num_tokens, 1, 2);
+}
+
+extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32_t hidden_size, const uint16_t* w,
+                                    const uint16_t* w_vision, const uint8_t* image_mask, int32_t num_experts,
+                                    float* logits, void* workspace, size_t workspace_size, void* stream) {
+  if (num_tokens < 0 || hidden_size <= 0 || num_experts <= 0 || num_experts > 4096) return MI355MOE_EINVAL;
+  if (hidden_size % 64) return MI355MOE_EUNSUPPORTED;
+  if (num_tokens == 0) return MI355MOE_OK;
+  if (x == nullptr || w == nullptr || logits == nullptr) return MI355MOE_EINVAL;
+  if (num_tokens > INT32_MAX / 2) return MI355MOE_EINVAL;
+  const bool dual = w_vision != nullptr && image_mask != nullptr;
+  if (workspace == nullptr || workspace_size < mi355moe_gate_logits_workspace_size(num_tokens)) return -4;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  int32_t* ids = (int32_t*)ws;
+  int32_t* mapping = (int32_t*)(ws + al256((size_t)num_tokens * 4));
+  int32_t* gather = (int32_t*)(ws + 2 * al256((size_t)num_tokens * 4));
+  int64_t* group_list = (int64_t*)(ws + 3 * al256((size_t)num_tokens * 4));
+  int32_t* tile_prefix = (int32_t*)(ws + 3 * al256((size_t)num_tokens * 4) + 256);
+  void* dws = ws + 3 * al256((size_t)num_tokens * 4) + 512;
+  int rc;
+  GGParams p = {};
+  p.A = (const uint8_t*)x;
+  p.lda_bytes = (int64_t)hidden_size * 2;
+  p.B = (const uint8_t*)w;
+  p.b_row_bytes = (int64_t)hidden_size * 2;
+  p.K = hidden_size;
+  p.N = num_experts;
+  p.Ntot = num_experts;
+  p.n_tiles = (num_experts + mi355_gg_bn() - 1) / mi355_gg_bn();
+  p.C = logits;
+  p.ldc = num_experts;
+  if (dual) {
+    hipLaunchKernelGGL(mask_to_ids_kernel, dim3((unsigned)((num_tokens + 255) / 256)), dim3(256), 0, st, image_mask,
+                       num_tokens, ids);
+    rc = mi355_dispatch_enqueue(ids, MI355MOE_IDS_INT32, num_tokens, 1, 2, nullptr, nullptr, group_list, mapping,
+                                gather, nullptr, dws, st);
+    if (rc) return rc;
+    p.G = 2;
+    p.b_group_stride = (int64_t)((const char*)w_vision - (const char*)w);
+    p.a_row_index = gather;
+    p.a_row_div = 1;
+    p.c_row_index = gather;
+  } else {
+    hipLaunchKernelGGL(single_group_list_kernel, dim3(1), dim3(1), 0, st, num_tokens, group_list);
+    p.G = 1;
+    p.a_row_div = 1;
+  }
+  p.group_list = group_list;
+  p.tile_prefix = tile_prefix;
+  rc = mi355_plan_tiles(group_list, p.G, tile_prefix, st);
+  if (rc) return rc;
+  return mi355_grouped_gemm(p, false, false, EPI_STORE_F32, st);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Plain grouped GEMM (bf16 in/out)
+// ---------------------------------------------------------------------------------------------
+extern "C" size_t mi355moe_grouped_gemm_workspace_size(int32_t num_groups) {
+  return al256((size_t)(num_groups + 1) * 4);
+}
+
+extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim, const uint16_t* w,
+                                          int32_t layout, int32_t num_groups, int32_t ndim,
+                                          const int64_t* group_list, uint16_t* out, void* workspace,
+                                          size_t workspace_size, void* stream) {
+  if (rows < 0 || kdim <= 0 || ndim <= 0 || num_groups <= 0 || num_groups > 4096) return MI355MOE_EINVAL;
+  if (layout != MI355MOE_LAYOUT_EIO && layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
+  if (kdim % 64 || ndim % 8) return MI355MOE_EUNSUPPORTED;
+  if (rows == 0) return MI355MOE_OK;
+  if (x == nullptr || w == nullptr || group_list == nullptr || out == nullptr) return MI355MOE_EINVAL;
+  if (workspace == nullptr || workspace_size < mi355moe_grouped_gemm_workspace_size(num_groups)) return -4;
+  hipStream_t st = (hipStream_t)stream;
+  GGParams p = {};
+  p.A = (const uint8_t*)x;
+  p.lda_bytes = (int64_t)kdim * 2;
+  p.a_row_div = 1;
+  p.B = (const uint8_t*)w;
+  p.b_group_stride = (int64_t)kdim * ndim * 2;
+  p.b_row_bytes = layout == MI355MOE_LAYOUT_EOI ? (int64_t)kdim * 2 : (int64_t)ndim * 2;
+  p.K = kdim;
+  p.N = ndim;
+  p.Ntot = ndim;
+  p.n_tiles = (ndim + mi355_gg_bn() - 1) / mi355_gg_bn();
+  p.G = num_groups;
+  p.group_list = group_list;
+  p.tile_prefix = (int32_t*)workspace;
+  p.C = out;
+  p.ldc = ndim;
+  int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st);
+  if (rc) return rc;
+  return mi355_grouped_gemm(p, false, layout == MI355MOE_LAYOUT_EIO, EPI_STORE_BF16, st);
+}
+
+extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,
+                                           const uint8_t* col_data, const uint8_t* col_scale, int32_t num_groups,
+                                           int32_t ndim, const int64_t* group_list, uint16_t* out, void* workspace,
+                                           size_t workspace_size, void* stream) {
+  if (rows < 0 || kdim <= 0 || ndim <= 0 || num_groups <= 0 || num_groups > 4096) return MI355MOE_EINVAL;
+  if (kdim % 128 || ndim % 16) return MI355MOE_EUNSUPPORTED;
+  if (rows == 0) return MI355MOE_OK;
+  if (xq == nullptr || x_scale == nullptr || col_data == nullptr || col_scale == nullptr || group_list == nullptr ||
+      out == nullptr)
+    return MI355MOE_EINVAL;
+  if (workspace == nullptr || workspace_size < mi355moe_grouped_gemm_workspace_size(num_groups)) return -4;
+  hipStream_t st = (hipStream_t)stream;
+  GGParams p = {};
+  p.A = xq;
+  p.lda_bytes = kdim;
+  p.a_row_div = 1;
+  p.a_scale = x_scale;
+  p.B = col_data;
+  p.b_group_stride = (int64_t)kdim * ndim;
+  p.b_row_bytes = ndim;
+  p.b_scale = col_scale;
+  p.b_scale_group_stride = (int64_t)(kdim / 64) * ndim * 2;
+  p.K = kdim;
+  p.N = ndim;
+  p.Ntot = ndim;
+  p.n_tiles = (ndim + mi355_gg_bn() - 1) / mi355_gg_bn();
+  p.G = num_groups;
+  p.group_list = group_list;
+  p.tile_prefix = (int32_t*)workspace;
+  p.C = out;
+  p.ldc = ndim;
+  int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st);
+  if (rc) return rc;
+  return mi355_grouped_gemm(p, true, true, EPI_STORE_BF16, st);
+}
+
+// ---------------------------------------------------------------------------------------------
+// MegaMoE expert forward
+// ---------------------------------------------------------------------------------------------
+struct FwdLayout {
+  size_t dispatch, counts, group_list, mapping, gather, tile_prefix, act, act_scale, y, xq, xs, total;
+};
+
+static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
+  FwdLayout L = {};
+  const size_t T = (size_t)a.num_tokens, K = (size_t)a.top_k, E = (size_t)a.num_experts;
+  const size_t H = (size_t)a.hidden_size, I = (size_t)a.intermediate_size, R = T * K;
+  const bool mx = a.precision == MI355MOE_PRECISION_MXFP8;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += al256(bytes); return o; };
+  L.dispatch = take(mi355moe_dispatch_workspace_size(a.num_tokens, a.top_k, a.num_experts));
+  L.counts = take(E * 4);
+  L.group_list = take(E * 8);
+  L.mapping = take(R * 4);
+  L.gather = take(R * 4);
+  L.tile_prefix = take((E + 1) * 4);
+  L.act = take(R * I * (mx ? 1 : 2));
+  L.act_scale = mx ? take(R * (I / 32)) : 0;
+  L.y = take(R * H * 2);
+  L.xq = mx ? take(T * H) : 0;
+  L.xs = mx ? take(T * (H / 32)) : 0;
+  L.total = off;
+  return L;
+}
+
+static int validate_fwd(const MI355MoeForwardArgs& a) {
+  if (a.num_tokens < 0 || a.hidden_size <= 0 || a.intermediate_size <= 0 || a.num_experts <= 0 || a.top_k <= 0)
+    return MI355MOE_EINVAL;
+  if (a.num_experts > 4096 || a.top_k > 64 || a.top_k > a.num_experts) return MI355MOE_EINVAL;
+  if (a.ids_dtype != MI355MOE_IDS_INT32 && a.ids_dtype != MI355MOE_IDS_INT64) return MI355MOE_EINVAL;
+  if (a.precision != MI355MOE_PRECISION_BF16 && a.precision != MI355MOE_PRECISION_MXFP8) return MI355MOE_EINVAL;
+  if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
+  if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;
+  if (a.precision == MI355MOE_PRECISION_MXFP8) {
+    if (a.weight_layout != MI355MOE_LAYOUT_EIO) return MI355MOE_EINVAL;
+    if (a.hidden_size % 128 || a.intermediate_size % 128) return MI355MOE_EUNSUPPORTED;
+  } else {
+    if (a.hidden_size % 64 || a.intermediate_size % 64) return MI355MOE_EUNSUPPORTED;
+  }
+  // GMM1 produces I columns in 128-column tiles; GMM2 produces H columns in 256-column tiles.
+  if (a.intermediate_size % 128 || a.hidden_size % 8) return MI355MOE_EUNSUPPORTED;
+  if (a.num_tokens > 0) {
+    if (a.hidden == nullptr || a.topk_ids == nullptr || a.topk_weights == nullptr || a.w1 == nullptr ||
+        a.w2 == nullptr || a.out == nullptr)
+      return MI355MOE_EINVAL;
+    if (a.precision == MI355MOE_PRECISION_MXFP8 && (a.w1_scale == nullptr || a.w2_scale == nullptr))
+      return MI355MOE_EINVAL;
+  }
+  return MI355MOE_OK;
+}
+
+extern "C" size_t mi355moe_moe_forward_workspace_size(const MI355MoeForwardArgs* args) {
+  if (args == nullptr || validate_fwd(*args) != MI355MOE_OK) return 0;
+  return fwd_layout(*args).total;
+}
+
+extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* workspace, size_t workspace_size,
+                                    void* stream) {
+  if (args == nullptr) return MI355MOE_EINVAL;
+  const MI355MoeForwardArgs& a = *args;
+  int rc = validate_fwd(a);
+  if (rc) return rc;
+  if (a.num_tokens == 0) return MI355MOE_OK;
+  FwdLayout L = fwd_layout(a);
+  if (workspace == nullptr || workspace_size < L.total) return -4;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const int64_t T = a.num_tokens;
+  const int K = a.top_k, E = a.num_experts, H = a.hidden_size, I = a.intermediate_size;
+  const bool mx = a.precision == MI355MOE_PRECISION_MXFP8;
+  const bool eoi = a.weight_layout == MI355MOE_LAYOUT_EOI;
+
+  int32_t* counts = (int32_t*)(ws + L.counts);
+  int64_t* group_list = (int64_t*)(ws + L.group_list);
+  int32_t* mapping = (int32_t*)(ws + L.mapping);
+  int32_t* gather = (int32_t*)(ws + L.gather);
+  int32_t* tile_prefix = (int32_t*)(ws + L.tile_prefix);
+  rc = mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, T, K, E, counts, nullptr, group_list, mapping, gather,
+                              a.error_flag, ws + L.dispatch, st);
+  if (rc) return rc;
+  rc = mi355_plan_tiles(group_list, E, tile_prefix, st);
+  if (rc) return rc;
+  const uint8_t* a1 = (const uint8_t*)a.hidden;
+  if (mx) {
+    rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), st);
+    if (rc) return rc;
+    a1 = (const uint8_t*)(ws + L.xq);
+  }
+  const int esize = mx ? 1 : 2;
+  // GMM1: [R, H] x [H, 2I] -> SwiGLU -> act [R, I]
+  GGParams p1 = {};
+  p1.A = a1;
+  p1.lda_bytes = (int64_t)H * esize;
+  p1.a_row_index = gather;
+  p1.a_row_div = K;
+  p1.a_scale = mx ? (const uint8_t*)(ws + L.xs) : nullptr;
+  p1.B = (const uint8_t*)a.w1;
+  p1.b_group_stride = (int64_t)H * 2 * I * esize;
+  p1.b_row_bytes = eoi ? (int64_t)H * esize : (int64_t)2 * I * esize;
+  p1.b_scale = a.w1_scale;
+  p1.b_scale_group_stride = (int64_t)(H / 64) * 2 * I * 2;
+  p1.K = H;
+  p1.N = I;
+  p1.Ntot = 2 * I;
+  p1.n_tiles = I / 128;
+  p1.G = E;
+  p1.group_list = group_list;
+  p1.tile_prefix = tile_prefix;
+  p1.C = ws + L.act;
+  p1.ldc = I;
+  p1.c_scale = mx ? (uint8_t*)(ws + L.act_scale) : nullptr;
+  rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st);
+  if (rc) return rc;
+  // GMM2: [R, I] x [I, H] -> y [R, H] bf16
+  GGParams p2 = {};
+  p2.A = (const uint8_t*)(ws + L.act);
+  p2.lda_bytes = (int64_t)I * esize;
+  p2.a_row_div = 1;
+  p2.a_scale = mx ? (const uint8_t*)(ws + L.act_scale) : nullptr;
+  p2.B = (const uint8_t*)a.w2;
+  p2.b_group_stride = (int64_t)I * H * esize;
+  p2.b_row_bytes = eoi ? (int64_t)I * esize : (int64_t)H * esize;
+  p2.b_scale = a.w2_scale;
+  p2.b_scale_group_stride = (int64_t)(I / 64) * H * 2;
+  p2.K = I;
+  p2.N = H;
+  p2.Ntot = H;
+  p2.n_tiles = (H + mi355_gg_bn() - 1) / mi355_gg_bn();
+  p2.G = E;
+  p2.group_list = group_list;
+  p2.tile_prefix = tile_prefix;
+  p2.C = ws + L.y;
+  p2.ldc = H;
+  rc = mi355_grouped_gemm(p2, mx, !eoi, EPI_STORE_BF16, st);
+  if (rc) return rc;
+  return mi355_unpermute_enqueue((const uint16_t*)(ws + L.y), mapping, a.topk_weights, T, K, H, a.out, st);
+}

@@ -1,0 +1,268 @@
+// Dispatch metadata, token permute and combine (unpermute) for gfx950.
+//
+// Dispatch is three stream-ordered launches with no host round trip:
+//   1. hist:    one wavefront per contiguous chunk of routed slots builds an LDS histogram with
+//               LDS atomics and writes its per-chunk counts (no global atomics, so the result is
+//               independent of scheduling).
+//   2. scan:    one 1024-thread block turns the per-chunk counts into per-expert totals, the
+//               exclusive expert offsets, the inclusive group_list and, in place, each chunk's
+//               starting rank inside every expert.
+//   3. permute: each chunk wavefront replays its slots in order; lanes routed to the same
+//               expert in one 64-slot round are ranked with ballots, which keeps the
+//               permutation stable (slot order is preserved inside an expert).
+// Reference semantics: bincount (modules/mega_moe/route.py:186-211), EP=1 metadata
+// (route.py:309-390), permutation convention (tests/ut/examples/moe/test_native_experts.py:59-80,
+// ops/common/mega_moe/utilities.asc:176-204), unpermute (route.py:1029-1051).
+#pragma clang fp contract(off)
+#include "common.h"
+#include "scan.h"
+#include "../../include/mi355moe.h"
+
+#define DISPATCH_MAX_EXPERTS 4096
+
+struct DispatchPlan {
+  int64_t slots;
+  int64_t chunk;
+  int32_t chunks;
+};
+
+static DispatchPlan make_dispatch_plan(int64_t num_tokens, int32_t top_k) {
+  DispatchPlan p;
+  p.slots = num_tokens * (int64_t)top_k;
+  int64_t chunk = (p.slots + 127) / 128;
+  chunk = ((chunk + 63) / 64) * 64;
+  if (chunk < 1024) chunk = 1024;
+  p.chunk = chunk;
+  p.chunks = (int32_t)((p.slots + chunk - 1) / chunk);
+  if (p.chunks < 1) p.chunks = 1;
+  return p;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+extern "C" size_t mi355moe_dispatch_workspace_size(int64_t num_tokens, int32_t top_k,
+                                                   int32_t num_experts) {
+  DispatchPlan p = make_dispatch_plan(num_tokens, top_k);
+  // per-chunk counts [chunks][E] + expert starts [E] (int32)
+  return align256((size_t)p.chunks * num_experts * 4) + align256((size_t)num_experts * 4);
+}
+
+MI355_DEV int load_id(const void* ids, int dtype, int64_t s) {
+  if (dtype == MI355MOE_IDS_INT64) {
+    int64_t v = ((const int64_t*)ids)[s];
+    return (v < INT32_MIN || v > INT32_MAX) ? -1 : (int)v;
+  }
+  return ((const int32_t*)ids)[s];
+}
+
+__global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* ids, int dtype, int64_t slots,
+                                                           int64_t chunk, int E, int32_t* chunk_counts,
+                                                           int32_t* error_flag) {
+  extern __shared__ int32_t hist[];
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) hist[e] = 0;
+  __syncthreads();
+  const int64_t begin = (int64_t)blockIdx.x * chunk;
+  const int64_t end = begin + chunk < slots ? begin + chunk : slots;
+  bool bad = false;
+  for (int64_t s = begin + lane; s < end; s += 64) {
+    int id = load_id(ids, dtype, s);
+    if (id >= 0 && id < E) atomicAdd(&hist[id], 1);
+    else bad = true;
+  }
+  if (bad && error_flag != nullptr) error_flag[0] = 1;
+  __syncthreads();
+  int32_t* out = chunk_counts + (int64_t)blockIdx.x * E;
+  for (int e = lane; e < E; e += 64) out[e] = hist[e];
+}
+
+__global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* chunk_counts, int chunks, int E,
+                                                             int32_t* counts, int64_t* expert_offsets,
+                                                             int64_t* group_list, int32_t* expert_start) {
+  __shared__ int64_t vals[DISPATCH_MAX_EXPERTS];
+  __shared__ int64_t wsum[17];
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    int32_t run = 0;
+    for (int b = 0; b < chunks; ++b) {
+      int32_t c = chunk_counts[(int64_t)b * E + e];
+      chunk_counts[(int64_t)b * E + e] = run;
+      run += c;
+    }
+    vals[e] = run;
+    if (counts != nullptr) counts[e] = run;
+  }
+  __syncthreads();
+  block_exclusive_scan_1024(vals, E, wsum);
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    int64_t start = vals[e];
+    int64_t cnt = (e + 1 < E ? vals[e + 1] : wsum[16]) - start;
+    if (expert_offsets != nullptr) expert_offsets[e] = start;
+    if (group_list != nullptr) group_list[e] = start + cnt;
+    expert_start[e] = (int32_t)start;
+  }
+}
+
+__global__ __launch_bounds__(64) void dispatch_permute_kernel(const void* ids, int dtype, int64_t slots,
+                                                              int64_t chunk, int E,
+                                                              const int32_t* chunk_base,
+                                                              const int32_t* expert_start,
+                                                              int32_t* mapping, int32_t* gather_index) {
+  extern __shared__ int32_t running[];
+  const int lane = threadIdx.x;
+  const int32_t* base = chunk_base + (int64_t)blockIdx.x * E;
+  for (int e = lane; e < E; e += 64) running[e] = expert_start[e] + base[e];
+  __syncthreads();
+  const int64_t begin = (int64_t)blockIdx.x * chunk;
+  const int64_t end = begin + chunk < slots ? begin + chunk : slots;
+  int bits = 1;
+  while ((1 << bits) < E) ++bits;
+  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
+  for (int64_t s0 = begin; s0 < end; s0 += 64) {
+    const int64_t s = s0 + lane;
+    int id = s < end ? load_id(ids, dtype, s) : -1;
+    bool valid = id >= 0 && id < E;
+    uint64_t match = __ballot(valid);
+    for (int b = 0; b < bits; ++b) {
+      bool bit = valid && ((id >> b) & 1);
+      uint64_t m1 = __ballot(bit);
+      match &= bit ? m1 : ~m1;
+    }
+    int dest = -1;
+    if (valid) dest = running[id] + __popcll(match & lt);
+    __syncthreads();
+    if (valid && (match & lt) == 0) running[id] += __popcll(match);
+    __syncthreads();
+    if (s < end) {
+      mapping[s] = dest;
+      if (valid && gather_index != nullptr) gather_index[dest] = (int32_t)s;
+    }
+  }
+}
+
+// Internal: enqueue the three dispatch launches. expert_start_ws/chunk_ws come from workspace.
+int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E,
+                           int32_t* counts, int64_t* expert_offsets, int64_t* group_list,
+                           int32_t* mapping, int32_t* gather_index, int32_t* error_flag,
+                           void* workspace, hipStream_t stream) {
+  DispatchPlan p = make_dispatch_plan(num_tokens, top_k);
+  int32_t* chunk_counts = (int32_t*)workspace;
+  int32_t* expert_start = (int32_t*)((char*)workspace + align256((size_t)p.chunks * E * 4));
+  size_t lds = (size_t)E * 4;
+  hipLaunchKernelGGL(dispatch_hist_kernel, dim3(p.chunks), dim3(64), lds, stream, ids, dtype, p.slots,
+                     p.chunk, E, chunk_counts, error_flag);
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, stream, chunk_counts, p.chunks, E,
+                     counts, expert_offsets, group_list, expert_start);
+  if (p.slots > 0)
+    hipLaunchKernelGGL(dispatch_permute_kernel, dim3(p.chunks), dim3(64), lds, stream, ids, dtype, p.slots,
+                       p.chunk, E, chunk_counts, expert_start, mapping, gather_index);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+extern "C" int mi355moe_dispatch(const MI355MoeDispatchArgs* args, void* workspace, size_t workspace_size,
+                                 void* stream) {
+  if (args == nullptr) return MI355MOE_EINVAL;
+  const MI355MoeDispatchArgs& a = *args;
+  if (a.num_tokens < 0 || a.top_k <= 0 || a.num_experts <= 0 || a.num_experts > DISPATCH_MAX_EXPERTS)
+    return MI355MOE_EINVAL;
+  if (a.ids_dtype != MI355MOE_IDS_INT32 && a.ids_dtype != MI355MOE_IDS_INT64) return MI355MOE_EINVAL;
+  if ((a.topk_ids == nullptr || a.mapping == nullptr) && a.num_tokens > 0) return MI355MOE_EINVAL;
+  if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;
+  size_t need = mi355moe_dispatch_workspace_size(a.num_tokens, a.top_k, a.num_experts);
+  if (workspace == nullptr || workspace_size < need) return -4;
+  return mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, a.num_tokens, a.top_k, a.num_experts, a.counts,
+                                a.expert_offsets, a.group_list, a.mapping, a.gather_index, a.error_flag,
+                                workspace, (hipStream_t)stream);
+}
+
+// routed[mapping[s]] = x[s / K], 16-byte vectors; one block row per slot.
+__global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t* x, int64_t slots, int K, int H,
+                                                           const int32_t* mapping, uint16_t* routed) {
+  const int64_t s = blockIdx.x;
+  if (s >= slots) return;
+  const int32_t dest = mapping[s];
+  if (dest < 0) return;
+  const int64_t t = s / K;
+  const uint4* src = (const uint4*)(x + t * (int64_t)H);
+  uint4* dst = (uint4*)(routed + (int64_t)dest * H);
+  for (int v = threadIdx.x; v < H / 8; v += blockDim.x) dst[v] = src[v];
+}
+
+extern "C" int mi355moe_token_permute(const uint16_t* x, int64_t num_tokens, int32_t hidden_size,
+                                      const void* topk_ids, int32_t ids_dtype, int32_t top_k,
+                                      int32_t num_experts, uint16_t* routed, int32_t* mapping,
+                                      void* workspace, size_t workspace_size, void* stream) {
+  if (num_tokens < 0 || hidden_size <= 0 || hidden_size % 8 || top_k <= 0 || num_experts <= 0 ||
+      num_experts > DISPATCH_MAX_EXPERTS)
+    return MI355MOE_EINVAL;
+  if (ids_dtype != MI355MOE_IDS_INT32 && ids_dtype != MI355MOE_IDS_INT64) return MI355MOE_EINVAL;
+  if (num_tokens > 0 && (x == nullptr || topk_ids == nullptr || routed == nullptr || mapping == nullptr))
+    return MI355MOE_EINVAL;
+  if (num_tokens * (int64_t)top_k > INT32_MAX) return MI355MOE_EINVAL;
+  size_t need = mi355moe_dispatch_workspace_size(num_tokens, top_k, num_experts);
+  if (workspace == nullptr || workspace_size < need) return -4;
+  hipStream_t st = (hipStream_t)stream;
+  int rc = mi355_dispatch_enqueue(topk_ids, ids_dtype, num_tokens, top_k, num_experts, nullptr, nullptr,
+                                  nullptr, mapping, nullptr, nullptr, workspace, st);
+  if (rc) return rc;
+  int64_t slots = num_tokens * top_k;
+  if (slots > 0)
+    hipLaunchKernelGGL(permute_rows_kernel, dim3((unsigned)slots), dim3(hidden_size >= 2048 ? 256 : 64), 0, st,
+                       x, slots, top_k, hidden_size, mapping, routed);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+// out[t] = bf16(sum_k p[t,k] * y[mapping[t*K+k]]) with fp32 accumulation in ascending k; the
+// product and the sum are rounded separately (no fma), so the result is reproducible bit for bit.
+// One block per token; each thread handles 8 consecutive columns (one 16-byte vector).
+__global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, const int32_t* mapping,
+                                                        const float* probs, int64_t T, int K, int H,
+                                                        uint16_t* out) {
+  const int64_t t = blockIdx.x;
+  if (t >= T) return;
+  __shared__ int32_t rows[64];
+  __shared__ float ps[64];
+  if (threadIdx.x < K) {
+    rows[threadIdx.x] = mapping[t * K + threadIdx.x];
+    ps[threadIdx.x] = probs != nullptr ? probs[t * K + threadIdx.x] : 1.0f;
+  }
+  __syncthreads();
+  for (int v = threadIdx.x; v < H / 8; v += blockDim.x) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int k = 0; k < K; ++k) {
+      int32_t r = rows[k];
+      if (r < 0) continue;
+      uint4 q = ((const uint4*)(y + (int64_t)r * H))[v];
+      float p = ps[k];
+      uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = acc[2 * i] + p * bf16_to_f32((uint16_t)(w[i] & 0xffff));
+        acc[2 * i + 1] = acc[2 * i + 1] + p * bf16_to_f32((uint16_t)(w[i] >> 16));
+      }
+    }
+    uint4 o;
+    o.x = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+    o.y = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+    o.z = f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
+    o.w = f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+    ((uint4*)(out + t * (int64_t)H))[v] = o;
+  }
+}
+
+int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const float* probs, int64_t T, int K,
+                            int H, uint16_t* out, hipStream_t stream) {
+  if (T == 0) return MI355MOE_OK;
+  hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)T), dim3(H >= 2048 ? 256 : 128), 0, stream, y, mapping,
+                     probs, T, K, H, out);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+extern "C" int mi355moe_token_unpermute(const uint16_t* y, const int32_t* mapping, const float* probs,
+                                        int64_t num_tokens, int32_t top_k, int32_t hidden_size,
+                                        uint16_t* out, void* stream) {
+  if (num_tokens < 0 || top_k <= 0 || top_k > 64 || hidden_size <= 0 || hidden_size % 8) return MI355MOE_EINVAL;
+  if (num_tokens > 0 && (y == nullptr || mapping == nullptr || out == nullptr)) return MI355MOE_EINVAL;
+  return mi355_unpermute_enqueue(y, mapping, probs, num_tokens, top_k, hidden_size, out, (hipStream_t)stream);
+}

@@ -1,0 +1,41 @@
+// Internal interface of the persistent grouped GEMM (gemm.hip) and the other kernel files.
+#pragma once
+#include "common.h"
+
+enum { EPI_STORE_BF16 = 0, EPI_STORE_F32 = 1, EPI_SWIGLU_BF16 = 2, EPI_SWIGLU_MX = 3 };
+
+struct GGParams {
+  const uint8_t* A;          // [rowsA, K] elements (bf16 or e4m3), row stride lda_bytes
+  int64_t lda_bytes;
+  const int32_t* a_row_index;  // routed row -> index (or NULL: identity)
+  int32_t a_row_div;           // source row = a_row_index[r] / a_row_div
+  const uint8_t* a_scale;    // MX: [rowsA, K/32]
+  const uint8_t* B;          // per group: NK [Ntot, K] or KN [K, Ntot]
+  int64_t b_group_stride;    // bytes
+  int64_t b_row_bytes;       // NK: K*esize ; KN: Ntot*esize
+  const uint8_t* b_scale;    // MX col_scale [G, K/64, Ntot, 2]
+  int64_t b_scale_group_stride;  // bytes = (K/64)*Ntot*2
+  int32_t K;                 // reduction length (elements)
+  int32_t N;                 // output columns (SwiGLU: I; otherwise Ntot)
+  int32_t Ntot;              // weight columns (SwiGLU: 2I)
+  int32_t n_tiles;
+  int32_t G;
+  const int64_t* group_list; // inclusive cumulative rows per group
+  const int32_t* tile_prefix;  // [G+1]
+  void* C;
+  int64_t ldc;               // elements (bf16/f32) or bytes (e4m3)
+  const int32_t* c_row_index;  // optional output row scatter (EPI_STORE_F32)
+  uint8_t* c_scale;          // EPI_SWIGLU_MX: [rows, N/32]
+};
+
+
+int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
+int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream);
+int mi355_gg_bm();
+int mi355_gg_bn();
+int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
+                           int64_t* expert_offsets, int64_t* group_list, int32_t* mapping, int32_t* gather_index,
+                           int32_t* error_flag, void* workspace, hipStream_t stream);
+int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const float* probs, int64_t T, int K, int H,
+                            uint16_t* out, hipStream_t stream);
+int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, hipStream_t st);

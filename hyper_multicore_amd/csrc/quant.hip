@@ -1,0 +1,97 @@
+// OCP MX (v1.0) quantisation kernels: e4m3fn elements, one e8m0 shared exponent per 32 values.
+// scale exponent = floor(log2(amax)) - 8 (8 = exponent of the largest e4m3 power of two), element
+// = round-to-nearest-even(v / 2^scale) saturated to +-448.
+// Row axis follows the quant_x task (ops/common/mega_moe/adapters/arch35/quantization/
+// dual_axis_mxfp8_worker.h:39-66, blocks along the hidden dimension); the column form writes the
+// forward MX weight root (modules/mega_moe/backends/mxfp8/weights.py:61-86: col_data [G,K,N],
+// col_scale [G,K/64,N,2], 32-blocks along K for every column).
+#include "common.h"
+#include "../../include/mi355moe.h"
+
+// One thread per 32-element block of a row.
+__global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint16_t* x, int64_t rows, int cols,
+                                                            uint8_t* q, uint8_t* scale) {
+  const int nb = cols / 32;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= rows * nb) return;
+  const int64_t r = id / nb;
+  const int b = (int)(id - r * nb);
+  const uint4* src = (const uint4*)(x + r * cols + b * 32);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint4 u = src[i];
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i * 8 + 2 * j] = bf16_to_f32((uint16_t)(w[j] & 0xffff));
+      v[i * 8 + 2 * j + 1] = bf16_to_f32((uint16_t)(w[j] >> 16));
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  uint32_t code = mx_scale_code(amax);
+  uint32_t out[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    out[i] = f32_to_e4m3(mx_apply_inv_scale(v[4 * i], code)) |
+             (f32_to_e4m3(mx_apply_inv_scale(v[4 * i + 1], code)) << 8) |
+             (f32_to_e4m3(mx_apply_inv_scale(v[4 * i + 2], code)) << 16) |
+             (f32_to_e4m3(mx_apply_inv_scale(v[4 * i + 3], code)) << 24);
+  }
+  uint4* dst = (uint4*)(q + r * cols + b * 32);
+  dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+  dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+  scale[r * nb + b] = (uint8_t)code;
+}
+
+// One thread per (group, 32-row block along K, column).
+__global__ __launch_bounds__(256) void mx_quant_cols_kernel(const uint16_t* w, int G, int K, int N,
+                                                            uint8_t* col_data, uint8_t* col_scale) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int kb_n = K / 32;
+  if (id >= (int64_t)G * kb_n * N) return;
+  const int n = (int)(id % N);
+  const int64_t gk = id / N;
+  const int kb = (int)(gk % kb_n);
+  const int g = (int)(gk / kb_n);
+  const uint16_t* src = w + ((int64_t)g * K + kb * 32) * N + n;
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    v[i] = bf16_to_f32(src[(int64_t)i * N]);
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  uint32_t code = mx_scale_code(amax);
+  uint8_t* dst = col_data + ((int64_t)g * K + kb * 32) * N + n;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) dst[(int64_t)i * N] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+  col_scale[(((int64_t)g * (K / 64) + kb / 2) * N + n) * 2 + (kb & 1)] = (uint8_t)code;
+}
+
+int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, hipStream_t st) {
+  int64_t n = rows * (cols / 32);
+  if (n == 0) return MI355MOE_OK;
+  hipLaunchKernelGGL(mx_quant_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, rows, cols, q,
+                     scale);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+extern "C" int mi355moe_mx_quantize_rows(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q,
+                                         uint8_t* scale, void* stream) {
+  if (rows < 0 || cols <= 0 || cols % 32) return MI355MOE_EINVAL;
+  if (rows > 0 && (x == nullptr || q == nullptr || scale == nullptr)) return MI355MOE_EINVAL;
+  return mi355_mx_quant_rows(x, rows, cols, q, scale, (hipStream_t)stream);
+}
+
+extern "C" int mi355moe_mx_quantize_cols(const uint16_t* w, int32_t groups, int32_t kdim, int32_t cols,
+                                         uint8_t* col_data, uint8_t* col_scale, void* stream) {
+  if (groups <= 0 || kdim <= 0 || kdim % 64 || cols <= 0) return MI355MOE_EINVAL;
+  if (w == nullptr || col_data == nullptr || col_scale == nullptr) return MI355MOE_EINVAL;
+  int64_t n = (int64_t)groups * (kdim / 32) * cols;
+  hipLaunchKernelGGL(mx_quant_cols_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, w,
+                     groups, kdim, cols, col_data, col_scale);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}

@@ -1,0 +1,207 @@
+// MegaGate route kernel for gfx950: fp32 scoring, correction bias (text / vision), optional
+// group-limited selection, top-k with lowest-index tie-break, gather, renormalisation and scale.
+//
+// Semantics follow MegaGate._torch_forward (hyper_multicore/modules/mega_gate/module.py:189-227)
+// and the native route pipeline order (ops/hyper_mega_gate/op_kernel/route_pipeline.h:73-562):
+//   score   = softmax(l) | sigmoid(l) | sqrt(softplus(l))   (softplus: l>20 ? l : compensated log1p)
+//   biased  = score + (mask[t] ? bias_vl : bias)
+//   idx     = top-k of biased (group-limited when groups > 1)
+//   w       = score[idx];  K>1: w = w / (sum_k w + 1e-20);  w = w * routed_scaling_factor
+// One 64-lane wavefront owns one token row; expert e lives in lane e % 64, register slot e / 64.
+// The selected experts are emitted in descending biased score, ties broken by lower expert id.
+#pragma clang fp contract(off)
+#include "common.h"
+#include "detmath.h"
+#include "../../include/mi355moe.h"
+
+#define ROUTER_MAX_SLOTS 16  // E <= 1024
+
+MI355_DEV float score_fn(float l, int scoring) {
+  if (scoring == MI355MOE_SCORE_SIGMOID) {
+    return 1.0f / (1.0f + det_expf(-l));
+  }
+  // sqrt(softplus(l)) in the route pipeline's compensated order (route_pipeline.h:104-130)
+  float e = det_expf(fminf(l, 20.0f));
+  float u = e + 1.0f;
+  float sp;
+  if (u == 1.0f) {
+    sp = e;
+  } else {
+    float ratio = e / (u - 1.0f);
+    sp = det_logf(u) * ratio;
+  }
+  if (l > 20.0f) sp = l;
+  return sqrtf(sp);
+}
+
+// Wave argmax over (value, index): larger value wins, ties -> smaller index. Returns winner in all lanes.
+MI355_DEV void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    float ov = __shfl_xor(v, m, 64);
+    int oi = __shfl_xor(i, m, 64);
+    bool take = (ov > v) || (ov == v && oi < i);
+    v = take ? ov : v;
+    i = take ? oi : i;
+  }
+}
+
+__global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= a.num_tokens) return;
+  const int E = a.num_experts;
+  const int slots = (E + 63) >> 6;
+  const float* lrow = a.logits + t * (int64_t)a.logits_row_stride;
+  const float* bias = a.bias;
+  if (a.image_mask != nullptr && a.bias_vl != nullptr && a.image_mask[t]) bias = a.bias_vl;
+
+  float score[ROUTER_MAX_SLOTS];
+  float biased[ROUTER_MAX_SLOTS];
+  const float NEG_INF = -__builtin_inff();
+
+  if (a.scoring == MI355MOE_SCORE_SOFTMAX) {
+    float lv[ROUTER_MAX_SLOTS];
+    float mx = NEG_INF;
+#pragma unroll
+    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+      int e = j * 64 + lane;
+      lv[j] = (j < slots && e < E) ? lrow[e] : NEG_INF;
+      mx = fmaxf(mx, lv[j]);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+      int e = j * 64 + lane;
+      if (j < slots && e < E) {
+        lv[j] = det_expf(lv[j] - mx);
+        part = part + lv[j];
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) part = part + __shfl_xor(part, m, 64);
+#pragma unroll
+    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+      int e = j * 64 + lane;
+      score[j] = (j < slots && e < E) ? lv[j] / part : 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+      int e = j * 64 + lane;
+      score[j] = (j < slots && e < E) ? score_fn(lrow[e], a.scoring) : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+    int e = j * 64 + lane;
+    bool valid = j < slots && e < E;
+    biased[j] = valid ? score[j] + bias[e] : NEG_INF;
+    if (valid && a.scores_out != nullptr) a.scores_out[t * (int64_t)E + e] = score[j];
+  }
+
+  // Group-limited selection (DeepSeek-V3 form): group score = sum of the two largest biased
+  // scores in the group; keep the top `topk_groups` groups (ties -> lower group id).
+  if (a.num_groups > 1) {
+    const int G = a.num_groups;
+    const int S = E / G;
+    float my_gscore = NEG_INF;  // lane g holds the score of group g
+    for (int g = 0; g < G; ++g) {
+      float t1 = NEG_INF, t2 = NEG_INF;
+#pragma unroll
+      for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+        int e = j * 64 + lane;
+        if (j < slots && e < E && e / S == g) {
+          float v = biased[j];
+          if (v > t1) { t2 = t1; t1 = v; } else if (v > t2) { t2 = v; }
+        }
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        float o1 = __shfl_xor(t1, m, 64), o2 = __shfl_xor(t2, m, 64);
+        float n1, n2;
+        if (t1 >= o1) { n1 = t1; n2 = fmaxf(t2, o1); } else { n1 = o1; n2 = fmaxf(t1, o2); }
+        t1 = n1; t2 = n2;
+      }
+      if (lane == g) my_gscore = t1 + t2;
+    }
+    uint64_t keep = 0;
+    for (int r = 0; r < a.topk_groups; ++r) {
+      float v = (lane < G && !((keep >> lane) & 1ull)) ? my_gscore : NEG_INF;
+      int i = lane < G && !((keep >> lane) & 1ull) ? lane : 0x7fffffff;
+      wave_argmax(v, i);
+      if (i < G) keep |= 1ull << i;
+    }
+#pragma unroll
+    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+      int e = j * 64 + lane;
+      if (j < slots && e < E && !((keep >> (e / S)) & 1ull)) biased[j] = NEG_INF;
+    }
+  }
+
+  // Top-k by repeated wave argmax; lane k keeps the k-th selection.
+  const int K = a.top_k;
+  uint32_t taken = 0;
+  int my_idx = -1;
+  float my_w = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    float bv = NEG_INF;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+      int e = j * 64 + lane;
+      if (j < slots && e < E && !((taken >> j) & 1u)) {
+        if (biased[j] > bv || bi == 0x7fffffff) { bv = biased[j]; bi = e; }
+      }
+    }
+    wave_argmax(bv, bi);
+    if ((bi & 63) == lane) {
+      int j = bi >> 6;
+      taken |= 1u << j;
+    }
+    // the owner lane broadcasts the unbiased score
+    float sel = 0.0f;
+#pragma unroll
+    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) if ((bi >> 6) == j) sel = score[j];
+    sel = __shfl(sel, bi & 63, 64);
+    if (lane == k) { my_idx = bi; my_w = sel; }
+  }
+  float w = my_w;
+  if (K > 1) {
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum = sum + __shfl(my_w, k, 64);
+    float denom = sum + 1.0e-20f;
+    w = my_w / denom;
+  }
+  w = w * a.routed_scaling_factor;
+  if (lane < K) {
+    a.weights_out[t * K + lane] = w;
+    if (a.indices_out != nullptr) a.indices_out[t * K + lane] = (int64_t)my_idx;
+    if (a.indices32_out != nullptr) a.indices32_out[t * K + lane] = my_idx;
+  }
+}
+
+extern "C" int mi355moe_gate_route(const MI355MoeRouteArgs* args, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  if (args == nullptr) return MI355MOE_EINVAL;
+  const MI355MoeRouteArgs& a = *args;
+  if (a.num_tokens < 0 || a.num_experts <= 0 || a.num_experts > 64 * ROUTER_MAX_SLOTS) return MI355MOE_EINVAL;
+  if (a.top_k <= 0 || a.top_k > a.num_experts || a.top_k > 64) return MI355MOE_EINVAL;
+  if (a.scoring != MI355MOE_SCORE_SOFTMAX && a.scoring != MI355MOE_SCORE_SIGMOID &&
+      a.scoring != MI355MOE_SCORE_SQRTSOFTPLUS) return MI355MOE_EINVAL;
+  if (a.num_groups < 1 || a.num_groups > 64 || a.num_experts % a.num_groups) return MI355MOE_EINVAL;
+  if (a.num_groups > 1) {
+    if (a.num_experts / a.num_groups < 2) return MI355MOE_EINVAL;
+    if (a.topk_groups < 1 || a.topk_groups > a.num_groups) return MI355MOE_EINVAL;
+    if (a.topk_groups * (a.num_experts / a.num_groups) < a.top_k) return MI355MOE_EINVAL;
+  }
+  if (a.logits == nullptr || a.bias == nullptr || a.weights_out == nullptr) return MI355MOE_EINVAL;
+  if (a.indices_out == nullptr && a.indices32_out == nullptr) return MI355MOE_EINVAL;
+  if (a.logits_row_stride < a.num_experts) return MI355MOE_EINVAL;
+  if (a.num_tokens == 0) return MI355MOE_OK;
+  dim3 grid((unsigned)((a.num_tokens + 3) / 4));
+  hipLaunchKernelGGL(mi355_route_kernel, grid, dim3(256), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}

@@ -1,0 +1,232 @@
+"""MegaMoeExperts executor on the gfx950 kernels (expert-parallel degree 1).
+
+Public surface mirrors hyper_multicore/modules/mega_moe/module.py:141-535: the executor owns no
+parameters; ``forward(hidden_states, topk_ids, topk_weights, *, expert_weights,
+tokens_per_expert=None)`` returns bf16 in the input shape. BF16 weights are accepted in the EIO
+``([E,H,2I], [E,I,H])`` or EOI ``([E,2I,H], [E,H,I])`` layout (inferred from the shapes and bound
+on first use); MXFP8 weights are MX roots carrying ``col_data`` (e4m3fn, EIO) and ``col_scale``
+(uint8 e8m0 ``[E, M/64, N, 2]``), see :func:`hyper_multicore_amd.mxfp8.quantize_expert_weight`.
+
+Only the default numerics are implemented (no SwiGLU clamp, probabilities applied after FC2);
+``ep_group`` must be ``None`` or a group of size 1.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from . import ops
+
+__all__ = ["MegaMoeExperts", "MegaMoeNumericsOptions", "MegaMoeTuningOptions", "MegaMoeSchedulerOptions"]
+
+_COMMUNICATION_SPLIT = 128
+
+
+@dataclass(frozen=True)
+class MegaMoeNumericsOptions:
+    """Numerical semantics (modules/mega_moe/numerics.py:21-50)."""
+
+    partial_weight_grad_dtype: str | None = None
+    swiglu_limit: float | None = None
+    clamp_after_silu: bool = False
+    apply_probs_before_fc2: bool = False
+
+
+@dataclass(frozen=True)
+class MegaMoeSchedulerOptions:
+    """Accepted for API compatibility (experimental/_mega_moe.py); the gfx950 work list is fixed."""
+
+    policy: str | None = None
+    queue_ready_lookahead: int | None = None
+    batch_experts: bool = False
+    nominal_schedule: bool = False
+    lowering: str | None = None
+
+
+@dataclass(frozen=True)
+class MegaMoeTuningOptions:
+    """Accepted for API compatibility (experimental/_mega_moe.py:22-100). The EP transport knobs
+    (dispatch mode, capacity factors, splits) have no effect at EP=1 but are validated."""
+
+    dispatch_mode: str = "push"
+    initial_capacity_factor: float | None = None
+    capacity_growth_factor: float | None = None
+    dispatch_split: int = _COMMUNICATION_SPLIT
+    combine_split: int = _COMMUNICATION_SPLIT
+    scheduler: MegaMoeSchedulerOptions = MegaMoeSchedulerOptions()
+
+
+def _positive_int(name: str, value: Any) -> int:
+    if not isinstance(value, int) or isinstance(value, bool) or value <= 0:
+        raise ValueError(f"{name} must be a positive integer, got {value!r}.")
+    return value
+
+
+class MegaMoeExperts(torch.nn.Module):
+    """Execute router-selected experts with the gfx950 MegaMoE kernels on one GPU."""
+
+    def __init__(self, *, hidden_size: int, intermediate_size: int, num_experts: int, top_k: int,
+                 ep_group: Any | None = None, precision: str = "bf16",
+                 numerics_options: MegaMoeNumericsOptions | None = None,
+                 tuning_options: MegaMoeTuningOptions | None = None,
+                 expert_placement: Any | None = None) -> None:
+        super().__init__()
+        for name, value in (("hidden_size", hidden_size), ("intermediate_size", intermediate_size),
+                            ("num_experts", num_experts), ("top_k", top_k)):
+            _positive_int(name, value)
+        if top_k > num_experts:
+            raise ValueError(f"top_k ({top_k}) cannot exceed num_experts ({num_experts}).")
+        if precision not in ("bf16", "mxfp8"):
+            raise ValueError("MegaMoE precision must be bf16 or mxfp8")
+        if numerics_options is not None and not isinstance(numerics_options, MegaMoeNumericsOptions):
+            raise TypeError("numerics_options must be MegaMoeNumericsOptions or None")
+        if tuning_options is not None and not isinstance(tuning_options, MegaMoeTuningOptions):
+            raise TypeError("tuning_options must be MegaMoeTuningOptions or None")
+        numerics = numerics_options or MegaMoeNumericsOptions()
+        tuning = tuning_options or MegaMoeTuningOptions()
+        for name, value in (("apply_probs_before_fc2", numerics.apply_probs_before_fc2),
+                            ("clamp_after_silu", numerics.clamp_after_silu)):
+            if not isinstance(value, bool):
+                raise TypeError(f"{name} must be a boolean")
+        if precision == "mxfp8" and (numerics.swiglu_limit is not None or numerics.apply_probs_before_fc2):
+            raise ValueError("MXFP8 does not support clamp or before-FC2 probability weighting")
+        if numerics.swiglu_limit is not None or numerics.apply_probs_before_fc2:
+            raise NotImplementedError("the gfx950 kernels implement the default numerics only "
+                                      "(no SwiGLU clamp, probabilities after FC2)")
+        if numerics.partial_weight_grad_dtype not in (None, "native", "float32"):
+            raise ValueError("partial_weight_grad_dtype must be native, float32 or None")
+        if tuning.dispatch_mode not in ("push", "pull"):
+            raise ValueError("dispatch_mode must be push or pull")
+        for name, split in (("dispatch_split", tuning.dispatch_split), ("combine_split", tuning.combine_split)):
+            if not isinstance(split, int) or isinstance(split, bool) or split <= 0 or split % _COMMUNICATION_SPLIT:
+                raise ValueError(f"{name} must be a positive integer multiple of {_COMMUNICATION_SPLIT}, got {split!r}.")
+        if precision == "mxfp8" and (tuning.scheduler.batch_experts or tuning.scheduler.nominal_schedule
+                                     or tuning.scheduler.lowering == "compact"):
+            raise ValueError("MXFP8 requires dense per-expert lowering")
+        ep_size = 1
+        if ep_group is not None:
+            size = getattr(ep_group, "size", None)
+            ep_size = size() if callable(size) else 1
+            if ep_size != 1:
+                raise ValueError("this build runs every expert on one GPU: ep_group must have size 1")
+        if expert_placement is not None and getattr(expert_placement, "strategy", "none") != "none":
+            raise ValueError("adaptive expert placement requires an EP group with more than one rank")
+        if precision == "mxfp8" and (hidden_size % 64 or intermediate_size % 64):
+            raise ValueError("MXFP8 requires hidden_size and intermediate_size divisible by 64")
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.num_experts = num_experts
+        self.top_k = top_k
+        self.ep_size = ep_size
+        self.local_experts = num_experts
+        self._precision = precision
+        self._numerics = numerics
+        self._tuning = tuning
+        self._layout: str | None = None
+        local, hidden, inter = num_experts, hidden_size, intermediate_size
+        self._weight_shapes = {
+            "EIO": ((local, hidden, inter * 2), (local, inter, hidden)),
+            "EOI": ((local, inter * 2, hidden), (local, hidden, inter)),
+        }
+
+    @property
+    def precision(self) -> str:
+        return self._precision
+
+    @property
+    def swiglu_limit(self) -> float | None:
+        return self._numerics.swiglu_limit
+
+    @property
+    def clamp_after_silu(self) -> bool:
+        return self._numerics.clamp_after_silu
+
+    @property
+    def apply_probs_before_fc2(self) -> bool:
+        return self._numerics.apply_probs_before_fc2
+
+    def share_execution_resources(self, *others: "MegaMoeExperts") -> None:
+        """No-op: each call allocates its workspace from torch's caching allocator."""
+
+    def close(self) -> None:
+        """No-op: the executor holds no device resources between calls."""
+
+    def _infer_layout(self, shape1: tuple, shape2: tuple) -> str:
+        actual = (shape1, shape2)
+        if actual == self._weight_shapes["EIO"]:
+            return "EIO"
+        if actual == self._weight_shapes["EOI"]:
+            return "EOI"
+        raise ValueError(f"expert_weights must have EIO shapes {self._weight_shapes['EIO']} or "
+                         f"EOI shapes {self._weight_shapes['EOI']}, got {actual}.")
+
+    def _bf16_weights(self, hidden: torch.Tensor, expert_weights: tuple):
+        try:
+            w1, w2 = expert_weights
+            shape1, shape2 = tuple(w1.shape), tuple(w2.shape)
+        except (AttributeError, TypeError, ValueError) as error:
+            raise ValueError("expert_weights must contain two tensors") from error
+        layout = self._layout or self._infer_layout(shape1, shape2)
+        expected1, expected2 = self._weight_shapes[layout]
+        if shape1 != expected1:
+            raise ValueError(f"gate_up_weight must have shape {expected1}, got {shape1}.")
+        if shape2 != expected2:
+            raise ValueError(f"down_weight must have shape {expected2}, got {shape2}.")
+        if w1.device != hidden.device or w2.device != hidden.device:
+            raise ValueError("expert weights and hidden states must be on the same GPU.")
+        if w1.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
+            raise TypeError("expert weights and hidden states must all use BF16.")
+        if layout == "EOI" and (not w1.is_contiguous() or not w2.is_contiguous()):
+            raise ValueError("EOI expert weights must be contiguous for zero-copy execution.")
+        self._layout = layout
+        return layout, w1.contiguous(), w2.contiguous()
+
+    def _mx_weights(self, hidden: torch.Tensor, expert_weights: tuple):
+        from .mxfp8 import resolve_forward_weight
+        try:
+            r1, r2 = expert_weights
+        except (TypeError, ValueError) as error:
+            raise ValueError("expert_weights must contain two MX roots") from error
+        E, H, I = self.num_experts, self.hidden_size, self.intermediate_size
+        d1, s1 = resolve_forward_weight(r1, (E, H, 2 * I), hidden.device)
+        d2, s2 = resolve_forward_weight(r2, (E, I, H), hidden.device)
+        return d1, s1, d2, s2
+
+    def forward(self, hidden_states: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, *,
+                expert_weights: tuple, tokens_per_expert: torch.Tensor | None = None) -> torch.Tensor:
+        """Route token states through the configured experts (module.py:497-535)."""
+        if hidden_states.ndim < 2 or hidden_states.shape[-1] != self.hidden_size:
+            raise ValueError("hidden_states must have at least two dimensions and configured "
+                             f"hidden size {self.hidden_size}, got {tuple(hidden_states.shape)}.")
+        flat = hidden_states.reshape(-1, self.hidden_size)
+        route_shape = (flat.shape[0], self.top_k)
+        if tuple(topk_ids.shape) != route_shape:
+            raise ValueError(f"topk_ids must have shape {route_shape}, got {tuple(topk_ids.shape)}.")
+        if tuple(topk_weights.shape) != route_shape:
+            raise ValueError(f"topk_weights must have shape {route_shape}, got {tuple(topk_weights.shape)}.")
+        if tokens_per_expert is not None and tuple(tokens_per_expert.shape) != (self.num_experts,):
+            raise ValueError(f"tokens_per_expert must have shape ({self.num_experts},), "
+                             f"got {tuple(tokens_per_expert.shape)}.")
+        if hidden_states.dtype != torch.bfloat16 or hidden_states.device.type != "cuda":
+            raise TypeError("MegaMoeExperts requires BF16 GPU hidden states.")
+        if topk_ids.dtype not in (torch.int32, torch.int64):
+            raise TypeError("topk_ids must be int32 or int64")
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("MegaMoeExperts runs eagerly; graph capture is not supported")
+        if flat.shape[0] == 0:
+            return torch.empty_like(hidden_states)
+        if tokens_per_expert is not None:
+            tokens_per_expert = tokens_per_expert.to(torch.int32)
+        if self._precision == "bf16":
+            layout, w1, w2 = self._bf16_weights(flat, expert_weights)
+            out = ops.moe_forward(flat, topk_ids, topk_weights, w1, w2, num_experts=self.num_experts,
+                                  intermediate_size=self.intermediate_size, precision="bf16", layout=layout,
+                                  tokens_per_expert=tokens_per_expert)
+        else:
+            d1, s1, d2, s2 = self._mx_weights(flat, expert_weights)
+            out = ops.moe_forward(flat, topk_ids, topk_weights, d1, d2, num_experts=self.num_experts,
+                                  intermediate_size=self.intermediate_size, precision="mxfp8", layout="EIO",
+                                  w1_scale=s1, w2_scale=s2, tokens_per_expert=tokens_per_expert)
+        return out.reshape(hidden_states.shape)

@@ -1,0 +1,52 @@
+"""MXFP8 expert-weight roots (modules/mega_moe/backends/mxfp8/weights.py:21-86 convention).
+
+A root is a tensor (or any object) carrying the forward physical fields
+``col_data`` (``torch.float8_e4m3fn``, viewable as ``[E, M, N]``) and ``col_scale``
+(``torch.uint8`` e8m0, viewable as ``[E, M/64, N, 2]``: the two 32-blocks of each 64-row group
+along the reduction axis M, for every output column N). ``quantize_expert_weight`` builds such a
+root from a bf16 ``[E, M, N]`` weight on the GPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+__all__ = ["quantize_expert_weight", "resolve_forward_weight"]
+
+
+def quantize_expert_weight(weight: torch.Tensor) -> torch.Tensor:
+    """Return a root holding ``col_data`` / ``col_scale`` for a bf16 EIO weight ``[E, M, N]``.
+
+    The root is a one-element bf16 tensor expanded to the logical shape ``[E, M, N]`` on the
+    weight's device; only the physical attributes are read by the executor.
+    """
+    if weight.ndim != 3:
+        raise ValueError("expected an EIO expert weight [E, M, N]")
+    E, M, N = weight.shape
+    if M % 64 or N % 64:
+        raise ValueError(f"MegaMoE MXFP8 expert shape requires M/N divisible by 64, got {tuple(weight.shape)}.")
+    data, scale = ops.mx_quantize_cols(weight.to(torch.bfloat16))
+    root = torch.empty((1, 1, 1), dtype=torch.bfloat16, device=weight.device).expand(E, M, N)
+    root.col_data = data
+    root.col_scale = scale
+    root.logical_shape = (E, M, N)
+    return root
+
+
+def resolve_forward_weight(root, logical_shape: tuple[int, int, int], device: torch.device):
+    """Validate and return (col_data uint8 view [E,M,N], col_scale uint8 [E,M/64,N,2])."""
+    data = getattr(root, "col_data", None)
+    scale = getattr(root, "col_scale", None)
+    if data is None or scale is None:
+        raise ValueError("MegaMoE MXFP8 current root is missing required col data/scale.")
+    if data.dtype != torch.float8_e4m3fn or scale.dtype != torch.uint8:
+        raise TypeError("MegaMoE MXFP8 physical storage requires E4M3FN data and packed uint8 E8M0 scales.")
+    if not data.is_contiguous() or not scale.is_contiguous():
+        raise ValueError("MX physical data and scale must be contiguous; implicit copies are forbidden")
+    if data.device != device or scale.device != device:
+        raise ValueError("MX physical data, scales and hidden states must share a device")
+    E, M, N = logical_shape
+    if data.numel() != E * M * N or scale.numel() != E * (M // 64) * N * 2:
+        raise ValueError(f"MX root does not hold an [E, M, N] = {logical_shape} weight")
+    return data.view(torch.uint8).view(E, M, N), scale.view(E, M // 64, N, 2)

@@ -1,0 +1,329 @@
+"""Functional torch-level operators over the gfx950 C ABI (``include/mi355moe.h``).
+
+Every operator validates dtype / device / shape on the host (raising ``ValueError`` or
+``TypeError`` like the reference's torch op layer, torch/csrc/*.cpp ``TORCH_CHECK``s), allocates
+its outputs and workspace with torch's caching allocator and enqueues the HIP kernels on the
+current stream. Nothing here synchronises the host and nothing falls back to a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError("expected a torch.Tensor")
+        if t.device.type != "cuda":
+            raise TypeError(f"gfx950 operators need tensors on the GPU, got {t.device}")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError("all tensors must be on the same GPU")
+    return device
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _ids_dtype(ids: torch.Tensor) -> int:
+    if ids.dtype == torch.int32:
+        return _lib.IDS_INT32
+    if ids.dtype == torch.int64:
+        return _lib.IDS_INT64
+    raise TypeError("topk_ids must be int32 or int64")
+
+
+# ------------------------------------------------------------------------------------------------
+# MegaGate
+# ------------------------------------------------------------------------------------------------
+def gate_logits(x: torch.Tensor, weight: torch.Tensor, weight_vision: torch.Tensor | None = None,
+                image_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 logits [T, E] = x [T, H] (bf16) @ weight[E, H]^T (bf16), fp32 accumulation.
+
+    With ``weight_vision`` and ``image_mask`` ([T] bool), masked tokens use ``weight_vision``.
+    """
+    lib = _lib.load()
+    device = _require_gpu(x, weight, weight_vision, image_mask)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("router projection takes bf16 hidden states and bf16 weights")
+    if x.ndim != 2 or weight.ndim != 2 or weight.shape[1] != x.shape[1]:
+        raise ValueError(f"bad router shapes x{tuple(x.shape)} w{tuple(weight.shape)}")
+    if (weight_vision is None) != (image_mask is None):
+        raise ValueError("weight_vision and image_mask go together")
+    if weight_vision is not None:
+        if weight_vision.shape != weight.shape or weight_vision.dtype != torch.bfloat16:
+            raise ValueError("weight_vision must match weight")
+        if image_mask.dtype != torch.bool or image_mask.numel() != x.shape[0]:
+            raise ValueError("image_mask must be bool [T]")
+        weight_vision = weight_vision.contiguous()
+        image_mask = image_mask.reshape(-1).contiguous()
+    x = x.contiguous()
+    weight = weight.contiguous()
+    T, H = x.shape
+    E = weight.shape[0]
+    out = torch.empty((T, E), dtype=torch.float32, device=device)
+    ws = _workspace(lib.mi355moe_gate_logits_workspace_size(T), device)
+    rc = lib.mi355moe_gate_logits(_ptr(x), T, H, _ptr(weight), _ptr(weight_vision), _ptr(image_mask), E,
+                                  _ptr(out), _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(rc, "mi355moe_gate_logits")
+    return out
+
+
+def gate_route(logits: torch.Tensor, bias: torch.Tensor, *, top_k: int, scoring_func: str,
+               routed_scaling_factor: float, bias_vl: torch.Tensor | None = None,
+               image_mask: torch.Tensor | None = None, num_groups: int = 1, topk_groups: int = 1,
+               return_scores: bool = False):
+    """Route fp32 logits [T, E]: returns (weights fp32 [T,K], indices int64 [T,K][, scores [T,E]]).
+
+    Mirrors hyper_multicore::mega_gate_route (torch/csrc/mega_gate.cpp:65-82) for all three
+    scoring functions, plus the group-limited selection when ``num_groups > 1``.
+    """
+    lib = _lib.load()
+    device = _require_gpu(logits, bias, bias_vl, image_mask)
+    if logits.dtype != torch.float32 or logits.ndim != 2:
+        raise TypeError("logits must be fp32 [tokens, experts]")
+    T, E = logits.shape
+    if bias.dtype != torch.float32 or bias.shape != (E,):
+        raise ValueError("bias must be fp32 [num_experts]")
+    if bias_vl is not None and (bias_vl.dtype != torch.float32 or bias_vl.shape != (E,)):
+        raise ValueError("bias_vl must be fp32 [num_experts]")
+    if image_mask is not None:
+        if image_mask.dtype != torch.bool or image_mask.numel() != T:
+            raise ValueError("image_mask must be bool with one entry per token")
+        image_mask = image_mask.reshape(-1).contiguous()
+    if scoring_func not in _lib.SCORE:
+        raise ValueError(f"unsupported scoring_func: {scoring_func!r}")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    weights = torch.empty((T, top_k), dtype=torch.float32, device=device)
+    indices = torch.empty((T, top_k), dtype=torch.int64, device=device)
+    scores = torch.empty((T, E), dtype=torch.float32, device=device) if return_scores else None
+    args = _lib.RouteArgs(
+        logits=_ptr(logits), logits_row_stride=logits.stride(0), bias=_ptr(bias.contiguous()),
+        bias_vl=_ptr(bias_vl.contiguous() if bias_vl is not None else None), image_mask=_ptr(image_mask),
+        weights_out=_ptr(weights), indices_out=_ptr(indices), indices32_out=None, scores_out=_ptr(scores),
+        num_tokens=T, num_experts=E, top_k=top_k, scoring=_lib.SCORE[scoring_func], num_groups=num_groups,
+        topk_groups=topk_groups, routed_scaling_factor=float(routed_scaling_factor))
+    rc = lib.mi355moe_gate_route(ctypes.byref(args), _stream(device))
+    _lib.check(rc, "mi355moe_gate_route")
+    return (weights, indices, scores) if return_scores else (weights, indices)
+
+
+# ------------------------------------------------------------------------------------------------
+# Dispatch / permute / combine
+# ------------------------------------------------------------------------------------------------
+@dataclass
+class DispatchResult:
+    """Route metadata at EP=1 (modules/mega_moe/route.py RouteMetadata fields that survive EP=1)."""
+
+    counts: torch.Tensor          # int32 [E]
+    expert_offsets: torch.Tensor  # int64 [E] exclusive prefix (dispatch_src_off)
+    group_list: torch.Tensor      # int64 [E] inclusive prefix
+    mapping: torch.Tensor         # int32 [T*K] slot -> routed row
+    gather_index: torch.Tensor    # int32 [T*K] routed row -> slot
+    error_flag: torch.Tensor      # int32 [1], 1 if an id was outside [0, E)
+
+
+def dispatch(topk_ids: torch.Tensor, num_experts: int) -> DispatchResult:
+    """Histogram + scan + stable permutation of the routed slots of ``topk_ids`` [T, K]."""
+    lib = _lib.load()
+    device = _require_gpu(topk_ids)
+    if topk_ids.ndim != 2:
+        raise ValueError("topk_ids must be [tokens, top_k]")
+    ids = topk_ids.contiguous()
+    T, K = ids.shape
+    R = T * K
+    counts = torch.empty(num_experts, dtype=torch.int32, device=device)
+    offsets = torch.empty(num_experts, dtype=torch.int64, device=device)
+    group_list = torch.empty(num_experts, dtype=torch.int64, device=device)
+    mapping = torch.empty(R, dtype=torch.int32, device=device)
+    gather = torch.empty(R, dtype=torch.int32, device=device)
+    err = torch.zeros(1, dtype=torch.int32, device=device)
+    ws = _workspace(lib.mi355moe_dispatch_workspace_size(T, K, num_experts), device)
+    args = _lib.DispatchArgs(topk_ids=_ptr(ids), ids_dtype=_ids_dtype(ids), top_k=K, num_tokens=T,
+                             num_experts=num_experts, counts=_ptr(counts), expert_offsets=_ptr(offsets),
+                             group_list=_ptr(group_list), mapping=_ptr(mapping), gather_index=_ptr(gather),
+                             error_flag=_ptr(err))
+    rc = lib.mi355moe_dispatch(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(rc, "mi355moe_dispatch")
+    return DispatchResult(counts, offsets, group_list, mapping, gather, err)
+
+
+def token_permute(tokens: torch.Tensor, topk_ids: torch.Tensor, num_experts: int):
+    """(routed bf16 [T*K, H], mapping int32 [T*K]) like npu_moe_token_permute (route.py:281-295)."""
+    lib = _lib.load()
+    device = _require_gpu(tokens, topk_ids)
+    if tokens.dtype != torch.bfloat16 or tokens.ndim != 2:
+        raise TypeError("tokens must be bf16 [T, H]")
+    ids = topk_ids.contiguous()
+    T, K = ids.shape
+    if tokens.shape[0] != T:
+        raise ValueError("tokens and topk_ids disagree on the token count")
+    H = tokens.shape[1]
+    x = tokens.contiguous()
+    routed = torch.empty((T * K, H), dtype=torch.bfloat16, device=device)
+    mapping = torch.empty(T * K, dtype=torch.int32, device=device)
+    ws = _workspace(lib.mi355moe_dispatch_workspace_size(T, K, num_experts), device)
+    rc = lib.mi355moe_token_permute(_ptr(x), T, H, _ptr(ids), _ids_dtype(ids), K, num_experts, _ptr(routed),
+                                    _ptr(mapping), _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(rc, "mi355moe_token_permute")
+    return routed, mapping
+
+
+def token_unpermute(values: torch.Tensor, mapping: torch.Tensor, probs: torch.Tensor | None,
+                    top_k: int) -> torch.Tensor:
+    """out[t] = bf16(sum_k probs[t,k] * values[mapping[t*K+k]]) in ascending k, fp32 accumulate."""
+    lib = _lib.load()
+    device = _require_gpu(values, mapping, probs)
+    if values.dtype != torch.bfloat16 or values.ndim != 2:
+        raise TypeError("values must be bf16 [rows, H]")
+    if mapping.dtype != torch.int32 or mapping.numel() % top_k:
+        raise ValueError("mapping must be int32 [T*K]")
+    T = mapping.numel() // top_k
+    H = values.shape[1]
+    if probs is not None:
+        if probs.shape != (T, top_k):
+            raise ValueError("probs must be [T, K]")
+        probs = probs.to(torch.float32).contiguous()
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    rc = lib.mi355moe_token_unpermute(_ptr(values.contiguous()), _ptr(mapping.contiguous()), _ptr(probs), T,
+                                      top_k, H, _ptr(out), _stream(device))
+    _lib.check(rc, "mi355moe_token_unpermute")
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# MX quantisation
+# ------------------------------------------------------------------------------------------------
+def mx_quantize_rows(x: torch.Tensor):
+    """bf16 [M, N] -> (e4m3 data uint8 [M, N], e8m0 scale uint8 [M, N/32]); blocks along N."""
+    lib = _lib.load()
+    device = _require_gpu(x)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.shape[1] % 32:
+        raise ValueError("mx_quantize_rows takes bf16 [M, N] with N % 32 == 0")
+    x = x.contiguous()
+    M, N = x.shape
+    q = torch.empty((M, N), dtype=torch.uint8, device=device)
+    s = torch.empty((M, N // 32), dtype=torch.uint8, device=device)
+    _lib.check(lib.mi355moe_mx_quantize_rows(_ptr(x), M, N, _ptr(q), _ptr(s), _stream(device)),
+               "mi355moe_mx_quantize_rows")
+    return q, s
+
+
+def mx_quantize_cols(w: torch.Tensor):
+    """bf16 [G, K, N] -> (col_data e4m3fn [G, K, N], col_scale uint8 [G, K/64, N, 2])."""
+    lib = _lib.load()
+    device = _require_gpu(w)
+    if w.dtype != torch.bfloat16 or w.ndim != 3 or w.shape[1] % 64:
+        raise ValueError("mx_quantize_cols takes bf16 [G, K, N] with K % 64 == 0")
+    w = w.contiguous()
+    G, K, N = w.shape
+    data = torch.empty((G, K, N), dtype=torch.float8_e4m3fn, device=device)
+    scale = torch.empty((G, K // 64, N, 2), dtype=torch.uint8, device=device)
+    _lib.check(lib.mi355moe_mx_quantize_cols(_ptr(w), G, K, N, _ptr(data), _ptr(scale), _stream(device)),
+               "mi355moe_mx_quantize_cols")
+    return data, scale
+
+
+# ------------------------------------------------------------------------------------------------
+# Grouped GEMM and the full expert forward
+# ------------------------------------------------------------------------------------------------
+def grouped_gemm_bf16(x: torch.Tensor, weights: torch.Tensor, group_list: torch.Tensor,
+                      layout: str = "EIO") -> torch.Tensor:
+    """Concatenated per-group ``x[seg_g] @ W_g``; group_list = int64 inclusive row cumsum.
+
+    layout "EIO": weights [G, K, N]; "EOI": weights [G, N, K].
+    """
+    lib = _lib.load()
+    device = _require_gpu(x, weights, group_list)
+    if x.dtype != torch.bfloat16 or weights.dtype != torch.bfloat16:
+        raise TypeError("grouped_gemm_bf16 takes bf16 operands")
+    G = weights.shape[0]
+    if layout == "EIO":
+        K, N = weights.shape[1], weights.shape[2]
+    elif layout == "EOI":
+        N, K = weights.shape[1], weights.shape[2]
+    else:
+        raise ValueError(f"unknown layout {layout!r}")
+    if x.shape[1] != K or group_list.shape != (G,) or group_list.dtype != torch.int64:
+        raise ValueError("shape mismatch in grouped_gemm_bf16")
+    rows = x.shape[0]
+    out = torch.empty((rows, N), dtype=torch.bfloat16, device=device)
+    ws = _workspace(lib.mi355moe_grouped_gemm_workspace_size(G), device)
+    rc = lib.mi355moe_grouped_gemm_bf16(_ptr(x.contiguous()), rows, K, _ptr(weights.contiguous()),
+                                        _lib.LAYOUT[layout], G, N, _ptr(group_list.contiguous()), _ptr(out),
+                                        _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(rc, "mi355moe_grouped_gemm_bf16")
+    return out
+
+
+def grouped_gemm_mxfp8(xq: torch.Tensor, x_scale: torch.Tensor, col_data: torch.Tensor, col_scale: torch.Tensor,
+                       group_list: torch.Tensor) -> torch.Tensor:
+    """MX grouped GEMM: xq e4m3 [rows, K] (+ e8m0 [rows, K/32]) times col_data [G, K, N]
+    (+ col_scale [G, K/64, N, 2]) per group segment; bf16 [rows, N] out."""
+    lib = _lib.load()
+    device = _require_gpu(xq, x_scale, col_data, col_scale, group_list)
+    G, K, N = col_data.shape
+    rows = xq.shape[0]
+    if xq.shape != (rows, K) or x_scale.shape != (rows, K // 32) or col_scale.shape != (G, K // 64, N, 2):
+        raise ValueError("shape mismatch in grouped_gemm_mxfp8")
+    if group_list.shape != (G,) or group_list.dtype != torch.int64:
+        raise ValueError("group_list must be int64 [G]")
+    out = torch.empty((rows, N), dtype=torch.bfloat16, device=device)
+    ws = _workspace(lib.mi355moe_grouped_gemm_workspace_size(G), device)
+    rc = lib.mi355moe_grouped_gemm_mxfp8(_ptr(xq.contiguous()), _ptr(x_scale.contiguous()), rows, K,
+                                         _ptr(col_data.contiguous()), _ptr(col_scale.contiguous()), G, N,
+                                         _ptr(group_list.contiguous()), _ptr(out), _ptr(ws), ws.numel(),
+                                         _stream(device))
+    _lib.check(rc, "mi355moe_grouped_gemm_mxfp8")
+    return out
+
+
+def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w1: torch.Tensor,
+                w2: torch.Tensor, *, num_experts: int, intermediate_size: int, precision: str = "bf16",
+                layout: str = "EIO", w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
+                tokens_per_expert: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                error_flag: torch.Tensor | None = None) -> torch.Tensor:
+    """Expert forward at EP=1 through ``mi355moe_moe_forward``; returns bf16 [T, H]."""
+    lib = _lib.load()
+    device = _require_gpu(hidden, topk_ids, topk_weights, w1, w2, w1_scale, w2_scale, tokens_per_expert)
+    if hidden.dtype != torch.bfloat16 or hidden.ndim != 2:
+        raise TypeError("hidden must be bf16 [T, H]")
+    T, H = hidden.shape
+    K = topk_ids.shape[1]
+    hidden = hidden.contiguous()
+    ids = topk_ids.contiguous()
+    probs = topk_weights.to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    args = _lib.ForwardArgs(
+        hidden=_ptr(hidden), num_tokens=T, hidden_size=H, intermediate_size=intermediate_size,
+        num_experts=num_experts, top_k=K, topk_ids=_ptr(ids), ids_dtype=_ids_dtype(ids),
+        precision=_lib.PRECISION[precision], topk_weights=_ptr(probs), weight_layout=_lib.LAYOUT[layout],
+        reserved0=0, w1=_ptr(w1), w2=_ptr(w2), w1_scale=_ptr(w1_scale), w2_scale=_ptr(w2_scale),
+        tokens_per_expert=_ptr(tokens_per_expert), out=_ptr(out), error_flag=_ptr(error_flag))
+    need = lib.mi355moe_moe_forward_workspace_size(ctypes.byref(args))
+    if need == 0 and T > 0:
+        _lib.check(lib.mi355moe_moe_forward(ctypes.byref(args), None, 0, _stream(device)), "mi355moe_moe_forward")
+    ws = _workspace(need, device)
+    rc = lib.mi355moe_moe_forward(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(rc, "mi355moe_moe_forward")
+    return out

@@ -1,0 +1,229 @@
+/*
+ * mi355moe.h - C ABI of the MI355X (gfx950) MegaGate -> MegaMoE forward path, expert-parallel
+ * degree 1 (every expert on one GPU).
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers unless stated otherwise; tensors are dense row-major.
+ *   - `stream` is a hipStream_t passed as void*; work is enqueued asynchronously on it and no
+ *     entry point synchronises the host.
+ *   - Return 0 on success, a negative MI355MOE_E* code on invalid arguments or launch failure.
+ *     Nothing is enqueued when an argument check fails.
+ *   - bf16 is passed as uint16_t storage; e4m3 (OCP fp8 e4m3fn) and e8m0 as uint8_t.
+ *
+ * The reference interfaces each entry point replaces are cited per declaration
+ * (paths relative to the hyper-multicore source tree).
+ */
+#ifndef MI355MOE_H_
+#define MI355MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355MOE_ABI_VERSION 1
+
+enum {
+  MI355MOE_OK_CODE = 0,
+  MI355MOE_EINVAL_CODE = -1,      /* invalid argument / shape / alignment */
+  MI355MOE_ELAUNCH_CODE = -2,     /* HIP launch error */
+  MI355MOE_EUNSUPPORTED_CODE = -3, /* valid request outside what this build implements */
+  MI355MOE_EWORKSPACE_CODE = -4   /* workspace missing or too small */
+};
+
+enum { MI355MOE_SCORE_SOFTMAX = 0, MI355MOE_SCORE_SIGMOID = 1, MI355MOE_SCORE_SQRTSOFTPLUS = 2 };
+enum { MI355MOE_IDS_INT32 = 0, MI355MOE_IDS_INT64 = 1 };
+enum { MI355MOE_PRECISION_BF16 = 0, MI355MOE_PRECISION_MXFP8 = 1 };
+/* Expert weight layouts (modules/mega_moe/module.py:276-279):
+ *   EIO: w1 [E, H, 2I], w2 [E, I, H]   (input-major rows, output contiguous)
+ *   EOI: w1 [E, 2I, H], w2 [E, H, I]   (output-major rows, input contiguous) */
+enum { MI355MOE_LAYOUT_EIO = 0, MI355MOE_LAYOUT_EOI = 1 };
+
+/* ---------------------------------------------------------------------------------------------
+ * ABI version of the loaded library (no reference counterpart; used by the loader check).
+ */
+int mi355moe_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Router projection: logits[t, e] = sum_h x[t, h] * w[e, h], bf16 inputs, fp32 accumulate and
+ * fp32 output. Replaces the fp32 projection F.linear(x.float(), W.float())
+ * (modules/mega_gate/function.py:176-178, modules/mega_gate/module.py:195-198); bf16 x bf16
+ * products are exact in fp32, only the summation order differs from the reference.
+ * When w_vision and image_mask are given, tokens with image_mask[t] != 0 use w_vision instead of
+ * w (per-modality router matrices); this needs `workspace` of
+ * mi355moe_gate_logits_workspace_size() bytes, otherwise workspace may be NULL.
+ */
+size_t mi355moe_gate_logits_workspace_size(int64_t num_tokens);
+int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32_t hidden_size,
+                         const uint16_t* w, const uint16_t* w_vision, const uint8_t* image_mask,
+                         int32_t num_experts, float* logits, void* workspace,
+                         size_t workspace_size, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Route: scores, correction bias, (group-limited) top-k, gather, renormalise, scale.
+ * Replaces hyper_multicore::mega_gate_route / aclnnHyperMegaGateRoute
+ * (torch/csrc/mega_gate_registration.cpp:16-42, torch/csrc/mega_gate.cpp:65-82,
+ *  ops/hyper_mega_gate/op_kernel/route_pipeline.h:73-562) and the torch path
+ * MegaGate._torch_forward (modules/mega_gate/module.py:189-227) for softmax / sigmoid.
+ * Output order within a row: descending biased score, ties by lower expert id.
+ * num_groups == 1 selects plain top-k; num_groups > 1 selects the DeepSeek-V3 group-limited form
+ * (group score = sum of the top-2 biased scores of the group; keep topk_groups groups).
+ */
+typedef struct MI355MoeRouteArgs {
+  const float* logits;        /* [T, E] fp32, row stride logits_row_stride elements */
+  int64_t logits_row_stride;
+  const float* bias;          /* [E] fp32 correction bias (text tokens) */
+  const float* bias_vl;       /* [E] fp32 vision bias or NULL */
+  const uint8_t* image_mask;  /* [T] bool or NULL: nonzero selects bias_vl */
+  float* weights_out;         /* [T, K] fp32 routing weights */
+  int64_t* indices_out;       /* [T, K] int64 expert ids (NULL allowed if indices32_out given) */
+  int32_t* indices32_out;     /* [T, K] int32 expert ids or NULL */
+  float* scores_out;          /* [T, E] fp32 unbiased scores or NULL */
+  int64_t num_tokens;
+  int32_t num_experts;        /* <= 1024 */
+  int32_t top_k;              /* <= min(E, 64) */
+  int32_t scoring;            /* MI355MOE_SCORE_* */
+  int32_t num_groups;         /* 1 = no grouping; divides E */
+  int32_t topk_groups;
+  float routed_scaling_factor;
+} MI355MoeRouteArgs;
+int mi355moe_gate_route(const MI355MoeRouteArgs* args, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Dispatch metadata: per-expert histogram (LDS atomics), exclusive scan and the stable
+ * permutation of the T*K routed slots (slot s = t*K + k) by expert id.
+ * Replaces _resolve_counts / bincount (modules/mega_moe/route.py:186-211), the EP=1 case of
+ * _compute_route_metadata (route.py:309-390) and the mapping half of moe_token_permute_out /
+ * npu_moe_token_permute (route.py:281-306, torch/csrc/moe_token_permute_out.cpp:50-60).
+ *   counts[e]          number of slots routed to e                           (int32)
+ *   expert_offsets[e]  exclusive prefix of counts = dispatch_src_off at EP=1  (int64, optional)
+ *   group_list[e]      inclusive prefix of counts                             (int64, optional)
+ *   mapping[s]         routed row of slot s (scatter map), -1 for an id outside [0, E)
+ *   gather_index[r]    slot held by routed row r                              (optional)
+ *   error_flag         set to 1 when any id is outside [0, E) (optional, int32)
+ * Routed rows are expert-major; within an expert they keep ascending slot order.
+ */
+typedef struct MI355MoeDispatchArgs {
+  const void* topk_ids;       /* [T, K] int32 or int64 */
+  int32_t ids_dtype;          /* MI355MOE_IDS_* */
+  int32_t top_k;
+  int64_t num_tokens;
+  int32_t num_experts;        /* <= 4096 */
+  int32_t* counts;
+  int64_t* expert_offsets;
+  int64_t* group_list;
+  int32_t* mapping;
+  int32_t* gather_index;
+  int32_t* error_flag;
+} MI355MoeDispatchArgs;
+size_t mi355moe_dispatch_workspace_size(int64_t num_tokens, int32_t top_k, int32_t num_experts);
+int mi355moe_dispatch(const MI355MoeDispatchArgs* args, void* workspace, size_t workspace_size,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Token permute: routed[mapping[t*K+k]] = x[t]; also writes `mapping` (int32 [T*K]).
+ * Replaces hyper_multicore::moe_token_permute_out(tokens, indices, out!, mapping!)
+ * (torch/csrc/registration.cpp:15-16, torch/csrc/moe_token_permute_out.cpp:25-72).
+ */
+int mi355moe_token_permute(const uint16_t* x, int64_t num_tokens, int32_t hidden_size,
+                           const void* topk_ids, int32_t ids_dtype, int32_t top_k,
+                           int32_t num_experts, uint16_t* routed, int32_t* mapping,
+                           void* workspace, size_t workspace_size, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Token unpermute (combine): out[t] = bf16( sum_{k=0..K-1} p[t,k] * y[mapping[t*K+k]] ), fp32
+ * accumulation in ascending k, a single bf16 rounding; slots with mapping < 0 contribute 0;
+ * probs == NULL means p = 1.
+ * Replaces npu_moe_token_unpermute(y, mapping, probs) as used by restore_topk_output
+ * (modules/mega_moe/route.py:1029-1051, backends/mxfp8/execution.py:103).
+ */
+int mi355moe_token_unpermute(const uint16_t* y, const int32_t* mapping, const float* probs,
+                             int64_t num_tokens, int32_t top_k, int32_t hidden_size,
+                             uint16_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * MX (OCP MX v1.0) quantisation, e4m3fn elements with one e8m0 scale per 32 elements:
+ * scale = 2^(floor(log2(amax)) - 8), element = RNE(v / scale) saturated to +-448.
+ * rows:  x [M, N] bf16 -> q [M, N] e4m3, scale [M, N/32] e8m0 (blocks along N).
+ *        Replaces the row axis of DynamicMxQuantWithDualAxis (quant_x task,
+ *        ops/common/mega_moe/adapters/arch35/quantization/dual_axis_mxfp8_worker.h:39-66).
+ * cols:  w [G, Kd, N] bf16 -> col_data [G, Kd, N] e4m3, col_scale [G, Kd/64, N, 2] e8m0
+ *        (blocks of 32 along Kd per column) - the forward MX weight root layout
+ *        (modules/mega_moe/backends/mxfp8/weights.py:61-86).
+ */
+int mi355moe_mx_quantize_rows(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q,
+                              uint8_t* scale, void* stream);
+int mi355moe_mx_quantize_cols(const uint16_t* w, int32_t groups, int32_t kdim, int32_t cols,
+                              uint8_t* col_data, uint8_t* col_scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Grouped GEMM over consecutive row segments (one segment per group):
+ *   out[r, :] = x[r, :] @ W_g        for rows r of group g,
+ * group_list is the int64 inclusive cumulative row count per group (the grouped_matmul
+ * group_list convention, tests/common/multicore/moe_reference.py:185-200).
+ * bf16 weights: layout EIO -> W_g stored [K, N]; EOI -> stored [N, K].
+ * Output bf16 (rounded once from the fp32 accumulator).
+ * Replaces the per-expert GMM tasks (ops/hyper_mega_moe/op_kernel/worker_kernel.cpp:225-299).
+ */
+size_t mi355moe_grouped_gemm_workspace_size(int32_t num_groups);
+int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim,
+                               const uint16_t* w, int32_t layout, int32_t num_groups,
+                               int32_t ndim, const int64_t* group_list, uint16_t* out,
+                               void* workspace, size_t workspace_size, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * MXFP8 grouped GEMM: out[r, :] = dequant(xq[r, :]) @ dequant(W_g), bf16 output, fp32 accumulate.
+ * xq [rows, K] e4m3 with x_scale [rows, K/32] e8m0 (blocks along K); W_g = col_data [G, K, N]
+ * e4m3 with col_scale [G, K/64, N, 2] (the forward MX weight root). K % 128 == 0, N % 16 == 0.
+ * Replaces the MX GMM task (ops/common/mega_moe/adapters/arch35/gmm/mxfp8_worker.h:15-159, NN
+ * layout, contracts/mx_gmm_descriptor.h:18-87).
+ */
+int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,
+                                const uint8_t* col_data, const uint8_t* col_scale, int32_t num_groups,
+                                int32_t ndim, const int64_t* group_list, uint16_t* out, void* workspace,
+                                size_t workspace_size, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * MegaMoE expert forward at EP=1: dispatch -> (MX quant) -> GMM1 + fused SwiGLU (+ MX requant)
+ * -> GMM2 -> combine.  Replaces the MegaMoeExperts.forward launch chain
+ * (modules/mega_moe/module.py:497-535 -> backends/bf16/autograd.py:398-443 -> hyper_multicore::
+ * mega_moe, torch/csrc/registration.cpp:30-60; backends/mxfp8/execution.py:64-117 ->
+ * hyper_multicore::mega_moe_mxfp8, torch/csrc/mega_moe_mxfp8.cpp:7-46).
+ * SwiGLU: gate = left half of the 2I projection, act = bf16(silu(g) * u) with g, u the bf16
+ * GMM1 outputs (tests/common/multicore/fp32_expert_reference.py:22-26).
+ * MXFP8: w1/w2 are col_data e4m3 EIO [E,H,2I] / [E,I,H] with col_scale [E,H/64,2I,2] /
+ * [E,I/64,H,2]; H and I must be multiples of 64 (docs: MXFP8 weight contract).
+ * tokens_per_expert (optional) is a trusted int32 histogram of topk_ids; when NULL it is
+ * computed. Workspace: mi355moe_moe_forward_workspace_size(args) bytes.
+ */
+typedef struct MI355MoeForwardArgs {
+  const uint16_t* hidden;     /* [T, H] bf16 */
+  int64_t num_tokens;
+  int32_t hidden_size;
+  int32_t intermediate_size;
+  int32_t num_experts;
+  int32_t top_k;
+  const void* topk_ids;       /* [T, K] */
+  int32_t ids_dtype;
+  int32_t precision;          /* MI355MOE_PRECISION_* */
+  const float* topk_weights;  /* [T, K] fp32 */
+  int32_t weight_layout;      /* MI355MOE_LAYOUT_* (MXFP8: EIO only) */
+  int32_t reserved0;
+  const void* w1;
+  const void* w2;
+  const uint8_t* w1_scale;
+  const uint8_t* w2_scale;
+  const int32_t* tokens_per_expert; /* optional [E] int32 */
+  uint16_t* out;              /* [T, H] bf16 */
+  int32_t* error_flag;        /* optional: set to 1 for ids outside [0, E) */
+} MI355MoeForwardArgs;
+size_t mi355moe_moe_forward_workspace_size(const MI355MoeForwardArgs* args);
+int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* workspace, size_t workspace_size,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI355MOE_H_ */

@@ -1,0 +1,334 @@
+"""TEST INFRASTRUCTURE ONLY - torch-CPU restatement of the MegaGate -> MegaMoE forward path.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use this module; the
+product package never imports it. Each function cites the reference code it restates.
+
+Pinning (see tests/test_oracle.py): the route against the closed torch forms and the
+DeepSeek-V3 grouped form; route metadata and the permutation against the reference tests'
+known answers (tests/golden/*.json); MX quantisation against torch's own float8_e4m3fn cast and
+the OCP MX invariants; the expert math against the TorchExperts loop and closed forms.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import build_oracle
+
+_router_lib = None
+
+
+def _router():
+    global _router_lib
+    if _router_lib is None:
+        _router_lib = build_oracle.load()
+    return _router_lib
+
+
+SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
+
+
+# ------------------------------------------------------------------------------------------------
+# Router
+# ------------------------------------------------------------------------------------------------
+def det_expf(x: float) -> float:
+    return _router().oracle_det_expf(float(x))
+
+
+def det_logf(x: float) -> float:
+    return _router().oracle_det_logf(float(x))
+
+
+def route_c(logits: np.ndarray, bias: np.ndarray, *, top_k: int, scoring_func: str, routed_scaling_factor: float,
+            bias_vl: np.ndarray | None = None, image_mask: np.ndarray | None = None, num_groups: int = 1,
+            topk_groups: int = 1):
+    """C oracle of the route (router_ref.c): returns (weights f32 [T,K], indices i64 [T,K], scores f32 [T,E]).
+
+    Restates module.py:199-227 / route_pipeline.h:73-562 with the gfx950 kernel's fp32 order.
+    """
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    bias = np.ascontiguousarray(bias, dtype=np.float32)
+    bvl = None if bias_vl is None else np.ascontiguousarray(bias_vl, dtype=np.float32)
+    mask = None if image_mask is None else np.ascontiguousarray(image_mask, dtype=np.uint8).reshape(-1)
+    weights = np.empty((T, top_k), np.float32)
+    indices = np.empty((T, top_k), np.int64)
+    scores = np.empty((T, E), np.float32)
+    p = lambda a: None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+    rc = _router().oracle_route(p(logits), T, E, p(bias), p(bvl), p(mask), top_k, SCORING[scoring_func],
+                                num_groups, topk_groups, ctypes.c_float(routed_scaling_factor), p(weights),
+                                p(indices), p(scores))
+    if rc != 0:
+        raise ValueError(f"oracle_route rejected the arguments ({rc})")
+    return weights, indices, scores
+
+
+def gate_logits_reference(x: torch.Tensor, weight: torch.Tensor, weight_vl: torch.Tensor | None = None,
+                          image_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear(x.float(), W.float()) (module.py:195-198); per-modality weights select by mask."""
+    x = x.reshape(-1, x.shape[-1]).float()
+    logits = F.linear(x, weight.float())
+    if weight_vl is not None:
+        vis = F.linear(x, weight_vl.float())
+        logits = torch.where(image_mask.reshape(-1, 1), vis, logits)
+    return logits
+
+
+def route_reference(logits: torch.Tensor, bias: torch.Tensor, *, top_k: int, scoring_func: str,
+                    routed_scaling_factor: float, bias_vl: torch.Tensor | None = None,
+                    image_mask: torch.Tensor | None = None, num_groups: int = 1, topk_groups: int = 1):
+    """Torch-op form of MegaGate._torch_forward (module.py:199-227) after the projection.
+
+    num_groups > 1 applies the DeepSeek-V3 group-limited selection in its published torch form
+    (group score = topk(2).sum per group, topk of groups, masked_fill, topk) - the build's
+    extension; with num_groups == 1 this is exactly the reference's plain biased top-k.
+    Returns (weights [T,K], indices [T,K] from topk(sorted=False), scores [T,E]).
+    """
+    logits = logits.float()
+    if scoring_func == "sqrtsoftplus":
+        scores = F.softplus(logits).sqrt()
+    elif scoring_func == "softmax":
+        scores = logits.softmax(dim=-1)
+    elif scoring_func == "sigmoid":
+        scores = logits.sigmoid()
+    else:
+        raise ValueError(scoring_func)
+    correction = bias
+    if image_mask is not None and bias_vl is not None:
+        correction = torch.where(image_mask.reshape(-1, 1), bias_vl.unsqueeze(0), bias.unsqueeze(0))
+    biased = scores + correction
+    if num_groups > 1:
+        T, E = biased.shape
+        group_scores = biased.view(T, num_groups, -1).topk(2, dim=-1).values.sum(dim=-1)
+        group_idx = group_scores.topk(topk_groups, dim=-1, sorted=False).indices
+        group_mask = torch.zeros_like(group_scores).scatter_(1, group_idx, 1.0)
+        expert_mask = group_mask.unsqueeze(-1).expand(T, num_groups, E // num_groups).reshape(T, E)
+        biased = biased.masked_fill(expert_mask == 0, float("-inf"))
+    indices = torch.topk(biased, top_k, dim=-1, sorted=False).indices
+    weights = scores.gather(1, indices)
+    if top_k > 1:
+        weights = weights / (weights.sum(dim=-1, keepdim=True) + 1.0e-20)
+    return weights * routed_scaling_factor, indices, scores
+
+
+# ------------------------------------------------------------------------------------------------
+# Dispatch metadata and permutation
+# ------------------------------------------------------------------------------------------------
+def expert_counts(ids: torch.Tensor, num_experts: int) -> torch.Tensor:
+    """bincount(ids.flatten(), minlength=E) as int32 (route.py:186-211)."""
+    return torch.bincount(ids.reshape(-1).to(torch.int64), minlength=num_experts).to(torch.int32)
+
+
+def route_metadata(counts_by_source: torch.Tensor, *, rank: int, ep_size: int, dispatch_mode: str = "push",
+                   received_counts: torch.Tensor | None = None, counts: torch.Tensor | None = None) -> dict:
+    """Restatement of _compute_route_metadata's tensor path (route.py:309-390).
+
+    counts_by_source is [EP, E]: row p = the expert histogram of source rank p.
+    """
+    E = counts_by_source.shape[1]
+    local = E // ep_size
+    if counts is None:
+        counts = counts_by_source[rank]
+    if received_counts is None:
+        received_counts = counts_by_source[:, rank * local:(rank + 1) * local]
+    source_prefix = counts_by_source.cumsum(dim=1, dtype=torch.int64) - counts_by_source
+    dest = counts_by_source.reshape(ep_size, ep_size, local).permute(1, 2, 0).contiguous()
+    dest_flat = dest.reshape(ep_size, -1)
+    dest_prefix = (dest_flat.cumsum(dim=1, dtype=torch.int64) - dest_flat).reshape(ep_size, local, ep_size)
+    local_dest_prefix = dest_prefix[rank]
+    local_dest_counts = dest[rank]
+    lo, hi = rank * local, (rank + 1) * local
+    pull = dispatch_mode == "pull"
+    return {
+        "dispatch_src_off": (source_prefix[:, lo:hi].reshape(-1) if pull else source_prefix[rank]).to(torch.int64),
+        "dispatch_target_off": (local_dest_prefix.T.reshape(-1) if pull
+                                else dest_prefix[:, :, rank].reshape(-1)).to(torch.int64),
+        "dispatch_size": (received_counts.reshape(-1) if pull else counts).to(torch.int32),
+        "combine_src_off": local_dest_prefix.T.reshape(-1).to(torch.int64),
+        "combine_target_off": source_prefix[:, lo:hi].reshape(-1).to(torch.int64),
+        "combine_size": received_counts.reshape(-1).to(torch.int32),
+        "group_list": (local_dest_prefix[:, -1] + local_dest_counts[:, -1]).to(torch.int64),
+    }
+
+
+def stable_permutation(ids: torch.Tensor, num_experts: int):
+    """Stable sort of flat slots s = t*K + k by expert id (npu_moe_token_permute convention,
+    route.py:281-295; utilities.asc:176-204). Returns (mapping [R] slot->row, gather [R] row->slot),
+    both int32. Ids outside [0, E) get mapping -1 and no row."""
+    flat = ids.reshape(-1).to(torch.int64)
+    valid = (flat >= 0) & (flat < num_experts)
+    key = torch.where(valid, flat, torch.full_like(flat, num_experts))
+    order = torch.sort(key, stable=True).indices
+    n_valid = int(valid.sum())
+    gather = order[:n_valid].to(torch.int32)
+    mapping = torch.full((flat.numel(),), -1, dtype=torch.int32)
+    mapping[gather.long()] = torch.arange(n_valid, dtype=torch.int32)
+    return mapping, gather
+
+
+def permute_tokens(x: torch.Tensor, ids: torch.Tensor, num_experts: int):
+    """routed[mapping[s]] = x[s // K] (moe_token_permute_out, moe_token_permute_out.cpp:50-60)."""
+    K = ids.shape[1]
+    mapping, gather = stable_permutation(ids, num_experts)
+    return x[(gather.long() // K)], mapping
+
+
+def unpermute_tokens(values: torch.Tensor, mapping: torch.Tensor, probs: torch.Tensor | None, top_k: int):
+    """Build contract of the combine: fp32 sum over k ascending of p * bf16 row, one bf16 round."""
+    T = mapping.numel() // top_k
+    out = torch.zeros((T, values.shape[1]), dtype=torch.float32)
+    m = mapping.reshape(T, top_k).long()
+    for k in range(top_k):
+        rows = values.float()[m[:, k].clamp(min=0)]
+        p = torch.ones(T) if probs is None else probs[:, k].float()
+        contrib = rows * p[:, None]
+        contrib[m[:, k] < 0] = 0.0
+        out = out + contrib
+    return out.to(torch.bfloat16)
+
+
+# ------------------------------------------------------------------------------------------------
+# OCP MX (e4m3fn + e8m0 per 32)
+# ------------------------------------------------------------------------------------------------
+def mx_quantize(x: torch.Tensor, dim: int = -1):
+    """Quantise fp32/bf16 x in 32-element blocks along ``dim``: scale exponent
+    floor(log2(amax)) - 8 (OCP MX v1.0), elements cast with torch's float8_e4m3fn RNE after
+    saturation to +-448. Returns (e4m3 codes uint8 like x, e8m0 codes uint8 with dim/32)."""
+    x = x.float().movedim(dim, -1)
+    shape = x.shape
+    blocks = x.reshape(*shape[:-1], shape[-1] // 32, 32)
+    amax = blocks.abs().amax(dim=-1)
+    _, exp = torch.frexp(amax)  # amax = m * 2^exp, m in [0.5, 1)
+    shared = torch.where(amax > 0, exp - 1 - 8, torch.full_like(exp, -127)).clamp(-127, 127)
+    scaled = torch.ldexp(blocks, (-shared).unsqueeze(-1).to(torch.float32))
+    scaled = scaled.clamp(-448.0, 448.0)
+    q = scaled.to(torch.float8_e4m3fn).view(torch.uint8).reshape(shape)
+    codes = (shared + 127).to(torch.uint8)
+    return q.movedim(-1, dim), codes.movedim(-1, dim)
+
+
+def mx_dequantize(q: torch.Tensor, codes: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    """Inverse of mx_quantize: e4m3 value * 2^(code - 127), fp32."""
+    q = q.movedim(dim, -1)
+    codes = codes.movedim(dim, -1)
+    vals = q.contiguous().view(torch.float8_e4m3fn).float()
+    shape = vals.shape
+    blocks = vals.reshape(*shape[:-1], shape[-1] // 32, 32)
+    out = torch.ldexp(blocks, (codes.to(torch.float32) - 127.0).unsqueeze(-1))
+    return out.reshape(shape).movedim(-1, dim)
+
+
+def col_scale_to_blocks(col_scale: torch.Tensor) -> torch.Tensor:
+    """[G, K/64, N, 2] packed e8m0 (weights.py:61-86) -> [G, K/32, N] one code per 32-block."""
+    G, K64, N, _ = col_scale.shape
+    return col_scale.permute(0, 1, 3, 2).reshape(G, K64 * 2, N)
+
+
+def mx_quantize_weight_cols(w: torch.Tensor):
+    """bf16 [G, K, N] -> (col_data codes uint8 [G,K,N], col_scale uint8 [G,K/64,N,2])."""
+    q, codes = mx_quantize(w.float(), dim=1)  # codes [G, K/32, N]
+    G, K32, N = codes.shape
+    col_scale = codes.reshape(G, K32 // 2, 2, N).permute(0, 1, 3, 2).contiguous()
+    return q, col_scale
+
+
+def mx_dequantize_weight_cols(col_data: torch.Tensor, col_scale: torch.Tensor) -> torch.Tensor:
+    codes = col_scale_to_blocks(col_scale)
+    return mx_dequantize(col_data.view(torch.uint8), codes, dim=1)
+
+
+# ------------------------------------------------------------------------------------------------
+# Expert math
+# ------------------------------------------------------------------------------------------------
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).float()
+
+
+def expert_forward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, w1: torch.Tensor,
+                             w2: torch.Tensor, *, layout: str = "EIO", precision: str = "bf16",
+                             w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
+                             num_experts: int | None = None) -> torch.Tensor:
+    """fp32-accumulate expert forward with the reference's bf16 rounding points
+    (fp32_expert_reference.py:22-26): U = bf16(x @ W1), act = bf16(silu(g) * u) with g the left
+    half, y = bf16(act @ W2); combine = fp32 sum over k ascending of p * y, one bf16 rounding.
+
+    precision "mxfp8": x quantised per 32 along H, W1/W2 given as col_data/col_scale (EIO),
+    act = silu(g) * u quantised per 32 along I before the down projection (mxfp8/graph.py:140-146).
+    """
+    T, H = hidden.shape
+    K = ids.shape[1]
+    E = num_experts if num_experts is not None else w1.shape[0]
+    if precision == "bf16":
+        W1 = w1.float() if layout == "EIO" else w1.float().transpose(1, 2)
+        W2 = w2.float() if layout == "EIO" else w2.float().transpose(1, 2)
+        xin = hidden.float()
+    else:
+        W1 = mx_dequantize_weight_cols(w1, w1_scale)
+        W2 = mx_dequantize_weight_cols(w2, w2_scale)
+        q, s = mx_quantize(hidden.float(), dim=-1)
+        xin = mx_dequantize(q, s, dim=-1)
+    I = W1.shape[2] // 2
+    mapping, gather = stable_permutation(ids, E)
+    y = torch.zeros((gather.numel(), H), dtype=torch.float32)
+    flat = ids.reshape(-1).long()
+    start = 0
+    for e in range(E):
+        n = int((flat == e).sum())
+        if n == 0:
+            continue
+        rows = gather[start:start + n].long() // K
+        u = _bf16(xin[rows] @ W1[e])
+        g, up = u[:, :I], u[:, I:]
+        act = F.silu(g) * up
+        if precision == "bf16":
+            act = _bf16(act)
+        else:
+            aq, asc = mx_quantize(act, dim=-1)
+            act = mx_dequantize(aq, asc, dim=-1)
+        y[start:start + n] = _bf16(act @ W2[e])
+        start += n
+    return unpermute_tokens(y.to(torch.bfloat16), mapping, probs, K)
+
+
+def torch_experts_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, gate_w: torch.Tensor,
+                            up_w: torch.Tensor, down_w: torch.Tensor) -> torch.Tensor:
+    """The TorchExperts CPU loop (tests/common/multicore/moe_reference.py:170-181): weights are
+    [E, I, H] gate / up and [E, H, I] down; bf16 F.linear, bf16 weighted rows, bf16 index_add in
+    expert-major order."""
+    output = torch.zeros_like(hidden)
+    for expert in range(gate_w.shape[0]):
+        rows, slots = torch.where(ids == expert)
+        if rows.numel() == 0:
+            continue
+        source = hidden.index_select(0, rows)
+        gate = F.linear(source, gate_w[expert])
+        up = F.linear(source, up_w[expert])
+        activation = (F.silu(gate.float()) * up.float()).to(hidden.dtype)
+        value = F.linear(activation, down_w[expert])
+        weighted = (value.float() * probs[rows, slots, None]).to(hidden.dtype)
+        output = output.index_add(0, rows, weighted)
+    return output
+
+
+def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.double().reshape(-1)
+    b = b.double().reshape(-1)
+    return float(torch.linalg.vector_norm(a - b) / max(float(torch.linalg.vector_norm(b)), 1e-30))
+
+
+def moe_flops(tokens: int, top_k: int, hidden: int, inter: int, experts: int) -> float:
+    """Algorithmic FLOPs: expert GEMMs 6*R*H*I plus router 2*T*H*E."""
+    return 6.0 * tokens * top_k * hidden * inter + 2.0 * tokens * hidden * experts
+
+
+def ulp_distance(a: float, b: float) -> int:
+    ai = np.array([a], np.float32).view(np.int32)[0]
+    bi = np.array([b], np.float32).view(np.int32)[0]
+    return abs(int(ai) - int(bi))
+
+
+__all__ = [n for n in dir() if not n.startswith("_") and n not in ("annotations", "ctypes", "math", "np", "torch", "F")]

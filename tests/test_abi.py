@@ -1,0 +1,70 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol declared in include/*.h, and
+rejects bad arguments before touching the GPU (no compute calls are made here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared_symbols():
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = header.read_text()
+        for m in re.finditer(r"^\s*(?:int|size_t|void)\s+(mi355moe_\w+)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    declared = _declared_symbols()
+    assert declared, "no declarations found"
+    missing = [n for n in declared if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(_lib.EXPORTED) == declared
+    assert lib.mi355moe_abi_version() == _lib.ABI_VERSION
+
+
+def test_invalid_arguments_rejected_without_launch():
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    args = _lib.RouteArgs(num_tokens=4, num_experts=0, top_k=1, scoring=0, num_groups=1, topk_groups=1)
+    assert lib.mi355moe_gate_route(ctypes.byref(args), None) == _lib.EINVAL
+    args = _lib.RouteArgs(num_tokens=4, num_experts=8, top_k=9, scoring=0, num_groups=1, topk_groups=1)
+    assert lib.mi355moe_gate_route(ctypes.byref(args), None) == _lib.EINVAL
+    args = _lib.RouteArgs(num_tokens=4, num_experts=256, top_k=8, scoring=1, num_groups=8, topk_groups=0)
+    assert lib.mi355moe_gate_route(ctypes.byref(args), None) == _lib.EINVAL
+    d = _lib.DispatchArgs(num_tokens=4, top_k=2, num_experts=8, ids_dtype=7)
+    assert lib.mi355moe_dispatch(ctypes.byref(d), None, 0, None) == _lib.EINVAL
+    d = _lib.DispatchArgs(num_tokens=4, top_k=2, num_experts=8, ids_dtype=0, topk_ids=1, mapping=1)
+    assert lib.mi355moe_dispatch(ctypes.byref(d), None, 0, None) == _lib.EWORKSPACE
+    f = _lib.ForwardArgs(num_tokens=16, hidden_size=1000, intermediate_size=512, num_experts=8, top_k=2,
+                         ids_dtype=0, precision=1, weight_layout=0)
+    assert lib.mi355moe_moe_forward_workspace_size(ctypes.byref(f)) == 0
+    assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
+    f = _lib.ForwardArgs(num_tokens=16, hidden_size=1024, intermediate_size=512, num_experts=8, top_k=2,
+                         ids_dtype=0, precision=1, weight_layout=1)  # MXFP8 needs EIO
+    assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+
+
+def test_workspace_sizes():
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    assert lib.mi355moe_dispatch_workspace_size(8192, 8, 256) >= 256 * 4
+    f = _lib.ForwardArgs(num_tokens=8192, hidden_size=7168, intermediate_size=2048, num_experts=256, top_k=8,
+                         ids_dtype=1, precision=0, weight_layout=1, hidden=1, topk_ids=1, topk_weights=1, w1=1, w2=1,
+                         out=1)
+    need = lib.mi355moe_moe_forward_workspace_size(ctypes.byref(f))
+    R = 8192 * 8
+    assert need >= R * 2048 * 2 + R * 7168 * 2  # act + expert outputs
+
+
+def test_gpu_ops_refuse_cpu_tensors():
+    import torch
+    from hyper_multicore_amd import ops
+    with pytest.raises(TypeError):
+        ops.gate_route(torch.zeros(2, 8), torch.zeros(8), top_k=2, scoring_func="softmax", routed_scaling_factor=1.0)

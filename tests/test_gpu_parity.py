@@ -1,0 +1,322 @@
+"""GPU parity: every gfx950 kernel through the C ABI against the CPU oracle on seeded inputs.
+
+Bars: router indices / weights / scores, dispatch metadata, permutation, MX quantisation and the
+combine are bit-exact; GEMM outputs are within rel-L2 1e-2 (bf16) / 3e-2 (MXFP8) of the
+fp32-accumulate oracle on the same rounded operands.
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+BF16_REL_L2 = 1e-2
+MXFP8_REL_L2 = 3e-2
+
+
+def _seed(s):
+    torch.manual_seed(s)
+    return torch.Generator().manual_seed(s)
+
+
+# ------------------------------------------------------------------------------------------------
+# Router
+# ------------------------------------------------------------------------------------------------
+ROUTE_CASES = [
+    # name, T, E, K, scoring, groups, topk_groups, scale, use_vl
+    ("small_softmax", 1024, 8, 2, "softmax", 1, 1, 1.0, False),
+    ("dsv3_sigmoid_grouped", 2048, 256, 8, "sigmoid", 8, 4, 2.5, False),
+    ("mm_softmax_vl", 1024, 128, 8, "softmax", 1, 1, 1.0, True),
+    ("sqrtsoftplus_384", 512, 384, 6, "sqrtsoftplus", 1, 1, 1.5, False),
+    ("odd_experts_k1", 333, 100, 1, "sigmoid", 1, 1, 1.0, False),
+    ("softmax_1024", 64, 1024, 16, "softmax", 1, 1, 1.0, False),
+]
+
+
+@pytest.mark.parametrize("case", ROUTE_CASES, ids=[c[0] for c in ROUTE_CASES])
+def test_route_bit_exact_vs_c_oracle(gpu, case):
+    from hyper_multicore_amd import ops
+    name, T, E, K, scoring, G, TG, scale, use_vl = case
+    g = _seed(zlib.crc32(name.encode()) & 0xffff)
+    logits = torch.randn(T, E, generator=g) * 3
+    if scoring == "sqrtsoftplus":
+        logits[0, :8] = torch.tensor([-80.0, -20.0, -1e-7, 0.0, 20.0 - 2 ** -19, 20.0, 20.0 + 2 ** -19, 80.0])
+    bias = torch.randn(E, generator=g) * 0.01
+    bias_vl = torch.randn(E, generator=g) * 0.01 if use_vl else None
+    mask = (torch.rand(T, generator=g) < 0.5) if use_vl else None
+    w_ref, i_ref, s_ref = orc.route_c(logits.numpy(), bias.numpy(), top_k=K, scoring_func=scoring,
+                                      routed_scaling_factor=scale,
+                                      bias_vl=None if bias_vl is None else bias_vl.numpy(),
+                                      image_mask=None if mask is None else mask.numpy(), num_groups=G,
+                                      topk_groups=TG)
+    w, i, s = ops.gate_route(logits.to(gpu), bias.to(gpu), top_k=K, scoring_func=scoring,
+                             routed_scaling_factor=scale, bias_vl=None if bias_vl is None else bias_vl.to(gpu),
+                             image_mask=None if mask is None else mask.to(gpu), num_groups=G, topk_groups=TG,
+                             return_scores=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(i.cpu().numpy(), i_ref), "indices differ"
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32)), "scores differ"
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32)), "weights differ"
+
+
+def test_route_matches_torch_reference_sets(gpu):
+    """Index sets equal the torch reference form (module.py:199-227) except on near-tie rows."""
+    from hyper_multicore_amd import ops
+    g = _seed(7)
+    T, E, K = 4096, 256, 8
+    logits = torch.randn(T, E, generator=g)
+    bias = torch.randn(E, generator=g) * 0.01
+    w, i = ops.gate_route(logits.to(gpu), bias.to(gpu), top_k=K, scoring_func="sigmoid", routed_scaling_factor=2.5,
+                          num_groups=8, topk_groups=4)
+    w_ref, i_ref, _ = orc.route_reference(logits, bias, top_k=K, scoring_func="sigmoid", routed_scaling_factor=2.5,
+                                          num_groups=8, topk_groups=4)
+    got = torch.sort(i.cpu(), dim=1).values
+    want = torch.sort(i_ref, dim=1).values
+    same = (got == want).all(dim=1)
+    assert same.float().mean() > 0.999
+    order = torch.argsort(i.cpu(), dim=1)
+    order_ref = torch.argsort(i_ref, dim=1)
+    torch.testing.assert_close(w.cpu().gather(1, order)[same], w_ref.gather(1, order_ref)[same], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("T,H,E,dual", [(1024, 1024, 8, False), (777, 7168, 256, False), (1000, 4096, 128, True)])
+def test_gate_logits(gpu, T, H, E, dual):
+    from hyper_multicore_amd import ops
+    g = _seed(T + H)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    wv = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16) if dual else None
+    mask = (torch.rand(T, generator=g) < 0.5) if dual else None
+    out = ops.gate_logits(x.to(gpu), w.to(gpu), None if wv is None else wv.to(gpu),
+                          None if mask is None else mask.to(gpu))
+    ref = orc.gate_logits_reference(x, w, wv, mask)
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-5, atol=2e-5)
+
+
+# ------------------------------------------------------------------------------------------------
+# Dispatch / permute / combine
+# ------------------------------------------------------------------------------------------------
+def _ids(kind, T, K, E, g, dtype):
+    if kind == "random":
+        ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    elif kind == "skewed":
+        ids = torch.randint(0, max(1, E // 8), (T, K), generator=g)
+    elif kind == "single":
+        ids = torch.zeros(T, K, dtype=torch.int64)
+    else:
+        raise ValueError(kind)
+    return ids.to(dtype)
+
+
+@pytest.mark.parametrize("T,K,E,kind,dtype", [
+    (7, 1, 6, "random", torch.int32), (1024, 2, 8, "random", torch.int64), (8192, 8, 256, "random", torch.int32),
+    (128, 8, 256, "skewed", torch.int64), (3000, 4, 64, "single", torch.int32), (16384, 8, 128, "random", torch.int64),
+    (1, 8, 4096, "random", torch.int32)])
+def test_dispatch_bit_exact(gpu, T, K, E, kind, dtype):
+    from hyper_multicore_amd import ops
+    g = _seed(T * 31 + E)
+    ids = _ids(kind, T, K, E, g, dtype)
+    d = ops.dispatch(ids.to(gpu), E)
+    counts = orc.expert_counts(ids, E)
+    mapping, gather = orc.stable_permutation(ids, E)
+    assert torch.equal(d.counts.cpu(), counts)
+    assert torch.equal(d.group_list.cpu(), counts.cumsum(0).to(torch.int64))
+    assert torch.equal(d.expert_offsets.cpu(), counts.cumsum(0).to(torch.int64) - counts.to(torch.int64))
+    assert torch.equal(d.mapping.cpu(), mapping)
+    assert torch.equal(d.gather_index.cpu(), gather)
+    assert int(d.error_flag.cpu()) == 0
+
+
+def test_dispatch_invalid_ids_flagged(gpu):
+    from hyper_multicore_amd import ops
+    ids = torch.tensor([[0, 1], [5, 2], [-1, 3]], dtype=torch.int32)
+    d = ops.dispatch(ids.to(gpu), 4)
+    mapping, gather = orc.stable_permutation(ids, 4)
+    assert int(d.error_flag.cpu()) == 1
+    assert torch.equal(d.mapping.cpu(), mapping)
+    assert torch.equal(d.counts.cpu(), torch.tensor([1, 1, 1, 1], dtype=torch.int32))
+
+
+def test_permute_kat_and_unpermute(gpu):
+    """Gather order [0,1,3,4,5,6,2] <=> scatter mapping [0,1,6,2,3,4,5]
+    (tests/ut/examples/moe/test_native_experts.py:59-80)."""
+    from hyper_multicore_amd import ops
+    ids = torch.tensor([[0], [0], [2], [1], [1], [1], [1]], dtype=torch.int64)
+    x = torch.arange(7 * 8, dtype=torch.float32).reshape(7, 8).to(torch.bfloat16)
+    routed, mapping = ops.token_permute(x.to(gpu), ids.to(gpu), 3)
+    assert mapping.cpu().tolist() == [0, 1, 6, 2, 3, 4, 5]
+    assert torch.equal(routed.cpu(), x[torch.tensor([0, 1, 3, 4, 5, 6, 2])])
+    back = ops.token_unpermute(routed, mapping, None, 1)
+    assert torch.equal(back.cpu(), x)
+
+
+@pytest.mark.parametrize("T,K,E,H", [(1024, 2, 8, 1024), (513, 8, 256, 7168), (64, 8, 128, 4096)])
+def test_permute_unpermute_bit_exact(gpu, T, K, E, H):
+    from hyper_multicore_amd import ops
+    g = _seed(T + K + H)
+    ids = _ids("random", T, K, E, g, torch.int64)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    probs = torch.rand(T, K, generator=g)
+    routed, mapping = ops.token_permute(x.to(gpu), ids.to(gpu), E)
+    r_ref, m_ref = orc.permute_tokens(x, ids, E)
+    assert torch.equal(mapping.cpu(), m_ref)
+    assert torch.equal(routed.cpu(), r_ref)
+    y = torch.randn(T * K, H, generator=g).to(torch.bfloat16)
+    out = ops.token_unpermute(y.to(gpu), mapping, probs.to(gpu), K)
+    ref = orc.unpermute_tokens(y, m_ref, probs, K)
+    assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+# ------------------------------------------------------------------------------------------------
+# MX quantisation
+# ------------------------------------------------------------------------------------------------
+def test_mx_quantize_rows_bit_exact(gpu):
+    from hyper_multicore_amd import ops
+    g = _seed(11)
+    x = torch.randn(300, 7168, generator=g) * torch.logspace(-6, 6, 300).unsqueeze(1)
+    x[0, :32] = 0.0
+    x[1, :32] = 1e-30
+    x[2, :32] = 500.0
+    x = x.to(torch.bfloat16)
+    q, s = ops.mx_quantize_rows(x.to(gpu))
+    q_ref, s_ref = orc.mx_quantize(x.float(), dim=-1)
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(q.cpu(), q_ref)
+
+
+def test_mx_quantize_cols_bit_exact(gpu):
+    from hyper_multicore_amd import ops
+    g = _seed(12)
+    w = (torch.randn(3, 256, 384, generator=g) * 0.006).to(torch.bfloat16)
+    d, s = ops.mx_quantize_cols(w.to(gpu))
+    d_ref, s_ref = orc.mx_quantize_weight_cols(w)
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(d.cpu().view(torch.uint8), d_ref)
+
+
+# ------------------------------------------------------------------------------------------------
+# GEMMs and the full expert forward
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("layout", ["EIO", "EOI"])
+@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [0, 0, 7], [256] * 4])
+def test_grouped_gemm_bf16(gpu, layout, counts):
+    from hyper_multicore_amd import ops
+    g = _seed(sum(counts) + len(layout))
+    G, Kd, N = len(counts), 512, 768
+    rows = sum(counts)
+    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
+    wl = w if layout == "EIO" else w.transpose(1, 2).contiguous()
+    gl = torch.tensor(counts).cumsum(0).to(torch.int64)
+    out = ops.grouped_gemm_bf16(x.to(gpu), wl.to(gpu), gl.to(gpu), layout).cpu()
+    starts = [0, *gl.tolist()]
+    ref = torch.cat([x[starts[i]:starts[i + 1]].float() @ w[i].float() for i in range(G)]).to(torch.bfloat16)
+    assert orc.rel_l2(out, ref) < 2e-3
+    torch.testing.assert_close(out.float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+
+
+def _expert_inputs(T, H, I, E, K, g, wscale=0.02):
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    probs = torch.rand(T, K, generator=g)
+    probs = probs / probs.sum(1, keepdim=True)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * wscale).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * wscale).to(torch.bfloat16)
+    return x, ids, probs, w1, w2
+
+
+@pytest.mark.parametrize("layout", ["EIO", "EOI"])
+def test_moe_forward_bf16_small(gpu, layout):
+    """Config 1 shape: T=1024, E=8, K=2, H=1024, I=512."""
+    from hyper_multicore_amd import ops
+    g = _seed(2024)
+    T, H, I, E, K = 1024, 1024, 512, 8, 2
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
+    if layout == "EOI":
+        w1d, w2d = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
+    else:
+        w1d, w2d = w1, w2
+    out = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d.to(gpu), w2d.to(gpu), num_experts=E,
+                          intermediate_size=I, layout=layout).cpu()
+    ref = orc.expert_forward_reference(x, ids, probs, w1, w2, layout="EIO")
+    assert orc.rel_l2(out, ref) < BF16_REL_L2
+    # the reference's own golden loop (bf16 F.linear, expert-major bf16 index_add)
+    gate_w = w1[:, :, :I].transpose(1, 2).contiguous()
+    up_w = w1[:, :, I:].transpose(1, 2).contiguous()
+    down_w = w2.transpose(1, 2).contiguous()
+    golden = orc.torch_experts_reference(x, ids, probs, gate_w, up_w, down_w)
+    assert orc.rel_l2(out, golden) < BF16_REL_L2
+
+
+@pytest.mark.parametrize("T,H,I,E,K", [(1024, 1024, 512, 8, 2), (300, 1024, 256, 16, 4)])
+def test_moe_forward_mxfp8_small(gpu, T, H, I, E, K):
+    from hyper_multicore_amd import ops
+    g = _seed(T + E)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
+    d1, s1 = ops.mx_quantize_cols(w1.to(gpu))
+    d2, s2 = ops.mx_quantize_cols(w2.to(gpu))
+    out = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8),
+                          num_experts=E, intermediate_size=I, precision="mxfp8", w1_scale=s1, w2_scale=s2).cpu()
+    ref = orc.expert_forward_reference(x, ids, probs, d1.cpu().view(torch.uint8), d2.cpu().view(torch.uint8),
+                                       precision="mxfp8", w1_scale=s1.cpu(), w2_scale=s2.cpu())
+    assert orc.rel_l2(out, ref) < MXFP8_REL_L2
+    bf16_ref = orc.expert_forward_reference(x, ids, probs, w1, w2)
+    assert orc.rel_l2(out, bf16_ref) < 0.15  # quantisation error only (informational bound)
+
+
+def test_modules_end_to_end(gpu):
+    """MegaGate -> MegaMoeExperts through the public modules (DSv3 routing form, reduced sizes)."""
+    import hyper_multicore_amd as hm
+    g = _seed(99)
+    T, H, I, E, K = 512, 1024, 256, 64, 8
+    gate = hm.MegaGate(hidden_size=H, num_experts=E, top_k=K, scoring_func="sigmoid", routed_scaling_factor=2.5,
+                       num_expert_groups=8, topk_groups=4).to(gpu)
+    with torch.no_grad():
+        gate.bias.copy_(torch.randn(E, generator=g) * 0.01)
+    gate = gate.to(torch.bfloat16)
+    assert gate.bias.dtype == torch.float32
+    x = torch.randn(2, T // 2, H, generator=g).to(torch.bfloat16)
+    logits, weights, ids = gate(x.to(gpu))
+    ref_logits = orc.gate_logits_reference(x, gate.weight.detach().cpu())
+    torch.testing.assert_close(logits.cpu(), ref_logits, rtol=1e-5, atol=2e-5)
+    w_ref, i_ref, _ = orc.route_c(logits.cpu().numpy(), gate.bias.detach().cpu().numpy(), top_k=K,
+                                  scoring_func="sigmoid", routed_scaling_factor=2.5, num_groups=8, topk_groups=4)
+    assert np.array_equal(ids.cpu().numpy(), i_ref)
+    assert np.array_equal(weights.cpu().numpy(), w_ref)
+    experts = hm.MegaMoeExperts(hidden_size=H, intermediate_size=I, num_experts=E, top_k=K)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16)
+    out = experts(x.to(gpu), ids, weights, expert_weights=(w1.to(gpu), w2.to(gpu)))
+    assert out.shape == x.shape and out.dtype == torch.bfloat16
+    ref = orc.expert_forward_reference(x.reshape(T, H), ids.cpu(), weights.cpu(), w1, w2)
+    assert orc.rel_l2(out.cpu().reshape(T, H), ref) < BF16_REL_L2
+    mx = hm.MegaMoeExperts(hidden_size=H, intermediate_size=I, num_experts=E, top_k=K, precision="mxfp8")
+    r1, r2 = hm.quantize_expert_weight(w1.to(gpu)), hm.quantize_expert_weight(w2.to(gpu))
+    out_mx = mx(x.to(gpu), ids, weights, expert_weights=(r1, r2))
+    ref_mx = orc.expert_forward_reference(x.reshape(T, H), ids.cpu(), weights.cpu(),
+                                          r1.col_data.cpu().view(torch.uint8), r2.col_data.cpu().view(torch.uint8),
+                                          precision="mxfp8", w1_scale=r1.col_scale.cpu(), w2_scale=r2.col_scale.cpu())
+    assert orc.rel_l2(out_mx.cpu().reshape(T, H), ref_mx) < MXFP8_REL_L2
+
+
+@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2])
+def test_grouped_gemm_mxfp8(gpu, counts):
+    from hyper_multicore_amd import ops
+    g = _seed(sum(counts) + 5)
+    G, Kd, N = len(counts), 512, 768
+    rows = sum(counts)
+    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
+    xq, xs = ops.mx_quantize_rows(x.to(gpu))
+    d, s = ops.mx_quantize_cols(w.to(gpu))
+    gl = torch.tensor(counts).cumsum(0).to(torch.int64)
+    out = ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), s, gl.to(gpu)).cpu()
+    xd = orc.mx_dequantize(xq.cpu(), xs.cpu(), dim=-1)
+    wd = orc.mx_dequantize_weight_cols(d.cpu().view(torch.uint8), s.cpu())
+    starts = [0, *gl.tolist()]
+    ref = torch.cat([xd[starts[i]:starts[i + 1]] @ wd[i] for i in range(G)]).to(torch.bfloat16)
+    assert orc.rel_l2(out, ref) < 5e-3
