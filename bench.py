@@ -1,0 +1,303 @@
+"""Benchmark of the MegaGate -> MegaMoE layer forward on one MI355X (synthetic data).
+
+One step = one full MoE layer forward over one batch: router projection (bf16 MFMA, fp32 out),
+route (scores, bias, group-limited top-k, renorm, scale), dispatch (histogram, scan, stable
+permutation), [MX activation quant], GMM1 + fused SwiGLU [+ MX requant], GMM2 and the combine.
+Inputs and weights are resident in HBM before the timed region.
+
+Prints ONE JSON line: tokens/s for the workload, the roofline of the dominant kernel (GMM1,
+timed with HIP events recorded by the library on its own stream), and a CPU baseline (the
+oracle's restatement of the reference CPU path, on a bounded token prefix). Other configs are
+reported under "extra" (``--extra none`` skips them).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config dsv3_bf16] [--extra all]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {"bf16": 2.5e15, "mxfp8": 5.0e15, "hbm": 8.0e12}
+
+# BASELINE.json configs (index in "configs")
+CONFIGS = {
+    "small_bf16": dict(idx=0, T=1024, E=8, K=2, H=1024, I=512, scoring="softmax", groups=1, topk_groups=1,
+                       scale=1.0, precision="bf16", wstd=0.02, zipf=None, multimodal=False),
+    "dsv3_bf16": dict(idx=1, T=8192, E=256, K=8, H=7168, I=2048, scoring="sigmoid", groups=8, topk_groups=4,
+                      scale=2.5, precision="bf16", wstd=0.006, zipf=None, multimodal=False),
+    "dsv3_mxfp8": dict(idx=2, T=8192, E=256, K=8, H=7168, I=2048, scoring="sigmoid", groups=8, topk_groups=4,
+                       scale=2.5, precision="mxfp8", wstd=0.006, zipf=None, multimodal=False),
+    "dsv3_decode_mxfp8": dict(idx=3, T=128, E=256, K=8, H=7168, I=2048, scoring="sigmoid", groups=8,
+                              topk_groups=4, scale=2.5, precision="mxfp8", wstd=0.006, zipf=1.1, multimodal=False),
+    "multimodal_bf16": dict(idx=4, T=16384, E=128, K=8, H=4096, I=1536, scoring="softmax", groups=1,
+                            topk_groups=1, scale=1.0, precision="bf16", wstd=0.02, zipf=None, multimodal=True),
+}
+SEED = 1234
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Layer:
+    """Synthetic inputs + weights of one config, resident on the GPU."""
+
+    def __init__(self, name: str, device: torch.device):
+        from hyper_multicore_amd import ops
+        self.ops = ops
+        self.name = name
+        c = self.c = CONFIGS[name]
+        g = torch.Generator(device=device).manual_seed(SEED + c["idx"])
+        T, E, H, I = c["T"], c["E"], c["H"], c["I"]
+        self.x = torch.randn(T, H, device=device, generator=g).to(torch.bfloat16)
+        self.wr = (torch.randn(E, H, device=device, generator=g) * 0.02).to(torch.bfloat16)
+        self.bias = torch.zeros(E, device=device)
+        self.wr_vl = None
+        self.mask = None
+        self.skew = None
+        if c["multimodal"]:
+            self.mask = torch.rand(T, device=device, generator=g) < 0.5
+            self.x[self.mask] = (self.x[self.mask].float() * 0.5).to(torch.bfloat16)
+            self.wr_vl = (torch.randn(E, H, device=device, generator=g) * 0.02).to(torch.bfloat16)
+        else:
+            self.bias = torch.randn(E, device=device, generator=g) * 0.01
+        if c["zipf"] is not None:
+            # Expert popularity ~ Zipf(s): a seeded rank per expert, and Gumbel-top-k logits
+            # log p_e + G_te dominate the router logits, so top-k samples experts without
+            # replacement in proportion to p_e (sigmoid is monotone).
+            rank = torch.randperm(E, device=device, generator=g).float() + 1.0
+            logp = -c["zipf"] * torch.log(rank)
+            u = torch.rand(T, E, device=device, generator=g).clamp_(1e-9, 1 - 1e-9)
+            self.skew = 8.0 * (logp - torch.log(-torch.log(u)))
+        w1 = torch.randn(E, 2 * I, H, device=device, generator=g).mul_(c["wstd"]).to(torch.bfloat16)  # EOI
+        w2 = torch.randn(E, H, I, device=device, generator=g).mul_(c["wstd"]).to(torch.bfloat16)      # EOI
+        if c["precision"] == "bf16":
+            self.w1, self.w2, self.s1, self.s2, self.layout = w1, w2, None, None, "EOI"
+        else:
+            d1, s1 = ops.mx_quantize_cols(w1.transpose(1, 2).contiguous())  # EIO [E, H, 2I]
+            del w1
+            d2, s2 = ops.mx_quantize_cols(w2.transpose(1, 2).contiguous())  # EIO [E, I, H]
+            del w2
+            self.w1, self.w2, self.s1, self.s2, self.layout = d1.view(torch.uint8), d2.view(torch.uint8), s1, s2, "EIO"
+        torch.cuda.synchronize()
+        self.out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
+
+    def step(self, stage_events=None):
+        c, ops = self.c, self.ops
+        logits = ops.gate_logits(self.x, self.wr, self.wr_vl, self.mask if self.wr_vl is not None else None)
+        if self.skew is not None:
+            logits = logits + self.skew
+        weights, ids = ops.gate_route(logits, self.bias, top_k=c["K"], scoring_func=c["scoring"],
+                                      routed_scaling_factor=c["scale"], num_groups=c["groups"],
+                                      topk_groups=c["topk_groups"])
+        ops.moe_forward(self.x, ids, weights, self.w1, self.w2, num_experts=c["E"], intermediate_size=c["I"],
+                        precision=c["precision"], layout=self.layout, w1_scale=self.s1, w2_scale=self.s2,
+                        out=self.out, stage_events=stage_events)
+        return ids
+
+    def counts(self):
+        ids = self.step()
+        torch.cuda.synchronize()
+        return torch.bincount(ids.reshape(-1), minlength=self.c["E"]).cpu()
+
+
+def gmm_work(c: dict, counts: torch.Tensor) -> dict:
+    """Algorithmic FLOPs and bytes of GMM1 (the dominant kernel) and of the whole layer."""
+    T, E, K, H, I = c["T"], c["E"], c["K"], c["H"], c["I"]
+    R = T * K
+    active = int((counts > 0).sum())
+    mx = c["precision"] == "mxfp8"
+    wbytes = 1.0 + 1.0 / 32 if mx else 2.0        # weight bytes per element (e4m3 + e8m0 / 32)
+    abytes = 1.0 + 1.0 / 32 if mx else 2.0
+    g1_flops = 2.0 * R * H * 2 * I
+    g1_bytes = active * H * 2 * I * wbytes + T * H * abytes + R * I * abytes
+    layer_flops = 6.0 * R * H * I + 2.0 * T * H * E
+    layer_bytes = (active * 3 * H * I * wbytes + T * H * 2 * 2 + E * H * 2 + T * K * 16)
+    return dict(active=active, g1_flops=g1_flops, g1_bytes=g1_bytes, layer_flops=layer_flops,
+                layer_bytes=layer_bytes)
+
+
+def measure(layer: Layer, steps: int, warmup: int) -> dict:
+    for _ in range(warmup):
+        layer.step()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for s in range(steps):
+        layer.step(stage_events=ev[s])
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
+    stage = {"dispatch": [], "gmm1": [], "gmm2": [], "combine": []}
+    for e in ev:
+        stage["dispatch"].append(e[0].elapsed_time(e[1]))
+        stage["gmm1"].append(e[1].elapsed_time(e[2]))
+        stage["gmm2"].append(e[2].elapsed_time(e[3]))
+        stage["combine"].append(e[3].elapsed_time(e[4]))
+    avg = {k: sum(v) / len(v) for k, v in stage.items()}
+    return dict(ms_per_step=total_ms / steps, wall_s=wall, stage_ms=avg)
+
+
+def roofline(c: dict, work: dict, gmm1_ms: float) -> dict:
+    mx = c["precision"] == "mxfp8"
+    peak_flops = PEAK["mxfp8" if mx else "bf16"]
+    t_mfma = work["g1_flops"] / peak_flops
+    t_hbm = work["g1_bytes"] / PEAK["hbm"]
+    sec = gmm1_ms * 1e-3
+    if t_hbm > t_mfma:
+        achieved = work["g1_bytes"] / sec / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm"] / 1e9, "unit": "GB/s",
+                "frac": round(achieved / (PEAK["hbm"] / 1e9), 4), "traffic": None,
+                "kernel": "grouped_gemm GMM1+SwiGLU", "mfma_frac": round(work["g1_flops"] / sec / peak_flops, 4)}
+    achieved = work["g1_flops"] / sec / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak_flops / 1e12, "unit": "TFLOP/s",
+            "frac": round(achieved / (peak_flops / 1e12), 4), "traffic": None, "kernel": "grouped_gemm GMM1+SwiGLU",
+            "hbm_frac": round(work["g1_bytes"] / sec / PEAK["hbm"], 4)}
+
+
+def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
+    """The oracle's restatement of the reference CPU path (MegaGate._torch_forward + the
+    TorchExperts CPU loop, bf16 F.linear) on a prefix of the same synthetic batch."""
+    from oracle import moe_oracle as orc
+    c = layer.c
+    threads = torch.get_num_threads()
+    T = c["T"]
+    sample = min(T, 1024 if c["H"] <= 1024 else 256)
+    x = layer.x[:sample].cpu()
+    wr = layer.wr.cpu()
+    bias = layer.bias.cpu()
+    if c["precision"] == "bf16":
+        w1 = layer.w1.cpu()   # EOI [E, 2I, H]
+        w2 = layer.w2.cpu()   # EOI [E, H, I]
+    else:
+        w1 = orc.mx_dequantize_weight_cols(layer.w1.cpu(), layer.s1.cpu()).to(torch.bfloat16).transpose(1, 2).contiguous()
+        w2 = orc.mx_dequantize_weight_cols(layer.w2.cpu(), layer.s2.cpu()).to(torch.bfloat16).transpose(1, 2).contiguous()
+    I = c["I"]
+    gate_w, up_w = w1[:, :I], w1[:, I:]
+    mask = layer.mask[:sample].cpu() if layer.mask is not None else None
+    wvl = layer.wr_vl.cpu() if layer.wr_vl is not None else None
+    skew = layer.skew[:sample].cpu() if layer.skew is not None else None
+
+    def run():
+        logits = orc.gate_logits_reference(x, wr, wvl, mask)
+        if skew is not None:
+            logits = logits + skew
+        w, ids, _ = orc.route_reference(logits, bias, top_k=c["K"], scoring_func=c["scoring"],
+                                        routed_scaling_factor=c["scale"], num_groups=c["groups"],
+                                        topk_groups=c["topk_groups"])
+        return orc.torch_experts_reference(x, ids, w, gate_w, up_w, w2)
+
+    run()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(sample / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"first {sample} of {T} tokens of the {name} batch, median of {len(times)} after 1 warm-up; "
+                      f"torch CPU {torch.__version__}, os.cpu_count()={os.cpu_count()}, cpu={platform.processor() or platform.machine()}"}
+
+
+def run_config(name: str, device, steps: int, warmup: int) -> dict:
+    layer = Layer(name, device)
+    counts = layer.counts()
+    work = gmm_work(layer.c, counts)
+    m = measure(layer, steps, warmup)
+    c = layer.c
+    ms = m["ms_per_step"]
+    res = {
+        "tokens_per_s": round(c["T"] / (ms * 1e-3), 1),
+        "ms_per_step": round(ms, 4),
+        "layer_tflops": round(work["layer_flops"] / (ms * 1e-3) / 1e12, 1),
+        "layer_mfma_frac": round(work["layer_flops"] / (ms * 1e-3) / PEAK[c["precision"]], 4),
+        "layer_hbm_frac": round(work["layer_bytes"] / (ms * 1e-3) / PEAK["hbm"], 4),
+        "active_experts": work["active"],
+        "stage_ms": {k: round(v, 4) for k, v in m["stage_ms"].items()},
+        "roofline": roofline(c, work, m["stage_ms"]["gmm1"]),
+    }
+    return res, layer
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="dsv3_bf16", choices=sorted(CONFIGS))
+    ap.add_argument("--extra", default="all", help="'all', 'none' or comma list of extra configs")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X only: this build runs every expert on one GPU (EP=1) and has no "
+              "multi-GPU path; run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    from hyper_multicore_amd import _lib
+    _lib.load()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    log(f"[bench] workload {args.config}: steps={args.steps} warmup={args.warmup}")
+    res, layer = run_config(args.config, device, args.steps, args.warmup)
+    c = layer.c
+    cpu = None if args.no_cpu else cpu_baseline(args.config, layer)
+    del layer
+    torch.cuda.empty_cache()
+    extra = {}
+    names = [] if args.extra == "none" else (sorted(CONFIGS) if args.extra == "all" else args.extra.split(","))
+    for name in names:
+        if name == args.config:
+            continue
+        log(f"[bench] extra {name}")
+        r, lyr = run_config(name, device, max(5, args.steps // 2), max(2, args.warmup // 2))
+        extra[name] = r
+        del lyr
+        torch.cuda.empty_cache()
+    line = {
+        "metric": "MoE layer tokens/s + achieved TFLOP/s (% MFMA peak), DSv3 shape, 1 MI355X",
+        "value": res["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if c["precision"] == "bf16" else "mxfp8(e4m3+e8m0/32)",
+        "data": "synthetic (seeded normal activations / random-init weights of the config's shapes)",
+        "config": {"workload": args.config, "baseline_config_index": c["idx"], "tokens": c["T"], "experts": c["E"],
+                   "top_k": c["K"], "hidden": c["H"], "intermediate": c["I"], "router": c["scoring"],
+                   "groups": f"{c['groups']}/{c['topk_groups']}", "parallelism": "ep1"},
+        "layer_tflops": res["layer_tflops"],
+        "layer_mfma_frac": res["layer_mfma_frac"],
+        "active_experts": res["active_experts"],
+        "stage_ms": res["stage_ms"],
+        "roofline": res["roofline"],
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

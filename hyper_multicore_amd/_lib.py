@@ -55,6 +55,7 @@ class ForwardArgs(Structure):
         ("topk_weights", c_void_p), ("weight_layout", c_int32), ("reserved0", c_int32),
         ("w1", c_void_p), ("w2", c_void_p), ("w1_scale", c_void_p), ("w2_scale", c_void_p),
         ("tokens_per_expert", c_void_p), ("out", c_void_p), ("error_flag", c_void_p),
+        ("stage_events", POINTER(c_void_p)), ("num_stage_events", c_int32), ("reserved1", c_int32),
     ]
 
 

@@ -221,7 +221,13 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   if (a.num_tokens == 0) return MI355MOE_OK;
   FwdLayout L = fwd_layout(a);
   if (workspace == nullptr || workspace_size < L.total) return -4;
+  if (a.num_stage_events < 0 || a.num_stage_events > 5 || (a.num_stage_events > 0 && a.stage_events == nullptr))
+    return MI355MOE_EINVAL;
   hipStream_t st = (hipStream_t)stream;
+  auto mark = [&](int i) {
+    if (i < a.num_stage_events && a.stage_events[i] != nullptr) hipEventRecord((hipEvent_t)a.stage_events[i], st);
+  };
+  mark(0);
   char* ws = (char*)workspace;
   const int64_t T = a.num_tokens;
   const int K = a.top_k, E = a.num_experts, H = a.hidden_size, I = a.intermediate_size;
@@ -244,6 +250,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
     if (rc) return rc;
     a1 = (const uint8_t*)(ws + L.xq);
   }
+  mark(1);
   const int esize = mx ? 1 : 2;
   // GMM1: [R, H] x [H, 2I] -> SwiGLU -> act [R, I]
   GGParams p1 = {};
@@ -269,6 +276,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.c_scale = mx ? (uint8_t*)(ws + L.act_scale) : nullptr;
   rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st);
   if (rc) return rc;
+  mark(2);
   // GMM2: [R, I] x [I, H] -> y [R, H] bf16
   GGParams p2 = {};
   p2.A = (const uint8_t*)(ws + L.act);
@@ -291,5 +299,8 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p2.ldc = H;
   rc = mi355_grouped_gemm(p2, mx, !eoi, EPI_STORE_BF16, st);
   if (rc) return rc;
-  return mi355_unpermute_enqueue((const uint16_t*)(ws + L.y), mapping, a.topk_weights, T, K, H, a.out, st);
+  mark(3);
+  rc = mi355_unpermute_enqueue((const uint16_t*)(ws + L.y), mapping, a.topk_weights, T, K, H, a.out, st);
+  mark(4);
+  return rc;
 }

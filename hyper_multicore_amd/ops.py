@@ -301,8 +301,12 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
                 w2: torch.Tensor, *, num_experts: int, intermediate_size: int, precision: str = "bf16",
                 layout: str = "EIO", w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
                 tokens_per_expert: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                error_flag: torch.Tensor | None = None) -> torch.Tensor:
-    """Expert forward at EP=1 through ``mi355moe_moe_forward``; returns bf16 [T, H]."""
+                error_flag: torch.Tensor | None = None, stage_events=None) -> torch.Tensor:
+    """Expert forward at EP=1 through ``mi355moe_moe_forward``; returns bf16 [T, H].
+
+    ``stage_events``: optional list of up to 5 ``torch.cuda.Event(enable_timing=True)`` recorded
+    at the stage boundaries (start, after dispatch, after GMM1, after GMM2, after combine).
+    """
     lib = _lib.load()
     device = _require_gpu(hidden, topk_ids, topk_weights, w1, w2, w1_scale, w2_scale, tokens_per_expert)
     if hidden.dtype != torch.bfloat16 or hidden.ndim != 2:
@@ -320,6 +324,15 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
         precision=_lib.PRECISION[precision], topk_weights=_ptr(probs), weight_layout=_lib.LAYOUT[layout],
         reserved0=0, w1=_ptr(w1), w2=_ptr(w2), w1_scale=_ptr(w1_scale), w2_scale=_ptr(w2_scale),
         tokens_per_expert=_ptr(tokens_per_expert), out=_ptr(out), error_flag=_ptr(error_flag))
+    if stage_events:
+        handles = []
+        for ev in stage_events:
+            if ev.cuda_event == 0:  # events are created lazily on first record
+                ev.record()
+            handles.append(ev.cuda_event)
+        arr = (ctypes.c_void_p * len(handles))(*handles)
+        args.stage_events = ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p))
+        args.num_stage_events = len(handles)
     need = lib.mi355moe_moe_forward_workspace_size(ctypes.byref(args))
     if need == 0 and T > 0:
         _lib.check(lib.mi355moe_moe_forward(ctypes.byref(args), None, 0, _stream(device)), "mi355moe_moe_forward")

@@ -218,6 +218,12 @@ typedef struct MI355MoeForwardArgs {
   const int32_t* tokens_per_expert; /* optional [E] int32 */
   uint16_t* out;              /* [T, H] bf16 */
   int32_t* error_flag;        /* optional: set to 1 for ids outside [0, E) */
+  /* Optional timing hooks (no reference counterpart): hipEvent_t handles recorded on `stream`
+   * at the stage boundaries [0] start, [1] after dispatch + MX activation quant, [2] after GMM1,
+   * [3] after GMM2, [4] after combine. num_stage_events may be 0..5. */
+  void* const* stage_events;
+  int32_t num_stage_events;
+  int32_t reserved1;
 } MI355MoeForwardArgs;
 size_t mi355moe_moe_forward_workspace_size(const MI355MoeForwardArgs* args);
 int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* workspace, size_t workspace_size,
