@@ -41,7 +41,10 @@ struct GGLds {
   static constexpr int AS_BYTES = GG_BM * 4;           // 512 B
   static constexpr int BS_BYTES = 2 * GG_BN * 2;       // 1 KB
   static constexpr int STAGE = A_BYTES + B_BYTES + AS_BYTES + BS_BYTES;
-  static constexpr int TOTAL = 2 * STAGE;
+  static constexpr int NSTAGE = 3;
+  static constexpr int PREFIX_MAX = 1024;              // groups whose tile prefix is kept in LDS
+  static constexpr int PREFIX_OFF = NSTAGE * STAGE;
+  static constexpr int TOTAL = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
 };
 
 MI355_DEV void lds_load16(const void* g, uint32_t lds_off_uniform, uint8_t* smem) {
@@ -50,7 +53,21 @@ MI355_DEV void lds_load16(const void* g, uint32_t lds_off_uniform, uint8_t* smem
 MI355_DEV void lds_load4(const void* g, uint32_t lds_off_uniform, uint8_t* smem) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(smem + lds_off_uniform), 4, 0, 0);
 }
-MI355_DEV void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector-memory loads of this wave are outstanding (loads retire in order).
+// Workgroup barrier without the release fence of __syncthreads (which would wait for every
+// outstanding global load, including the prefetched stages): LDS reads of this wave are drained,
+// the direct-to-LDS loads are ordered by the explicit vmcnt waits.
+MI355_DEV void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+}
+template <int N>
+MI355_DEV void wait_vm_le() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else if constexpr (N == 13) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");
+  else static_assert(N == 0, "unsupported vmcnt");
+}
 
 // Tile column j (0..255) -> weight column. SwiGLU: per 128-column half h, 64 gate then 64 up.
 MI355_DEV int tile_col_to_weight_col(int j, int nt, int I, bool swiglu) {
@@ -60,10 +77,174 @@ MI355_DEV int tile_col_to_weight_col(int j, int nt, int I, bool swiglu) {
   return jj < 64 ? base + jj : I + base + (jj - 64);
 }
 
+struct FragBF16 {
+  v8bf a[2];
+  v8bf b[4];
+};
+struct FragMX {
+  v8i a[2];
+  v8i b[4];
+  int sa[2];
+  int sb[4];
+};
+
+template <bool B_KN>
+MI355_DEV void load_frag_bf16(const uint8_t* As, const uint8_t* Bs, int ks, int wm, int wn, int lane, FragBF16& f) {
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    int r = wm * 64 + mi * 32 + (lane & 31);
+    int c = (ks * 2 + (lane >> 5)) ^ ((r >> 1) & 7);
+    f.a[mi] = *(const v8bf*)(As + r * 128 + c * 16);
+  }
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    if (!B_KN) {
+      int n = wn * 128 + ni * 32 + (lane & 31);
+      int c = (ks * 2 + (lane >> 5)) ^ ((n >> 1) & 7);
+      f.b[ni] = *(const v8bf*)(Bs + n * 128 + c * 16);
+    } else {
+      int g16 = lane >> 4, m = lane & 15;
+      int nb = wn * 128 + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
+      int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2);
+      int k1 = k0 + 4;
+      int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
+      int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
+      v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off0));
+      v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
+      typedef __attribute__((ext_vector_type(8))) short v8s;
+      v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      f.b[ni] = __builtin_bit_cast(v8bf, both);
+    }
+  }
+}
+
+// Scaled-MFMA operand order: lane r + 32g holds bytes 0-15 = K 16g + i and bytes 16-31 =
+// K 32 + 16g + i of the 64-K step, and supplies the e8m0 scale of 32-block g.
+MI355_DEV void load_frag_mx(const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs, const uint8_t* BSs, int ks,
+                            int wm, int wn, int lane, FragMX& f) {
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    int r = wm * 64 + mi * 32 + (lane & 31);
+    int c0 = ks * 4 + (lane >> 5);
+    v4i lo = *(const v4i*)(As + r * 128 + ((c0 ^ ((r >> 1) & 7)) << 4));
+    v4i hi = *(const v4i*)(As + r * 128 + (((c0 + 2) ^ ((r >> 1) & 7)) << 4));
+    f.a[mi] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    f.sa[mi] = ASs[r * 4 + ks * 2 + (lane >> 5)];
+  }
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    int g16 = lane >> 4, m = lane & 15;
+    int nb = wn * 128 + ni * 32 + (g16 & 1) * 16;
+    int parts[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      int k = ks * 64 + (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
+      int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
+      v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
+      parts[2 * q] = v[0];
+      parts[2 * q + 1] = v[1];
+    }
+    f.b[ni] = (v8i){parts[0], parts[1], parts[2], parts[3], parts[4], parts[5], parts[6], parts[7]};
+    int n = wn * 128 + ni * 32 + (lane & 31);
+    f.sb[ni] = BSs[ks * 512 + n * 2 + (lane >> 5)];
+  }
+}
+
+template <int NM>
+MI355_DEV void mfma_bf16(v16f (&acc)[2][4], const FragBF16& f) {
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+      acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
+}
+template <int NM>
+MI355_DEV void mfma_mx(v16f (&acc)[2][4], const FragMX& f) {
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+      acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0, f.sa[mi],
+                                                                     0, f.sb[ni]);
+}
+
+// Per-thread copy plan of one work item (global sources of this thread's 16-byte chunks).
+struct CopyPlan {
+  const uint8_t* a[4];
+  const uint8_t* b[8];
+  const uint8_t* s[2];
+};
+
+template <bool MX, bool B_KN>
+MI355_DEV void issue_stage(const GGParams& p, const CopyPlan& cp, int kt, int stage, int wave, uint8_t* smem) {
+  constexpr int ESIZE = MX ? 1 : 2;
+  const uint32_t base = stage * GGLds::STAGE;
+  const int64_t koff = (int64_t)kt * GG_KB;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lds_load16(cp.a[j] + koff, base + (wave * 4 + j) * 1024, smem);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint8_t* src = B_KN ? cp.b[j] + (int64_t)kt * (GG_KB / ESIZE) * p.b_row_bytes : cp.b[j] + koff;
+    lds_load16(src, base + GGLds::A_BYTES + (wave * 8 + j) * 1024, smem);
+  }
+  if (MX) {
+    if (wave < 2) {
+      lds_load4(cp.s[0] + kt * 4, base + GGLds::A_BYTES + GGLds::B_BYTES + wave * 256, smem);
+    } else {
+      const int64_t ks = (int64_t)kt * 2 * p.Ntot * 2;  // two 64-K groups per stage
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        lds_load4(cp.s[h] + ks, base + GGLds::A_BYTES + GGLds::B_BYTES + GGLds::AS_BYTES + (wave - 2) * 512 + h * 256,
+                  smem);
+    }
+  }
+}
+
+// K loop over a 3-stage LDS ring; NM = number of valid 32-row subtiles this wave computes.
+template <bool MX, bool B_KN, int NM>
+MI355_DEV void k_loop(const GGParams& p, const CopyPlan& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
+                      v16f (&acc)[2][4]) {
+  constexpr int LOADS = MX ? 13 : 12;  // minimum loads per wave per stage
+  issue_stage<MX, B_KN>(p, cp, 0, 0, wave, smem);
+  if (nk > 1) issue_stage<MX, B_KN>(p, cp, 1, 1, wave, smem);
+  int stage = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) wait_vm_le<LOADS>(); else wait_vm_le<0>();
+    lds_barrier();
+    if (kt + 2 < nk) {
+      int s2 = stage + 2;
+      if (s2 >= 3) s2 -= 3;
+      issue_stage<MX, B_KN>(p, cp, kt + 2, s2, wave, smem);
+    }
+    const uint8_t* As = smem + stage * GGLds::STAGE;
+    const uint8_t* Bs = As + GGLds::A_BYTES;
+    if constexpr (NM > 0) {
+      if constexpr (!MX) {
+        FragBF16 f[2];
+        load_frag_bf16<B_KN>(As, Bs, 0, wm, wn, lane, f[0]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          if (ks + 1 < 4) load_frag_bf16<B_KN>(As, Bs, ks + 1, wm, wn, lane, f[(ks + 1) & 1]);
+          mfma_bf16<NM>(acc, f[ks & 1]);
+        }
+      } else {
+        const uint8_t* ASs = Bs + GGLds::B_BYTES;
+        const uint8_t* BSs = ASs + GGLds::AS_BYTES;
+        FragMX f[2];
+        load_frag_mx(As, Bs, ASs, BSs, 0, wm, wn, lane, f[0]);
+        load_frag_mx(As, Bs, ASs, BSs, 1, wm, wn, lane, f[1]);
+        mfma_mx<NM>(acc, f[0]);
+        mfma_mx<NM>(acc, f[1]);
+      }
+    }
+    stage = stage == 2 ? 0 : stage + 1;
+  }
+}
+
 template <bool MX, bool B_KN, int EPI>
 __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  __shared__ int32_t s_prefix[4097];
+  int32_t* s_prefix = (int32_t*)(smem + GGLds::PREFIX_OFF);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -71,9 +252,12 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
   constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX);
   constexpr int ESIZE = MX ? 1 : 2;
 
-  for (int g = tid; g <= p.G; g += GG_THREADS) s_prefix[g] = p.tile_prefix[g];
+  const bool prefix_in_lds = p.G <= GGLds::PREFIX_MAX;
+  const int32_t* prefix = prefix_in_lds ? s_prefix : p.tile_prefix;
+  if (prefix_in_lds)
+    for (int g = tid; g <= p.G; g += GG_THREADS) s_prefix[g] = p.tile_prefix[g];
   __syncthreads();
-  const int total = s_prefix[p.G] * p.n_tiles;
+  const int total = prefix[p.G] * p.n_tiles;
   const int nk = p.K * ESIZE / GG_KB;
   const int xcd = blockIdx.x & 7;
   const int per_xcd = gridDim.x >> 3;
@@ -84,13 +268,13 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     if (L >= total) break;
     // ---- decode work item -------------------------------------------------------------
     int lo = 0, hi = p.G - 1;
-    while (lo < hi) {  // largest g with s_prefix[g]*n_tiles <= L
+    while (lo < hi) {  // largest g with prefix[g]*n_tiles <= L
       int mid = (lo + hi + 1) >> 1;
-      if (s_prefix[mid] * p.n_tiles <= L) lo = mid; else hi = mid - 1;
+      if (prefix[mid] * p.n_tiles <= L) lo = mid; else hi = mid - 1;
     }
     const int g = lo;
-    const int mtiles = s_prefix[g + 1] - s_prefix[g];
-    const int local = L - s_prefix[g] * p.n_tiles;
+    const int mtiles = prefix[g + 1] - prefix[g];
+    const int local = L - prefix[g] * p.n_tiles;
     const int nt = local / mtiles;
     const int mt = local - nt * mtiles;
     const int64_t row_begin = (g == 0 ? 0 : p.group_list[g - 1]);
@@ -99,8 +283,7 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     const int rows_valid = (int)((row_end - tile_row0) < GG_BM ? (row_end - tile_row0) : GG_BM);
 
     // ---- per-thread copy sources ------------------------------------------------------
-    // A: 16 KB per stage = 1024 chunks; thread handles chunk ids wave*256 + j*64 + lane, j<4.
-    const uint8_t* a_src[4];
+    CopyPlan cp;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       int L16 = wave * 256 + j * 64 + lane;
@@ -109,10 +292,9 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
       int rr = r < rows_valid ? r : rows_valid - 1;
       int64_t routed = tile_row0 + rr;
       int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
-      a_src[j] = p.A + src * p.lda_bytes + c * 16;
+      cp.a[j] = p.A + src * p.lda_bytes + c * 16;
     }
     const uint8_t* bgrp = p.B + (int64_t)g * p.b_group_stride;
-    const uint8_t* b_src[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       int L16 = wave * 512 + j * 64 + lane;
@@ -121,31 +303,31 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
         int c = cs ^ ((r >> 1) & 7);
         int wc = tile_col_to_weight_col(r, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 1;
-        b_src[j] = bgrp + (int64_t)wc * p.b_row_bytes + c * 16;
+        cp.b[j] = bgrp + (int64_t)wc * p.b_row_bytes + c * 16;
       } else if (MX) {
         int k = L16 >> 4, cs = L16 & 15;
         int c = cs ^ (k & 15);
         int wc = tile_col_to_weight_col(c * 16, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 16;
-        b_src[j] = bgrp + (int64_t)k * p.b_row_bytes + wc;
+        cp.b[j] = bgrp + (int64_t)k * p.b_row_bytes + wc;
       } else {
         int k = L16 >> 5, cs = L16 & 31;
         int c = cs ^ ((k & 7) << 1);
         int wc = tile_col_to_weight_col(c * 8, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 8;
-        b_src[j] = bgrp + (int64_t)k * p.b_row_bytes + (int64_t)wc * 2;
+        cp.b[j] = bgrp + (int64_t)k * p.b_row_bytes + (int64_t)wc * 2;
       }
     }
     // MX scales: waves 0/1 copy A scale dwords (rows 0..63 / 64..127), waves 2/3 copy the two
     // 64-K groups of B scales (256 columns x 2 bytes = 128 dwords = 2 instructions each).
-    const uint8_t* s_src[2] = {nullptr, nullptr};
+    cp.s[0] = cp.s[1] = nullptr;
     if (MX) {
       if (wave < 2) {
         int r = wave * 64 + lane;
         int rr = r < rows_valid ? r : rows_valid - 1;
         int64_t routed = tile_row0 + rr;
         int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
-        s_src[0] = p.a_scale + src * (p.K / 32);
+        cp.s[0] = p.a_scale + src * (p.K / 32);
       } else {
         int gi = wave - 2;
 #pragma unroll
@@ -153,33 +335,10 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
           int j = (h * 64 + lane) * 2;  // tile column pair (j, j+1)
           int wc = tile_col_to_weight_col(j, nt, p.N, SWIGLU);
           if (wc >= p.Ntot) wc = p.Ntot - 2;
-          s_src[h] = p.b_scale + (int64_t)g * p.b_scale_group_stride + ((int64_t)gi * p.Ntot + wc) * 2;
+          cp.s[h] = p.b_scale + (int64_t)g * p.b_scale_group_stride + ((int64_t)gi * p.Ntot + wc) * 2;
         }
       }
     }
-
-    auto issue_stage = [&](int kt, int stage) {
-      const uint32_t base = stage * GGLds::STAGE;
-      const int64_t koff = (int64_t)kt * GG_KB;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lds_load16(a_src[j] + koff, base + (wave * 4 + j) * 1024, smem);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint8_t* src = B_KN ? b_src[j] + (int64_t)kt * (GG_KB / ESIZE) * p.b_row_bytes : b_src[j] + koff;
-        lds_load16(src, base + GGLds::A_BYTES + (wave * 8 + j) * 1024, smem);
-      }
-      if (MX) {
-        if (wave < 2) {
-          lds_load4(s_src[0] + kt * 4, base + GGLds::A_BYTES + GGLds::B_BYTES + wave * 256, smem);
-        } else {
-          const int64_t ks = (int64_t)kt * 2 * p.Ntot * 2;  // two 64-K groups per stage
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            lds_load4(s_src[h] + ks, base + GGLds::A_BYTES + GGLds::B_BYTES + GGLds::AS_BYTES +
-                                         (wave - 2) * 512 + h * 256, smem);
-        }
-      }
-    };
 
     v16f acc[2][4];
 #pragma unroll
@@ -189,107 +348,12 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const bool mi_on[2] = {wm * 64 < rows_valid, wm * 64 + 32 < rows_valid};
-
-    issue_stage(0, 0);
-    wait_vm();
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int stage = kt & 1;
-      if (kt + 1 < nk) issue_stage(kt + 1, stage ^ 1);
-      const uint8_t* As = smem + stage * GGLds::STAGE;
-      const uint8_t* Bs = As + GGLds::A_BYTES;
-      if (!MX) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          v8bf af[2], bfr[4];
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-            int r = wm * 64 + mi * 32 + (lane & 31);
-            int c = (ks * 2 + (lane >> 5)) ^ ((r >> 1) & 7);
-            af[mi] = *(const v8bf*)(As + r * 128 + c * 16);
-          }
-#pragma unroll
-          for (int ni = 0; ni < 4; ++ni) {
-            if (!B_KN) {
-              int n = wn * 128 + ni * 32 + (lane & 31);
-              int c = (ks * 2 + (lane >> 5)) ^ ((n >> 1) & 7);
-              bfr[ni] = *(const v8bf*)(Bs + n * 128 + c * 16);
-            } else {
-              int g16 = lane >> 4, m = lane & 15;
-              int nb = wn * 128 + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
-              v4s lo, hi;
-              {
-                int k = ks * 16 + (g16 >> 1) * 8 + (m >> 2);
-                int off = k * 512 + (((nb >> 3) ^ ((k & 7) << 1)) << 4) + (nb & 7) * 2;
-                lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off));
-              }
-              {
-                int k = ks * 16 + (g16 >> 1) * 8 + 4 + (m >> 2);
-                int off = k * 512 + (((nb >> 3) ^ ((k & 7) << 1)) << 4) + (nb & 7) * 2;
-                hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off));
-              }
-              typedef __attribute__((ext_vector_type(8))) short v8s;
-              v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-              bfr[ni] = __builtin_bit_cast(v8bf, both);
-            }
-          }
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-            if (!mi_on[mi]) continue;
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni)
-              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
-          }
-        }
-      } else {
-        const uint8_t* ASs = Bs + GGLds::B_BYTES;
-        const uint8_t* BSs = ASs + GGLds::AS_BYTES;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          v8i af[2], bfr[4];
-          int sa[2], sb[4];
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-            int r = wm * 64 + mi * 32 + (lane & 31);
-            // scaled-MFMA K order: bytes 0-15 hold K = 16g + i, bytes 16-31 hold K = 32 + 16g + i
-            // (g = lane / 32), so the e8m0 block g of this 64-K step spans both lane halves.
-            int c0 = ks * 4 + (lane >> 5);
-            v4i lo = *(const v4i*)(As + r * 128 + ((c0 ^ ((r >> 1) & 7)) << 4));
-            v4i hi = *(const v4i*)(As + r * 128 + (((c0 + 2) ^ ((r >> 1) & 7)) << 4));
-            af[mi] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            sa[mi] = ASs[r * 4 + ks * 2 + (lane >> 5)];
-          }
-#pragma unroll
-          for (int ni = 0; ni < 4; ++ni) {
-            int g16 = lane >> 4, m = lane & 15;
-            int nb = wn * 128 + ni * 32 + (g16 & 1) * 16;
-            int parts[8];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              int k = ks * 64 + (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
-              int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
-              v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
-              parts[2 * q] = v[0];
-              parts[2 * q + 1] = v[1];
-            }
-            bfr[ni] = (v8i){parts[0], parts[1], parts[2], parts[3], parts[4], parts[5], parts[6], parts[7]};
-            int n = wn * 128 + ni * 32 + (lane & 31);
-            sb[ni] = BSs[ks * 512 + n * 2 + (lane >> 5)];
-          }
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-            if (!mi_on[mi]) continue;
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni)
-              acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0,
-                                                                             sa[mi], 0, sb[ni]);
-          }
-        }
-      }
-      wait_vm();
-      __syncthreads();
-    }
+    __syncthreads();  // the previous item's last stage / epilogue reads are done before refilling
+    const int nm = wm * 64 + 32 < rows_valid ? 2 : (wm * 64 < rows_valid ? 1 : 0);
+    if (nm == 2) k_loop<MX, B_KN, 2>(p, cp, nk, wave, wm, wn, lane, smem, acc);
+    else if (nm == 1) k_loop<MX, B_KN, 1>(p, cp, nk, wave, wm, wn, lane, smem, acc);
+    else k_loop<MX, B_KN, 0>(p, cp, nk, wave, wm, wn, lane, smem, acc);
+    __syncthreads();  // all waves are done reading the ring before the epilogue reuses LDS
 
     // ---- epilogue -----------------------------------------------------------------------
     if (EPI == EPI_STORE_F32) {

@@ -1,0 +1,91 @@
+"""Host-side logic of the drop-in modules (CPU only; no kernel launches)."""
+import pytest
+import torch
+
+import hyper_multicore_amd as hm
+from hyper_multicore_amd import ops
+
+
+def test_megagate_validation_mirrors_reference():
+    kw = dict(hidden_size=16, num_experts=8, top_k=2, scoring_func="softmax", routed_scaling_factor=1.0)
+    hm.MegaGate(**kw)
+    for bad in (dict(top_k=9), dict(hidden_size=0), dict(scoring_func="relu"),
+                dict(routed_scaling_factor=float("inf")), dict(initializer_range=-1.0),
+                dict(num_expert_groups=3), dict(num_expert_groups=4, topk_groups=5),
+                dict(num_expert_groups=4, topk_groups=1, top_k=3)):
+        with pytest.raises(ValueError):
+            hm.MegaGate(**{**kw, **bad})
+
+
+def test_megagate_keeps_fp32_biases_under_dtype_change():
+    gate = hm.MegaGate(hidden_size=16, num_experts=8, top_k=2, scoring_func="sigmoid", routed_scaling_factor=1.0,
+                       vision_enabled=True).to(torch.bfloat16)
+    assert gate.weight.dtype == torch.bfloat16
+    assert gate.bias.dtype == torch.float32 and gate.bias_vl.dtype == torch.float32
+    assert torch.count_nonzero(gate.bias) == 0
+
+
+def test_megagate_from_module_shares_parameters():
+    src = torch.nn.Module()
+    src.weight = torch.nn.Parameter(torch.randn(8, 16))
+    src.bias = torch.nn.Parameter(torch.zeros(8))
+    gate = hm.MegaGate.from_module(src, top_k=2, scoring_func="softmax", routed_scaling_factor=1.0)
+    assert gate.weight is src.weight and gate.bias is src.bias
+    with pytest.raises(ValueError):
+        hm.MegaGate.from_module(src)  # top_k etc. missing
+
+
+def test_megagate_forward_errors():
+    gate = hm.MegaGate(hidden_size=16, num_experts=8, top_k=2, scoring_func="softmax", routed_scaling_factor=1.0)
+    x = torch.randn(1, 4, 16)
+    with pytest.raises(ValueError):
+        gate(x, image_mask=torch.ones(1, 4, dtype=torch.bool))  # no vision bias
+    with pytest.raises(RuntimeError):
+        gate(x)  # the gfx950 path needs a GPU; there is no CPU fallback
+
+
+def test_megamoe_options_and_validation():
+    kw = dict(hidden_size=128, intermediate_size=64, num_experts=4, top_k=2)
+    ex = hm.MegaMoeExperts(**kw)
+    assert ex.precision == "bf16" and ex.swiglu_limit is None and not ex.apply_probs_before_fc2
+    with pytest.raises(ValueError):
+        hm.MegaMoeExperts(**kw, precision="fp16")
+    with pytest.raises(ValueError):
+        hm.MegaMoeExperts(**{**kw, "top_k": 5})
+    with pytest.raises(ValueError):
+        hm.MegaMoeExperts(**kw, precision="mxfp8",
+                          numerics_options=hm.MegaMoeNumericsOptions(apply_probs_before_fc2=True))
+    with pytest.raises(NotImplementedError):
+        hm.MegaMoeExperts(**kw, numerics_options=hm.MegaMoeNumericsOptions(swiglu_limit=7.0))
+    with pytest.raises(TypeError):
+        hm.MegaMoeExperts(**kw, numerics_options=dict(swiglu_limit=None))
+    with pytest.raises(ValueError):
+        hm.MegaMoeExperts(**kw, tuning_options=hm.MegaMoeTuningOptions(dispatch_split=100))
+
+    class Group:
+        def size(self):
+            return 2
+    with pytest.raises(ValueError):
+        hm.MegaMoeExperts(**kw, ep_group=Group())
+
+
+def test_megamoe_layout_inference_and_input_checks():
+    ex = hm.MegaMoeExperts(hidden_size=128, intermediate_size=64, num_experts=4, top_k=2)
+    assert ex._infer_layout((4, 128, 128), (4, 64, 128)) == "EIO"
+    assert ex._infer_layout((4, 128, 128), (4, 128, 64)) == "EOI"
+    with pytest.raises(ValueError):
+        ex._infer_layout((4, 128, 64), (4, 64, 128))
+    x = torch.randn(6, 128).to(torch.bfloat16)
+    ids = torch.zeros(6, 2, dtype=torch.int64)
+    w = torch.rand(6, 2)
+    with pytest.raises(ValueError):
+        ex(x, ids[:, :1], w, expert_weights=(None, None))
+    with pytest.raises(TypeError):
+        ex(x, ids, w, expert_weights=(None, None))  # CPU hidden states
+
+
+def test_ops_reject_cpu_tensors():
+    with pytest.raises(TypeError):
+        ops.dispatch(torch.zeros(4, 2, dtype=torch.int64), 8)
+    with pytest.raises(TypeError):
+        ops.mx_quantize_rows(torch.zeros(4, 32, dtype=torch.bfloat16))

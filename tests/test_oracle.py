@@ -1,0 +1,321 @@
+"""Pin the CPU oracle (CPU only): against the reference tests' known answers (tests/golden),
+closed forms, independent formulations and brute force on tiny inputs."""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import moe_oracle as orc
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _ulp(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+# ------------------------------------------------------------------------------------------------
+# deterministic exp / log against the textbook functions
+# ------------------------------------------------------------------------------------------------
+def test_det_exp_log_within_two_ulp_of_libm():
+    xs = np.concatenate([np.linspace(-86.9, 88.7, 20001), np.array([0.0, -0.0, 1e-30, -1e-30, 1.0, -1.0])])
+    got = np.array([orc.det_expf(float(np.float32(x))) for x in xs], np.float32)
+    want = np.exp(xs.astype(np.float32).astype(np.float64)).astype(np.float32)
+    assert _ulp(got, want).max() <= 2
+    assert orc.det_expf(0.0) == 1.0
+    assert orc.det_expf(-100.0) == 0.0 and math.isinf(orc.det_expf(100.0))
+    us = np.concatenate([np.linspace(1.0, 3e4, 20001), np.array([1.0 + 2 ** -23, 2.0, 1e20, 3e38])])
+    got = np.array([orc.det_logf(float(np.float32(u))) for u in us], np.float32)
+    want = np.log(us.astype(np.float32).astype(np.float64)).astype(np.float32)
+    assert _ulp(got, want).max() <= 2
+    assert orc.det_logf(1.0) == 0.0
+
+
+# ------------------------------------------------------------------------------------------------
+# route: C oracle vs the torch closed forms of MegaGate._torch_forward (module.py:199-227)
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("scoring", ["softmax", "sigmoid", "sqrtsoftplus"])
+def test_route_c_matches_torch_forms(scoring):
+    g = torch.Generator().manual_seed(3)
+    T, E, K = 512, 64, 6
+    logits = torch.randn(T, E, generator=g) * 3
+    bias = torch.randn(E, generator=g) * 0.05
+    w, idx, s = orc.route_c(logits.numpy(), bias.numpy(), top_k=K, scoring_func=scoring, routed_scaling_factor=1.5)
+    w_ref, i_ref, s_ref = orc.route_reference(logits, bias, top_k=K, scoring_func=scoring,
+                                              routed_scaling_factor=1.5)
+    # exp/log are within 2 ulp of libm; softmax adds the sum order and the division
+    assert _ulp(s, s_ref.numpy()).max() <= (8 if scoring == "softmax" else 4)
+    same = (np.sort(idx, 1) == np.sort(i_ref.numpy(), 1)).all(1)
+    assert same.mean() > 0.995
+    wr = np.take_along_axis(w_ref.numpy(), np.argsort(i_ref.numpy(), 1), 1)
+    wc = np.take_along_axis(w, np.argsort(idx, 1), 1)
+    np.testing.assert_allclose(wc[same], wr[same], rtol=2e-6, atol=1e-7)
+
+
+def test_sqrtsoftplus_branch_points():
+    """_test_mega_gate.py:722-749 branch points; scores vs F.softplus(l).sqrt()."""
+    pts = torch.tensor([[-80.0, -20.0, -1e-7, 0.0, 20.0 - 2 ** -19, 20.0, 20.0 + 2 ** -19, 80.0]])
+    _, _, s = orc.route_c(pts.numpy(), np.zeros(8, np.float32), top_k=2, scoring_func="sqrtsoftplus",
+                          routed_scaling_factor=1.0)
+    want = F.softplus(pts).sqrt().numpy()
+    assert _ulp(s, want).max() <= 2
+    assert s[0, 7] == np.float32(math.sqrt(80.0))  # threshold branch is exact
+    assert s[0, 6] == np.sqrt(np.float32(20.0 + 2 ** -19))
+
+
+def test_route_grouped_matches_deepseek_form_and_reduces_to_plain():
+    g = torch.Generator().manual_seed(4)
+    T, E, K = 2048, 256, 8
+    logits = torch.randn(T, E, generator=g)
+    bias = torch.randn(E, generator=g) * 0.01
+    w, idx, _ = orc.route_c(logits.numpy(), bias.numpy(), top_k=K, scoring_func="sigmoid",
+                            routed_scaling_factor=2.5, num_groups=8, topk_groups=4)
+    _, i_ref, _ = orc.route_reference(logits, bias, top_k=K, scoring_func="sigmoid", routed_scaling_factor=2.5,
+                                      num_groups=8, topk_groups=4)
+    same = (np.sort(idx, 1) == np.sort(i_ref.numpy(), 1)).all(1)
+    assert same.mean() > 0.995
+    # selected experts come from at most 4 groups
+    assert (np.array([len(set((r // 32).tolist())) for r in idx]) <= 4).all()
+    # keeping every group is the plain biased top-k
+    w_all, i_all, _ = orc.route_c(logits.numpy(), bias.numpy(), top_k=K, scoring_func="sigmoid",
+                                  routed_scaling_factor=2.5, num_groups=8, topk_groups=8)
+    w_plain, i_plain, _ = orc.route_c(logits.numpy(), bias.numpy(), top_k=K, scoring_func="sigmoid",
+                                      routed_scaling_factor=2.5)
+    assert np.array_equal(i_all, i_plain) and np.array_equal(w_all, w_plain)
+
+
+def test_route_grouped_brute_force_tiny():
+    """E=8, G=4, keep 2 groups, K=3: enumerate the definition directly."""
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        logits = rng.standard_normal((1, 8)).astype(np.float32)
+        bias = (rng.standard_normal(8) * 0.1).astype(np.float32)
+        _, idx, s = orc.route_c(logits, bias, top_k=3, scoring_func="sigmoid", routed_scaling_factor=1.0,
+                                num_groups=4, topk_groups=2)
+        b = s[0] + bias
+        gs = [sorted(b[2 * g:2 * g + 2])[::-1] for g in range(4)]
+        gscore = [float(np.float32(x[0]) + np.float32(x[1])) for x in gs]
+        keep = sorted(range(4), key=lambda g: (-gscore[g], g))[:2]
+        cand = [e for e in range(8) if e // 2 in keep]
+        want = sorted(cand, key=lambda e: (-b[e], e))[:3]
+        assert idx[0].tolist() == want
+
+
+def test_route_order_ties_and_k1():
+    logits = np.zeros((1, 8), np.float32)
+    bias = np.array([0, 1, 1, 0, 2, 1, 0, 0], np.float32) * 0.1
+    w, idx, _ = orc.route_c(logits, bias, top_k=4, scoring_func="sigmoid", routed_scaling_factor=1.0)
+    assert idx[0].tolist() == [4, 1, 2, 5]  # descending biased score, ties -> lower id
+    np.testing.assert_allclose(w[0], np.full(4, 0.25, np.float32), rtol=1e-7)
+    w1, i1, s1 = orc.route_c(np.array([[0.3, 2.0, -1.0]], np.float32), np.zeros(3, np.float32), top_k=1,
+                             scoring_func="softmax", routed_scaling_factor=2.0)
+    assert i1[0, 0] == 1 and w1[0, 0] == np.float32(s1[0, 1] * np.float32(2.0))  # K=1: no renormalisation
+
+
+def test_route_vision_bias_selects_per_token():
+    g = np.random.default_rng(1)
+    logits = g.standard_normal((64, 16)).astype(np.float32)
+    bias = np.zeros(16, np.float32)
+    bias_vl = np.zeros(16, np.float32)
+    bias_vl[3] = 10.0
+    mask = np.arange(64) % 2 == 1
+    _, idx, _ = orc.route_c(logits, bias, top_k=2, scoring_func="softmax", routed_scaling_factor=1.0,
+                            bias_vl=bias_vl, image_mask=mask)
+    assert (idx[mask, 0] == 3).all()
+    _, idx_ref, _ = orc.route_reference(torch.from_numpy(logits), torch.from_numpy(bias), top_k=2,
+                                        scoring_func="softmax", routed_scaling_factor=1.0,
+                                        bias_vl=torch.from_numpy(bias_vl), image_mask=torch.from_numpy(mask))
+    assert (np.sort(idx, 1) == np.sort(idx_ref.numpy(), 1)).all()
+
+
+# ------------------------------------------------------------------------------------------------
+# route metadata and permutation: reference known answers
+# ------------------------------------------------------------------------------------------------
+def test_route_metadata_matches_reference_kat():
+    kat = json.loads((GOLDEN / "route_metadata_kat.json").read_text())
+    counts_by_source = torch.tensor(kat["global_counts"], dtype=torch.int32)
+    supplied = torch.tensor(kat["supplied_counts"], dtype=torch.int32)
+    received = counts_by_source[:, 2:4].contiguous()
+    assert received.tolist() == kat["expected_received_counts"]
+    for mode in ("push", "pull"):
+        md = orc.route_metadata(counts_by_source, rank=kat["rank"], ep_size=kat["ep_size"], dispatch_mode=mode,
+                                received_counts=received, counts=supplied)
+        for field, value in kat[mode].items():
+            if field == "expert_capacity":
+                assert int(md["group_list"][-1]) == value
+                continue
+            assert md[field].tolist() == value, (mode, field)
+            assert md[field].dtype == (torch.int32 if field.endswith("size") else torch.int64)
+
+
+def test_route_metadata_ep1_is_plain_prefix_sums():
+    g = torch.Generator().manual_seed(5)
+    for E in (2, 6, 64, 256):
+        counts = torch.randint(0, 1024, (1, E), dtype=torch.int32, generator=g)
+        counts[0, 0] = 0
+        md = orc.route_metadata(counts, rank=0, ep_size=1)
+        incl = counts[0].to(torch.int64).cumsum(0)
+        assert torch.equal(md["dispatch_src_off"], incl - counts[0])
+        assert torch.equal(md["group_list"], incl)
+        assert torch.equal(md["combine_src_off"], md["dispatch_src_off"])
+        assert torch.equal(md["dispatch_size"], counts[0])
+
+
+def test_permutation_matches_reference_kat():
+    kat = json.loads((GOLDEN / "permute_kat.json").read_text())
+    ids = torch.tensor(kat["topk_ids"])
+    mapping, gather = orc.stable_permutation(ids, kat["num_experts"])
+    assert gather.tolist() == kat["gather_order"]
+    assert mapping.tolist() == kat["scatter_mapping"]
+
+
+def test_permutation_invariants_and_brute_force():
+    g = torch.Generator().manual_seed(6)
+    T, K, E = 300, 4, 17
+    ids = torch.randint(0, E, (T, K), generator=g)
+    mapping, gather = orc.stable_permutation(ids, E)
+    flat = ids.reshape(-1).tolist()
+    want = sorted(range(T * K), key=lambda s: (flat[s], s))
+    assert gather.tolist() == want
+    assert sorted(mapping.tolist()) == list(range(T * K))
+    assert all(gather[mapping[s]] == s for s in range(T * K))
+    counts = orc.expert_counts(ids, E)
+    assert counts.tolist() == [flat.count(e) for e in range(E)]
+    x = torch.randn(T, 8).to(torch.bfloat16)
+    routed, m2 = orc.permute_tokens(x, ids, E)
+    assert torch.equal(m2, mapping)
+    assert torch.equal(routed[mapping.long()], x.repeat_interleave(K, 0))
+
+
+def test_unpermute_closed_form():
+    g = torch.Generator().manual_seed(7)
+    T, K, H = 50, 3, 16
+    y = torch.randn(T * K, H, generator=g).to(torch.bfloat16)
+    mapping = torch.randperm(T * K, generator=g).to(torch.int32)
+    p = torch.rand(T, K, generator=g)
+    out = orc.unpermute_tokens(y, mapping, p, K)
+    want = sum(y.float()[mapping.view(T, K)[:, k].long()] * p[:, k:k + 1] for k in range(K)).to(torch.bfloat16)
+    assert torch.equal(out, want)
+    ident = orc.unpermute_tokens(y[:T], torch.arange(T, dtype=torch.int32), None, 1)
+    assert torch.equal(ident, y[:T])
+
+
+# ------------------------------------------------------------------------------------------------
+# MX quantisation (OCP MX v1.0, e4m3fn + e8m0 / 32)
+# ------------------------------------------------------------------------------------------------
+def test_mx_known_codes():
+    def q(vals):
+        x = torch.zeros(1, 32)
+        x[0, :len(vals)] = torch.tensor(vals)
+        x[0, 31] = 448.0  # pins the block scale at 2^0 (floor(log2 448) - 8 = 0)
+        codes, scale = orc.mx_quantize(x)
+        assert int(scale[0, 0]) == 127
+        return codes[0, :len(vals)].tolist()
+    assert q([1.0, -1.0, 448.0, 0.0]) == [0x38, 0xB8, 0x7E, 0x00]
+    assert q([2 ** -9, 2 ** -10, 3 * 2 ** -10, 2 ** -6]) == [0x01, 0x00, 0x02, 0x08]  # subnormals, RNE ties
+    assert q([1.0625, 1.1875, 240.0, 232.0]) == [0x38, 0x3A, 0x77, 0x76]  # ties to even mantissa
+
+
+def test_mx_invariants():
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(64, 256, generator=g) * torch.logspace(-8, 8, 64).unsqueeze(1)
+    x[0] = 0.0
+    codes, scale = orc.mx_quantize(x)
+    deq = orc.mx_dequantize(codes, scale)
+    blocks = x.reshape(64, 8, 32)
+    amax = blocks.abs().amax(-1)
+    s = (scale.to(torch.float32) - 127).reshape(64, 8)
+    nz = amax > 0
+    # scale exponent = floor(log2(amax)) - 8
+    assert torch.equal(s[nz], torch.floor(torch.log2(amax[nz])) - 8)
+    # scaled block maximum lies in [256, 512) before saturation at 448
+    scaled_max = amax[nz] / torch.pow(2.0, s[nz])
+    assert (scaled_max >= 256).all() and (scaled_max < 512).all()
+    # relative error of every normal e4m3 element is at most 2^-4 (half a mantissa step)
+    rel = ((deq - x).abs() / x.abs().clamp(min=1e-30)).reshape(64, 8, 32)
+    norm = (x.reshape(64, 8, 32).abs() >= torch.pow(2.0, s).unsqueeze(-1) * 2 ** -6) & \
+           (x.reshape(64, 8, 32).abs() <= torch.pow(2.0, s).unsqueeze(-1) * 448)
+    assert rel[norm].max() <= 2 ** -4 + 1e-7
+    assert (deq[0] == 0).all()
+
+
+def test_mx_weight_col_layout_roundtrip():
+    g = torch.Generator().manual_seed(9)
+    w = torch.randn(2, 128, 96, generator=g).to(torch.bfloat16)
+    data, col_scale = orc.mx_quantize_weight_cols(w)
+    assert col_scale.shape == (2, 2, 96, 2)
+    codes, scale = orc.mx_quantize(w.float(), dim=1)  # [2, 4, 96]
+    assert torch.equal(col_scale[:, 1, 5, 0], scale[:, 2, 5])
+    assert torch.equal(col_scale[:, 1, 5, 1], scale[:, 3, 5])
+    deq = orc.mx_dequantize_weight_cols(data, col_scale)
+    # half a step: 2^-4 relative for normal elements, 2^(s-10) on the subnormal grid
+    step = torch.pow(2.0, scale.float() - 127 - 10).repeat_interleave(32, dim=1)
+    bound = torch.maximum(w.float().abs() * 2 ** -4, step)
+    # OCP MX floor scaling saturates elements above 448 * 2^s to exactly +-448 * 2^s
+    top = torch.pow(2.0, scale.float() - 127).repeat_interleave(32, dim=1) * 448
+    sat = w.float().abs() > top
+    assert torch.equal(deq[sat], torch.sign(w.float()[sat]) * top[sat])
+    assert ((deq - w.float()).abs()[~sat] <= bound[~sat]).all()
+
+
+# ------------------------------------------------------------------------------------------------
+# expert math
+# ------------------------------------------------------------------------------------------------
+def _inputs(T=96, H=64, I=32, E=4, K=2, seed=10):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    p = torch.rand(T, K, generator=g)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.1).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.1).to(torch.bfloat16)
+    return x, ids, p, w1, w2
+
+
+def test_expert_reference_matches_torch_experts_loop():
+    x, ids, p, w1, w2 = _inputs()
+    I = w2.shape[1]
+    ours = orc.expert_forward_reference(x, ids, p, w1, w2)
+    golden = orc.torch_experts_reference(x, ids, p, w1[:, :, :I].transpose(1, 2), w1[:, :, I:].transpose(1, 2),
+                                         w2.transpose(1, 2))
+    assert orc.rel_l2(ours, golden) < 1e-2
+    eoi = orc.expert_forward_reference(x, ids, p, w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous(),
+                                       layout="EOI")
+    assert torch.equal(eoi, ours)
+
+
+def test_expert_reference_single_expert_closed_form():
+    """One expert, K=1, p=1: fp32_expert_reference.py:22-26 rounding points."""
+    x, _, _, w1, w2 = _inputs(E=1, K=1)
+    ids = torch.zeros(x.shape[0], 1, dtype=torch.int64)
+    out = orc.expert_forward_reference(x, ids, torch.ones(x.shape[0], 1), w1, w2)
+    proj = (x.float() @ w1[0].float()).bfloat16().float()
+    gate, up = proj.chunk(2, dim=-1)
+    act = (F.silu(gate) * up).bfloat16().float()
+    want = (act @ w2[0].float()).bfloat16()
+    assert torch.equal(out, want)
+
+
+def test_expert_reference_linear_in_probs():
+    x, ids, p, w1, w2 = _inputs()
+    a = orc.expert_forward_reference(x, ids, p, w1, w2).float()
+    b = orc.expert_forward_reference(x, ids, 2 * p, w1, w2).float()
+    assert torch.allclose(b, 2 * a, rtol=1e-2, atol=1e-2)
+
+
+def test_mxfp8_reference_close_to_bf16():
+    x, ids, p, w1, w2 = _inputs(H=128, I=64)
+    d1, s1 = orc.mx_quantize_weight_cols(w1)
+    d2, s2 = orc.mx_quantize_weight_cols(w2)
+    mx = orc.expert_forward_reference(x, ids, p, d1, d2, precision="mxfp8", w1_scale=s1, w2_scale=s2)
+    bf = orc.expert_forward_reference(x, ids, p, w1, w2)
+    assert orc.rel_l2(mx, bf) < 0.1
+
+
+def test_flops_formula():
+    assert orc.moe_flops(8192, 8, 7168, 2048, 256) == pytest.approx(5.772e12 + 3.0e10, rel=2e-3)
