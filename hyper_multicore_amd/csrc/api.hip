@@ -121,7 +121,8 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
                                            int32_t ndim, const int64_t* group_list, uint16_t* out, void* workspace,
                                            size_t workspace_size, void* stream) {
   if (rows < 0 || kdim <= 0 || ndim <= 0 || num_groups <= 0 || num_groups > 4096) return MI355MOE_EINVAL;
-  if (kdim % 128 || ndim % 16) return MI355MOE_EUNSUPPORTED;
+  // the GEMM fetches 16 activation scale codes per row at a time: K/32 must be a multiple of 16
+  if (kdim % 512 || ndim % 16) return MI355MOE_EUNSUPPORTED;
   if (rows == 0) return MI355MOE_OK;
   if (xq == nullptr || x_scale == nullptr || col_data == nullptr || col_scale == nullptr || group_list == nullptr ||
       out == nullptr)
@@ -133,6 +134,7 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
   p.lda_bytes = kdim;
   p.a_row_div = 1;
   p.a_scale = x_scale;
+  p.a_scale_ld = kdim / 32;
   p.B = col_data;
   p.b_group_stride = (int64_t)kdim * ndim;
   p.b_row_bytes = ndim;
@@ -173,10 +175,10 @@ static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
   L.gather = take(R * 4);
   L.tile_prefix = take((E + 1) * 4);
   L.act = take(R * I * (mx ? 1 : 2));
-  L.act_scale = mx ? take(R * (I / 32)) : 0;
+  L.act_scale = mx ? take(R * mi355_mx_scale_ld(I)) : 0;
   L.y = take(R * H * 2);
   L.xq = mx ? take(T * H) : 0;
-  L.xs = mx ? take(T * (H / 32)) : 0;
+  L.xs = mx ? take(T * mi355_mx_scale_ld(H)) : 0;
   L.total = off;
   return L;
 }
@@ -246,7 +248,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   if (rc) return rc;
   const uint8_t* a1 = (const uint8_t*)a.hidden;
   if (mx) {
-    rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), st);
+    rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), mi355_mx_scale_ld(H), st);
     if (rc) return rc;
     a1 = (const uint8_t*)(ws + L.xq);
   }
@@ -259,6 +261,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.a_row_index = gather;
   p1.a_row_div = K;
   p1.a_scale = mx ? (const uint8_t*)(ws + L.xs) : nullptr;
+  p1.a_scale_ld = mi355_mx_scale_ld(H);
   p1.B = (const uint8_t*)a.w1;
   p1.b_group_stride = (int64_t)H * 2 * I * esize;
   p1.b_row_bytes = eoi ? (int64_t)H * esize : (int64_t)2 * I * esize;
@@ -274,6 +277,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.C = ws + L.act;
   p1.ldc = I;
   p1.c_scale = mx ? (uint8_t*)(ws + L.act_scale) : nullptr;
+  p1.c_scale_ld = mi355_mx_scale_ld(I);
   rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st);
   if (rc) return rc;
   mark(2);
@@ -283,6 +287,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p2.lda_bytes = (int64_t)I * esize;
   p2.a_row_div = 1;
   p2.a_scale = mx ? (const uint8_t*)(ws + L.act_scale) : nullptr;
+  p2.a_scale_ld = mi355_mx_scale_ld(I);
   p2.B = (const uint8_t*)a.w2;
   p2.b_group_stride = (int64_t)I * H * esize;
   p2.b_row_bytes = eoi ? (int64_t)I * esize : (int64_t)H * esize;

@@ -9,7 +9,8 @@ struct GGParams {
   int64_t lda_bytes;
   const int32_t* a_row_index;  // routed row -> index (or NULL: identity)
   int32_t a_row_div;           // source row = a_row_index[r] / a_row_div
-  const uint8_t* a_scale;    // MX: [rowsA, K/32]
+  const uint8_t* a_scale;    // MX: [rowsA, K/32] with row stride a_scale_ld (multiple of 16 bytes)
+  int64_t a_scale_ld;
   const uint8_t* B;          // per group: NK [Ntot, K] or KN [K, Ntot]
   int64_t b_group_stride;    // bytes
   int64_t b_row_bytes;       // NK: K*esize ; KN: Ntot*esize
@@ -25,7 +26,8 @@ struct GGParams {
   void* C;
   int64_t ldc;               // elements (bf16/f32) or bytes (e4m3)
   const int32_t* c_row_index;  // optional output row scatter (EPI_STORE_F32)
-  uint8_t* c_scale;          // EPI_SWIGLU_MX: [rows, N/32]
+  uint8_t* c_scale;          // EPI_SWIGLU_MX: [rows, N/32] with row stride c_scale_ld
+  int64_t c_scale_ld;
 };
 
 
@@ -38,4 +40,8 @@ int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int t
                            int32_t* error_flag, void* workspace, hipStream_t stream);
 int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const float* probs, int64_t T, int K, int H,
                             uint16_t* out, hipStream_t stream);
-int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, hipStream_t st);
+int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
+                        hipStream_t st);
+// Row stride (bytes) of the internal MX activation-scale buffers: K/32 rounded up to 16 so the
+// GEMM can fetch 16 codes (8 K stages) of a row with one 16-byte load.
+inline int64_t mi355_mx_scale_ld(int64_t k) { return ((k / 32 + 15) / 16) * 16; }

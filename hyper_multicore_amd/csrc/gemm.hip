@@ -7,53 +7,67 @@
 // in rounds so that each XCD takes a contiguous run of items per round (m fastest): items that
 // share a weight slice run at the same time on one XCD and share its L2.
 //
-// Workgroup: 256 threads = 4 wavefronts in a 2 (M) x 2 (N) grid; tile BM=128 x BN=256; each
-// wavefront computes 64 x 128 with 32x32 MFMA (bf16: v_mfma_f32_32x32x16_bf16; MXFP8:
+// Workgroup: 512 threads = 8 wavefronts (two per SIMD, which both the HBM stream and the LDS
+// read rate need) in a 4 (M) x 2 (N) grid; tile BM=256 x BN=256; each wavefront computes
+// 64 x 128 with 2 x 4 32x32 MFMAs (bf16: v_mfma_f32_32x32x16_bf16; MXFP8:
 // v_mfma_scale_f32_32x32x64_f8f6f4 with per-lane e8m0 scales: lane r + 32b supplies the scale
 // of 32-block b of row / column r, and its operand bytes 0-15 / 16-31 hold K = 16b + i /
-// 32 + 16b + i of the 64-K step). K advances 128 bytes per stage
-// (64 bf16 or 128 e4m3). Global -> LDS copies use the direct-to-LDS 16-byte loads; two LDS
-// stages are double buffered.
+// 32 + 16b + i of the 64-K step). A stage holds 64 bytes of K per row (32 bf16 or 64 e4m3);
+// global -> LDS copies use the direct-to-LDS loads into a 4-deep ring (three stages in flight).
 //
 // LDS layouts (16-byte chunk granularity, XOR swizzled against bank conflicts):
-//   K-contiguous operand rows (A always; B in EOI layout): row r at r*128, chunk c stored at
-//     c ^ ((r >> 1) & 7); read with ds_read_b128.
+//   K-contiguous operand rows (A always; B in EOI layout): row r at r*64, chunk c stored at
+//     c ^ ((r >> 2) & 3); read with ds_read_b128.
 //   N-contiguous B (EIO bf16 / MX col_data): row k holds 256 columns; bf16 chunk c stored at
 //     c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows); read
 //     with the transposing ds_read_b64_tr_b16 / ds_read_b64_tr_b8.
+//   MX scales per stage: A one dword per row (the row's two e8m0 codes, 2-byte DMA zero-extends),
+//     B the two codes of every tile column (col_scale's [.., N, 2] pairs).
 //
 // Epilogues: bf16 store, fp32 store (router logits, optional row scatter), SwiGLU -> bf16 and
 // SwiGLU -> MXFP8 requant. For SwiGLU the B tile columns are gate/up interleaved in 64-column
 // groups so that each lane holds the gate and up value of the same output element.
+#include <type_traits>
 #include "common.h"
 #include "scan.h"
 #include "../../include/mi355moe.h"
 #include "gemm.h"
 
-#define GG_BM 128
+#define GG_BM 256
 #define GG_BN 256
-#define GG_KB 128  // bytes of K per stage per row
-#define GG_THREADS 256
+#define GG_KB 64  // bytes of K per stage per row
+#define GG_THREADS 512
+#define GG_WAVES 8
 
 struct GGLds {
+  // Decoupled rings: activations A (re-read from L2 by the tiles of one expert) and weights B
+  // (streamed once from HBM, so it gets the deeper ring: five stages = 80 KB in flight per CU).
   static constexpr int A_BYTES = GG_BM * GG_KB;        // 16 KB
-  static constexpr int B_BYTES = GG_BN * GG_KB;        // 32 KB
-  static constexpr int AS_BYTES = GG_BM * 4;           // 512 B
-  static constexpr int BS_BYTES = 2 * GG_BN * 2;       // 1 KB
-  static constexpr int STAGE = A_BYTES + B_BYTES + AS_BYTES + BS_BYTES;
-  static constexpr int NSTAGE = 3;
+  static constexpr int B_BYTES = GG_BN * GG_KB;        // 16 KB
+  static constexpr int BS_BYTES = GG_BN * 2;           // 512 B (MX: two codes per column)
+  static constexpr int B_SLOT = B_BYTES + BS_BYTES;
+  static constexpr int A_SLOTS = 3;                    // A(k+2) issued at iteration k
+  static constexpr int B_SLOTS = 6;                    // B(k+5) issued at iteration k
+  static constexpr int AS_GROUP = 8;                   // MX: A scale codes fetched per 8 stages
+  static constexpr int AS_SLOT = GG_BM * 16;           // 4 KB: 16 codes per row
+  static constexpr int B_OFF = A_SLOTS * A_BYTES;
+  static constexpr int AS_OFF = B_OFF + B_SLOTS * B_SLOT;
   static constexpr int PREFIX_MAX = 1024;              // groups whose tile prefix is kept in LDS
-  static constexpr int PREFIX_OFF = NSTAGE * STAGE;
+  static constexpr int PREFIX_OFF = AS_OFF + 2 * AS_SLOT;
   static constexpr int TOTAL = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
+  static_assert(GG_BM * (GG_BN * 2 + 16) <= AS_OFF, "bf16 epilogue staging must fit the rings");
+  static_assert(GG_BM * (128 * 4 + 16) <= AS_OFF, "SwiGLU epilogue staging must fit the rings");
+  static_assert(TOTAL <= 160 * 1024, "LDS budget");
 };
 
-MI355_DEV void lds_load16(const void* g, uint32_t lds_off_uniform, uint8_t* smem) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(smem + lds_off_uniform), 16, 0, 0);
+template <int SZ>
+MI355_DEV void lds_dma(const void* g, uint32_t lds_off_uniform, uint8_t* smem) {
+  auto* dst = (__attribute__((address_space(3))) void*)(smem + lds_off_uniform);
+  if constexpr (SZ == 16) __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
+  else if constexpr (SZ == 4) __builtin_amdgcn_global_load_lds(g, dst, 4, 0, 0);
+  else if constexpr (SZ == 2) __builtin_amdgcn_global_load_lds(g, dst, 2, 0, 0);
+  else static_assert(SZ == 16, "unsupported DMA size");
 }
-MI355_DEV void lds_load4(const void* g, uint32_t lds_off_uniform, uint8_t* smem) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(smem + lds_off_uniform), 4, 0, 0);
-}
-// Wait until at most N vector-memory loads of this wave are outstanding (loads retire in order).
 // Workgroup barrier without the release fence of __syncthreads (which would wait for every
 // outstanding global load, including the prefetched stages): LDS reads of this wave are drained,
 // the direct-to-LDS loads are ordered by the explicit vmcnt waits.
@@ -61,11 +75,14 @@ MI355_DEV void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 }
+// Wait until at most N vector-memory loads of this wave are outstanding (loads retire in order).
 template <int N>
 MI355_DEV void wait_vm_le() {
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-  else if constexpr (N == 13) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");
+  else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   else static_assert(N == 0, "unsupported vmcnt");
 }
 
@@ -77,167 +94,180 @@ MI355_DEV int tile_col_to_weight_col(int j, int nt, int I, bool swiglu) {
   return jj < 64 ? base + jj : I + base + (jj - 64);
 }
 
-struct FragBF16 {
-  v8bf a[2];
-  v8bf b[4];
-};
-struct FragMX {
-  v8i a[2];
-  v8i b[4];
-  int sa[2];
-  int sb[4];
-};
+MI355_DEV int a_chunk_off(int r, int c) { return r * GG_KB + ((c ^ ((r >> 2) & 3)) << 4); }
 
+// ---- fragment loads (one K step: 16 bf16 or 64 e4m3) ------------------------------------------
+MI355_DEV v8bf read_a_bf16(const uint8_t* As, int r, int ks, int lane) {
+  return *(const v8bf*)(As + a_chunk_off(r, ks * 2 + (lane >> 5)));
+}
 template <bool B_KN>
-MI355_DEV void load_frag_bf16(const uint8_t* As, const uint8_t* Bs, int ks, int wm, int wn, int lane, FragBF16& f) {
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    int r = wm * 64 + mi * 32 + (lane & 31);
-    int c = (ks * 2 + (lane >> 5)) ^ ((r >> 1) & 7);
-    f.a[mi] = *(const v8bf*)(As + r * 128 + c * 16);
-  }
-#pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
-    if (!B_KN) {
-      int n = wn * 128 + ni * 32 + (lane & 31);
-      int c = (ks * 2 + (lane >> 5)) ^ ((n >> 1) & 7);
-      f.b[ni] = *(const v8bf*)(Bs + n * 128 + c * 16);
-    } else {
-      int g16 = lane >> 4, m = lane & 15;
-      int nb = wn * 128 + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
-      int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2);
-      int k1 = k0 + 4;
-      int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
-      int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
-      v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off0));
-      v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
-      typedef __attribute__((ext_vector_type(8))) short v8s;
-      v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      f.b[ni] = __builtin_bit_cast(v8bf, both);
-    }
-  }
-}
-
-// Scaled-MFMA operand order: lane r + 32g holds bytes 0-15 = K 16g + i and bytes 16-31 =
-// K 32 + 16g + i of the 64-K step, and supplies the e8m0 scale of 32-block g.
-MI355_DEV void load_frag_mx(const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs, const uint8_t* BSs, int ks,
-                            int wm, int wn, int lane, FragMX& f) {
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    int r = wm * 64 + mi * 32 + (lane & 31);
-    int c0 = ks * 4 + (lane >> 5);
-    v4i lo = *(const v4i*)(As + r * 128 + ((c0 ^ ((r >> 1) & 7)) << 4));
-    v4i hi = *(const v4i*)(As + r * 128 + (((c0 + 2) ^ ((r >> 1) & 7)) << 4));
-    f.a[mi] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    f.sa[mi] = ASs[r * 4 + ks * 2 + (lane >> 5)];
-  }
-#pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
-    int g16 = lane >> 4, m = lane & 15;
-    int nb = wn * 128 + ni * 32 + (g16 & 1) * 16;
-    int parts[8];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      int k = ks * 64 + (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
-      int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
-      v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
-      parts[2 * q] = v[0];
-      parts[2 * q + 1] = v[1];
-    }
-    f.b[ni] = (v8i){parts[0], parts[1], parts[2], parts[3], parts[4], parts[5], parts[6], parts[7]};
+MI355_DEV v8bf read_b_bf16(const uint8_t* Bs, int wn, int ni, int ks, int lane) {
+  if (!B_KN) {
     int n = wn * 128 + ni * 32 + (lane & 31);
-    f.sb[ni] = BSs[ks * 512 + n * 2 + (lane >> 5)];
+    return *(const v8bf*)(Bs + a_chunk_off(n, ks * 2 + (lane >> 5)));
   }
+  int g16 = lane >> 4, m = lane & 15;
+  int nb = wn * 128 + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
+  int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2);
+  int k1 = k0 + 4;
+  int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
+  int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
+  v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off0));
+  v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
+  typedef __attribute__((ext_vector_type(8))) short v8s;
+  v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(v8bf, both);
+}
+MI355_DEV v8i read_a_mx(const uint8_t* As, int r, int lane) {
+  int c0 = lane >> 5;
+  v4i lo = *(const v4i*)(As + a_chunk_off(r, c0));
+  v4i hi = *(const v4i*)(As + a_chunk_off(r, c0 + 2));
+  return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+MI355_DEV v8i read_b_mx(const uint8_t* Bs, int wn, int ni, int lane) {
+  int g16 = lane >> 4, m = lane & 15;
+  int nb = wn * 128 + ni * 32 + (g16 & 1) * 16;
+  int parts[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int k = (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
+    int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
+    v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
+    parts[2 * q] = v[0];
+    parts[2 * q + 1] = v[1];
+  }
+  return (v8i){parts[0], parts[1], parts[2], parts[3], parts[4], parts[5], parts[6], parts[7]};
 }
 
-template <int NM>
-MI355_DEV void mfma_bf16(v16f (&acc)[2][4], const FragBF16& f) {
-#pragma unroll
-  for (int mi = 0; mi < NM; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
-      acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
-}
-template <int NM>
-MI355_DEV void mfma_mx(v16f (&acc)[2][4], const FragMX& f) {
-#pragma unroll
-  for (int mi = 0; mi < NM; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
-      acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0, f.sa[mi],
-                                                                     0, f.sb[ni]);
-}
-
-// Per-thread copy plan of one work item (global sources of this thread's 16-byte chunks).
+// ---- copy plan -------------------------------------------------------------------------------
+// Per stage the workgroup copies A 16 KB and B 16 KB: each wave issues 2 + 2 16-byte DMA
+// instructions; MX adds the B scale codes (waves 4-5, one 4-byte DMA for 128 columns each) and,
+// every 8 stages, 16 A scale codes per row (waves 0-3, one 16-byte DMA for 64 rows each).
 struct CopyPlan {
-  const uint8_t* a[4];
-  const uint8_t* b[8];
-  const uint8_t* s[2];
+  const uint8_t* a[2];
+  const uint8_t* b[2];
+  const uint8_t* s;        // MX: A scale row (waves 0-3) or B scale column pair (waves 4-5)
+  int64_t b_stage_stride;  // bytes to advance B per stage
+  int64_t bs_stage_stride; // bytes to advance the B scales per stage
 };
 
-template <bool MX, bool B_KN>
-MI355_DEV void issue_stage(const GGParams& p, const CopyPlan& cp, int kt, int stage, int wave, uint8_t* smem) {
-  constexpr int ESIZE = MX ? 1 : 2;
-  const uint32_t base = stage * GGLds::STAGE;
+template <bool MX>
+MI355_DEV void issue_a(const CopyPlan& cp, int kt, int wave, uint8_t* smem) {
+#ifdef GG_ABLATE_DMA
+  if (wave < 64) return;
+#endif
+  const uint32_t base = (kt % GGLds::A_SLOTS) * GGLds::A_BYTES;
   const int64_t koff = (int64_t)kt * GG_KB;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) lds_load16(cp.a[j] + koff, base + (wave * 4 + j) * 1024, smem);
+  for (int j = 0; j < 2; ++j) lds_dma<16>(cp.a[j] + koff, base + (wave * 2 + j) * 1024, smem);
+}
+template <bool MX>
+MI355_DEV void issue_b(const CopyPlan& cp, int kt, int wave, uint8_t* smem) {
+#ifdef GG_ABLATE_DMA
+  if (wave < 64) return;
+#endif
+  const uint32_t base = GGLds::B_OFF + (kt % GGLds::B_SLOTS) * GGLds::B_SLOT;
+  const int64_t boff = (int64_t)kt * cp.b_stage_stride;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint8_t* src = B_KN ? cp.b[j] + (int64_t)kt * (GG_KB / ESIZE) * p.b_row_bytes : cp.b[j] + koff;
-    lds_load16(src, base + GGLds::A_BYTES + (wave * 8 + j) * 1024, smem);
-  }
-  if (MX) {
-    if (wave < 2) {
-      lds_load4(cp.s[0] + kt * 4, base + GGLds::A_BYTES + GGLds::B_BYTES + wave * 256, smem);
-    } else {
-      const int64_t ks = (int64_t)kt * 2 * p.Ntot * 2;  // two 64-K groups per stage
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        lds_load4(cp.s[h] + ks, base + GGLds::A_BYTES + GGLds::B_BYTES + GGLds::AS_BYTES + (wave - 2) * 512 + h * 256,
-                  smem);
-    }
-  }
+  for (int j = 0; j < 2; ++j) lds_dma<16>(cp.b[j] + boff, base + (wave * 2 + j) * 1024, smem);
+  if (MX && (wave == 4 || wave == 5))
+    lds_dma<4>(cp.s + kt * cp.bs_stage_stride, base + GGLds::B_BYTES + (wave - 4) * 256, smem);
+}
+// MX: A scale codes of stages 8*grp .. 8*grp+7 (16 bytes per row) into AS slot grp & 1.
+MI355_DEV void issue_as(const CopyPlan& cp, int grp, int wave, uint8_t* smem) {
+#ifdef GG_ABLATE_DMA
+  if (wave < 64) return;
+#endif
+  if (wave < 4) lds_dma<16>(cp.s + grp * 16, GGLds::AS_OFF + (grp & 1) * GGLds::AS_SLOT + wave * 1024, smem);
 }
 
-// K loop over a 3-stage LDS ring; NM = number of valid 32-row subtiles this wave computes.
-template <bool MX, bool B_KN, int NM>
-MI355_DEV void k_loop(const GGParams& p, const CopyPlan& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
+// K loop. Issue order (per wave): B0 B1 B2 AS0 A0 B3 A1 B4 | A2 B5 [AS1] | A3 B6 | ... : iteration
+// k issues A(k+2), B(k+5) and, every 8 stages, the next A scale group. At the top of iteration k
+// the loads younger than A(k) are B(k+3), A(k+1), B(k+4) (plus scale groups on waves 0-3), so
+// waiting for at most that many keeps A(k), B(k) and the scale group of stage k complete.
+// A wave whose 32 A rows (and 64 scale rows) all lie past the tile's last valid row copies no
+// A at all (LA = false, decode and ragged tiles); it waits on its B groups alone: younger than
+// B(k) are B(k+1) .. B(k+4).
+// NM = number of valid 32-row subtiles this wave computes (0..2).
+template <int N>
+MI355_DEV void wait_vm_b_only(int ahead) {
+  // ahead = number of later B groups issued (0..4), 2 loads each at least
+  if (ahead >= 4) wait_vm_le<8>();
+  else if (ahead == 3) wait_vm_le<6>();
+  else if (ahead == 2) wait_vm_le<4>();
+  else if (ahead == 1) wait_vm_le<2>();
+  else wait_vm_le<0>();
+}
+template <bool MX, bool B_KN, int NM, bool LA>
+MI355_DEV void k_loop(const CopyPlan& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
                       v16f (&acc)[2][4]) {
-  constexpr int LOADS = MX ? 13 : 12;  // minimum loads per wave per stage
-  issue_stage<MX, B_KN>(p, cp, 0, 0, wave, smem);
-  if (nk > 1) issue_stage<MX, B_KN>(p, cp, 1, 1, wave, smem);
-  int stage = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) wait_vm_le<LOADS>(); else wait_vm_le<0>();
-    lds_barrier();
-    if (kt + 2 < nk) {
-      int s2 = stage + 2;
-      if (s2 >= 3) s2 -= 3;
-      issue_stage<MX, B_KN>(p, cp, kt + 2, s2, wave, smem);
+  for (int j = 0; j < 3 && j < nk; ++j) issue_b<MX>(cp, j, wave, smem);
+  if (LA) {
+    if (MX) issue_as(cp, 0, wave, smem);
+    issue_a<MX>(cp, 0, wave, smem);
+  }
+  if (nk > 3) issue_b<MX>(cp, 3, wave, smem);
+  if (LA && nk > 1) issue_a<MX>(cp, 1, wave, smem);
+  if (nk > 4) issue_b<MX>(cp, 4, wave, smem);
+  for (int k = 0; k < nk; ++k) {
+    if (LA) {
+      if (k + 4 < nk) wait_vm_le<6>();
+      else if (k + 3 < nk) wait_vm_le<4>();
+      else if (k + 1 < nk) wait_vm_le<2>();
+      else wait_vm_le<0>();
+    } else {
+      wait_vm_b_only<0>(nk - 1 - k < 4 ? nk - 1 - k : 4);
     }
-    const uint8_t* As = smem + stage * GGLds::STAGE;
-    const uint8_t* Bs = As + GGLds::A_BYTES;
+    lds_barrier();
+    if (LA && k + 2 < nk) issue_a<MX>(cp, k + 2, wave, smem);
+    if (k + 5 < nk) issue_b<MX>(cp, k + 5, wave, smem);
+    if (LA && MX && (k & (GGLds::AS_GROUP - 1)) == 0 && k + GGLds::AS_GROUP < nk)
+      issue_as(cp, k / GGLds::AS_GROUP + 1, wave, smem);
+#ifdef GG_ABLATE_COMPUTE
+    if (wave < 64) continue;
+#endif
     if constexpr (NM > 0) {
+      const uint8_t* As = smem + (k % GGLds::A_SLOTS) * GGLds::A_BYTES;
+      const uint8_t* Bs = smem + GGLds::B_OFF + (k % GGLds::B_SLOTS) * GGLds::B_SLOT;
       if constexpr (!MX) {
-        FragBF16 f[2];
-        load_frag_bf16<B_KN>(As, Bs, 0, wm, wn, lane, f[0]);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          if (ks + 1 < 4) load_frag_bf16<B_KN>(As, Bs, ks + 1, wm, wn, lane, f[(ks + 1) & 1]);
-          mfma_bf16<NM>(acc, f[ks & 1]);
+        for (int ks = 0; ks < 2; ++ks) {
+          v8bf a[2], b[4];
+#pragma unroll
+          for (int ni = 0; ni < 4; ++ni) b[ni] = read_b_bf16<B_KN>(Bs, wn, ni, ks, lane);
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi) a[mi] = read_a_bf16(As, wm * 64 + mi * 32 + (lane & 31), ks, lane);
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
         }
       } else {
-        const uint8_t* ASs = Bs + GGLds::B_BYTES;
-        const uint8_t* BSs = ASs + GGLds::AS_BYTES;
-        FragMX f[2];
-        load_frag_mx(As, Bs, ASs, BSs, 0, wm, wn, lane, f[0]);
-        load_frag_mx(As, Bs, ASs, BSs, 1, wm, wn, lane, f[1]);
-        mfma_mx<NM>(acc, f[0]);
-        mfma_mx<NM>(acc, f[1]);
+        const uint8_t* BSs = Bs + GGLds::B_BYTES;
+        const uint8_t* ASs = smem + GGLds::AS_OFF + ((k / GGLds::AS_GROUP) & 1) * GGLds::AS_SLOT +
+                             (k & (GGLds::AS_GROUP - 1)) * 2;
+        v8i a[2], b[4];
+        int sa[2], sb[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+          b[ni] = read_b_mx(Bs, wn, ni, lane);
+          sb[ni] = BSs[(wn * 128 + ni * 32 + (lane & 31)) * 2 + (lane >> 5)];
+        }
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) {
+          int r = wm * 64 + mi * 32 + (lane & 31);
+          a[mi] = read_a_mx(As, r, lane);
+          sa[mi] = ASs[r * 16 + (lane >> 5)];
+        }
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < 4; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], b[ni], acc[mi][ni], 0, 0, 0, sa[mi],
+                                                                           0, sb[ni]);
       }
     }
-    stage = stage == 2 ? 0 : stage + 1;
   }
 }
 
@@ -285,10 +315,10 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     // ---- per-thread copy sources ------------------------------------------------------
     CopyPlan cp;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int L16 = wave * 256 + j * 64 + lane;
-      int r = L16 >> 3, cs = L16 & 7;
-      int c = cs ^ ((r >> 1) & 7);
+    for (int j = 0; j < 2; ++j) {
+      int L16 = wave * 128 + j * 64 + lane;
+      int r = L16 >> 2, cs = L16 & 3;
+      int c = cs ^ ((r >> 2) & 3);
       int rr = r < rows_valid ? r : rows_valid - 1;
       int64_t routed = tile_row0 + rr;
       int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
@@ -296,11 +326,11 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     }
     const uint8_t* bgrp = p.B + (int64_t)g * p.b_group_stride;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int L16 = wave * 512 + j * 64 + lane;
+    for (int j = 0; j < 2; ++j) {
+      int L16 = wave * 128 + j * 64 + lane;
       if (!B_KN) {
-        int r = L16 >> 3, cs = L16 & 7;
-        int c = cs ^ ((r >> 1) & 7);
+        int r = L16 >> 2, cs = L16 & 3;
+        int c = cs ^ ((r >> 2) & 3);
         int wc = tile_col_to_weight_col(r, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 1;
         cp.b[j] = bgrp + (int64_t)wc * p.b_row_bytes + c * 16;
@@ -318,25 +348,24 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
         cp.b[j] = bgrp + (int64_t)k * p.b_row_bytes + (int64_t)wc * 2;
       }
     }
-    // MX scales: waves 0/1 copy A scale dwords (rows 0..63 / 64..127), waves 2/3 copy the two
-    // 64-K groups of B scales (256 columns x 2 bytes = 128 dwords = 2 instructions each).
-    cp.s[0] = cp.s[1] = nullptr;
+    cp.b_stage_stride = B_KN ? (int64_t)(GG_KB / ESIZE) * p.b_row_bytes : GG_KB;
+    cp.s = nullptr;
+    cp.bs_stage_stride = 0;
     if (MX) {
-      if (wave < 2) {
+      if (wave < 4) {
+        // A scales: row wave*64 + lane (16 codes = 8 stages per fetch)
         int r = wave * 64 + lane;
         int rr = r < rows_valid ? r : rows_valid - 1;
         int64_t routed = tile_row0 + rr;
         int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
-        cp.s[0] = p.a_scale + src * (p.K / 32);
+        cp.s = p.a_scale + src * p.a_scale_ld;
       } else {
-        int gi = wave - 2;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          int j = (h * 64 + lane) * 2;  // tile column pair (j, j+1)
-          int wc = tile_col_to_weight_col(j, nt, p.N, SWIGLU);
-          if (wc >= p.Ntot) wc = p.Ntot - 2;
-          cp.s[h] = p.b_scale + (int64_t)g * p.b_scale_group_stride + ((int64_t)gi * p.Ntot + wc) * 2;
-        }
+        // B scales: tile columns ((wave-4)*64 + lane)*2 .. +1, one col_scale group per stage
+        int j = ((wave & 1) * 64 + lane) * 2;
+        int wc = tile_col_to_weight_col(j, nt, p.N, SWIGLU);
+        if (wc >= p.Ntot) wc = p.Ntot - 2;
+        cp.s = p.b_scale + (int64_t)g * p.b_scale_group_stride + (int64_t)wc * 2;
+        cp.bs_stage_stride = (int64_t)p.Ntot * 2;
       }
     }
 
@@ -349,13 +378,24 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     __syncthreads();  // the previous item's last stage / epilogue reads are done before refilling
-    const int nm = wm * 64 + 32 < rows_valid ? 2 : (wm * 64 < rows_valid ? 1 : 0);
-    if (nm == 2) k_loop<MX, B_KN, 2>(p, cp, nk, wave, wm, wn, lane, smem, acc);
-    else if (nm == 1) k_loop<MX, B_KN, 1>(p, cp, nk, wave, wm, wn, lane, smem, acc);
-    else k_loop<MX, B_KN, 0>(p, cp, nk, wave, wm, wn, lane, smem, acc);
+    const int rows_w = rows_valid - wm * 64;
+    const int nm = rows_w >= 33 ? 2 : (rows_w >= 1 ? 1 : 0);
+    // this wave copies A rows wave*32 .. +31 (and, MX waves 0-3, scale rows wave*64 .. +63)
+    const bool la = wave * 32 < rows_valid;
+    if (la) {
+      if (nm == 2) k_loop<MX, B_KN, 2, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 1) k_loop<MX, B_KN, 1, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else k_loop<MX, B_KN, 0, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+    } else {
+      if (nm == 2) k_loop<MX, B_KN, 2, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 1) k_loop<MX, B_KN, 1, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else k_loop<MX, B_KN, 0, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+    }
     __syncthreads();  // all waves are done reading the ring before the epilogue reuses LDS
 
     // ---- epilogue -----------------------------------------------------------------------
+    // acc[mi][ni][r] holds row wm*64 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4,
+    // column wn*128 + ni*32 + lane%32 of the tile.
     if (EPI == EPI_STORE_F32) {
       float* C = (float*)p.C;
 #pragma unroll
@@ -446,7 +486,7 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
             uint8_t* dst = C + (tile_row0 + row) * p.ldc + nt * 128 + blk * 32;
             *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
             *(uint4*)(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-            p.c_scale[(tile_row0 + row) * (p.N / 32) + nt * 4 + blk] = (uint8_t)code;
+            p.c_scale[(tile_row0 + row) * p.c_scale_ld + nt * 4 + blk] = (uint8_t)code;
           }
         }
       }

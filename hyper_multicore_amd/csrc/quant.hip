@@ -10,7 +10,7 @@
 
 // One thread per 32-element block of a row.
 __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint16_t* x, int64_t rows, int cols,
-                                                            uint8_t* q, uint8_t* scale) {
+                                                            uint8_t* q, uint8_t* scale, int64_t scale_ld) {
   const int nb = cols / 32;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= rows * nb) return;
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint16_t* x, i
   uint4* dst = (uint4*)(q + r * cols + b * 32);
   dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
   dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
-  scale[r * nb + b] = (uint8_t)code;
+  scale[r * scale_ld + b] = (uint8_t)code;
 }
 
 // One thread per (group, 32-row block along K, column).
@@ -71,11 +71,12 @@ __global__ __launch_bounds__(256) void mx_quant_cols_kernel(const uint16_t* w, i
   col_scale[(((int64_t)g * (K / 64) + kb / 2) * N + n) * 2 + (kb & 1)] = (uint8_t)code;
 }
 
-int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, hipStream_t st) {
+int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
+                        hipStream_t st) {
   int64_t n = rows * (cols / 32);
   if (n == 0) return MI355MOE_OK;
   hipLaunchKernelGGL(mx_quant_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, rows, cols, q,
-                     scale);
+                     scale, scale_ld);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
@@ -83,7 +84,7 @@ extern "C" int mi355moe_mx_quantize_rows(const uint16_t* x, int64_t rows, int32_
                                          uint8_t* scale, void* stream) {
   if (rows < 0 || cols <= 0 || cols % 32) return MI355MOE_EINVAL;
   if (rows > 0 && (x == nullptr || q == nullptr || scale == nullptr)) return MI355MOE_EINVAL;
-  return mi355_mx_quant_rows(x, rows, cols, q, scale, (hipStream_t)stream);
+  return mi355_mx_quant_rows(x, rows, cols, q, scale, cols / 32, (hipStream_t)stream);
 }
 
 extern "C" int mi355moe_mx_quantize_cols(const uint16_t* w, int32_t groups, int32_t kdim, int32_t cols,
