@@ -176,7 +176,7 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
     c = layer.c
     threads = torch.get_num_threads()
     T = c["T"]
-    sample = min(T, 1024 if c["H"] <= 1024 else 256)
+    sample = min(T, 1024 if c["H"] <= 1024 else 4096)
     x = layer.x[:sample].cpu()
     wr = layer.wr.cpu()
     bias = layer.bias.cpu()
