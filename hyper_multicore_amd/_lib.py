@@ -62,7 +62,7 @@ class ForwardArgs(Structure):
 # (name, restype, argtypes)
 _SIGNATURES = [
     ("mi355moe_abi_version", c_int32, []),
-    ("mi355moe_gate_logits_workspace_size", c_size_t, [c_int64]),
+    ("mi355moe_gate_logits_workspace_size", c_size_t, [c_int64, c_int32, c_int32]),
     ("mi355moe_gate_logits", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
                                        c_void_p, c_void_p, c_size_t, c_void_p]),
     ("mi355moe_gate_route", c_int32, [POINTER(RouteArgs), c_void_p]),

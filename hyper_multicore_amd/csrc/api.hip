@@ -19,21 +19,54 @@ __global__ void mask_to_ids_kernel(const uint8_t* mask, int64_t T, int32_t* ids)
 
 __global__ void single_group_list_kernel(int64_t rows, int64_t* group_list) { group_list[0] = rows; }
 
-extern "C" size_t mi355moe_gate_logits_workspace_size(int64_t num_tokens) {
-  // ids[T] + mapping[T] + gather[T] + group_list[2] + tile_prefix[3] + dispatch workspace
-  return al256((size_t)num_tokens * 4) * 3 + 256 + 256 + mi355moe_dispatch_workspace_size(num_tokens, 1, 2);
+// Split-K factor of the router projection: enough work items for every CU (the tile is 256 x 256,
+// so T=8192 gives only 32 tiles), each split at least 4 K stages of 32. Deterministic: split s
+// writes its own partial buffer and the reduction adds the splits in ascending order.
+static int router_splits(int64_t T, int H, int E) {
+  const int64_t tiles = ((T + 255) / 256) * ((E + 255) / 256);
+  const int kst = H / 32;
+  int best = 1;
+  for (int s = 1; s <= kst / 4; ++s) {
+    if (kst % s) continue;
+    best = s;
+    if (tiles * s >= 512) break;
+  }
+  return best;
+}
+
+extern "C" size_t mi355moe_gate_logits_workspace_size(int64_t num_tokens, int32_t hidden_size, int32_t num_experts) {
+  // ids[T] + mapping[T] + gather[T] + group_list[2] + tile_prefix[3] + dispatch workspace + partials
+  size_t base = al256((size_t)num_tokens * 4) * 3 + 256 + 256 + mi355moe_dispatch_workspace_size(num_tokens, 1, 2);
+  if (hidden_size <= 0 || num_experts <= 0) return base;
+  int s = router_splits(num_tokens, hidden_size, num_experts);
+  return base + (s > 1 ? al256((size_t)s * num_tokens * num_experts * 4) : 0);
+}
+
+// logits[t, e] = sum_s partial[s, row(t), e] in ascending s (row(t) = routed row of token t).
+__global__ void splitk_reduce_kernel(const float* partial, int splits, int64_t split_stride, int64_t T, int E,
+                                     const int32_t* row_of_token_inv, float* out) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * E) return;
+  int64_t r = i / E;
+  int e = (int)(i - r * E);
+  float acc = partial[i];
+  for (int s = 1; s < splits; ++s) acc += partial[s * split_stride + i];
+  int64_t orow = row_of_token_inv ? (int64_t)row_of_token_inv[r] : r;
+  out[orow * E + e] = acc;
 }
 
 extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32_t hidden_size, const uint16_t* w,
                                     const uint16_t* w_vision, const uint8_t* image_mask, int32_t num_experts,
                                     float* logits, void* workspace, size_t workspace_size, void* stream) {
   if (num_tokens < 0 || hidden_size <= 0 || num_experts <= 0 || num_experts > 4096) return MI355MOE_EINVAL;
-  if (hidden_size % 64) return MI355MOE_EUNSUPPORTED;
+  if (hidden_size % 128) return MI355MOE_EUNSUPPORTED;
   if (num_tokens == 0) return MI355MOE_OK;
   if (x == nullptr || w == nullptr || logits == nullptr) return MI355MOE_EINVAL;
   if (num_tokens > INT32_MAX / 2) return MI355MOE_EINVAL;
   const bool dual = w_vision != nullptr && image_mask != nullptr;
-  if (workspace == nullptr || workspace_size < mi355moe_gate_logits_workspace_size(num_tokens)) return -4;
+  if (workspace == nullptr ||
+      workspace_size < mi355moe_gate_logits_workspace_size(num_tokens, hidden_size, num_experts))
+    return -4;
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int32_t* ids = (int32_t*)ws;
@@ -42,6 +75,9 @@ extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32
   int64_t* group_list = (int64_t*)(ws + 3 * al256((size_t)num_tokens * 4));
   int32_t* tile_prefix = (int32_t*)(ws + 3 * al256((size_t)num_tokens * 4) + 256);
   void* dws = ws + 3 * al256((size_t)num_tokens * 4) + 512;
+  float* partial = (float*)(ws + 3 * al256((size_t)num_tokens * 4) + 512 +
+                            mi355moe_dispatch_workspace_size(num_tokens, 1, 2));
+  const int splits = router_splits(num_tokens, hidden_size, num_experts);
   int rc;
   GGParams p = {};
   p.A = (const uint8_t*)x;
@@ -52,8 +88,10 @@ extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32
   p.N = num_experts;
   p.Ntot = num_experts;
   p.n_tiles = (num_experts + mi355_gg_bn() - 1) / mi355_gg_bn();
-  p.C = logits;
+  p.C = splits > 1 ? (void*)partial : (void*)logits;
   p.ldc = num_experts;
+  p.k_splits = splits;
+  p.c_split_stride = (int64_t)num_tokens * num_experts;
   if (dual) {
     hipLaunchKernelGGL(mask_to_ids_kernel, dim3((unsigned)((num_tokens + 255) / 256)), dim3(256), 0, st, image_mask,
                        num_tokens, ids);
@@ -64,7 +102,8 @@ extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32
     p.b_group_stride = (int64_t)((const char*)w_vision - (const char*)w);
     p.a_row_index = gather;
     p.a_row_div = 1;
-    p.c_row_index = gather;
+    // with split-K the partials stay in routed order and the reduction scatters them
+    p.c_row_index = splits > 1 ? nullptr : gather;
   } else {
     hipLaunchKernelGGL(single_group_list_kernel, dim3(1), dim3(1), 0, st, num_tokens, group_list);
     p.G = 1;
@@ -74,7 +113,12 @@ extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32
   p.tile_prefix = tile_prefix;
   rc = mi355_plan_tiles(group_list, p.G, tile_prefix, st);
   if (rc) return rc;
-  return mi355_grouped_gemm(p, false, false, EPI_STORE_F32, st);
+  rc = mi355_grouped_gemm(p, false, false, EPI_STORE_F32, st);
+  if (rc || splits == 1) return rc;
+  const int64_t n = num_tokens * num_experts;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, partial, splits,
+                     p.c_split_stride, num_tokens, num_experts, dual ? gather : nullptr, logits);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -28,6 +28,8 @@ struct GGParams {
   const int32_t* c_row_index;  // optional output row scatter (EPI_STORE_F32)
   uint8_t* c_scale;          // EPI_SWIGLU_MX: [rows, N/32] with row stride c_scale_ld
   int64_t c_scale_ld;
+  int32_t k_splits;          // EPI_STORE_F32 only: >1 splits K; split s writes C + s * c_split_stride
+  int64_t c_split_stride;    // elements
 };
 
 

@@ -287,8 +287,9 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
   if (prefix_in_lds)
     for (int g = tid; g <= p.G; g += GG_THREADS) s_prefix[g] = p.tile_prefix[g];
   __syncthreads();
-  const int total = prefix[p.G] * p.n_tiles;
-  const int nk = p.K * ESIZE / GG_KB;
+  const int splits = (EPI == EPI_STORE_F32 && p.k_splits > 1) ? p.k_splits : 1;
+  const int total = prefix[p.G] * p.n_tiles * splits;
+  const int nk = p.K / splits * ESIZE / GG_KB;  // stages per work item
   const int xcd = blockIdx.x & 7;
   const int per_xcd = gridDim.x >> 3;
   const int slot = blockIdx.x >> 3;
@@ -297,14 +298,16 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     const int L = round * (int)gridDim.x + xcd * per_xcd + slot;
     if (L >= total) break;
     // ---- decode work item -------------------------------------------------------------
+    const int split = splits > 1 ? L % splits : 0;
+    const int LT = splits > 1 ? L / splits : L;
     int lo = 0, hi = p.G - 1;
-    while (lo < hi) {  // largest g with prefix[g]*n_tiles <= L
+    while (lo < hi) {  // largest g with prefix[g]*n_tiles <= LT
       int mid = (lo + hi + 1) >> 1;
-      if (prefix[mid] * p.n_tiles <= L) lo = mid; else hi = mid - 1;
+      if (prefix[mid] * p.n_tiles <= LT) lo = mid; else hi = mid - 1;
     }
     const int g = lo;
     const int mtiles = prefix[g + 1] - prefix[g];
-    const int local = L - prefix[g] * p.n_tiles;
+    const int local = LT - prefix[g] * p.n_tiles;
     const int nt = local / mtiles;
     const int mt = local - nt * mtiles;
     const int64_t row_begin = (g == 0 ? 0 : p.group_list[g - 1]);
@@ -349,6 +352,14 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
       }
     }
     cp.b_stage_stride = B_KN ? (int64_t)(GG_KB / ESIZE) * p.b_row_bytes : GG_KB;
+    if (splits > 1) {
+      const int64_t k0_stages = (int64_t)split * nk;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        cp.a[j] += k0_stages * GG_KB;
+        cp.b[j] += k0_stages * cp.b_stage_stride;
+      }
+    }
     cp.s = nullptr;
     cp.bs_stage_stride = 0;
     if (MX) {
@@ -409,7 +420,7 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
             if (row < rows_valid && col < p.N) {
               int64_t routed = tile_row0 + row;
               int64_t orow = p.c_row_index ? (int64_t)p.c_row_index[routed] : routed;
-              C[orow * p.ldc + col] = acc[mi][ni][r];
+              C[split * p.c_split_stride + orow * p.ldc + col] = acc[mi][ni][r];
             }
           }
     } else if (EPI == EPI_STORE_BF16) {

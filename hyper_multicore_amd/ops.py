@@ -80,7 +80,7 @@ def gate_logits(x: torch.Tensor, weight: torch.Tensor, weight_vision: torch.Tens
     T, H = x.shape
     E = weight.shape[0]
     out = torch.empty((T, E), dtype=torch.float32, device=device)
-    ws = _workspace(lib.mi355moe_gate_logits_workspace_size(T), device)
+    ws = _workspace(lib.mi355moe_gate_logits_workspace_size(T, H, E), device)
     rc = lib.mi355moe_gate_logits(_ptr(x), T, H, _ptr(weight), _ptr(weight_vision), _ptr(image_mask), E,
                                   _ptr(out), _ptr(ws), ws.numel(), _stream(device))
     _lib.check(rc, "mi355moe_gate_logits")

@@ -48,14 +48,14 @@ int mi355moe_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
  * Router projection: logits[t, e] = sum_h x[t, h] * w[e, h], bf16 inputs, fp32 accumulate and
- * fp32 output. Replaces the fp32 projection F.linear(x.float(), W.float())
+ * fp32 output (deterministic split-K: fixed K chunks summed in ascending order). H % 128 == 0. Replaces the fp32 projection F.linear(x.float(), W.float())
  * (modules/mega_gate/function.py:176-178, modules/mega_gate/module.py:195-198); bf16 x bf16
  * products are exact in fp32, only the summation order differs from the reference.
  * When w_vision and image_mask are given, tokens with image_mask[t] != 0 use w_vision instead of
- * w (per-modality router matrices); this needs `workspace` of
- * mi355moe_gate_logits_workspace_size() bytes, otherwise workspace may be NULL.
+ * w (per-modality router matrices). `workspace` must hold
+ * mi355moe_gate_logits_workspace_size() bytes.
  */
-size_t mi355moe_gate_logits_workspace_size(int64_t num_tokens);
+size_t mi355moe_gate_logits_workspace_size(int64_t num_tokens, int32_t hidden_size, int32_t num_experts);
 int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32_t hidden_size,
                          const uint16_t* w, const uint16_t* w_vision, const uint8_t* image_mask,
                          int32_t num_experts, float* logits, void* workspace,
