@@ -11,7 +11,7 @@ from ctypes import POINTER, Structure, c_float, c_int32, c_int64, c_size_t, c_ui
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmi355moe.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
@@ -75,11 +75,14 @@ _SIGNATURES = [
     ("mi355moe_mx_quantize_rows", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p]),
     ("mi355moe_mx_quantize_cols", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                             c_void_p]),
+    ("mi355moe_mx_weight_scale_ld", c_int64, [c_int32]),
+    ("mi355moe_mx_weight_to_eoi", c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                            c_void_p]),
     ("mi355moe_grouped_gemm_workspace_size", c_size_t, [c_int32]),
     ("mi355moe_grouped_gemm_bf16", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                              c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("mi355moe_grouped_gemm_mxfp8", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
-                                              c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+                                              c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("mi355moe_moe_forward_workspace_size", c_size_t, [POINTER(ForwardArgs)]),
     ("mi355moe_moe_forward", c_int32, [POINTER(ForwardArgs), c_void_p, c_size_t, c_void_p]),
 ]

@@ -161,10 +161,13 @@ extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32
 }
 
 extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,
-                                           const uint8_t* col_data, const uint8_t* col_scale, int32_t num_groups,
-                                           int32_t ndim, const int64_t* group_list, uint16_t* out, void* workspace,
-                                           size_t workspace_size, void* stream) {
+                                           const uint8_t* col_data, const uint8_t* col_scale, int32_t layout,
+                                           int32_t num_groups, int32_t ndim, const int64_t* group_list, uint16_t* out,
+                                           void* workspace, size_t workspace_size, void* stream) {
   if (rows < 0 || kdim <= 0 || ndim <= 0 || num_groups <= 0 || num_groups > 4096) return MI355MOE_EINVAL;
+  if (layout != MI355MOE_LAYOUT_EIO && layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
+  const bool eoi = layout == MI355MOE_LAYOUT_EOI;
+  if (eoi && !mi355_mx_eoi_enabled()) return MI355MOE_EUNSUPPORTED;
   // the GEMM fetches 16 activation scale codes per row at a time: K/32 must be a multiple of 16
   if (kdim % 512 || ndim % 16) return MI355MOE_EUNSUPPORTED;
   if (rows == 0) return MI355MOE_OK;
@@ -181,9 +184,10 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
   p.a_scale_ld = kdim / 32;
   p.B = col_data;
   p.b_group_stride = (int64_t)kdim * ndim;
-  p.b_row_bytes = ndim;
+  p.b_row_bytes = eoi ? kdim : ndim;
   p.b_scale = col_scale;
-  p.b_scale_group_stride = (int64_t)(kdim / 64) * ndim * 2;
+  p.b_scale_ld = mi355_mx_scale_ld(kdim);
+  p.b_scale_group_stride = eoi ? (int64_t)ndim * p.b_scale_ld : (int64_t)(kdim / 64) * ndim * 2;
   p.K = kdim;
   p.N = ndim;
   p.Ntot = ndim;
@@ -195,7 +199,7 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
   p.ldc = ndim;
   int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st);
   if (rc) return rc;
-  return mi355_grouped_gemm(p, true, true, EPI_STORE_BF16, st);
+  return mi355_grouped_gemm(p, true, !eoi, EPI_STORE_BF16, st);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -236,7 +240,7 @@ static int validate_fwd(const MI355MoeForwardArgs& a) {
   if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;
   if (a.precision == MI355MOE_PRECISION_MXFP8) {
-    if (a.weight_layout != MI355MOE_LAYOUT_EIO) return MI355MOE_EINVAL;
+    if (a.weight_layout == MI355MOE_LAYOUT_EOI && !mi355_mx_eoi_enabled()) return MI355MOE_EUNSUPPORTED;
     if (a.hidden_size % 128 || a.intermediate_size % 128) return MI355MOE_EUNSUPPORTED;
   } else {
     if (a.hidden_size % 64 || a.intermediate_size % 64) return MI355MOE_EUNSUPPORTED;
@@ -310,7 +314,8 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.b_group_stride = (int64_t)H * 2 * I * esize;
   p1.b_row_bytes = eoi ? (int64_t)H * esize : (int64_t)2 * I * esize;
   p1.b_scale = a.w1_scale;
-  p1.b_scale_group_stride = (int64_t)(H / 64) * 2 * I * 2;
+  p1.b_scale_ld = mi355_mx_scale_ld(H);
+  p1.b_scale_group_stride = eoi ? (int64_t)2 * I * p1.b_scale_ld : (int64_t)(H / 64) * 2 * I * 2;
   p1.K = H;
   p1.N = I;
   p1.Ntot = 2 * I;
@@ -336,7 +341,8 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p2.b_group_stride = (int64_t)I * H * esize;
   p2.b_row_bytes = eoi ? (int64_t)I * esize : (int64_t)H * esize;
   p2.b_scale = a.w2_scale;
-  p2.b_scale_group_stride = (int64_t)(I / 64) * H * 2;
+  p2.b_scale_ld = mi355_mx_scale_ld(I);
+  p2.b_scale_group_stride = eoi ? (int64_t)H * p2.b_scale_ld : (int64_t)(I / 64) * H * 2;
   p2.K = I;
   p2.N = H;
   p2.Ntot = H;

@@ -7,13 +7,17 @@
 // in rounds so that each XCD takes a contiguous run of items per round (m fastest): items that
 // share a weight slice run at the same time on one XCD and share its L2.
 //
-// Workgroup: 512 threads = 8 wavefronts (two per SIMD, which both the HBM stream and the LDS
-// read rate need) in a 4 (M) x 2 (N) grid; tile BM=256 x BN=256; each wavefront computes
-// 64 x 128 with 2 x 4 32x32 MFMAs (bf16: v_mfma_f32_32x32x16_bf16; MXFP8:
-// v_mfma_scale_f32_32x32x64_f8f6f4 with per-lane e8m0 scales: lane r + 32b supplies the scale
-// of 32-block b of row / column r, and its operand bytes 0-15 / 16-31 hold K = 16b + i /
-// 32 + 16b + i of the 64-K step). A stage holds 64 bytes of K per row (32 bf16 or 64 e4m3);
-// global -> LDS copies use the direct-to-LDS loads into a 4-deep ring (three stages in flight).
+// Workgroup: 256 threads = 4 wavefronts, one per SIMD, in a 2 (M) x 2 (N) grid; tile BM=256 x
+// BN=256; each wavefront computes 128 x 128 with 4 x 4 32x32 MFMAs (bf16:
+// v_mfma_f32_32x32x16_bf16; MXFP8: v_mfma_scale_f32_32x32x64_f8f6f4 with per-lane e8m0 scales:
+// lane r + 32b supplies the scale of 32-block b of row / column r, and its operand bytes 0-15 /
+// 16-31 hold K = 16b + i / 32 + 16b + i of the 64-K step). With one wave per SIMD each wave owns
+// 512 registers: the accumulators live in the AGPRs, two stages of operand fragments in VGPRs.
+// A stage holds 64 bytes of K per row (32 bf16 or 64 e4m3). Global -> LDS copies use the
+// direct-to-LDS loads into decoupled rings (activations 3 slots, weights 5 slots). Each K step is
+// software-pipelined inside the wave: after the stage barrier the wave interleaves the MFMAs of
+// stage k with the LDS fragment reads of stage k+1 and with its share of the copies that refill
+// the slots of stage k, so the matrix cores, the LDS and the copy engine work at the same time.
 //
 // LDS layouts (16-byte chunk granularity, XOR swizzled against bank conflicts):
 //   K-contiguous operand rows (A always; B in EOI layout): row r at r*64, chunk c stored at
@@ -21,8 +25,9 @@
 //   N-contiguous B (EIO bf16 / MX col_data): row k holds 256 columns; bf16 chunk c stored at
 //     c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows); read
 //     with the transposing ds_read_b64_tr_b16 / ds_read_b64_tr_b8.
-//   MX scales per stage: A one dword per row (the row's two e8m0 codes, 2-byte DMA zero-extends),
-//     B the two codes of every tile column (col_scale's [.., N, 2] pairs).
+//   MX scales: A rows get 16 codes (8 stages) per copy into a 2-slot ring; B in EIO layout the two
+//     codes of every tile column per stage (col_scale's [.., N, 2] pairs) with the B stage; B in
+//     EOI layout 16 codes per column per 8 stages, like A.
 //
 // Epilogues: bf16 store, fp32 store (router logits, optional row scatter), SwiGLU -> bf16 and
 // SwiGLU -> MXFP8 requant. For SwiGLU the B tile columns are gate/up interleaved in 64-column
@@ -33,39 +38,72 @@
 #include "../../include/mi355moe.h"
 #include "gemm.h"
 
+// Tile configuration: one 4-wave workgroup per CU (one wave per SIMD, so each wave owns the
+// SIMD's whole register file: 128 x 128 fp32 accumulators plus two stages of operand fragments).
 #define GG_BM 256
 #define GG_BN 256
+#define GG_WAVES 4
+#define GG_WM 128  // rows per wave
+#define GG_MI (GG_WM / 32)
+#define GG_A_SLOTS 3
+#define GG_B_SLOTS 5
+#define GG_PREFIX_MAX 1024
 #define GG_KB 64  // bytes of K per stage per row
-#define GG_THREADS 512
-#define GG_WAVES 8
+#define GG_THREADS (64 * GG_WAVES)
 
 struct GGLds {
   // Decoupled rings: activations A (re-read from L2 by the tiles of one expert) and weights B
-  // (streamed once from HBM, so it gets the deeper ring: five stages = 80 KB in flight per CU).
+  // (streamed once from HBM, so it gets the deeper ring).
   static constexpr int A_BYTES = GG_BM * GG_KB;        // 16 KB
   static constexpr int B_BYTES = GG_BN * GG_KB;        // 16 KB
   static constexpr int BS_BYTES = GG_BN * 2;           // 512 B (MX: two codes per column)
   static constexpr int B_SLOT = B_BYTES + BS_BYTES;
-  static constexpr int A_SLOTS = 3;                    // A(k+2) issued at iteration k
-  static constexpr int B_SLOTS = 6;                    // B(k+5) issued at iteration k
+  static constexpr int A_SLOTS = GG_A_SLOTS;           // A(k + A_SLOTS) issued at iteration k
+  static constexpr int B_SLOTS = GG_B_SLOTS;           // B(k + B_SLOTS) issued at iteration k
   static constexpr int AS_GROUP = 8;                   // MX: A scale codes fetched per 8 stages
-  static constexpr int AS_SLOT = GG_BM * 16;           // 4 KB: 16 codes per row
+  static constexpr int AS_SLOT = GG_BM * 16;           // 16 codes per row
   static constexpr int B_OFF = A_SLOTS * A_BYTES;
   static constexpr int AS_OFF = B_OFF + B_SLOTS * B_SLOT;
-  static constexpr int PREFIX_MAX = 1024;              // groups whose tile prefix is kept in LDS
-  static constexpr int PREFIX_OFF = AS_OFF + 2 * AS_SLOT;
+  static constexpr int PREFIX_MAX = GG_PREFIX_MAX;     // groups whose tile prefix is kept in LDS
+  static constexpr int BSR_SLOT = GG_BN * 16;          // MX NK weights: 16 scale codes per column
+  static constexpr int BSR_OFF = AS_OFF + 2 * AS_SLOT;
+  static constexpr int PREFIX_OFF = BSR_OFF + 2 * BSR_SLOT;
   static constexpr int TOTAL = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
-  static_assert(GG_BM * (GG_BN * 2 + 16) <= AS_OFF, "bf16 epilogue staging must fit the rings");
-  static_assert(GG_BM * (128 * 4 + 16) <= AS_OFF, "SwiGLU epilogue staging must fit the rings");
+  // DMA instructions per wave per stage (64 lanes x 16 bytes each)
+  static constexpr int A_INSTR = GG_BM * (GG_KB / 16) / 64 / GG_WAVES;
+  static constexpr int B_INSTR = GG_BN * (GG_KB / 16) / 64 / GG_WAVES;
+  static constexpr int AS_WAVES = GG_BM / 64;          // waves that fetch A scale rows (64 each)
+  // epilogue staging (overlays the rings and the A scale slots, never the tile prefix)
+  static constexpr int EPI_RS_BF16 = GG_BN * 2 + 16;   // bf16 row stride
+  static constexpr int EPI_RS_ACT = 128 * 4 + 16;      // SwiGLU fp32 row stride
+  static_assert(A_SLOTS >= 3 && A_SLOTS <= B_SLOTS, "ring depths");
+  static_assert(GG_BM * EPI_RS_BF16 <= PREFIX_OFF, "bf16 epilogue staging must fit");
+  static_assert(GG_BM * EPI_RS_ACT <= PREFIX_OFF, "SwiGLU epilogue staging must fit");
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
+  static_assert(AS_WAVES <= GG_WAVES && GG_WAVES >= 2, "MX scale copies need waves");
 };
 
+// Direct global -> LDS copy: lane i of the wave writes its SZ bytes at LDS address M0 + SZ*i
+// (SZ = 16) or M0 + 4*i (SZ = 4). Written as inline assembly on purpose: for the compiler's
+// builtin, the backend must assume the copy may alias every later LDS read and inserts a wait for
+// all outstanding vector-memory loads before the next ds_read, which would drain the whole
+// prefetch ring each stage. Completion is tracked here with explicit vmcnt waits (loads of a wave
+// retire in order) and made visible to the other waves by the following workgroup barrier.
+// M0 is a reserved register that the compiler sets right before each of its own uses, so the
+// assembly may overwrite it.
 template <int SZ>
-MI355_DEV void lds_dma(const void* g, uint32_t lds_off_uniform, uint8_t* smem) {
-  auto* dst = (__attribute__((address_space(3))) void*)(smem + lds_off_uniform);
-  if constexpr (SZ == 16) __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
-  else if constexpr (SZ == 4) __builtin_amdgcn_global_load_lds(g, dst, 4, 0, 0);
-  else if constexpr (SZ == 2) __builtin_amdgcn_global_load_lds(g, dst, 2, 0, 0);
+MI355_DEV void lds_dma(const void* g, uint32_t lds_off_uniform, uint8_t* smem, int enable = 1) {
+  // `enable` (wave-uniform) skips the copy inside the assembly, so a conditional copy adds no
+  // branch to the surrounding code and the MFMAs around it keep their place.
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(smem + lds_off_uniform));
+  const int en = __builtin_amdgcn_readfirstlane(enable);
+  if constexpr (SZ == 16)
+    asm volatile("s_cmp_eq_u32 %2, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc");
+  else if constexpr (SZ == 4)
+    asm volatile("s_cmp_eq_u32 %2, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dword %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc");
   else static_assert(SZ == 16, "unsupported DMA size");
 }
 // Workgroup barrier without the release fence of __syncthreads (which would wait for every
@@ -75,15 +113,20 @@ MI355_DEV void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 }
-// Wait until at most N vector-memory loads of this wave are outstanding (loads retire in order).
-template <int N>
-MI355_DEV void wait_vm_le() {
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else static_assert(N == 0, "unsupported vmcnt");
+// Wait until at most n vector-memory loads of this wave are outstanding (loads retire in order).
+// n is wave-uniform; the switch maps it onto the immediate of s_waitcnt.
+MI355_DEV void wait_vm(int n) {
+  switch (n) {
+#define GG_WAIT_CASE(N) case N: asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); break;
+    GG_WAIT_CASE(1) GG_WAIT_CASE(2) GG_WAIT_CASE(3) GG_WAIT_CASE(4) GG_WAIT_CASE(5) GG_WAIT_CASE(6)
+    GG_WAIT_CASE(7) GG_WAIT_CASE(8) GG_WAIT_CASE(9) GG_WAIT_CASE(10) GG_WAIT_CASE(11) GG_WAIT_CASE(12)
+    GG_WAIT_CASE(13) GG_WAIT_CASE(14) GG_WAIT_CASE(15) GG_WAIT_CASE(16) GG_WAIT_CASE(17) GG_WAIT_CASE(18)
+    GG_WAIT_CASE(19) GG_WAIT_CASE(20) GG_WAIT_CASE(21) GG_WAIT_CASE(22) GG_WAIT_CASE(23) GG_WAIT_CASE(24)
+#undef GG_WAIT_CASE
+    default:
+      if (n <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  }
 }
 
 // Tile column j (0..255) -> weight column. SwiGLU: per 128-column half h, 64 gate then 64 up.
@@ -100,53 +143,17 @@ MI355_DEV int a_chunk_off(int r, int c) { return r * GG_KB + ((c ^ ((r >> 2) & 3
 MI355_DEV v8bf read_a_bf16(const uint8_t* As, int r, int ks, int lane) {
   return *(const v8bf*)(As + a_chunk_off(r, ks * 2 + (lane >> 5)));
 }
-template <bool B_KN>
-MI355_DEV v8bf read_b_bf16(const uint8_t* Bs, int wn, int ni, int ks, int lane) {
-  if (!B_KN) {
-    int n = wn * 128 + ni * 32 + (lane & 31);
-    return *(const v8bf*)(Bs + a_chunk_off(n, ks * 2 + (lane >> 5)));
-  }
-  int g16 = lane >> 4, m = lane & 15;
-  int nb = wn * 128 + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
-  int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2);
-  int k1 = k0 + 4;
-  int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
-  int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
-  v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off0));
-  v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
-  typedef __attribute__((ext_vector_type(8))) short v8s;
-  v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(v8bf, both);
-}
-MI355_DEV v8i read_a_mx(const uint8_t* As, int r, int lane) {
-  int c0 = lane >> 5;
-  v4i lo = *(const v4i*)(As + a_chunk_off(r, c0));
-  v4i hi = *(const v4i*)(As + a_chunk_off(r, c0 + 2));
-  return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-MI355_DEV v8i read_b_mx(const uint8_t* Bs, int wn, int ni, int lane) {
-  int g16 = lane >> 4, m = lane & 15;
-  int nb = wn * 128 + ni * 32 + (g16 & 1) * 16;
-  int parts[8];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    int k = (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
-    int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
-    v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
-    parts[2 * q] = v[0];
-    parts[2 * q + 1] = v[1];
-  }
-  return (v8i){parts[0], parts[1], parts[2], parts[3], parts[4], parts[5], parts[6], parts[7]};
-}
 
 // ---- copy plan -------------------------------------------------------------------------------
-// Per stage the workgroup copies A 16 KB and B 16 KB: each wave issues 2 + 2 16-byte DMA
-// instructions; MX adds the B scale codes (waves 4-5, one 4-byte DMA for 128 columns each) and,
-// every 8 stages, 16 A scale codes per row (waves 0-3, one 16-byte DMA for 64 rows each).
+// Per stage each wave issues A_INSTR + B_INSTR 16-byte DMA instructions; MX adds the B scale codes
+// (waves 0 and 1, one 4-byte DMA for 128 columns each) and, every 8 stages, 16 A scale codes per
+// row (AS_WAVES waves, one 16-byte DMA for 64 rows each).
 struct CopyPlan {
-  const uint8_t* a[2];
-  const uint8_t* b[2];
-  const uint8_t* s;        // MX: A scale row (waves 0-3) or B scale column pair (waves 4-5)
+  const uint8_t* a[GGLds::A_INSTR];
+  const uint8_t* b[GGLds::B_INSTR];
+  const uint8_t* s;        // MX: A scale row (waves < AS_WAVES)
+  const uint8_t* bs;       // MX KN: B scale column pair (waves 0 and 1)
+  const uint8_t* bsr;      // MX NK: B scale row (row wave*64 + lane of the tile)
   int64_t b_stage_stride;  // bytes to advance B per stage
   int64_t bs_stage_stride; // bytes to advance the B scales per stage
 };
@@ -159,116 +166,297 @@ MI355_DEV void issue_a(const CopyPlan& cp, int kt, int wave, uint8_t* smem) {
   const uint32_t base = (kt % GGLds::A_SLOTS) * GGLds::A_BYTES;
   const int64_t koff = (int64_t)kt * GG_KB;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) lds_dma<16>(cp.a[j] + koff, base + (wave * 2 + j) * 1024, smem);
+  for (int j = 0; j < GGLds::A_INSTR; ++j)
+    lds_dma<16>(cp.a[j] + koff, base + (wave * GGLds::A_INSTR + j) * 1024, smem);
 }
-template <bool MX>
+MI355_DEV bool is_bs_wave(int wave) { return wave < 2; }
+template <bool MX, bool B_KN>
 MI355_DEV void issue_b(const CopyPlan& cp, int kt, int wave, uint8_t* smem) {
+  // (MX with K-contiguous weights has no per-stage scale copy: its scales come in groups)
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
   const uint32_t base = GGLds::B_OFF + (kt % GGLds::B_SLOTS) * GGLds::B_SLOT;
   const int64_t boff = (int64_t)kt * cp.b_stage_stride;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) lds_dma<16>(cp.b[j] + boff, base + (wave * 2 + j) * 1024, smem);
-  if (MX && (wave == 4 || wave == 5))
-    lds_dma<4>(cp.s + kt * cp.bs_stage_stride, base + GGLds::B_BYTES + (wave - 4) * 256, smem);
+  for (int j = 0; j < GGLds::B_INSTR; ++j)
+    lds_dma<16>(cp.b[j] + boff, base + (wave * GGLds::B_INSTR + j) * 1024, smem);
+  if (MX && B_KN && is_bs_wave(wave))
+    lds_dma<4>(cp.bs + kt * cp.bs_stage_stride, base + GGLds::B_BYTES + wave * 256, smem);
 }
 // MX: A scale codes of stages 8*grp .. 8*grp+7 (16 bytes per row) into AS slot grp & 1.
 MI355_DEV void issue_as(const CopyPlan& cp, int grp, int wave, uint8_t* smem) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
-  if (wave < 4) lds_dma<16>(cp.s + grp * 16, GGLds::AS_OFF + (grp & 1) * GGLds::AS_SLOT + wave * 1024, smem);
+  if (wave < GGLds::AS_WAVES)
+    lds_dma<16>(cp.s + grp * 16, GGLds::AS_OFF + (grp & 1) * GGLds::AS_SLOT + wave * 1024, smem);
 }
 
-// K loop. Issue order (per wave): B0 B1 B2 AS0 A0 B3 A1 B4 | A2 B5 [AS1] | A3 B6 | ... : iteration
-// k issues A(k+2), B(k+5) and, every 8 stages, the next A scale group. At the top of iteration k
-// the loads younger than A(k) are B(k+3), A(k+1), B(k+4) (plus scale groups on waves 0-3), so
-// waiting for at most that many keeps A(k), B(k) and the scale group of stage k complete.
-// A wave whose 32 A rows (and 64 scale rows) all lie past the tile's last valid row copies no
-// A at all (LA = false, decode and ragged tiles); it waits on its B groups alone: younger than
-// B(k) are B(k+1) .. B(k+4).
-// NM = number of valid 32-row subtiles this wave computes (0..2).
-template <int N>
-MI355_DEV void wait_vm_b_only(int ahead) {
-  // ahead = number of later B groups issued (0..4), 2 loads each at least
-  if (ahead >= 4) wait_vm_le<8>();
-  else if (ahead == 3) wait_vm_le<6>();
-  else if (ahead == 2) wait_vm_le<4>();
-  else if (ahead == 1) wait_vm_le<2>();
-  else wait_vm_le<0>();
+#ifdef GG_TRACE
+__device__ unsigned long long gg_trace[4 * 8 * 64 * 5];
+#define GG_T(pt) if (blockIdx.x < 4 && k < 64 && lane == 0) gg_trace[((blockIdx.x * 8 + wave) * 64 + k) * 5 + pt] = __builtin_amdgcn_s_memtime();
+extern "C" int mi355_gg_trace_read(void* host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(gg_trace), sizeof(gg_trace)) == hipSuccess ? 0 : -1;
 }
+#else
+#define GG_T(pt)
+#endif
+
+// Operand fragments of one stage for one wave (GG_WM rows x 128 columns x one stage of K). Values
+// that are read in several LDS instructions are kept as the raw pieces and joined only when the
+// MFMA consumes them, so that issuing the reads never forces a wait for their data.
+template <bool MX, bool B_KN> struct Frags;
+template <> struct Frags<false, false> { v8bf a[2][GG_MI], b[2][4]; };  // [ks][mi], [ks][ni]
+template <> struct Frags<false, true> { v8bf a[2][GG_MI]; v4s bl[2][4], bh[2][4]; };
+template <> struct Frags<true, true> { v4i al[GG_MI], ah[GG_MI]; v2i bp[4][4]; int sa[GG_MI], sb[4]; };
+template <> struct Frags<true, false> { v4i al[GG_MI], ah[GG_MI], bl[4], bh[4]; int sa[GG_MI], sb[4]; };
+
+// Element-wise fragment reads and MFMAs and the copies of one iteration, so that one pipelined
+// step can interleave them: MFMA t, then its share of the LDS reads of the next stage
+// and of the DMA copies. The wave never stalls on the DMA queue or on the LDS return queue for
+// long while the matrix core has work.
+template <bool MX, int NM> struct StepShape {
+  static constexpr int MFMAS = MX ? NM * 4 : 2 * NM * 4;
+  static constexpr int READS = MX ? 4 + NM : 2 * (4 + NM);  // fragment elements of a stage
+  static constexpr int ITEMS = GGLds::B_INSTR + 1 + GGLds::A_INSTR;  // B copies, B scales, A copies
+};
+
+template <bool MX, bool B_KN, int NM>
+MI355_DEV void read_elem(Frags<MX, B_KN>& f, int e, const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs,
+                         const uint8_t* BSRs, int wm, int wn, int lane) {
+  if constexpr (!MX) {
+    const int ks = e / (4 + NM), q = e % (4 + NM);
+    if (q < 4) {
+      if constexpr (!B_KN) {
+        const int n = wn * 128 + q * 32 + (lane & 31);
+        f.b[ks][q] = *(const v8bf*)(Bs + a_chunk_off(n, ks * 2 + (lane >> 5)));
+      } else {
+        const int g16 = lane >> 4, m = lane & 15;
+        const int nb = wn * 128 + q * 32 + (g16 & 1) * 16 + 4 * (m & 3);
+        const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
+        const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
+        const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
+        f.bl[ks][q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off0));
+        f.bh[ks][q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
+      }
+    } else {
+      f.a[ks][q - 4] = read_a_bf16(As, wm * GG_WM + (q - 4) * 32 + (lane & 31), ks, lane);
+    }
+  } else {
+    if (e < 4) {
+      if constexpr (B_KN) {
+        const int g16 = lane >> 4, m = lane & 15;
+        const int nb = wn * 128 + e * 32 + (g16 & 1) * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int k = (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
+          const int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
+          f.bp[e][q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
+        }
+        f.sb[e] = Bs[GGLds::B_BYTES + (wn * 128 + e * 32 + (lane & 31)) * 2 + (lane >> 5)];
+      } else {
+        // K-contiguous weight rows: same fragment layout as the activations
+        const int n = wn * 128 + e * 32 + (lane & 31);
+        const int c0 = lane >> 5;
+        f.bl[e] = *(const v4i*)(Bs + a_chunk_off(n, c0));
+        f.bh[e] = *(const v4i*)(Bs + a_chunk_off(n, c0 + 2));
+        f.sb[e] = BSRs[n * 16 + (lane >> 5)];
+      }
+    } else {
+      const int r = wm * GG_WM + (e - 4) * 32 + (lane & 31);
+      const int c0 = lane >> 5;
+      f.al[e - 4] = *(const v4i*)(As + a_chunk_off(r, c0));
+      f.ah[e - 4] = *(const v4i*)(As + a_chunk_off(r, c0 + 2));
+      f.sa[e - 4] = ASs[r * 16 + (lane >> 5)];
+    }
+  }
+}
+
+template <bool MX, bool B_KN, int NM>
+MI355_DEV void mfma_elem(const Frags<MX, B_KN>& f, v16f (&acc)[GG_MI][4], int t) {
+  if constexpr (!MX) {
+    const int ks = t / (NM * 4), mi = (t / 4) % NM, ni = t % 4;
+    v8bf b;
+    if constexpr (!B_KN) b = f.b[ks][ni];
+    else b = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.bl[ks][ni], f.bh[ks][ni], 0, 1, 2, 3, 4, 5, 6, 7));
+    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[ks][mi], b, acc[mi][ni], 0, 0, 0);
+  } else {
+    const int mi = t / 4, ni = t % 4;
+    const v8i a = __builtin_shufflevector(f.al[mi], f.ah[mi], 0, 1, 2, 3, 4, 5, 6, 7);
+    v8i b;
+    if constexpr (B_KN) {
+      const v4i b01 = __builtin_shufflevector(f.bp[ni][0], f.bp[ni][1], 0, 1, 2, 3);
+      const v4i b23 = __builtin_shufflevector(f.bp[ni][2], f.bp[ni][3], 0, 1, 2, 3);
+      b = __builtin_shufflevector(b01, b23, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      b = __builtin_shufflevector(f.bl[ni], f.bh[ni], 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[mi][ni], 0, 0, 0, f.sa[mi], 0, f.sb[ni]);
+  }
+}
+
+// Copy item it of iteration i (same order as issue_iteration: B copies, B scales, A copies).
+template <bool MX, bool B_KN, bool LA>
+MI355_DEV void issue_item(const CopyPlan& cp, int i, int nk, int wave, uint8_t* smem, int it) {
+#ifdef GG_ABLATE_DMA
+  if (wave < 64) return;
+#endif
+  constexpr int DA = GGLds::A_SLOTS, DB = GGLds::B_SLOTS;
+  if (it < GGLds::B_INSTR) {
+    const int kt = i + DB;
+    lds_dma<16>(cp.b[it] + (int64_t)kt * cp.b_stage_stride,
+                GGLds::B_OFF + (kt % GGLds::B_SLOTS) * GGLds::B_SLOT + (wave * GGLds::B_INSTR + it) * 1024, smem,
+                kt < nk);
+  } else if (it == GGLds::B_INSTR) {
+    const int kt = i + DB;
+    if constexpr (MX && B_KN)
+      lds_dma<4>(cp.bs + kt * cp.bs_stage_stride,
+                 GGLds::B_OFF + (kt % GGLds::B_SLOTS) * GGLds::B_SLOT + GGLds::B_BYTES + (wave & 1) * 256, smem,
+                 is_bs_wave(wave) && kt < nk);
+  } else if constexpr (LA) {
+    const int j = it - GGLds::B_INSTR - 1;
+    const int kt = i + DA;
+    lds_dma<16>(cp.a[j] + (int64_t)kt * GG_KB, (kt % GGLds::A_SLOTS) * GGLds::A_BYTES + (wave * GGLds::A_INSTR + j) * 1024,
+                smem, kt < nk);
+  }
+}
+
+// MX: the scale groups due at iteration i (every AS_GROUP stages: A rows and, for K-contiguous
+// weights, B rows), each as one conditional copy.
+template <bool MX, bool B_KN, bool LA>
+MI355_DEV void issue_scales_item(const CopyPlan& cp, int i, int nk, int wave, uint8_t* smem) {
+#ifdef GG_ABLATE_DMA
+  if (wave < 64) return;
+#endif
+  if constexpr (MX) {
+    const int grp = i / GGLds::AS_GROUP + 1;
+    const bool due = (i & (GGLds::AS_GROUP - 1)) == 0 && i + GGLds::AS_GROUP < nk;
+    if constexpr (LA)
+      lds_dma<16>(cp.s + grp * 16, GGLds::AS_OFF + (grp & 1) * GGLds::AS_SLOT + (wave & 3) * 1024, smem,
+                  due && wave < GGLds::AS_WAVES);
+    if constexpr (!B_KN)
+      lds_dma<16>(cp.bsr + grp * 16, GGLds::BSR_OFF + (grp & 1) * GGLds::BSR_SLOT + (wave & 3) * 1024, smem, due);
+  }
+}
+
+// Loads of stage j still allowed in flight (younger than stage j's last load) once iterations
+// up to `last` have issued. Iteration i issues B(i + DB), then A(i + DA) (DB = B_SLOTS >= DA =
+// A_SLOTS; the prologue runs iterations -DB .. -1), each only below nk. Stage j's last load is A(j)
+// (iteration j - DA; B(j) came earlier) for a wave that copies A, else B(j) (iteration j - DB).
+// Scale groups issued between are not counted, which only makes the wait stricter. Loads of one
+// wave retire in order.
+template <bool LA>
+MI355_DEV int younger_than(int j, int last, int nk, int la_n, int lb_n) {
+  constexpr int DA = GGLds::A_SLOTS, DB = GGLds::B_SLOTS;
+  const int from = (LA ? j - DA : j - DB) + 1;
+  // iterations i in [from, last] with i + DB < nk, and (A) with 0 <= i + DA < nk
+  const int nb = min(last, nk - DB - 1) - from + 1;
+  int n = (nb > 0 ? nb : 0) * lb_n;
+  if (LA) {
+    const int na = min(last, nk - DA - 1) - max(from, -DA) + 1;
+    n += (na > 0 ? na : 0) * la_n;
+  }
+  return n;
+}
+
+template <bool MX, bool B_KN, bool LA>
+MI355_DEV void issue_iteration(const CopyPlan& cp, int i, int nk, int wave, uint8_t* smem) {
+  constexpr int DA = GGLds::A_SLOTS, DB = GGLds::B_SLOTS;
+  if (i + DB < nk) issue_b<MX, B_KN>(cp, i + DB, wave, smem);
+  if (LA && i + DA >= 0 && i + DA < nk) {
+    if (MX && i + DA == 0) issue_as(cp, 0, wave, smem);
+    issue_a<MX>(cp, i + DA, wave, smem);
+  }
+  if (LA && MX && i >= 0 && (i & (GGLds::AS_GROUP - 1)) == 0 && i + GGLds::AS_GROUP < nk)
+    issue_as(cp, i / GGLds::AS_GROUP + 1, wave, smem);
+}
+
+// K loop, software-pipelined in each wave: iteration k (after barrier k) refills the ring slots of
+// stage k, reads the fragments of stage k+1 into one register set and runs the MFMAs of stage k
+// from the other, so LDS reads and DMA issue overlap the matrix cores. Before barrier k every wave
+// has waited for its own copies of stage k+1 (so stage k+1 is complete in LDS after the barrier)
+// and drained its LDS reads of stage k (read during iteration k-1), so stage k's slots are free.
+// A-scale group g+1 (stages 8g+8 ..) is issued at iteration 8g into the slot of group g-1, whose
+// last stage was read during iteration 8g-2.
+// NM = number of 32-row subtiles this wave computes (0, 1, 2 or 4).
 template <bool MX, bool B_KN, int NM, bool LA>
 MI355_DEV void k_loop(const CopyPlan& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
-                      v16f (&acc)[2][4]) {
-  for (int j = 0; j < 3 && j < nk; ++j) issue_b<MX>(cp, j, wave, smem);
-  if (LA) {
-    if (MX) issue_as(cp, 0, wave, smem);
-    issue_a<MX>(cp, 0, wave, smem);
+                      v16f (&acc)[GG_MI][4]) {
+  constexpr int DB = GGLds::B_SLOTS;
+  const int la_n = GGLds::A_INSTR;
+  const int lb_n = GGLds::B_INSTR + ((MX && B_KN && is_bs_wave(wave)) ? 1 : 0);  // loads per B stage
+  if constexpr (MX && !B_KN) lds_dma<16>(cp.bsr, GGLds::BSR_OFF + (wave & 3) * 1024, smem);  // B scale group 0
+  for (int i = -DB; i < 0; ++i) issue_iteration<MX, B_KN, LA>(cp, i, nk, wave, smem);
+  Frags<MX, B_KN> f0, f1;
+  wait_vm(younger_than<LA>(0, -1, nk, la_n, lb_n));
+  lds_barrier();
+  if constexpr (NM > 0) {
+    const uint8_t* ASs = smem + GGLds::AS_OFF;
+#pragma unroll
+    for (int e = 0; e < StepShape<MX, NM>::READS; ++e)
+      read_elem<MX, B_KN, NM>(f0, e, smem, smem + GGLds::B_OFF, ASs, smem + GGLds::BSR_OFF, wm, wn, lane);
   }
-  if (nk > 3) issue_b<MX>(cp, 3, wave, smem);
-  if (LA && nk > 1) issue_a<MX>(cp, 1, wave, smem);
-  if (nk > 4) issue_b<MX>(cp, 4, wave, smem);
-  for (int k = 0; k < nk; ++k) {
-    if (LA) {
-      if (k + 4 < nk) wait_vm_le<6>();
-      else if (k + 3 < nk) wait_vm_le<4>();
-      else if (k + 1 < nk) wait_vm_le<2>();
-      else wait_vm_le<0>();
-    } else {
-      wait_vm_b_only<0>(nk - 1 - k < 4 ? nk - 1 - k : 4);
-    }
+  // one pipelined iteration with a next stage (k + 1 < nk)
+  using SS = StepShape<MX, NM>;
+  auto step = [&](int k, Frags<MX, B_KN>& cur, Frags<MX, B_KN>& nxt) {
+    __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs of the previous stage above the barrier
+    GG_T(0)
+    wait_vm(younger_than<LA>(k + 1, k - 1, nk, la_n, lb_n));
+    GG_T(1)
     lds_barrier();
-    if (LA && k + 2 < nk) issue_a<MX>(cp, k + 2, wave, smem);
-    if (k + 5 < nk) issue_b<MX>(cp, k + 5, wave, smem);
-    if (LA && MX && (k & (GGLds::AS_GROUP - 1)) == 0 && k + GGLds::AS_GROUP < nk)
-      issue_as(cp, k / GGLds::AS_GROUP + 1, wave, smem);
-#ifdef GG_ABLATE_COMPUTE
-    if (wave < 64) continue;
-#endif
-    if constexpr (NM > 0) {
-      const uint8_t* As = smem + (k % GGLds::A_SLOTS) * GGLds::A_BYTES;
-      const uint8_t* Bs = smem + GGLds::B_OFF + (k % GGLds::B_SLOTS) * GGLds::B_SLOT;
-      if constexpr (!MX) {
+    __builtin_amdgcn_sched_barrier(0);
+    GG_T(2)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));  // recompute lane-dependent LDS offsets here rather than hold them
+    const int kn = k + 1;
+    const uint8_t* As = smem + (kn % GGLds::A_SLOTS) * GGLds::A_BYTES;
+    const uint8_t* Bs = smem + GGLds::B_OFF + (kn % GGLds::B_SLOTS) * GGLds::B_SLOT;
+    const uint8_t* ASs = smem + GGLds::AS_OFF + ((kn / GGLds::AS_GROUP) & 1) * GGLds::AS_SLOT +
+                         (kn & (GGLds::AS_GROUP - 1)) * 2;
+    const uint8_t* BSRs = smem + GGLds::BSR_OFF + ((kn / GGLds::AS_GROUP) & 1) * GGLds::BSR_SLOT +
+                          (kn & (GGLds::AS_GROUP - 1)) * 2;
+    constexpr int T = SS::MFMAS > 0 ? SS::MFMAS : 1;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          v8bf a[2], b[4];
+    for (int t = 0; t < T; ++t) {
+#ifndef GG_ABLATE_COMPUTE
+      if constexpr (NM > 0) {
+        mfma_elem<MX, B_KN, NM>(cur, acc, t);
 #pragma unroll
-          for (int ni = 0; ni < 4; ++ni) b[ni] = read_b_bf16<B_KN>(Bs, wn, ni, ks, lane);
-#pragma unroll
-          for (int mi = 0; mi < NM; ++mi) a[mi] = read_a_bf16(As, wm * 64 + mi * 32 + (lane & 31), ks, lane);
-#pragma unroll
-          for (int mi = 0; mi < NM; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni)
-              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
-        }
-      } else {
-        const uint8_t* BSs = Bs + GGLds::B_BYTES;
-        const uint8_t* ASs = smem + GGLds::AS_OFF + ((k / GGLds::AS_GROUP) & 1) * GGLds::AS_SLOT +
-                             (k & (GGLds::AS_GROUP - 1)) * 2;
-        v8i a[2], b[4];
-        int sa[2], sb[4];
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-          b[ni] = read_b_mx(Bs, wn, ni, lane);
-          sb[ni] = BSs[(wn * 128 + ni * 32 + (lane & 31)) * 2 + (lane >> 5)];
-        }
-#pragma unroll
-        for (int mi = 0; mi < NM; ++mi) {
-          int r = wm * 64 + mi * 32 + (lane & 31);
-          a[mi] = read_a_mx(As, r, lane);
-          sa[mi] = ASs[r * 16 + (lane >> 5)];
-        }
-#pragma unroll
-        for (int mi = 0; mi < NM; ++mi)
-#pragma unroll
-          for (int ni = 0; ni < 4; ++ni)
-            acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], b[ni], acc[mi][ni], 0, 0, 0, sa[mi],
-                                                                           0, sb[ni]);
+        for (int e = t * SS::READS / T; e < (t + 1) * SS::READS / T; ++e)
+          read_elem<MX, B_KN, NM>(nxt, e, As, Bs, ASs, BSRs, wm, wn, ln);
       }
+#endif
+#pragma unroll
+      for (int it = t * SS::ITEMS / T; it < (t + 1) * SS::ITEMS / T; ++it)
+        issue_item<MX, B_KN, LA>(cp, k, nk, wave, smem, it);
+      if (t == T / 2 - 1) { GG_T(3) }
+      __builtin_amdgcn_sched_barrier(0);  // keep this interleave order
     }
+    issue_scales_item<MX, B_KN, LA>(cp, k, nk, wave, smem);
+    GG_T(4)
+  };
+  // Stages 0 .. nk-2 are pipelined steps (each reads the next stage), taken in pairs so that the
+  // two fragment sets keep fixed registers; an odd count starts with one step and a copy.
+  int k = 0;
+  if ((nk - 1) & 1) {
+    step(0, f0, f1);
+    f0 = f1;
+    k = 1;
   }
+  for (; k < nk - 1; k += 2) {
+    step(k, f0, f1);
+    step(k + 1, f1, f0);
+  }
+  // last stage: its fragments are in f0 and it issues no copies
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#ifndef GG_ABLATE_COMPUTE
+  if constexpr (NM > 0) {
+#pragma unroll
+    for (int t = 0; t < StepShape<MX, NM>::MFMAS; ++t) mfma_elem<MX, B_KN, NM>(f0, acc, t);
+  }
+#endif
 }
 
 template <bool MX, bool B_KN, int EPI>
@@ -318,8 +506,8 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     // ---- per-thread copy sources ------------------------------------------------------
     CopyPlan cp;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      int L16 = wave * 128 + j * 64 + lane;
+    for (int j = 0; j < GGLds::A_INSTR; ++j) {
+      int L16 = (wave * GGLds::A_INSTR + j) * 64 + lane;
       int r = L16 >> 2, cs = L16 & 3;
       int c = cs ^ ((r >> 2) & 3);
       int rr = r < rows_valid ? r : rows_valid - 1;
@@ -329,8 +517,8 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     }
     const uint8_t* bgrp = p.B + (int64_t)g * p.b_group_stride;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      int L16 = wave * 128 + j * 64 + lane;
+    for (int j = 0; j < GGLds::B_INSTR; ++j) {
+      int L16 = (wave * GGLds::B_INSTR + j) * 64 + lane;
       if (!B_KN) {
         int r = L16 >> 2, cs = L16 & 3;
         int c = cs ^ ((r >> 2) & 3);
@@ -355,67 +543,77 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     if (splits > 1) {
       const int64_t k0_stages = (int64_t)split * nk;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        cp.a[j] += k0_stages * GG_KB;
-        cp.b[j] += k0_stages * cp.b_stage_stride;
-      }
+      for (int j = 0; j < GGLds::A_INSTR; ++j) cp.a[j] += k0_stages * GG_KB;
+#pragma unroll
+      for (int j = 0; j < GGLds::B_INSTR; ++j) cp.b[j] += k0_stages * cp.b_stage_stride;
     }
     cp.s = nullptr;
+    cp.bs = nullptr;
+    cp.bsr = nullptr;
     cp.bs_stage_stride = 0;
     if (MX) {
-      if (wave < 4) {
+      if (wave < GGLds::AS_WAVES) {
         // A scales: row wave*64 + lane (16 codes = 8 stages per fetch)
         int r = wave * 64 + lane;
         int rr = r < rows_valid ? r : rows_valid - 1;
         int64_t routed = tile_row0 + rr;
         int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
         cp.s = p.a_scale + src * p.a_scale_ld;
-      } else {
-        // B scales: tile columns ((wave-4)*64 + lane)*2 .. +1, one col_scale group per stage
-        int j = ((wave & 1) * 64 + lane) * 2;
+      }
+      if (!B_KN) {
+        // B row scales: tile column wave*64 + lane (16 codes = 8 stages per fetch)
+        int wc = tile_col_to_weight_col(wave * 64 + lane, nt, p.N, SWIGLU);
+        if (wc >= p.Ntot) wc = p.Ntot - 1;
+        cp.bsr = p.b_scale + ((int64_t)g * p.Ntot + wc) * p.b_scale_ld;
+      } else if (is_bs_wave(wave)) {
+        // B scales: tile columns (wave*64 + lane)*2 .. +1, one col_scale group per stage
+        int j = (wave * 64 + lane) * 2;
         int wc = tile_col_to_weight_col(j, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 2;
-        cp.s = p.b_scale + (int64_t)g * p.b_scale_group_stride + (int64_t)wc * 2;
+        cp.bs = p.b_scale + (int64_t)g * p.b_scale_group_stride + (int64_t)wc * 2;
         cp.bs_stage_stride = (int64_t)p.Ntot * 2;
       }
     }
 
-    v16f acc[2][4];
+    v16f acc[GG_MI][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < GG_MI; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     __syncthreads();  // the previous item's last stage / epilogue reads are done before refilling
-    const int rows_w = rows_valid - wm * 64;
-    const int nm = rows_w >= 33 ? 2 : (rows_w >= 1 ? 1 : 0);
-    // this wave copies A rows wave*32 .. +31 (and, MX waves 0-3, scale rows wave*64 .. +63)
-    const bool la = wave * 32 < rows_valid;
+    const int rows_w = rows_valid - wm * GG_WM;
+    const int nm = rows_w > 64 ? 4 : (rows_w > 32 ? 2 : (rows_w >= 1 ? 1 : 0));
+    // this wave copies A rows wave*RPW .. +RPW-1 (and, MX scale waves, scale rows wave*64 .. +63)
+    constexpr int RPW = GGLds::A_INSTR * 16;  // A rows per wave
+    const bool la = wave * RPW < rows_valid;
     if (la) {
-      if (nm == 2) k_loop<MX, B_KN, 2, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      if (nm == 4) k_loop<MX, B_KN, 4, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 2) k_loop<MX, B_KN, 2, true>(cp, nk, wave, wm, wn, lane, smem, acc);
       else if (nm == 1) k_loop<MX, B_KN, 1, true>(cp, nk, wave, wm, wn, lane, smem, acc);
       else k_loop<MX, B_KN, 0, true>(cp, nk, wave, wm, wn, lane, smem, acc);
     } else {
-      if (nm == 2) k_loop<MX, B_KN, 2, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      if (nm == 4) k_loop<MX, B_KN, 4, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 2) k_loop<MX, B_KN, 2, false>(cp, nk, wave, wm, wn, lane, smem, acc);
       else if (nm == 1) k_loop<MX, B_KN, 1, false>(cp, nk, wave, wm, wn, lane, smem, acc);
       else k_loop<MX, B_KN, 0, false>(cp, nk, wave, wm, wn, lane, smem, acc);
     }
     __syncthreads();  // all waves are done reading the ring before the epilogue reuses LDS
 
     // ---- epilogue -----------------------------------------------------------------------
-    // acc[mi][ni][r] holds row wm*64 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4,
+    // acc[mi][ni][r] holds row wm*GG_WM + mi*32 + 8*(r/4) + 4*(lane/32) + r%4,
     // column wn*128 + ni*32 + lane%32 of the tile.
     if (EPI == EPI_STORE_F32) {
       float* C = (float*)p.C;
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int mi = 0; mi < GG_MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
+        for (int ni = 0; ni < 4; ++ni) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            int row = wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            int row = wm * GG_WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             int col = nt * GG_BN + wn * 128 + ni * 32 + (lane & 31);
             if (row < rows_valid && col < p.N) {
               int64_t routed = tile_row0 + row;
@@ -423,18 +621,22 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
               C[split * p.c_split_stride + orow * p.ldc + col] = acc[mi][ni][r];
             }
           }
+          __builtin_amdgcn_sched_barrier(0);
+        }
     } else if (EPI == EPI_STORE_BF16) {
-      constexpr int RS = GG_BN * 2 + 16;  // staged row stride (bytes)
+      constexpr int RS = GGLds::EPI_RS_BF16;  // staged row stride (bytes)
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int mi = 0; mi < GG_MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
+        for (int ni = 0; ni < 4; ++ni) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            int row = wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            int row = wm * GG_WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             int col = wn * 128 + ni * 32 + (lane & 31);
             *(uint16_t*)(smem + row * RS + col * 2) = f32_to_bf16(acc[mi][ni][r]);
           }
+          __builtin_amdgcn_sched_barrier(0);  // one 32x32 block at a time: bounded register use
+        }
       __syncthreads();
       uint16_t* C = (uint16_t*)p.C;
       for (int id = tid; id < GG_BM * (GG_BN / 8); id += GG_THREADS) {
@@ -446,20 +648,22 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
       __syncthreads();
     } else {
       // SwiGLU: subtiles ni=0,1 hold gate, ni=2,3 the matching up columns.
-      constexpr int RS = 128 * 4 + 16;  // fp32 staged act row stride
+      constexpr int RS = GGLds::EPI_RS_ACT;  // fp32 staged act row stride
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int mi = 0; mi < GG_MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < 2; ++ni) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            int row = wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            int row = wm * GG_WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             int col = wn * 64 + ni * 32 + (lane & 31);
             float gte = bf16_to_f32(f32_to_bf16(acc[mi][ni][r]));
             float up = bf16_to_f32(f32_to_bf16(acc[mi][ni + 2][r]));
             float act = gte / (1.0f + __expf(-gte)) * up;
             *(float*)(smem + row * RS + col * 4) = act;
           }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       __syncthreads();
       if (EPI == EPI_SWIGLU_BF16) {
         uint16_t* C = (uint16_t*)p.C;
@@ -572,7 +776,13 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
       }
     }
   }
-  if (!b_kn) return MI355MOE_EUNSUPPORTED;
+  if (!b_kn) {
+    switch (epi) {
+      case EPI_STORE_BF16: return launch_gg<true, false, EPI_STORE_BF16>(p, stream);
+      case EPI_SWIGLU_MX: return launch_gg<true, false, EPI_SWIGLU_MX>(p, stream);
+      default: return MI355MOE_EUNSUPPORTED;
+    }
+  }
   switch (epi) {
     case EPI_STORE_BF16: return launch_gg<true, true, EPI_STORE_BF16>(p, stream);
     case EPI_SWIGLU_MX: return launch_gg<true, true, EPI_SWIGLU_MX>(p, stream);

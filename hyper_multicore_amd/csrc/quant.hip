@@ -6,6 +6,7 @@
 // forward MX weight root (modules/mega_moe/backends/mxfp8/weights.py:61-86: col_data [G,K,N],
 // col_scale [G,K/64,N,2], 32-blocks along K for every column).
 #include "common.h"
+#include "gemm.h"
 #include "../../include/mi355moe.h"
 
 // One thread per 32-element block of a row.
@@ -94,5 +95,51 @@ extern "C" int mi355moe_mx_quantize_cols(const uint16_t* w, int32_t groups, int3
   int64_t n = (int64_t)groups * (kdim / 32) * cols;
   hipLaunchKernelGGL(mx_quant_cols_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, w,
                      groups, kdim, cols, col_data, col_scale);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+// ---- MX weight re-layout: [G, K, N] (+ col_scale [G, K/64, N, 2]) -> [G, N, K] (+ [G, N, ld]) ----
+// One 64 (K) x 64 (N) byte tile per workgroup, transposed through LDS.
+__global__ __launch_bounds__(256) void mx_weight_to_eoi_kernel(const uint8_t* src, int K, int N, uint8_t* dst) {
+  __shared__ uint8_t tile[64][64 + 4];
+  const int g = blockIdx.z, k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const uint8_t* s = src + (int64_t)g * K * N;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int kk = i / 64, nn = i % 64;
+    tile[kk][nn] = (k0 + kk < K && n0 + nn < N) ? s[(int64_t)(k0 + kk) * N + n0 + nn] : 0;
+  }
+  __syncthreads();
+  uint8_t* d = dst + (int64_t)g * N * K;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int nn = i / 64, kk = i % 64;
+    if (k0 + kk < K && n0 + nn < N) d[(int64_t)(n0 + nn) * K + k0 + kk] = tile[kk][nn];
+  }
+}
+
+__global__ __launch_bounds__(256) void mx_weight_scale_to_eoi_kernel(const uint8_t* col_scale, int G, int K, int N,
+                                                                     int64_t ld, uint8_t* scale) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (int64_t)G * N * ld) return;
+  const int64_t c = id % ld, gn = id / ld;
+  const int n = (int)(gn % N), g = (int)(gn / N);
+  uint8_t v = 0;
+  if (c < K / 32) v = col_scale[(((int64_t)g * (K / 64) + c / 2) * N + n) * 2 + (c & 1)];
+  scale[id] = v;
+}
+
+extern "C" int64_t mi355moe_mx_weight_scale_ld(int32_t kdim) { return kdim > 0 ? mi355_mx_scale_ld(kdim) : 0; }
+
+extern "C" int mi355moe_mx_weight_to_eoi(const uint8_t* col_data, const uint8_t* col_scale, int32_t groups,
+                                         int32_t kdim, int32_t cols, uint8_t* data, uint8_t* scale, void* stream) {
+  if (groups <= 0 || kdim <= 0 || cols <= 0 || kdim % 64 || groups > 65535) return MI355MOE_EINVAL;
+  if (col_data == nullptr || col_scale == nullptr || data == nullptr || scale == nullptr) return MI355MOE_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(mx_weight_to_eoi_kernel, dim3((cols + 63) / 64, (kdim + 63) / 64, groups), dim3(256), 0, st,
+                     col_data, kdim, cols, data);
+  if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
+  const int64_t ld = mi355_mx_scale_ld(kdim);
+  const int64_t n = (int64_t)groups * cols * ld;
+  hipLaunchKernelGGL(mx_weight_scale_to_eoi_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, col_scale,
+                     groups, kdim, cols, ld, scale);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }

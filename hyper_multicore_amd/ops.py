@@ -275,23 +275,51 @@ def grouped_gemm_bf16(x: torch.Tensor, weights: torch.Tensor, group_list: torch.
     return out
 
 
-def grouped_gemm_mxfp8(xq: torch.Tensor, x_scale: torch.Tensor, col_data: torch.Tensor, col_scale: torch.Tensor,
-                       group_list: torch.Tensor) -> torch.Tensor:
-    """MX grouped GEMM: xq e4m3 [rows, K] (+ e8m0 [rows, K/32]) times col_data [G, K, N]
-    (+ col_scale [G, K/64, N, 2]) per group segment; bf16 [rows, N] out."""
+def mx_weight_to_eoi(col_data: torch.Tensor, col_scale: torch.Tensor):
+    """Re-layout an MX weight root (col_data [G, K, N], col_scale [G, K/64, N, 2]) with K contiguous:
+    (data e4m3fn [G, N, K], scale uint8 [G, N, ld]), ld = K/32 padded to a multiple of 16. Values
+    and scales are unchanged; the GEMM reads this layout without transposing LDS loads."""
     lib = _lib.load()
-    device = _require_gpu(xq, x_scale, col_data, col_scale, group_list)
+    device = _require_gpu(col_data, col_scale)
+    if col_data.ndim != 3 or col_data.shape[1] % 64:
+        raise ValueError("mx_weight_to_eoi takes col_data [G, K, N] with K % 64 == 0")
     G, K, N = col_data.shape
+    if col_scale.shape != (G, K // 64, N, 2):
+        raise ValueError("col_scale must be [G, K/64, N, 2]")
+    ld = lib.mi355moe_mx_weight_scale_ld(K)
+    data = torch.empty((G, N, K), dtype=torch.float8_e4m3fn, device=device)
+    scale = torch.empty((G, N, ld), dtype=torch.uint8, device=device)
+    _lib.check(lib.mi355moe_mx_weight_to_eoi(_ptr(col_data.contiguous()), _ptr(col_scale.contiguous()), G, K, N,
+                                             _ptr(data), _ptr(scale), _stream(device)), "mi355moe_mx_weight_to_eoi")
+    return data, scale
+
+
+def grouped_gemm_mxfp8(xq: torch.Tensor, x_scale: torch.Tensor, w_data: torch.Tensor, w_scale: torch.Tensor,
+                       group_list: torch.Tensor, layout: str = "EIO") -> torch.Tensor:
+    """MX grouped GEMM: xq e4m3 [rows, K] (+ e8m0 [rows, K/32]) times the group weight, per group
+    segment; bf16 [rows, N] out. layout "EIO": w_data = col_data [G, K, N], w_scale = col_scale
+    [G, K/64, N, 2]; "EOI": the :func:`mx_weight_to_eoi` form [G, N, K] + [G, N, ld]."""
+    lib = _lib.load()
+    device = _require_gpu(xq, x_scale, w_data, w_scale, group_list)
+    G = w_data.shape[0]
+    if layout == "EIO":
+        K, N = w_data.shape[1], w_data.shape[2]
+        scale_ok = w_scale.shape == (G, K // 64, N, 2)
+    elif layout == "EOI":
+        N, K = w_data.shape[1], w_data.shape[2]
+        scale_ok = w_scale.shape == (G, N, lib.mi355moe_mx_weight_scale_ld(K))
+    else:
+        raise ValueError(f"unknown layout {layout!r}")
     rows = xq.shape[0]
-    if xq.shape != (rows, K) or x_scale.shape != (rows, K // 32) or col_scale.shape != (G, K // 64, N, 2):
+    if xq.shape != (rows, K) or x_scale.shape != (rows, K // 32) or not scale_ok:
         raise ValueError("shape mismatch in grouped_gemm_mxfp8")
     if group_list.shape != (G,) or group_list.dtype != torch.int64:
         raise ValueError("group_list must be int64 [G]")
     out = torch.empty((rows, N), dtype=torch.bfloat16, device=device)
     ws = _workspace(lib.mi355moe_grouped_gemm_workspace_size(G), device)
     rc = lib.mi355moe_grouped_gemm_mxfp8(_ptr(xq.contiguous()), _ptr(x_scale.contiguous()), rows, K,
-                                         _ptr(col_data.contiguous()), _ptr(col_scale.contiguous()), G, N,
-                                         _ptr(group_list.contiguous()), _ptr(out), _ptr(ws), ws.numel(),
+                                         _ptr(w_data.contiguous()), _ptr(w_scale.contiguous()), _lib.LAYOUT[layout],
+                                         G, N, _ptr(group_list.contiguous()), _ptr(out), _ptr(ws), ws.numel(),
                                          _stream(device))
     _lib.check(rc, "mi355moe_grouped_gemm_mxfp8")
     return out

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MI355MOE_ABI_VERSION 1
+#define MI355MOE_ABI_VERSION 2
 
 enum {
   MI355MOE_OK_CODE = 0,
@@ -159,6 +159,18 @@ int mi355moe_mx_quantize_cols(const uint16_t* w, int32_t groups, int32_t kdim, i
                               uint8_t* col_data, uint8_t* col_scale, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * MX weight re-layout for the GEMM (no reference counterpart: a one-time weight preparation, like
+ * a pre-shuffled weight, that leaves every value and scale unchanged). Takes the forward MX weight
+ * root (col_data [G, Kd, N] e4m3, col_scale [G, Kd/64, N, 2]) and writes the same weight with K
+ * contiguous: data [G, N, Kd] e4m3 and scale [G, N, ld] e8m0, ld = mi355moe_mx_weight_scale_ld(Kd)
+ * (Kd/32 codes per row, zero padded to a multiple of 16). The GEMM then reads weight fragments with
+ * plain 16-byte LDS loads instead of transposing byte loads.
+ */
+int64_t mi355moe_mx_weight_scale_ld(int32_t kdim);
+int mi355moe_mx_weight_to_eoi(const uint8_t* col_data, const uint8_t* col_scale, int32_t groups, int32_t kdim,
+                              int32_t cols, uint8_t* data, uint8_t* scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Grouped GEMM over consecutive row segments (one segment per group):
  *   out[r, :] = x[r, :] @ W_g        for rows r of group g,
  * group_list is the int64 inclusive cumulative row count per group (the grouped_matmul
@@ -175,13 +187,16 @@ int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim,
 
 /* ---------------------------------------------------------------------------------------------
  * MXFP8 grouped GEMM: out[r, :] = dequant(xq[r, :]) @ dequant(W_g), bf16 output, fp32 accumulate.
- * xq [rows, K] e4m3 with x_scale [rows, K/32] e8m0 (blocks along K); W_g = col_data [G, K, N]
- * e4m3 with col_scale [G, K/64, N, 2] (the forward MX weight root). K % 128 == 0, N % 16 == 0.
+ * xq [rows, K] e4m3 with x_scale [rows, K/32] e8m0 (blocks along K). Weights by layout:
+ *   EIO: w_data = col_data [G, K, N] e4m3, w_scale = col_scale [G, K/64, N, 2] (the forward MX
+ *        weight root);
+ *   EOI: w_data [G, N, K], w_scale [G, N, mi355moe_mx_weight_scale_ld(K)] (mi355moe_mx_weight_to_eoi).
+ * K % 512 == 0, N % 16 == 0.
  * Replaces the MX GMM task (ops/common/mega_moe/adapters/arch35/gmm/mxfp8_worker.h:15-159, NN
  * layout, contracts/mx_gmm_descriptor.h:18-87).
  */
 int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,
-                                const uint8_t* col_data, const uint8_t* col_scale, int32_t num_groups,
+                                const uint8_t* w_data, const uint8_t* w_scale, int32_t layout, int32_t num_groups,
                                 int32_t ndim, const int64_t* group_list, uint16_t* out, void* workspace,
                                 size_t workspace_size, void* stream);
 
@@ -194,7 +209,9 @@ int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64
  * SwiGLU: gate = left half of the 2I projection, act = bf16(silu(g) * u) with g, u the bf16
  * GMM1 outputs (tests/common/multicore/fp32_expert_reference.py:22-26).
  * MXFP8: w1/w2 are col_data e4m3 EIO [E,H,2I] / [E,I,H] with col_scale [E,H/64,2I,2] /
- * [E,I/64,H,2]; H and I must be multiples of 64 (docs: MXFP8 weight contract).
+ * [E,I/64,H,2] (docs: MXFP8 weight contract), or, with weight_layout EOI, the same weights after
+ * mi355moe_mx_weight_to_eoi: [E,2I,H] / [E,H,I] with row scales [E,2I,ld(H)] / [E,H,ld(I)].
+ * H and I must be multiples of 128.
  * tokens_per_expert (optional) is a trusted int32 histogram of topk_ids; when NULL it is
  * computed. Workspace: mi355moe_moe_forward_workspace_size(args) bytes.
  */
@@ -209,7 +226,7 @@ typedef struct MI355MoeForwardArgs {
   int32_t ids_dtype;
   int32_t precision;          /* MI355MOE_PRECISION_* */
   const float* topk_weights;  /* [T, K] fp32 */
-  int32_t weight_layout;      /* MI355MOE_LAYOUT_* (MXFP8: EIO only) */
+  int32_t weight_layout;      /* MI355MOE_LAYOUT_* */
   int32_t reserved0;
   const void* w1;
   const void* w2;

@@ -13,7 +13,7 @@ def _declared_symbols():
     names = set()
     for header in (ROOT / "include").glob("*.h"):
         text = header.read_text()
-        for m in re.finditer(r"^\s*(?:int|size_t|void)\s+(mi355moe_\w+)\s*\(", text, re.M):
+        for m in re.finditer(r"^\s*(?:int|int64_t|size_t|void)\s+(mi355moe_\w+)\s*\(", text, re.M):
             names.add(m.group(1))
     return names
 
@@ -47,8 +47,10 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.mi355moe_moe_forward_workspace_size(ctypes.byref(f)) == 0
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
     f = _lib.ForwardArgs(num_tokens=16, hidden_size=1024, intermediate_size=512, num_experts=8, top_k=2,
-                         ids_dtype=0, precision=1, weight_layout=1)  # MXFP8 needs EIO
+                         ids_dtype=0, precision=1, weight_layout=2)  # no such layout
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+    f.weight_layout = 1  # MXFP8 EOI (re-laid-out weights): operands missing, or the path switched off
+    assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
 
 
 def test_workspace_sizes():
