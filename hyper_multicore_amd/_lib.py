@@ -17,6 +17,8 @@ OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 IDS_INT32, IDS_INT64 = 0, 1
 PRECISION = {"bf16": 0, "mxfp8": 1}
+NUMERICS_CLAMP_AFTER_SILU = 1
+NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}
 
 _ERRORS = {
@@ -52,10 +54,10 @@ class ForwardArgs(Structure):
         ("hidden", c_void_p), ("num_tokens", c_int64), ("hidden_size", c_int32),
         ("intermediate_size", c_int32), ("num_experts", c_int32), ("top_k", c_int32),
         ("topk_ids", c_void_p), ("ids_dtype", c_int32), ("precision", c_int32),
-        ("topk_weights", c_void_p), ("weight_layout", c_int32), ("reserved0", c_int32),
+        ("topk_weights", c_void_p), ("weight_layout", c_int32), ("numerics_flags", c_int32),
         ("w1", c_void_p), ("w2", c_void_p), ("w1_scale", c_void_p), ("w2_scale", c_void_p),
         ("tokens_per_expert", c_void_p), ("out", c_void_p), ("error_flag", c_void_p),
-        ("stage_events", POINTER(c_void_p)), ("num_stage_events", c_int32), ("reserved1", c_int32),
+        ("stage_events", POINTER(c_void_p)), ("num_stage_events", c_int32), ("swiglu_limit", c_float),
     ]
 
 

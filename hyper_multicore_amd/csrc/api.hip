@@ -3,6 +3,7 @@
 // All launches are enqueued on the caller's stream; nothing synchronises the host.
 #include "common.h"
 #include "gemm.h"
+#include <cmath>
 #include "../../include/mi355moe.h"
 
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -239,6 +240,12 @@ static int validate_fwd(const MI355MoeForwardArgs& a) {
   if (a.precision != MI355MOE_PRECISION_BF16 && a.precision != MI355MOE_PRECISION_MXFP8) return MI355MOE_EINVAL;
   if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;
+  if (a.numerics_flags & ~(MI355MOE_NUMERICS_CLAMP_AFTER_SILU | MI355MOE_NUMERICS_PROBS_BEFORE_FC2))
+    return MI355MOE_EINVAL;
+  if (!(a.swiglu_limit >= 0.0f) || a.swiglu_limit == INFINITY) return MI355MOE_EINVAL;  // NaN, negative, inf
+  const bool options = a.swiglu_limit > 0.0f || (a.numerics_flags & MI355MOE_NUMERICS_PROBS_BEFORE_FC2);
+  if (options && a.precision == MI355MOE_PRECISION_MXFP8) return MI355MOE_EINVAL;  // module.py:132
+  if (options && !mi355_numerics_options_enabled()) return MI355MOE_EUNSUPPORTED;
   if (a.precision == MI355MOE_PRECISION_MXFP8) {
     if (a.weight_layout == MI355MOE_LAYOUT_EOI && !mi355_mx_eoi_enabled()) return MI355MOE_EUNSUPPORTED;
     if (a.hidden_size % 128 || a.intermediate_size % 128) return MI355MOE_EUNSUPPORTED;
@@ -327,6 +334,10 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.ldc = I;
   p1.c_scale = mx ? (uint8_t*)(ws + L.act_scale) : nullptr;
   p1.c_scale_ld = mi355_mx_scale_ld(I);
+  const bool before_fc2 = (a.numerics_flags & MI355MOE_NUMERICS_PROBS_BEFORE_FC2) != 0;
+  p1.swiglu_limit = a.swiglu_limit;
+  p1.swiglu_after_silu = (a.numerics_flags & MI355MOE_NUMERICS_CLAMP_AFTER_SILU) != 0;
+  p1.row_prob = before_fc2 ? a.topk_weights : nullptr;
   rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st);
   if (rc) return rc;
   mark(2);
@@ -355,7 +366,9 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   rc = mi355_grouped_gemm(p2, mx, !eoi, EPI_STORE_BF16, st);
   if (rc) return rc;
   mark(3);
-  rc = mi355_unpermute_enqueue((const uint16_t*)(ws + L.y), mapping, a.topk_weights, T, K, H, a.out, st);
+  // probabilities applied before FC2 are not applied again: the combine sums the K rows
+  rc = mi355_unpermute_enqueue((const uint16_t*)(ws + L.y), mapping, before_fc2 ? nullptr : a.topk_weights, T, K, H,
+                               a.out, st);
   mark(4);
   return rc;
 }

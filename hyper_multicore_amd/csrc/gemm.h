@@ -29,6 +29,9 @@ struct GGParams {
   const int32_t* c_row_index;  // optional output row scatter (EPI_STORE_F32)
   uint8_t* c_scale;          // EPI_SWIGLU_MX: [rows, N/32] with row stride c_scale_ld
   int64_t c_scale_ld;
+  float swiglu_limit;        // EPI_SWIGLU_BF16: > 0 clamps the SwiGLU inputs (0: no clamp)
+  int32_t swiglu_after_silu; // EPI_SWIGLU_BF16: clamp SiLU(gate) instead of gate
+  const float* row_prob;     // EPI_SWIGLU_BF16: probability of slot a_row_index[r] multiplies row r
   int32_t k_splits;          // EPI_STORE_F32 only: >1 splits K; split s writes C + s * c_split_stride
   int64_t c_split_stride;    // elements
 };
@@ -40,6 +43,9 @@ int mi355_gg_bm();
 // MX GEMM with K-contiguous (EOI) weights: switched off until its GPU parity tests have run
 // (the grouped GEMM then rejects that layout with MI355MOE_EUNSUPPORTED).
 inline bool mi355_mx_eoi_enabled() { return false; }
+// BF16 numerics options (SwiGLU clamp, probabilities before FC2): switched off until their GPU
+// parity tests have run (the forward then answers MI355MOE_EUNSUPPORTED).
+inline bool mi355_numerics_options_enabled() { return false; }
 int mi355_gg_bn();
 int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
                            int64_t* expert_offsets, int64_t* group_list, int32_t* mapping, int32_t* gather_index,

@@ -659,7 +659,20 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
             int col = wn * 64 + ni * 32 + (lane & 31);
             float gte = bf16_to_f32(f32_to_bf16(acc[mi][ni][r]));
             float up = bf16_to_f32(f32_to_bf16(acc[mi][ni + 2][r]));
-            float act = gte / (1.0f + __expf(-gte)) * up;
+            float act;
+            if (EPI == EPI_SWIGLU_BF16 && p.swiglu_limit > 0.0f) {
+              // MegaMoeNumericsOptions clamp: up to [-L, L]; gate to <= L before SiLU, or SiLU(gate)
+              // to <= L after it
+              const float L = p.swiglu_limit;
+              up = fminf(fmaxf(up, -L), L);
+              if (p.swiglu_after_silu) act = fminf(gte / (1.0f + __expf(-gte)), L) * up;
+              else {
+                const float gc = fminf(gte, L);
+                act = gc / (1.0f + __expf(-gc)) * up;
+              }
+            } else {
+              act = gte / (1.0f + __expf(-gte)) * up;
+            }
             *(float*)(smem + row * RS + col * 4) = act;
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -671,11 +684,21 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
           int row = id >> 4, ch = id & 15;
           if (row < rows_valid) {
             const float* s = (const float*)(smem + row * RS + ch * 32);
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = s[i];
+            if (p.row_prob != nullptr) {
+              // probabilities before FC2: bf16(fp32(bf16(act)) * p) (two roundings, the reference
+              // contract); row r of the tile is slot a_row_index[r]
+              const float pr = p.row_prob[p.a_row_index[tile_row0 + row]];
+#pragma unroll
+              for (int i = 0; i < 8; ++i) v[i] = bf16_to_f32(f32_to_bf16(v[i])) * pr;
+            }
             uint4 o;
-            o.x = f32_to_bf16(s[0]) | ((uint32_t)f32_to_bf16(s[1]) << 16);
-            o.y = f32_to_bf16(s[2]) | ((uint32_t)f32_to_bf16(s[3]) << 16);
-            o.z = f32_to_bf16(s[4]) | ((uint32_t)f32_to_bf16(s[5]) << 16);
-            o.w = f32_to_bf16(s[6]) | ((uint32_t)f32_to_bf16(s[7]) << 16);
+            o.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+            o.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+            o.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+            o.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
             *(uint4*)(C + (tile_row0 + row) * p.ldc + nt * 128 + ch * 8) = o;
           }
         }

@@ -329,8 +329,12 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
                 w2: torch.Tensor, *, num_experts: int, intermediate_size: int, precision: str = "bf16",
                 layout: str = "EIO", w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
                 tokens_per_expert: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                error_flag: torch.Tensor | None = None, stage_events=None) -> torch.Tensor:
+                error_flag: torch.Tensor | None = None, stage_events=None, swiglu_limit: float | None = None,
+                clamp_after_silu: bool = False, apply_probs_before_fc2: bool = False) -> torch.Tensor:
     """Expert forward at EP=1 through ``mi355moe_moe_forward``; returns bf16 [T, H].
+
+    BF16 numerics options as ``MegaMoeNumericsOptions`` (``swiglu_limit``, ``clamp_after_silu``,
+    ``apply_probs_before_fc2``).
 
     ``stage_events``: optional list of up to 5 ``torch.cuda.Event(enable_timing=True)`` recorded
     at the stage boundaries (start, after dispatch, after GMM1, after GMM2, after combine).
@@ -350,7 +354,10 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
         hidden=_ptr(hidden), num_tokens=T, hidden_size=H, intermediate_size=intermediate_size,
         num_experts=num_experts, top_k=K, topk_ids=_ptr(ids), ids_dtype=_ids_dtype(ids),
         precision=_lib.PRECISION[precision], topk_weights=_ptr(probs), weight_layout=_lib.LAYOUT[layout],
-        reserved0=0, w1=_ptr(w1), w2=_ptr(w2), w1_scale=_ptr(w1_scale), w2_scale=_ptr(w2_scale),
+        numerics_flags=(_lib.NUMERICS_CLAMP_AFTER_SILU if clamp_after_silu else 0)
+        | (_lib.NUMERICS_PROBS_BEFORE_FC2 if apply_probs_before_fc2 else 0),
+        swiglu_limit=0.0 if swiglu_limit is None else float(swiglu_limit),
+        w1=_ptr(w1), w2=_ptr(w2), w1_scale=_ptr(w1_scale), w2_scale=_ptr(w2_scale),
         tokens_per_expert=_ptr(tokens_per_expert), out=_ptr(out), error_flag=_ptr(error_flag))
     if stage_events:
         handles = []

@@ -214,7 +214,13 @@ int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64
  * H and I must be multiples of 128.
  * tokens_per_expert (optional) is a trusted int32 histogram of topk_ids; when NULL it is
  * computed. Workspace: mi355moe_moe_forward_workspace_size(args) bytes.
+ * BF16 numerics options (MegaMoeNumericsOptions, modules/mega_moe/numerics.py; docs/mega_moe.md
+ * "numerics"): swiglu_limit L > 0 clamps the SwiGLU inputs, up to [-L, L] and gate to <= L before
+ * SiLU, or SiLU(gate) to <= L after it with MI355MOE_NUMERICS_CLAMP_AFTER_SILU;
+ * MI355MOE_NUMERICS_PROBS_BEFORE_FC2 feeds FC2 with bf16(bf16(act) * p) and combines unweighted.
+ * MXFP8 rejects both (module.py:132).
  */
+enum { MI355MOE_NUMERICS_CLAMP_AFTER_SILU = 1, MI355MOE_NUMERICS_PROBS_BEFORE_FC2 = 2 };
 typedef struct MI355MoeForwardArgs {
   const uint16_t* hidden;     /* [T, H] bf16 */
   int64_t num_tokens;
@@ -227,7 +233,7 @@ typedef struct MI355MoeForwardArgs {
   int32_t precision;          /* MI355MOE_PRECISION_* */
   const float* topk_weights;  /* [T, K] fp32 */
   int32_t weight_layout;      /* MI355MOE_LAYOUT_* */
-  int32_t reserved0;
+  int32_t numerics_flags;     /* MI355MOE_NUMERICS_* bits (BF16 only; MegaMoeNumericsOptions) */
   const void* w1;
   const void* w2;
   const uint8_t* w1_scale;
@@ -240,7 +246,7 @@ typedef struct MI355MoeForwardArgs {
    * [3] after GMM2, [4] after combine. num_stage_events may be 0..5. */
   void* const* stage_events;
   int32_t num_stage_events;
-  int32_t reserved1;
+  float swiglu_limit;         /* > 0: SwiGLU clamp limit L (BF16 only); 0: no clamp */
 } MI355MoeForwardArgs;
 size_t mi355moe_moe_forward_workspace_size(const MI355MoeForwardArgs* args);
 int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* workspace, size_t workspace_size,

@@ -248,17 +248,41 @@ def _bf16(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.bfloat16).float()
 
 
+def swiglu_reference(g: torch.Tensor, u: torch.Tensor, swiglu_limit: float | None = None,
+                     clamp_after_silu: bool = False) -> torch.Tensor:
+    """fp32 SwiGLU activation of the bf16 GMM1 halves (docs/mega_moe.md:253-262, numerics.py):
+    no limit: silu(g) * u; limit L before SiLU: silu(min(g, L)) * clamp(u, -L, L); after SiLU:
+    min(silu(g), L) * clamp(u, -L, L)."""
+    gate, up = g.float(), u.float()
+    if swiglu_limit is None:
+        return F.silu(gate) * up
+    L = float(swiglu_limit)
+    up = up.clamp(-L, L)
+    if clamp_after_silu:
+        return F.silu(gate).clamp(max=L) * up
+    return F.silu(gate.clamp(max=L)) * up
+
+
 def expert_forward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, w1: torch.Tensor,
                              w2: torch.Tensor, *, layout: str = "EIO", precision: str = "bf16",
                              w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
-                             num_experts: int | None = None) -> torch.Tensor:
+                             num_experts: int | None = None, swiglu_limit: float | None = None,
+                             clamp_after_silu: bool = False, apply_probs_before_fc2: bool = False) -> torch.Tensor:
     """fp32-accumulate expert forward with the reference's bf16 rounding points
     (fp32_expert_reference.py:22-26): U = bf16(x @ W1), act = bf16(silu(g) * u) with g the left
     half, y = bf16(act @ W2); combine = fp32 sum over k ascending of p * y, one bf16 rounding.
 
     precision "mxfp8": x quantised per 32 along H, W1/W2 given as col_data/col_scale (EIO),
     act = silu(g) * u quantised per 32 along I before the down projection (mxfp8/graph.py:140-146).
+
+    bf16 numerics options (docs/mega_moe.md:218-270; module.py:132 rejects them for MXFP8):
+    ``swiglu_limit`` / ``clamp_after_silu`` as in :func:`swiglu_reference`;
+    ``apply_probs_before_fc2``: the FC2 input is bf16(fp32(bf16(act)) * p) with p the routed row's
+    probability, and the combine sums the K rows unweighted (execution.py:75-77,
+    autograd.py:124-126).
     """
+    if precision != "bf16" and (swiglu_limit is not None or apply_probs_before_fc2):
+        raise ValueError("MXFP8 does not support clamp or before-FC2 probability weighting")
     T, H = hidden.shape
     K = ids.shape[1]
     E = num_experts if num_experts is not None else w1.shape[0]
@@ -280,18 +304,21 @@ def expert_forward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: tor
         n = int((flat == e).sum())
         if n == 0:
             continue
-        rows = gather[start:start + n].long() // K
+        slots = gather[start:start + n].long()
+        rows = slots // K
         u = _bf16(xin[rows] @ W1[e])
         g, up = u[:, :I], u[:, I:]
-        act = F.silu(g) * up
+        act = swiglu_reference(g, up, swiglu_limit, clamp_after_silu)
         if precision == "bf16":
             act = _bf16(act)
+            if apply_probs_before_fc2:
+                act = _bf16(act * probs.reshape(-1)[slots].float()[:, None])
         else:
             aq, asc = mx_quantize(act, dim=-1)
             act = mx_dequantize(aq, asc, dim=-1)
         y[start:start + n] = _bf16(act @ W2[e])
         start += n
-    return unpermute_tokens(y.to(torch.bfloat16), mapping, probs, K)
+    return unpermute_tokens(y.to(torch.bfloat16), mapping, None if apply_probs_before_fc2 else probs, K)
 
 
 def torch_experts_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, gate_w: torch.Tensor,

@@ -53,6 +53,24 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
 
 
+def test_numerics_options_validation():
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    base = dict(num_tokens=16, hidden_size=1024, intermediate_size=512, num_experts=8, top_k=2, ids_dtype=0,
+                precision=0, weight_layout=0)
+    f = _lib.ForwardArgs(**base, numerics_flags=4)  # unknown bit
+    assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+    for bad in (-1.0, float("nan"), float("inf")):
+        f = _lib.ForwardArgs(**base, swiglu_limit=bad)
+        assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+    f = _lib.ForwardArgs(**{**base, "precision": 1}, swiglu_limit=7.0)  # MXFP8 rejects the options
+    assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+    f = _lib.ForwardArgs(**{**base, "precision": 1}, numerics_flags=2)
+    assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+    f = _lib.ForwardArgs(**base, swiglu_limit=7.0)
+    assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
+
+
 def test_workspace_sizes():
     from hyper_multicore_amd import _lib
     lib = _lib.load()

@@ -378,3 +378,39 @@ def test_moe_forward_mxfp8_eoi_matches_eio(gpu):
     out_eoi = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), e1.view(torch.uint8), e2.view(torch.uint8),
                               w1_scale=t1, w2_scale=t2, layout="EOI", **args).cpu()
     assert torch.equal(out_eio, out_eoi)
+
+
+_NUMERICS_SKIP = pytest.mark.skip(
+    reason="BF16 numerics options are switched off in the library until this test has run on the GPU")
+
+
+@_NUMERICS_SKIP
+@pytest.mark.parametrize("limit,after,before_fc2", [(7.0, False, False), (0.25, True, False), (None, False, True),
+                                                    (0.5, False, True)])
+def test_moe_forward_bf16_numerics_options(gpu, limit, after, before_fc2):
+    from hyper_multicore_amd import ops
+    T, H, I, E, K = 512, 1024, 512, 16, 4
+    g = _seed(T + E + 7)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
+    opts = dict(swiglu_limit=limit, clamp_after_silu=after, apply_probs_before_fc2=before_fc2)
+    out = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1.to(gpu), w2.to(gpu), num_experts=E,
+                          intermediate_size=I, **opts).cpu()
+    ref = orc.expert_forward_reference(x, ids, probs, w1, w2, **opts)
+    assert orc.rel_l2(out, ref) < BF16_REL_L2
+    plain = orc.expert_forward_reference(x, ids, probs, w1, w2)
+    if limit is not None and limit < 1.0:
+        assert orc.rel_l2(ref, plain) > 0.05  # the clamp is active at this limit
+
+
+@_NUMERICS_SKIP
+def test_moe_forward_probs_before_fc2_power_of_two_is_bit_exact_to_after(gpu):
+    from hyper_multicore_amd import ops
+    T, H, I, E, K = 384, 1024, 256, 8, 2
+    g = _seed(T + 3)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
+    p2 = torch.pow(2.0, torch.randint(-3, 3, probs.shape, generator=g).float())
+    args = dict(num_experts=E, intermediate_size=I)
+    a = ops.moe_forward(x.to(gpu), ids.to(gpu), p2.to(gpu), w1.to(gpu), w2.to(gpu), **args).cpu()
+    b = ops.moe_forward(x.to(gpu), ids.to(gpu), p2.to(gpu), w1.to(gpu), w2.to(gpu), apply_probs_before_fc2=True,
+                        **args).cpu()
+    assert torch.equal(a, b)

@@ -319,3 +319,75 @@ def test_mxfp8_reference_close_to_bf16():
 
 def test_flops_formula():
     assert orc.moe_flops(8192, 8, 7168, 2048, 256) == pytest.approx(5.772e12 + 3.0e10, rel=2e-3)
+
+
+# ---- bf16 numerics options (docs/mega_moe.md numerics section; module.py:132) -------------------
+def _silu(x: float) -> float:
+    return x / (1.0 + math.exp(-x))
+
+
+def test_swiglu_clamp_branch_points():
+    """Known values on each side of the limit L = 7 for both clamp positions."""
+    L = 7.0
+    g = torch.tensor([-30.0, -1.0, 3.0, 7.0, 7.5, 8.0, 40.0])
+    u = torch.tensor([2.0, -50.0, 50.0, 1.0, -3.0, 6.5, -7.25])
+    before = orc.swiglu_reference(g, u, L, clamp_after_silu=False)
+    after = orc.swiglu_reference(g, u, L, clamp_after_silu=True)
+    for i in range(g.numel()):
+        gi, ui = float(g[i]), max(-L, min(L, float(u[i])))
+        assert float(before[i]) == pytest.approx(_silu(min(gi, L)) * ui, rel=1e-6, abs=1e-30)
+        assert float(after[i]) == pytest.approx(min(_silu(gi), L) * ui, rel=1e-6, abs=1e-30)
+    # the positions define different functions: gate 8 -> silu(7) before, min(silu(8), 7) = 7 after
+    assert float(before[5]) == pytest.approx(_silu(7.0) * 6.5, rel=1e-6)
+    assert float(after[5]) == pytest.approx(7.0 * 6.5, rel=1e-6)
+    # up is clamped symmetrically in both modes
+    assert float(before[1]) == pytest.approx(_silu(-1.0) * -7.0, rel=1e-6)
+
+
+def test_swiglu_without_limit_and_with_huge_limit_is_plain():
+    g = torch.randn(1000, generator=torch.Generator().manual_seed(3)) * 4
+    u = torch.randn(1000, generator=torch.Generator().manual_seed(4)) * 4
+    plain = F.silu(g) * u
+    assert torch.equal(orc.swiglu_reference(g, u), plain)
+    for after in (False, True):
+        assert torch.equal(orc.swiglu_reference(g, u, 1e30, clamp_after_silu=after), plain)
+
+
+def test_expert_reference_options_default_equivalence():
+    x, ids, p, w1, w2 = _inputs()
+    base = orc.expert_forward_reference(x, ids, p, w1, w2)
+    same = orc.expert_forward_reference(x, ids, p, w1, w2, swiglu_limit=None, clamp_after_silu=True)
+    assert torch.equal(base, same)  # clamp_after_silu alone changes nothing (needs a limit)
+    huge = orc.expert_forward_reference(x, ids, p, w1, w2, swiglu_limit=1e30)
+    assert torch.equal(base, huge)
+
+
+def test_probs_before_fc2_with_power_of_two_probs_equals_after():
+    """With p = 2^k the two extra bf16 roundings are exact, so weighting before FC2 (and an
+    unweighted combine) gives bit-identical outputs to weighting in the combine: this pins which
+    slot's probability multiplies each routed row."""
+    x, ids, p, w1, w2 = _inputs(T=64, E=6, K=3, seed=21)
+    g = torch.Generator().manual_seed(22)
+    p2 = torch.pow(2.0, torch.randint(-3, 3, p.shape, generator=g).float())
+    a = orc.expert_forward_reference(x, ids, p2, w1, w2)
+    b = orc.expert_forward_reference(x, ids, p2, w1, w2, apply_probs_before_fc2=True)
+    assert torch.equal(a, b)
+    # and a row-permuted probability tensor breaks it
+    c = orc.expert_forward_reference(x, ids, p2.flip(0), w1, w2, apply_probs_before_fc2=True)
+    assert not torch.equal(a, c)
+
+
+def test_probs_before_fc2_keeps_two_roundings():
+    x, ids, p, w1, w2 = _inputs(T=64, E=4, K=2, seed=23)
+    a = orc.expert_forward_reference(x, ids, p, w1, w2).float()
+    b = orc.expert_forward_reference(x, ids, p, w1, w2, apply_probs_before_fc2=True).float()
+    assert orc.rel_l2(a, b) < 2e-2 and not torch.equal(a, b)
+
+
+def test_mxfp8_rejects_numerics_options():
+    x, ids, p, w1, w2 = _inputs(H=128, I=64)
+    d1, s1 = orc.mx_quantize_weight_cols(w1)
+    d2, s2 = orc.mx_quantize_weight_cols(w2)
+    with pytest.raises(ValueError):
+        orc.expert_forward_reference(x, ids, p, d1, d2, precision="mxfp8", w1_scale=s1, w2_scale=s2,
+                                     swiglu_limit=7.0)
