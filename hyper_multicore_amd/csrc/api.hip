@@ -156,9 +156,10 @@ extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32
   p.tile_prefix = (int32_t*)workspace;
   p.C = out;
   p.ldc = ndim;
-  int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st);
+  const bool small = mi355_use_small_tiles(rows, num_groups);
+  int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st, small);
   if (rc) return rc;
-  return mi355_grouped_gemm(p, false, layout == MI355MOE_LAYOUT_EIO, EPI_STORE_BF16, st);
+  return mi355_grouped_gemm(p, false, layout == MI355MOE_LAYOUT_EIO, EPI_STORE_BF16, st, small);
 }
 
 extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,
@@ -198,9 +199,10 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
   p.tile_prefix = (int32_t*)workspace;
   p.C = out;
   p.ldc = ndim;
-  int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st);
+  const bool small = mi355_use_small_tiles(rows, num_groups);
+  int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st, small);
   if (rc) return rc;
-  return mi355_grouped_gemm(p, true, !eoi, EPI_STORE_BF16, st);
+  return mi355_grouped_gemm(p, true, !eoi, EPI_STORE_BF16, st, small);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -299,7 +301,9 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   rc = mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, T, K, E, counts, nullptr, group_list, mapping, gather,
                               a.error_flag, ws + L.dispatch, st);
   if (rc) return rc;
-  rc = mi355_plan_tiles(group_list, E, tile_prefix, st);
+  // decode shapes (few routed rows per expert) use the 64-row tiles
+  const bool small = mi355_use_small_tiles(T * K, E);
+  rc = mi355_plan_tiles(group_list, E, tile_prefix, st, small);
   if (rc) return rc;
   const uint8_t* a1 = (const uint8_t*)a.hidden;
   if (mx) {
@@ -338,7 +342,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.swiglu_limit = a.swiglu_limit;
   p1.swiglu_after_silu = (a.numerics_flags & MI355MOE_NUMERICS_CLAMP_AFTER_SILU) != 0;
   p1.row_prob = before_fc2 ? a.topk_weights : nullptr;
-  rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st);
+  rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st, small);
   if (rc) return rc;
   mark(2);
   // GMM2: [R, I] x [I, H] -> y [R, H] bf16
@@ -363,7 +367,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p2.tile_prefix = tile_prefix;
   p2.C = ws + L.y;
   p2.ldc = H;
-  rc = mi355_grouped_gemm(p2, mx, !eoi, EPI_STORE_BF16, st);
+  rc = mi355_grouped_gemm(p2, mx, !eoi, EPI_STORE_BF16, st, small);
   if (rc) return rc;
   mark(3);
   // probabilities applied before FC2 are not applied again: the combine sums the K rows

@@ -37,15 +37,21 @@ struct GGParams {
 };
 
 
-int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
-int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream);
-int mi355_gg_bm();
+int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, bool small = false);
+int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream, bool small = false);
+int mi355_gg_bm(bool small = false);
 // MX GEMM with K-contiguous (EOI) weights: switched off until its GPU parity tests have run
 // (the grouped GEMM then rejects that layout with MI355MOE_EUNSUPPORTED).
 inline bool mi355_mx_eoi_enabled() { return false; }
 // BF16 numerics options (SwiGLU clamp, probabilities before FC2): switched off until their GPU
 // parity tests have run (the forward then answers MI355MOE_EUNSUPPORTED).
 inline bool mi355_numerics_options_enabled() { return false; }
+// The 64-row tile configuration (two workgroups per CU) for grouped GEMMs whose groups average at
+// most 32 rows (decode): switched off until its GPU parity tests have run.
+inline bool mi355_small_tiles_enabled() { return false; }
+inline bool mi355_use_small_tiles(int64_t rows, int groups) {
+  return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;
+}
 int mi355_gg_bn();
 int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
                            int64_t* expert_offsets, int64_t* group_list, int32_t* mapping, int32_t* gather_index,

@@ -38,50 +38,57 @@
 #include "../../include/mi355moe.h"
 #include "gemm.h"
 
-// Tile configuration: one 4-wave workgroup per CU (one wave per SIMD, so each wave owns the
-// SIMD's whole register file: 128 x 128 fp32 accumulators plus two stages of operand fragments).
-#define GG_BM 256
-#define GG_BN 256
-#define GG_WAVES 4
-#define GG_WM 128  // rows per wave
-#define GG_MI (GG_WM / 32)
-#define GG_A_SLOTS 3
-#define GG_B_SLOTS 5
-#define GG_PREFIX_MAX 1024
-#define GG_KB 64  // bytes of K per stage per row
-#define GG_THREADS (64 * GG_WAVES)
-
-struct GGLds {
+// Tile configurations (compile time). Both use 4 waves, tiles of BN = 256 weight columns and
+// 64-byte K stages (32 bf16 or 64 e4m3 per row):
+//   GGBig   - BM = 256, one workgroup per CU, waves in a 2 x 2 grid of 128 x 128 wave tiles (one
+//             wave per SIMD owning all 512 registers); prefill shapes.
+//   GGSmall - BM = 64, two workgroups per CU (the weight stream of one CU then runs through two
+//             independent pipelines), waves in a 1 x 4 grid of 64 x 64 wave tiles; decode shapes
+//             where experts see a few rows each.
+template <int BM_, int WGM_, int A_SLOTS_, int B_SLOTS_, int PREFIX_MAX_, int WG_PER_CU_>
+struct GGCfg {
+  static constexpr int BM = BM_;
+  static constexpr int BN = 256;
+  static constexpr int KB = 64;                        // bytes of K per stage per row
+  static constexpr int WAVES = 4;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int WG_PER_CU = WG_PER_CU_;
+  static constexpr int WGM = WGM_, WGN = WAVES / WGM_; // wave grid
+  static constexpr int WM = BM / WGM, WN = BN / WGN;   // wave tile
+  static constexpr int MI = WM / 32, NI = WN / 32;     // 32 x 32 MFMA subtiles per wave
   // Decoupled rings: activations A (re-read from L2 by the tiles of one expert) and weights B
   // (streamed once from HBM, so it gets the deeper ring).
-  static constexpr int A_BYTES = GG_BM * GG_KB;        // 16 KB
-  static constexpr int B_BYTES = GG_BN * GG_KB;        // 16 KB
-  static constexpr int BS_BYTES = GG_BN * 2;           // 512 B (MX: two codes per column)
+  static constexpr int A_BYTES = BM * KB;
+  static constexpr int B_BYTES = BN * KB;              // 16 KB
+  static constexpr int BS_BYTES = BN * 2;              // 512 B (MX EIO: two codes per column)
   static constexpr int B_SLOT = B_BYTES + BS_BYTES;
-  static constexpr int A_SLOTS = GG_A_SLOTS;           // A(k + A_SLOTS) issued at iteration k
-  static constexpr int B_SLOTS = GG_B_SLOTS;           // B(k + B_SLOTS) issued at iteration k
-  static constexpr int AS_GROUP = 8;                   // MX: A scale codes fetched per 8 stages
-  static constexpr int AS_SLOT = GG_BM * 16;           // 16 codes per row
+  static constexpr int A_SLOTS = A_SLOTS_;             // A(k + A_SLOTS) issued at iteration k
+  static constexpr int B_SLOTS = B_SLOTS_;             // B(k + B_SLOTS) issued at iteration k
+  static constexpr int AS_GROUP = 8;                   // MX: scale codes fetched per 8 stages
+  static constexpr int AS_SLOT = BM * 16;              // 16 codes per row
   static constexpr int B_OFF = A_SLOTS * A_BYTES;
   static constexpr int AS_OFF = B_OFF + B_SLOTS * B_SLOT;
-  static constexpr int PREFIX_MAX = GG_PREFIX_MAX;     // groups whose tile prefix is kept in LDS
-  static constexpr int BSR_SLOT = GG_BN * 16;          // MX NK weights: 16 scale codes per column
+  static constexpr int PREFIX_MAX = PREFIX_MAX_;       // groups whose tile prefix is kept in LDS
+  static constexpr int BSR_SLOT = BN * 16;             // MX EOI weights: 16 scale codes per column
   static constexpr int BSR_OFF = AS_OFF + 2 * AS_SLOT;
   static constexpr int PREFIX_OFF = BSR_OFF + 2 * BSR_SLOT;
   static constexpr int TOTAL = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
   // DMA instructions per wave per stage (64 lanes x 16 bytes each)
-  static constexpr int A_INSTR = GG_BM * (GG_KB / 16) / 64 / GG_WAVES;
-  static constexpr int B_INSTR = GG_BN * (GG_KB / 16) / 64 / GG_WAVES;
-  static constexpr int AS_WAVES = GG_BM / 64;          // waves that fetch A scale rows (64 each)
-  // epilogue staging (overlays the rings and the A scale slots, never the tile prefix)
-  static constexpr int EPI_RS_BF16 = GG_BN * 2 + 16;   // bf16 row stride
-  static constexpr int EPI_RS_ACT = 128 * 4 + 16;      // SwiGLU fp32 row stride
+  static constexpr int A_INSTR = BM * (KB / 16) / 64 / WAVES;
+  static constexpr int B_INSTR = BN * (KB / 16) / 64 / WAVES;
+  static constexpr int AS_WAVES = BM / 64;             // waves that fetch A scale rows (64 each)
+  // epilogue staging (overlays the rings and the scale slots, never the tile prefix)
+  static constexpr int EPI_RS_BF16 = BN * 2 + 16;      // bf16 row stride
+  static constexpr int EPI_RS_ACT = (BN / 2) * 4 + 16; // SwiGLU fp32 row stride
   static_assert(A_SLOTS >= 3 && A_SLOTS <= B_SLOTS, "ring depths");
-  static_assert(GG_BM * EPI_RS_BF16 <= PREFIX_OFF, "bf16 epilogue staging must fit");
-  static_assert(GG_BM * EPI_RS_ACT <= PREFIX_OFF, "SwiGLU epilogue staging must fit");
-  static_assert(TOTAL <= 160 * 1024, "LDS budget");
-  static_assert(AS_WAVES <= GG_WAVES && GG_WAVES >= 2, "MX scale copies need waves");
+  static_assert(BM * EPI_RS_BF16 <= PREFIX_OFF, "bf16 epilogue staging must fit");
+  static_assert(BM * EPI_RS_ACT <= PREFIX_OFF, "SwiGLU epilogue staging must fit");
+  static_assert(TOTAL * WG_PER_CU <= 160 * 1024, "LDS budget");
+  static_assert(AS_WAVES >= 1 && AS_WAVES <= WAVES && WAVES * 64 == BN, "scale copies: 64 rows / columns a wave");
+  static_assert(A_INSTR >= 1 && NI % 2 == 0 && MI >= 1, "tile shape");
 };
+using GGBig = GGCfg<256, 2, 3, 5, 1024, 1>;
+using GGSmall = GGCfg<64, 1, 3, 3, 256, 2>;
 
 // Direct global -> LDS copy: lane i of the wave writes its SZ bytes at LDS address M0 + SZ*i
 // (SZ = 16) or M0 + 4*i (SZ = 4). Written as inline assembly on purpose: for the compiler's
@@ -129,15 +136,20 @@ MI355_DEV void wait_vm(int n) {
   }
 }
 
-// Tile column j (0..255) -> weight column. SwiGLU: per 128-column half h, 64 gate then 64 up.
+// Tile column j (0..BN-1) -> weight column. SwiGLU: the columns of each wave tile (WN wide) are
+// WN/2 gate columns followed by the matching WN/2 up columns, so a lane holds gate and up of the
+// same output element.
+template <class C>
 MI355_DEV int tile_col_to_weight_col(int j, int nt, int I, bool swiglu) {
-  if (!swiglu) return nt * GG_BN + j;
-  int h = j >> 7, jj = j & 127;
-  int base = nt * 128 + h * 64;
-  return jj < 64 ? base + jj : I + base + (jj - 64);
+  if (!swiglu) return nt * C::BN + j;
+  constexpr int H = C::WN / 2;
+  static_assert(C::WN == 128 || C::WN == 64, "wave tile width");
+  int q = j >> (C::WN == 128 ? 7 : 6), jj = j & (C::WN - 1);
+  int base = nt * (C::BN / 2) + q * H;
+  return jj < H ? base + jj : I + base + (jj - H);
 }
 
-MI355_DEV int a_chunk_off(int r, int c) { return r * GG_KB + ((c ^ ((r >> 2) & 3)) << 4); }
+MI355_DEV int a_chunk_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 
 // ---- fragment loads (one K step: 16 bf16 or 64 e4m3) ------------------------------------------
 MI355_DEV v8bf read_a_bf16(const uint8_t* As, int r, int ks, int lane) {
@@ -146,51 +158,54 @@ MI355_DEV v8bf read_a_bf16(const uint8_t* As, int r, int ks, int lane) {
 
 // ---- copy plan -------------------------------------------------------------------------------
 // Per stage each wave issues A_INSTR + B_INSTR 16-byte DMA instructions; MX adds the B scale codes
-// (waves 0 and 1, one 4-byte DMA for 128 columns each) and, every 8 stages, 16 A scale codes per
-// row (AS_WAVES waves, one 16-byte DMA for 64 rows each).
+// (EIO weights: waves 0 and 1, one 4-byte DMA for 128 columns each, per stage) and, every 8
+// stages, 16 scale codes per A row (AS_WAVES waves, 64 rows each) and, for EOI weights, per B
+// column (every wave, 64 columns each).
+template <class C>
 struct CopyPlan {
-  const uint8_t* a[GGLds::A_INSTR];
-  const uint8_t* b[GGLds::B_INSTR];
+  const uint8_t* a[C::A_INSTR];
+  const uint8_t* b[C::B_INSTR];
   const uint8_t* s;        // MX: A scale row (waves < AS_WAVES)
-  const uint8_t* bs;       // MX KN: B scale column pair (waves 0 and 1)
-  const uint8_t* bsr;      // MX NK: B scale row (row wave*64 + lane of the tile)
+  const uint8_t* bs;       // MX EIO: B scale column pair (waves 0 and 1)
+  const uint8_t* bsr;      // MX EOI: B scale row (tile column wave*64 + lane)
   int64_t b_stage_stride;  // bytes to advance B per stage
   int64_t bs_stage_stride; // bytes to advance the B scales per stage
 };
 
-template <bool MX>
-MI355_DEV void issue_a(const CopyPlan& cp, int kt, int wave, uint8_t* smem) {
+template <class C, bool MX>
+MI355_DEV void issue_a(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
-  const uint32_t base = (kt % GGLds::A_SLOTS) * GGLds::A_BYTES;
-  const int64_t koff = (int64_t)kt * GG_KB;
+  const uint32_t base = (kt % C::A_SLOTS) * C::A_BYTES;
+  const int64_t koff = (int64_t)kt * C::KB;
 #pragma unroll
-  for (int j = 0; j < GGLds::A_INSTR; ++j)
-    lds_dma<16>(cp.a[j] + koff, base + (wave * GGLds::A_INSTR + j) * 1024, smem);
+  for (int j = 0; j < C::A_INSTR; ++j)
+    lds_dma<16>(cp.a[j] + koff, base + (wave * C::A_INSTR + j) * 1024, smem);
 }
 MI355_DEV bool is_bs_wave(int wave) { return wave < 2; }
-template <bool MX, bool B_KN>
-MI355_DEV void issue_b(const CopyPlan& cp, int kt, int wave, uint8_t* smem) {
+template <class C, bool MX, bool B_KN>
+MI355_DEV void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
   // (MX with K-contiguous weights has no per-stage scale copy: its scales come in groups)
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
-  const uint32_t base = GGLds::B_OFF + (kt % GGLds::B_SLOTS) * GGLds::B_SLOT;
+  const uint32_t base = C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT;
   const int64_t boff = (int64_t)kt * cp.b_stage_stride;
 #pragma unroll
-  for (int j = 0; j < GGLds::B_INSTR; ++j)
-    lds_dma<16>(cp.b[j] + boff, base + (wave * GGLds::B_INSTR + j) * 1024, smem);
+  for (int j = 0; j < C::B_INSTR; ++j)
+    lds_dma<16>(cp.b[j] + boff, base + (wave * C::B_INSTR + j) * 1024, smem);
   if (MX && B_KN && is_bs_wave(wave))
-    lds_dma<4>(cp.bs + kt * cp.bs_stage_stride, base + GGLds::B_BYTES + wave * 256, smem);
+    lds_dma<4>(cp.bs + kt * cp.bs_stage_stride, base + C::B_BYTES + wave * 256, smem);
 }
 // MX: A scale codes of stages 8*grp .. 8*grp+7 (16 bytes per row) into AS slot grp & 1.
-MI355_DEV void issue_as(const CopyPlan& cp, int grp, int wave, uint8_t* smem) {
+template <class C>
+MI355_DEV void issue_as(const CopyPlan<C>& cp, int grp, int wave, uint8_t* smem) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
-  if (wave < GGLds::AS_WAVES)
-    lds_dma<16>(cp.s + grp * 16, GGLds::AS_OFF + (grp & 1) * GGLds::AS_SLOT + wave * 1024, smem);
+  if (wave < C::AS_WAVES)
+    lds_dma<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + wave * 1024, smem);
 }
 
 #ifdef GG_TRACE
@@ -203,37 +218,45 @@ extern "C" int mi355_gg_trace_read(void* host) {
 #define GG_T(pt)
 #endif
 
-// Operand fragments of one stage for one wave (GG_WM rows x 128 columns x one stage of K). Values
+// Operand fragments of one stage for one wave (WM rows x WN columns x one stage of K). Values
 // that are read in several LDS instructions are kept as the raw pieces and joined only when the
 // MFMA consumes them, so that issuing the reads never forces a wait for their data.
-template <bool MX, bool B_KN> struct Frags;
-template <> struct Frags<false, false> { v8bf a[2][GG_MI], b[2][4]; };  // [ks][mi], [ks][ni]
-template <> struct Frags<false, true> { v8bf a[2][GG_MI]; v4s bl[2][4], bh[2][4]; };
-template <> struct Frags<true, true> { v4i al[GG_MI], ah[GG_MI]; v2i bp[4][4]; int sa[GG_MI], sb[4]; };
-template <> struct Frags<true, false> { v4i al[GG_MI], ah[GG_MI], bl[4], bh[4]; int sa[GG_MI], sb[4]; };
+template <class C, bool MX, bool B_KN> struct Frags;
+template <class C> struct Frags<C, false, false> { v8bf a[2][C::MI], b[2][C::NI]; };  // [ks][mi], [ks][ni]
+template <class C> struct Frags<C, false, true> { v8bf a[2][C::MI]; v4s bl[2][C::NI], bh[2][C::NI]; };
+template <class C> struct Frags<C, true, true> {
+  v4i al[C::MI], ah[C::MI];
+  v2i bp[C::NI][4];
+  int sa[C::MI], sb[C::NI];
+};
+template <class C> struct Frags<C, true, false> {
+  v4i al[C::MI], ah[C::MI], bl[C::NI], bh[C::NI];
+  int sa[C::MI], sb[C::NI];
+};
 
 // Element-wise fragment reads and MFMAs and the copies of one iteration, so that one pipelined
 // step can interleave them: MFMA t, then its share of the LDS reads of the next stage
 // and of the DMA copies. The wave never stalls on the DMA queue or on the LDS return queue for
 // long while the matrix core has work.
-template <bool MX, int NM> struct StepShape {
-  static constexpr int MFMAS = MX ? NM * 4 : 2 * NM * 4;
-  static constexpr int READS = MX ? 4 + NM : 2 * (4 + NM);  // fragment elements of a stage
-  static constexpr int ITEMS = GGLds::B_INSTR + 1 + GGLds::A_INSTR;  // B copies, B scales, A copies
+template <class C, bool MX, int NM> struct StepShape {
+  static constexpr int MFMAS = MX ? NM * C::NI : 2 * NM * C::NI;
+  static constexpr int READS = MX ? C::NI + NM : 2 * (C::NI + NM);  // fragment elements of a stage
+  static constexpr int ITEMS = C::B_INSTR + 1 + C::A_INSTR;          // B copies, B scales, A copies
 };
 
-template <bool MX, bool B_KN, int NM>
-MI355_DEV void read_elem(Frags<MX, B_KN>& f, int e, const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs,
+template <class C, bool MX, bool B_KN, int NM>
+MI355_DEV void read_elem(Frags<C, MX, B_KN>& f, int e, const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs,
                          const uint8_t* BSRs, int wm, int wn, int lane) {
+  constexpr int NI = C::NI;
   if constexpr (!MX) {
-    const int ks = e / (4 + NM), q = e % (4 + NM);
-    if (q < 4) {
+    const int ks = e / (NI + NM), q = e % (NI + NM);
+    if (q < NI) {
       if constexpr (!B_KN) {
-        const int n = wn * 128 + q * 32 + (lane & 31);
+        const int n = wn * C::WN + q * 32 + (lane & 31);
         f.b[ks][q] = *(const v8bf*)(Bs + a_chunk_off(n, ks * 2 + (lane >> 5)));
       } else {
         const int g16 = lane >> 4, m = lane & 15;
-        const int nb = wn * 128 + q * 32 + (g16 & 1) * 16 + 4 * (m & 3);
+        const int nb = wn * C::WN + q * 32 + (g16 & 1) * 16 + 4 * (m & 3);
         const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
         const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
         const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
@@ -241,48 +264,49 @@ MI355_DEV void read_elem(Frags<MX, B_KN>& f, int e, const uint8_t* As, const uin
         f.bh[ks][q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
       }
     } else {
-      f.a[ks][q - 4] = read_a_bf16(As, wm * GG_WM + (q - 4) * 32 + (lane & 31), ks, lane);
+      f.a[ks][q - NI] = read_a_bf16(As, wm * C::WM + (q - NI) * 32 + (lane & 31), ks, lane);
     }
   } else {
-    if (e < 4) {
+    if (e < NI) {
       if constexpr (B_KN) {
         const int g16 = lane >> 4, m = lane & 15;
-        const int nb = wn * 128 + e * 32 + (g16 & 1) * 16;
+        const int nb = wn * C::WN + e * 32 + (g16 & 1) * 16;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int k = (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
           const int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
           f.bp[e][q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
         }
-        f.sb[e] = Bs[GGLds::B_BYTES + (wn * 128 + e * 32 + (lane & 31)) * 2 + (lane >> 5)];
+        f.sb[e] = Bs[C::B_BYTES + (wn * C::WN + e * 32 + (lane & 31)) * 2 + (lane >> 5)];
       } else {
         // K-contiguous weight rows: same fragment layout as the activations
-        const int n = wn * 128 + e * 32 + (lane & 31);
+        const int n = wn * C::WN + e * 32 + (lane & 31);
         const int c0 = lane >> 5;
         f.bl[e] = *(const v4i*)(Bs + a_chunk_off(n, c0));
         f.bh[e] = *(const v4i*)(Bs + a_chunk_off(n, c0 + 2));
         f.sb[e] = BSRs[n * 16 + (lane >> 5)];
       }
     } else {
-      const int r = wm * GG_WM + (e - 4) * 32 + (lane & 31);
+      const int r = wm * C::WM + (e - NI) * 32 + (lane & 31);
       const int c0 = lane >> 5;
-      f.al[e - 4] = *(const v4i*)(As + a_chunk_off(r, c0));
-      f.ah[e - 4] = *(const v4i*)(As + a_chunk_off(r, c0 + 2));
-      f.sa[e - 4] = ASs[r * 16 + (lane >> 5)];
+      f.al[e - NI] = *(const v4i*)(As + a_chunk_off(r, c0));
+      f.ah[e - NI] = *(const v4i*)(As + a_chunk_off(r, c0 + 2));
+      f.sa[e - NI] = ASs[r * 16 + (lane >> 5)];
     }
   }
 }
 
-template <bool MX, bool B_KN, int NM>
-MI355_DEV void mfma_elem(const Frags<MX, B_KN>& f, v16f (&acc)[GG_MI][4], int t) {
+template <class C, bool MX, bool B_KN, int NM>
+MI355_DEV void mfma_elem(const Frags<C, MX, B_KN>& f, v16f (&acc)[C::MI][C::NI], int t) {
+  constexpr int NI = C::NI;
   if constexpr (!MX) {
-    const int ks = t / (NM * 4), mi = (t / 4) % NM, ni = t % 4;
+    const int ks = t / (NM * NI), mi = (t / NI) % NM, ni = t % NI;
     v8bf b;
     if constexpr (!B_KN) b = f.b[ks][ni];
     else b = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.bl[ks][ni], f.bh[ks][ni], 0, 1, 2, 3, 4, 5, 6, 7));
     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[ks][mi], b, acc[mi][ni], 0, 0, 0);
   } else {
-    const int mi = t / 4, ni = t % 4;
+    const int mi = t / NI, ni = t % NI;
     const v8i a = __builtin_shufflevector(f.al[mi], f.ah[mi], 0, 1, 2, 3, 4, 5, 6, 7);
     v8i b;
     if constexpr (B_KN) {
@@ -297,46 +321,44 @@ MI355_DEV void mfma_elem(const Frags<MX, B_KN>& f, v16f (&acc)[GG_MI][4], int t)
 }
 
 // Copy item it of iteration i (same order as issue_iteration: B copies, B scales, A copies).
-template <bool MX, bool B_KN, bool LA>
-MI355_DEV void issue_item(const CopyPlan& cp, int i, int nk, int wave, uint8_t* smem, int it) {
+template <class C, bool MX, bool B_KN, bool LA>
+MI355_DEV void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem, int it) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
-  constexpr int DA = GGLds::A_SLOTS, DB = GGLds::B_SLOTS;
-  if (it < GGLds::B_INSTR) {
+  constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
+  if (it < C::B_INSTR) {
     const int kt = i + DB;
     lds_dma<16>(cp.b[it] + (int64_t)kt * cp.b_stage_stride,
-                GGLds::B_OFF + (kt % GGLds::B_SLOTS) * GGLds::B_SLOT + (wave * GGLds::B_INSTR + it) * 1024, smem,
-                kt < nk);
-  } else if (it == GGLds::B_INSTR) {
+                C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + (wave * C::B_INSTR + it) * 1024, smem, kt < nk);
+  } else if (it == C::B_INSTR) {
     const int kt = i + DB;
     if constexpr (MX && B_KN)
-      lds_dma<4>(cp.bs + kt * cp.bs_stage_stride,
-                 GGLds::B_OFF + (kt % GGLds::B_SLOTS) * GGLds::B_SLOT + GGLds::B_BYTES + (wave & 1) * 256, smem,
-                 is_bs_wave(wave) && kt < nk);
+      lds_dma<4>(cp.bs + kt * cp.bs_stage_stride, C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + C::B_BYTES + (wave & 1) * 256,
+                 smem, is_bs_wave(wave) && kt < nk);
   } else if constexpr (LA) {
-    const int j = it - GGLds::B_INSTR - 1;
+    const int j = it - C::B_INSTR - 1;
     const int kt = i + DA;
-    lds_dma<16>(cp.a[j] + (int64_t)kt * GG_KB, (kt % GGLds::A_SLOTS) * GGLds::A_BYTES + (wave * GGLds::A_INSTR + j) * 1024,
-                smem, kt < nk);
+    lds_dma<16>(cp.a[j] + (int64_t)kt * C::KB, (kt % C::A_SLOTS) * C::A_BYTES + (wave * C::A_INSTR + j) * 1024, smem,
+                kt < nk);
   }
 }
 
 // MX: the scale groups due at iteration i (every AS_GROUP stages: A rows and, for K-contiguous
 // weights, B rows), each as one conditional copy.
-template <bool MX, bool B_KN, bool LA>
-MI355_DEV void issue_scales_item(const CopyPlan& cp, int i, int nk, int wave, uint8_t* smem) {
+template <class C, bool MX, bool B_KN, bool LA>
+MI355_DEV void issue_scales_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
   if constexpr (MX) {
-    const int grp = i / GGLds::AS_GROUP + 1;
-    const bool due = (i & (GGLds::AS_GROUP - 1)) == 0 && i + GGLds::AS_GROUP < nk;
+    const int grp = i / C::AS_GROUP + 1;
+    const bool due = (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk;
     if constexpr (LA)
-      lds_dma<16>(cp.s + grp * 16, GGLds::AS_OFF + (grp & 1) * GGLds::AS_SLOT + (wave & 3) * 1024, smem,
-                  due && wave < GGLds::AS_WAVES);
+      lds_dma<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 3) * 1024, smem,
+                  due && wave < C::AS_WAVES);
     if constexpr (!B_KN)
-      lds_dma<16>(cp.bsr + grp * 16, GGLds::BSR_OFF + (grp & 1) * GGLds::BSR_SLOT + (wave & 3) * 1024, smem, due);
+      lds_dma<16>(cp.bsr + grp * 16, C::BSR_OFF + (grp & 1) * C::BSR_SLOT + (wave & 3) * 1024, smem, due);
   }
 }
 
@@ -346,9 +368,9 @@ MI355_DEV void issue_scales_item(const CopyPlan& cp, int i, int nk, int wave, ui
 // (iteration j - DA; B(j) came earlier) for a wave that copies A, else B(j) (iteration j - DB).
 // Scale groups issued between are not counted, which only makes the wait stricter. Loads of one
 // wave retire in order.
-template <bool LA>
+template <class C, bool LA>
 MI355_DEV int younger_than(int j, int last, int nk, int la_n, int lb_n) {
-  constexpr int DA = GGLds::A_SLOTS, DB = GGLds::B_SLOTS;
+  constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
   const int from = (LA ? j - DA : j - DB) + 1;
   // iterations i in [from, last] with i + DB < nk, and (A) with 0 <= i + DA < nk
   const int nb = min(last, nk - DB - 1) - from + 1;
@@ -360,16 +382,16 @@ MI355_DEV int younger_than(int j, int last, int nk, int la_n, int lb_n) {
   return n;
 }
 
-template <bool MX, bool B_KN, bool LA>
-MI355_DEV void issue_iteration(const CopyPlan& cp, int i, int nk, int wave, uint8_t* smem) {
-  constexpr int DA = GGLds::A_SLOTS, DB = GGLds::B_SLOTS;
-  if (i + DB < nk) issue_b<MX, B_KN>(cp, i + DB, wave, smem);
+template <class C, bool MX, bool B_KN, bool LA>
+MI355_DEV void issue_iteration(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
+  constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
+  if (i + DB < nk) issue_b<C, MX, B_KN>(cp, i + DB, wave, smem);
   if (LA && i + DA >= 0 && i + DA < nk) {
-    if (MX && i + DA == 0) issue_as(cp, 0, wave, smem);
-    issue_a<MX>(cp, i + DA, wave, smem);
+    if (MX && i + DA == 0) issue_as<C>(cp, 0, wave, smem);
+    issue_a<C, MX>(cp, i + DA, wave, smem);
   }
-  if (LA && MX && i >= 0 && (i & (GGLds::AS_GROUP - 1)) == 0 && i + GGLds::AS_GROUP < nk)
-    issue_as(cp, i / GGLds::AS_GROUP + 1, wave, smem);
+  if (LA && MX && i >= 0 && (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk)
+    issue_as<C>(cp, i / C::AS_GROUP + 1, wave, smem);
 }
 
 // K loop, software-pipelined in each wave: iteration k (after barrier k) refills the ring slots of
@@ -380,29 +402,29 @@ MI355_DEV void issue_iteration(const CopyPlan& cp, int i, int nk, int wave, uint
 // A-scale group g+1 (stages 8g+8 ..) is issued at iteration 8g into the slot of group g-1, whose
 // last stage was read during iteration 8g-2.
 // NM = number of 32-row subtiles this wave computes (0, 1, 2 or 4).
-template <bool MX, bool B_KN, int NM, bool LA>
-MI355_DEV void k_loop(const CopyPlan& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
-                      v16f (&acc)[GG_MI][4]) {
-  constexpr int DB = GGLds::B_SLOTS;
-  const int la_n = GGLds::A_INSTR;
-  const int lb_n = GGLds::B_INSTR + ((MX && B_KN && is_bs_wave(wave)) ? 1 : 0);  // loads per B stage
-  if constexpr (MX && !B_KN) lds_dma<16>(cp.bsr, GGLds::BSR_OFF + (wave & 3) * 1024, smem);  // B scale group 0
-  for (int i = -DB; i < 0; ++i) issue_iteration<MX, B_KN, LA>(cp, i, nk, wave, smem);
-  Frags<MX, B_KN> f0, f1;
-  wait_vm(younger_than<LA>(0, -1, nk, la_n, lb_n));
+template <class C, bool MX, bool B_KN, int NM, bool LA>
+MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
+                      v16f (&acc)[C::MI][C::NI]) {
+  constexpr int DB = C::B_SLOTS;
+  const int la_n = C::A_INSTR;
+  const int lb_n = C::B_INSTR + ((MX && B_KN && is_bs_wave(wave)) ? 1 : 0);  // loads per B stage
+  if constexpr (MX && !B_KN) lds_dma<16>(cp.bsr, C::BSR_OFF + (wave & 3) * 1024, smem);  // B scale group 0
+  for (int i = -DB; i < 0; ++i) issue_iteration<C, MX, B_KN, LA>(cp, i, nk, wave, smem);
+  Frags<C, MX, B_KN> f0, f1;
+  wait_vm(younger_than<C, LA>(0, -1, nk, la_n, lb_n));
   lds_barrier();
+  using SS = StepShape<C, MX, NM>;
   if constexpr (NM > 0) {
-    const uint8_t* ASs = smem + GGLds::AS_OFF;
+    const uint8_t* ASs = smem + C::AS_OFF;
 #pragma unroll
-    for (int e = 0; e < StepShape<MX, NM>::READS; ++e)
-      read_elem<MX, B_KN, NM>(f0, e, smem, smem + GGLds::B_OFF, ASs, smem + GGLds::BSR_OFF, wm, wn, lane);
+    for (int e = 0; e < SS::READS; ++e)
+      read_elem<C, MX, B_KN, NM>(f0, e, smem, smem + C::B_OFF, ASs, smem + C::BSR_OFF, wm, wn, lane);
   }
   // one pipelined iteration with a next stage (k + 1 < nk)
-  using SS = StepShape<MX, NM>;
-  auto step = [&](int k, Frags<MX, B_KN>& cur, Frags<MX, B_KN>& nxt) {
+  auto step = [&](int k, Frags<C, MX, B_KN>& cur, Frags<C, MX, B_KN>& nxt) {
     __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs of the previous stage above the barrier
     GG_T(0)
-    wait_vm(younger_than<LA>(k + 1, k - 1, nk, la_n, lb_n));
+    wait_vm(younger_than<C, LA>(k + 1, k - 1, nk, la_n, lb_n));
     GG_T(1)
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -410,30 +432,28 @@ MI355_DEV void k_loop(const CopyPlan& cp, int nk, int wave, int wm, int wn, int 
     int ln = lane;
     asm volatile("" : "+v"(ln));  // recompute lane-dependent LDS offsets here rather than hold them
     const int kn = k + 1;
-    const uint8_t* As = smem + (kn % GGLds::A_SLOTS) * GGLds::A_BYTES;
-    const uint8_t* Bs = smem + GGLds::B_OFF + (kn % GGLds::B_SLOTS) * GGLds::B_SLOT;
-    const uint8_t* ASs = smem + GGLds::AS_OFF + ((kn / GGLds::AS_GROUP) & 1) * GGLds::AS_SLOT +
-                         (kn & (GGLds::AS_GROUP - 1)) * 2;
-    const uint8_t* BSRs = smem + GGLds::BSR_OFF + ((kn / GGLds::AS_GROUP) & 1) * GGLds::BSR_SLOT +
-                          (kn & (GGLds::AS_GROUP - 1)) * 2;
+    const uint8_t* As = smem + (kn % C::A_SLOTS) * C::A_BYTES;
+    const uint8_t* Bs = smem + C::B_OFF + (kn % C::B_SLOTS) * C::B_SLOT;
+    const uint8_t* ASs = smem + C::AS_OFF + ((kn / C::AS_GROUP) & 1) * C::AS_SLOT + (kn & (C::AS_GROUP - 1)) * 2;
+    const uint8_t* BSRs = smem + C::BSR_OFF + ((kn / C::AS_GROUP) & 1) * C::BSR_SLOT + (kn & (C::AS_GROUP - 1)) * 2;
     constexpr int T = SS::MFMAS > 0 ? SS::MFMAS : 1;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
 #ifndef GG_ABLATE_COMPUTE
       if constexpr (NM > 0) {
-        mfma_elem<MX, B_KN, NM>(cur, acc, t);
+        mfma_elem<C, MX, B_KN, NM>(cur, acc, t);
 #pragma unroll
         for (int e = t * SS::READS / T; e < (t + 1) * SS::READS / T; ++e)
-          read_elem<MX, B_KN, NM>(nxt, e, As, Bs, ASs, BSRs, wm, wn, ln);
+          read_elem<C, MX, B_KN, NM>(nxt, e, As, Bs, ASs, BSRs, wm, wn, ln);
       }
 #endif
 #pragma unroll
       for (int it = t * SS::ITEMS / T; it < (t + 1) * SS::ITEMS / T; ++it)
-        issue_item<MX, B_KN, LA>(cp, k, nk, wave, smem, it);
+        issue_item<C, MX, B_KN, LA>(cp, k, nk, wave, smem, it);
       if (t == T / 2 - 1) { GG_T(3) }
       __builtin_amdgcn_sched_barrier(0);  // keep this interleave order
     }
-    issue_scales_item<MX, B_KN, LA>(cp, k, nk, wave, smem);
+    issue_scales_item<C, MX, B_KN, LA>(cp, k, nk, wave, smem);
     GG_T(4)
   };
   // Stages 0 .. nk-2 are pipelined steps (each reads the next stage), taken in pairs so that the
@@ -454,30 +474,30 @@ MI355_DEV void k_loop(const CopyPlan& cp, int nk, int wave, int wm, int wn, int 
 #ifndef GG_ABLATE_COMPUTE
   if constexpr (NM > 0) {
 #pragma unroll
-    for (int t = 0; t < StepShape<MX, NM>::MFMAS; ++t) mfma_elem<MX, B_KN, NM>(f0, acc, t);
+    for (int t = 0; t < SS::MFMAS; ++t) mfma_elem<C, MX, B_KN, NM>(f0, acc, t);
   }
 #endif
 }
 
-template <bool MX, bool B_KN, int EPI>
-__global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p) {
+template <class C, bool MX, bool B_KN, int EPI>
+__global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(GGParams p) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  int32_t* s_prefix = (int32_t*)(smem + GGLds::PREFIX_OFF);
+  int32_t* s_prefix = (int32_t*)(smem + C::PREFIX_OFF);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = (int)((unsigned)wave / C::WGN), wn = (int)((unsigned)wave % C::WGN);
   constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX);
   constexpr int ESIZE = MX ? 1 : 2;
 
-  const bool prefix_in_lds = p.G <= GGLds::PREFIX_MAX;
+  const bool prefix_in_lds = p.G <= C::PREFIX_MAX;
   const int32_t* prefix = prefix_in_lds ? s_prefix : p.tile_prefix;
   if (prefix_in_lds)
-    for (int g = tid; g <= p.G; g += GG_THREADS) s_prefix[g] = p.tile_prefix[g];
+    for (int g = tid; g <= p.G; g += C::THREADS) s_prefix[g] = p.tile_prefix[g];
   __syncthreads();
   const int splits = (EPI == EPI_STORE_F32 && p.k_splits > 1) ? p.k_splits : 1;
   const int total = prefix[p.G] * p.n_tiles * splits;
-  const int nk = p.K / splits * ESIZE / GG_KB;  // stages per work item
+  const int nk = p.K / splits * ESIZE / C::KB;  // stages per work item
   const int xcd = blockIdx.x & 7;
   const int per_xcd = gridDim.x >> 3;
   const int slot = blockIdx.x >> 3;
@@ -500,14 +520,14 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     const int mt = local - nt * mtiles;
     const int64_t row_begin = (g == 0 ? 0 : p.group_list[g - 1]);
     const int64_t row_end = p.group_list[g];
-    const int64_t tile_row0 = row_begin + (int64_t)mt * GG_BM;
-    const int rows_valid = (int)((row_end - tile_row0) < GG_BM ? (row_end - tile_row0) : GG_BM);
+    const int64_t tile_row0 = row_begin + (int64_t)mt * C::BM;
+    const int rows_valid = (int)((row_end - tile_row0) < C::BM ? (row_end - tile_row0) : C::BM);
 
     // ---- per-thread copy sources ------------------------------------------------------
-    CopyPlan cp;
+    CopyPlan<C> cp;
 #pragma unroll
-    for (int j = 0; j < GGLds::A_INSTR; ++j) {
-      int L16 = (wave * GGLds::A_INSTR + j) * 64 + lane;
+    for (int j = 0; j < C::A_INSTR; ++j) {
+      int L16 = (wave * C::A_INSTR + j) * 64 + lane;
       int r = L16 >> 2, cs = L16 & 3;
       int c = cs ^ ((r >> 2) & 3);
       int rr = r < rows_valid ? r : rows_valid - 1;
@@ -517,42 +537,42 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
     }
     const uint8_t* bgrp = p.B + (int64_t)g * p.b_group_stride;
 #pragma unroll
-    for (int j = 0; j < GGLds::B_INSTR; ++j) {
-      int L16 = (wave * GGLds::B_INSTR + j) * 64 + lane;
+    for (int j = 0; j < C::B_INSTR; ++j) {
+      int L16 = (wave * C::B_INSTR + j) * 64 + lane;
       if (!B_KN) {
         int r = L16 >> 2, cs = L16 & 3;
         int c = cs ^ ((r >> 2) & 3);
-        int wc = tile_col_to_weight_col(r, nt, p.N, SWIGLU);
+        int wc = tile_col_to_weight_col<C>(r, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 1;
         cp.b[j] = bgrp + (int64_t)wc * p.b_row_bytes + c * 16;
       } else if (MX) {
         int k = L16 >> 4, cs = L16 & 15;
         int c = cs ^ (k & 15);
-        int wc = tile_col_to_weight_col(c * 16, nt, p.N, SWIGLU);
+        int wc = tile_col_to_weight_col<C>(c * 16, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 16;
         cp.b[j] = bgrp + (int64_t)k * p.b_row_bytes + wc;
       } else {
         int k = L16 >> 5, cs = L16 & 31;
         int c = cs ^ ((k & 7) << 1);
-        int wc = tile_col_to_weight_col(c * 8, nt, p.N, SWIGLU);
+        int wc = tile_col_to_weight_col<C>(c * 8, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 8;
         cp.b[j] = bgrp + (int64_t)k * p.b_row_bytes + (int64_t)wc * 2;
       }
     }
-    cp.b_stage_stride = B_KN ? (int64_t)(GG_KB / ESIZE) * p.b_row_bytes : GG_KB;
+    cp.b_stage_stride = B_KN ? (int64_t)(C::KB / ESIZE) * p.b_row_bytes : C::KB;
     if (splits > 1) {
       const int64_t k0_stages = (int64_t)split * nk;
 #pragma unroll
-      for (int j = 0; j < GGLds::A_INSTR; ++j) cp.a[j] += k0_stages * GG_KB;
+      for (int j = 0; j < C::A_INSTR; ++j) cp.a[j] += k0_stages * C::KB;
 #pragma unroll
-      for (int j = 0; j < GGLds::B_INSTR; ++j) cp.b[j] += k0_stages * cp.b_stage_stride;
+      for (int j = 0; j < C::B_INSTR; ++j) cp.b[j] += k0_stages * cp.b_stage_stride;
     }
     cp.s = nullptr;
     cp.bs = nullptr;
     cp.bsr = nullptr;
     cp.bs_stage_stride = 0;
     if (MX) {
-      if (wave < GGLds::AS_WAVES) {
+      if (wave < C::AS_WAVES) {
         // A scales: row wave*64 + lane (16 codes = 8 stages per fetch)
         int r = wave * 64 + lane;
         int rr = r < rows_valid ? r : rows_valid - 1;
@@ -562,103 +582,103 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
       }
       if (!B_KN) {
         // B row scales: tile column wave*64 + lane (16 codes = 8 stages per fetch)
-        int wc = tile_col_to_weight_col(wave * 64 + lane, nt, p.N, SWIGLU);
+        int wc = tile_col_to_weight_col<C>(wave * 64 + lane, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 1;
         cp.bsr = p.b_scale + ((int64_t)g * p.Ntot + wc) * p.b_scale_ld;
       } else if (is_bs_wave(wave)) {
         // B scales: tile columns (wave*64 + lane)*2 .. +1, one col_scale group per stage
         int j = (wave * 64 + lane) * 2;
-        int wc = tile_col_to_weight_col(j, nt, p.N, SWIGLU);
+        int wc = tile_col_to_weight_col<C>(j, nt, p.N, SWIGLU);
         if (wc >= p.Ntot) wc = p.Ntot - 2;
         cp.bs = p.b_scale + (int64_t)g * p.b_scale_group_stride + (int64_t)wc * 2;
         cp.bs_stage_stride = (int64_t)p.Ntot * 2;
       }
     }
 
-    v16f acc[GG_MI][4];
+    v16f acc[C::MI][C::NI];
 #pragma unroll
-    for (int i = 0; i < GG_MI; ++i)
+    for (int i = 0; i < C::MI; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < C::NI; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     __syncthreads();  // the previous item's last stage / epilogue reads are done before refilling
-    const int rows_w = rows_valid - wm * GG_WM;
-    const int nm = rows_w > 64 ? 4 : (rows_w > 32 ? 2 : (rows_w >= 1 ? 1 : 0));
+    const int rows_w = rows_valid - wm * C::WM;
+    const int nm = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
     // this wave copies A rows wave*RPW .. +RPW-1 (and, MX scale waves, scale rows wave*64 .. +63)
-    constexpr int RPW = GGLds::A_INSTR * 16;  // A rows per wave
+    constexpr int RPW = C::A_INSTR * 16;  // A rows per wave
     const bool la = wave * RPW < rows_valid;
     if (la) {
-      if (nm == 4) k_loop<MX, B_KN, 4, true>(cp, nk, wave, wm, wn, lane, smem, acc);
-      else if (nm == 2) k_loop<MX, B_KN, 2, true>(cp, nk, wave, wm, wn, lane, smem, acc);
-      else if (nm == 1) k_loop<MX, B_KN, 1, true>(cp, nk, wave, wm, wn, lane, smem, acc);
-      else k_loop<MX, B_KN, 0, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      if (C::MI >= 4 && nm == 4) k_loop<C, MX, B_KN, (C::MI >= 4 ? 4 : 1), true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 2) k_loop<C, MX, B_KN, 2, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 1) k_loop<C, MX, B_KN, 1, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else k_loop<C, MX, B_KN, 0, true>(cp, nk, wave, wm, wn, lane, smem, acc);
     } else {
-      if (nm == 4) k_loop<MX, B_KN, 4, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-      else if (nm == 2) k_loop<MX, B_KN, 2, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-      else if (nm == 1) k_loop<MX, B_KN, 1, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-      else k_loop<MX, B_KN, 0, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      if (C::MI >= 4 && nm == 4) k_loop<C, MX, B_KN, (C::MI >= 4 ? 4 : 1), false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 2) k_loop<C, MX, B_KN, 2, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 1) k_loop<C, MX, B_KN, 1, false>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else k_loop<C, MX, B_KN, 0, false>(cp, nk, wave, wm, wn, lane, smem, acc);
     }
     __syncthreads();  // all waves are done reading the ring before the epilogue reuses LDS
 
     // ---- epilogue -----------------------------------------------------------------------
-    // acc[mi][ni][r] holds row wm*GG_WM + mi*32 + 8*(r/4) + 4*(lane/32) + r%4,
-    // column wn*128 + ni*32 + lane%32 of the tile.
+    // acc[mi][ni][r] holds row wm*WM + mi*32 + 8*(r/4) + 4*(lane/32) + r%4,
+    // column wn*WN + ni*32 + lane%32 of the tile.
     if (EPI == EPI_STORE_F32) {
-      float* C = (float*)p.C;
+      float* outp = (float*)p.C;
 #pragma unroll
-      for (int mi = 0; mi < GG_MI; ++mi)
+      for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
+        for (int ni = 0; ni < C::NI; ++ni) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            int row = wm * GG_WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            int col = nt * GG_BN + wn * 128 + ni * 32 + (lane & 31);
+            int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            int col = nt * C::BN + wn * C::WN + ni * 32 + (lane & 31);
             if (row < rows_valid && col < p.N) {
               int64_t routed = tile_row0 + row;
               int64_t orow = p.c_row_index ? (int64_t)p.c_row_index[routed] : routed;
-              C[split * p.c_split_stride + orow * p.ldc + col] = acc[mi][ni][r];
+              outp[split * p.c_split_stride + orow * p.ldc + col] = acc[mi][ni][r];
             }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
     } else if (EPI == EPI_STORE_BF16) {
-      constexpr int RS = GGLds::EPI_RS_BF16;  // staged row stride (bytes)
+      constexpr int RS = C::EPI_RS_BF16;  // staged row stride (bytes)
 #pragma unroll
-      for (int mi = 0; mi < GG_MI; ++mi)
+      for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
+        for (int ni = 0; ni < C::NI; ++ni) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            int row = wm * GG_WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            int col = wn * 128 + ni * 32 + (lane & 31);
+            int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            int col = wn * C::WN + ni * 32 + (lane & 31);
             *(uint16_t*)(smem + row * RS + col * 2) = f32_to_bf16(acc[mi][ni][r]);
           }
           __builtin_amdgcn_sched_barrier(0);  // one 32x32 block at a time: bounded register use
         }
       __syncthreads();
-      uint16_t* C = (uint16_t*)p.C;
-      for (int id = tid; id < GG_BM * (GG_BN / 8); id += GG_THREADS) {
+      uint16_t* outp = (uint16_t*)p.C;
+      for (int id = tid; id < C::BM * (C::BN / 8); id += C::THREADS) {
         int row = id >> 5, ch = id & 31;
-        int col = nt * GG_BN + ch * 8;
+        int col = nt * C::BN + ch * 8;
         if (row < rows_valid && col < p.N)
-          *(uint4*)(C + (tile_row0 + row) * p.ldc + col) = *(const uint4*)(smem + row * RS + ch * 16);
+          *(uint4*)(outp + (tile_row0 + row) * p.ldc + col) = *(const uint4*)(smem + row * RS + ch * 16);
       }
       __syncthreads();
     } else {
-      // SwiGLU: subtiles ni=0,1 hold gate, ni=2,3 the matching up columns.
-      constexpr int RS = GGLds::EPI_RS_ACT;  // fp32 staged act row stride
+      // SwiGLU: subtiles ni < NI/2 hold gate, ni + NI/2 the matching up columns.
+      constexpr int RS = C::EPI_RS_ACT;  // fp32 staged act row stride
 #pragma unroll
-      for (int mi = 0; mi < GG_MI; ++mi)
+      for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
+        for (int ni = 0; ni < C::NI / 2; ++ni) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            int row = wm * GG_WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            int col = wn * 64 + ni * 32 + (lane & 31);
+            int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            int col = wn * (C::WN / 2) + ni * 32 + (lane & 31);
             float gte = bf16_to_f32(f32_to_bf16(acc[mi][ni][r]));
-            float up = bf16_to_f32(f32_to_bf16(acc[mi][ni + 2][r]));
+            float up = bf16_to_f32(f32_to_bf16(acc[mi][ni + C::NI / 2][r]));
             float act;
             if (EPI == EPI_SWIGLU_BF16 && p.swiglu_limit > 0.0f) {
               // MegaMoeNumericsOptions clamp: up to [-L, L]; gate to <= L before SiLU, or SiLU(gate)
@@ -679,8 +699,8 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
         }
       __syncthreads();
       if (EPI == EPI_SWIGLU_BF16) {
-        uint16_t* C = (uint16_t*)p.C;
-        for (int id = tid; id < GG_BM * 16; id += GG_THREADS) {
+        uint16_t* outp = (uint16_t*)p.C;
+        for (int id = tid; id < C::BM * 16; id += C::THREADS) {
           int row = id >> 4, ch = id & 15;
           if (row < rows_valid) {
             const float* s = (const float*)(smem + row * RS + ch * 32);
@@ -699,12 +719,12 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
             o.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
             o.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
             o.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
-            *(uint4*)(C + (tile_row0 + row) * p.ldc + nt * 128 + ch * 8) = o;
+            *(uint4*)(outp + (tile_row0 + row) * p.ldc + nt * (C::BN / 2) + ch * 8) = o;
           }
         }
       } else {
-        uint8_t* C = (uint8_t*)p.C;
-        for (int id = tid; id < GG_BM * 4; id += GG_THREADS) {
+        uint8_t* outp = (uint8_t*)p.C;
+        for (int id = tid; id < C::BM * 4; id += C::THREADS) {
           int row = id >> 2, blk = id & 3;
           if (row < rows_valid) {
             const float* s = (const float*)(smem + row * RS + blk * 128);
@@ -721,7 +741,7 @@ __global__ __launch_bounds__(GG_THREADS, 1) void grouped_gemm_kernel(GGParams p)
               uint32_t b3 = f32_to_e4m3(mx_apply_inv_scale(s[4 * i + 3], code));
               w[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
             }
-            uint8_t* dst = C + (tile_row0 + row) * p.ldc + nt * 128 + blk * 32;
+            uint8_t* dst = outp + (tile_row0 + row) * p.ldc + nt * (C::BN / 2) + blk * 32;
             *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
             *(uint4*)(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
             p.c_scale[(tile_row0 + row) * p.c_scale_ld + nt * 4 + blk] = (uint8_t)code;
@@ -760,58 +780,68 @@ static int num_cus() {
   return g_num_cus;
 }
 
-template <bool MX, bool B_KN, int EPI>
+template <class C, bool MX, bool B_KN, int EPI>
 static int launch_gg(const GGParams& p, hipStream_t stream) {
   static bool configured = false;
-  auto kern = grouped_gemm_kernel<MX, B_KN, EPI>;
+  auto kern = grouped_gemm_kernel<C, MX, B_KN, EPI>;
   if (!configured) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, GGLds::TOTAL) != hipSuccess)
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::TOTAL) != hipSuccess)
       return MI355MOE_ELAUNCH;
     configured = true;
   }
-  int grid = (num_cus() / 8) * 8;
+  int grid = (num_cus() / 8) * 8 * C::WG_PER_CU;
   if (grid < 8) grid = 8;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(GG_THREADS), GGLds::TOTAL, stream, p);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(C::THREADS), C::TOTAL, stream, p);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
-int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream) {
-  hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, stream, group_list, G, GG_BM, tile_prefix);
+int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream, bool small) {
+  hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, stream, group_list, G, mi355_gg_bm(small), tile_prefix);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
-// Internal dispatcher used by the C-ABI entry points.
-// kind: 0 plain bf16 out, 1 fp32 out, 2 swiglu bf16, 3 swiglu mx
-int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream) {
+template <class C>
+static int dispatch_gg(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream) {
   if (!mx) {
     if (!b_kn) {
       switch (epi) {
-        case EPI_STORE_BF16: return launch_gg<false, false, EPI_STORE_BF16>(p, stream);
-        case EPI_STORE_F32: return launch_gg<false, false, EPI_STORE_F32>(p, stream);
-        case EPI_SWIGLU_BF16: return launch_gg<false, false, EPI_SWIGLU_BF16>(p, stream);
+        case EPI_STORE_BF16: return launch_gg<C, false, false, EPI_STORE_BF16>(p, stream);
+        case EPI_STORE_F32: return launch_gg<C, false, false, EPI_STORE_F32>(p, stream);
+        case EPI_SWIGLU_BF16: return launch_gg<C, false, false, EPI_SWIGLU_BF16>(p, stream);
         default: return MI355MOE_EUNSUPPORTED;
       }
     } else {
       switch (epi) {
-        case EPI_STORE_BF16: return launch_gg<false, true, EPI_STORE_BF16>(p, stream);
-        case EPI_SWIGLU_BF16: return launch_gg<false, true, EPI_SWIGLU_BF16>(p, stream);
+        case EPI_STORE_BF16: return launch_gg<C, false, true, EPI_STORE_BF16>(p, stream);
+        case EPI_SWIGLU_BF16: return launch_gg<C, false, true, EPI_SWIGLU_BF16>(p, stream);
         default: return MI355MOE_EUNSUPPORTED;
       }
     }
   }
   if (!b_kn) {
     switch (epi) {
-      case EPI_STORE_BF16: return launch_gg<true, false, EPI_STORE_BF16>(p, stream);
-      case EPI_SWIGLU_MX: return launch_gg<true, false, EPI_SWIGLU_MX>(p, stream);
+      case EPI_STORE_BF16: return launch_gg<C, true, false, EPI_STORE_BF16>(p, stream);
+      case EPI_SWIGLU_MX: return launch_gg<C, true, false, EPI_SWIGLU_MX>(p, stream);
       default: return MI355MOE_EUNSUPPORTED;
     }
   }
   switch (epi) {
-    case EPI_STORE_BF16: return launch_gg<true, true, EPI_STORE_BF16>(p, stream);
-    case EPI_SWIGLU_MX: return launch_gg<true, true, EPI_SWIGLU_MX>(p, stream);
+    case EPI_STORE_BF16: return launch_gg<C, true, true, EPI_STORE_BF16>(p, stream);
+    case EPI_SWIGLU_MX: return launch_gg<C, true, true, EPI_SWIGLU_MX>(p, stream);
     default: return MI355MOE_EUNSUPPORTED;
   }
 }
 
-int mi355_gg_bm() { return GG_BM; }
-int mi355_gg_bn() { return GG_BN; }
+// Internal dispatcher used by the C-ABI entry points. `small` selects the 64-row tile
+// configuration (the tile prefix must have been planned with the same one).
+int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, bool small) {
+  if (small) {
+    // the EPI_STORE_F32 router projection keeps the big tiles
+    if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
+    return dispatch_gg<GGSmall>(p, mx, b_kn, epi, stream);
+  }
+  return dispatch_gg<GGBig>(p, mx, b_kn, epi, stream);
+}
+
+int mi355_gg_bm(bool small) { return small ? GGSmall::BM : GGBig::BM; }
+int mi355_gg_bn() { return GGBig::BN; }

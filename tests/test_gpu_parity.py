@@ -414,3 +414,69 @@ def test_moe_forward_probs_before_fc2_power_of_two_is_bit_exact_to_after(gpu):
     b = ops.moe_forward(x.to(gpu), ids.to(gpu), p2.to(gpu), w1.to(gpu), w2.to(gpu), apply_probs_before_fc2=True,
                         **args).cpu()
     assert torch.equal(a, b)
+
+
+def _decode_counts(G, seed, hi=40):
+    g = torch.Generator().manual_seed(seed)
+    c = torch.randint(0, hi, (G,), generator=g)
+    c[torch.randperm(G, generator=g)[: G // 3]] = 0  # many empty groups, as in skewed decode routing
+    return c.tolist()
+
+
+@pytest.mark.parametrize("layout", ["EIO", "EOI"])
+def test_grouped_gemm_bf16_decode_shape(gpu, layout):
+    """Many groups with a few rows each (the decode tile path once it is enabled)."""
+    from hyper_multicore_amd import ops
+    counts = _decode_counts(64, 5)
+    g = _seed(sum(counts))
+    G, Kd, N = len(counts), 1024, 768
+    rows = sum(counts)
+    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
+    wl = w if layout == "EIO" else w.transpose(1, 2).contiguous()
+    gl = torch.tensor(counts).cumsum(0).to(torch.int64)
+    out = ops.grouped_gemm_bf16(x.to(gpu), wl.to(gpu), gl.to(gpu), layout).cpu()
+    starts = [0, *gl.tolist()]
+    ref = torch.cat([x[starts[i]:starts[i + 1]].float() @ w[i].float() for i in range(G)]).to(torch.bfloat16)
+    assert orc.rel_l2(out, ref) < 2e-3
+
+
+def test_grouped_gemm_mxfp8_decode_shape(gpu):
+    from hyper_multicore_amd import ops
+    counts = _decode_counts(48, 6)
+    g = _seed(sum(counts) + 1)
+    G, Kd, N = len(counts), 1024, 512
+    rows = sum(counts)
+    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
+    xq, xs = ops.mx_quantize_rows(x.to(gpu))
+    d, s = ops.mx_quantize_cols(w.to(gpu))
+    gl = torch.tensor(counts).cumsum(0).to(torch.int64)
+    out = ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), s, gl.to(gpu)).cpu()
+    xd = orc.mx_dequantize(xq.cpu(), xs.cpu(), dim=-1)
+    wd = orc.mx_dequantize_weight_cols(d.cpu().view(torch.uint8), s.cpu())
+    starts = [0, *gl.tolist()]
+    ref = torch.cat([xd[starts[i]:starts[i + 1]] @ wd[i] for i in range(G)]).to(torch.bfloat16)
+    assert orc.rel_l2(out, ref) < 5e-3
+
+
+@pytest.mark.parametrize("precision", ["bf16", "mxfp8"])
+def test_moe_forward_decode_shape(gpu, precision):
+    """T=32 tokens, top-8 of 64 experts: 256 routed rows, about 4 per expert."""
+    from hyper_multicore_amd import ops
+    T, H, I, E, K = 32, 1024, 512, 64, 8
+    g = _seed(T * E + (precision == "mxfp8"))
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
+    if precision == "bf16":
+        out = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1.to(gpu), w2.to(gpu), num_experts=E,
+                              intermediate_size=I).cpu()
+        ref = orc.expert_forward_reference(x, ids, probs, w1, w2)
+        assert orc.rel_l2(out, ref) < BF16_REL_L2
+    else:
+        d1, s1 = ops.mx_quantize_cols(w1.to(gpu))
+        d2, s2 = ops.mx_quantize_cols(w2.to(gpu))
+        out = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8),
+                              num_experts=E, intermediate_size=I, precision="mxfp8", w1_scale=s1, w2_scale=s2).cpu()
+        ref = orc.expert_forward_reference(x, ids, probs, d1.cpu().view(torch.uint8), d2.cpu().view(torch.uint8),
+                                           precision="mxfp8", w1_scale=s1.cpu(), w2_scale=s2.cpu())
+        assert orc.rel_l2(out, ref) < MXFP8_REL_L2
