@@ -17,6 +17,9 @@ OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 IDS_INT32, IDS_INT64 = 0, 1
 PRECISION = {"bf16": 0, "mxfp8": 1}
+FEATURE_MX_EOI = 1
+FEATURE_NUMERICS = 2
+FEATURE_DECODE_TILES = 4
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}
@@ -64,6 +67,7 @@ class ForwardArgs(Structure):
 # (name, restype, argtypes)
 _SIGNATURES = [
     ("mi355moe_abi_version", c_int32, []),
+    ("mi355moe_features", c_int32, []),
     ("mi355moe_gate_logits_workspace_size", c_size_t, [c_int64, c_int32, c_int32]),
     ("mi355moe_gate_logits", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
                                        c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -12,12 +12,14 @@ Only the default numerics are implemented (no SwiGLU clamp, probabilities applie
 """
 from __future__ import annotations
 
+import math
+import struct
 from dataclasses import dataclass
 from typing import Any
 
 import torch
 
-from . import ops
+from . import _lib, ops
 
 __all__ = ["MegaMoeExperts", "MegaMoeNumericsOptions", "MegaMoeTuningOptions", "MegaMoeSchedulerOptions"]
 
@@ -58,6 +60,23 @@ class MegaMoeTuningOptions:
     scheduler: MegaMoeSchedulerOptions = MegaMoeSchedulerOptions()
 
 
+def _check_swiglu_limit(limit: Any) -> None:
+    """None, or a finite positive number whose float32 value is finite and positive (the kernel
+    takes it as float32; module.py:55-79 applies the same rule)."""
+    if limit is None:
+        return
+    ok = isinstance(limit, (int, float)) and not isinstance(limit, bool)
+    if ok:
+        try:
+            as_f32 = struct.unpack("<f", struct.pack("<f", float(limit)))[0]
+        except (OverflowError, ValueError):
+            as_f32 = float("inf")
+        ok = math.isfinite(float(limit)) and math.isfinite(as_f32) and as_f32 > 0.0
+    if not ok:
+        raise ValueError("swiglu_limit must be None or a finite positive float32-representable number, "
+                         f"got {limit!r}.")
+
+
 def _positive_int(name: str, value: Any) -> int:
     if not isinstance(value, int) or isinstance(value, bool) or value <= 0:
         raise ValueError(f"{name} must be a positive integer, got {value!r}.")
@@ -90,11 +109,13 @@ class MegaMoeExperts(torch.nn.Module):
                             ("clamp_after_silu", numerics.clamp_after_silu)):
             if not isinstance(value, bool):
                 raise TypeError(f"{name} must be a boolean")
+        _check_swiglu_limit(numerics.swiglu_limit)
         if precision == "mxfp8" and (numerics.swiglu_limit is not None or numerics.apply_probs_before_fc2):
             raise ValueError("MXFP8 does not support clamp or before-FC2 probability weighting")
-        if numerics.swiglu_limit is not None or numerics.apply_probs_before_fc2:
-            raise NotImplementedError("the gfx950 kernels implement the default numerics only "
-                                      "(no SwiGLU clamp, probabilities after FC2)")
+        if ((numerics.swiglu_limit is not None or numerics.apply_probs_before_fc2)
+                and not ops.features() & _lib.FEATURE_NUMERICS):
+            raise NotImplementedError("this build of the gfx950 library has the SwiGLU clamp and the "
+                                      "before-FC2 probabilities switched off")
         if numerics.partial_weight_grad_dtype not in (None, "native", "float32"):
             raise ValueError("partial_weight_grad_dtype must be native, float32 or None")
         if tuning.dispatch_mode not in ("push", "pull"):
@@ -184,7 +205,10 @@ class MegaMoeExperts(torch.nn.Module):
         return layout, w1.contiguous(), w2.contiguous()
 
     def _mx_weights(self, hidden: torch.Tensor, expert_weights: tuple):
-        from .mxfp8 import resolve_forward_weight
+        """(layout, w1 data, w1 scales, w2 data, w2 scales): the roots' EIO fields, or their
+        K-contiguous re-layout (prepared once per root and cached on it) when the library has that
+        GEMM path switched on."""
+        from .mxfp8 import prepared_eoi_weight, resolve_forward_weight
         try:
             r1, r2 = expert_weights
         except (TypeError, ValueError) as error:
@@ -192,7 +216,11 @@ class MegaMoeExperts(torch.nn.Module):
         E, H, I = self.num_experts, self.hidden_size, self.intermediate_size
         d1, s1 = resolve_forward_weight(r1, (E, H, 2 * I), hidden.device)
         d2, s2 = resolve_forward_weight(r2, (E, I, H), hidden.device)
-        return d1, s1, d2, s2
+        if ops.features() & _lib.FEATURE_MX_EOI:
+            e1, t1 = prepared_eoi_weight(r1, d1, s1)
+            e2, t2 = prepared_eoi_weight(r2, d2, s2)
+            return "EOI", e1, t1, e2, t2
+        return "EIO", d1, s1, d2, s2
 
     def forward(self, hidden_states: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, *,
                 expert_weights: tuple, tokens_per_expert: torch.Tensor | None = None) -> torch.Tensor:
@@ -221,12 +249,15 @@ class MegaMoeExperts(torch.nn.Module):
             tokens_per_expert = tokens_per_expert.to(torch.int32)
         if self._precision == "bf16":
             layout, w1, w2 = self._bf16_weights(flat, expert_weights)
+            nm = self._numerics
             out = ops.moe_forward(flat, topk_ids, topk_weights, w1, w2, num_experts=self.num_experts,
                                   intermediate_size=self.intermediate_size, precision="bf16", layout=layout,
-                                  tokens_per_expert=tokens_per_expert)
+                                  tokens_per_expert=tokens_per_expert, swiglu_limit=nm.swiglu_limit,
+                                  clamp_after_silu=nm.clamp_after_silu,
+                                  apply_probs_before_fc2=nm.apply_probs_before_fc2)
         else:
-            d1, s1, d2, s2 = self._mx_weights(flat, expert_weights)
+            layout, d1, s1, d2, s2 = self._mx_weights(flat, expert_weights)
             out = ops.moe_forward(flat, topk_ids, topk_weights, d1, d2, num_experts=self.num_experts,
-                                  intermediate_size=self.intermediate_size, precision="mxfp8", layout="EIO",
+                                  intermediate_size=self.intermediate_size, precision="mxfp8", layout=layout,
                                   w1_scale=s1, w2_scale=s2, tokens_per_expert=tokens_per_expert)
         return out.reshape(hidden_states.shape)

@@ -12,7 +12,7 @@ import torch
 
 from . import ops
 
-__all__ = ["quantize_expert_weight", "resolve_forward_weight"]
+__all__ = ["quantize_expert_weight", "resolve_forward_weight", "prepared_eoi_weight"]
 
 
 def quantize_expert_weight(weight: torch.Tensor) -> torch.Tensor:
@@ -50,3 +50,21 @@ def resolve_forward_weight(root, logical_shape: tuple[int, int, int], device: to
     if data.numel() != E * M * N or scale.numel() != E * (M // 64) * N * 2:
         raise ValueError(f"MX root does not hold an [E, M, N] = {logical_shape} weight")
     return data.view(torch.uint8).view(E, M, N), scale.view(E, M // 64, N, 2)
+
+
+def prepared_eoi_weight(root, data: torch.Tensor, scale: torch.Tensor):
+    """The K-contiguous re-layout of a root's (data, scale) for the GEMM (``ops.mx_weight_to_eoi``),
+    built on first use and cached on the root. The cache is keyed on the storage of the root's
+    fields, so a root whose ``col_data`` / ``col_scale`` are replaced is re-laid-out again; in-place
+    writes into the same storage are not detected (roots are treated as immutable weights)."""
+    key = (data.data_ptr(), scale.data_ptr(), tuple(data.shape), data.device)
+    cached = getattr(root, "_mi355_eoi", None)
+    if cached is not None and cached[0] == key:
+        return cached[1], cached[2]
+    d, s = ops.mx_weight_to_eoi(data, scale)
+    d = d.view(torch.uint8)
+    try:
+        root._mi355_eoi = (key, d, s)
+    except AttributeError:  # roots without attribute storage are re-laid-out per call
+        pass
+    return d, s

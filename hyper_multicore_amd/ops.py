@@ -275,6 +275,11 @@ def grouped_gemm_bf16(x: torch.Tensor, weights: torch.Tensor, group_list: torch.
     return out
 
 
+def features() -> int:
+    """Bit set of the optional paths the loaded library has switched on (``_lib.FEATURE_*``)."""
+    return int(_lib.load().mi355moe_features())
+
+
 def mx_weight_to_eoi(col_data: torch.Tensor, col_scale: torch.Tensor):
     """Re-layout an MX weight root (col_data [G, K, N], col_scale [G, K/64, N, 2]) with K contiguous:
     (data e4m3fn [G, N, K], scale uint8 [G, N, ld]), ld = K/32 padded to a multiple of 16. Values

@@ -46,6 +46,15 @@ enum { MI355MOE_LAYOUT_EIO = 0, MI355MOE_LAYOUT_EOI = 1 };
  */
 int mi355moe_abi_version(void);
 
+/* Optional paths this build has switched on (no reference counterpart): a bit set of
+ * MI355MOE_FEATURE_*. A path whose bit is clear answers MI355MOE_EUNSUPPORTED. */
+enum {
+  MI355MOE_FEATURE_MX_EOI = 1,        /* MXFP8 GEMMs on re-laid-out (K-contiguous) weights */
+  MI355MOE_FEATURE_NUMERICS = 2,      /* BF16 SwiGLU clamp / probabilities before FC2 */
+  MI355MOE_FEATURE_DECODE_TILES = 4,  /* 64-row tiles for groups averaging <= 32 rows */
+};
+int mi355moe_features(void);
+
 /* ---------------------------------------------------------------------------------------------
  * Router projection: logits[t, e] = sum_h x[t, h] * w[e, h], bf16 inputs, fp32 accumulate and
  * fp32 output (deterministic split-K: fixed K chunks summed in ascending order). H % 128 == 0. Replaces the fp32 projection F.linear(x.float(), W.float())

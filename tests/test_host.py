@@ -55,8 +55,16 @@ def test_megamoe_options_and_validation():
     with pytest.raises(ValueError):
         hm.MegaMoeExperts(**kw, precision="mxfp8",
                           numerics_options=hm.MegaMoeNumericsOptions(apply_probs_before_fc2=True))
-    with pytest.raises(NotImplementedError):
+    from hyper_multicore_amd import _lib, ops
+    if ops.features() & _lib.FEATURE_NUMERICS:
         hm.MegaMoeExperts(**kw, numerics_options=hm.MegaMoeNumericsOptions(swiglu_limit=7.0))
+    else:
+        with pytest.raises(NotImplementedError):
+            hm.MegaMoeExperts(**kw, numerics_options=hm.MegaMoeNumericsOptions(swiglu_limit=7.0))
+    # swiglu_limit: finite, positive, and still finite and positive as float32 (module.py:55-79)
+    for bad in (-1.0, 0.0, float("nan"), float("inf"), 1e39, 1e-50, True, "7"):
+        with pytest.raises(ValueError):
+            hm.MegaMoeExperts(**kw, numerics_options=hm.MegaMoeNumericsOptions(swiglu_limit=bad))
     with pytest.raises(TypeError):
         hm.MegaMoeExperts(**kw, numerics_options=dict(swiglu_limit=None))
     with pytest.raises(ValueError):
