@@ -7,8 +7,10 @@ tokens_per_expert=None)`` returns bf16 in the input shape. BF16 weights are acce
 on first use); MXFP8 weights are MX roots carrying ``col_data`` (e4m3fn, EIO) and ``col_scale``
 (uint8 e8m0 ``[E, M/64, N, 2]``), see :func:`hyper_multicore_amd.mxfp8.quantize_expert_weight`.
 
-Only the default numerics are implemented (no SwiGLU clamp, probabilities applied after FC2);
-``ep_group`` must be ``None`` or a group of size 1.
+The BF16 numerics options (``swiglu_limit``, ``clamp_after_silu``, ``apply_probs_before_fc2``) run
+when the loaded library reports them switched on (``ops.features()``), otherwise the constructor
+raises ``NotImplementedError``; MXFP8 rejects them as the reference does. ``ep_group`` must be
+``None`` or a group of size 1.
 """
 from __future__ import annotations
 
