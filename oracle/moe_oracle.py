@@ -321,6 +321,68 @@ def expert_forward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: tor
     return unpermute_tokens(y.to(torch.bfloat16), mapping, None if apply_probs_before_fc2 else probs, K)
 
 
+def expert_backward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, w1: torch.Tensor,
+                              w2: torch.Tensor, grad_out: torch.Tensor, *, layout: str = "EIO",
+                              num_experts: int | None = None):
+    """Backward of the bf16 expert forward (combine included) with the reference's rounding points.
+
+    Expert part (fp32_expert_reference.py:27-35): with the recomputed bf16 projection U = [g | u],
+    silu = silu(g) and act = bf16(silu * u) of the forward,
+        gA = bf16(dY @ W2^T), gG = bf16(gA * u * s * (1 + g * (1 - s))) with s = sigmoid(g),
+        gU = bf16(gA * silu), dU = [gG | gU], dW1_e = X_e^T dU_e, dW2_e = act_e^T dY_e (fp32),
+        dX_routed = bf16(dU @ W1^T).
+    Combine / permutation (restore_topk_output route.py:1029-1051 and moe_token_permute_grad;
+    build contract, the torch_npu ops are closed): dY_r = bf16(fp32(dOut[t]) * p[t, k]) for the
+    routed row r of slot (t, k); dp[t, k] = sum_h fp32(y_r[h]) * fp32(dOut[t, h]) with y the bf16
+    expert output; dX[t] = bf16(sum_k fp32(dX_routed[r])).
+
+    Returns (dX bf16 [T, H], dW1 fp32 in w1's layout, dW2 fp32 in w2's layout, dp fp32 [T, K]).
+    """
+    T, H = hidden.shape
+    K = ids.shape[1]
+    E = num_experts if num_experts is not None else w1.shape[0]
+    W1 = w1.float() if layout == "EIO" else w1.float().transpose(1, 2)  # [E, H, 2I]
+    W2 = w2.float() if layout == "EIO" else w2.float().transpose(1, 2)  # [E, I, H]
+    I = W1.shape[2] // 2
+    x = hidden.float()
+    dout = grad_out.float()
+    mapping, gather = stable_permutation(ids, E)
+    flat = ids.reshape(-1).long()
+    pflat = probs.reshape(-1).float()
+    dW1 = torch.zeros(E, H, 2 * I)
+    dW2 = torch.zeros(E, I, H)
+    dxr = torch.zeros(gather.numel(), H)
+    dp = torch.zeros(T * K)
+    start = 0
+    for e in range(E):
+        n = int((flat == e).sum())
+        if n == 0:
+            continue
+        slots = gather[start:start + n].long()
+        rows = slots // K
+        xe = x[rows]
+        u_all = _bf16(xe @ W1[e])
+        g, up = u_all[:, :I], u_all[:, I:]
+        silu = F.silu(g)
+        act = _bf16(silu * up)
+        y = _bf16(act @ W2[e])
+        dy = _bf16(dout[rows] * pflat[slots][:, None])
+        dp[slots] = (y * dout[rows]).sum(1)
+        ga = _bf16(dy @ W2[e].T)
+        sg = torch.sigmoid(g)
+        gg = _bf16(ga * up * sg * (1 + g * (1 - sg)))
+        gu = _bf16(ga * silu)
+        du = torch.cat([gg, gu], dim=1)
+        dW1[e] = xe.T @ du
+        dW2[e] = act.T @ dy
+        dxr[start:start + n] = _bf16(du @ W1[e].T)
+        start += n
+    dx = unpermute_tokens(dxr.to(torch.bfloat16), mapping, None, K)
+    if layout == "EOI":
+        dW1, dW2 = dW1.transpose(1, 2).contiguous(), dW2.transpose(1, 2).contiguous()
+    return dx, dW1, dW2, dp.reshape(T, K)
+
+
 def torch_experts_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, gate_w: torch.Tensor,
                             up_w: torch.Tensor, down_w: torch.Tensor) -> torch.Tensor:
     """The TorchExperts CPU loop (tests/common/multicore/moe_reference.py:170-181): weights are

@@ -391,3 +391,73 @@ def test_mxfp8_rejects_numerics_options():
     with pytest.raises(ValueError):
         orc.expert_forward_reference(x, ids, p, d1, d2, precision="mxfp8", w1_scale=s1, w2_scale=s2,
                                      swiglu_limit=7.0)
+
+
+# ---- backward restatement ----------------------------------------------------------------------
+def _autograd_backward(x, ids, p, w1, w2, dout):
+    """fp32 autograd of the same expert forward without the intermediate bf16 roundings."""
+    E, H, I2 = w1.shape
+    I = I2 // 2
+    xx = x.float().clone().requires_grad_(True)
+    W1 = w1.float().clone().requires_grad_(True)
+    W2 = w2.float().clone().requires_grad_(True)
+    pp = p.float().clone().requires_grad_(True)
+    out = torch.zeros(x.shape[0], H)
+    for t in range(x.shape[0]):
+        for k in range(ids.shape[1]):
+            e = int(ids[t, k])
+            u = xx[t] @ W1[e]
+            act = F.silu(u[:I]) * u[I:]
+            out = out.index_add(0, torch.tensor([t]), (pp[t, k] * (act @ W2[e]))[None])
+    (out * dout.float()).sum().backward()
+    return xx.grad, W1.grad, W2.grad, pp.grad
+
+
+def test_backward_reference_matches_fp32_autograd():
+    x, ids, p, w1, w2 = _inputs(T=24, H=32, I=16, E=4, K=2, seed=31)
+    dout = torch.randn(24, 32, generator=torch.Generator().manual_seed(32)).to(torch.bfloat16)
+    dx, dw1, dw2, dp = orc.expert_backward_reference(x, ids, p, w1, w2, dout)
+    ax, aw1, aw2, ap = _autograd_backward(x, ids, p, w1, w2, dout)
+    assert orc.rel_l2(dx.float(), ax) < 2e-2
+    assert orc.rel_l2(dw1, aw1) < 2e-2
+    assert orc.rel_l2(dw2, aw2) < 2e-2
+    assert orc.rel_l2(dp, ap) < 2e-2
+
+
+def test_backward_reference_single_expert_closed_form():
+    """E = 1, K = 1, p = 1: the expert part is exactly fp32_expert_reference.py:27-35's chain."""
+    g = torch.Generator().manual_seed(33)
+    T, H, I = 16, 32, 8
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(1, H, 2 * I, generator=g) * 0.1).to(torch.bfloat16)
+    w2 = (torch.randn(1, I, H, generator=g) * 0.1).to(torch.bfloat16)
+    dout = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.zeros(T, 1, dtype=torch.int64)
+    dx, dw1, dw2, dp = orc.expert_backward_reference(x, ids, torch.ones(T, 1), w1, w2, dout)
+    proj = (x.float() @ w1[0].float()).bfloat16().float()
+    gate, up = proj[:, :I], proj[:, I:]
+    act = (F.silu(gate) * up).bfloat16().float()
+    y = (act @ w2[0].float()).bfloat16().float()
+    ga = (dout.float() @ w2[0].float().T).bfloat16().float()
+    s = gate.sigmoid()
+    gg = (ga * up * s * (1 + gate * (1 - s))).bfloat16().float()
+    gu = (ga * F.silu(gate)).bfloat16().float()
+    du = torch.cat([gg, gu], 1)
+    assert torch.equal(dw1[0], x.float().T @ du)
+    assert torch.equal(dw2[0], act.T @ dout.float())
+    assert torch.equal(dx, (du @ w1[0].float().T).bfloat16())
+    assert torch.allclose(dp[:, 0], (y * dout.float()).sum(1), rtol=1e-6, atol=1e-6)
+
+
+def test_backward_reference_layouts_and_scaling():
+    x, ids, p, w1, w2 = _inputs(T=20, H=32, I=16, E=3, K=2, seed=34)
+    dout = torch.randn(20, 32, generator=torch.Generator().manual_seed(35)).to(torch.bfloat16)
+    a = orc.expert_backward_reference(x, ids, p, w1, w2, dout)
+    b = orc.expert_backward_reference(x, ids, p, w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous(),
+                                      dout, layout="EOI")
+    assert torch.equal(a[0], b[0]) and torch.equal(a[3], b[3])
+    assert torch.equal(a[1], b[1].transpose(1, 2)) and torch.equal(a[2], b[2].transpose(1, 2))
+    # every gradient is linear in the upstream gradient; scaling by 2 is exact through the bf16 roundings
+    c = orc.expert_backward_reference(x, ids, p, w1, w2, (dout.float() * 2).to(torch.bfloat16))
+    for u, v in zip(a, c):
+        assert torch.equal(v.float(), 2 * u.float())
