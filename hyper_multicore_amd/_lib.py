@@ -20,6 +20,7 @@ PRECISION = {"bf16": 0, "mxfp8": 1}
 FEATURE_MX_EOI = 1
 FEATURE_NUMERICS = 2
 FEATURE_DECODE_TILES = 4
+FEATURE_BACKWARD = 8
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}
@@ -64,6 +65,17 @@ class ForwardArgs(Structure):
     ]
 
 
+class BackwardArgs(Structure):
+    """MI355MoeBackwardArgs in include/mi355moe.h."""
+    _fields_ = [
+        ("hidden", c_void_p), ("num_tokens", c_int64), ("hidden_size", c_int32), ("intermediate_size", c_int32),
+        ("num_experts", c_int32), ("top_k", c_int32), ("topk_ids", c_void_p), ("ids_dtype", c_int32),
+        ("weight_layout", c_int32), ("topk_weights", c_void_p), ("w1", c_void_p), ("w2", c_void_p),
+        ("grad_out", c_void_p), ("grad_hidden", c_void_p), ("grad_w1", c_void_p), ("grad_w2", c_void_p),
+        ("grad_topk_weights", c_void_p), ("weight_grad_dtype", c_int32), ("reserved", c_int32),
+    ]
+
+
 # (name, restype, argtypes)
 _SIGNATURES = [
     ("mi355moe_abi_version", c_int32, []),
@@ -91,6 +103,8 @@ _SIGNATURES = [
                                               c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("mi355moe_moe_forward_workspace_size", c_size_t, [POINTER(ForwardArgs)]),
     ("mi355moe_moe_forward", c_int32, [POINTER(ForwardArgs), c_void_p, c_size_t, c_void_p]),
+    ("mi355moe_moe_backward_workspace_size", c_size_t, [POINTER(BackwardArgs)]),
+    ("mi355moe_moe_backward", c_int32, [POINTER(BackwardArgs), c_void_p, c_size_t, c_void_p]),
 ]
 EXPORTED = [name for name, _, _ in _SIGNATURES]
 

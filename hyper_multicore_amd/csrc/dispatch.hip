@@ -187,6 +187,14 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t* x, in
   for (int v = threadIdx.x; v < H / 8; v += blockDim.x) dst[v] = src[v];
 }
 
+int mi355_permute_rows_enqueue(const uint16_t* x, int64_t slots, int K, int H, const int32_t* mapping,
+                                uint16_t* routed, hipStream_t st) {
+  if (slots == 0) return MI355MOE_OK;
+  hipLaunchKernelGGL(permute_rows_kernel, dim3((unsigned)slots), dim3(H >= 2048 ? 256 : 64), 0, st, x, slots, K, H,
+                     mapping, routed);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
 extern "C" int mi355moe_token_permute(const uint16_t* x, int64_t num_tokens, int32_t hidden_size,
                                       const void* topk_ids, int32_t ids_dtype, int32_t top_k,
                                       int32_t num_experts, uint16_t* routed, int32_t* mapping,

@@ -34,10 +34,19 @@ struct GGParams {
   const float* row_prob;     // EPI_SWIGLU_BF16: probability of slot a_row_index[r] multiplies row r
   int32_t k_splits;          // EPI_STORE_F32 only: >1 splits K; split s writes C + s * c_split_stride
   int64_t c_split_stride;    // elements
+  // Grouped-K mode (weight gradients): C_g[m, n] = sum over the routed rows r of group g of
+  // A[r, m] * B[r, n]; A [rows, m_rows] (row stride lda_bytes) and B [rows, N] (b_row_bytes) are
+  // both read K-major, group_list gives the row ranges, C_g = C + g * c_group_stride (elements).
+  int32_t m_rows;
+  int32_t m_tiles;
+  int64_t c_group_stride;
+  const uint8_t* zero_row;   // >= 2 * max(m_rows, N) zero bytes (rows past a group's end)
 };
 
 
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, bool small = false);
+// Grouped-K bf16 GEMM (weight gradients), EPI_STORE_F32 or EPI_STORE_BF16.
+int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t stream);
 int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream, bool small = false);
 int mi355_gg_bm(bool small = false);
 // MX GEMM with K-contiguous (EOI) weights: switched off until its GPU parity tests have run
@@ -49,6 +58,8 @@ inline bool mi355_numerics_options_enabled() { return false; }
 // The 64-row tile configuration (two workgroups per CU) for grouped GEMMs whose groups average at
 // most 32 rows (decode): switched off until its GPU parity tests have run.
 inline bool mi355_small_tiles_enabled() { return false; }
+// Expert backward (bf16): switched off until its GPU parity tests have run.
+inline bool mi355_backward_enabled() { return false; }
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {
   return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;
 }
@@ -56,6 +67,8 @@ int mi355_gg_bn();
 int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
                            int64_t* expert_offsets, int64_t* group_list, int32_t* mapping, int32_t* gather_index,
                            int32_t* error_flag, void* workspace, hipStream_t stream);
+int mi355_permute_rows_enqueue(const uint16_t* x, int64_t slots, int K, int H, const int32_t* mapping,
+                                uint16_t* routed, hipStream_t st);
 int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const float* probs, int64_t T, int K, int H,
                             uint16_t* out, hipStream_t stream);
 int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,

@@ -170,31 +170,62 @@ struct CopyPlan {
   const uint8_t* bsr;      // MX EOI: B scale row (tile column wave*64 + lane)
   int64_t b_stage_stride;  // bytes to advance B per stage
   int64_t bs_stage_stride; // bytes to advance the B scales per stage
+  // grouped-K mode: a[j] / b[j] point at the copy's column of row 0, rows are K
+  const uint8_t* zero;     // zero row read by copies past the group's last row
+  int64_t lda_k, ldb_k;    // row strides (bytes)
+  int a_k[C::A_INSTR], b_k[C::B_INSTR];      // K row of each copy within a stage
+  int a_col[C::A_INSTR], b_col[C::B_INSTR];  // byte column of each copy
+  int k0, k_end;           // routed-row range of the group
 };
 
-template <class C, bool MX>
+// Source of copy j at stage kt.
+template <class C, bool GK>
+MI355_DEV const uint8_t* a_src(const CopyPlan<C>& cp, int j, int kt) {
+  if constexpr (!GK) {
+    return cp.a[j] + (int64_t)kt * C::KB;
+  } else {
+    const int r = cp.k0 + kt * 32 + cp.a_k[j];
+    return r < cp.k_end ? cp.a[j] + (int64_t)r * cp.lda_k : cp.zero + cp.a_col[j];
+  }
+}
+template <class C, bool GK>
+MI355_DEV const uint8_t* b_src(const CopyPlan<C>& cp, int j, int kt) {
+  if constexpr (!GK) {
+    return cp.b[j] + (int64_t)kt * cp.b_stage_stride;
+  } else {
+    const int r = cp.k0 + kt * 32 + cp.b_k[j];
+    return r < cp.k_end ? cp.b[j] + (int64_t)r * cp.ldb_k : cp.zero + cp.b_col[j];
+  }
+}
+
+template <class C, bool MX, bool GK>
 MI355_DEV void issue_a(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
   const uint32_t base = (kt % C::A_SLOTS) * C::A_BYTES;
-  const int64_t koff = (int64_t)kt * C::KB;
 #pragma unroll
   for (int j = 0; j < C::A_INSTR; ++j)
-    lds_dma<16>(cp.a[j] + koff, base + (wave * C::A_INSTR + j) * 1024, smem);
+    lds_dma<16>(a_src<C, GK>(cp, j, kt), base + (wave * C::A_INSTR + j) * 1024, smem);
 }
 MI355_DEV bool is_bs_wave(int wave) { return wave < 2; }
-template <class C, bool MX, bool B_KN>
+template <class C, bool MX, bool B_KN, bool GK>
 MI355_DEV void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
   // (MX with K-contiguous weights has no per-stage scale copy: its scales come in groups)
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
   const uint32_t base = C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT;
-  const int64_t boff = (int64_t)kt * cp.b_stage_stride;
+  if constexpr (!GK) {
+    const int64_t boff = (int64_t)kt * cp.b_stage_stride;
 #pragma unroll
-  for (int j = 0; j < C::B_INSTR; ++j)
-    lds_dma<16>(cp.b[j] + boff, base + (wave * C::B_INSTR + j) * 1024, smem);
+    for (int j = 0; j < C::B_INSTR; ++j)
+      lds_dma<16>(cp.b[j] + boff, base + (wave * C::B_INSTR + j) * 1024, smem);
+  } else {
+#pragma unroll
+    for (int j = 0; j < C::B_INSTR; ++j)
+      lds_dma<16>(b_src<C, GK>(cp, j, kt), base + (wave * C::B_INSTR + j) * 1024, smem);
+  }
   if (MX && B_KN && is_bs_wave(wave))
     lds_dma<4>(cp.bs + kt * cp.bs_stage_stride, base + C::B_BYTES + wave * 256, smem);
 }
@@ -221,9 +252,12 @@ extern "C" int mi355_gg_trace_read(void* host) {
 // Operand fragments of one stage for one wave (WM rows x WN columns x one stage of K). Values
 // that are read in several LDS instructions are kept as the raw pieces and joined only when the
 // MFMA consumes them, so that issuing the reads never forces a wait for their data.
-template <class C, bool MX, bool B_KN> struct Frags;
+template <class C, bool MX, bool B_KN, bool A_KN = false> struct Frags;
 template <class C> struct Frags<C, false, false> { v8bf a[2][C::MI], b[2][C::NI]; };  // [ks][mi], [ks][ni]
 template <class C> struct Frags<C, false, true> { v8bf a[2][C::MI]; v4s bl[2][C::NI], bh[2][C::NI]; };
+template <class C> struct Frags<C, false, true, true> {  // grouped-K: A K-major like B
+  v4s al[2][C::MI], ah[2][C::MI], bl[2][C::NI], bh[2][C::NI];
+};
 template <class C> struct Frags<C, true, true> {
   v4i al[C::MI], ah[C::MI];
   v2i bp[C::NI][4];
@@ -233,6 +267,18 @@ template <class C> struct Frags<C, true, false> {
   v4i al[C::MI], ah[C::MI], bl[C::NI], bh[C::NI];
   int sa[C::MI], sb[C::NI];
 };
+
+// bf16 fragment of 32 rows / columns x 16 K (ks) from a K-major LDS tile (512-byte K rows of 256
+// bf16, chunks swizzled with (k & 7) << 1), read with two transposing loads.
+MI355_DEV void read_kn16(const uint8_t* S, int base, int ks, int lane, v4s& lo, v4s& hi) {
+  const int g16 = lane >> 4, m = lane & 15;
+  const int nb = base + (g16 & 1) * 16 + 4 * (m & 3);
+  const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
+  const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
+  const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
+  lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, S + off0));
+  hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, S + off1));
+}
 
 // Element-wise fragment reads and MFMAs and the copies of one iteration, so that one pipelined
 // step can interleave them: MFMA t, then its share of the LDS reads of the next stage
@@ -244,8 +290,8 @@ template <class C, bool MX, int NM> struct StepShape {
   static constexpr int ITEMS = C::B_INSTR + 1 + C::A_INSTR;          // B copies, B scales, A copies
 };
 
-template <class C, bool MX, bool B_KN, int NM>
-MI355_DEV void read_elem(Frags<C, MX, B_KN>& f, int e, const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs,
+template <class C, bool MX, bool B_KN, int NM, bool A_KN = false>
+MI355_DEV void read_elem(Frags<C, MX, B_KN, A_KN>& f, int e, const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs,
                          const uint8_t* BSRs, int wm, int wn, int lane) {
   constexpr int NI = C::NI;
   if constexpr (!MX) {
@@ -264,7 +310,8 @@ MI355_DEV void read_elem(Frags<C, MX, B_KN>& f, int e, const uint8_t* As, const 
         f.bh[ks][q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
       }
     } else {
-      f.a[ks][q - NI] = read_a_bf16(As, wm * C::WM + (q - NI) * 32 + (lane & 31), ks, lane);
+      if constexpr (A_KN) read_kn16(As, wm * C::WM + (q - NI) * 32, ks, lane, f.al[ks][q - NI], f.ah[ks][q - NI]);
+      else f.a[ks][q - NI] = read_a_bf16(As, wm * C::WM + (q - NI) * 32 + (lane & 31), ks, lane);
     }
   } else {
     if (e < NI) {
@@ -296,15 +343,18 @@ MI355_DEV void read_elem(Frags<C, MX, B_KN>& f, int e, const uint8_t* As, const 
   }
 }
 
-template <class C, bool MX, bool B_KN, int NM>
-MI355_DEV void mfma_elem(const Frags<C, MX, B_KN>& f, v16f (&acc)[C::MI][C::NI], int t) {
+template <class C, bool MX, bool B_KN, int NM, bool A_KN = false>
+MI355_DEV void mfma_elem(const Frags<C, MX, B_KN, A_KN>& f, v16f (&acc)[C::MI][C::NI], int t) {
   constexpr int NI = C::NI;
   if constexpr (!MX) {
     const int ks = t / (NM * NI), mi = (t / NI) % NM, ni = t % NI;
     v8bf b;
     if constexpr (!B_KN) b = f.b[ks][ni];
     else b = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.bl[ks][ni], f.bh[ks][ni], 0, 1, 2, 3, 4, 5, 6, 7));
-    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[ks][mi], b, acc[mi][ni], 0, 0, 0);
+    v8bf a;
+    if constexpr (A_KN) a = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.al[ks][mi], f.ah[ks][mi], 0, 1, 2, 3, 4, 5, 6, 7));
+    else a = f.a[ks][mi];
+    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[mi][ni], 0, 0, 0);
   } else {
     const int mi = t / NI, ni = t % NI;
     const v8i a = __builtin_shufflevector(f.al[mi], f.ah[mi], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -321,7 +371,7 @@ MI355_DEV void mfma_elem(const Frags<C, MX, B_KN>& f, v16f (&acc)[C::MI][C::NI],
 }
 
 // Copy item it of iteration i (same order as issue_iteration: B copies, B scales, A copies).
-template <class C, bool MX, bool B_KN, bool LA>
+template <class C, bool MX, bool B_KN, bool LA, bool GK = false>
 MI355_DEV void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem, int it) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
@@ -329,7 +379,7 @@ MI355_DEV void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_
   constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
   if (it < C::B_INSTR) {
     const int kt = i + DB;
-    lds_dma<16>(cp.b[it] + (int64_t)kt * cp.b_stage_stride,
+    lds_dma<16>(b_src<C, GK>(cp, it, kt),
                 C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + (wave * C::B_INSTR + it) * 1024, smem, kt < nk);
   } else if (it == C::B_INSTR) {
     const int kt = i + DB;
@@ -339,7 +389,7 @@ MI355_DEV void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_
   } else if constexpr (LA) {
     const int j = it - C::B_INSTR - 1;
     const int kt = i + DA;
-    lds_dma<16>(cp.a[j] + (int64_t)kt * C::KB, (kt % C::A_SLOTS) * C::A_BYTES + (wave * C::A_INSTR + j) * 1024, smem,
+    lds_dma<16>(a_src<C, GK>(cp, j, kt), (kt % C::A_SLOTS) * C::A_BYTES + (wave * C::A_INSTR + j) * 1024, smem,
                 kt < nk);
   }
 }
@@ -382,13 +432,13 @@ MI355_DEV int younger_than(int j, int last, int nk, int la_n, int lb_n) {
   return n;
 }
 
-template <class C, bool MX, bool B_KN, bool LA>
+template <class C, bool MX, bool B_KN, bool LA, bool GK = false>
 MI355_DEV void issue_iteration(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
   constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
-  if (i + DB < nk) issue_b<C, MX, B_KN>(cp, i + DB, wave, smem);
+  if (i + DB < nk) issue_b<C, MX, B_KN, GK>(cp, i + DB, wave, smem);
   if (LA && i + DA >= 0 && i + DA < nk) {
     if (MX && i + DA == 0) issue_as<C>(cp, 0, wave, smem);
-    issue_a<C, MX>(cp, i + DA, wave, smem);
+    issue_a<C, MX, GK>(cp, i + DA, wave, smem);
   }
   if (LA && MX && i >= 0 && (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk)
     issue_as<C>(cp, i / C::AS_GROUP + 1, wave, smem);
@@ -402,15 +452,16 @@ MI355_DEV void issue_iteration(const CopyPlan<C>& cp, int i, int nk, int wave, u
 // A-scale group g+1 (stages 8g+8 ..) is issued at iteration 8g into the slot of group g-1, whose
 // last stage was read during iteration 8g-2.
 // NM = number of 32-row subtiles this wave computes (0, 1, 2 or 4).
-template <class C, bool MX, bool B_KN, int NM, bool LA>
+template <class C, bool MX, bool B_KN, int NM, bool LA, bool GK = false>
 MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
                       v16f (&acc)[C::MI][C::NI]) {
+  // grouped-K mode: A is read K-major like B (and the caller skips groups without rows)
   constexpr int DB = C::B_SLOTS;
   const int la_n = C::A_INSTR;
   const int lb_n = C::B_INSTR + ((MX && B_KN && is_bs_wave(wave)) ? 1 : 0);  // loads per B stage
   if constexpr (MX && !B_KN) lds_dma<16>(cp.bsr, C::BSR_OFF + (wave & 3) * 1024, smem);  // B scale group 0
-  for (int i = -DB; i < 0; ++i) issue_iteration<C, MX, B_KN, LA>(cp, i, nk, wave, smem);
-  Frags<C, MX, B_KN> f0, f1;
+  for (int i = -DB; i < 0; ++i) issue_iteration<C, MX, B_KN, LA, GK>(cp, i, nk, wave, smem);
+  Frags<C, MX, B_KN, GK> f0, f1;
   wait_vm(younger_than<C, LA>(0, -1, nk, la_n, lb_n));
   lds_barrier();
   using SS = StepShape<C, MX, NM>;
@@ -418,10 +469,10 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
     const uint8_t* ASs = smem + C::AS_OFF;
 #pragma unroll
     for (int e = 0; e < SS::READS; ++e)
-      read_elem<C, MX, B_KN, NM>(f0, e, smem, smem + C::B_OFF, ASs, smem + C::BSR_OFF, wm, wn, lane);
+      read_elem<C, MX, B_KN, NM, GK>(f0, e, smem, smem + C::B_OFF, ASs, smem + C::BSR_OFF, wm, wn, lane);
   }
   // one pipelined iteration with a next stage (k + 1 < nk)
-  auto step = [&](int k, Frags<C, MX, B_KN>& cur, Frags<C, MX, B_KN>& nxt) {
+  auto step = [&](int k, Frags<C, MX, B_KN, GK>& cur, Frags<C, MX, B_KN, GK>& nxt) {
     __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs of the previous stage above the barrier
     GG_T(0)
     wait_vm(younger_than<C, LA>(k + 1, k - 1, nk, la_n, lb_n));
@@ -441,15 +492,15 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
     for (int t = 0; t < T; ++t) {
 #ifndef GG_ABLATE_COMPUTE
       if constexpr (NM > 0) {
-        mfma_elem<C, MX, B_KN, NM>(cur, acc, t);
+        mfma_elem<C, MX, B_KN, NM, GK>(cur, acc, t);
 #pragma unroll
         for (int e = t * SS::READS / T; e < (t + 1) * SS::READS / T; ++e)
-          read_elem<C, MX, B_KN, NM>(nxt, e, As, Bs, ASs, BSRs, wm, wn, ln);
+          read_elem<C, MX, B_KN, NM, GK>(nxt, e, As, Bs, ASs, BSRs, wm, wn, ln);
       }
 #endif
 #pragma unroll
       for (int it = t * SS::ITEMS / T; it < (t + 1) * SS::ITEMS / T; ++it)
-        issue_item<C, MX, B_KN, LA>(cp, k, nk, wave, smem, it);
+        issue_item<C, MX, B_KN, LA, GK>(cp, k, nk, wave, smem, it);
       if (t == T / 2 - 1) { GG_T(3) }
       __builtin_amdgcn_sched_barrier(0);  // keep this interleave order
     }
@@ -474,7 +525,7 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
 #ifndef GG_ABLATE_COMPUTE
   if constexpr (NM > 0) {
 #pragma unroll
-    for (int t = 0; t < SS::MFMAS; ++t) mfma_elem<C, MX, B_KN, NM>(f0, acc, t);
+    for (int t = 0; t < SS::MFMAS; ++t) mfma_elem<C, MX, B_KN, NM, GK>(f0, acc, t);
   }
 #endif
 }
@@ -753,6 +804,128 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
   }
 }
 
+// Grouped-K GEMM (weight gradients): C_g[m, n] = sum over the rows r of group g (group_list) of
+// A[r, m] * B[r, n], bf16 in, fp32 accumulate, C_g = C + g * c_group_stride (fp32 or bf16 store).
+// Both operands are read K-major (rows = K) into the same LDS layout as an EIO weight tile and
+// read with transposing loads; rows past a group's end come from a zero row, so groups of any
+// size (including none: C_g = 0) are exact. Work items are (group, m-tile, n-tile), m fastest.
+template <class C, int EPI>
+__global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_wgrad_kernel(GGParams p) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (int)((unsigned)wave / C::WGN), wn = (int)((unsigned)wave % C::WGN);
+  const int per_g = p.m_tiles * p.n_tiles;
+  const int total = p.G * per_g;
+  const int xcd = blockIdx.x & 7;
+  const int per_xcd = gridDim.x >> 3;
+  const int slot = blockIdx.x >> 3;
+  for (int round = 0;; ++round) {
+    const int L = round * (int)gridDim.x + xcd * per_xcd + slot;
+    if (L >= total) break;
+    const int g = L / per_g, local = L - g * per_g;
+    const int nt = local / p.m_tiles, mt = local - nt * p.m_tiles;
+    const int k0 = g == 0 ? 0 : (int)p.group_list[g - 1];
+    const int kend = (int)p.group_list[g];
+    const int nk = (kend - k0 + 31) / 32;  // 32 K rows per stage
+    const int m0 = mt * C::BM;
+    const int rows_valid = min(C::BM, p.m_rows - m0);
+
+    CopyPlan<C> cp;
+    cp.zero = p.zero_row;
+    cp.lda_k = p.lda_bytes;
+    cp.ldb_k = p.b_row_bytes;
+    cp.k0 = k0;
+    cp.k_end = kend;
+#pragma unroll
+    for (int j = 0; j < C::A_INSTR; ++j) {
+      const int L16 = (wave * C::A_INSTR + j) * 64 + lane;
+      const int k = L16 >> 5, cs = L16 & 31;
+      const int c = cs ^ ((k & 7) << 1);
+      int col = m0 + c * 8;
+      if (col > p.m_rows - 8) col = p.m_rows - 8;
+      cp.a[j] = p.A + (int64_t)col * 2;
+      cp.a_k[j] = k;
+      cp.a_col[j] = col * 2;
+    }
+#pragma unroll
+    for (int j = 0; j < C::B_INSTR; ++j) {
+      const int L16 = (wave * C::B_INSTR + j) * 64 + lane;
+      const int k = L16 >> 5, cs = L16 & 31;
+      const int c = cs ^ ((k & 7) << 1);
+      int col = nt * C::BN + c * 8;
+      if (col > p.N - 8) col = p.N - 8;
+      cp.b[j] = p.B + (int64_t)col * 2;
+      cp.b_k[j] = k;
+      cp.b_col[j] = col * 2;
+    }
+    cp.b_stage_stride = 0;
+    cp.s = cp.bs = cp.bsr = nullptr;
+    cp.bs_stage_stride = 0;
+
+    v16f acc[C::MI][C::NI];
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NI; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    __syncthreads();  // the previous item's epilogue reads are done before refilling
+    if (nk > 0) {
+      const int rows_w = rows_valid - wm * C::WM;
+      const int nm = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
+      if (C::MI >= 4 && nm == 4) k_loop<C, false, true, (C::MI >= 4 ? 4 : 1), true, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 2) k_loop<C, false, true, 2, true, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else if (nm == 1) k_loop<C, false, true, 1, true, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+      else k_loop<C, false, true, 0, true, true>(cp, nk, wave, wm, wn, lane, smem, acc);
+    }
+    __syncthreads();  // all waves are done reading the ring before the epilogue reuses LDS
+
+    // acc[mi][ni][r] holds row (m) wm*WM + mi*32 + 8*(r/4) + 4*(lane/32) + r%4 and column (n)
+    // wn*WN + ni*32 + lane%32 of the tile
+    if constexpr (EPI == EPI_STORE_F32) {
+      float* outp = (float*)p.C + (int64_t)g * p.c_group_stride;
+#pragma unroll
+      for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < C::NI; ++ni) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int col = nt * C::BN + wn * C::WN + ni * 32 + (lane & 31);
+            if (row < rows_valid && col < p.N) outp[(int64_t)(m0 + row) * p.ldc + col] = acc[mi][ni][r];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+      constexpr int RS = C::EPI_RS_BF16;
+#pragma unroll
+      for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < C::NI; ++ni) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int col = wn * C::WN + ni * 32 + (lane & 31);
+            *(uint16_t*)(smem + row * RS + col * 2) = f32_to_bf16(acc[mi][ni][r]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      __syncthreads();
+      uint16_t* outp = (uint16_t*)p.C + (int64_t)g * p.c_group_stride;
+      for (int id = tid; id < C::BM * (C::BN / 8); id += C::THREADS) {
+        const int row = id >> 5, ch = id & 31;
+        const int col = nt * C::BN + ch * 8;
+        if (row < rows_valid && col < p.N)
+          *(uint4*)(outp + (int64_t)(m0 + row) * p.ldc + col) = *(const uint4*)(smem + row * RS + ch * 16);
+      }
+      __syncthreads();
+    }
+  }
+}
+
 // tile_prefix[g] = sum_{g' < g} ceil(rows_g' / BM) from an inclusive group_list.
 __global__ __launch_bounds__(1024) void plan_tiles_kernel(const int64_t* group_list, int G, int bm,
                                                           int32_t* tile_prefix) {
@@ -828,6 +1001,32 @@ static int dispatch_gg(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   switch (epi) {
     case EPI_STORE_BF16: return launch_gg<C, true, true, EPI_STORE_BF16>(p, stream);
     case EPI_SWIGLU_MX: return launch_gg<C, true, true, EPI_SWIGLU_MX>(p, stream);
+    default: return MI355MOE_EUNSUPPORTED;
+  }
+}
+
+template <class C, int EPI>
+static int launch_wgrad(const GGParams& p, hipStream_t stream) {
+  static bool configured = false;
+  auto kern = grouped_gemm_wgrad_kernel<C, EPI>;
+  if (!configured) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::TOTAL) != hipSuccess)
+      return MI355MOE_ELAUNCH;
+    configured = true;
+  }
+  int grid = (num_cus() / 8) * 8 * C::WG_PER_CU;
+  if (grid < 8) grid = 8;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(C::THREADS), C::TOTAL, stream, p);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t stream) {
+  if (p.m_rows % 8 || p.N % 8 || p.m_tiles != (p.m_rows + GGBig::BM - 1) / GGBig::BM ||
+      p.n_tiles != (p.N + GGBig::BN - 1) / GGBig::BN || p.zero_row == nullptr)
+    return MI355MOE_EINVAL;
+  switch (epi) {
+    case EPI_STORE_F32: return launch_wgrad<GGBig, EPI_STORE_F32>(p, stream);
+    case EPI_STORE_BF16: return launch_wgrad<GGBig, EPI_STORE_BF16>(p, stream);
     default: return MI355MOE_EUNSUPPORTED;
   }
 }

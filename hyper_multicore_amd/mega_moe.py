@@ -7,7 +7,10 @@ tokens_per_expert=None)`` returns bf16 in the input shape. BF16 weights are acce
 on first use); MXFP8 weights are MX roots carrying ``col_data`` (e4m3fn, EIO) and ``col_scale``
 (uint8 e8m0 ``[E, M/64, N, 2]``), see :func:`hyper_multicore_amd.mxfp8.quantize_expert_weight`.
 
-The BF16 numerics options (``swiglu_limit``, ``clamp_after_silu``, ``apply_probs_before_fc2``) run
+Gradients: with the library's backward switched on (``ops.features()``), a bf16 forward under
+autograd with default numerics records a function whose backward computes the gradients of the
+hidden states, both expert weights and the routing weights on the GPU; otherwise the output carries
+no autograd history. The BF16 numerics options (``swiglu_limit``, ``clamp_after_silu``, ``apply_probs_before_fc2``) run
 when the loaded library reports them switched on (``ops.features()``), otherwise the constructor
 raises ``NotImplementedError``; MXFP8 rejects them as the reference does. ``ep_group`` must be
 ``None`` or a group of size 1.
@@ -83,6 +86,29 @@ def _positive_int(name: str, value: Any) -> int:
     if not isinstance(value, int) or isinstance(value, bool) or value <= 0:
         raise ValueError(f"{name} must be a positive integer, got {value!r}.")
     return value
+
+
+class _MoeFunction(torch.autograd.Function):
+    """bf16 expert forward with the library's backward (autograd.py:672-760 role); the forward
+    intermediates are recomputed in the backward, so only the inputs are saved."""
+
+    @staticmethod
+    def forward(ctx, hidden, topk_weights, w1, w2, topk_ids, num_experts, intermediate_size, layout,
+                weight_grad_dtype):
+        ctx.save_for_backward(hidden, topk_weights, w1, w2, topk_ids)
+        ctx.meta = (num_experts, intermediate_size, layout, weight_grad_dtype)
+        return ops.moe_forward(hidden, topk_ids, topk_weights, w1, w2, num_experts=num_experts,
+                               intermediate_size=intermediate_size, precision="bf16", layout=layout)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        hidden, topk_weights, w1, w2, topk_ids = ctx.saved_tensors
+        num_experts, inter, layout, grad_dtype = ctx.meta
+        gx, g1, g2, gp = ops.moe_backward(hidden, topk_ids, topk_weights, w1, w2, grad_out, num_experts=num_experts,
+                                          intermediate_size=inter, layout=layout, weight_grad_dtype=grad_dtype,
+                                          need_topk_grad=ctx.needs_input_grad[1])
+        gp = gp.to(topk_weights.dtype) if gp is not None else None
+        return gx, gp, g1, g2, None, None, None, None, None
 
 
 class MegaMoeExperts(torch.nn.Module):
@@ -252,11 +278,19 @@ class MegaMoeExperts(torch.nn.Module):
         if self._precision == "bf16":
             layout, w1, w2 = self._bf16_weights(flat, expert_weights)
             nm = self._numerics
-            out = ops.moe_forward(flat, topk_ids, topk_weights, w1, w2, num_experts=self.num_experts,
-                                  intermediate_size=self.intermediate_size, precision="bf16", layout=layout,
-                                  tokens_per_expert=tokens_per_expert, swiglu_limit=nm.swiglu_limit,
-                                  clamp_after_silu=nm.clamp_after_silu,
-                                  apply_probs_before_fc2=nm.apply_probs_before_fc2)
+            default_numerics = nm.swiglu_limit is None and not nm.apply_probs_before_fc2
+            wants_grad = torch.is_grad_enabled() and any(
+                t.requires_grad for t in (flat, topk_weights, w1, w2))
+            if wants_grad and default_numerics and ops.features() & _lib.FEATURE_BACKWARD:
+                grad_dtype = torch.float32 if nm.partial_weight_grad_dtype == "float32" else torch.bfloat16
+                out = _MoeFunction.apply(flat, topk_weights, w1, w2, topk_ids, self.num_experts,
+                                         self.intermediate_size, layout, grad_dtype)
+            else:
+                out = ops.moe_forward(flat, topk_ids, topk_weights, w1, w2, num_experts=self.num_experts,
+                                      intermediate_size=self.intermediate_size, precision="bf16", layout=layout,
+                                      tokens_per_expert=tokens_per_expert, swiglu_limit=nm.swiglu_limit,
+                                      clamp_after_silu=nm.clamp_after_silu,
+                                      apply_probs_before_fc2=nm.apply_probs_before_fc2)
         else:
             layout, d1, s1, d2, s2 = self._mx_weights(flat, expert_weights)
             out = ops.moe_forward(flat, topk_ids, topk_weights, d1, d2, num_experts=self.num_experts,

@@ -380,3 +380,45 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
     rc = lib.mi355moe_moe_forward(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(device))
     _lib.check(rc, "mi355moe_moe_forward")
     return out
+
+
+def moe_backward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w1: torch.Tensor,
+                 w2: torch.Tensor, grad_out: torch.Tensor, *, num_experts: int, intermediate_size: int,
+                 layout: str = "EIO", weight_grad_dtype: torch.dtype = torch.bfloat16,
+                 need_topk_grad: bool = True):
+    """Gradients of :func:`moe_forward` (bf16, default numerics) through ``mi355moe_moe_backward``:
+    returns (grad_hidden bf16 [T, H], grad_w1, grad_w2 in the weights' layout and
+    ``weight_grad_dtype``, grad_topk_weights fp32 [T, K] or None)."""
+    lib = _lib.load()
+    device = _require_gpu(hidden, topk_ids, topk_weights, w1, w2, grad_out)
+    if hidden.dtype != torch.bfloat16 or hidden.ndim != 2 or grad_out.shape != hidden.shape:
+        raise TypeError("hidden and grad_out must be bf16 [T, H]")
+    if w1.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
+        raise TypeError("expert weights must be bf16")
+    if weight_grad_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("weight_grad_dtype must be bfloat16 or float32")
+    T, H = hidden.shape
+    K = topk_ids.shape[1]
+    hidden = hidden.contiguous()
+    ids = topk_ids.contiguous()
+    probs = topk_weights.to(torch.float32).contiguous()
+    dout = grad_out.to(torch.bfloat16).contiguous()
+    w1 = w1.contiguous()
+    w2 = w2.contiguous()
+    grad_hidden = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    grad_w1 = torch.empty(w1.shape, dtype=weight_grad_dtype, device=device)
+    grad_w2 = torch.empty(w2.shape, dtype=weight_grad_dtype, device=device)
+    grad_p = torch.empty((T, K), dtype=torch.float32, device=device) if need_topk_grad else None
+    args = _lib.BackwardArgs(
+        hidden=_ptr(hidden), num_tokens=T, hidden_size=H, intermediate_size=intermediate_size,
+        num_experts=num_experts, top_k=K, topk_ids=_ptr(ids), ids_dtype=_ids_dtype(ids),
+        weight_layout=_lib.LAYOUT[layout], topk_weights=_ptr(probs), w1=_ptr(w1), w2=_ptr(w2),
+        grad_out=_ptr(dout), grad_hidden=_ptr(grad_hidden), grad_w1=_ptr(grad_w1), grad_w2=_ptr(grad_w2),
+        grad_topk_weights=_ptr(grad_p), weight_grad_dtype=1 if weight_grad_dtype == torch.float32 else 0)
+    need = lib.mi355moe_moe_backward_workspace_size(ctypes.byref(args))
+    if need == 0 and T > 0:
+        _lib.check(lib.mi355moe_moe_backward(ctypes.byref(args), None, 0, _stream(device)), "mi355moe_moe_backward")
+    ws = _workspace(need, device)
+    rc = lib.mi355moe_moe_backward(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(rc, "mi355moe_moe_backward")
+    return grad_hidden, grad_w1, grad_w2, grad_p

@@ -52,6 +52,7 @@ enum {
   MI355MOE_FEATURE_MX_EOI = 1,        /* MXFP8 GEMMs on re-laid-out (K-contiguous) weights */
   MI355MOE_FEATURE_NUMERICS = 2,      /* BF16 SwiGLU clamp / probabilities before FC2 */
   MI355MOE_FEATURE_DECODE_TILES = 4,  /* 64-row tiles for groups averaging <= 32 rows */
+  MI355MOE_FEATURE_BACKWARD = 8,      /* mi355moe_moe_backward */
 };
 int mi355moe_features(void);
 
@@ -260,6 +261,45 @@ typedef struct MI355MoeForwardArgs {
 size_t mi355moe_moe_forward_workspace_size(const MI355MoeForwardArgs* args);
 int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* workspace, size_t workspace_size,
                          void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * MegaMoE expert backward at EP=1, BF16 (the gradients of mi355moe_moe_forward with the default
+ * numerics). Replaces MegaMoeFunction.backward (modules/mega_moe/backends/bf16/autograd.py:672-760,
+ * the hyper_multicore::mega_moe_grad launch) together with the backward of the combine
+ * (restore_topk_output, route.py:1029-1051) and of the permutation (moe_token_permute_grad).
+ * The forward intermediates are recomputed. Rounding points follow the reference's fp32 expert
+ * reference (tests/common/multicore/fp32_expert_reference.py:27-35):
+ *   dY[r] = bf16(p[t,k] * dOut[t]), dp[t,k] = sum_h y[r,h] * dOut[t,h] (fp32),
+ *   gA = bf16(dY W2^T), dU = [bf16(gA u s (1 + g (1 - s))) | bf16(gA silu(g))], s = sigmoid(g),
+ *   dW2_e = act_e^T dY_e, dW1_e = X_e^T dU_e (fp32 accumulate, stored in weight_grad_dtype),
+ *   dX[t] = bf16(sum_k bf16(dU W1^T)[r]).
+ * Gradients have the weights' layout. grad_topk_weights may be NULL.
+ */
+enum { MI355MOE_GRAD_BF16 = 0, MI355MOE_GRAD_FP32 = 1 };
+typedef struct MI355MoeBackwardArgs {
+  const uint16_t* hidden;     /* [T, H] bf16 */
+  int64_t num_tokens;
+  int32_t hidden_size;
+  int32_t intermediate_size;
+  int32_t num_experts;
+  int32_t top_k;
+  const void* topk_ids;       /* [T, K] */
+  int32_t ids_dtype;
+  int32_t weight_layout;      /* MI355MOE_LAYOUT_* */
+  const float* topk_weights;  /* [T, K] fp32 */
+  const uint16_t* w1;         /* bf16 EIO [E, H, 2I] or EOI [E, 2I, H] */
+  const uint16_t* w2;         /* bf16 EIO [E, I, H] or EOI [E, H, I] */
+  const uint16_t* grad_out;   /* [T, H] bf16 */
+  uint16_t* grad_hidden;      /* [T, H] bf16 */
+  void* grad_w1;              /* like w1, weight_grad_dtype */
+  void* grad_w2;              /* like w2, weight_grad_dtype */
+  float* grad_topk_weights;   /* optional [T, K] fp32 */
+  int32_t weight_grad_dtype;  /* MI355MOE_GRAD_* (partial_weight_grad_dtype native / float32) */
+  int32_t reserved;
+} MI355MoeBackwardArgs;
+size_t mi355moe_moe_backward_workspace_size(const MI355MoeBackwardArgs* args);
+int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* workspace, size_t workspace_size,
+                          void* stream);
 
 #ifdef __cplusplus
 }

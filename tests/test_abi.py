@@ -71,6 +71,22 @@ def test_numerics_options_validation():
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
 
 
+def test_backward_validation():
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    base = dict(num_tokens=16, hidden_size=1024, intermediate_size=512, num_experts=8, top_k=2, ids_dtype=0,
+                weight_layout=0)
+    f = _lib.BackwardArgs(**base, weight_grad_dtype=2)
+    assert lib.mi355moe_moe_backward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+    f = _lib.BackwardArgs(**{**base, "weight_layout": 3})
+    assert lib.mi355moe_moe_backward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
+    f = _lib.BackwardArgs(**{**base, "hidden_size": 1000})
+    assert lib.mi355moe_moe_backward(ctypes.byref(f), None, 0, None) == _lib.EUNSUPPORTED
+    f = _lib.BackwardArgs(**base)  # valid shape, operands missing (or the path switched off)
+    assert lib.mi355moe_moe_backward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
+    assert lib.mi355moe_moe_backward_workspace_size(ctypes.byref(f)) == 0 or lib.mi355moe_features() & 8
+
+
 def test_workspace_sizes():
     from hyper_multicore_amd import _lib
     lib = _lib.load()
