@@ -2,7 +2,9 @@
 #pragma once
 #include "common.h"
 
-enum { EPI_STORE_BF16 = 0, EPI_STORE_F32 = 1, EPI_SWIGLU_BF16 = 2, EPI_SWIGLU_MX = 3 };
+// EPI_SWIGLU_BF16_NUM is EPI_SWIGLU_BF16 with the numerics options (clamp, probabilities before FC2);
+// callers ask for EPI_SWIGLU_BF16 and the dispatcher picks it when one of the options is set.
+enum { EPI_STORE_BF16 = 0, EPI_STORE_F32 = 1, EPI_SWIGLU_BF16 = 2, EPI_SWIGLU_MX = 3, EPI_SWIGLU_BF16_NUM = 4 };
 
 struct GGParams {
   const uint8_t* A;          // [rowsA, K] elements (bf16 or e4m3), row stride lda_bytes

@@ -538,7 +538,7 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = (int)((unsigned)wave / C::WGN), wn = (int)((unsigned)wave % C::WGN);
-  constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX);
+  constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX || EPI == EPI_SWIGLU_BF16_NUM);
   constexpr int ESIZE = MX ? 1 : 2;
 
   const bool prefix_in_lds = p.G <= C::PREFIX_MAX;
@@ -731,7 +731,7 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
             float gte = bf16_to_f32(f32_to_bf16(acc[mi][ni][r]));
             float up = bf16_to_f32(f32_to_bf16(acc[mi][ni + C::NI / 2][r]));
             float act;
-            if (EPI == EPI_SWIGLU_BF16 && p.swiglu_limit > 0.0f) {
+            if (EPI == EPI_SWIGLU_BF16_NUM && p.swiglu_limit > 0.0f) {
               // MegaMoeNumericsOptions clamp: up to [-L, L]; gate to <= L before SiLU, or SiLU(gate)
               // to <= L after it
               const float L = p.swiglu_limit;
@@ -749,27 +749,34 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
           __builtin_amdgcn_sched_barrier(0);
         }
       __syncthreads();
-      if (EPI == EPI_SWIGLU_BF16) {
+      if (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_BF16_NUM) {
         uint16_t* outp = (uint16_t*)p.C;
         for (int id = tid; id < C::BM * 16; id += C::THREADS) {
           int row = id >> 4, ch = id & 15;
           if (row < rows_valid) {
             const float* s = (const float*)(smem + row * RS + ch * 32);
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = s[i];
-            if (p.row_prob != nullptr) {
-              // probabilities before FC2: bf16(fp32(bf16(act)) * p) (two roundings, the reference
-              // contract); row r of the tile is slot a_row_index[r]
-              const float pr = p.row_prob[p.a_row_index[tile_row0 + row]];
-#pragma unroll
-              for (int i = 0; i < 8; ++i) v[i] = bf16_to_f32(f32_to_bf16(v[i])) * pr;
-            }
             uint4 o;
-            o.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-            o.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-            o.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
-            o.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+            if (EPI == EPI_SWIGLU_BF16_NUM) {
+              float v[8];
+#pragma unroll
+              for (int i = 0; i < 8; ++i) v[i] = s[i];
+              if (p.row_prob != nullptr) {
+                // probabilities before FC2: bf16(fp32(bf16(act)) * p) (two roundings, the reference
+                // contract); row r of the tile is slot a_row_index[r]
+                const float pr = p.row_prob[p.a_row_index[tile_row0 + row]];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = bf16_to_f32(f32_to_bf16(v[i])) * pr;
+              }
+              o.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+              o.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+              o.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+              o.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+            } else {
+              o.x = f32_to_bf16(s[0]) | ((uint32_t)f32_to_bf16(s[1]) << 16);
+              o.y = f32_to_bf16(s[2]) | ((uint32_t)f32_to_bf16(s[3]) << 16);
+              o.z = f32_to_bf16(s[4]) | ((uint32_t)f32_to_bf16(s[5]) << 16);
+              o.w = f32_to_bf16(s[6]) | ((uint32_t)f32_to_bf16(s[7]) << 16);
+            }
             *(uint4*)(outp + (tile_row0 + row) * p.ldc + nt * (C::BN / 2) + ch * 8) = o;
           }
         }
@@ -981,12 +988,14 @@ static int dispatch_gg(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
         case EPI_STORE_BF16: return launch_gg<C, false, false, EPI_STORE_BF16>(p, stream);
         case EPI_STORE_F32: return launch_gg<C, false, false, EPI_STORE_F32>(p, stream);
         case EPI_SWIGLU_BF16: return launch_gg<C, false, false, EPI_SWIGLU_BF16>(p, stream);
+        case EPI_SWIGLU_BF16_NUM: return launch_gg<C, false, false, EPI_SWIGLU_BF16_NUM>(p, stream);
         default: return MI355MOE_EUNSUPPORTED;
       }
     } else {
       switch (epi) {
         case EPI_STORE_BF16: return launch_gg<C, false, true, EPI_STORE_BF16>(p, stream);
         case EPI_SWIGLU_BF16: return launch_gg<C, false, true, EPI_SWIGLU_BF16>(p, stream);
+        case EPI_SWIGLU_BF16_NUM: return launch_gg<C, false, true, EPI_SWIGLU_BF16_NUM>(p, stream);
         default: return MI355MOE_EUNSUPPORTED;
       }
     }
@@ -1034,6 +1043,8 @@ int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t stream) {
 // Internal dispatcher used by the C-ABI entry points. `small` selects the 64-row tile
 // configuration (the tile prefix must have been planned with the same one).
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, bool small) {
+  if (epi == EPI_SWIGLU_BF16_NUM) return MI355MOE_EINVAL;  // internal: chosen from the options below
+  if (epi == EPI_SWIGLU_BF16 && (p.swiglu_limit > 0.0f || p.row_prob != nullptr)) epi = EPI_SWIGLU_BF16_NUM;
   if (small) {
     // the EPI_STORE_F32 router projection keeps the big tiles
     if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
