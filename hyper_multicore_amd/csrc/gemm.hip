@@ -37,58 +37,8 @@
 #include "scan.h"
 #include "../../include/mi355moe.h"
 #include "gemm.h"
+#include "gemm_plan.h"
 
-// Tile configurations (compile time). Both use 4 waves, tiles of BN = 256 weight columns and
-// 64-byte K stages (32 bf16 or 64 e4m3 per row):
-//   GGBig   - BM = 256, one workgroup per CU, waves in a 2 x 2 grid of 128 x 128 wave tiles (one
-//             wave per SIMD owning all 512 registers); prefill shapes.
-//   GGSmall - BM = 64, two workgroups per CU (the weight stream of one CU then runs through two
-//             independent pipelines), waves in a 1 x 4 grid of 64 x 64 wave tiles; decode shapes
-//             where experts see a few rows each.
-template <int BM_, int WGM_, int A_SLOTS_, int B_SLOTS_, int PREFIX_MAX_, int WG_PER_CU_>
-struct GGCfg {
-  static constexpr int BM = BM_;
-  static constexpr int BN = 256;
-  static constexpr int KB = 64;                        // bytes of K per stage per row
-  static constexpr int WAVES = 4;
-  static constexpr int THREADS = 64 * WAVES;
-  static constexpr int WG_PER_CU = WG_PER_CU_;
-  static constexpr int WGM = WGM_, WGN = WAVES / WGM_; // wave grid
-  static constexpr int WM = BM / WGM, WN = BN / WGN;   // wave tile
-  static constexpr int MI = WM / 32, NI = WN / 32;     // 32 x 32 MFMA subtiles per wave
-  // Decoupled rings: activations A (re-read from L2 by the tiles of one expert) and weights B
-  // (streamed once from HBM, so it gets the deeper ring).
-  static constexpr int A_BYTES = BM * KB;
-  static constexpr int B_BYTES = BN * KB;              // 16 KB
-  static constexpr int BS_BYTES = BN * 2;              // 512 B (MX EIO: two codes per column)
-  static constexpr int B_SLOT = B_BYTES + BS_BYTES;
-  static constexpr int A_SLOTS = A_SLOTS_;             // A(k + A_SLOTS) issued at iteration k
-  static constexpr int B_SLOTS = B_SLOTS_;             // B(k + B_SLOTS) issued at iteration k
-  static constexpr int AS_GROUP = 8;                   // MX: scale codes fetched per 8 stages
-  static constexpr int AS_SLOT = BM * 16;              // 16 codes per row
-  static constexpr int B_OFF = A_SLOTS * A_BYTES;
-  static constexpr int AS_OFF = B_OFF + B_SLOTS * B_SLOT;
-  static constexpr int PREFIX_MAX = PREFIX_MAX_;       // groups whose tile prefix is kept in LDS
-  static constexpr int BSR_SLOT = BN * 16;             // MX EOI weights: 16 scale codes per column
-  static constexpr int BSR_OFF = AS_OFF + 2 * AS_SLOT;
-  static constexpr int PREFIX_OFF = BSR_OFF + 2 * BSR_SLOT;
-  static constexpr int TOTAL = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
-  // DMA instructions per wave per stage (64 lanes x 16 bytes each)
-  static constexpr int A_INSTR = BM * (KB / 16) / 64 / WAVES;
-  static constexpr int B_INSTR = BN * (KB / 16) / 64 / WAVES;
-  static constexpr int AS_WAVES = BM / 64;             // waves that fetch A scale rows (64 each)
-  // epilogue staging (overlays the rings and the scale slots, never the tile prefix)
-  static constexpr int EPI_RS_BF16 = BN * 2 + 16;      // bf16 row stride
-  static constexpr int EPI_RS_ACT = (BN / 2) * 4 + 16; // SwiGLU fp32 row stride
-  static_assert(A_SLOTS >= 3 && A_SLOTS <= B_SLOTS, "ring depths");
-  static_assert(BM * EPI_RS_BF16 <= PREFIX_OFF, "bf16 epilogue staging must fit");
-  static_assert(BM * EPI_RS_ACT <= PREFIX_OFF, "SwiGLU epilogue staging must fit");
-  static_assert(TOTAL * WG_PER_CU <= 160 * 1024, "LDS budget");
-  static_assert(AS_WAVES >= 1 && AS_WAVES <= WAVES && WAVES * 64 == BN, "scale copies: 64 rows / columns a wave");
-  static_assert(A_INSTR >= 1 && NI % 2 == 0 && MI >= 1, "tile shape");
-};
-using GGBig = GGCfg<256, 2, 3, 5, 1024, 1>;
-using GGSmall = GGCfg<64, 1, 3, 3, 256, 2>;
 
 // Direct global -> LDS copy: lane i of the wave writes its SZ bytes at LDS address M0 + SZ*i
 // (SZ = 16) or M0 + 4*i (SZ = 4). Written as inline assembly on purpose: for the compiler's
@@ -113,6 +63,13 @@ MI355_DEV void lds_dma(const void* g, uint32_t lds_off_uniform, uint8_t* smem, i
                  "global_load_lds_dword %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc");
   else static_assert(SZ == 16, "unsupported DMA size");
 }
+// The copy policy of the kernels (see gemm_plan.h).
+struct DevDma {
+  template <int SZ>
+  MI355_DEV static void copy(const void* g, uint32_t lds_off_uniform, uint8_t* smem, int enable) {
+    lds_dma<SZ>(g, lds_off_uniform, smem, enable);
+  }
+};
 // Workgroup barrier without the release fence of __syncthreads (which would wait for every
 // outstanding global load, including the prefetched stages): LDS reads of this wave are drained,
 // the direct-to-LDS loads are ordered by the explicit vmcnt waits.
@@ -136,108 +93,12 @@ MI355_DEV void wait_vm(int n) {
   }
 }
 
-// Tile column j (0..BN-1) -> weight column. SwiGLU: the columns of each wave tile (WN wide) are
-// WN/2 gate columns followed by the matching WN/2 up columns, so a lane holds gate and up of the
-// same output element.
-template <class C>
-MI355_DEV int tile_col_to_weight_col(int j, int nt, int I, bool swiglu) {
-  if (!swiglu) return nt * C::BN + j;
-  constexpr int H = C::WN / 2;
-  static_assert(C::WN == 128 || C::WN == 64, "wave tile width");
-  int q = j >> (C::WN == 128 ? 7 : 6), jj = j & (C::WN - 1);
-  int base = nt * (C::BN / 2) + q * H;
-  return jj < H ? base + jj : I + base + (jj - H);
-}
-
-MI355_DEV int a_chunk_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 
 // ---- fragment loads (one K step: 16 bf16 or 64 e4m3) ------------------------------------------
 MI355_DEV v8bf read_a_bf16(const uint8_t* As, int r, int ks, int lane) {
   return *(const v8bf*)(As + a_chunk_off(r, ks * 2 + (lane >> 5)));
 }
 
-// ---- copy plan -------------------------------------------------------------------------------
-// Per stage each wave issues A_INSTR + B_INSTR 16-byte DMA instructions; MX adds the B scale codes
-// (EIO weights: waves 0 and 1, one 4-byte DMA for 128 columns each, per stage) and, every 8
-// stages, 16 scale codes per A row (AS_WAVES waves, 64 rows each) and, for EOI weights, per B
-// column (every wave, 64 columns each).
-template <class C>
-struct CopyPlan {
-  const uint8_t* a[C::A_INSTR];
-  const uint8_t* b[C::B_INSTR];
-  const uint8_t* s;        // MX: A scale row (waves < AS_WAVES)
-  const uint8_t* bs;       // MX EIO: B scale column pair (waves 0 and 1)
-  const uint8_t* bsr;      // MX EOI: B scale row (tile column wave*64 + lane)
-  int64_t b_stage_stride;  // bytes to advance B per stage
-  int64_t bs_stage_stride; // bytes to advance the B scales per stage
-  // grouped-K mode: a[j] / b[j] point at the copy's column of row 0, rows are K
-  const uint8_t* zero;     // zero row read by copies past the group's last row
-  int64_t lda_k, ldb_k;    // row strides (bytes)
-  int a_k[C::A_INSTR], b_k[C::B_INSTR];      // K row of each copy within a stage
-  int a_col[C::A_INSTR], b_col[C::B_INSTR];  // byte column of each copy
-  int k0, k_end;           // routed-row range of the group
-};
-
-// Source of copy j at stage kt.
-template <class C, bool GK>
-MI355_DEV const uint8_t* a_src(const CopyPlan<C>& cp, int j, int kt) {
-  if constexpr (!GK) {
-    return cp.a[j] + (int64_t)kt * C::KB;
-  } else {
-    const int r = cp.k0 + kt * 32 + cp.a_k[j];
-    return r < cp.k_end ? cp.a[j] + (int64_t)r * cp.lda_k : cp.zero + cp.a_col[j];
-  }
-}
-template <class C, bool GK>
-MI355_DEV const uint8_t* b_src(const CopyPlan<C>& cp, int j, int kt) {
-  if constexpr (!GK) {
-    return cp.b[j] + (int64_t)kt * cp.b_stage_stride;
-  } else {
-    const int r = cp.k0 + kt * 32 + cp.b_k[j];
-    return r < cp.k_end ? cp.b[j] + (int64_t)r * cp.ldb_k : cp.zero + cp.b_col[j];
-  }
-}
-
-template <class C, bool MX, bool GK>
-MI355_DEV void issue_a(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
-  const uint32_t base = (kt % C::A_SLOTS) * C::A_BYTES;
-#pragma unroll
-  for (int j = 0; j < C::A_INSTR; ++j)
-    lds_dma<16>(a_src<C, GK>(cp, j, kt), base + (wave * C::A_INSTR + j) * 1024, smem);
-}
-MI355_DEV bool is_bs_wave(int wave) { return wave < 2; }
-template <class C, bool MX, bool B_KN, bool GK>
-MI355_DEV void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
-  // (MX with K-contiguous weights has no per-stage scale copy: its scales come in groups)
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
-  const uint32_t base = C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT;
-  if constexpr (!GK) {
-    const int64_t boff = (int64_t)kt * cp.b_stage_stride;
-#pragma unroll
-    for (int j = 0; j < C::B_INSTR; ++j)
-      lds_dma<16>(cp.b[j] + boff, base + (wave * C::B_INSTR + j) * 1024, smem);
-  } else {
-#pragma unroll
-    for (int j = 0; j < C::B_INSTR; ++j)
-      lds_dma<16>(b_src<C, GK>(cp, j, kt), base + (wave * C::B_INSTR + j) * 1024, smem);
-  }
-  if (MX && B_KN && is_bs_wave(wave))
-    lds_dma<4>(cp.bs + kt * cp.bs_stage_stride, base + C::B_BYTES + wave * 256, smem);
-}
-// MX: A scale codes of stages 8*grp .. 8*grp+7 (16 bytes per row) into AS slot grp & 1.
-template <class C>
-MI355_DEV void issue_as(const CopyPlan<C>& cp, int grp, int wave, uint8_t* smem) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
-  if (wave < C::AS_WAVES)
-    lds_dma<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + wave * 1024, smem);
-}
 
 #ifdef GG_TRACE
 __device__ unsigned long long gg_trace[4 * 8 * 64 * 5];
@@ -284,11 +145,6 @@ MI355_DEV void read_kn16(const uint8_t* S, int base, int ks, int lane, v4s& lo, 
 // step can interleave them: MFMA t, then its share of the LDS reads of the next stage
 // and of the DMA copies. The wave never stalls on the DMA queue or on the LDS return queue for
 // long while the matrix core has work.
-template <class C, bool MX, int NM> struct StepShape {
-  static constexpr int MFMAS = MX ? NM * C::NI : 2 * NM * C::NI;
-  static constexpr int READS = MX ? C::NI + NM : 2 * (C::NI + NM);  // fragment elements of a stage
-  static constexpr int ITEMS = C::B_INSTR + 1 + C::A_INSTR;          // B copies, B scales, A copies
-};
 
 template <class C, bool MX, bool B_KN, int NM, bool A_KN = false>
 MI355_DEV void read_elem(Frags<C, MX, B_KN, A_KN>& f, int e, const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs,
@@ -370,80 +226,6 @@ MI355_DEV void mfma_elem(const Frags<C, MX, B_KN, A_KN>& f, v16f (&acc)[C::MI][C
   }
 }
 
-// Copy item it of iteration i (same order as issue_iteration: B copies, B scales, A copies).
-template <class C, bool MX, bool B_KN, bool LA, bool GK = false>
-MI355_DEV void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem, int it) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
-  constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
-  if (it < C::B_INSTR) {
-    const int kt = i + DB;
-    lds_dma<16>(b_src<C, GK>(cp, it, kt),
-                C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + (wave * C::B_INSTR + it) * 1024, smem, kt < nk);
-  } else if (it == C::B_INSTR) {
-    const int kt = i + DB;
-    if constexpr (MX && B_KN)
-      lds_dma<4>(cp.bs + kt * cp.bs_stage_stride, C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + C::B_BYTES + (wave & 1) * 256,
-                 smem, is_bs_wave(wave) && kt < nk);
-  } else if constexpr (LA) {
-    const int j = it - C::B_INSTR - 1;
-    const int kt = i + DA;
-    lds_dma<16>(a_src<C, GK>(cp, j, kt), (kt % C::A_SLOTS) * C::A_BYTES + (wave * C::A_INSTR + j) * 1024, smem,
-                kt < nk);
-  }
-}
-
-// MX: the scale groups due at iteration i (every AS_GROUP stages: A rows and, for K-contiguous
-// weights, B rows), each as one conditional copy.
-template <class C, bool MX, bool B_KN, bool LA>
-MI355_DEV void issue_scales_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
-  if constexpr (MX) {
-    const int grp = i / C::AS_GROUP + 1;
-    const bool due = (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk;
-    if constexpr (LA)
-      lds_dma<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 3) * 1024, smem,
-                  due && wave < C::AS_WAVES);
-    if constexpr (!B_KN)
-      lds_dma<16>(cp.bsr + grp * 16, C::BSR_OFF + (grp & 1) * C::BSR_SLOT + (wave & 3) * 1024, smem, due);
-  }
-}
-
-// Loads of stage j still allowed in flight (younger than stage j's last load) once iterations
-// up to `last` have issued. Iteration i issues B(i + DB), then A(i + DA) (DB = B_SLOTS >= DA =
-// A_SLOTS; the prologue runs iterations -DB .. -1), each only below nk. Stage j's last load is A(j)
-// (iteration j - DA; B(j) came earlier) for a wave that copies A, else B(j) (iteration j - DB).
-// Scale groups issued between are not counted, which only makes the wait stricter. Loads of one
-// wave retire in order.
-template <class C, bool LA>
-MI355_DEV int younger_than(int j, int last, int nk, int la_n, int lb_n) {
-  constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
-  const int from = (LA ? j - DA : j - DB) + 1;
-  // iterations i in [from, last] with i + DB < nk, and (A) with 0 <= i + DA < nk
-  const int nb = min(last, nk - DB - 1) - from + 1;
-  int n = (nb > 0 ? nb : 0) * lb_n;
-  if (LA) {
-    const int na = min(last, nk - DA - 1) - max(from, -DA) + 1;
-    n += (na > 0 ? na : 0) * la_n;
-  }
-  return n;
-}
-
-template <class C, bool MX, bool B_KN, bool LA, bool GK = false>
-MI355_DEV void issue_iteration(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
-  constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
-  if (i + DB < nk) issue_b<C, MX, B_KN, GK>(cp, i + DB, wave, smem);
-  if (LA && i + DA >= 0 && i + DA < nk) {
-    if (MX && i + DA == 0) issue_as<C>(cp, 0, wave, smem);
-    issue_a<C, MX, GK>(cp, i + DA, wave, smem);
-  }
-  if (LA && MX && i >= 0 && (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk)
-    issue_as<C>(cp, i / C::AS_GROUP + 1, wave, smem);
-}
-
 // K loop, software-pipelined in each wave: iteration k (after barrier k) refills the ring slots of
 // stage k, reads the fragments of stage k+1 into one register set and runs the MFMAs of stage k
 // from the other, so LDS reads and DMA issue overlap the matrix cores. Before barrier k every wave
@@ -456,11 +238,8 @@ template <class C, bool MX, bool B_KN, int NM, bool LA, bool GK = false>
 MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
                       v16f (&acc)[C::MI][C::NI]) {
   // grouped-K mode: A is read K-major like B (and the caller skips groups without rows)
-  constexpr int DB = C::B_SLOTS;
-  const int la_n = C::A_INSTR;
-  const int lb_n = C::B_INSTR + ((MX && B_KN && is_bs_wave(wave)) ? 1 : 0);  // loads per B stage
-  if constexpr (MX && !B_KN) lds_dma<16>(cp.bsr, C::BSR_OFF + (wave & 3) * 1024, smem);  // B scale group 0
-  for (int i = -DB; i < 0; ++i) issue_iteration<C, MX, B_KN, LA, GK>(cp, i, nk, wave, smem);
+  using D = DevDma;
+#include "gemm_kloop_prologue.inc"
   Frags<C, MX, B_KN, GK> f0, f1;
   wait_vm(younger_than<C, LA>(0, -1, nk, la_n, lb_n));
   lds_barrier();
@@ -500,11 +279,11 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
 #endif
 #pragma unroll
       for (int it = t * SS::ITEMS / T; it < (t + 1) * SS::ITEMS / T; ++it)
-        issue_item<C, MX, B_KN, LA, GK>(cp, k, nk, wave, smem, it);
+        issue_item<C, MX, B_KN, LA, GK, DevDma>(cp, k, nk, wave, smem, it);
       if (t == T / 2 - 1) { GG_T(3) }
       __builtin_amdgcn_sched_barrier(0);  // keep this interleave order
     }
-    issue_scales_item<C, MX, B_KN, LA>(cp, k, nk, wave, smem);
+    issue_scales_item<C, MX, B_KN, LA, DevDma>(cp, k, nk, wave, smem);
     GG_T(4)
   };
   // Stages 0 .. nk-2 are pipelined steps (each reads the next stage), taken in pairs so that the
@@ -556,95 +335,8 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
   for (int round = 0;; ++round) {
     const int L = round * (int)gridDim.x + xcd * per_xcd + slot;
     if (L >= total) break;
-    // ---- decode work item -------------------------------------------------------------
-    const int split = splits > 1 ? L % splits : 0;
-    const int LT = splits > 1 ? L / splits : L;
-    int lo = 0, hi = p.G - 1;
-    while (lo < hi) {  // largest g with prefix[g]*n_tiles <= LT
-      int mid = (lo + hi + 1) >> 1;
-      if (prefix[mid] * p.n_tiles <= LT) lo = mid; else hi = mid - 1;
-    }
-    const int g = lo;
-    const int mtiles = prefix[g + 1] - prefix[g];
-    const int local = LT - prefix[g] * p.n_tiles;
-    const int nt = local / mtiles;
-    const int mt = local - nt * mtiles;
-    const int64_t row_begin = (g == 0 ? 0 : p.group_list[g - 1]);
-    const int64_t row_end = p.group_list[g];
-    const int64_t tile_row0 = row_begin + (int64_t)mt * C::BM;
-    const int rows_valid = (int)((row_end - tile_row0) < C::BM ? (row_end - tile_row0) : C::BM);
-
-    // ---- per-thread copy sources ------------------------------------------------------
-    CopyPlan<C> cp;
-#pragma unroll
-    for (int j = 0; j < C::A_INSTR; ++j) {
-      int L16 = (wave * C::A_INSTR + j) * 64 + lane;
-      int r = L16 >> 2, cs = L16 & 3;
-      int c = cs ^ ((r >> 2) & 3);
-      int rr = r < rows_valid ? r : rows_valid - 1;
-      int64_t routed = tile_row0 + rr;
-      int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
-      cp.a[j] = p.A + src * p.lda_bytes + c * 16;
-    }
-    const uint8_t* bgrp = p.B + (int64_t)g * p.b_group_stride;
-#pragma unroll
-    for (int j = 0; j < C::B_INSTR; ++j) {
-      int L16 = (wave * C::B_INSTR + j) * 64 + lane;
-      if (!B_KN) {
-        int r = L16 >> 2, cs = L16 & 3;
-        int c = cs ^ ((r >> 2) & 3);
-        int wc = tile_col_to_weight_col<C>(r, nt, p.N, SWIGLU);
-        if (wc >= p.Ntot) wc = p.Ntot - 1;
-        cp.b[j] = bgrp + (int64_t)wc * p.b_row_bytes + c * 16;
-      } else if (MX) {
-        int k = L16 >> 4, cs = L16 & 15;
-        int c = cs ^ (k & 15);
-        int wc = tile_col_to_weight_col<C>(c * 16, nt, p.N, SWIGLU);
-        if (wc >= p.Ntot) wc = p.Ntot - 16;
-        cp.b[j] = bgrp + (int64_t)k * p.b_row_bytes + wc;
-      } else {
-        int k = L16 >> 5, cs = L16 & 31;
-        int c = cs ^ ((k & 7) << 1);
-        int wc = tile_col_to_weight_col<C>(c * 8, nt, p.N, SWIGLU);
-        if (wc >= p.Ntot) wc = p.Ntot - 8;
-        cp.b[j] = bgrp + (int64_t)k * p.b_row_bytes + (int64_t)wc * 2;
-      }
-    }
-    cp.b_stage_stride = B_KN ? (int64_t)(C::KB / ESIZE) * p.b_row_bytes : C::KB;
-    if (splits > 1) {
-      const int64_t k0_stages = (int64_t)split * nk;
-#pragma unroll
-      for (int j = 0; j < C::A_INSTR; ++j) cp.a[j] += k0_stages * C::KB;
-#pragma unroll
-      for (int j = 0; j < C::B_INSTR; ++j) cp.b[j] += k0_stages * cp.b_stage_stride;
-    }
-    cp.s = nullptr;
-    cp.bs = nullptr;
-    cp.bsr = nullptr;
-    cp.bs_stage_stride = 0;
-    if (MX) {
-      if (wave < C::AS_WAVES) {
-        // A scales: row wave*64 + lane (16 codes = 8 stages per fetch)
-        int r = wave * 64 + lane;
-        int rr = r < rows_valid ? r : rows_valid - 1;
-        int64_t routed = tile_row0 + rr;
-        int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
-        cp.s = p.a_scale + src * p.a_scale_ld;
-      }
-      if (!B_KN) {
-        // B row scales: tile column wave*64 + lane (16 codes = 8 stages per fetch)
-        int wc = tile_col_to_weight_col<C>(wave * 64 + lane, nt, p.N, SWIGLU);
-        if (wc >= p.Ntot) wc = p.Ntot - 1;
-        cp.bsr = p.b_scale + ((int64_t)g * p.Ntot + wc) * p.b_scale_ld;
-      } else if (is_bs_wave(wave)) {
-        // B scales: tile columns (wave*64 + lane)*2 .. +1, one col_scale group per stage
-        int j = (wave * 64 + lane) * 2;
-        int wc = tile_col_to_weight_col<C>(j, nt, p.N, SWIGLU);
-        if (wc >= p.Ntot) wc = p.Ntot - 2;
-        cp.bs = p.b_scale + (int64_t)g * p.b_scale_group_stride + (int64_t)wc * 2;
-        cp.bs_stage_stride = (int64_t)p.Ntot * 2;
-      }
-    }
+    // ---- decode work item, per-thread copy sources -------------------------------------
+#include "gemm_item_fwd.inc"
 
     v16f acc[C::MI][C::NI];
 #pragma unroll
@@ -657,9 +349,8 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
     __syncthreads();  // the previous item's last stage / epilogue reads are done before refilling
     const int rows_w = rows_valid - wm * C::WM;
     const int nm = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
-    // this wave copies A rows wave*RPW .. +RPW-1 (and, MX scale waves, scale rows wave*64 .. +63)
-    constexpr int RPW = C::A_INSTR * 16;  // A rows per wave
-    const bool la = wave * RPW < rows_valid;
+    // this wave copies A rows wave*A_INSTR*16 .. (and, MX scale waves, scale rows wave*64 .. +63)
+    const bool la = wave_copies_a<C>(wave, rows_valid);
     if (la) {
       if (C::MI >= 4 && nm == 4) k_loop<C, MX, B_KN, (C::MI >= 4 ? 4 : 1), true>(cp, nk, wave, wm, wn, lane, smem, acc);
       else if (nm == 2) k_loop<C, MX, B_KN, 2, true>(cp, nk, wave, wm, wn, lane, smem, acc);
@@ -831,45 +522,7 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_wgrad_k
   for (int round = 0;; ++round) {
     const int L = round * (int)gridDim.x + xcd * per_xcd + slot;
     if (L >= total) break;
-    const int g = L / per_g, local = L - g * per_g;
-    const int nt = local / p.m_tiles, mt = local - nt * p.m_tiles;
-    const int k0 = g == 0 ? 0 : (int)p.group_list[g - 1];
-    const int kend = (int)p.group_list[g];
-    const int nk = (kend - k0 + 31) / 32;  // 32 K rows per stage
-    const int m0 = mt * C::BM;
-    const int rows_valid = min(C::BM, p.m_rows - m0);
-
-    CopyPlan<C> cp;
-    cp.zero = p.zero_row;
-    cp.lda_k = p.lda_bytes;
-    cp.ldb_k = p.b_row_bytes;
-    cp.k0 = k0;
-    cp.k_end = kend;
-#pragma unroll
-    for (int j = 0; j < C::A_INSTR; ++j) {
-      const int L16 = (wave * C::A_INSTR + j) * 64 + lane;
-      const int k = L16 >> 5, cs = L16 & 31;
-      const int c = cs ^ ((k & 7) << 1);
-      int col = m0 + c * 8;
-      if (col > p.m_rows - 8) col = p.m_rows - 8;
-      cp.a[j] = p.A + (int64_t)col * 2;
-      cp.a_k[j] = k;
-      cp.a_col[j] = col * 2;
-    }
-#pragma unroll
-    for (int j = 0; j < C::B_INSTR; ++j) {
-      const int L16 = (wave * C::B_INSTR + j) * 64 + lane;
-      const int k = L16 >> 5, cs = L16 & 31;
-      const int c = cs ^ ((k & 7) << 1);
-      int col = nt * C::BN + c * 8;
-      if (col > p.N - 8) col = p.N - 8;
-      cp.b[j] = p.B + (int64_t)col * 2;
-      cp.b_k[j] = k;
-      cp.b_col[j] = col * 2;
-    }
-    cp.b_stage_stride = 0;
-    cp.s = cp.bs = cp.bsr = nullptr;
-    cp.bs_stage_stride = 0;
+#include "gemm_item_wgrad.inc"
 
     v16f acc[C::MI][C::NI];
 #pragma unroll

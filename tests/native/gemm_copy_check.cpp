@@ -1,0 +1,992 @@
+// Host-side copy checker for the grouped GEMM (test infrastructure; never runs on a GPU).
+//
+// The library's host code (api.hip, backward.hip, dispatch.hip, quant.hip, gemm.hip compiled for the
+// host only, with every optional path switched on) is linked against this file, which supplies:
+//   * stand-ins for the HIP runtime entry points the host code calls (kernel launches do nothing,
+//     hipMemsetAsync writes host memory), so all "device" buffers are plain host allocations;
+//   * host versions of the internal enqueue functions whose results later stages read (dispatch
+//     metadata, tile prefix) and of the grouped GEMM launches, which, instead of launching, run the
+//     GEMM's copy schedule on the host for every work item, wave and lane: the same copy-plan code
+//     and issue functions the kernels compile (gemm_plan.h and its .inc fragments), with a recorder
+//     as the copy instruction.
+// Every recorded copy is checked for:
+//   1. its global source lying inside one live allocation (16 or 4 bytes per lane);
+//   2. its LDS destination lying inside the ring slot of its stage (below the tile prefix);
+//   3. its source being exactly the element the LDS fragment reads expect at that LDS position,
+//      computed from the tensor shapes of the C-ABI call (independently of the GGParams the host
+//      code built) for rows and columns that reach the output;
+//   4. the vmcnt wait before each stage leaving only loads younger than that stage in flight, and
+//      every ring slot being refilled only after the stage it held has been read;
+//   5. full coverage of each stage's weight slot (and scale slots) by the four waves.
+// The epilogue's output ranges are checked against the output allocation, and every host-side read
+// of the index arrays runs under AddressSanitizer.
+//
+// Usage: gemm_copy_check [scenario-name ...]   (no argument: all scenarios). Exit status 0 when
+// every check passed.
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../hyper_multicore_amd/csrc/gemm_plan.h"
+#include "../../include/mi355moe.h"
+
+// ------------------------------------------------------------------------------------------------
+// Allocations and error reporting
+struct Alloc {
+  uint8_t* p;
+  size_t n;
+  std::string name;
+};
+static std::vector<Alloc> g_allocs;
+static long g_errors = 0, g_copies = 0, g_items = 0, g_gemms = 0;
+static std::string g_scenario;
+
+#define CHECK_FAIL(...)                                         \
+  do {                                                          \
+    if (g_errors < 30) {                                        \
+      fprintf(stderr, "[%s] ", g_scenario.c_str());             \
+      fprintf(stderr, __VA_ARGS__);                             \
+      fputc('\n', stderr);                                      \
+    }                                                           \
+    ++g_errors;                                                 \
+  } while (0)
+
+static uint8_t* mk(const char* name, size_t n, int fill = 0x5a) {
+  uint8_t* p = (uint8_t*)malloc(n ? n : 1);
+  if (!p) {
+    fprintf(stderr, "out of memory (%s, %zu bytes)\n", name, n);
+    exit(2);
+  }
+  memset(p, fill, n);
+  g_allocs.push_back({p, n, name});
+  return p;
+}
+static void free_all() {
+  for (auto& a : g_allocs) free(a.p);
+  g_allocs.clear();
+}
+static const Alloc* find_alloc(const void* q, size_t sz) {
+  const uint8_t* b = (const uint8_t*)q;
+  for (const auto& a : g_allocs)
+    if (b >= a.p && b + sz <= a.p + a.n) return &a;
+  return nullptr;
+}
+static const Alloc* alloc_of(const void* q) { return find_alloc(q, 1); }
+
+// ------------------------------------------------------------------------------------------------
+// HIP runtime stand-ins (the host code only enqueues; nothing here touches a GPU)
+static long g_launches = 0;
+extern "C" {
+void** __hipRegisterFatBinary(const void*) {
+  static void* handle = nullptr;
+  return &handle;
+}
+void __hipRegisterFunction(void**, const void*, char*, const char*, unsigned int, uint3*, uint3*, dim3*, dim3*, int*) {}
+void __hipUnregisterFatBinary(void**) {}
+hipError_t __hipPushCallConfiguration(dim3, dim3, size_t, hipStream_t) { return hipSuccess; }
+hipError_t __hipPopCallConfiguration(dim3* g, dim3* b, size_t* s, hipStream_t* st) {
+  *g = dim3(1);
+  *b = dim3(1);
+  *s = 0;
+  *st = nullptr;
+  return hipSuccess;
+}
+hipError_t hipLaunchKernel(const void*, dim3, dim3, void**, size_t, hipStream_t) {
+  ++g_launches;
+  return hipSuccess;
+}
+hipError_t hipMemsetAsync(void* dst, int value, size_t n, hipStream_t) {
+  if (n && !find_alloc(dst, n)) {
+    CHECK_FAIL("hipMemsetAsync of %zu bytes outside every allocation", n);
+    return hipErrorInvalidValue;
+  }
+  memset(dst, value, n);
+  return hipSuccess;
+}
+hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }
+hipError_t hipGetLastError(void) { return hipSuccess; }
+hipError_t hipFuncSetAttribute(const void*, hipFuncAttribute, int) { return hipSuccess; }
+hipError_t hipGetDevice(int* d) {
+  *d = 0;
+  return hipSuccess;
+}
+hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
+  *v = 256;
+  return hipSuccess;
+}
+}
+
+// ------------------------------------------------------------------------------------------------
+// Host versions of the enqueue functions whose outputs the GEMM set-up reads
+int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t, bool small) {
+  const int bm = mi355_gg_bm(small);
+  if (!find_alloc(tile_prefix, (size_t)(G + 1) * 4)) CHECK_FAIL("tile prefix of %d groups outside its buffer", G);
+  int64_t acc = 0;
+  for (int g = 0; g < G; ++g) {
+    const int64_t rows = group_list[g] - (g ? group_list[g - 1] : 0);
+    tile_prefix[g] = (int32_t)acc;
+    acc += rows > 0 ? (rows + bm - 1) / bm : 0;
+  }
+  tile_prefix[G] = (int32_t)acc;
+  return MI355MOE_OK;
+}
+
+// Stable counting sort of the T*K slots by expert id (the dispatch contract of include/mi355moe.h).
+int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t T, int K, int E, int32_t* counts, int64_t* offsets,
+                           int64_t* group_list, int32_t* mapping, int32_t* gather, int32_t* error_flag, void*,
+                           hipStream_t) {
+  const int64_t S = T * K;
+  std::vector<int64_t> c(E, 0);
+  auto id_of = [&](int64_t s) -> int64_t {
+    return dtype == MI355MOE_IDS_INT64 ? ((const int64_t*)ids)[s] : (int64_t)((const int32_t*)ids)[s];
+  };
+  bool bad = false;
+  for (int64_t s = 0; s < S; ++s) {
+    const int64_t e = id_of(s);
+    if (e < 0 || e >= E) bad = true;
+    else ++c[e];
+  }
+  std::vector<int64_t> start(E, 0);
+  for (int e = 1; e < E; ++e) start[e] = start[e - 1] + c[e - 1];
+  for (int e = 0; e < E; ++e) {
+    if (counts) counts[e] = (int32_t)c[e];
+    if (offsets) offsets[e] = start[e];
+    if (group_list) group_list[e] = start[e] + c[e];
+  }
+  std::vector<int64_t> next = start;
+  for (int64_t s = 0; s < S; ++s) {
+    const int64_t e = id_of(s);
+    const int64_t r = (e < 0 || e >= E) ? -1 : next[e]++;
+    if (mapping) mapping[s] = (int32_t)r;
+    if (gather && r >= 0) gather[r] = (int32_t)s;
+  }
+  if (error_flag && bad) *error_flag = 1;
+  return MI355MOE_OK;
+}
+int mi355_permute_rows_enqueue(const uint16_t*, int64_t, int, int, const int32_t*, uint16_t*, hipStream_t) {
+  return MI355MOE_OK;
+}
+int mi355_unpermute_enqueue(const uint16_t*, const int32_t*, const float*, int64_t, int, int, uint16_t*, hipStream_t) {
+  return MI355MOE_OK;
+}
+int mi355_mx_quant_rows(const uint16_t*, int64_t, int, uint8_t*, uint8_t*, int64_t, hipStream_t) {
+  return MI355MOE_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Expected operand layout: where the element the LDS reads expect lives, from the shapes of the
+// C-ABI call. A scenario that knows the operands of a GEMM sets `g_expect` before the call; GEMMs on
+// the library's internal buffers fall back to the addressing implied by their GGParams, and are
+// then still bounds-checked against the allocations.
+struct Expect {
+  bool set = false;
+  const uint8_t* A = nullptr;  // [rowsA, Kd] elements, row stride a_row_bytes
+  int64_t a_row_bytes = 0;
+  const uint8_t* a_scale = nullptr;  // MX: [rowsA, a_scale_ld] codes
+  int64_t a_scale_ld = 0;
+  const uint8_t* B = nullptr;  // [G, Kd, Ntot] (EIO) or [G, Ntot, Kd] (EOI) elements
+  const uint8_t* b_scale = nullptr;  // MX EIO: [G, Kd/64, Ntot, 2]; MX EOI: [G, Ntot, b_scale_ld]
+  int64_t b_scale_ld = 0;
+};
+static Expect g_expect;
+
+struct Layout {
+  const uint8_t* A;
+  int64_t a_row_bytes;
+  const int32_t* gather;
+  int gather_div;
+  const uint8_t* as;
+  int64_t as_ld;
+  const uint8_t* B;
+  bool eoi;
+  int64_t Kd, Ntot;
+  int esize;
+  const uint8_t* bs;
+  int64_t bs_ld;
+  int64_t src_row(int64_t routed) const { return gather ? gather[routed] / gather_div : routed; }
+  const uint8_t* a_at(int64_t routed, int64_t kbyte) const { return A + src_row(routed) * a_row_bytes + kbyte; }
+  const uint8_t* b_at(int g, int64_t k, int64_t col) const {
+    const int64_t e = eoi ? ((int64_t)g * Ntot + col) * Kd + k : ((int64_t)g * Kd + k) * Ntot + col;
+    return B + e * esize;
+  }
+  const uint8_t* as_at(int64_t routed, int64_t code) const { return as + src_row(routed) * as_ld + code; }
+  // MX EIO col_scale [G, Kd/64, Ntot, 2]: the two codes of column col for the 64-K group kg
+  const uint8_t* bs_col_at(int g, int64_t kg, int64_t col) const { return bs + (((int64_t)g * (Kd / 64) + kg) * Ntot + col) * 2; }
+  // MX EOI row scales [G, Ntot, bs_ld]
+  const uint8_t* bs_row_at(int g, int64_t col, int64_t code) const { return bs + ((int64_t)g * Ntot + col) * bs_ld + code; }
+};
+
+// Tile column n (0 .. BN-1) of n-tile nt -> weight column; false when its output column is past N.
+// (SwiGLU: each WN-wide wave tile holds WN/2 gate columns and then the WN/2 matching up columns.)
+template <class C>
+static bool tile_weight_col(int n, int nt, int N, bool swiglu, int64_t* wcol) {
+  if (!swiglu) {
+    const int64_t o = (int64_t)nt * C::BN + n;
+    *wcol = o;
+    return o < N;
+  }
+  const int H = C::WN / 2, q = n / C::WN, jj = n % C::WN;
+  const int64_t o = (int64_t)nt * (C::BN / 2) + q * H + (jj % H);
+  *wcol = jj < H ? o : N + o;
+  return o < N;
+}
+
+// ------------------------------------------------------------------------------------------------
+// The recorder used as the copy instruction
+struct Rec {
+  const uint8_t* g;
+  int sz;
+  uint32_t off;
+  int iter;  // pipelined step whose barrier preceded the copy (-1: before the K loop)
+};
+struct Wait {
+  size_t pos;  // copies recorded before the wait
+  int stage;   // stage read after the following barrier
+  int n;       // loads allowed in flight
+};
+static std::vector<Rec>* g_rec = nullptr;
+static int g_iter = -1;
+struct CheckDma {
+  template <int SZ>
+  static void copy(const void* g, uint32_t off, uint8_t*, int enable) {
+    if (!enable) return;
+    g_rec->push_back({(const uint8_t*)g, SZ, off, g_iter});
+  }
+};
+
+enum Region { R_A = 0, R_B, R_BS, R_AS, R_BSR, R_N };
+static const char* region_name(int r) {
+  static const char* n[] = {"A", "B", "B-scale", "A-scale", "B-row-scale"};
+  return n[r];
+}
+
+// One lane's copy sequence of one work item, replayed in the K loop's order (k_loop in gemm.hip:
+// prologue, the wait for stage 0, then for every pipelined step k the wait for stage k + 1 and the
+// copy items of the step).
+template <class C, bool MX, bool B_KN, bool LA, bool GK>
+static void record_schedule(const CopyPlan<C>& cp, int nk, int wave, std::vector<Rec>& rec, std::vector<Wait>& waits) {
+  uint8_t* smem = nullptr;
+  g_rec = &rec;
+  g_iter = -1;
+  {
+    using D = CheckDma;
+#include "../../hyper_multicore_amd/csrc/gemm_kloop_prologue.inc"
+    waits.push_back({rec.size(), 0, younger_than<C, LA>(0, -1, nk, la_n, lb_n)});
+    for (int k = 0; k < nk - 1; ++k) {
+      waits.push_back({rec.size(), k + 1, younger_than<C, LA>(k + 1, k - 1, nk, la_n, lb_n)});
+      g_iter = k;
+      for (int it = 0; it < StepShape<C, MX, 1>::ITEMS; ++it) issue_item<C, MX, B_KN, LA, GK, D>(cp, k, nk, wave, smem, it);
+      issue_scales_item<C, MX, B_KN, LA, D>(cp, k, nk, wave, smem);
+    }
+  }
+  g_rec = nullptr;
+}
+
+// Per work item bookkeeping shared by the lanes
+struct ItemCtx {
+  int g, nt, split, nk;
+  int64_t tile_row0;  // forward: first routed row; grouped-K: unused
+  int rows_valid;
+  // grouped-K
+  int k0, kend, m0;
+  std::vector<uint8_t> cov[R_N];  // coverage bitmaps [stage or group][slot bytes]
+};
+
+struct Decoded {
+  int region, slot, stage;  // stage (A/B/BS) or scale group (AS/BSR)
+  uint32_t rel;             // byte offset of this lane's data inside the slot
+};
+
+template <class C>
+static bool classify(uint32_t pos, int sz, Decoded& d) {
+  if (pos + sz > (uint32_t)C::PREFIX_OFF) return false;
+  if (pos < (uint32_t)C::B_OFF) {
+    d.region = R_A;
+    d.slot = pos / C::A_BYTES;
+    d.rel = pos % C::A_BYTES;
+    return d.rel + sz <= (uint32_t)C::A_BYTES;
+  }
+  if (pos < (uint32_t)C::AS_OFF) {
+    const uint32_t q = pos - C::B_OFF;
+    d.slot = q / C::B_SLOT;
+    const uint32_t rel = q % C::B_SLOT;
+    if (rel < (uint32_t)C::B_BYTES) {
+      d.region = R_B;
+      d.rel = rel;
+      return rel + sz <= (uint32_t)C::B_BYTES;
+    }
+    d.region = R_BS;
+    d.rel = rel - C::B_BYTES;
+    return d.rel + sz <= (uint32_t)C::BS_BYTES;
+  }
+  if (pos < (uint32_t)C::BSR_OFF) {
+    const uint32_t q = pos - C::AS_OFF;
+    d.region = R_AS;
+    d.slot = q / C::AS_SLOT;
+    d.rel = q % C::AS_SLOT;
+    return d.rel + sz <= (uint32_t)C::AS_SLOT;
+  }
+  const uint32_t q = pos - C::BSR_OFF;
+  d.region = R_BSR;
+  d.slot = q / C::BSR_SLOT;
+  d.rel = q % C::BSR_SLOT;
+  return d.slot < 2 && d.rel + sz <= (uint32_t)C::BSR_SLOT;
+}
+
+// The element the fragment reads expect at LDS byte `rel` of a slot of `region` holding `stage`,
+// or nullptr when that position feeds only rows / columns the epilogue drops.
+template <class C, bool MX, bool B_KN, bool SWIGLU, bool GK>
+static const uint8_t* expected_src(const GGParams& p, const Layout& L, const ItemCtx& it, int region, int stage,
+                                   uint32_t rel, bool* zero_ok) {
+  *zero_ok = false;
+  int64_t wcol;
+  if constexpr (GK) {
+    // both operands K-major: K row k (32 per stage) at k*512, 16-byte chunk c stored at c ^ ((k&7)<<1)
+    const int k = rel / 512, cpos = (rel % 512) / 16, c = cpos ^ ((k & 7) << 1);
+    const int64_t row = (int64_t)it.k0 + (int64_t)stage * 32 + k;
+    if (region == R_A) {
+      const int64_t m = (int64_t)it.m0 + c * 8;
+      if (m >= p.m_rows) return nullptr;
+      if (row >= it.kend) {
+        *zero_ok = true;
+        return nullptr;
+      }
+      return L.A + row * L.a_row_bytes + m * 2;
+    }
+    const int64_t n = (int64_t)it.nt * C::BN + c * 8;
+    if (n >= p.N) return nullptr;
+    if (row >= it.kend) {
+      *zero_ok = true;
+      return nullptr;
+    }
+    return L.B + row * L.Ntot * 2 + n * 2;
+  } else {
+    const int64_t kstage = (int64_t)it.split * it.nk + stage;  // stage index along the full K
+    switch (region) {
+      case R_A: {
+        const int r = rel / 64, cpos = (rel % 64) / 16, c = cpos ^ ((r >> 2) & 3);
+        if (r >= it.rows_valid) return nullptr;
+        return L.a_at(it.tile_row0 + r, kstage * C::KB + c * 16);
+      }
+      case R_B: {
+        if (!B_KN) {  // K-contiguous weight rows, laid out like the activations
+          const int n = rel / 64, cpos = (rel % 64) / 16, c = cpos ^ ((n >> 2) & 3);
+          if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+          return L.b_at(it.g, (kstage * C::KB + c * 16) / L.esize, wcol);
+        }
+        if (MX) {  // 64 K rows of 256 bytes, chunk c at c ^ (k & 15), 16 columns per chunk
+          const int k = rel / 256, cpos = (rel % 256) / 16, c = cpos ^ (k & 15);
+          if (!tile_weight_col<C>(c * 16, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+          return L.b_at(it.g, kstage * 64 + k, wcol);
+        }
+        // bf16: 32 K rows of 512 bytes, chunk c at c ^ ((k & 7) << 1), 8 columns per chunk
+        const int k = rel / 512, cpos = (rel % 512) / 16, c = cpos ^ ((k & 7) << 1);
+        if (!tile_weight_col<C>(c * 8, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+        return L.b_at(it.g, kstage * 32 + k, wcol);
+      }
+      case R_BS: {  // two codes for each of tile columns 2m, 2m+1 (4 bytes per lane)
+        const int n = (rel / 4) * 2;
+        if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+        return L.bs_col_at(it.g, kstage, wcol);
+      }
+      case R_AS: {  // 16 codes (8 stages) per row
+        const int r = rel / 16;
+        if (r >= it.rows_valid) return nullptr;
+        return L.as_at(it.tile_row0 + r, (int64_t)stage * 16);
+      }
+      case R_BSR: {  // 16 codes (8 stages) per tile column
+        const int n = rel / 16;
+        if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+        return L.bs_row_at(it.g, wcol, (int64_t)stage * 16);
+      }
+    }
+  }
+  return nullptr;
+}
+
+// Checks one lane's copies of one work item; accumulates the coverage of the item's slots.
+template <class C, bool MX, bool B_KN, bool SWIGLU, bool GK>
+static void check_lane(const GGParams& p, const Layout& L, ItemCtx& it, int wave, int lane, bool la,
+                       const std::vector<Rec>& rec, const std::vector<Wait>& waits) {
+  const int slots[R_N] = {C::A_SLOTS, C::B_SLOTS, C::B_SLOTS, 2, 2};
+  const int per_fill[R_N] = {C::A_INSTR, C::B_INSTR, 1, 1, 1};
+  int fills[R_N][8] = {};
+  std::vector<Decoded> dec(rec.size());
+  for (size_t i = 0; i < rec.size(); ++i) {
+    const Rec& r = rec[i];
+    ++g_copies;
+    if (!find_alloc(r.g, r.sz)) {
+      const Alloc* a = alloc_of(r.g);
+      CHECK_FAIL("copy %zu (wave %d lane %d, group %d n-tile %d) reads %d bytes outside every allocation%s%s", i, wave,
+                 lane, it.g, it.nt, r.sz, a ? ": past the end of " : "", a ? a->name.c_str() : "");
+      continue;
+    }
+    Decoded& d = dec[i];
+    Decoded first_lane, last_lane;
+    const uint32_t pos = r.off + (uint32_t)r.sz * lane;
+    const bool ok = classify<C>(pos, r.sz, d) && classify<C>(r.off, r.sz, first_lane) &&
+                    classify<C>(r.off + 63u * r.sz, r.sz, last_lane) && first_lane.region == last_lane.region &&
+                    first_lane.slot == last_lane.slot;
+    if (!ok) {
+      CHECK_FAIL("copy %zu (wave %d lane %d) writes LDS %u..%u outside one ring slot", i, wave, lane, r.off,
+                 r.off + 64u * r.sz);
+      d.region = -1;
+      continue;
+    }
+    if (d.slot >= slots[d.region]) {
+      CHECK_FAIL("copy %zu writes slot %d of the %s ring (%d slots)", i, d.slot, region_name(d.region), slots[d.region]);
+      d.region = -1;
+      continue;
+    }
+    // stage (or scale group) held: slots are filled in stage order, per_fill copies per stage
+    const int f = fills[d.region][d.slot]++;
+    d.stage = d.slot + slots[d.region] * (f / per_fill[d.region]);
+    const bool group = d.region == R_AS || d.region == R_BSR;
+    if ((group ? 8 * d.stage : d.stage) >= it.nk) {
+      CHECK_FAIL("copy %zu loads %s %s %d of an item with %d stages", i, region_name(d.region), group ? "group" : "stage",
+                 d.stage, it.nk);
+      continue;
+    }
+    // ring reuse: the previous occupant of the slot was read in the step before its stage
+    const int prev = d.stage - slots[d.region];
+    if (prev >= 0) {
+      const int prev_last = group ? 8 * prev + 7 : prev;
+      if (prev_last > r.iter)
+        CHECK_FAIL("copy %zu refills the %s slot of %s %d at step %d while stage %d may still be read", i,
+                   region_name(d.region), group ? "group" : "stage", prev, r.iter, prev_last);
+    }
+    // source element
+    bool zero_ok = false;
+    const uint8_t* want = expected_src<C, MX, B_KN, SWIGLU, GK>(p, L, it, d.region, d.stage, d.rel, &zero_ok);
+    if (zero_ok) {
+      const Alloc* z = alloc_of(p.zero_row);
+      if (!z || r.g < p.zero_row || r.g + r.sz > p.zero_row + z->n) {
+        CHECK_FAIL("grouped-K copy %zu past the group end does not read the zero row", i);
+      } else {
+        for (int b = 0; b < r.sz; ++b)
+          if (r.g[b] != 0) {
+            CHECK_FAIL("zero row holds a nonzero byte");
+            break;
+          }
+      }
+    } else if (want != nullptr && want != r.g) {
+      CHECK_FAIL("copy %zu (wave %d lane %d, group %d n-tile %d, %s %s %d, LDS byte %u) reads %+lld bytes from the "
+                 "expected element",
+                 i, wave, lane, it.g, it.nt, region_name(d.region), group ? "group" : "stage", d.stage, d.rel,
+                 (long long)(r.g - want));
+    }
+    // coverage
+    auto& cov = it.cov[d.region];
+    const int unit = d.region == R_A ? C::A_BYTES
+                   : d.region == R_B ? C::B_BYTES
+                   : d.region == R_BS ? C::BS_BYTES
+                   : d.region == R_AS ? C::AS_SLOT : C::BSR_SLOT;
+    const size_t base = (size_t)d.stage * unit + d.rel;
+    if (base + r.sz <= cov.size())
+      for (int b = 0; b < r.sz; ++b) {
+        if (cov[base + b]) {
+          CHECK_FAIL("LDS byte %u of %s %d written twice", d.rel + b, region_name(d.region), d.stage);
+          break;
+        }
+        cov[base + b] = 1;
+      }
+  }
+  // waits: before the barrier that precedes reading stage j, every load of stage j (and of its
+  // scale group) issued by this wave is older than the n loads allowed in flight
+  for (const Wait& w : waits) {
+    const size_t done = w.pos >= (size_t)w.n ? w.pos - w.n : 0;
+    for (size_t i = 0; i < rec.size(); ++i) {
+      const Decoded& d = dec[i];
+      if (d.region < 0) continue;
+      const bool group = d.region == R_AS || d.region == R_BSR;
+      const bool needed = group ? d.stage == w.stage / C::AS_GROUP : d.stage == w.stage;
+      if (needed && i >= done)
+        CHECK_FAIL("wave %d: the wait before stage %d (vmcnt %d after %zu loads) leaves load %zu (%s %d) in flight",
+                   wave, w.stage, w.n, w.pos, i, region_name(d.region), d.stage);
+    }
+  }
+  (void)la;
+}
+
+// Coverage of one item: every byte of each weight / scale slot a stage reads was written once;
+// activation rows inside the tile were written.
+template <class C, bool MX, bool B_KN, bool GK>
+static void check_coverage(const ItemCtx& it) {
+  auto full = [&](int region, int stages, int unit, int used, const char* what) {
+    for (int s = 0; s < stages; ++s)
+      for (int b = 0; b < used; ++b)
+        if (!it.cov[region][(size_t)s * unit + b]) {
+          CHECK_FAIL("group %d n-tile %d: byte %d of %s %d never loaded", it.g, it.nt, b, what, s);
+          return;
+        }
+  };
+  const int ngroups = (it.nk + C::AS_GROUP - 1) / C::AS_GROUP;
+  full(R_B, it.nk, C::B_BYTES, C::B_BYTES, "weight stage");
+  if (GK) full(R_A, it.nk, C::A_BYTES, C::A_BYTES, "activation stage");
+  else full(R_A, it.nk, C::A_BYTES, it.rows_valid * 64, "activation stage");
+  if (MX && B_KN) full(R_BS, it.nk, C::BS_BYTES, C::BS_BYTES, "weight scale stage");
+  if (MX && !B_KN) full(R_BSR, ngroups, C::BSR_SLOT, C::BSR_SLOT, "weight row-scale group");
+  if (MX) full(R_AS, ngroups, C::AS_SLOT, it.rows_valid * 16, "activation scale group");
+}
+
+static void check_range(const void* base, int64_t lo, int64_t hi, const char* what) {
+  if (hi <= lo) return;
+  const uint8_t* b = (const uint8_t*)base;
+  if (!find_alloc(b + lo, (size_t)(hi - lo))) CHECK_FAIL("%s writes bytes %lld..%lld outside its allocation", what,
+                                                         (long long)lo, (long long)hi);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Forward grouped GEMM: all work items, waves and lanes
+template <class C, bool MX, bool B_KN, int EPI>
+static int sim_forward(const GGParams& p) {
+  constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX || EPI == EPI_SWIGLU_BF16_NUM);
+  constexpr int ESIZE = MX ? 1 : 2;
+  ++g_gemms;
+  // the kernel's own checks on the parameters it assumes
+  if (!find_alloc(p.tile_prefix, (size_t)(p.G + 1) * 4)) CHECK_FAIL("tile prefix outside its buffer");
+  if (!find_alloc(p.group_list, (size_t)p.G * 8)) CHECK_FAIL("group list outside its buffer");
+  const int32_t* prefix = p.tile_prefix;
+  // the two set-up lines of grouped_gemm_kernel
+  const int splits = (EPI == EPI_STORE_F32 && p.k_splits > 1) ? p.k_splits : 1;
+  const int total = prefix[p.G] * p.n_tiles * splits;
+  const int nk = p.K / splits * ESIZE / C::KB;  // stages per work item
+  if (nk < 1) CHECK_FAIL("K = %d gives %d stages", p.K, nk);
+  Layout lay;
+  if (g_expect.set) {
+    lay = {g_expect.A, g_expect.a_row_bytes, p.a_row_index, p.a_row_div, g_expect.a_scale, g_expect.a_scale_ld,
+         g_expect.B, !B_KN, p.K, p.Ntot, ESIZE, g_expect.b_scale, g_expect.b_scale_ld};
+  } else {
+    lay = {p.A, p.lda_bytes, p.a_row_index, p.a_row_div, p.a_scale, p.a_scale_ld, p.B, !B_KN, p.K, p.Ntot, ESIZE,
+         p.b_scale, p.b_scale_ld};
+  }
+  for (int L_item = 0; L_item < total; ++L_item) {
+    ItemCtx ctx;
+    std::vector<Rec> rec;
+    std::vector<Wait> waits;
+    bool first = true;
+    for (int wave = 0; wave < C::WAVES; ++wave)
+      for (int lane = 0; lane < 64; ++lane) {
+        const int L = L_item;
+#include "../../hyper_multicore_amd/csrc/gemm_item_fwd.inc"
+        (void)mt;
+        if (first) {
+          first = false;
+          ++g_items;
+          ctx.g = g;
+          ctx.nt = nt;
+          ctx.split = split;
+          ctx.nk = nk;
+          ctx.tile_row0 = tile_row0;
+          ctx.rows_valid = rows_valid;
+          ctx.cov[R_A].assign((size_t)nk * C::A_BYTES, 0);
+          ctx.cov[R_B].assign((size_t)nk * C::B_BYTES, 0);
+          ctx.cov[R_BS].assign((size_t)nk * C::BS_BYTES, 0);
+          const int ng = (nk + 7) / 8 + 1;
+          ctx.cov[R_AS].assign((size_t)ng * C::AS_SLOT, 0);
+          ctx.cov[R_BSR].assign((size_t)ng * C::BSR_SLOT, 0);
+          if (rows_valid < 1 || rows_valid > C::BM) CHECK_FAIL("item %d: %d valid rows", L_item, rows_valid);
+          if (g < 0 || g >= p.G || nt < 0 || nt >= p.n_tiles) CHECK_FAIL("item %d decodes to group %d n-tile %d", L_item, g, nt);
+          // epilogue output range of this tile
+          const int64_t r0 = tile_row0, r1 = tile_row0 + rows_valid - 1;
+          if (EPI == EPI_STORE_BF16) {
+            const int64_t cols = std::min<int64_t>(C::BN, p.N - (int64_t)nt * C::BN);
+            check_range(p.C, (r0 * p.ldc + (int64_t)nt * C::BN) * 2, (r1 * p.ldc + (int64_t)nt * C::BN + cols) * 2,
+                        "bf16 epilogue");
+          } else if (EPI == EPI_STORE_F32) {
+            const int64_t cols = std::min<int64_t>(C::BN, p.N - (int64_t)nt * C::BN);
+            for (int64_t r = r0; r <= r1; ++r) {
+              const int64_t orow = p.c_row_index ? p.c_row_index[r] : r;
+              const int64_t at = split * p.c_split_stride + orow * p.ldc + (int64_t)nt * C::BN;
+              check_range(p.C, at * 4, (at + cols) * 4, "fp32 epilogue");
+            }
+          } else if (EPI == EPI_SWIGLU_MX) {
+            check_range(p.C, r0 * p.ldc + (int64_t)nt * (C::BN / 2), r1 * p.ldc + (int64_t)nt * (C::BN / 2) + C::BN / 2,
+                        "MX SwiGLU epilogue");
+            check_range(p.c_scale, r0 * p.c_scale_ld + nt * 4, r1 * p.c_scale_ld + nt * 4 + 4, "MX SwiGLU scales");
+            if ((int64_t)nt * (C::BN / 2) + C::BN / 2 > p.N) CHECK_FAIL("MX SwiGLU tile past N = %d", p.N);
+          } else {
+            check_range(p.C, (r0 * p.ldc + (int64_t)nt * (C::BN / 2)) * 2,
+                        (r1 * p.ldc + (int64_t)nt * (C::BN / 2) + C::BN / 2) * 2, "SwiGLU epilogue");
+            if ((int64_t)nt * (C::BN / 2) + C::BN / 2 > p.N) CHECK_FAIL("SwiGLU tile past N = %d", p.N);
+            if (EPI == EPI_SWIGLU_BF16_NUM && p.row_prob != nullptr)
+              for (int64_t r = r0; r <= r1; ++r)
+                if (!find_alloc(p.row_prob + p.a_row_index[r], 4)) CHECK_FAIL("row probability of row %lld", (long long)r);
+          }
+        }
+        const bool la = wave_copies_a<C>(wave, rows_valid);
+        rec.clear();
+        waits.clear();
+        if (la) record_schedule<C, MX, B_KN, true, false>(cp, nk, wave, rec, waits);
+        else record_schedule<C, MX, B_KN, false, false>(cp, nk, wave, rec, waits);
+        check_lane<C, MX, B_KN, SWIGLU, false>(p, lay, ctx, wave, lane, la, rec, waits);
+      }
+    check_coverage<C, MX, B_KN, false>(ctx);
+  }
+  return MI355MOE_OK;
+}
+
+template <class C, int EPI>
+static int sim_wgrad(const GGParams& p) {
+  ++g_gemms;
+  if (!find_alloc(p.group_list, (size_t)p.G * 8)) CHECK_FAIL("group list outside its buffer");
+  const int per_g = p.m_tiles * p.n_tiles;
+  const int total = p.G * per_g;
+  Layout Lo = {p.A, p.lda_bytes, nullptr, 1, nullptr, 0, p.B, false, 0, 0, 2, nullptr, 0};
+  if (g_expect.set) {
+    Lo.A = g_expect.A;
+    Lo.a_row_bytes = g_expect.a_row_bytes;
+    Lo.B = g_expect.B;
+  }
+  Lo.Ntot = p.b_row_bytes / 2;  // B rows hold N bf16 (grouped-K: row stride of the routed rows)
+  if (g_expect.set) Lo.Ntot = p.N;
+  for (int L_item = 0; L_item < total; ++L_item) {
+    ItemCtx ctx;
+    std::vector<Rec> rec;
+    std::vector<Wait> waits;
+    bool first = true;
+    for (int wave = 0; wave < C::WAVES; ++wave)
+      for (int lane = 0; lane < 64; ++lane) {
+        const int L = L_item;
+#include "../../hyper_multicore_amd/csrc/gemm_item_wgrad.inc"
+        (void)mt;
+        if (first) {
+          first = false;
+          ++g_items;
+          ctx.g = g;
+          ctx.nt = nt;
+          ctx.split = 0;
+          ctx.nk = nk;
+          ctx.k0 = k0;
+          ctx.kend = kend;
+          ctx.m0 = m0;
+          ctx.rows_valid = rows_valid;
+          ctx.cov[R_A].assign((size_t)std::max(nk, 0) * C::A_BYTES, 0);
+          ctx.cov[R_B].assign((size_t)std::max(nk, 0) * C::B_BYTES, 0);
+          const int64_t cols = std::min<int64_t>(C::BN, p.N - (int64_t)nt * C::BN);
+          const int esz = EPI == EPI_STORE_F32 ? 4 : 2;
+          const int64_t at0 = (int64_t)g * p.c_group_stride + (int64_t)m0 * p.ldc + (int64_t)nt * C::BN;
+          const int64_t at1 = (int64_t)g * p.c_group_stride + (int64_t)(m0 + rows_valid - 1) * p.ldc + (int64_t)nt * C::BN + cols;
+          check_range(p.C, at0 * esz, at1 * esz, "weight-gradient epilogue");
+        }
+        if (nk <= 0) continue;
+        rec.clear();
+        waits.clear();
+        record_schedule<C, false, true, true, true>(cp, nk, wave, rec, waits);
+        check_lane<C, false, true, false, true>(p, Lo, ctx, wave, lane, true, rec, waits);
+      }
+    if (ctx.nk > 0) check_coverage<C, false, true, true>(ctx);
+  }
+  return MI355MOE_OK;
+}
+
+// The grouped GEMM entry points the host code calls, run on the host
+template <class C>
+static int sim_dispatch(const GGParams& p, bool mx, bool b_kn, int epi) {
+  if (!mx) {
+    if (!b_kn) {
+      switch (epi) {
+        case EPI_STORE_BF16: return sim_forward<C, false, false, EPI_STORE_BF16>(p);
+        case EPI_STORE_F32: return sim_forward<C, false, false, EPI_STORE_F32>(p);
+        case EPI_SWIGLU_BF16: return sim_forward<C, false, false, EPI_SWIGLU_BF16>(p);
+        case EPI_SWIGLU_BF16_NUM: return sim_forward<C, false, false, EPI_SWIGLU_BF16_NUM>(p);
+      }
+    } else {
+      switch (epi) {
+        case EPI_STORE_BF16: return sim_forward<C, false, true, EPI_STORE_BF16>(p);
+        case EPI_SWIGLU_BF16: return sim_forward<C, false, true, EPI_SWIGLU_BF16>(p);
+        case EPI_SWIGLU_BF16_NUM: return sim_forward<C, false, true, EPI_SWIGLU_BF16_NUM>(p);
+      }
+    }
+  } else if (!b_kn) {
+    switch (epi) {
+      case EPI_STORE_BF16: return sim_forward<C, true, false, EPI_STORE_BF16>(p);
+      case EPI_SWIGLU_MX: return sim_forward<C, true, false, EPI_SWIGLU_MX>(p);
+    }
+  } else {
+    switch (epi) {
+      case EPI_STORE_BF16: return sim_forward<C, true, true, EPI_STORE_BF16>(p);
+      case EPI_SWIGLU_MX: return sim_forward<C, true, true, EPI_SWIGLU_MX>(p);
+    }
+  }
+  CHECK_FAIL("no kernel for mx=%d b_kn=%d epilogue %d", mx, b_kn, epi);
+  return MI355MOE_EUNSUPPORTED;
+}
+
+// Library internals replaced by the simulation (same signatures as gemm.h)
+int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t, bool small) {
+  // the dispatcher's choice of the numerics epilogue (gemm.hip, mi355_grouped_gemm)
+  if (epi == EPI_SWIGLU_BF16_NUM) return MI355MOE_EINVAL;
+  if (epi == EPI_SWIGLU_BF16 && (p.swiglu_limit > 0.0f || p.row_prob != nullptr)) epi = EPI_SWIGLU_BF16_NUM;
+  if (small) {
+    if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
+    return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
+  }
+  return sim_dispatch<GGBig>(p, mx, b_kn, epi);
+}
+int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t) {
+  if (p.m_rows % 8 || p.N % 8 || p.m_tiles != (p.m_rows + GGBig::BM - 1) / GGBig::BM ||
+      p.n_tiles != (p.N + GGBig::BN - 1) / GGBig::BN || p.zero_row == nullptr)
+    return MI355MOE_EINVAL;
+  if (epi == EPI_STORE_F32) return sim_wgrad<GGBig, EPI_STORE_F32>(p);
+  if (epi == EPI_STORE_BF16) return sim_wgrad<GGBig, EPI_STORE_BF16>(p);
+  return MI355MOE_EUNSUPPORTED;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Scenarios: C-ABI calls with host buffers sized from the shapes the header documents
+static std::mt19937_64 g_rng(20261201);
+
+static std::vector<int64_t> cumsum(const std::vector<int>& counts) {
+  std::vector<int64_t> gl(counts.size());
+  int64_t a = 0;
+  for (size_t i = 0; i < counts.size(); ++i) gl[i] = a += counts[i];
+  return gl;
+}
+
+static int expect_rc(int rc, int want, const char* what) {
+  if (rc != want) CHECK_FAIL("%s returned %d (expected %d)", what, rc, want);
+  return rc;
+}
+
+static void gemm_bf16(std::vector<int> counts, int K, int N, int layout) {
+  const int G = (int)counts.size();
+  const auto glv = cumsum(counts);
+  const int64_t rows = glv.back();
+  uint8_t* x = mk("x", (size_t)rows * K * 2);
+  uint8_t* w = mk("w", (size_t)G * K * N * 2);
+  uint8_t* out = mk("out", (size_t)rows * N * 2);
+  int64_t* gl = (int64_t*)mk("group_list", G * 8);
+  memcpy(gl, glv.data(), G * 8);
+  const size_t wsz = mi355moe_grouped_gemm_workspace_size(G);
+  uint8_t* ws = mk("workspace", wsz);
+  g_expect = Expect();
+  g_expect.set = true;
+  g_expect.A = x;
+  g_expect.a_row_bytes = (int64_t)K * 2;
+  g_expect.B = w;
+  expect_rc(mi355moe_grouped_gemm_bf16((const uint16_t*)x, rows, K, (const uint16_t*)w, layout, G, N, gl,
+                                       (uint16_t*)out, ws, wsz, nullptr),
+            0, "grouped_gemm_bf16");
+  g_expect = Expect();
+}
+
+static void gemm_mx(std::vector<int> counts, int K, int N, int layout) {
+  const int G = (int)counts.size();
+  const auto glv = cumsum(counts);
+  const int64_t rows = glv.back();
+  uint8_t* xq = mk("xq", (size_t)rows * K);
+  uint8_t* xs = mk("x_scale", (size_t)rows * (K / 32));
+  uint8_t* wd = mk("w_data", (size_t)G * K * N);
+  const bool eoi = layout == MI355MOE_LAYOUT_EOI;
+  const int64_t sld = mi355moe_mx_weight_scale_ld(K);
+  uint8_t* wsc = eoi ? mk("w_scale_eoi", (size_t)G * N * sld) : mk("col_scale", (size_t)G * (K / 64) * N * 2);
+  uint8_t* out = mk("out", (size_t)rows * N * 2);
+  int64_t* gl = (int64_t*)mk("group_list", G * 8);
+  memcpy(gl, glv.data(), G * 8);
+  const size_t wsz = mi355moe_grouped_gemm_workspace_size(G);
+  uint8_t* ws = mk("workspace", wsz);
+  g_expect = Expect();
+  g_expect.set = true;
+  g_expect.A = xq;
+  g_expect.a_row_bytes = K;
+  g_expect.a_scale = xs;
+  g_expect.a_scale_ld = K / 32;
+  g_expect.B = wd;
+  g_expect.b_scale = wsc;
+  g_expect.b_scale_ld = sld;
+  expect_rc(mi355moe_grouped_gemm_mxfp8(xq, xs, rows, K, wd, wsc, layout, G, N, gl, (uint16_t*)out, ws, wsz, nullptr),
+            0, "grouped_gemm_mxfp8");
+  g_expect = Expect();
+}
+
+// Routed ids for T tokens: distinct experts per token, drawn from a skewed popularity.
+static std::vector<int64_t> route_ids(int64_t T, int K, int E, double skew) {
+  std::vector<double> wgt(E);
+  for (int e = 0; e < E; ++e) wgt[e] = 1.0 / std::pow(1.0 + e, skew);
+  std::vector<int> perm(E);
+  for (int e = 0; e < E; ++e) perm[e] = e;
+  std::shuffle(perm.begin(), perm.end(), g_rng);
+  std::vector<int64_t> ids((size_t)T * K);
+  for (int64_t t = 0; t < T; ++t) {
+    std::vector<double> w = wgt;
+    for (int k = 0; k < K; ++k) {
+      std::discrete_distribution<int> d(w.begin(), w.end());
+      const int e = d(g_rng);
+      w[e] = 0.0;
+      ids[(size_t)t * K + k] = perm[e];
+    }
+  }
+  return ids;
+}
+
+static void moe_forward(int64_t T, int K, int E, int H, int I, int precision, int layout, double skew,
+                        int numerics = 0, float limit = 0.0f) {
+  const bool mx = precision == MI355MOE_PRECISION_MXFP8;
+  const bool eoi = layout == MI355MOE_LAYOUT_EOI;
+  const auto idv = route_ids(T, K, E, skew);
+  uint8_t* hidden = mk("hidden", (size_t)T * H * 2);
+  int64_t* ids = (int64_t*)mk("topk_ids", idv.size() * 8);
+  memcpy(ids, idv.data(), idv.size() * 8);
+  float* wts = (float*)mk("topk_weights", (size_t)T * K * 4, 0);
+  const int esz = mx ? 1 : 2;
+  uint8_t* w1 = mk("w1", (size_t)E * H * 2 * I * esz);
+  uint8_t* w2 = mk("w2", (size_t)E * I * H * esz);
+  uint8_t *s1 = nullptr, *s2 = nullptr;
+  if (mx) {
+    if (eoi) {
+      s1 = mk("w1_scale_eoi", (size_t)E * 2 * I * mi355moe_mx_weight_scale_ld(H));
+      s2 = mk("w2_scale_eoi", (size_t)E * H * mi355moe_mx_weight_scale_ld(I));
+    } else {
+      s1 = mk("w1_col_scale", (size_t)E * (H / 64) * 2 * I * 2);
+      s2 = mk("w2_col_scale", (size_t)E * (I / 64) * H * 2);
+    }
+  }
+  uint8_t* out = mk("out", (size_t)T * H * 2);
+  MI355MoeForwardArgs a = {};
+  a.hidden = (const uint16_t*)hidden;
+  a.num_tokens = T;
+  a.hidden_size = H;
+  a.intermediate_size = I;
+  a.num_experts = E;
+  a.top_k = K;
+  a.topk_ids = ids;
+  a.ids_dtype = MI355MOE_IDS_INT64;
+  a.precision = precision;
+  a.topk_weights = wts;
+  a.weight_layout = layout;
+  a.numerics_flags = numerics;
+  a.swiglu_limit = limit;
+  a.w1 = w1;
+  a.w2 = w2;
+  a.w1_scale = s1;
+  a.w2_scale = s2;
+  a.out = (uint16_t*)out;
+  const size_t wsz = mi355moe_moe_forward_workspace_size(&a);
+  uint8_t* ws = mk("workspace", wsz);
+  g_expect = Expect();  // internal operands: addressing from GGParams, bounds from the allocations
+  expect_rc(mi355moe_moe_forward(&a, ws, wsz, nullptr), 0, "moe_forward");
+}
+
+static void moe_backward(int64_t T, int K, int E, int H, int I, int layout, int grad_dtype, double skew) {
+  const auto idv = route_ids(T, K, E, skew);
+  uint8_t* hidden = mk("hidden", (size_t)T * H * 2);
+  int64_t* ids = (int64_t*)mk("topk_ids", idv.size() * 8);
+  memcpy(ids, idv.data(), idv.size() * 8);
+  float* wts = (float*)mk("topk_weights", (size_t)T * K * 4, 0);
+  uint8_t* w1 = mk("w1", (size_t)E * H * 2 * I * 2);
+  uint8_t* w2 = mk("w2", (size_t)E * I * H * 2);
+  uint8_t* gout = mk("grad_out", (size_t)T * H * 2);
+  uint8_t* gh = mk("grad_hidden", (size_t)T * H * 2);
+  const int gsz = grad_dtype == MI355MOE_GRAD_FP32 ? 4 : 2;
+  uint8_t* gw1 = mk("grad_w1", (size_t)E * H * 2 * I * gsz);
+  uint8_t* gw2 = mk("grad_w2", (size_t)E * I * H * gsz);
+  float* gp = (float*)mk("grad_topk_weights", (size_t)T * K * 4);
+  MI355MoeBackwardArgs a = {};
+  a.hidden = (const uint16_t*)hidden;
+  a.num_tokens = T;
+  a.hidden_size = H;
+  a.intermediate_size = I;
+  a.num_experts = E;
+  a.top_k = K;
+  a.topk_ids = ids;
+  a.ids_dtype = MI355MOE_IDS_INT64;
+  a.weight_layout = layout;
+  a.topk_weights = wts;
+  a.w1 = (const uint16_t*)w1;
+  a.w2 = (const uint16_t*)w2;
+  a.grad_out = (const uint16_t*)gout;
+  a.grad_hidden = (uint16_t*)gh;
+  a.grad_w1 = gw1;
+  a.grad_w2 = gw2;
+  a.grad_topk_weights = gp;
+  a.weight_grad_dtype = grad_dtype;
+  const size_t wsz = mi355moe_moe_backward_workspace_size(&a);
+  uint8_t* ws = mk("workspace", wsz);
+  g_expect = Expect();
+  expect_rc(mi355moe_moe_backward(&a, ws, wsz, nullptr), 0, "moe_backward");
+}
+
+struct Scenario {
+  const char* name;
+  std::function<void()> run;
+};
+
+static std::vector<Scenario> scenarios() {
+  const int L_EIO = MI355MOE_LAYOUT_EIO, L_EOI = MI355MOE_LAYOUT_EOI;
+  const int BF = MI355MOE_PRECISION_BF16, MX = MI355MOE_PRECISION_MXFP8;
+  std::vector<Scenario> s;
+  // grouped GEMM C-ABI: ragged and empty groups, partial tiles, N not a multiple of the tile
+  s.push_back({"gemm_bf16_eio", [=] { gemm_bf16({100, 0, 300, 1, 129}, 1024, 768, L_EIO); }});
+  s.push_back({"gemm_bf16_eoi", [=] { gemm_bf16({100, 0, 300, 1, 129}, 1024, 768, L_EOI); }});
+  s.push_back({"gemm_bf16_eio_narrow", [=] { gemm_bf16({3, 40, 0, 513}, 128, 200, L_EIO); }});
+  s.push_back({"gemm_bf16_eoi_narrow", [=] { gemm_bf16({3, 40, 0, 513}, 128, 200, L_EOI); }});
+  s.push_back({"gemm_mx_eio", [=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EIO); }});
+  s.push_back({"gemm_mx_eoi", [=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EOI); }});
+  s.push_back({"gemm_mx_eoi_long_k", [=] { gemm_mx({256, 256}, 2560, 272, L_EOI); }});
+  s.push_back({"gemm_mx_eio_long_k", [=] { gemm_mx({256, 256}, 2560, 272, L_EIO); }});
+  // decode-shaped groups (the 64-row tiles): at most 32 rows per group on average
+  s.push_back({"gemm_bf16_eio_decode", [=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 512, 1024, L_EIO); }});
+  s.push_back({"gemm_bf16_eoi_decode", [=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 512, 1024, L_EOI); }});
+  s.push_back({"gemm_mx_eio_decode", [=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 512, L_EIO); }});
+  s.push_back({"gemm_mx_eoi_decode", [=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 512, L_EOI); }});
+  // many groups: the tile prefix comes from global memory past the LDS copy
+  s.push_back({"gemm_bf16_many_groups", [=] {
+                 std::vector<int> c(1100, 0);
+                 for (size_t i = 0; i < c.size(); i += 3) c[i] = 1 + (int)(i % 7);
+                 gemm_bf16(c, 64, 256, L_EIO);
+               }});
+  // MegaMoE forward, bf16 and MX, both layouts; prefill-like and decode-like routing
+  s.push_back({"moe_bf16_eio", [=] { moe_forward(96, 4, 16, 512, 256, BF, L_EIO, 1.1); }});
+  s.push_back({"moe_bf16_eoi", [=] { moe_forward(96, 4, 16, 512, 256, BF, L_EOI, 1.1); }});
+  s.push_back({"moe_bf16_eio_prefill", [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); }});
+  s.push_back({"moe_mx_eio", [=] { moe_forward(96, 4, 16, 512, 256, MX, L_EIO, 1.1); }});
+  s.push_back({"moe_mx_eoi", [=] { moe_forward(96, 4, 16, 512, 256, MX, L_EOI, 1.1); }});
+  s.push_back({"moe_mx_eoi_prefill", [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EOI, 0.0); }});
+  s.push_back({"moe_mx_eio_prefill", [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); }});
+  s.push_back({"moe_bf16_numerics_clamp", [=] { moe_forward(96, 4, 16, 512, 256, BF, L_EIO, 1.1, 0, 7.0f); }});
+  s.push_back({"moe_bf16_numerics_after_silu",
+               [=] { moe_forward(96, 4, 16, 512, 256, BF, L_EOI, 1.1, MI355MOE_NUMERICS_CLAMP_AFTER_SILU, 7.0f); }});
+  s.push_back({"moe_bf16_probs_before_fc2",
+               [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0, MI355MOE_NUMERICS_PROBS_BEFORE_FC2); }});
+  // expert backward
+  s.push_back({"bwd_eio_f32", [=] { moe_backward(96, 4, 8, 256, 128, L_EIO, MI355MOE_GRAD_FP32, 1.1); }});
+  s.push_back({"bwd_eoi_bf16", [=] { moe_backward(96, 4, 8, 256, 128, L_EOI, MI355MOE_GRAD_BF16, 1.1); }});
+  s.push_back({"bwd_eio_bf16_prefill", [=] { moe_backward(300, 2, 3, 384, 256, L_EIO, MI355MOE_GRAD_BF16, 0.0); }});
+  return s;
+}
+
+int main(int argc, char** argv) {
+  const auto all = scenarios();
+  if (argc == 2 && std::string(argv[1]) == "--list") {
+    for (const auto& sc : all) printf("%s\n", sc.name);
+    return 0;
+  }
+  int ran = 0;
+  for (const auto& sc : all) {
+    bool pick = argc < 2;
+    for (int i = 1; i < argc; ++i) pick |= std::string(argv[i]) == sc.name;
+    if (!pick) continue;
+    g_scenario = sc.name;
+    const long e0 = g_errors, c0 = g_copies, i0 = g_items, m0 = g_gemms;
+    sc.run();
+    free_all();
+    printf("%-32s %s  gemms=%ld items=%ld copies=%ld\n", sc.name, g_errors == e0 ? "ok" : "FAILED", g_gemms - m0,
+           g_items - i0, g_copies - c0);
+    fflush(stdout);
+    ++ran;
+  }
+  if (ran == 0) {
+    fprintf(stderr, "no scenario matched\n");
+    return 2;
+  }
+  printf("%d scenarios, %ld errors\n", ran, g_errors);
+  return g_errors ? 1 : 0;
+}

@@ -1,0 +1,54 @@
+"""Host-side copy checker of the grouped GEMM (runs on the CPU).
+
+Builds tests/native/gemm_copy_check (the library's host code with every optional path switched
+on, linked with host versions of the GEMM launches that replay each kernel's copy schedule) and
+runs its scenarios: the grouped GEMM C-ABI (bf16 / MXFP8, EIO / EOI weights, decode-shaped groups,
+more groups than the LDS tile prefix holds), the MegaMoE forward (both precisions and layouts, the
+numerics options) and the expert backward. For every copy of every work item, wave and lane the
+checker verifies the global source (inside a live allocation and equal to the element the fragment
+reads expect), the LDS destination slot, the vmcnt waits and the ring-slot reuse; see the header of
+tests/native/gemm_copy_check.cpp.
+"""
+import shutil
+import subprocess
+
+import pytest
+
+from tests.native import build_check
+
+
+def _toolchain():
+    return shutil.which("objcopy") and shutil.which("nm") and (build_check._rocm() / "bin" / "hipcc").exists()
+
+
+@pytest.fixture(scope="module")
+def checker():
+    if not _toolchain():
+        pytest.skip("hipcc / binutils not available")
+    return build_check.build()
+
+
+SCENARIOS = [
+    "gemm_bf16_eio", "gemm_bf16_eoi", "gemm_bf16_eio_narrow", "gemm_bf16_eoi_narrow",
+    "gemm_mx_eio", "gemm_mx_eoi", "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k",
+    "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode", "gemm_mx_eio_decode", "gemm_mx_eoi_decode",
+    "gemm_bf16_many_groups",
+    "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi",
+    "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
+    "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2",
+    "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill",
+]
+
+
+def test_scenario_list_matches(checker):
+    """Every scenario the checker knows is run here (and no name here is unknown to it)."""
+    r = subprocess.run([str(checker), "--list"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.split() == SCENARIOS
+
+
+@pytest.mark.parametrize("name", SCENARIOS)
+def test_copy_schedule(checker, name):
+    r = subprocess.run([str(checker), name], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, f"{r.stdout}\n{r.stderr}"
+    assert f"{name}" in r.stdout and " ok " in r.stdout
