@@ -11,7 +11,7 @@ from ctypes import POINTER, Structure, c_float, c_int32, c_int64, c_size_t, c_ui
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmi355moe.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
@@ -21,6 +21,7 @@ FEATURE_MX_EOI = 1
 FEATURE_NUMERICS = 2
 FEATURE_DECODE_TILES = 4
 FEATURE_BACKWARD = 8
+FEATURE_ROUTE_GRAD = 16
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}
@@ -41,6 +42,15 @@ class RouteArgs(Structure):
         ("scores_out", c_void_p),
         ("num_tokens", c_int64), ("num_experts", c_int32), ("top_k", c_int32), ("scoring", c_int32),
         ("num_groups", c_int32), ("topk_groups", c_int32), ("routed_scaling_factor", c_float),
+    ]
+
+
+class RouteGradArgs(Structure):
+    _fields_ = [
+        ("logits", c_void_p), ("logits_row_stride", c_int64), ("scores", c_void_p), ("indices", c_void_p),
+        ("indices32", c_void_p), ("grad_weights", c_void_p), ("grad_logits", c_void_p), ("accumulate", c_int32),
+        ("scoring", c_int32), ("num_tokens", c_int64), ("num_experts", c_int32), ("top_k", c_int32),
+        ("routed_scaling_factor", c_float), ("reserved", c_int32),
     ]
 
 
@@ -84,6 +94,7 @@ _SIGNATURES = [
     ("mi355moe_gate_logits", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
                                        c_void_p, c_void_p, c_size_t, c_void_p]),
     ("mi355moe_gate_route", c_int32, [POINTER(RouteArgs), c_void_p]),
+    ("mi355moe_gate_route_grad", c_int32, [POINTER(RouteGradArgs), c_void_p]),
     ("mi355moe_dispatch_workspace_size", c_size_t, [c_int64, c_int32, c_int32]),
     ("mi355moe_dispatch", c_int32, [POINTER(DispatchArgs), c_void_p, c_size_t, c_void_p]),
     ("mi355moe_token_permute", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_int32,

@@ -1,0 +1,23 @@
+// Feature gates of the optional paths (reported by mi355moe_features).
+#pragma once
+
+// Optional paths, each switched off until its GPU parity tests have run (a switched-off path answers
+// MI355MOE_EUNSUPPORTED, or the forward keeps the default tiles). MI355_CHECK_ALL_PATHS is defined
+// only by the host-side copy checker under tests/native, which drives the host code of every path
+// (it never runs on a GPU).
+#ifdef MI355_CHECK_ALL_PATHS
+#define MI355_PATH_ON true
+#else
+#define MI355_PATH_ON false
+#endif
+// MX GEMM with K-contiguous (EOI) weights.
+inline bool mi355_mx_eoi_enabled() { return MI355_PATH_ON; }
+// BF16 numerics options (SwiGLU clamp, probabilities before FC2).
+inline bool mi355_numerics_options_enabled() { return MI355_PATH_ON; }
+// The 64-row tile configuration (two workgroups per CU) for grouped GEMMs whose groups average at
+// most 32 rows (decode).
+inline bool mi355_small_tiles_enabled() { return MI355_PATH_ON; }
+// Expert backward (bf16).
+inline bool mi355_backward_enabled() { return MI355_PATH_ON; }
+// MegaGate RouteGrad (gradient of the routing weights with respect to the logits).
+inline bool mi355_route_grad_enabled() { return MI355_PATH_ON; }

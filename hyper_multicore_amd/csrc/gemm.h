@@ -51,24 +51,7 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
 int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t stream);
 int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream, bool small = false);
 int mi355_gg_bm(bool small = false);
-// Optional paths, each switched off until its GPU parity tests have run (a switched-off path answers
-// MI355MOE_EUNSUPPORTED, or the forward keeps the default tiles). MI355_CHECK_ALL_PATHS is defined
-// only by the host-side copy checker under tests/native, which drives the host code of every path
-// (it never runs on a GPU).
-#ifdef MI355_CHECK_ALL_PATHS
-#define MI355_PATH_ON true
-#else
-#define MI355_PATH_ON false
-#endif
-// MX GEMM with K-contiguous (EOI) weights.
-inline bool mi355_mx_eoi_enabled() { return MI355_PATH_ON; }
-// BF16 numerics options (SwiGLU clamp, probabilities before FC2).
-inline bool mi355_numerics_options_enabled() { return MI355_PATH_ON; }
-// The 64-row tile configuration (two workgroups per CU) for grouped GEMMs whose groups average at
-// most 32 rows (decode).
-inline bool mi355_small_tiles_enabled() { return MI355_PATH_ON; }
-// Expert backward (bf16).
-inline bool mi355_backward_enabled() { return MI355_PATH_ON; }
+#include "features.h"
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {
   return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;
 }

@@ -12,6 +12,7 @@
 #pragma clang fp contract(off)
 #include "common.h"
 #include "detmath.h"
+#include "features.h"
 #include "../../include/mi355moe.h"
 
 #define ROUTER_MAX_SLOTS 16  // E <= 1024
@@ -203,5 +204,99 @@ extern "C" int mi355moe_gate_route(const MI355MoeRouteArgs* args, void* stream_)
   if (a.num_tokens == 0) return MI355MOE_OK;
   dim3 grid((unsigned)((a.num_tokens + 3) / 4));
   hipLaunchKernelGGL(mi355_route_kernel, grid, dim3(256), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+// ---------------------------------------------------------------------------------------------
+// RouteGrad: one wavefront per token row, lane k < K owns selected slot k, expert e lives in lane
+// e % 64, slot e / 64 (as in the forward). The operation order is the torch-autograd order of the
+// routing-weight expression that the reference's RouteGrad pipeline reproduces
+// (ops/hyper_mega_gate_grad/op_kernel/route_grad_pipeline.h:138-189: Muls, the div backward cross
+// term -k0 * ((sel / D) / D), ReduceSum over K, the direct term k0 / D, Add; then
+// op_api/hyper_mega_gate_route_grad_post.cpp: ScatterElementsV2 add into zeros, Muls 2, RealDiv,
+// SoftplusV2Grad(beta 1, threshold 20)); the K sums run in ascending k.
+__global__ __launch_bounds__(256) void mi355_route_grad_kernel(MI355MoeRouteGradArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= a.num_tokens) return;
+  const int E = a.num_experts, K = a.top_k;
+  const float* srow = a.scores + t * (int64_t)E;
+  const float* lrow = a.logits + t * a.logits_row_stride;
+  float* orow = a.grad_logits + t * (int64_t)E;
+  // selected slot k = lane
+  int id = -1;
+  float gw = 0.0f, sel = 0.0f;
+  if (lane < K) {
+    const int64_t v = a.indices != nullptr ? a.indices[t * K + lane] : (int64_t)a.indices32[t * K + lane];
+    if (v >= 0 && v < E) {
+      id = (int)v;
+      sel = srow[id];
+    }
+    gw = a.grad_weights[t * K + lane];
+  }
+  const float scale = a.routed_scaling_factor;
+  float g;
+  if (K == 1) {
+    g = gw * scale;
+  } else {
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum = sum + __shfl(sel, k, 64);
+    const float D = sum + 1.0e-20f;
+    const float k0 = gw * scale;
+    const float cross = (-k0) * ((sel / D) / D);
+    float row = 0.0f;
+    for (int k = 0; k < K; ++k) row = row + __shfl(cross, k, 64);
+    g = k0 / D + row;
+  }
+  float dot = 0.0f;
+  if (a.scoring == MI355MOE_SCORE_SOFTMAX)
+    for (int k = 0; k < K; ++k) dot = dot + __shfl(g, k, 64) * __shfl(sel, k, 64);
+  const int slots = (E + 63) >> 6;
+  for (int j = 0; j < slots; ++j) {
+    const int e = j * 64 + lane;
+    // scatter-add of the selected-score gradients into zeros
+    float sg = 0.0f;
+    for (int k = 0; k < K; ++k) {
+      const int ik = __shfl(id, k, 64);
+      const float gk = __shfl(g, k, 64);
+      if (ik == e) sg = sg + gk;
+    }
+    if (e >= E) continue;
+    const float s = srow[e];
+    float r;
+    if (a.scoring == MI355MOE_SCORE_SQRTSOFTPLUS) {
+      const float q = sg / (2.0f * s);
+      const float l = lrow[e];
+      if (l > 20.0f) {
+        r = q;
+      } else {
+        const float z = det_expf(l);
+        r = (q * z) / (z + 1.0f);
+      }
+    } else if (a.scoring == MI355MOE_SCORE_SIGMOID) {
+      r = (sg * (1.0f - s)) * s;
+    } else {
+      r = s * (sg - dot);
+    }
+    orow[e] = a.accumulate ? orow[e] + r : r;
+  }
+}
+
+extern "C" int mi355moe_gate_route_grad(const MI355MoeRouteGradArgs* args, void* stream_) {
+  if (args == nullptr) return MI355MOE_EINVAL;
+  const MI355MoeRouteGradArgs& a = *args;
+  if (a.num_tokens < 0 || a.num_experts <= 0 || a.num_experts > 64 * ROUTER_MAX_SLOTS) return MI355MOE_EINVAL;
+  if (a.top_k <= 0 || a.top_k > a.num_experts || a.top_k > 64) return MI355MOE_EINVAL;
+  if (a.scoring != MI355MOE_SCORE_SOFTMAX && a.scoring != MI355MOE_SCORE_SIGMOID &&
+      a.scoring != MI355MOE_SCORE_SQRTSOFTPLUS)
+    return MI355MOE_EINVAL;
+  if (a.scores == nullptr || a.grad_weights == nullptr || a.grad_logits == nullptr) return MI355MOE_EINVAL;
+  if (a.indices == nullptr && a.indices32 == nullptr) return MI355MOE_EINVAL;
+  if (a.scoring == MI355MOE_SCORE_SQRTSOFTPLUS && (a.logits == nullptr || a.logits_row_stride < a.num_experts))
+    return MI355MOE_EINVAL;
+  if (!mi355_route_grad_enabled()) return MI355MOE_EUNSUPPORTED;
+  if (a.num_tokens == 0) return MI355MOE_OK;
+  hipLaunchKernelGGL(mi355_route_grad_kernel, dim3((unsigned)((a.num_tokens + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream_, a);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }

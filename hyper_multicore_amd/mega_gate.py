@@ -10,6 +10,13 @@ its torch path, module.py:266-271). Extensions over the reference, all off by de
 ``num_expert_groups`` / ``topk_groups`` select the DeepSeek-V3 group-limited top-k, and
 ``vision_router=True`` adds a separate projection ``weight_vl [E, H]`` used for tokens whose
 ``image_mask`` is set.
+
+Training: when the library reports RouteGrad on (``ops.features()``), outputs computed with grad
+enabled carry an autograd function (the reference's ``_MegaGateRouteFunction`` plus the projection's
+autograd, modules/mega_gate/function.py:96-207): the routing-weight gradient reaches the fp32 logits
+through the RouteGrad kernel (added to the gradient of the returned logits), and the projection
+backward ``dX = dL @ W``, ``dW = dL^T @ X`` runs as fp32 GEMMs, per modality. The ranking biases get
+no gradient. Otherwise the outputs are forward-only.
 """
 from __future__ import annotations
 
@@ -18,8 +25,9 @@ from collections.abc import Callable
 from typing import Any
 
 import torch
+from torch.autograd.function import once_differentiable
 
-from . import ops
+from . import _lib, ops
 
 __all__ = ["MegaGate"]
 
@@ -36,6 +44,57 @@ def _keep_fp32(module: torch.nn.Module, fn: Callable, names: tuple[str, ...]) ->
         return out
 
     return apply
+
+
+class _MegaGateFunction(torch.autograd.Function):  # pylint: disable=abstract-method,arguments-differ
+    """Projection + route with the RouteGrad backward (modules/mega_gate/function.py:96-160)."""
+
+    @staticmethod
+    def forward(ctx, flat, weight, weight_vl, mask, bias, bias_vl, cfg):
+        ctx.set_materialize_grads(False)
+        logits = ops.gate_logits(flat, weight, weight_vl, mask if weight_vl is not None else None)
+        weights, indices, scores = ops.gate_route(
+            logits, bias, top_k=cfg["top_k"], scoring_func=cfg["scoring_func"],
+            routed_scaling_factor=cfg["routed_scaling_factor"], bias_vl=bias_vl,
+            image_mask=mask if bias_vl is not None else None, num_groups=cfg["num_groups"],
+            topk_groups=cfg["topk_groups"], return_scores=True)
+        ctx.save_for_backward(flat, weight, weight_vl, mask, logits, scores, indices)
+        ctx.cfg = cfg
+        ctx.mark_non_differentiable(indices)
+        return logits, weights, indices
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_logits, grad_weights, _grad_indices):
+        flat, weight, weight_vl, mask, logits, scores, indices = ctx.saved_tensors
+        cfg = ctx.cfg
+        grad = None
+        if grad_logits is not None:
+            grad = grad_logits.to(torch.float32).contiguous().clone()
+        if grad_weights is not None:
+            grad = ops.gate_route_grad(logits, scores, indices, grad_weights, top_k=cfg["top_k"],
+                                       scoring_func=cfg["scoring_func"],
+                                       routed_scaling_factor=cfg["routed_scaling_factor"], grad_logits=grad)
+        if grad is None:
+            return None, None, None, None, None, None, None
+        need_x, need_w, need_wvl = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        # logits = X.float() @ W.float()^T per modality (function.py:176-178)
+        rows = [(None, weight, need_w)] if weight_vl is None else [(~mask, weight, need_w), (mask, weight_vl, need_wvl)]
+        dx = torch.empty(flat.shape, dtype=torch.float32, device=flat.device) if need_x else None
+        dws = []
+        for sel, w, need in rows:
+            g = grad if sel is None else grad[sel]
+            x = flat if sel is None else flat[sel]
+            if need_x:
+                part = g @ w.to(torch.float32)
+                if sel is None:
+                    dx = part
+                else:
+                    dx[sel] = part
+            dws.append((g.t() @ x.to(torch.float32)).to(w.dtype) if need else None)
+        dw = dws[0]
+        dwvl = dws[1] if len(dws) > 1 else None
+        return (dx.to(flat.dtype) if dx is not None else None), dw, dwvl, None, None, None, None
 
 
 class MegaGate(torch.nn.Module):
@@ -155,8 +214,17 @@ class MegaGate(torch.nn.Module):
             return (torch.empty((0, E), dtype=torch.float32, device=dev),
                     torch.empty((0, K), dtype=torch.float32, device=dev),
                     torch.empty((0, K), dtype=torch.int64, device=dev))
-        logits = ops.gate_logits(flat, weight, weight_vl, mask if weight_vl is not None else None)
         use_vl = mask is not None and self.bias_vl is not None
+        wants_grad = torch.is_grad_enabled() and (
+            flat.requires_grad or weight.requires_grad or (weight_vl is not None and weight_vl.requires_grad))
+        if wants_grad and ops.features() & _lib.FEATURE_ROUTE_GRAD:
+            cfg = {"top_k": self.top_k, "scoring_func": self.scoring_func,
+                   "routed_scaling_factor": self.routed_scaling_factor, "num_groups": self.num_expert_groups,
+                   "topk_groups": self.topk_groups}
+            return _MegaGateFunction.apply(
+                flat, weight, weight_vl, mask, self.bias.detach().to(torch.float32),
+                self.bias_vl.detach().to(torch.float32) if use_vl else None, cfg)
+        logits = ops.gate_logits(flat, weight, weight_vl, mask if weight_vl is not None else None)
         weights, indices = ops.gate_route(
             logits, self.bias.detach().to(torch.float32), top_k=self.top_k, scoring_func=self.scoring_func,
             routed_scaling_factor=self.routed_scaling_factor,

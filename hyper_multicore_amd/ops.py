@@ -127,6 +127,50 @@ def gate_route(logits: torch.Tensor, bias: torch.Tensor, *, top_k: int, scoring_
     return (weights, indices, scores) if return_scores else (weights, indices)
 
 
+def gate_route_grad(logits: torch.Tensor, scores: torch.Tensor, indices: torch.Tensor, grad_weights: torch.Tensor, *,
+                    top_k: int, scoring_func: str, routed_scaling_factor: float,
+                    grad_logits: torch.Tensor | None = None) -> torch.Tensor:
+    """Gradient of the routing weights w.r.t. the fp32 logits (RouteGrad), fp32 [T, E].
+
+    Mirrors hyper_multicore::mega_gate_route_grad (torch/csrc/mega_gate.cpp:182-197) for the three
+    scoring functions; ``scores`` are the forward's unbiased scores (``gate_route(...,
+    return_scores=True)``). When ``grad_logits`` is given the route gradient is added to it in place
+    (the gradient the logits output already carries) and it is returned.
+    """
+    lib = _lib.load()
+    device = _require_gpu(logits, scores, indices, grad_weights, grad_logits)
+    if logits.dtype != torch.float32 or logits.ndim != 2 or logits.stride(1) != 1:
+        raise TypeError("logits must be fp32 [tokens, experts] with contiguous rows")
+    T, E = logits.shape
+    if scores.dtype != torch.float32 or scores.shape != (T, E) or not scores.is_contiguous():
+        raise ValueError("scores must be contiguous fp32 [tokens, experts]")
+    if indices.shape != (T, top_k) or indices.dtype not in (torch.int64, torch.int32):
+        raise ValueError("indices must be int32/int64 [tokens, top_k]")
+    if grad_weights.shape != (T, top_k):
+        raise ValueError("grad_weights must be [tokens, top_k]")
+    if scoring_func not in _lib.SCORE:
+        raise ValueError(f"unsupported scoring_func: {scoring_func!r}")
+    indices = indices.contiguous()
+    grad_weights = grad_weights.to(torch.float32).contiguous()
+    accumulate = grad_logits is not None
+    if accumulate:
+        if grad_logits.dtype != torch.float32 or grad_logits.shape != (T, E) or not grad_logits.is_contiguous():
+            raise ValueError("grad_logits must be contiguous fp32 [tokens, experts]")
+        out = grad_logits
+    else:
+        out = torch.empty((T, E), dtype=torch.float32, device=device)
+    i64 = indices.dtype == torch.int64
+    args = _lib.RouteGradArgs(
+        logits=_ptr(logits), logits_row_stride=logits.stride(0), scores=_ptr(scores),
+        indices=_ptr(indices) if i64 else None, indices32=None if i64 else _ptr(indices),
+        grad_weights=_ptr(grad_weights), grad_logits=_ptr(out), accumulate=int(accumulate),
+        scoring=_lib.SCORE[scoring_func], num_tokens=T, num_experts=E, top_k=top_k,
+        routed_scaling_factor=float(routed_scaling_factor), reserved=0)
+    rc = lib.mi355moe_gate_route_grad(ctypes.byref(args), _stream(device))
+    _lib.check(rc, "mi355moe_gate_route_grad")
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
 # Dispatch / permute / combine
 # ------------------------------------------------------------------------------------------------

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MI355MOE_ABI_VERSION 2
+#define MI355MOE_ABI_VERSION 3
 
 enum {
   MI355MOE_OK_CODE = 0,
@@ -53,6 +53,7 @@ enum {
   MI355MOE_FEATURE_NUMERICS = 2,      /* BF16 SwiGLU clamp / probabilities before FC2 */
   MI355MOE_FEATURE_DECODE_TILES = 4,  /* 64-row tiles for groups averaging <= 32 rows */
   MI355MOE_FEATURE_BACKWARD = 8,      /* mi355moe_moe_backward */
+  MI355MOE_FEATURE_ROUTE_GRAD = 16,   /* mi355moe_gate_route_grad */
 };
 int mi355moe_features(void);
 
@@ -100,6 +101,45 @@ typedef struct MI355MoeRouteArgs {
   float routed_scaling_factor;
 } MI355MoeRouteArgs;
 int mi355moe_gate_route(const MI355MoeRouteArgs* args, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * RouteGrad: the gradient of the routing weights of mi355moe_gate_route with respect to the fp32
+ * logits, for the selected experts `indices` and upstream grad_weights [T, K]:
+ *   g_k  = K == 1 ? gw_k * scale : k0_k / D + sum_j -k0_j * ((sel_j / D) / D),  k0 = gw * scale,
+ *          sel = scores[idx], D = sum_k sel_k + 1e-20   (sums in ascending k)
+ *   sg_e = g_k where e = idx_k, else 0
+ *   sqrt-softplus: grad = l > 20 ? q : (q * exp(l)) / (exp(l) + 1),  q = sg / (2 * score)
+ *   sigmoid:       grad = (sg * (1 - score)) * score
+ *   softmax:       grad = score * (sg - sum_k g_k * sel_k)
+ * scores are the forward's unbiased scores (scores_out of mi355moe_gate_route); the group-limited
+ * selection and the correction biases do not enter the gradient. With accumulate != 0 the result
+ * is added to grad_logits (a gradient already held for the logits output), else it overwrites it.
+ * An expert whose score is 0 (sqrt-softplus with softplus(l) == 0) gets 0 / 0 = NaN, as in the
+ * reference's RealDiv. Ids outside [0, E) select nothing.
+ * Replaces hyper_multicore::mega_gate_route_grad -> aclnnHyperMegaGateRouteGrad
+ * (torch/csrc/mega_gate.cpp:182-197, ops/hyper_mega_gate_grad/op_host/op_api/
+ * hyper_mega_gate_route_grad.cpp:94-120, op_kernel/route_grad_pipeline.h:138-189), which takes the
+ * selected scores and the denominator as inputs; here they are recomputed from scores and indices
+ * with the forward's summation order. The sigmoid / softmax forms are torch autograd of
+ * MegaGate._torch_forward (modules/mega_gate/module.py:199-227), the reference's path for those.
+ */
+typedef struct MI355MoeRouteGradArgs {
+  const float* logits;        /* [T, E] fp32, row stride logits_row_stride (read for sqrt-softplus) */
+  int64_t logits_row_stride;
+  const float* scores;        /* [T, E] fp32 forward scores, row stride E */
+  const int64_t* indices;     /* [T, K] int64 expert ids (or NULL with indices32) */
+  const int32_t* indices32;   /* [T, K] int32 expert ids or NULL */
+  const float* grad_weights;  /* [T, K] fp32 */
+  float* grad_logits;         /* [T, E] fp32 out, row stride E */
+  int32_t accumulate;
+  int32_t scoring;            /* MI355MOE_SCORE_* */
+  int64_t num_tokens;
+  int32_t num_experts;        /* <= 1024 */
+  int32_t top_k;              /* <= min(E, 64) */
+  float routed_scaling_factor;
+  int32_t reserved;
+} MI355MoeRouteGradArgs;
+int mi355moe_gate_route_grad(const MI355MoeRouteGradArgs* args, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Dispatch metadata: per-expert histogram (LDS atomics), exclusive scan and the stable

@@ -22,7 +22,8 @@ def build() -> Path:
 
 
 def load() -> ctypes.CDLL:
-    if not LIB.exists():
+    src = ORACLE_DIR / "router_ref.c"
+    if not LIB.exists() or LIB.stat().st_mtime < src.stat().st_mtime:
         build()
     lib = ctypes.CDLL(str(LIB))
     lib.oracle_det_expf.restype = ctypes.c_float
@@ -33,6 +34,9 @@ def load() -> ctypes.CDLL:
     lib.oracle_route.restype = ctypes.c_int
     lib.oracle_route.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_int,
                                  ctypes.c_int, ctypes.c_int, ctypes.c_float, vp, vp, vp]
+    lib.oracle_route_grad.restype = ctypes.c_int
+    lib.oracle_route_grad.argtypes = [vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_float, ctypes.c_int, vp]
     return lib
 
 

@@ -67,6 +67,51 @@ def route_c(logits: np.ndarray, bias: np.ndarray, *, top_k: int, scoring_func: s
     return weights, indices, scores
 
 
+def route_grad_c(logits: np.ndarray, scores: np.ndarray, indices: np.ndarray, grad_weights: np.ndarray, *,
+                 top_k: int, scoring_func: str, routed_scaling_factor: float,
+                 accumulate_into: np.ndarray | None = None) -> np.ndarray:
+    """C oracle of RouteGrad (router_ref.c: oracle_route_grad): d(routing weights)/d(logits) applied to
+    grad_weights [T,K], as fp32 [T,E] (added to ``accumulate_into`` when given).
+
+    Restates route_grad_pipeline.h:138-189 and op_api/hyper_mega_gate_route_grad.cpp:109-120 (the
+    torch-autograd operation order of module.py:199-227) for sqrt-softplus, and torch autograd of the
+    sigmoid / softmax scores.
+    """
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    indices = np.ascontiguousarray(indices, dtype=np.int64)
+    grad_weights = np.ascontiguousarray(grad_weights, dtype=np.float32)
+    if scores.shape != (T, E) or indices.shape != (T, top_k) or grad_weights.shape != (T, top_k):
+        raise ValueError("route_grad_c: shape mismatch")
+    out = (np.array(accumulate_into, dtype=np.float32, copy=True) if accumulate_into is not None
+           else np.zeros((T, E), np.float32))
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    rc = _router().oracle_route_grad(p(logits), p(scores), p(indices), p(grad_weights), T, E, top_k,
+                                     SCORING[scoring_func], ctypes.c_float(routed_scaling_factor),
+                                     1 if accumulate_into is not None else 0, p(out))
+    if rc != 0:
+        raise ValueError(f"oracle_route_grad rejected the arguments ({rc})")
+    return out
+
+
+def route_grad_torch(logits: torch.Tensor, indices: torch.Tensor, grad_weights: torch.Tensor, *,
+                     top_k: int, scoring_func: str, routed_scaling_factor: float) -> torch.Tensor:
+    """torch autograd of the routing weights w.r.t. fp32 logits (the expression of module.py:199-227 /
+    _test_mega_gate.py:752-777) for fixed indices."""
+    logits = logits.detach().float().clone().requires_grad_(True)
+    if scoring_func == "sqrtsoftplus":
+        scores = F.softplus(logits).sqrt()
+    elif scoring_func == "softmax":
+        scores = logits.softmax(dim=-1)
+    else:
+        scores = logits.sigmoid()
+    selected = scores.gather(1, indices)
+    weights = selected / (selected.sum(dim=-1, keepdim=True) + 1.0e-20) if top_k > 1 else selected
+    weights = weights * routed_scaling_factor
+    return torch.autograd.grad(weights, logits, grad_outputs=grad_weights.float())[0]
+
+
 def gate_logits_reference(x: torch.Tensor, weight: torch.Tensor, weight_vl: torch.Tensor | None = None,
                           image_mask: torch.Tensor | None = None) -> torch.Tensor:
     """F.linear(x.float(), W.float()) (module.py:195-198); per-modality weights select by mask."""

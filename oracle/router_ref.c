@@ -165,3 +165,75 @@ int oracle_route(const float* logits, int64_t T, int E, const float* bias, const
   free(taken);
   return 0;
 }
+
+/*
+ * Route backward with respect to the logits (RouteGrad), for the routing weights of oracle_route:
+ *   s = score(l);  sel = s[idx];  D = sum_k sel + 1e-20 (K > 1);  w = (K > 1 ? sel / D : sel) * scale
+ * in the operation order of torch autograd of that expression, which the reference's native
+ * RouteGrad reproduces for sqrt-softplus (route_grad_pipeline.h:138-189: k0 = gw * scale, the
+ * div backward cross term -k0 * ((sel / D) / D), a row sum, direct term k0 / D, their sum;
+ * op_api/hyper_mega_gate_route_grad.cpp:109-120 and hyper_mega_gate_route_grad_post.cpp:68-141:
+ * scatter-add into zeros, score * 2, RealDiv, SoftplusV2Grad with beta 1 and threshold 20):
+ *   g_k   = K == 1 ? gw_k * scale : k0_k / D + sum_j (-k0_j * ((sel_j / D) / D))   (sum ascending j)
+ *   sg_e  = 0 + g_k for e = idx_k, else 0
+ *   sqrt-softplus: q = sg / (2 s);  out = l > 20 ? q : (q * z) / (z + 1),  z = exp(l)
+ *   sigmoid:       out = (sg * (1 - s)) * s                     (torch sigmoid_backward)
+ *   softmax:       out = s * (sg - sum_e sg_e s_e)              (torch softmax_backward_data; the sum
+ *                                                                runs over the selected experts in
+ *                                                                ascending k, the other terms are 0)
+ * The softmax / sigmoid forms are torch autograd of MegaGate._torch_forward (module.py:199-227),
+ * the reference's path for those scores. exp is oracle_det_expf (the kernel's). When accumulate
+ * is nonzero the result is added to out (out = out + grad). Returns 0 on success.
+ */
+int oracle_route_grad(const float* logits, const float* scores, const int64_t* indices, const float* grad_w,
+                      int64_t T, int E, int K, int scoring, float scale, int accumulate, float* out) {
+  if (E <= 0 || K <= 0 || K > E || scoring < 0 || scoring > 2) return -1;
+  float* sg = (float*)malloc(sizeof(float) * (size_t)E);
+  float* g = (float*)malloc(sizeof(float) * (size_t)K);
+  if (!sg || !g) return -2;
+  for (int64_t t = 0; t < T; ++t) {
+    const float* l = logits + t * E;
+    const float* s = scores + t * E;
+    const int64_t* idx = indices + t * K;
+    const float* gw = grad_w + t * K;
+    if (K == 1) {
+      g[0] = gw[0] * scale;
+    } else {
+      float sum = 0.0f;
+      for (int k = 0; k < K; ++k) sum = sum + s[idx[k]];
+      const float D = sum + 1.0e-20f;
+      float row = 0.0f;
+      for (int k = 0; k < K; ++k) {
+        const float k0 = gw[k] * scale;
+        const float cross = (-k0) * ((s[idx[k]] / D) / D);
+        row = row + cross;
+      }
+      for (int k = 0; k < K; ++k) g[k] = (gw[k] * scale) / D + row;
+    }
+    for (int e = 0; e < E; ++e) sg[e] = 0.0f;
+    for (int k = 0; k < K; ++k) sg[idx[k]] = sg[idx[k]] + g[k];
+    float dot = 0.0f;
+    if (scoring == 0)
+      for (int k = 0; k < K; ++k) dot = dot + g[k] * s[idx[k]];
+    for (int e = 0; e < E; ++e) {
+      float r;
+      if (scoring == 2) {
+        const float q = sg[e] / (2.0f * s[e]);
+        if (l[e] > 20.0f) {
+          r = q;
+        } else {
+          const float z = oracle_det_expf(l[e]);
+          r = (q * z) / (z + 1.0f);
+        }
+      } else if (scoring == 1) {
+        r = (sg[e] * (1.0f - s[e])) * s[e];
+      } else {
+        r = s[e] * (sg[e] - dot);
+      }
+      out[t * E + e] = accumulate ? out[t * E + e] + r : r;
+    }
+  }
+  free(sg);
+  free(g);
+  return 0;
+}

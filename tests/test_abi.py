@@ -87,6 +87,26 @@ def test_backward_validation():
     assert lib.mi355moe_moe_backward_workspace_size(ctypes.byref(f)) == 0 or lib.mi355moe_features() & 8
 
 
+def test_route_grad_validation():
+    """RouteGrad rejects bad shapes / missing operands before any launch; with valid (dummy) pointers it
+    answers EUNSUPPORTED while the path is switched off."""
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    base = dict(logits=1, logits_row_stride=64, scores=1, indices=1, grad_weights=1, grad_logits=1, scoring=2,
+                num_tokens=16, num_experts=64, top_k=8, routed_scaling_factor=2.5)
+    for bad in ({"num_experts": 1025}, {"top_k": 65}, {"top_k": 0}, {"scoring": 3}, {"scores": None},
+                {"indices": None}, {"grad_weights": None}, {"grad_logits": None}, {"logits": None},
+                {"logits_row_stride": 32}, {"num_tokens": -1}):
+        a = _lib.RouteGradArgs(**{**base, **bad})
+        assert lib.mi355moe_gate_route_grad(ctypes.byref(a), None) == _lib.EINVAL, bad
+    # sigmoid / softmax gradients do not read the logits
+    # (never with the path on: the dummy pointers would reach a kernel)
+    if not lib.mi355moe_features() & _lib.FEATURE_ROUTE_GRAD:
+        a = _lib.RouteGradArgs(**{**base, "scoring": 1, "logits": None})
+        assert lib.mi355moe_gate_route_grad(ctypes.byref(a), None) == _lib.EUNSUPPORTED
+    assert lib.mi355moe_gate_route_grad(None, None) == _lib.EINVAL
+
+
 def test_workspace_sizes():
     from hyper_multicore_amd import _lib
     lib = _lib.load()

@@ -461,3 +461,137 @@ def test_backward_reference_layouts_and_scaling():
     c = orc.expert_backward_reference(x, ids, p, w1, w2, (dout.float() * 2).to(torch.bfloat16))
     for u, v in zip(a, c):
         assert torch.equal(v.float(), 2 * u.float())
+
+
+# ------------------------------------------------------------------------------------------------
+# RouteGrad (router_ref.c: oracle_route_grad)
+# ------------------------------------------------------------------------------------------------
+_SCALE = 2.5
+
+
+def _torch_scores(logits: torch.Tensor, scoring: str) -> torch.Tensor:
+    if scoring == "sqrtsoftplus":
+        return F.softplus(logits).sqrt()
+    return logits.sigmoid() if scoring == "sigmoid" else logits.softmax(dim=-1)
+
+
+def _route_grad_pair(logits, scoring, top_k, grad=None, seed=0):
+    """(oracle, torch autograd) on the same forward state (torch's scores and top-k indices)."""
+    scores = _torch_scores(logits, scoring)
+    indices = torch.topk(scores, top_k, dim=-1, sorted=False).indices
+    if grad is None:
+        g = torch.Generator().manual_seed(seed)
+        grad = torch.randn(indices.shape, generator=g)
+    ours = orc.route_grad_c(logits.numpy(), scores.numpy(), indices.numpy(), grad.numpy(), top_k=top_k,
+                            scoring_func=scoring, routed_scaling_factor=_SCALE)
+    ref = orc.route_grad_torch(logits, indices, grad, top_k=top_k, scoring_func=scoring,
+                               routed_scaling_factor=_SCALE)
+    return torch.from_numpy(ours), ref, scores, indices
+
+
+@pytest.mark.parametrize("scoring,top_k", [("sigmoid", 1), ("sigmoid", 2), ("softmax", 1)])
+def test_route_grad_operation_order_bit_exact(scoring, top_k):
+    """Where no exp and no reassociable sum enter (sigmoid K <= 2, softmax K = 1), the restated order
+    reproduces torch autograd bit for bit - the reference's own operation-order contract
+    (_test_mega_gate.py:752-777, rtol = atol = 0, upstream ((idx + 1) / E) / 2)."""
+    torch.manual_seed(2302)
+    logits = torch.randn(257, 33) * 3
+    scores = _torch_scores(logits, scoring)
+    idx = torch.topk(scores, top_k, dim=-1, sorted=False).indices
+    upstream = ((idx.float() + 1) / logits.shape[1]) / 2
+    ours, ref, _, _ = _route_grad_pair(logits, scoring, top_k, grad=upstream)
+    assert torch.equal(ours, ref)
+
+
+@pytest.mark.parametrize("top_k", [1, 2])
+def test_route_grad_sqrtsoftplus_exact_where_exp_is_exact(top_k):
+    """sqrt-softplus chain (scatter, * 2, RealDiv, SoftplusV2Grad threshold 20): with logits 0 (exp = 1)
+    or above the threshold (no exp) the restated order is bit-exact with torch autograd."""
+    g = torch.Generator().manual_seed(7)
+    logits = torch.where(torch.rand(129, 16, generator=g) < 0.5, torch.zeros(129, 16),
+                         20.0 + torch.rand(129, 16, generator=g) * 30)
+    ours, ref, _, _ = _route_grad_pair(logits, "sqrtsoftplus", top_k, seed=3)
+    assert torch.equal(ours, ref)
+
+
+@pytest.mark.parametrize("scoring", ["sqrtsoftplus", "sigmoid", "softmax"])
+@pytest.mark.parametrize("top_k", [1, 2, 3, 7, 8])
+def test_route_grad_matches_torch_autograd(scoring, top_k):
+    """General shapes at the reference's RouteGrad batch tolerance (_test_mega_gate.py:780-806:
+    rtol 1e-5, atol 1e-6); remaining differences are the K-sum order and exp's last bit."""
+    torch.manual_seed(2309 + top_k)
+    logits = torch.randn(300, 64) * 3
+    ours, ref, _, _ = _route_grad_pair(logits, scoring, top_k, seed=top_k)
+    torch.testing.assert_close(ours, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_route_grad_extremes_nan_inf_pattern():
+    """The reference's extreme logits (_test_mega_gate.py:809-858): softplus underflow and threshold
+    neighbours; NaN / Inf positions equal torch autograd's and finite values agree."""
+    logits = torch.tensor(((-120.0, -20.0, -1.0, 0.0, 19.999, 20.0, 20.001, 80.0),
+                           (-100.0, -2.0, -0.0, 0.5, 19.5, 20.0, 21.0, 60.0)))
+    grad = torch.tensor(((0.75, -1.25, 2.0), (-0.5, 1.5, -2.25)))
+    ours, ref, _, _ = _route_grad_pair(logits, "sqrtsoftplus", 3, grad=grad)
+    assert torch.equal(torch.isnan(ours), torch.isnan(ref))
+    assert torch.equal(torch.isinf(ours), torch.isinf(ref))
+    finite = torch.isfinite(ref)
+    torch.testing.assert_close(ours[finite], ref[finite], rtol=1e-5, atol=1e-6)
+
+
+def test_route_grad_invariants():
+    """Gradient only on the selected experts for sigmoid / sqrt-softplus; softmax rows sum to ~0;
+    accumulate adds exactly; K = 1 closed form for sqrt-softplus."""
+    torch.manual_seed(11)
+    logits = torch.randn(64, 32) * 2
+    for scoring in ("sigmoid", "sqrtsoftplus"):
+        ours, _, _, idx = _route_grad_pair(logits, scoring, 4, seed=5)
+        sel = torch.zeros_like(ours, dtype=torch.bool).scatter_(1, idx, True)
+        assert torch.all(ours[~sel] == 0)
+        assert torch.all(ours[sel] != 0)
+    ours, _, _, _ = _route_grad_pair(logits, "softmax", 4, seed=5)
+    assert float(ours.sum(dim=1).abs().max()) < 1e-6
+    scores = _torch_scores(logits, "sqrtsoftplus")
+    idx = torch.topk(scores, 1, dim=-1, sorted=False).indices
+    gw = torch.randn(64, 1, generator=torch.Generator().manual_seed(9))
+    base = torch.randn(64, 32, generator=torch.Generator().manual_seed(10))
+    plain = orc.route_grad_c(logits.numpy(), scores.numpy(), idx.numpy(), gw.numpy(), top_k=1,
+                             scoring_func="sqrtsoftplus", routed_scaling_factor=_SCALE)
+    acc = orc.route_grad_c(logits.numpy(), scores.numpy(), idx.numpy(), gw.numpy(), top_k=1,
+                           scoring_func="sqrtsoftplus", routed_scaling_factor=_SCALE,
+                           accumulate_into=base.numpy())
+    assert np.array_equal(acc, (base.numpy() + plain).astype(np.float32))
+    # K = 1: d/dl [scale * sqrt(softplus(l))] = scale * sigmoid(l) / (2 sqrt(softplus(l)))
+    l_sel = logits.gather(1, idx).double()
+    closed = gw.double() * _SCALE * torch.sigmoid(l_sel) / (2 * F.softplus(l_sel).sqrt())
+    torch.testing.assert_close(torch.from_numpy(plain).gather(1, idx).double(), closed, rtol=1e-6, atol=1e-7)
+
+
+def test_route_grad_sqrtsoftplus_softplus_grad_association():
+    """K = 1 sqrt-softplus on random logits: the SoftplusV2Grad step is (q * z) / (z + 1). Torch's own
+    exp inside softplus_backward is not reproducible here, so the pin is statistical: the restated
+    chain agrees bit for bit with torch autograd on >= 97% of the selected entries, while the other
+    association q * (z / (z + 1)) disagrees on a sizeable fraction."""
+    torch.manual_seed(77)
+    logits = torch.randn(2048, 8) * 4
+    ours, ref, scores, idx = _route_grad_pair(logits, "sqrtsoftplus", 1, seed=78)
+    a = ours.gather(1, idx).reshape(-1)
+    b = ref.gather(1, idx).reshape(-1)
+    agree = float((a == b).float().mean())
+    assert agree >= 0.97, agree
+    # the alternative association, computed from the same oracle pieces, is distinguishable
+    gw = torch.randn(idx.shape, generator=torch.Generator().manual_seed(78))
+    l_sel = logits.gather(1, idx).reshape(-1)
+    q = (gw.reshape(-1) * _SCALE) / (2.0 * scores.gather(1, idx).reshape(-1))
+    z = torch.tensor([orc.det_expf(float(v)) for v in l_sel])
+    alt = torch.where(l_sel > 20, q, q * (z / (z + 1)))
+    assert float((alt == b).float().mean()) < agree - 0.1
+
+
+def test_route_grad_denominator_epsilon():
+    """Scores near 1e-20 (sigmoid of logits near -46): the + 1e-20 of the denominator is visible, and
+    the restated order still equals torch autograd bit for bit (K = 2)."""
+    g = torch.Generator().manual_seed(21)
+    logits = -46.0 + torch.rand(64, 6, generator=g)
+    ours, ref, scores, _ = _route_grad_pair(logits, "sigmoid", 2, seed=22)
+    assert float(scores.max()) < 1e-19
+    assert torch.equal(ours, ref)
