@@ -47,6 +47,9 @@ struct Alloc {
 static std::vector<Alloc> g_allocs;
 static long g_errors = 0, g_copies = 0, g_items = 0, g_gemms = 0;
 static std::string g_scenario;
+// Use the 256-row tiles even where the library would pick the 64-row ones (the state of a build with
+// the decode tiles switched off): planning and launch both follow it.
+static bool g_force_big = false;
 
 #define CHECK_FAIL(...)                                         \
   do {                                                          \
@@ -126,6 +129,7 @@ hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
 // ------------------------------------------------------------------------------------------------
 // Host versions of the enqueue functions whose outputs the GEMM set-up reads
 int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t, bool small) {
+  if (g_force_big) small = false;
   const int bm = mi355_gg_bm(small);
   if (!find_alloc(tile_prefix, (size_t)(G + 1) * 4)) CHECK_FAIL("tile prefix of %d groups outside its buffer", G);
   int64_t acc = 0;
@@ -725,6 +729,7 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   // the dispatcher's choice of the numerics epilogue (gemm.hip, mi355_grouped_gemm)
   if (epi == EPI_SWIGLU_BF16_NUM) return MI355MOE_EINVAL;
   if (epi == EPI_SWIGLU_BF16 && (p.swiglu_limit > 0.0f || p.row_prob != nullptr)) epi = EPI_SWIGLU_BF16_NUM;
+  if (g_force_big) small = false;
   if (small) {
     if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
     return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
@@ -937,6 +942,26 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"gemm_bf16_eoi_decode", [=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 512, 1024, L_EOI); }});
   s.push_back({"gemm_mx_eio_decode", [=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 512, L_EIO); }});
   s.push_back({"gemm_mx_eoi_decode", [=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 512, L_EOI); }});
+  // the same decode shapes on the 256-row tiles (a build with the decode tiles off)
+  auto decode_counts = [](int G, unsigned seed) {
+    std::mt19937 r(seed);
+    std::vector<int> c(G);
+    for (auto& v : c) v = (int)(r() % 40);
+    for (int i = 0; i < G / 3; ++i) c[r() % G] = 0;
+    return c;
+  };
+  auto big = [](std::function<void()> f) {
+    return [f] {
+      g_force_big = true;
+      f();
+      g_force_big = false;
+    };
+  };
+  s.push_back({"gemm_bf16_eio_decode_big", big([=] { gemm_bf16(decode_counts(64, 5), 1024, 768, L_EIO); })});
+  s.push_back({"gemm_bf16_eoi_decode_big", big([=] { gemm_bf16(decode_counts(64, 5), 1024, 768, L_EOI); })});
+  s.push_back({"gemm_mx_eio_decode_big", big([=] { gemm_mx(decode_counts(48, 6), 1024, 512, L_EIO); })});
+  s.push_back({"moe_bf16_eio_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); })});
+  s.push_back({"moe_mx_eio_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); })});
   // many groups: the tile prefix comes from global memory past the LDS copy
   s.push_back({"gemm_bf16_many_groups", [=] {
                  std::vector<int> c(1100, 0);

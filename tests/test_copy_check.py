@@ -32,6 +32,8 @@ SCENARIOS = [
     "gemm_bf16_eio", "gemm_bf16_eoi", "gemm_bf16_eio_narrow", "gemm_bf16_eoi_narrow",
     "gemm_mx_eio", "gemm_mx_eoi", "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k",
     "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode", "gemm_mx_eio_decode", "gemm_mx_eoi_decode",
+    "gemm_bf16_eio_decode_big", "gemm_bf16_eoi_decode_big", "gemm_mx_eio_decode_big", "moe_bf16_eio_decode_big",
+    "moe_mx_eio_decode_big",
     "gemm_bf16_many_groups",
     "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi",
     "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
