@@ -22,6 +22,7 @@ FEATURE_NUMERICS = 2
 FEATURE_DECODE_TILES = 4
 FEATURE_BACKWARD = 8
 FEATURE_ROUTE_GRAD = 16
+FEATURE_MX_WEIGHT_PREP = 32
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}
@@ -104,6 +105,8 @@ _SIGNATURES = [
     ("mi355moe_mx_quantize_rows", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p]),
     ("mi355moe_mx_quantize_cols", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                             c_void_p]),
+    ("mi355moe_mx_quantize_weight", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                              c_void_p, c_void_p]),
     ("mi355moe_mx_weight_scale_ld", c_int64, [c_int32]),
     ("mi355moe_mx_weight_to_eoi", c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                             c_void_p]),

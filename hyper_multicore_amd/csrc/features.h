@@ -21,3 +21,5 @@ inline bool mi355_small_tiles_enabled() { return MI355_PATH_ON; }
 inline bool mi355_backward_enabled() { return MI355_PATH_ON; }
 // MegaGate RouteGrad (gradient of the routing weights with respect to the logits).
 inline bool mi355_route_grad_enabled() { return MI355_PATH_ON; }
+// Dual-axis MX weight quantisation (col and row axes of the MXFP8 weight root in one pass).
+inline bool mi355_mx_weight_prep_enabled() { return MI355_PATH_ON; }

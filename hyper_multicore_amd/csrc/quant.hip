@@ -98,6 +98,63 @@ extern "C" int mi355moe_mx_quantize_cols(const uint16_t* w, int32_t groups, int3
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
+// ---- dual-axis MX weight quantisation ---------------------------------------------------------
+// One workgroup per (group, 32-row block, 256-column block); thread c owns column n0 + c. Column
+// axis: the thread's 32 values form one block (scale [G, M/64, N, 2]). Row axis: the 32 threads of
+// a half-wave own 32 consecutive columns, so each row's block amax is a 32-lane reduction
+// (scale [G, M, N/64, 2] = [G*M, N/32] codes). Loads and stores are row-contiguous across threads.
+// Both axes use the same code / element conversions as mx_quant_rows_kernel and
+// mx_quant_cols_kernel, so each axis equals what those kernels write.
+__global__ __launch_bounds__(256) void mx_quant_weight_dual_kernel(const uint16_t* w, int M, int N, uint8_t* col_data,
+                                                                   uint8_t* col_scale, uint8_t* row_data,
+                                                                   uint8_t* row_scale) {
+  const int g = blockIdx.z, mb = blockIdx.y;
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  const bool live = n < N;  // N % 32 == 0: a half-wave is all live or all dead
+  const int64_t base = ((int64_t)g * M + mb * 32) * N;
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    v[i] = live ? bf16_to_f32(w[base + (int64_t)i * N + n]) : 0.0f;
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  if (col_data != nullptr) {
+    const uint32_t code = mx_scale_code(amax);
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) col_data[base + (int64_t)i * N + n] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+      col_scale[(((int64_t)g * (M / 64) + mb / 2) * N + n) * 2 + (mb & 1)] = (uint8_t)code;
+    }
+  }
+  if (row_data != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      float a = fabsf(v[i]);
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
+      const uint32_t code = mx_scale_code(a);
+      if (live) {
+        row_data[base + (int64_t)i * N + n] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+        if ((threadIdx.x & 31) == 0) row_scale[((int64_t)g * M + mb * 32 + i) * (N / 32) + n / 32] = (uint8_t)code;
+      }
+    }
+  }
+}
+
+extern "C" int mi355moe_mx_quantize_weight(const uint16_t* w, int32_t groups, int32_t rows, int32_t cols,
+                                           uint8_t* col_data, uint8_t* col_scale, uint8_t* row_data,
+                                           uint8_t* row_scale, void* stream) {
+  if (groups <= 0 || groups > 65535 || rows <= 0 || cols <= 0 || rows % 64 || cols % 64) return MI355MOE_EINVAL;
+  if (w == nullptr || (col_data == nullptr) != (col_scale == nullptr) || (row_data == nullptr) != (row_scale == nullptr))
+    return MI355MOE_EINVAL;
+  if (col_data == nullptr && row_data == nullptr) return MI355MOE_EINVAL;
+  if (!mi355_mx_weight_prep_enabled()) return MI355MOE_EUNSUPPORTED;
+  hipLaunchKernelGGL(mx_quant_weight_dual_kernel, dim3((cols + 255) / 256, rows / 32, groups), dim3(256), 0,
+                     (hipStream_t)stream, w, rows, cols, col_data, col_scale, row_data, row_scale);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
 // ---- MX weight re-layout: [G, K, N] (+ col_scale [G, K/64, N, 2]) -> [G, N, K] (+ [G, N, ld]) ----
 // One 64 (K) x 64 (N) byte tile per workgroup, transposed through LDS.
 __global__ __launch_bounds__(256) void mx_weight_to_eoi_kernel(const uint8_t* src, int K, int N, uint8_t* dst) {

@@ -10,14 +10,17 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
+from . import _lib, ops
 
 __all__ = ["quantize_expert_weight", "resolve_forward_weight", "prepared_eoi_weight"]
 
 
-def quantize_expert_weight(weight: torch.Tensor) -> torch.Tensor:
+def quantize_expert_weight(weight: torch.Tensor, *, backward_axis: bool = False) -> torch.Tensor:
     """Return a root holding ``col_data`` / ``col_scale`` for a bf16 EIO weight ``[E, M, N]``.
 
+    With ``backward_axis=True`` the root also carries the backward axis ``row_data`` / ``row_scale``
+    (``[E, M, N]`` e4m3 and ``[E, M, N/64, 2]``: blocks of 32 along N), both axes quantised in one
+    pass by the dual-axis kernel (needs the library's MX weight-preparation feature).
     The root is a one-element bf16 tensor expanded to the logical shape ``[E, M, N]`` on the
     weight's device; only the physical attributes are read by the executor.
     """
@@ -26,10 +29,18 @@ def quantize_expert_weight(weight: torch.Tensor) -> torch.Tensor:
     E, M, N = weight.shape
     if M % 64 or N % 64:
         raise ValueError(f"MegaMoE MXFP8 expert shape requires M/N divisible by 64, got {tuple(weight.shape)}.")
-    data, scale = ops.mx_quantize_cols(weight.to(torch.bfloat16))
+    row_data = row_scale = None
+    if backward_axis:
+        if not ops.features() & _lib.FEATURE_MX_WEIGHT_PREP:
+            raise NotImplementedError("the dual-axis MX weight quantisation is switched off in this build")
+        data, scale, row_data, row_scale = ops.mx_quantize_weight(weight.to(torch.bfloat16))
+    else:
+        data, scale = ops.mx_quantize_cols(weight.to(torch.bfloat16))
     root = torch.empty((1, 1, 1), dtype=torch.bfloat16, device=weight.device).expand(E, M, N)
     root.col_data = data
     root.col_scale = scale
+    root.row_data = row_data
+    root.row_scale = row_scale
     root.logical_shape = (E, M, N)
     return root
 

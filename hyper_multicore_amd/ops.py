@@ -287,6 +287,28 @@ def mx_quantize_cols(w: torch.Tensor):
     return data, scale
 
 
+def mx_quantize_weight(w: torch.Tensor, *, col: bool = True, row: bool = True):
+    """Dual-axis MX weight quantisation of bf16 [G, M, N] (the MXFP8 weight root's physical fields,
+    modules/mega_moe/backends/mxfp8/weights.py:24-97): returns (col_data e4m3fn [G, M, N], col_scale
+    uint8 [G, M/64, N, 2], row_data e4m3fn [G, M, N], row_scale uint8 [G, M, N/64, 2]), None for an
+    axis not asked for. M and N must be multiples of 64."""
+    lib = _lib.load()
+    device = _require_gpu(w)
+    if w.dtype != torch.bfloat16 or w.ndim != 3 or w.shape[1] % 64 or w.shape[2] % 64:
+        raise ValueError("mx_quantize_weight takes bf16 [G, M, N] with M % 64 == 0 and N % 64 == 0")
+    if not (col or row):
+        raise ValueError("ask for at least one axis")
+    w = w.contiguous()
+    G, M, N = w.shape
+    cd = torch.empty((G, M, N), dtype=torch.float8_e4m3fn, device=device) if col else None
+    cs = torch.empty((G, M // 64, N, 2), dtype=torch.uint8, device=device) if col else None
+    rd = torch.empty((G, M, N), dtype=torch.float8_e4m3fn, device=device) if row else None
+    rs = torch.empty((G, M, N // 64, 2), dtype=torch.uint8, device=device) if row else None
+    _lib.check(lib.mi355moe_mx_quantize_weight(_ptr(w), G, M, N, _ptr(cd), _ptr(cs), _ptr(rd), _ptr(rs),
+                                               _stream(device)), "mi355moe_mx_quantize_weight")
+    return cd, cs, rd, rs
+
+
 # ------------------------------------------------------------------------------------------------
 # Grouped GEMM and the full expert forward
 # ------------------------------------------------------------------------------------------------

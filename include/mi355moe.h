@@ -54,6 +54,7 @@ enum {
   MI355MOE_FEATURE_DECODE_TILES = 4,  /* 64-row tiles for groups averaging <= 32 rows */
   MI355MOE_FEATURE_BACKWARD = 8,      /* mi355moe_moe_backward */
   MI355MOE_FEATURE_ROUTE_GRAD = 16,   /* mi355moe_gate_route_grad */
+  MI355MOE_FEATURE_MX_WEIGHT_PREP = 32, /* mi355moe_mx_quantize_weight */
 };
 int mi355moe_features(void);
 
@@ -207,6 +208,21 @@ int mi355moe_mx_quantize_rows(const uint16_t* x, int64_t rows, int32_t cols, uin
                               uint8_t* scale, void* stream);
 int mi355moe_mx_quantize_cols(const uint16_t* w, int32_t groups, int32_t kdim, int32_t cols,
                               uint8_t* col_data, uint8_t* col_scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Dual-axis MX weight quantisation: the physical fields of an MXFP8 expert-weight root
+ * (modules/mega_moe/backends/mxfp8/weights.py:24-97) from a bf16 weight w [G, M, N] in one pass:
+ *   col_data [G, M, N] e4m3, col_scale [G, M/64, N, 2]  (blocks of 32 along M for every column;
+ *                                                        the forward axis, = mi355moe_mx_quantize_cols)
+ *   row_data [G, M, N] e4m3, row_scale [G, M, N/64, 2]  (blocks of 32 along N for every row; the
+ *                                                        backward axis, = mi355moe_mx_quantize_rows
+ *                                                        of the [G*M, N] view)
+ * Either pair may be NULL (not both). M % 64 == 0 and N % 64 == 0 (weights.py:52-53).
+ * Replaces the caller-side dual-axis weight quantisation the reference expects roots to carry
+ * (npu_dynamic_mx_quant_with_dual_axis, tests/torch/_replay_mega_moe_arch35.py:55).
+ */
+int mi355moe_mx_quantize_weight(const uint16_t* w, int32_t groups, int32_t rows, int32_t cols, uint8_t* col_data,
+                                uint8_t* col_scale, uint8_t* row_data, uint8_t* row_scale, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * MX weight re-layout for the GEMM (no reference counterpart: a one-time weight preparation, like

@@ -107,6 +107,18 @@ def test_route_grad_validation():
     assert lib.mi355moe_gate_route_grad(None, None) == _lib.EINVAL
 
 
+def test_mx_quantize_weight_validation():
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    q = lib.mi355moe_mx_quantize_weight
+    for args in ((1, 0, 64, 64, 1, 1, 1, 1), (1, 2, 96, 64, 1, 1, 1, 1), (1, 2, 64, 96, 1, 1, 1, 1),
+                 (None, 2, 64, 64, 1, 1, 1, 1), (1, 2, 64, 64, None, None, None, None), (1, 2, 64, 64, 1, None, 1, 1),
+                 (1, 2, 64, 64, 1, 1, None, 1)):
+        assert q(*args, None) == _lib.EINVAL, args
+    if not lib.mi355moe_features() & _lib.FEATURE_MX_WEIGHT_PREP:  # never launches with dummy pointers
+        assert q(1, 2, 64, 64, 1, 1, None, None, None) == _lib.EUNSUPPORTED
+
+
 def test_workspace_sizes():
     from hyper_multicore_amd import _lib
     lib = _lib.load()
