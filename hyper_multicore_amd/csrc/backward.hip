@@ -182,9 +182,8 @@ extern "C" int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* wor
   const bool f32 = a.weight_grad_dtype == MI355MOE_GRAD_FP32;
   const size_t wsz = f32 ? 4 : 2;
   if (T == 0) {  // no rows: the weight gradients are zero
-    if (hipMemsetAsync(a.grad_w1, 0, (size_t)E * H * 2 * I * wsz, st) != hipSuccess) return MI355MOE_ELAUNCH;
-    if (hipMemsetAsync(a.grad_w2, 0, (size_t)E * I * H * wsz, st) != hipSuccess) return MI355MOE_ELAUNCH;
-    return MI355MOE_OK;
+    const int rz = mi355_zero_enqueue(a.grad_w1, (size_t)E * H * 2 * I * wsz, st);
+    return rz ? rz : mi355_zero_enqueue(a.grad_w2, (size_t)E * I * H * wsz, st);
   }
   BwdLayout L = bwd_layout(a);
   if (workspace == nullptr || workspace_size < L.total) return MI355MOE_EWORKSPACE_CODE;
@@ -208,7 +207,8 @@ extern "C" int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* wor
   if (rc) return rc;
   rc = mi355_plan_tiles(group_list, E, tile_prefix, st);
   if (rc) return rc;
-  if (hipMemsetAsync(ws + L.zero, 0, (size_t)(H > 2 * I ? H : 2 * I) * 2, st) != hipSuccess) return MI355MOE_ELAUNCH;
+  rc = mi355_zero_enqueue(ws + L.zero, (size_t)(H > 2 * I ? H : 2 * I) * 2, st);
+  if (rc) return rc;
   rc = mi355_permute_rows_enqueue(a.hidden, R, K, H, mapping, xg, st);  // X in routed order
   if (rc) return rc;
 

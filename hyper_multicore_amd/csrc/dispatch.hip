@@ -187,6 +187,22 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t* x, in
   for (int v = threadIdx.x; v < H / 8; v += blockDim.x) dst[v] = src[v];
 }
 
+// Zero `bytes` (a multiple of 16, 16-byte aligned) with a fill kernel: stream-ordered like a memset
+// and safe to record in a captured graph.
+__global__ __launch_bounds__(256) void zero16_kernel(uint4* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
+int mi355_zero_enqueue(void* p, size_t bytes, hipStream_t st) {
+  if (bytes == 0) return MI355MOE_OK;
+  if (p == nullptr || bytes % 16 || ((uintptr_t)p & 15)) return MI355MOE_EINVAL;
+  const int64_t n = (int64_t)(bytes / 16);
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, st, (uint4*)p, n);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
 int mi355_permute_rows_enqueue(const uint16_t* x, int64_t slots, int K, int H, const int32_t* mapping,
                                 uint16_t* routed, hipStream_t st) {
   if (slots == 0) return MI355MOE_OK;

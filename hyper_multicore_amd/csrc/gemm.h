@@ -59,6 +59,7 @@ int mi355_gg_bn();
 int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
                            int64_t* expert_offsets, int64_t* group_list, int32_t* mapping, int32_t* gather_index,
                            int32_t* error_flag, void* workspace, hipStream_t stream);
+int mi355_zero_enqueue(void* p, size_t bytes, hipStream_t st);
 int mi355_permute_rows_enqueue(const uint16_t* x, int64_t slots, int K, int H, const int32_t* mapping,
                                 uint16_t* routed, hipStream_t st);
 int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const float* probs, int64_t T, int K, int H,

@@ -602,15 +602,17 @@ __global__ __launch_bounds__(1024) void plan_tiles_kernel(const int64_t* group_l
   if (threadIdx.x == 0) tile_prefix[G] = (int32_t)total;
 }
 
-static int g_num_cus = 0;
+// CU count of the current device, cached per device (the persistent grids are sized from it).
+static int g_num_cus[64] = {};
 static int num_cus() {
-  if (g_num_cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    g_num_cus = n;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (g_num_cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_num_cus[dev] = n;
   }
-  return g_num_cus;
+  return g_num_cus[dev];
 }
 
 template <class C, bool MX, bool B_KN, int EPI>

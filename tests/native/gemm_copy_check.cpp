@@ -174,6 +174,15 @@ int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t T, int K, int E, 
   if (error_flag && bad) *error_flag = 1;
   return MI355MOE_OK;
 }
+int mi355_zero_enqueue(void* p, size_t bytes, hipStream_t) {
+  if (bytes && !find_alloc(p, bytes)) {
+    CHECK_FAIL("zero fill of %zu bytes outside every allocation", bytes);
+    return MI355MOE_EINVAL;
+  }
+  if (bytes % 16 || ((uintptr_t)p & 15)) return MI355MOE_EINVAL;
+  memset(p, 0, bytes);
+  return MI355MOE_OK;
+}
 int mi355_permute_rows_enqueue(const uint16_t*, int64_t, int, int, const int32_t*, uint16_t*, hipStream_t) {
   return MI355MOE_OK;
 }
