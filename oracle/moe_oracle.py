@@ -428,6 +428,134 @@ def expert_backward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: to
     return dx, dW1, dW2, dp.reshape(T, K)
 
 
+def mx_quantize_grouped_rows(x: torch.Tensor, counts: list[int]):
+    """Column-axis MX quantisation of a routed-row matrix x [R, C] (rows grouped by expert, counts[e]
+    rows each): every column in blocks of 32 rows that start at each expert's first row, a partial
+    last block zero-padded (the grouped packed column axis of dual_axis_mxfp8_worker.h:24-33,
+    x_col / a_col / dy_col / du_col of mxfp8/execution.py:28-35).
+
+    Returns (codes uint8 [R, C], packed scales uint8 [(R + 63) // 64 + E, C, 2], dequantised fp32
+    [R, C]). Expert e's scales start at 64-row group floor(start_e / 64) + e (its pairs cover 64 rows
+    each); pair slots of 32-row blocks past the expert's rows hold code 0.
+    """
+    x = x.float()
+    R, C = x.shape
+    E = len(counts)
+    codes = torch.zeros((R, C), dtype=torch.uint8)
+    deq = torch.zeros((R, C), dtype=torch.float32)
+    packed = torch.zeros(((R + 63) // 64 + E, C, 2), dtype=torch.uint8)
+    start = 0
+    for e, n in enumerate(counts):
+        if n == 0:
+            continue
+        nb = (n + 31) // 32
+        blk = torch.zeros((nb * 32, C), dtype=torch.float32)
+        blk[:n] = x[start:start + n]
+        q, sc = mx_quantize(blk, dim=0)  # q [nb*32, C], sc [nb, C]
+        codes[start:start + n] = q[:n]
+        deq[start:start + n] = mx_dequantize(q, sc, dim=0)[:n]
+        base = start // 64 + e
+        for b in range(nb):
+            packed[base + b // 2, :, b % 2] = sc[b]
+        start += n
+    return codes, packed, deq
+
+
+def mx_dequantize_weight_rows(row_data: torch.Tensor, row_scale: torch.Tensor) -> torch.Tensor:
+    """Backward axis of an MX root: row_data [E, M, N] e4m3 codes, row_scale [E, M, N/64, 2] (blocks of
+    32 along N) -> fp32 [E, M, N]."""
+    E, M, N = row_data.shape
+    return mx_dequantize(row_data.view(torch.uint8), row_scale.reshape(E, M, N // 32), dim=-1)
+
+
+def expert_backward_reference_mx(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor,
+                                 w1_col: tuple[torch.Tensor, torch.Tensor], w2_col: tuple[torch.Tensor, torch.Tensor],
+                                 w1_row: tuple[torch.Tensor, torch.Tensor], w2_row: tuple[torch.Tensor, torch.Tensor],
+                                 grad_out: torch.Tensor, *, num_experts: int | None = None):
+    """MXFP8 expert backward (mxfp8/graph.py:147-154, mxfp8/execution.py:119-164), fp32 accumulation of
+    the dequantised operands, in the EIO weight layout:
+      forward recompute   U = bf16(Q_H(x) W1c), act = silu(g) u (fp32), y = bf16(Q_I(act) W2c)
+      combine backward    dY = bf16(p dOut), dp = <y, dOut>
+      quant_dy            dy_row = Q_H(dY) (blocks along H), dy_col = Q_rows(dY) (blocks of 32 routed
+                          rows from each expert's start)
+      dw2 (TN)            dW2_e = Q_rows(act)_e^T dy_col_e
+      da (NT)             da = bf16(dy_row W2r_e^T), W2r the root's row axis (blocks along H)
+      swiglu_grad_quant   dU = [da u s (1 + g (1 - s)) | da silu(g)] in fp32 (no bf16 rounding: the
+                          gradient is quantised straight away), du_row = Q_2I(dU), du_col = Q_rows(dU)
+      dw1 (TN)            dW1_e = Q_rows(x)_e^T du_col_e
+      dx (NT)             dXr = bf16(du_row W1r_e^T), W1r blocks along 2I
+      permute backward    dX[t] = bf16(sum_k dXr[mapping[t, k]])
+    w*_col = (col_data, col_scale) as mx_quantize_weight_cols returns; w*_row = (row_data [E, M, N],
+    row_scale [E, M, N/64, 2]). Whether the fused SwiGLU-gradient quantisation rounds dU to bf16
+    first is not visible in the reference (ops-nn source absent): parity unpinned at that point.
+    Returns (dX bf16 [T, H], dW1 fp32 [E, H, 2I], dW2 fp32 [E, I, H], dp fp32 [T, K]).
+    """
+    T, H = hidden.shape
+    K = ids.shape[1]
+    E = num_experts if num_experts is not None else w1_col[0].shape[0]
+    W1c = mx_dequantize_weight_cols(*w1_col)       # [E, H, 2I]
+    W2c = mx_dequantize_weight_cols(*w2_col)       # [E, I, H]
+    W1r = mx_dequantize_weight_rows(*w1_row)       # [E, H, 2I]
+    W2r = mx_dequantize_weight_rows(*w2_row)       # [E, I, H]
+    I = W1c.shape[2] // 2
+    q, s = mx_quantize(hidden.float(), dim=-1)
+    xq = mx_dequantize(q, s, dim=-1)
+    dout = grad_out.float()
+    mapping, gather = stable_permutation(ids, E)
+    flat = ids.reshape(-1).long()
+    pflat = probs.reshape(-1).float()
+    counts = [int((flat == e).sum()) for e in range(E)]
+    R = gather.numel()
+    rows_all = gather.long() // K
+    x_r = hidden.float()[rows_all]
+    U = torch.zeros(R, 2 * I)
+    act = torch.zeros(R, I)
+    y = torch.zeros(R, H)
+    start = 0
+    for e, n in enumerate(counts):
+        if n:
+            sl = slice(start, start + n)
+            U[sl] = _bf16(xq[rows_all[sl]] @ W1c[e])
+            act[sl] = F.silu(U[sl, :I]) * U[sl, I:]
+            aq, asc = mx_quantize(act[sl], dim=-1)
+            y[sl] = _bf16(mx_dequantize(aq, asc, dim=-1) @ W2c[e])
+        start += n
+    dy = _bf16(dout[rows_all] * pflat[gather.long()][:, None])
+    dp = torch.zeros(T * K)
+    dp[gather.long()] = (y * dout[rows_all]).sum(1)
+    dq, dsc = mx_quantize(dy, dim=-1)
+    dy_row = mx_dequantize(dq, dsc, dim=-1)
+    _, _, dy_col = mx_quantize_grouped_rows(dy, counts)
+    _, _, a_col = mx_quantize_grouped_rows(act, counts)
+    _, _, x_col = mx_quantize_grouped_rows(x_r, counts)
+    dW1 = torch.zeros(E, H, 2 * I)
+    dW2 = torch.zeros(E, I, H)
+    da = torch.zeros(R, I)
+    start = 0
+    for e, n in enumerate(counts):
+        if n:
+            sl = slice(start, start + n)
+            dW2[e] = a_col[sl].T @ dy_col[sl]
+            da[sl] = _bf16(dy_row[sl] @ W2r[e].T)
+        start += n
+    g, u = U[:, :I], U[:, I:]
+    sg = torch.sigmoid(g)
+    dU = torch.cat([da * u * sg * (1 + g * (1 - sg)), da * (g * sg)], dim=1)
+    uq, usc = mx_quantize(dU, dim=-1)
+    du_row = mx_dequantize(uq, usc, dim=-1)
+    _, _, du_col = mx_quantize_grouped_rows(dU, counts)
+    dxr = torch.zeros(R, H)
+    start = 0
+    for e, n in enumerate(counts):
+        if n:
+            sl = slice(start, start + n)
+            dW1[e] = x_col[sl].T @ du_col[sl]
+            dxr[sl] = _bf16(du_row[sl] @ W1r[e].T)
+        start += n
+    dx = unpermute_tokens(dxr.to(torch.bfloat16), mapping, None, K)
+    return dx, dW1, dW2, dp.reshape(T, K)
+
+
 def torch_experts_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, gate_w: torch.Tensor,
                             up_w: torch.Tensor, down_w: torch.Tensor) -> torch.Tensor:
     """The TorchExperts CPU loop (tests/common/multicore/moe_reference.py:170-181): weights are

@@ -595,3 +595,100 @@ def test_route_grad_denominator_epsilon():
     ours, ref, scores, _ = _route_grad_pair(logits, "sigmoid", 2, seed=22)
     assert float(scores.max()) < 1e-19
     assert torch.equal(ours, ref)
+
+
+# ------------------------------------------------------------------------------------------------
+# MXFP8 expert backward (oracle)
+# ------------------------------------------------------------------------------------------------
+def test_grouped_row_quant_aligned_experts_equal_plain_column_quant():
+    """Experts of 64-multiple sizes start on 64-row boundaries: the grouped column axis is the plain
+    column quantisation of the whole matrix, and the packed scales are its codes with group e shifted
+    by e."""
+    g = torch.Generator().manual_seed(3)
+    counts = [64, 128, 0, 192]
+    x = torch.randn(sum(counts), 96, generator=g) * 3
+    codes, packed, deq = orc.mx_quantize_grouped_rows(x, counts)
+    q, sc = orc.mx_quantize(x, dim=0)  # sc [R/32, C]
+    assert torch.equal(codes, q)
+    assert torch.equal(deq, orc.mx_dequantize(q, sc, dim=0))
+    start = 0
+    for e, n in enumerate(counts):
+        for b in range(n // 32):
+            assert torch.equal(packed[start // 64 + e + b // 2, :, b % 2], sc[start // 32 + b])
+        start += n
+
+
+def test_grouped_row_quant_blocks_restart_at_each_expert():
+    """A 1-row expert gets the closed-form code of each value (floor(log2 |v|) - 8) and the unused odd
+    slot of its pair stays 0; a boundary inside a 32-row block changes the result versus global
+    blocks; scale regions of consecutive experts never overlap."""
+    g = torch.Generator().manual_seed(4)
+    counts = [1, 45, 33, 0, 64]
+    x = torch.randn(sum(counts), 64, generator=g)
+    codes, packed, _ = orc.mx_quantize_grouped_rows(x, counts)
+    v = x[0].abs()
+    want = (torch.floor(torch.log2(v)) - 8 + 127).to(torch.uint8)
+    assert torch.equal(packed[0, :, 0], want)
+    assert torch.all(packed[0, :, 1] == 0)
+    q_global, _ = orc.mx_quantize(torch.cat([x, torch.zeros(32 - x.shape[0] % 32, 64)]), dim=0)
+    assert not torch.equal(codes, q_global[: x.shape[0]])
+    used, start = set(), 0
+    for e, n in enumerate(counts):
+        slots = {start // 64 + e + j for j in range((n + 63) // 64)}
+        assert not (slots & used) and all(s < packed.shape[0] for s in slots)
+        used |= slots
+        start += n
+
+
+def _mx_backward_inputs(T=64, H=256, I=128, E=4, K=2, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    p = torch.rand(T, K, generator=g)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.05).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.05).to(torch.bfloat16)
+    dout = torch.randn(T, H, generator=g).to(torch.bfloat16)
+
+    def roots(w):
+        Ee, M, N = w.shape
+        q, s = orc.mx_quantize(w.float(), dim=-1)
+        return orc.mx_quantize_weight_cols(w), (q, s.reshape(Ee, M, N // 64, 2))
+
+    (c1, r1), (c2, r2) = roots(w1), roots(w2)
+    return x, ids, p, w1, w2, dout, c1, c2, r1, r2
+
+
+def test_mx_backward_reference_scale_equivariance():
+    """Scaling dOut by 2^k scales dY and every MX block scale by 2^k exactly: dX, dW1, dW2, dp scale
+    exactly by 2^k."""
+    x, ids, p, _, _, dout, c1, c2, r1, r2 = _mx_backward_inputs()
+    a = orc.expert_backward_reference_mx(x, ids, p, c1, c2, r1, r2, dout)
+    b = orc.expert_backward_reference_mx(x, ids, p, c1, c2, r1, r2, (dout.float() * 8).to(torch.bfloat16))
+    for u, v in zip(a, b):
+        assert torch.equal(u.float() * 8, v.float())
+
+
+def test_mx_backward_reference_expert_relabeling():
+    """Relabelling experts (weights permuted alike) moves their row blocks but not their contents:
+    dX and dp are identical and the weight gradients are permuted - pins the per-expert alignment of
+    the grouped column quantisation."""
+    x, ids, p, _, _, dout, c1, c2, r1, r2 = _mx_backward_inputs(T=80, E=5, seed=1)
+    perm = torch.tensor([3, 0, 4, 1, 2])  # new id of expert e is perm[e]
+    inv = torch.argsort(perm)
+    ids2 = perm[ids]
+
+    def pick(root):
+        return tuple(t[inv] for t in root)
+
+    a = orc.expert_backward_reference_mx(x, ids, p, c1, c2, r1, r2, dout)
+    b = orc.expert_backward_reference_mx(x, ids2, p, pick(c1), pick(c2), pick(r1), pick(r2), dout)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[3], b[3])
+    assert torch.equal(a[1], b[1][perm]) and torch.equal(a[2], b[2][perm])
+
+
+def test_mx_backward_reference_close_to_bf16_backward():
+    x, ids, p, w1, w2, dout, c1, c2, r1, r2 = _mx_backward_inputs(seed=2)
+    a = orc.expert_backward_reference_mx(x, ids, p, c1, c2, r1, r2, dout)
+    b = orc.expert_backward_reference(x, ids, p, w1, w2, dout)
+    for u, v in zip(a, b):
+        assert orc.rel_l2(u.float(), v.float()) < 0.12
