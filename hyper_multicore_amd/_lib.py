@@ -23,6 +23,7 @@ FEATURE_DECODE_TILES = 4
 FEATURE_BACKWARD = 8
 FEATURE_ROUTE_GRAD = 16
 FEATURE_MX_WEIGHT_PREP = 32
+FEATURE_MX_BACKWARD = 64
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}
@@ -83,7 +84,9 @@ class BackwardArgs(Structure):
         ("num_experts", c_int32), ("top_k", c_int32), ("topk_ids", c_void_p), ("ids_dtype", c_int32),
         ("weight_layout", c_int32), ("topk_weights", c_void_p), ("w1", c_void_p), ("w2", c_void_p),
         ("grad_out", c_void_p), ("grad_hidden", c_void_p), ("grad_w1", c_void_p), ("grad_w2", c_void_p),
-        ("grad_topk_weights", c_void_p), ("weight_grad_dtype", c_int32), ("reserved", c_int32),
+        ("grad_topk_weights", c_void_p), ("weight_grad_dtype", c_int32), ("precision", c_int32),
+        ("w1_scale", c_void_p), ("w2_scale", c_void_p), ("w1_row", c_void_p), ("w2_row", c_void_p),
+        ("w1_row_scale", c_void_p), ("w2_row_scale", c_void_p),
     ]
 
 

@@ -15,7 +15,8 @@ extern "C" int mi355moe_features(void) {
          (mi355_small_tiles_enabled() ? MI355MOE_FEATURE_DECODE_TILES : 0) |
          (mi355_backward_enabled() ? MI355MOE_FEATURE_BACKWARD : 0) |
          (mi355_route_grad_enabled() ? MI355MOE_FEATURE_ROUTE_GRAD : 0) |
-         (mi355_mx_weight_prep_enabled() ? MI355MOE_FEATURE_MX_WEIGHT_PREP : 0);
+         (mi355_mx_weight_prep_enabled() ? MI355MOE_FEATURE_MX_WEIGHT_PREP : 0) |
+         (mi355_mx_backward_enabled() ? MI355MOE_FEATURE_MX_BACKWARD : 0);
 }
 
 // ---------------------------------------------------------------------------------------------

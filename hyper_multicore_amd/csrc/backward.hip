@@ -144,8 +144,19 @@ int validate_bwd(const MI355MoeBackwardArgs& a) {
   if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   if (a.weight_grad_dtype != MI355MOE_GRAD_BF16 && a.weight_grad_dtype != MI355MOE_GRAD_FP32) return MI355MOE_EINVAL;
   if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;
+  if (a.precision != MI355MOE_PRECISION_BF16 && a.precision != MI355MOE_PRECISION_MXFP8) return MI355MOE_EINVAL;
   if (a.hidden_size % 64 || a.intermediate_size % 128) return MI355MOE_EUNSUPPORTED;
-  if (!mi355_backward_enabled()) return MI355MOE_EUNSUPPORTED;
+  if (a.precision == MI355MOE_PRECISION_MXFP8) {
+    // EIO roots only; the data-gradient GEMMs fetch 16 row-scale codes of the weights at a time
+    if (a.weight_layout != MI355MOE_LAYOUT_EIO) return MI355MOE_EUNSUPPORTED;
+    if (a.hidden_size % 512 || a.intermediate_size % 256) return MI355MOE_EUNSUPPORTED;
+    if (!mi355_mx_backward_enabled()) return MI355MOE_EUNSUPPORTED;
+    if (a.num_tokens > 0 && (a.w1_scale == nullptr || a.w2_scale == nullptr || a.w1_row == nullptr ||
+                             a.w2_row == nullptr || a.w1_row_scale == nullptr || a.w2_row_scale == nullptr))
+      return MI355MOE_EINVAL;
+  } else if (!mi355_backward_enabled()) {
+    return MI355MOE_EUNSUPPORTED;
+  }
   if (a.grad_w1 == nullptr || a.grad_w2 == nullptr) return MI355MOE_EINVAL;
   if (a.num_tokens > 0 &&
       (a.hidden == nullptr || a.topk_ids == nullptr || a.topk_weights == nullptr || a.w1 == nullptr ||
@@ -162,10 +173,189 @@ int launch_rows(void (*kern)(const uint16_t*, int64_t, int, uint16_t*), const ui
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
+// ---- MXFP8 -------------------------------------------------------------------------------------
+struct MxBwdLayout {
+  size_t dispatch, counts, group_list, mapping, gather, tile_prefix, block_prefix, xq, xs, u, aq, as, acol, acs, y,
+      dy, dyq, dys, dycol, dycs, da, duq, dus, ducol, ducs, xcol, xcs, zero, total;
+};
+
+MxBwdLayout mx_bwd_layout(const MI355MoeBackwardArgs& a) {
+  MxBwdLayout L = {};
+  const size_t T = (size_t)a.num_tokens, K = (size_t)a.top_k, E = (size_t)a.num_experts;
+  const size_t H = (size_t)a.hidden_size, I = (size_t)a.intermediate_size, R = T * K;
+  const size_t CG = (R + 63) / 64 + E;  // 64-row scale groups of the grouped column axis
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += al256(bytes); return o; };
+  L.dispatch = take(mi355moe_dispatch_workspace_size(a.num_tokens, a.top_k, a.num_experts));
+  L.counts = take(E * 4);
+  L.group_list = take(E * 8);
+  L.mapping = take(R * 4);
+  L.gather = take(R * 4);
+  L.tile_prefix = take((E + 1) * 4);
+  L.block_prefix = take((E + 1) * 4);
+  L.xq = take(T * H);                                  // x along H (GMM1 recompute)
+  L.xs = take(T * (size_t)mi355_mx_scale_ld(H));
+  L.u = take(R * 2 * I * 2);                           // U bf16
+  L.aq = take(R * I);                                  // act along I (GMM2 recompute)
+  L.as = take(R * (size_t)mi355_mx_scale_ld(I));
+  L.acol = take(R * I);                                // act along the routed rows (dW2)
+  L.acs = take(CG * I * 2);
+  L.y = take(R * H * 2);                               // y, later the routed input gradients
+  L.dy = take(R * H * 2);
+  L.dyq = take(R * H);                                 // dY along H (gA)
+  L.dys = take(R * (size_t)mi355_mx_scale_ld(H));
+  L.dycol = take(R * H);                               // dY along the routed rows (dW2)
+  L.dycs = take(CG * H * 2);
+  L.da = take(R * I * 2);                              // gA bf16
+  L.duq = take(R * 2 * I);                             // dU along 2I (dX)
+  L.dus = take(R * (size_t)mi355_mx_scale_ld(2 * I));
+  L.ducol = take(R * 2 * I);                           // dU along the routed rows (dW1)
+  L.ducs = take(CG * 2 * I * 2);
+  L.xcol = take(R * H);                                // X along the routed rows (dW1)
+  L.xcs = take(CG * H * 2);
+  L.zero = take(H > 2 * I ? H : 2 * I);
+  L.total = off;
+  return L;
+}
+
+int mx_backward(const MI355MoeBackwardArgs& a, char* ws, const MxBwdLayout& L, hipStream_t st) {
+  const int64_t T = a.num_tokens;
+  const int K = a.top_k, E = a.num_experts, H = a.hidden_size, I = a.intermediate_size;
+  const int64_t R = T * K;
+  const bool f32 = a.weight_grad_dtype == MI355MOE_GRAD_FP32;
+  int64_t* group_list = (int64_t*)(ws + L.group_list);
+  int32_t* mapping = (int32_t*)(ws + L.mapping);
+  int32_t* gather = (int32_t*)(ws + L.gather);
+  int32_t* tile_prefix = (int32_t*)(ws + L.tile_prefix);
+  int32_t* block_prefix = (int32_t*)(ws + L.block_prefix);
+  uint16_t* u = (uint16_t*)(ws + L.u);
+  uint16_t* y = (uint16_t*)(ws + L.y);
+  uint16_t* dy = (uint16_t*)(ws + L.dy);
+  uint16_t* da = (uint16_t*)(ws + L.da);
+  const uint8_t* zero = (const uint8_t*)(ws + L.zero);
+  const int64_t ldH = mi355_mx_scale_ld(H), ldI = mi355_mx_scale_ld(I), ld2I = mi355_mx_scale_ld(2 * I);
+
+  int rc = mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, T, K, E, (int32_t*)(ws + L.counts), nullptr, group_list,
+                                  mapping, gather, nullptr, ws + L.dispatch, st);
+  if (rc) return rc;
+  if ((rc = mi355_plan_tiles(group_list, E, tile_prefix, st))) return rc;
+  if ((rc = mi355_plan_row_blocks(group_list, E, 32, block_prefix, st))) return rc;
+  if ((rc = mi355_zero_enqueue(ws + L.zero, (size_t)(H > 2 * I ? H : 2 * I), st))) return rc;
+  if ((rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), ldH, st))) return rc;
+
+  // MX grouped GEMM over the routed rows: out [R, N] bf16 = A [R, Kd] (row scales a_ld) @ W_g.
+  // Forward weights: col_data [E, Kd, N] with col_scale (b_kn); backward weights: row_data of the
+  // transposed product, [E, N, Kd] K-contiguous with row scales [E * N, Kd / 32].
+  auto gmm = [&](const uint8_t* A, const uint8_t* As, int64_t a_ld, const int32_t* a_index, int a_div, int Kd,
+                 const uint8_t* W, const uint8_t* Ws, bool b_kn, int N, uint16_t* out) {
+    GGParams p = {};
+    p.A = A;
+    p.lda_bytes = Kd;
+    p.a_row_index = a_index;
+    p.a_row_div = a_div;
+    p.a_scale = As;
+    p.a_scale_ld = a_ld;
+    p.B = W;
+    p.b_group_stride = (int64_t)Kd * N;
+    p.b_row_bytes = b_kn ? N : Kd;
+    p.b_scale = Ws;
+    p.b_scale_ld = b_kn ? 0 : Kd / 32;
+    p.b_scale_group_stride = b_kn ? (int64_t)(Kd / 64) * N * 2 : (int64_t)N * (Kd / 32);
+    p.K = Kd;
+    p.N = N;
+    p.Ntot = N;
+    p.n_tiles = (N + mi355_gg_bn() - 1) / mi355_gg_bn();
+    p.G = E;
+    p.group_list = group_list;
+    p.tile_prefix = tile_prefix;
+    p.C = out;
+    p.ldc = N;
+    return mi355_grouped_gemm(p, true, b_kn, EPI_STORE_BF16, st);
+  };
+  // Weight gradient C_g [M, N] = Q_rows(A)_g^T Q_rows(B)_g (grouped packed column scales).
+  auto wgrad = [&](const uint8_t* A, const uint8_t* As, int M, const uint8_t* B, const uint8_t* Bs, int N, void* out) {
+    GGParams p = {};
+    p.A = A;
+    p.lda_bytes = M;
+    p.a_scale = As;
+    p.B = B;
+    p.b_row_bytes = N;
+    p.b_scale = Bs;
+    p.N = N;
+    p.Ntot = N;
+    p.m_rows = M;
+    p.m_tiles = (M + mi355_gg_bm() - 1) / mi355_gg_bm();
+    p.n_tiles = (N + mi355_gg_bn() - 1) / mi355_gg_bn();
+    p.G = E;
+    p.group_list = group_list;
+    p.C = out;
+    p.ldc = N;
+    p.c_group_stride = (int64_t)M * N;
+    p.zero_row = zero;
+    return mi355_grouped_gemm_wgrad(p, f32 ? EPI_STORE_F32 : EPI_STORE_BF16, st, true);
+  };
+  auto quant = [&](int mode, const uint16_t* src, const int32_t* g_index, int g_div, int64_t src_ld, int C,
+                   size_t rowq, size_t rows, int64_t row_ld, size_t colq, size_t cols) {
+    MxGroupedQuant q = {};
+    q.mode = mode;
+    q.src = src;
+    q.gather = g_index;
+    q.gather_div = g_div;
+    q.src_ld = src_ld;
+    q.U = u;
+    q.da = da;
+    q.R = R;
+    q.C = C;
+    q.G = E;
+    q.group_list = group_list;
+    q.block_prefix = block_prefix;
+    q.row_data = rowq ? (uint8_t*)(ws + rowq) : nullptr;
+    q.row_scale = rowq ? (uint8_t*)(ws + rows) : nullptr;
+    q.row_scale_ld = row_ld;
+    q.col_data = colq ? (uint8_t*)(ws + colq) : nullptr;
+    q.col_scale = colq ? (uint8_t*)(ws + cols) : nullptr;
+    return mi355_mx_quant_grouped(q, st);
+  };
+  const uint8_t* w1 = (const uint8_t*)a.w1;
+  const uint8_t* w2 = (const uint8_t*)a.w2;
+  // forward recompute: U = Q(x) W1 (rows gathered from the tokens), act, y = Q(act) W2
+  if ((rc = gmm((const uint8_t*)(ws + L.xq), (const uint8_t*)(ws + L.xs), ldH, gather, K, H, w1, a.w1_scale, true,
+                2 * I, u)))
+    return rc;
+  if ((rc = quant(MX_Q_SWIGLU, nullptr, nullptr, 1, 0, I, L.aq, L.as, ldI, L.acol, L.acs))) return rc;
+  if ((rc = gmm((const uint8_t*)(ws + L.aq), (const uint8_t*)(ws + L.as), ldI, nullptr, 1, I, w2, a.w2_scale, true, H,
+                y)))
+    return rc;
+  // combine backward: dY = bf16(p dOut), dp = <y, dOut>
+  hipLaunchKernelGGL(dy_dp_kernel, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, gather, K, H,
+                     dy, a.grad_topk_weights);
+  if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
+  if ((rc = quant(MX_Q_BF16, dy, nullptr, 1, H, H, L.dyq, L.dys, ldH, L.dycol, L.dycs))) return rc;
+  // dW2 [E, I, H] = Q_rows(act)^T Q_rows(dY);  gA = bf16(Q_H(dY) W2_row^T)
+  if ((rc = wgrad((const uint8_t*)(ws + L.acol), (const uint8_t*)(ws + L.acs), I, (const uint8_t*)(ws + L.dycol),
+                  (const uint8_t*)(ws + L.dycs), H, a.grad_w2)))
+    return rc;
+  if ((rc = gmm((const uint8_t*)(ws + L.dyq), (const uint8_t*)(ws + L.dys), ldH, nullptr, 1, H, a.w2_row,
+                a.w2_row_scale, false, I, da)))
+    return rc;
+  // SwiGLU gradient, quantised along 2I and along the routed rows; X along the routed rows
+  if ((rc = quant(MX_Q_SWIGLU_BWD, nullptr, nullptr, 1, 0, 2 * I, L.duq, L.dus, ld2I, L.ducol, L.ducs))) return rc;
+  if ((rc = quant(MX_Q_BF16, a.hidden, gather, K, H, H, 0, 0, 0, L.xcol, L.xcs))) return rc;
+  // dW1 [E, H, 2I] = Q_rows(X)^T Q_rows(dU);  dX_routed = bf16(Q_2I(dU) W1_row^T) (into y)
+  if ((rc = wgrad((const uint8_t*)(ws + L.xcol), (const uint8_t*)(ws + L.xcs), H, (const uint8_t*)(ws + L.ducol),
+                  (const uint8_t*)(ws + L.ducs), 2 * I, a.grad_w1)))
+    return rc;
+  if ((rc = gmm((const uint8_t*)(ws + L.duq), (const uint8_t*)(ws + L.dus), ld2I, nullptr, 1, 2 * I, a.w1_row,
+                a.w1_row_scale, false, H, y)))
+    return rc;
+  return mi355_unpermute_enqueue(y, mapping, nullptr, T, K, H, a.grad_hidden, st);
+}
+
 }  // namespace
 
 extern "C" size_t mi355moe_moe_backward_workspace_size(const MI355MoeBackwardArgs* args) {
   if (args == nullptr || validate_bwd(*args) != MI355MOE_OK) return 0;
+  if (args->precision == MI355MOE_PRECISION_MXFP8) return mx_bwd_layout(*args).total;
   return bwd_layout(*args).total;
 }
 
@@ -184,6 +374,11 @@ extern "C" int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* wor
   if (T == 0) {  // no rows: the weight gradients are zero
     const int rz = mi355_zero_enqueue(a.grad_w1, (size_t)E * H * 2 * I * wsz, st);
     return rz ? rz : mi355_zero_enqueue(a.grad_w2, (size_t)E * I * H * wsz, st);
+  }
+  if (a.precision == MI355MOE_PRECISION_MXFP8) {
+    const MxBwdLayout ML = mx_bwd_layout(a);
+    if (workspace == nullptr || workspace_size < ML.total) return MI355MOE_EWORKSPACE_CODE;
+    return mx_backward(a, (char*)workspace, ML, st);
   }
   BwdLayout L = bwd_layout(a);
   if (workspace == nullptr || workspace_size < L.total) return MI355MOE_EWORKSPACE_CODE;

@@ -23,3 +23,5 @@ inline bool mi355_backward_enabled() { return MI355_PATH_ON; }
 inline bool mi355_route_grad_enabled() { return MI355_PATH_ON; }
 // Dual-axis MX weight quantisation (col and row axes of the MXFP8 weight root in one pass).
 inline bool mi355_mx_weight_prep_enabled() { return MI355_PATH_ON; }
+// MXFP8 expert backward (needs the MX K-contiguous GEMM path for its data-gradient GEMMs).
+inline bool mi355_mx_backward_enabled() { return MI355_PATH_ON; }

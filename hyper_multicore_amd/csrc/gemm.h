@@ -47,10 +47,42 @@ struct GGParams {
 
 
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, bool small = false);
-// Grouped-K bf16 GEMM (weight gradients), EPI_STORE_F32 or EPI_STORE_BF16.
-int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t stream);
+// Grouped-K GEMM (weight gradients), EPI_STORE_F32 or EPI_STORE_BF16; bf16 operands, or with `mx`
+// e4m3 operands with grouped packed column scales in a_scale / b_scale.
+int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t stream, bool mx = false);
 int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hipStream_t stream, bool small = false);
 int mi355_gg_bm(bool small = false);
+// block_prefix[g] = sum_{g' < g} ceil(rows_g' / rows) (rows-row blocks per group), [G] = the total.
+int mi355_plan_row_blocks(const int64_t* group_list, int G, int rows, int32_t* block_prefix, hipStream_t stream);
+// Routed-row MX quantisation for the MXFP8 backward (quant.hip): the row axis (blocks of 32 columns,
+// scales [R, row_scale_ld]) and / or the grouped column axis (blocks of 32 rows from each group's
+// first row; packed scales [(R + 63) / 64 + G, C, 2], group g's pairs from 64-row group
+// start_g / 64 + g) of a routed matrix [R, C] whose values are:
+//   MX_Q_BF16        bf16 rows src[(gather ? gather[r] / gather_div : r) * src_ld + c]
+//   MX_Q_SWIGLU      silu(g) * u of U [R, 2C] (the forward's fp32 activation), C = I
+//   MX_Q_SWIGLU_BWD  [da u s (1 + g (1 - s)) | da g s] from U [R, C] and da [R, C / 2], fp32
+enum { MX_Q_BF16 = 0, MX_Q_SWIGLU = 1, MX_Q_SWIGLU_BWD = 2 };
+struct MxGroupedQuant {
+  int mode;
+  const uint16_t* src;
+  const int32_t* gather;
+  int32_t gather_div;
+  int64_t src_ld;
+  const uint16_t* U;
+  const uint16_t* da;
+  int64_t R;
+  int32_t C;
+  int32_t G;
+  const int64_t* group_list;
+  const int32_t* block_prefix;  // mi355_plan_row_blocks(..., 32, ...)
+  uint8_t* row_data;
+  uint8_t* row_scale;
+  int64_t row_scale_ld;
+  uint8_t* col_data;
+  uint8_t* col_scale;
+};
+int mi355_mx_quant_grouped(const MxGroupedQuant& q, hipStream_t stream);
+int mi355_num_cus();  // CU count of the current device (cached per device)
 #include "features.h"
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {
   return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;

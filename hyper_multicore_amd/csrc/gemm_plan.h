@@ -64,6 +64,7 @@ struct GGCfg {
   static_assert(TOTAL * WG_PER_CU <= 160 * 1024, "LDS budget");
   static_assert(AS_WAVES >= 1 && AS_WAVES <= WAVES && WAVES * 64 == BN, "scale copies: 64 rows / columns a wave");
   static_assert(A_INSTR >= 1 && NI % 2 == 0 && MI >= 1, "tile shape");
+  static_assert(A_SLOTS * BS_BYTES <= 2 * AS_SLOT, "grouped-K MX: per-stage A column scales fit the AS area");
 };
 using GGBig = GGCfg<256, 2, 3, 5, 1024, 1>;
 using GGSmall = GGCfg<64, 1, 3, 3, 256, 2>;
@@ -103,26 +104,32 @@ struct CopyPlan {
   int a_k[C::A_INSTR], b_k[C::B_INSTR];      // K row of each copy within a stage
   int a_col[C::A_INSTR], b_col[C::B_INSTR];  // byte column of each copy
   int k0, k_end;           // routed-row range of the group
+  int64_t as_stage_stride; // grouped-K MX: bytes to advance the A column scales per stage
 };
 
 MI355_HD bool is_bs_wave(int wave) { return wave < 2; }
+// Grouped-K MX: waves 2 and 3 copy the per-stage column scales of A (as waves 0 and 1 do for B).
+MI355_HD bool is_as_wave(int wave) { return wave >= 2; }
+// Grouped-K mode: routed rows (K) per stage - 32 bf16 rows or 64 e4m3 rows of 256 columns.
+template <bool MX>
+constexpr int gk_rows() { return MX ? 64 : 32; }
 
 // Source of copy j at stage kt.
-template <class C, bool GK>
+template <class C, bool GK, bool MX = false>
 MI355_HD const uint8_t* a_src(const CopyPlan<C>& cp, int j, int kt) {
   if constexpr (!GK) {
     return cp.a[j] + (int64_t)kt * C::KB;
   } else {
-    const int r = cp.k0 + kt * 32 + cp.a_k[j];
+    const int r = cp.k0 + kt * gk_rows<MX>() + cp.a_k[j];
     return r < cp.k_end ? cp.a[j] + (int64_t)r * cp.lda_k : cp.zero + cp.a_col[j];
   }
 }
-template <class C, bool GK>
+template <class C, bool GK, bool MX = false>
 MI355_HD const uint8_t* b_src(const CopyPlan<C>& cp, int j, int kt) {
   if constexpr (!GK) {
     return cp.b[j] + (int64_t)kt * cp.b_stage_stride;
   } else {
-    const int r = cp.k0 + kt * 32 + cp.b_k[j];
+    const int r = cp.k0 + kt * gk_rows<MX>() + cp.b_k[j];
     return r < cp.k_end ? cp.b[j] + (int64_t)r * cp.ldb_k : cp.zero + cp.b_col[j];
   }
 }
@@ -136,7 +143,11 @@ MI355_HD void issue_a(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
   const uint32_t base = (kt % C::A_SLOTS) * C::A_BYTES;
 #pragma unroll
   for (int j = 0; j < C::A_INSTR; ++j)
-    D::template copy<16>(a_src<C, GK>(cp, j, kt), base + (wave * C::A_INSTR + j) * 1024, smem, 1);
+    D::template copy<16>(a_src<C, GK, MX>(cp, j, kt), base + (wave * C::A_INSTR + j) * 1024, smem, 1);
+  if constexpr (MX && GK)
+    if (is_as_wave(wave))
+      D::template copy<4>(cp.s + kt * cp.as_stage_stride, C::AS_OFF + (kt % C::A_SLOTS) * C::BS_BYTES + (wave & 1) * 256,
+                          smem, 1);
 }
 template <class C, bool MX, bool B_KN, bool GK, class D>
 MI355_HD void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
@@ -153,7 +164,7 @@ MI355_HD void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
   } else {
 #pragma unroll
     for (int j = 0; j < C::B_INSTR; ++j)
-      D::template copy<16>(b_src<C, GK>(cp, j, kt), base + (wave * C::B_INSTR + j) * 1024, smem, 1);
+      D::template copy<16>(b_src<C, GK, MX>(cp, j, kt), base + (wave * C::B_INSTR + j) * 1024, smem, 1);
   }
   if (MX && B_KN && is_bs_wave(wave))
     D::template copy<4>(cp.bs + kt * cp.bs_stage_stride, base + C::B_BYTES + wave * 256, smem, 1);
@@ -170,13 +181,15 @@ MI355_HD void issue_as(const CopyPlan<C>& cp, int grp, int wave, uint8_t* smem) 
 
 // Work of one pipelined K step of a wave that computes NM 32-row subtiles: MFMAs, LDS fragment
 // reads of the next stage and copy items (issue_item), interleaved by the K loop.
-template <class C, bool MX, int NM> struct StepShape {
+template <class C, bool MX, int NM, bool GK = false> struct StepShape {
   static constexpr int MFMAS = MX ? NM * C::NI : 2 * NM * C::NI;
   static constexpr int READS = MX ? C::NI + NM : 2 * (C::NI + NM);  // fragment elements of a stage
-  static constexpr int ITEMS = C::B_INSTR + 1 + C::A_INSTR;          // B copies, B scales, A copies
+  // B copies, B scales, A copies (grouped-K MX: and the A column scales)
+  static constexpr int ITEMS = C::B_INSTR + 1 + C::A_INSTR + ((MX && GK) ? 1 : 0);
 };
 
-// Copy item it of iteration i (same order as issue_iteration: B copies, B scales, A copies).
+// Copy item it of iteration i (same order as issue_iteration: B copies, B scales, A copies, and in
+// grouped-K MX mode the A column scales).
 template <class C, bool MX, bool B_KN, bool LA, bool GK, class D>
 MI355_HD void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem, int it) {
 #ifdef GG_ABLATE_DMA
@@ -185,7 +198,7 @@ MI355_HD void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t
   constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
   if (it < C::B_INSTR) {
     const int kt = i + DB;
-    D::template copy<16>(b_src<C, GK>(cp, it, kt),
+    D::template copy<16>(b_src<C, GK, MX>(cp, it, kt),
                          C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + (wave * C::B_INSTR + it) * 1024, smem, kt < nk);
   } else if (it == C::B_INSTR) {
     const int kt = i + DB;
@@ -196,19 +209,25 @@ MI355_HD void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t
   } else if constexpr (LA) {
     const int j = it - C::B_INSTR - 1;
     const int kt = i + DA;
-    D::template copy<16>(a_src<C, GK>(cp, j, kt), (kt % C::A_SLOTS) * C::A_BYTES + (wave * C::A_INSTR + j) * 1024,
-                         smem, kt < nk);
+    if (!(MX && GK) || j < C::A_INSTR) {
+      D::template copy<16>(a_src<C, GK, MX>(cp, j, kt),
+                           (kt % C::A_SLOTS) * C::A_BYTES + (wave * C::A_INSTR + j) * 1024, smem, kt < nk);
+    } else if constexpr (MX && GK) {
+      D::template copy<4>(cp.s + kt * cp.as_stage_stride,
+                          C::AS_OFF + (kt % C::A_SLOTS) * C::BS_BYTES + (wave & 1) * 256, smem,
+                          is_as_wave(wave) && kt < nk);
+    }
   }
 }
 
 // MX: the scale groups due at iteration i (every AS_GROUP stages: A rows and, for K-contiguous
 // weights, B rows), each as one conditional copy.
-template <class C, bool MX, bool B_KN, bool LA, class D>
+template <class C, bool MX, bool B_KN, bool LA, class D, bool GK = false>
 MI355_HD void issue_scales_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
 #ifdef GG_ABLATE_DMA
   if (wave < 64) return;
 #endif
-  if constexpr (MX) {
+  if constexpr (MX && !GK) {
     const int grp = i / C::AS_GROUP + 1;
     const bool due = (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk;
     if constexpr (LA)
@@ -247,10 +266,10 @@ MI355_HD void issue_iteration(const CopyPlan<C>& cp, int i, int nk, int wave, ui
   constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
   if (i + DB < nk) issue_b<C, MX, B_KN, GK, D>(cp, i + DB, wave, smem);
   if (LA && i + DA >= 0 && i + DA < nk) {
-    if (MX && i + DA == 0) issue_as<C, D>(cp, 0, wave, smem);
+    if (MX && !GK && i + DA == 0) issue_as<C, D>(cp, 0, wave, smem);
     issue_a<C, MX, GK, D>(cp, i + DA, wave, smem);
   }
-  if (LA && MX && i >= 0 && (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk)
+  if (LA && MX && !GK && i >= 0 && (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk)
     issue_as<C, D>(cp, i / C::AS_GROUP + 1, wave, smem);
 }
 

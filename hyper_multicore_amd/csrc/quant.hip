@@ -155,6 +155,95 @@ extern "C" int mi355moe_mx_quantize_weight(const uint16_t* w, int32_t groups, in
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
+// ---- routed-row MX quantisation (MXFP8 backward) ---------------------------------------------
+// One workgroup per (32-row block of a group, 256 columns); thread c owns column c0 + c, as in the
+// dual weight kernel: the column block is in-thread, each row block a 32-lane reduction.
+template <int MODE>
+MI355_DEV float mx_q_value(const MxGroupedQuant& q, int64_t r, int c) {
+  if constexpr (MODE == MX_Q_BF16) {
+    const int64_t sr = q.gather != nullptr ? (int64_t)(q.gather[r] / q.gather_div) : r;
+    return bf16_to_f32(q.src[sr * q.src_ld + c]);
+  } else if constexpr (MODE == MX_Q_SWIGLU) {
+    const int I = q.C;
+    const float gte = bf16_to_f32(q.U[r * 2 * I + c]);
+    const float up = bf16_to_f32(q.U[r * 2 * I + I + c]);
+    return gte / (1.0f + __expf(-gte)) * up;
+  } else {
+    const int I = q.C / 2;
+    const int cc = c < I ? c : c - I;
+    const float g = bf16_to_f32(q.U[r * 2 * I + cc]);
+    const float a = bf16_to_f32(q.da[r * I + cc]);
+    const float s = 1.0f / (1.0f + __expf(-g));
+    if (c < I) return a * bf16_to_f32(q.U[r * 2 * I + I + cc]) * s * (1.0f + g * (1.0f - s));
+    return a * (g * s);
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void mx_quant_grouped_kernel(MxGroupedQuant q) {
+  const int bi = blockIdx.y;
+  if (bi >= q.block_prefix[q.G]) return;
+  int lo = 0, hi = q.G - 1;
+  while (lo < hi) {  // largest g with block_prefix[g] <= bi
+    const int mid = (lo + hi + 1) >> 1;
+    if (q.block_prefix[mid] <= bi) lo = mid; else hi = mid - 1;
+  }
+  const int g = lo;
+  const int64_t start = g == 0 ? 0 : q.group_list[g - 1];
+  const int64_t n = q.group_list[g] - start;
+  const int b = bi - q.block_prefix[g];
+  const int64_t r0 = start + 32 * (int64_t)b;
+  const int nrows = (int)((n - 32 * (int64_t)b) < 32 ? (n - 32 * (int64_t)b) : 32);
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const bool live = c < q.C;  // C % 32 == 0: half-waves are uniformly live or dead
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    v[i] = (live && i < nrows) ? mx_q_value<MODE>(q, r0 + i, c) : 0.0f;
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  if (q.col_data != nullptr && live) {
+    const uint32_t code = mx_scale_code(amax);
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (i < nrows) q.col_data[(r0 + i) * q.C + c] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+    uint8_t* pair = q.col_scale + ((start / 64 + g + b / 2) * q.C + c) * 2;
+    pair[b & 1] = (uint8_t)code;
+    if (!(b & 1) && 32 * (int64_t)(b + 1) >= n) pair[1] = 0;  // the pair's second block lies past the group
+  }
+  if (q.row_data != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      float a = fabsf(v[i]);
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
+      const uint32_t code = mx_scale_code(a);
+      if (live && i < nrows) {
+        q.row_data[(r0 + i) * q.C + c] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+        if ((threadIdx.x & 31) == 0) q.row_scale[(r0 + i) * q.row_scale_ld + c / 32] = (uint8_t)code;
+      }
+    }
+  }
+}
+
+int mi355_mx_quant_grouped(const MxGroupedQuant& q, hipStream_t st) {
+  if (q.R <= 0) return MI355MOE_OK;
+  if (q.C <= 0 || q.C % 32 || q.G <= 0 || q.group_list == nullptr || q.block_prefix == nullptr) return MI355MOE_EINVAL;
+  const int64_t max_blocks = (q.R + 31) / 32 + q.G;  // the device-planned count never exceeds this
+  if (max_blocks > 65535) return MI355MOE_EUNSUPPORTED;
+  const dim3 grid((unsigned)((q.C + 255) / 256), (unsigned)max_blocks);
+  switch (q.mode) {
+    case MX_Q_BF16: hipLaunchKernelGGL(mx_quant_grouped_kernel<MX_Q_BF16>, grid, dim3(256), 0, st, q); break;
+    case MX_Q_SWIGLU: hipLaunchKernelGGL(mx_quant_grouped_kernel<MX_Q_SWIGLU>, grid, dim3(256), 0, st, q); break;
+    case MX_Q_SWIGLU_BWD:
+      hipLaunchKernelGGL(mx_quant_grouped_kernel<MX_Q_SWIGLU_BWD>, grid, dim3(256), 0, st, q);
+      break;
+    default: return MI355MOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
 // ---- MX weight re-layout: [G, K, N] (+ col_scale [G, K/64, N, 2]) -> [G, N, K] (+ [G, N, ld]) ----
 // One 64 (K) x 64 (N) byte tile per workgroup, transposed through LDS.
 __global__ __launch_bounds__(256) void mx_weight_to_eoi_kernel(const uint8_t* src, int K, int N, uint8_t* dst) {

@@ -55,6 +55,7 @@ enum {
   MI355MOE_FEATURE_BACKWARD = 8,      /* mi355moe_moe_backward */
   MI355MOE_FEATURE_ROUTE_GRAD = 16,   /* mi355moe_gate_route_grad */
   MI355MOE_FEATURE_MX_WEIGHT_PREP = 32, /* mi355moe_mx_quantize_weight */
+  MI355MOE_FEATURE_MX_BACKWARD = 64,  /* mi355moe_moe_backward with precision MXFP8 */
 };
 int mi355moe_features(void);
 
@@ -330,6 +331,17 @@ int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* workspace, size_
  *   dW2_e = act_e^T dY_e, dW1_e = X_e^T dU_e (fp32 accumulate, stored in weight_grad_dtype),
  *   dX[t] = bf16(sum_k bf16(dU W1^T)[r]).
  * Gradients have the weights' layout. grad_topk_weights may be NULL.
+ *
+ * precision MXFP8 (EIO weights only, the reference's MX roots): w1 / w2 are the forward axis
+ * col_data with w1_scale / w2_scale col_scale (as for mi355moe_moe_forward), and w1_row / w2_row
+ * with w1_row_scale / w2_row_scale the backward axis row_data [E, M, N] / row_scale [E, M, N/64, 2]
+ * (mi355moe_mx_quantize_weight). The graph follows the reference's MX backward
+ * (modules/mega_moe/backends/mxfp8/graph.py:147-154, execution.py:119-164): forward recompute
+ * (U bf16, act fp32 quantised along I and along the routed rows, y bf16), dY and dp as above,
+ * dY quantised along H and along the routed rows (32-row blocks from each expert's first row),
+ * dW2 = Q_rows(act)^T Q_rows(dY), gA = bf16(Q_H(dY) W2_row^T), the SwiGLU gradient kept in fp32
+ * and quantised along 2I and along the routed rows, dW1 = Q_rows(X)^T Q_rows(dU),
+ * dX_routed = bf16(Q_2I(dU) W1_row^T), dX = bf16(sum_k dX_routed). H % 512 == 0, I % 256 == 0.
  */
 enum { MI355MOE_GRAD_BF16 = 0, MI355MOE_GRAD_FP32 = 1 };
 typedef struct MI355MoeBackwardArgs {
@@ -351,7 +363,13 @@ typedef struct MI355MoeBackwardArgs {
   void* grad_w2;              /* like w2, weight_grad_dtype */
   float* grad_topk_weights;   /* optional [T, K] fp32 */
   int32_t weight_grad_dtype;  /* MI355MOE_GRAD_* (partial_weight_grad_dtype native / float32) */
-  int32_t reserved;
+  int32_t precision;          /* MI355MOE_PRECISION_* (0 = BF16) */
+  const uint8_t* w1_scale;    /* MXFP8: col_scale [E, H/64, 2I, 2] */
+  const uint8_t* w2_scale;    /* MXFP8: col_scale [E, I/64, H, 2] */
+  const uint8_t* w1_row;      /* MXFP8: row_data [E, H, 2I] e4m3 */
+  const uint8_t* w2_row;      /* MXFP8: row_data [E, I, H] e4m3 */
+  const uint8_t* w1_row_scale; /* MXFP8: row_scale [E, H, 2I/64, 2] */
+  const uint8_t* w2_row_scale; /* MXFP8: row_scale [E, I, H/64, 2] */
 } MI355MoeBackwardArgs;
 size_t mi355moe_moe_backward_workspace_size(const MI355MoeBackwardArgs* args);
 int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* workspace, size_t workspace_size,

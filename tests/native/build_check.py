@@ -24,10 +24,10 @@ OUT = HERE / "_build"
 LIB_SOURCES = ["api.hip", "backward.hip", "dispatch.hip", "quant.hip", "gemm.hip"]
 # internal functions defined by the checker instead (made weak in the library objects)
 REPLACED = {
-    "gemm.hip": ["mi355_grouped_gemm", "mi355_grouped_gemm_wgrad", "mi355_plan_tiles"],
+    "gemm.hip": ["mi355_grouped_gemm", "mi355_plan_tiles", "mi355_plan_row_blocks"],
     "dispatch.hip": ["mi355_dispatch_enqueue", "mi355_permute_rows_enqueue", "mi355_unpermute_enqueue",
                      "mi355_zero_enqueue"],
-    "quant.hip": ["mi355_mx_quant_rows"],
+    "quant.hip": ["mi355_mx_quant_rows", "mi355_mx_quant_grouped"],
 }
 FLAGS = ["-x", "hip", "--cuda-host-only", "-O1", "-g", "-std=c++17", "-fsanitize=address",
          "-fno-omit-frame-pointer", "-DMI355_CHECK_ALL_PATHS", "-Wno-unused-result", "-Wno-unused-variable",

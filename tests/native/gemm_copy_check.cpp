@@ -142,6 +142,61 @@ int mi355_plan_tiles(const int64_t* group_list, int G, int32_t* tile_prefix, hip
   return MI355MOE_OK;
 }
 
+int mi355_plan_row_blocks(const int64_t* group_list, int G, int rows, int32_t* prefix, hipStream_t) {
+  if (!find_alloc(prefix, (size_t)(G + 1) * 4)) CHECK_FAIL("block prefix of %d groups outside its buffer", G);
+  int64_t acc = 0;
+  for (int g = 0; g < G; ++g) {
+    const int64_t n = group_list[g] - (g ? group_list[g - 1] : 0);
+    prefix[g] = (int32_t)acc;
+    acc += n > 0 ? (n + rows - 1) / rows : 0;
+  }
+  prefix[G] = (int32_t)acc;
+  return MI355MOE_OK;
+}
+
+// The routed-row MX quantisation (quant.hip mx_quant_grouped_kernel) replayed for its addresses: every
+// block's reads of its source and writes of data and scales must stay inside their allocations, and
+// the launch must cover every planned block.
+static void check_span(const void* base, int64_t lo, int64_t hi, const char* what) {
+  if (hi > lo && !find_alloc((const uint8_t*)base + lo, (size_t)(hi - lo)))
+    CHECK_FAIL("%s: bytes %lld..%lld outside every allocation", what, (long long)lo, (long long)hi);
+}
+int mi355_mx_quant_grouped(const MxGroupedQuant& q, hipStream_t) {
+  if (q.R <= 0) return MI355MOE_OK;
+  if (q.C <= 0 || q.C % 32 || q.G <= 0 || q.group_list == nullptr || q.block_prefix == nullptr) return MI355MOE_EINVAL;
+  const int64_t max_blocks = (q.R + 31) / 32 + q.G;
+  if (q.block_prefix[q.G] > max_blocks) CHECK_FAIL("planned %d row blocks, launch covers %lld", q.block_prefix[q.G],
+                                                   (long long)max_blocks);
+  for (int g = 0; g < q.G; ++g) {
+    const int64_t start = g ? q.group_list[g - 1] : 0, n = q.group_list[g] - start;
+    for (int64_t b = 0; 32 * b < n; ++b) {
+      const int64_t r0 = start + 32 * b, nrows = std::min<int64_t>(32, n - 32 * b);
+      for (int64_t i = 0; i < nrows; ++i) {
+        const int64_t r = r0 + i;
+        if (q.mode == MX_Q_BF16) {
+          const int64_t sr = q.gather ? q.gather[r] / q.gather_div : r;
+          check_span(q.src, sr * q.src_ld * 2, (sr * q.src_ld + q.C) * 2, "quant source row");
+        } else if (q.mode == MX_Q_SWIGLU) {
+          check_span(q.U, r * 2 * q.C * 2, (r + 1) * 2 * q.C * 2, "quant U row");
+        } else {
+          check_span(q.U, r * q.C * 2, (r + 1) * q.C * 2, "quant U row");
+          check_span(q.da, r * (q.C / 2) * 2, (r + 1) * (q.C / 2) * 2, "quant gA row");
+        }
+        if (q.row_data) {
+          check_span(q.row_data, r * q.C, (r + 1) * q.C, "row-axis data");
+          check_span(q.row_scale, r * q.row_scale_ld, r * q.row_scale_ld + q.C / 32, "row-axis scales");
+        }
+        if (q.col_data) check_span(q.col_data, r * q.C, (r + 1) * q.C, "column-axis data");
+      }
+      if (q.col_data) {
+        const int64_t pair = (start / 64 + g + b / 2) * q.C * 2;
+        check_span(q.col_scale, pair, pair + (int64_t)q.C * 2, "column-axis scales");
+      }
+    }
+  }
+  return MI355MOE_OK;
+}
+
 // Stable counting sort of the T*K slots by expert id (the dispatch contract of include/mi355moe.h).
 int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t T, int K, int E, int32_t* counts, int64_t* offsets,
                            int64_t* group_list, int32_t* mapping, int32_t* gather, int32_t* error_flag, void*,
@@ -274,9 +329,10 @@ struct CheckDma {
   }
 };
 
-enum Region { R_A = 0, R_B, R_BS, R_AS, R_BSR, R_N };
+// R_ASS: grouped-K MX only - the per-stage column scales of A, A_SLOTS slots of 512 bytes at AS_OFF
+enum Region { R_A = 0, R_B, R_BS, R_AS, R_BSR, R_ASS, R_N };
 static const char* region_name(int r) {
-  static const char* n[] = {"A", "B", "B-scale", "A-scale", "B-row-scale"};
+  static const char* n[] = {"A", "B", "B-scale", "A-scale", "B-row-scale", "A-column-scale"};
   return n[r];
 }
 
@@ -295,8 +351,9 @@ static void record_schedule(const CopyPlan<C>& cp, int nk, int wave, std::vector
     for (int k = 0; k < nk - 1; ++k) {
       waits.push_back({rec.size(), k + 1, younger_than<C, LA>(k + 1, k - 1, nk, la_n, lb_n)});
       g_iter = k;
-      for (int it = 0; it < StepShape<C, MX, 1>::ITEMS; ++it) issue_item<C, MX, B_KN, LA, GK, D>(cp, k, nk, wave, smem, it);
-      issue_scales_item<C, MX, B_KN, LA, D>(cp, k, nk, wave, smem);
+      for (int it = 0; it < StepShape<C, MX, 1, GK>::ITEMS; ++it)
+        issue_item<C, MX, B_KN, LA, GK, D>(cp, k, nk, wave, smem, it);
+      issue_scales_item<C, MX, B_KN, LA, D, GK>(cp, k, nk, wave, smem);
     }
   }
   g_rec = nullptr;
@@ -318,8 +375,15 @@ struct Decoded {
 };
 
 template <class C>
-static bool classify(uint32_t pos, int sz, Decoded& d) {
+static bool classify(uint32_t pos, int sz, Decoded& d, bool gk_mx) {
   if (pos + sz > (uint32_t)C::PREFIX_OFF) return false;
+  if (gk_mx && pos >= (uint32_t)C::AS_OFF && pos < (uint32_t)C::BSR_OFF) {
+    const uint32_t q = pos - C::AS_OFF;
+    d.region = R_ASS;
+    d.slot = q / C::BS_BYTES;
+    d.rel = q % C::BS_BYTES;
+    return d.rel + sz <= (uint32_t)C::BS_BYTES;
+  }
   if (pos < (uint32_t)C::B_OFF) {
     d.region = R_A;
     d.slot = pos / C::A_BYTES;
@@ -361,25 +425,28 @@ static const uint8_t* expected_src(const GGParams& p, const Layout& L, const Ite
   *zero_ok = false;
   int64_t wcol;
   if constexpr (GK) {
-    // both operands K-major: K row k (32 per stage) at k*512, 16-byte chunk c stored at c ^ ((k&7)<<1)
-    const int k = rel / 512, cpos = (rel % 512) / 16, c = cpos ^ ((k & 7) << 1);
-    const int64_t row = (int64_t)it.k0 + (int64_t)stage * 32 + k;
-    if (region == R_A) {
-      const int64_t m = (int64_t)it.m0 + c * 8;
-      if (m >= p.m_rows) return nullptr;
-      if (row >= it.kend) {
-        *zero_ok = true;
-        return nullptr;
-      }
-      return L.A + row * L.a_row_bytes + m * 2;
+    // both operands K-major. bf16: K row k (32 per stage) at k*512, chunk c stored at c ^ ((k&7)<<1),
+    // 8 columns per chunk; MX: K row k (64 per stage) at k*256, chunk c at c ^ (k & 15), 16 columns
+    constexpr int ES = MX ? 1 : 2;
+    constexpr int RB = MX ? 256 : 512;
+    if (region == R_BS || region == R_ASS) {  // MX: two codes for each of columns 2m, 2m+1 per stage
+      const int64_t grp = (int64_t)(it.k0 / 64) + it.g + stage;
+      const int64_t col = (region == R_ASS ? (int64_t)it.m0 : (int64_t)it.nt * C::BN) + (rel / 4) * 2;
+      const int64_t cols = region == R_ASS ? p.m_rows : p.N;
+      if (col >= cols) return nullptr;
+      return (region == R_ASS ? p.a_scale : p.b_scale) + (grp * cols + col) * 2;
     }
-    const int64_t n = (int64_t)it.nt * C::BN + c * 8;
-    if (n >= p.N) return nullptr;
+    const int k = rel / RB, cpos = (rel % RB) / 16;
+    const int c = MX ? (cpos ^ (k & 15)) : (cpos ^ ((k & 7) << 1));
+    const int64_t row = (int64_t)it.k0 + (int64_t)stage * (MX ? 64 : 32) + k;
+    const int64_t col = (region == R_A ? (int64_t)it.m0 : (int64_t)it.nt * C::BN) + c * (16 / ES);
+    if (col >= (region == R_A ? p.m_rows : p.N)) return nullptr;
     if (row >= it.kend) {
       *zero_ok = true;
       return nullptr;
     }
-    return L.B + row * L.Ntot * 2 + n * 2;
+    if (region == R_A) return L.A + row * L.a_row_bytes + col * ES;
+    return L.B + row * L.Ntot * ES + col * ES;
   } else {
     const int64_t kstage = (int64_t)it.split * it.nk + stage;  // stage index along the full K
     switch (region) {
@@ -428,8 +495,8 @@ static const uint8_t* expected_src(const GGParams& p, const Layout& L, const Ite
 template <class C, bool MX, bool B_KN, bool SWIGLU, bool GK>
 static void check_lane(const GGParams& p, const Layout& L, ItemCtx& it, int wave, int lane, bool la,
                        const std::vector<Rec>& rec, const std::vector<Wait>& waits) {
-  const int slots[R_N] = {C::A_SLOTS, C::B_SLOTS, C::B_SLOTS, 2, 2};
-  const int per_fill[R_N] = {C::A_INSTR, C::B_INSTR, 1, 1, 1};
+  const int slots[R_N] = {C::A_SLOTS, C::B_SLOTS, C::B_SLOTS, 2, 2, C::A_SLOTS};
+  const int per_fill[R_N] = {C::A_INSTR, C::B_INSTR, 1, 1, 1, 1};
   int fills[R_N][8] = {};
   std::vector<Decoded> dec(rec.size());
   for (size_t i = 0; i < rec.size(); ++i) {
@@ -444,8 +511,8 @@ static void check_lane(const GGParams& p, const Layout& L, ItemCtx& it, int wave
     Decoded& d = dec[i];
     Decoded first_lane, last_lane;
     const uint32_t pos = r.off + (uint32_t)r.sz * lane;
-    const bool ok = classify<C>(pos, r.sz, d) && classify<C>(r.off, r.sz, first_lane) &&
-                    classify<C>(r.off + 63u * r.sz, r.sz, last_lane) && first_lane.region == last_lane.region &&
+    const bool ok = classify<C>(pos, r.sz, d, GK && MX) && classify<C>(r.off, r.sz, first_lane, GK && MX) &&
+                    classify<C>(r.off + 63u * r.sz, r.sz, last_lane, GK && MX) && first_lane.region == last_lane.region &&
                     first_lane.slot == last_lane.slot;
     if (!ok) {
       CHECK_FAIL("copy %zu (wave %d lane %d) writes LDS %u..%u outside one ring slot", i, wave, lane, r.off,
@@ -500,7 +567,7 @@ static void check_lane(const GGParams& p, const Layout& L, ItemCtx& it, int wave
     const int unit = d.region == R_A ? C::A_BYTES
                    : d.region == R_B ? C::B_BYTES
                    : d.region == R_BS ? C::BS_BYTES
-                   : d.region == R_AS ? C::AS_SLOT : C::BSR_SLOT;
+                   : d.region == R_AS ? C::AS_SLOT : d.region == R_BSR ? C::BSR_SLOT : C::BS_BYTES;
     const size_t base = (size_t)d.stage * unit + d.rel;
     if (base + r.sz <= cov.size())
       for (int b = 0; b < r.sz; ++b) {
@@ -546,7 +613,8 @@ static void check_coverage(const ItemCtx& it) {
   else full(R_A, it.nk, C::A_BYTES, it.rows_valid * 64, "activation stage");
   if (MX && B_KN) full(R_BS, it.nk, C::BS_BYTES, C::BS_BYTES, "weight scale stage");
   if (MX && !B_KN) full(R_BSR, ngroups, C::BSR_SLOT, C::BSR_SLOT, "weight row-scale group");
-  if (MX) full(R_AS, ngroups, C::AS_SLOT, it.rows_valid * 16, "activation scale group");
+  if (MX && !GK) full(R_AS, ngroups, C::AS_SLOT, it.rows_valid * 16, "activation scale group");
+  if (MX && GK) full(R_ASS, it.nk, C::BS_BYTES, C::BS_BYTES, "A column-scale stage");
 }
 
 static void check_range(const void* base, int64_t lo, int64_t hi, const char* what) {
@@ -646,19 +714,20 @@ static int sim_forward(const GGParams& p) {
   return MI355MOE_OK;
 }
 
-template <class C, int EPI>
+template <class C, bool MX, int EPI>
 static int sim_wgrad(const GGParams& p) {
   ++g_gemms;
   if (!find_alloc(p.group_list, (size_t)p.G * 8)) CHECK_FAIL("group list outside its buffer");
   const int per_g = p.m_tiles * p.n_tiles;
   const int total = p.G * per_g;
-  Layout Lo = {p.A, p.lda_bytes, nullptr, 1, nullptr, 0, p.B, false, 0, 0, 2, nullptr, 0};
+  constexpr int ES = MX ? 1 : 2;
+  Layout Lo = {p.A, p.lda_bytes, nullptr, 1, nullptr, 0, p.B, false, 0, 0, ES, nullptr, 0};
   if (g_expect.set) {
     Lo.A = g_expect.A;
     Lo.a_row_bytes = g_expect.a_row_bytes;
     Lo.B = g_expect.B;
   }
-  Lo.Ntot = p.b_row_bytes / 2;  // B rows hold N bf16 (grouped-K: row stride of the routed rows)
+  Lo.Ntot = p.b_row_bytes / ES;  // B rows hold N elements (grouped-K: row stride of the routed rows)
   if (g_expect.set) Lo.Ntot = p.N;
   for (int L_item = 0; L_item < total; ++L_item) {
     ItemCtx ctx;
@@ -683,6 +752,8 @@ static int sim_wgrad(const GGParams& p) {
           ctx.rows_valid = rows_valid;
           ctx.cov[R_A].assign((size_t)std::max(nk, 0) * C::A_BYTES, 0);
           ctx.cov[R_B].assign((size_t)std::max(nk, 0) * C::B_BYTES, 0);
+          ctx.cov[R_BS].assign((size_t)std::max(nk, 0) * C::BS_BYTES, 0);
+          ctx.cov[R_ASS].assign((size_t)std::max(nk, 0) * C::BS_BYTES, 0);
           const int64_t cols = std::min<int64_t>(C::BN, p.N - (int64_t)nt * C::BN);
           const int esz = EPI == EPI_STORE_F32 ? 4 : 2;
           const int64_t at0 = (int64_t)g * p.c_group_stride + (int64_t)m0 * p.ldc + (int64_t)nt * C::BN;
@@ -692,10 +763,10 @@ static int sim_wgrad(const GGParams& p) {
         if (nk <= 0) continue;
         rec.clear();
         waits.clear();
-        record_schedule<C, false, true, true, true>(cp, nk, wave, rec, waits);
-        check_lane<C, false, true, false, true>(p, Lo, ctx, wave, lane, true, rec, waits);
+        record_schedule<C, MX, true, true, true>(cp, nk, wave, rec, waits);
+        check_lane<C, MX, true, false, true>(p, Lo, ctx, wave, lane, true, rec, waits);
       }
-    if (ctx.nk > 0) check_coverage<C, false, true, true>(ctx);
+    if (ctx.nk > 0) check_coverage<C, MX, true, true>(ctx);
   }
   return MI355MOE_OK;
 }
@@ -745,12 +816,18 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   }
   return sim_dispatch<GGBig>(p, mx, b_kn, epi);
 }
-int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t) {
-  if (p.m_rows % 8 || p.N % 8 || p.m_tiles != (p.m_rows + GGBig::BM - 1) / GGBig::BM ||
+int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t, bool mx) {
+  // the checks of gemm_wgrad.hip's mi355_grouped_gemm_wgrad
+  const int align = mx ? 16 : 8;
+  if (p.m_rows % align || p.N % align || p.m_tiles != (p.m_rows + GGBig::BM - 1) / GGBig::BM ||
       p.n_tiles != (p.N + GGBig::BN - 1) / GGBig::BN || p.zero_row == nullptr)
     return MI355MOE_EINVAL;
-  if (epi == EPI_STORE_F32) return sim_wgrad<GGBig, EPI_STORE_F32>(p);
-  if (epi == EPI_STORE_BF16) return sim_wgrad<GGBig, EPI_STORE_BF16>(p);
+  if (mx && (p.a_scale == nullptr || p.b_scale == nullptr)) return MI355MOE_EINVAL;
+  const Alloc* z = alloc_of(p.zero_row);
+  const int64_t need = (int64_t)std::max(p.m_rows, p.N) * (mx ? 1 : 2);
+  if (!z || p.zero_row + need > z->p + z->n) CHECK_FAIL("zero row shorter than %lld bytes", (long long)need);
+  if (epi == EPI_STORE_F32) return mx ? sim_wgrad<GGBig, true, EPI_STORE_F32>(p) : sim_wgrad<GGBig, false, EPI_STORE_F32>(p);
+  if (epi == EPI_STORE_BF16) return mx ? sim_wgrad<GGBig, true, EPI_STORE_BF16>(p) : sim_wgrad<GGBig, false, EPI_STORE_BF16>(p);
   return MI355MOE_EUNSUPPORTED;
 }
 
@@ -889,14 +966,16 @@ static void moe_forward(int64_t T, int K, int E, int H, int I, int precision, in
   expect_rc(mi355moe_moe_forward(&a, ws, wsz, nullptr), 0, "moe_forward");
 }
 
-static void moe_backward(int64_t T, int K, int E, int H, int I, int layout, int grad_dtype, double skew) {
+static void moe_backward(int64_t T, int K, int E, int H, int I, int layout, int grad_dtype, double skew,
+                         bool mx = false) {
   const auto idv = route_ids(T, K, E, skew);
   uint8_t* hidden = mk("hidden", (size_t)T * H * 2);
   int64_t* ids = (int64_t*)mk("topk_ids", idv.size() * 8);
   memcpy(ids, idv.data(), idv.size() * 8);
   float* wts = (float*)mk("topk_weights", (size_t)T * K * 4, 0);
-  uint8_t* w1 = mk("w1", (size_t)E * H * 2 * I * 2);
-  uint8_t* w2 = mk("w2", (size_t)E * I * H * 2);
+  const int esz = mx ? 1 : 2;
+  uint8_t* w1 = mk("w1", (size_t)E * H * 2 * I * esz);
+  uint8_t* w2 = mk("w2", (size_t)E * I * H * esz);
   uint8_t* gout = mk("grad_out", (size_t)T * H * 2);
   uint8_t* gh = mk("grad_hidden", (size_t)T * H * 2);
   const int gsz = grad_dtype == MI355MOE_GRAD_FP32 ? 4 : 2;
@@ -922,6 +1001,15 @@ static void moe_backward(int64_t T, int K, int E, int H, int I, int layout, int 
   a.grad_w2 = gw2;
   a.grad_topk_weights = gp;
   a.weight_grad_dtype = grad_dtype;
+  if (mx) {
+    a.precision = MI355MOE_PRECISION_MXFP8;
+    a.w1_scale = mk("w1_col_scale", (size_t)E * (H / 64) * 2 * I * 2);
+    a.w2_scale = mk("w2_col_scale", (size_t)E * (I / 64) * H * 2);
+    a.w1_row = mk("w1_row_data", (size_t)E * H * 2 * I);
+    a.w2_row = mk("w2_row_data", (size_t)E * I * H);
+    a.w1_row_scale = mk("w1_row_scale", (size_t)E * H * (2 * I / 32));
+    a.w2_row_scale = mk("w2_row_scale", (size_t)E * I * (H / 32));
+  }
   const size_t wsz = mi355moe_moe_backward_workspace_size(&a);
   uint8_t* ws = mk("workspace", wsz);
   g_expect = Expect();
@@ -994,6 +1082,8 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"bwd_eio_f32", [=] { moe_backward(96, 4, 8, 256, 128, L_EIO, MI355MOE_GRAD_FP32, 1.1); }});
   s.push_back({"bwd_eoi_bf16", [=] { moe_backward(96, 4, 8, 256, 128, L_EOI, MI355MOE_GRAD_BF16, 1.1); }});
   s.push_back({"bwd_eio_bf16_prefill", [=] { moe_backward(300, 2, 3, 384, 256, L_EIO, MI355MOE_GRAD_BF16, 0.0); }});
+  s.push_back({"bwd_mx_f32", [=] { moe_backward(96, 4, 8, 512, 256, L_EIO, MI355MOE_GRAD_FP32, 1.1, true); }});
+  s.push_back({"bwd_mx_bf16_prefill", [=] { moe_backward(300, 2, 3, 1024, 512, L_EIO, MI355MOE_GRAD_BF16, 0.0, true); }});
   return s;
 }
 

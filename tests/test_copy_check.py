@@ -38,7 +38,7 @@ SCENARIOS = [
     "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi",
     "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
     "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2",
-    "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill",
+    "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill",
 ]
 
 
