@@ -10,7 +10,9 @@ on first use); MXFP8 weights are MX roots carrying ``col_data`` (e4m3fn, EIO) an
 Gradients: with the library's backward switched on (``ops.features()``), a bf16 forward under
 autograd with default numerics records a function whose backward computes the gradients of the
 hidden states, both expert weights and the routing weights on the GPU; otherwise the output carries
-no autograd history. The BF16 numerics options (``swiglu_limit``, ``clamp_after_silu``, ``apply_probs_before_fc2``) run
+no autograd history. MXFP8 likewise once the library reports its MX backward on: the backward reads
+the roots' ``row_data`` / ``row_scale`` axis (``quantize_expert_weight(w, backward_axis=True)``) and
+returns the root gradients in the roots' dtype. The BF16 numerics options (``swiglu_limit``, ``clamp_after_silu``, ``apply_probs_before_fc2``) run
 when the loaded library reports them switched on (``ops.features()``), otherwise the constructor
 raises ``NotImplementedError``; MXFP8 rejects them as the reference does. ``ep_group`` must be
 ``None`` or a group of size 1.
@@ -109,6 +111,41 @@ class _MoeFunction(torch.autograd.Function):
                                           need_topk_grad=ctx.needs_input_grad[1])
         gp = gp.to(topk_weights.dtype) if gp is not None else None
         return gx, gp, g1, g2, None, None, None, None, None
+
+
+class _MxMoeFunction(torch.autograd.Function):
+    """MXFP8 expert forward with the library's MX backward (mxfp8/autograd.py:35-86 role): the forward
+    reads the roots' column axis, the backward resolves the roots again and reads both axes (the
+    reference re-resolves after its parameter hooks); forward intermediates are recomputed."""
+
+    @staticmethod
+    def forward(ctx, hidden, topk_weights, root1, root2, topk_ids, executor, weight_grad_dtype):
+        layout, d1, s1, d2, s2 = executor._mx_weights(hidden, (root1, root2))
+        ctx.save_for_backward(hidden, topk_weights, topk_ids)
+        ctx.roots = (root1, root2)
+        ctx.meta = (executor.num_experts, executor.hidden_size, executor.intermediate_size, weight_grad_dtype)
+        return ops.moe_forward(hidden, topk_ids, topk_weights, d1, d2, num_experts=executor.num_experts,
+                               intermediate_size=executor.intermediate_size, precision="mxfp8", layout=layout,
+                               w1_scale=s1, w2_scale=s2)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        from .mxfp8 import resolve_backward_weight, resolve_forward_weight
+        hidden, topk_weights, topk_ids = ctx.saved_tensors
+        E, H, I, grad_dtype = ctx.meta
+        r1, r2 = ctx.roots
+        fields = []
+        for root, shape in ((r1, (E, H, 2 * I)), (r2, (E, I, H))):
+            col = resolve_forward_weight(root, shape, hidden.device)
+            row = resolve_backward_weight(root, shape, hidden.device)
+            fields.append((*col, *row))
+        gx, g1, g2, gp = ops.moe_backward_mxfp8(hidden, topk_ids, topk_weights, fields[0], fields[1], grad_out,
+                                                num_experts=E, intermediate_size=I, weight_grad_dtype=grad_dtype,
+                                                need_topk_grad=ctx.needs_input_grad[1])
+        g1 = g1.reshape(r1.shape).to(r1.dtype) if ctx.needs_input_grad[2] else None
+        g2 = g2.reshape(r2.shape).to(r2.dtype) if ctx.needs_input_grad[3] else None
+        gp = gp.to(topk_weights.dtype) if gp is not None else None
+        return gx, gp, g1, g2, None, None, None
 
 
 class MegaMoeExperts(torch.nn.Module):
@@ -292,6 +329,15 @@ class MegaMoeExperts(torch.nn.Module):
                                       clamp_after_silu=nm.clamp_after_silu,
                                       apply_probs_before_fc2=nm.apply_probs_before_fc2)
         else:
+            roots = tuple(expert_weights) if isinstance(expert_weights, (tuple, list)) else ()
+            wants_grad = torch.is_grad_enabled() and (
+                flat.requires_grad or topk_weights.requires_grad
+                or any(isinstance(r, torch.Tensor) and r.requires_grad for r in roots))
+            if wants_grad and len(roots) == 2 and ops.features() & _lib.FEATURE_MX_BACKWARD:
+                nm = self._numerics
+                grad_dtype = torch.float32 if nm.partial_weight_grad_dtype == "float32" else torch.bfloat16
+                out = _MxMoeFunction.apply(flat, topk_weights, roots[0], roots[1], topk_ids, self, grad_dtype)
+                return out.reshape(hidden_states.shape)
             layout, d1, s1, d2, s2 = self._mx_weights(flat, expert_weights)
             out = ops.moe_forward(flat, topk_ids, topk_weights, d1, d2, num_experts=self.num_experts,
                                   intermediate_size=self.intermediate_size, precision="mxfp8", layout=layout,

@@ -12,7 +12,7 @@ import torch
 
 from . import _lib, ops
 
-__all__ = ["quantize_expert_weight", "resolve_forward_weight", "prepared_eoi_weight"]
+__all__ = ["quantize_expert_weight", "resolve_forward_weight", "resolve_backward_weight", "prepared_eoi_weight"]
 
 
 def quantize_expert_weight(weight: torch.Tensor, *, backward_axis: bool = False) -> torch.Tensor:
@@ -61,6 +61,25 @@ def resolve_forward_weight(root, logical_shape: tuple[int, int, int], device: to
     if data.numel() != E * M * N or scale.numel() != E * (M // 64) * N * 2:
         raise ValueError(f"MX root does not hold an [E, M, N] = {logical_shape} weight")
     return data.view(torch.uint8).view(E, M, N), scale.view(E, M // 64, N, 2)
+
+
+def resolve_backward_weight(root, logical_shape: tuple[int, int, int], device: torch.device):
+    """The backward axis of a root (weights.py:59-78 'row' pair): (row_data uint8 view [E, M, N],
+    row_scale uint8 [E, M, N/64, 2]), blocks of 32 along N for every row."""
+    data = getattr(root, "row_data", None)
+    scale = getattr(root, "row_scale", None)
+    if data is None or scale is None:
+        raise ValueError("MegaMoE MXFP8 current root is missing required row data/scale.")
+    if data.dtype != torch.float8_e4m3fn or scale.dtype != torch.uint8:
+        raise TypeError("MegaMoE MXFP8 physical storage requires E4M3FN data and packed uint8 E8M0 scales.")
+    if not data.is_contiguous() or not scale.is_contiguous():
+        raise ValueError("MX physical data and scale must be contiguous; implicit copies are forbidden")
+    if data.device != device or scale.device != device:
+        raise ValueError("MX physical data, scales and hidden states must share a device")
+    E, M, N = logical_shape
+    if data.numel() != E * M * N or scale.numel() != E * M * (N // 64) * 2:
+        raise ValueError(f"MX root does not hold an [E, M, N] = {logical_shape} weight")
+    return data.view(torch.uint8).view(E, M, N), scale.view(E, M, N // 64, 2)
 
 
 def prepared_eoi_weight(root, data: torch.Tensor, scale: torch.Tensor):

@@ -8,6 +8,7 @@ current stream. Nothing here synchronises the host and nothing falls back to a C
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass
 
 import torch
@@ -481,6 +482,59 @@ def moe_backward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: tor
         weight_layout=_lib.LAYOUT[layout], topk_weights=_ptr(probs), w1=_ptr(w1), w2=_ptr(w2),
         grad_out=_ptr(dout), grad_hidden=_ptr(grad_hidden), grad_w1=_ptr(grad_w1), grad_w2=_ptr(grad_w2),
         grad_topk_weights=_ptr(grad_p), weight_grad_dtype=1 if weight_grad_dtype == torch.float32 else 0)
+    need = lib.mi355moe_moe_backward_workspace_size(ctypes.byref(args))
+    if need == 0 and T > 0:
+        _lib.check(lib.mi355moe_moe_backward(ctypes.byref(args), None, 0, _stream(device)), "mi355moe_moe_backward")
+    ws = _workspace(need, device)
+    rc = lib.mi355moe_moe_backward(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(rc, "mi355moe_moe_backward")
+    return grad_hidden, grad_w1, grad_w2, grad_p
+
+
+def moe_backward_mxfp8(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                       w1: tuple, w2: tuple, grad_out: torch.Tensor, *, num_experts: int, intermediate_size: int,
+                       weight_grad_dtype: torch.dtype = torch.bfloat16, need_topk_grad: bool = True):
+    """Gradients of the MXFP8 :func:`moe_forward` (mxfp8/graph.py:147-154) through
+    ``mi355moe_moe_backward``. ``w1`` / ``w2`` are (col_data, col_scale, row_data, row_scale) of the
+    EIO MX roots: col_data [E, M, N] e4m3, col_scale [E, M/64, N, 2], row_data [E, M, N] e4m3,
+    row_scale [E, M, N/64, 2]. Returns (grad_hidden bf16 [T, H], grad_w1 [E, H, 2I], grad_w2
+    [E, I, H] in ``weight_grad_dtype``, grad_topk_weights fp32 [T, K] or None)."""
+    lib = _lib.load()
+    device = _require_gpu(hidden, topk_ids, topk_weights, grad_out, *w1, *w2)
+    if hidden.dtype != torch.bfloat16 or hidden.ndim != 2 or grad_out.shape != hidden.shape:
+        raise TypeError("hidden and grad_out must be bf16 [T, H]")
+    if weight_grad_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("weight_grad_dtype must be bfloat16 or float32")
+    T, H = hidden.shape
+    K = topk_ids.shape[1]
+    E, I = num_experts, intermediate_size
+    shapes = (((E, H, 2 * I), (E, H // 64, 2 * I, 2), (E, H, 2 * I), (E, H, 2 * I // 64, 2)),
+              ((E, I, H), (E, I // 64, H, 2), (E, I, H), (E, I, H // 64, 2)))
+    fields = []
+    for root, want in zip((w1, w2), shapes):
+        if len(root) != 4:
+            raise ValueError("MX weights must be (col_data, col_scale, row_data, row_scale)")
+        for t, shape in zip(root, want):
+            if t.numel() != math.prod(shape) or t.element_size() != 1 or not t.is_contiguous():
+                raise ValueError(f"MX weight field must be a contiguous 1-byte tensor of shape {shape}")
+        fields.append([t.view(torch.uint8) for t in root])
+    hidden = hidden.contiguous()
+    ids = topk_ids.contiguous()
+    probs = topk_weights.to(torch.float32).contiguous()
+    dout = grad_out.to(torch.bfloat16).contiguous()
+    grad_hidden = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    grad_w1 = torch.empty((E, H, 2 * I), dtype=weight_grad_dtype, device=device)
+    grad_w2 = torch.empty((E, I, H), dtype=weight_grad_dtype, device=device)
+    grad_p = torch.empty((T, K), dtype=torch.float32, device=device) if need_topk_grad else None
+    (c1, s1, r1, rs1), (c2, s2, r2, rs2) = fields
+    args = _lib.BackwardArgs(
+        hidden=_ptr(hidden), num_tokens=T, hidden_size=H, intermediate_size=I, num_experts=E, top_k=K,
+        topk_ids=_ptr(ids), ids_dtype=_ids_dtype(ids), weight_layout=_lib.LAYOUT["EIO"], topk_weights=_ptr(probs),
+        w1=_ptr(c1), w2=_ptr(c2), grad_out=_ptr(dout), grad_hidden=_ptr(grad_hidden), grad_w1=_ptr(grad_w1),
+        grad_w2=_ptr(grad_w2), grad_topk_weights=_ptr(grad_p),
+        weight_grad_dtype=1 if weight_grad_dtype == torch.float32 else 0, precision=_lib.PRECISION["mxfp8"],
+        w1_scale=_ptr(s1), w2_scale=_ptr(s2), w1_row=_ptr(r1), w2_row=_ptr(r2), w1_row_scale=_ptr(rs1),
+        w2_row_scale=_ptr(rs2))
     need = lib.mi355moe_moe_backward_workspace_size(ctypes.byref(args))
     if need == 0 and T > 0:
         _lib.check(lib.mi355moe_moe_backward(ctypes.byref(args), None, 0, _stream(device)), "mi355moe_moe_backward")

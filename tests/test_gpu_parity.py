@@ -655,3 +655,73 @@ def test_mx_quantize_weight_dual_axis(gpu, G, M, N):
     # one axis only
     cd2, cs2, rd2, rs2 = ops.mx_quantize_weight(w.to(gpu), row=False)
     assert rd2 is None and rs2 is None and torch.equal(cd2.view(torch.uint8), cd.view(torch.uint8))
+
+
+# ------------------------------------------------------------------------------------------------
+# MXFP8 expert backward
+# ------------------------------------------------------------------------------------------------
+_MX_BACKWARD_SKIP = pytest.mark.skip(
+    reason="the MXFP8 expert backward is switched off in the library until this test has run on the GPU")
+
+
+def _mx_roots(w: torch.Tensor):
+    """(col_data, col_scale, row_data, row_scale) of an EIO bf16 weight through the oracle."""
+    E, M, N = w.shape
+    cd, cs = orc.mx_quantize_weight_cols(w)
+    rd, rs = orc.mx_quantize(w.float(), dim=-1)
+    return cd, cs, rd, rs.reshape(E, M, N // 64, 2)
+
+
+@_MX_BACKWARD_SKIP
+@pytest.mark.parametrize("T,E,K,skew", [(256, 8, 2, False), (96, 16, 4, True)])
+@pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16])
+def test_moe_backward_mxfp8_matches_oracle(gpu, T, E, K, skew, grad_dtype):
+    from hyper_multicore_amd import ops
+    H, I = 512, 256
+    g = _seed(T + E + K + 101)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g, wscale=0.05)
+    if skew:
+        ids[:, 0] = 0  # one hot expert, several nearly empty ones
+    dout = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    r1, r2 = _mx_roots(w1), _mx_roots(w2)
+    gx, g1, g2, gp = ops.moe_backward_mxfp8(
+        x.to(gpu), ids.to(gpu), probs.to(gpu), tuple(t.to(gpu) for t in r1), tuple(t.to(gpu) for t in r2),
+        dout.to(gpu), num_experts=E, intermediate_size=I, weight_grad_dtype=grad_dtype)
+    rx, rw1, rw2, rp = orc.expert_backward_reference_mx(x, ids, probs, r1[:2], r2[:2], r1[2:], r2[2:], dout,
+                                                        num_experts=E)
+    assert g1.dtype == grad_dtype and g1.shape == (E, H, 2 * I) and g2.shape == (E, I, H)
+    assert orc.rel_l2(gx.cpu(), rx) < MXFP8_REL_L2
+    assert orc.rel_l2(g1.cpu().float(), rw1) < MXFP8_REL_L2
+    assert orc.rel_l2(g2.cpu().float(), rw2) < MXFP8_REL_L2
+    assert orc.rel_l2(gp.cpu(), rp) < MXFP8_REL_L2
+
+
+@_MX_BACKWARD_SKIP
+def test_mxfp8_module_autograd(gpu):
+    import hyper_multicore_amd as hm
+    T, H, I, E, K = 128, 512, 256, 8, 2
+    g = _seed(131)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g, wscale=0.05)
+    dout = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    roots = []
+    for w in (w1, w2):
+        root = torch.nn.Parameter(w.to(gpu))
+        cd, cs, rd, rs = hm.ops.mx_quantize_weight(w.to(gpu))
+        root.col_data, root.col_scale, root.row_data, root.row_scale = cd, cs, rd, rs
+        roots.append(root)
+    ex = hm.MegaMoeExperts(hidden_size=H, intermediate_size=I, num_experts=E, top_k=K, precision="mxfp8",
+                           numerics_options=hm.MegaMoeNumericsOptions(partial_weight_grad_dtype="float32"))
+    xg = x.to(gpu).requires_grad_(True)
+    pg = probs.to(gpu).requires_grad_(True)
+    out = ex(xg, ids.to(gpu), pg, expert_weights=tuple(roots))
+    out.backward(dout.to(gpu))
+    r1 = tuple(t.cpu() for t in (roots[0].col_data.view(torch.uint8), roots[0].col_scale,
+                                 roots[0].row_data.view(torch.uint8), roots[0].row_scale))
+    r2 = tuple(t.cpu() for t in (roots[1].col_data.view(torch.uint8), roots[1].col_scale,
+                                 roots[1].row_data.view(torch.uint8), roots[1].row_scale))
+    rx, rw1, rw2, rp = orc.expert_backward_reference_mx(x, ids, probs, r1[:2], r2[:2], r1[2:], r2[2:], dout)
+    assert roots[0].grad.dtype == torch.bfloat16 and roots[0].grad.shape == (E, H, 2 * I)
+    assert orc.rel_l2(xg.grad.cpu(), rx) < MXFP8_REL_L2
+    assert orc.rel_l2(roots[0].grad.cpu().float(), rw1) < MXFP8_REL_L2
+    assert orc.rel_l2(roots[1].grad.cpu().float(), rw2) < MXFP8_REL_L2
+    assert orc.rel_l2(pg.grad.cpu(), rp) < MXFP8_REL_L2
