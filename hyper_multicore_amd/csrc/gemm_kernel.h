@@ -66,10 +66,6 @@ MI355_DEV void wait_vm(int n) {
 }
 
 
-// ---- fragment loads (one K step: 16 bf16 or 64 e4m3) ------------------------------------------
-MI355_DEV v8bf read_a_bf16(const uint8_t* As, int r, int ks, int lane) {
-  return *(const v8bf*)(As + a_chunk_off(r, ks * 2 + (lane >> 5)));
-}
 
 
 #ifdef GG_TRACE
@@ -81,146 +77,6 @@ extern "C" int mi355_gg_trace_read(void* host) {
 #else
 #define GG_T(pt)
 #endif
-
-// Operand fragments of one stage for one wave (WM rows x WN columns x one stage of K). Values
-// that are read in several LDS instructions are kept as the raw pieces and joined only when the
-// MFMA consumes them, so that issuing the reads never forces a wait for their data.
-template <class C, bool MX, bool B_KN, bool A_KN = false> struct Frags;
-template <class C> struct Frags<C, false, false> { v8bf a[2][C::MI], b[2][C::NI]; };  // [ks][mi], [ks][ni]
-template <class C> struct Frags<C, false, true> { v8bf a[2][C::MI]; v4s bl[2][C::NI], bh[2][C::NI]; };
-template <class C> struct Frags<C, false, true, true> {  // grouped-K: A K-major like B
-  v4s al[2][C::MI], ah[2][C::MI], bl[2][C::NI], bh[2][C::NI];
-};
-template <class C> struct Frags<C, true, true> {
-  v4i al[C::MI], ah[C::MI];
-  v2i bp[C::NI][4];
-  int sa[C::MI], sb[C::NI];
-};
-template <class C> struct Frags<C, true, true, true> {  // grouped-K MX: A K-major like B
-  v2i ap[C::MI][4], bp[C::NI][4];
-  int sa[C::MI], sb[C::NI];
-};
-template <class C> struct Frags<C, true, false> {
-  v4i al[C::MI], ah[C::MI], bl[C::NI], bh[C::NI];
-  int sa[C::MI], sb[C::NI];
-};
-
-// bf16 fragment of 32 rows / columns x 16 K (ks) from a K-major LDS tile (512-byte K rows of 256
-// bf16, chunks swizzled with (k & 7) << 1), read with two transposing loads.
-MI355_DEV void read_kn16(const uint8_t* S, int base, int ks, int lane, v4s& lo, v4s& hi) {
-  const int g16 = lane >> 4, m = lane & 15;
-  const int nb = base + (g16 & 1) * 16 + 4 * (m & 3);
-  const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
-  const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
-  const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
-  lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, S + off0));
-  hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, S + off1));
-}
-
-// Element-wise fragment reads and MFMAs and the copies of one iteration, so that one pipelined
-// step can interleave them: MFMA t, then its share of the LDS reads of the next stage
-// and of the DMA copies. The wave never stalls on the DMA queue or on the LDS return queue for
-// long while the matrix core has work.
-
-template <class C, bool MX, bool B_KN, int NM, bool A_KN = false>
-MI355_DEV void read_elem(Frags<C, MX, B_KN, A_KN>& f, int e, const uint8_t* As, const uint8_t* Bs, const uint8_t* ASs,
-                         const uint8_t* BSRs, int wm, int wn, int lane) {
-  constexpr int NI = C::NI;
-  if constexpr (!MX) {
-    const int ks = e / (NI + NM), q = e % (NI + NM);
-    if (q < NI) {
-      if constexpr (!B_KN) {
-        const int n = wn * C::WN + q * 32 + (lane & 31);
-        f.b[ks][q] = *(const v8bf*)(Bs + a_chunk_off(n, ks * 2 + (lane >> 5)));
-      } else {
-        const int g16 = lane >> 4, m = lane & 15;
-        const int nb = wn * C::WN + q * 32 + (g16 & 1) * 16 + 4 * (m & 3);
-        const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
-        const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
-        const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
-        f.bl[ks][q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off0));
-        f.bh[ks][q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(v4s, Bs + off1));
-      }
-    } else {
-      if constexpr (A_KN) read_kn16(As, wm * C::WM + (q - NI) * 32, ks, lane, f.al[ks][q - NI], f.ah[ks][q - NI]);
-      else f.a[ks][q - NI] = read_a_bf16(As, wm * C::WM + (q - NI) * 32 + (lane & 31), ks, lane);
-    }
-  } else {
-    if (e < NI) {
-      if constexpr (B_KN) {
-        const int g16 = lane >> 4, m = lane & 15;
-        const int nb = wn * C::WN + e * 32 + (g16 & 1) * 16;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int k = (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
-          const int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
-          f.bp[e][q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, Bs + off));
-        }
-        f.sb[e] = Bs[C::B_BYTES + (wn * C::WN + e * 32 + (lane & 31)) * 2 + (lane >> 5)];
-      } else {
-        // K-contiguous weight rows: same fragment layout as the activations
-        const int n = wn * C::WN + e * 32 + (lane & 31);
-        const int c0 = lane >> 5;
-        f.bl[e] = *(const v4i*)(Bs + a_chunk_off(n, c0));
-        f.bh[e] = *(const v4i*)(Bs + a_chunk_off(n, c0 + 2));
-        f.sb[e] = BSRs[n * 16 + (lane >> 5)];
-      }
-    } else if constexpr (A_KN) {
-      // grouped-K: A tile K-major (64 rows of 256 bytes), read like the EIO weight tile; the two
-      // codes of row m (K rows 0-31 / 32-63 of the stage) follow at ASs + 2m
-      const int mi = e - NI;
-      const int g16 = lane >> 4, m = lane & 15;
-      const int mb = wm * C::WM + mi * 32 + (g16 & 1) * 16;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int k = (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
-        const int off = k * 256 + (((mb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
-        f.ap[mi][q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(v2i, As + off));
-      }
-      f.sa[mi] = ASs[(wm * C::WM + mi * 32 + (lane & 31)) * 2 + (lane >> 5)];
-    } else {
-      const int r = wm * C::WM + (e - NI) * 32 + (lane & 31);
-      const int c0 = lane >> 5;
-      f.al[e - NI] = *(const v4i*)(As + a_chunk_off(r, c0));
-      f.ah[e - NI] = *(const v4i*)(As + a_chunk_off(r, c0 + 2));
-      f.sa[e - NI] = ASs[r * 16 + (lane >> 5)];
-    }
-  }
-}
-
-template <class C, bool MX, bool B_KN, int NM, bool A_KN = false>
-MI355_DEV void mfma_elem(const Frags<C, MX, B_KN, A_KN>& f, v16f (&acc)[C::MI][C::NI], int t) {
-  constexpr int NI = C::NI;
-  if constexpr (!MX) {
-    const int ks = t / (NM * NI), mi = (t / NI) % NM, ni = t % NI;
-    v8bf b;
-    if constexpr (!B_KN) b = f.b[ks][ni];
-    else b = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.bl[ks][ni], f.bh[ks][ni], 0, 1, 2, 3, 4, 5, 6, 7));
-    v8bf a;
-    if constexpr (A_KN) a = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.al[ks][mi], f.ah[ks][mi], 0, 1, 2, 3, 4, 5, 6, 7));
-    else a = f.a[ks][mi];
-    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[mi][ni], 0, 0, 0);
-  } else {
-    const int mi = t / NI, ni = t % NI;
-    v8i a;
-    if constexpr (A_KN) {
-      const v4i a01 = __builtin_shufflevector(f.ap[mi][0], f.ap[mi][1], 0, 1, 2, 3);
-      const v4i a23 = __builtin_shufflevector(f.ap[mi][2], f.ap[mi][3], 0, 1, 2, 3);
-      a = __builtin_shufflevector(a01, a23, 0, 1, 2, 3, 4, 5, 6, 7);
-    } else {
-      a = __builtin_shufflevector(f.al[mi], f.ah[mi], 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-    v8i b;
-    if constexpr (B_KN) {
-      const v4i b01 = __builtin_shufflevector(f.bp[ni][0], f.bp[ni][1], 0, 1, 2, 3);
-      const v4i b23 = __builtin_shufflevector(f.bp[ni][2], f.bp[ni][3], 0, 1, 2, 3);
-      b = __builtin_shufflevector(b01, b23, 0, 1, 2, 3, 4, 5, 6, 7);
-    } else {
-      b = __builtin_shufflevector(f.bl[ni], f.bh[ni], 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-    acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[mi][ni], 0, 0, 0, f.sa[mi], 0, f.sb[ni]);
-  }
-}
 
 // K loop, software-pipelined in each wave: iteration k (after barrier k) refills the ring slots of
 // stage k, reads the fragments of stage k+1 into one register set and runs the MFMAs of stage k

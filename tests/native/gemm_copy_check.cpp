@@ -30,6 +30,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <memory>
 #include <random>
 #include <string>
 #include <vector>
@@ -625,6 +626,316 @@ static void check_range(const void* base, int64_t lo, int64_t hi, const char* wh
 }
 
 // ------------------------------------------------------------------------------------------------
+// Functional emulation of a work item: the copies land in an emulated LDS, the fragment reads and
+// MFMAs run through the kernels' own read_elem / mfma_elem with an emulation of the lane-crossing
+// instructions (transposing LDS loads, 32x32 MFMAs), and the accumulators are compared with a
+// reference GEMM of the same operands. The instruction models: ds_read_b64_tr_b16 - each 16-lane
+// group's four 16-bit values per lane form a 4 x 16 block (lane i holds row i / 4, columns
+// 4 (i % 4) ..), and lane o receives column o; ds_read_b64_tr_b8 - 8 x 16 bytes (lane i holds row
+// i / 2, columns 8 (i % 2) ..); v_mfma_f32_32x32x16_bf16 - lane l holds row / column l % 32 and
+// K = 8 (l / 32) + j; v_mfma_scale_f32_32x32x64_f8f6f4 - byte j / 16 + j of lane l holds
+// K = 16 (l / 32) + j / 32 + 16 (l / 32) + j, lane r + 32 b supplies the scale of K block b of row /
+// column r; accumulator element r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+// Paths that already pass on the GPU (EIO bf16 and MX, EOI bf16) calibrate these models.
+static bool g_emulate = false;
+static long g_emulated_items = 0;
+
+static float bf16f(uint16_t v) {
+  uint32_t u = (uint32_t)v << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static float e4m3f(uint8_t v) {
+  const int sign = v >> 7, e = (v >> 3) & 15, m = v & 7;
+  float r;
+  if (e == 15 && m == 7) r = NAN;
+  else if (e == 0) r = std::ldexp((float)m, -9);
+  else r = std::ldexp(1.0f + m / 8.0f, e - 7);
+  return sign ? -r : r;
+}
+static float e8m0f(int code) { return std::ldexp(1.0f, (code & 255) - 127); }
+
+struct EmuState {
+  int pass = 0;  // 0: record the transposing loads' addresses, 1: replay their results
+  int lane = 0, idx = 0;
+  std::vector<const uint8_t*> addr;  // [call * 64 + lane]
+  std::vector<int> kind;             // per call: 16 (b16) or 8 (b8)
+  std::vector<uint64_t> val;         // [call * 64 + lane]
+  // MFMA operands of the current call, per lane
+  uint8_t a[64][32], b[64][32];
+  int sa[64], sb[64];
+  v16f* acc[64];
+};
+static EmuState g_emu;
+
+struct EmuOps {
+  static uint64_t take(const uint8_t* p, int kind) {
+    EmuState& e = g_emu;
+    const size_t slot = (size_t)e.idx * 64 + e.lane;
+    if (e.pass == 0) {
+      if (e.addr.size() < slot + 1) e.addr.resize((size_t)(e.idx + 1) * 64, nullptr);
+      if ((int)e.kind.size() < e.idx + 1) e.kind.resize(e.idx + 1, 0);
+      e.addr[slot] = p;
+      e.kind[e.idx] = kind;
+      ++e.idx;
+      return 0;
+    }
+    ++e.idx;
+    return e.val[slot];
+  }
+  static v4s tr16(const uint8_t* p) {
+    const uint64_t v = take(p, 16);
+    v4s r;
+    memcpy(&r, &v, 8);
+    return r;
+  }
+  static v2i tr8(const uint8_t* p) {
+    const uint64_t v = take(p, 8);
+    v2i r;
+    memcpy(&r, &v, 8);
+    return r;
+  }
+  static void mfma_bf16(v8bf a, v8bf b, v16f& acc) {
+    memcpy(g_emu.a[g_emu.lane], &a, 16);
+    memcpy(g_emu.b[g_emu.lane], &b, 16);
+    g_emu.acc[g_emu.lane] = &acc;
+  }
+  static void mfma_f8(v8i a, v8i b, v16f& acc, int sa, int sb) {
+    memcpy(g_emu.a[g_emu.lane], &a, 32);
+    memcpy(g_emu.b[g_emu.lane], &b, 32);
+    g_emu.sa[g_emu.lane] = sa;
+    g_emu.sb[g_emu.lane] = sb;
+    g_emu.acc[g_emu.lane] = &acc;
+  }
+};
+
+// results of the recorded transposing loads
+static void emu_resolve_loads() {
+  EmuState& e = g_emu;
+  const int calls = (int)e.kind.size();
+  e.val.assign((size_t)calls * 64, 0);
+  for (int c = 0; c < calls; ++c)
+    for (int grp = 0; grp < 4; ++grp) {
+      uint8_t in[16][8];
+      for (int i = 0; i < 16; ++i) memcpy(in[i], e.addr[(size_t)c * 64 + grp * 16 + i], 8);
+      for (int o = 0; o < 16; ++o) {
+        uint8_t out[8];
+        if (e.kind[c] == 16) {  // 4 x 16 block of 16-bit values
+          for (int r = 0; r < 4; ++r) {
+            const int lane = 4 * r + o / 4, j = o % 4;
+            memcpy(out + 2 * r, in[lane] + 2 * j, 2);
+          }
+        } else {  // 8 x 16 block of bytes
+          for (int r = 0; r < 8; ++r) {
+            const int lane = 2 * r + o / 8, j = o % 8;
+            out[r] = in[lane][j];
+          }
+        }
+        memcpy(&e.val[(size_t)c * 64 + grp * 16 + o], out, 8);
+      }
+    }
+}
+
+static void emu_resolve_mfma(bool f8) {
+  EmuState& e = g_emu;
+  float d[32][32];
+  for (int row = 0; row < 32; ++row)
+    for (int col = 0; col < 32; ++col) {
+      double sum = 0.0;
+      if (!f8) {
+        for (int k = 0; k < 16; ++k) {
+          uint16_t av, bv;
+          memcpy(&av, e.a[row + 32 * (k / 8)] + 2 * (k % 8), 2);
+          memcpy(&bv, e.b[col + 32 * (k / 8)] + 2 * (k % 8), 2);
+          sum += (double)bf16f(av) * bf16f(bv);
+        }
+      } else {
+        for (int k = 0; k < 64; ++k) {
+          const int half = (k % 32) / 16, byte = (k / 32) * 16 + k % 16, blk = k / 32;
+          const float av = e4m3f(e.a[row + 32 * half][byte]) * e8m0f(e.sa[row + 32 * blk]);
+          const float bv = e4m3f(e.b[col + 32 * half][byte]) * e8m0f(e.sb[col + 32 * blk]);
+          sum += (double)av * bv;
+        }
+      }
+      d[row][col] = (float)sum;
+    }
+  for (int l = 0; l < 64; ++l)
+    for (int r = 0; r < 16; ++r) {
+      const int row = 8 * (r / 4) + 4 * (l / 32) + r % 4, col = l % 32;
+      (*e.acc[l])[r] += d[row][col];
+    }
+}
+
+// Copies land in the emulated LDS at once: every read of a slot happens after its stage's copies and
+// before the slot is refilled (the copy checks above establish both).
+static int g_fill_lane = 0;
+struct FillDma {
+  template <int SZ>
+  static void copy(const void* g, uint32_t off, uint8_t* smem, int enable) {
+    if (!enable) return;
+    memcpy(smem + off + (uint32_t)SZ * g_fill_lane, g, SZ);
+  }
+};
+
+template <class C, bool MX, bool B_KN, bool LA, bool GK>
+static void fill_prologue(const CopyPlan<C>& cp, int nk, int wave, uint8_t* smem) {
+  using D = FillDma;
+#include "../../hyper_multicore_amd/csrc/gemm_kloop_prologue.inc"
+  (void)la_n;
+  (void)lb_n;
+}
+template <class C, bool MX, bool B_KN, bool LA, bool GK>
+static void fill_step(const CopyPlan<C>& cp, int k, int nk, int wave, uint8_t* smem) {
+  for (int it = 0; it < StepShape<C, MX, 1, GK>::ITEMS; ++it)
+    issue_item<C, MX, B_KN, LA, GK, FillDma>(cp, k, nk, wave, smem, it);
+  issue_scales_item<C, MX, B_KN, LA, FillDma, GK>(cp, k, nk, wave, smem);
+}
+
+template <class C, bool MX, bool B_KN, bool GK>
+struct EmuWaveTile {
+  using F = Frags<C, MX, B_KN, GK>;
+  F f0[64], f1[64];
+  v16f acc[64][C::MI][C::NI];
+};
+
+// LDS slot pointers of stage kn, as the K loop computes them
+template <class C, bool MX, bool GK>
+static void stage_ptrs(uint8_t* smem, int kn, const uint8_t*& As, const uint8_t*& Bs, const uint8_t*& ASs,
+                       const uint8_t*& BSRs) {
+  As = smem + (kn % C::A_SLOTS) * C::A_BYTES;
+  Bs = smem + C::B_OFF + (kn % C::B_SLOTS) * C::B_SLOT;
+  if (MX && GK) ASs = smem + C::AS_OFF + (kn % C::A_SLOTS) * C::BS_BYTES;
+  else ASs = smem + C::AS_OFF + ((kn / C::AS_GROUP) & 1) * C::AS_SLOT + (kn & (C::AS_GROUP - 1)) * 2;
+  BSRs = smem + C::BSR_OFF + ((kn / C::AS_GROUP) & 1) * C::BSR_SLOT + (kn & (C::AS_GROUP - 1)) * 2;
+}
+
+template <class C, bool MX, bool B_KN, int NM, bool GK>
+static void emu_read_stage(typename EmuWaveTile<C, MX, B_KN, GK>::F (&f)[64], uint8_t* smem, int kn, int wm, int wn) {
+  const uint8_t *As, *Bs, *ASs, *BSRs;
+  stage_ptrs<C, MX, GK>(smem, kn, As, Bs, ASs, BSRs);
+  using SS = StepShape<C, MX, NM, GK>;
+  for (int e = 0; e < SS::READS; ++e) {
+    g_emu.pass = 0;
+    g_emu.addr.clear();
+    g_emu.kind.clear();
+    typename EmuWaveTile<C, MX, B_KN, GK>::F scratch;
+    for (int l = 0; l < 64; ++l) {
+      g_emu.lane = l;
+      g_emu.idx = 0;
+      read_elem<C, MX, B_KN, NM, GK, EmuOps>(scratch, e, As, Bs, ASs, BSRs, wm, wn, l);
+    }
+    if (!g_emu.kind.empty()) emu_resolve_loads();
+    g_emu.pass = 1;
+    for (int l = 0; l < 64; ++l) {
+      g_emu.lane = l;
+      g_emu.idx = 0;
+      read_elem<C, MX, B_KN, NM, GK, EmuOps>(f[l], e, As, Bs, ASs, BSRs, wm, wn, l);
+    }
+  }
+}
+
+template <class C, bool MX, bool B_KN, int NM, bool GK>
+static void emu_mfma_stage(const typename EmuWaveTile<C, MX, B_KN, GK>::F (&f)[64],
+                           v16f (&acc)[64][C::MI][C::NI]) {
+  using SS = StepShape<C, MX, NM, GK>;
+  for (int t = 0; t < SS::MFMAS; ++t) {
+    for (int l = 0; l < 64; ++l) {
+      g_emu.lane = l;
+      mfma_elem<C, MX, B_KN, NM, GK, EmuOps>(f[l], acc[l], t);
+    }
+    emu_resolve_mfma(MX);
+  }
+}
+
+// The K loop of one wave: reads of stage k + 1 and MFMAs of stage k per step, copies of all waves
+// applied in iteration order (they never touch a slot that is being read).
+template <class C, bool MX, bool B_KN, int NM, bool GK>
+static void emu_wave_loop(EmuWaveTile<C, MX, B_KN, GK>& w, uint8_t* smem, int nk, int wm, int wn, int k) {
+  if constexpr (NM > 0) {
+    if (k < 0) {  // prologue read of stage 0
+      emu_read_stage<C, MX, B_KN, NM, GK>(w.f0, smem, 0, wm, wn);
+      return;
+    }
+    auto& cur = (k & 1) ? w.f1 : w.f0;
+    auto& nxt = (k & 1) ? w.f0 : w.f1;
+    emu_mfma_stage<C, MX, B_KN, NM, GK>(cur, w.acc);
+    if (k + 1 < nk) emu_read_stage<C, MX, B_KN, NM, GK>(nxt, smem, k + 1, wm, wn);
+  }
+}
+template <class C, bool MX, bool B_KN, bool GK>
+static void emu_wave_step(EmuWaveTile<C, MX, B_KN, GK>& w, int nm, uint8_t* smem, int nk, int wm, int wn, int k) {
+  if (C::MI >= 4 && nm == 4) emu_wave_loop<C, MX, B_KN, (C::MI >= 4 ? 4 : 1), GK>(w, smem, nk, wm, wn, k);
+  else if (nm == 2) emu_wave_loop<C, MX, B_KN, 2, GK>(w, smem, nk, wm, wn, k);
+  else if (nm == 1) emu_wave_loop<C, MX, B_KN, 1, GK>(w, smem, nk, wm, wn, k);
+}
+
+// Runs one work item; cps[wave][lane] are the lanes' copy plans. value(row, col) returns the
+// reference of accumulator tile element (row, col) or NAN where the tile position is not compared.
+template <class C, bool MX, bool B_KN, bool GK>
+static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la)[C::WAVES], const int (&nm)[C::WAVES],
+                         int nk, const std::function<double(int, int)>& value, const char* what) {
+  std::vector<uint8_t> lds(C::TOTAL, 0);
+  uint8_t* smem = lds.data();
+  auto tiles = std::make_unique<EmuWaveTile<C, MX, B_KN, GK>[]>(C::WAVES);
+  for (int w = 0; w < C::WAVES; ++w)
+    for (int l = 0; l < 64; ++l)
+      for (int i = 0; i < C::MI; ++i)
+        for (int j = 0; j < C::NI; ++j)
+          for (int r = 0; r < 16; ++r) tiles[w].acc[l][i][j][r] = 0.0f;
+  for (int w = 0; w < C::WAVES; ++w)
+    for (int l = 0; l < 64; ++l) {
+      g_fill_lane = l;
+      if (la[w]) fill_prologue<C, MX, B_KN, true, GK>(cps[w][l], nk, w, smem);
+      else fill_prologue<C, MX, B_KN, false, GK>(cps[w][l], nk, w, smem);
+    }
+  for (int w = 0; w < C::WAVES; ++w)
+    emu_wave_step<C, MX, B_KN, GK>(tiles[w], nm[w], smem, nk, w / C::WGN, w % C::WGN, -1);
+  for (int k = 0; k < nk; ++k) {
+    for (int w = 0; w < C::WAVES; ++w)
+      emu_wave_step<C, MX, B_KN, GK>(tiles[w], nm[w], smem, nk, w / C::WGN, w % C::WGN, k);
+    if (k + 1 < nk)
+      for (int w = 0; w < C::WAVES; ++w)
+        for (int l = 0; l < 64; ++l) {
+          g_fill_lane = l;
+          if (la[w]) fill_step<C, MX, B_KN, true, GK>(cps[w][l], k, nk, w, smem);
+          else fill_step<C, MX, B_KN, false, GK>(cps[w][l], k, nk, w, smem);
+        }
+  }
+  // compare the accumulators with the reference
+  double max_ref = 0.0, max_err = 0.0;
+  int bad_row = -1, bad_col = -1;
+  double bad_got = 0.0, bad_want = 0.0;
+  for (int w = 0; w < C::WAVES; ++w) {
+    const int wm = w / C::WGN, wn = w % C::WGN;
+    if (nm[w] == 0) continue;
+    for (int l = 0; l < 64; ++l)
+      for (int i = 0; i < nm[w]; ++i)
+        for (int j = 0; j < C::NI; ++j)
+          for (int r = 0; r < 16; ++r) {
+            const int row = wm * C::WM + i * 32 + 8 * (r / 4) + 4 * (l / 32) + r % 4;
+            const int col = wn * C::WN + j * 32 + l % 32;
+            const double want = value(row, col);
+            if (std::isnan(want)) continue;
+            const double got = tiles[w].acc[l][i][j][r];
+            max_ref = std::max(max_ref, std::fabs(want));
+            const double err = std::fabs(got - want);
+            if (!(err <= max_err)) {
+              max_err = err;
+              bad_row = row;
+              bad_col = col;
+              bad_got = got;
+              bad_want = want;
+            }
+          }
+  }
+  ++g_emulated_items;
+  if (!(max_err <= 1e-4 * std::max(max_ref, 1e-30)))
+    CHECK_FAIL("%s: emulated tile differs from the reference GEMM: max |err| %.3g (max |ref| %.3g) at tile "
+               "(%d, %d): %.6g vs %.6g", what, max_err, max_ref, bad_row, bad_col, bad_got, bad_want);
+}
+
+// ------------------------------------------------------------------------------------------------
 // Forward grouped GEMM: all work items, waves and lanes
 template <class C, bool MX, bool B_KN, int EPI>
 static int sim_forward(const GGParams& p) {
@@ -648,15 +959,18 @@ static int sim_forward(const GGParams& p) {
     lay = {p.A, p.lda_bytes, p.a_row_index, p.a_row_div, p.a_scale, p.a_scale_ld, p.B, !B_KN, p.K, p.Ntot, ESIZE,
          p.b_scale, p.b_scale_ld};
   }
+  auto cps = std::make_unique<CopyPlan<C>[][64]>(C::WAVES);
   for (int L_item = 0; L_item < total; ++L_item) {
     ItemCtx ctx;
     std::vector<Rec> rec;
     std::vector<Wait> waits;
     bool first = true;
+    bool las[C::WAVES];
     for (int wave = 0; wave < C::WAVES; ++wave)
       for (int lane = 0; lane < 64; ++lane) {
         const int L = L_item;
 #include "../../hyper_multicore_amd/csrc/gemm_item_fwd.inc"
+        cps[wave][lane] = cp;
         (void)mt;
         if (first) {
           first = false;
@@ -703,6 +1017,7 @@ static int sim_forward(const GGParams& p) {
           }
         }
         const bool la = wave_copies_a<C>(wave, rows_valid);
+        las[wave] = la;
         rec.clear();
         waits.clear();
         if (la) record_schedule<C, MX, B_KN, true, false>(cp, nk, wave, rec, waits);
@@ -710,6 +1025,48 @@ static int sim_forward(const GGParams& p) {
         check_lane<C, MX, B_KN, SWIGLU, false>(p, lay, ctx, wave, lane, la, rec, waits);
       }
     check_coverage<C, MX, B_KN, false>(ctx);
+    if (g_emulate) {
+      int nms[C::WAVES];
+      for (int w = 0; w < C::WAVES; ++w) {  // the kernel's subtile count per wave
+        const int rows_w = ctx.rows_valid - (w / C::WGN) * C::WM;
+        nms[w] = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
+      }
+      const int Kper = p.K / splits;
+      auto value = [&](int row, int col) -> double {
+        int64_t wc;
+        if (row >= ctx.rows_valid || !tile_weight_col<C>(col, ctx.nt, p.N, SWIGLU, &wc)) return NAN;
+        const int64_t r = ctx.tile_row0 + row;
+        const int64_t sr = p.a_row_index ? p.a_row_index[r] / p.a_row_div : r;
+        double sum = 0.0;
+        for (int k = ctx.split * Kper; k < (ctx.split + 1) * Kper; ++k) {
+          double av, bv;
+          if (!MX) {
+            uint16_t a16, b16;
+            memcpy(&a16, p.A + sr * p.lda_bytes + 2 * (int64_t)k, 2);
+            const uint8_t* bp = p.B + (int64_t)ctx.g * p.b_group_stride +
+                                (B_KN ? (int64_t)k * p.b_row_bytes + wc * 2 : wc * p.b_row_bytes + 2 * (int64_t)k);
+            memcpy(&b16, bp, 2);
+            av = bf16f(a16);
+            bv = bf16f(b16);
+          } else {
+            av = e4m3f(p.A[sr * p.lda_bytes + k]) * e8m0f(p.a_scale[sr * p.a_scale_ld + k / 32]);
+            const uint8_t* gb = p.B + (int64_t)ctx.g * p.b_group_stride;
+            if (B_KN) {
+              bv = e4m3f(gb[(int64_t)k * p.b_row_bytes + wc]) *
+                   e8m0f(p.b_scale[(int64_t)ctx.g * p.b_scale_group_stride + ((k / 64) * (int64_t)p.Ntot + wc) * 2 +
+                                   ((k / 32) & 1)]);
+            } else {
+              bv = e4m3f(gb[wc * p.b_row_bytes + k]) *
+                   e8m0f(p.b_scale[((int64_t)ctx.g * p.Ntot + wc) * p.b_scale_ld + k / 32]);
+            }
+          }
+          sum += av * bv;
+        }
+        return sum;
+      };
+      emulate_item<C, MX, B_KN, false>(*reinterpret_cast<const CopyPlan<C>(*)[C::WAVES][64]>(cps.get()), las, nms, nk,
+                                        value, "forward item");
+    }
   }
   return MI355MOE_OK;
 }
@@ -729,6 +1086,7 @@ static int sim_wgrad(const GGParams& p) {
   }
   Lo.Ntot = p.b_row_bytes / ES;  // B rows hold N elements (grouped-K: row stride of the routed rows)
   if (g_expect.set) Lo.Ntot = p.N;
+  auto cps = std::make_unique<CopyPlan<C>[][64]>(C::WAVES);
   for (int L_item = 0; L_item < total; ++L_item) {
     ItemCtx ctx;
     std::vector<Rec> rec;
@@ -738,6 +1096,7 @@ static int sim_wgrad(const GGParams& p) {
       for (int lane = 0; lane < 64; ++lane) {
         const int L = L_item;
 #include "../../hyper_multicore_amd/csrc/gemm_item_wgrad.inc"
+        cps[wave][lane] = cp;
         (void)mt;
         if (first) {
           first = false;
@@ -767,6 +1126,38 @@ static int sim_wgrad(const GGParams& p) {
         check_lane<C, MX, true, false, true>(p, Lo, ctx, wave, lane, true, rec, waits);
       }
     if (ctx.nk > 0) check_coverage<C, MX, true, true>(ctx);
+    if (g_emulate && ctx.nk > 0) {
+      bool las[C::WAVES];
+      int nms[C::WAVES];
+      for (int w = 0; w < C::WAVES; ++w) {
+        las[w] = true;
+        const int rows_w = ctx.rows_valid - (w / C::WGN) * C::WM;
+        nms[w] = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
+      }
+      auto value = [&](int row, int col) -> double {
+        const int64_t m = (int64_t)ctx.m0 + row, n = (int64_t)ctx.nt * C::BN + col;
+        if (row >= ctx.rows_valid || n >= p.N) return NAN;
+        double sum = 0.0;
+        for (int64_t r = ctx.k0; r < ctx.kend; ++r) {
+          double av, bv;
+          if (!MX) {
+            uint16_t a16, b16;
+            memcpy(&a16, p.A + r * p.lda_bytes + 2 * m, 2);
+            memcpy(&b16, p.B + r * p.b_row_bytes + 2 * n, 2);
+            av = bf16f(a16);
+            bv = bf16f(b16);
+          } else {
+            const int64_t grp = ctx.k0 / 64 + ctx.g + (r - ctx.k0) / 64, half = ((r - ctx.k0) / 32) & 1;
+            av = e4m3f(p.A[r * p.lda_bytes + m]) * e8m0f(p.a_scale[(grp * p.m_rows + m) * 2 + half]);
+            bv = e4m3f(p.B[r * p.b_row_bytes + n]) * e8m0f(p.b_scale[(grp * p.N + n) * 2 + half]);
+          }
+          sum += av * bv;
+        }
+        return sum;
+      };
+      emulate_item<C, MX, true, true>(*reinterpret_cast<const CopyPlan<C>(*)[C::WAVES][64]>(cps.get()), las, nms,
+                                       ctx.nk, value, "grouped-K item");
+    }
   }
   return MI355MOE_OK;
 }
@@ -835,6 +1226,29 @@ int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t, bool mx) {
 // Scenarios: C-ABI calls with host buffers sized from the shapes the header documents
 static std::mt19937_64 g_rng(20261201);
 
+// Random operands for the emulated scenarios: bf16 in +-[0.5, 2), e4m3 codes except the NaN code,
+// e8m0 scale codes near 2^0.
+static void fill_bf16(uint8_t* p, size_t count) {
+  std::uniform_real_distribution<float> u(0.5f, 2.0f);
+  for (size_t i = 0; i < count; ++i) {
+    float v = u(g_rng) * ((g_rng() & 1) ? -1.0f : 1.0f);
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    const uint16_t h = (uint16_t)(b >> 16);
+    memcpy(p + 2 * i, &h, 2);
+  }
+}
+static void fill_e4m3(uint8_t* p, size_t count) {
+  for (size_t i = 0; i < count; ++i) {
+    uint8_t v = (uint8_t)(g_rng() & 0xff);
+    if ((v & 0x7f) == 0x7f) v ^= 1;
+    p[i] = v;
+  }
+}
+static void fill_codes(uint8_t* p, size_t count) {
+  for (size_t i = 0; i < count; ++i) p[i] = (uint8_t)(120 + g_rng() % 14);
+}
+
 static std::vector<int64_t> cumsum(const std::vector<int>& counts) {
   std::vector<int64_t> gl(counts.size());
   int64_t a = 0;
@@ -853,6 +1267,10 @@ static void gemm_bf16(std::vector<int> counts, int K, int N, int layout) {
   const int64_t rows = glv.back();
   uint8_t* x = mk("x", (size_t)rows * K * 2);
   uint8_t* w = mk("w", (size_t)G * K * N * 2);
+  if (g_emulate) {
+    fill_bf16(x, (size_t)rows * K);
+    fill_bf16(w, (size_t)G * K * N);
+  }
   uint8_t* out = mk("out", (size_t)rows * N * 2);
   int64_t* gl = (int64_t*)mk("group_list", G * 8);
   memcpy(gl, glv.data(), G * 8);
@@ -879,6 +1297,12 @@ static void gemm_mx(std::vector<int> counts, int K, int N, int layout) {
   const bool eoi = layout == MI355MOE_LAYOUT_EOI;
   const int64_t sld = mi355moe_mx_weight_scale_ld(K);
   uint8_t* wsc = eoi ? mk("w_scale_eoi", (size_t)G * N * sld) : mk("col_scale", (size_t)G * (K / 64) * N * 2);
+  if (g_emulate) {
+    fill_e4m3(xq, (size_t)rows * K);
+    fill_codes(xs, (size_t)rows * (K / 32));
+    fill_e4m3(wd, (size_t)G * K * N);
+    fill_codes(wsc, eoi ? (size_t)G * N * sld : (size_t)G * (K / 64) * N * 2);
+  }
   uint8_t* out = mk("out", (size_t)rows * N * 2);
   int64_t* gl = (int64_t*)mk("group_list", G * 8);
   memcpy(gl, glv.data(), G * 8);
@@ -1016,6 +1440,52 @@ static void moe_backward(int64_t T, int K, int E, int H, int I, int layout, int 
   expect_rc(mi355moe_moe_backward(&a, ws, wsz, nullptr), 0, "moe_backward");
 }
 
+// The grouped-K GEMM on its own (as backward.hip calls it), operands [rows, M] / [rows, N] grouped by
+// `counts`; MX operands with grouped packed column scales.
+static void wgrad_direct(std::vector<int> counts, int M, int N, bool mx, int epi) {
+  const int G = (int)counts.size();
+  const auto glv = cumsum(counts);
+  const int64_t R = glv.back();
+  const int es = mx ? 1 : 2;
+  uint8_t* A = mk("A", (size_t)R * M * es);
+  uint8_t* B = mk("B", (size_t)R * N * es);
+  const size_t groups = (size_t)(R + 63) / 64 + G;
+  uint8_t* As = mx ? mk("A_col_scale", groups * M * 2) : nullptr;
+  uint8_t* Bs = mx ? mk("B_col_scale", groups * N * 2) : nullptr;
+  if (mx) {
+    fill_e4m3(A, (size_t)R * M);
+    fill_e4m3(B, (size_t)R * N);
+    fill_codes(As, groups * M * 2);
+    fill_codes(Bs, groups * N * 2);
+  } else {
+    fill_bf16(A, (size_t)R * M);
+    fill_bf16(B, (size_t)R * N);
+  }
+  uint8_t* zero = mk("zero_row", (size_t)std::max(M, N) * es, 0);
+  int64_t* gl = (int64_t*)mk("group_list", G * 8);
+  memcpy(gl, glv.data(), G * 8);
+  uint8_t* out = mk("dW", (size_t)G * M * N * (epi == EPI_STORE_F32 ? 4 : 2));
+  GGParams p = {};
+  p.A = A;
+  p.lda_bytes = (int64_t)M * es;
+  p.a_scale = As;
+  p.B = B;
+  p.b_row_bytes = (int64_t)N * es;
+  p.b_scale = Bs;
+  p.N = N;
+  p.Ntot = N;
+  p.m_rows = M;
+  p.m_tiles = (M + GGBig::BM - 1) / GGBig::BM;
+  p.n_tiles = (N + GGBig::BN - 1) / GGBig::BN;
+  p.G = G;
+  p.group_list = gl;
+  p.C = out;
+  p.ldc = N;
+  p.c_group_stride = (int64_t)M * N;
+  p.zero_row = zero;
+  expect_rc(mi355_grouped_gemm_wgrad(p, epi, nullptr, mx), 0, "grouped_gemm_wgrad");
+}
+
 struct Scenario {
   const char* name;
   std::function<void()> run;
@@ -1059,6 +1529,25 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"gemm_mx_eio_decode_big", big([=] { gemm_mx(decode_counts(48, 6), 1024, 512, L_EIO); })});
   s.push_back({"moe_bf16_eio_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); })});
   s.push_back({"moe_mx_eio_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); })});
+  // functional emulation (random operands; accumulators vs a reference GEMM). The EIO bf16 / MX and
+  // EOI bf16 cases run on the GPU already and calibrate the instruction models.
+  auto emu = [](std::function<void()> f) {
+    return [f] {
+      g_emulate = true;
+      f();
+      g_emulate = false;
+    };
+  };
+  s.push_back({"emu_bf16_eio", emu([=] { gemm_bf16({70, 0, 129, 5}, 256, 512, L_EIO); })});
+  s.push_back({"emu_bf16_eoi", emu([=] { gemm_bf16({70, 0, 129, 5}, 256, 512, L_EOI); })});
+  s.push_back({"emu_mx_eio", emu([=] { gemm_mx({70, 0, 129, 5}, 1024, 256, L_EIO); })});
+  s.push_back({"emu_mx_eoi", emu([=] { gemm_mx({70, 0, 129, 5}, 1024, 256, L_EOI); })});
+  s.push_back({"emu_bf16_eio_decode", emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EIO); })});
+  s.push_back({"emu_bf16_eoi_decode", emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EOI); })});
+  s.push_back({"emu_mx_eio_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })});
+  s.push_back({"emu_mx_eoi_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EOI); })});
+  s.push_back({"emu_wgrad_bf16", emu([=] { wgrad_direct({40, 0, 97, 33}, 256, 512, false, EPI_STORE_F32); })});
+  s.push_back({"emu_wgrad_mx", emu([=] { wgrad_direct({40, 0, 97, 160}, 256, 256, true, EPI_STORE_F32); })});
   // many groups: the tile prefix comes from global memory past the LDS copy
   s.push_back({"gemm_bf16_many_groups", [=] {
                  std::vector<int> c(1100, 0);
@@ -1099,11 +1588,11 @@ int main(int argc, char** argv) {
     for (int i = 1; i < argc; ++i) pick |= std::string(argv[i]) == sc.name;
     if (!pick) continue;
     g_scenario = sc.name;
-    const long e0 = g_errors, c0 = g_copies, i0 = g_items, m0 = g_gemms;
+    const long e0 = g_errors, c0 = g_copies, i0 = g_items, m0 = g_gemms, u0 = g_emulated_items;
     sc.run();
     free_all();
-    printf("%-32s %s  gemms=%ld items=%ld copies=%ld\n", sc.name, g_errors == e0 ? "ok" : "FAILED", g_gemms - m0,
-           g_items - i0, g_copies - c0);
+    printf("%-32s %s  gemms=%ld items=%ld copies=%ld emulated=%ld\n", sc.name, g_errors == e0 ? "ok" : "FAILED",
+           g_gemms - m0, g_items - i0, g_copies - c0, g_emulated_items - u0);
     fflush(stdout);
     ++ran;
   }

@@ -6,8 +6,9 @@ runs its scenarios: the grouped GEMM C-ABI (bf16 / MXFP8, EIO / EOI weights, dec
 more groups than the LDS tile prefix holds), the MegaMoE forward (both precisions and layouts, the
 numerics options) and the expert backward. For every copy of every work item, wave and lane the
 checker verifies the global source (inside a live allocation and equal to the element the fragment
-reads expect), the LDS destination slot, the vmcnt waits and the ring-slot reuse; see the header of
-tests/native/gemm_copy_check.cpp.
+reads expect), the LDS destination slot, the vmcnt waits and the ring-slot reuse; the emu_* scenarios
+also run the kernels' fragment reads and MFMAs through an emulation of the lane-crossing instructions
+and compare the accumulators with a reference GEMM. See the header of tests/native/gemm_copy_check.cpp.
 """
 import shutil
 import subprocess
@@ -29,16 +30,16 @@ def checker():
 
 
 SCENARIOS = [
-    "gemm_bf16_eio", "gemm_bf16_eoi", "gemm_bf16_eio_narrow", "gemm_bf16_eoi_narrow",
-    "gemm_mx_eio", "gemm_mx_eoi", "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k",
-    "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode", "gemm_mx_eio_decode", "gemm_mx_eoi_decode",
-    "gemm_bf16_eio_decode_big", "gemm_bf16_eoi_decode_big", "gemm_mx_eio_decode_big", "moe_bf16_eio_decode_big",
-    "moe_mx_eio_decode_big",
-    "gemm_bf16_many_groups",
-    "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi",
-    "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
-    "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2",
-    "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill",
+    "gemm_bf16_eio", "gemm_bf16_eoi", "gemm_bf16_eio_narrow", "gemm_bf16_eoi_narrow", "gemm_mx_eio",
+    "gemm_mx_eoi", "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k", "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode",
+    "gemm_mx_eio_decode", "gemm_mx_eoi_decode", "gemm_bf16_eio_decode_big", "gemm_bf16_eoi_decode_big",
+    "gemm_mx_eio_decode_big", "moe_bf16_eio_decode_big", "moe_mx_eio_decode_big", "emu_bf16_eio",
+    "emu_bf16_eoi", "emu_mx_eio", "emu_mx_eoi", "emu_bf16_eio_decode", "emu_bf16_eoi_decode",
+    "emu_mx_eio_decode", "emu_mx_eoi_decode", "emu_wgrad_bf16", "emu_wgrad_mx", "gemm_bf16_many_groups",
+    "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill",
+    "moe_mx_eio_prefill", "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu",
+    "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32",
+    "bwd_mx_bf16_prefill",
 ]
 
 
