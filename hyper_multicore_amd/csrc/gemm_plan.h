@@ -23,7 +23,9 @@
 //   GGSmall - BM = 64, two workgroups per CU (the weight stream of one CU then runs through two
 //             independent pipelines), waves in a 1 x 4 grid of 64 x 64 wave tiles; decode shapes
 //             where experts see a few rows each.
-template <int BM_, int WGM_, int A_SLOTS_, int B_SLOTS_, int PREFIX_MAX_, int WG_PER_CU_>
+// AS_N_ / BSR_N_: slots of the MX activation-scale ring and of the MX EOI weight row-scale ring
+// (2, or 0 for a configuration that never runs those paths and spends the LDS on its rings).
+template <int BM_, int WGM_, int A_SLOTS_, int B_SLOTS_, int PREFIX_MAX_, int WG_PER_CU_, int AS_N_ = 2, int BSR_N_ = 2>
 struct GGCfg {
   static constexpr int BM = BM_;
   static constexpr int BN = 256;
@@ -45,11 +47,12 @@ struct GGCfg {
   static constexpr int AS_GROUP = 8;                   // MX: scale codes fetched per 8 stages
   static constexpr int AS_SLOT = BM * 16;              // 16 codes per row
   static constexpr int B_OFF = A_SLOTS * A_BYTES;
+  static constexpr int AS_N = AS_N_, BSR_N = BSR_N_;
   static constexpr int AS_OFF = B_OFF + B_SLOTS * B_SLOT;
   static constexpr int PREFIX_MAX = PREFIX_MAX_;       // groups whose tile prefix is kept in LDS
   static constexpr int BSR_SLOT = BN * 16;             // MX EOI weights: 16 scale codes per column
-  static constexpr int BSR_OFF = AS_OFF + 2 * AS_SLOT;
-  static constexpr int PREFIX_OFF = BSR_OFF + 2 * BSR_SLOT;
+  static constexpr int BSR_OFF = AS_OFF + AS_N * AS_SLOT;
+  static constexpr int PREFIX_OFF = BSR_OFF + BSR_N * BSR_SLOT;
   static constexpr int TOTAL = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
   // DMA instructions per wave per stage (64 lanes x 16 bytes each)
   static constexpr int A_INSTR = BM * (KB / 16) / 64 / WAVES;
@@ -64,7 +67,9 @@ struct GGCfg {
   static_assert(TOTAL * WG_PER_CU <= 160 * 1024, "LDS budget");
   static_assert(AS_WAVES >= 1 && AS_WAVES <= WAVES && WAVES * 64 == BN, "scale copies: 64 rows / columns a wave");
   static_assert(A_INSTR >= 1 && NI % 2 == 0 && MI >= 1, "tile shape");
-  static_assert(A_SLOTS * BS_BYTES <= 2 * AS_SLOT, "grouped-K MX: per-stage A column scales fit the AS area");
+  static_assert(AS_N == 0 || A_SLOTS * BS_BYTES <= AS_N * AS_SLOT,
+                "grouped-K MX: per-stage A column scales fit the AS area");
+  static_assert((AS_N == 0 || AS_N == 2) && (BSR_N == 0 || BSR_N == 2), "scale rings have two slots or none");
 };
 using GGBig = GGCfg<256, 2, 3, 5, 1024, 1>;
 using GGSmall = GGCfg<64, 1, 3, 3, 256, 2>;

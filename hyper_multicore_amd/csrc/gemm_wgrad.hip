@@ -12,6 +12,7 @@
 // m fastest.
 template <class C, bool MX, int EPI>
 __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_wgrad_kernel(GGParams p) {
+  static_assert(!MX || C::AS_N == 2, "MX needs the AS area for the per-stage column scales of A");
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;

@@ -51,6 +51,10 @@ static std::string g_scenario;
 // Use the 256-row tiles even where the library would pick the 64-row ones (the state of a build with
 // the decode tiles switched off): planning and launch both follow it.
 static bool g_force_big = false;
+// The forward tile-configuration variant the scenario runs (gemm.hip selects it from
+// MI355MOE_GG_VARIANT; gemm_var.hip builds it).
+static int g_variant = 0;
+using GGB6 = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0>;  // gemm_var.hip
 
 #define CHECK_FAIL(...)                                         \
   do {                                                          \
@@ -1180,10 +1184,16 @@ static int sim_dispatch(const GGParams& p, bool mx, bool b_kn, int epi) {
         case EPI_SWIGLU_BF16_NUM: return sim_forward<C, false, true, EPI_SWIGLU_BF16_NUM>(p);
       }
     }
+  } else if constexpr (C::AS_N == 0) {
+    return MI355MOE_EUNSUPPORTED;
   } else if (!b_kn) {
-    switch (epi) {
-      case EPI_STORE_BF16: return sim_forward<C, true, false, EPI_STORE_BF16>(p);
-      case EPI_SWIGLU_MX: return sim_forward<C, true, false, EPI_SWIGLU_MX>(p);
+    if constexpr (C::BSR_N == 0) {
+      return MI355MOE_EUNSUPPORTED;
+    } else {
+      switch (epi) {
+        case EPI_STORE_BF16: return sim_forward<C, true, false, EPI_STORE_BF16>(p);
+        case EPI_SWIGLU_MX: return sim_forward<C, true, false, EPI_SWIGLU_MX>(p);
+      }
     }
   } else {
     switch (epi) {
@@ -1204,6 +1214,10 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   if (small) {
     if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
     return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
+  }
+  if (g_variant == MI355_GG_VARIANT_B6) {
+    const int rc = sim_dispatch<GGB6>(p, mx, b_kn, epi);
+    if (rc != MI355MOE_EUNSUPPORTED) return rc;
   }
   return sim_dispatch<GGBig>(p, mx, b_kn, epi);
 }
@@ -1546,6 +1560,19 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_bf16_eoi_decode", emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EOI); })});
   s.push_back({"emu_mx_eio_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })});
   s.push_back({"emu_mx_eoi_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EOI); })});
+  auto b6 = [](std::function<void()> f) {
+    return [f] {
+      g_variant = MI355_GG_VARIANT_B6;
+      f();
+      g_variant = 0;
+    };
+  };
+  s.push_back({"emu_b6_bf16_eio", b6(emu([=] { gemm_bf16({70, 0, 129, 300}, 512, 512, L_EIO); }))});
+  s.push_back({"emu_b6_bf16_eoi", b6(emu([=] { gemm_bf16({70, 0, 129, 300}, 512, 512, L_EOI); }))});
+  s.push_back({"emu_b6_mx_eio", b6(emu([=] { gemm_mx({70, 0, 129, 300}, 1024, 256, L_EIO); }))});
+  s.push_back({"b6_moe_bf16", b6([=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
+  s.push_back({"b6_moe_mx_eio", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
+  s.push_back({"b6_moe_mx_eoi", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EOI, 0.0); })});
   s.push_back({"emu_wgrad_bf16", emu([=] { wgrad_direct({40, 0, 97, 33}, 256, 512, false, EPI_STORE_F32); })});
   s.push_back({"emu_wgrad_mx", emu([=] { wgrad_direct({40, 0, 97, 160}, 256, 256, true, EPI_STORE_F32); })});
   // many groups: the tile prefix comes from global memory past the LDS copy
