@@ -18,6 +18,23 @@ BF16_REL_L2 = 1e-2
 MXFP8_REL_L2 = 3e-2
 
 
+def _library_features() -> int:
+    try:
+        from hyper_multicore_amd import _lib
+        return int(_lib.load().mi355moe_features())
+    except Exception:  # the library is not built: collection still works, the GPU tests fail loudly later
+        return 0
+
+
+_FEATURES = _library_features()
+
+
+def _needs(bit: int, what: str):
+    """Run a test only when the library has the optional path switched on (mi355moe_features)."""
+    return pytest.mark.skipif(not (_FEATURES & bit),
+                              reason=f"{what} is switched off in the library until its GPU tests have run")
+
+
 def _seed(s):
     torch.manual_seed(s)
     return torch.Generator().manual_seed(s)
@@ -338,7 +355,7 @@ def test_mx_weight_to_eoi_is_a_pure_relayout(gpu):
     assert int(se.cpu()[:, :, Kd // 32:].abs().sum()) == 0
 
 
-@pytest.mark.skip(reason="MXFP8 EOI GEMM path is switched off in the library until this test has run on the GPU")
+@_needs(1, "the MXFP8 EOI GEMM path")
 @pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2, [3, 40, 0, 513]])
 def test_grouped_gemm_mxfp8_eoi_matches_eio(gpu, counts):
     """Both weight layouts feed the MFMAs identical operands: the outputs are bit-identical."""
@@ -362,7 +379,7 @@ def test_grouped_gemm_mxfp8_eoi_matches_eio(gpu, counts):
     assert orc.rel_l2(out_eoi, ref) < 5e-3
 
 
-@pytest.mark.skip(reason="MXFP8 EOI GEMM path is switched off in the library until this test has run on the GPU")
+@_needs(1, "the MXFP8 EOI GEMM path")
 def test_moe_forward_mxfp8_eoi_matches_eio(gpu):
     from hyper_multicore_amd import ops
     T, H, I, E, K = 700, 1024, 512, 16, 4
@@ -380,8 +397,7 @@ def test_moe_forward_mxfp8_eoi_matches_eio(gpu):
     assert torch.equal(out_eio, out_eoi)
 
 
-_NUMERICS_SKIP = pytest.mark.skip(
-    reason="BF16 numerics options are switched off in the library until this test has run on the GPU")
+_NUMERICS_SKIP = _needs(2, "the BF16 numerics options")
 
 
 @_NUMERICS_SKIP
@@ -482,8 +498,7 @@ def test_moe_forward_decode_shape(gpu, precision):
         assert orc.rel_l2(out, ref) < MXFP8_REL_L2
 
 
-_BACKWARD_SKIP = pytest.mark.skip(
-    reason="the expert backward is switched off in the library until this test has run on the GPU")
+_BACKWARD_SKIP = _needs(8, "the expert backward")
 
 
 @_BACKWARD_SKIP
@@ -547,8 +562,7 @@ def test_module_autograd_gradients(gpu):
 # ------------------------------------------------------------------------------------------------
 # RouteGrad
 # ------------------------------------------------------------------------------------------------
-_ROUTE_GRAD_SKIP = pytest.mark.skip(
-    reason="RouteGrad is switched off in the library until this test has run on the GPU")
+_ROUTE_GRAD_SKIP = _needs(16, "RouteGrad")
 
 
 @_ROUTE_GRAD_SKIP
@@ -631,8 +645,7 @@ def test_megagate_module_gradients_match_torch(gpu, scoring, K, vision):
 # ------------------------------------------------------------------------------------------------
 # Dual-axis MX weight quantisation
 # ------------------------------------------------------------------------------------------------
-@pytest.mark.skip(reason="the dual-axis MX weight quantisation is switched off in the library until this test "
-                         "has run on the GPU")
+@_needs(32, "the dual-axis MX weight quantisation")
 @pytest.mark.parametrize("G,M,N", [(3, 128, 320), (2, 64, 64), (1, 192, 1024)])
 def test_mx_quantize_weight_dual_axis(gpu, G, M, N):
     """Both axes equal the single-axis kernels and the oracle bit for bit (col: blocks along M per
@@ -660,8 +673,7 @@ def test_mx_quantize_weight_dual_axis(gpu, G, M, N):
 # ------------------------------------------------------------------------------------------------
 # MXFP8 expert backward
 # ------------------------------------------------------------------------------------------------
-_MX_BACKWARD_SKIP = pytest.mark.skip(
-    reason="the MXFP8 expert backward is switched off in the library until this test has run on the GPU")
+_MX_BACKWARD_SKIP = _needs(64, "the MXFP8 expert backward")
 
 
 def _mx_roots(w: torch.Tensor):
