@@ -1,8 +1,11 @@
-// Device building blocks of the persistent grouped GEMM shared by gemm.hip (forward kernels) and
-// gemm_wgrad.hip (grouped-K weight-gradient kernels): the direct-to-LDS copy and the waits, operand
-// fragments, the LDS fragment reads and MFMAs, and the software-pipelined K loop. The kernels of the
-// two files are compiled in separate translation units: with both kernel families in one module the
-// compiler schedules the forward kernels' scalar address code differently.
+// Device building blocks of the persistent grouped GEMM shared by gemm.hip (forward kernels, default
+// configurations), gemm_var.hip (configuration variants) and gemm_wgrad.hip (grouped-K weight-gradient
+// kernels): the direct-to-LDS copy and the waits, the software-pipelined K loop, the forward kernel
+// and its launch. The three files are separate translation units: with other kernel families in the
+// same module the compiler schedules the default kernels' scalar address code differently.
+// Measurement builds of gemm.hip only (never shipped): -DGG_ABLATE_COMPUTE drops the MFMAs and LDS
+// fragment reads (copy ceiling), -DGG_ABLATE_DMA drops the copies (compute ceiling), -DGG_TRACE records
+// per-step timestamps of the first workgroups (read back with mi355_gg_trace_read).
 #pragma once
 #include <type_traits>
 #include "common.h"
@@ -64,9 +67,6 @@ MI355_DEV void wait_vm(int n) {
       else asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
   }
 }
-
-
-
 
 #ifdef GG_TRACE
 __device__ unsigned long long gg_trace[4 * 8 * 64 * 5];
