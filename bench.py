@@ -177,6 +177,11 @@ def roofline(c: dict, work: dict, gmm1_ms: float) -> dict:
             "hbm_frac": round(work["g1_bytes"] / sec / PEAK["hbm"], 4)}
 
 
+def _library_features() -> int:
+    from hyper_multicore_amd import ops
+    return ops.features()
+
+
 def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
     """The oracle's restatement of the reference CPU path (MegaGate._torch_forward + the
     TorchExperts CPU loop, bf16 F.linear) on a prefix of the same synthetic batch."""
@@ -296,7 +301,9 @@ def main() -> int:
         "config": {"workload": args.config, "baseline_config_index": c["idx"], "tokens": c["T"], "experts": c["E"],
                    "top_k": c["K"], "hidden": c["H"], "intermediate": c["I"], "router": c["scoring"],
                    "groups": f"{c['groups']}/{c['topk_groups']}", "parallelism": "ep1",
-                   "weight_layout": res["weight_layout"]},
+                   "weight_layout": res["weight_layout"],
+                   "gemm_variant": os.environ.get("MI355MOE_GG_VARIANT", "default"),
+                   "library_features": _library_features()},
         "layer_tflops": res["layer_tflops"],
         "layer_mfma_frac": res["layer_mfma_frac"],
         "active_experts": res["active_experts"],
