@@ -24,6 +24,8 @@ FEATURE_BACKWARD = 8
 FEATURE_ROUTE_GRAD = 16
 FEATURE_MX_WEIGHT_PREP = 32
 FEATURE_MX_BACKWARD = 64
+FEATURE_DIRECT_GEMM = 128
+GEMM_VARIANT = {"default": 0, "b6": 1, "dv": 2}
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}
@@ -94,6 +96,7 @@ class BackwardArgs(Structure):
 _SIGNATURES = [
     ("mi355moe_abi_version", c_int32, []),
     ("mi355moe_features", c_int32, []),
+    ("mi355moe_set_gemm_variant", c_int32, [c_int32]),
     ("mi355moe_gate_logits_workspace_size", c_size_t, [c_int64, c_int32, c_int32]),
     ("mi355moe_gate_logits", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
                                        c_void_p, c_void_p, c_size_t, c_void_p]),

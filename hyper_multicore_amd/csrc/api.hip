@@ -16,7 +16,15 @@ extern "C" int mi355moe_features(void) {
          (mi355_backward_enabled() ? MI355MOE_FEATURE_BACKWARD : 0) |
          (mi355_route_grad_enabled() ? MI355MOE_FEATURE_ROUTE_GRAD : 0) |
          (mi355_mx_weight_prep_enabled() ? MI355MOE_FEATURE_MX_WEIGHT_PREP : 0) |
-         (mi355_mx_backward_enabled() ? MI355MOE_FEATURE_MX_BACKWARD : 0);
+         (mi355_mx_backward_enabled() ? MI355MOE_FEATURE_MX_BACKWARD : 0) |
+         (mi355_direct_gemm_enabled() ? MI355MOE_FEATURE_DIRECT_GEMM : 0);
+}
+
+extern "C" int mi355moe_set_gemm_variant(int variant) {
+  if (variant != MI355_GG_VARIANT_DEFAULT && variant != MI355_GG_VARIANT_B6 && variant != MI355_GG_VARIANT_DV)
+    return MI355MOE_EUNSUPPORTED;
+  if (variant == MI355_GG_VARIANT_DV && !mi355_direct_gemm_enabled()) return MI355MOE_EUNSUPPORTED;
+  return mi355_gg_set_variant(variant);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -152,6 +160,7 @@ extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32
   GGParams p = {};
   p.A = (const uint8_t*)x;
   p.lda_bytes = (int64_t)kdim * 2;
+  p.a_bytes = rows * kdim * 2;
   p.a_row_div = 1;
   p.B = (const uint8_t*)w;
   p.b_group_stride = (int64_t)kdim * ndim * 2;
@@ -190,6 +199,7 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
   GGParams p = {};
   p.A = xq;
   p.lda_bytes = kdim;
+  p.a_bytes = rows * kdim;
   p.a_row_div = 1;
   p.a_scale = x_scale;
   p.a_scale_ld = kdim / 32;
@@ -326,6 +336,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   GGParams p1 = {};
   p1.A = a1;
   p1.lda_bytes = (int64_t)H * esize;
+  p1.a_bytes = T * H * esize;
   p1.a_row_index = gather;
   p1.a_row_div = K;
   p1.a_scale = mx ? (const uint8_t*)(ws + L.xs) : nullptr;
@@ -358,6 +369,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   GGParams p2 = {};
   p2.A = (const uint8_t*)(ws + L.act);
   p2.lda_bytes = (int64_t)I * esize;
+  p2.a_bytes = T * K * I * esize;
   p2.a_row_div = 1;
   p2.a_scale = mx ? (const uint8_t*)(ws + L.act_scale) : nullptr;
   p2.a_scale_ld = mi355_mx_scale_ld(I);

@@ -43,6 +43,10 @@ struct GGParams {
   int32_t m_tiles;
   int64_t c_group_stride;
   const uint8_t* zero_row;   // >= 2 * max(m_rows, N) zero bytes (rows past a group's end)
+  // Bytes of the activation tensor A (0: not given). The direct-weight configuration addresses A
+  // with 32-bit offsets and runs only when this is set and below 4 GiB. Last member, so the other
+  // members keep their kernel-argument offsets.
+  int64_t a_bytes;
 };
 
 
@@ -83,12 +87,16 @@ struct MxGroupedQuant {
 };
 int mi355_mx_quant_grouped(const MxGroupedQuant& q, hipStream_t stream);
 int mi355_num_cus();  // CU count of the current device (cached per device)
-// Forward tile-configuration variants for measurement (MI355MOE_GG_VARIANT=b6; default 0). A variant
+// Forward tile-configuration variants for measurement (MI355MOE_GG_VARIANT=b6 or dv; default 0). A variant
 // keeps the default's tile height, so tile plans are shared; it answers MI355MOE_EUNSUPPORTED for the
 // paths it does not build, which then run on the default configuration.
-enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1 };
+enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1, MI355_GG_VARIANT_DV = 2 };
 int mi355_gg_variant();
+int mi355_gg_set_variant(int variant);  // returns the previous variant
 int mi355_grouped_gemm_variant(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
+// The direct-weight configuration (gemm_direct.hip), variant "dv"; MI355MOE_EUNSUPPORTED outside its
+// domain (K-contiguous weights, K a multiple of 8 stages, bf16 store / SwiGLU epilogues).
+int mi355_grouped_gemm_direct(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
 #include "features.h"
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {
   return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;

@@ -93,12 +93,23 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   return dispatch_gg<GGBig>(p, mx, b_kn, epi, stream);
 }
 
+// The forward configuration variant: initially from MI355MOE_GG_VARIANT, then as set through
+// mi355moe_set_gemm_variant (a measurement control).
+static int g_gg_variant = -1;
 int mi355_gg_variant() {
-  static const int v = [] {
+  if (g_gg_variant < 0) {
     const char* s = getenv("MI355MOE_GG_VARIANT");
-    return (s != nullptr && strcmp(s, "b6") == 0) ? (int)MI355_GG_VARIANT_B6 : (int)MI355_GG_VARIANT_DEFAULT;
-  }();
-  return v;
+    int v = MI355_GG_VARIANT_DEFAULT;
+    if (s != nullptr && strcmp(s, "b6") == 0) v = MI355_GG_VARIANT_B6;
+    if (s != nullptr && strcmp(s, "dv") == 0 && mi355_direct_gemm_enabled()) v = MI355_GG_VARIANT_DV;
+    g_gg_variant = v;
+  }
+  return g_gg_variant;
+}
+int mi355_gg_set_variant(int variant) {
+  const int prev = mi355_gg_variant();
+  g_gg_variant = variant;
+  return prev;
 }
 
 int mi355_gg_bm(bool small) { return small ? GGSmall::BM : GGBig::BM; }

@@ -220,141 +220,7 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
     }
     __syncthreads();  // all waves are done reading the ring before the epilogue reuses LDS
 
-    // ---- epilogue -----------------------------------------------------------------------
-    // acc[mi][ni][r] holds row wm*WM + mi*32 + 8*(r/4) + 4*(lane/32) + r%4,
-    // column wn*WN + ni*32 + lane%32 of the tile.
-    if (EPI == EPI_STORE_F32) {
-      float* outp = (float*)p.C;
-#pragma unroll
-      for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < C::NI; ++ni) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            int col = nt * C::BN + wn * C::WN + ni * 32 + (lane & 31);
-            if (row < rows_valid && col < p.N) {
-              int64_t routed = tile_row0 + row;
-              int64_t orow = p.c_row_index ? (int64_t)p.c_row_index[routed] : routed;
-              outp[split * p.c_split_stride + orow * p.ldc + col] = acc[mi][ni][r];
-            }
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-    } else if (EPI == EPI_STORE_BF16) {
-      constexpr int RS = C::EPI_RS_BF16;  // staged row stride (bytes)
-#pragma unroll
-      for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < C::NI; ++ni) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            int col = wn * C::WN + ni * 32 + (lane & 31);
-            *(uint16_t*)(smem + row * RS + col * 2) = f32_to_bf16(acc[mi][ni][r]);
-          }
-          __builtin_amdgcn_sched_barrier(0);  // one 32x32 block at a time: bounded register use
-        }
-      __syncthreads();
-      uint16_t* outp = (uint16_t*)p.C;
-      for (int id = tid; id < C::BM * (C::BN / 8); id += C::THREADS) {
-        int row = id >> 5, ch = id & 31;
-        int col = nt * C::BN + ch * 8;
-        if (row < rows_valid && col < p.N)
-          *(uint4*)(outp + (tile_row0 + row) * p.ldc + col) = *(const uint4*)(smem + row * RS + ch * 16);
-      }
-      __syncthreads();
-    } else {
-      // SwiGLU: subtiles ni < NI/2 hold gate, ni + NI/2 the matching up columns.
-      constexpr int RS = C::EPI_RS_ACT;  // fp32 staged act row stride
-#pragma unroll
-      for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < C::NI / 2; ++ni) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            int row = wm * C::WM + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            int col = wn * (C::WN / 2) + ni * 32 + (lane & 31);
-            float gte = bf16_to_f32(f32_to_bf16(acc[mi][ni][r]));
-            float up = bf16_to_f32(f32_to_bf16(acc[mi][ni + C::NI / 2][r]));
-            float act;
-            if (EPI == EPI_SWIGLU_BF16_NUM && p.swiglu_limit > 0.0f) {
-              // MegaMoeNumericsOptions clamp: up to [-L, L]; gate to <= L before SiLU, or SiLU(gate)
-              // to <= L after it
-              const float L = p.swiglu_limit;
-              up = fminf(fmaxf(up, -L), L);
-              if (p.swiglu_after_silu) act = fminf(gte / (1.0f + __expf(-gte)), L) * up;
-              else {
-                const float gc = fminf(gte, L);
-                act = gc / (1.0f + __expf(-gc)) * up;
-              }
-            } else {
-              act = gte / (1.0f + __expf(-gte)) * up;
-            }
-            *(float*)(smem + row * RS + col * 4) = act;
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      __syncthreads();
-      if (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_BF16_NUM) {
-        uint16_t* outp = (uint16_t*)p.C;
-        for (int id = tid; id < C::BM * 16; id += C::THREADS) {
-          int row = id >> 4, ch = id & 15;
-          if (row < rows_valid) {
-            const float* s = (const float*)(smem + row * RS + ch * 32);
-            uint4 o;
-            if (EPI == EPI_SWIGLU_BF16_NUM) {
-              float v[8];
-#pragma unroll
-              for (int i = 0; i < 8; ++i) v[i] = s[i];
-              if (p.row_prob != nullptr) {
-                // probabilities before FC2: bf16(fp32(bf16(act)) * p) (two roundings, the reference
-                // contract); row r of the tile is slot a_row_index[r]
-                const float pr = p.row_prob[p.a_row_index[tile_row0 + row]];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = bf16_to_f32(f32_to_bf16(v[i])) * pr;
-              }
-              o.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-              o.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-              o.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
-              o.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
-            } else {
-              o.x = f32_to_bf16(s[0]) | ((uint32_t)f32_to_bf16(s[1]) << 16);
-              o.y = f32_to_bf16(s[2]) | ((uint32_t)f32_to_bf16(s[3]) << 16);
-              o.z = f32_to_bf16(s[4]) | ((uint32_t)f32_to_bf16(s[5]) << 16);
-              o.w = f32_to_bf16(s[6]) | ((uint32_t)f32_to_bf16(s[7]) << 16);
-            }
-            *(uint4*)(outp + (tile_row0 + row) * p.ldc + nt * (C::BN / 2) + ch * 8) = o;
-          }
-        }
-      } else {
-        uint8_t* outp = (uint8_t*)p.C;
-        for (int id = tid; id < C::BM * 4; id += C::THREADS) {
-          int row = id >> 2, blk = id & 3;
-          if (row < rows_valid) {
-            const float* s = (const float*)(smem + row * RS + blk * 128);
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(s[i]));
-            uint32_t code = mx_scale_code(amax);
-            uint32_t w[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              uint32_t b0 = f32_to_e4m3(mx_apply_inv_scale(s[4 * i + 0], code));
-              uint32_t b1 = f32_to_e4m3(mx_apply_inv_scale(s[4 * i + 1], code));
-              uint32_t b2 = f32_to_e4m3(mx_apply_inv_scale(s[4 * i + 2], code));
-              uint32_t b3 = f32_to_e4m3(mx_apply_inv_scale(s[4 * i + 3], code));
-              w[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-            }
-            uint8_t* dst = outp + (tile_row0 + row) * p.ldc + nt * (C::BN / 2) + blk * 32;
-            *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
-            *(uint4*)(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-            p.c_scale[(tile_row0 + row) * p.c_scale_ld + nt * 4 + blk] = (uint8_t)code;
-          }
-        }
-      }
-      __syncthreads();
-    }
+#include "gemm_epilogue.inc"
   }
 }
 

@@ -347,6 +347,19 @@ def features() -> int:
     return int(_lib.load().mi355moe_features())
 
 
+def set_gemm_variant(name: str) -> str:
+    """Select the forward grouped-GEMM configuration for the following calls in this process
+    ("default", "b6" or "dv"; a measurement control, mi355moe_set_gemm_variant) and return the
+    previous one. Raises ``ValueError`` for an unknown name and ``RuntimeError`` when the library
+    has the variant switched off."""
+    if name not in _lib.GEMM_VARIANT:
+        raise ValueError(f"unknown GEMM variant {name!r}; expected one of {sorted(_lib.GEMM_VARIANT)}")
+    rc = int(_lib.load().mi355moe_set_gemm_variant(_lib.GEMM_VARIANT[name]))
+    if rc < 0:
+        raise RuntimeError(f"GEMM variant {name!r} is switched off in this library build")
+    return {v: k for k, v in _lib.GEMM_VARIANT.items()}[rc]
+
+
 def mx_weight_to_eoi(col_data: torch.Tensor, col_scale: torch.Tensor):
     """Re-layout an MX weight root (col_data [G, K, N], col_scale [G, K/64, N, 2]) with K contiguous:
     (data e4m3fn [G, N, K], scale uint8 [G, N, ld]), ld = K/32 padded to a multiple of 16. Values

@@ -136,3 +136,26 @@ def test_gpu_ops_refuse_cpu_tensors():
     from hyper_multicore_amd import ops
     with pytest.raises(TypeError):
         ops.gate_route(torch.zeros(2, 8), torch.zeros(8), top_k=2, scoring_func="softmax", routed_scaling_factor=1.0)
+
+
+def test_gemm_variant_control():
+    """The measurement control selects known variants only, returns the previous one, and refuses a
+    variant whose feature bit is clear (host-side state only; nothing is launched)."""
+    from hyper_multicore_amd import _lib, ops
+    lib = _lib.load()
+    assert lib.mi355moe_set_gemm_variant(7) == _lib.EUNSUPPORTED
+    prev = lib.mi355moe_set_gemm_variant(_lib.GEMM_VARIANT["b6"])
+    assert prev in _lib.GEMM_VARIANT.values()
+    assert lib.mi355moe_set_gemm_variant(prev) == _lib.GEMM_VARIANT["b6"]
+    direct_on = bool(ops.features() & _lib.FEATURE_DIRECT_GEMM)
+    rc = lib.mi355moe_set_gemm_variant(_lib.GEMM_VARIANT["dv"])
+    if direct_on:
+        assert rc == prev
+        lib.mi355moe_set_gemm_variant(prev)
+    else:
+        assert rc == _lib.EUNSUPPORTED
+        with pytest.raises(RuntimeError):
+            ops.set_gemm_variant("dv")
+    with pytest.raises(ValueError):
+        ops.set_gemm_variant("fastest")
+    assert ops.set_gemm_variant("default") in _lib.GEMM_VARIANT
