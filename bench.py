@@ -11,6 +11,7 @@ oracle's restatement of the reference CPU path, on a bounded token prefix). Othe
 reported under "extra" (``--extra none`` skips them).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config dsv3_bf16] [--extra all]
+                      [--gemm-variant default|b6|dv] [--gemm-shapes]
 """
 from __future__ import annotations
 
@@ -249,6 +250,56 @@ def run_config(name: str, device, steps: int, warmup: int) -> dict:
     return res, layer
 
 
+def gemm_shapes(device, reps: int) -> dict:
+    """Grouped GEMMs of the DSv3 expert shapes on their own (256 experts x 256 rows; GMM1 shape
+    N = 4096, K = 7168 and GMM2 shape N = 7168, K = 2048), per weight layout and precision, timed
+    with events on the stream the library launches on, for every GEMM variant the library has on."""
+    from hyper_multicore_amd import _lib, ops
+    g = torch.Generator(device=device).manual_seed(SEED)
+    G, rows = 256, 256
+    gl = torch.full((G,), rows, dtype=torch.int64, device=device).cumsum(0)
+    feats = ops.features()
+    variants = ["default", "b6"] + (["dv"] if feats & _lib.FEATURE_DIRECT_GEMM else [])
+    out = {}
+    for name, N, K in (("gmm1_shape", 4096, 7168), ("gmm2_shape", 7168, 2048)):
+        x = torch.randn(G * rows, K, device=device, generator=g).to(torch.bfloat16)
+        w = (torch.randn(G, N, K, device=device, generator=g) * 0.006).to(torch.bfloat16)  # EOI
+        runs = {"bf16_EOI": lambda: ops.grouped_gemm_bf16(x, w, gl, "EOI")}
+        xq, xs = ops.mx_quantize_rows(x)
+        d, sc = ops.mx_quantize_cols(w.transpose(1, 2).contiguous())  # EIO col_data
+        runs["mxfp8_EIO"] = lambda: ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), sc, gl)
+        if feats & _lib.FEATURE_MX_EOI:
+            de, se = ops.mx_weight_to_eoi(d, sc)
+            runs["mxfp8_EOI"] = lambda: ops.grouped_gemm_mxfp8(xq, xs, de.view(torch.uint8), se, gl, layout="EOI")
+        flops = 2.0 * G * rows * N * K
+        for key, fn in runs.items():
+            mx = key.startswith("mxfp8")
+            wbytes = G * N * K * ((1 + 1 / 32) if mx else 2)
+            for v in variants:
+                prev = ops.set_gemm_variant(v)
+                try:
+                    fn()
+                    torch.cuda.synchronize()
+                    t0 = torch.cuda.Event(enable_timing=True)
+                    t1 = torch.cuda.Event(enable_timing=True)
+                    t0.record()
+                    for _ in range(reps):
+                        fn()
+                    t1.record()
+                    torch.cuda.synchronize()
+                    ms = t0.elapsed_time(t1) / reps
+                finally:
+                    ops.set_gemm_variant(prev)
+                peak = PEAK["mxfp8" if mx else "bf16"]
+                out[f"{name}/{key}/{v}"] = {"ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
+                                           "mfma_frac": round(flops / (ms * 1e-3) / peak, 4),
+                                           "weight_tb_s": round(wbytes / (ms * 1e-3) / 1e12, 3)}
+                log(f"[bench] {name}/{key}/{v}: {out[f'{name}/{key}/{v}']}")
+        del x, w, xq, xs, d, sc
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,6 +308,10 @@ def main() -> int:
     ap.add_argument("--config", default="dsv3_bf16", choices=sorted(CONFIGS))
     ap.add_argument("--extra", default="all", help="'all', 'none' or comma list of extra configs")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv"],
+                    help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
+    ap.add_argument("--gemm-shapes", action="store_true",
+                    help="time the DSv3-shape grouped GEMMs on their own per layout and variant (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X only: this build runs every expert on one GPU (EP=1) and has no "
@@ -269,6 +324,15 @@ def main() -> int:
     _lib.load()
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    from hyper_multicore_amd import ops
+    if args.gemm_shapes:
+        print(json.dumps({"gemm_shapes": gemm_shapes(device, max(3, args.steps // 2)),
+                          "library_features": _library_features()}), flush=True)
+        return 0
+    if args.gemm_variant is not None:
+        ops.set_gemm_variant(args.gemm_variant)
+    gemm_variant = ops.set_gemm_variant("default")
+    ops.set_gemm_variant(gemm_variant)
     log(f"[bench] workload {args.config}: steps={args.steps} warmup={args.warmup}")
     res, layer = run_config(args.config, device, args.steps, args.warmup)
     c = layer.c
@@ -302,7 +366,7 @@ def main() -> int:
                    "top_k": c["K"], "hidden": c["H"], "intermediate": c["I"], "router": c["scoring"],
                    "groups": f"{c['groups']}/{c['topk_groups']}", "parallelism": "ep1",
                    "weight_layout": res["weight_layout"],
-                   "gemm_variant": os.environ.get("MI355MOE_GG_VARIANT", "default"),
+                   "gemm_variant": gemm_variant,
                    "library_features": _library_features()},
         "layer_tflops": res["layer_tflops"],
         "layer_mfma_frac": res["layer_mfma_frac"],
