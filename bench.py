@@ -11,7 +11,7 @@ oracle's restatement of the reference CPU path, on a bounded token prefix). Othe
 reported under "extra" (``--extra none`` skips them).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config dsv3_bf16] [--extra all]
-                      [--gemm-variant default|b6|dv] [--gemm-shapes]
+                      [--gemm-variant default|b6|dv|sp|sp4] [--gemm-shapes]
 """
 from __future__ import annotations
 
@@ -259,7 +259,8 @@ def gemm_shapes(device, reps: int) -> dict:
     G, rows = 256, 256
     gl = torch.full((G,), rows, dtype=torch.int64, device=device).cumsum(0)
     feats = ops.features()
-    variants = ["default", "b6"] + (["dv"] if feats & _lib.FEATURE_DIRECT_GEMM else [])
+    variants = (["default", "b6"] + (["dv"] if feats & _lib.FEATURE_DIRECT_GEMM else [])
+                + (["sp", "sp4"] if feats & _lib.FEATURE_SPLIT_ROLES else []))
     out = {}
     for name, N, K in (("gmm1_shape", 4096, 7168), ("gmm2_shape", 7168, 2048)):
         x = torch.randn(G * rows, K, device=device, generator=g).to(torch.bfloat16)
@@ -308,7 +309,7 @@ def main() -> int:
     ap.add_argument("--config", default="dsv3_bf16", choices=sorted(CONFIGS))
     ap.add_argument("--extra", default="all", help="'all', 'none' or comma list of extra configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv"],
+    ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv", "sp", "sp4"],
                     help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="time the DSv3-shape grouped GEMMs on their own per layout and variant (one JSON line)")

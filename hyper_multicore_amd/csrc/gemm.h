@@ -87,10 +87,11 @@ struct MxGroupedQuant {
 };
 int mi355_mx_quant_grouped(const MxGroupedQuant& q, hipStream_t stream);
 int mi355_num_cus();  // CU count of the current device (cached per device)
-// Forward tile-configuration variants for measurement (MI355MOE_GG_VARIANT=b6 or dv; default 0). A variant
+// Forward tile-configuration variants for measurement (MI355MOE_GG_VARIANT=b6, dv, sp or sp4; default 0). A variant
 // keeps the default's tile height, so tile plans are shared; it answers MI355MOE_EUNSUPPORTED for the
 // paths it does not build, which then run on the default configuration.
-enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1, MI355_GG_VARIANT_DV = 2 };
+enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1, MI355_GG_VARIANT_DV = 2, MI355_GG_VARIANT_SP = 3,
+       MI355_GG_VARIANT_SP4 = 4 };
 int mi355_gg_variant();
 int mi355_gg_set_variant(int variant);  // returns the previous variant
 int mi355_grouped_gemm_variant(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);

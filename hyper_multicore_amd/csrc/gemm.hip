@@ -102,6 +102,8 @@ int mi355_gg_variant() {
     int v = MI355_GG_VARIANT_DEFAULT;
     if (s != nullptr && strcmp(s, "b6") == 0) v = MI355_GG_VARIANT_B6;
     if (s != nullptr && strcmp(s, "dv") == 0 && mi355_direct_gemm_enabled()) v = MI355_GG_VARIANT_DV;
+    if (s != nullptr && strcmp(s, "sp") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP;
+    if (s != nullptr && strcmp(s, "sp4") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP4;
     g_gg_variant = v;
   }
   return g_gg_variant;

@@ -25,15 +25,6 @@ struct DevMem {
   }
 };
 
-// A wave-uniform pointer held in scalar registers (the group index comes from an LDS search, which
-// the compiler cannot see is uniform; the scalar-base loads need the base in SGPRs).
-MI355_DEV const uint8_t* direct_uniform(const uint8_t* ptr) {
-  const uint64_t v = (uint64_t)(uintptr_t)ptr;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
 // Registers written by loads that have landed: uses below this point depend on it.
 MI355_DEV void direct_tie(v4i& a, v4i& b, v4i& c, v4i& d) { asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)); }
 MI355_DEV void direct_tie(v4i& a, v4i& b) { asm volatile("" : "+v"(a), "+v"(b)); }
@@ -150,12 +141,13 @@ __global__ __launch_bounds__(GGDirect::THREADS, 1) void grouped_gemm_direct_kern
   for (int round = 0;; ++round) {
     const int L = round * (int)gridDim.x + xcd * per_xcd + slot;
     if (L >= total) break;
+    constexpr bool copy_role_a = true, copy_role_b = true;
 #include "gemm_item_fwd.inc"
     DirectPlan d = direct_plan(p, g, nt, tile_row0, rows_valid, SWIGLU, MX, wave, lane);
-    d.a_base = direct_uniform(d.a_base);
-    d.as_base = direct_uniform(d.as_base);
-    d.b_base = direct_uniform(d.b_base);
-    d.bs_base = direct_uniform(d.bs_base);
+    d.a_base = gg_uniform(d.a_base);
+    d.as_base = gg_uniform(d.as_base);
+    d.b_base = gg_uniform(d.b_base);
+    d.bs_base = gg_uniform(d.bs_base);
 
     v16f acc[C::MI][C::NI];
 #pragma unroll

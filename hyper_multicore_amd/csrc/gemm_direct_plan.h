@@ -43,6 +43,8 @@ struct GGDirect {
   static constexpr int A_BYTES = BM * KB;               // 16 KB
   static constexpr int A_INSTR = BM * (KB / 16) / 64 / WAVES;
   static constexpr int B_INSTR = 1;                     // (weight copies of the LDS plan: unused)
+  static constexpr bool SPLIT = false, OFFS = false;    // (the LDS plan's copy roles and addressing: unused)
+  static constexpr int A_PER = A_INSTR, B_PER = B_INSTR;
   static constexpr int B_LOADS = 2 * NI;                // 16-byte weight loads per stage and lane
   static constexpr int AS_GROUP = 8;                    // MX: scale codes per fetch = 8 stages
   static constexpr int AS_SLOT = BM * 16;

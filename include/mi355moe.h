@@ -57,19 +57,22 @@ enum {
   MI355MOE_FEATURE_MX_WEIGHT_PREP = 32, /* mi355moe_mx_quantize_weight */
   MI355MOE_FEATURE_MX_BACKWARD = 64,  /* mi355moe_moe_backward with precision MXFP8 */
   MI355MOE_FEATURE_DIRECT_GEMM = 128, /* grouped-GEMM configuration "dv" (mi355moe_set_gemm_variant) */
+  MI355MOE_FEATURE_SPLIT_ROLES = 256, /* grouped-GEMM configurations "sp" / "sp4" (split copy roles) */
 };
 int mi355moe_features(void);
 
 /* Forward grouped-GEMM configuration used by the calls that follow in this process (a measurement
  * control; no counterpart in the reference, whose GEMM tiling is fixed by its tuning tables):
- * MI355MOE_GEMM_DEFAULT, MI355MOE_GEMM_B6 (256 x 256 tiles with a sixth weight slot) or
+ * MI355MOE_GEMM_DEFAULT, MI355MOE_GEMM_B6 (256 x 256 tiles with a sixth weight slot),
  * MI355MOE_GEMM_DIRECT ("dv": K-contiguous weights loaded straight into registers, activations
  * through an 8-slot LDS ring; bf16 EOI and MXFP8 EOI GEMMs whose K is a whole number of 8 stages,
- * others keep the default). The initial value comes from the environment variable
- * MI355MOE_GG_VARIANT ("b6", "dv"). Returns the previous variant, or MI355MOE_EUNSUPPORTED (and
+ * others keep the default), MI355MOE_GEMM_SPLIT / _SPLIT_A4 ("sp" / "sp4": two waves copy the
+ * activations and two the weights, 3 + 6 or 4 + 5 ring slots; MXFP8 GEMMs on EIO weight roots). The
+ * initial value comes from the environment variable MI355MOE_GG_VARIANT ("b6", "dv", "sp", "sp4"). Returns the previous variant, or MI355MOE_EUNSUPPORTED (and
  * changes nothing) for an unknown variant or one whose feature bit is clear. Not synchronised with
  * calls running on other host threads. */
-enum { MI355MOE_GEMM_DEFAULT = 0, MI355MOE_GEMM_B6 = 1, MI355MOE_GEMM_DIRECT = 2 };
+enum { MI355MOE_GEMM_DEFAULT = 0, MI355MOE_GEMM_B6 = 1, MI355MOE_GEMM_DIRECT = 2, MI355MOE_GEMM_SPLIT = 3,
+       MI355MOE_GEMM_SPLIT_A4 = 4 };
 int mi355moe_set_gemm_variant(int variant);
 
 /* ---------------------------------------------------------------------------------------------

@@ -55,6 +55,8 @@ static bool g_force_big = false;
 // MI355MOE_GG_VARIANT; gemm_var.hip builds it).
 static int g_variant = 0;
 using GGB6 = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0>;  // gemm_var.hip
+using GGSplit = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0, true>;   // gemm_var.hip (sp)
+using GGSplitA4 = GGCfg<256, 2, 4, 5, 1024, 1, 2, 0, true>; // gemm_var.hip (sp4)
 
 #define CHECK_FAIL(...)                                         \
   do {                                                          \
@@ -332,6 +334,10 @@ struct CheckDma {
     if (!enable) return;
     g_rec->push_back({(const uint8_t*)g, SZ, off, g_iter});
   }
+  template <int SZ>
+  static void copy_so(const uint8_t* base, uint32_t voff, uint32_t off, uint8_t* smem, int enable) {
+    copy<SZ>(base + voff, off, smem, enable);
+  }
 };
 
 // R_ASS: grouped-K MX only - the per-stage column scales of A, A_SLOTS slots of 512 bytes at AS_OFF
@@ -344,7 +350,7 @@ static const char* region_name(int r) {
 // One lane's copy sequence of one work item, replayed in the K loop's order (k_loop in gemm.hip:
 // prologue, the wait for stage 0, then for every pipelined step k the wait for stage k + 1 and the
 // copy items of the step).
-template <class C, bool MX, bool B_KN, bool LA, bool GK>
+template <class C, bool MX, bool B_KN, bool LA, bool GK, bool LB = true>
 static void record_schedule(const CopyPlan<C>& cp, int nk, int wave, std::vector<Rec>& rec, std::vector<Wait>& waits) {
   uint8_t* smem = nullptr;
   g_rec = &rec;
@@ -357,7 +363,7 @@ static void record_schedule(const CopyPlan<C>& cp, int nk, int wave, std::vector
       waits.push_back({rec.size(), k + 1, younger_than<C, LA>(k + 1, k - 1, nk, la_n, lb_n)});
       g_iter = k;
       for (int it = 0; it < StepShape<C, MX, 1, GK>::ITEMS; ++it)
-        issue_item<C, MX, B_KN, LA, GK, D>(cp, k, nk, wave, smem, it);
+        issue_item<C, MX, B_KN, LA, GK, D, LB>(cp, k, nk, wave, smem, it);
       issue_scales_item<C, MX, B_KN, LA, D, GK>(cp, k, nk, wave, smem);
     }
   }
@@ -501,7 +507,7 @@ template <class C, bool MX, bool B_KN, bool SWIGLU, bool GK>
 static void check_lane(const GGParams& p, const Layout& L, ItemCtx& it, int wave, int lane, bool la,
                        const std::vector<Rec>& rec, const std::vector<Wait>& waits) {
   const int slots[R_N] = {C::A_SLOTS, C::B_SLOTS, C::B_SLOTS, 2, 2, C::A_SLOTS};
-  const int per_fill[R_N] = {C::A_INSTR, C::B_INSTR, 1, 1, 1, 1};
+  const int per_fill[R_N] = {C::A_PER, C::B_PER, 1, C::SPLIT ? 2 : 1, 1, 1};
   int fills[R_N][8] = {};
   std::vector<Decoded> dec(rec.size());
   for (size_t i = 0; i < rec.size(); ++i) {
@@ -780,19 +786,23 @@ struct FillDma {
     if (!enable) return;
     memcpy(smem + off + (uint32_t)SZ * g_fill_lane, g, SZ);
   }
+  template <int SZ>
+  static void copy_so(const uint8_t* base, uint32_t voff, uint32_t off, uint8_t* smem, int enable) {
+    copy<SZ>(base + voff, off, smem, enable);
+  }
 };
 
-template <class C, bool MX, bool B_KN, bool LA, bool GK>
+template <class C, bool MX, bool B_KN, bool LA, bool GK, bool LB = true>
 static void fill_prologue(const CopyPlan<C>& cp, int nk, int wave, uint8_t* smem) {
   using D = FillDma;
 #include "../../hyper_multicore_amd/csrc/gemm_kloop_prologue.inc"
   (void)la_n;
   (void)lb_n;
 }
-template <class C, bool MX, bool B_KN, bool LA, bool GK>
+template <class C, bool MX, bool B_KN, bool LA, bool GK, bool LB = true>
 static void fill_step(const CopyPlan<C>& cp, int k, int nk, int wave, uint8_t* smem) {
   for (int it = 0; it < StepShape<C, MX, 1, GK>::ITEMS; ++it)
-    issue_item<C, MX, B_KN, LA, GK, FillDma>(cp, k, nk, wave, smem, it);
+    issue_item<C, MX, B_KN, LA, GK, FillDma, LB>(cp, k, nk, wave, smem, it);
   issue_scales_item<C, MX, B_KN, LA, FillDma, GK>(cp, k, nk, wave, smem);
 }
 
@@ -890,8 +900,11 @@ static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la
   for (int w = 0; w < C::WAVES; ++w)
     for (int l = 0; l < 64; ++l) {
       g_fill_lane = l;
-      if (la[w]) fill_prologue<C, MX, B_KN, true, GK>(cps[w][l], nk, w, smem);
-      else fill_prologue<C, MX, B_KN, false, GK>(cps[w][l], nk, w, smem);
+      const bool lb = wave_copies_b<C>(w);
+      if (la[w] && lb) fill_prologue<C, MX, B_KN, true, GK>(cps[w][l], nk, w, smem);
+      else if (la[w]) fill_prologue<C, MX, B_KN, true, GK, false>(cps[w][l], nk, w, smem);
+      else if (lb) fill_prologue<C, MX, B_KN, false, GK>(cps[w][l], nk, w, smem);
+      else fill_prologue<C, MX, B_KN, false, GK, false>(cps[w][l], nk, w, smem);
     }
   for (int w = 0; w < C::WAVES; ++w)
     emu_wave_step<C, MX, B_KN, GK>(tiles[w], nm[w], smem, nk, w / C::WGN, w % C::WGN, -1);
@@ -902,8 +915,11 @@ static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la
       for (int w = 0; w < C::WAVES; ++w)
         for (int l = 0; l < 64; ++l) {
           g_fill_lane = l;
-          if (la[w]) fill_step<C, MX, B_KN, true, GK>(cps[w][l], k, nk, w, smem);
-          else fill_step<C, MX, B_KN, false, GK>(cps[w][l], k, nk, w, smem);
+          const bool lb = wave_copies_b<C>(w);
+          if (la[w] && lb) fill_step<C, MX, B_KN, true, GK>(cps[w][l], k, nk, w, smem);
+          else if (la[w]) fill_step<C, MX, B_KN, true, GK, false>(cps[w][l], k, nk, w, smem);
+          else if (lb) fill_step<C, MX, B_KN, false, GK>(cps[w][l], k, nk, w, smem);
+          else fill_step<C, MX, B_KN, false, GK, false>(cps[w][l], k, nk, w, smem);
         }
   }
   // compare the accumulators with the reference
@@ -973,6 +989,7 @@ static int sim_forward(const GGParams& p) {
     for (int wave = 0; wave < C::WAVES; ++wave)
       for (int lane = 0; lane < 64; ++lane) {
         const int L = L_item;
+        const bool copy_role_a = !C::SPLIT || wave < 2, copy_role_b = !C::SPLIT || wave >= 2;
 #include "../../hyper_multicore_amd/csrc/gemm_item_fwd.inc"
         cps[wave][lane] = cp;
         (void)mt;
@@ -1021,11 +1038,14 @@ static int sim_forward(const GGParams& p) {
           }
         }
         const bool la = wave_copies_a<C>(wave, rows_valid);
+        const bool lb = wave_copies_b<C>(wave);
         las[wave] = la;
         rec.clear();
         waits.clear();
-        if (la) record_schedule<C, MX, B_KN, true, false>(cp, nk, wave, rec, waits);
-        else record_schedule<C, MX, B_KN, false, false>(cp, nk, wave, rec, waits);
+        if (la && lb) record_schedule<C, MX, B_KN, true, false>(cp, nk, wave, rec, waits);
+        else if (la) record_schedule<C, MX, B_KN, true, false, false>(cp, nk, wave, rec, waits);
+        else if (lb) record_schedule<C, MX, B_KN, false, false>(cp, nk, wave, rec, waits);
+        else record_schedule<C, MX, B_KN, false, false, false>(cp, nk, wave, rec, waits);
         check_lane<C, MX, B_KN, SWIGLU, false>(p, lay, ctx, wave, lane, la, rec, waits);
       }
     check_coverage<C, MX, B_KN, false>(ctx);
@@ -1295,6 +1315,7 @@ static int sim_direct(const GGParams& p) {
     for (int wave = 0; wave < C::WAVES; ++wave)
       for (int lane = 0; lane < 64; ++lane) {
         const int L = L_item;
+        constexpr bool copy_role_a = true, copy_role_b = true;
 #include "../../hyper_multicore_amd/csrc/gemm_item_fwd.inc"
         (void)cp;
         (void)mt;
@@ -1522,6 +1543,7 @@ static int sim_direct_dispatch(const GGParams& p, bool mx, bool b_kn, int epi) {
   return epi == EPI_STORE_BF16 ? sim_direct<true, EPI_STORE_BF16>(p) : sim_direct<true, EPI_SWIGLU_MX>(p);
 }
 static long g_direct_gemms = 0;
+static long g_split_gemms = 0;
 
 // The grouped GEMM entry points the host code calls, run on the host
 template <class C>
@@ -1575,6 +1597,14 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   if (g_variant == MI355_GG_VARIANT_B6) {
     const int rc = sim_dispatch<GGB6>(p, mx, b_kn, epi);
     if (rc != MI355MOE_EUNSUPPORTED) return rc;
+  }
+  if ((g_variant == MI355_GG_VARIANT_SP || g_variant == MI355_GG_VARIANT_SP4) && gg_split_applies(p, mx, b_kn, epi)) {
+    ++g_split_gemms;
+    if (epi == EPI_SWIGLU_MX)
+      return g_variant == MI355_GG_VARIANT_SP ? sim_forward<GGSplit, true, true, EPI_SWIGLU_MX>(p)
+                                              : sim_forward<GGSplitA4, true, true, EPI_SWIGLU_MX>(p);
+    return g_variant == MI355_GG_VARIANT_SP ? sim_forward<GGSplit, true, true, EPI_STORE_BF16>(p)
+                                            : sim_forward<GGSplitA4, true, true, EPI_STORE_BF16>(p);
   }
   if (g_variant == MI355_GG_VARIANT_DV) {
     const int rc = sim_direct_dispatch(p, mx, b_kn, epi);
@@ -1937,6 +1967,28 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"b6_moe_bf16", b6([=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
   s.push_back({"b6_moe_mx_eio", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
   s.push_back({"b6_moe_mx_eoi", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EOI, 0.0); })});
+  // split copy roles (variants sp: 3 activation / 6 weight slots; sp4: 4 / 5), MXFP8 EIO; each scenario
+  // must run them
+  auto sp = [](int v, std::function<void()> f) {
+    return [v, f] {
+      const long before = g_split_gemms;
+      g_variant = v;
+      f();
+      g_variant = 0;
+      if (g_split_gemms == before) CHECK_FAIL("the split-role configuration ran no GEMM");
+    };
+  };
+  const int SP = MI355_GG_VARIANT_SP, SP4 = MI355_GG_VARIANT_SP4;
+  s.push_back({"sp_gemm_mx_eio", sp(SP, [=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EIO); })});
+  s.push_back({"sp_gemm_mx_eio_long_k", sp(SP, [=] { gemm_mx({256, 256}, 2560, 272, L_EIO); })});
+  s.push_back({"sp_gemm_mx_eio_decode_big", big(sp(SP, [=] { gemm_mx(decode_counts(48, 6), 1024, 512, L_EIO); }))});
+  s.push_back({"sp_moe_mx_eio", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
+  s.push_back({"sp_moe_mx_eio_decode_big", big(sp(SP, [=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); }))});
+  s.push_back({"sp4_gemm_mx_eio", sp(SP4, [=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EIO); })});
+  s.push_back({"sp4_moe_mx_eio", sp(SP4, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
+  s.push_back({"emu_sp_mx_eio", sp(SP, emu([=] { gemm_mx({70, 0, 129, 300}, 1024, 256, L_EIO); }))});
+  s.push_back({"emu_sp_mx_eio_decode", big(sp(SP, emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })))});
+  s.push_back({"emu_sp4_mx_eio", sp(SP4, emu([=] { gemm_mx({200, 33}, 1024, 256, L_EIO); }))});
   // the direct-weight configuration (variant dv): K-contiguous weights only; each scenario must run it
   auto dv = [](std::function<void()> f) {
     return [f] {

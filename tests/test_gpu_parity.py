@@ -472,6 +472,47 @@ def test_moe_forward_bf16_direct_matches_default(gpu):
     assert orc.rel_l2(out_dv, ref) < BF16_REL_L2
 
 
+_SPLIT_SKIP = _needs(256, "the split-role GEMM configurations")
+
+
+@_SPLIT_SKIP
+@pytest.mark.parametrize("variant", ["sp", "sp4"])
+@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2, [3, 40, 0, 513], [5, 0, 17, 1, 33]])
+def test_grouped_gemm_mxfp8_split_roles_match_default(gpu, counts, variant):
+    """Split copy roles change which wave copies what, not the MFMAs or their K order: the MXFP8 EIO
+    grouped GEMM is bit-identical to the default configuration."""
+    from hyper_multicore_amd import ops
+    g = _seed(sum(counts) + 13)
+    G, Kd, N = len(counts), 1024, 768
+    rows = sum(counts)
+    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
+    xq, xs = ops.mx_quantize_rows(x.to(gpu))
+    d, s = ops.mx_quantize_cols(w.to(gpu))
+    gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
+    out_def = ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), s, gl).cpu()
+    with _gemm_variant(variant):
+        out_sp = ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), s, gl).cpu()
+    assert torch.equal(out_sp, out_def)
+
+
+@_SPLIT_SKIP
+def test_moe_forward_mxfp8_split_roles_match_default(gpu):
+    from hyper_multicore_amd import ops
+    T, H, I, E, K = 700, 1024, 512, 16, 4
+    g = _seed(T + E + 7)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
+    d1, s1 = ops.mx_quantize_cols(w1.to(gpu))
+    d2, s2 = ops.mx_quantize_cols(w2.to(gpu))
+    args = dict(num_experts=E, intermediate_size=I, precision="mxfp8", w1_scale=s1, w2_scale=s2)
+    out_def = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8),
+                              **args).cpu()
+    with _gemm_variant("sp"):
+        out_sp = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8),
+                                 **args).cpu()
+    assert torch.equal(out_sp, out_def)
+
+
 _NUMERICS_SKIP = _needs(2, "the BF16 numerics options")
 
 
