@@ -98,6 +98,9 @@ int mi355_grouped_gemm_variant(const GGParams& p, bool mx, bool b_kn, int epi, h
 // The direct-weight configuration (gemm_direct.hip), variant "dv"; MI355MOE_EUNSUPPORTED outside its
 // domain (K-contiguous weights, K a multiple of 8 stages, bf16 store / SwiGLU epilogues).
 int mi355_grouped_gemm_direct(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
+// The split-role configurations (gemm_split.hip), variants sp / sp4; MI355MOE_EUNSUPPORTED outside
+// their domain (gg_split_applies).
+int mi355_grouped_gemm_split(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
 #include "features.h"
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {
   return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;

@@ -147,6 +147,49 @@ def run(asm_path: Path | None = None) -> list[str]:
     return findings
 
 
+SPLIT_KERNEL = re.compile(r"^(_Z\d+grouped_gemm_kernelI5GGCfgI\w*Lb1EE\w*):")  # GGCfg<..., SPLIT = true>
+
+
+def compile_asm_of(src: Path, out: Path) -> None:
+    hipcc = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "bin" / "hipcc"
+    cmd = [str(hipcc), "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{REPO / 'include'}", "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed:\n{r.stderr}")
+
+
+def run_split(asm_path: Path | None = None) -> list[str]:
+    """Findings for the split-role kernels of gemm_split.hip: their K loops must hold no spill traffic,
+    and their scalar-base copies must take the base from scalar registers."""
+    tmp = None
+    if asm_path is None:
+        tmp = tempfile.TemporaryDirectory()
+        asm_path = Path(tmp.name) / "gemm_split.s"
+        compile_asm_of(REPO / "hyper_multicore_amd" / "csrc" / "gemm_split.hip", asm_path)
+    asm = asm_path.read_text().split("\n")
+    findings, loops = [], 0
+    starts = [(i, m.group(1)) for i, l in enumerate(asm) if (m := SPLIT_KERNEL.match(l))]
+    for i, name in starts:
+        end = next(j for j in range(i, len(asm)) if "s_endpgm" in asm[j])
+        body = asm[i:end]
+        for t in _instructions(body):
+            if t.startswith("global_load_lds_dwordx4"):
+                parts = [p.strip() for p in t[len("global_load_lds_dwordx4"):].split(",")]
+                if len(parts) < 2 or not (parts[1] == "off" or parts[1].startswith("s[")):
+                    findings.append(f"{name}: copy without a scalar base: {t}")
+        for a, b in _k_loops(body):
+            loops += 1
+            spills = [t for t in _instructions(body[a:b]) if t.startswith("scratch_")]
+            if spills:
+                findings.append(f"{name}: {len(spills)} spill instructions in a K loop, e.g. {spills[0]}")
+    if loops == 0:
+        findings.append("no K loop found in the split-role kernels")
+    if tmp is not None:
+        tmp.cleanup()
+    return findings
+
+
 if __name__ == "__main__":
     found = run(Path(sys.argv[1]) if len(sys.argv) > 1 else None)
     for x in found[:40]:

@@ -1,4 +1,5 @@
-"""Compiled-code checks of the direct-weight grouped GEMM (CPU only; see tests/native/isa_check.py).
+"""Compiled-code checks of the direct-weight and split-role grouped GEMMs (CPU only; see
+tests/native/isa_check.py).
 
 The kernels load weight fragments into registers with inline assembly that the compiler does not
 track, so their correctness also depends on the compiler's register allocation; these tests read the
@@ -66,3 +67,13 @@ def test_direct_kernels_compiled_code(tmp_path):
     asm = Path(tmp_path) / "gemm_direct.s"
     isa_check.compile_asm(asm)
     assert isa_check.run(asm) == []
+
+
+@pytest.mark.skipif(not (isa_check.Path("/opt/rocm/bin/hipcc").exists() or shutil.which("hipcc")),
+                    reason="hipcc not available")
+def test_split_role_kernels_compiled_code(tmp_path):
+    """The split-role MXFP8 kernels (gemm_split.hip): no spill traffic in their K loops (the compiler's
+    waits for spill reloads would drain the copy ring) and scalar bases for the offset-form copies."""
+    asm = Path(tmp_path) / "gemm_split.s"
+    isa_check.compile_asm_of(isa_check.REPO / "hyper_multicore_amd" / "csrc" / "gemm_split.hip", asm)
+    assert isa_check.run_split(asm) == []
