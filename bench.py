@@ -161,7 +161,20 @@ def measure(layer: Layer, steps: int, warmup: int) -> dict:
     return dict(ms_per_step=total_ms / steps, wall_s=wall, stage_ms=avg)
 
 
-def roofline(c: dict, work: dict, gmm1_ms: float) -> dict:
+def measured_traffic(workload: str, variant: str, root: str = ROOT):
+    """HBM bytes per GMM1 launch from the committed rocprofv3 counter passes of the same workload and
+    GEMM variant (profiles/traffic_<workload>_<variant>.json: FETCH_SIZE and WRITE_SIZE in KiB per
+    dispatch, each scaled by the factor the same counter reads for a plain copy kernel of known size),
+    or None when no such record exists."""
+    path = os.path.join(root, "profiles", f"traffic_{workload}_{variant}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    return round((rec["fetch_kib"] * rec["fetch_factor"] + rec["write_kib"] * rec["write_factor"]) * 1024.0)
+
+
+def roofline(c: dict, work: dict, gmm1_ms: float, traffic=None) -> dict:
     mx = c["precision"] == "mxfp8"
     peak_flops = PEAK["mxfp8" if mx else "bf16"]
     t_mfma = work["g1_flops"] / peak_flops
@@ -170,11 +183,11 @@ def roofline(c: dict, work: dict, gmm1_ms: float) -> dict:
     if t_hbm > t_mfma:
         achieved = work["g1_bytes"] / sec / 1e9
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm"] / 1e9, "unit": "GB/s",
-                "frac": round(achieved / (PEAK["hbm"] / 1e9), 4), "traffic": None,
+                "frac": round(achieved / (PEAK["hbm"] / 1e9), 4), "traffic": traffic,
                 "kernel": "grouped_gemm GMM1+SwiGLU", "mfma_frac": round(work["g1_flops"] / sec / peak_flops, 4)}
     achieved = work["g1_flops"] / sec / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak_flops / 1e12, "unit": "TFLOP/s",
-            "frac": round(achieved / (peak_flops / 1e12), 4), "traffic": None, "kernel": "grouped_gemm GMM1+SwiGLU",
+            "frac": round(achieved / (peak_flops / 1e12), 4), "traffic": traffic, "kernel": "grouped_gemm GMM1+SwiGLU",
             "hbm_frac": round(work["g1_bytes"] / sec / PEAK["hbm"], 4)}
 
 
@@ -229,7 +242,7 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
                       f"torch CPU {torch.__version__}, os.cpu_count()={os.cpu_count()}, cpu={platform.processor() or platform.machine()}"}
 
 
-def run_config(name: str, device, steps: int, warmup: int) -> dict:
+def run_config(name: str, device, steps: int, warmup: int, variant: str = "default") -> dict:
     layer = Layer(name, device)
     counts = layer.counts()
     work = gmm_work(layer.c, counts)
@@ -245,7 +258,7 @@ def run_config(name: str, device, steps: int, warmup: int) -> dict:
         "active_experts": work["active"],
         "weight_layout": layer.layout,
         "stage_ms": {k: round(v, 4) for k, v in m["stage_ms"].items()},
-        "roofline": roofline(c, work, m["stage_ms"]["gmm1"]),
+        "roofline": roofline(c, work, m["stage_ms"]["gmm1"], measured_traffic(name, variant)),
     }
     return res, layer
 
@@ -335,7 +348,7 @@ def main() -> int:
     gemm_variant = ops.set_gemm_variant("default")
     ops.set_gemm_variant(gemm_variant)
     log(f"[bench] workload {args.config}: steps={args.steps} warmup={args.warmup}")
-    res, layer = run_config(args.config, device, args.steps, args.warmup)
+    res, layer = run_config(args.config, device, args.steps, args.warmup, gemm_variant)
     c = layer.c
     cpu = None if args.no_cpu else cpu_baseline(args.config, layer)
     del layer
@@ -346,7 +359,7 @@ def main() -> int:
         if name == args.config:
             continue
         log(f"[bench] extra {name}")
-        r, lyr = run_config(name, device, max(5, args.steps // 2), max(2, args.warmup // 2))
+        r, lyr = run_config(name, device, max(5, args.steps // 2), max(2, args.warmup // 2), gemm_variant)
         extra[name] = r
         del lyr
         torch.cuda.empty_cache()

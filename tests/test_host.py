@@ -97,3 +97,19 @@ def test_ops_reject_cpu_tensors():
         ops.dispatch(torch.zeros(4, 2, dtype=torch.int64), 8)
     with pytest.raises(TypeError):
         ops.mx_quantize_rows(torch.zeros(4, 32, dtype=torch.bfloat16))
+
+
+def test_bench_traffic_record(tmp_path):
+    """roofline.traffic comes from a committed counter record of the same workload and GEMM variant:
+    FETCH_SIZE / WRITE_SIZE KiB per dispatch, each times its copy-kernel calibration factor."""
+    import json
+    import bench
+    (tmp_path / "profiles").mkdir()
+    rec = {"fetch_kib": 1000.0, "fetch_factor": 0.5, "write_kib": 10.0, "write_factor": 2.0}
+    (tmp_path / "profiles" / "traffic_dsv3_bf16_dv.json").write_text(json.dumps(rec))
+    assert bench.measured_traffic("dsv3_bf16", "dv", root=str(tmp_path)) == (500 + 20) * 1024
+    assert bench.measured_traffic("dsv3_bf16", "default", root=str(tmp_path)) is None
+    c = bench.CONFIGS["dsv3_bf16"]
+    work = {"g1_flops": 1e12, "g1_bytes": 1e10}
+    r = bench.roofline(c, work, 2.0, traffic=123)
+    assert r["traffic"] == 123 and r["bound"] == "hbm" and r["unit"] == "GB/s"
