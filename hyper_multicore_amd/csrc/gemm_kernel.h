@@ -48,8 +48,10 @@ struct DevDma {
   template <int SZ>
   MI355_DEV static void copy_so(const uint8_t* base, uint32_t off, uint32_t lds_off_uniform, uint8_t* smem, int enable) {
     static_assert(SZ == 16, "scalar-base copies are 16 bytes");
+    // LDS address as the LDS base of the shared array plus the offset (32-bit arithmetic; casting the
+    // generic pointer smem + offset instead costs a null check and a 64-bit value per distinct offset)
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(smem + lds_off_uniform));
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem + lds_off_uniform);
     const int en = __builtin_amdgcn_readfirstlane(enable);
     asm volatile("s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
                  "global_load_lds_dwordx4 %0, %1\n1:" ::"v"(off), "s"(base), "s"(m0), "s"(en) : "memory", "scc");
