@@ -2006,6 +2006,16 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"dv_gemm_bf16_decode_big", big(dv([=] { gemm_bf16(decode_counts(64, 5), 1024, 768, L_EOI); }))});
   s.push_back({"dv_moe_bf16_eoi", dv([=] { moe_forward(640, 2, 4, 512, 512, BF, L_EOI, 0.0); })});
   s.push_back({"dv_moe_mx_eoi", dv([=] { moe_forward(640, 2, 4, 512, 512, MX, L_EOI, 0.0); })});
+  auto many = [] {
+    std::vector<int> c(1100, 0);
+    for (size_t i = 0; i < c.size(); i += 3) c[i] = 1 + (int)(i % 7);
+    return c;
+  };
+  s.push_back({"dv_gemm_bf16_many_groups", big(dv([=] { gemm_bf16(many(), 256, 256, L_EOI); }))});
+  s.push_back({"dv_gemm_bf16_narrow", dv([=] { gemm_bf16({3, 40, 0, 513, 1}, 256, 200, L_EOI); })});
+  s.push_back({"sp_gemm_mx_many_groups", big(sp(SP, [=] { gemm_mx(many(), 512, 256, L_EIO); }))});
+  s.push_back({"sp_gemm_mx_narrow", sp(SP, [=] { gemm_mx({3, 40, 0, 513, 1}, 512, 272, L_EIO); })});
+  s.push_back({"emu_dv_bf16_narrow", dv(emu([=] { gemm_bf16({3, 40, 0, 300, 1}, 256, 200, L_EOI); }))});
   s.push_back({"emu_dv_bf16", dv(emu([=] { gemm_bf16({70, 0, 129, 5}, 512, 512, L_EOI); }))});
   s.push_back({"emu_dv_bf16_one_turn", dv(emu([=] { gemm_bf16({70, 0, 129, 5, 40}, 256, 256, L_EOI); }))});
   s.push_back({"emu_dv_mx", dv(emu([=] { gemm_mx({70, 0, 129, 5}, 1024, 256, L_EOI); }))});
