@@ -228,7 +228,12 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
                                         topk_groups=c["topk_groups"])
         return orc.torch_experts_reference(x, ids, w, gate_w, up_w, w2)
 
-    run()  # warm-up
+    ref = run()  # warm-up
+    agree = None
+    try:  # the GPU output of the same tokens (the last timed step) against the CPU path's output
+        agree = round(orc.rel_l2(layer.out[:sample].float().cpu(), ref.float()), 6)
+    except Exception as e:  # a reported figure, never a reason to lose the bench line
+        log(f"[bench] sample agreement not computed: {e}")
     times = []
     t_end = time.perf_counter() + budget_s
     while len(times) < 3 and (not times or time.perf_counter() < t_end):
@@ -238,6 +243,7 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
     times.sort()
     med = times[len(times) // 2]
     return {"value": round(sample / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "gpu_rel_l2": agree,
             "sample": f"first {sample} of {T} tokens of the {name} batch, median of {len(times)} after 1 warm-up; "
                       f"torch CPU {torch.__version__}, os.cpu_count()={os.cpu_count()}, cpu={platform.processor() or platform.machine()}"}
 
