@@ -251,6 +251,7 @@ int mx_backward(const MI355MoeBackwardArgs& a, char* ws, const MxBwdLayout& L, h
     GGParams p = {};
     p.A = A;
     p.lda_bytes = Kd;
+    p.a_bytes = (a_index != nullptr ? T : R) * Kd;  // A holds the tokens when gathered, else the routed rows
     p.a_row_index = a_index;
     p.a_row_div = a_div;
     p.a_scale = As;
@@ -413,6 +414,7 @@ extern "C" int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* wor
     GGParams p = {};
     p.A = (const uint8_t*)A;
     p.lda_bytes = (int64_t)Kd * 2;
+    p.a_bytes = R * Kd * 2;
     p.a_row_div = 1;
     p.B = (const uint8_t*)W;
     p.b_group_stride = w_group * 2;
