@@ -1,0 +1,147 @@
+"""The torch operator layer (torch.ops.hyper_multicore_mi355): registration, schemas, fake (Meta)
+shape inference and host validation on the CPU; on the GPU every operator equals the functional
+operator it wraps bit for bit (same kernels, same inputs)."""
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+import hyper_multicore_amd  # noqa: F401  (registers the operators)
+from hyper_multicore_amd import torch_ops
+
+ns = torch.ops.hyper_multicore_mi355
+BF = torch.bfloat16
+
+
+def test_every_operator_is_registered_with_a_fake_kernel():
+    for name in torch_ops.OPERATORS:
+        op = getattr(ns, name).default
+        assert op._schema.name == f"hyper_multicore_mi355::{name}"
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "Meta"), name
+
+
+def test_out_variants_declare_their_mutations():
+    s = ns.moe_token_permute_out.default._schema
+    assert [a.name for a in s.arguments if a.alias_info is not None and a.alias_info.is_write] == ["output", "mapping"]
+    s = ns.moe_forward_out.default._schema
+    assert [a.name for a in s.arguments if a.alias_info is not None and a.alias_info.is_write] == ["out"]
+
+
+def test_fake_shapes_of_the_forward_path():
+    T, H, E, K, I = 37, 128, 16, 4, 64
+    with FakeTensorMode():
+        x = torch.empty(T, H, dtype=BF)
+        logits = ns.gate_logits(x, torch.empty(E, H, dtype=BF))
+        assert logits.shape == (T, E) and logits.dtype == torch.float32
+        w, ids, scores = ns.mega_gate_route(logits, torch.empty(E), None, None, K, 2.5, False, "sigmoid", 4, 2)
+        assert (w.shape, w.dtype, ids.shape, ids.dtype, scores.shape) == ((T, K), torch.float32, (T, K), torch.int64,
+                                                                          (T, E))
+        counts, offs, gl, mapping, gather, err = ns.dispatch(ids, E)
+        assert (counts.dtype, gl.dtype, mapping.shape, gather.shape, err.shape) == (torch.int32, torch.int64, (T * K,),
+                                                                                    (T * K,), (1,))
+        routed, m = ns.token_permute(x, ids, E)
+        assert routed.shape == (T * K, H) and m.dtype == torch.int32
+        ns.moe_token_permute_out(x, ids, torch.empty(T * K, H, dtype=BF), torch.empty(T * K, dtype=torch.int32))
+        u = ns.grouped_gemm_bf16(routed, torch.empty(E, 2 * I, H, dtype=BF), gl, "EOI")
+        assert u.shape == (T * K, 2 * I) and u.dtype == BF
+        q, s = ns.mx_quantize_rows(routed)
+        assert q.shape == (T * K, H) and s.shape == (T * K, H // 32) and q.dtype == torch.uint8
+        y = ns.grouped_gemm_mxfp8(q, s, torch.empty(E, H, 2 * I, dtype=torch.uint8),
+                                  torch.empty(E, H // 64, 2 * I, 2, dtype=torch.uint8), gl)
+        assert y.shape == (T * K, 2 * I)
+        out = ns.combine(routed, mapping, w, K)
+        assert out.shape == (T, H) and out.dtype == BF
+        f = ns.moe_forward(x, ids, w, torch.empty(E, H, 2 * I, dtype=BF), torch.empty(E, I, H, dtype=BF), None, None,
+                           E, I)
+        assert f.shape == (T, H) and f.dtype == BF
+        g = ns.mega_gate_route_grad(logits, scores, ids, w, K, 2.5, "sigmoid")
+        assert g.shape == (T, E)
+
+
+def test_fake_kernels_validate_like_the_real_ones():
+    with FakeTensorMode():
+        x = torch.empty(8, 64, dtype=BF)
+        ids = torch.empty(8, 2, dtype=torch.int64)
+        with pytest.raises(ValueError):
+            ns.gate_logits(x, torch.empty(4, 32, dtype=BF))
+        with pytest.raises(ValueError):  # output of the wrong shape
+            ns.moe_token_permute_out(x, ids, torch.empty(8, 64, dtype=BF), torch.empty(16, dtype=torch.int32))
+        with pytest.raises(ValueError):  # int64 mapping
+            ns.moe_token_permute_out(x, ids, torch.empty(16, 64, dtype=BF), torch.empty(16, dtype=torch.int64))
+        with pytest.raises(ValueError):
+            ns.moe_forward(x, ids, torch.empty(8, 3), x, x, None, None, 4, 32)
+        with pytest.raises(ValueError):
+            ns.moe_forward(x, ids, torch.empty(8, 2), x, x, None, None, 4, 32, "fp16")
+        with pytest.raises(ValueError):
+            ns.grouped_gemm_bf16(x, torch.empty(2, 64, 64, dtype=BF), torch.empty(2, dtype=torch.int64), "KN")
+
+
+def test_cpu_tensors_fail_loudly():
+    x = torch.zeros(8, 64, dtype=BF)
+    with pytest.raises(TypeError, match="GPU"):
+        ns.gate_logits(x, torch.zeros(4, 64, dtype=BF))
+    ids = torch.zeros(8, 2, dtype=torch.int64)
+    with pytest.raises(TypeError, match="GPU"):
+        ns.moe_token_permute_out(x, ids, torch.empty(16, 64, dtype=BF), torch.empty(16, dtype=torch.int32))
+    with pytest.raises(TypeError, match="GPU"):
+        ns.dispatch(ids, 4)
+
+
+# ------------------------------------------------------------------------------------------------
+# GPU: the operators equal the functional operators
+# ------------------------------------------------------------------------------------------------
+def _routed_inputs(device, T=300, H=256, E=16, K=4, I=128, seed=11):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn(T, H, generator=g).to(BF).to(device)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(BF).to(device)
+    bias = (torch.randn(E, generator=g) * 0.01).to(device)
+    w1 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(BF).to(device)  # EOI
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(BF).to(device)
+    return x, wr, bias, w1, w2, E, K, I
+
+
+@pytest.mark.gpu
+def test_gpu_router_and_dispatch_ops_equal_functional(gpu):
+    from hyper_multicore_amd import ops
+    x, wr, bias, _, _, E, K, _ = _routed_inputs(gpu)
+    logits = ns.gate_logits(x, wr)
+    assert torch.equal(logits, ops.gate_logits(x, wr))
+    w, ids, scores = ns.mega_gate_route(logits, bias, None, None, K, 2.5, False, "sigmoid", 4, 2)
+    w2_, ids2, sc2 = ops.gate_route(logits, bias, top_k=K, scoring_func="sigmoid", routed_scaling_factor=2.5,
+                                    num_groups=4, topk_groups=2, return_scores=True)
+    assert torch.equal(w, w2_) and torch.equal(ids, ids2) and torch.equal(scores, sc2)
+    d = ops.dispatch(ids, E)
+    got = ns.dispatch(ids, E)
+    for a, b in zip(got, (d.counts, d.expert_offsets, d.group_list, d.mapping, d.gather_index, d.error_flag)):
+        assert torch.equal(a, b)
+    routed, mapping = ops.token_permute(x, ids, E)
+    r2, m2 = ns.token_permute(x, ids, E)
+    assert torch.equal(r2, routed) and torch.equal(m2, mapping)
+    for n_exp in (E, -1):  # explicit and derived expert count
+        out = torch.full_like(routed, float("nan"))
+        m = torch.full_like(mapping, -1)
+        ns.moe_token_permute_out(x, ids, out, m, n_exp)
+        assert torch.equal(out, routed) and torch.equal(m, mapping)
+    assert torch.equal(ns.combine(routed, mapping, w, K), ops.token_unpermute(routed, mapping, w, K))
+    assert torch.equal(ns.combine(routed, mapping, None, K), ops.token_unpermute(routed, mapping, None, K))
+
+
+@pytest.mark.gpu
+def test_gpu_gemm_and_forward_ops_equal_functional(gpu):
+    from hyper_multicore_amd import ops
+    x, wr, bias, w1, w2, E, K, I = _routed_inputs(gpu)
+    w, ids = ops.gate_route(ops.gate_logits(x, wr), bias, top_k=K, scoring_func="softmax", routed_scaling_factor=1.0)
+    d = ops.dispatch(ids, E)
+    routed, _ = ops.token_permute(x, ids, E)
+    assert torch.equal(ns.grouped_gemm_bf16(routed, w1, d.group_list, "EOI"),
+                       ops.grouped_gemm_bf16(routed, w1, d.group_list, "EOI"))
+    q, s = ns.mx_quantize_rows(routed)
+    q2, s2 = ops.mx_quantize_rows(routed)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+    cd, cs = ops.mx_quantize_cols(w1.transpose(1, 2).contiguous())
+    assert torch.equal(ns.grouped_gemm_mxfp8(q, s, cd.view(torch.uint8), cs, d.group_list),
+                       ops.grouped_gemm_mxfp8(q, s, cd.view(torch.uint8), cs, d.group_list))
+    ref = ops.moe_forward(x, ids, w, w1, w2, num_experts=E, intermediate_size=I, layout="EOI")
+    assert torch.equal(ns.moe_forward(x, ids, w, w1, w2, None, None, E, I, "bf16", "EOI"), ref)
+    out = torch.full_like(x, float("nan"))
+    ns.moe_forward_out(x, ids, w, w1, w2, None, None, E, I, out, "bf16", "EOI")
+    assert torch.equal(out, ref)
