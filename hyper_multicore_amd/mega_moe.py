@@ -115,14 +115,21 @@ class _MoeFunction(torch.autograd.Function):
 
 class _MxMoeFunction(torch.autograd.Function):
     """MXFP8 expert forward with the library's MX backward (mxfp8/autograd.py:35-86 role): the forward
-    reads the roots' column axis, the backward resolves the roots again and reads both axes (the
-    reference re-resolves after its parameter hooks); forward intermediates are recomputed."""
+    reads the roots' column axis; the backward resolves the roots again for their row axis (the
+    reference re-resolves after its parameter hooks, so a root whose owner has replaced the row fields
+    or released the column fields since the forward works, test_mxfp8_root_lifecycle.py:31-73). The
+    forward intermediates are recomputed from the column axis the forward read, which the context
+    keeps."""
 
     @staticmethod
     def forward(ctx, hidden, topk_weights, root1, root2, topk_ids, executor, weight_grad_dtype):
+        from .mxfp8 import resolve_forward_weight
         layout, d1, s1, d2, s2 = executor._mx_weights(hidden, (root1, root2))
         ctx.save_for_backward(hidden, topk_weights, topk_ids)
         ctx.roots = (root1, root2)
+        E, H, I = executor.num_experts, executor.hidden_size, executor.intermediate_size
+        ctx.cols = (resolve_forward_weight(root1, (E, H, 2 * I), hidden.device),
+                    resolve_forward_weight(root2, (E, I, H), hidden.device))
         ctx.meta = (executor.num_experts, executor.hidden_size, executor.intermediate_size, weight_grad_dtype)
         return ops.moe_forward(hidden, topk_ids, topk_weights, d1, d2, num_experts=executor.num_experts,
                                intermediate_size=executor.intermediate_size, precision="mxfp8", layout=layout,
@@ -130,15 +137,15 @@ class _MxMoeFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        from .mxfp8 import resolve_backward_weight, resolve_forward_weight
+        from .mxfp8 import resolve_backward_weight
         hidden, topk_weights, topk_ids = ctx.saved_tensors
         E, H, I, grad_dtype = ctx.meta
         r1, r2 = ctx.roots
         fields = []
-        for root, shape in ((r1, (E, H, 2 * I)), (r2, (E, I, H))):
-            col = resolve_forward_weight(root, shape, hidden.device)
+        for root, shape, col in ((r1, (E, H, 2 * I), ctx.cols[0]), (r2, (E, I, H), ctx.cols[1])):
             row = resolve_backward_weight(root, shape, hidden.device)
             fields.append((*col, *row))
+        ctx.cols = None
         gx, g1, g2, gp = ops.moe_backward_mxfp8(hidden, topk_ids, topk_weights, fields[0], fields[1], grad_out,
                                                 num_experts=E, intermediate_size=I, weight_grad_dtype=grad_dtype,
                                                 need_topk_grad=ctx.needs_input_grad[1])

@@ -113,3 +113,59 @@ def test_bench_traffic_record(tmp_path):
     work = {"g1_flops": 1e12, "g1_bytes": 1e10}
     r = bench.roofline(c, work, 2.0, traffic=123)
     assert r["traffic"] == 123 and r["bound"] == "hbm" and r["unit"] == "GB/s"
+
+
+def _physical(root, shape):
+    """Attach packed column and row axes to an MX root (the reference's FSDP root fields)."""
+    e, m, n = shape
+    root.col_data = torch.empty(shape, dtype=torch.float8_e4m3fn)
+    root.col_scale = torch.empty((e, m // 64, n, 2), dtype=torch.uint8)
+    root.row_data = torch.empty(shape, dtype=torch.float8_e4m3fn)
+    root.row_scale = torch.empty((e, m, n // 64, 2), dtype=torch.uint8)
+
+
+def test_mx_backward_resolves_fresh_row_axis_and_keeps_forward_columns(monkeypatch):
+    """The MX autograd function reads the row axis the owner materialised after the forward (fields
+    replaced, column axis released), as test_mxfp8_root_lifecycle.py:31-73 requires of the reference;
+    the recompute uses the column axis the forward read. The GPU calls are replaced by recorders."""
+    from hyper_multicore_amd import mega_moe
+    E, H, I, T, K = 2, 64, 64, 4, 1
+    shapes = ((E, H, 2 * I), (E, I, H))
+    roots = [torch.nn.Parameter(torch.empty(s, dtype=torch.bfloat16)) for s in shapes]
+    for r, s in zip(roots, shapes):
+        _physical(r, s)
+    fwd_cols = [(r.col_data.data_ptr(), r.col_scale.data_ptr()) for r in roots]
+    seen = {}
+
+    def fake_forward(hidden, ids, probs, d1, d2, **kw):
+        seen["forward"] = (d1.data_ptr(), kw["w1_scale"].data_ptr(), d2.data_ptr(), kw["w2_scale"].data_ptr())
+        return hidden.clone()
+
+    def fake_backward(hidden, ids, probs, w1, w2, grad_out, **kw):
+        seen["backward"] = [tuple(t.data_ptr() for t in w) for w in (w1, w2)]
+        return (grad_out.clone(), torch.zeros(E, H, 2 * I), torch.zeros(E, I, H),
+                torch.zeros(T, K) if kw["need_topk_grad"] else None)
+
+    monkeypatch.setattr(ops, "features", lambda: 0)
+    monkeypatch.setattr(ops, "moe_forward", fake_forward)
+    monkeypatch.setattr(ops, "moe_backward_mxfp8", fake_backward)
+    ex = hm.MegaMoeExperts(hidden_size=H, intermediate_size=I, num_experts=E, top_k=K, precision="mxfp8")
+    x = torch.ones((T, H), dtype=torch.bfloat16, requires_grad=True)
+    probs = torch.ones((T, K), requires_grad=True)
+    ids = torch.zeros((T, K), dtype=torch.int64)
+    y = mega_moe._MxMoeFunction.apply(x, probs, roots[0], roots[1], ids, ex, torch.float32)
+    assert seen["forward"] == (*fwd_cols[0], *fwd_cols[1])
+    for r, s in zip(roots, shapes):  # the owner gathers a fresh row axis and releases the column axis
+        _physical(r, s)
+        r.col_data = r.col_scale = None
+    y.sum().backward()
+    for got, r, cols in zip(seen["backward"], roots, fwd_cols):
+        assert got == (*cols, r.row_data.data_ptr(), r.row_scale.data_ptr())
+    assert torch.equal(x.grad, torch.ones_like(x))
+    assert all(torch.equal(r.grad, torch.zeros_like(r)) for r in roots)
+    for r, s in zip(roots, shapes):  # a root without its row axis is reported by name
+        _physical(r, s)
+        del r.row_data
+    y = mega_moe._MxMoeFunction.apply(x, probs, roots[0], roots[1], ids, ex, torch.float32)
+    with pytest.raises(ValueError, match="missing required row data/scale"):
+        y.sum().backward()
