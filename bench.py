@@ -284,9 +284,11 @@ def gemm_shapes(device, reps: int) -> dict:
     for name, N, K in (("gmm1_shape", 4096, 7168), ("gmm2_shape", 7168, 2048)):
         x = torch.randn(G * rows, K, device=device, generator=g).to(torch.bfloat16)
         w = (torch.randn(G, N, K, device=device, generator=g) * 0.006).to(torch.bfloat16)  # EOI
-        runs = {"bf16_EOI": lambda: ops.grouped_gemm_bf16(x, w, gl, "EOI")}
+        w_eio = w.transpose(1, 2).contiguous()  # [G, K, N]
+        runs = {"bf16_EOI": lambda: ops.grouped_gemm_bf16(x, w, gl, "EOI"),
+                "bf16_EIO": lambda: ops.grouped_gemm_bf16(x, w_eio, gl, "EIO")}
         xq, xs = ops.mx_quantize_rows(x)
-        d, sc = ops.mx_quantize_cols(w.transpose(1, 2).contiguous())  # EIO col_data
+        d, sc = ops.mx_quantize_cols(w_eio)  # EIO col_data
         runs["mxfp8_EIO"] = lambda: ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), sc, gl)
         if feats & _lib.FEATURE_MX_EOI:
             de, se = ops.mx_weight_to_eoi(d, sc)
@@ -315,7 +317,7 @@ def gemm_shapes(device, reps: int) -> dict:
                                            "mfma_frac": round(flops / (ms * 1e-3) / peak, 4),
                                            "weight_tb_s": round(wbytes / (ms * 1e-3) / 1e12, 3)}
                 log(f"[bench] {name}/{key}/{v}: {out[f'{name}/{key}/{v}']}")
-        del x, w, xq, xs, d, sc
+        del x, w, w_eio, xq, xs, d, sc
         torch.cuda.empty_cache()
     return out
 

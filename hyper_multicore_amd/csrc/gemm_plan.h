@@ -95,10 +95,12 @@ MI355_HD bool gg_offsets_fit(const GGParams& p) {
   return p.a_bytes > 0 && p.a_bytes < lim && p.b_group_stride > 0 && p.b_group_stride < lim;
 }
 
-// The GEMMs the split-role configurations run: MXFP8 on EIO weight roots (col_data / col_scale), the
-// bf16 store and MX SwiGLU epilogues, 32-bit offsets within reach.
+// The GEMMs the split-role configurations run: EIO weights (N contiguous; MXFP8 roots' col_data /
+// col_scale or bf16 [E, K, N]), the bf16 store and the SwiGLU epilogue of the precision (MX requant /
+// bf16 without the numerics options), 32-bit offsets within reach.
 MI355_HD bool gg_split_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
-  return mx && b_kn && (epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_MX) && gg_offsets_fit(p);
+  const bool epi_ok = epi == EPI_STORE_BF16 || epi == (mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16);
+  return b_kn && epi_ok && gg_offsets_fit(p);
 }
 
 // Tile column j (0..BN-1) -> weight column. SwiGLU: the columns of each wave tile (WN wide) are

@@ -4,7 +4,7 @@
 //   b6 - GGBig's 256 x 256 tiles with a sixth weight slot in the LDS of the MX weight row-scale ring
 //        (bf16 and MX with EIO weights; MX with K-contiguous weights keeps the default).
 //   dv - the direct-weight configuration of gemm_direct.hip (K-contiguous weights: bf16 EOI, MX EOI).
-//   sp, sp4 - the split copy roles of gemm_split.hip (MXFP8 GEMMs on EIO weight roots).
+//   sp, sp4 - the split copy roles of gemm_split.hip (GEMMs on EIO weights, bf16 and MXFP8).
 #include "gemm_kernel.h"
 
 using GGB6 = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0>;

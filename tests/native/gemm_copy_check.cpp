@@ -1600,11 +1600,14 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   }
   if ((g_variant == MI355_GG_VARIANT_SP || g_variant == MI355_GG_VARIANT_SP4) && gg_split_applies(p, mx, b_kn, epi)) {
     ++g_split_gemms;
-    if (epi == EPI_SWIGLU_MX)
-      return g_variant == MI355_GG_VARIANT_SP ? sim_forward<GGSplit, true, true, EPI_SWIGLU_MX>(p)
-                                              : sim_forward<GGSplitA4, true, true, EPI_SWIGLU_MX>(p);
-    return g_variant == MI355_GG_VARIANT_SP ? sim_forward<GGSplit, true, true, EPI_STORE_BF16>(p)
-                                            : sim_forward<GGSplitA4, true, true, EPI_STORE_BF16>(p);
+    const bool sp = g_variant == MI355_GG_VARIANT_SP;
+    if (mx && epi == EPI_SWIGLU_MX)
+      return sp ? sim_forward<GGSplit, true, true, EPI_SWIGLU_MX>(p) : sim_forward<GGSplitA4, true, true, EPI_SWIGLU_MX>(p);
+    if (mx) return sp ? sim_forward<GGSplit, true, true, EPI_STORE_BF16>(p) : sim_forward<GGSplitA4, true, true, EPI_STORE_BF16>(p);
+    if (epi == EPI_SWIGLU_BF16)
+      return sp ? sim_forward<GGSplit, false, true, EPI_SWIGLU_BF16>(p)
+                : sim_forward<GGSplitA4, false, true, EPI_SWIGLU_BF16>(p);
+    return sp ? sim_forward<GGSplit, false, true, EPI_STORE_BF16>(p) : sim_forward<GGSplitA4, false, true, EPI_STORE_BF16>(p);
   }
   if (g_variant == MI355_GG_VARIANT_DV) {
     const int rc = sim_direct_dispatch(p, mx, b_kn, epi);
@@ -1989,6 +1992,13 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_sp_mx_eio", sp(SP, emu([=] { gemm_mx({70, 0, 129, 300}, 1024, 256, L_EIO); }))});
   s.push_back({"emu_sp_mx_eio_decode", big(sp(SP, emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })))});
   s.push_back({"emu_sp4_mx_eio", sp(SP4, emu([=] { gemm_mx({200, 33}, 1024, 256, L_EIO); }))});
+  s.push_back({"sp_gemm_bf16_eio", sp(SP, [=] { gemm_bf16({100, 0, 300, 1, 129}, 512, 768, L_EIO); })});
+  s.push_back({"sp_gemm_bf16_eio_decode_big", big(sp(SP, [=] { gemm_bf16(decode_counts(48, 6), 512, 512, L_EIO); }))});
+  s.push_back({"sp_moe_bf16_eio", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
+  s.push_back({"sp4_moe_bf16_eio", sp(SP4, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
+  s.push_back({"emu_sp_bf16_eio", sp(SP, emu([=] { gemm_bf16({70, 0, 129, 300}, 512, 512, L_EIO); }))});
+  s.push_back({"emu_sp_bf16_eio_decode", big(sp(SP, emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EIO); })))});
+  s.push_back({"emu_sp4_bf16_eio", sp(SP4, emu([=] { gemm_bf16({200, 33}, 512, 256, L_EIO); }))});
   // the direct-weight configuration (variant dv): K-contiguous weights only; each scenario must run it
   auto dv = [](std::function<void()> f) {
     return [f] {

@@ -513,6 +513,38 @@ def test_moe_forward_mxfp8_split_roles_match_default(gpu):
     assert torch.equal(out_sp, out_def)
 
 
+@_SPLIT_SKIP
+@pytest.mark.parametrize("variant", ["sp", "sp4"])
+@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2, [3, 40, 0, 513], [5, 0, 17, 1, 33]])
+def test_grouped_gemm_bf16_eio_split_roles_match_default(gpu, counts, variant):
+    """The bf16 grouped GEMM on EIO weights [G, K, N] with split copy roles is bit-identical to the
+    default configuration (same MFMAs in the same K order)."""
+    from hyper_multicore_amd import ops
+    g = _seed(sum(counts) + 17)
+    G, Kd, N = len(counts), 1024, 768
+    x = torch.randn(sum(counts), Kd, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16).to(gpu)
+    gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
+    out_def = ops.grouped_gemm_bf16(x, w, gl, "EIO").cpu()
+    with _gemm_variant(variant):
+        out_sp = ops.grouped_gemm_bf16(x, w, gl, "EIO").cpu()
+    assert torch.equal(out_sp, out_def)
+
+
+@_SPLIT_SKIP
+def test_moe_forward_bf16_eio_split_roles_match_default(gpu):
+    from hyper_multicore_amd import ops
+    T, H, I, E, K = 700, 1024, 512, 16, 4
+    g = _seed(T + E + 11)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
+    args = dict(num_experts=E, intermediate_size=I, precision="bf16", layout="EIO")
+    ins = [t.to(gpu) for t in (x, ids, probs, w1, w2)]
+    out_def = ops.moe_forward(*ins, **args).cpu()
+    with _gemm_variant("sp"):
+        out_sp = ops.moe_forward(*ins, **args).cpu()
+    assert torch.equal(out_sp, out_def)
+
+
 _NUMERICS_SKIP = _needs(2, "the BF16 numerics options")
 
 

@@ -61,6 +61,34 @@ def test_checker_flags_a_vector_base(tmp_path):
     assert any("scalar base" in f for f in _findings(text, tmp_path))
 
 
+SPLIT_SYNTH = """
+_Z19grouped_gemm_kernelI5GGCfgILi256ELb1EEv8GGParams:
+  s_waitcnt vmcnt(0)
+.LBB0_1:
+{first}
+  s_barrier
+""" + "  v_mfma_f32_32x32x16_bf16 a[0:15], v[20:23], v[24:27], a[0:15]\n" * 16 + """
+  global_load_lds_dwordx4 v11, s[4:5]
+  s_barrier
+{second}
+  s_cbranch_scc1 .LBB0_1
+  s_endpgm
+"""
+
+
+def test_split_checker_flags_spills_only_in_steady_loops(tmp_path):
+    p = Path(tmp_path) / "s.s"
+    mfmas = "  v_mfma_f32_32x32x16_bf16 a[0:15], v[20:23], v[24:27], a[0:15]\n" * 16
+    spill = "  scratch_load_dword v40, off, off offset:8"
+    p.write_text(SPLIT_SYNTH.format(first=spill, second=mfmas))  # both barrier intervals compute
+    assert any("spill" in f for f in isa_check.run_split(p))
+    p.write_text(SPLIT_SYNTH.format(first="", second=mfmas))
+    assert isa_check.run_split(p) == []
+    # a per-item path: one barrier interval is the prologue's wait only, so the loop is not a steady K loop
+    p.write_text(SPLIT_SYNTH.format(first=spill, second=""))
+    assert isa_check.run_split(p) == ["no K loop found in the split-role kernels"]
+
+
 @pytest.mark.skipif(not (isa_check.Path("/opt/rocm/bin/hipcc").exists() or shutil.which("hipcc")),
                     reason="hipcc not available")
 def test_direct_kernels_compiled_code(tmp_path):
@@ -72,8 +100,9 @@ def test_direct_kernels_compiled_code(tmp_path):
 @pytest.mark.skipif(not (isa_check.Path("/opt/rocm/bin/hipcc").exists() or shutil.which("hipcc")),
                     reason="hipcc not available")
 def test_split_role_kernels_compiled_code(tmp_path):
-    """The split-role MXFP8 kernels (gemm_split.hip): no spill traffic in their K loops (the compiler's
-    waits for spill reloads would drain the copy ring) and scalar bases for the offset-form copies."""
+    """The split-role kernels (gemm_split.hip, MXFP8 and bf16 on EIO weights): no spill traffic in their
+    steady K loops (the compiler's waits for spill reloads would drain the copy ring) and scalar bases
+    for the offset-form copies."""
     asm = Path(tmp_path) / "gemm_split.s"
     isa_check.compile_asm_of(isa_check.REPO / "hyper_multicore_amd" / "csrc" / "gemm_split.hip", asm)
     assert isa_check.run_split(asm) == []
