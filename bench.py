@@ -52,7 +52,7 @@ def log(msg: str) -> None:
 class Layer:
     """Synthetic inputs + weights of one config, resident on the GPU."""
 
-    def __init__(self, name: str, device: torch.device):
+    def __init__(self, name: str, device: torch.device, bf16_layout: str = "EOI"):
         from hyper_multicore_amd import _lib, ops
         self.ops = ops
         self._lib = _lib
@@ -82,7 +82,11 @@ class Layer:
             self.skew = 8.0 * (logp - torch.log(-torch.log(u)))
         w1 = torch.randn(E, 2 * I, H, device=device, generator=g).mul_(c["wstd"]).to(torch.bfloat16)  # EOI
         w2 = torch.randn(E, H, I, device=device, generator=g).mul_(c["wstd"]).to(torch.bfloat16)      # EOI
-        if c["precision"] == "bf16":
+        if c["precision"] == "bf16" and bf16_layout == "EIO":  # the reference module's default layout
+            w1e, w2e = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
+            del w1, w2
+            self.w1, self.w2, self.s1, self.s2, self.layout = w1e, w2e, None, None, "EIO"
+        elif c["precision"] == "bf16":
             self.w1, self.w2, self.s1, self.s2, self.layout = w1, w2, None, None, "EOI"
         else:
             d1, s1 = ops.mx_quantize_cols(w1.transpose(1, 2).contiguous())  # EIO [E, H, 2I]
@@ -208,8 +212,10 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
     wr = layer.wr.cpu()
     bias = layer.bias.cpu()
     if c["precision"] == "bf16":
-        w1 = layer.w1.cpu()   # EOI [E, 2I, H]
+        w1 = layer.w1.cpu()   # EOI [E, 2I, H] (EIO [E, H, 2I] transposed back below)
         w2 = layer.w2.cpu()   # EOI [E, H, I]
+        if layer.layout == "EIO":
+            w1, w2 = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
     else:
         w1 = orc.mx_dequantize_weight_cols(layer.w1.cpu(), layer.s1.cpu()).to(torch.bfloat16).transpose(1, 2).contiguous()
         w2 = orc.mx_dequantize_weight_cols(layer.w2.cpu(), layer.s2.cpu()).to(torch.bfloat16).transpose(1, 2).contiguous()
@@ -248,8 +254,9 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
                       f"torch CPU {torch.__version__}, os.cpu_count()={os.cpu_count()}, cpu={platform.processor() or platform.machine()}"}
 
 
-def run_config(name: str, device, steps: int, warmup: int, variant: str = "default") -> dict:
-    layer = Layer(name, device)
+def run_config(name: str, device, steps: int, warmup: int, variant: str = "default",
+               bf16_layout: str = "EOI") -> dict:
+    layer = Layer(name, device, bf16_layout)
     counts = layer.counts()
     work = gmm_work(layer.c, counts)
     m = measure(layer, steps, warmup)
@@ -264,7 +271,9 @@ def run_config(name: str, device, steps: int, warmup: int, variant: str = "defau
         "active_experts": work["active"],
         "weight_layout": layer.layout,
         "stage_ms": {k: round(v, 4) for k, v in m["stage_ms"].items()},
-        "roofline": roofline(c, work, m["stage_ms"]["gmm1"], measured_traffic(name, variant)),
+        "roofline": roofline(c, work, m["stage_ms"]["gmm1"],
+                             measured_traffic(name, variant if layer.layout == "EOI" or c["precision"] != "bf16"
+                                              else f"{variant}_EIO")),
     }
     return res, layer
 
@@ -332,6 +341,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv", "sp", "sp4"],
                     help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
+    ap.add_argument("--bf16-layout", default="EOI", choices=["EOI", "EIO"],
+                    help="expert-weight layout of the bf16 configs (EIO: the reference module's default)")
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="time the DSv3-shape grouped GEMMs on their own per layout and variant (one JSON line)")
     args = ap.parse_args()
@@ -356,7 +367,7 @@ def main() -> int:
     gemm_variant = ops.set_gemm_variant("default")
     ops.set_gemm_variant(gemm_variant)
     log(f"[bench] workload {args.config}: steps={args.steps} warmup={args.warmup}")
-    res, layer = run_config(args.config, device, args.steps, args.warmup, gemm_variant)
+    res, layer = run_config(args.config, device, args.steps, args.warmup, gemm_variant, args.bf16_layout)
     c = layer.c
     cpu = None if args.no_cpu else cpu_baseline(args.config, layer)
     del layer
@@ -367,7 +378,8 @@ def main() -> int:
         if name == args.config:
             continue
         log(f"[bench] extra {name}")
-        r, lyr = run_config(name, device, max(5, args.steps // 2), max(2, args.warmup // 2), gemm_variant)
+        r, lyr = run_config(name, device, max(5, args.steps // 2), max(2, args.warmup // 2), gemm_variant,
+                            args.bf16_layout)
         extra[name] = r
         del lyr
         torch.cuda.empty_cache()
