@@ -89,7 +89,7 @@ def test_cpu_tensors_fail_loudly():
 # ------------------------------------------------------------------------------------------------
 # GPU: the operators equal the functional operators
 # ------------------------------------------------------------------------------------------------
-def _routed_inputs(device, T=300, H=256, E=16, K=4, I=128, seed=11):
+def _routed_inputs(device, T=300, H=1024, E=16, K=4, I=512, seed=11):
     g = torch.Generator(device="cpu").manual_seed(seed)
     x = torch.randn(T, H, generator=g).to(BF).to(device)
     wr = (torch.randn(E, H, generator=g) * 0.02).to(BF).to(device)
