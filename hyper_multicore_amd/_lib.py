@@ -109,6 +109,8 @@ _SIGNATURES = [
                                          c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("mi355moe_token_unpermute", c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32,
                                            c_void_p, c_void_p]),
+    ("mi355moe_token_unpermute_grad", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32,
+                                                c_void_p, c_void_p, c_void_p]),
     ("mi355moe_mx_quantize_rows", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p]),
     ("mi355moe_mx_quantize_cols", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                             c_void_p]),

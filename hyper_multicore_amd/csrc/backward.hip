@@ -38,12 +38,27 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const uint16_t* U, int6
   *(uint4*)(act + r * I + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
 }
 
-// One block per routed row: dY[r] = bf16(p * dOut[t]) and dp[s] = sum_h y[r, h] * dOut[t, h].
+// dY[r] = bf16(p * dOut[t]) and dp[s] = sum_h y[r, h] * dOut[t, h] for routed row r of slot s = t*K + k.
+// BY_SLOT false: one block per routed row r, index = gather (row -> slot). BY_SLOT true: one block per
+// slot s, index = mapping (slot -> row); a slot whose row lies outside [0, R) writes no row and dp 0.
+template <bool BY_SLOT>
 __global__ __launch_bounds__(256) void dy_dp_kernel(const uint16_t* y, const uint16_t* dout, const float* probs,
-                                                    const int32_t* gather, int K, int H, uint16_t* dy, float* dp) {
+                                                    const int32_t* index, int K, int H, int64_t R, uint16_t* dy,
+                                                    float* dp) {
   __shared__ float part[4];
-  const int64_t r = blockIdx.x;
-  const int32_t s = gather[r];
+  int64_t r;
+  int32_t s;
+  if constexpr (BY_SLOT) {
+    s = (int32_t)blockIdx.x;
+    r = index[s];
+    if (r < 0 || r >= R) {
+      if (dp != nullptr && threadIdx.x == 0) dp[s] = 0.0f;
+      return;
+    }
+  } else {
+    r = blockIdx.x;
+    s = index[r];
+  }
   const int64_t t = s / K;
   const float p = probs[s];
   float acc = 0.0f;
@@ -328,8 +343,8 @@ int mx_backward(const MI355MoeBackwardArgs& a, char* ws, const MxBwdLayout& L, h
                 y)))
     return rc;
   // combine backward: dY = bf16(p dOut), dp = <y, dOut>
-  hipLaunchKernelGGL(dy_dp_kernel, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, gather, K, H,
-                     dy, a.grad_topk_weights);
+  hipLaunchKernelGGL(dy_dp_kernel<false>, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, gather, K,
+                     H, R, dy, a.grad_topk_weights);
   if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
   if ((rc = quant(MX_Q_BF16, dy, nullptr, 1, H, H, L.dyq, L.dys, ldH, L.dycol, L.dycs))) return rc;
   // dW2 [E, I, H] = Q_rows(act)^T Q_rows(dY);  gA = bf16(Q_H(dY) W2_row^T)
@@ -353,6 +368,26 @@ int mx_backward(const MI355MoeBackwardArgs& a, char* ws, const MxBwdLayout& L, h
 }
 
 }  // namespace
+
+extern "C" int mi355moe_token_unpermute_grad(const uint16_t* permuted, const uint16_t* grad_out, const int32_t* mapping,
+                                             const float* probs, int64_t num_tokens, int32_t top_k,
+                                             int32_t hidden_size, uint16_t* grad_permuted, float* grad_probs,
+                                             void* stream) {
+  if (num_tokens < 0 || top_k <= 0 || hidden_size <= 0 || hidden_size % 8) return MI355MOE_EINVAL;
+  const int64_t R = num_tokens * top_k;
+  if (R > 0x7fffffff) return MI355MOE_EUNSUPPORTED;  // one block per slot
+  if (num_tokens > 0) {
+    if (permuted == nullptr || grad_out == nullptr || mapping == nullptr || probs == nullptr ||
+        grad_permuted == nullptr)
+      return MI355MOE_EINVAL;
+    if (((uintptr_t)permuted | (uintptr_t)grad_out | (uintptr_t)grad_permuted) & 15) return MI355MOE_EINVAL;
+  }
+  if (!mi355_backward_enabled()) return MI355MOE_EUNSUPPORTED;
+  if (R == 0) return MI355MOE_OK;
+  hipLaunchKernelGGL(dy_dp_kernel<true>, dim3((unsigned)R), dim3(256), 0, (hipStream_t)stream, permuted, grad_out,
+                     probs, mapping, top_k, hidden_size, R, grad_permuted, grad_probs);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
 
 extern "C" size_t mi355moe_moe_backward_workspace_size(const MI355MoeBackwardArgs* args) {
   if (args == nullptr || validate_bwd(*args) != MI355MOE_OK) return 0;
@@ -459,8 +494,8 @@ extern "C" int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* wor
   rc = gmm(act, I, a.w2, !eoi, eoi ? I : H, w2_group, H, y);
   if (rc) return rc;
   // combine backward
-  hipLaunchKernelGGL(dy_dp_kernel, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, gather, K, H,
-                     dy, a.grad_topk_weights);
+  hipLaunchKernelGGL(dy_dp_kernel<false>, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, gather, K,
+                     H, R, dy, a.grad_topk_weights);
   if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
   // down backward: gA = dY W2^T (W2 read transposed: EIO [I, H] rows are the N index -> NK)
   rc = gmm(dy, H, a.w2, eoi, eoi ? I : H, w2_group, I, ga);

@@ -255,6 +255,37 @@ def token_unpermute(values: torch.Tensor, mapping: torch.Tensor, probs: torch.Te
     return out
 
 
+def token_unpermute_grad(values: torch.Tensor, grad_out: torch.Tensor, mapping: torch.Tensor, probs: torch.Tensor,
+                         top_k: int, *, grad_values: torch.Tensor | None = None,
+                         grad_probs: torch.Tensor | None = None):
+    """Gradient of :func:`token_unpermute` with probabilities: (grad_values bf16 [T*K, H] with
+    grad_values[mapping[t*K+k]] = bf16(p[t,k] * grad_out[t]), grad_probs fp32 [T, K] with
+    grad_probs[t,k] = <values[mapping[t*K+k]], grad_out[t]>), like hyper_multicore::
+    mega_moe_unpermute_grad_out (torch/csrc/mega_moe_unpermute.cpp:16-62). Written into
+    ``grad_values`` / ``grad_probs`` when given (contiguous, shaped as above)."""
+    lib = _lib.load()
+    device = _require_gpu(values, grad_out, mapping, probs, grad_values, grad_probs)
+    if values.dtype != torch.bfloat16 or grad_out.dtype != torch.bfloat16 or values.ndim != 2 or grad_out.ndim != 2:
+        raise TypeError("values and grad_out must be bf16 matrices")
+    if mapping.dtype != torch.int32 or mapping.ndim != 1 or probs.dtype != torch.float32:
+        raise TypeError("mapping must be int32 [T*K] and probs float32 [T, K]")
+    T, H = grad_out.shape
+    if probs.shape != (T, top_k) or mapping.numel() != T * top_k or values.shape != (T * top_k, H):
+        raise ValueError("unpermute gradient needs all top-k rows: values [T*K, H], probs [T, K], mapping [T*K]")
+    if grad_values is None:
+        grad_values = torch.empty((T * top_k, H), dtype=torch.bfloat16, device=device)
+    if grad_probs is None:
+        grad_probs = torch.empty((T, top_k), dtype=torch.float32, device=device)
+    if (grad_values.shape != values.shape or grad_values.dtype != torch.bfloat16 or not grad_values.is_contiguous()
+            or grad_probs.shape != probs.shape or grad_probs.dtype != torch.float32 or not grad_probs.is_contiguous()):
+        raise ValueError("grad_values / grad_probs must be contiguous and shaped like values / probs")
+    rc = lib.mi355moe_token_unpermute_grad(_ptr(values.contiguous()), _ptr(grad_out.contiguous()),
+                                           _ptr(mapping.contiguous()), _ptr(probs.contiguous()), T, top_k, H,
+                                           _ptr(grad_values), _ptr(grad_probs), _stream(device))
+    _lib.check(rc, "mi355moe_token_unpermute_grad")
+    return grad_values, grad_probs
+
+
 # ------------------------------------------------------------------------------------------------
 # MX quantisation
 # ------------------------------------------------------------------------------------------------

@@ -26,7 +26,9 @@ Operators (schema differences from the reference are noted per operator):
   routed_scaling_factor, scoring_func) -> grad_logits`` (mega_gate_registration.cpp:31-41).
 * ``dispatch(topk_ids, num_experts) -> (counts, expert_offsets, group_list, mapping,
   gather_index, error_flag)``.
-* ``combine(values, mapping, probs?, top_k) -> out`` (the unpermute).
+* ``combine(values, mapping, probs?, top_k) -> out`` (the unpermute) and
+  ``mega_moe_unpermute_grad_out(permuted_tokens, grad_output, sorted_indices, probs, grad_permuted!,
+  grad_probs!)``, its gradient (registration.cpp:17-20; returns nothing instead of the aliases).
 * ``mx_quantize_rows(x) -> (data, scale)``.
 * ``grouped_gemm_bf16(x, weights, group_list, layout) -> out``.
 * ``grouped_gemm_mxfp8(xq, x_scale, w_data, w_scale, group_list, layout) -> out``.
@@ -45,8 +47,8 @@ from . import _lib, ops
 
 NAMESPACE = "hyper_multicore_mi355"
 OPERATORS = ("moe_token_permute_out", "token_permute", "gate_logits", "mega_gate_route", "mega_gate_route_grad",
-             "dispatch", "combine", "mx_quantize_rows", "grouped_gemm_bf16", "grouped_gemm_mxfp8", "moe_forward",
-             "moe_forward_out")
+             "mega_moe_unpermute_grad_out", "dispatch", "combine", "mx_quantize_rows", "grouped_gemm_bf16",
+             "grouped_gemm_mxfp8", "moe_forward", "moe_forward_out")
 
 
 def _name(op: str) -> str:
@@ -186,6 +188,32 @@ def _(values, mapping, probs, top_k):
     if mapping.numel() % top_k:
         raise ValueError("mapping must be int32 [T*K]")
     return values.new_empty((mapping.numel() // top_k, values.shape[1]))
+
+
+def _check_unpermute_grad(permuted_tokens, grad_output, sorted_indices, probs, grad_permuted, grad_probs) -> None:
+    if permuted_tokens.ndim != 2 or grad_output.ndim != 2 or probs.ndim != 2 or sorted_indices.ndim != 1:
+        raise ValueError("unpermute requires matrix tokens, gradients and probabilities, and flat indices")
+    if grad_permuted.shape != permuted_tokens.shape or grad_probs.shape != probs.shape:
+        raise ValueError("unpermute output shapes must match tokens and probabilities")
+    if (permuted_tokens.shape[1] != grad_output.shape[1] or grad_output.shape[0] != probs.shape[0]
+            or permuted_tokens.shape[0] != probs.numel() or sorted_indices.numel() != permuted_tokens.shape[0]):
+        raise ValueError("unpermute requires all top-k rows without padding or dropped tokens")
+
+
+@torch.library.custom_op(_name("mega_moe_unpermute_grad_out"), mutates_args=("grad_permuted", "grad_probs"))
+def mega_moe_unpermute_grad_out(permuted_tokens: torch.Tensor, grad_output: torch.Tensor,
+                                sorted_indices: torch.Tensor, probs: torch.Tensor, grad_permuted: torch.Tensor,
+                                grad_probs: torch.Tensor) -> None:
+    """The reference's out-variant unpermute gradient (registration.cpp:17-20,
+    mega_moe_unpermute.cpp:16-62); ``sorted_indices`` is the slot -> routed-row mapping."""
+    _check_unpermute_grad(permuted_tokens, grad_output, sorted_indices, probs, grad_permuted, grad_probs)
+    ops.token_unpermute_grad(permuted_tokens, grad_output, sorted_indices, probs, probs.shape[1],
+                             grad_values=grad_permuted, grad_probs=grad_probs)
+
+
+@mega_moe_unpermute_grad_out.register_fake
+def _(permuted_tokens, grad_output, sorted_indices, probs, grad_permuted, grad_probs):
+    _check_unpermute_grad(permuted_tokens, grad_output, sorted_indices, probs, grad_permuted, grad_probs)
 
 
 # ---- MX quantisation and grouped GEMMs ------------------------------------------------------------

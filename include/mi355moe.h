@@ -212,6 +212,20 @@ int mi355moe_token_unpermute(const uint16_t* y, const int32_t* mapping, const fl
                              uint16_t* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Token unpermute gradient: for every slot s = t*K + k with routed row r = mapping[s],
+ *   grad_permuted[r] = bf16( p[s] * grad_out[t] )   and   grad_probs[s] = sum_h y[r,h] * grad_out[t,h]
+ * (fp32 products and accumulation). y = permuted [T*K, H] bf16, grad_out [T, H] bf16, probs fp32 [T, K];
+ * rows 16-byte aligned (H % 8 == 0). A slot whose row lies outside [0, T*K) writes no row and
+ * grad_probs 0; grad_probs may be NULL. Part of the expert backward (MI355MOE_FEATURE_BACKWARD;
+ * -3 while that is switched off).
+ * Replaces hyper_multicore::mega_moe_unpermute_grad_out -> aclnnMoeTokenUnpermuteGrad, non-padded
+ * (torch/csrc/mega_moe_unpermute.cpp:56-62, registration.cpp:17-20).
+ */
+int mi355moe_token_unpermute_grad(const uint16_t* permuted, const uint16_t* grad_out, const int32_t* mapping,
+                                  const float* probs, int64_t num_tokens, int32_t top_k, int32_t hidden_size,
+                                  uint16_t* grad_permuted, float* grad_probs, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * MX (OCP MX v1.0) quantisation, e4m3fn elements with one e8m0 scale per 32 elements:
  * scale = 2^(floor(log2(amax)) - 8), element = RNE(v / scale) saturated to +-448.
  * rows:  x [M, N] bf16 -> q [M, N] e4m3, scale [M, N/32] e8m0 (blocks along N).

@@ -236,6 +236,23 @@ def unpermute_tokens(values: torch.Tensor, mapping: torch.Tensor, probs: torch.T
     return out.to(torch.bfloat16)
 
 
+def unpermute_grad_reference(values: torch.Tensor, grad_out: torch.Tensor, mapping: torch.Tensor,
+                             probs: torch.Tensor, top_k: int):
+    """Gradient of the weighted unpermute (mega_moe_unpermute_grad_out -> aclnnMoeTokenUnpermuteGrad,
+    non-padded; torch/csrc/mega_moe_unpermute.cpp:56-62): for slot s = t*K + k and row r = mapping[s],
+    grad_values[r] = bf16(fp32(grad_out[t]) * p[s]) and grad_probs[s] = sum_h fp32(values[r, h]) *
+    fp32(grad_out[t, h]) (fp32 accumulation; the order is not part of the contract). Returns
+    (grad_values bf16 [T*K, H], grad_probs fp32 [T, K]); rows no slot maps to stay zero."""
+    T = mapping.numel() // top_k
+    m = mapping.reshape(-1).long()
+    g = grad_out.float()[torch.arange(T * top_k) // top_k]  # [T*K, H], the token row of each slot
+    p = probs.reshape(-1).float()
+    grad_values = torch.zeros((values.shape[0], values.shape[1]), dtype=torch.bfloat16)
+    grad_values[m] = (g * p[:, None]).to(torch.bfloat16)
+    grad_probs = (values.float()[m] * g).sum(dim=1).reshape(T, top_k)
+    return grad_values, grad_probs
+
+
 # ------------------------------------------------------------------------------------------------
 # OCP MX (e4m3fn + e8m0 per 32)
 # ------------------------------------------------------------------------------------------------

@@ -206,6 +206,37 @@ def test_unpermute_closed_form():
     assert torch.equal(ident, y[:T])
 
 
+def test_unpermute_grad_is_the_autograd_of_the_unpermute():
+    """The restated unpermute gradient equals torch autograd of out[t] = sum_k p[t,k] y[mapping[t*K+k]]:
+    the row gradient bit for bit (the same fp32 product, rounded once to bf16), the probability
+    gradient to fp32 accumulation error (against float64 autograd). A transposed slot order, a
+    gradient scattered to the slot instead of the row, or p taken from the wrong slot each fail."""
+    g = torch.Generator().manual_seed(11)
+    T, K, H = 37, 3, 64
+    y = torch.randn(T * K, H, generator=g).to(torch.bfloat16)
+    mapping = torch.randperm(T * K, generator=g).to(torch.int32)
+    p = torch.rand(T, K, generator=g)
+    dout = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    gv, gp = orc.unpermute_grad_reference(y, dout, mapping, p, K)
+
+    yy = y.float().requires_grad_(True)
+    pp = p.clone().requires_grad_(True)
+    m = mapping.view(T, K).long()
+    out = sum(yy[m[:, k]] * pp[:, k:k + 1] for k in range(K))
+    out.backward(dout.float())
+    assert torch.equal(gv, yy.grad.to(torch.bfloat16))
+    y64 = y.double().requires_grad_(True)
+    p64 = p.double().requires_grad_(True)
+    sum(y64[m[:, k]] * p64[:, k:k + 1] for k in range(K)).backward(dout.double())
+    assert torch.allclose(gp.double(), p64.grad, rtol=1e-5, atol=1e-5)
+    # known answer: T = 1, K = 2, rows swapped by the mapping
+    y2 = torch.tensor([[1.0, 2.0], [3.0, 4.0]]).to(torch.bfloat16)
+    gv2, gp2 = orc.unpermute_grad_reference(y2, torch.tensor([[1.0, -1.0]]).to(torch.bfloat16),
+                                            torch.tensor([1, 0], dtype=torch.int32), torch.tensor([[0.25, 0.5]]), 2)
+    assert torch.equal(gv2.float(), torch.tensor([[0.5, -0.5], [0.25, -0.25]]))
+    assert torch.equal(gp2, torch.tensor([[-1.0, -1.0]]))
+
+
 # ------------------------------------------------------------------------------------------------
 # MX quantisation (OCP MX v1.0, e4m3fn + e8m0 / 32)
 # ------------------------------------------------------------------------------------------------

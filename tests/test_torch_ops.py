@@ -57,6 +57,22 @@ def test_fake_shapes_of_the_forward_path():
         assert g.shape == (T, E)
 
 
+def test_fake_unpermute_grad_checks_shapes_like_the_reference():
+    T, K, H = 6, 2, 64
+    with FakeTensorMode():
+        y = torch.empty(T * K, H, dtype=BF)
+        args = [y, torch.empty(T, H, dtype=BF), torch.empty(T * K, dtype=torch.int32), torch.empty(T, K)]
+        ns.mega_moe_unpermute_grad_out(*args, torch.empty(T * K, H, dtype=BF), torch.empty(T, K))
+        with pytest.raises(ValueError, match="output shapes"):
+            ns.mega_moe_unpermute_grad_out(*args, torch.empty(T, H, dtype=BF), torch.empty(T, K))
+        with pytest.raises(ValueError, match="all top-k rows"):
+            ns.mega_moe_unpermute_grad_out(y, torch.empty(T, H, dtype=BF), torch.empty(T, dtype=torch.int32),
+                                           torch.empty(T, K), torch.empty(T * K, H, dtype=BF), torch.empty(T, K))
+    s = ns.mega_moe_unpermute_grad_out.default._schema
+    assert [a.name for a in s.arguments if a.alias_info is not None and a.alias_info.is_write] == \
+        ["grad_permuted", "grad_probs"]
+
+
 def test_fake_kernels_validate_like_the_real_ones():
     with FakeTensorMode():
         x = torch.empty(8, 64, dtype=BF)
@@ -145,3 +161,32 @@ def test_gpu_gemm_and_forward_ops_equal_functional(gpu):
     out = torch.full_like(x, float("nan"))
     ns.moe_forward_out(x, ids, w, w1, w2, None, None, E, I, out, "bf16", "EOI")
     assert torch.equal(out, ref)
+
+
+@pytest.mark.gpu
+def test_gpu_unpermute_grad_matches_oracle(gpu):
+    """The unpermute gradient through the C ABI (part of the expert backward): the row gradient bit-exact,
+    the probability gradient within fp32 accumulation error; a slot mapped outside the rows writes none."""
+    from hyper_multicore_amd import _lib, ops
+    from oracle import moe_oracle as orc
+    if not ops.features() & _lib.FEATURE_BACKWARD:
+        pytest.skip("the expert backward is switched off in the library until its GPU tests have run")
+    g = torch.Generator().manual_seed(23)
+    T, K, H = 333, 4, 1024
+    y = torch.randn(T * K, H, generator=g).to(BF)
+    mapping = torch.randperm(T * K, generator=g).to(torch.int32)
+    p = torch.rand(T, K, generator=g)
+    dout = torch.randn(T, H, generator=g).to(BF)
+    gv, gp = (torch.full((T * K, H), float("nan"), dtype=BF, device=gpu),
+                        torch.full((T, K), float("nan"), device=gpu))
+    ns.mega_moe_unpermute_grad_out(y.to(gpu), dout.to(gpu), mapping.to(gpu), p.to(gpu), gv, gp)
+    rv, rp = orc.unpermute_grad_reference(y, dout, mapping, p, K)
+    assert torch.equal(gv.cpu(), rv)
+    assert torch.allclose(gp.cpu(), rp, rtol=1e-5, atol=1e-5)
+    bad = mapping.clone()
+    bad[5] = T * K  # outside the rows
+    gv2, gp2 = ops.token_unpermute_grad(y.to(gpu), dout.to(gpu), bad.to(gpu), p.to(gpu), K)
+    assert gp2[1, 1].item() == 0.0
+    keep = torch.ones(T * K, dtype=torch.bool)
+    keep[mapping[5].long()] = False  # the row slot 5 would have written
+    assert torch.equal(gv2.cpu()[keep], rv[keep])
