@@ -36,6 +36,9 @@ Operators (schema differences from the reference are noted per operator):
   intermediate_size, precision, layout, swiglu_limit, clamp_after_silu, apply_probs_before_fc2)
   -> out`` and ``moe_forward_out(..., out!)`` (the reference's ``mega_moe`` writes caller-owned
   buffers, registration.cpp:30-60).
+* ``moe_backward(hidden, topk_ids, topk_weights, w1, w2, grad_out, num_experts, intermediate_size,
+  layout, fp32_weight_grad) -> (grad_hidden, grad_w1, grad_w2, grad_topk_weights)`` — the bf16
+  ``mega_moe_grad`` (registration.cpp:62-107) at EP=1, with its buffers internal.
 """
 from __future__ import annotations
 
@@ -48,7 +51,7 @@ from . import _lib, ops
 NAMESPACE = "hyper_multicore_mi355"
 OPERATORS = ("moe_token_permute_out", "token_permute", "gate_logits", "mega_gate_route", "mega_gate_route_grad",
              "mega_moe_unpermute_grad_out", "dispatch", "combine", "mx_quantize_rows", "grouped_gemm_bf16",
-             "grouped_gemm_mxfp8", "moe_forward", "moe_forward_out")
+             "grouped_gemm_mxfp8", "moe_forward", "moe_forward_out", "moe_backward")
 
 
 def _name(op: str) -> str:
@@ -319,3 +322,31 @@ def _(hidden, topk_ids, topk_weights, w1, w2, w1_scale, w2_scale, num_experts, i
     _check_forward(hidden, topk_ids, topk_weights, precision, layout)
     if out.shape != hidden.shape:
         raise ValueError("out must be shaped like hidden")
+
+
+@torch.library.custom_op(_name("moe_backward"), mutates_args=())
+def moe_backward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w1: torch.Tensor,
+                 w2: torch.Tensor, grad_out: torch.Tensor, num_experts: int, intermediate_size: int,
+                 layout: str = "EIO", fp32_weight_grad: bool = False
+                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients of the bf16 ``moe_forward`` (default numerics): (grad_hidden bf16 [T, H], grad_w1,
+    grad_w2 in the weights' layout, fp32 when ``fp32_weight_grad`` else bf16, grad_topk_weights fp32
+    [T, K]); the reference's ``mega_moe_grad`` (registration.cpp:62-107) at EP=1. Needs the expert
+    backward switched on in the library."""
+    _check_forward(hidden, topk_ids, topk_weights, "bf16", layout)
+    gx, g1, g2, gp = ops.moe_backward(hidden, topk_ids, topk_weights, w1, w2, grad_out, num_experts=num_experts,
+                                      intermediate_size=intermediate_size, layout=layout,
+                                      weight_grad_dtype=torch.float32 if fp32_weight_grad else torch.bfloat16,
+                                      need_topk_grad=True)
+    return gx, g1, g2, gp
+
+
+@moe_backward.register_fake
+def _(hidden, topk_ids, topk_weights, w1, w2, grad_out, num_experts, intermediate_size, layout="EIO",
+      fp32_weight_grad=False):
+    _check_forward(hidden, topk_ids, topk_weights, "bf16", layout)
+    if grad_out.shape != hidden.shape:
+        raise ValueError("grad_out must be shaped like hidden")
+    wd = torch.float32 if fp32_weight_grad else torch.bfloat16
+    return (hidden.new_empty(tuple(hidden.shape)), w1.new_empty(tuple(w1.shape), dtype=wd),
+            w2.new_empty(tuple(w2.shape), dtype=wd), hidden.new_empty(tuple(topk_ids.shape), dtype=torch.float32))

@@ -55,6 +55,11 @@ def test_fake_shapes_of_the_forward_path():
         assert f.shape == (T, H) and f.dtype == BF
         g = ns.mega_gate_route_grad(logits, scores, ids, w, K, 2.5, "sigmoid")
         assert g.shape == (T, E)
+        w1, w2 = torch.empty(E, H, 2 * I, dtype=BF), torch.empty(E, I, H, dtype=BF)
+        gx, g1, g2, gp = ns.moe_backward(x, ids, w, w1, w2, f, E, I, "EIO", True)
+        assert (gx.shape, g1.shape, g1.dtype, g2.shape, gp.shape) == ((T, H), (E, H, 2 * I), torch.float32,
+                                                                       (E, I, H), (T, K))
+        assert ns.moe_backward(x, ids, w, w1, w2, f, E, I)[1].dtype == BF
 
 
 def test_fake_unpermute_grad_checks_shapes_like_the_reference():
@@ -190,3 +195,18 @@ def test_gpu_unpermute_grad_matches_oracle(gpu):
     keep = torch.ones(T * K, dtype=torch.bool)
     keep[mapping[5].long()] = False  # the row slot 5 would have written
     assert torch.equal(gv2.cpu()[keep], rv[keep])
+
+
+@pytest.mark.gpu
+def test_gpu_moe_backward_op_equals_functional(gpu):
+    from hyper_multicore_amd import _lib, ops
+    if not ops.features() & _lib.FEATURE_BACKWARD:
+        pytest.skip("the expert backward is switched off in the library until its GPU tests have run")
+    x, wr, bias, w1, w2, E, K, I = _routed_inputs(gpu)
+    w, ids = ops.gate_route(ops.gate_logits(x, wr), bias, top_k=K, scoring_func="softmax", routed_scaling_factor=1.0)
+    dout = torch.randn_like(x)
+    got = ns.moe_backward(x, ids, w, w1, w2, dout, E, I, "EOI", True)
+    want = ops.moe_backward(x, ids, w, w1, w2, dout, num_experts=E, intermediate_size=I, layout="EOI",
+                            weight_grad_dtype=torch.float32)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
