@@ -18,12 +18,13 @@ Operators (schema differences from the reference are noted per operator):
 * ``token_permute(tokens, indices, num_experts) -> (routed, mapping)``.
 * ``gate_logits(x, weight, weight_vision?, image_mask?) -> logits`` (fp32 projection).
 * ``mega_gate_route(logits, text_bias, vision_bias?, image_mask?, top_k, routed_scaling_factor,
-  use_vision_bias, scoring_func, num_groups, topk_groups) -> (weights, indices, route_scores)`` —
-  the reference's ``mega_gate_route`` (mega_gate_registration.cpp:19-30) with the scoring function
-  and group limits as arguments instead of its ``runtime_config`` bytes; the reference's
-  ``selected_scores`` / ``normalization_denominator`` diagnostics are not produced.
-* ``mega_gate_route_grad(logits, route_scores, expert_indices, grad_routing_weights, top_k,
-  routed_scaling_factor, scoring_func) -> grad_logits`` (mega_gate_registration.cpp:31-41).
+  use_vision_bias, scoring_func, num_groups, topk_groups) -> (weights, indices, route_scores,
+  selected_scores, normalization_denominator)`` — the reference's ``mega_gate_route``
+  (mega_gate_registration.cpp:19-30) with the scoring function and group limits as arguments instead
+  of its ``runtime_config`` bytes (and no diagnostic buffer).
+* ``mega_gate_route_grad(logits, route_scores, selected_scores, normalization_denominator,
+  expert_indices, grad_routing_weights, top_k, routed_scaling_factor, scoring_func) -> grad_logits``
+  (mega_gate_registration.cpp:31-41).
 * ``dispatch(topk_ids, num_experts) -> (counts, expert_offsets, group_list, mapping,
   gather_index, error_flag)``.
 * ``combine(values, mapping, probs?, top_k) -> out`` (the unpermute) and
@@ -123,19 +124,35 @@ def _(x, weight, weight_vision=None, image_mask=None):
     return x.new_empty((x.shape[0], weight.shape[0]), dtype=torch.float32)
 
 
+def _selected_and_denominator(scores: torch.Tensor, indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The unbiased scores of the selected experts [T, K] and sum_k of them + 1e-20 [T, 1], summed in
+    ascending k from 0 in fp32 as the route kernel normalises (route_pipeline.h:424-466: Sum, then
+    Adds 1e-20)."""
+    selected = scores.gather(1, indices)
+    den = torch.zeros((scores.shape[0], 1), dtype=torch.float32, device=scores.device)
+    for k in range(indices.shape[1]):
+        den = den + selected[:, k:k + 1]
+    return selected, den + 1.0e-20
+
+
 @torch.library.custom_op(_name("mega_gate_route"), mutates_args=())
 def mega_gate_route(logits: torch.Tensor, text_bias: torch.Tensor, vision_bias: Optional[torch.Tensor],
                     image_mask: Optional[torch.Tensor], top_k: int, routed_scaling_factor: float,
                     use_vision_bias: bool, scoring_func: str = "sigmoid", num_groups: int = 1,
-                    topk_groups: int = 1) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(weights fp32 [T, K], indices int64 [T, K], unbiased route scores fp32 [T, E])."""
+                    topk_groups: int = 1) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                                   torch.Tensor]:
+    """(routing weights fp32 [T, K], expert indices int64 [T, K], unbiased route scores fp32 [T, E],
+    selected scores fp32 [T, K], normalization denominator fp32 [T, 1]) like the reference's five
+    outputs (mega_gate.cpp:65-82)."""
     if use_vision_bias and (vision_bias is None or image_mask is None):
         raise ValueError("use_vision_bias needs vision_bias and image_mask")
-    return ops.gate_route(logits, text_bias, top_k=top_k, scoring_func=scoring_func,
-                          routed_scaling_factor=routed_scaling_factor,
-                          bias_vl=vision_bias if use_vision_bias else None,
-                          image_mask=image_mask if use_vision_bias else None, num_groups=num_groups,
-                          topk_groups=topk_groups, return_scores=True)
+    w, ids, scores = ops.gate_route(logits, text_bias, top_k=top_k, scoring_func=scoring_func,
+                                    routed_scaling_factor=routed_scaling_factor,
+                                    bias_vl=vision_bias if use_vision_bias else None,
+                                    image_mask=image_mask if use_vision_bias else None, num_groups=num_groups,
+                                    topk_groups=topk_groups, return_scores=True)
+    selected, den = _selected_and_denominator(scores, ids)
+    return w, ids, scores, selected, den
 
 
 @mega_gate_route.register_fake
@@ -144,21 +161,39 @@ def _(logits, text_bias, vision_bias, image_mask, top_k, routed_scaling_factor, 
     if logits.ndim != 2:
         raise TypeError("logits must be fp32 [tokens, experts]")
     T = logits.shape[0]
-    return (logits.new_empty((T, top_k), dtype=torch.float32), logits.new_empty((T, top_k), dtype=torch.int64),
-            logits.new_empty(tuple(logits.shape), dtype=torch.float32))
+    f = torch.float32
+    return (logits.new_empty((T, top_k), dtype=f), logits.new_empty((T, top_k), dtype=torch.int64),
+            logits.new_empty(tuple(logits.shape), dtype=f), logits.new_empty((T, top_k), dtype=f),
+            logits.new_empty((T, 1), dtype=f))
+
+
+def _check_route_grad(logits, route_scores, selected_scores, normalization_denominator, expert_indices,
+                      grad_routing_weights) -> None:
+    T = logits.shape[0]
+    if (route_scores.shape != logits.shape or selected_scores.shape != grad_routing_weights.shape
+            or tuple(normalization_denominator.shape) != (T, 1) or expert_indices.shape != grad_routing_weights.shape):
+        raise ValueError("route gradient shapes must match the forward's outputs")
 
 
 @torch.library.custom_op(_name("mega_gate_route_grad"), mutates_args=())
-def mega_gate_route_grad(logits: torch.Tensor, route_scores: torch.Tensor, expert_indices: torch.Tensor,
+def mega_gate_route_grad(logits: torch.Tensor, route_scores: torch.Tensor, selected_scores: torch.Tensor,
+                         normalization_denominator: torch.Tensor, expert_indices: torch.Tensor,
                          grad_routing_weights: torch.Tensor, top_k: int, routed_scaling_factor: float,
                          scoring_func: str = "sigmoid") -> torch.Tensor:
+    """Gradient of the routing weights with respect to the logits (mega_gate_registration.cpp:31-41).
+    The selected scores and the denominator are checked for shape and recomputed from the route
+    scores and indices on the device, in the order the forward used."""
+    _check_route_grad(logits, route_scores, selected_scores, normalization_denominator, expert_indices,
+                      grad_routing_weights)
     return ops.gate_route_grad(logits, route_scores, expert_indices, grad_routing_weights, top_k=top_k,
                                scoring_func=scoring_func, routed_scaling_factor=routed_scaling_factor)
 
 
 @mega_gate_route_grad.register_fake
-def _(logits, route_scores, expert_indices, grad_routing_weights, top_k, routed_scaling_factor,
-      scoring_func="sigmoid"):
+def _(logits, route_scores, selected_scores, normalization_denominator, expert_indices, grad_routing_weights, top_k,
+      routed_scaling_factor, scoring_func="sigmoid"):
+    _check_route_grad(logits, route_scores, selected_scores, normalization_denominator, expert_indices,
+                      grad_routing_weights)
     return logits.new_empty(tuple(logits.shape), dtype=torch.float32)
 
 

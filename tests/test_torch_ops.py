@@ -19,6 +19,17 @@ def test_every_operator_is_registered_with_a_fake_kernel():
         assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "Meta"), name
 
 
+def test_route_diagnostics_restate_the_normalisation():
+    """selected_scores / normalization_denominator as the route kernel normalises: sum from 0 in
+    ascending k, then + 1e-20 (checked on the CPU helper the operator uses)."""
+    scores = torch.tensor([[0.5, 0.25, 0.125, 1e-30]])
+    ids = torch.tensor([[3, 0, 2]])
+    sel, den = torch_ops._selected_and_denominator(scores, ids)
+    assert torch.equal(sel, torch.tensor([[1e-30, 0.5, 0.125]]))
+    want = ((torch.tensor(0.0) + 1e-30) + 0.5) + 0.125
+    assert den.shape == (1, 1) and den.item() == (want + torch.tensor(1e-20, dtype=torch.float32)).item()
+
+
 def test_out_variants_declare_their_mutations():
     s = ns.moe_token_permute_out.default._schema
     assert [a.name for a in s.arguments if a.alias_info is not None and a.alias_info.is_write] == ["output", "mapping"]
@@ -32,9 +43,11 @@ def test_fake_shapes_of_the_forward_path():
         x = torch.empty(T, H, dtype=BF)
         logits = ns.gate_logits(x, torch.empty(E, H, dtype=BF))
         assert logits.shape == (T, E) and logits.dtype == torch.float32
-        w, ids, scores = ns.mega_gate_route(logits, torch.empty(E), None, None, K, 2.5, False, "sigmoid", 4, 2)
+        w, ids, scores, sel, den = ns.mega_gate_route(logits, torch.empty(E), None, None, K, 2.5, False, "sigmoid",
+                                                      4, 2)
         assert (w.shape, w.dtype, ids.shape, ids.dtype, scores.shape) == ((T, K), torch.float32, (T, K), torch.int64,
                                                                           (T, E))
+        assert (sel.shape, den.shape, den.dtype) == ((T, K), (T, 1), torch.float32)
         counts, offs, gl, mapping, gather, err = ns.dispatch(ids, E)
         assert (counts.dtype, gl.dtype, mapping.shape, gather.shape, err.shape) == (torch.int32, torch.int64, (T * K,),
                                                                                     (T * K,), (1,))
@@ -53,7 +66,7 @@ def test_fake_shapes_of_the_forward_path():
         f = ns.moe_forward(x, ids, w, torch.empty(E, H, 2 * I, dtype=BF), torch.empty(E, I, H, dtype=BF), None, None,
                            E, I)
         assert f.shape == (T, H) and f.dtype == BF
-        g = ns.mega_gate_route_grad(logits, scores, ids, w, K, 2.5, "sigmoid")
+        g = ns.mega_gate_route_grad(logits, scores, sel, den, ids, w, K, 2.5, "sigmoid")
         assert g.shape == (T, E)
         w1, w2 = torch.empty(E, H, 2 * I, dtype=BF), torch.empty(E, I, H, dtype=BF)
         gx, g1, g2, gp = ns.moe_backward(x, ids, w, w1, w2, f, E, I, "EIO", True)
@@ -126,10 +139,13 @@ def test_gpu_router_and_dispatch_ops_equal_functional(gpu):
     x, wr, bias, _, _, E, K, _ = _routed_inputs(gpu)
     logits = ns.gate_logits(x, wr)
     assert torch.equal(logits, ops.gate_logits(x, wr))
-    w, ids, scores = ns.mega_gate_route(logits, bias, None, None, K, 2.5, False, "sigmoid", 4, 2)
+    w, ids, scores, sel, den = ns.mega_gate_route(logits, bias, None, None, K, 2.5, False, "sigmoid", 4, 2)
     w2_, ids2, sc2 = ops.gate_route(logits, bias, top_k=K, scoring_func="sigmoid", routed_scaling_factor=2.5,
                                     num_groups=4, topk_groups=2, return_scores=True)
     assert torch.equal(w, w2_) and torch.equal(ids, ids2) and torch.equal(scores, sc2)
+    assert torch.equal(sel, sc2.gather(1, ids2))
+    # the weights are the selected scores over the denominator, times the scale
+    assert torch.allclose(w, sel / den * 2.5, rtol=1e-6, atol=0.0)
     d = ops.dispatch(ids, E)
     got = ns.dispatch(ids, E)
     for a, b in zip(got, (d.counts, d.expert_offsets, d.group_list, d.mapping, d.gather_index, d.error_flag)):
