@@ -53,6 +53,18 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
 
 
+def test_unpermute_grad_validation():
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    f = lib.mi355moe_token_unpermute_grad
+    assert f(16, 16, 16, 16, 4, 2, 1004, 16, 16, None) == _lib.EINVAL        # hidden % 8
+    assert f(None, 16, 16, 16, 4, 2, 1024, 16, 16, None) == _lib.EINVAL      # missing rows
+    assert f(24, 16, 16, 16, 4, 2, 1024, 16, 16, None) == _lib.EINVAL        # rows not 16-byte aligned
+    assert f(16, 16, 16, 16, -1, 2, 1024, 16, 16, None) == _lib.EINVAL
+    if not lib.mi355moe_features() & _lib.FEATURE_BACKWARD:  # nothing is launched while switched off
+        assert f(16, 16, 16, 16, 4, 2, 1024, 16, 16, None) == _lib.EUNSUPPORTED
+
+
 def test_numerics_options_validation():
     from hyper_multicore_amd import _lib
     lib = _lib.load()
