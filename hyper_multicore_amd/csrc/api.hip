@@ -22,7 +22,7 @@ extern "C" int mi355moe_features(void) {
 }
 
 extern "C" int mi355moe_set_gemm_variant(int variant) {
-  if (variant < MI355_GG_VARIANT_DEFAULT || variant > MI355_GG_VARIANT_SP4) return MI355MOE_EUNSUPPORTED;
+  if (variant < MI355_GG_VARIANT_DEFAULT || variant > MI355_GG_VARIANT_PP) return MI355MOE_EUNSUPPORTED;
   if (variant == MI355_GG_VARIANT_DV && !mi355_direct_gemm_enabled()) return MI355MOE_EUNSUPPORTED;
   if ((variant == MI355_GG_VARIANT_SP || variant == MI355_GG_VARIANT_SP4) && !mi355_split_roles_enabled())
     return MI355MOE_EUNSUPPORTED;

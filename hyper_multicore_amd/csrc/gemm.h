@@ -47,6 +47,12 @@ struct GGParams {
   // with 32-bit offsets and runs only when this is set and below 4 GiB. Last member, so the other
   // members keep their kernel-argument offsets.
   int64_t a_bytes;
+  // Stage-major MX scales (the 8-wave configuration, gemm_pp.hip): when a_scale_stage_stride (bytes
+  // per 64-K stage) is set, a_scale holds [K/64][source rows][4] - the stage's two codes of each
+  // source row and two pad bytes - so one 4-byte copy per row brings a stage's codes. When
+  // c_scale_stage_stride is set, the MX SwiGLU epilogue writes c_scale in that form.
+  int64_t a_scale_stage_stride;
+  int64_t c_scale_stage_stride;
 };
 
 
@@ -91,7 +97,7 @@ int mi355_num_cus();  // CU count of the current device (cached per device)
 // keeps the default's tile height, so tile plans are shared; it answers MI355MOE_EUNSUPPORTED for the
 // paths it does not build, which then run on the default configuration.
 enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1, MI355_GG_VARIANT_DV = 2, MI355_GG_VARIANT_SP = 3,
-       MI355_GG_VARIANT_SP4 = 4 };
+       MI355_GG_VARIANT_SP4 = 4, MI355_GG_VARIANT_PP = 5 };
 int mi355_gg_variant();
 int mi355_gg_set_variant(int variant);  // returns the previous variant
 int mi355_grouped_gemm_variant(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
@@ -101,6 +107,10 @@ int mi355_grouped_gemm_direct(const GGParams& p, bool mx, bool b_kn, int epi, hi
 // The split-role configurations (gemm_split.hip), variants sp / sp4; MI355MOE_EUNSUPPORTED outside
 // their domain (gg_split_applies).
 int mi355_grouped_gemm_split(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
+// The 8-wave ping-pong configuration (gemm_pp.hip); MI355MOE_EUNSUPPORTED outside its domain
+// (mi355_gg_pp_applies). Tile plans are those of the 256-row configuration.
+bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi);
+int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
 #include "features.h"
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {
   return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;

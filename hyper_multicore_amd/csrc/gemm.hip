@@ -86,7 +86,10 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
     return dispatch_gg<GGSmall>(p, mx, b_kn, epi, stream);
   }
   const int variant = mi355_gg_variant();
-  if (variant != MI355_GG_VARIANT_DEFAULT) {
+  if (variant == MI355_GG_VARIANT_PP) {
+    const int rc = mi355_grouped_gemm_pp(p, mx, b_kn, epi, stream);
+    if (rc != MI355MOE_EUNSUPPORTED) return rc;
+  } else if (variant != MI355_GG_VARIANT_DEFAULT) {
     const int rc = mi355_grouped_gemm_variant(p, mx, b_kn, epi, stream, variant);
     if (rc != MI355MOE_EUNSUPPORTED) return rc;
   }
@@ -104,6 +107,7 @@ int mi355_gg_variant() {
     if (s != nullptr && strcmp(s, "dv") == 0 && mi355_direct_gemm_enabled()) v = MI355_GG_VARIANT_DV;
     if (s != nullptr && strcmp(s, "sp") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP;
     if (s != nullptr && strcmp(s, "sp4") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP4;
+    if (s != nullptr && strcmp(s, "pp") == 0) v = MI355_GG_VARIANT_PP;
     g_gg_variant = v;
   }
   return g_gg_variant;

@@ -1,0 +1,590 @@
+// Persistent grouped GEMM for gfx950 (MI355X), 8-wave ping-pong configuration: bf16 and MXFP8.
+//
+// Work list: as in gemm.hip - every (group, 256-row m-tile, 256-column n-tile) is one work item,
+// decoded on the device from the tile prefix; one workgroup per CU, work item L of round r goes to
+// workgroup 8 * slot + xcd, so each XCD runs a contiguous run of items (m fastest) and the n-tiles
+// that re-read one expert's activation rows run at the same time on one XCD and share its L2.
+//
+// Workgroup: 512 threads = 8 wavefronts, two per SIMD. Wave w computes rows 128 * (w / 4) ..+127
+// and columns 64 * (w % 4) ..+63 of the 256 x 256 tile (4 x 2 blocks of 32 x 32; bf16
+// v_mfma_f32_32x32x16_bf16, MXFP8 v_mfma_scale_f32_32x32x64_f8f6f4). The waves form two groups,
+// 0-3 and 4-7, one wave of each on every SIMD.
+//
+// K stages are 128 bytes per row (64 bf16 or 128 e4m3): whole 128-byte lines per row and stage,
+// which the memory system streams markedly faster than half lines when one operand is re-read from
+// L2 while the other streams from HBM. A stage is 64 KB of operands, so the LDS ring has two slots:
+// the copies of stage q + 1 go out at the start of the interval in which stage q is used, into the
+// slot that stage q - 1 left. A stage is used in two half-steps of 64 bytes of K (one set of
+// operand fragments in registers at a time). Between two barriers the groups alternate on every
+// SIMD: group 0 reads half 0 of stage q while group 1 issues the MFMAs of half 1 of stage q - 1,
+// then group 0 issues half 0's MFMAs while group 1 reads half 0, and so on, so each SIMD's matrix
+// core is fed alternately by its two waves while the other one reads LDS. Before the barrier that
+// ends the interval every wave waits for its own copies (loads of a wave retire in order; every wave
+// issues the same copies per stage). The stages of all work items of a workgroup form one stream,
+// so the next item's first stage is in flight while the current item finishes; copies past the end
+// of the stream re-read the last stage into the free slot, which keeps the counts exact.
+//
+// LDS layouts (16-byte chunks, XOR swizzled against bank conflicts):
+//   K-contiguous rows (activations; EOI weights): row r at r * 128, chunk c at c ^ ((r >> 1) & 7),
+//     read with ds_read_b128;
+//   N-contiguous weights (EIO bf16, MX col_data): K row k of the stage holds 256 columns; bf16
+//     chunk c at c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows),
+//     read with ds_read_b64_tr_b16 / ds_read_b64_tr_b8;
+//   MX scales of a stage: activation row r's four codes at r * 4 (the stage-major activation-scale
+//     layout [K/128][rows][4], copied one dword per row); weight tile column j's two codes of 64-K
+//     step s at s * 512 + j * 2 (the MX root's col_scale pairs).
+//
+// Epilogues: bf16 store, SwiGLU -> bf16 and SwiGLU -> MXFP8 requant (a 32-column MX block is the 32
+// lanes of a half-wavefront, so the block maximum is a 5-step lane butterfly); each 32 x 32 block
+// goes through a wave-private LDS staging block so the global stores are 16 bytes per lane. For SwiGLU the 64 weight columns of a wave are 32 gate then
+// the matching 32 up columns, so a lane holds gate and up of the same output element.
+#include "common.h"
+#include "gemm.h"
+#include "../../include/mi355moe.h"
+
+namespace {
+
+constexpr int BM = 256, BN = 256;
+constexpr int KB = 128;  // bytes of K per row and stage
+constexpr int S = 2;     // ring slots
+constexpr int WAVES = 8, THREADS = 64 * WAVES;
+constexpr int WM = 128, WN = 64, MI = WM / 32, NI = WN / 32;
+constexpr int A_BYTES = BM * KB, B_BYTES = BN * KB, AS_BYTES = BM * 4, BS_BYTES = 2 * BN * 2;
+constexpr int B_OFF = A_BYTES, AS_OFF = B_OFF + B_BYTES, BS_OFF = AS_OFF + AS_BYTES;
+constexpr int SLOT = BS_OFF + BS_BYTES;
+constexpr int PREFIX_OFF = S * SLOT;
+constexpr int PREFIX_MAX = 1024;  // groups whose tile prefix and row ends are kept in LDS
+constexpr int ROWS_OFF = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
+constexpr int EPI_BLOCK = 32 * 64;  // a wave's epilogue staging: one 32 x 32 bf16 block
+constexpr int EPI_OFF = (ROWS_OFF + PREFIX_MAX * 4 + 15) & ~15;
+constexpr int TOTAL = EPI_OFF + WAVES * EPI_BLOCK;
+constexpr int CPW = A_BYTES / 1024 / WAVES;  // 1 KB copies per operand, wave and stage
+static_assert(TOTAL <= 160 * 1024, "LDS budget");
+static_assert(SLOT % 16 == 0, "copy destinations are 16-byte aligned");
+static_assert(CPW == 4 && B_BYTES / 1024 / WAVES == CPW, "four 1 KB copies per operand and wave");
+
+// Tile column j (0..255) -> weight column; SwiGLU: wave tile q's 64 columns are gate columns
+// nt * 128 + 32 q .. +31, then the up columns I + the same.
+__device__ __forceinline__ int tile_col(int j, int nt, int I, bool swiglu) {
+  if (!swiglu) return nt * BN + j;
+  const int q = j >> 6, jj = j & 63;
+  const int base = nt * (BN / 2) + q * 32;
+  return jj < 32 ? base + jj : I + base + (jj - 32);
+}
+
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Direct global -> LDS copies: lane i writes its 16 (4) bytes at LDS address M0 + 16 i (4 i). Inline
+// assembly, so that the compiler does not treat the copy as an alias of every later LDS read (its
+// builtin makes it wait for all outstanding loads before the next ds_read).
+// The source is a wave-uniform base in scalar registers plus a 32-bit per-lane offset.
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
+               : "memory");
+}
+// A pointer known to be wave-uniform, held in scalar registers.
+__device__ __forceinline__ const uint8_t* uni_ptr(const uint8_t* ptr) {
+  const uint64_t v = (uint64_t)(uintptr_t)ptr;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Workgroup barrier without a memory fence: the copies are ordered by the explicit vmcnt waits.
+__device__ __forceinline__ void barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+struct Item {
+  int64_t row0;  // first routed row of the tile
+  int rows;      // valid rows (1..256)
+  int nt;        // n-tile
+  int g;         // group
+};
+
+#define LDSP(T, p) ((const __attribute__((address_space(3))) T*)(p))
+
+// Work item L from the tile prefix and the groups' row ends, both in LDS (LDS reads only: a global
+// or generic load here would make the wave wait for all of its outstanding copies).
+__device__ __forceinline__ void decode(const GGParams& p, const uint8_t* smem, int L, Item& it) {
+  const __attribute__((address_space(3))) int32_t* prefix = LDSP(int32_t, smem + PREFIX_OFF);
+  const __attribute__((address_space(3))) int32_t* rows = LDSP(int32_t, smem + ROWS_OFF);
+  int lo = 0, hi = p.G - 1;
+  while (lo < hi) {  // largest g with prefix[g] * n_tiles <= L
+    const int mid = (lo + hi + 1) >> 1;
+    if (prefix[mid] * p.n_tiles <= L) lo = mid; else hi = mid - 1;
+  }
+  const int g = uni(lo);
+  const int mtiles = uni(prefix[g + 1] - prefix[g]);
+  const int local = L - uni(prefix[g]) * p.n_tiles;
+  const int nt = local / mtiles;
+  const int mt = local - nt * mtiles;
+  const int64_t row_begin = g == 0 ? 0 : uni(rows[g - 1]);
+  const int64_t row_end = uni(rows[g]);
+  it.g = g;
+  it.nt = nt;
+  it.row0 = row_begin + (int64_t)mt * BM;
+  const int64_t left = row_end - it.row0;
+  it.rows = uni((int)(left < BM ? left : BM));
+}
+
+// Copy sources of one work item: wave-uniform bases of stage 0 (stage k adds k * the stride) and
+// per-lane 32-bit offsets (the activations, one group's weights and the scale arrays are below
+// 4 GiB, which mi355_gg_pp_applies checks).
+struct Plan {
+  const uint8_t* a_base;
+  const uint8_t* b_base;
+  const uint8_t* s_base;  // MX: activation scales (waves 0-3) or the group's weight scales (waves 4-7)
+  uint32_t ao[CPW], bo[CPW], so;
+  int64_t b_stride, s_stride;
+};
+
+// Activation and EOI-weight copies: copy i (0..31) of a stage covers rows 8 i ..+7, lane l row
+// 8 i + l / 8 and LDS position l % 8, which holds chunk (l % 8) ^ ((row >> 1) & 7).
+__device__ __forceinline__ int row_of(int i, int lane) { return i * 8 + (lane >> 3); }
+__device__ __forceinline__ int chunk_of(int r, int lane) { return (lane & 7) ^ ((r >> 1) & 7); }
+
+template <bool MX, bool B_KN, bool SWIGLU>
+__device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int wave, int lane, Plan& pl) {
+  constexpr int ESIZE = MX ? 1 : 2;
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int r = row_of(wave * CPW + j, lane);
+    const int rr = r < it.rows ? r : it.rows - 1;
+    const int64_t routed = it.row0 + rr;
+    const int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
+    pl.ao[j] = (uint32_t)(src * p.lda_bytes + chunk_of(r, lane) * 16);
+  }
+  pl.a_base = uni_ptr(p.A);
+  pl.b_base = uni_ptr(p.B + (int64_t)it.g * p.b_group_stride);
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int i = wave * CPW + j;
+    if constexpr (!B_KN) {
+      const int r = row_of(i, lane);
+      int wc = tile_col(r, it.nt, p.N, SWIGLU);
+      if (wc >= p.Ntot) wc = p.Ntot - 1;
+      pl.bo[j] = (uint32_t)((int64_t)wc * p.b_row_bytes + chunk_of(r, lane) * 16);
+    } else if constexpr (MX) {
+      const int L16 = i * 64 + lane;  // K rows of 256 bytes: copy i covers K rows 4 i ..+3
+      const int k = L16 >> 4;
+      const int c = (L16 & 15) ^ (k & 15);
+      int wc = tile_col(c * 16, it.nt, p.N, SWIGLU);
+      if (wc > p.Ntot - 16) wc = p.Ntot - 16;
+      pl.bo[j] = (uint32_t)((int64_t)k * p.b_row_bytes + wc);
+    } else {
+      const int L16 = i * 64 + lane;  // K rows of 512 bytes: copy i covers K rows 2 i, 2 i + 1
+      const int k = L16 >> 5;
+      const int c = (L16 & 31) ^ ((k & 7) << 1);
+      int wc = tile_col(c * 8, it.nt, p.N, SWIGLU);
+      if (wc > p.Ntot - 8) wc = p.Ntot - 8;
+      pl.bo[j] = (uint32_t)((int64_t)k * p.b_row_bytes + (int64_t)wc * 2);
+    }
+  }
+  pl.b_stride = B_KN ? (int64_t)(KB / ESIZE) * p.b_row_bytes : KB;
+  pl.s_base = pl.a_base;
+  pl.so = 0;
+  pl.s_stride = 0;
+  if constexpr (MX) {
+    if (wave < 4) {
+      const int r = wave * 64 + lane;
+      const int rr = r < it.rows ? r : it.rows - 1;
+      const int64_t routed = it.row0 + rr;
+      const int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
+      pl.s_base = uni_ptr(p.a_scale);
+      pl.so = (uint32_t)(src * 4);
+      pl.s_stride = p.a_scale_stage_stride;
+    } else {
+      // col_scale [G, K/64, Ntot, 2]: wave 4 + 2 s + h copies 64-K step s, tile columns 128 h ..+127
+      const int st = (wave >> 1) & 1;
+      const int j = (wave & 1) * 128 + lane * 2;
+      int wc = tile_col(j, it.nt, p.N, SWIGLU);
+      if (wc > p.Ntot - 2) wc = p.Ntot - 2;
+      pl.s_base = uni_ptr(p.b_scale + (int64_t)it.g * p.b_scale_group_stride);
+      pl.so = (uint32_t)(((int64_t)st * p.Ntot + wc) * 2);
+      pl.s_stride = (int64_t)p.Ntot * 4;  // two 64-K steps per stage
+    }
+  }
+}
+
+template <bool MX>
+__device__ __forceinline__ void issue_stage(const Plan& pl, int k, uint32_t slot, int wave) {
+  const uint8_t* ab = uni_ptr(pl.a_base + (int64_t)k * KB);
+  const uint8_t* bb = uni_ptr(pl.b_base + (int64_t)k * pl.b_stride);
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) dma16(ab, pl.ao[j], uni(slot + (wave * CPW + j) * 1024));
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) dma16(bb, pl.bo[j], uni(slot + B_OFF + (wave * CPW + j) * 1024));
+  if constexpr (MX)
+    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), pl.so,
+         uni(slot + (wave < 4 ? AS_OFF + wave * 256 : BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256)));
+}
+
+// LDS offset of 16-byte chunk c of K-contiguous row r
+__device__ __forceinline__ int chunk_off(int r, int c) { return r * KB + ((c ^ ((r >> 1) & 7)) << 4); }
+
+// Operand fragments of one half-step (64 bytes of K).
+template <bool MX, bool B_KN> struct Frags;
+template <> struct Frags<false, false> { v8bf a[2][MI], b[2][NI]; };
+template <> struct Frags<false, true> { v8bf a[2][MI]; v4s bl[2][NI], bh[2][NI]; };
+template <> struct Frags<true, false> { v4i al[MI], ah[MI], bl[NI], bh[NI]; int sa[MI], sb[NI]; };
+template <> struct Frags<true, true> { v4i al[MI], ah[MI]; v2i bp[NI][4]; int sa[MI], sb[NI]; };
+
+template <bool MX, bool B_KN>
+__device__ __forceinline__ void read_frags(Frags<MX, B_KN>& f, const uint8_t* slot, int h, int grp, int wq, int lane) {
+  const uint8_t* As = slot;
+  const uint8_t* Bs = slot + B_OFF;
+  if constexpr (!MX) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int ks = h * 2 + s2;  // 16-K step of the stage
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const int r = grp * WM + mi * 32 + (lane & 31);
+        f.a[s2][mi] = *LDSP(v8bf, As + chunk_off(r, ks * 2 + (lane >> 5)));
+      }
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        if constexpr (!B_KN) {
+          const int n = wq * WN + ni * 32 + (lane & 31);
+          f.b[s2][ni] = *LDSP(v8bf, Bs + chunk_off(n, ks * 2 + (lane >> 5)));
+        } else {
+          const int g16 = lane >> 4, m = lane & 15;
+          const int nb = wq * WN + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
+          const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
+          const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
+          const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
+          f.bl[s2][ni] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4s*)LDSP(v4s, Bs + off0));
+          f.bh[s2][ni] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4s*)LDSP(v4s, Bs + off1));
+        }
+      }
+    }
+  } else {
+    // one 64-K step h: lane r + 32 g holds K 16 g .. +15 and 32 + 16 g .. +15 of the step
+    const uint8_t* ASs = slot + AS_OFF;
+    const uint8_t* BSs = slot + BS_OFF;
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const int r = grp * WM + mi * 32 + (lane & 31);
+      const int c0 = h * 4 + (lane >> 5);
+      f.al[mi] = *LDSP(v4i, As + chunk_off(r, c0));
+      f.ah[mi] = *LDSP(v4i, As + chunk_off(r, c0 + 2));
+      f.sa[mi] = *LDSP(uint8_t, ASs + r * 4 + h * 2 + (lane >> 5));
+    }
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const int n = wq * WN + ni * 32 + (lane & 31);
+      if constexpr (!B_KN) {
+        const int c0 = h * 4 + (lane >> 5);
+        f.bl[ni] = *LDSP(v4i, Bs + chunk_off(n, c0));
+        f.bh[ni] = *LDSP(v4i, Bs + chunk_off(n, c0 + 2));
+      } else {
+        const int g16 = lane >> 4, m = lane & 15;
+        const int nb = wq * WN + ni * 32 + (g16 & 1) * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int k = h * 64 + (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
+          const int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
+          f.bp[ni][q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (__attribute__((address_space(3))) v2i*)LDSP(v2i, Bs + off));
+        }
+      }
+      f.sb[ni] = *LDSP(uint8_t, BSs + h * 512 + n * 2 + (lane >> 5));
+    }
+  }
+}
+
+template <bool MX, bool B_KN>
+__device__ __forceinline__ void mfmas(const Frags<MX, B_KN>& f, v16f (&acc)[MI][NI]) {
+  if constexpr (!MX) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          v8bf b;
+          if constexpr (!B_KN) b = f.b[s2][ni];
+          else b = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.bl[s2][ni], f.bh[s2][ni], 0, 1, 2, 3, 4, 5, 6, 7));
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s2][mi], b, acc[mi][ni], 0, 0, 0);
+        }
+  } else {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const v8i a = __builtin_shufflevector(f.al[mi], f.ah[mi], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        v8i b;
+        if constexpr (!B_KN) {
+          b = __builtin_shufflevector(f.bl[ni], f.bh[ni], 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+          const v4i b01 = __builtin_shufflevector(f.bp[ni][0], f.bp[ni][1], 0, 1, 2, 3);
+          const v4i b23 = __builtin_shufflevector(f.bp[ni][2], f.bp[ni][3], 0, 1, 2, 3);
+          b = __builtin_shufflevector(b01, b23, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+        acc[mi][ni] =
+            __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[mi][ni], 0, 0, 0, f.sa[mi], 0, f.sb[ni]);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
+  // the gate and up projections are rounded to bf16 (the GMM1 output), SiLU(gate) * up in fp32
+  const float gte = bf16_to_f32(f32_to_bf16(g_acc));
+  const float up = bf16_to_f32(f32_to_bf16(u_acc));
+  return gte / (1.0f + __expf(-gte)) * up;
+}
+
+// Staging offset of element (row, byte column cb) of a 32 x 64-byte block: 16-byte chunks swizzled
+// with (row >> 2) & 3, so the two half-wavefronts (rows r and r + 4) write different banks.
+__device__ __forceinline__ int stage_off(int row, int cb) { return row * 64 + ((((cb >> 4) ^ (row >> 2)) & 3) << 4) + (cb & 15); }
+
+// acc[mi][ni][r] holds row grp * 128 + mi * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
+// wq * 64 + ni * 32 + lane % 32 of the tile. Each 32 x 32 output block goes through the wave's LDS
+// staging block (LDS operations of a wave complete in order) and is written with 16-byte stores.
+template <int EPI>
+__device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[MI][NI], int grp, int wq,
+                                         int lane, uint8_t* stage) {
+  __attribute__((address_space(3))) uint8_t* st = (__attribute__((address_space(3))) uint8_t*)stage;
+  constexpr int NB = EPI == EPI_STORE_BF16 ? NI : 1;  // output blocks per 32 rows
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    const int row_base = grp * WM + mi * 32;  // first tile row of the block
+    if (row_base >= it.rows) continue;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      // ---- write the block into the staging area
+      if constexpr (EPI == EPI_SWIGLU_MX) {
+        const int cb = it.nt * 4 + wq;  // 32-column MX block of the output row
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const float act = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
+          float amax = fabsf(act);
+#pragma unroll
+          for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+          const uint32_t code = mx_scale_code(amax);
+          *(st + stage_off(row, lane & 31)) = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(act, code));
+          if ((lane & 31) == 0 && row_base + row < it.rows) {
+            const int64_t orow = it.row0 + row_base + row;
+            if (p.c_scale_stage_stride)
+              p.c_scale[(cb >> 2) * p.c_scale_stage_stride + orow * 4 + (cb & 3)] = (uint8_t)code;
+            else
+              p.c_scale[orow * p.c_scale_ld + cb] = (uint8_t)code;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          float v;
+          if constexpr (EPI == EPI_STORE_BF16) v = acc[mi][nb][r];
+          else v = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
+          *(__attribute__((address_space(3))) uint16_t*)(st + stage_off(row, (lane & 31) * 2)) = f32_to_bf16(v);
+        }
+      }
+      // ---- read back 16 bytes per lane and store (rows of 64 bytes, bf16; 32 bytes, e4m3)
+      if constexpr (EPI == EPI_SWIGLU_MX) {
+        const int row = lane >> 1, c = lane & 1;
+        const v4i v = *LDSP(v4i, st + stage_off(row, c * 16));
+        if (row_base + row < it.rows) {
+          const int64_t orow = it.row0 + row_base + row;
+          *(v4i*)((uint8_t*)p.C + orow * p.ldc + (it.nt * 4 + wq) * 32 + c * 16) = v;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int idx = i * 64 + lane;
+          const int row = idx >> 2, c = idx & 3;
+          const v4i v = *LDSP(v4i, st + stage_off(row, c * 16));
+          const int col = EPI == EPI_STORE_BF16 ? it.nt * BN + wq * WN + nb * 32 + c * 8
+                                                : it.nt * (BN / 2) + wq * 32 + c * 8;
+          if (row_base + row < it.rows && col < p.N) {
+            const int64_t orow = it.row0 + row_base + row;
+            *(v4i*)((uint16_t*)p.C + orow * p.ldc + col) = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <bool MX, bool B_KN, int EPI>
+__global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
+  constexpr bool SWIGLU = EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX;
+  constexpr int ESIZE = MX ? 1 : 2;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  int32_t* s_prefix = (int32_t*)(smem + PREFIX_OFF);
+  int32_t* s_rows = (int32_t*)(smem + ROWS_OFF);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = uni(tid >> 6);
+  const int grp = wave >> 2, wq = wave & 3;
+
+  for (int g = tid; g <= p.G; g += THREADS) {
+    s_prefix[g] = p.tile_prefix[g];
+    if (g < p.G) s_rows[g] = (int32_t)p.group_list[g];
+  }
+  __syncthreads();
+  const int total = uni(s_prefix[p.G]) * p.n_tiles;
+  const int nk = p.K * ESIZE / KB;
+  const int grid = (int)gridDim.x;
+  const int L0 = (int)(blockIdx.x & 7) * (grid >> 3) + (int)(blockIdx.x >> 3);
+  if (L0 >= total) return;
+  const int n_items = (total - L0 + grid - 1) / grid;
+  const int nq = n_items * nk;
+  const uint32_t lds0 = uni((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem);
+
+  // copy cursor: item cL, stage ck
+  int cL = L0, ck = 0;
+  Item ci;
+  decode(p, smem, cL, ci);
+  Plan pl;
+  make_plan<MX, B_KN, SWIGLU>(p, ci, wave, lane, pl);
+  auto issue_next = [&](int q) {
+    issue_stage<MX>(pl, ck, lds0 + (uint32_t)((q % S) * SLOT), wave);
+    if (++ck == nk) {
+      if (cL + grid < total) {
+        cL += grid;
+        decode(p, smem, cL, ci);
+        make_plan<MX, B_KN, SWIGLU>(p, ci, wave, lane, pl);
+        ck = 0;
+      } else {
+        ck = nk - 1;  // past the end: repeat the last stage into the free slot
+      }
+    }
+  };
+
+  // compute cursor: item it, stage kk; `live`: this wave's 128 rows hold rows of the item
+  int kL = L0, kk = 0;
+  Item it;
+  decode(p, smem, kL, it);
+  bool live = it.rows > grp * WM;
+  v16f acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+
+  auto finish_stage = [&]() {
+    if (++kk == nk) {
+      if (live) epilogue<EPI>(p, it, acc, grp, wq, lane, smem + EPI_OFF + wave * EPI_BLOCK);
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+      kk = 0;
+      kL += grid;
+      if (kL < total) {
+        decode(p, smem, kL, it);
+        live = it.rows > grp * WM;
+      }
+    }
+  };
+
+  issue_next(0);
+  wait_vm0();
+  barrier();
+  Frags<MX, B_KN> f;
+  if (grp == 0) {
+    for (int q = 0; q < nq; ++q) {
+      issue_next(q + 1);
+      const uint8_t* slot = smem + (q % S) * SLOT;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (live) read_frags<MX, B_KN>(f, slot, h, grp, wq, lane);
+        wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+        if (live) mfmas<MX, B_KN>(f, acc);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      finish_stage();
+      wait_vm0();
+      barrier();
+    }
+  } else {
+    for (int q = 0; q < nq; ++q) {
+      issue_next(q + 1);
+      if (q > 0) {  // half 1 of stage q - 1, read before the barrier
+        if (live) mfmas<MX, B_KN>(f, acc);
+        finish_stage();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* slot = smem + (q % S) * SLOT;
+      if (live) read_frags<MX, B_KN>(f, slot, 0, grp, wq, lane);
+      wait_lgkm0();
+      __builtin_amdgcn_sched_barrier(0);
+      if (live) mfmas<MX, B_KN>(f, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      if (live) read_frags<MX, B_KN>(f, slot, 1, grp, wq, lane);
+      wait_lgkm0();
+      wait_vm0();
+      barrier();
+    }
+    if (live) mfmas<MX, B_KN>(f, acc);
+    finish_stage();
+  }
+  wait_vm0();  // no copy may still write the LDS when the workgroup ends
+}
+
+template <bool MX, bool B_KN, int EPI>
+int launch_pp(const GGParams& p, hipStream_t stream) {
+  auto kern = gg_pp_kernel<MX, B_KN, EPI>;
+  static bool configured = false;
+  if (!configured) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, TOTAL) != hipSuccess)
+      return MI355MOE_ELAUNCH;
+    configured = true;
+  }
+  int grid = (mi355_num_cus() / 8) * 8;
+  if (grid < 8) grid = 8;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), TOTAL, stream, p);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+}  // namespace
+
+bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
+  if (p.k_splits > 1 || p.c_row_index != nullptr) return false;
+  if (p.G > PREFIX_MAX) return false;  // the work list is decoded from LDS
+  if (p.swiglu_limit > 0.0f || p.row_prob != nullptr) return false;  // numerics options: default kernel
+  const int esize = mx ? 1 : 2;
+  if ((int64_t)p.K * esize % KB != 0) return false;
+  if (mx && p.a_scale_stage_stride == 0) return false;  // needs the stage-major activation scales
+  // 32-bit copy offsets: the activations and one group's weights below 4 GiB
+  const int64_t lim = (int64_t)1 << 32;
+  if (p.a_bytes <= 0 || p.a_bytes >= lim || p.b_group_stride >= lim) return false;
+  if (mx && (p.a_scale_stage_stride >= lim || p.b_scale_group_stride >= lim)) return false;
+  if (mx && !b_kn) return false;  // MX weights: the root's col_data / col_scale layout
+  if (mx) return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_MX;
+  return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_BF16;
+}
+
+int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream) {
+  if (!mi355_gg_pp_applies(p, mx, b_kn, epi)) return MI355MOE_EUNSUPPORTED;
+  if (!mx) {
+    if (!b_kn) return epi == EPI_STORE_BF16 ? launch_pp<false, false, EPI_STORE_BF16>(p, stream)
+                                            : launch_pp<false, false, EPI_SWIGLU_BF16>(p, stream);
+    return epi == EPI_STORE_BF16 ? launch_pp<false, true, EPI_STORE_BF16>(p, stream)
+                                 : launch_pp<false, true, EPI_SWIGLU_BF16>(p, stream);
+  }
+  return epi == EPI_STORE_BF16 ? launch_pp<true, true, EPI_STORE_BF16>(p, stream)
+                               : launch_pp<true, true, EPI_SWIGLU_MX>(p, stream);
+}

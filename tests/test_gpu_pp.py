@@ -1,0 +1,87 @@
+"""GPU tests of the 8-wave ping-pong grouped-GEMM configuration (gemm_pp.hip): it runs the same
+MFMAs in the same K order per output element as the 4-wave configuration, so its outputs are
+bit-identical to it; and both match the fp32-accumulate oracle."""
+import contextlib
+
+import pytest
+import torch
+
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+BF16_REL_L2 = 1e-2
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from hyper_multicore_amd import _lib
+    _lib.load()
+    return torch.device("cuda:0")
+
+
+def _seed(s):
+    torch.manual_seed(s)
+    return torch.Generator().manual_seed(s)
+
+
+@contextlib.contextmanager
+def _variant(name):
+    from hyper_multicore_amd import ops
+    prev = ops.set_gemm_variant(name)
+    try:
+        yield
+    finally:
+        ops.set_gemm_variant(prev)
+
+
+COUNTS = [[100, 0, 300, 1, 129], [0, 0, 7], [256] * 4, [3, 40, 0, 513], [1], [600, 255, 257]]
+
+
+@pytest.mark.parametrize("layout", ["EOI", "EIO"])
+@pytest.mark.parametrize("Kd", [256, 2048])
+@pytest.mark.parametrize("counts", COUNTS)
+def test_grouped_gemm_bf16_pp_matches_default(gpu, counts, Kd, layout):
+    from hyper_multicore_amd import ops
+    print(f"[pp] bf16 {layout} K={Kd} counts={counts}", flush=True)
+    g = _seed(sum(counts) + Kd + (layout == "EIO"))
+    G, N = len(counts), 768
+    rows = sum(counts)
+    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)  # [G, K, N]
+    wd = (w if layout == "EIO" else w.transpose(1, 2).contiguous()).to(gpu)
+    gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
+    out_def = ops.grouped_gemm_bf16(x.to(gpu), wd, gl, layout).cpu()
+    with _variant("pp"):
+        out_pp = ops.grouped_gemm_bf16(x.to(gpu), wd, gl, layout).cpu()
+    assert torch.equal(out_pp, out_def)
+    starts = [0, *gl.cpu().tolist()]
+    ref = torch.cat([x[starts[i]:starts[i + 1]].float() @ w[i].float() for i in range(G)]).to(torch.bfloat16)
+    assert orc.rel_l2(out_pp, ref) < 2e-3
+
+
+@pytest.mark.parametrize("layout", ["EOI", "EIO"])
+def test_moe_forward_bf16_pp_matches_default(gpu, layout):
+    from hyper_multicore_amd import ops
+    T, H, I, E, K = 700, 1024, 512, 16, 4
+    print(f"[pp] moe_forward bf16 {layout}", flush=True)
+    g = _seed(T + E + 3)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    probs = torch.rand(T, K, generator=g)
+    probs = probs / probs.sum(1, keepdim=True)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16)
+    if layout == "EOI":
+        w1d, w2d = w1.transpose(1, 2).contiguous().to(gpu), w2.transpose(1, 2).contiguous().to(gpu)
+    else:
+        w1d, w2d = w1.to(gpu), w2.to(gpu)
+    args = dict(num_experts=E, intermediate_size=I, layout=layout)
+    out_def = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d, w2d, **args).cpu()
+    with _variant("pp"):
+        out_pp = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d, w2d, **args).cpu()
+    assert torch.equal(out_pp, out_def)
+    ref = orc.expert_forward_reference(x, ids, probs, w1, w2, layout="EIO")
+    assert orc.rel_l2(out_pp, ref) < BF16_REL_L2
