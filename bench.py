@@ -287,7 +287,7 @@ def gemm_shapes(device, reps: int) -> dict:
     G, rows = 256, 256
     gl = torch.full((G,), rows, dtype=torch.int64, device=device).cumsum(0)
     feats = ops.features()
-    variants = ["default", "pp"]
+    variants = ["default", "w4"]
     out = {}
     for name, N, K in (("gmm1_shape", 4096, 7168), ("gmm2_shape", 7168, 2048)):
         x = torch.randn(G * rows, K, device=device, generator=g).to(torch.bfloat16)
@@ -338,7 +338,7 @@ def main() -> int:
     ap.add_argument("--config", default="dsv3_bf16", choices=sorted(CONFIGS))
     ap.add_argument("--extra", default="all", help="'all', 'none' or comma list of extra configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv", "sp", "sp4", "pp"],
+    ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv", "sp", "sp4", "pp", "w4"],
                     help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
     ap.add_argument("--bf16-layout", default="EOI", choices=["EOI", "EIO"],
                     help="expert-weight layout of the bf16 configs (EIO: the reference module's default)")

@@ -26,7 +26,7 @@ FEATURE_MX_WEIGHT_PREP = 32
 FEATURE_MX_BACKWARD = 64
 FEATURE_DIRECT_GEMM = 128
 FEATURE_SPLIT_ROLES = 256
-GEMM_VARIANT = {"default": 0, "b6": 1, "dv": 2, "sp": 3, "sp4": 4, "pp": 5}
+GEMM_VARIANT = {"default": 0, "b6": 1, "dv": 2, "sp": 3, "sp4": 4, "pp": 5, "w4": 6}
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1}

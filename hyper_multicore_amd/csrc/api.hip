@@ -4,6 +4,7 @@
 #include "common.h"
 #include "gemm.h"
 #include <cmath>
+#include <algorithm>
 #include "../../include/mi355moe.h"
 
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -22,7 +23,7 @@ extern "C" int mi355moe_features(void) {
 }
 
 extern "C" int mi355moe_set_gemm_variant(int variant) {
-  if (variant < MI355_GG_VARIANT_DEFAULT || variant > MI355_GG_VARIANT_PP) return MI355MOE_EUNSUPPORTED;
+  if (variant < MI355_GG_VARIANT_DEFAULT || variant > MI355_GG_VARIANT_W4) return MI355MOE_EUNSUPPORTED;
   if (variant == MI355_GG_VARIANT_DV && !mi355_direct_gemm_enabled()) return MI355MOE_EUNSUPPORTED;
   if ((variant == MI355_GG_VARIANT_SP || variant == MI355_GG_VARIANT_SP4) && !mi355_split_roles_enabled())
     return MI355MOE_EUNSUPPORTED;
@@ -247,10 +248,11 @@ static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
   L.gather = take(R * 4);
   L.tile_prefix = take((E + 1) * 4);
   L.act = take(R * I * (mx ? 1 : 2));
-  L.act_scale = mx ? take(R * mi355_mx_scale_ld(I)) : 0;
+  L.act_scale = mx ? take(std::max(R * mi355_mx_scale_ld(I), R * (I / 32) + 256)) : 0;
   L.y = take(R * H * 2);
   L.xq = mx ? take(T * H) : 0;
-  L.xs = mx ? take(T * mi355_mx_scale_ld(H)) : 0;
+  // MX token scales: [T, ld] for the 4-wave GEMM, or stage-major over the routed rows [H/128][R][4]
+  L.xs = mx ? take(std::max(T * mi355_mx_scale_ld(H), R * (H / 32) + 256)) : 0;
   L.total = off;
   return L;
 }
@@ -327,8 +329,14 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   rc = mi355_plan_tiles(group_list, E, tile_prefix, st, small);
   if (rc) return rc;
   const uint8_t* a1 = (const uint8_t*)a.hidden;
+  // MX on the 8-wave GEMM: activation scales stage-major (one 4-byte copy per row and 128-K stage)
+  const bool pp_mx = mx && !eoi &&
+                     mi355_gg_pp_usable(true, true, H, E, T * H, (int64_t)H * 2 * I) &&
+                     mi355_gg_pp_usable(true, true, I, E, T * K * I, (int64_t)I * H);
   if (mx) {
-    rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), mi355_mx_scale_ld(H), st);
+    // with the 8-wave GEMM the token scales go to each token's routed rows (read in tile order)
+    rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), mi355_mx_scale_ld(H), st,
+                             pp_mx ? T * K * 4 : 0, pp_mx ? mapping : nullptr, K);
     if (rc) return rc;
     a1 = (const uint8_t*)(ws + L.xq);
   }
@@ -360,6 +368,11 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.ldc = I;
   p1.c_scale = mx ? (uint8_t*)(ws + L.act_scale) : nullptr;
   p1.c_scale_ld = mi355_mx_scale_ld(I);
+  if (pp_mx) {
+    p1.a_scale_stage_stride = T * K * 4;
+    p1.a_scale_routed = 1;
+    p1.c_scale_stage_stride = T * K * 4;
+  }
   const bool before_fc2 = (a.numerics_flags & MI355MOE_NUMERICS_PROBS_BEFORE_FC2) != 0;
   p1.swiglu_limit = a.swiglu_limit;
   p1.swiglu_after_silu = (a.numerics_flags & MI355MOE_NUMERICS_CLAMP_AFTER_SILU) != 0;
@@ -375,6 +388,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p2.a_row_div = 1;
   p2.a_scale = mx ? (const uint8_t*)(ws + L.act_scale) : nullptr;
   p2.a_scale_ld = mi355_mx_scale_ld(I);
+  if (pp_mx) p2.a_scale_stage_stride = T * K * 4;
   p2.B = (const uint8_t*)a.w2;
   p2.b_group_stride = (int64_t)I * H * esize;
   p2.b_row_bytes = eoi ? (int64_t)I * esize : (int64_t)H * esize;

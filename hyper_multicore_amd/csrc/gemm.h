@@ -48,11 +48,15 @@ struct GGParams {
   // members keep their kernel-argument offsets.
   int64_t a_bytes;
   // Stage-major MX scales (the 8-wave configuration, gemm_pp.hip): when a_scale_stage_stride (bytes
-  // per 64-K stage) is set, a_scale holds [K/64][source rows][4] - the stage's two codes of each
-  // source row and two pad bytes - so one 4-byte copy per row brings a stage's codes. When
-  // c_scale_stage_stride is set, the MX SwiGLU epilogue writes c_scale in that form.
+  // per 128-K stage) is set, a_scale holds code planes [K/128][4][P] (P = a_scale_stage_stride / 4):
+  // code j of stage s of routed row r at a_scale[s * stride + j * P + r], so a tile's codes of a
+  // stage are four contiguous runs. When c_scale_stage_stride is set, the MX SwiGLU epilogue writes
+  // c_scale in that form. The planes are indexed by routed row (a_scale_routed must be set when
+  // a_row_index gathers the rows), and hold at least 256 bytes past the last row (a tile reads whole
+  // 256-row runs).
   int64_t a_scale_stage_stride;
   int64_t c_scale_stage_stride;
+  int32_t a_scale_routed;
 };
 
 
@@ -97,7 +101,7 @@ int mi355_num_cus();  // CU count of the current device (cached per device)
 // keeps the default's tile height, so tile plans are shared; it answers MI355MOE_EUNSUPPORTED for the
 // paths it does not build, which then run on the default configuration.
 enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1, MI355_GG_VARIANT_DV = 2, MI355_GG_VARIANT_SP = 3,
-       MI355_GG_VARIANT_SP4 = 4, MI355_GG_VARIANT_PP = 5 };
+       MI355_GG_VARIANT_SP4 = 4, MI355_GG_VARIANT_PP = 5, MI355_GG_VARIANT_W4 = 6 };
 int mi355_gg_variant();
 int mi355_gg_set_variant(int variant);  // returns the previous variant
 int mi355_grouped_gemm_variant(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
@@ -110,6 +114,9 @@ int mi355_grouped_gemm_split(const GGParams& p, bool mx, bool b_kn, int epi, hip
 // The 8-wave ping-pong configuration (gemm_pp.hip); MI355MOE_EUNSUPPORTED outside its domain
 // (mi355_gg_pp_applies). Tile plans are those of the 256-row configuration.
 bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi);
+// Whether the 8-wave configuration takes forward GEMMs of these extents under the current variant
+// (the caller then lays the MX activation scales out stage-major).
+bool mi355_gg_pp_usable(bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride);
 int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
 #include "features.h"
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {
@@ -124,8 +131,11 @@ int mi355_permute_rows_enqueue(const uint16_t* x, int64_t slots, int K, int H, c
                                 uint16_t* routed, hipStream_t st);
 int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const float* probs, int64_t T, int K, int H,
                             uint16_t* out, hipStream_t stream);
+// scale_stage_stride > 0 writes the scales as stage-major code planes ([cols/128][4][stride / 4]); with
+// `mapping`, to the routed rows mapping[r * fanout + k] of each row r (negative entries skipped).
 int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
-                        hipStream_t st);
+                        hipStream_t st, int64_t scale_stage_stride = 0, const int32_t* mapping = nullptr,
+                        int fanout = 1);
 // Row stride (bytes) of the internal MX activation-scale buffers: K/32 rounded up to 16 so the
 // GEMM can fetch 16 codes (8 K stages) of a row with one 16-byte load.
 inline int64_t mi355_mx_scale_ld(int64_t k) { return ((k / 32 + 15) / 16) * 16; }

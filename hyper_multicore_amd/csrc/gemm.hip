@@ -86,10 +86,14 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
     return dispatch_gg<GGSmall>(p, mx, b_kn, epi, stream);
   }
   const int variant = mi355_gg_variant();
-  if (variant == MI355_GG_VARIANT_PP) {
+  // the 8-wave configuration first (the default); the 4-wave kernels below for what it does not take
+  if (variant == MI355_GG_VARIANT_DEFAULT || variant == MI355_GG_VARIANT_PP) {
     const int rc = mi355_grouped_gemm_pp(p, mx, b_kn, epi, stream);
     if (rc != MI355MOE_EUNSUPPORTED) return rc;
-  } else if (variant != MI355_GG_VARIANT_DEFAULT) {
+  }
+  // stage-major MX scales are read and written by the 8-wave configuration only
+  if (p.a_scale_stage_stride != 0 || p.c_scale_stage_stride != 0) return MI355MOE_EUNSUPPORTED;
+  if (variant != MI355_GG_VARIANT_DEFAULT && variant != MI355_GG_VARIANT_PP && variant != MI355_GG_VARIANT_W4) {
     const int rc = mi355_grouped_gemm_variant(p, mx, b_kn, epi, stream, variant);
     if (rc != MI355MOE_EUNSUPPORTED) return rc;
   }
@@ -108,6 +112,7 @@ int mi355_gg_variant() {
     if (s != nullptr && strcmp(s, "sp") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP;
     if (s != nullptr && strcmp(s, "sp4") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP4;
     if (s != nullptr && strcmp(s, "pp") == 0) v = MI355_GG_VARIANT_PP;
+    if (s != nullptr && strcmp(s, "w4") == 0) v = MI355_GG_VARIANT_W4;
     g_gg_variant = v;
   }
   return g_gg_variant;

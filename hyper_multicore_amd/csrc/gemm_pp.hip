@@ -30,9 +30,10 @@
 //   N-contiguous weights (EIO bf16, MX col_data): K row k of the stage holds 256 columns; bf16
 //     chunk c at c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows),
 //     read with ds_read_b64_tr_b16 / ds_read_b64_tr_b8;
-//   MX scales of a stage: activation row r's four codes at r * 4 (the stage-major activation-scale
-//     layout [K/128][rows][4], copied one dword per row); weight tile column j's two codes of 64-K
-//     step s at s * 512 + j * 2 (the MX root's col_scale pairs).
+//   MX scales of a stage: code j (0..3) of tile row r at j * 512 + row0 % 4 + r (from the
+//     stage-major code planes of the activation scales: two 256-byte runs per code from the 4-aligned
+//     address at or below the tile's first row); weight tile column j's two codes of 64-K step s at
+//     s * 512 + j * 2 (the MX root's col_scale pairs).
 //
 // Epilogues: bf16 store, SwiGLU -> bf16 and SwiGLU -> MXFP8 requant (a 32-column MX block is the 32
 // lanes of a half-wavefront, so the block maximum is a 5-step lane butterfly); each 32 x 32 block
@@ -49,13 +50,17 @@ constexpr int KB = 128;  // bytes of K per row and stage
 constexpr int S = 2;     // ring slots
 constexpr int WAVES = 8, THREADS = 64 * WAVES;
 constexpr int WM = 128, WN = 64, MI = WM / 32, NI = WN / 32;
-constexpr int A_BYTES = BM * KB, B_BYTES = BN * KB, AS_BYTES = BM * 4, BS_BYTES = 2 * BN * 2;
+// MX scales of a stage: 4 activation code planes of 512 bytes (the 256 tile rows from the 4-aligned
+// row at or below the first one), 2 x 256 weight code pairs
+constexpr int AS_PLANE = 512;
+constexpr int A_BYTES = BM * KB, B_BYTES = BN * KB, AS_BYTES = 4 * AS_PLANE, BS_BYTES = 2 * BN * 2;
 constexpr int B_OFF = A_BYTES, AS_OFF = B_OFF + B_BYTES, BS_OFF = AS_OFF + AS_BYTES;
 constexpr int SLOT = BS_OFF + BS_BYTES;
 constexpr int PREFIX_OFF = S * SLOT;
 constexpr int PREFIX_MAX = 1024;  // groups whose tile prefix and row ends are kept in LDS
 constexpr int ROWS_OFF = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
 constexpr int EPI_BLOCK = 32 * 64;  // a wave's epilogue staging: one 32 x 32 bf16 block
+constexpr int MX_CODES = 32 * 32;   // in it, after a 32 x 32 e4m3 block: the block's 32 scale codes
 constexpr int EPI_OFF = (ROWS_OFF + PREFIX_MAX * 4 + 15) & ~15;
 constexpr int TOTAL = EPI_OFF + WAVES * EPI_BLOCK;
 constexpr int CPW = A_BYTES / 1024 / WAVES;  // 1 KB copies per operand, wave and stage
@@ -144,9 +149,10 @@ __device__ __forceinline__ void decode(const GGParams& p, const uint8_t* smem, i
 struct Plan {
   const uint8_t* a_base;
   const uint8_t* b_base;
-  const uint8_t* s_base;  // MX: activation scales (waves 0-3) or the group's weight scales (waves 4-7)
-  uint32_t ao[CPW], bo[CPW], so;
-  int64_t b_stride, s_stride;
+  const uint8_t* s_base;   // MX: activation code plane run (every wave)
+  const uint8_t* bs_base;  // MX: the group's weight scales (waves 0-3; waves 4-7 repeat them)
+  uint32_t ao[CPW], bo[CPW], so, bso;
+  int64_t b_stride, s_stride, b_scale_stride;
 };
 
 // Activation and EOI-weight copies: copy i (0..31) of a stage covers rows 8 i ..+7, lane l row
@@ -193,27 +199,25 @@ __device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int
   }
   pl.b_stride = B_KN ? (int64_t)(KB / ESIZE) * p.b_row_bytes : KB;
   pl.s_base = pl.a_base;
+  pl.bs_base = pl.a_base;
   pl.so = 0;
+  pl.bso = 0;
   pl.s_stride = 0;
   if constexpr (MX) {
-    if (wave < 4) {
-      const int r = wave * 64 + lane;
-      const int rr = r < it.rows ? r : it.rows - 1;
-      const int64_t routed = it.row0 + rr;
-      const int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
-      pl.s_base = uni_ptr(p.a_scale);
-      pl.so = (uint32_t)(src * 4);
-      pl.s_stride = p.a_scale_stage_stride;
-    } else {
-      // col_scale [G, K/64, Ntot, 2]: wave 4 + 2 s + h copies 64-K step s, tile columns 128 h ..+127
-      const int st = (wave >> 1) & 1;
-      const int j = (wave & 1) * 128 + lane * 2;
-      int wc = tile_col(j, it.nt, p.N, SWIGLU);
-      if (wc > p.Ntot - 2) wc = p.Ntot - 2;
-      pl.s_base = uni_ptr(p.b_scale + (int64_t)it.g * p.b_scale_group_stride);
-      pl.so = (uint32_t)(((int64_t)st * p.Ntot + wc) * 2);
-      pl.s_stride = (int64_t)p.Ntot * 4;  // two 64-K steps per stage
-    }
+    // code plane wave / 2, bytes 256 (wave % 2) + 4 lane from the 4-aligned row at or below row0
+    // (rows past the item read the next rows or the planes' padding)
+    pl.s_base = uni_ptr(p.a_scale + (wave >> 1) * (p.a_scale_stage_stride >> 2) + (it.row0 & ~(int64_t)3));
+    pl.so = (uint32_t)((wave & 1) * 256 + lane * 4);
+    pl.s_stride = p.a_scale_stage_stride;
+    // col_scale [G, K/64, Ntot, 2]: wave w (and w + 4) copies 64-K step (w >> 1) & 1, tile columns
+    // 128 (w & 1) ..+127
+    const int st = (wave >> 1) & 1;
+    const int j = (wave & 1) * 128 + lane * 2;
+    int wc = tile_col(j, it.nt, p.N, SWIGLU);
+    if (wc > p.Ntot - 2) wc = p.Ntot - 2;
+    pl.bs_base = uni_ptr(p.b_scale + (int64_t)it.g * p.b_scale_group_stride);
+    pl.bso = (uint32_t)(((int64_t)st * p.Ntot + wc) * 2);
+    pl.b_scale_stride = (int64_t)p.Ntot * 4;  // two 64-K steps per stage
   }
 }
 
@@ -225,9 +229,11 @@ __device__ __forceinline__ void issue_stage(const Plan& pl, int k, uint32_t slot
   for (int j = 0; j < CPW; ++j) dma16(ab, pl.ao[j], uni(slot + (wave * CPW + j) * 1024));
 #pragma unroll
   for (int j = 0; j < CPW; ++j) dma16(bb, pl.bo[j], uni(slot + B_OFF + (wave * CPW + j) * 1024));
-  if constexpr (MX)
-    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), pl.so,
-         uni(slot + (wave < 4 ? AS_OFF + wave * 256 : BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256)));
+  if constexpr (MX) {
+    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), pl.so, uni(slot + AS_OFF + (wave >> 1) * AS_PLANE + (wave & 1) * 256));
+    dma4(uni_ptr(pl.bs_base + (int64_t)k * pl.b_scale_stride), pl.bso,
+         uni(slot + BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256));
+  }
 }
 
 // LDS offset of 16-byte chunk c of K-contiguous row r
@@ -240,8 +246,10 @@ template <> struct Frags<false, true> { v8bf a[2][MI]; v4s bl[2][NI], bh[2][NI];
 template <> struct Frags<true, false> { v4i al[MI], ah[MI], bl[NI], bh[NI]; int sa[MI], sb[NI]; };
 template <> struct Frags<true, true> { v4i al[MI], ah[MI]; v2i bp[NI][4]; int sa[MI], sb[NI]; };
 
+// a_off: the item's first routed row modulo 4 (the offset of the MX activation code planes)
 template <bool MX, bool B_KN>
-__device__ __forceinline__ void read_frags(Frags<MX, B_KN>& f, const uint8_t* slot, int h, int grp, int wq, int lane) {
+__device__ __forceinline__ void read_frags(Frags<MX, B_KN>& f, const uint8_t* slot, int h, int grp, int wq, int lane,
+                                           int a_off) {
   const uint8_t* As = slot;
   const uint8_t* Bs = slot + B_OFF;
   if constexpr (!MX) {
@@ -281,7 +289,7 @@ __device__ __forceinline__ void read_frags(Frags<MX, B_KN>& f, const uint8_t* sl
       const int c0 = h * 4 + (lane >> 5);
       f.al[mi] = *LDSP(v4i, As + chunk_off(r, c0));
       f.ah[mi] = *LDSP(v4i, As + chunk_off(r, c0 + 2));
-      f.sa[mi] = *LDSP(uint8_t, ASs + r * 4 + h * 2 + (lane >> 5));
+      f.sa[mi] = *LDSP(uint8_t, ASs + (h * 2 + (lane >> 5)) * AS_PLANE + a_off + r);
     }
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
@@ -341,6 +349,21 @@ __device__ __forceinline__ void mfmas(const Frags<MX, B_KN>& f, v16f (&acc)[MI][
   }
 }
 
+// Maximum over the 32 lanes of each half-wavefront: DPP within rows of 16 lanes (xor 1, xor 2, half-row
+// mirror, row mirror), then one lane exchange between the two rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false);
+  return fmaxf(v, __int_as_float(o));
+}
+__device__ __forceinline__ float half_wave_max(float v) {
+  v = dpp_max<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_max<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_max<0x141>(v);  // row_half_mirror
+  v = dpp_max<0x140>(v);  // row_mirror
+  return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+
 __device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
   // the gate and up projections are rounded to bf16 (the GMM1 output), SiLU(gate) * up in fp32
   const float gte = bf16_to_f32(f32_to_bf16(g_acc));
@@ -351,6 +374,8 @@ __device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
 // Staging offset of element (row, byte column cb) of a 32 x 64-byte block: 16-byte chunks swizzled
 // with (row >> 2) & 3, so the two half-wavefronts (rows r and r + 4) write different banks.
 __device__ __forceinline__ int stage_off(int row, int cb) { return row * 64 + ((((cb >> 4) ^ (row >> 2)) & 3) << 4) + (cb & 15); }
+// The same for a 32 x 32-byte block (e4m3)
+__device__ __forceinline__ int stage_off8(int row, int cb) { return row * 32 + ((((cb >> 4) ^ (row >> 2)) & 1) << 4) + (cb & 15); }
 
 // acc[mi][ni][r] holds row grp * 128 + mi * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
 // wq * 64 + ni * 32 + lane % 32 of the tile. Each 32 x 32 output block goes through the wave's LDS
@@ -368,23 +393,14 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
     for (int nb = 0; nb < NB; ++nb) {
       // ---- write the block into the staging area
       if constexpr (EPI == EPI_SWIGLU_MX) {
-        const int cb = it.nt * 4 + wq;  // 32-column MX block of the output row
+        // e4m3 block in rows 0..31 of the staging block (32 bytes each), the 32 codes after it
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
           const float act = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
-          float amax = fabsf(act);
-#pragma unroll
-          for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-          const uint32_t code = mx_scale_code(amax);
-          *(st + stage_off(row, lane & 31)) = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(act, code));
-          if ((lane & 31) == 0 && row_base + row < it.rows) {
-            const int64_t orow = it.row0 + row_base + row;
-            if (p.c_scale_stage_stride)
-              p.c_scale[(cb >> 2) * p.c_scale_stage_stride + orow * 4 + (cb & 3)] = (uint8_t)code;
-            else
-              p.c_scale[orow * p.c_scale_ld + cb] = (uint8_t)code;
-          }
+          const uint32_t code = mx_scale_code(half_wave_max(fabsf(act)));
+          *(st + stage_off8(row, lane & 31)) = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(act, code));
+          if ((lane & 31) == 0) *(st + MX_CODES + row) = (uint8_t)code;
         }
       } else {
 #pragma unroll
@@ -399,10 +415,28 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
       // ---- read back 16 bytes per lane and store (rows of 64 bytes, bf16; 32 bytes, e4m3)
       if constexpr (EPI == EPI_SWIGLU_MX) {
         const int row = lane >> 1, c = lane & 1;
-        const v4i v = *LDSP(v4i, st + stage_off(row, c * 16));
-        if (row_base + row < it.rows) {
+        const v4i v = *LDSP(v4i, st + stage_off8(row, c * 16));
+        const int cb = it.nt * 4 + wq;  // 32-column MX block of the output rows
+        const int nrows = it.rows - row_base;  // valid rows of this 32-row block (>= 1)
+        if (row < nrows) {
           const int64_t orow = it.row0 + row_base + row;
-          *(v4i*)((uint8_t*)p.C + orow * p.ldc + (it.nt * 4 + wq) * 32 + c * 16) = v;
+          *(v4i*)((uint8_t*)p.C + orow * p.ldc + cb * 32 + c * 16) = v;
+        }
+        if (p.c_scale_stage_stride) {
+          // code plane cb % 4 of stage cb / 4: 32 consecutive rows, 4 per lane (bytes at the end)
+          uint8_t* plane = p.c_scale + (cb >> 2) * p.c_scale_stage_stride + (cb & 3) * (p.c_scale_stage_stride >> 2) +
+                           it.row0 + row_base;
+          if (lane < 8) {
+            const uint32_t w4 = *LDSP(uint32_t, st + MX_CODES + lane * 4);
+            if (lane * 4 + 4 <= nrows) {
+              *(uint32_t*)(plane + lane * 4) = w4;
+            } else {
+              for (int i = 0; i < 4; ++i)
+                if (lane * 4 + i < nrows) plane[lane * 4 + i] = (uint8_t)(w4 >> (8 * i));
+            }
+          }
+        } else if (lane < 32 && lane < nrows) {
+          p.c_scale[(it.row0 + row_base + lane) * p.c_scale_ld + cb] = *(st + MX_CODES + lane);
         }
       } else {
 #pragma unroll
@@ -509,7 +543,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       const uint8_t* slot = smem + (q % S) * SLOT;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        if (live) read_frags<MX, B_KN>(f, slot, h, grp, wq, lane);
+        if (live) read_frags<MX, B_KN>(f, slot, h, grp, wq, lane, (int)(it.row0 & 3));
         wait_lgkm0();
         __builtin_amdgcn_sched_barrier(0);
         if (live) mfmas<MX, B_KN>(f, acc);
@@ -528,12 +562,12 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* slot = smem + (q % S) * SLOT;
-      if (live) read_frags<MX, B_KN>(f, slot, 0, grp, wq, lane);
+      if (live) read_frags<MX, B_KN>(f, slot, 0, grp, wq, lane, (int)(it.row0 & 3));
       wait_lgkm0();
       __builtin_amdgcn_sched_barrier(0);
       if (live) mfmas<MX, B_KN>(f, acc);
       __builtin_amdgcn_sched_barrier(0);
-      if (live) read_frags<MX, B_KN>(f, slot, 1, grp, wq, lane);
+      if (live) read_frags<MX, B_KN>(f, slot, 1, grp, wq, lane, (int)(it.row0 & 3));
       wait_lgkm0();
       wait_vm0();
       barrier();
@@ -573,8 +607,18 @@ bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
   if (p.a_bytes <= 0 || p.a_bytes >= lim || p.b_group_stride >= lim) return false;
   if (mx && (p.a_scale_stage_stride >= lim || p.b_scale_group_stride >= lim)) return false;
   if (mx && !b_kn) return false;  // MX weights: the root's col_data / col_scale layout
+  if (mx && p.a_row_index != nullptr && !p.a_scale_routed) return false;  // code planes by routed row
   if (mx) return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_MX;
   return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_BF16;
+}
+
+bool mi355_gg_pp_usable(bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride) {
+  const int v = mi355_gg_variant();
+  if (v != MI355_GG_VARIANT_DEFAULT && v != MI355_GG_VARIANT_PP) return false;
+  if (mx && !b_kn) return false;
+  if (G > PREFIX_MAX || K * (mx ? 1 : 2) % KB != 0) return false;
+  const int64_t lim = (int64_t)1 << 32;
+  return a_bytes > 0 && a_bytes < lim && b_group_stride > 0 && b_group_stride < lim;
 }
 
 int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream) {

@@ -10,8 +10,15 @@
 #include "../../include/mi355moe.h"
 
 // One thread per 32-element block of a row.
+// scale_stage_stride = 0: scales [rows, scale_ld]; otherwise stage-major code planes
+// [cols/128][4][P] (P = scale_stage_stride / 4 rows per plane; code j of a 128-column stage of row r
+// at plane j, the 8-wave GEMM's activation-scale layout). With `mapping` (slot -> routed row, `fanout`
+// slots per row) the codes of row r go to the routed rows mapping[r * fanout + k] instead, so a GEMM
+// over routed rows reads them in order.
 __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint16_t* x, int64_t rows, int cols,
-                                                            uint8_t* q, uint8_t* scale, int64_t scale_ld) {
+                                                            uint8_t* q, uint8_t* scale, int64_t scale_ld,
+                                                            int64_t scale_stage_stride, const int32_t* mapping,
+                                                            int fanout) {
   const int nb = cols / 32;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= rows * nb) return;
@@ -44,7 +51,19 @@ __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint16_t* x, i
   uint4* dst = (uint4*)(q + r * cols + b * 32);
   dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
   dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
-  scale[r * scale_ld + b] = (uint8_t)code;
+  if (scale_stage_stride) {
+    uint8_t* plane = scale + (b >> 2) * scale_stage_stride + (b & 3) * (scale_stage_stride >> 2);
+    if (mapping != nullptr) {
+      for (int k = 0; k < fanout; ++k) {
+        const int32_t rr = mapping[r * fanout + k];
+        if (rr >= 0) plane[rr] = (uint8_t)code;
+      }
+    } else {
+      plane[r] = (uint8_t)code;
+    }
+  } else {
+    scale[r * scale_ld + b] = (uint8_t)code;
+  }
 }
 
 // One thread per (group, 32-row block along K, column).
@@ -73,11 +92,11 @@ __global__ __launch_bounds__(256) void mx_quant_cols_kernel(const uint16_t* w, i
 }
 
 int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
-                        hipStream_t st) {
+                        hipStream_t st, int64_t scale_stage_stride, const int32_t* mapping, int fanout) {
   int64_t n = rows * (cols / 32);
   if (n == 0) return MI355MOE_OK;
   hipLaunchKernelGGL(mx_quant_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, rows, cols, q,
-                     scale, scale_ld);
+                     scale, scale_ld, scale_stage_stride, mapping, fanout);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 

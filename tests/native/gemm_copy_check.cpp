@@ -1585,6 +1585,10 @@ static int sim_dispatch(const GGParams& p, bool mx, bool b_kn, int epi) {
 }
 
 // Library internals replaced by the simulation (same signatures as gemm.h)
+// The checker replays the 4-wave kernels' copy plans: the library's moe_forward is steered onto them
+// (the 8-wave configuration has its own GPU bit-identity tests against them).
+bool mi355_gg_pp_usable(bool, bool, int64_t, int, int64_t, int64_t) { return false; }
+
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t, bool small) {
   // the dispatcher's choice of the numerics epilogue (gemm.hip, mi355_grouped_gemm)
   if (epi == EPI_SWIGLU_BF16_NUM) return MI355MOE_EINVAL;

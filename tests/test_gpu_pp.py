@@ -1,6 +1,6 @@
-"""GPU tests of the 8-wave ping-pong grouped-GEMM configuration (gemm_pp.hip): it runs the same
-MFMAs in the same K order per output element as the 4-wave configuration, so its outputs are
-bit-identical to it; and both match the fp32-accumulate oracle."""
+"""GPU tests of the 8-wave ping-pong grouped-GEMM configuration (gemm_pp.hip, the default): it runs
+the same MFMAs in the same K order per output element as the 4-wave configuration (variant "w4"),
+so its outputs are bit-identical to it; and both match the fp32-accumulate oracle."""
 import contextlib
 
 import pytest
@@ -53,7 +53,8 @@ def test_grouped_gemm_bf16_pp_matches_default(gpu, counts, Kd, layout):
     w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)  # [G, K, N]
     wd = (w if layout == "EIO" else w.transpose(1, 2).contiguous()).to(gpu)
     gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
-    out_def = ops.grouped_gemm_bf16(x.to(gpu), wd, gl, layout).cpu()
+    with _variant("w4"):
+        out_def = ops.grouped_gemm_bf16(x.to(gpu), wd, gl, layout).cpu()
     with _variant("pp"):
         out_pp = ops.grouped_gemm_bf16(x.to(gpu), wd, gl, layout).cpu()
     assert torch.equal(out_pp, out_def)
@@ -79,9 +80,67 @@ def test_moe_forward_bf16_pp_matches_default(gpu, layout):
     else:
         w1d, w2d = w1.to(gpu), w2.to(gpu)
     args = dict(num_experts=E, intermediate_size=I, layout=layout)
-    out_def = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d, w2d, **args).cpu()
+    with _variant("w4"):
+        out_def = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d, w2d, **args).cpu()
     with _variant("pp"):
         out_pp = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d, w2d, **args).cpu()
     assert torch.equal(out_pp, out_def)
     ref = orc.expert_forward_reference(x, ids, probs, w1, w2, layout="EIO")
     assert orc.rel_l2(out_pp, ref) < BF16_REL_L2
+
+
+@pytest.mark.parametrize("T,H,I,E,K", [(700, 1024, 512, 16, 4), (64, 1024, 256, 64, 8), (300, 2048, 384, 8, 2)])
+def test_moe_forward_mxfp8_pp_matches_w4(gpu, T, H, I, E, K):
+    """MXFP8 forward on the 8-wave GEMMs (stage-major activation scales, col_data / col_scale weights)
+    equals the 4-wave path bit for bit, and the MX-emulating oracle to the MX bar."""
+    from hyper_multicore_amd import ops
+    print(f"[pp] moe_forward mxfp8 T={T} H={H} I={I} E={E} K={K}", flush=True)
+    g = _seed(T + E + 9)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    probs = torch.rand(T, K, generator=g)
+    probs = probs / probs.sum(1, keepdim=True)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16)
+    d1, s1 = ops.mx_quantize_cols(w1.to(gpu))
+    d2, s2 = ops.mx_quantize_cols(w2.to(gpu))
+    args = dict(num_experts=E, intermediate_size=I, precision="mxfp8", w1_scale=s1, w2_scale=s2)
+    ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8))
+    with _variant("w4"):
+        out_w4 = ops.moe_forward(*ins, **args).cpu()
+    with _variant("pp"):
+        out_pp = ops.moe_forward(*ins, **args).cpu()
+    assert torch.equal(out_pp, out_w4)
+    ref = orc.expert_forward_reference(x, ids, probs, d1.cpu().view(torch.uint8), d2.cpu().view(torch.uint8),
+                                       precision="mxfp8", w1_scale=s1.cpu(), w2_scale=s2.cpu())
+    assert orc.rel_l2(out_pp, ref) < 3e-2
+
+
+@pytest.mark.parametrize("precision", ["bf16", "mxfp8"])
+def test_moe_forward_decode_shape_pp(gpu, precision):
+    """Decode shape (a few routed rows per expert, many empty experts) on the 8-wave GEMMs."""
+    from hyper_multicore_amd import ops
+    T, H, I, E, K = 16, 2048, 512, 64, 8
+    g = _seed(77 + (precision == "mxfp8"))
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    probs = torch.rand(T, K, generator=g)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16)
+    if precision == "mxfp8":
+        d1, s1 = ops.mx_quantize_cols(w1.to(gpu))
+        d2, s2 = ops.mx_quantize_cols(w2.to(gpu))
+        args = dict(num_experts=E, intermediate_size=I, precision="mxfp8", w1_scale=s1, w2_scale=s2)
+        wts = (d1.view(torch.uint8), d2.view(torch.uint8))
+    else:
+        args = dict(num_experts=E, intermediate_size=I)
+        wts = (w1.to(gpu), w2.to(gpu))
+    ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), *wts)
+    with _variant("w4"):
+        out_w4 = ops.moe_forward(*ins, **args).cpu()
+    with _variant("pp"):
+        out_pp = ops.moe_forward(*ins, **args).cpu()
+    assert torch.equal(out_pp, out_w4)
+    if precision == "bf16":
+        ref = orc.expert_forward_reference(x, ids, probs, w1, w2, layout="EIO")
+        assert orc.rel_l2(out_pp, ref) < BF16_REL_L2
