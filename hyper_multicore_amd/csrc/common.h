@@ -18,10 +18,9 @@ typedef __attribute__((ext_vector_type(8))) __bf16 v8bf;
 // ---- bf16 <-> f32 (round to nearest even, NaN kept quiet) -------------------------------
 MI355_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 MI355_DEV uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : r);  // select, no branch
 }
 
 // ---- OCP MX e4m3fn / e8m0 --------------------------------------------------------------
@@ -43,15 +42,24 @@ MI355_DEV uint32_t f32_to_e4m3(float v) {
   }
   return sign | code;
 }
-// Shared-exponent of a 32-element block (OCP MX v1.0): floor(log2(amax)) - 8, as e8m0 code.
+// Shared exponent of a 32-element block as e8m0 code: the smallest e with amax <= 448 * 2^e (the
+// reference's MX scale algorithm 1, so no element saturates). With amax = M * 2^E, M in [1, 2),
+// 448 * 2^(E-8) = 1.75 * 2^E: e = E - 8 for M <= 1.75 (mantissa bits <= 0x600000), E - 7 above.
+// Clamped to [-127, 127]; all-zero (and fp32-subnormal) blocks get 2^-127.
 MI355_DEV uint32_t mx_scale_code(float amax) {
-  if (!(amax > 0.0f)) return 0u;  // all-zero block: any scale; use 2^-127
-  int32_t e = (int32_t)((__float_as_uint(amax) >> 23) & 0xff) - 127;  // floor(log2) for normals
-  if (e == -127) e = -127;                                               // fp32 denormal amax
-  int32_t s = e - 8;
+  if (!(amax > 0.0f)) return 0u;
+  const uint32_t bits = __float_as_uint(amax);
+  const int32_t E = (int32_t)((bits >> 23) & 0xff) - 127;
+  if (E == -127) return 0u;
+  int32_t s = E - 8 + ((bits & 0x7fffffu) > 0x600000u ? 1 : 0);
   if (s < -127) s = -127;
   if (s > 127) s = 127;
   return (uint32_t)(s + 127);
+}
+// e4m3fn code of v with |v| <= 448 (an element scaled by mx_scale_code's exponent): the hardware
+// conversion (round to nearest even), equal to f32_to_e4m3 on that range.
+MI355_DEV uint32_t f32_to_e4m3_inrange(float v) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xffu;
 }
 // Multiply by 2^-(code-127) exactly (power-of-two scaling).
 MI355_DEV float mx_apply_inv_scale(float v, uint32_t code) { return ldexpf(v, 127 - (int)code); }

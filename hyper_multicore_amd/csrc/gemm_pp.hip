@@ -35,9 +35,9 @@
 //     address at or below the tile's first row); weight tile column j's two codes of 64-K step s at
 //     s * 512 + j * 2 (the MX root's col_scale pairs).
 //
-// Epilogues: bf16 store, SwiGLU -> bf16 and SwiGLU -> MXFP8 requant (a 32-column MX block is the 32
-// lanes of a half-wavefront, so the block maximum is a 5-step lane butterfly); each 32 x 32 block
-// goes through a wave-private LDS staging block so the global stores are 16 bytes per lane. For SwiGLU the 64 weight columns of a wave are 32 gate then
+// Epilogues: bf16 store, SwiGLU -> bf16 (each 32 x 32 block through a wave-private LDS staging block,
+// so the global stores are 16 bytes per lane) and SwiGLU -> MXFP8 requant (fp32 values staged 16 rows
+// at a time, then 4 lanes per 32-element MX block: block maximum by two DPP steps, 8-byte stores). For SwiGLU the 64 weight columns of a wave are 32 gate then
 // the matching 32 up columns, so a lane holds gate and up of the same output element.
 #include "common.h"
 #include "gemm.h"
@@ -60,7 +60,6 @@ constexpr int PREFIX_OFF = S * SLOT;
 constexpr int PREFIX_MAX = 1024;  // groups whose tile prefix and row ends are kept in LDS
 constexpr int ROWS_OFF = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
 constexpr int EPI_BLOCK = 32 * 64;  // a wave's epilogue staging: one 32 x 32 bf16 block
-constexpr int MX_CODES = 32 * 32;   // in it, after a 32 x 32 e4m3 block: the block's 32 scale codes
 constexpr int EPI_OFF = (ROWS_OFF + PREFIX_MAX * 4 + 15) & ~15;
 constexpr int TOTAL = EPI_OFF + WAVES * EPI_BLOCK;
 constexpr int CPW = A_BYTES / 1024 / WAVES;  // 1 KB copies per operand, wave and stage
@@ -349,19 +348,11 @@ __device__ __forceinline__ void mfmas(const Frags<MX, B_KN>& f, v16f (&acc)[MI][
   }
 }
 
-// Maximum over the 32 lanes of each half-wavefront: DPP within rows of 16 lanes (xor 1, xor 2, half-row
-// mirror, row mirror), then one lane exchange between the two rows.
+// max(v, v of the lane selected by the DPP control CTRL)
 template <int CTRL>
 __device__ __forceinline__ float dpp_max(float v) {
   const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false);
   return fmaxf(v, __int_as_float(o));
-}
-__device__ __forceinline__ float half_wave_max(float v) {
-  v = dpp_max<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v = dpp_max<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v = dpp_max<0x141>(v);  // row_half_mirror
-  v = dpp_max<0x140>(v);  // row_mirror
-  return fmaxf(v, __shfl_xor(v, 16, 64));
 }
 
 __device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
@@ -374,15 +365,17 @@ __device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
 // Staging offset of element (row, byte column cb) of a 32 x 64-byte block: 16-byte chunks swizzled
 // with (row >> 2) & 3, so the two half-wavefronts (rows r and r + 4) write different banks.
 __device__ __forceinline__ int stage_off(int row, int cb) { return row * 64 + ((((cb >> 4) ^ (row >> 2)) & 3) << 4) + (cb & 15); }
-// The same for a 32 x 32-byte block (e4m3)
-__device__ __forceinline__ int stage_off8(int row, int cb) { return row * 32 + ((((cb >> 4) ^ (row >> 2)) & 1) << 4) + (cb & 15); }
 
 // acc[mi][ni][r] holds row grp * 128 + mi * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
 // wq * 64 + ni * 32 + lane % 32 of the tile. Each 32 x 32 output block goes through the wave's LDS
 // staging block (LDS operations of a wave complete in order) and is written with 16-byte stores.
 template <int EPI>
 __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[MI][NI], int grp, int wq,
-                                         int lane, uint8_t* stage) {
+                                         int lane_in, uint8_t* stage) {
+  // the lane index through an empty asm: the staging offsets below are recomputed here instead of
+  // being hoisted out of the K loop (where they would take registers for the whole loop)
+  int lane = lane_in;
+  asm volatile("" : "+v"(lane));
   __attribute__((address_space(3))) uint8_t* st = (__attribute__((address_space(3))) uint8_t*)stage;
   constexpr int NB = EPI == EPI_STORE_BF16 ? NI : 1;  // output blocks per 32 rows
 #pragma unroll
@@ -393,14 +386,45 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
     for (int nb = 0; nb < NB; ++nb) {
       // ---- write the block into the staging area
       if constexpr (EPI == EPI_SWIGLU_MX) {
-        // e4m3 block in rows 0..31 of the staging block (32 bytes each), the 32 codes after it
+        // Two halves of 16 rows: the fp32 SwiGLU values go to the staging block (16 rows x 128 bytes),
+        // then 4 lanes per row quantise 8 values each (block maximum over the 4 lanes by DPP) and
+        // write 8 e4m3 bytes; the row's scale code goes to its code plane.
+        const int cb = it.nt * 4 + wq;  // 32-column MX block of the output rows
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          const float act = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
-          const uint32_t code = mx_scale_code(half_wave_max(fabsf(act)));
-          *(st + stage_off8(row, lane & 31)) = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(act, code));
-          if ((lane & 31) == 0) *(st + MX_CODES + row) = (uint8_t)code;
+        for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+          for (int r = 8 * hh; r < 8 * hh + 8; ++r) {
+            const int lrow = 8 * ((r >> 2) & 1) + 4 * (lane >> 5) + (r & 3);  // row within the half
+            const float act = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
+            *(__attribute__((address_space(3))) float*)(st + lrow * 128 + ((((lane & 31) >> 2) ^ (lrow & 7)) << 4) +
+                                                       (lane & 3) * 4) = act;
+          }
+          const int lrow = lane >> 2, part = lane & 3;  // 8 values: columns 8 part ..+7 of row lrow
+          const v4f v0 = *LDSP(v4f, st + lrow * 128 + (((2 * part) ^ (lrow & 7)) << 4));
+          const v4f v1 = *LDSP(v4f, st + lrow * 128 + (((2 * part + 1) ^ (lrow & 7)) << 4));
+          float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
+                             fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
+          amax = dpp_max<0xB1>(amax);  // quad_perm [1, 0, 3, 2]
+          amax = dpp_max<0x4E>(amax);  // quad_perm [2, 3, 0, 1]
+          const uint32_t code = mx_scale_code(amax);
+          uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            w0 |= f32_to_e4m3_inrange(mx_apply_inv_scale(v0[i], code)) << (8 * i);
+            w1 |= f32_to_e4m3_inrange(mx_apply_inv_scale(v1[i], code)) << (8 * i);
+          }
+          const int row = hh * 16 + lrow;  // row within the 32-row block
+          if (row_base + row < it.rows) {
+            const int64_t orow = it.row0 + row_base + row;
+            *(v2i*)((uint8_t*)p.C + orow * p.ldc + cb * 32 + part * 8) = v2i{(int)w0, (int)w1};
+            if (part == 0) {
+              if (p.c_scale_stage_stride)
+                p.c_scale[(cb >> 2) * p.c_scale_stage_stride + (cb & 3) * (p.c_scale_stage_stride >> 2) + orow] =
+                    (uint8_t)code;
+              else
+                p.c_scale[orow * p.c_scale_ld + cb] = (uint8_t)code;
+            }
+          }
         }
       } else {
 #pragma unroll
@@ -414,30 +438,7 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
       }
       // ---- read back 16 bytes per lane and store (rows of 64 bytes, bf16; 32 bytes, e4m3)
       if constexpr (EPI == EPI_SWIGLU_MX) {
-        const int row = lane >> 1, c = lane & 1;
-        const v4i v = *LDSP(v4i, st + stage_off8(row, c * 16));
-        const int cb = it.nt * 4 + wq;  // 32-column MX block of the output rows
-        const int nrows = it.rows - row_base;  // valid rows of this 32-row block (>= 1)
-        if (row < nrows) {
-          const int64_t orow = it.row0 + row_base + row;
-          *(v4i*)((uint8_t*)p.C + orow * p.ldc + cb * 32 + c * 16) = v;
-        }
-        if (p.c_scale_stage_stride) {
-          // code plane cb % 4 of stage cb / 4: 32 consecutive rows, 4 per lane (bytes at the end)
-          uint8_t* plane = p.c_scale + (cb >> 2) * p.c_scale_stage_stride + (cb & 3) * (p.c_scale_stage_stride >> 2) +
-                           it.row0 + row_base;
-          if (lane < 8) {
-            const uint32_t w4 = *LDSP(uint32_t, st + MX_CODES + lane * 4);
-            if (lane * 4 + 4 <= nrows) {
-              *(uint32_t*)(plane + lane * 4) = w4;
-            } else {
-              for (int i = 0; i < 4; ++i)
-                if (lane * 4 + i < nrows) plane[lane * 4 + i] = (uint8_t)(w4 >> (8 * i));
-            }
-          }
-        } else if (lane < 32 && lane < nrows) {
-          p.c_scale[(it.row0 + row_base + lane) * p.c_scale_ld + cb] = *(st + MX_CODES + lane);
-        }
+        // written above
       } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {

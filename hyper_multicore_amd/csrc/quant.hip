@@ -43,10 +43,10 @@ __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint16_t* x, i
   uint32_t out[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    out[i] = f32_to_e4m3(mx_apply_inv_scale(v[4 * i], code)) |
-             (f32_to_e4m3(mx_apply_inv_scale(v[4 * i + 1], code)) << 8) |
-             (f32_to_e4m3(mx_apply_inv_scale(v[4 * i + 2], code)) << 16) |
-             (f32_to_e4m3(mx_apply_inv_scale(v[4 * i + 3], code)) << 24);
+    out[i] = f32_to_e4m3_inrange(mx_apply_inv_scale(v[4 * i], code)) |
+             (f32_to_e4m3_inrange(mx_apply_inv_scale(v[4 * i + 1], code)) << 8) |
+             (f32_to_e4m3_inrange(mx_apply_inv_scale(v[4 * i + 2], code)) << 16) |
+             (f32_to_e4m3_inrange(mx_apply_inv_scale(v[4 * i + 3], code)) << 24);
   }
   uint4* dst = (uint4*)(q + r * cols + b * 32);
   dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void mx_quant_cols_kernel(const uint16_t* w, i
   uint32_t code = mx_scale_code(amax);
   uint8_t* dst = col_data + ((int64_t)g * K + kb * 32) * N + n;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) dst[(int64_t)i * N] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+  for (int i = 0; i < 32; ++i) dst[(int64_t)i * N] = (uint8_t)f32_to_e4m3_inrange(mx_apply_inv_scale(v[i], code));
   col_scale[(((int64_t)g * (K / 64) + kb / 2) * N + n) * 2 + (kb & 1)] = (uint8_t)code;
 }
 
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void mx_quant_weight_dual_kernel(const uint16_
     const uint32_t code = mx_scale_code(amax);
     if (live) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) col_data[base + (int64_t)i * N + n] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+      for (int i = 0; i < 32; ++i) col_data[base + (int64_t)i * N + n] = (uint8_t)f32_to_e4m3_inrange(mx_apply_inv_scale(v[i], code));
       col_scale[(((int64_t)g * (M / 64) + mb / 2) * N + n) * 2 + (mb & 1)] = (uint8_t)code;
     }
   }
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void mx_quant_weight_dual_kernel(const uint16_
       for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
       const uint32_t code = mx_scale_code(a);
       if (live) {
-        row_data[base + (int64_t)i * N + n] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+        row_data[base + (int64_t)i * N + n] = (uint8_t)f32_to_e4m3_inrange(mx_apply_inv_scale(v[i], code));
         if ((threadIdx.x & 31) == 0) row_scale[((int64_t)g * M + mb * 32 + i) * (N / 32) + n / 32] = (uint8_t)code;
       }
     }
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void mx_quant_grouped_kernel(MxGroupedQuant q)
     const uint32_t code = mx_scale_code(amax);
 #pragma unroll
     for (int i = 0; i < 32; ++i)
-      if (i < nrows) q.col_data[(r0 + i) * q.C + c] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+      if (i < nrows) q.col_data[(r0 + i) * q.C + c] = (uint8_t)f32_to_e4m3_inrange(mx_apply_inv_scale(v[i], code));
     uint8_t* pair = q.col_scale + ((start / 64 + g + b / 2) * q.C + c) * 2;
     pair[b & 1] = (uint8_t)code;
     if (!(b & 1) && 32 * (int64_t)(b + 1) >= n) pair[1] = 0;  // the pair's second block lies past the group
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(256) void mx_quant_grouped_kernel(MxGroupedQuant q)
       for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
       const uint32_t code = mx_scale_code(a);
       if (live && i < nrows) {
-        q.row_data[(r0 + i) * q.C + c] = (uint8_t)f32_to_e4m3(mx_apply_inv_scale(v[i], code));
+        q.row_data[(r0 + i) * q.C + c] = (uint8_t)f32_to_e4m3_inrange(mx_apply_inv_scale(v[i], code));
         if ((threadIdx.x & 31) == 0) q.row_scale[(r0 + i) * q.row_scale_ld + c / 32] = (uint8_t)code;
       }
     }

@@ -254,18 +254,37 @@ def unpermute_grad_reference(values: torch.Tensor, grad_out: torch.Tensor, mappi
 
 
 # ------------------------------------------------------------------------------------------------
-# OCP MX (e4m3fn + e8m0 per 32)
+# MX (e4m3fn + e8m0 per 32)
 # ------------------------------------------------------------------------------------------------
-def mx_quantize(x: torch.Tensor, dim: int = -1):
-    """Quantise fp32/bf16 x in 32-element blocks along ``dim``: scale exponent
-    floor(log2(amax)) - 8 (OCP MX v1.0), elements cast with torch's float8_e4m3fn RNE after
-    saturation to +-448. Returns (e4m3 codes uint8 like x, e8m0 codes uint8 with dim/32)."""
+def mx_shared_exponent(amax: torch.Tensor, scale_alg: int = 1) -> torch.Tensor:
+    """e8m0 exponent of 32-element blocks with maxima ``amax`` (int32, clamped to [-127, 127]; -127 for
+    all-zero blocks).
+
+    scale_alg 1 (the reference's MX quantisers: dual_axis_mxfp8_worker.h:44 sets ``tiling.scaleAlg = 1``
+    and instantiates the SwiGLU quantiser with the same algorithm, :79-80; the weight roots use
+    ``npu_dynamic_mx_quant_with_dual_axis(scale_alg=1)``, _replay_mega_moe_arch35.py:55): the smallest
+    e with amax <= 448 * 2^e, i.e. ceil(log2(amax / 448)), so no element saturates. With amax = M * 2^E,
+    M in [1, 2): 448 * 2^(E-8) = 1.75 * 2^E, hence e = E - 8 for M <= 1.75 and E - 7 above.
+    scale_alg 0 (OCP MX v1.0): floor(log2(amax)) - 8 = E - 8; elements above 448 * 2^e saturate."""
+    m, exp = torch.frexp(amax)  # amax = m * 2^exp, m in [0.5, 1): E = exp - 1, M = 2 m
+    e = exp - 1 - 8
+    if scale_alg == 1:
+        e = e + (m > 0.875).to(e.dtype)
+    elif scale_alg != 0:
+        raise ValueError(f"unknown MX scale algorithm {scale_alg}")
+    return torch.where(amax > 0, e, torch.full_like(e, -127)).clamp(-127, 127)
+
+
+def mx_quantize(x: torch.Tensor, dim: int = -1, scale_alg: int = 1):
+    """Quantise fp32/bf16 x in 32-element blocks along ``dim``: shared exponent from
+    :func:`mx_shared_exponent` (scale algorithm 1 by default, as the reference), elements cast with
+    torch's float8_e4m3fn RNE after saturation to +-448 (which only scale algorithm 0 reaches).
+    Returns (e4m3 codes uint8 like x, e8m0 codes uint8 with dim/32)."""
     x = x.float().movedim(dim, -1)
     shape = x.shape
     blocks = x.reshape(*shape[:-1], shape[-1] // 32, 32)
     amax = blocks.abs().amax(dim=-1)
-    _, exp = torch.frexp(amax)  # amax = m * 2^exp, m in [0.5, 1)
-    shared = torch.where(amax > 0, exp - 1 - 8, torch.full_like(exp, -127)).clamp(-127, 127)
+    shared = mx_shared_exponent(amax, scale_alg)
     scaled = torch.ldexp(blocks, (-shared).unsqueeze(-1).to(torch.float32))
     scaled = scaled.clamp(-448.0, 448.0)
     q = scaled.to(torch.float8_e4m3fn).view(torch.uint8).reshape(shape)
@@ -290,9 +309,9 @@ def col_scale_to_blocks(col_scale: torch.Tensor) -> torch.Tensor:
     return col_scale.permute(0, 1, 3, 2).reshape(G, K64 * 2, N)
 
 
-def mx_quantize_weight_cols(w: torch.Tensor):
+def mx_quantize_weight_cols(w: torch.Tensor, scale_alg: int = 1):
     """bf16 [G, K, N] -> (col_data codes uint8 [G,K,N], col_scale uint8 [G,K/64,N,2])."""
-    q, codes = mx_quantize(w.float(), dim=1)  # codes [G, K/32, N]
+    q, codes = mx_quantize(w.float(), dim=1, scale_alg=scale_alg)  # codes [G, K/32, N]
     G, K32, N = codes.shape
     col_scale = codes.reshape(G, K32 // 2, 2, N).permute(0, 1, 3, 2).contiguous()
     return q, col_scale

@@ -238,32 +238,83 @@ def test_unpermute_grad_is_the_autograd_of_the_unpermute():
 
 
 # ------------------------------------------------------------------------------------------------
-# MX quantisation (OCP MX v1.0, e4m3fn + e8m0 / 32)
+# MX quantisation (e4m3fn + e8m0 / 32; the reference's scale algorithm 1, OCP MX v1.0 as option 0)
 # ------------------------------------------------------------------------------------------------
 def test_mx_known_codes():
     def q(vals):
         x = torch.zeros(1, 32)
         x[0, :len(vals)] = torch.tensor(vals)
-        x[0, 31] = 448.0  # pins the block scale at 2^0 (floor(log2 448) - 8 = 0)
-        codes, scale = orc.mx_quantize(x)
-        assert int(scale[0, 0]) == 127
+        x[0, 31] = 448.0  # pins the block scale at 2^0 under both rules (448 = 1.75 * 2^8)
+        for alg in (0, 1):
+            codes, scale = orc.mx_quantize(x, scale_alg=alg)
+            assert int(scale[0, 0]) == 127
         return codes[0, :len(vals)].tolist()
     assert q([1.0, -1.0, 448.0, 0.0]) == [0x38, 0xB8, 0x7E, 0x00]
     assert q([2 ** -9, 2 ** -10, 3 * 2 ** -10, 2 ** -6]) == [0x01, 0x00, 0x02, 0x08]  # subnormals, RNE ties
     assert q([1.0625, 1.1875, 240.0, 232.0]) == [0x38, 0x3A, 0x77, 0x76]  # ties to even mantissa
 
 
+def test_mx_scale_algorithm_known_blocks():
+    """Known answers at the two rules' boundary: a block maximum M * 2^E with mantissa M <= 1.75 keeps
+    exponent E - 8 under scale algorithm 1 (1.75 * 2^E = 448 * 2^(E-8)); above 1.75 it moves to E - 7,
+    where the OCP rule (algorithm 0) keeps E - 8 and saturates the maximum to 448."""
+    cases = [  # (block max, algorithm-1 exponent, algorithm-0 exponent, algorithm-1 e4m3 code of the max)
+        (448.0, 0, 0, 0x7E),           # M = 1.75, E = 8: exact 448 either way
+        (449.0, 1, 0, 0x76),           # M just above 1.75: 449 / 2 = 224.5 -> 224 (0x76)
+        (511.0, 1, 0, 0x78),           # 255.5 -> 256 (nearest of 240 and 256)
+        (1.75, -8, -8, 0x7E),          # M = 1.75, E = 0
+        (1.875, -7, -8, 0x77),         # 1.875 * 2^7 = 240
+        (1.0, -8, -8, 0x78),           # 256
+        (3.5 * 2 ** -20, -27, -27, 0x7E),
+        (2.0 ** -130, -127, -127, None),  # fp32 subnormal maximum: clamped exponent
+    ]
+    for amax, e1, e0, code in cases:
+        x = torch.zeros(1, 32)
+        x[0, 3] = amax
+        x[0, 7] = -amax / 4
+        c1, s1 = orc.mx_quantize(x, scale_alg=1)
+        c0, s0 = orc.mx_quantize(x, scale_alg=0)
+        assert int(s1[0, 0]) - 127 == e1, (amax, int(s1[0, 0]) - 127)
+        assert int(s0[0, 0]) - 127 == e0, (amax, int(s0[0, 0]) - 127)
+        if code is not None:
+            assert int(c1[0, 3]) == code
+            assert int(c1[0, 7]) == (code - 0x10) | 0x80  # -max / 4: exponent field two lower
+    # the OCP rule saturates the 449 block's maximum to 448; algorithm 1 represents it (224 * 2)
+    x = torch.zeros(1, 32)
+    x[0, 0] = 449.0
+    c0, s0 = orc.mx_quantize(x, scale_alg=0)
+    c1, s1 = orc.mx_quantize(x, scale_alg=1)
+    assert float(orc.mx_dequantize(c0, s0)[0, 0]) == 448.0
+    assert float(orc.mx_dequantize(c1, s1)[0, 0]) == 448.0  # 449 -> 224.5 -> 224 (RNE) -> 448
+    x[0, 0] = 500.0
+    c0, s0 = orc.mx_quantize(x, scale_alg=0)
+    c1, s1 = orc.mx_quantize(x, scale_alg=1)
+    assert float(orc.mx_dequantize(c0, s0)[0, 0]) == 448.0  # clipped by 10 %
+    assert float(orc.mx_dequantize(c1, s1)[0, 0]) == 512.0  # 250 -> 256 (step 16 in [128, 256)), * 2
+
+
 def test_mx_invariants():
     g = torch.Generator().manual_seed(8)
     x = torch.randn(64, 256, generator=g) * torch.logspace(-8, 8, 64).unsqueeze(1)
     x[0] = 0.0
+    # the reference's rule: 2^e is the smallest power of two with amax <= 448 * 2^e (brute force)
     codes, scale = orc.mx_quantize(x)
+    amax = x.reshape(64, 8, 32).abs().amax(-1)
+    s = (scale.to(torch.float32) - 127).reshape(64, 8)
+    nz = amax > 0
+    assert (amax[nz] <= 448 * torch.pow(2.0, s[nz])).all()
+    assert (amax[nz] > 448 * torch.pow(2.0, s[nz] - 1)).all()
+    deq = orc.mx_dequantize(codes, scale)
+    rel = ((deq - x).abs() / x.abs().clamp(min=1e-30)).reshape(64, 8, 32)
+    norm = x.reshape(64, 8, 32).abs() >= torch.pow(2.0, s).unsqueeze(-1) * 2 ** -6
+    assert rel[norm].max() <= 2 ** -4 + 1e-7  # no element saturates: half a step everywhere
+    codes, scale = orc.mx_quantize(x, scale_alg=0)
     deq = orc.mx_dequantize(codes, scale)
     blocks = x.reshape(64, 8, 32)
     amax = blocks.abs().amax(-1)
     s = (scale.to(torch.float32) - 127).reshape(64, 8)
     nz = amax > 0
-    # scale exponent = floor(log2(amax)) - 8
+    # OCP scale exponent = floor(log2(amax)) - 8
     assert torch.equal(s[nz], torch.floor(torch.log2(amax[nz])) - 8)
     # scaled block maximum lies in [256, 512) before saturation at 448
     scaled_max = amax[nz] / torch.pow(2.0, s[nz])
@@ -279,9 +330,9 @@ def test_mx_invariants():
 def test_mx_weight_col_layout_roundtrip():
     g = torch.Generator().manual_seed(9)
     w = torch.randn(2, 128, 96, generator=g).to(torch.bfloat16)
-    data, col_scale = orc.mx_quantize_weight_cols(w)
+    data, col_scale = orc.mx_quantize_weight_cols(w, scale_alg=0)
     assert col_scale.shape == (2, 2, 96, 2)
-    codes, scale = orc.mx_quantize(w.float(), dim=1)  # [2, 4, 96]
+    codes, scale = orc.mx_quantize(w.float(), dim=1, scale_alg=0)  # [2, 4, 96]
     assert torch.equal(col_scale[:, 1, 5, 0], scale[:, 2, 5])
     assert torch.equal(col_scale[:, 1, 5, 1], scale[:, 3, 5])
     deq = orc.mx_dequantize_weight_cols(data, col_scale)
