@@ -231,7 +231,7 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
 // MegaMoE expert forward
 // ---------------------------------------------------------------------------------------------
 struct FwdLayout {
-  size_t dispatch, counts, group_list, mapping, gather, tile_prefix, act, act_scale, y, xq, xs, total;
+  size_t dispatch, counts, group_list, mapping, gather, tile_prefix, act, act_scale, act_f32, y, xq, xs, total;
 };
 
 static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
@@ -249,6 +249,7 @@ static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
   L.tile_prefix = take((E + 1) * 4);
   L.act = take(R * I * (mx ? 1 : 2));
   L.act_scale = mx ? take(std::max(R * mi355_mx_scale_ld(I), R * (I / 32) + 256)) : 0;
+  L.act_f32 = mx ? take(R * I * 4) : 0;  // 8-wave MX path: fp32 SwiGLU output before its quantisation
   L.y = take(R * H * 2);
   L.xq = mx ? take(T * H) : 0;
   // MX token scales: [T, ld] for the 4-wave GEMM, or stage-major over the routed rows [H/128][R][4]
@@ -371,13 +372,22 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   if (pp_mx) {
     p1.a_scale_stage_stride = T * K * 4;
     p1.a_scale_routed = 1;
-    p1.c_scale_stage_stride = T * K * 4;
   }
   const bool before_fc2 = (a.numerics_flags & MI355MOE_NUMERICS_PROBS_BEFORE_FC2) != 0;
   p1.swiglu_limit = a.swiglu_limit;
   p1.swiglu_after_silu = (a.numerics_flags & MI355MOE_NUMERICS_CLAMP_AFTER_SILU) != 0;
   p1.row_prob = before_fc2 ? a.topk_weights : nullptr;
-  rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st, small);
+  if (pp_mx) {
+    // SwiGLU output in fp32, then its MX quantisation into act (e4m3) and the code planes
+    p1.C = ws + L.act_f32;
+    p1.ldc = I;
+    rc = mi355_grouped_gemm(p1, true, true, EPI_SWIGLU_F32, st, small);
+    if (rc) return rc;
+    rc = mi355_mx_quant_act((const float*)(ws + L.act_f32), T * K, I, (uint8_t*)(ws + L.act),
+                            (uint8_t*)(ws + L.act_scale), T * K * 4, st);
+  } else {
+    rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st, small);
+  }
   if (rc) return rc;
   mark(2);
   // GMM2: [R, I] x [I, H] -> y [R, H] bf16

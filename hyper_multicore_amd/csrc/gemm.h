@@ -4,7 +4,9 @@
 
 // EPI_SWIGLU_BF16_NUM is EPI_SWIGLU_BF16 with the numerics options (clamp, probabilities before FC2);
 // callers ask for EPI_SWIGLU_BF16 and the dispatcher picks it when one of the options is set.
-enum { EPI_STORE_BF16 = 0, EPI_STORE_F32 = 1, EPI_SWIGLU_BF16 = 2, EPI_SWIGLU_MX = 3, EPI_SWIGLU_BF16_NUM = 4 };
+// EPI_SWIGLU_F32 (8-wave configuration, MX inputs): the fp32 SwiGLU output, for mi355_mx_quant_act.
+enum { EPI_STORE_BF16 = 0, EPI_STORE_F32 = 1, EPI_SWIGLU_BF16 = 2, EPI_SWIGLU_MX = 3, EPI_SWIGLU_BF16_NUM = 4,
+       EPI_SWIGLU_F32 = 5 };
 
 struct GGParams {
   const uint8_t* A;          // [rowsA, K] elements (bf16 or e4m3), row stride lda_bytes
@@ -133,6 +135,10 @@ int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const flo
                             uint16_t* out, hipStream_t stream);
 // scale_stage_stride > 0 writes the scales as stage-major code planes ([cols/128][4][stride / 4]); with
 // `mapping`, to the routed rows mapping[r * fanout + k] of each row r (negative entries skipped).
+// MX quantisation of fp32 rows (the SwiGLU output of EPI_SWIGLU_F32) into e4m3 [rows, cols] and the
+// stage-major code planes [cols/128][4][stage_stride / 4] (one thread per 32-element block).
+int mi355_mx_quant_act(const float* act, int64_t rows, int cols, uint8_t* q, uint8_t* planes, int64_t stage_stride,
+                       hipStream_t st);
 int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
                         hipStream_t st, int64_t scale_stage_stride = 0, const int32_t* mapping = nullptr,
                         int fanout = 1);

@@ -36,8 +36,9 @@
 //     s * 512 + j * 2 (the MX root's col_scale pairs).
 //
 // Epilogues: bf16 store, SwiGLU -> bf16 (each 32 x 32 block through a wave-private LDS staging block,
-// so the global stores are 16 bytes per lane) and SwiGLU -> MXFP8 requant (fp32 values staged 16 rows
-// at a time, then 4 lanes per 32-element MX block: block maximum by two DPP steps, 8-byte stores). For SwiGLU the 64 weight columns of a wave are 32 gate then
+// so the global stores are 16 bytes per lane) and, for MX inputs, SwiGLU -> fp32 (staged 16 rows at a
+// time, 32-byte stores), which mi355_mx_quant_act then quantises: a requant in this epilogue would
+// run its VALU work while the other wave group waits at the stage barrier. For SwiGLU the 64 weight columns of a wave are 32 gate then
 // the matching 32 up columns, so a lane holds gate and up of the same output element.
 #include "common.h"
 #include "gemm.h"
@@ -151,6 +152,7 @@ struct Plan {
   const uint8_t* s_base;   // MX: activation code plane run (every wave)
   const uint8_t* bs_base;  // MX: the group's weight scales (waves 0-3; waves 4-7 repeat them)
   uint32_t ao[CPW], bo[CPW], so, bso;
+  int a_copies;  // activation copies of this wave (8-row groups past the item's rows are skipped)
   int64_t b_stride, s_stride, b_scale_stride;
 };
 
@@ -171,6 +173,11 @@ __device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int
     pl.ao[j] = (uint32_t)(src * p.lda_bytes + chunk_of(r, lane) * 16);
   }
   pl.a_base = uni_ptr(p.A);
+  {
+    const int first = wave * CPW * 8;  // first tile row of this wave's activation copies
+    const int n = (it.rows - first + 7) / 8;
+    pl.a_copies = uni(n < 0 ? 0 : (n > CPW ? CPW : n));
+  }
   pl.b_base = uni_ptr(p.B + (int64_t)it.g * p.b_group_stride);
 #pragma unroll
   for (int j = 0; j < CPW; ++j) {
@@ -224,8 +231,11 @@ template <bool MX>
 __device__ __forceinline__ void issue_stage(const Plan& pl, int k, uint32_t slot, int wave) {
   const uint8_t* ab = uni_ptr(pl.a_base + (int64_t)k * KB);
   const uint8_t* bb = uni_ptr(pl.b_base + (int64_t)k * pl.b_stride);
+  // (the waits are for all outstanding copies, so a wave may issue fewer; LDS rows that are not
+  // refilled hold stale data that only feeds accumulator rows the epilogue does not store)
 #pragma unroll
-  for (int j = 0; j < CPW; ++j) dma16(ab, pl.ao[j], uni(slot + (wave * CPW + j) * 1024));
+  for (int j = 0; j < CPW; ++j)
+    if (j < pl.a_copies) dma16(ab, pl.ao[j], uni(slot + (wave * CPW + j) * 1024));
 #pragma unroll
   for (int j = 0; j < CPW; ++j) dma16(bb, pl.bo[j], uni(slot + B_OFF + (wave * CPW + j) * 1024));
   if constexpr (MX) {
@@ -348,13 +358,6 @@ __device__ __forceinline__ void mfmas(const Frags<MX, B_KN>& f, v16f (&acc)[MI][
   }
 }
 
-// max(v, v of the lane selected by the DPP control CTRL)
-template <int CTRL>
-__device__ __forceinline__ float dpp_max(float v) {
-  const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false);
-  return fmaxf(v, __int_as_float(o));
-}
-
 __device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
   // the gate and up projections are rounded to bf16 (the GMM1 output), SiLU(gate) * up in fp32
   const float gte = bf16_to_f32(f32_to_bf16(g_acc));
@@ -385,11 +388,10 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       // ---- write the block into the staging area
-      if constexpr (EPI == EPI_SWIGLU_MX) {
-        // Two halves of 16 rows: the fp32 SwiGLU values go to the staging block (16 rows x 128 bytes),
-        // then 4 lanes per row quantise 8 values each (block maximum over the 4 lanes by DPP) and
-        // write 8 e4m3 bytes; the row's scale code goes to its code plane.
-        const int cb = it.nt * 4 + wq;  // 32-column MX block of the output rows
+      if constexpr (EPI == EPI_SWIGLU_F32) {
+        // Two halves of 16 rows: the fp32 SwiGLU values go through the staging block (16 rows x 128
+        // bytes) and out as 32 bytes per lane (row lane / 4, columns 8 (lane % 4) ..+7).
+        const int cb = it.nt * 4 + wq;  // 32-column block of the output rows
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
@@ -399,31 +401,14 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
             *(__attribute__((address_space(3))) float*)(st + lrow * 128 + ((((lane & 31) >> 2) ^ (lrow & 7)) << 4) +
                                                        (lane & 3) * 4) = act;
           }
-          const int lrow = lane >> 2, part = lane & 3;  // 8 values: columns 8 part ..+7 of row lrow
+          const int lrow = lane >> 2, part = lane & 3;
           const v4f v0 = *LDSP(v4f, st + lrow * 128 + (((2 * part) ^ (lrow & 7)) << 4));
           const v4f v1 = *LDSP(v4f, st + lrow * 128 + (((2 * part + 1) ^ (lrow & 7)) << 4));
-          float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
-                             fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
-          amax = dpp_max<0xB1>(amax);  // quad_perm [1, 0, 3, 2]
-          amax = dpp_max<0x4E>(amax);  // quad_perm [2, 3, 0, 1]
-          const uint32_t code = mx_scale_code(amax);
-          uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            w0 |= f32_to_e4m3_inrange(mx_apply_inv_scale(v0[i], code)) << (8 * i);
-            w1 |= f32_to_e4m3_inrange(mx_apply_inv_scale(v1[i], code)) << (8 * i);
-          }
-          const int row = hh * 16 + lrow;  // row within the 32-row block
+          const int row = hh * 16 + lrow;
           if (row_base + row < it.rows) {
-            const int64_t orow = it.row0 + row_base + row;
-            *(v2i*)((uint8_t*)p.C + orow * p.ldc + cb * 32 + part * 8) = v2i{(int)w0, (int)w1};
-            if (part == 0) {
-              if (p.c_scale_stage_stride)
-                p.c_scale[(cb >> 2) * p.c_scale_stage_stride + (cb & 3) * (p.c_scale_stage_stride >> 2) + orow] =
-                    (uint8_t)code;
-              else
-                p.c_scale[orow * p.c_scale_ld + cb] = (uint8_t)code;
-            }
+            float* dst = (float*)p.C + (it.row0 + row_base + row) * p.ldc + cb * 32 + part * 8;
+            *(v4f*)dst = v0;
+            *(v4f*)(dst + 4) = v1;
           }
         }
       } else {
@@ -437,7 +422,7 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
         }
       }
       // ---- read back 16 bytes per lane and store (rows of 64 bytes, bf16; 32 bytes, e4m3)
-      if constexpr (EPI == EPI_SWIGLU_MX) {
+      if constexpr (EPI == EPI_SWIGLU_F32) {
         // written above
       } else {
 #pragma unroll
@@ -459,7 +444,7 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
 
 template <bool MX, bool B_KN, int EPI>
 __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
-  constexpr bool SWIGLU = EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX;
+  constexpr bool SWIGLU = EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_F32;
   constexpr int ESIZE = MX ? 1 : 2;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   int32_t* s_prefix = (int32_t*)(smem + PREFIX_OFF);
@@ -609,7 +594,7 @@ bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
   if (mx && (p.a_scale_stage_stride >= lim || p.b_scale_group_stride >= lim)) return false;
   if (mx && !b_kn) return false;  // MX weights: the root's col_data / col_scale layout
   if (mx && p.a_row_index != nullptr && !p.a_scale_routed) return false;  // code planes by routed row
-  if (mx) return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_MX;
+  if (mx) return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_F32;
   return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_BF16;
 }
 
@@ -631,5 +616,5 @@ int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStr
                                  : launch_pp<false, true, EPI_SWIGLU_BF16>(p, stream);
   }
   return epi == EPI_STORE_BF16 ? launch_pp<true, true, EPI_STORE_BF16>(p, stream)
-                               : launch_pp<true, true, EPI_SWIGLU_MX>(p, stream);
+                               : launch_pp<true, true, EPI_SWIGLU_F32>(p, stream);
 }

@@ -91,6 +91,45 @@ __global__ __launch_bounds__(256) void mx_quant_cols_kernel(const uint16_t* w, i
   col_scale[(((int64_t)g * (K / 64) + kb / 2) * N + n) * 2 + (kb & 1)] = (uint8_t)code;
 }
 
+// Thread (row, block b), rows fastest so that the code-plane bytes of a warp are contiguous.
+__global__ __launch_bounds__(256) void mx_quant_act_kernel(const float* act, int64_t rows, int cols, uint8_t* q,
+                                                          uint8_t* planes, int64_t stage_stride) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int nb = cols / 32;
+  if (id >= rows * nb) return;
+  const int b = (int)(id / rows);
+  const int64_t r = id - (int64_t)b * rows;
+  const v4f* src = (const v4f*)(act + r * cols + b * 32);
+  v4f v[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = src[i];
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
+  }
+  const uint32_t code = mx_scale_code(amax);
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    w[i] = f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][0], code)) |
+           (f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][1], code)) << 8) |
+           (f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][2], code)) << 16) |
+           (f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][3], code)) << 24);
+  uint4* dst = (uint4*)(q + r * cols + b * 32);
+  dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  planes[(b >> 2) * stage_stride + (b & 3) * (stage_stride >> 2) + r] = (uint8_t)code;
+}
+
+int mi355_mx_quant_act(const float* act, int64_t rows, int cols, uint8_t* q, uint8_t* planes, int64_t stage_stride,
+                       hipStream_t st) {
+  const int64_t n = rows * (cols / 32);
+  if (n == 0) return MI355MOE_OK;
+  hipLaunchKernelGGL(mx_quant_act_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, act, rows, cols, q,
+                     planes, stage_stride);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
 int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
                         hipStream_t st, int64_t scale_stage_stride, const int32_t* mapping, int fanout) {
   int64_t n = rows * (cols / 32);
