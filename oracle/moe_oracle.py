@@ -402,6 +402,46 @@ def expert_forward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: tor
     return unpermute_tokens(y.to(torch.bfloat16), mapping, None if apply_probs_before_fc2 else probs, K)
 
 
+def expert_forward_reference_tokens(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor,
+                                    tokens: torch.Tensor, expert_weights, *, precision: str = "bf16") -> torch.Tensor:
+    """:func:`expert_forward_reference` restricted to the token rows ``tokens`` (same rounding points,
+    fp32 accumulate; fp32_expert_reference.py:22-26, moe_reference.py:170-181), for layers whose
+    weights are too large to expand at once. ``expert_weights(e)`` returns the fp32 weights of expert
+    e as (W1 [H, 2I], W2 [I, H]); for MXFP8 they are the dequantised roots and the activations are
+    MX-quantised per row (a routed row's quantisation depends on that row only). Returns bf16
+    [len(tokens), H]: out[i] = bf16(sum over k ascending of p[t, k] * y[t, k]) for t = tokens[i]."""
+    tok = tokens.long()
+    K = ids.shape[1]
+    x = hidden.float()[tok]
+    if precision != "bf16":
+        q, s = mx_quantize(x, dim=-1)
+        x = mx_dequantize(q, s, dim=-1)
+    sel = ids[tok].long()                      # [n, K]
+    p = probs[tok].float()
+    n, H = x.shape
+    y = torch.zeros((n, K, H), dtype=torch.float32)
+    for e in torch.unique(sel).tolist():
+        if e < 0:
+            continue
+        rows, ks = (sel == e).nonzero(as_tuple=True)
+        W1, W2 = expert_weights(e)
+        I = W1.shape[1] // 2
+        u = _bf16(x[rows] @ W1)
+        act = swiglu_reference(u[:, :I], u[:, I:])
+        if precision == "bf16":
+            act = _bf16(act)
+        else:
+            aq, asc = mx_quantize(act, dim=-1)
+            act = mx_dequantize(aq, asc, dim=-1)
+        y[rows, ks] = _bf16(act @ W2)
+    out = torch.zeros((n, H), dtype=torch.float32)
+    for k in range(K):
+        contrib = y[:, k] * p[:, k:k + 1]
+        contrib[sel[:, k] < 0] = 0.0
+        out = out + contrib
+    return out.to(torch.bfloat16)
+
+
 def expert_backward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor, w1: torch.Tensor,
                               w2: torch.Tensor, grad_out: torch.Tensor, *, layout: str = "EIO",
                               num_experts: int | None = None):

@@ -774,3 +774,31 @@ def test_mx_backward_reference_close_to_bf16_backward():
     b = orc.expert_backward_reference(x, ids, p, w1, w2, dout)
     for u, v in zip(a, b):
         assert orc.rel_l2(u.float(), v.float()) < 0.12
+
+
+@pytest.mark.parametrize("precision", ["bf16", "mxfp8"])
+def test_expert_forward_tokens_equals_full_reference(precision):
+    """The sampled-token reference reproduces the full reference's rows bit for bit (bf16 EIO weights
+    and MXFP8 col_data roots)."""
+    g = torch.Generator().manual_seed(21)
+    T, H, I, E, K = 40, 128, 64, 6, 3
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    ids[5, 1] = -1  # a dropped slot
+    probs = torch.rand(T, K, generator=g)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.05).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.05).to(torch.bfloat16)
+    tokens = torch.tensor([0, 5, 7, 22, 39])
+    if precision == "bf16":
+        full = orc.expert_forward_reference(x, ids, probs, w1, w2, num_experts=E)
+        sub = orc.expert_forward_reference_tokens(x, ids, probs, tokens, lambda e: (w1[e].float(), w2[e].float()))
+    else:
+        d1, s1 = orc.mx_quantize_weight_cols(w1)
+        d2, s2 = orc.mx_quantize_weight_cols(w2)
+        full = orc.expert_forward_reference(x, ids, probs, d1, d2, precision="mxfp8", w1_scale=s1, w2_scale=s2,
+                                            num_experts=E)
+        W1 = orc.mx_dequantize_weight_cols(d1, s1)
+        W2 = orc.mx_dequantize_weight_cols(d2, s2)
+        sub = orc.expert_forward_reference_tokens(x, ids, probs, tokens, lambda e: (W1[e], W2[e]),
+                                                  precision="mxfp8")
+    assert torch.equal(sub, full[tokens])
