@@ -11,7 +11,7 @@ from ctypes import POINTER, Structure, c_float, c_int32, c_int64, c_size_t, c_ui
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmi355moe.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
@@ -89,7 +89,7 @@ class BackwardArgs(Structure):
         ("grad_out", c_void_p), ("grad_hidden", c_void_p), ("grad_w1", c_void_p), ("grad_w2", c_void_p),
         ("grad_topk_weights", c_void_p), ("weight_grad_dtype", c_int32), ("precision", c_int32),
         ("w1_scale", c_void_p), ("w2_scale", c_void_p), ("w1_row", c_void_p), ("w2_row", c_void_p),
-        ("w1_row_scale", c_void_p), ("w2_row_scale", c_void_p),
+        ("w1_row_scale", c_void_p), ("w2_row_scale", c_void_p), ("error_flag", c_void_p),
     ]
 
 

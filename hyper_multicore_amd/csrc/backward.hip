@@ -251,7 +251,7 @@ int mx_backward(const MI355MoeBackwardArgs& a, char* ws, const MxBwdLayout& L, h
   const int64_t ldH = mi355_mx_scale_ld(H), ldI = mi355_mx_scale_ld(I), ld2I = mi355_mx_scale_ld(2 * I);
 
   int rc = mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, T, K, E, (int32_t*)(ws + L.counts), nullptr, group_list,
-                                  mapping, gather, nullptr, ws + L.dispatch, st);
+                                  mapping, gather, a.error_flag, ws + L.dispatch, st);
   if (rc) return rc;
   if ((rc = mi355_plan_tiles(group_list, E, tile_prefix, st))) return rc;
   if ((rc = mi355_plan_row_blocks(group_list, E, 32, block_prefix, st))) return rc;
@@ -343,7 +343,8 @@ int mx_backward(const MI355MoeBackwardArgs& a, char* ws, const MxBwdLayout& L, h
                 y)))
     return rc;
   // combine backward: dY = bf16(p dOut), dp = <y, dOut>
-  hipLaunchKernelGGL(dy_dp_kernel<false>, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, gather, K,
+  // one block per slot through slot -> row (a slot with an id outside [0, E) has no row)
+  hipLaunchKernelGGL(dy_dp_kernel<true>, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, mapping, K,
                      H, R, dy, a.grad_topk_weights);
   if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
   if ((rc = quant(MX_Q_BF16, dy, nullptr, 1, H, H, L.dyq, L.dys, ldH, L.dycol, L.dycs))) return rc;
@@ -434,7 +435,7 @@ extern "C" int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* wor
   const uint8_t* zero = (const uint8_t*)(ws + L.zero);
 
   rc = mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, T, K, E, (int32_t*)(ws + L.counts), nullptr, group_list,
-                              mapping, gather, nullptr, ws + L.dispatch, st);
+                              mapping, gather, a.error_flag, ws + L.dispatch, st);
   if (rc) return rc;
   rc = mi355_plan_tiles(group_list, E, tile_prefix, st);
   if (rc) return rc;
@@ -494,7 +495,8 @@ extern "C" int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* wor
   rc = gmm(act, I, a.w2, !eoi, eoi ? I : H, w2_group, H, y);
   if (rc) return rc;
   // combine backward
-  hipLaunchKernelGGL(dy_dp_kernel<false>, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, gather, K,
+  // one block per slot through slot -> row (a slot with an id outside [0, E) has no row)
+  hipLaunchKernelGGL(dy_dp_kernel<true>, dim3((unsigned)R), dim3(256), 0, st, y, a.grad_out, a.topk_weights, mapping, K,
                      H, R, dy, a.grad_topk_weights);
   if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
   // down backward: gA = dY W2^T (W2 read transposed: EIO [I, H] rows are the N index -> NK)

@@ -13,16 +13,16 @@
 // MX GEMM with K-contiguous (EOI) weights.
 inline bool mi355_mx_eoi_enabled() { return MI355_PATH_ON; }
 // BF16 numerics options (SwiGLU clamp, probabilities before FC2).
-inline bool mi355_numerics_options_enabled() { return MI355_PATH_ON; }
+inline bool mi355_numerics_options_enabled() { return true; }
 // The 64-row tile configuration (two workgroups per CU) for grouped GEMMs whose groups average at
 // most 32 rows (decode).
 inline bool mi355_small_tiles_enabled() { return MI355_PATH_ON; }
 // Expert backward (bf16).
 inline bool mi355_backward_enabled() { return MI355_PATH_ON; }
 // MegaGate RouteGrad (gradient of the routing weights with respect to the logits).
-inline bool mi355_route_grad_enabled() { return MI355_PATH_ON; }
+inline bool mi355_route_grad_enabled() { return true; }
 // Dual-axis MX weight quantisation (col and row axes of the MXFP8 weight root in one pass).
-inline bool mi355_mx_weight_prep_enabled() { return MI355_PATH_ON; }
+inline bool mi355_mx_weight_prep_enabled() { return true; }
 // MXFP8 expert backward (needs the MX K-contiguous GEMM path for its data-gradient GEMMs).
 inline bool mi355_mx_backward_enabled() { return MI355_PATH_ON; }
 // The direct-weight grouped-GEMM configuration (gemm_direct.hip), selectable as variant "dv".

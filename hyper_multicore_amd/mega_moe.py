@@ -90,6 +90,23 @@ def _positive_int(name: str, value: Any) -> int:
     return value
 
 
+ROUTE_COUNT_ERROR = "MegaMoe counts must describe the actual distinct Top-K routes"
+
+
+def validate_routes(topk_ids: torch.Tensor, num_experts: int, tokens_per_expert: torch.Tensor | None = None) -> None:
+    """Refuse routes whose counts cannot describe the actual Top-K routes (route.py:566-593 raises
+    RuntimeError before any expert work): an id outside [0, E), or ``tokens_per_expert`` that is not
+    the histogram of the ids. One reduction on the ids' device and one host read (the reference also
+    reads its route summary on the host)."""
+    ids = topk_ids.reshape(-1)
+    bad = ((ids < 0) | (ids >= num_experts)).any()
+    if tokens_per_expert is not None:
+        hist = torch.bincount(ids.clamp(0, num_experts - 1).long(), minlength=num_experts)
+        bad = bad | (hist != tokens_per_expert.reshape(-1).to(hist.dtype)).any()
+    if bool(bad):
+        raise RuntimeError(ROUTE_COUNT_ERROR)
+
+
 class _MoeFunction(torch.autograd.Function):
     """bf16 expert forward with the library's backward (autograd.py:672-760 role); the forward
     intermediates are recomputed in the backward, so only the inputs are saved."""
@@ -317,6 +334,7 @@ class MegaMoeExperts(torch.nn.Module):
             raise RuntimeError("MegaMoeExperts runs eagerly; graph capture is not supported")
         if flat.shape[0] == 0:
             return torch.empty_like(hidden_states)
+        validate_routes(topk_ids, self.num_experts, tokens_per_expert)
         if tokens_per_expert is not None:
             tokens_per_expert = tokens_per_expert.to(torch.int32)
         if self._precision == "bf16":

@@ -496,7 +496,7 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
 def moe_backward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w1: torch.Tensor,
                  w2: torch.Tensor, grad_out: torch.Tensor, *, num_experts: int, intermediate_size: int,
                  layout: str = "EIO", weight_grad_dtype: torch.dtype = torch.bfloat16,
-                 need_topk_grad: bool = True):
+                 need_topk_grad: bool = True, error_flag: torch.Tensor | None = None):
     """Gradients of :func:`moe_forward` (bf16, default numerics) through ``mi355moe_moe_backward``:
     returns (grad_hidden bf16 [T, H], grad_w1, grad_w2 in the weights' layout and
     ``weight_grad_dtype``, grad_topk_weights fp32 [T, K] or None)."""
@@ -525,7 +525,8 @@ def moe_backward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: tor
         num_experts=num_experts, top_k=K, topk_ids=_ptr(ids), ids_dtype=_ids_dtype(ids),
         weight_layout=_lib.LAYOUT[layout], topk_weights=_ptr(probs), w1=_ptr(w1), w2=_ptr(w2),
         grad_out=_ptr(dout), grad_hidden=_ptr(grad_hidden), grad_w1=_ptr(grad_w1), grad_w2=_ptr(grad_w2),
-        grad_topk_weights=_ptr(grad_p), weight_grad_dtype=1 if weight_grad_dtype == torch.float32 else 0)
+        grad_topk_weights=_ptr(grad_p), weight_grad_dtype=1 if weight_grad_dtype == torch.float32 else 0,
+        error_flag=_ptr(error_flag))
     need = lib.mi355moe_moe_backward_workspace_size(ctypes.byref(args))
     if need == 0 and T > 0:
         _lib.check(lib.mi355moe_moe_backward(ctypes.byref(args), None, 0, _stream(device)), "mi355moe_moe_backward")
@@ -537,7 +538,8 @@ def moe_backward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: tor
 
 def moe_backward_mxfp8(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                        w1: tuple, w2: tuple, grad_out: torch.Tensor, *, num_experts: int, intermediate_size: int,
-                       weight_grad_dtype: torch.dtype = torch.bfloat16, need_topk_grad: bool = True):
+                       weight_grad_dtype: torch.dtype = torch.bfloat16, need_topk_grad: bool = True,
+                       error_flag: torch.Tensor | None = None):
     """Gradients of the MXFP8 :func:`moe_forward` (mxfp8/graph.py:147-154) through
     ``mi355moe_moe_backward``. ``w1`` / ``w2`` are (col_data, col_scale, row_data, row_scale) of the
     EIO MX roots: col_data [E, M, N] e4m3, col_scale [E, M/64, N, 2], row_data [E, M, N] e4m3,
@@ -578,7 +580,7 @@ def moe_backward_mxfp8(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weight
         grad_w2=_ptr(grad_w2), grad_topk_weights=_ptr(grad_p),
         weight_grad_dtype=1 if weight_grad_dtype == torch.float32 else 0, precision=_lib.PRECISION["mxfp8"],
         w1_scale=_ptr(s1), w2_scale=_ptr(s2), w1_row=_ptr(r1), w2_row=_ptr(r2), w1_row_scale=_ptr(rs1),
-        w2_row_scale=_ptr(rs2))
+        w2_row_scale=_ptr(rs2), error_flag=_ptr(error_flag))
     need = lib.mi355moe_moe_backward_workspace_size(ctypes.byref(args))
     if need == 0 and T > 0:
         _lib.check(lib.mi355moe_moe_backward(ctypes.byref(args), None, 0, _stream(device)), "mi355moe_moe_backward")

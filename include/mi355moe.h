@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MI355MOE_ABI_VERSION 3
+#define MI355MOE_ABI_VERSION 4
 
 enum {
   MI355MOE_OK_CODE = 0,
@@ -400,6 +400,7 @@ typedef struct MI355MoeBackwardArgs {
   const uint8_t* w2_row;      /* MXFP8: row_data [E, I, H] e4m3 */
   const uint8_t* w1_row_scale; /* MXFP8: row_scale [E, H, 2I/64, 2] */
   const uint8_t* w2_row_scale; /* MXFP8: row_scale [E, I, H/64, 2] */
+  int32_t* error_flag;        /* optional [1] int32: set to 1 when an id lies outside [0, E) (ABI 4) */
 } MI355MoeBackwardArgs;
 size_t mi355moe_moe_backward_workspace_size(const MI355MoeBackwardArgs* args);
 int mi355moe_moe_backward(const MI355MoeBackwardArgs* args, void* workspace, size_t workspace_size,

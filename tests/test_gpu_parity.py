@@ -885,3 +885,28 @@ def test_mxfp8_module_autograd(gpu):
     assert orc.rel_l2(roots[0].grad.cpu().float(), rw1) < MXFP8_REL_L2
     assert orc.rel_l2(roots[1].grad.cpu().float(), rw2) < MXFP8_REL_L2
     assert orc.rel_l2(pg.grad.cpu(), rp) < MXFP8_REL_L2
+
+
+def test_module_refuses_invalid_routes(gpu):
+    """MegaMoeExperts raises RuntimeError for an id outside [0, E) and for tokens_per_expert that is not
+    the ids' histogram (route.py:566-593), before launching any expert work."""
+    import hyper_multicore_amd as hm
+    from hyper_multicore_amd.mega_moe import ROUTE_COUNT_ERROR
+    T, H, I, E, K = 8, 256, 128, 4, 2
+    g = _seed(99)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(gpu)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    experts = hm.MegaMoeExperts(hidden_size=H, intermediate_size=I, num_experts=E, top_k=K)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(gpu)
+    probs = torch.full((T, K), 0.5, device=gpu)
+    experts(x, ids, probs, expert_weights=(w1, w2))
+    bad = ids.clone()
+    bad[3, 1] = E
+    with pytest.raises(RuntimeError, match=ROUTE_COUNT_ERROR):
+        experts(x, bad, probs, expert_weights=(w1, w2))
+    wrong = torch.bincount(ids.reshape(-1), minlength=E).to(torch.int32)
+    wrong[0] += 1
+    wrong[1] -= 1
+    with pytest.raises(RuntimeError, match=ROUTE_COUNT_ERROR):
+        experts(x, ids, probs, expert_weights=(w1, w2), tokens_per_expert=wrong)

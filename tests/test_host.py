@@ -169,3 +169,18 @@ def test_mx_backward_resolves_fresh_row_axis_and_keeps_forward_columns(monkeypat
     y = mega_moe._MxMoeFunction.apply(x, probs, roots[0], roots[1], ids, ex, torch.float32)
     with pytest.raises(ValueError, match="missing required row data/scale"):
         y.sum().backward()
+
+
+def test_invalid_routes_raise_like_the_reference():
+    """route.py:566-593: counts that do not describe the actual Top-K routes raise RuntimeError."""
+    from hyper_multicore_amd.mega_moe import ROUTE_COUNT_ERROR, validate_routes
+    ids = torch.tensor([[0, 1], [2, 3], [1, 2]])
+    validate_routes(ids, 4)
+    validate_routes(ids, 4, torch.tensor([1, 2, 2, 1]))
+    for bad in (torch.tensor([[0, 1], [2, 4], [1, 2]]), torch.tensor([[0, -1], [2, 3], [1, 2]])):
+        with pytest.raises(RuntimeError, match=ROUTE_COUNT_ERROR):
+            validate_routes(bad, 4)
+    with pytest.raises(RuntimeError, match=ROUTE_COUNT_ERROR):
+        validate_routes(ids, 4, torch.tensor([1, 2, 1, 2]))  # not the histogram
+    with pytest.raises(RuntimeError, match=ROUTE_COUNT_ERROR):
+        validate_routes(ids.to(torch.int32), 3)  # id 3 outside [0, 3)
