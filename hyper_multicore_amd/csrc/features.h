@@ -18,7 +18,7 @@ inline bool mi355_numerics_options_enabled() { return true; }
 // most 32 rows (decode).
 inline bool mi355_small_tiles_enabled() { return MI355_PATH_ON; }
 // Expert backward (bf16).
-inline bool mi355_backward_enabled() { return MI355_PATH_ON; }
+inline bool mi355_backward_enabled() { return true; }
 // MegaGate RouteGrad (gradient of the routing weights with respect to the logits).
 inline bool mi355_route_grad_enabled() { return true; }
 // Dual-axis MX weight quantisation (col and row axes of the MXFP8 weight root in one pass).
