@@ -11,7 +11,7 @@
 #define MI355_PATH_ON false
 #endif
 // MX GEMM with K-contiguous (EOI) weights.
-inline bool mi355_mx_eoi_enabled() { return MI355_PATH_ON; }
+inline bool mi355_mx_eoi_enabled() { return true; }
 // BF16 numerics options (SwiGLU clamp, probabilities before FC2).
 inline bool mi355_numerics_options_enabled() { return true; }
 // The 64-row tile configuration (two workgroups per CU) for grouped GEMMs whose groups average at
