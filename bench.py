@@ -52,7 +52,7 @@ def log(msg: str) -> None:
 class Layer:
     """Synthetic inputs + weights of one config, resident on the GPU."""
 
-    def __init__(self, name: str, device: torch.device, bf16_layout: str = "EOI"):
+    def __init__(self, name: str, device: torch.device, bf16_layout: str = "EOI", mx_layout: str = "EIO"):
         from hyper_multicore_amd import _lib, ops
         self.ops = ops
         self._lib = _lib
@@ -94,9 +94,10 @@ class Layer:
             d2, s2 = ops.mx_quantize_cols(w2.transpose(1, 2).contiguous())  # EIO [E, I, H]
             del w2
             self.w1, self.w2, self.s1, self.s2, self.layout = d1.view(torch.uint8), d2.view(torch.uint8), s1, s2, "EIO"
-            if ops.features() & self._lib.FEATURE_MX_EOI:
+            if mx_layout == "EOI":
                 # one-time weight preparation (outside the timed region, like loading a checkpoint):
-                # the same values and scales with K contiguous, read without transposing LDS loads
+                # the same values and scales with K contiguous (the 4-wave GEMM configuration reads
+                # them without transposing LDS loads; the default 8-wave one takes the EIO root)
                 e1, t1 = ops.mx_weight_to_eoi(d1, s1)
                 e2, t2 = ops.mx_weight_to_eoi(d2, s2)
                 del d1, s1, d2, s2
@@ -255,8 +256,8 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
 
 
 def run_config(name: str, device, steps: int, warmup: int, variant: str = "default",
-               bf16_layout: str = "EOI") -> dict:
-    layer = Layer(name, device, bf16_layout)
+               bf16_layout: str = "EOI", mx_layout: str = "EIO") -> dict:
+    layer = Layer(name, device, bf16_layout, mx_layout)
     counts = layer.counts()
     work = gmm_work(layer.c, counts)
     m = measure(layer, steps, warmup)
@@ -342,6 +343,8 @@ def main() -> int:
                     help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
     ap.add_argument("--bf16-layout", default="EOI", choices=["EOI", "EIO"],
                     help="expert-weight layout of the bf16 configs (EIO: the reference module's default)")
+    ap.add_argument("--mx-layout", default="EIO", choices=["EIO", "EOI"],
+                    help="MX expert-weight layout (EIO: the reference's col_data root; EOI: re-laid out once)")
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="time the DSv3-shape grouped GEMMs on their own per layout and variant (one JSON line)")
     args = ap.parse_args()
@@ -363,10 +366,10 @@ def main() -> int:
         return 0
     if args.gemm_variant is not None:
         ops.set_gemm_variant(args.gemm_variant)
-    gemm_variant = ops.set_gemm_variant("default")
-    ops.set_gemm_variant(gemm_variant)
+    gemm_variant = ops.gemm_variant()
     log(f"[bench] workload {args.config}: steps={args.steps} warmup={args.warmup}")
-    res, layer = run_config(args.config, device, args.steps, args.warmup, gemm_variant, args.bf16_layout)
+    res, layer = run_config(args.config, device, args.steps, args.warmup, gemm_variant, args.bf16_layout,
+                            args.mx_layout)
     c = layer.c
     cpu = None if args.no_cpu else cpu_baseline(args.config, layer)
     del layer
@@ -378,7 +381,7 @@ def main() -> int:
             continue
         log(f"[bench] extra {name}")
         r, lyr = run_config(name, device, max(5, args.steps // 2), max(2, args.warmup // 2), gemm_variant,
-                            args.bf16_layout)
+                            args.bf16_layout, args.mx_layout)
         extra[name] = r
         del lyr
         torch.cuda.empty_cache()

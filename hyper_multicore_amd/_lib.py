@@ -11,7 +11,7 @@ from ctypes import POINTER, Structure, c_float, c_int32, c_int64, c_size_t, c_ui
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmi355moe.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
@@ -77,6 +77,7 @@ class ForwardArgs(Structure):
         ("w1", c_void_p), ("w2", c_void_p), ("w1_scale", c_void_p), ("w2_scale", c_void_p),
         ("tokens_per_expert", c_void_p), ("out", c_void_p), ("error_flag", c_void_p),
         ("stage_events", POINTER(c_void_p)), ("num_stage_events", c_int32), ("swiglu_limit", c_float),
+        ("gemm_variant", c_int32),
     ]
 
 
@@ -97,7 +98,6 @@ class BackwardArgs(Structure):
 _SIGNATURES = [
     ("mi355moe_abi_version", c_int32, []),
     ("mi355moe_features", c_int32, []),
-    ("mi355moe_set_gemm_variant", c_int32, [c_int32]),
     ("mi355moe_gate_logits_workspace_size", c_size_t, [c_int64, c_int32, c_int32]),
     ("mi355moe_gate_logits", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
                                        c_void_p, c_void_p, c_size_t, c_void_p]),
@@ -121,9 +121,10 @@ _SIGNATURES = [
                                             c_void_p]),
     ("mi355moe_grouped_gemm_workspace_size", c_size_t, [c_int32]),
     ("mi355moe_grouped_gemm_bf16", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_int32,
-                                             c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+                                             c_void_p, c_void_p, c_int32, c_void_p, c_size_t, c_void_p]),
     ("mi355moe_grouped_gemm_mxfp8", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
-                                              c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+                                              c_int32, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_size_t,
+                                              c_void_p]),
     ("mi355moe_moe_forward_workspace_size", c_size_t, [POINTER(ForwardArgs)]),
     ("mi355moe_moe_forward", c_int32, [POINTER(ForwardArgs), c_void_p, c_size_t, c_void_p]),
     ("mi355moe_moe_backward_workspace_size", c_size_t, [POINTER(BackwardArgs)]),

@@ -22,12 +22,12 @@ extern "C" int mi355moe_features(void) {
          (mi355_split_roles_enabled() ? MI355MOE_FEATURE_SPLIT_ROLES : 0);
 }
 
-extern "C" int mi355moe_set_gemm_variant(int variant) {
-  if (variant < MI355_GG_VARIANT_DEFAULT || variant > MI355_GG_VARIANT_W4) return MI355MOE_EUNSUPPORTED;
-  if (variant == MI355_GG_VARIANT_DV && !mi355_direct_gemm_enabled()) return MI355MOE_EUNSUPPORTED;
+bool mi355_gg_variant_valid(int variant) {
+  if (variant < MI355_GG_VARIANT_DEFAULT || variant > MI355_GG_VARIANT_W4) return false;
+  if (variant == MI355_GG_VARIANT_DV && !mi355_direct_gemm_enabled()) return false;
   if ((variant == MI355_GG_VARIANT_SP || variant == MI355_GG_VARIANT_SP4) && !mi355_split_roles_enabled())
-    return MI355MOE_EUNSUPPORTED;
-  return mi355_gg_set_variant(variant);
+    return false;
+  return true;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -151,8 +151,9 @@ extern "C" size_t mi355moe_grouped_gemm_workspace_size(int32_t num_groups) {
 
 extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim, const uint16_t* w,
                                           int32_t layout, int32_t num_groups, int32_t ndim,
-                                          const int64_t* group_list, uint16_t* out, void* workspace,
-                                          size_t workspace_size, void* stream) {
+                                          const int64_t* group_list, uint16_t* out, int32_t gemm_variant,
+                                          void* workspace, size_t workspace_size, void* stream) {
+  if (!mi355_gg_variant_valid(gemm_variant)) return MI355MOE_EUNSUPPORTED;
   if (rows < 0 || kdim <= 0 || ndim <= 0 || num_groups <= 0 || num_groups > 4096) return MI355MOE_EINVAL;
   if (layout != MI355MOE_LAYOUT_EIO && layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   if (kdim % 64 || ndim % 8) return MI355MOE_EUNSUPPORTED;
@@ -161,6 +162,7 @@ extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32
   if (workspace == nullptr || workspace_size < mi355moe_grouped_gemm_workspace_size(num_groups)) return -4;
   hipStream_t st = (hipStream_t)stream;
   GGParams p = {};
+  p.variant = gemm_variant;
   p.A = (const uint8_t*)x;
   p.lda_bytes = (int64_t)kdim * 2;
   p.a_bytes = rows * kdim * 2;
@@ -186,7 +188,9 @@ extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32
 extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,
                                            const uint8_t* col_data, const uint8_t* col_scale, int32_t layout,
                                            int32_t num_groups, int32_t ndim, const int64_t* group_list, uint16_t* out,
-                                           void* workspace, size_t workspace_size, void* stream) {
+                                           int32_t gemm_variant, void* workspace, size_t workspace_size,
+                                           void* stream) {
+  if (!mi355_gg_variant_valid(gemm_variant)) return MI355MOE_EUNSUPPORTED;
   if (rows < 0 || kdim <= 0 || ndim <= 0 || num_groups <= 0 || num_groups > 4096) return MI355MOE_EINVAL;
   if (layout != MI355MOE_LAYOUT_EIO && layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   const bool eoi = layout == MI355MOE_LAYOUT_EOI;
@@ -200,6 +204,7 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
   if (workspace == nullptr || workspace_size < mi355moe_grouped_gemm_workspace_size(num_groups)) return -4;
   hipStream_t st = (hipStream_t)stream;
   GGParams p = {};
+  p.variant = gemm_variant;
   p.A = xq;
   p.lda_bytes = kdim;
   p.a_bytes = rows * kdim;
@@ -264,6 +269,7 @@ static int validate_fwd(const MI355MoeForwardArgs& a) {
   if (a.num_experts > 4096 || a.top_k > 64 || a.top_k > a.num_experts) return MI355MOE_EINVAL;
   if (a.ids_dtype != MI355MOE_IDS_INT32 && a.ids_dtype != MI355MOE_IDS_INT64) return MI355MOE_EINVAL;
   if (a.precision != MI355MOE_PRECISION_BF16 && a.precision != MI355MOE_PRECISION_MXFP8) return MI355MOE_EINVAL;
+  if (!mi355_gg_variant_valid(a.gemm_variant)) return MI355MOE_EUNSUPPORTED;
   if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;
   if (a.numerics_flags & ~(MI355MOE_NUMERICS_CLAMP_AFTER_SILU | MI355MOE_NUMERICS_PROBS_BEFORE_FC2))
@@ -332,8 +338,8 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   const uint8_t* a1 = (const uint8_t*)a.hidden;
   // MX on the 8-wave GEMM: activation scales stage-major (one 4-byte copy per row and 128-K stage)
   const bool pp_mx = mx && !eoi &&
-                     mi355_gg_pp_usable(true, true, H, E, T * H, (int64_t)H * 2 * I) &&
-                     mi355_gg_pp_usable(true, true, I, E, T * K * I, (int64_t)I * H);
+                     mi355_gg_pp_usable(a.gemm_variant, true, true, H, E, T * H, (int64_t)H * 2 * I) &&
+                     mi355_gg_pp_usable(a.gemm_variant, true, true, I, E, T * K * I, (int64_t)I * H);
   if (mx) {
     // with the 8-wave GEMM the token scales go to each token's routed rows (read in tile order)
     rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), mi355_mx_scale_ld(H), st,
@@ -345,6 +351,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   const int esize = mx ? 1 : 2;
   // GMM1: [R, H] x [H, 2I] -> SwiGLU -> act [R, I]
   GGParams p1 = {};
+  p1.variant = a.gemm_variant;
   p1.A = a1;
   p1.lda_bytes = (int64_t)H * esize;
   p1.a_bytes = T * H * esize;
@@ -392,6 +399,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   mark(2);
   // GMM2: [R, I] x [I, H] -> y [R, H] bf16
   GGParams p2 = {};
+  p2.variant = a.gemm_variant;
   p2.A = (const uint8_t*)(ws + L.act);
   p2.lda_bytes = (int64_t)I * esize;
   p2.a_bytes = T * K * I * esize;

@@ -59,6 +59,8 @@ struct GGParams {
   int64_t a_scale_stage_stride;
   int64_t c_scale_stage_stride;
   int32_t a_scale_routed;
+  // Tile-configuration variant of this call (MI355_GG_VARIANT_*; 0: the default).
+  int32_t variant;
 };
 
 
@@ -99,13 +101,13 @@ struct MxGroupedQuant {
 };
 int mi355_mx_quant_grouped(const MxGroupedQuant& q, hipStream_t stream);
 int mi355_num_cus();  // CU count of the current device (cached per device)
-// Forward tile-configuration variants for measurement (MI355MOE_GG_VARIANT=b6, dv, sp or sp4; default 0). A variant
-// keeps the default's tile height, so tile plans are shared; it answers MI355MOE_EUNSUPPORTED for the
-// paths it does not build, which then run on the default configuration.
+// Forward tile-configuration variants, chosen per call (GGParams::variant; 0 = the default, the 8-wave
+// configuration where it applies). A variant keeps the default's tile height, so tile plans are
+// shared; it answers MI355MOE_EUNSUPPORTED for the paths it does not build, which then run on the
+// default configuration.
 enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1, MI355_GG_VARIANT_DV = 2, MI355_GG_VARIANT_SP = 3,
        MI355_GG_VARIANT_SP4 = 4, MI355_GG_VARIANT_PP = 5, MI355_GG_VARIANT_W4 = 6 };
-int mi355_gg_variant();
-int mi355_gg_set_variant(int variant);  // returns the previous variant
+bool mi355_gg_variant_valid(int variant);  // known, and its feature bit set
 int mi355_grouped_gemm_variant(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
 // The direct-weight configuration (gemm_direct.hip), variant "dv"; MI355MOE_EUNSUPPORTED outside its
 // domain (K-contiguous weights, K a multiple of 8 stages, bf16 store / SwiGLU epilogues).
@@ -118,7 +120,7 @@ int mi355_grouped_gemm_split(const GGParams& p, bool mx, bool b_kn, int epi, hip
 bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi);
 // Whether the 8-wave configuration takes forward GEMMs of these extents under the current variant
 // (the caller then lays the MX activation scales out stage-major).
-bool mi355_gg_pp_usable(bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride);
+bool mi355_gg_pp_usable(int variant, bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride);
 int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
 #include "features.h"
 inline bool mi355_use_small_tiles(int64_t rows, int groups) {

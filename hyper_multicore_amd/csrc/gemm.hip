@@ -85,7 +85,7 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
     if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
     return dispatch_gg<GGSmall>(p, mx, b_kn, epi, stream);
   }
-  const int variant = mi355_gg_variant();
+  const int variant = p.variant;
   // the 8-wave configuration first (the default); the 4-wave kernels below for what it does not take
   if (variant == MI355_GG_VARIANT_DEFAULT || variant == MI355_GG_VARIANT_PP) {
     const int rc = mi355_grouped_gemm_pp(p, mx, b_kn, epi, stream);
@@ -100,28 +100,6 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   return dispatch_gg<GGBig>(p, mx, b_kn, epi, stream);
 }
 
-// The forward configuration variant: initially from MI355MOE_GG_VARIANT, then as set through
-// mi355moe_set_gemm_variant (a measurement control).
-static int g_gg_variant = -1;
-int mi355_gg_variant() {
-  if (g_gg_variant < 0) {
-    const char* s = getenv("MI355MOE_GG_VARIANT");
-    int v = MI355_GG_VARIANT_DEFAULT;
-    if (s != nullptr && strcmp(s, "b6") == 0) v = MI355_GG_VARIANT_B6;
-    if (s != nullptr && strcmp(s, "dv") == 0 && mi355_direct_gemm_enabled()) v = MI355_GG_VARIANT_DV;
-    if (s != nullptr && strcmp(s, "sp") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP;
-    if (s != nullptr && strcmp(s, "sp4") == 0 && mi355_split_roles_enabled()) v = MI355_GG_VARIANT_SP4;
-    if (s != nullptr && strcmp(s, "pp") == 0) v = MI355_GG_VARIANT_PP;
-    if (s != nullptr && strcmp(s, "w4") == 0) v = MI355_GG_VARIANT_W4;
-    g_gg_variant = v;
-  }
-  return g_gg_variant;
-}
-int mi355_gg_set_variant(int variant) {
-  const int prev = mi355_gg_variant();
-  g_gg_variant = variant;
-  return prev;
-}
 
 int mi355_gg_bm(bool small) { return small ? GGSmall::BM : GGBig::BM; }
 int mi355_gg_bn() { return GGBig::BN; }

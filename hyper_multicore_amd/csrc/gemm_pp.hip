@@ -598,8 +598,8 @@ bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
   return epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_BF16;
 }
 
-bool mi355_gg_pp_usable(bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride) {
-  const int v = mi355_gg_variant();
+bool mi355_gg_pp_usable(int variant, bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride) {
+  const int v = variant;
   if (v != MI355_GG_VARIANT_DEFAULT && v != MI355_GG_VARIANT_PP) return false;
   if (mx && !b_kn) return false;
   if (G > PREFIX_MAX || K * (mx ? 1 : 2) % KB != 0) return false;

@@ -7,8 +7,10 @@ current stream. Nothing here synchronises the host and nothing falls back to a C
 """
 from __future__ import annotations
 
+import contextvars
 import ctypes
 import math
+import os
 from dataclasses import dataclass
 
 import torch
@@ -345,7 +347,7 @@ def mx_quantize_weight(w: torch.Tensor, *, col: bool = True, row: bool = True):
 # Grouped GEMM and the full expert forward
 # ------------------------------------------------------------------------------------------------
 def grouped_gemm_bf16(x: torch.Tensor, weights: torch.Tensor, group_list: torch.Tensor,
-                      layout: str = "EIO") -> torch.Tensor:
+                      layout: str = "EIO", *, gemm_variant: str | None = None) -> torch.Tensor:
     """Concatenated per-group ``x[seg_g] @ W_g``; group_list = int64 inclusive row cumsum.
 
     layout "EIO": weights [G, K, N]; "EOI": weights [G, N, K].
@@ -368,7 +370,7 @@ def grouped_gemm_bf16(x: torch.Tensor, weights: torch.Tensor, group_list: torch.
     ws = _workspace(lib.mi355moe_grouped_gemm_workspace_size(G), device)
     rc = lib.mi355moe_grouped_gemm_bf16(_ptr(x.contiguous()), rows, K, _ptr(weights.contiguous()),
                                         _lib.LAYOUT[layout], G, N, _ptr(group_list.contiguous()), _ptr(out),
-                                        _ptr(ws), ws.numel(), _stream(device))
+                                        _variant_code(gemm_variant), _ptr(ws), ws.numel(), _stream(device))
     _lib.check(rc, "mi355moe_grouped_gemm_bf16")
     return out
 
@@ -378,17 +380,40 @@ def features() -> int:
     return int(_lib.load().mi355moe_features())
 
 
-def set_gemm_variant(name: str) -> str:
-    """Select the forward grouped-GEMM configuration for the following calls in this process
-    ("default", "b6" or "dv"; a measurement control, mi355moe_set_gemm_variant) and return the
-    previous one. Raises ``ValueError`` for an unknown name and ``RuntimeError`` when the library
-    has the variant switched off."""
+# Measurement default of the grouped-GEMM configuration for calls that do not name one: set with
+# set_gemm_variant (per thread / asyncio context), initially the MI355MOE_GG_VARIANT environment
+# variable, else "default". The library itself keeps no variant state; every call passes its own.
+_GEMM_VARIANT: contextvars.ContextVar[str | None] = contextvars.ContextVar("mi355moe_gemm_variant", default=None)
+_VARIANT_FEATURE = {"dv": _lib.FEATURE_DIRECT_GEMM, "sp": _lib.FEATURE_SPLIT_ROLES, "sp4": _lib.FEATURE_SPLIT_ROLES}
+
+
+def _check_variant(name: str) -> str:
     if name not in _lib.GEMM_VARIANT:
         raise ValueError(f"unknown GEMM variant {name!r}; expected one of {sorted(_lib.GEMM_VARIANT)}")
-    rc = int(_lib.load().mi355moe_set_gemm_variant(_lib.GEMM_VARIANT[name]))
-    if rc < 0:
+    bit = _VARIANT_FEATURE.get(name, 0)
+    if bit and not features() & bit:
         raise RuntimeError(f"GEMM variant {name!r} is switched off in this library build")
-    return {v: k for k, v in _lib.GEMM_VARIANT.items()}[rc]
+    return name
+
+
+def gemm_variant() -> str:
+    """The grouped-GEMM configuration used by calls that do not name one."""
+    name = _GEMM_VARIANT.get()
+    return name if name is not None else os.environ.get("MI355MOE_GG_VARIANT", "default") or "default"
+
+
+def _variant_code(name: str | None) -> int:
+    return _lib.GEMM_VARIANT[_check_variant(gemm_variant() if name is None else name)]
+
+
+def set_gemm_variant(name: str) -> str:
+    """Make ``name`` the grouped-GEMM configuration of the following calls in this thread / context
+    that do not pass ``gemm_variant`` (a measurement control) and return the previous one. Raises
+    ``ValueError`` for an unknown name and ``RuntimeError`` when the library has the variant switched
+    off."""
+    prev = gemm_variant()
+    _GEMM_VARIANT.set(_check_variant(name))
+    return prev
 
 
 def mx_weight_to_eoi(col_data: torch.Tensor, col_scale: torch.Tensor):
@@ -411,7 +436,8 @@ def mx_weight_to_eoi(col_data: torch.Tensor, col_scale: torch.Tensor):
 
 
 def grouped_gemm_mxfp8(xq: torch.Tensor, x_scale: torch.Tensor, w_data: torch.Tensor, w_scale: torch.Tensor,
-                       group_list: torch.Tensor, layout: str = "EIO") -> torch.Tensor:
+                       group_list: torch.Tensor, layout: str = "EIO", *,
+                       gemm_variant: str | None = None) -> torch.Tensor:
     """MX grouped GEMM: xq e4m3 [rows, K] (+ e8m0 [rows, K/32]) times the group weight, per group
     segment; bf16 [rows, N] out. layout "EIO": w_data = col_data [G, K, N], w_scale = col_scale
     [G, K/64, N, 2]; "EOI": the :func:`mx_weight_to_eoi` form [G, N, K] + [G, N, ld]."""
@@ -435,8 +461,8 @@ def grouped_gemm_mxfp8(xq: torch.Tensor, x_scale: torch.Tensor, w_data: torch.Te
     ws = _workspace(lib.mi355moe_grouped_gemm_workspace_size(G), device)
     rc = lib.mi355moe_grouped_gemm_mxfp8(_ptr(xq.contiguous()), _ptr(x_scale.contiguous()), rows, K,
                                          _ptr(w_data.contiguous()), _ptr(w_scale.contiguous()), _lib.LAYOUT[layout],
-                                         G, N, _ptr(group_list.contiguous()), _ptr(out), _ptr(ws), ws.numel(),
-                                         _stream(device))
+                                         G, N, _ptr(group_list.contiguous()), _ptr(out),
+                                         _variant_code(gemm_variant), _ptr(ws), ws.numel(), _stream(device))
     _lib.check(rc, "mi355moe_grouped_gemm_mxfp8")
     return out
 
@@ -446,7 +472,8 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
                 layout: str = "EIO", w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
                 tokens_per_expert: torch.Tensor | None = None, out: torch.Tensor | None = None,
                 error_flag: torch.Tensor | None = None, stage_events=None, swiglu_limit: float | None = None,
-                clamp_after_silu: bool = False, apply_probs_before_fc2: bool = False) -> torch.Tensor:
+                clamp_after_silu: bool = False, apply_probs_before_fc2: bool = False,
+                gemm_variant: str | None = None) -> torch.Tensor:
     """Expert forward at EP=1 through ``mi355moe_moe_forward``; returns bf16 [T, H].
 
     BF16 numerics options as ``MegaMoeNumericsOptions`` (``swiglu_limit``, ``clamp_after_silu``,
@@ -454,6 +481,9 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
 
     ``stage_events``: optional list of up to 5 ``torch.cuda.Event(enable_timing=True)`` recorded
     at the stage boundaries (start, after dispatch, after GMM1, after GMM2, after combine).
+
+    ``gemm_variant``: grouped-GEMM configuration of both expert GEMMs (``_lib.GEMM_VARIANT``; None:
+    :func:`gemm_variant`).
     """
     lib = _lib.load()
     device = _require_gpu(hidden, topk_ids, topk_weights, w1, w2, w1_scale, w2_scale, tokens_per_expert)
@@ -474,7 +504,8 @@ def moe_forward(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torc
         | (_lib.NUMERICS_PROBS_BEFORE_FC2 if apply_probs_before_fc2 else 0),
         swiglu_limit=0.0 if swiglu_limit is None else float(swiglu_limit),
         w1=_ptr(w1), w2=_ptr(w2), w1_scale=_ptr(w1_scale), w2_scale=_ptr(w2_scale),
-        tokens_per_expert=_ptr(tokens_per_expert), out=_ptr(out), error_flag=_ptr(error_flag))
+        tokens_per_expert=_ptr(tokens_per_expert), out=_ptr(out), error_flag=_ptr(error_flag),
+        gemm_variant=_variant_code(gemm_variant))
     if stage_events:
         handles = []
         for ev in stage_events:

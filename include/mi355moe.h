@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MI355MOE_ABI_VERSION 4
+#define MI355MOE_ABI_VERSION 5
 
 enum {
   MI355MOE_OK_CODE = 0,
@@ -56,24 +56,27 @@ enum {
   MI355MOE_FEATURE_ROUTE_GRAD = 16,   /* mi355moe_gate_route_grad */
   MI355MOE_FEATURE_MX_WEIGHT_PREP = 32, /* mi355moe_mx_quantize_weight */
   MI355MOE_FEATURE_MX_BACKWARD = 64,  /* mi355moe_moe_backward with precision MXFP8 */
-  MI355MOE_FEATURE_DIRECT_GEMM = 128, /* grouped-GEMM configuration "dv" (mi355moe_set_gemm_variant) */
+  MI355MOE_FEATURE_DIRECT_GEMM = 128, /* grouped-GEMM configuration "dv" (MI355MOE_GEMM_DIRECT) */
   MI355MOE_FEATURE_SPLIT_ROLES = 256, /* grouped-GEMM configurations "sp" / "sp4" (split copy roles) */
 };
 int mi355moe_features(void);
 
-/* Forward grouped-GEMM configuration used by the calls that follow in this process (a measurement
- * control; no counterpart in the reference, whose GEMM tiling is fixed by its tuning tables):
- * MI355MOE_GEMM_DEFAULT, MI355MOE_GEMM_B6 (256 x 256 tiles with a sixth weight slot),
- * MI355MOE_GEMM_DIRECT ("dv": K-contiguous weights loaded straight into registers, activations
- * through an 8-slot LDS ring; bf16 EOI and MXFP8 EOI GEMMs whose K is a whole number of 8 stages,
- * others keep the default), MI355MOE_GEMM_SPLIT / _SPLIT_A4 ("sp" / "sp4": two waves copy the
- * activations and two the weights, 3 + 6 or 4 + 5 ring slots; MXFP8 GEMMs on EIO weight roots). The
- * initial value comes from the environment variable MI355MOE_GG_VARIANT ("b6", "dv", "sp", "sp4"). Returns the previous variant, or MI355MOE_EUNSUPPORTED (and
- * changes nothing) for an unknown variant or one whose feature bit is clear. Not synchronised with
- * calls running on other host threads. */
+/* Grouped-GEMM configuration of a call (the gemm_variant argument of the grouped GEMMs and of
+ * MI355MoeForwardArgs; a measurement control with no counterpart in the reference, whose GEMM tiling
+ * is fixed by its tuning tables). The library holds no variant state: every call names its own.
+ *   MI355MOE_GEMM_DEFAULT: the 8-wave 256 x 256 configuration where it applies, else the 4-wave one;
+ *   MI355MOE_GEMM_PP: the 8-wave configuration where it applies (same as DEFAULT);
+ *   MI355MOE_GEMM_W4: the 4-wave 256 x 256 configuration (128 x 128 wave tiles);
+ *   MI355MOE_GEMM_B6: the 4-wave configuration with a sixth weight slot;
+ *   MI355MOE_GEMM_DIRECT ("dv"): bf16 K-contiguous weights loaded straight into registers,
+ *     activations through an 8-slot LDS ring (bf16 EOI GEMMs whose K is a whole number of 8 stages);
+ *   MI355MOE_GEMM_SPLIT / _SPLIT_A4 ("sp" / "sp4"): two waves copy the activations and two the
+ *     weights, 3 + 6 or 4 + 5 ring slots (MXFP8 GEMMs on EIO weight roots).
+ * A GEMM outside a variant's domain runs on the default configuration. An unknown variant, or one
+ * whose feature bit is clear, makes the call answer MI355MOE_EUNSUPPORTED. The expert backward
+ * always uses the default. */
 enum { MI355MOE_GEMM_DEFAULT = 0, MI355MOE_GEMM_B6 = 1, MI355MOE_GEMM_DIRECT = 2, MI355MOE_GEMM_SPLIT = 3,
-       MI355MOE_GEMM_SPLIT_A4 = 4 };
-int mi355moe_set_gemm_variant(int variant);
+       MI355MOE_GEMM_SPLIT_A4 = 4, MI355MOE_GEMM_PP = 5, MI355MOE_GEMM_W4 = 6 };
 
 /* ---------------------------------------------------------------------------------------------
  * Router projection: logits[t, e] = sum_h x[t, h] * w[e, h], bf16 inputs, fp32 accumulate and
@@ -279,7 +282,7 @@ int mi355moe_mx_weight_to_eoi(const uint8_t* col_data, const uint8_t* col_scale,
 size_t mi355moe_grouped_gemm_workspace_size(int32_t num_groups);
 int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim,
                                const uint16_t* w, int32_t layout, int32_t num_groups,
-                               int32_t ndim, const int64_t* group_list, uint16_t* out,
+                               int32_t ndim, const int64_t* group_list, uint16_t* out, int32_t gemm_variant,
                                void* workspace, size_t workspace_size, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
@@ -294,8 +297,8 @@ int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim,
  */
 int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,
                                 const uint8_t* w_data, const uint8_t* w_scale, int32_t layout, int32_t num_groups,
-                                int32_t ndim, const int64_t* group_list, uint16_t* out, void* workspace,
-                                size_t workspace_size, void* stream);
+                                int32_t ndim, const int64_t* group_list, uint16_t* out, int32_t gemm_variant,
+                                void* workspace, size_t workspace_size, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * MegaMoE expert forward at EP=1: dispatch -> (MX quant) -> GMM1 + fused SwiGLU (+ MX requant)
@@ -344,6 +347,7 @@ typedef struct MI355MoeForwardArgs {
   void* const* stage_events;
   int32_t num_stage_events;
   float swiglu_limit;         /* > 0: SwiGLU clamp limit L (BF16 only); 0: no clamp */
+  int32_t gemm_variant;       /* MI355MOE_GEMM_* of both expert GEMMs (0: the default) */
 } MI355MoeForwardArgs;
 size_t mi355moe_moe_forward_workspace_size(const MI355MoeForwardArgs* args);
 int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* workspace, size_t workspace_size,

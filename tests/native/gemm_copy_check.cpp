@@ -51,8 +51,8 @@ static std::string g_scenario;
 // Use the 256-row tiles even where the library would pick the 64-row ones (the state of a build with
 // the decode tiles switched off): planning and launch both follow it.
 static bool g_force_big = false;
-// The forward tile-configuration variant the scenario runs (gemm.hip selects it from
-// MI355MOE_GG_VARIANT; gemm_var.hip builds it).
+// The forward tile-configuration variant the scenario passes through the C ABI (gemm_variant
+// argument / MI355MoeForwardArgs::gemm_variant; gemm_var.hip builds the variants).
 static int g_variant = 0;
 using GGB6 = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0>;  // gemm_var.hip
 using GGSplit = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0, true>;   // gemm_var.hip (sp)
@@ -1587,7 +1587,7 @@ static int sim_dispatch(const GGParams& p, bool mx, bool b_kn, int epi) {
 // Library internals replaced by the simulation (same signatures as gemm.h)
 // The checker replays the 4-wave kernels' copy plans: the library's moe_forward is steered onto them
 // (the 8-wave configuration has its own GPU bit-identity tests against them).
-bool mi355_gg_pp_usable(bool, bool, int64_t, int, int64_t, int64_t) { return false; }
+bool mi355_gg_pp_usable(int, bool, bool, int64_t, int, int64_t, int64_t) { return false; }
 
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t, bool small) {
   // the dispatcher's choice of the numerics epilogue (gemm.hip, mi355_grouped_gemm)
@@ -1598,13 +1598,13 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
     if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
     return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
   }
-  if (g_variant == MI355_GG_VARIANT_B6) {
+  if (p.variant == MI355_GG_VARIANT_B6) {
     const int rc = sim_dispatch<GGB6>(p, mx, b_kn, epi);
     if (rc != MI355MOE_EUNSUPPORTED) return rc;
   }
-  if ((g_variant == MI355_GG_VARIANT_SP || g_variant == MI355_GG_VARIANT_SP4) && gg_split_applies(p, mx, b_kn, epi)) {
+  if ((p.variant == MI355_GG_VARIANT_SP || p.variant == MI355_GG_VARIANT_SP4) && gg_split_applies(p, mx, b_kn, epi)) {
     ++g_split_gemms;
-    const bool sp = g_variant == MI355_GG_VARIANT_SP;
+    const bool sp = p.variant == MI355_GG_VARIANT_SP;
     if (mx && epi == EPI_SWIGLU_MX)
       return sp ? sim_forward<GGSplit, true, true, EPI_SWIGLU_MX>(p) : sim_forward<GGSplitA4, true, true, EPI_SWIGLU_MX>(p);
     if (mx) return sp ? sim_forward<GGSplit, true, true, EPI_STORE_BF16>(p) : sim_forward<GGSplitA4, true, true, EPI_STORE_BF16>(p);
@@ -1613,7 +1613,7 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
                 : sim_forward<GGSplitA4, false, true, EPI_SWIGLU_BF16>(p);
     return sp ? sim_forward<GGSplit, false, true, EPI_STORE_BF16>(p) : sim_forward<GGSplitA4, false, true, EPI_STORE_BF16>(p);
   }
-  if (g_variant == MI355_GG_VARIANT_DV) {
+  if (p.variant == MI355_GG_VARIANT_DV) {
     const int rc = sim_direct_dispatch(p, mx, b_kn, epi);
     if (rc != MI355MOE_EUNSUPPORTED) {
       ++g_direct_gemms;
@@ -1697,7 +1697,7 @@ static void gemm_bf16(std::vector<int> counts, int K, int N, int layout) {
   g_expect.a_row_bytes = (int64_t)K * 2;
   g_expect.B = w;
   expect_rc(mi355moe_grouped_gemm_bf16((const uint16_t*)x, rows, K, (const uint16_t*)w, layout, G, N, gl,
-                                       (uint16_t*)out, ws, wsz, nullptr),
+                                       (uint16_t*)out, g_variant, ws, wsz, nullptr),
             0, "grouped_gemm_bf16");
   g_expect = Expect();
 }
@@ -1732,7 +1732,7 @@ static void gemm_mx(std::vector<int> counts, int K, int N, int layout) {
   g_expect.B = wd;
   g_expect.b_scale = wsc;
   g_expect.b_scale_ld = sld;
-  expect_rc(mi355moe_grouped_gemm_mxfp8(xq, xs, rows, K, wd, wsc, layout, G, N, gl, (uint16_t*)out, ws, wsz, nullptr),
+  expect_rc(mi355moe_grouped_gemm_mxfp8(xq, xs, rows, K, wd, wsc, layout, G, N, gl, (uint16_t*)out, g_variant, ws, wsz, nullptr),
             0, "grouped_gemm_mxfp8");
   g_expect = Expect();
 }
@@ -1794,6 +1794,7 @@ static void moe_forward(int64_t T, int K, int E, int H, int I, int precision, in
   a.weight_layout = layout;
   a.numerics_flags = numerics;
   a.swiglu_limit = limit;
+  a.gemm_variant = g_variant;
   a.w1 = w1;
   a.w2 = w2;
   a.w1_scale = s1;

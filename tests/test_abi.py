@@ -1,6 +1,7 @@
 """CPU checks of the C-ABI library: it loads, exports every symbol declared in include/*.h, and
 rejects bad arguments before touching the GPU (no compute calls are made here)."""
 import ctypes
+import os
 import re
 from pathlib import Path
 
@@ -150,24 +151,33 @@ def test_gpu_ops_refuse_cpu_tensors():
         ops.gate_route(torch.zeros(2, 8), torch.zeros(8), top_k=2, scoring_func="softmax", routed_scaling_factor=1.0)
 
 
-def test_gemm_variant_control():
-    """The measurement control selects known variants only, returns the previous one, and refuses a
-    variant whose feature bit is clear (host-side state only; nothing is launched)."""
+def test_gemm_variant_is_per_call():
+    """The GEMM configuration is an argument of each call: an unknown variant is refused before
+    anything is enqueued (null pointers, so no launch is possible), a known one reaches the ordinary
+    argument checks. The Python default is per thread and never reaches the library as state."""
+    import threading
     from hyper_multicore_amd import _lib, ops
     lib = _lib.load()
-    assert lib.mi355moe_set_gemm_variant(7) == _lib.EUNSUPPORTED
-    prev = lib.mi355moe_set_gemm_variant(_lib.GEMM_VARIANT["b6"])
-    assert prev in _lib.GEMM_VARIANT.values()
-    assert lib.mi355moe_set_gemm_variant(prev) == _lib.GEMM_VARIANT["b6"]
-    direct_on = bool(ops.features() & _lib.FEATURE_DIRECT_GEMM)
-    rc = lib.mi355moe_set_gemm_variant(_lib.GEMM_VARIANT["dv"])
-    if direct_on:
-        assert rc == prev
-        lib.mi355moe_set_gemm_variant(prev)
-    else:
-        assert rc == _lib.EUNSUPPORTED
-        with pytest.raises(RuntimeError):
-            ops.set_gemm_variant("dv")
+    for bad in (-1, 7):
+        assert lib.mi355moe_grouped_gemm_bf16(None, 4, 64, None, 0, 1, 8, None, None, bad, None, 0, None) \
+            == _lib.EUNSUPPORTED
+        assert lib.mi355moe_grouped_gemm_mxfp8(None, None, 4, 512, None, None, 0, 1, 16, None, None, bad, None, 0,
+                                               None) == _lib.EUNSUPPORTED
+        args = _lib.ForwardArgs(num_tokens=4, hidden_size=128, intermediate_size=128, num_experts=4, top_k=2,
+                                ids_dtype=_lib.IDS_INT32, precision=_lib.PRECISION["bf16"], gemm_variant=bad)
+        assert lib.mi355moe_moe_forward(ctypes.byref(args), None, 0, None) == _lib.EUNSUPPORTED
+    # a valid variant passes the variant check and fails on the null operands instead
+    assert lib.mi355moe_grouped_gemm_bf16(None, 4, 64, None, 0, 1, 8, None, None, _lib.GEMM_VARIANT["w4"], None, 0,
+                                          None) == _lib.EINVAL
     with pytest.raises(ValueError):
         ops.set_gemm_variant("fastest")
-    assert ops.set_gemm_variant("default") in _lib.GEMM_VARIANT
+    prev = ops.set_gemm_variant("w4")
+    try:
+        seen = []
+        t = threading.Thread(target=lambda: seen.append(ops.gemm_variant()))
+        t.start()
+        t.join()
+        # a new thread starts from the process default, not from this thread's setting
+        assert ops.gemm_variant() == "w4" and seen == [os.environ.get("MI355MOE_GG_VARIANT") or "default"]
+    finally:
+        ops.set_gemm_variant(prev)

@@ -299,6 +299,8 @@ def test_modules_end_to_end(gpu):
     assert gate.bias.dtype == torch.float32
     x = torch.randn(2, T // 2, H, generator=g).to(torch.bfloat16)
     logits, weights, ids = gate(x.to(gpu))
+    # the gate's outputs carry autograd history (RouteGrad); the checks below read values only
+    logits, weights = logits.detach(), weights.detach()
     ref_logits = orc.gate_logits_reference(x, gate.weight.detach().cpu())
     torch.testing.assert_close(logits.cpu(), ref_logits, rtol=1e-5, atol=2e-5)
     w_ref, i_ref, _ = orc.route_c(logits.cpu().numpy(), gate.bias.detach().cpu().numpy(), top_k=K,
@@ -438,7 +440,9 @@ def test_grouped_gemm_bf16_direct_matches_default(gpu, counts, Kd):
 @_needs(1, "the MXFP8 EOI GEMM path")
 @pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2, [3, 40, 0, 513]])
 def test_grouped_gemm_mxfp8_direct_matches_eio(gpu, counts):
-    """MX EOI weights on the direct-weight configuration: bit-identical to the default EIO GEMM."""
+    """MX EOI weights with variant "dv": the library refuses MXFP8 on the direct-weight configuration
+    (its outputs were wrong in every second 32-column block on the GPU), so the call runs on the
+    default configuration and stays bit-identical to the EIO GEMM."""
     from hyper_multicore_amd import ops
     g = _seed(sum(counts) + 11)
     G, Kd, N = len(counts), 1024, 768

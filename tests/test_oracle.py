@@ -701,15 +701,19 @@ def test_grouped_row_quant_aligned_experts_equal_plain_column_quant():
 
 
 def test_grouped_row_quant_blocks_restart_at_each_expert():
-    """A 1-row expert gets the closed-form code of each value (floor(log2 |v|) - 8) and the unused odd
+    """A 1-row expert gets the closed-form code of each value (scale algorithm 1: the smallest e with
+    |v| <= 448 * 2^e, i.e. floor(log2 |v|) - 8, plus 1 when the mantissa exceeds 1.75) and the unused odd
     slot of its pair stays 0; a boundary inside a 32-row block changes the result versus global
     blocks; scale regions of consecutive experts never overlap."""
     g = torch.Generator().manual_seed(4)
     counts = [1, 45, 33, 0, 64]
     x = torch.randn(sum(counts), 64, generator=g)
     codes, packed, _ = orc.mx_quantize_grouped_rows(x, counts)
-    v = x[0].abs()
-    want = (torch.floor(torch.log2(v)) - 8 + 127).to(torch.uint8)
+    v = x[0].abs().double()
+    e = torch.floor(torch.log2(v))
+    e = e - 8 + (v / torch.exp2(e) > 1.75).double()
+    assert torch.all(v <= 448 * torch.exp2(e)) and torch.all(v > 448 * torch.exp2(e - 1))
+    want = (e + 127).to(torch.uint8)
     assert torch.equal(packed[0, :, 0], want)
     assert torch.all(packed[0, :, 1] == 0)
     q_global, _ = orc.mx_quantize(torch.cat([x, torch.zeros(32 - x.shape[0] % 32, 64)]), dim=0)
