@@ -179,7 +179,7 @@ extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32
   p.tile_prefix = (int32_t*)workspace;
   p.C = out;
   p.ldc = ndim;
-  const bool small = mi355_use_small_tiles(rows, num_groups);
+  const bool small = mi355_use_small_tiles(rows, num_groups, gemm_variant);
   int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st, small);
   if (rc) return rc;
   return mi355_grouped_gemm(p, false, layout == MI355MOE_LAYOUT_EIO, EPI_STORE_BF16, st, small);
@@ -226,7 +226,7 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
   p.tile_prefix = (int32_t*)workspace;
   p.C = out;
   p.ldc = ndim;
-  const bool small = mi355_use_small_tiles(rows, num_groups);
+  const bool small = mi355_use_small_tiles(rows, num_groups, gemm_variant);
   int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st, small);
   if (rc) return rc;
   return mi355_grouped_gemm(p, true, !eoi, EPI_STORE_BF16, st, small);
@@ -332,12 +332,13 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
                               a.error_flag, ws + L.dispatch, st);
   if (rc) return rc;
   // decode shapes (few routed rows per expert) use the 64-row tiles
-  const bool small = mi355_use_small_tiles(T * K, E);
+  const bool small = mi355_use_small_tiles(T * K, E, a.gemm_variant);
   rc = mi355_plan_tiles(group_list, E, tile_prefix, st, small);
   if (rc) return rc;
   const uint8_t* a1 = (const uint8_t*)a.hidden;
-  // MX on the 8-wave GEMM: activation scales stage-major (one 4-byte copy per row and 128-K stage)
-  const bool pp_mx = mx && !eoi &&
+  // MX on the 8-wave GEMM: activation scales stage-major (one 4-byte copy per row and 128-K stage);
+  // the 64-row tiles read row-major scales and a tile plan in 64-row units
+  const bool pp_mx = mx && !eoi && !small &&
                      mi355_gg_pp_usable(a.gemm_variant, true, true, H, E, T * H, (int64_t)H * 2 * I) &&
                      mi355_gg_pp_usable(a.gemm_variant, true, true, I, E, T * K * I, (int64_t)I * H);
   if (mx) {

@@ -16,7 +16,7 @@ inline bool mi355_mx_eoi_enabled() { return true; }
 inline bool mi355_numerics_options_enabled() { return true; }
 // The 64-row tile configuration (two workgroups per CU) for grouped GEMMs whose groups average at
 // most 32 rows (decode).
-inline bool mi355_small_tiles_enabled() { return MI355_PATH_ON; }
+inline bool mi355_small_tiles_enabled() { return true; }
 // Expert backward (bf16).
 inline bool mi355_backward_enabled() { return true; }
 // MegaGate RouteGrad (gradient of the routing weights with respect to the logits).

@@ -123,8 +123,9 @@ bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi);
 bool mi355_gg_pp_usable(int variant, bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride);
 int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
 #include "features.h"
-inline bool mi355_use_small_tiles(int64_t rows, int groups) {
-  return mi355_small_tiles_enabled() && rows <= (int64_t)groups * 32;
+inline bool mi355_use_small_tiles(int64_t rows, int groups, int variant) {
+  // a variant named explicitly keeps the 256-row tiles
+  return mi355_small_tiles_enabled() && variant == 0 && rows <= (int64_t)groups * 32;
 }
 int mi355_gg_bn();
 int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
