@@ -19,6 +19,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -140,6 +141,16 @@ def gmm_work(c: dict, counts: torch.Tensor) -> dict:
                 layer_bytes=layer_bytes)
 
 
+def m_tiles(c: dict, counts: torch.Tensor, variant: str = "default", decode_tiles: bool = True) -> dict:
+    """Row tiles the expert GEMMs run (per column block) against the ideal R / BM, and the fraction
+    of tile rows that are padding: the M-tail waste of ragged groups. BM is 64 on the decode tiles
+    (routed rows <= 32 per expert under the default variant), else 256."""
+    R = c["T"] * c["K"]
+    bm = 64 if decode_tiles and variant == "default" and R <= c["E"] * 32 else 256
+    tiles = int(((counts + bm - 1) // bm).sum())
+    return {"bm": bm, "tiles": tiles, "ideal": -(-R // bm), "padded_row_frac": round(1 - R / (tiles * bm), 4)}
+
+
 def measure(layer: Layer, steps: int, warmup: int) -> dict:
     for _ in range(warmup):
         layer.step()
@@ -166,12 +177,12 @@ def measure(layer: Layer, steps: int, warmup: int) -> dict:
     return dict(ms_per_step=total_ms / steps, wall_s=wall, stage_ms=avg)
 
 
-def measured_traffic(workload: str, variant: str, root: str = ROOT):
-    """HBM bytes per GMM1 launch from the committed rocprofv3 counter passes of the same workload and
-    GEMM variant (profiles/traffic_<workload>_<variant>.json: FETCH_SIZE and WRITE_SIZE in KiB per
-    dispatch, each scaled by the factor the same counter reads for a plain copy kernel of known size),
-    or None when no such record exists."""
-    path = os.path.join(root, "profiles", f"traffic_{workload}_{variant}.json")
+def measured_traffic(workload: str, variant: str, layout: str, root: str = ROOT):
+    """HBM bytes per GMM1 launch from the committed rocprofv3 counter passes of the same workload,
+    GEMM variant and weight layout (profiles/traffic_<workload>_<variant>_<layout>.json, written by
+    ``--summarize``: FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the factor the same
+    counter reads for a plain copy kernel of known size), or None when no such record exists."""
+    path = os.path.join(root, "profiles", f"traffic_{workload}_{variant}_{layout}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -180,25 +191,43 @@ def measured_traffic(workload: str, variant: str, root: str = ROOT):
 
 
 def roofline(c: dict, work: dict, gmm1_ms: float, traffic=None) -> dict:
+    """Roofline of the GMM1 kernel (grouped GEMM + SwiGLU epilogue): algorithmic bytes or flops per
+    launch over its average launch duration (HIP events around that one kernel on the library's
+    stream). traffic = measured HBM bytes per launch (None without a counter record)."""
     mx = c["precision"] == "mxfp8"
     peak_flops = PEAK["mxfp8" if mx else "bf16"]
     t_mfma = work["g1_flops"] / peak_flops
     t_hbm = work["g1_bytes"] / PEAK["hbm"]
     sec = gmm1_ms * 1e-3
+    common = {"traffic": traffic, "algorithmic_bytes": round(work["g1_bytes"]),
+              "traffic_ratio": None if traffic is None else round(traffic / work["g1_bytes"], 3),
+              "kernel": "grouped_gemm GMM1+SwiGLU", "launch_ms": round(gmm1_ms, 4)}
     if t_hbm > t_mfma:
         achieved = work["g1_bytes"] / sec / 1e9
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm"] / 1e9, "unit": "GB/s",
-                "frac": round(achieved / (PEAK["hbm"] / 1e9), 4), "traffic": traffic,
-                "kernel": "grouped_gemm GMM1+SwiGLU", "mfma_frac": round(work["g1_flops"] / sec / peak_flops, 4)}
+                "frac": round(achieved / (PEAK["hbm"] / 1e9), 4), **common,
+                "mfma_frac": round(work["g1_flops"] / sec / peak_flops, 4)}
     achieved = work["g1_flops"] / sec / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak_flops / 1e12, "unit": "TFLOP/s",
-            "frac": round(achieved / (peak_flops / 1e12), 4), "traffic": traffic, "kernel": "grouped_gemm GMM1+SwiGLU",
+            "frac": round(achieved / (peak_flops / 1e12), 4), **common,
             "hbm_frac": round(work["g1_bytes"] / sec / PEAK["hbm"], 4)}
 
 
 def _library_features() -> int:
     from hyper_multicore_amd import ops
     return ops.features()
+
+
+def cpu_model() -> str:
+    """The host CPU's model string (/proc/cpuinfo), else what platform reports."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
@@ -252,7 +281,8 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
     return {"value": round(sample / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "gpu_rel_l2": agree,
             "sample": f"first {sample} of {T} tokens of the {name} batch, median of {len(times)} after 1 warm-up; "
-                      f"torch CPU {torch.__version__}, os.cpu_count()={os.cpu_count()}, cpu={platform.processor() or platform.machine()}"}
+                      f"torch CPU {torch.__version__}, os.cpu_count()={os.cpu_count()}",
+            "cpu_model": cpu_model()}
 
 
 def run_config(name: str, device, steps: int, warmup: int, variant: str = "default",
@@ -270,13 +300,127 @@ def run_config(name: str, device, steps: int, warmup: int, variant: str = "defau
         "layer_mfma_frac": round(work["layer_flops"] / (ms * 1e-3) / PEAK[c["precision"]], 4),
         "layer_hbm_frac": round(work["layer_bytes"] / (ms * 1e-3) / PEAK["hbm"], 4),
         "active_experts": work["active"],
+        "m_tiles": m_tiles(c, counts, variant, bool(layer.ops.features() & layer._lib.FEATURE_DECODE_TILES)),
         "weight_layout": layer.layout,
         "stage_ms": {k: round(v, 4) for k, v in m["stage_ms"].items()},
         "roofline": roofline(c, work, m["stage_ms"]["gmm1"],
-                             measured_traffic(name, variant if layer.layout == "EOI" or c["precision"] != "bf16"
-                                              else f"{variant}_EIO")),
+                             measured_traffic(name, variant, layer.layout)),
     }
     return res, layer
+
+
+# ------------------------------------------------------------------------------------------------
+# Profiles: the rocprofv3 commands behind profiles/ and their reduction to the committed summaries
+# ------------------------------------------------------------------------------------------------
+COPY_BYTES = 1 << 31  # calibration copy: reads and writes exactly this many bytes
+GMM1_KERNEL = re.compile(r"(gg_pp|grouped_gemm\w*)_kernel<.*, ([2-5])>\(")  # SwiGLU epilogues 2..5
+
+
+def profile_commands(workload: str, out: str = "$GRAFT_REPO_ROOT/gpurun_out/prof") -> dict:
+    """The commands (run from anywhere on the GPU box) whose output --summarize reduces; each counter
+    pass runs on its own, as rocprofv3 does not split counters over passes."""
+    root = "$GRAFT_REPO_ROOT"
+    pre = "cd /tmp && export TMPDIR=/tmp && "
+    bench = f"python3 {root}/bench.py --config {workload} --extra none --no-cpu"
+    d = f"{out}/{workload}"
+    cmds = {"kernel_trace": f"mkdir -p {d} && {pre}timeout -s KILL 300 rocprofv3 --kernel-trace --stats --output-format csv -d {d}/kt "
+                            f"-o run -- {bench} --steps 10 --warmup 3 > {d}/bench.json"}
+    for tag, counters in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE"), ("mfma", "MfmaUtil")):
+        cmds[tag] = (f"{pre}timeout -s KILL 300 rocprofv3 --pmc {counters} --output-format csv -d {d}/{tag} -o pmc -- "
+                     f"{bench} --steps 2 --warmup 1 > /dev/null")
+    return cmds
+
+
+def calibration_commands(out: str = "$GRAFT_REPO_ROOT/gpurun_out/prof") -> dict:
+    copy = (f"python3 -c \"import torch; a = torch.empty({COPY_BYTES}, dtype=torch.uint8, device='cuda'); "
+            f"b = torch.empty_like(a); b.copy_(a); torch.cuda.synchronize()\"")
+    return {tag: f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc {c} --output-format csv "
+                 f"-d {out}/copy/{tag} -o pmc -- {copy}"
+            for tag, c in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE"))}
+
+
+def _csv_rows(folder: str, suffix: str) -> list:
+    import csv
+    import glob
+    rows = []
+    for path in sorted(glob.glob(os.path.join(folder, "**", f"*{suffix}"), recursive=True)):
+        with open(path) as f:
+            rows += list(csv.DictReader(f))
+    if not rows:
+        raise FileNotFoundError(f"no *{suffix} under {folder}")
+    return rows
+
+
+def _counter_mean(folder: str, counter: str, match) -> float:
+    vals = [float(r["Counter_Value"]) for r in _csv_rows(folder, "counter_collection.csv")
+            if r["Counter_Name"] == counter and match(r["Kernel_Name"])]
+    if not vals:
+        raise ValueError(f"no {counter} samples of the kernel in {folder}")
+    return sum(vals) / len(vals)
+
+
+def summarize(workload: str, out: str, dest: str = os.path.join(ROOT, "profiles")) -> str:
+    """Reduce the outputs of profile_commands(workload) and calibration_commands() under ``out`` to
+    profiles/grouped_gemm_<workload>.txt and profiles/traffic_<workload>_<variant>_<layout>.json."""
+    d = os.path.join(out, workload)
+    with open(os.path.join(d, "bench.json")) as f:
+        line = json.loads([x for x in f.read().splitlines() if x.startswith("{")][-1])
+    stats = _csv_rows(os.path.join(d, "kt"), "kernel_stats.csv")
+    stats.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    gmm1 = [r for r in stats if GMM1_KERNEL.search(r["Name"])]
+    if not gmm1:
+        raise ValueError("no GMM1 (SwiGLU-epilogue grouped GEMM) kernel in the trace")
+    g1 = gmm1[0]["Name"]
+    is_g1 = lambda name: name == g1  # noqa: E731
+    copy_kib = COPY_BYTES / 1024.0
+    is_copy = lambda name: "copyBuffer" in name  # noqa: E731
+    fetch_factor = copy_kib / _counter_mean(os.path.join(out, "copy", "fetch"), "FETCH_SIZE", is_copy)
+    write_factor = copy_kib / _counter_mean(os.path.join(out, "copy", "write"), "WRITE_SIZE", is_copy)
+    fetch = _counter_mean(os.path.join(d, "fetch"), "FETCH_SIZE", is_g1)
+    write = _counter_mean(os.path.join(d, "write"), "WRITE_SIZE", is_g1)
+    mfma = _counter_mean(os.path.join(d, "mfma"), "MfmaUtil", is_g1)
+    traffic = (fetch * fetch_factor + write * write_factor) * 1024.0
+    cfg = line["config"]
+    variant, layout = cfg.get("gemm_variant", "default"), cfg.get("weight_layout", "EIO")
+    rf = line["roofline"]
+    avg_us = float(gmm1[0]["AverageNs"]) / 1e3
+    cmds = profile_commands(workload)
+    cal = calibration_commands()
+    lines = [f"# rocprofv3 summary: MoE layer forward, workload {workload} (GEMM variant {variant}, {layout} weights)",
+             "# commands (GPU box; $GRAFT_REPO_ROOT = the repository root there):"]
+    lines += [f"#   {k}: {v}" for k, v in cmds.items()]
+    lines += [f"#   copy calibration {k}: {v}" for k, v in cal.items()]
+    lines += [f"# reduced with: python3 bench.py --summarize {workload} --profile-dir <prof dir>", "",
+              "kernel trace (durations in microseconds; top 14 by total time)",
+              f"{'kernel':<90} {'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'total_ms':>10}"]
+    for r in stats[:14]:
+        lines.append(f"{r['Name'][:90]:<90} {int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>10.1f} "
+                     f"{float(r['MinNs']) / 1e3:>10.1f} {float(r['MaxNs']) / 1e3:>10.1f} "
+                     f"{float(r['TotalDurationNs']) / 1e6:>10.3f}")
+    alg = rf.get("algorithmic_bytes")
+    lines += ["", f"GMM1 kernel: {g1}",
+              f"  rocprofv3 average duration: {avg_us:.1f} us; bench HIP-event launch time: "
+              f"{rf.get('launch_ms', float('nan')) * 1e3:.1f} us",
+              f"  FETCH_SIZE {fetch:.0f} KiB/dispatch x {fetch_factor:.3f} (copy calibration: {COPY_BYTES} B copy reads "
+              f"{copy_kib / fetch_factor:.0f} KiB) ; WRITE_SIZE {write:.0f} KiB/dispatch x {write_factor:.3f}",
+              f"  HBM traffic per launch: {traffic / 1e9:.3f} GB; algorithmic bytes: "
+              f"{(alg or 0) / 1e9:.3f} GB; ratio {traffic / alg if alg else float('nan'):.3f}",
+              f"  MfmaUtil (MFMA busy / (GPU active cycles x SIMDs)): {mfma:.1f} %",
+              f"  roofline from rocprofv3 duration: {(alg or 0) / (avg_us * 1e-6) / 1e9:.1f} GB/s = "
+              f"{(alg or 0) / (avg_us * 1e-6) / PEAK['hbm']:.4f} of HBM peak",
+              "", f"bench line of the kernel-trace run: {json.dumps({k: line[k] for k in ('value', 'ms_per_step')})}",
+              f"roofline: {json.dumps(rf)}"]
+    os.makedirs(dest, exist_ok=True)
+    txt = os.path.join(dest, f"grouped_gemm_{workload}.txt")
+    with open(txt, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    with open(os.path.join(dest, f"traffic_{workload}_{variant}_{layout}.json"), "w") as f:
+        json.dump({"kernel": g1, "fetch_kib": round(fetch, 1), "fetch_factor": round(fetch_factor, 4),
+                   "write_kib": round(write, 1), "write_factor": round(write_factor, 4),
+                   "mfma_util_pct": round(mfma, 2), "rocprof_avg_us": round(avg_us, 1),
+                   "source": os.path.basename(txt)}, f, indent=1)
+        f.write("\n")
+    return txt
 
 
 def gemm_shapes(device, reps: int) -> dict:
@@ -347,7 +491,19 @@ def main() -> int:
                     help="MX expert-weight layout (EIO: the reference's col_data root; EOI: re-laid out once)")
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="time the DSv3-shape grouped GEMMs on their own per layout and variant (one JSON line)")
+    ap.add_argument("--profile-commands", metavar="WORKLOAD", default=None,
+                    help="print the rocprofv3 commands behind profiles/ for WORKLOAD ('copy': the calibration)")
+    ap.add_argument("--summarize", metavar="WORKLOAD", default=None,
+                    help="reduce the rocprofv3 output of --profile-commands WORKLOAD into profiles/")
+    ap.add_argument("--profile-dir", default=os.path.join(ROOT, "gpurun_out", "prof"))
     args = ap.parse_args()
+    if args.profile_commands is not None:
+        cmds = calibration_commands() if args.profile_commands == "copy" else profile_commands(args.profile_commands)
+        print("\n".join(cmds.values()))
+        return 0
+    if args.summarize is not None:
+        print(summarize(args.summarize, args.profile_dir))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X only: this build runs every expert on one GPU (EP=1) and has no "
               "multi-GPU path; run with --gpus 1.", file=sys.stderr)

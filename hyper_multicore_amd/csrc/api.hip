@@ -389,15 +389,19 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
     // SwiGLU output in fp32, then its MX quantisation into act (e4m3) and the code planes
     p1.C = ws + L.act_f32;
     p1.ldc = I;
+    // the quantisation belongs to GMM2's stage (as the token quantisation precedes GMM1's), so the
+    // GMM1 stage events bracket the GEMM kernel alone
     rc = mi355_grouped_gemm(p1, true, true, EPI_SWIGLU_F32, st, small);
     if (rc) return rc;
+    mark(2);
     rc = mi355_mx_quant_act((const float*)(ws + L.act_f32), T * K, I, (uint8_t*)(ws + L.act),
                             (uint8_t*)(ws + L.act_scale), T * K * 4, st);
+    if (rc) return rc;
   } else {
     rc = mi355_grouped_gemm(p1, mx, !eoi, mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16, st, small);
+    if (rc) return rc;
+    mark(2);
   }
-  if (rc) return rc;
-  mark(2);
   // GMM2: [R, I] x [I, H] -> y [R, H] bf16
   GGParams p2 = {};
   p2.variant = a.gemm_variant;

@@ -342,8 +342,9 @@ typedef struct MI355MoeForwardArgs {
   uint16_t* out;              /* [T, H] bf16 */
   int32_t* error_flag;        /* optional: set to 1 for ids outside [0, E) */
   /* Optional timing hooks (no reference counterpart): hipEvent_t handles recorded on `stream`
-   * at the stage boundaries [0] start, [1] after dispatch + MX activation quant, [2] after GMM1,
-   * [3] after GMM2, [4] after combine. num_stage_events may be 0..5. */
+   * at the stage boundaries [0] start, [1] after dispatch + MX activation quant, [2] after the GMM1
+   * kernel, [3] after GMM2 (including the MX quantisation of its input when that is a kernel of its
+   * own), [4] after combine. num_stage_events may be 0..5. */
   void* const* stage_events;
   int32_t num_stage_events;
   float swiglu_limit;         /* > 0: SwiGLU clamp limit L (BF16 only); 0: no clamp */
