@@ -106,13 +106,58 @@ def test_bench_traffic_record(tmp_path):
     import bench
     (tmp_path / "profiles").mkdir()
     rec = {"fetch_kib": 1000.0, "fetch_factor": 0.5, "write_kib": 10.0, "write_factor": 2.0}
-    (tmp_path / "profiles" / "traffic_dsv3_bf16_dv.json").write_text(json.dumps(rec))
-    assert bench.measured_traffic("dsv3_bf16", "dv", root=str(tmp_path)) == (500 + 20) * 1024
-    assert bench.measured_traffic("dsv3_bf16", "default", root=str(tmp_path)) is None
+    (tmp_path / "profiles" / "traffic_dsv3_bf16_dv_EOI.json").write_text(json.dumps(rec))
+    assert bench.measured_traffic("dsv3_bf16", "dv", "EOI", root=str(tmp_path)) == (500 + 20) * 1024
+    assert bench.measured_traffic("dsv3_bf16", "dv", "EIO", root=str(tmp_path)) is None
+    assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) is None
     c = bench.CONFIGS["dsv3_bf16"]
     work = {"g1_flops": 1e12, "g1_bytes": 1e10}
-    r = bench.roofline(c, work, 2.0, traffic=123)
-    assert r["traffic"] == 123 and r["bound"] == "hbm" and r["unit"] == "GB/s"
+    r = bench.roofline(c, work, 2.0, traffic=2e10)
+    assert r["traffic"] == 2e10 and r["bound"] == "hbm" and r["unit"] == "GB/s"
+    assert r["traffic_ratio"] == 2.0 and r["algorithmic_bytes"] == 1e10 and r["achieved"] == 5000.0
+
+
+def _write_csv(path, header, rows):
+    import csv
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(header)
+        w.writerows(rows)
+
+
+def test_bench_profile_summary(tmp_path):
+    """--summarize picks the SwiGLU-epilogue grouped GEMM as GMM1, scales its counters by what the same
+    counters read for the calibration copy, and writes the traffic record the bench line reads back."""
+    import json
+    import bench
+    out = tmp_path / "prof"
+    cnt = ["Kernel_Name", "Counter_Name", "Counter_Value"]
+    copy_kib = bench.COPY_BYTES / 1024
+    _write_csv(out / "copy" / "fetch" / "pmc_counter_collection.csv", cnt,
+               [["__amd_rocclr_copyBuffer", "FETCH_SIZE", copy_kib / 2], ["other", "FETCH_SIZE", 1.0]])
+    _write_csv(out / "copy" / "write" / "pmc_counter_collection.csv", cnt,
+               [["__amd_rocclr_copyBuffer", "WRITE_SIZE", copy_kib]])
+    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2>(GGParams)"
+    g2 = "void (anonymous namespace)::gg_pp_kernel<false, false, 0>(GGParams)"
+    d = out / "dsv3_bf16"
+    _write_csv(d / "fetch" / "pmc_counter_collection.csv", cnt,
+               [[g1, "FETCH_SIZE", 900.0], [g1, "FETCH_SIZE", 1100.0], [g2, "FETCH_SIZE", 5.0]])
+    _write_csv(d / "write" / "pmc_counter_collection.csv", cnt, [[g1, "WRITE_SIZE", 100.0]])
+    _write_csv(d / "mfma" / "pmc_counter_collection.csv", cnt, [[g1, "MfmaUtil", 40.0]])
+    st = ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs"]
+    _write_csv(d / "kt" / "run_kernel_stats.csv", st,
+               [[g2, 10, 3e7, 3e6, 30, 3e6, 3e6], [g1, 10, 6e7, 6e6, 60, 6e6, 6e6]])
+    line = {"value": 1.0, "ms_per_step": 9.0, "config": {"gemm_variant": "default", "weight_layout": "EOI"},
+            "roofline": {"algorithmic_bytes": 2048 * 1024, "launch_ms": 6.1}}
+    (d / "bench.json").write_text("[bench] noise\n" + json.dumps(line) + "\n")
+    txt = bench.summarize("dsv3_bf16", str(out), dest=str(tmp_path / "profiles"))
+    rec = json.loads((tmp_path / "profiles" / "traffic_dsv3_bf16_default_EOI.json").read_text())
+    assert rec["kernel"] == g1 and rec["fetch_kib"] == 1000.0 and rec["fetch_factor"] == 2.0
+    assert rec["write_factor"] == 1.0 and rec["rocprof_avg_us"] == 6000.0 and rec["mfma_util_pct"] == 40.0
+    assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) == (2000 + 100) * 1024
+    text = open(txt).read()
+    assert "ratio 1.025" in text and "rocprofv3 --pmc FETCH_SIZE" in text
 
 
 def _physical(root, shape):
