@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmi355moe.so"
 ABI_VERSION = 5
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
+NOALLOC_MAX_GROUPS = 4096
 SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 IDS_INT32, IDS_INT64 = 0, 1
 PRECISION = {"bf16": 0, "mxfp8": 1}
@@ -122,6 +123,8 @@ _SIGNATURES = [
     ("mi355moe_grouped_gemm_workspace_size", c_size_t, [c_int32]),
     ("mi355moe_grouped_gemm_bf16", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                              c_void_p, c_void_p, c_int32, c_void_p, c_size_t, c_void_p]),
+    ("mi355moe_grouped_gemm_bf16_noalloc", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32,
+                                                     c_int32, c_void_p, c_void_p, c_int32, c_void_p]),
     ("mi355moe_grouped_gemm_mxfp8", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
                                               c_int32, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_size_t,
                                               c_void_p]),

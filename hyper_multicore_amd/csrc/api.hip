@@ -5,6 +5,7 @@
 #include "gemm.h"
 #include <cmath>
 #include <algorithm>
+#include <mutex>
 #include "../../include/mi355moe.h"
 
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -149,18 +150,23 @@ extern "C" size_t mi355moe_grouped_gemm_workspace_size(int32_t num_groups) {
   return al256((size_t)(num_groups + 1) * 4);
 }
 
-extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim, const uint16_t* w,
-                                          int32_t layout, int32_t num_groups, int32_t ndim,
-                                          const int64_t* group_list, uint16_t* out, int32_t gemm_variant,
-                                          void* workspace, size_t workspace_size, void* stream) {
+// Argument checks of the bf16 grouped GEMM shared by both entry points (workspace aside).
+static int grouped_gemm_bf16_check(const uint16_t* x, int64_t rows, int32_t kdim, const uint16_t* w, int32_t layout,
+                                   int32_t num_groups, int32_t ndim, const int64_t* group_list, uint16_t* out,
+                                   int32_t gemm_variant) {
   if (!mi355_gg_variant_valid(gemm_variant)) return MI355MOE_EUNSUPPORTED;
   if (rows < 0 || kdim <= 0 || ndim <= 0 || num_groups <= 0 || num_groups > 4096) return MI355MOE_EINVAL;
   if (layout != MI355MOE_LAYOUT_EIO && layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   if (kdim % 64 || ndim % 8) return MI355MOE_EUNSUPPORTED;
   if (rows == 0) return MI355MOE_OK;
   if (x == nullptr || w == nullptr || group_list == nullptr || out == nullptr) return MI355MOE_EINVAL;
-  if (workspace == nullptr || workspace_size < mi355moe_grouped_gemm_workspace_size(num_groups)) return -4;
-  hipStream_t st = (hipStream_t)stream;
+  return MI355MOE_OK;
+}
+
+// Plans the tiles into tile_prefix ([num_groups + 1] int32, fully written) and launches the GEMM.
+static int grouped_gemm_bf16_launch(const uint16_t* x, int64_t rows, int32_t kdim, const uint16_t* w,
+                                    int32_t layout, int32_t num_groups, int32_t ndim, const int64_t* group_list,
+                                    uint16_t* out, int32_t gemm_variant, int32_t* tile_prefix, hipStream_t st) {
   GGParams p = {};
   p.variant = gemm_variant;
   p.A = (const uint8_t*)x;
@@ -176,13 +182,58 @@ extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32
   p.n_tiles = (ndim + mi355_gg_bn() - 1) / mi355_gg_bn();
   p.G = num_groups;
   p.group_list = group_list;
-  p.tile_prefix = (int32_t*)workspace;
+  p.tile_prefix = tile_prefix;
   p.C = out;
   p.ldc = ndim;
   const bool small = mi355_use_small_tiles(rows, num_groups, gemm_variant);
-  int rc = mi355_plan_tiles(group_list, num_groups, (int32_t*)workspace, st, small);
+  int rc = mi355_plan_tiles(group_list, num_groups, tile_prefix, st, small);
   if (rc) return rc;
   return mi355_grouped_gemm(p, false, layout == MI355MOE_LAYOUT_EIO, EPI_STORE_BF16, st, small);
+}
+
+extern "C" int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim, const uint16_t* w,
+                                          int32_t layout, int32_t num_groups, int32_t ndim,
+                                          const int64_t* group_list, uint16_t* out, int32_t gemm_variant,
+                                          void* workspace, size_t workspace_size, void* stream) {
+  int rc = grouped_gemm_bf16_check(x, rows, kdim, w, layout, num_groups, ndim, group_list, out, gemm_variant);
+  if (rc || rows == 0) return rc;
+  if (workspace == nullptr || workspace_size < mi355moe_grouped_gemm_workspace_size(num_groups)) return -4;
+  return grouped_gemm_bf16_launch(x, rows, kdim, w, layout, num_groups, ndim, group_list, out, gemm_variant,
+                                  (int32_t*)workspace, (hipStream_t)stream);
+}
+
+// The no-allocation variant's tile plan: one array per GPU (its own copy at its own address),
+// held until the process ends. Host code never passes `scratch` itself (its host-side name is not a
+// device address); it uses the per-device address from hipGetSymbolAddress below.
+static __device__ __align__(256) int32_t scratch[MI355MOE_NOALLOC_MAX_GROUPS + 1];
+static constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices] = {};
+static std::mutex g_scratch_mutex;
+
+// The current device's address of `scratch`, looked up once per device with that device current.
+static int32_t* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return (int32_t*)g_scratch_ptr[dev];
+}
+
+extern "C" int mi355moe_grouped_gemm_bf16_noalloc(const uint16_t* x, int64_t rows, int32_t kdim, const uint16_t* w,
+                                                  int32_t layout, int32_t num_groups, int32_t ndim,
+                                                  const int64_t* group_list, uint16_t* out, int32_t gemm_variant,
+                                                  void* stream) {
+  if (num_groups > MI355MOE_NOALLOC_MAX_GROUPS) return MI355MOE_EWORKSPACE;
+  int rc = grouped_gemm_bf16_check(x, rows, kdim, w, layout, num_groups, ndim, group_list, out, gemm_variant);
+  if (rc || rows == 0) return rc;
+  int32_t* plan = scratch_on_current_device();
+  if (plan == nullptr) return MI355MOE_ELAUNCH;
+  return grouped_gemm_bf16_launch(x, rows, kdim, w, layout, num_groups, ndim, group_list, out, gemm_variant, plan,
+                                  (hipStream_t)stream);
 }
 
 extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64_t rows, int32_t kdim,

@@ -73,3 +73,4 @@ MI355_DEV int wave_shfl_xor(int v, int m) { return __shfl_xor(v, m, 64); }
 #define MI355MOE_EINVAL -1
 #define MI355MOE_ELAUNCH -2
 #define MI355MOE_EUNSUPPORTED -3
+#define MI355MOE_EWORKSPACE -4

@@ -286,6 +286,24 @@ int mi355moe_grouped_gemm_bf16(const uint16_t* x, int64_t rows, int32_t kdim,
                                void* workspace, size_t workspace_size, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * mi355moe_grouped_gemm_bf16 without a workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Same arguments and results as mi355moe_grouped_gemm_bf16 (bit-
+ * identical), minus the workspace: the tile plan lives in a static device array of
+ * MI355MOE_NOALLOC_MAX_GROUPS + 1 int32 per GPU (16 KB, held until the process ends; each call
+ * writes all of the plan it reads, so no state carries over). num_groups above the maximum answers
+ * MI355MOE_EWORKSPACE_CODE. Calls no hipMalloc / hipFree. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other host threads) race and must be
+ * ordered by the caller. The first call on a device looks the array's address up (hipGetSymbolAddress)
+ * with that device current.
+ */
+#define MI355MOE_NOALLOC_MAX_GROUPS 4096
+int mi355moe_grouped_gemm_bf16_noalloc(const uint16_t* x, int64_t rows, int32_t kdim,
+                                       const uint16_t* w, int32_t layout, int32_t num_groups,
+                                       int32_t ndim, const int64_t* group_list, uint16_t* out,
+                                       int32_t gemm_variant, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * MXFP8 grouped GEMM: out[r, :] = dequant(xq[r, :]) @ dequant(W_g), bf16 output, fp32 accumulate.
  * xq [rows, K] e4m3 with x_scale [rows, K/32] e8m0 (blocks along K). Weights by layout:
  *   EIO: w_data = col_data [G, K, N] e4m3, w_scale = col_scale [G, K/64, N, 2] (the forward MX
