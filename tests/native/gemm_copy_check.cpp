@@ -82,10 +82,16 @@ static void free_all() {
   for (auto& a : g_allocs) free(a.p);
   g_allocs.clear();
 }
+// The host stand-in of the library's static device array (`scratch` of the no-allocation entry point):
+// hipGetSymbolAddress answers this address, which stays valid for the whole run, as the device array
+// does for the process.
+alignas(256) static uint8_t g_symbol_scratch[(MI355MOE_NOALLOC_MAX_GROUPS + 1) * 4];
+static const Alloc g_symbol_alloc = {g_symbol_scratch, sizeof(g_symbol_scratch), "scratch (static device array)"};
 static const Alloc* find_alloc(const void* q, size_t sz) {
   const uint8_t* b = (const uint8_t*)q;
   for (const auto& a : g_allocs)
     if (b >= a.p && b + sz <= a.p + a.n) return &a;
+  if (b >= g_symbol_alloc.p && b + sz <= g_symbol_alloc.p + g_symbol_alloc.n) return &g_symbol_alloc;
   return nullptr;
 }
 static const Alloc* alloc_of(const void* q) { return find_alloc(q, 1); }
@@ -100,6 +106,13 @@ void** __hipRegisterFatBinary(const void*) {
 }
 void __hipRegisterFunction(void**, const void*, char*, const char*, unsigned int, uint3*, uint3*, dim3*, dim3*, int*) {}
 void __hipUnregisterFatBinary(void**) {}
+void __hipRegisterVar(void**, void*, char*, const char*, int, size_t, int, int) {}
+static long g_symbol_lookups = 0;
+hipError_t hipGetSymbolAddress(void** ptr, const void*) {
+  ++g_symbol_lookups;
+  *ptr = g_symbol_scratch;
+  return hipSuccess;
+}
 hipError_t __hipPushCallConfiguration(dim3, dim3, size_t, hipStream_t) { return hipSuccess; }
 hipError_t __hipPopCallConfiguration(dim3* g, dim3* b, size_t* s, hipStream_t* st) {
   *g = dim3(1);
@@ -1676,7 +1689,7 @@ static int expect_rc(int rc, int want, const char* what) {
   return rc;
 }
 
-static void gemm_bf16(std::vector<int> counts, int K, int N, int layout) {
+static void gemm_bf16(std::vector<int> counts, int K, int N, int layout, bool noalloc = false) {
   const int G = (int)counts.size();
   const auto glv = cumsum(counts);
   const int64_t rows = glv.back();
@@ -1696,9 +1709,14 @@ static void gemm_bf16(std::vector<int> counts, int K, int N, int layout) {
   g_expect.A = x;
   g_expect.a_row_bytes = (int64_t)K * 2;
   g_expect.B = w;
-  expect_rc(mi355moe_grouped_gemm_bf16((const uint16_t*)x, rows, K, (const uint16_t*)w, layout, G, N, gl,
-                                       (uint16_t*)out, g_variant, ws, wsz, nullptr),
-            0, "grouped_gemm_bf16");
+  if (noalloc)
+    expect_rc(mi355moe_grouped_gemm_bf16_noalloc((const uint16_t*)x, rows, K, (const uint16_t*)w, layout, G, N, gl,
+                                                 (uint16_t*)out, g_variant, nullptr),
+              0, "grouped_gemm_bf16_noalloc");
+  else
+    expect_rc(mi355moe_grouped_gemm_bf16((const uint16_t*)x, rows, K, (const uint16_t*)w, layout, G, N, gl,
+                                         (uint16_t*)out, g_variant, ws, wsz, nullptr),
+              0, "grouped_gemm_bf16");
   g_expect = Expect();
 }
 
@@ -2042,6 +2060,13 @@ static std::vector<Scenario> scenarios() {
                  std::vector<int> c(1100, 0);
                  for (size_t i = 0; i < c.size(); i += 3) c[i] = 1 + (int)(i % 7);
                  gemm_bf16(c, 64, 256, L_EIO);
+               }});
+  // the no-allocation entry point: the tile plan in the static array, looked up once; a second,
+  // smaller call reads only what it planned
+  s.push_back({"gemm_bf16_noalloc", [=] {
+                 gemm_bf16({300, 0, 513, 77, 1}, 512, 512, L_EIO, true);
+                 gemm_bf16({5, 40}, 256, 256, L_EOI, true);
+                 if (g_symbol_lookups != 1) CHECK_FAIL("scratch address looked up %ld times", g_symbol_lookups);
                }});
   // MegaMoE forward, bf16 and MX, both layouts; prefill-like and decode-like routing
   s.push_back({"moe_bf16_eio", [=] { moe_forward(96, 4, 16, 512, 256, BF, L_EIO, 1.1); }});

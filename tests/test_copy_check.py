@@ -43,7 +43,7 @@ SCENARIOS = [
     "dv_gemm_mx", "dv_gemm_mx_long_k", "dv_gemm_bf16_decode_big", "dv_moe_bf16_eoi", "dv_moe_mx_eoi",
     "dv_gemm_bf16_many_groups", "dv_gemm_bf16_narrow", "sp_gemm_mx_many_groups", "sp_gemm_mx_narrow",
     "emu_dv_bf16_narrow", "emu_dv_bf16", "emu_dv_bf16_one_turn", "emu_dv_mx", "emu_dv_mx_long_k", "emu_wgrad_bf16",
-    "emu_wgrad_mx", "gemm_bf16_many_groups", "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio",
+    "emu_wgrad_mx", "gemm_bf16_many_groups", "gemm_bf16_noalloc", "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio",
     "moe_mx_eoi", "moe_mx_eoi_prefill", "moe_mx_eio_prefill", "moe_bf16_numerics_clamp",
     "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16",
     "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill"
