@@ -146,13 +146,18 @@ __device__ __forceinline__ void decode(const GGParams& p, const uint8_t* smem, i
 // Copy sources of one work item: wave-uniform bases of stage 0 (stage k adds k * the stride) and
 // per-lane 32-bit offsets (the activations, one group's weights and the scale arrays are below
 // 4 GiB, which mi355_gg_pp_applies checks).
+// Only the gathered activation offsets are kept per lane; the weight and scale offsets are functions
+// of the lane and the item's n-tile, recomputed for every stage (holding them across the K loop
+// pushed the MX kernels past their registers, and a spill reload between the copies waits for all
+// of them).
 struct Plan {
   const uint8_t* a_base;
   const uint8_t* b_base;
   const uint8_t* s_base;   // MX: activation code plane run (every wave)
   const uint8_t* bs_base;  // MX: the group's weight scales (waves 0-3; waves 4-7 repeat them)
-  uint32_t ao[CPW], bo[CPW], so, bso;
+  uint32_t ao[CPW];
   int a_copies;  // activation copies of this wave (8-row groups past the item's rows are skipped)
+  int nt;        // the item's n-tile
   int64_t b_stride, s_stride, b_scale_stride;
 };
 
@@ -179,56 +184,51 @@ __device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int
     pl.a_copies = uni(n < 0 ? 0 : (n > CPW ? CPW : n));
   }
   pl.b_base = uni_ptr(p.B + (int64_t)it.g * p.b_group_stride);
-#pragma unroll
-  for (int j = 0; j < CPW; ++j) {
-    const int i = wave * CPW + j;
-    if constexpr (!B_KN) {
-      const int r = row_of(i, lane);
-      int wc = tile_col(r, it.nt, p.N, SWIGLU);
-      if (wc >= p.Ntot) wc = p.Ntot - 1;
-      pl.bo[j] = (uint32_t)((int64_t)wc * p.b_row_bytes + chunk_of(r, lane) * 16);
-    } else if constexpr (MX) {
-      const int L16 = i * 64 + lane;  // K rows of 256 bytes: copy i covers K rows 4 i ..+3
-      const int k = L16 >> 4;
-      const int c = (L16 & 15) ^ (k & 15);
-      int wc = tile_col(c * 16, it.nt, p.N, SWIGLU);
-      if (wc > p.Ntot - 16) wc = p.Ntot - 16;
-      pl.bo[j] = (uint32_t)((int64_t)k * p.b_row_bytes + wc);
-    } else {
-      const int L16 = i * 64 + lane;  // K rows of 512 bytes: copy i covers K rows 2 i, 2 i + 1
-      const int k = L16 >> 5;
-      const int c = (L16 & 31) ^ ((k & 7) << 1);
-      int wc = tile_col(c * 8, it.nt, p.N, SWIGLU);
-      if (wc > p.Ntot - 8) wc = p.Ntot - 8;
-      pl.bo[j] = (uint32_t)((int64_t)k * p.b_row_bytes + (int64_t)wc * 2);
-    }
-  }
+  pl.nt = uni(it.nt);
   pl.b_stride = B_KN ? (int64_t)(KB / ESIZE) * p.b_row_bytes : KB;
   pl.s_base = pl.a_base;
   pl.bs_base = pl.a_base;
-  pl.so = 0;
-  pl.bso = 0;
   pl.s_stride = 0;
   if constexpr (MX) {
     // code plane wave / 2, bytes 256 (wave % 2) + 4 lane from the 4-aligned row at or below row0
     // (rows past the item read the next rows or the planes' padding)
     pl.s_base = uni_ptr(p.a_scale + (wave >> 1) * (p.a_scale_stage_stride >> 2) + (it.row0 & ~(int64_t)3));
-    pl.so = (uint32_t)((wave & 1) * 256 + lane * 4);
     pl.s_stride = p.a_scale_stage_stride;
-    // col_scale [G, K/64, Ntot, 2]: wave w (and w + 4) copies 64-K step (w >> 1) & 1, tile columns
-    // 128 (w & 1) ..+127
-    const int st = (wave >> 1) & 1;
-    const int j = (wave & 1) * 128 + lane * 2;
-    int wc = tile_col(j, it.nt, p.N, SWIGLU);
-    if (wc > p.Ntot - 2) wc = p.Ntot - 2;
     pl.bs_base = uni_ptr(p.b_scale + (int64_t)it.g * p.b_scale_group_stride);
-    pl.bso = (uint32_t)(((int64_t)st * p.Ntot + wc) * 2);
     pl.b_scale_stride = (int64_t)p.Ntot * 4;  // two 64-K steps per stage
   }
 }
 
-template <bool MX>
-__device__ __forceinline__ void issue_stage(const Plan& pl, int k, uint32_t slot, int wave) {
+template <bool MX, bool B_KN, bool SWIGLU>
+__device__ __forceinline__ uint32_t b_off(const GGParams& p, int nt, int i, int lane) {
+  if constexpr (!B_KN) {  // K-contiguous weights: like the activations, one weight row per tile column
+    const int r = row_of(i, lane);
+    int wc = tile_col(r, nt, p.N, SWIGLU);
+    if (wc >= p.Ntot) wc = p.Ntot - 1;
+    return (uint32_t)wc * (uint32_t)p.b_row_bytes + (uint32_t)(chunk_of(r, lane) * 16);
+  } else if constexpr (MX) {
+    const int L16 = i * 64 + lane;  // K rows of 256 bytes: copy i covers K rows 4 i ..+3
+    const int k = L16 >> 4;
+    const int c = (L16 & 15) ^ (k & 15);
+    int wc = tile_col(c * 16, nt, p.N, SWIGLU);
+    if (wc > p.Ntot - 16) wc = p.Ntot - 16;
+    return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc;
+  } else {
+    const int L16 = i * 64 + lane;  // K rows of 512 bytes: copy i covers K rows 2 i, 2 i + 1
+    const int k = L16 >> 5;
+    const int c = (L16 & 31) ^ ((k & 7) << 1);
+    int wc = tile_col(c * 8, nt, p.N, SWIGLU);
+    if (wc > p.Ntot - 8) wc = p.Ntot - 8;
+    return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc * 2u;
+  }
+}
+
+// `lane` is an opaque copy made per stage, so that the offsets derived from it are recomputed here
+// rather than hoisted out of the K loop into registers.
+template <bool MX, bool B_KN, bool SWIGLU>
+__device__ __forceinline__ void issue_stage(const GGParams& p, const Plan& pl, int k, uint32_t slot, int wave,
+                                            int lane) {
+  asm volatile("" : "+v"(lane));
   const uint8_t* ab = uni_ptr(pl.a_base + (int64_t)k * KB);
   const uint8_t* bb = uni_ptr(pl.b_base + (int64_t)k * pl.b_stride);
   // (the waits are for all outstanding copies, so a wave may issue fewer; LDS rows that are not
@@ -237,10 +237,18 @@ __device__ __forceinline__ void issue_stage(const Plan& pl, int k, uint32_t slot
   for (int j = 0; j < CPW; ++j)
     if (j < pl.a_copies) dma16(ab, pl.ao[j], uni(slot + (wave * CPW + j) * 1024));
 #pragma unroll
-  for (int j = 0; j < CPW; ++j) dma16(bb, pl.bo[j], uni(slot + B_OFF + (wave * CPW + j) * 1024));
+  for (int j = 0; j < CPW; ++j)
+    dma16(bb, b_off<MX, B_KN, SWIGLU>(p, pl.nt, wave * CPW + j, lane), uni(slot + B_OFF + (wave * CPW + j) * 1024));
   if constexpr (MX) {
-    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), pl.so, uni(slot + AS_OFF + (wave >> 1) * AS_PLANE + (wave & 1) * 256));
-    dma4(uni_ptr(pl.bs_base + (int64_t)k * pl.b_scale_stride), pl.bso,
+    // activation code planes: plane wave / 2, bytes 256 (wave % 2) + 4 lane of the item's run;
+    // col_scale [G, K/64, Ntot, 2]: wave w (and w + 4) copies 64-K step (w >> 1) & 1, tile columns
+    // 128 (w & 1) ..+127
+    const uint32_t so = (uint32_t)((wave & 1) * 256 + lane * 4);
+    int wc = tile_col((wave & 1) * 128 + lane * 2, pl.nt, p.N, SWIGLU);
+    if (wc > p.Ntot - 2) wc = p.Ntot - 2;
+    const uint32_t bso = (uint32_t)((((wave >> 1) & 1) * p.Ntot + wc) * 2);
+    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), so, uni(slot + AS_OFF + (wave >> 1) * AS_PLANE + (wave & 1) * 256));
+    dma4(uni_ptr(pl.bs_base + (int64_t)k * pl.b_scale_stride), bso,
          uni(slot + BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256));
   }
 }
@@ -475,7 +483,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   Plan pl;
   make_plan<MX, B_KN, SWIGLU>(p, ci, wave, lane, pl);
   auto issue_next = [&](int q) {
-    issue_stage<MX>(pl, ck, lds0 + (uint32_t)((q % S) * SLOT), wave);
+    issue_stage<MX, B_KN, SWIGLU>(p, pl, ck, lds0 + (uint32_t)((q % S) * SLOT), wave, lane);
     if (++ck == nk) {
       if (cL + grid < total) {
         cL += grid;

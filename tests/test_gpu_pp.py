@@ -37,15 +37,17 @@ def _variant(name):
         ops.set_gemm_variant(prev)
 
 
+VARIANTS = ["pp"]
 COUNTS = [[100, 0, 300, 1, 129], [0, 0, 7], [256] * 4, [3, 40, 0, 513], [1], [600, 255, 257]]
 
 
 @pytest.mark.parametrize("layout", ["EOI", "EIO"])
 @pytest.mark.parametrize("Kd", [256, 2048])
 @pytest.mark.parametrize("counts", COUNTS)
-def test_grouped_gemm_bf16_pp_matches_default(gpu, counts, Kd, layout):
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_grouped_gemm_bf16_pp_matches_default(gpu, variant, counts, Kd, layout):
     from hyper_multicore_amd import ops
-    print(f"[pp] bf16 {layout} K={Kd} counts={counts}", flush=True)
+    print(f"[pp] {variant} bf16 {layout} K={Kd} counts={counts}", flush=True)
     g = _seed(sum(counts) + Kd + (layout == "EIO"))
     G, N = len(counts), 768
     rows = sum(counts)
@@ -55,7 +57,7 @@ def test_grouped_gemm_bf16_pp_matches_default(gpu, counts, Kd, layout):
     gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
     with _variant("w4"):
         out_def = ops.grouped_gemm_bf16(x.to(gpu), wd, gl, layout).cpu()
-    with _variant("pp"):
+    with _variant(variant):
         out_pp = ops.grouped_gemm_bf16(x.to(gpu), wd, gl, layout).cpu()
     assert torch.equal(out_pp, out_def)
     starts = [0, *gl.cpu().tolist()]
@@ -64,7 +66,8 @@ def test_grouped_gemm_bf16_pp_matches_default(gpu, counts, Kd, layout):
 
 
 @pytest.mark.parametrize("layout", ["EOI", "EIO"])
-def test_moe_forward_bf16_pp_matches_default(gpu, layout):
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_moe_forward_bf16_pp_matches_default(gpu, variant, layout):
     from hyper_multicore_amd import ops
     T, H, I, E, K = 700, 1024, 512, 16, 4
     print(f"[pp] moe_forward bf16 {layout}", flush=True)
@@ -82,7 +85,7 @@ def test_moe_forward_bf16_pp_matches_default(gpu, layout):
     args = dict(num_experts=E, intermediate_size=I, layout=layout)
     with _variant("w4"):
         out_def = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d, w2d, **args).cpu()
-    with _variant("pp"):
+    with _variant(variant):
         out_pp = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1d, w2d, **args).cpu()
     assert torch.equal(out_pp, out_def)
     ref = orc.expert_forward_reference(x, ids, probs, w1, w2, layout="EIO")
@@ -90,7 +93,8 @@ def test_moe_forward_bf16_pp_matches_default(gpu, layout):
 
 
 @pytest.mark.parametrize("T,H,I,E,K", [(700, 1024, 512, 16, 4), (64, 1024, 256, 64, 8), (300, 2048, 384, 8, 2)])
-def test_moe_forward_mxfp8_pp_matches_w4(gpu, T, H, I, E, K):
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_moe_forward_mxfp8_pp_matches_w4(gpu, variant, T, H, I, E, K):
     """MXFP8 forward on the 8-wave GEMMs (stage-major activation scales, col_data / col_scale weights)
     equals the 4-wave path bit for bit, and the MX-emulating oracle to the MX bar."""
     from hyper_multicore_amd import ops
@@ -108,7 +112,7 @@ def test_moe_forward_mxfp8_pp_matches_w4(gpu, T, H, I, E, K):
     ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8))
     with _variant("w4"):
         out_w4 = ops.moe_forward(*ins, **args).cpu()
-    with _variant("pp"):
+    with _variant(variant):
         out_pp = ops.moe_forward(*ins, **args).cpu()
     assert torch.equal(out_pp, out_w4)
     ref = orc.expert_forward_reference(x, ids, probs, d1.cpu().view(torch.uint8), d2.cpu().view(torch.uint8),
@@ -117,7 +121,8 @@ def test_moe_forward_mxfp8_pp_matches_w4(gpu, T, H, I, E, K):
 
 
 @pytest.mark.parametrize("precision", ["bf16", "mxfp8"])
-def test_moe_forward_decode_shape_pp(gpu, precision):
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_moe_forward_decode_shape_pp(gpu, variant, precision):
     """Decode shape (a few routed rows per expert, many empty experts) on the 8-wave GEMMs."""
     from hyper_multicore_amd import ops
     T, H, I, E, K = 16, 2048, 512, 64, 8
@@ -138,7 +143,7 @@ def test_moe_forward_decode_shape_pp(gpu, precision):
     ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), *wts)
     with _variant("w4"):
         out_w4 = ops.moe_forward(*ins, **args).cpu()
-    with _variant("pp"):
+    with _variant(variant):
         out_pp = ops.moe_forward(*ins, **args).cpu()
     assert torch.equal(out_pp, out_w4)
     if precision == "bf16":
