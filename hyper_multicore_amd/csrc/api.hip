@@ -169,6 +169,7 @@ static int grouped_gemm_bf16_launch(const uint16_t* x, int64_t rows, int32_t kdi
                                     uint16_t* out, int32_t gemm_variant, int32_t* tile_prefix, hipStream_t st) {
   GGParams p = {};
   p.variant = gemm_variant;
+  p.rows_hint = rows;
   p.A = (const uint8_t*)x;
   p.lda_bytes = (int64_t)kdim * 2;
   p.a_bytes = rows * kdim * 2;
@@ -404,6 +405,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   // GMM1: [R, H] x [H, 2I] -> SwiGLU -> act [R, I]
   GGParams p1 = {};
   p1.variant = a.gemm_variant;
+  p1.rows_hint = T * K;
   p1.A = a1;
   p1.lda_bytes = (int64_t)H * esize;
   p1.a_bytes = T * H * esize;
@@ -456,6 +458,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   // GMM2: [R, I] x [I, H] -> y [R, H] bf16
   GGParams p2 = {};
   p2.variant = a.gemm_variant;
+  p2.rows_hint = T * K;
   p2.A = (const uint8_t*)(ws + L.act);
   p2.lda_bytes = (int64_t)I * esize;
   p2.a_bytes = T * K * I * esize;

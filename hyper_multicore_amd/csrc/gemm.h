@@ -61,6 +61,9 @@ struct GGParams {
   int32_t a_scale_routed;
   // Tile-configuration variant of this call (MI355_GG_VARIANT_*; 0: the default).
   int32_t variant;
+  // Rows of the whole GEMM when the caller knows them (0: not given); the 8-wave bf16 configuration
+  // picks its tile height from their average per group.
+  int64_t rows_hint;
 };
 
 

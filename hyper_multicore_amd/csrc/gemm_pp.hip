@@ -5,10 +5,13 @@
 // workgroup 8 * slot + xcd, so each XCD runs a contiguous run of items (m fastest) and the n-tiles
 // that re-read one expert's activation rows run at the same time on one XCD and share its L2.
 //
-// Workgroup: 512 threads = 8 wavefronts, two per SIMD. Wave w computes rows 128 * (w / 4) ..+127
-// and columns 64 * (w % 4) ..+63 of the 256 x 256 tile (4 x 2 blocks of 32 x 32; bf16
-// v_mfma_f32_32x32x16_bf16, MXFP8 v_mfma_scale_f32_32x32x64_f8f6f4). The waves form two groups,
-// 0-3 and 4-7, one wave of each on every SIMD.
+// Workgroup: 512 threads = 8 wavefronts, two per SIMD. Tiles are BM x 256 (BM = 320 for bf16, 256
+// for MXFP8). The waves form two groups, 0-3 and 4-7, one wave of each on every SIMD; wave w
+// computes columns 64 * (w % 4) ..+63 of the 32-row blocks 2 mi + w / 4 (mi < BM / 64), 2 x BM / 64
+// blocks of 32 x 32 (bf16 v_mfma_f32_32x32x16_bf16, MXFP8 v_mfma_scale_f32_32x32x64_f8f6f4). The row
+// blocks alternate between the groups and the activation copies between the waves, so a tile that
+// is not full keeps the two groups and the eight waves evenly loaded; bf16 waves skip the MFMAs of
+// row blocks past the item's rows.
 //
 // K stages are 128 bytes per row (64 bf16 or 128 e4m3): whole 128-byte lines per row and stage,
 // which the memory system streams markedly faster than half lines when one operand is re-read from
@@ -46,27 +49,45 @@
 
 namespace {
 
-constexpr int BM = 256, BN = 256;
+constexpr int BN = 256;
 constexpr int KB = 128;  // bytes of K per row and stage
 constexpr int S = 2;     // ring slots
 constexpr int WAVES = 8, THREADS = 64 * WAVES;
-constexpr int WM = 128, WN = 64, MI = WM / 32, NI = WN / 32;
+constexpr int WN = 64, NI = WN / 32;
 // MX scales of a stage: 4 activation code planes of 512 bytes (the 256 tile rows from the 4-aligned
 // row at or below the first one), 2 x 256 weight code pairs
 constexpr int AS_PLANE = 512;
-constexpr int A_BYTES = BM * KB, B_BYTES = BN * KB, AS_BYTES = 4 * AS_PLANE, BS_BYTES = 2 * BN * 2;
-constexpr int B_OFF = A_BYTES, AS_OFF = B_OFF + B_BYTES, BS_OFF = AS_OFF + AS_BYTES;
-constexpr int SLOT = BS_OFF + BS_BYTES;
-constexpr int PREFIX_OFF = S * SLOT;
-constexpr int PREFIX_MAX = 1024;  // groups whose tile prefix and row ends are kept in LDS
-constexpr int ROWS_OFF = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
-constexpr int EPI_BLOCK = 32 * 64;  // a wave's epilogue staging: one 32 x 32 bf16 block
-constexpr int EPI_OFF = (ROWS_OFF + PREFIX_MAX * 4 + 15) & ~15;
-constexpr int TOTAL = EPI_OFF + WAVES * EPI_BLOCK;
-constexpr int CPW = A_BYTES / 1024 / WAVES;  // 1 KB copies per operand, wave and stage
-static_assert(TOTAL <= 160 * 1024, "LDS budget");
-static_assert(SLOT % 16 == 0, "copy destinations are 16-byte aligned");
-static_assert(CPW == 4 && B_BYTES / 1024 / WAVES == CPW, "four 1 KB copies per operand and wave");
+constexpr int B_BYTES = BN * KB, AS_BYTES = 4 * AS_PLANE, BS_BYTES = 2 * BN * 2;
+constexpr int CPW_B = B_BYTES / 1024 / WAVES;  // 1 KB weight copies per wave and stage
+static_assert(CPW_B == 4, "four 1 KB weight copies per wave");
+
+// Tile height and LDS layout. Tiles are 256 rows, or 320 for bf16 GEMMs whose groups average at most
+// 320 rows (TALL): each m-tile streams its group's weights, whose lines miss L2, and the
+// workgroup's memory requests in flight are what bounds the kernel, so an expert of 257..320 routed
+// rows (DeepSeek-V3 prefill routes 256 on average, with a wide spread) is one m-tile instead of a
+// full one and a short one that streams the weights again. When groups are large multiples of 256
+// rows the fifth row block costs more than the tiles it saves. MX tiles stay 256 rows (no registers
+// left for a fifth row block).
+template <bool MX_, bool TALL>
+struct Cfg {
+  static constexpr bool MX = MX_;
+  static constexpr int BM = (MX || !TALL) ? 256 : 320;
+  static constexpr int WM = BM / 2, MI = WM / 32;  // rows per wave group, 32-row blocks per wave
+  static constexpr int A_BYTES = BM * KB;
+  static constexpr int CPW_A = A_BYTES / 1024 / WAVES;  // 1 KB activation copies per wave and stage
+  static constexpr int B_OFF = A_BYTES, AS_OFF = B_OFF + B_BYTES, BS_OFF = AS_OFF + AS_BYTES;
+  static constexpr int SLOT = MX ? BS_OFF + BS_BYTES : AS_OFF;
+  static constexpr int PREFIX_OFF = S * SLOT;
+  static constexpr int PREFIX_MAX = BM > 256 ? 512 : 1024;  // groups whose tile prefix and row ends are in LDS
+  static constexpr int ROWS_OFF = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
+  // a wave's epilogue staging: 16 rows of a 32-column bf16 block (MX: 16 rows of 32 fp32 columns)
+  static constexpr int EPI_BLOCK = MX ? 2048 : 1024;
+  static constexpr int EPI_OFF = (ROWS_OFF + PREFIX_MAX * 4 + 15) & ~15;
+  static constexpr int TOTAL = EPI_OFF + WAVES * EPI_BLOCK;
+  static_assert(TOTAL <= 160 * 1024, "LDS budget");
+  static_assert(SLOT % 16 == 0, "copy destinations are 16-byte aligned");
+  static_assert(A_BYTES % (1024 * WAVES) == 0, "whole 1 KB activation copies per wave");
+};
 
 // Tile column j (0..255) -> weight column; SwiGLU: wave tile q's 64 columns are gate columns
 // nt * 128 + 32 q .. +31, then the up columns I + the same.
@@ -112,7 +133,7 @@ __device__ __forceinline__ void barrier() {
 
 struct Item {
   int64_t row0;  // first routed row of the tile
-  int rows;      // valid rows (1..256)
+  int rows;      // valid rows (1..BM)
   int nt;        // n-tile
   int g;         // group
 };
@@ -121,9 +142,11 @@ struct Item {
 
 // Work item L from the tile prefix and the groups' row ends, both in LDS (LDS reads only: a global
 // or generic load here would make the wave wait for all of its outstanding copies).
+template <class C>
 __device__ __forceinline__ void decode(const GGParams& p, const uint8_t* smem, int L, Item& it) {
-  const __attribute__((address_space(3))) int32_t* prefix = LDSP(int32_t, smem + PREFIX_OFF);
-  const __attribute__((address_space(3))) int32_t* rows = LDSP(int32_t, smem + ROWS_OFF);
+  constexpr int BM = C::BM;
+  const __attribute__((address_space(3))) int32_t* prefix = LDSP(int32_t, smem + C::PREFIX_OFF);
+  const __attribute__((address_space(3))) int32_t* rows = LDSP(int32_t, smem + C::ROWS_OFF);
   int lo = 0, hi = p.G - 1;
   while (lo < hi) {  // largest g with prefix[g] * n_tiles <= L
     const int mid = (lo + hi + 1) >> 1;
@@ -150,28 +173,31 @@ __device__ __forceinline__ void decode(const GGParams& p, const uint8_t* smem, i
 // of the lane and the item's n-tile, recomputed for every stage (holding them across the K loop
 // pushed the MX kernels past their registers, and a spill reload between the copies waits for all
 // of them).
+template <int CPW_A>
 struct Plan {
   const uint8_t* a_base;
   const uint8_t* b_base;
   const uint8_t* s_base;   // MX: activation code plane run (every wave)
   const uint8_t* bs_base;  // MX: the group's weight scales (waves 0-3; waves 4-7 repeat them)
-  uint32_t ao[CPW];
+  uint32_t ao[CPW_A];
   int a_copies;  // activation copies of this wave (8-row groups past the item's rows are skipped)
   int nt;        // the item's n-tile
   int64_t b_stride, s_stride, b_scale_stride;
 };
 
-// Activation and EOI-weight copies: copy i (0..31) of a stage covers rows 8 i ..+7, lane l row
+// Activation and EOI-weight copies: copy i of a stage covers rows 8 i ..+7, lane l row
 // 8 i + l / 8 and LDS position l % 8, which holds chunk (l % 8) ^ ((row >> 1) & 7).
 __device__ __forceinline__ int row_of(int i, int lane) { return i * 8 + (lane >> 3); }
 __device__ __forceinline__ int chunk_of(int r, int lane) { return (lane & 7) ^ ((r >> 1) & 7); }
 
-template <bool MX, bool B_KN, bool SWIGLU>
-__device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int wave, int lane, Plan& pl) {
-  constexpr int ESIZE = MX ? 1 : 2;
+template <class C, bool B_KN, bool SWIGLU>
+__device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int wave, int lane,
+                                          Plan<C::CPW_A>& pl) {
+  constexpr bool MX = C::MX;
+  constexpr int ESIZE = MX ? 1 : 2, CPW = C::CPW_A;
 #pragma unroll
   for (int j = 0; j < CPW; ++j) {
-    const int r = row_of(wave * CPW + j, lane);
+    const int r = row_of(j * WAVES + wave, lane);
     const int rr = r < it.rows ? r : it.rows - 1;
     const int64_t routed = it.row0 + rr;
     const int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
@@ -179,8 +205,9 @@ __device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int
   }
   pl.a_base = uni_ptr(p.A);
   {
-    const int first = wave * CPW * 8;  // first tile row of this wave's activation copies
-    const int n = (it.rows - first + 7) / 8;
+    // copies of 8-row groups holding rows of the item: the wave's are j * WAVES + wave
+    const int groups = (it.rows + 7) / 8;
+    const int n = (groups - wave + WAVES - 1) / WAVES;
     pl.a_copies = uni(n < 0 ? 0 : (n > CPW ? CPW : n));
   }
   pl.b_base = uni_ptr(p.B + (int64_t)it.g * p.b_group_stride);
@@ -225,9 +252,11 @@ __device__ __forceinline__ uint32_t b_off(const GGParams& p, int nt, int i, int 
 
 // `lane` is an opaque copy made per stage, so that the offsets derived from it are recomputed here
 // rather than hoisted out of the K loop into registers.
-template <bool MX, bool B_KN, bool SWIGLU>
-__device__ __forceinline__ void issue_stage(const GGParams& p, const Plan& pl, int k, uint32_t slot, int wave,
-                                            int lane) {
+template <class C, bool B_KN, bool SWIGLU>
+__device__ __forceinline__ void issue_stage(const GGParams& p, const Plan<C::CPW_A>& pl, int k, uint32_t slot,
+                                            int wave, int lane) {
+  constexpr bool MX = C::MX;
+  constexpr int CPW = C::CPW_A;
   asm volatile("" : "+v"(lane));
   const uint8_t* ab = uni_ptr(pl.a_base + (int64_t)k * KB);
   const uint8_t* bb = uni_ptr(pl.b_base + (int64_t)k * pl.b_stride);
@@ -235,10 +264,11 @@ __device__ __forceinline__ void issue_stage(const GGParams& p, const Plan& pl, i
   // refilled hold stale data that only feeds accumulator rows the epilogue does not store)
 #pragma unroll
   for (int j = 0; j < CPW; ++j)
-    if (j < pl.a_copies) dma16(ab, pl.ao[j], uni(slot + (wave * CPW + j) * 1024));
+    if (j < pl.a_copies) dma16(ab, pl.ao[j], uni(slot + (j * WAVES + wave) * 1024));
 #pragma unroll
-  for (int j = 0; j < CPW; ++j)
-    dma16(bb, b_off<MX, B_KN, SWIGLU>(p, pl.nt, wave * CPW + j, lane), uni(slot + B_OFF + (wave * CPW + j) * 1024));
+  for (int j = 0; j < CPW_B; ++j)
+    dma16(bb, b_off<MX, B_KN, SWIGLU>(p, pl.nt, wave * CPW_B + j, lane),
+          uni(slot + C::B_OFF + (wave * CPW_B + j) * 1024));
   if constexpr (MX) {
     // activation code planes: plane wave / 2, bytes 256 (wave % 2) + 4 lane of the item's run;
     // col_scale [G, K/64, Ntot, 2]: wave w (and w + 4) copies 64-K step (w >> 1) & 1, tile columns
@@ -247,9 +277,10 @@ __device__ __forceinline__ void issue_stage(const GGParams& p, const Plan& pl, i
     int wc = tile_col((wave & 1) * 128 + lane * 2, pl.nt, p.N, SWIGLU);
     if (wc > p.Ntot - 2) wc = p.Ntot - 2;
     const uint32_t bso = (uint32_t)((((wave >> 1) & 1) * p.Ntot + wc) * 2);
-    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), so, uni(slot + AS_OFF + (wave >> 1) * AS_PLANE + (wave & 1) * 256));
+    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), so,
+         uni(slot + C::AS_OFF + (wave >> 1) * AS_PLANE + (wave & 1) * 256));
     dma4(uni_ptr(pl.bs_base + (int64_t)k * pl.b_scale_stride), bso,
-         uni(slot + BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256));
+         uni(slot + C::BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256));
   }
 }
 
@@ -257,25 +288,31 @@ __device__ __forceinline__ void issue_stage(const GGParams& p, const Plan& pl, i
 __device__ __forceinline__ int chunk_off(int r, int c) { return r * KB + ((c ^ ((r >> 1) & 7)) << 4); }
 
 // Operand fragments of one half-step (64 bytes of K).
-template <bool MX, bool B_KN> struct Frags;
-template <> struct Frags<false, false> { v8bf a[2][MI], b[2][NI]; };
-template <> struct Frags<false, true> { v8bf a[2][MI]; v4s bl[2][NI], bh[2][NI]; };
-template <> struct Frags<true, false> { v4i al[MI], ah[MI], bl[NI], bh[NI]; int sa[MI], sb[NI]; };
-template <> struct Frags<true, true> { v4i al[MI], ah[MI]; v2i bp[NI][4]; int sa[MI], sb[NI]; };
+template <bool MX, bool B_KN, int MI> struct Frags;
+template <int MI> struct Frags<false, false, MI> { v8bf a[2][MI], b[2][NI]; };
+template <int MI> struct Frags<false, true, MI> { v8bf a[2][MI]; v4s bl[2][NI], bh[2][NI]; };
+template <int MI> struct Frags<true, false, MI> { v4i al[MI], ah[MI], bl[NI], bh[NI]; int sa[MI], sb[NI]; };
+template <int MI> struct Frags<true, true, MI> { v4i al[MI], ah[MI]; v2i bp[NI][4]; int sa[MI], sb[NI]; };
 
 // a_off: the item's first routed row modulo 4 (the offset of the MX activation code planes)
-template <bool MX, bool B_KN>
-__device__ __forceinline__ void read_frags(Frags<MX, B_KN>& f, const uint8_t* slot, int h, int grp, int wq, int lane,
-                                           int a_off) {
+template <class C, bool B_KN>
+__device__ __forceinline__ void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int h, int grp, int wq,
+                                           int lane, int a_off, int nmi) {
+  constexpr bool MX = C::MX;
+  constexpr int MI = C::MI;
+  // bf16 tiles of five row blocks: the fragment addresses are recomputed per read (held across the
+  // K loop they would take about 28 registers)
+  if constexpr (!MX && MI > 4) asm volatile("" : "+v"(lane));
   const uint8_t* As = slot;
-  const uint8_t* Bs = slot + B_OFF;
+  const uint8_t* Bs = slot + C::B_OFF;
   if constexpr (!MX) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       const int ks = h * 2 + s2;  // 16-K step of the stage
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
-        const int r = grp * WM + mi * 32 + (lane & 31);
+        if (MI > 4 && mi >= nmi) continue;  // row block without rows of the item
+        const int r = (2 * mi + grp) * 32 + (lane & 31);
         f.a[s2][mi] = *LDSP(v8bf, As + chunk_off(r, ks * 2 + (lane >> 5)));
       }
 #pragma unroll
@@ -298,11 +335,11 @@ __device__ __forceinline__ void read_frags(Frags<MX, B_KN>& f, const uint8_t* sl
     }
   } else {
     // one 64-K step h: lane r + 32 g holds K 16 g .. +15 and 32 + 16 g .. +15 of the step
-    const uint8_t* ASs = slot + AS_OFF;
-    const uint8_t* BSs = slot + BS_OFF;
+    const uint8_t* ASs = slot + C::AS_OFF;
+    const uint8_t* BSs = slot + C::BS_OFF;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      const int r = grp * WM + mi * 32 + (lane & 31);
+      const int r = (2 * mi + grp) * 32 + (lane & 31);
       const int c0 = h * 4 + (lane >> 5);
       f.al[mi] = *LDSP(v4i, As + chunk_off(r, c0));
       f.ah[mi] = *LDSP(v4i, As + chunk_off(r, c0 + 2));
@@ -331,8 +368,10 @@ __device__ __forceinline__ void read_frags(Frags<MX, B_KN>& f, const uint8_t* sl
   }
 }
 
-template <bool MX, bool B_KN>
-__device__ __forceinline__ void mfmas(const Frags<MX, B_KN>& f, v16f (&acc)[MI][NI]) {
+// nmi: the wave's row blocks that hold rows of the item (bf16 320-row tiles skip the others, so a
+// tile of up to 256 rows issues the MFMAs a 256-row tile would)
+template <bool MX, bool B_KN, int MI>
+__device__ __forceinline__ void mfmas(const Frags<MX, B_KN, MI>& f, v16f (&acc)[MI][NI], int nmi) {
   if constexpr (!MX) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
@@ -340,6 +379,7 @@ __device__ __forceinline__ void mfmas(const Frags<MX, B_KN>& f, v16f (&acc)[MI][
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
+          if (MI > 4 && mi >= nmi) continue;
           v8bf b;
           if constexpr (!B_KN) b = f.b[s2][ni];
           else b = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.bl[s2][ni], f.bh[s2][ni], 0, 1, 2, 3, 4, 5, 6, 7));
@@ -377,12 +417,14 @@ __device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
 // with (row >> 2) & 3, so the two half-wavefronts (rows r and r + 4) write different banks.
 __device__ __forceinline__ int stage_off(int row, int cb) { return row * 64 + ((((cb >> 4) ^ (row >> 2)) & 3) << 4) + (cb & 15); }
 
-// acc[mi][ni][r] holds row grp * 128 + mi * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
+// acc[mi][ni][r] holds row (2 mi + grp) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
 // wq * 64 + ni * 32 + lane % 32 of the tile. Each 32 x 32 output block goes through the wave's LDS
-// staging block (LDS operations of a wave complete in order) and is written with 16-byte stores.
-template <int EPI>
-__device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[MI][NI], int grp, int wq,
-                                         int lane_in, uint8_t* stage) {
+// staging block 16 rows at a time (LDS operations of a wave complete in order) and is written with
+// 16-byte stores.
+template <class C, int EPI>
+__device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[C::MI][NI], int grp,
+                                         int wq, int lane_in, uint8_t* stage) {
+  constexpr int MI = C::MI;
   // the lane index through an empty asm: the staging offsets below are recomputed here instead of
   // being hoisted out of the K loop (where they would take registers for the whole loop)
   int lane = lane_in;
@@ -391,7 +433,7 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
   constexpr int NB = EPI == EPI_STORE_BF16 ? NI : 1;  // output blocks per 32 rows
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
-    const int row_base = grp * WM + mi * 32;  // first tile row of the block
+    const int row_base = (2 * mi + grp) * 32;  // first tile row of the block
     if (row_base >= it.rows) continue;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -420,28 +462,24 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
           }
         }
       } else {
+        // two halves of 16 rows: bf16 values into the staging block (16 rows x 64 bytes), then
+        // 16 bytes per lane (row lane / 4, columns 8 (lane % 4) ..+7) out
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          float v;
-          if constexpr (EPI == EPI_STORE_BF16) v = acc[mi][nb][r];
-          else v = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
-          *(__attribute__((address_space(3))) uint16_t*)(st + stage_off(row, (lane & 31) * 2)) = f32_to_bf16(v);
-        }
-      }
-      // ---- read back 16 bytes per lane and store (rows of 64 bytes, bf16; 32 bytes, e4m3)
-      if constexpr (EPI == EPI_SWIGLU_F32) {
-        // written above
-      } else {
+        for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int idx = i * 64 + lane;
-          const int row = idx >> 2, c = idx & 3;
+          for (int r = 8 * hh; r < 8 * hh + 8; ++r) {
+            const int row = 8 * ((r >> 2) & 1) + 4 * (lane >> 5) + (r & 3);  // row within the half
+            float v;
+            if constexpr (EPI == EPI_STORE_BF16) v = acc[mi][nb][r];
+            else v = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
+            *(__attribute__((address_space(3))) uint16_t*)(st + stage_off(row, (lane & 31) * 2)) = f32_to_bf16(v);
+          }
+          const int row = lane >> 2, c = lane & 3;
           const v4i v = *LDSP(v4i, st + stage_off(row, c * 16));
           const int col = EPI == EPI_STORE_BF16 ? it.nt * BN + wq * WN + nb * 32 + c * 8
                                                 : it.nt * (BN / 2) + wq * 32 + c * 8;
-          if (row_base + row < it.rows && col < p.N) {
-            const int64_t orow = it.row0 + row_base + row;
+          if (row_base + hh * 16 + row < it.rows && col < p.N) {
+            const int64_t orow = it.row0 + row_base + hh * 16 + row;
             *(v4i*)((uint16_t*)p.C + orow * p.ldc + col) = v;
           }
         }
@@ -450,21 +488,58 @@ __device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, cons
   }
 }
 
-template <bool MX, bool B_KN, int EPI>
+template <bool MX, bool B_KN, int EPI, bool TALL>
 __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
+  using C = Cfg<MX, TALL>;
+  constexpr int MI = C::MI, S_SLOT = C::SLOT;
   constexpr bool SWIGLU = EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_F32;
   constexpr int ESIZE = MX ? 1 : 2;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  int32_t* s_prefix = (int32_t*)(smem + PREFIX_OFF);
-  int32_t* s_rows = (int32_t*)(smem + ROWS_OFF);
+  int32_t* s_prefix = (int32_t*)(smem + C::PREFIX_OFF);
+  int32_t* s_rows = (int32_t*)(smem + C::ROWS_OFF);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = uni(tid >> 6);
   const int grp = wave >> 2, wq = wave & 3;
 
-  for (int g = tid; g <= p.G; g += THREADS) {
-    s_prefix[g] = p.tile_prefix[g];
-    if (g < p.G) s_rows[g] = (int32_t)p.group_list[g];
+  // The work list: m-tiles of C::BM rows per group and their exclusive prefix, from group_list (the
+  // tile height is this kernel's own, so no host-side plan is read). Thread t takes groups
+  // PER t ..+PER-1; a scan over the threads gives each its first tile.
+  {
+    constexpr int PER = (C::PREFIX_MAX + THREADS - 1) / THREADS;
+    int cnt[PER];
+    int local = 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int g = tid * PER + u;
+      cnt[u] = 0;
+      if (g < p.G) {
+        const int64_t end = p.group_list[g];
+        const int64_t rows = end - (g == 0 ? 0 : p.group_list[g - 1]);
+        cnt[u] = rows > 0 ? (int)((rows + C::BM - 1) / C::BM) : 0;
+        s_rows[g] = (int32_t)end;
+      }
+      local += cnt[u];
+    }
+    int incl = local;  // inclusive scan within the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    int32_t* wsum = (int32_t*)(smem + C::EPI_OFF);  // the epilogue staging is free until the first item ends
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    int run = base + incl - local;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int g = tid * PER + u;
+      if (g < p.G) s_prefix[g] = run;
+      run += cnt[u];
+    }
+    if (tid == THREADS - 1) s_prefix[p.G] = run;
   }
   __syncthreads();
   const int total = uni(s_prefix[p.G]) * p.n_tiles;
@@ -479,16 +554,16 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   // copy cursor: item cL, stage ck
   int cL = L0, ck = 0;
   Item ci;
-  decode(p, smem, cL, ci);
-  Plan pl;
-  make_plan<MX, B_KN, SWIGLU>(p, ci, wave, lane, pl);
+  decode<C>(p, smem, cL, ci);
+  Plan<C::CPW_A> pl;
+  make_plan<C, B_KN, SWIGLU>(p, ci, wave, lane, pl);
   auto issue_next = [&](int q) {
-    issue_stage<MX, B_KN, SWIGLU>(p, pl, ck, lds0 + (uint32_t)((q % S) * SLOT), wave, lane);
+    issue_stage<C, B_KN, SWIGLU>(p, pl, ck, lds0 + (uint32_t)((q % S) * S_SLOT), wave, lane);
     if (++ck == nk) {
       if (cL + grid < total) {
         cL += grid;
-        decode(p, smem, cL, ci);
-        make_plan<MX, B_KN, SWIGLU>(p, ci, wave, lane, pl);
+        decode<C>(p, smem, cL, ci);
+        make_plan<C, B_KN, SWIGLU>(p, ci, wave, lane, pl);
         ck = 0;
       } else {
         ck = nk - 1;  // past the end: repeat the last stage into the free slot
@@ -499,8 +574,14 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   // compute cursor: item it, stage kk; `live`: this wave's 128 rows hold rows of the item
   int kL = L0, kk = 0;
   Item it;
-  decode(p, smem, kL, it);
-  bool live = it.rows > grp * WM;
+  decode<C>(p, smem, kL, it);
+  // row blocks of this wave's group that hold rows of the item; `live`: any
+  auto row_blocks = [&]() {
+    const int n = ((it.rows + 31) / 32 - grp + 1) / 2;
+    return uni(n < 0 ? 0 : (n > MI ? MI : n));
+  };
+  int nmi = row_blocks();
+  bool live = nmi > 0;
   v16f acc[MI][NI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
@@ -511,7 +592,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
 
   auto finish_stage = [&]() {
     if (++kk == nk) {
-      if (live) epilogue<EPI>(p, it, acc, grp, wq, lane, smem + EPI_OFF + wave * EPI_BLOCK);
+      if (live) epilogue<C, EPI>(p, it, acc, grp, wq, lane, smem + C::EPI_OFF + wave * C::EPI_BLOCK);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -521,8 +602,9 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       kk = 0;
       kL += grid;
       if (kL < total) {
-        decode(p, smem, kL, it);
-        live = it.rows > grp * WM;
+        decode<C>(p, smem, kL, it);
+        nmi = row_blocks();
+        live = nmi > 0;
       }
     }
   };
@@ -530,17 +612,17 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   issue_next(0);
   wait_vm0();
   barrier();
-  Frags<MX, B_KN> f;
+  Frags<MX, B_KN, MI> f;
   if (grp == 0) {
     for (int q = 0; q < nq; ++q) {
       issue_next(q + 1);
-      const uint8_t* slot = smem + (q % S) * SLOT;
+      const uint8_t* slot = smem + (q % S) * S_SLOT;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        if (live) read_frags<MX, B_KN>(f, slot, h, grp, wq, lane, (int)(it.row0 & 3));
+        if (live) read_frags<C, B_KN>(f, slot, h, grp, wq, lane, (int)(it.row0 & 3), nmi);
         wait_lgkm0();
         __builtin_amdgcn_sched_barrier(0);
-        if (live) mfmas<MX, B_KN>(f, acc);
+        if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
         __builtin_amdgcn_sched_barrier(0);
       }
       finish_stage();
@@ -551,47 +633,60 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
     for (int q = 0; q < nq; ++q) {
       issue_next(q + 1);
       if (q > 0) {  // half 1 of stage q - 1, read before the barrier
-        if (live) mfmas<MX, B_KN>(f, acc);
+        if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
         finish_stage();
       }
       __builtin_amdgcn_sched_barrier(0);
-      const uint8_t* slot = smem + (q % S) * SLOT;
-      if (live) read_frags<MX, B_KN>(f, slot, 0, grp, wq, lane, (int)(it.row0 & 3));
+      const uint8_t* slot = smem + (q % S) * S_SLOT;
+      if (live) read_frags<C, B_KN>(f, slot, 0, grp, wq, lane, (int)(it.row0 & 3), nmi);
       wait_lgkm0();
       __builtin_amdgcn_sched_barrier(0);
-      if (live) mfmas<MX, B_KN>(f, acc);
+      if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
       __builtin_amdgcn_sched_barrier(0);
-      if (live) read_frags<MX, B_KN>(f, slot, 1, grp, wq, lane, (int)(it.row0 & 3));
+      if (live) read_frags<C, B_KN>(f, slot, 1, grp, wq, lane, (int)(it.row0 & 3), nmi);
       wait_lgkm0();
       wait_vm0();
       barrier();
     }
-    if (live) mfmas<MX, B_KN>(f, acc);
+    if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
     finish_stage();
   }
   wait_vm0();  // no copy may still write the LDS when the workgroup ends
 }
 
-template <bool MX, bool B_KN, int EPI>
-int launch_pp(const GGParams& p, hipStream_t stream) {
-  auto kern = gg_pp_kernel<MX, B_KN, EPI>;
+template <bool MX, bool B_KN, int EPI, bool TALL>
+int launch_pp_k(const GGParams& p, hipStream_t stream) {
+  using C = Cfg<MX, TALL>;
+  auto kern = gg_pp_kernel<MX, B_KN, EPI, TALL>;
   static bool configured = false;
   if (!configured) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, TOTAL) != hipSuccess)
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::TOTAL) != hipSuccess)
       return MI355MOE_ELAUNCH;
     configured = true;
   }
   int grid = (mi355_num_cus() / 8) * 8;
   if (grid < 8) grid = 8;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), TOTAL, stream, p);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), C::TOTAL, stream, p);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+// 320-row tiles for bf16 when the caller's row count averages at most 320 per group
+bool pp_tall(const GGParams& p, bool mx) {
+  return !mx && p.rows_hint > 0 && p.rows_hint <= (int64_t)p.G * 320 && p.G <= Cfg<false, true>::PREFIX_MAX;
+}
+
+template <bool MX, bool B_KN, int EPI>
+int launch_pp(const GGParams& p, hipStream_t stream) {
+  if constexpr (!MX)
+    if (pp_tall(p, MX)) return launch_pp_k<MX, B_KN, EPI, true>(p, stream);
+  return launch_pp_k<MX, B_KN, EPI, false>(p, stream);
 }
 
 }  // namespace
 
 bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
   if (p.k_splits > 1 || p.c_row_index != nullptr) return false;
-  if (p.G > PREFIX_MAX) return false;  // the work list is decoded from LDS
+  if (p.G > Cfg<false, false>::PREFIX_MAX) return false;  // the work list is in LDS
   if (p.swiglu_limit > 0.0f || p.row_prob != nullptr) return false;  // numerics options: default kernel
   const int esize = mx ? 1 : 2;
   if ((int64_t)p.K * esize % KB != 0) return false;
@@ -610,7 +705,7 @@ bool mi355_gg_pp_usable(int variant, bool mx, bool b_kn, int64_t K, int G, int64
   const int v = variant;
   if (v != MI355_GG_VARIANT_DEFAULT && v != MI355_GG_VARIANT_PP) return false;
   if (mx && !b_kn) return false;
-  if (G > PREFIX_MAX || K * (mx ? 1 : 2) % KB != 0) return false;
+  if (G > Cfg<false, false>::PREFIX_MAX || K * (mx ? 1 : 2) % KB != 0) return false;
   const int64_t lim = (int64_t)1 << 32;
   return a_bytes > 0 && a_bytes < lim && b_group_stride > 0 && b_group_stride < lim;
 }
