@@ -10,6 +10,7 @@ changed.
 """
 from __future__ import annotations
 
+import fcntl
 import hashlib
 import os
 import re
@@ -59,12 +60,20 @@ def _run(cmd: list[str]) -> str:
 
 
 def build() -> Path:
+    """Build the checker once per source digest; concurrent callers (pytest-xdist workers) wait on a
+    file lock instead of building the same objects at the same time."""
+    OUT.mkdir(parents=True, exist_ok=True)
+    with open(OUT / ".lock", "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        return _build_locked()
+
+
+def _build_locked() -> Path:
     exe = OUT / "gemm_copy_check"
     stamp = OUT / "stamp"
     digest = _digest()
     if exe.exists() and stamp.exists() and stamp.read_text() == digest:
         return exe
-    OUT.mkdir(parents=True, exist_ok=True)
     hipcc = str(_rocm() / "bin" / "hipcc")
     objs = []
     for src in LIB_SOURCES:
