@@ -403,7 +403,8 @@ def expert_forward_reference(hidden: torch.Tensor, ids: torch.Tensor, probs: tor
 
 
 def expert_forward_reference_tokens(hidden: torch.Tensor, ids: torch.Tensor, probs: torch.Tensor,
-                                    tokens: torch.Tensor, expert_weights, *, precision: str = "bf16") -> torch.Tensor:
+                                    tokens: torch.Tensor, expert_weights, *, precision: str = "bf16",
+                                    scale_alg: int = 1) -> torch.Tensor:
     """:func:`expert_forward_reference` restricted to the token rows ``tokens`` (same rounding points,
     fp32 accumulate; fp32_expert_reference.py:22-26, moe_reference.py:170-181), for layers whose
     weights are too large to expand at once. ``expert_weights(e)`` returns the fp32 weights of expert
@@ -414,7 +415,7 @@ def expert_forward_reference_tokens(hidden: torch.Tensor, ids: torch.Tensor, pro
     K = ids.shape[1]
     x = hidden.float()[tok]
     if precision != "bf16":
-        q, s = mx_quantize(x, dim=-1)
+        q, s = mx_quantize(x, dim=-1, scale_alg=scale_alg)
         x = mx_dequantize(q, s, dim=-1)
     sel = ids[tok].long()                      # [n, K]
     p = probs[tok].float()
@@ -431,7 +432,7 @@ def expert_forward_reference_tokens(hidden: torch.Tensor, ids: torch.Tensor, pro
         if precision == "bf16":
             act = _bf16(act)
         else:
-            aq, asc = mx_quantize(act, dim=-1)
+            aq, asc = mx_quantize(act, dim=-1, scale_alg=scale_alg)
             act = mx_dequantize(aq, asc, dim=-1)
         y[rows, ks] = _bf16(act @ W2)
     out = torch.zeros((n, H), dtype=torch.float32)
