@@ -1,15 +1,9 @@
 // Feature gates of the optional paths (reported by mi355moe_features).
 #pragma once
 
-// Optional paths, each switched off until its GPU parity tests have run (a switched-off path answers
-// MI355MOE_EUNSUPPORTED, or the forward keeps the default tiles). MI355_CHECK_ALL_PATHS is defined
-// only by the host-side copy checker under tests/native, which drives the host code of every path
-// (it never runs on a GPU).
-#ifdef MI355_CHECK_ALL_PATHS
-#define MI355_PATH_ON true
-#else
-#define MI355_PATH_ON false
-#endif
+// Optional paths. Each was switched on after its GPU parity tests passed; a path switched off answers
+// MI355MOE_EUNSUPPORTED (or the forward keeps the default tiles) and mi355moe_features() clears its
+// bit, which the GPU tests of that path read to skip.
 // MX GEMM with K-contiguous (EOI) weights.
 inline bool mi355_mx_eoi_enabled() { return true; }
 // BF16 numerics options (SwiGLU clamp, probabilities before FC2).

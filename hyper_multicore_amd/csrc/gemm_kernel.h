@@ -3,9 +3,6 @@
 // kernels): the direct-to-LDS copy and the waits, the software-pipelined K loop, the forward kernel
 // and its launch. The three files are separate translation units: with other kernel families in the
 // same module the compiler schedules the default kernels' scalar address code differently.
-// Measurement builds of gemm.hip only (never shipped): -DGG_ABLATE_COMPUTE drops the MFMAs and LDS
-// fragment reads (copy ceiling), -DGG_ABLATE_DMA drops the copies (compute ceiling), -DGG_TRACE records
-// per-step timestamps of the first workgroups (read back with mi355_gg_trace_read).
 #pragma once
 #include <type_traits>
 #include "common.h"
@@ -88,15 +85,6 @@ MI355_DEV void wait_vm(int n) {
   }
 }
 
-#ifdef GG_TRACE
-__device__ unsigned long long gg_trace[4 * 8 * 64 * 5];
-#define GG_T(pt) if (blockIdx.x < 4 && k < 64 && lane == 0) gg_trace[((blockIdx.x * 8 + wave) * 64 + k) * 5 + pt] = __builtin_amdgcn_s_memtime();
-extern "C" int mi355_gg_trace_read(void* host) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(gg_trace), sizeof(gg_trace)) == hipSuccess ? 0 : -1;
-}
-#else
-#define GG_T(pt)
-#endif
 
 // K loop, software-pipelined in each wave: iteration k (after barrier k) refills the ring slots of
 // stage k, reads the fragments of stage k+1 into one register set and runs the MFMAs of stage k
@@ -125,12 +113,9 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
   // one pipelined iteration with a next stage (k + 1 < nk)
   auto step = [&](int k, Frags<C, MX, B_KN, GK>& cur, Frags<C, MX, B_KN, GK>& nxt) {
     __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs of the previous stage above the barrier
-    GG_T(0)
     wait_vm(younger_than<C, LA>(k + 1, k - 1, nk, la_n, lb_n));
-    GG_T(1)
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    GG_T(2)
     int ln = lane;
     asm volatile("" : "+v"(ln));  // recompute lane-dependent LDS offsets here rather than hold them
     const int kn = k + 1;
@@ -143,22 +128,18 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
     constexpr int T = SS::MFMAS > 0 ? SS::MFMAS : 1;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-#ifndef GG_ABLATE_COMPUTE
       if constexpr (NM > 0) {
         mfma_elem<C, MX, B_KN, NM, GK>(cur, acc, t);
 #pragma unroll
         for (int e = t * SS::READS / T; e < (t + 1) * SS::READS / T; ++e)
           read_elem<C, MX, B_KN, NM, GK>(nxt, e, As, Bs, ASs, BSRs, wm, wn, ln);
       }
-#endif
 #pragma unroll
       for (int it = t * SS::ITEMS / T; it < (t + 1) * SS::ITEMS / T; ++it)
         issue_item<C, MX, B_KN, LA, GK, DevDma, LB>(cp, k, nk, wave, smem, it);
-      if (t == T / 2 - 1) { GG_T(3) }
       __builtin_amdgcn_sched_barrier(0);  // keep this interleave order
     }
     issue_scales_item<C, MX, B_KN, LA, DevDma, GK>(cp, k, nk, wave, smem);
-    GG_T(4)
   };
   // Stages 0 .. nk-2 are pipelined steps (each reads the next stage), taken in pairs so that the
   // two fragment sets keep fixed registers; an odd count starts with one step and a copy.
@@ -175,12 +156,10 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
   // last stage: its fragments are in f0 and it issues no copies
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#ifndef GG_ABLATE_COMPUTE
   if constexpr (NM > 0) {
 #pragma unroll
     for (int t = 0; t < SS::MFMAS; ++t) mfma_elem<C, MX, B_KN, NM, GK>(f0, acc, t);
   }
-#endif
 }
 
 // One work item of a split-role configuration (C::SPLIT) for the waves of role ROLE (0: the two

@@ -186,9 +186,6 @@ MI355_HD const uint8_t* b_src(const CopyPlan<C>& cp, int j, int kt) {
 // ---- copy issue order --------------------------------------------------------------------------
 template <class C, bool MX, bool GK, class D>
 MI355_HD void issue_a(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
   const uint32_t base = (kt % C::A_SLOTS) * C::A_BYTES;
 #pragma unroll
   for (int j = 0; j < C::A_PER; ++j) {
@@ -206,9 +203,6 @@ MI355_HD void issue_a(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
 template <class C, bool MX, bool B_KN, bool GK, class D>
 MI355_HD void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
   // (MX with K-contiguous weights has no per-stage scale copy: its scales come in groups)
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
   const uint32_t base = C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT;
   if constexpr (!GK) {
     const int64_t boff = (int64_t)kt * cp.b_stage_stride;
@@ -231,9 +225,6 @@ MI355_HD void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
 // MX: A scale codes of stages 8*grp .. 8*grp+7 (16 bytes per row) into AS slot grp & 1.
 template <class C, class D>
 MI355_HD void issue_as(const CopyPlan<C>& cp, int grp, int wave, uint8_t* smem) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
   if constexpr (C::SPLIT) {  // an activation-copying wave: its two 64-row scale blocks
     D::template copy<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 1) * 2048, smem, 1);
     D::template copy<16>(cp.s2 + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 1) * 2048 + 1024, smem, 1);
@@ -255,9 +246,6 @@ template <class C, bool MX, int NM, bool GK = false> struct StepShape {
 // grouped-K MX mode the A column scales). LB: the wave copies weights (always, unless split roles).
 template <class C, bool MX, bool B_KN, bool LA, bool GK, class D, bool LB = true>
 MI355_HD void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem, int it) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
   constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
   if (it < C::B_PER) {
     const int kt = i + DB;
@@ -296,9 +284,6 @@ MI355_HD void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t
 // weights, B rows), each as one conditional copy.
 template <class C, bool MX, bool B_KN, bool LA, class D, bool GK = false>
 MI355_HD void issue_scales_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
-#ifdef GG_ABLATE_DMA
-  if (wave < 64) return;
-#endif
   if constexpr (MX && !GK) {
     const int grp = i / C::AS_GROUP + 1;
     const bool due = (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk;

@@ -1,7 +1,7 @@
 """Build the host-side grouped-GEMM copy checker (test infrastructure, CPU only).
 
 The library sources are compiled for the host only (``--cuda-host-only``) with every optional path
-switched on (``-DMI355_CHECK_ALL_PATHS``) and AddressSanitizer, the internal enqueue functions the
+switched on and AddressSanitizer, the internal enqueue functions the
 checker replaces are made weak, and everything is linked with ``gemm_copy_check.cpp`` and no HIP
 runtime. Output goes to ``tests/native/_build`` (git-ignored); a build is reused while no input
 changed.
@@ -31,7 +31,7 @@ REPLACED = {
     "quant.hip": ["mi355_mx_quant_rows", "mi355_mx_quant_grouped"],
 }
 FLAGS = ["-x", "hip", "--cuda-host-only", "-O1", "-g", "-std=c++17", "-fsanitize=address",
-         "-fno-omit-frame-pointer", "-DMI355_CHECK_ALL_PATHS", "-Wno-unused-result", "-Wno-unused-variable",
+         "-fno-omit-frame-pointer", "-Wno-unused-result", "-Wno-unused-variable",
          f"-I{REPO / 'include'}"]
 
 
