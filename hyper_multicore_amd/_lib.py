@@ -57,6 +57,7 @@ class RouteGradArgs(Structure):
         ("indices32", c_void_p), ("grad_weights", c_void_p), ("grad_logits", c_void_p), ("accumulate", c_int32),
         ("scoring", c_int32), ("num_tokens", c_int64), ("num_experts", c_int32), ("top_k", c_int32),
         ("routed_scaling_factor", c_float), ("reserved", c_int32),
+        ("selected_scores", c_void_p), ("denominator", c_void_p),
     ]
 
 

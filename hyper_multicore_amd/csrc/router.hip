@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void mi355_route_grad_kernel(MI355MoeRouteGrad
     const int64_t v = a.indices != nullptr ? a.indices[t * K + lane] : (int64_t)a.indices32[t * K + lane];
     if (v >= 0 && v < E) {
       id = (int)v;
-      sel = srow[id];
+      sel = a.selected_scores != nullptr ? a.selected_scores[t * K + lane] : srow[id];
     }
     gw = a.grad_weights[t * K + lane];
   }
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) void mi355_route_grad_kernel(MI355MoeRouteGrad
   } else {
     float sum = 0.0f;
     for (int k = 0; k < K; ++k) sum = sum + __shfl(sel, k, 64);
-    const float D = sum + 1.0e-20f;
+    const float D = a.denominator != nullptr ? a.denominator[t] : sum + 1.0e-20f;
     const float k0 = gw * scale;
     const float cross = (-k0) * ((sel / D) / D);
     float row = 0.0f;

@@ -132,16 +132,19 @@ def gate_route(logits: torch.Tensor, bias: torch.Tensor, *, top_k: int, scoring_
 
 def gate_route_grad(logits: torch.Tensor, scores: torch.Tensor, indices: torch.Tensor, grad_weights: torch.Tensor, *,
                     top_k: int, scoring_func: str, routed_scaling_factor: float,
-                    grad_logits: torch.Tensor | None = None) -> torch.Tensor:
+                    grad_logits: torch.Tensor | None = None, selected_scores: torch.Tensor | None = None,
+                    denominator: torch.Tensor | None = None) -> torch.Tensor:
     """Gradient of the routing weights w.r.t. the fp32 logits (RouteGrad), fp32 [T, E].
 
     Mirrors hyper_multicore::mega_gate_route_grad (torch/csrc/mega_gate.cpp:182-197) for the three
     scoring functions; ``scores`` are the forward's unbiased scores (``gate_route(...,
     return_scores=True)``). When ``grad_logits`` is given the route gradient is added to it in place
-    (the gradient the logits output already carries) and it is returned.
+    (the gradient the logits output already carries) and it is returned. ``selected_scores`` fp32
+    [T, K] and ``denominator`` fp32 [T, 1] (the forward's diagnostics) are used as given; without them
+    both are recomputed from ``scores`` and ``indices`` in the forward's order.
     """
     lib = _lib.load()
-    device = _require_gpu(logits, scores, indices, grad_weights, grad_logits)
+    device = _require_gpu(logits, scores, indices, grad_weights, grad_logits, selected_scores, denominator)
     if logits.dtype != torch.float32 or logits.ndim != 2 or logits.stride(1) != 1:
         raise TypeError("logits must be fp32 [tokens, experts] with contiguous rows")
     T, E = logits.shape
@@ -162,13 +165,22 @@ def gate_route_grad(logits: torch.Tensor, scores: torch.Tensor, indices: torch.T
         out = grad_logits
     else:
         out = torch.empty((T, E), dtype=torch.float32, device=device)
+    if selected_scores is not None:
+        if selected_scores.dtype != torch.float32 or selected_scores.shape != (T, top_k):
+            raise ValueError("selected_scores must be fp32 [tokens, top_k]")
+        selected_scores = selected_scores.contiguous()
+    if denominator is not None:
+        if denominator.dtype != torch.float32 or denominator.numel() != T or denominator.shape[0] != T:
+            raise ValueError("denominator must be fp32 [tokens, 1]")
+        denominator = denominator.contiguous()
     i64 = indices.dtype == torch.int64
     args = _lib.RouteGradArgs(
         logits=_ptr(logits), logits_row_stride=logits.stride(0), scores=_ptr(scores),
         indices=_ptr(indices) if i64 else None, indices32=None if i64 else _ptr(indices),
         grad_weights=_ptr(grad_weights), grad_logits=_ptr(out), accumulate=int(accumulate),
         scoring=_lib.SCORE[scoring_func], num_tokens=T, num_experts=E, top_k=top_k,
-        routed_scaling_factor=float(routed_scaling_factor), reserved=0)
+        routed_scaling_factor=float(routed_scaling_factor), reserved=0,
+        selected_scores=_ptr(selected_scores), denominator=_ptr(denominator))
     rc = lib.mi355moe_gate_route_grad(ctypes.byref(args), _stream(device))
     _lib.check(rc, "mi355moe_gate_route_grad")
     return out
@@ -257,6 +269,17 @@ def token_unpermute(values: torch.Tensor, mapping: torch.Tensor, probs: torch.Te
     return out
 
 
+def _overlaps(a: torch.Tensor | None, b: torch.Tensor | None) -> bool:
+    """Whether the memory of two tensors intersects (their element spans)."""
+    if a is None or b is None or a.numel() == 0 or b.numel() == 0:
+        return False
+    def span(t):  # [first byte, one past the last byte) of the elements
+        last = sum((n - 1) * st for n, st in zip(t.shape, t.stride()))
+        return t.data_ptr(), t.data_ptr() + (last + 1) * t.element_size()
+    (a0, a1), (b0, b1) = span(a), span(b)
+    return a0 < b1 and b0 < a1
+
+
 def token_unpermute_grad(values: torch.Tensor, grad_out: torch.Tensor, mapping: torch.Tensor, probs: torch.Tensor,
                          top_k: int, *, grad_values: torch.Tensor | None = None,
                          grad_probs: torch.Tensor | None = None):
@@ -264,7 +287,9 @@ def token_unpermute_grad(values: torch.Tensor, grad_out: torch.Tensor, mapping: 
     grad_values[mapping[t*K+k]] = bf16(p[t,k] * grad_out[t]), grad_probs fp32 [T, K] with
     grad_probs[t,k] = <values[mapping[t*K+k]], grad_out[t]>), like hyper_multicore::
     mega_moe_unpermute_grad_out (torch/csrc/mega_moe_unpermute.cpp:16-62). Written into
-    ``grad_values`` / ``grad_probs`` when given (contiguous, shaped as above)."""
+    ``grad_values`` / ``grad_probs`` when given (contiguous, shaped as above); rows of grad_values that
+    no slot maps to are zero in a freshly allocated result and left as they are in a given one. The
+    outputs may not overlap the inputs or each other (mega_moe_unpermute.cpp:47-52)."""
     lib = _lib.load()
     device = _require_gpu(values, grad_out, mapping, probs, grad_values, grad_probs)
     if values.dtype != torch.bfloat16 or grad_out.dtype != torch.bfloat16 or values.ndim != 2 or grad_out.ndim != 2:
@@ -274,8 +299,13 @@ def token_unpermute_grad(values: torch.Tensor, grad_out: torch.Tensor, mapping: 
     T, H = grad_out.shape
     if probs.shape != (T, top_k) or mapping.numel() != T * top_k or values.shape != (T * top_k, H):
         raise ValueError("unpermute gradient needs all top-k rows: values [T*K, H], probs [T, K], mapping [T*K]")
+    for out_t, name in ((grad_values, "grad_values"), (grad_probs, "grad_probs")):
+        if any(_overlaps(out_t, t) for t in (values, grad_out, mapping, probs)):
+            raise ValueError(f"{name} must not overlap the inputs")
+    if _overlaps(grad_values, grad_probs):
+        raise ValueError("grad_values and grad_probs must not overlap")
     if grad_values is None:
-        grad_values = torch.empty((T * top_k, H), dtype=torch.bfloat16, device=device)
+        grad_values = torch.zeros((T * top_k, H), dtype=torch.bfloat16, device=device)
     if grad_probs is None:
         grad_probs = torch.empty((T, top_k), dtype=torch.float32, device=device)
     if (grad_values.shape != values.shape or grad_values.dtype != torch.bfloat16 or not grad_values.is_contiguous()

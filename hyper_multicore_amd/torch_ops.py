@@ -181,12 +181,12 @@ def mega_gate_route_grad(logits: torch.Tensor, route_scores: torch.Tensor, selec
                          grad_routing_weights: torch.Tensor, top_k: int, routed_scaling_factor: float,
                          scoring_func: str = "sigmoid") -> torch.Tensor:
     """Gradient of the routing weights with respect to the logits (mega_gate_registration.cpp:31-41).
-    The selected scores and the denominator are checked for shape and recomputed from the route
-    scores and indices on the device, in the order the forward used."""
+    The selected scores and the denominator are consumed as given, like the reference's RouteGrad."""
     _check_route_grad(logits, route_scores, selected_scores, normalization_denominator, expert_indices,
                       grad_routing_weights)
     return ops.gate_route_grad(logits, route_scores, expert_indices, grad_routing_weights, top_k=top_k,
-                               scoring_func=scoring_func, routed_scaling_factor=routed_scaling_factor)
+                               scoring_func=scoring_func, routed_scaling_factor=routed_scaling_factor,
+                               selected_scores=selected_scores, denominator=normalization_denominator)
 
 
 @mega_gate_route_grad.register_fake

@@ -159,6 +159,12 @@ typedef struct MI355MoeRouteGradArgs {
   int32_t top_k;              /* <= min(E, 64) */
   float routed_scaling_factor;
   int32_t reserved;
+  /* Optional forward diagnostics (the reference's selected_scores / normalization_denominator
+   * outputs of mega_gate_route, consumed by its RouteGrad): selected scores [T, K] fp32 and the
+   * normalisation denominator [T] fp32 (sum of the selected scores + 1e-20). When given they are
+   * used as they are; when NULL they are recomputed from scores and indices in the forward's order. */
+  const float* selected_scores;
+  const float* denominator;
 } MI355MoeRouteGradArgs;
 int mi355moe_gate_route_grad(const MI355MoeRouteGradArgs* args, void* stream);
 

@@ -757,6 +757,30 @@ def test_route_grad_int32_indices_and_accumulate(gpu):
 
 
 @_ROUTE_GRAD_SKIP
+@pytest.mark.parametrize("scoring", ["sigmoid", "sqrtsoftplus"])
+def test_route_grad_consumes_given_diagnostics(gpu, scoring):
+    """The selected scores and the denominator are consumed as given (the reference's RouteGrad takes
+    them from the forward): the forward's own values reproduce the recomputed gradient bit for bit,
+    and doubling both halves every term of the selected-score gradient exactly (powers of two), so the
+    logit gradient of sigmoid and sqrt-softplus scores halves bit for bit."""
+    from hyper_multicore_amd import ops, torch_ops
+    T, E, K = 300, 64, 6
+    g = _seed(93)
+    logits = torch.randn(T, E, generator=g).to(gpu)
+    bias = (torch.randn(E, generator=g) * 0.1).to(gpu)
+    w, idx, scores, sel, den = torch.ops.hyper_multicore_mi355.mega_gate_route(
+        logits, bias, None, None, K, 2.5, False, scoring)
+    gw = torch.randn(T, K, generator=g).to(gpu)
+    args = dict(top_k=K, scoring_func=scoring, routed_scaling_factor=2.5)
+    plain = ops.gate_route_grad(logits, scores, idx, gw, **args)
+    given = torch.ops.hyper_multicore_mi355.mega_gate_route_grad(logits, scores, sel, den, idx, gw, K, 2.5, scoring)
+    assert torch.equal(given, plain)
+    doubled = ops.gate_route_grad(logits, scores, idx, gw, selected_scores=sel * 2, denominator=den * 2, **args)
+    assert torch.equal(doubled, plain / 2)
+    assert not torch.equal(doubled, plain)
+
+
+@_ROUTE_GRAD_SKIP
 @pytest.mark.parametrize("scoring,K", [("sqrtsoftplus", 6), ("sigmoid", 8), ("softmax", 2), ("sqrtsoftplus", 1)])
 @pytest.mark.parametrize("vision", [False, True])
 def test_megagate_module_gradients_match_torch(gpu, scoring, K, vision):

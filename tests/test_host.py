@@ -229,3 +229,15 @@ def test_invalid_routes_raise_like_the_reference():
         validate_routes(ids, 4, torch.tensor([1, 2, 1, 2]))  # not the histogram
     with pytest.raises(RuntimeError, match=ROUTE_COUNT_ERROR):
         validate_routes(ids.to(torch.int32), 3)  # id 3 outside [0, 3)
+
+
+def test_output_overlap_check():
+    """The no-overlap check of the unpermute gradient's outputs (mega_moe_unpermute.cpp:47-52): spans
+    that share memory overlap, disjoint ones do not."""
+    from hyper_multicore_amd.ops import _overlaps
+    a = torch.zeros(100)
+    assert _overlaps(a, a[50:]) and _overlaps(a[10:20], a[15:30])
+    assert not _overlaps(a[:50], a[50:]) and not _overlaps(a, torch.zeros(10)) and not _overlaps(a, None)
+    m = torch.zeros(64, 32)
+    assert not _overlaps(m[:32], m[32:]) and _overlaps(m[:, :16], m[:, 16:])  # row blocks vs column halves
+    assert not _overlaps(m, torch.zeros(64, 32))

@@ -211,6 +211,18 @@ def test_gpu_unpermute_grad_matches_oracle(gpu):
     keep = torch.ones(T * K, dtype=torch.bool)
     keep[mapping[5].long()] = False  # the row slot 5 would have written
     assert torch.equal(gv2.cpu()[keep], rv[keep])
+    assert int(gv2.cpu()[mapping[5].long()].view(torch.int16).abs().sum()) == 0  # unwritten row: zeros
+    # outputs overlapping the inputs or each other are refused (mega_moe_unpermute.cpp:47-52)
+    yg, pg = y.to(gpu), p.to(gpu)
+    with pytest.raises(ValueError, match="overlap"):
+        ops.token_unpermute_grad(yg, dout.to(gpu), mapping.to(gpu), pg, K, grad_values=yg)
+    with pytest.raises(ValueError, match="overlap"):
+        ops.token_unpermute_grad(yg, dout.to(gpu), mapping.to(gpu), pg, K, grad_probs=pg)
+    both = torch.empty(T * K * H * 2 + T * K * 4, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError, match="overlap"):
+        ops.token_unpermute_grad(yg, dout.to(gpu), mapping.to(gpu), pg, K,
+                                 grad_values=both[:T * K * H * 2].view(BF).view(T * K, H),
+                                 grad_probs=both[:T * K * 4].view(torch.float32).view(T, K))
 
 
 @pytest.mark.gpu
