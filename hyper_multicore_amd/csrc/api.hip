@@ -288,7 +288,8 @@ extern "C" int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_s
 // MegaMoE expert forward
 // ---------------------------------------------------------------------------------------------
 struct FwdLayout {
-  size_t dispatch, counts, group_list, mapping, gather, tile_prefix, act, act_scale, act_f32, y, xq, xs, total;
+  size_t dispatch, counts, group_list, mapping, gather, tile_prefix, act, act_scale, act_f32, y, xq, xs, tok_codes,
+      total;
 };
 
 static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
@@ -311,6 +312,7 @@ static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
   L.xq = mx ? take(T * H) : 0;
   // MX token scales: [T, ld] for the 4-wave GEMM, or stage-major over the routed rows [H/128][R][4]
   L.xs = mx ? take(std::max(T * mi355_mx_scale_ld(H), R * (H / 32) + 256)) : 0;
+  L.tok_codes = mx ? take(T * (H / 32)) : 0;  // per-token codes before they go to the routed rows' planes
   L.total = off;
   return L;
 }
@@ -395,8 +397,12 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
                      mi355_gg_pp_usable(a.gemm_variant, true, true, I, E, T * K * I, (int64_t)I * H);
   if (mx) {
     // with the 8-wave GEMM the token scales go to each token's routed rows (read in tile order)
-    rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), mi355_mx_scale_ld(H), st,
-                             pp_mx ? T * K * 4 : 0, pp_mx ? mapping : nullptr, K);
+    if (pp_mx)
+      rc = mi355_mx_quant_tokens_to_planes(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.tok_codes), gather,
+                                           K, group_list, E, (uint8_t*)(ws + L.xs), T * K * 4, st);
+    else
+      rc = mi355_mx_quant_rows(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.xs), mi355_mx_scale_ld(H),
+                               st);
     if (rc) return rc;
     a1 = (const uint8_t*)(ws + L.xq);
   }

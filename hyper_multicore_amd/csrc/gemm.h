@@ -145,6 +145,11 @@ int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const flo
 // stage-major code planes [cols/128][4][stage_stride / 4] (one thread per 32-element block).
 int mi355_mx_quant_act(const float* act, int64_t rows, int cols, uint8_t* q, uint8_t* planes, int64_t stage_stride,
                        hipStream_t st);
+// MX quantisation of token rows into q [tokens, cols] and per-token codes [tokens, cols/32] (scratch),
+// then the stage-major code planes by routed row (gather: routed row -> slot, fanout slots per token).
+int mi355_mx_quant_tokens_to_planes(const uint16_t* x, int64_t tokens, int cols, uint8_t* q, uint8_t* codes,
+                                    const int32_t* gather, int fanout, const int64_t* group_list, int groups,
+                                    uint8_t* planes, int64_t stage_stride, hipStream_t st);
 int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
                         hipStream_t st, int64_t scale_stage_stride = 0, const int32_t* mapping = nullptr,
                         int fanout = 1);

@@ -130,6 +130,55 @@ int mi355_mx_quant_act(const float* act, int64_t rows, int cols, uint8_t* q, uin
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
+// Stage-major code planes by routed row from per-token codes [tokens, nb]: one thread per 4
+// consecutive routed rows and 32-block b, so each thread writes 4 bytes and a wavefront 256
+// consecutive bytes of one plane. Routed row rr holds the codes of token gather[rr] / fanout; rows
+// at or past the routed-row count (group_list[groups - 1]) get code 0 (nothing reads them as rows
+// of a group).
+__global__ __launch_bounds__(256) void mx_codes_to_planes_kernel(const uint8_t* codes, int nb, const int32_t* gather,
+                                                                 int fanout, const int64_t* group_list, int groups,
+                                                                 int64_t R, uint8_t* planes, int64_t stage_stride) {
+  const int64_t R4 = (R + 3) / 4;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= R4 * nb) return;
+  const int b = (int)(id / R4);
+  const int64_t r0 = (id - b * R4) * 4;
+  const int64_t valid = group_list[groups - 1];
+  uint8_t* plane = planes + (b >> 2) * stage_stride + (b & 3) * (stage_stride >> 2);
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t rr = r0 + i;
+    uint32_t c = 0;
+    if (rr < valid && rr < R) {
+      const int32_t s = gather[rr];
+      if (s >= 0) c = codes[(int64_t)(s / fanout) * nb + b];
+    }
+    w |= c << (8 * i);
+  }
+  if ((R & 3) == 0) {
+    *(uint32_t*)(plane + r0) = w;
+  } else {
+    for (int i = 0; i < 4 && r0 + i < R; ++i) plane[r0 + i] = (uint8_t)(w >> (8 * i));
+  }
+}
+
+int mi355_mx_quant_tokens_to_planes(const uint16_t* x, int64_t tokens, int cols, uint8_t* q, uint8_t* codes,
+                                    const int32_t* gather, int fanout, const int64_t* group_list, int groups,
+                                    uint8_t* planes, int64_t stage_stride, hipStream_t st) {
+  const int nb = cols / 32;
+  const int64_t n = tokens * nb;
+  if (n == 0) return MI355MOE_OK;
+  hipLaunchKernelGGL(mx_quant_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, tokens, cols, q,
+                     codes, (int64_t)nb, (int64_t)0, (const int32_t*)nullptr, 1);
+  if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
+  const int64_t R = tokens * fanout;
+  const int64_t m = (R + 3) / 4 * nb;
+  hipLaunchKernelGGL(mx_codes_to_planes_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, codes, nb, gather,
+                     fanout, group_list, groups, R, planes, stage_stride);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
 int mi355_mx_quant_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* scale, int64_t scale_ld,
                         hipStream_t st, int64_t scale_stage_stride, const int32_t* mapping, int fanout) {
   int64_t n = rows * (cols / 32);
