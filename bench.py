@@ -143,10 +143,16 @@ def gmm_work(c: dict, counts: torch.Tensor) -> dict:
 
 def m_tiles(c: dict, counts: torch.Tensor, variant: str = "default", decode_tiles: bool = True) -> dict:
     """Row tiles the expert GEMMs run (per column block) against the ideal R / BM, and the fraction
-    of tile rows that are padding: the M-tail waste of ragged groups. BM is 64 on the decode tiles
-    (routed rows <= 32 per expert under the default variant), else 256."""
+    of tile rows that are padding: the M-tail waste of ragged groups. BM is the library's choice: 64
+    on the decode tiles (routed rows <= 32 per expert under the default variant), 320 for bf16 when
+    groups average at most 320 rows, else 256."""
     R = c["T"] * c["K"]
-    bm = 64 if decode_tiles and variant == "default" and R <= c["E"] * 32 else 256
+    if decode_tiles and variant == "default" and R <= c["E"] * 32:
+        bm = 64
+    elif c["precision"] == "bf16" and variant in ("default", "pp") and R <= c["E"] * 320:
+        bm = 320  # the 8-wave configuration's tall bf16 tiles (groups averaging at most 320 rows)
+    else:
+        bm = 256
     tiles = int(((counts + bm - 1) // bm).sum())
     return {"bm": bm, "tiles": tiles, "ideal": -(-R // bm), "padded_row_frac": round(1 - R / (tiles * bm), 4)}
 
@@ -563,6 +569,7 @@ def main() -> int:
         "layer_tflops": res["layer_tflops"],
         "layer_mfma_frac": res["layer_mfma_frac"],
         "active_experts": res["active_experts"],
+        "m_tiles": res["m_tiles"],
         "stage_ms": res["stage_ms"],
         "roofline": res["roofline"],
         "cpu_baseline": cpu,
