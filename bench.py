@@ -319,7 +319,8 @@ def run_config(name: str, device, steps: int, warmup: int, variant: str = "defau
 # Profiles: the rocprofv3 commands behind profiles/ and their reduction to the committed summaries
 # ------------------------------------------------------------------------------------------------
 COPY_BYTES = 1 << 31  # calibration copy: reads and writes exactly this many bytes
-GMM1_KERNEL = re.compile(r"(gg_pp|grouped_gemm\w*)_kernel<.*, ([2-5])>\(")  # SwiGLU epilogues 2..5
+# SwiGLU epilogues (2..5): the 8-wave kernel's third template argument, the 4-wave kernels' last
+GMM1_KERNEL = re.compile(r"gg_pp_kernel<\w+, \w+, [2-5][,>]|grouped_gemm\w*_kernel<.*, [2-5]>\(")
 
 
 def profile_commands(workload: str, out: str = "$GRAFT_REPO_ROOT/gpurun_out/prof") -> dict:

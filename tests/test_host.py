@@ -138,8 +138,12 @@ def test_bench_profile_summary(tmp_path):
                [["__amd_rocclr_copyBuffer", "FETCH_SIZE", copy_kib / 2], ["other", "FETCH_SIZE", 1.0]])
     _write_csv(out / "copy" / "write" / "pmc_counter_collection.csv", cnt,
                [["__amd_rocclr_copyBuffer", "WRITE_SIZE", copy_kib]])
-    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2>(GGParams)"
-    g2 = "void (anonymous namespace)::gg_pp_kernel<false, false, 0>(GGParams)"
+    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true>(GGParams)"
+    g2 = "void (anonymous namespace)::gg_pp_kernel<false, false, 0, true>(GGParams)"
+    for name, is_g1 in ((g1, True), (g2, False), ("void grouped_gemm_kernel<GGCfg<64, 1, 3, 3, 256, 2, 2, 2, false>, "
+                                                   "true, true, 3>(GGParams)", True),
+                        ("void grouped_gemm_kernel<false, false, 1>(GGParams)", False)):
+        assert bool(bench.GMM1_KERNEL.search(name)) == is_g1, name
     d = out / "dsv3_bf16"
     _write_csv(d / "fetch" / "pmc_counter_collection.csv", cnt,
                [[g1, "FETCH_SIZE", 900.0], [g1, "FETCH_SIZE", 1100.0], [g2, "FETCH_SIZE", 5.0]])
