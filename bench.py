@@ -53,7 +53,7 @@ def log(msg: str) -> None:
 class Layer:
     """Synthetic inputs + weights of one config, resident on the GPU."""
 
-    def __init__(self, name: str, device: torch.device, bf16_layout: str = "EOI", mx_layout: str = "EIO"):
+    def __init__(self, name: str, device: torch.device, bf16_layout: str = "EOI", mx_layout: str = "EIO_GU"):
         from hyper_multicore_amd import _lib, ops
         self.ops = ops
         self._lib = _lib
@@ -103,6 +103,13 @@ class Layer:
                 e2, t2 = ops.mx_weight_to_eoi(d2, s2)
                 del d1, s1, d2, s2
                 self.w1, self.w2, self.s1, self.s2, self.layout = e1.view(torch.uint8), e2.view(torch.uint8), t1, t2, "EOI"
+            elif mx_layout == "EIO_GU":
+                # one-time weight preparation: W1's gate and up columns interleaved in 128-column
+                # blocks, so a GMM1 tile reads its gate and up columns as one run per weight row
+                self.w1, self.s1 = ops.interleave_gate_up(d1, s1)
+                del d1, s1
+                self.w1 = self.w1.view(torch.uint8)
+                self.layout = "EIO_GU"
         torch.cuda.synchronize()
         self.out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
 
@@ -118,6 +125,20 @@ class Layer:
                         precision=c["precision"], layout=self.layout, w1_scale=self.s1, w2_scale=self.s2,
                         out=self.out, stage_events=stage_events)
         return ids
+
+    def w1_root(self, experts=slice(None)):
+        """W1 (and its MX col_scale) of the given experts with gate columns [0, I) then up columns
+        [I, 2I), whatever layout the layer runs: the weights the CPU references take."""
+        w1, s1 = self.w1[experts], None if self.s1 is None else self.s1[experts]
+        if self.layout != "EIO_GU":
+            return w1, s1
+        I = self.c["I"]
+        blocks = lambda t, half: torch.cat([t[..., b * 256 + half * 128: b * 256 + half * 128 + 128]
+                                            for b in range(I // 128)], dim=-1)
+        w1 = torch.cat([blocks(w1, 0), blocks(w1, 1)], dim=-1)
+        s1 = torch.cat([blocks(s1.transpose(-1, -2), 0), blocks(s1.transpose(-1, -2), 1)],
+                       dim=-1).transpose(-1, -2).contiguous()
+        return w1, s1
 
     def counts(self):
         ids = self.step()
@@ -253,7 +274,9 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
         if layer.layout == "EIO":
             w1, w2 = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
     else:
-        w1 = orc.mx_dequantize_weight_cols(layer.w1.cpu(), layer.s1.cpu()).to(torch.bfloat16).transpose(1, 2).contiguous()
+        w1r, s1r = layer.w1_root()
+        w1 = orc.mx_dequantize_weight_cols(w1r.cpu(), s1r.cpu()).to(torch.bfloat16).transpose(1, 2).contiguous()
+        del w1r, s1r
         w2 = orc.mx_dequantize_weight_cols(layer.w2.cpu(), layer.s2.cpu()).to(torch.bfloat16).transpose(1, 2).contiguous()
     I = c["I"]
     gate_w, up_w = w1[:, :I], w1[:, I:]
@@ -292,7 +315,7 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
 
 
 def run_config(name: str, device, steps: int, warmup: int, variant: str = "default",
-               bf16_layout: str = "EOI", mx_layout: str = "EIO") -> dict:
+               bf16_layout: str = "EOI", mx_layout: str = "EIO_GU") -> dict:
     layer = Layer(name, device, bf16_layout, mx_layout)
     counts = layer.counts()
     work = gmm_work(layer.c, counts)
@@ -494,8 +517,10 @@ def main() -> int:
                     help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
     ap.add_argument("--bf16-layout", default="EOI", choices=["EOI", "EIO"],
                     help="expert-weight layout of the bf16 configs (EIO: the reference module's default)")
-    ap.add_argument("--mx-layout", default="EIO", choices=["EIO", "EOI"],
-                    help="MX expert-weight layout (EIO: the reference's col_data root; EOI: re-laid out once)")
+    ap.add_argument("--mx-layout", default="EIO_GU", choices=["EIO", "EOI", "EIO_GU"],
+                    help="MX expert-weight layout (EIO: the reference's col_data root; EOI: re-laid out once with "
+                         "K contiguous; EIO_GU: the root with W1's gate and up columns interleaved once, as the "
+                         "MegaMoE module prepares it)")
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="time the DSv3-shape grouped GEMMs on their own per layout and variant (one JSON line)")
     ap.add_argument("--profile-commands", metavar="WORKLOAD", default=None,

@@ -11,7 +11,7 @@ from ctypes import POINTER, Structure, c_float, c_int32, c_int64, c_size_t, c_ui
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmi355moe.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 NOALLOC_MAX_GROUPS = 4096
@@ -30,7 +30,7 @@ FEATURE_SPLIT_ROLES = 256
 GEMM_VARIANT = {"default": 0, "b6": 1, "dv": 2, "sp": 3, "sp4": 4, "pp": 5, "w4": 6}
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
-LAYOUT = {"EIO": 0, "EOI": 1}
+LAYOUT = {"EIO": 0, "EOI": 1, "EIO_GU": 2}
 
 _ERRORS = {
     EINVAL: "invalid argument",
@@ -121,6 +121,7 @@ _SIGNATURES = [
     ("mi355moe_mx_weight_scale_ld", c_int64, [c_int32]),
     ("mi355moe_mx_weight_to_eoi", c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                             c_void_p]),
+    ("mi355moe_interleave_gate_up", c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p]),
     ("mi355moe_grouped_gemm_workspace_size", c_size_t, [c_int32]),
     ("mi355moe_grouped_gemm_bf16", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                              c_void_p, c_void_p, c_int32, c_void_p, c_size_t, c_void_p]),

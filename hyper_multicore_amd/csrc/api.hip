@@ -324,7 +324,9 @@ static int validate_fwd(const MI355MoeForwardArgs& a) {
   if (a.ids_dtype != MI355MOE_IDS_INT32 && a.ids_dtype != MI355MOE_IDS_INT64) return MI355MOE_EINVAL;
   if (a.precision != MI355MOE_PRECISION_BF16 && a.precision != MI355MOE_PRECISION_MXFP8) return MI355MOE_EINVAL;
   if (!mi355_gg_variant_valid(a.gemm_variant)) return MI355MOE_EUNSUPPORTED;
-  if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
+  if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI &&
+      a.weight_layout != MI355MOE_LAYOUT_EIO_GU)
+    return MI355MOE_EINVAL;
   if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;
   if (a.numerics_flags & ~(MI355MOE_NUMERICS_CLAMP_AFTER_SILU | MI355MOE_NUMERICS_PROBS_BEFORE_FC2))
     return MI355MOE_EINVAL;
@@ -432,6 +434,7 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   p1.G = E;
   p1.group_list = group_list;
   p1.tile_prefix = tile_prefix;
+  p1.gate_up_interleaved = a.weight_layout == MI355MOE_LAYOUT_EIO_GU;
   p1.C = ws + L.act;
   p1.ldc = I;
   p1.c_scale = mx ? (uint8_t*)(ws + L.act_scale) : nullptr;

@@ -156,6 +156,7 @@ int validate_bwd(const MI355MoeBackwardArgs& a) {
     return MI355MOE_EINVAL;
   if (a.num_experts > 4096 || a.top_k > 64 || a.top_k > a.num_experts) return MI355MOE_EINVAL;
   if (a.ids_dtype != MI355MOE_IDS_INT32 && a.ids_dtype != MI355MOE_IDS_INT64) return MI355MOE_EINVAL;
+  if (a.weight_layout == MI355MOE_LAYOUT_EIO_GU) return MI355MOE_EUNSUPPORTED;  // forward-only layout
   if (a.weight_layout != MI355MOE_LAYOUT_EIO && a.weight_layout != MI355MOE_LAYOUT_EOI) return MI355MOE_EINVAL;
   if (a.weight_grad_dtype != MI355MOE_GRAD_BF16 && a.weight_grad_dtype != MI355MOE_GRAD_FP32) return MI355MOE_EINVAL;
   if (a.num_tokens * (int64_t)a.top_k > INT32_MAX) return MI355MOE_EINVAL;

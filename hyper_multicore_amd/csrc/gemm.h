@@ -64,7 +64,20 @@ struct GGParams {
   // Rows of the whole GEMM when the caller knows them (0: not given); the 8-wave bf16 configuration
   // picks its tile height from their average per group.
   int64_t rows_hint;
+  // SwiGLU GEMMs: the weight's gate and up columns are interleaved in 128-column blocks (block b:
+  // gate columns 128 b ..+127, then up columns 128 b ..+127), so a tile's gate and up columns are
+  // one contiguous run per K row (0: gate columns [0, I) then up columns [I, 2I)).
+  int32_t gate_up_interleaved;
 };
+
+// Physical weight column of projection column c (gate: c < I, up: c >= I) in the gate/up
+// interleaved layout (identity when `gu` is 0).
+__host__ __device__ __forceinline__ int gate_up_col(int c, int I, int gu) {
+  const int up = (c >= I) ? 1 : 0;
+  const int cc = c - (up ? I : 0);
+  const int il = ((cc >> 7) << 8) + (up << 7) + (cc & 127);
+  return gu ? il : c;
+}
 
 
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, bool small = false);

@@ -124,7 +124,7 @@ MI355_HD DirectPlan direct_plan(const GGParams& p, int g, int nt, int64_t tile_r
   }
 #pragma unroll
   for (int q = 0; q < C::NI; ++q) {
-    int wc = tile_col_to_weight_col<C>(wave * C::WN + q * 32 + (lane & 31), nt, p.N, swiglu);
+    int wc = tile_col_to_weight_col<C>(wave * C::WN + q * 32 + (lane & 31), nt, p.N, swiglu, p.gate_up_interleaved);
     if (wc >= p.Ntot) wc = p.Ntot - 1;
     d.b[q] = (uint32_t)((int64_t)wc * p.b_row_bytes + 16 * (lane >> 5));
     d.bs[q] = mx ? (uint32_t)((int64_t)wc * p.b_scale_ld) : 0u;

@@ -107,13 +107,13 @@ MI355_HD bool gg_split_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
 // WN/2 gate columns followed by the matching WN/2 up columns, so a lane holds gate and up of the
 // same output element.
 template <class C>
-MI355_HD int tile_col_to_weight_col(int j, int nt, int I, bool swiglu) {
+MI355_HD int tile_col_to_weight_col(int j, int nt, int I, bool swiglu, int gu = 0) {
   if (!swiglu) return nt * C::BN + j;
   constexpr int H = C::WN / 2;
   static_assert(C::WN == 128 || C::WN == 64, "wave tile width");
   int q = j >> (C::WN == 128 ? 7 : 6), jj = j & (C::WN - 1);
   int base = nt * (C::BN / 2) + q * H;
-  return jj < H ? base + jj : I + base + (jj - H);
+  return gate_up_col(jj < H ? base + jj : I + base + (jj - H), I, gu);
 }
 
 MI355_HD int a_chunk_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }

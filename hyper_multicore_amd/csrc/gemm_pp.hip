@@ -91,11 +91,12 @@ struct Cfg {
 
 // Tile column j (0..255) -> weight column; SwiGLU: wave tile q's 64 columns are gate columns
 // nt * 128 + 32 q .. +31, then the up columns I + the same.
-__device__ __forceinline__ int tile_col(int j, int nt, int I, bool swiglu) {
+// With the gate/up interleaved weight layout the projection column goes through gate_up_col.
+__device__ __forceinline__ int tile_col(int j, int nt, int I, bool swiglu, int gu) {
   if (!swiglu) return nt * BN + j;
   const int q = j >> 6, jj = j & 63;
   const int base = nt * (BN / 2) + q * 32;
-  return jj < 32 ? base + jj : I + base + (jj - 32);
+  return gate_up_col(jj < 32 ? base + jj : I + base + (jj - 32), I, gu);
 }
 
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -230,21 +231,21 @@ template <bool MX, bool B_KN, bool SWIGLU>
 __device__ __forceinline__ uint32_t b_off(const GGParams& p, int nt, int i, int lane) {
   if constexpr (!B_KN) {  // K-contiguous weights: like the activations, one weight row per tile column
     const int r = row_of(i, lane);
-    int wc = tile_col(r, nt, p.N, SWIGLU);
+    int wc = tile_col(r, nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc >= p.Ntot) wc = p.Ntot - 1;
     return (uint32_t)wc * (uint32_t)p.b_row_bytes + (uint32_t)(chunk_of(r, lane) * 16);
   } else if constexpr (MX) {
     const int L16 = i * 64 + lane;  // K rows of 256 bytes: copy i covers K rows 4 i ..+3
     const int k = L16 >> 4;
     const int c = (L16 & 15) ^ (k & 15);
-    int wc = tile_col(c * 16, nt, p.N, SWIGLU);
+    int wc = tile_col(c * 16, nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc > p.Ntot - 16) wc = p.Ntot - 16;
     return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc;
   } else {
     const int L16 = i * 64 + lane;  // K rows of 512 bytes: copy i covers K rows 2 i, 2 i + 1
     const int k = L16 >> 5;
     const int c = (L16 & 31) ^ ((k & 7) << 1);
-    int wc = tile_col(c * 8, nt, p.N, SWIGLU);
+    int wc = tile_col(c * 8, nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc > p.Ntot - 8) wc = p.Ntot - 8;
     return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc * 2u;
   }
@@ -274,7 +275,7 @@ __device__ __forceinline__ void issue_stage(const GGParams& p, const Plan<C::CPW
     // col_scale [G, K/64, Ntot, 2]: wave w (and w + 4) copies 64-K step (w >> 1) & 1, tile columns
     // 128 (w & 1) ..+127
     const uint32_t so = (uint32_t)((wave & 1) * 256 + lane * 4);
-    int wc = tile_col((wave & 1) * 128 + lane * 2, pl.nt, p.N, SWIGLU);
+    int wc = tile_col((wave & 1) * 128 + lane * 2, pl.nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc > p.Ntot - 2) wc = p.Ntot - 2;
     const uint32_t bso = (uint32_t)((((wave >> 1) & 1) * p.Ntot + wc) * 2);
     dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), so,

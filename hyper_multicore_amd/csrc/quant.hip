@@ -396,3 +396,35 @@ extern "C" int mi355moe_mx_weight_to_eoi(const uint8_t* col_data, const uint8_t*
                      groups, kdim, cols, ld, scale);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
+
+// ---- gate/up interleave of the GMM1 weight (layout EIO_GU) ------------------------------------
+// One thread per 16-byte chunk of a row: a chunk lies inside one 128-column block (128 columns are
+// >= 128 bytes), so it moves whole to gate_up_col of its first column.
+__global__ __launch_bounds__(256) void interleave_gate_up_kernel(const uint4* src, int64_t rows, int I, int elem_bytes,
+                                                                 uint4* dst) {
+  const int64_t chunks_per_row = (int64_t)2 * I * elem_bytes / 16;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= rows * chunks_per_row) return;
+  const int64_t row = id / chunks_per_row;
+  const int chunk = (int)(id - row * chunks_per_row);
+  const int col = chunk * 16 / elem_bytes;
+  const int to = gate_up_col(col, I, 1) * elem_bytes / 16;
+  dst[row * chunks_per_row + to] = src[id];
+}
+
+extern "C" int mi355moe_interleave_gate_up(const void* src, int64_t rows, int32_t intermediate_size,
+                                           int32_t elem_bytes, void* dst, void* stream) {
+  if (rows < 0 || intermediate_size <= 0 || intermediate_size % 128 || (elem_bytes != 1 && elem_bytes != 2))
+    return MI355MOE_EINVAL;
+  if (rows == 0) return MI355MOE_OK;
+  if (src == nullptr || dst == nullptr || ((uintptr_t)src | (uintptr_t)dst) % 16) return MI355MOE_EINVAL;
+  const int64_t row_bytes = (int64_t)2 * intermediate_size * elem_bytes;
+  const char* s = (const char*)src;
+  const char* d = (const char*)dst;
+  if (s < d + rows * row_bytes && d < s + rows * row_bytes) return MI355MOE_EINVAL;  // overlap
+  const int64_t n = rows * (row_bytes / 16);
+  if ((n + 255) / 256 > INT32_MAX) return MI355MOE_EINVAL;
+  hipLaunchKernelGGL(interleave_gate_up_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint4*)src, rows, intermediate_size, elem_bytes, (uint4*)dst);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}

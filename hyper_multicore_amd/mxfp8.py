@@ -12,7 +12,8 @@ import torch
 
 from . import _lib, ops
 
-__all__ = ["quantize_expert_weight", "resolve_forward_weight", "resolve_backward_weight", "prepared_eoi_weight"]
+__all__ = ["quantize_expert_weight", "resolve_forward_weight", "resolve_backward_weight", "prepared_eoi_weight",
+           "prepared_gate_up_weight"]
 
 
 def quantize_expert_weight(weight: torch.Tensor, *, backward_axis: bool = False) -> torch.Tensor:
@@ -82,19 +83,31 @@ def resolve_backward_weight(root, logical_shape: tuple[int, int, int], device: t
     return data.view(torch.uint8).view(E, M, N), scale.view(E, M, N // 64, 2)
 
 
-def prepared_eoi_weight(root, data: torch.Tensor, scale: torch.Tensor):
-    """The K-contiguous re-layout of a root's (data, scale) for the GEMM (``ops.mx_weight_to_eoi``),
-    built on first use and cached on the root. The cache is keyed on the storage of the root's
-    fields, so a root whose ``col_data`` / ``col_scale`` are replaced is re-laid-out again; in-place
-    writes into the same storage are not detected (roots are treated as immutable weights)."""
+def _cached_on_root(root, attr: str, data: torch.Tensor, scale: torch.Tensor, prepare):
+    """prepare(data, scale), built on first use and cached on the root under `attr`. The cache is keyed
+    on the storage of the root's fields, so a root whose ``col_data`` / ``col_scale`` are replaced is
+    prepared again; in-place writes into the same storage are not detected (roots are treated as
+    immutable weights)."""
     key = (data.data_ptr(), scale.data_ptr(), tuple(data.shape), data.device)
-    cached = getattr(root, "_mi355_eoi", None)
+    cached = getattr(root, attr, None)
     if cached is not None and cached[0] == key:
         return cached[1], cached[2]
-    d, s = ops.mx_weight_to_eoi(data, scale)
+    d, s = prepare(data, scale)
     d = d.view(torch.uint8)
     try:
-        root._mi355_eoi = (key, d, s)
-    except AttributeError:  # roots without attribute storage are re-laid-out per call
+        setattr(root, attr, (key, d, s))
+    except AttributeError:  # roots without attribute storage are prepared per call
         pass
     return d, s
+
+
+def prepared_eoi_weight(root, data: torch.Tensor, scale: torch.Tensor):
+    """The K-contiguous re-layout of a root's (data, scale) for the GEMM (``ops.mx_weight_to_eoi``),
+    cached on the root."""
+    return _cached_on_root(root, "_mi355_eoi", data, scale, ops.mx_weight_to_eoi)
+
+
+def prepared_gate_up_weight(root, data: torch.Tensor, scale: torch.Tensor):
+    """The GMM1 root's (data, scale) with gate and up columns interleaved in 128-column blocks
+    (``ops.interleave_gate_up``, layout ``"EIO_GU"``), cached on the root."""
+    return _cached_on_root(root, "_mi355_gate_up", data, scale, ops.interleave_gate_up)

@@ -465,6 +465,30 @@ def mx_weight_to_eoi(col_data: torch.Tensor, col_scale: torch.Tensor):
     return data, scale
 
 
+def interleave_gate_up(w1: torch.Tensor, w1_scale: torch.Tensor | None = None):
+    """The GMM1 weight in layout ``"EIO_GU"``: w1 [E, H, 2I] (bf16, or MX col_data e4m3) with its gate
+    columns [0, I) and up columns [I, 2I) interleaved in 128-column blocks (gate 128 b ..+127, then up
+    128 b ..+127), and the MX col_scale [E, H/64, 2I, 2] the same way. Values are unchanged; the
+    forward with ``layout="EIO_GU"`` on these equals ``"EIO"`` on the originals bit for bit, and reads
+    each tile's gate and up columns as one run. Returns (w1, w1_scale or None); w2 stays EIO."""
+    lib = _lib.load()
+    device = _require_gpu(w1, w1_scale)
+    if w1.ndim != 3 or w1.shape[2] % 256 or w1.element_size() not in (1, 2):
+        raise ValueError("interleave_gate_up takes w1 [E, H, 2I] with I % 128 == 0")
+    E, H, I = w1.shape[0], w1.shape[1], w1.shape[2] // 2
+    out = torch.empty_like(w1, memory_format=torch.contiguous_format)
+    _lib.check(lib.mi355moe_interleave_gate_up(_ptr(w1.contiguous()), E * H, I, w1.element_size(), _ptr(out),
+                                               _stream(device)), "mi355moe_interleave_gate_up")
+    scale = None
+    if w1_scale is not None:
+        if w1_scale.shape != (E, H // 64, 2 * I, 2) or w1_scale.element_size() != 1:
+            raise ValueError("w1_scale must be the MX col_scale [E, H/64, 2I, 2]")
+        scale = torch.empty_like(w1_scale, memory_format=torch.contiguous_format)
+        _lib.check(lib.mi355moe_interleave_gate_up(_ptr(w1_scale.contiguous()), E * (H // 64), I, 2, _ptr(scale),
+                                                   _stream(device)), "mi355moe_interleave_gate_up")
+    return out, scale
+
+
 def grouped_gemm_mxfp8(xq: torch.Tensor, x_scale: torch.Tensor, w_data: torch.Tensor, w_scale: torch.Tensor,
                        group_list: torch.Tensor, layout: str = "EIO", *,
                        gemm_variant: str | None = None) -> torch.Tensor:

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MI355MOE_ABI_VERSION 5
+#define MI355MOE_ABI_VERSION 6
 
 enum {
   MI355MOE_OK_CODE = 0,
@@ -38,8 +38,11 @@ enum { MI355MOE_IDS_INT32 = 0, MI355MOE_IDS_INT64 = 1 };
 enum { MI355MOE_PRECISION_BF16 = 0, MI355MOE_PRECISION_MXFP8 = 1 };
 /* Expert weight layouts (modules/mega_moe/module.py:276-279):
  *   EIO: w1 [E, H, 2I], w2 [E, I, H]   (input-major rows, output contiguous)
- *   EOI: w1 [E, 2I, H], w2 [E, H, I]   (output-major rows, input contiguous) */
-enum { MI355MOE_LAYOUT_EIO = 0, MI355MOE_LAYOUT_EOI = 1 };
+ *   EOI: w1 [E, 2I, H], w2 [E, H, I]   (output-major rows, input contiguous)
+ *   EIO_GU (no reference counterpart; forward only): EIO, with w1's gate and up columns
+ *   interleaved in 128-column blocks by mi355moe_interleave_gate_up (and, for MXFP8, w1_scale's
+ *   columns the same way); w2 is plain EIO. */
+enum { MI355MOE_LAYOUT_EIO = 0, MI355MOE_LAYOUT_EOI = 1, MI355MOE_LAYOUT_EIO_GU = 2 };
 
 /* ---------------------------------------------------------------------------------------------
  * ABI version of the loaded library (no reference counterpart; used by the loader check).
@@ -277,6 +280,19 @@ int mi355moe_mx_weight_to_eoi(const uint8_t* col_data, const uint8_t* col_scale,
                               int32_t cols, uint8_t* data, uint8_t* scale, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Gate/up interleave of the GMM1 weight for MI355MOE_LAYOUT_EIO_GU (no reference counterpart: a
+ * one-time weight preparation that moves columns and changes no value). src holds `rows` rows of
+ * 2I elements of elem_bytes bytes each, gate columns [0, I) then up columns [I, 2I); dst gets, for
+ * each 128-column block b, gate columns 128 b ..+127 then up columns 128 b ..+127. Use
+ * rows = E * H with elem_bytes 2 (bf16 w1) or 1 (e4m3 col_data), and rows = E * H / 64 with
+ * elem_bytes 2 for the MXFP8 col_scale [E, H/64, 2I, 2] (one 2-byte pair per column).
+ * I % 128 == 0; src and dst must not overlap. A SwiGLU tile then reads its gate and up columns as
+ * one contiguous run per weight row instead of two runs 2I apart.
+ */
+int mi355moe_interleave_gate_up(const void* src, int64_t rows, int32_t intermediate_size, int32_t elem_bytes,
+                                void* dst, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Grouped GEMM over consecutive row segments (one segment per group):
  *   out[r, :] = x[r, :] @ W_g        for rows r of group g,
  * group_list is the int64 inclusive cumulative row count per group (the grouped_matmul
@@ -335,6 +351,8 @@ int mi355moe_grouped_gemm_mxfp8(const uint8_t* xq, const uint8_t* x_scale, int64
  * MXFP8: w1/w2 are col_data e4m3 EIO [E,H,2I] / [E,I,H] with col_scale [E,H/64,2I,2] /
  * [E,I/64,H,2] (docs: MXFP8 weight contract), or, with weight_layout EOI, the same weights after
  * mi355moe_mx_weight_to_eoi: [E,2I,H] / [E,H,I] with row scales [E,2I,ld(H)] / [E,H,ld(I)].
+ * weight_layout EIO_GU (bf16 and MXFP8): w1 and w1_scale after mi355moe_interleave_gate_up, w2 and
+ * w2_scale EIO; results are those of EIO on the original weights, bit for bit.
  * H and I must be multiples of 128.
  * tokens_per_expert (optional) is a trusted int32 histogram of topk_ids; when NULL it is
  * computed. Workspace: mi355moe_moe_forward_workspace_size(args) bytes.

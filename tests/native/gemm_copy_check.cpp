@@ -312,9 +312,11 @@ struct Layout {
 };
 
 // Tile column n (0 .. BN-1) of n-tile nt -> weight column; false when its output column is past N.
-// (SwiGLU: each WN-wide wave tile holds WN/2 gate columns and then the WN/2 matching up columns.)
+// (SwiGLU: each WN-wide wave tile holds WN/2 gate columns and then the WN/2 matching up columns.
+// With `gu` the weight stores gate and up columns in alternating 128-column blocks: output column o
+// has its gate column in block 2 (o / 128) and its up column in block 2 (o / 128) + 1.)
 template <class C>
-static bool tile_weight_col(int n, int nt, int N, bool swiglu, int64_t* wcol) {
+static bool tile_weight_col(int n, int nt, int N, bool swiglu, int gu, int64_t* wcol) {
   if (!swiglu) {
     const int64_t o = (int64_t)nt * C::BN + n;
     *wcol = o;
@@ -322,7 +324,10 @@ static bool tile_weight_col(int n, int nt, int N, bool swiglu, int64_t* wcol) {
   }
   const int H = C::WN / 2, q = n / C::WN, jj = n % C::WN;
   const int64_t o = (int64_t)nt * (C::BN / 2) + q * H + (jj % H);
-  *wcol = jj < H ? o : N + o;
+  if (gu)
+    *wcol = (o / 128) * 256 + (jj < H ? 0 : 128) + o % 128;
+  else
+    *wcol = jj < H ? o : N + o;
   return o < N;
 }
 
@@ -482,22 +487,22 @@ static const uint8_t* expected_src(const GGParams& p, const Layout& L, const Ite
       case R_B: {
         if (!B_KN) {  // K-contiguous weight rows, laid out like the activations
           const int n = rel / 64, cpos = (rel % 64) / 16, c = cpos ^ ((n >> 2) & 3);
-          if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+          if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
           return L.b_at(it.g, (kstage * C::KB + c * 16) / L.esize, wcol);
         }
         if (MX) {  // 64 K rows of 256 bytes, chunk c at c ^ (k & 15), 16 columns per chunk
           const int k = rel / 256, cpos = (rel % 256) / 16, c = cpos ^ (k & 15);
-          if (!tile_weight_col<C>(c * 16, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+          if (!tile_weight_col<C>(c * 16, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
           return L.b_at(it.g, kstage * 64 + k, wcol);
         }
         // bf16: 32 K rows of 512 bytes, chunk c at c ^ ((k & 7) << 1), 8 columns per chunk
         const int k = rel / 512, cpos = (rel % 512) / 16, c = cpos ^ ((k & 7) << 1);
-        if (!tile_weight_col<C>(c * 8, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+        if (!tile_weight_col<C>(c * 8, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
         return L.b_at(it.g, kstage * 32 + k, wcol);
       }
       case R_BS: {  // two codes for each of tile columns 2m, 2m+1 (4 bytes per lane)
         const int n = (rel / 4) * 2;
-        if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+        if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
         return L.bs_col_at(it.g, kstage, wcol);
       }
       case R_AS: {  // 16 codes (8 stages) per row
@@ -507,7 +512,7 @@ static const uint8_t* expected_src(const GGParams& p, const Layout& L, const Ite
       }
       case R_BSR: {  // 16 codes (8 stages) per tile column
         const int n = rel / 16;
-        if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, &wcol)) return nullptr;
+        if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
         return L.bs_row_at(it.g, wcol, (int64_t)stage * 16);
       }
     }
@@ -1071,7 +1076,7 @@ static int sim_forward(const GGParams& p) {
       const int Kper = p.K / splits;
       auto value = [&](int row, int col) -> double {
         int64_t wc;
-        if (row >= ctx.rows_valid || !tile_weight_col<C>(col, ctx.nt, p.N, SWIGLU, &wc)) return NAN;
+        if (row >= ctx.rows_valid || !tile_weight_col<C>(col, ctx.nt, p.N, SWIGLU, p.gate_up_interleaved, &wc)) return NAN;
         const int64_t r = ctx.tile_row0 + row;
         const int64_t sr = p.a_row_index ? p.a_row_index[r] / p.a_row_div : r;
         double sum = 0.0;
@@ -1364,7 +1369,7 @@ static int sim_direct(const GGParams& p) {
         // expected sources (independent of the plan): weight column of subtile q, activation chunk
         for (int q = 0; q < C::NI; ++q) {
           int64_t wc;
-          const bool live = tile_weight_col<C>(wave * C::WN + q * 32 + lane % 32, nt, p.N, SWIGLU, &wc);
+          const bool live = tile_weight_col<C>(wave * C::WN + q * 32 + lane % 32, nt, p.N, SWIGLU, p.gate_up_interleaved, &wc);
           if (!live) continue;
           for (int s = 0; s < nk; s += std::max(1, nk / 4))
             for (int h = 0; h < 2; ++h) {
@@ -1514,7 +1519,7 @@ static int sim_direct(const GGParams& p) {
                 const int row = i * 32 + 8 * (r / 4) + 4 * (l / 32) + r % 4;
                 const int col = w * C::WN + j * 32 + l % 32;
                 int64_t wc;
-                if (row >= rows_valid || !tile_weight_col<C>(col, nt, p.N, SWIGLU, &wc)) continue;
+                if (row >= rows_valid || !tile_weight_col<C>(col, nt, p.N, SWIGLU, p.gate_up_interleaved, &wc)) continue;
                 double want = 0.0;
                 for (int64_t kk = 0; kk < p.K; ++kk) {
                   double av, bv;
@@ -1926,7 +1931,7 @@ struct Scenario {
 };
 
 static std::vector<Scenario> scenarios() {
-  const int L_EIO = MI355MOE_LAYOUT_EIO, L_EOI = MI355MOE_LAYOUT_EOI;
+  const int L_EIO = MI355MOE_LAYOUT_EIO, L_EOI = MI355MOE_LAYOUT_EOI, L_GU = MI355MOE_LAYOUT_EIO_GU;
   const int BF = MI355MOE_PRECISION_BF16, MX = MI355MOE_PRECISION_MXFP8;
   std::vector<Scenario> s;
   // grouped GEMM C-ABI: ragged and empty groups, partial tiles, N not a multiple of the tile
@@ -1963,6 +1968,8 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"gemm_mx_eio_decode_big", big([=] { gemm_mx(decode_counts(48, 6), 1024, 512, L_EIO); })});
   s.push_back({"moe_bf16_eio_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); })});
   s.push_back({"moe_mx_eio_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); })});
+  s.push_back({"moe_bf16_gu_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_GU, 0.0); })});
+  s.push_back({"moe_mx_gu_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0); })});
   // functional emulation (random operands; accumulators vs a reference GEMM). The EIO bf16 / MX and
   // EOI bf16 cases run on the GPU already and calibrate the instruction models.
   auto emu = [](std::function<void()> f) {
@@ -1992,6 +1999,7 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_b6_mx_eio", b6(emu([=] { gemm_mx({70, 0, 129, 300}, 1024, 256, L_EIO); }))});
   s.push_back({"b6_moe_bf16", b6([=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
   s.push_back({"b6_moe_mx_eio", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
+  s.push_back({"b6_moe_mx_gu", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); })});
   s.push_back({"b6_moe_mx_eoi", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EOI, 0.0); })});
   // split copy roles (variants sp: 3 activation / 6 weight slots; sp4: 4 / 5), MXFP8 EIO; each scenario
   // must run them
@@ -2009,6 +2017,7 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"sp_gemm_mx_eio_long_k", sp(SP, [=] { gemm_mx({256, 256}, 2560, 272, L_EIO); })});
   s.push_back({"sp_gemm_mx_eio_decode_big", big(sp(SP, [=] { gemm_mx(decode_counts(48, 6), 1024, 512, L_EIO); }))});
   s.push_back({"sp_moe_mx_eio", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
+  s.push_back({"sp_moe_mx_gu", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); })});
   s.push_back({"sp_moe_mx_eio_decode_big", big(sp(SP, [=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); }))});
   s.push_back({"sp4_gemm_mx_eio", sp(SP4, [=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EIO); })});
   s.push_back({"sp4_moe_mx_eio", sp(SP4, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
@@ -2018,6 +2027,7 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"sp_gemm_bf16_eio", sp(SP, [=] { gemm_bf16({100, 0, 300, 1, 129}, 512, 768, L_EIO); })});
   s.push_back({"sp_gemm_bf16_eio_decode_big", big(sp(SP, [=] { gemm_bf16(decode_counts(48, 6), 512, 512, L_EIO); }))});
   s.push_back({"sp_moe_bf16_eio", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
+  s.push_back({"sp_moe_bf16_gu", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_GU, 0.0); })});
   s.push_back({"sp4_moe_bf16_eio", sp(SP4, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
   s.push_back({"emu_sp_bf16_eio", sp(SP, emu([=] { gemm_bf16({70, 0, 129, 300}, 512, 512, L_EIO); }))});
   s.push_back({"emu_sp_bf16_eio_decode", big(sp(SP, emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EIO); })))});
@@ -2076,6 +2086,8 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"moe_mx_eoi", [=] { moe_forward(96, 4, 16, 512, 256, MX, L_EOI, 1.1); }});
   s.push_back({"moe_mx_eoi_prefill", [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EOI, 0.0); }});
   s.push_back({"moe_mx_eio_prefill", [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); }});
+  s.push_back({"moe_mx_gu_prefill", [=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); }});
+  s.push_back({"moe_bf16_gu", [=] { moe_forward(96, 4, 16, 512, 256, BF, L_GU, 1.1); }});
   s.push_back({"moe_bf16_numerics_clamp", [=] { moe_forward(96, 4, 16, 512, 256, BF, L_EIO, 1.1, 0, 7.0f); }});
   s.push_back({"moe_bf16_numerics_after_silu",
                [=] { moe_forward(96, 4, 16, 512, 256, BF, L_EOI, 1.1, MI355MOE_NUMERICS_CLAMP_AFTER_SILU, 7.0f); }});

@@ -48,7 +48,7 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.mi355moe_moe_forward_workspace_size(ctypes.byref(f)) == 0
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
     f = _lib.ForwardArgs(num_tokens=16, hidden_size=1024, intermediate_size=512, num_experts=8, top_k=2,
-                         ids_dtype=0, precision=1, weight_layout=2)  # no such layout
+                         ids_dtype=0, precision=1, weight_layout=3)  # no such layout
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) == _lib.EINVAL
     f.weight_layout = 1  # MXFP8 EOI (re-laid-out weights): operands missing, or the path switched off
     assert lib.mi355moe_moe_forward(ctypes.byref(f), None, 0, None) in (_lib.EINVAL, _lib.EUNSUPPORTED)
@@ -181,3 +181,21 @@ def test_gemm_variant_is_per_call():
         assert ops.gemm_variant() == "w4" and seen == [os.environ.get("MI355MOE_GG_VARIANT") or "default"]
     finally:
         ops.set_gemm_variant(prev)
+
+
+def test_interleave_gate_up_validation():
+    """The gate/up interleave refuses bad sizes, element widths, misaligned or overlapping buffers
+    before any launch; the backward refuses the forward-only interleaved layout."""
+    from hyper_multicore_amd import _lib
+    lib = _lib.load()
+    f = lib.mi355moe_interleave_gate_up
+    assert f(None, 0, 128, 1, None, None) == _lib.OK  # nothing to move
+    assert f(16, 4, 192, 1, 4096, None) == _lib.EINVAL  # I % 128
+    assert f(16, 4, 128, 4, 4096, None) == _lib.EINVAL  # element width
+    assert f(None, 4, 128, 1, 4096, None) == _lib.EINVAL
+    assert f(16, 4, 128, 1, 4104, None) == _lib.EINVAL  # dst not 16-byte aligned
+    assert f(4096, 4, 128, 2, 4096 + 512, None) == _lib.EINVAL  # overlap (rows of 512 bytes)
+    b = _lib.BackwardArgs(num_tokens=16, hidden_size=1024, intermediate_size=512, num_experts=8, top_k=2,
+                          ids_dtype=0, weight_layout=_lib.LAYOUT["EIO_GU"])
+    assert lib.mi355moe_moe_backward_workspace_size(ctypes.byref(b)) == 0
+    assert lib.mi355moe_moe_backward(ctypes.byref(b), None, 0, None) == _lib.EUNSUPPORTED

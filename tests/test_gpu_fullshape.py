@@ -23,7 +23,8 @@ def _expert_weights(layer, e):
         if layer.layout == "EOI":
             return layer.w1[e].float().t().contiguous().cpu(), layer.w2[e].float().t().contiguous().cpu()
         return layer.w1[e].float().cpu(), layer.w2[e].float().cpu()
-    w1 = orc.mx_dequantize_weight_cols(layer.w1[e:e + 1], layer.s1[e:e + 1])[0]
+    w1r, s1r = layer.w1_root(slice(e, e + 1))
+    w1 = orc.mx_dequantize_weight_cols(w1r, s1r)[0]
     w2 = orc.mx_dequantize_weight_cols(layer.w2[e:e + 1], layer.s2[e:e + 1])[0]
     return w1.cpu(), w2.cpu()
 

@@ -195,9 +195,11 @@ def test_mx_backward_resolves_fresh_row_axis_and_keeps_forward_columns(monkeypat
         return (grad_out.clone(), torch.zeros(E, H, 2 * I), torch.zeros(E, I, H),
                 torch.zeros(T, K) if kw["need_topk_grad"] else None)
 
+    from hyper_multicore_amd import mxfp8
     monkeypatch.setattr(ops, "features", lambda: 0)
     monkeypatch.setattr(ops, "moe_forward", fake_forward)
     monkeypatch.setattr(ops, "moe_backward_mxfp8", fake_backward)
+    monkeypatch.setattr(mxfp8, "prepared_gate_up_weight", lambda root, d, s: (d, s))  # the GPU re-layout
     ex = hm.MegaMoeExperts(hidden_size=H, intermediate_size=I, num_experts=E, top_k=K, precision="mxfp8")
     x = torch.ones((T, H), dtype=torch.bfloat16, requires_grad=True)
     probs = torch.ones((T, K), requires_grad=True)
