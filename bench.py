@@ -83,10 +83,14 @@ class Layer:
             self.skew = 8.0 * (logp - torch.log(-torch.log(u)))
         w1 = torch.randn(E, 2 * I, H, device=device, generator=g).mul_(c["wstd"]).to(torch.bfloat16)  # EOI
         w2 = torch.randn(E, H, I, device=device, generator=g).mul_(c["wstd"]).to(torch.bfloat16)      # EOI
-        if c["precision"] == "bf16" and bf16_layout == "EIO":  # the reference module's default layout
+        if c["precision"] == "bf16" and bf16_layout in ("EIO", "EIO_GU"):  # EIO: the reference module's default
             w1e, w2e = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
             del w1, w2
             self.w1, self.w2, self.s1, self.s2, self.layout = w1e, w2e, None, None, "EIO"
+            if bf16_layout == "EIO_GU":
+                self.w1, _ = ops.interleave_gate_up(w1e)
+                del w1e
+                self.layout = "EIO_GU"
         elif c["precision"] == "bf16":
             self.w1, self.w2, self.s1, self.s2, self.layout = w1, w2, None, None, "EOI"
         else:
@@ -136,8 +140,9 @@ class Layer:
         blocks = lambda t, half: torch.cat([t[..., b * 256 + half * 128: b * 256 + half * 128 + 128]
                                             for b in range(I // 128)], dim=-1)
         w1 = torch.cat([blocks(w1, 0), blocks(w1, 1)], dim=-1)
-        s1 = torch.cat([blocks(s1.transpose(-1, -2), 0), blocks(s1.transpose(-1, -2), 1)],
-                       dim=-1).transpose(-1, -2).contiguous()
+        if s1 is not None:
+            s1 = torch.cat([blocks(s1.transpose(-1, -2), 0), blocks(s1.transpose(-1, -2), 1)],
+                           dim=-1).transpose(-1, -2).contiguous()
         return w1, s1
 
     def counts(self):
@@ -269,9 +274,9 @@ def cpu_baseline(name: str, layer: Layer, budget_s: float = 20.0) -> dict:
     wr = layer.wr.cpu()
     bias = layer.bias.cpu()
     if c["precision"] == "bf16":
-        w1 = layer.w1.cpu()   # EOI [E, 2I, H] (EIO [E, H, 2I] transposed back below)
-        w2 = layer.w2.cpu()   # EOI [E, H, I]
-        if layer.layout == "EIO":
+        w1 = layer.w1_root()[0].cpu()   # EOI [E, 2I, H] (EIO [E, H, 2I] transposed back below)
+        w2 = layer.w2.cpu()             # EOI [E, H, I]
+        if layer.layout in ("EIO", "EIO_GU"):
             w1, w2 = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
     else:
         w1r, s1r = layer.w1_root()
@@ -515,7 +520,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv", "sp", "sp4", "pp", "w4"],
                     help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
-    ap.add_argument("--bf16-layout", default="EOI", choices=["EOI", "EIO"],
+    ap.add_argument("--bf16-layout", default="EOI", choices=["EOI", "EIO", "EIO_GU"],
                     help="expert-weight layout of the bf16 configs (EIO: the reference module's default)")
     ap.add_argument("--mx-layout", default="EIO_GU", choices=["EIO", "EOI", "EIO_GU"],
                     help="MX expert-weight layout (EIO: the reference's col_data root; EOI: re-laid out once with "

@@ -22,7 +22,7 @@ def _expert_weights(layer, e):
     if layer.c["precision"] == "bf16":
         if layer.layout == "EOI":
             return layer.w1[e].float().t().contiguous().cpu(), layer.w2[e].float().t().contiguous().cpu()
-        return layer.w1[e].float().cpu(), layer.w2[e].float().cpu()
+        return layer.w1_root(e)[0].float().cpu(), layer.w2[e].float().cpu()
     w1r, s1r = layer.w1_root(slice(e, e + 1))
     w1 = orc.mx_dequantize_weight_cols(w1r, s1r)[0]
     w2 = orc.mx_dequantize_weight_cols(layer.w2[e:e + 1], layer.s2[e:e + 1])[0]
