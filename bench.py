@@ -209,6 +209,38 @@ def measure(layer: Layer, steps: int, warmup: int) -> dict:
     return dict(ms_per_step=total_ms / steps, wall_s=wall, stage_ms=avg)
 
 
+def measure_graph(layer: Layer, steps: int) -> dict:
+    """The same step captured once into a HIP graph (torch.cuda.CUDAGraph) and replayed `steps` times:
+    the eager step's kernels without the host launch path between them (what a serving loop that
+    replays a captured decode step runs). The replay's output must equal the eager step's bit for bit."""
+    layer.step()
+    torch.cuda.synchronize()
+    eager_out = layer.out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on a side stream before capture (torch's capture recipe)
+        layer.step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        layer.step()
+    layer.out.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    matches = bool(torch.equal(layer.out, eager_out))
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del graph
+    return {"ms_per_step": round(ms, 4), "tokens_per_s": round(layer.c["T"] / (ms * 1e-3), 1),
+            "matches_eager": matches}
+
+
 def measured_traffic(workload: str, variant: str, layout: str, root: str = ROOT):
     """HBM bytes per GMM1 launch from the committed rocprofv3 counter passes of the same workload,
     GEMM variant and weight layout (profiles/traffic_<workload>_<variant>_<layout>.json, written by
@@ -339,6 +371,7 @@ def run_config(name: str, device, steps: int, warmup: int, variant: str = "defau
         "stage_ms": {k: round(v, 4) for k, v in m["stage_ms"].items()},
         "roofline": roofline(c, work, m["stage_ms"]["gmm1"],
                              measured_traffic(name, variant, layer.layout)),
+        "graph": measure_graph(layer, steps),
     }
     return res, layer
 
@@ -603,6 +636,7 @@ def main() -> int:
         "m_tiles": res["m_tiles"],
         "stage_ms": res["stage_ms"],
         "roofline": res["roofline"],
+        "graph": res["graph"],
         "cpu_baseline": cpu,
         "extra": extra,
     }
