@@ -155,7 +155,7 @@ int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const flo
 // scale_stage_stride > 0 writes the scales as stage-major code planes ([cols/128][4][stride / 4]); with
 // `mapping`, to the routed rows mapping[r * fanout + k] of each row r (negative entries skipped).
 // MX quantisation of fp32 rows (the SwiGLU output of EPI_SWIGLU_F32) into e4m3 [rows, cols] and the
-// stage-major code planes [cols/128][4][stage_stride / 4] (one thread per 32-element block).
+// stage-major code planes [cols/128][4][stage_stride / 4] (tiles of 64 rows x 256 columns).
 int mi355_mx_quant_act(const float* act, int64_t rows, int cols, uint8_t* q, uint8_t* planes, int64_t stage_stride,
                        hipStream_t st);
 // MX quantisation of token rows into q [tokens, cols] and per-token codes [tokens, cols/32] (scratch),

@@ -91,75 +91,104 @@ __global__ __launch_bounds__(256) void mx_quant_cols_kernel(const uint16_t* w, i
   col_scale[(((int64_t)g * (K / 64) + kb / 2) * N + n) * 2 + (kb & 1)] = (uint8_t)code;
 }
 
-// Thread (row, block b), rows fastest so that the code-plane bytes of a warp are contiguous.
+// MX quantisation of the fp32 SwiGLU rows into e4m3 and the stage-major code planes. A workgroup
+// takes a tile of 64 rows x 256 columns (8 blocks of 32): each wave quantises 16 of its rows, a row as
+// one coalesced 1 KB read (lane l: columns 4l .. 4l+3, so lanes 8b .. 8b+7 hold block b and its
+// amax is a reduction over 8 lanes) and one 256-byte code write. The tile's scale codes go through
+// LDS so that each block's codes of the 64 rows are written as one 64-byte run of its plane.
+constexpr int QA_ROWS = 64;
 __global__ __launch_bounds__(256) void mx_quant_act_kernel(const float* act, int64_t rows, int cols, uint8_t* q,
                                                           uint8_t* planes, int64_t stage_stride) {
-  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int nb = cols / 32;
-  if (id >= rows * nb) return;
-  const int b = (int)(id / rows);
-  const int64_t r = id - (int64_t)b * rows;
-  const v4f* src = (const v4f*)(act + r * cols + b * 32);
-  v4f v[8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v[i] = src[i];
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
+  __shared__ __align__(16) uint8_t codes[8][QA_ROWS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * QA_ROWS;
+  const int c0 = blockIdx.y * 256;
+  const int col = c0 + 4 * lane;
+  const bool live = col < cols;  // a last chunk of 128 columns uses lanes 0 .. 31
+  for (int i = 0; i < QA_ROWS / 4; ++i) {
+    const int lr = wave * (QA_ROWS / 4) + i;
+    const int64_t r = r0 + lr;
+    if (r >= rows) break;  // wave-uniform
+    v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) v = *(const v4f*)(act + r * cols + col);
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const uint32_t code = mx_scale_code(amax);
+    const uint32_t w = f32_to_e4m3_inrange(mx_apply_inv_scale(v[0], code)) |
+                       (f32_to_e4m3_inrange(mx_apply_inv_scale(v[1], code)) << 8) |
+                       (f32_to_e4m3_inrange(mx_apply_inv_scale(v[2], code)) << 16) |
+                       (f32_to_e4m3_inrange(mx_apply_inv_scale(v[3], code)) << 24);
+    if (live) {
+      *(uint32_t*)(q + r * cols + col) = w;
+      if ((lane & 7) == 0) codes[lane >> 3][lr] = (uint8_t)code;
+    }
   }
-  const uint32_t code = mx_scale_code(amax);
-  uint32_t w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    w[i] = f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][0], code)) |
-           (f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][1], code)) << 8) |
-           (f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][2], code)) << 16) |
-           (f32_to_e4m3_inrange(mx_apply_inv_scale(v[i][3], code)) << 24);
-  uint4* dst = (uint4*)(q + r * cols + b * 32);
-  dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-  dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-  planes[(b >> 2) * stage_stride + (b & 3) * (stage_stride >> 2) + r] = (uint8_t)code;
+  __syncthreads();
+  // block j of the tile (global block b = c0 / 32 + j): rows r0 .. r0 + 63 of plane (b >> 2, b & 3),
+  // 4 bytes per thread
+  const int j = threadIdx.x >> 4, k = (threadIdx.x & 15) * 4;
+  const int b = c0 / 32 + j;
+  if (j < 8 && c0 + 32 * j < cols) {
+    uint8_t* plane = planes + (b >> 2) * stage_stride + (b & 3) * (stage_stride >> 2) + r0;
+    if (r0 + k + 4 <= rows && ((uintptr_t)(plane + k) & 3) == 0) {
+      *(uint32_t*)(plane + k) = *(const uint32_t*)&codes[j][k];
+    } else {  // the last rows, or planes whose row count is not a multiple of 4
+      for (int t = 0; t < 4 && r0 + k + t < rows; ++t) plane[k + t] = codes[j][k + t];
+    }
+  }
 }
 
 int mi355_mx_quant_act(const float* act, int64_t rows, int cols, uint8_t* q, uint8_t* planes, int64_t stage_stride,
                        hipStream_t st) {
-  const int64_t n = rows * (cols / 32);
-  if (n == 0) return MI355MOE_OK;
-  hipLaunchKernelGGL(mx_quant_act_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, act, rows, cols, q,
-                     planes, stage_stride);
+  if (rows == 0) return MI355MOE_OK;
+  if (cols % 128) return MI355MOE_EINVAL;
+  const dim3 grid((unsigned)((rows + QA_ROWS - 1) / QA_ROWS), (unsigned)((cols + 255) / 256));
+  hipLaunchKernelGGL(mx_quant_act_kernel, grid, dim3(256), 0, st, act, rows, cols, q, planes, stage_stride);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
 // Stage-major code planes by routed row from per-token codes [tokens, nb]: one thread per 4
-// consecutive routed rows and 32-block b, so each thread writes 4 bytes and a wavefront 256
-// consecutive bytes of one plane. Routed row rr holds the codes of token gather[rr] / fanout; rows
-// at or past the routed-row count (group_list[groups - 1]) get code 0 (nothing reads them as rows
-// of a group).
+// consecutive routed rows and BPT consecutive 32-blocks (BPT of the code planes; BPT = 8, or 4 when
+// nb % 8 != 0), rows fastest: a thread reads the 4 rows' gather entries once and each row's BPT codes
+// as one load, and writes 4 bytes to each of its planes (a wavefront: 256 consecutive bytes of each).
+// Routed row rr holds the codes of token gather[rr] / fanout; rows at or past the routed-row count
+// (group_list[groups - 1]) get code 0 (nothing reads them as rows of a group).
+template <int BPT>
 __global__ __launch_bounds__(256) void mx_codes_to_planes_kernel(const uint8_t* codes, int nb, const int32_t* gather,
                                                                  int fanout, const int64_t* group_list, int groups,
                                                                  int64_t R, uint8_t* planes, int64_t stage_stride) {
   const int64_t R4 = (R + 3) / 4;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= R4 * nb) return;
-  const int b = (int)(id / R4);
-  const int64_t r0 = (id - b * R4) * 4;
+  if (id >= R4 * (nb / BPT)) return;
+  const int b0 = (int)(id / R4) * BPT;
+  const int64_t r0 = (id - (b0 / BPT) * R4) * 4;
   const int64_t valid = group_list[groups - 1];
-  uint8_t* plane = planes + (b >> 2) * stage_stride + (b & 3) * (stage_stride >> 2);
-  uint32_t w = 0;
+  uint32_t w[BPT] = {};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t rr = r0 + i;
-    uint32_t c = 0;
+    uint64_t c8 = 0;
     if (rr < valid && rr < R) {
-      const int32_t s = gather[rr];
-      if (s >= 0) c = codes[(int64_t)(s / fanout) * nb + b];
+      const int32_t src = gather[rr];
+      if (src >= 0) {
+        const uint8_t* c = codes + (int64_t)(src / fanout) * nb + b0;
+        c8 = BPT == 8 ? *(const uint64_t*)c : *(const uint32_t*)c;
+      }
     }
-    w |= c << (8 * i);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) w[j] |= (uint32_t)((c8 >> (8 * j)) & 0xff) << (8 * i);
   }
-  if ((R & 3) == 0) {
-    *(uint32_t*)(plane + r0) = w;
-  } else {
-    for (int i = 0; i < 4 && r0 + i < R; ++i) plane[r0 + i] = (uint8_t)(w >> (8 * i));
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    const int b = b0 + j;
+    uint8_t* plane = planes + (b >> 2) * stage_stride + (b & 3) * (stage_stride >> 2);
+    if (r0 + 4 <= R && ((uintptr_t)(plane + r0) & 3) == 0) {
+      *(uint32_t*)(plane + r0) = w[j];
+    } else {
+      for (int i = 0; i < 4 && r0 + i < R; ++i) plane[r0 + i] = (uint8_t)(w[j] >> (8 * i));
+    }
   }
 }
 
@@ -173,9 +202,15 @@ int mi355_mx_quant_tokens_to_planes(const uint16_t* x, int64_t tokens, int cols,
                      codes, (int64_t)nb, (int64_t)0, (const int32_t*)nullptr, 1);
   if (hipGetLastError() != hipSuccess) return MI355MOE_ELAUNCH;
   const int64_t R = tokens * fanout;
-  const int64_t m = (R + 3) / 4 * nb;
-  hipLaunchKernelGGL(mx_codes_to_planes_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, codes, nb, gather,
-                     fanout, group_list, groups, R, planes, stage_stride);
+  if (nb % 4) return MI355MOE_EINVAL;  // cols % 128 == 0
+  const int bpt = nb % 8 == 0 ? 8 : 4;
+  const int64_t m = (R + 3) / 4 * (nb / bpt);
+  if (bpt == 8)
+    hipLaunchKernelGGL(mx_codes_to_planes_kernel<8>, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, codes, nb,
+                       gather, fanout, group_list, groups, R, planes, stage_stride);
+  else
+    hipLaunchKernelGGL(mx_codes_to_planes_kernel<4>, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, codes, nb,
+                       gather, fanout, group_list, groups, R, planes, stage_stride);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 

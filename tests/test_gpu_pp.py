@@ -92,7 +92,8 @@ def test_moe_forward_bf16_pp_matches_default(gpu, variant, layout):
     assert orc.rel_l2(out_pp, ref) < BF16_REL_L2
 
 
-@pytest.mark.parametrize("T,H,I,E,K", [(700, 1024, 512, 16, 4), (64, 1024, 256, 64, 8), (300, 2048, 384, 8, 2)])
+@pytest.mark.parametrize("T,H,I,E,K", [(700, 1024, 512, 16, 4), (64, 1024, 256, 64, 8), (300, 2048, 384, 8, 2),
+                                       (333, 1152, 256, 8, 4)])
 @pytest.mark.parametrize("variant", VARIANTS)
 def test_moe_forward_mxfp8_pp_matches_w4(gpu, variant, T, H, I, E, K):
     """MXFP8 forward on the 8-wave GEMMs (stage-major activation scales, col_data / col_scale weights)
