@@ -41,17 +41,19 @@ __global__ void mask_to_ids_kernel(const uint8_t* mask, int64_t T, int32_t* ids)
 
 __global__ void single_group_list_kernel(int64_t rows, int64_t* group_list) { group_list[0] = rows; }
 
-// Split-K factor of the router projection: enough work items for every CU (the tile is 256 x 256,
-// so T=8192 gives only 32 tiles), each split at least 4 K stages of 32. Deterministic: split s
-// writes its own partial buffer and the reduction adds the splits in ascending order.
+// Split-K factor of the router projection: one work item per CU (the 4-wave configuration runs one
+// workgroup per CU; the tile is 256 x 256, so T=8192 gives only 32 tiles), each split at least 4 K
+// stages of 32. More items would add a second round and partial tiles to write and read back.
+// Deterministic: split s writes its own partial buffer and the reduction adds them in a fixed order.
 static int router_splits(int64_t T, int H, int E) {
   const int64_t tiles = ((T + 255) / 256) * ((E + 255) / 256);
   const int kst = H / 32;
+  const int target = mi355_num_cus();
   int best = 1;
   for (int s = 1; s <= kst / 4; ++s) {
     if (kst % s) continue;
     best = s;
-    if (tiles * s >= 512) break;
+    if (tiles * s >= target) break;
   }
   return best;
 }
@@ -64,17 +66,31 @@ extern "C" size_t mi355moe_gate_logits_workspace_size(int64_t num_tokens, int32_
   return base + (s > 1 ? al256((size_t)s * num_tokens * num_experts * 4) : 0);
 }
 
-// logits[t, e] = sum_s partial[s, row(t), e] in ascending s (row(t) = routed row of token t).
-__global__ void splitk_reduce_kernel(const float* partial, int splits, int64_t split_stride, int64_t T, int E,
-                                     const int32_t* row_of_token_inv, float* out) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= T * E) return;
-  int64_t r = i / E;
-  int e = (int)(i - r * E);
-  float acc = partial[i];
-  for (int s = 1; s < splits; ++s) acc += partial[s * split_stride + i];
-  int64_t orow = row_of_token_inv ? (int64_t)row_of_token_inv[r] : r;
-  out[orow * E + e] = acc;
+// logits[t, e] = sum over s of partial[s, row(t), e] (row(t) = routed row of token t), in a fixed
+// order: a workgroup takes 64 elements; its 4 waves add the splits s = w, w + 4, w + 8, ... in
+// ascending order, and wave 0 adds the four sums in wave order (so each load chain is a quarter of
+// the splits long).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* partial, int splits, int64_t split_stride,
+                                                            int64_t T, int E, const int32_t* row_of_token_inv,
+                                                            float* out) {
+  __shared__ float sums[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = i < T * E;
+  float acc = 0.0f;
+  if (live) {
+    if (w < splits) acc = partial[w * split_stride + i];
+    for (int s = w + 4; s < splits; s += 4) acc += partial[s * split_stride + i];
+  }
+  sums[w][lane] = acc;
+  __syncthreads();
+  if (w != 0 || !live) return;
+  float total = sums[0][lane];
+  for (int q = 1; q < 4 && q < splits; ++q) total += sums[q][lane];
+  const int64_t r = i / E;
+  const int e = (int)(i - r * E);
+  const int64_t orow = row_of_token_inv ? (int64_t)row_of_token_inv[r] : r;
+  out[orow * E + e] = total;
 }
 
 extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32_t hidden_size, const uint16_t* w,
@@ -138,7 +154,7 @@ extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32
   rc = mi355_grouped_gemm(p, false, false, EPI_STORE_F32, st);
   if (rc || splits == 1) return rc;
   const int64_t n = num_tokens * num_experts;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, partial, splits,
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, st, partial, splits,
                      p.c_split_stride, num_tokens, num_experts, dual ? gather : nullptr, logits);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
