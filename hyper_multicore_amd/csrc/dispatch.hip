@@ -237,10 +237,13 @@ extern "C" int mi355moe_token_permute(const uint16_t* x, int64_t num_tokens, int
 
 // out[t] = bf16(sum_k p[t,k] * y[mapping[t*K+k]]) with fp32 accumulation in ascending k; the
 // product and the sum are rounded separately (no fma), so the result is reproducible bit for bit.
-// One block per token; each thread handles 8 consecutive columns (one 16-byte vector).
-__global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, const int32_t* mapping,
-                                                        const float* probs, int64_t T, int K, int H,
-                                                        uint16_t* out) {
+// Block (t, c): token t, columns 8 * 128 c .. of it, each thread one 16-byte vector (8 columns), so a
+// decode batch of few tokens still spreads over many workgroups. The K rows' vectors are loaded four
+// at a time before they are added (in ascending k).
+constexpr int UNPERMUTE_THREADS = 128;
+__global__ __launch_bounds__(UNPERMUTE_THREADS) void unpermute_kernel(const uint16_t* y, const int32_t* mapping,
+                                                                      const float* probs, int64_t T, int K, int H,
+                                                                      uint16_t* out) {
   const int64_t t = blockIdx.x;
   if (t >= T) return;
   __shared__ int32_t rows[64];
@@ -250,36 +253,44 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, const
     ps[threadIdx.x] = probs != nullptr ? probs[t * K + threadIdx.x] : 1.0f;
   }
   __syncthreads();
-  for (int v = threadIdx.x; v < H / 8; v += blockDim.x) {
-    float acc[8];
+  const int v = blockIdx.y * UNPERMUTE_THREADS + threadIdx.x;
+  if (v >= H / 8) return;
+  float acc[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int k = 0; k < K; ++k) {
-      int32_t r = rows[k];
-      if (r < 0) continue;
-      uint4 q = ((const uint4*)(y + (int64_t)r * H))[v];
-      float p = ps[k];
-      uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 4) {
+    uint4 q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t r = k0 + j < K ? rows[k0 + j] : -1;
+      q[j] = r >= 0 ? ((const uint4*)(y + (int64_t)r * H))[v] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (k0 + j >= K || rows[k0 + j] < 0) continue;
+      const float p = ps[k0 + j];
+      const uint32_t w[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         acc[2 * i] = acc[2 * i] + p * bf16_to_f32((uint16_t)(w[i] & 0xffff));
         acc[2 * i + 1] = acc[2 * i + 1] + p * bf16_to_f32((uint16_t)(w[i] >> 16));
       }
     }
-    uint4 o;
-    o.x = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
-    o.y = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
-    o.z = f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
-    o.w = f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
-    ((uint4*)(out + t * (int64_t)H))[v] = o;
   }
+  uint4 o;
+  o.x = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+  o.y = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+  o.z = f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
+  o.w = f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+  ((uint4*)(out + t * (int64_t)H))[v] = o;
 }
 
 int mi355_unpermute_enqueue(const uint16_t* y, const int32_t* mapping, const float* probs, int64_t T, int K,
                             int H, uint16_t* out, hipStream_t stream) {
   if (T == 0) return MI355MOE_OK;
-  hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)T), dim3(H >= 2048 ? 256 : 128), 0, stream, y, mapping,
-                     probs, T, K, H, out);
+  if (T > INT32_MAX) return MI355MOE_EINVAL;
+  const dim3 grid((unsigned)T, (unsigned)((H / 8 + UNPERMUTE_THREADS - 1) / UNPERMUTE_THREADS));
+  hipLaunchKernelGGL(unpermute_kernel, grid, dim3(UNPERMUTE_THREADS), 0, stream, y, mapping, probs, T, K, H, out);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
