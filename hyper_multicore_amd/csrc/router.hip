@@ -47,6 +47,9 @@ MI355_DEV void wave_argmax(float& v, int& i) {
   }
 }
 
+// SL: per-lane expert slots compiled in (expert e lives in lane e % 64, slot e / 64); the smallest of
+// 1, 2, 4, 8, 16 that holds E, so the unrolled per-slot loops carry no slots past E.
+template <int SL>
 __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -57,15 +60,15 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
   const float* bias = a.bias;
   if (a.image_mask != nullptr && a.bias_vl != nullptr && a.image_mask[t]) bias = a.bias_vl;
 
-  float score[ROUTER_MAX_SLOTS];
-  float biased[ROUTER_MAX_SLOTS];
+  float score[SL];
+  float biased[SL];
   const float NEG_INF = -__builtin_inff();
 
   if (a.scoring == MI355MOE_SCORE_SOFTMAX) {
-    float lv[ROUTER_MAX_SLOTS];
+    float lv[SL];
     float mx = NEG_INF;
 #pragma unroll
-    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+    for (int j = 0; j < SL; ++j) {
       int e = j * 64 + lane;
       lv[j] = (j < slots && e < E) ? lrow[e] : NEG_INF;
       mx = fmaxf(mx, lv[j]);
@@ -74,7 +77,7 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
     for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
     float part = 0.0f;
 #pragma unroll
-    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+    for (int j = 0; j < SL; ++j) {
       int e = j * 64 + lane;
       if (j < slots && e < E) {
         lv[j] = det_expf(lv[j] - mx);
@@ -84,19 +87,19 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) part = part + __shfl_xor(part, m, 64);
 #pragma unroll
-    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+    for (int j = 0; j < SL; ++j) {
       int e = j * 64 + lane;
       score[j] = (j < slots && e < E) ? lv[j] / part : 0.0f;
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+    for (int j = 0; j < SL; ++j) {
       int e = j * 64 + lane;
       score[j] = (j < slots && e < E) ? score_fn(lrow[e], a.scoring) : 0.0f;
     }
   }
 #pragma unroll
-  for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+  for (int j = 0; j < SL; ++j) {
     int e = j * 64 + lane;
     bool valid = j < slots && e < E;
     biased[j] = valid ? score[j] + bias[e] : NEG_INF;
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
     for (int g = 0; g < G; ++g) {
       float t1 = NEG_INF, t2 = NEG_INF;
 #pragma unroll
-      for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+      for (int j = 0; j < SL; ++j) {
         int e = j * 64 + lane;
         if (j < slots && e < E && e / S == g) {
           float v = biased[j];
@@ -136,7 +139,7 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
       if (i < G) keep |= 1ull << i;
     }
 #pragma unroll
-    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+    for (int j = 0; j < SL; ++j) {
       int e = j * 64 + lane;
       if (j < slots && e < E && !((keep >> (e / S)) & 1ull)) biased[j] = NEG_INF;
     }
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
     float bv = NEG_INF;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) {
+    for (int j = 0; j < SL; ++j) {
       int e = j * 64 + lane;
       if (j < slots && e < E && !((taken >> j) & 1u)) {
         if (biased[j] > bv || bi == 0x7fffffff) { bv = biased[j]; bi = e; }
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
     // the owner lane broadcasts the unbiased score
     float sel = 0.0f;
 #pragma unroll
-    for (int j = 0; j < ROUTER_MAX_SLOTS; ++j) if ((bi >> 6) == j) sel = score[j];
+    for (int j = 0; j < SL; ++j) if ((bi >> 6) == j) sel = score[j];
     sel = __shfl(sel, bi & 63, 64);
     if (lane == k) { my_idx = bi; my_w = sel; }
   }
@@ -203,7 +206,12 @@ extern "C" int mi355moe_gate_route(const MI355MoeRouteArgs* args, void* stream_)
   if (a.logits_row_stride < a.num_experts) return MI355MOE_EINVAL;
   if (a.num_tokens == 0) return MI355MOE_OK;
   dim3 grid((unsigned)((a.num_tokens + 3) / 4));
-  hipLaunchKernelGGL(mi355_route_kernel, grid, dim3(256), 0, stream, a);
+  const int slots = (a.num_experts + 63) / 64;
+  if (slots <= 1) hipLaunchKernelGGL(mi355_route_kernel<1>, grid, dim3(256), 0, stream, a);
+  else if (slots <= 2) hipLaunchKernelGGL(mi355_route_kernel<2>, grid, dim3(256), 0, stream, a);
+  else if (slots <= 4) hipLaunchKernelGGL(mi355_route_kernel<4>, grid, dim3(256), 0, stream, a);
+  else if (slots <= 8) hipLaunchKernelGGL(mi355_route_kernel<8>, grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(mi355_route_kernel<ROUTER_MAX_SLOTS>, grid, dim3(256), 0, stream, a);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
