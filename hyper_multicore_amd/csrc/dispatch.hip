@@ -19,6 +19,9 @@
 #include "../../include/mi355moe.h"
 
 #define DISPATCH_MAX_EXPERTS 4096
+// hist / permute read a chunk's ids in pieces of this many slots, all loads of a piece issued before
+// the piece is counted or ranked (a chunk is a multiple of 64 slots; a piece is 16 rounds of 64)
+#define DISPATCH_PIECE 1024
 
 struct DispatchPlan {
   int64_t slots;
@@ -47,15 +50,26 @@ extern "C" size_t mi355moe_dispatch_workspace_size(int64_t num_tokens, int32_t t
   return align256((size_t)p.chunks * num_experts * 4) + align256((size_t)num_experts * 4);
 }
 
-MI355_DEV int load_id(const void* ids, int dtype, int64_t s) {
-  if (dtype == MI355MOE_IDS_INT64) {
-    int64_t v = ((const int64_t*)ids)[s];
-    return (v < INT32_MIN || v > INT32_MAX) ? -1 : (int)v;
+// The ids of slots p0 + 64 r + lane (r < DISPATCH_PIECE / 64) of a chunk ending at `end`: all loads
+// issued first (slots past the end re-read the chunk's last slot; callers skip them), then int64 ids
+// outside the int32 range become -1 (invalid).
+template <typename IdT>
+MI355_DEV void load_piece(const IdT* ids, int64_t p0, int64_t end, int lane, int (&idv)[DISPATCH_PIECE / 64]) {
+  IdT raw[DISPATCH_PIECE / 64];
+#pragma unroll
+  for (int r = 0; r < DISPATCH_PIECE / 64; ++r) {
+    const int64_t s = p0 + r * 64 + lane;
+    raw[r] = ids[s < end ? s : end - 1];
   }
-  return ((const int32_t*)ids)[s];
+#pragma unroll
+  for (int r = 0; r < DISPATCH_PIECE / 64; ++r) {
+    const int64_t v = (int64_t)raw[r];
+    idv[r] = (v < INT32_MIN || v > INT32_MAX) ? -1 : (int)v;
+  }
 }
 
-__global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* ids, int dtype, int64_t slots,
+template <typename IdT>
+__global__ __launch_bounds__(64) void dispatch_hist_kernel(const IdT* ids, int64_t slots,
                                                            int64_t chunk, int E, int32_t* chunk_counts,
                                                            int32_t* error_flag) {
   extern __shared__ int32_t hist[];
@@ -65,10 +79,16 @@ __global__ __launch_bounds__(64) void dispatch_hist_kernel(const void* ids, int 
   const int64_t begin = (int64_t)blockIdx.x * chunk;
   const int64_t end = begin + chunk < slots ? begin + chunk : slots;
   bool bad = false;
-  for (int64_t s = begin + lane; s < end; s += 64) {
-    int id = load_id(ids, dtype, s);
-    if (id >= 0 && id < E) atomicAdd(&hist[id], 1);
-    else bad = true;
+  for (int64_t p0 = begin; p0 < end; p0 += DISPATCH_PIECE) {
+    int idv[DISPATCH_PIECE / 64];  // the piece's ids, loaded before they are counted
+    load_piece(ids, p0, end, lane, idv);
+#pragma unroll
+    for (int r = 0; r < DISPATCH_PIECE / 64; ++r) {
+      if (p0 + r * 64 + lane >= end) continue;  // past the chunk
+      const int id = idv[r];
+      if (id >= 0 && id < E) atomicAdd(&hist[id], 1);
+      else bad = true;
+    }
   }
   if (bad && error_flag != nullptr) error_flag[0] = 1;
   __syncthreads();
@@ -102,7 +122,8 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* chunk_coun
   }
 }
 
-__global__ __launch_bounds__(64) void dispatch_permute_kernel(const void* ids, int dtype, int64_t slots,
+template <typename IdT>
+__global__ __launch_bounds__(64) void dispatch_permute_kernel(const IdT* ids, int64_t slots,
                                                               int64_t chunk, int E,
                                                               const int32_t* chunk_base,
                                                               const int32_t* expert_start,
@@ -117,9 +138,15 @@ __global__ __launch_bounds__(64) void dispatch_permute_kernel(const void* ids, i
   int bits = 1;
   while ((1 << bits) < E) ++bits;
   const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  for (int64_t s0 = begin; s0 < end; s0 += 64) {
+  for (int64_t p0 = begin; p0 < end; p0 += DISPATCH_PIECE) {
+  int idv[DISPATCH_PIECE / 64];  // the piece's ids, loaded before its rounds
+  load_piece(ids, p0, end, lane, idv);
+#pragma unroll
+  for (int r = 0; r < DISPATCH_PIECE / 64; ++r) {
+    const int64_t s0 = p0 + r * 64;
+    if (s0 >= end) break;  // wave-uniform
     const int64_t s = s0 + lane;
-    int id = s < end ? load_id(ids, dtype, s) : -1;
+    const int id = s < end ? idv[r] : -1;
     bool valid = id >= 0 && id < E;
     uint64_t match = __ballot(valid);
     for (int b = 0; b < bits; ++b) {
@@ -127,15 +154,19 @@ __global__ __launch_bounds__(64) void dispatch_permute_kernel(const void* ids, i
       uint64_t m1 = __ballot(bit);
       match &= bit ? m1 : ~m1;
     }
+    // The block is one wavefront, whose LDS operations run in program order: every lane reads its
+    // expert's running rank before the first lane of each expert advances it. Compiler-only
+    // barriers keep that order; a workgroup barrier would also wait for this round's global stores.
     int dest = -1;
     if (valid) dest = running[id] + __popcll(match & lt);
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
     if (valid && (match & lt) == 0) running[id] += __popcll(match);
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
     if (s < end) {
       mapping[s] = dest;
       if (valid && gather_index != nullptr) gather_index[dest] = (int32_t)s;
     }
+  }
   }
 }
 
@@ -148,13 +179,20 @@ int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int t
   int32_t* chunk_counts = (int32_t*)workspace;
   int32_t* expert_start = (int32_t*)((char*)workspace + align256((size_t)p.chunks * E * 4));
   size_t lds = (size_t)E * 4;
-  hipLaunchKernelGGL(dispatch_hist_kernel, dim3(p.chunks), dim3(64), lds, stream, ids, dtype, p.slots,
-                     p.chunk, E, chunk_counts, error_flag);
+  if (dtype == MI355MOE_IDS_INT64)
+    hipLaunchKernelGGL(dispatch_hist_kernel<int64_t>, dim3(p.chunks), dim3(64), lds, stream, (const int64_t*)ids,
+                       p.slots, p.chunk, E, chunk_counts, error_flag);
+  else
+    hipLaunchKernelGGL(dispatch_hist_kernel<int32_t>, dim3(p.chunks), dim3(64), lds, stream, (const int32_t*)ids,
+                       p.slots, p.chunk, E, chunk_counts, error_flag);
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, stream, chunk_counts, p.chunks, E,
                      counts, expert_offsets, group_list, expert_start);
-  if (p.slots > 0)
-    hipLaunchKernelGGL(dispatch_permute_kernel, dim3(p.chunks), dim3(64), lds, stream, ids, dtype, p.slots,
-                       p.chunk, E, chunk_counts, expert_start, mapping, gather_index);
+  if (p.slots > 0 && dtype == MI355MOE_IDS_INT64)
+    hipLaunchKernelGGL(dispatch_permute_kernel<int64_t>, dim3(p.chunks), dim3(64), lds, stream, (const int64_t*)ids,
+                       p.slots, p.chunk, E, chunk_counts, expert_start, mapping, gather_index);
+  else if (p.slots > 0)
+    hipLaunchKernelGGL(dispatch_permute_kernel<int32_t>, dim3(p.chunks), dim3(64), lds, stream, (const int32_t*)ids,
+                       p.slots, p.chunk, E, chunk_counts, expert_start, mapping, gather_index);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
