@@ -103,10 +103,16 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* chunk_coun
   __shared__ int64_t wsum[17];
   for (int e = threadIdx.x; e < E; e += 1024) {
     int32_t run = 0;
-    for (int b = 0; b < chunks; ++b) {
-      int32_t c = chunk_counts[(int64_t)b * E + e];
-      chunk_counts[(int64_t)b * E + e] = run;
-      run += c;
+    for (int b0 = 0; b0 < chunks; b0 += 16) {  // 16 chunk counts loaded at a time, then ranked
+      int32_t c[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) c[j] = b0 + j < chunks ? chunk_counts[(int64_t)(b0 + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (b0 + j >= chunks) break;
+        chunk_counts[(int64_t)(b0 + j) * E + e] = run;
+        run += c[j];
+      }
     }
     vals[e] = run;
     if (counts != nullptr) counts[e] = run;
