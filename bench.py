@@ -108,7 +108,7 @@ class Layer:
                 del d1, s1, d2, s2
                 self.w1, self.w2, self.s1, self.s2, self.layout = e1.view(torch.uint8), e2.view(torch.uint8), t1, t2, "EOI"
             elif mx_layout == "EIO_GU":
-                # one-time weight preparation: W1's gate and up columns interleaved in 128-column
+                # one-time weight preparation: W1's gate and up columns interleaved in 64-column
                 # blocks, so a GMM1 tile reads its gate and up columns as one run per weight row
                 self.w1, self.s1 = ops.interleave_gate_up(d1, s1)
                 del d1, s1
@@ -137,8 +137,8 @@ class Layer:
         if self.layout != "EIO_GU":
             return w1, s1
         I = self.c["I"]
-        blocks = lambda t, half: torch.cat([t[..., b * 256 + half * 128: b * 256 + half * 128 + 128]
-                                            for b in range(I // 128)], dim=-1)
+        blocks = lambda t, half: torch.cat([t[..., b * 128 + half * 64: b * 128 + half * 64 + 64]
+                                            for b in range(I // 64)], dim=-1)
         w1 = torch.cat([blocks(w1, 0), blocks(w1, 1)], dim=-1)
         if s1 is not None:
             s1 = torch.cat([blocks(s1.transpose(-1, -2), 0), blocks(s1.transpose(-1, -2), 1)],

@@ -64,9 +64,10 @@ struct GGParams {
   // Rows of the whole GEMM when the caller knows them (0: not given); the 8-wave bf16 configuration
   // picks its tile height from their average per group.
   int64_t rows_hint;
-  // SwiGLU GEMMs: the weight's gate and up columns are interleaved in 128-column blocks (block b:
-  // gate columns 128 b ..+127, then up columns 128 b ..+127), so a tile's gate and up columns are
-  // one contiguous run per K row (0: gate columns [0, I) then up columns [I, 2I)).
+  // SwiGLU GEMMs: the weight's gate and up columns are interleaved in 64-column blocks (block b:
+  // gate columns 64 b ..+63, then up columns 64 b ..+63), so a tile's gate and up columns are one
+  // contiguous run per K row, and each 64 output columns' gate and up one 128-byte line of an MX
+  // weight row (0: gate columns [0, I) then up columns [I, 2I)).
   int32_t gate_up_interleaved;
 };
 
@@ -75,7 +76,7 @@ struct GGParams {
 __host__ __device__ __forceinline__ int gate_up_col(int c, int I, int gu) {
   const int up = (c >= I) ? 1 : 0;
   const int cc = c - (up ? I : 0);
-  const int il = ((cc >> 7) << 8) + (up << 7) + (cc & 127);
+  const int il = ((cc >> 6) << 7) + (up << 6) + (cc & 63);
   return gu ? il : c;
 }
 

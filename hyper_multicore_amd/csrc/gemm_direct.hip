@@ -142,6 +142,7 @@ __global__ __launch_bounds__(GGDirect::THREADS, 1) void grouped_gemm_direct_kern
     const int L = round * (int)gridDim.x + xcd * per_xcd + slot;
     if (L >= total) break;
     constexpr bool copy_role_a = true, copy_role_b = true;
+    constexpr int tail_from = INT32_MAX;  // no column halves in the direct-weight configuration
 #include "gemm_item_fwd.inc"
     DirectPlan d = direct_plan(p, g, nt, tile_row0, rows_valid, SWIGLU, MX, wave, lane);
     d.a_base = gg_uniform(d.a_base);

@@ -172,6 +172,7 @@ MI355_DEV void gg_split_item(const GGParams& p, const int32_t* prefix, int L, in
   constexpr int ESIZE = MX ? 1 : 2;
   constexpr bool copy_role_a = ROLE == 0, copy_role_b = ROLE == 1;
   const int wm = (int)((unsigned)wave / C::WGN), wn = (int)((unsigned)wave % C::WGN);
+  constexpr int tail_from = INT32_MAX;  // no column halves in the split-role configurations
 #include "gemm_item_fwd.inc"
   cp.a_base = gg_uniform(cp.a_base);
   cp.b_base = gg_uniform(cp.b_base);
@@ -224,8 +225,18 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
     for (int g = tid; g <= p.G; g += C::THREADS) s_prefix[g] = p.tile_prefix[g];
   __syncthreads();
   const int splits = (EPI == EPI_STORE_F32 && p.k_splits > 1) ? p.k_splits : 1;
-  const int total = prefix[p.G] * p.n_tiles * splits;
+  const int items = prefix[p.G] * p.n_tiles;
   const int nk = p.K / splits * ESIZE / C::KB;  // stages per work item
+  // A partial last round of whole items leaves most CUs idle while it streams its weights: its items
+  // run as two column halves each (half the weight lines per item, twice the workgroups), when the
+  // halves still fit in one round. Every output element keeps its own K loop, so the results are
+  // those of the whole items.
+  int tail_from = INT32_MAX;
+  if constexpr (C::HALF_TAIL && EPI != EPI_STORE_F32) {
+    const int full = items / (int)gridDim.x * (int)gridDim.x;
+    if (items > full && 2 * (items - full) <= (int)gridDim.x) tail_from = full;
+  }
+  const int total = splits > 1 ? items * splits : (tail_from < items ? tail_from + 2 * (items - tail_from) : items);
   const int xcd = blockIdx.x & 7;
   const int per_xcd = gridDim.x >> 3;
   const int slot = blockIdx.x >> 3;
@@ -253,7 +264,8 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
 
     __syncthreads();  // the previous item's last stage / epilogue reads are done before refilling
     const int rows_w = rows_valid - wm * C::WM;
-    const int nm = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
+    int nm = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
+    if (half >= 0 && (wn >> 1) != half) nm = 0;  // a column half: the other half's waves only copy
     // this wave copies A rows wave*A_INSTR*16 .. (and, MX scale waves, scale rows wave*64 .. +63)
     const bool la = wave_copies_a<C>(wave, rows_valid);
     if (la) {

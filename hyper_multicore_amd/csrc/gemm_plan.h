@@ -70,10 +70,13 @@ struct GGCfg {
   // OFFS: forward operand copies address a uniform base plus a per-lane 32-bit offset (the
   // scalar-base load form, one VGPR per copy instead of two; A and a group's weights < 4 GiB).
   static constexpr bool OFFS = SPLIT;
+  // the 64-row decode configuration runs the items of a partial last round as column halves
+  static constexpr bool HALF_TAIL = BM == 64;
   // epilogue staging (overlays the rings and the scale slots, never the tile prefix)
   static constexpr int EPI_RS_BF16 = BN * 2 + 16;      // bf16 row stride
   static constexpr int EPI_RS_ACT = (BN / 2) * 4 + 16; // SwiGLU fp32 row stride
   static_assert(A_SLOTS >= 3 && A_SLOTS <= B_SLOTS, "ring depths");
+  static_assert(!HALF_TAIL || (WGM == 1 && WN == 64), "column halves: wave tiles 2 h and 2 h + 1 of 64 columns");
   static_assert(BM * EPI_RS_BF16 <= PREFIX_OFF, "bf16 epilogue staging must fit");
   static_assert(BM * EPI_RS_ACT <= PREFIX_OFF, "SwiGLU epilogue staging must fit");
   static_assert(TOTAL * WG_PER_CU <= 160 * 1024, "LDS budget");

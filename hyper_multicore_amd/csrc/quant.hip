@@ -433,8 +433,8 @@ extern "C" int mi355moe_mx_weight_to_eoi(const uint8_t* col_data, const uint8_t*
 }
 
 // ---- gate/up interleave of the GMM1 weight (layout EIO_GU) ------------------------------------
-// One thread per 16-byte chunk of a row: a chunk lies inside one 128-column block (128 columns are
-// >= 128 bytes), so it moves whole to gate_up_col of its first column.
+// One thread per 16-byte chunk of a row: a chunk lies inside one 64-column block (64 columns are
+// >= 64 bytes), so it moves whole to gate_up_col of its first column.
 __global__ __launch_bounds__(256) void interleave_gate_up_kernel(const uint4* src, int64_t rows, int I, int elem_bytes,
                                                                  uint4* dst) {
   const int64_t chunks_per_row = (int64_t)2 * I * elem_bytes / 16;

@@ -108,6 +108,6 @@ def prepared_eoi_weight(root, data: torch.Tensor, scale: torch.Tensor):
 
 
 def prepared_gate_up_weight(root, data: torch.Tensor, scale: torch.Tensor):
-    """The GMM1 root's (data, scale) with gate and up columns interleaved in 128-column blocks
+    """The GMM1 root's (data, scale) with gate and up columns interleaved in 64-column blocks
     (``ops.interleave_gate_up``, layout ``"EIO_GU"``), cached on the root."""
     return _cached_on_root(root, "_mi355_gate_up", data, scale, ops.interleave_gate_up)

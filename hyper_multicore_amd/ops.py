@@ -467,8 +467,8 @@ def mx_weight_to_eoi(col_data: torch.Tensor, col_scale: torch.Tensor):
 
 def interleave_gate_up(w1: torch.Tensor, w1_scale: torch.Tensor | None = None):
     """The GMM1 weight in layout ``"EIO_GU"``: w1 [E, H, 2I] (bf16, or MX col_data e4m3) with its gate
-    columns [0, I) and up columns [I, 2I) interleaved in 128-column blocks (gate 128 b ..+127, then up
-    128 b ..+127), and the MX col_scale [E, H/64, 2I, 2] the same way. Values are unchanged; the
+    columns [0, I) and up columns [I, 2I) interleaved in 64-column blocks (gate 64 b ..+63, then up
+    64 b ..+63), and the MX col_scale [E, H/64, 2I, 2] the same way. Values are unchanged; the
     forward with ``layout="EIO_GU"`` on these equals ``"EIO"`` on the originals bit for bit, and reads
     each tile's gate and up columns as one run. Returns (w1, w1_scale or None); w2 stays EIO."""
     lib = _lib.load()

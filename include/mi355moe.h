@@ -40,7 +40,7 @@ enum { MI355MOE_PRECISION_BF16 = 0, MI355MOE_PRECISION_MXFP8 = 1 };
  *   EIO: w1 [E, H, 2I], w2 [E, I, H]   (input-major rows, output contiguous)
  *   EOI: w1 [E, 2I, H], w2 [E, H, I]   (output-major rows, input contiguous)
  *   EIO_GU (no reference counterpart; forward only): EIO, with w1's gate and up columns
- *   interleaved in 128-column blocks by mi355moe_interleave_gate_up (and, for MXFP8, w1_scale's
+ *   interleaved in 64-column blocks by mi355moe_interleave_gate_up (and, for MXFP8, w1_scale's
  *   columns the same way); w2 is plain EIO. */
 enum { MI355MOE_LAYOUT_EIO = 0, MI355MOE_LAYOUT_EOI = 1, MI355MOE_LAYOUT_EIO_GU = 2 };
 
@@ -283,7 +283,7 @@ int mi355moe_mx_weight_to_eoi(const uint8_t* col_data, const uint8_t* col_scale,
  * Gate/up interleave of the GMM1 weight for MI355MOE_LAYOUT_EIO_GU (no reference counterpart: a
  * one-time weight preparation that moves columns and changes no value). src holds `rows` rows of
  * 2I elements of elem_bytes bytes each, gate columns [0, I) then up columns [I, 2I); dst gets, for
- * each 128-column block b, gate columns 128 b ..+127 then up columns 128 b ..+127. Use
+ * each 64-column block b, gate columns 64 b ..+63 then up columns 64 b ..+63. Use
  * rows = E * H with elem_bytes 2 (bf16 w1) or 1 (e4m3 col_data), and rows = E * H / 64 with
  * elem_bytes 2 for the MXFP8 col_scale [E, H/64, 2I, 2] (one 2-byte pair per column).
  * I % 128 == 0; src and dst must not overlap. A SwiGLU tile then reads its gate and up columns as

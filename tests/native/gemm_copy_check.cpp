@@ -313,8 +313,8 @@ struct Layout {
 
 // Tile column n (0 .. BN-1) of n-tile nt -> weight column; false when its output column is past N.
 // (SwiGLU: each WN-wide wave tile holds WN/2 gate columns and then the WN/2 matching up columns.
-// With `gu` the weight stores gate and up columns in alternating 128-column blocks: output column o
-// has its gate column in block 2 (o / 128) and its up column in block 2 (o / 128) + 1.)
+// With `gu` the weight stores gate and up columns in alternating 64-column blocks: output column o
+// has its gate column in block 2 (o / 64) and its up column in block 2 (o / 64) + 1.)
 template <class C>
 static bool tile_weight_col(int n, int nt, int N, bool swiglu, int gu, int64_t* wcol) {
   if (!swiglu) {
@@ -325,7 +325,7 @@ static bool tile_weight_col(int n, int nt, int N, bool swiglu, int gu, int64_t* 
   const int H = C::WN / 2, q = n / C::WN, jj = n % C::WN;
   const int64_t o = (int64_t)nt * (C::BN / 2) + q * H + (jj % H);
   if (gu)
-    *wcol = (o / 128) * 256 + (jj < H ? 0 : 128) + o % 128;
+    *wcol = (o / 64) * 128 + (jj < H ? 0 : 64) + o % 64;
   else
     *wcol = jj < H ? o : N + o;
   return o < N;
@@ -391,6 +391,7 @@ static void record_schedule(const CopyPlan<C>& cp, int nk, int wave, std::vector
 // Per work item bookkeeping shared by the lanes
 struct ItemCtx {
   int g, nt, split, nk;
+  int half = -1;      // forward: the column half of the tile the item computes (-1: all of it)
   int64_t tile_row0;  // forward: first routed row; grouped-K: unused
   int rows_valid;
   // grouped-K
@@ -478,6 +479,8 @@ static const uint8_t* expected_src(const GGParams& p, const Layout& L, const Ite
     return L.B + row * L.Ntot * ES + col * ES;
   } else {
     const int64_t kstage = (int64_t)it.split * it.nk + stage;  // stage index along the full K
+    // a column half: positions of the other half's columns feed only the idle waves
+    auto other_half = [&](int n) { return it.half >= 0 && n / (C::BN / 2) != it.half; };
     switch (region) {
       case R_A: {
         const int r = rel / 64, cpos = (rel % 64) / 16, c = cpos ^ ((r >> 2) & 3);
@@ -487,21 +490,25 @@ static const uint8_t* expected_src(const GGParams& p, const Layout& L, const Ite
       case R_B: {
         if (!B_KN) {  // K-contiguous weight rows, laid out like the activations
           const int n = rel / 64, cpos = (rel % 64) / 16, c = cpos ^ ((n >> 2) & 3);
+          if (other_half(n)) return nullptr;
           if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
           return L.b_at(it.g, (kstage * C::KB + c * 16) / L.esize, wcol);
         }
         if (MX) {  // 64 K rows of 256 bytes, chunk c at c ^ (k & 15), 16 columns per chunk
           const int k = rel / 256, cpos = (rel % 256) / 16, c = cpos ^ (k & 15);
+          if (other_half(c * 16)) return nullptr;
           if (!tile_weight_col<C>(c * 16, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
           return L.b_at(it.g, kstage * 64 + k, wcol);
         }
         // bf16: 32 K rows of 512 bytes, chunk c at c ^ ((k & 7) << 1), 8 columns per chunk
         const int k = rel / 512, cpos = (rel % 512) / 16, c = cpos ^ ((k & 7) << 1);
+        if (other_half(c * 8)) return nullptr;
         if (!tile_weight_col<C>(c * 8, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
         return L.b_at(it.g, kstage * 32 + k, wcol);
       }
       case R_BS: {  // two codes for each of tile columns 2m, 2m+1 (4 bytes per lane)
         const int n = (rel / 4) * 2;
+        if (other_half(n)) return nullptr;
         if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
         return L.bs_col_at(it.g, kstage, wcol);
       }
@@ -512,6 +519,7 @@ static const uint8_t* expected_src(const GGParams& p, const Layout& L, const Ite
       }
       case R_BSR: {  // 16 codes (8 stages) per tile column
         const int n = rel / 16;
+        if (other_half(n)) return nullptr;
         if (!tile_weight_col<C>(n, it.nt, p.N, SWIGLU, p.gate_up_interleaved, &wcol)) return nullptr;
         return L.bs_row_at(it.g, wcol, (int64_t)stage * 16);
       }
@@ -973,6 +981,9 @@ static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la
                "(%d, %d): %.6g vs %.6g", what, max_err, max_ref, bad_row, bad_col, bad_got, bad_want);
 }
 
+// Forward work items that ran as a column half of their tile
+static long g_half_items = 0;
+
 // ------------------------------------------------------------------------------------------------
 // Forward grouped GEMM: all work items, waves and lanes
 template <class C, bool MX, bool B_KN, int EPI>
@@ -986,8 +997,16 @@ static int sim_forward(const GGParams& p) {
   const int32_t* prefix = p.tile_prefix;
   // the two set-up lines of grouped_gemm_kernel
   const int splits = (EPI == EPI_STORE_F32 && p.k_splits > 1) ? p.k_splits : 1;
-  const int total = prefix[p.G] * p.n_tiles * splits;
+  const int items = prefix[p.G] * p.n_tiles;
   const int nk = p.K / splits * ESIZE / C::KB;  // stages per work item
+  // the kernel's column halves of a partial last round, at launch_gg's grid on the stand-in's 256 CUs
+  int tail_from = INT32_MAX;
+  if (C::HALF_TAIL && EPI != EPI_STORE_F32) {
+    const int grid = (256 / 8) * 8 * C::WG_PER_CU;
+    const int full = items / grid * grid;
+    if (items > full && 2 * (items - full) <= grid) tail_from = full;
+  }
+  const int total = splits > 1 ? items * splits : (tail_from < items ? tail_from + 2 * (items - tail_from) : items);
   if (nk < 1) CHECK_FAIL("K = %d gives %d stages", p.K, nk);
   Layout lay;
   if (g_expect.set) {
@@ -1018,6 +1037,8 @@ static int sim_forward(const GGParams& p) {
           ctx.nt = nt;
           ctx.split = split;
           ctx.nk = nk;
+          ctx.half = half;
+          if (half >= 0) ++g_half_items;
           ctx.tile_row0 = tile_row0;
           ctx.rows_valid = rows_valid;
           ctx.cov[R_A].assign((size_t)nk * C::A_BYTES, 0);
@@ -1072,10 +1093,12 @@ static int sim_forward(const GGParams& p) {
       for (int w = 0; w < C::WAVES; ++w) {  // the kernel's subtile count per wave
         const int rows_w = ctx.rows_valid - (w / C::WGN) * C::WM;
         nms[w] = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
+        if (ctx.half >= 0 && ((w % C::WGN) >> 1) != ctx.half) nms[w] = 0;  // the other half's waves
       }
       const int Kper = p.K / splits;
       auto value = [&](int row, int col) -> double {
         int64_t wc;
+        if (ctx.half >= 0 && col / (C::BN / 2) != ctx.half) return NAN;
         if (row >= ctx.rows_valid || !tile_weight_col<C>(col, ctx.nt, p.N, SWIGLU, p.gate_up_interleaved, &wc)) return NAN;
         const int64_t r = ctx.tile_row0 + row;
         const int64_t sr = p.a_row_index ? p.a_row_index[r] / p.a_row_div : r;
@@ -1334,8 +1357,10 @@ static int sim_direct(const GGParams& p) {
       for (int lane = 0; lane < 64; ++lane) {
         const int L = L_item;
         constexpr bool copy_role_a = true, copy_role_b = true;
+        constexpr int tail_from = INT32_MAX;
 #include "../../hyper_multicore_amd/csrc/gemm_item_fwd.inc"
         (void)cp;
+        (void)half;
         (void)mt;
         (void)split;
         item_g = g;
@@ -1970,6 +1995,21 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"moe_mx_eio_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); })});
   s.push_back({"moe_bf16_gu_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_GU, 0.0); })});
   s.push_back({"moe_mx_gu_decode_big", big([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0); })});
+  // decode tiles whose partial last round runs as column halves; the wrapper fails the scenario when
+  // no item of it was a half
+  auto halves = [](std::function<void()> f) {
+    return [f] {
+      const long before = g_half_items;
+      f();
+      if (g_half_items == before) CHECK_FAIL("no work item ran as a column half");
+    };
+  };
+  s.push_back({"moe_mx_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); })});
+  s.push_back({"moe_mx_gu_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0); })});
+  s.push_back({"moe_bf16_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); })});
+  s.push_back({"moe_bf16_gu_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_GU, 0.0); })});
+  s.push_back({"moe_mx_eoi_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EOI, 0.0); })});
+  s.push_back({"gemm_bf16_eoi_decode_halves", halves([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 512, 1024, L_EOI); })});
   // functional emulation (random operands; accumulators vs a reference GEMM). The EIO bf16 / MX and
   // EOI bf16 cases run on the GPU already and calibrate the instruction models.
   auto emu = [](std::function<void()> f) {
@@ -1987,6 +2027,9 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_bf16_eoi_decode", emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EOI); })});
   s.push_back({"emu_mx_eio_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })});
   s.push_back({"emu_mx_eoi_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EOI); })});
+  s.push_back({"emu_mx_eio_decode_halves", halves(emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); }))});
+  s.push_back({"emu_bf16_eoi_decode_halves", halves(emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EOI); }))});
+  s.push_back({"emu_moe_mx_gu_decode_halves", halves(emu([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0); }))});
   auto b6 = [](std::function<void()> f) {
     return [f] {
       g_variant = MI355_GG_VARIANT_B6;

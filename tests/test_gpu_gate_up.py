@@ -1,6 +1,6 @@
 """GPU checks of the gate/up-interleaved GMM1 weight layout (EIO_GU).
 
-The preparation only moves columns: each 128-column block of the result is checked against the
+The preparation only moves columns: each 64-column block of the result is checked against the
 matching slice of the original, element for element. The forward on the prepared weights reads the
 same values into the same tile positions, so its output must equal the EIO forward on the original
 weights bit for bit, for both precisions, every GEMM configuration, and the decode (64-row tiles),
@@ -16,9 +16,9 @@ VARIANTS = ["default", "b6", "dv", "sp", "sp4", "pp", "w4"]
 
 def _blocks_of(w, I):
     """(gate blocks, up blocks) of the interleaved tensor's last axis, each [..., I]."""
-    nb = I // 128
-    gate = torch.cat([w[..., b * 256: b * 256 + 128] for b in range(nb)], dim=-1)
-    up = torch.cat([w[..., b * 256 + 128: b * 256 + 256] for b in range(nb)], dim=-1)
+    nb = I // 64
+    gate = torch.cat([w[..., b * 128: b * 128 + 64] for b in range(nb)], dim=-1)
+    up = torch.cat([w[..., b * 128 + 64: b * 128 + 128] for b in range(nb)], dim=-1)
     return gate, up
 
 
