@@ -1001,7 +1001,7 @@ static int sim_forward(const GGParams& p) {
   const int nk = p.K / splits * ESIZE / C::KB;  // stages per work item
   // the kernel's column halves of a partial last round, at launch_gg's grid on the stand-in's 256 CUs
   int tail_from = INT32_MAX;
-  if (C::HALF_TAIL && EPI != EPI_STORE_F32) {
+  if (C::HALF_TAIL && EPI != EPI_STORE_F32 && EPI != EPI_STORE_BF16) {
     const int grid = (256 / 8) * 8 * C::WG_PER_CU;
     const int full = items / grid * grid;
     if (items > full && 2 * (items - full) <= grid) tail_from = full;
@@ -2009,7 +2009,6 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"moe_bf16_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); })});
   s.push_back({"moe_bf16_gu_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_GU, 0.0); })});
   s.push_back({"moe_mx_eoi_decode_halves", halves([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EOI, 0.0); })});
-  s.push_back({"gemm_bf16_eoi_decode_halves", halves([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 512, 1024, L_EOI); })});
   // functional emulation (random operands; accumulators vs a reference GEMM). The EIO bf16 / MX and
   // EOI bf16 cases run on the GPU already and calibrate the instruction models.
   auto emu = [](std::function<void()> f) {
@@ -2027,8 +2026,8 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_bf16_eoi_decode", emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EOI); })});
   s.push_back({"emu_mx_eio_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })});
   s.push_back({"emu_mx_eoi_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EOI); })});
-  s.push_back({"emu_mx_eio_decode_halves", halves(emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); }))});
-  s.push_back({"emu_bf16_eoi_decode_halves", halves(emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EOI); }))});
+  s.push_back({"emu_moe_mx_decode_halves", halves(emu([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); }))});
+  s.push_back({"emu_moe_bf16_decode_halves", halves(emu([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); }))});
   s.push_back({"emu_moe_mx_gu_decode_halves", halves(emu([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0); }))});
   auto b6 = [](std::function<void()> f) {
     return [f] {
