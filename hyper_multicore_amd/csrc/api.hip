@@ -41,14 +41,20 @@ __global__ void mask_to_ids_kernel(const uint8_t* mask, int64_t T, int32_t* ids)
 
 __global__ void single_group_list_kernel(int64_t rows, int64_t* group_list) { group_list[0] = rows; }
 
-// Split-K factor of the router projection: one work item per CU (the 4-wave configuration runs one
-// workgroup per CU; the tile is 256 x 256, so T=8192 gives only 32 tiles), each split at least 4 K
-// stages of 32. More items would add a second round and partial tiles to write and read back.
-// Deterministic: split s writes its own partial buffer and the reduction adds them in a fixed order.
+// Decode-sized batches (few tokens) project on the 64-row tiles (two workgroups per CU): a 256-row
+// tile would be mostly padding.
+static bool router_small(int64_t T) { return T <= 256; }
+
+// Split-K factor of the router projection: one work item per workgroup slot (one per CU for the
+// 256 x 256 tiles, where T=8192 gives only 32 tiles; two per CU for the 64-row tiles), each split at
+// least 4 K stages of 32. More items would add a second round and partial tiles to write and read
+// back. Deterministic: split s writes its own partial buffer and the reduction adds them in a fixed
+// order.
 static int router_splits(int64_t T, int H, int E) {
-  const int64_t tiles = ((T + 255) / 256) * ((E + 255) / 256);
+  const int bm = mi355_gg_bm(router_small(T));
+  const int64_t tiles = ((T + bm - 1) / bm) * ((E + 255) / 256);
   const int kst = H / 32;
-  const int target = mi355_num_cus();
+  const int target = mi355_num_cus() * (router_small(T) ? 2 : 1);
   int best = 1;
   for (int s = 1; s <= kst / 4; ++s) {
     if (kst % s) continue;
@@ -149,9 +155,10 @@ extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32
   }
   p.group_list = group_list;
   p.tile_prefix = tile_prefix;
-  rc = mi355_plan_tiles(group_list, p.G, tile_prefix, st);
+  const bool small = router_small(num_tokens);
+  rc = mi355_plan_tiles(group_list, p.G, tile_prefix, st, small);
   if (rc) return rc;
-  rc = mi355_grouped_gemm(p, false, false, EPI_STORE_F32, st);
+  rc = mi355_grouped_gemm(p, false, false, EPI_STORE_F32, st, small);
   if (rc || splits == 1) return rc;
   const int64_t n = num_tokens * num_experts;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, st, partial, splits,

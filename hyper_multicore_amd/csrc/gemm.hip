@@ -80,11 +80,7 @@ int mi355_plan_row_blocks(const int64_t* group_list, int G, int rows, int32_t* b
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, bool small) {
   if (epi == EPI_SWIGLU_BF16_NUM) return MI355MOE_EINVAL;  // internal: chosen from the options below
   if (epi == EPI_SWIGLU_BF16 && (p.swiglu_limit > 0.0f || p.row_prob != nullptr)) epi = EPI_SWIGLU_BF16_NUM;
-  if (small) {
-    // the EPI_STORE_F32 router projection keeps the big tiles
-    if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
-    return dispatch_gg<GGSmall>(p, mx, b_kn, epi, stream);
-  }
+  if (small) return dispatch_gg<GGSmall>(p, mx, b_kn, epi, stream);
   const int variant = p.variant;
   // the 8-wave configuration first (the default); the 4-wave kernels below for what it does not take
   if (variant == MI355_GG_VARIANT_DEFAULT || variant == MI355_GG_VARIANT_PP) {

@@ -1637,10 +1637,7 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   if (epi == EPI_SWIGLU_BF16_NUM) return MI355MOE_EINVAL;
   if (epi == EPI_SWIGLU_BF16 && (p.swiglu_limit > 0.0f || p.row_prob != nullptr)) epi = EPI_SWIGLU_BF16_NUM;
   if (g_force_big) small = false;
-  if (small) {
-    if (epi == EPI_STORE_F32) return MI355MOE_EUNSUPPORTED;
-    return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
-  }
+  if (small) return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
   if (p.variant == MI355_GG_VARIANT_B6) {
     const int rc = sim_dispatch<GGB6>(p, mx, b_kn, epi);
     if (rc != MI355MOE_EUNSUPPORTED) return rc;

@@ -101,7 +101,9 @@ def test_route_matches_torch_reference_sets(gpu):
     torch.testing.assert_close(w.cpu().gather(1, order)[same], w_ref.gather(1, order_ref)[same], rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("T,H,E,dual", [(1024, 1024, 8, False), (777, 7168, 256, False), (1000, 4096, 128, True)])
+@pytest.mark.parametrize("T,H,E,dual", [(1024, 1024, 8, False), (777, 7168, 256, False), (1000, 4096, 128, True),
+                                         (128, 7168, 256, False), (200, 4096, 128, True), (1, 1024, 8, False),
+                                         (256, 2048, 64, False)])
 def test_gate_logits(gpu, T, H, E, dual):
     from hyper_multicore_amd import ops
     g = _seed(T + H)
