@@ -16,6 +16,7 @@
 #include "../../include/mi355moe.h"
 
 #define ROUTER_MAX_SLOTS 16  // E <= 1024
+#define ROUTER_FAST_GROUPS 16  // group-limited routing with at most this many groups takes the fast path
 
 MI355_DEV float score_fn(float l, int scoring) {
   if (scoring == MI355MOE_SCORE_SIGMOID) {
@@ -108,9 +109,56 @@ __global__ __launch_bounds__(256) void mi355_route_kernel(MI355MoeRouteArgs a) {
 
   // Group-limited selection (DeepSeek-V3 form): group score = sum of the two largest biased
   // scores in the group; keep the top `topk_groups` groups (ties -> lower group id).
-  if (a.num_groups > 1) {
-    const int G = a.num_groups;
-    const int S = E / G;
+  const int G = a.num_groups;
+  const int S = E / G;
+  if (G > 1 && G <= ROUTER_FAST_GROUPS && S <= 64 && 64 % S == 0 && E % 64 == 0) {
+    // Groups of S | 64 experts: slot j of lanes q S .. q S + S - 1 holds group j (64 / S) + q, so the
+    // top-2 reductions of all groups run at once (one independent chain per slot, xor steps inside
+    // the S-lane segments); the group scores go through the wave's LDS row to every lane, and each
+    // lane picks the top groups in registers (largest score, ties -> lower group id). The top-2
+    // merge and the sum are those of the general path below, so the scores are the same.
+    __shared__ float gscore[4][ROUTER_FAST_GROUPS];
+    const int wave = threadIdx.x >> 6;
+    float t1[SL], t2[SL];
+#pragma unroll
+    for (int j = 0; j < SL; ++j) {
+      t1[j] = j < slots ? biased[j] : NEG_INF;
+      t2[j] = NEG_INF;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      if (m >= S) continue;  // wave-uniform
+#pragma unroll
+      for (int j = 0; j < SL; ++j) {
+        const float o1 = __shfl_xor(t1[j], m, 64), o2 = __shfl_xor(t2[j], m, 64);
+        float n1, n2;
+        if (t1[j] >= o1) { n1 = t1[j]; n2 = fmaxf(t2[j], o1); } else { n1 = o1; n2 = fmaxf(t1[j], o2); }
+        t1[j] = n1; t2[j] = n2;
+      }
+    }
+    const int per_slot = 64 / S;
+#pragma unroll
+    for (int j = 0; j < SL; ++j)
+      if (j < slots && lane % S == 0) gscore[wave][j * per_slot + lane / S] = t1[j] + t2[j];
+    __builtin_amdgcn_wave_barrier();
+    float gs[ROUTER_FAST_GROUPS];
+#pragma unroll
+    for (int g = 0; g < ROUTER_FAST_GROUPS; ++g) gs[g] = g < G ? gscore[wave][g] : NEG_INF;
+    uint32_t keep = 0;
+    for (int r = 0; r < a.topk_groups; ++r) {
+      float bv = NEG_INF;
+      int bi = -1;
+#pragma unroll
+      for (int g = 0; g < ROUTER_FAST_GROUPS; ++g)
+        if (g < G && !((keep >> g) & 1u) && (bi < 0 || gs[g] > bv)) { bv = gs[g]; bi = g; }
+      keep |= 1u << bi;
+    }
+#pragma unroll
+    for (int j = 0; j < SL; ++j) {
+      int e = j * 64 + lane;
+      if (j < slots && e < E && !((keep >> (e / S)) & 1u)) biased[j] = NEG_INF;
+    }
+  } else if (G > 1) {
     float my_gscore = NEG_INF;  // lane g holds the score of group g
     for (int g = 0; g < G; ++g) {
       float t1 = NEG_INF, t2 = NEG_INF;

@@ -52,6 +52,14 @@ ROUTE_CASES = [
     ("sqrtsoftplus_384", 512, 384, 6, "sqrtsoftplus", 1, 1, 1.5, False),
     ("odd_experts_k1", 333, 100, 1, "sigmoid", 1, 1, 1.0, False),
     ("softmax_1024", 64, 1024, 16, "softmax", 1, 1, 1.0, False),
+    # group-limited routing: groups of 16, 32 (above) and 64 experts take the register path, 128 the
+    # general one
+    ("groups_of_16", 512, 128, 4, "sigmoid", 8, 3, 1.0, False),
+    ("groups_of_16_x16", 257, 256, 8, "sigmoid", 16, 5, 2.5, False),
+    ("groups_of_64", 300, 256, 6, "softmax", 4, 2, 1.0, False),
+    ("groups_of_128", 300, 256, 8, "sigmoid", 2, 1, 2.5, False),
+    ("decode_grouped", 128, 256, 8, "sigmoid", 8, 4, 2.5, False),
+    ("grouped_ties", 512, 256, 8, "sigmoid", 8, 4, 1.0, False),  # logits on a coarse grid, no bias
 ]
 
 
@@ -64,6 +72,9 @@ def test_route_bit_exact_vs_c_oracle(gpu, case):
     if scoring == "sqrtsoftplus":
         logits[0, :8] = torch.tensor([-80.0, -20.0, -1e-7, 0.0, 20.0 - 2 ** -19, 20.0, 20.0 + 2 ** -19, 80.0])
     bias = torch.randn(E, generator=g) * 0.01
+    if name.endswith("_ties"):  # many equal expert and group scores: the lower-id rules decide
+        logits = (logits * 2).round() / 2
+        bias = torch.zeros(E)
     bias_vl = torch.randn(E, generator=g) * 0.01 if use_vl else None
     mask = (torch.rand(T, generator=g) < 0.5) if use_vl else None
     w_ref, i_ref, s_ref = orc.route_c(logits.numpy(), bias.numpy(), top_k=K, scoring_func=scoring,
