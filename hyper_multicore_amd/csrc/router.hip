@@ -36,15 +36,30 @@ MI355_DEV float score_fn(float l, int scoring) {
   return sqrtf(sp);
 }
 
-// Wave argmax over (value, index): larger value wins, ties -> smaller index. Returns winner in all lanes.
+MI355_DEV void argmax_step(float& v, int& i, float ov, int oi) {
+  const bool take = (ov > v) || (ov == v && oi < i);
+  v = take ? ov : v;
+  i = take ? oi : i;
+}
+template <int CTRL>
+MI355_DEV void argmax_dpp(float& v, int& i) {
+  const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+  const int oi = __builtin_amdgcn_mov_dpp(i, CTRL, 0xF, 0xF, false);
+  argmax_step(v, i, ov, oi);
+}
+// (largest v, ties -> lowest i) over the wavefront, in every lane. The order is total, so the pairing
+// pattern does not change the result: within each 16-lane row, DPP moves (lane ^ 1, lane ^ 2, the
+// half-row mirror 7 - x, the row mirror 15 - x), then shuffles across rows (lane ^ 16, lane ^ 32).
 MI355_DEV void wave_argmax(float& v, int& i) {
+  argmax_dpp<0xB1>(v, i);   // quad_perm [1, 0, 3, 2]
+  argmax_dpp<0x4E>(v, i);   // quad_perm [2, 3, 0, 1]
+  argmax_dpp<0x141>(v, i);  // row_half_mirror
+  argmax_dpp<0x140>(v, i);  // row_mirror
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    float ov = __shfl_xor(v, m, 64);
-    int oi = __shfl_xor(i, m, 64);
-    bool take = (ov > v) || (ov == v && oi < i);
-    v = take ? ov : v;
-    i = take ? oi : i;
+  for (int m = 16; m <= 32; m <<= 1) {
+    const float ov = __shfl_xor(v, m, 64);
+    const int oi = __shfl_xor(i, m, 64);
+    argmax_step(v, i, ov, oi);
   }
 }
 
