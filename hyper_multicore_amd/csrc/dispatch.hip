@@ -32,9 +32,10 @@ struct DispatchPlan {
 static DispatchPlan make_dispatch_plan(int64_t num_tokens, int32_t top_k) {
   DispatchPlan p;
   p.slots = num_tokens * (int64_t)top_k;
+  // about 128 chunks (one wavefront each), at least 256 slots (4 rounds of 64) per chunk
   int64_t chunk = (p.slots + 127) / 128;
   chunk = ((chunk + 63) / 64) * 64;
-  if (chunk < 1024) chunk = 1024;
+  if (chunk < 256) chunk = 256;
   p.chunk = chunk;
   p.chunks = (int32_t)((p.slots + chunk - 1) / chunk);
   if (p.chunks < 1) p.chunks = 1;
