@@ -2023,9 +2023,9 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_bf16_eoi_decode", emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EOI); })});
   s.push_back({"emu_mx_eio_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })});
   s.push_back({"emu_mx_eoi_decode", emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EOI); })});
-  s.push_back({"emu_moe_mx_decode_halves", halves(emu([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); }))});
-  s.push_back({"emu_moe_bf16_decode_halves", halves(emu([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); }))});
-  s.push_back({"emu_moe_mx_gu_decode_halves", halves(emu([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0); }))});
+  s.push_back({"emu_moe_mx_decode_halves", halves(emu([=] { moe_forward(16, 4, 16, 512, 256, MX, L_EIO, 0.0); }))});
+  s.push_back({"emu_moe_bf16_decode_halves", halves(emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EIO, 0.0); }))});
+  s.push_back({"emu_moe_mx_gu_decode_halves", halves(emu([=] { moe_forward(16, 4, 16, 512, 256, MX, L_GU, 0.0); }))});
   auto b6 = [](std::function<void()> f) {
     return [f] {
       g_variant = MI355_GG_VARIANT_B6;
