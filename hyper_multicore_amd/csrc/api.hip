@@ -39,7 +39,12 @@ __global__ void mask_to_ids_kernel(const uint8_t* mask, int64_t T, int32_t* ids)
   if (t < T) ids[t] = mask[t] ? 1 : 0;
 }
 
-__global__ void single_group_list_kernel(int64_t rows, int64_t* group_list) { group_list[0] = rows; }
+// One group of `rows` rows: its group_list and its tile plan at tile height bm, in one launch.
+__global__ void single_group_plan_kernel(int64_t rows, int bm, int64_t* group_list, int32_t* tile_prefix) {
+  group_list[0] = rows;
+  tile_prefix[0] = 0;
+  tile_prefix[1] = (int32_t)((rows + bm - 1) / bm);
+}
 
 // Decode-sized batches (few tokens) project on the 64-row tiles (two workgroups per CU): a 256-row
 // tile would be mostly padding.
@@ -149,15 +154,19 @@ extern "C" int mi355moe_gate_logits(const uint16_t* x, int64_t num_tokens, int32
     // with split-K the partials stay in routed order and the reduction scatters them
     p.c_row_index = splits > 1 ? nullptr : gather;
   } else {
-    hipLaunchKernelGGL(single_group_list_kernel, dim3(1), dim3(1), 0, st, num_tokens, group_list);
     p.G = 1;
     p.a_row_div = 1;
   }
   p.group_list = group_list;
   p.tile_prefix = tile_prefix;
   const bool small = router_small(num_tokens);
-  rc = mi355_plan_tiles(group_list, p.G, tile_prefix, st, small);
-  if (rc) return rc;
+  if (dual) {
+    rc = mi355_plan_tiles(group_list, p.G, tile_prefix, st, small);
+    if (rc) return rc;
+  } else {
+    hipLaunchKernelGGL(single_group_plan_kernel, dim3(1), dim3(1), 0, st, num_tokens, mi355_gg_bm(small), group_list,
+                       tile_prefix);
+  }
   rc = mi355_grouped_gemm(p, false, false, EPI_STORE_F32, st, small);
   if (rc || splits == 1) return rc;
   const int64_t n = num_tokens * num_experts;
