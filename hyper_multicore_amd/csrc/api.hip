@@ -416,12 +416,10 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   int32_t* mapping = (int32_t*)(ws + L.mapping);
   int32_t* gather = (int32_t*)(ws + L.gather);
   int32_t* tile_prefix = (int32_t*)(ws + L.tile_prefix);
-  rc = mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, T, K, E, counts, nullptr, group_list, mapping, gather,
-                              a.error_flag, ws + L.dispatch, st);
-  if (rc) return rc;
-  // decode shapes (few routed rows per expert) use the 64-row tiles
+  // decode shapes (few routed rows per expert) use the 64-row tiles; the dispatch scan writes their plan
   const bool small = mi355_use_small_tiles(T * K, E, a.gemm_variant);
-  rc = mi355_plan_tiles(group_list, E, tile_prefix, st, small);
+  rc = mi355_dispatch_plan_enqueue(a.topk_ids, a.ids_dtype, T, K, E, counts, group_list, mapping, gather, a.error_flag,
+                                   ws + L.dispatch, tile_prefix, mi355_gg_bm(small), st);
   if (rc) return rc;
   const uint8_t* a1 = (const uint8_t*)a.hidden;
   // MX on the 8-wave GEMM: activation scales stage-major (one 4-byte copy per row and 128-K stage);

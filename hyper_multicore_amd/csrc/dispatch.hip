@@ -97,10 +97,14 @@ __global__ __launch_bounds__(64) void dispatch_hist_kernel(const IdT* ids, int64
   for (int e = lane; e < E; e += 64) out[e] = hist[e];
 }
 
+// With tile_prefix: also the grouped GEMM's tile plan at tile height bm (tile_prefix[e] = m-tiles of
+// the experts before e, [E] = all), which mi355_plan_tiles would compute from group_list.
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* chunk_counts, int chunks, int E,
                                                              int32_t* counts, int64_t* expert_offsets,
-                                                             int64_t* group_list, int32_t* expert_start) {
+                                                             int64_t* group_list, int32_t* expert_start,
+                                                             int32_t* tile_prefix, int bm) {
   __shared__ int64_t vals[DISPATCH_MAX_EXPERTS];
+  __shared__ int32_t tiles[DISPATCH_MAX_EXPERTS];
   __shared__ int64_t wsum[17];
   for (int e = threadIdx.x; e < E; e += 1024) {
     int32_t run = 0;
@@ -126,7 +130,15 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t* chunk_coun
     if (expert_offsets != nullptr) expert_offsets[e] = start;
     if (group_list != nullptr) group_list[e] = start + cnt;
     expert_start[e] = (int32_t)start;
+    tiles[e] = cnt > 0 ? (int32_t)((cnt + bm - 1) / bm) : 0;
   }
+  if (tile_prefix == nullptr) return;  // block-uniform
+  __syncthreads();  // every thread is done with vals
+  for (int e = threadIdx.x; e < E; e += 1024) vals[e] = tiles[e];
+  __syncthreads();
+  const int64_t total = block_exclusive_scan_1024(vals, E, wsum);
+  for (int e = threadIdx.x; e < E; e += 1024) tile_prefix[e] = (int32_t)vals[e];
+  if (threadIdx.x == 0) tile_prefix[E] = (int32_t)total;
 }
 
 template <typename IdT>
@@ -177,11 +189,11 @@ __global__ __launch_bounds__(64) void dispatch_permute_kernel(const IdT* ids, in
   }
 }
 
-// Internal: enqueue the three dispatch launches. expert_start_ws/chunk_ws come from workspace.
-int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E,
-                           int32_t* counts, int64_t* expert_offsets, int64_t* group_list,
-                           int32_t* mapping, int32_t* gather_index, int32_t* error_flag,
-                           void* workspace, hipStream_t stream) {
+// Internal: enqueue the three dispatch launches. expert_start_ws/chunk_ws come from workspace. With
+// tile_prefix, the scan also writes the grouped GEMM's tile plan at tile height bm.
+static int dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
+                            int64_t* expert_offsets, int64_t* group_list, int32_t* mapping, int32_t* gather_index,
+                            int32_t* error_flag, void* workspace, int32_t* tile_prefix, int bm, hipStream_t stream) {
   DispatchPlan p = make_dispatch_plan(num_tokens, top_k);
   int32_t* chunk_counts = (int32_t*)workspace;
   int32_t* expert_start = (int32_t*)((char*)workspace + align256((size_t)p.chunks * E * 4));
@@ -193,7 +205,7 @@ int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int t
     hipLaunchKernelGGL(dispatch_hist_kernel<int32_t>, dim3(p.chunks), dim3(64), lds, stream, (const int32_t*)ids,
                        p.slots, p.chunk, E, chunk_counts, error_flag);
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, stream, chunk_counts, p.chunks, E,
-                     counts, expert_offsets, group_list, expert_start);
+                     counts, expert_offsets, group_list, expert_start, tile_prefix, bm > 0 ? bm : 1);
   if (p.slots > 0 && dtype == MI355MOE_IDS_INT64)
     hipLaunchKernelGGL(dispatch_permute_kernel<int64_t>, dim3(p.chunks), dim3(64), lds, stream, (const int64_t*)ids,
                        p.slots, p.chunk, E, chunk_counts, expert_start, mapping, gather_index);
@@ -201,6 +213,20 @@ int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int t
     hipLaunchKernelGGL(dispatch_permute_kernel<int32_t>, dim3(p.chunks), dim3(64), lds, stream, (const int32_t*)ids,
                        p.slots, p.chunk, E, chunk_counts, expert_start, mapping, gather_index);
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
+}
+
+int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
+                           int64_t* expert_offsets, int64_t* group_list, int32_t* mapping, int32_t* gather_index,
+                           int32_t* error_flag, void* workspace, hipStream_t stream) {
+  return dispatch_enqueue(ids, dtype, num_tokens, top_k, E, counts, expert_offsets, group_list, mapping, gather_index,
+                          error_flag, workspace, nullptr, 0, stream);
+}
+
+int mi355_dispatch_plan_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
+                                int64_t* group_list, int32_t* mapping, int32_t* gather_index, int32_t* error_flag,
+                                void* workspace, int32_t* tile_prefix, int bm, hipStream_t stream) {
+  return dispatch_enqueue(ids, dtype, num_tokens, top_k, E, counts, nullptr, group_list, mapping, gather_index,
+                          error_flag, workspace, tile_prefix, bm, stream);
 }
 
 extern "C" int mi355moe_dispatch(const MI355MoeDispatchArgs* args, void* workspace, size_t workspace_size,

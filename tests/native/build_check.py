@@ -26,7 +26,7 @@ LIB_SOURCES = ["api.hip", "backward.hip", "dispatch.hip", "quant.hip", "gemm.hip
 # internal functions defined by the checker instead (made weak in the library objects)
 REPLACED = {
     "gemm.hip": ["mi355_grouped_gemm", "mi355_plan_tiles", "mi355_plan_row_blocks"],
-    "dispatch.hip": ["mi355_dispatch_enqueue", "mi355_permute_rows_enqueue", "mi355_unpermute_enqueue",
+    "dispatch.hip": ["mi355_dispatch_enqueue", "mi355_dispatch_plan_enqueue", "mi355_permute_rows_enqueue", "mi355_unpermute_enqueue",
                      "mi355_zero_enqueue"],
     "quant.hip": ["mi355_mx_quant_rows", "mi355_mx_quant_grouped"],
 }

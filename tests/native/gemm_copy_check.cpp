@@ -249,6 +249,16 @@ int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t T, int K, int E, 
   if (error_flag && bad) *error_flag = 1;
   return MI355MOE_OK;
 }
+
+// The dispatch with the tile plan: the two host versions above and below, in that order.
+int mi355_dispatch_plan_enqueue(const void* ids, int dtype, int64_t T, int K, int E, int32_t* counts,
+                                int64_t* group_list, int32_t* mapping, int32_t* gather, int32_t* error_flag,
+                                void* ws, int32_t* tile_prefix, int bm, hipStream_t st) {
+  const int rc = mi355_dispatch_enqueue(ids, dtype, T, K, E, counts, nullptr, group_list, mapping, gather,
+                                        error_flag, ws, st);
+  if (rc) return rc;
+  return mi355_plan_tiles(group_list, E, tile_prefix, st, bm == mi355_gg_bm(true));
+}
 int mi355_zero_enqueue(void* p, size_t bytes, hipStream_t) {
   if (bytes && !find_alloc(p, bytes)) {
     CHECK_FAIL("zero fill of %zu bytes outside every allocation", bytes);
