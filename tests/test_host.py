@@ -162,6 +162,40 @@ def test_bench_profile_summary(tmp_path):
     assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) == (2000 + 100) * 1024
     text = open(txt).read()
     assert "ratio 1.025" in text and "rocprofv3 --pmc FETCH_SIZE" in text
+    assert rec["rocprof_timed_us"] == 6000.0  # no kernel trace: the all-launch average
+
+
+def test_bench_profile_summary_times_the_timed_launches(tmp_path):
+    """The rocprofv3 GMM1 duration the summary sets beside the HIP-event time is the mean over the timed
+    steps' launches: after the routing-count step and the warm-up, before the graph replays."""
+    import json
+    import bench
+    out = tmp_path / "prof"
+    cnt = ["Kernel_Name", "Counter_Name", "Counter_Value"]
+    copy_kib = bench.COPY_BYTES / 1024
+    _write_csv(out / "copy" / "fetch" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "FETCH_SIZE", copy_kib]])
+    _write_csv(out / "copy" / "write" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "WRITE_SIZE", copy_kib]])
+    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true>(GGParams)"
+    d = out / "dsv3_bf16"
+    for tag, c in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE"), ("mfma", "MfmaUtil")):
+        _write_csv(d / tag / "pmc_counter_collection.csv", cnt, [[g1, c, 1.0]])
+    # 1 routing-count + 2 warm-up launches at 9 us, 3 timed at 5, 6 and 7 us, then 4 replays at 20 us
+    durations = [9, 9, 9, 5, 6, 7, 20, 20, 20, 20]
+    trace, t = [], 1000
+    for us in durations:
+        trace.append([g1, t, t + us * 1000])
+        t += 100000
+    _write_csv(d / "kt" / "run_kernel_trace.csv", ["Kernel_Name", "Start_Timestamp", "End_Timestamp"], trace[::-1])
+    avg = sum(durations) / len(durations) * 1000
+    _write_csv(d / "kt" / "run_kernel_stats.csv", ["Name", "Calls", "TotalDurationNs", "AverageNs", "MinNs", "MaxNs"],
+               [[g1, len(durations), avg * len(durations), avg, 5000, 20000]])
+    line = {"value": 1.0, "ms_per_step": 1.0, "steps": 3, "warmup": 2,
+            "config": {"gemm_variant": "default", "weight_layout": "EOI"},
+            "roofline": {"algorithmic_bytes": 1 << 20, "launch_ms": 0.006}}
+    (d / "bench.json").write_text(json.dumps(line) + "\n")
+    bench.summarize("dsv3_bf16", str(out), dest=str(tmp_path / "profiles"))
+    rec = json.loads((tmp_path / "profiles" / "traffic_dsv3_bf16_default_EOI.json").read_text())
+    assert rec["rocprof_timed_us"] == 6.0 and rec["rocprof_avg_us"] == 12.5
 
 
 def _physical(root, shape):
