@@ -105,24 +105,32 @@ __global__ __launch_bounds__(256) void mx_quant_act_kernel(const float* act, int
   const int c0 = blockIdx.y * 256;
   const int col = c0 + 4 * lane;
   const bool live = col < cols;  // a last chunk of 128 columns uses lanes 0 .. 31
-  for (int i = 0; i < QA_ROWS / 4; ++i) {
-    const int lr = wave * (QA_ROWS / 4) + i;
-    const int64_t r = r0 + lr;
-    if (r >= rows) break;  // wave-uniform
-    v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (live) v = *(const v4f*)(act + r * cols + col);
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    const uint32_t code = mx_scale_code(amax);
-    const uint32_t w = f32_to_e4m3_inrange(mx_apply_inv_scale(v[0], code)) |
-                       (f32_to_e4m3_inrange(mx_apply_inv_scale(v[1], code)) << 8) |
-                       (f32_to_e4m3_inrange(mx_apply_inv_scale(v[2], code)) << 16) |
-                       (f32_to_e4m3_inrange(mx_apply_inv_scale(v[3], code)) << 24);
-    if (live) {
-      *(uint32_t*)(q + r * cols + col) = w;
-      if ((lane & 7) == 0) codes[lane >> 3][lr] = (uint8_t)code;
+  constexpr int BATCH = 4;  // rows whose loads are issued together
+  for (int i0 = 0; i0 < QA_ROWS / 4; i0 += BATCH) {
+    v4f v[BATCH];
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const int64_t r = r0 + wave * (QA_ROWS / 4) + i0 + b;
+      v[b] = (live && r < rows) ? *(const v4f*)(act + r * cols + col) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const int lr = wave * (QA_ROWS / 4) + i0 + b;
+      const int64_t r = r0 + lr;
+      if (r >= rows) break;  // wave-uniform
+      float amax = fmaxf(fmaxf(fabsf(v[b][0]), fabsf(v[b][1])), fmaxf(fabsf(v[b][2]), fabsf(v[b][3])));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      amax = fmaxf(amax, __shfl_xor(amax, 4));
+      const uint32_t code = mx_scale_code(amax);
+      const uint32_t w = f32_to_e4m3_inrange(mx_apply_inv_scale(v[b][0], code)) |
+                         (f32_to_e4m3_inrange(mx_apply_inv_scale(v[b][1], code)) << 8) |
+                         (f32_to_e4m3_inrange(mx_apply_inv_scale(v[b][2], code)) << 16) |
+                         (f32_to_e4m3_inrange(mx_apply_inv_scale(v[b][3], code)) << 24);
+      if (live) {
+        *(uint32_t*)(q + r * cols + col) = w;
+        if ((lane & 7) == 0) codes[lane >> 3][lr] = (uint8_t)code;
+      }
     }
   }
   __syncthreads();
