@@ -149,6 +149,8 @@ def test_gpu_ops_refuse_cpu_tensors():
     from hyper_multicore_amd import ops
     with pytest.raises(TypeError):
         ops.gate_route(torch.zeros(2, 8), torch.zeros(8), top_k=2, scoring_func="softmax", routed_scaling_factor=1.0)
+    with pytest.raises(TypeError):  # the one-time weight preparation runs on the GPU only as well
+        ops.interleave_gate_up(torch.zeros(2, 64, 256, dtype=torch.bfloat16))
 
 
 def test_gemm_variant_is_per_call():
