@@ -281,3 +281,15 @@ def test_output_overlap_check():
     m = torch.zeros(64, 32)
     assert not _overlaps(m[:32], m[32:]) and _overlaps(m[:, :16], m[:, 16:])  # row blocks vs column halves
     assert not _overlaps(m, torch.zeros(64, 32))
+
+
+def test_bench_targets_block():
+    """The bench line's targets block sets the measured figures beside BASELINE.json's bars, for the
+    configs the run measured only."""
+    import bench
+    t = bench.targets({"dsv3_decode_mxfp8": {"roofline": {"frac": 0.66}, "layer_hbm_frac": 0.61},
+                       "dsv3_mxfp8": {"layer_mfma_frac": 0.19}})
+    assert t["dsv3_mxfp8_layer_mfma_frac"] == {"measured": 0.19, "bar": 0.55}
+    assert t["dsv3_decode_mxfp8_gmm1_hbm_frac"] == {"measured": 0.66, "bar": 0.65}
+    assert t["dsv3_decode_mxfp8_layer_hbm_frac"]["measured"] == 0.61
+    assert bench.targets({"small_bf16": {}}) == {}
