@@ -338,12 +338,12 @@ static FwdLayout fwd_layout(const MI355MoeForwardArgs& a) {
   L.gather = take(R * 4);
   L.tile_prefix = take((E + 1) * 4);
   L.act = take(R * I * (mx ? 1 : 2));
-  L.act_scale = mx ? take(std::max(R * mi355_mx_scale_ld(I), R * (I / 32) + 256)) : 0;
+  L.act_scale = mx ? take(std::max(R * mi355_mx_scale_ld(I), R * (I / 32) + 512)) : 0;
   L.act_f32 = mx ? take(R * I * 4) : 0;  // 8-wave MX path: fp32 SwiGLU output before its quantisation
   L.y = take(R * H * 2);
   L.xq = mx ? take(T * H) : 0;
   // MX token scales: [T, ld] for the 4-wave GEMM, or stage-major over the routed rows [H/128][R][4]
-  L.xs = mx ? take(std::max(T * mi355_mx_scale_ld(H), R * (H / 32) + 256)) : 0;
+  L.xs = mx ? take(std::max(T * mi355_mx_scale_ld(H), R * (H / 32) + 512)) : 0;
   L.tok_codes = mx ? take(T * (H / 32)) : 0;  // per-token codes before they go to the routed rows' planes
   L.total = off;
   return L;

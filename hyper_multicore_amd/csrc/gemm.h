@@ -54,8 +54,8 @@ struct GGParams {
   // code j of stage s of routed row r at a_scale[s * stride + j * P + r], so a tile's codes of a
   // stage are four contiguous runs. When c_scale_stage_stride is set, the MX SwiGLU epilogue writes
   // c_scale in that form. The planes are indexed by routed row (a_scale_routed must be set when
-  // a_row_index gathers the rows), and hold at least 256 bytes past the last row (a tile reads whole
-  // 256-row runs).
+  // a_row_index gathers the rows), and hold at least 512 bytes past the last row (a tile reads two
+  // 256-byte runs per plane from the 4-aligned row at or below its first row).
   int64_t a_scale_stage_stride;
   int64_t c_scale_stage_stride;
   int32_t a_scale_routed;

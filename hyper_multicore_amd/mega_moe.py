@@ -20,6 +20,7 @@ raises ``NotImplementedError``; MXFP8 rejects them as the reference does. ``ep_g
 from __future__ import annotations
 
 import math
+import os
 import struct
 from dataclasses import dataclass
 from typing import Any
@@ -91,6 +92,12 @@ def _positive_int(name: str, value: Any) -> int:
 
 
 ROUTE_COUNT_ERROR = "MegaMoe counts must describe the actual distinct Top-K routes"
+# Host-side route checks in MegaMoeExperts.forward (a debugging aid, off by default). Like the
+# reference's static-token path (route.py:186-211), the forward trusts tokens_per_expert and checks only
+# its shape, device and dtype; ids outside [0, E) are skipped on the device and reported through the
+# library's error flag. With MI355MOE_CHECK_ROUTES=1 the forward also runs validate_routes, which
+# waits for the device once per call.
+CHECK_ROUTES = os.environ.get("MI355MOE_CHECK_ROUTES", "0") == "1"
 
 
 def validate_routes(topk_ids: torch.Tensor, num_experts: int, tokens_per_expert: torch.Tensor | None = None) -> None:
@@ -332,7 +339,13 @@ class MegaMoeExperts(torch.nn.Module):
             raise RuntimeError("MegaMoeExperts runs eagerly; graph capture is not supported")
         if flat.shape[0] == 0:
             return torch.empty_like(hidden_states)
-        validate_routes(topk_ids, self.num_experts, tokens_per_expert)
+        if tokens_per_expert is not None:
+            if tokens_per_expert.device != topk_ids.device:
+                raise ValueError("tokens_per_expert must be on the route tensor device.")
+            if tokens_per_expert.dtype not in (torch.int32, torch.int64):
+                raise TypeError(f"tokens_per_expert must be int32 or int64, got {tokens_per_expert.dtype}.")
+        if CHECK_ROUTES:
+            validate_routes(topk_ids, self.num_experts, tokens_per_expert)
         if tokens_per_expert is not None:
             tokens_per_expert = tokens_per_expert.to(torch.int32)
         if self._precision == "bf16":

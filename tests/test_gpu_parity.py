@@ -93,7 +93,9 @@ def test_route_bit_exact_vs_c_oracle(gpu, case):
 
 
 def test_route_matches_torch_reference_sets(gpu):
-    """Index sets equal the torch reference form (module.py:199-227) except on near-tie rows."""
+    """Index sets equal the torch reference form (module.py:199-227) on every row that is not a near tie
+    below the scorings' rounding difference (tests/route_ties.py)."""
+    from tests.route_ties import set_mismatches
     from hyper_multicore_amd import ops
     g = _seed(7)
     T, E, K = 4096, 256, 8
@@ -105,11 +107,14 @@ def test_route_matches_torch_reference_sets(gpu):
                                           num_groups=8, topk_groups=4)
     got = torch.sort(i.cpu(), dim=1).values
     want = torch.sort(i_ref, dim=1).values
+    near, other = set_mismatches(i.cpu(), i_ref, logits.sigmoid() + bias, 8, 4)
+    print(f"[route] torch-form sets: {len(other)} rows differ, {len(near)} near-tie rows of {T}", flush=True)
+    assert other == [] and len(near) <= 2
     same = (got == want).all(dim=1)
-    assert same.float().mean() > 0.999
     order = torch.argsort(i.cpu(), dim=1)
     order_ref = torch.argsort(i_ref, dim=1)
-    torch.testing.assert_close(w.cpu().gather(1, order)[same], w_ref.gather(1, order_ref)[same], rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(w.cpu().gather(1, order)[same], w_ref.gather(1, order_ref)[same], rtol=1e-5,
+                               atol=1e-6)
 
 
 @pytest.mark.parametrize("T,H,E,dual", [(1024, 1024, 8, False), (777, 7168, 256, False), (1000, 4096, 128, True),
@@ -928,11 +933,15 @@ def test_mxfp8_module_autograd(gpu):
     assert orc.rel_l2(pg.grad.cpu(), rp) < MXFP8_REL_L2
 
 
-def test_module_refuses_invalid_routes(gpu):
-    """MegaMoeExperts raises RuntimeError for an id outside [0, E) and for tokens_per_expert that is not
-    the ids' histogram (route.py:566-593), before launching any expert work."""
+def test_module_refuses_invalid_routes(gpu, monkeypatch):
+    """With the route checks on (MI355MOE_CHECK_ROUTES=1), MegaMoeExperts raises RuntimeError for an id
+    outside [0, E) and for tokens_per_expert that is not the ids' histogram (route.py:566-593), before
+    launching any expert work. By default the forward trusts tokens_per_expert like the reference's
+    static path (route.py:186-211) and does not wait for the device."""
     import hyper_multicore_amd as hm
+    from hyper_multicore_amd import mega_moe
     from hyper_multicore_amd.mega_moe import ROUTE_COUNT_ERROR
+    monkeypatch.setattr(mega_moe, "CHECK_ROUTES", True)
     T, H, I, E, K = 8, 256, 128, 4, 2
     g = _seed(99)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(gpu)
@@ -951,3 +960,11 @@ def test_module_refuses_invalid_routes(gpu):
     wrong[1] -= 1
     with pytest.raises(RuntimeError, match=ROUTE_COUNT_ERROR):
         experts(x, ids, probs, expert_weights=(w1, w2), tokens_per_expert=wrong)
+    # default: the supplied histogram is trusted (the library recomputes the counts it uses)
+    monkeypatch.setattr(mega_moe, "CHECK_ROUTES", False)
+    torch.testing.assert_close(experts(x, ids, probs, expert_weights=(w1, w2), tokens_per_expert=wrong),
+                               experts(x, ids, probs, expert_weights=(w1, w2)), rtol=0, atol=0)
+    with pytest.raises(ValueError, match="route tensor device"):
+        experts(x, ids, probs, expert_weights=(w1, w2), tokens_per_expert=wrong.cpu())
+    with pytest.raises(TypeError, match="int32 or int64"):
+        experts(x, ids, probs, expert_weights=(w1, w2), tokens_per_expert=wrong.float())

@@ -806,3 +806,18 @@ def test_expert_forward_tokens_equals_full_reference(precision):
         sub = orc.expert_forward_reference_tokens(x, ids, probs, tokens, lambda e: (W1[e], W2[e]),
                                                   precision="mxfp8")
     assert torch.equal(sub, full[tokens])
+
+
+def test_route_set_mismatch_classifier():
+    """The near-tie classifier used by the torch-form routing comparisons: an exact tie at the K-th
+    place is a near tie; a swap of clearly separated experts is not."""
+    from tests.route_ties import set_mismatches
+    biased = torch.tensor([[0.9, 0.5, 0.5, 0.1], [0.9, 0.6, 0.5, 0.1]])
+    ids = torch.tensor([[0, 1], [0, 2]])
+    ids_torch = torch.tensor([[0, 2], [0, 1]])
+    near, other = set_mismatches(ids, ids_torch, biased)
+    assert near == [0] and other == [1]
+    # group-limited form: groups {0,1} and {2,3} with equal top-2 sums, the kept group differs
+    biased = torch.tensor([[0.5, 0.25, 0.625, 0.125]])
+    near, other = set_mismatches(torch.tensor([[0]]), torch.tensor([[2]]), biased, num_groups=2, topk_groups=1)
+    assert near == [0] and other == []
