@@ -11,7 +11,7 @@ oracle's restatement of the reference CPU path, on a bounded token prefix). Othe
 reported under "extra" (``--extra none`` skips them).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config dsv3_bf16] [--extra all]
-                      [--gemm-variant default|b6|dv|sp|sp4] [--gemm-shapes]
+                      [--gemm-variant default|pp|w4] [--gemm-shapes]
 """
 from __future__ import annotations
 
@@ -581,7 +581,7 @@ def main() -> int:
     ap.add_argument("--config", default="dsv3_bf16", choices=sorted(CONFIGS))
     ap.add_argument("--extra", default="all", help="'all', 'none' or comma list of extra configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--gemm-variant", default=None, choices=["default", "b6", "dv", "sp", "sp4", "pp", "w4"],
+    ap.add_argument("--gemm-variant", default=None, choices=["default", "pp", "w4"],
                     help="forward grouped-GEMM configuration (default: MI355MOE_GG_VARIANT or the library default)")
     ap.add_argument("--bf16-layout", default="EOI", choices=["EOI", "EIO", "EIO_GU"],
                     help="expert-weight layout of the bf16 configs (EIO: the reference module's default)")

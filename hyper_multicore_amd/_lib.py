@@ -11,7 +11,7 @@ from ctypes import POINTER, Structure, c_float, c_int32, c_int64, c_size_t, c_ui
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmi355moe.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED, EWORKSPACE = 0, -1, -2, -3, -4
 NOALLOC_MAX_GROUPS = 4096
@@ -25,9 +25,7 @@ FEATURE_BACKWARD = 8
 FEATURE_ROUTE_GRAD = 16
 FEATURE_MX_WEIGHT_PREP = 32
 FEATURE_MX_BACKWARD = 64
-FEATURE_DIRECT_GEMM = 128
-FEATURE_SPLIT_ROLES = 256
-GEMM_VARIANT = {"default": 0, "b6": 1, "dv": 2, "sp": 3, "sp4": 4, "pp": 5, "w4": 6}
+GEMM_VARIANT = {"default": 0, "pp": 5, "w4": 6}
 NUMERICS_CLAMP_AFTER_SILU = 1
 NUMERICS_PROBS_BEFORE_FC2 = 2
 LAYOUT = {"EIO": 0, "EOI": 1, "EIO_GU": 2}

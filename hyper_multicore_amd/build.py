@@ -16,7 +16,7 @@ REPO_DIR = PACKAGE_DIR.parent
 CSRC = PACKAGE_DIR / "csrc"
 OUT_DIR = PACKAGE_DIR / "_lib"
 LIB_NAME = "libmi355moe.so"
-SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "gemm_wgrad.hip", "gemm_var.hip", "gemm_split.hip", "gemm_direct.hip", "gemm_pp.hip", "quant.hip", "backward.hip", "api.hip"]
+SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "gemm_wgrad.hip", "gemm_pp.hip", "quant.hip", "backward.hip", "api.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -18,17 +18,11 @@ extern "C" int mi355moe_features(void) {
          (mi355_backward_enabled() ? MI355MOE_FEATURE_BACKWARD : 0) |
          (mi355_route_grad_enabled() ? MI355MOE_FEATURE_ROUTE_GRAD : 0) |
          (mi355_mx_weight_prep_enabled() ? MI355MOE_FEATURE_MX_WEIGHT_PREP : 0) |
-         (mi355_mx_backward_enabled() ? MI355MOE_FEATURE_MX_BACKWARD : 0) |
-         (mi355_direct_gemm_enabled() ? MI355MOE_FEATURE_DIRECT_GEMM : 0) |
-         (mi355_split_roles_enabled() ? MI355MOE_FEATURE_SPLIT_ROLES : 0);
+         (mi355_mx_backward_enabled() ? MI355MOE_FEATURE_MX_BACKWARD : 0);
 }
 
 bool mi355_gg_variant_valid(int variant) {
-  if (variant < MI355_GG_VARIANT_DEFAULT || variant > MI355_GG_VARIANT_W4) return false;
-  if (variant == MI355_GG_VARIANT_DV && !mi355_direct_gemm_enabled()) return false;
-  if ((variant == MI355_GG_VARIANT_SP || variant == MI355_GG_VARIANT_SP4) && !mi355_split_roles_enabled())
-    return false;
-  return true;
+  return variant == MI355_GG_VARIANT_DEFAULT || variant == MI355_GG_VARIANT_PP || variant == MI355_GG_VARIANT_W4;
 }
 
 // ---------------------------------------------------------------------------------------------

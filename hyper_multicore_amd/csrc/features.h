@@ -19,7 +19,3 @@ inline bool mi355_route_grad_enabled() { return true; }
 inline bool mi355_mx_weight_prep_enabled() { return true; }
 // MXFP8 expert backward (needs the MX K-contiguous GEMM path for its data-gradient GEMMs).
 inline bool mi355_mx_backward_enabled() { return true; }
-// The direct-weight grouped-GEMM configuration (gemm_direct.hip), selectable as variant "dv".
-inline bool mi355_direct_gemm_enabled() { return true; }
-// Split copy roles in the grouped GEMM (variants sp / sp4).
-inline bool mi355_split_roles_enabled() { return true; }

@@ -118,20 +118,12 @@ struct MxGroupedQuant {
 };
 int mi355_mx_quant_grouped(const MxGroupedQuant& q, hipStream_t stream);
 int mi355_num_cus();  // CU count of the current device (cached per device)
-// Forward tile-configuration variants, chosen per call (GGParams::variant; 0 = the default, the 8-wave
-// configuration where it applies). A variant keeps the default's tile height, so tile plans are
-// shared; it answers MI355MOE_EUNSUPPORTED for the paths it does not build, which then run on the
-// default configuration.
-enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_B6 = 1, MI355_GG_VARIANT_DV = 2, MI355_GG_VARIANT_SP = 3,
-       MI355_GG_VARIANT_SP4 = 4, MI355_GG_VARIANT_PP = 5, MI355_GG_VARIANT_W4 = 6 };
-bool mi355_gg_variant_valid(int variant);  // known, and its feature bit set
-int mi355_grouped_gemm_variant(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
-// The direct-weight configuration (gemm_direct.hip), variant "dv"; MI355MOE_EUNSUPPORTED outside its
-// domain (K-contiguous weights, K a multiple of 8 stages, bf16 store / SwiGLU epilogues).
-int mi355_grouped_gemm_direct(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream);
-// The split-role configurations (gemm_split.hip), variants sp / sp4; MI355MOE_EUNSUPPORTED outside
-// their domain (gg_split_applies).
-int mi355_grouped_gemm_split(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream, int variant);
+// Forward tile configurations, chosen per call (GGParams::variant): DEFAULT - the 8-wave configuration
+// where it applies, the 64-row tiles for decode-shaped GEMMs, else the 4-wave one; PP - the 8-wave
+// configuration where it applies for every row count, else the 4-wave one; W4 - the 4-wave one.
+// Values 1-4 are retired (configurations of earlier revisions) and refused.
+enum { MI355_GG_VARIANT_DEFAULT = 0, MI355_GG_VARIANT_PP = 5, MI355_GG_VARIANT_W4 = 6 };
+bool mi355_gg_variant_valid(int variant);
 // The 8-wave ping-pong configuration (gemm_pp.hip); MI355MOE_EUNSUPPORTED outside its domain
 // (mi355_gg_pp_applies). Tile plans are those of the 256-row configuration.
 bool mi355_gg_pp_applies(const GGParams& p, bool mx, bool b_kn, int epi);

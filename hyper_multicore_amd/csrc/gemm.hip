@@ -89,11 +89,6 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   }
   // stage-major MX scales are read and written by the 8-wave configuration only
   if (p.a_scale_stage_stride != 0 || p.c_scale_stage_stride != 0) return MI355MOE_EUNSUPPORTED;
-  if (variant == MI355_GG_VARIANT_B6 || variant == MI355_GG_VARIANT_DV || variant == MI355_GG_VARIANT_SP ||
-      variant == MI355_GG_VARIANT_SP4) {
-    const int rc = mi355_grouped_gemm_variant(p, mx, b_kn, epi, stream, variant);
-    if (rc != MI355MOE_EUNSUPPORTED) return rc;
-  }
   return dispatch_gg<GGBig>(p, mx, b_kn, epi, stream);
 }
 

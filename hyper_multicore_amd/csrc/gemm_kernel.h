@@ -1,8 +1,8 @@
-// Device building blocks of the persistent grouped GEMM shared by gemm.hip (forward kernels, default
-// configurations), gemm_var.hip (configuration variants) and gemm_wgrad.hip (grouped-K weight-gradient
-// kernels): the direct-to-LDS copy and the waits, the software-pipelined K loop, the forward kernel
-// and its launch. The three files are separate translation units: with other kernel families in the
-// same module the compiler schedules the default kernels' scalar address code differently.
+// Device building blocks of the persistent grouped GEMM shared by gemm.hip (forward kernels) and
+// gemm_wgrad.hip (grouped-K weight-gradient kernels): the direct-to-LDS copy and the waits, the
+// software-pipelined K loop, the forward kernel and its launch. The two files are separate
+// translation units: with other kernel families in the same module the compiler schedules the
+// forward kernels' scalar address code differently.
 #pragma once
 #include <type_traits>
 #include "common.h"
@@ -35,33 +35,13 @@ MI355_DEV void lds_dma(const void* g, uint32_t lds_off_uniform, uint8_t* smem, i
                  "global_load_lds_dword %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc");
   else static_assert(SZ == 16, "unsupported DMA size");
 }
-// The copy policy of the kernels (see gemm_plan.h). copy_so: the scalar-base + 32-bit vector-offset
-// form of the 16-byte copy (base wave-uniform, in SGPRs), for the OFFS configurations.
+// The copy policy of the kernels (see gemm_plan.h).
 struct DevDma {
   template <int SZ>
   MI355_DEV static void copy(const void* g, uint32_t lds_off_uniform, uint8_t* smem, int enable) {
     lds_dma<SZ>(g, lds_off_uniform, smem, enable);
   }
-  template <int SZ>
-  MI355_DEV static void copy_so(const uint8_t* base, uint32_t off, uint32_t lds_off_uniform, uint8_t* smem, int enable) {
-    static_assert(SZ == 16, "scalar-base copies are 16 bytes");
-    // LDS address as the LDS base of the shared array plus the offset (32-bit arithmetic; casting the
-    // generic pointer smem + offset instead costs a null check and a 64-bit value per distinct offset)
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem + lds_off_uniform);
-    const int en = __builtin_amdgcn_readfirstlane(enable);
-    asm volatile("s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
-                 "global_load_lds_dwordx4 %0, %1\n1:" ::"v"(off), "s"(base), "s"(m0), "s"(en) : "memory", "scc");
-  }
 };
-// A wave-uniform pointer held in scalar registers (values derived from an LDS search, such as the
-// group index, are not known to the compiler to be uniform; the scalar-base loads need SGPRs).
-MI355_DEV const uint8_t* gg_uniform(const uint8_t* ptr) {
-  const uint64_t v = (uint64_t)(uintptr_t)ptr;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
 // Workgroup barrier without the release fence of __syncthreads (which would wait for every
 // outstanding global load, including the prefetched stages): LDS reads of this wave are drained,
 // the direct-to-LDS loads are ordered by the explicit vmcnt waits.
@@ -94,7 +74,7 @@ MI355_DEV void wait_vm(int n) {
 // A-scale group g+1 (stages 8g+8 ..) is issued at iteration 8g into the slot of group g-1, whose
 // last stage was read during iteration 8g-2.
 // NM = number of 32-row subtiles this wave computes (0, 1, 2 or 4).
-template <class C, bool MX, bool B_KN, int NM, bool LA, bool GK = false, bool LB = true>
+template <class C, bool MX, bool B_KN, int NM, bool LA, bool GK = false>
 MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, int lane, uint8_t* smem,
                       v16f (&acc)[C::MI][C::NI]) {
   // grouped-K mode: A is read K-major like B (and the caller skips groups without rows)
@@ -136,7 +116,7 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
       }
 #pragma unroll
       for (int it = t * SS::ITEMS / T; it < (t + 1) * SS::ITEMS / T; ++it)
-        issue_item<C, MX, B_KN, LA, GK, DevDma, LB>(cp, k, nk, wave, smem, it);
+        issue_item<C, MX, B_KN, LA, GK, DevDma>(cp, k, nk, wave, smem, it);
       __builtin_amdgcn_sched_barrier(0);  // keep this interleave order
     }
     issue_scales_item<C, MX, B_KN, LA, DevDma, GK>(cp, k, nk, wave, smem);
@@ -160,50 +140,6 @@ MI355_DEV void k_loop(const CopyPlan<C>& cp, int nk, int wave, int wm, int wn, i
 #pragma unroll
     for (int t = 0; t < SS::MFMAS; ++t) mfma_elem<C, MX, B_KN, NM, GK>(f0, acc, t);
   }
-}
-
-// One work item of a split-role configuration (C::SPLIT) for the waves of role ROLE (0: the two
-// activation-copying waves, 1: the two weight-copying waves). The same steps as the work-item body of
-// grouped_gemm_kernel; every wave still computes its own 128 x 128 wave tile.
-template <class C, bool MX, bool B_KN, int EPI, int ROLE>
-MI355_DEV void gg_split_item(const GGParams& p, const int32_t* prefix, int L, int splits, int nk, int tid, int wave,
-                             int lane, uint8_t* smem) {
-  constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX || EPI == EPI_SWIGLU_BF16_NUM);
-  constexpr int ESIZE = MX ? 1 : 2;
-  constexpr bool copy_role_a = ROLE == 0, copy_role_b = ROLE == 1;
-  const int wm = (int)((unsigned)wave / C::WGN), wn = (int)((unsigned)wave % C::WGN);
-  constexpr int tail_from = INT32_MAX;  // no column halves in the split-role configurations
-#include "gemm_item_fwd.inc"
-  cp.a_base = gg_uniform(cp.a_base);
-  cp.b_base = gg_uniform(cp.b_base);
-  v16f acc[C::MI][C::NI];
-#pragma unroll
-  for (int i = 0; i < C::MI; ++i)
-#pragma unroll
-    for (int j = 0; j < C::NI; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  __syncthreads();  // the previous item's last stage / epilogue reads are done before refilling
-  const int rows_w = rows_valid - wm * C::WM;
-  const int nm = (C::MI >= 4 && rows_w > 64) ? 4 : ((C::MI >= 2 && rows_w > 32) ? 2 : (rows_w >= 1 ? 1 : 0));
-  if constexpr (ROLE == 1) {
-    if (C::MI >= 4 && nm == 4) k_loop<C, MX, B_KN, (C::MI >= 4 ? 4 : 1), false, false, true>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else if (nm == 2) k_loop<C, MX, B_KN, 2, false, false, true>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else if (nm == 1) k_loop<C, MX, B_KN, 1, false, false, true>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else k_loop<C, MX, B_KN, 0, false, false, true>(cp, nk, wave, wm, wn, lane, smem, acc);
-  } else if (wave_copies_a<C>(wave, rows_valid)) {
-    if (C::MI >= 4 && nm == 4) k_loop<C, MX, B_KN, (C::MI >= 4 ? 4 : 1), true, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else if (nm == 2) k_loop<C, MX, B_KN, 2, true, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else if (nm == 1) k_loop<C, MX, B_KN, 1, true, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else k_loop<C, MX, B_KN, 0, true, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-  } else {
-    if (C::MI >= 4 && nm == 4) k_loop<C, MX, B_KN, (C::MI >= 4 ? 4 : 1), false, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else if (nm == 2) k_loop<C, MX, B_KN, 2, false, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else if (nm == 1) k_loop<C, MX, B_KN, 1, false, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-    else k_loop<C, MX, B_KN, 0, false, false, false>(cp, nk, wave, wm, wn, lane, smem, acc);
-  }
-  __syncthreads();  // all waves are done reading the ring before the epilogue reuses LDS
-#include "gemm_epilogue.inc"
 }
 
 template <class C, bool MX, bool B_KN, int EPI>
@@ -245,13 +181,6 @@ __global__ __launch_bounds__(C::THREADS, C::WG_PER_CU) void grouped_gemm_kernel(
   for (int round = 0;; ++round) {
     const int L = round * (int)gridDim.x + xcd * per_xcd + slot;
     if (L >= total) break;
-    if constexpr (C::SPLIT) {
-      // split copy roles: each role's work item in its own instantiation (only its copy plan live)
-      if (wave < 2) gg_split_item<C, MX, B_KN, EPI, 0>(p, prefix, L, splits, nk, tid, wave, lane, smem);
-      else gg_split_item<C, MX, B_KN, EPI, 1>(p, prefix, L, splits, nk, tid, wave, lane, smem);
-      continue;
-    }
-    constexpr bool copy_role_a = true, copy_role_b = true;
     // ---- decode work item, per-thread copy sources -------------------------------------
 #include "gemm_item_fwd.inc"
 

@@ -25,8 +25,7 @@
 //             where experts see a few rows each.
 // AS_N_ / BSR_N_: slots of the MX activation-scale ring and of the MX EOI weight row-scale ring
 // (2, or 0 for a configuration that never runs those paths and spends the LDS on its rings).
-template <int BM_, int WGM_, int A_SLOTS_, int B_SLOTS_, int PREFIX_MAX_, int WG_PER_CU_, int AS_N_ = 2, int BSR_N_ = 2,
-          bool SPLIT_ = false>
+template <int BM_, int WGM_, int A_SLOTS_, int B_SLOTS_, int PREFIX_MAX_, int WG_PER_CU_, int AS_N_ = 2, int BSR_N_ = 2>
 struct GGCfg {
   static constexpr int BM = BM_;
   static constexpr int BN = 256;
@@ -59,17 +58,9 @@ struct GGCfg {
   static constexpr int A_INSTR = BM * (KB / 16) / 64 / WAVES;
   static constexpr int B_INSTR = BN * (KB / 16) / 64 / WAVES;
   static constexpr int AS_WAVES = BM / 64;             // waves that fetch A scale rows (64 each)
-  // Copy roles. By default every wave copies its share of both operands. With SPLIT, waves 0-1 copy
-  // only the activations (and their scales) and waves 2-3 only the weights (and theirs): a wave's
-  // loads retire in order, so a wave that copies both must wait for its weight copies of stage
-  // k + B_SLOTS - A_SLOTS + 1 when it waits for its activation copies of stage k + 1, and the
-  // weight ring hides only about A_SLOTS - 1 stages of latency; with split roles it hides B_SLOTS - 1.
-  static constexpr bool SPLIT = SPLIT_;
-  static constexpr int A_PER = SPLIT ? 2 * A_INSTR : A_INSTR;  // activation copies per copying wave and stage
-  static constexpr int B_PER = SPLIT ? 2 * B_INSTR : B_INSTR;  // weight copies per copying wave and stage
-  // OFFS: forward operand copies address a uniform base plus a per-lane 32-bit offset (the
-  // scalar-base load form, one VGPR per copy instead of two; A and a group's weights < 4 GiB).
-  static constexpr bool OFFS = SPLIT;
+  // Every wave copies its share of both operands.
+  static constexpr int A_PER = A_INSTR;  // activation copies per wave and stage
+  static constexpr int B_PER = B_INSTR;  // weight copies per wave and stage
   // the 64-row decode configuration runs the items of a partial last round as column halves
   static constexpr bool HALF_TAIL = BM == 64;
   // epilogue staging (overlays the rings and the scale slots, never the tile prefix)
@@ -85,26 +76,9 @@ struct GGCfg {
   static_assert(AS_N == 0 || A_SLOTS * BS_BYTES <= AS_N * AS_SLOT,
                 "grouped-K MX: per-stage A column scales fit the AS area");
   static_assert((AS_N == 0 || AS_N == 2) && (BSR_N == 0 || BSR_N == 2), "scale rings have two slots or none");
-  static_assert(!SPLIT || (WAVES == 4 && BSR_N == 0 && AS_WAVES == WAVES),
-                "split copy roles: 4 waves, two per role; no weight row-scale ring");
 };
 using GGBig = GGCfg<256, 2, 3, 5, 1024, 1>;
 using GGSmall = GGCfg<64, 1, 3, 3, 256, 2>;
-
-// OFFS configurations address their forward copies with 32-bit offsets from uniform bases: A and
-// one group's weights must stay below 4 GiB (otherwise the caller keeps the default configuration).
-MI355_HD bool gg_offsets_fit(const GGParams& p) {
-  const int64_t lim = (int64_t)1 << 32;
-  return p.a_bytes > 0 && p.a_bytes < lim && p.b_group_stride > 0 && p.b_group_stride < lim;
-}
-
-// The GEMMs the split-role configurations run: EIO weights (N contiguous; MXFP8 roots' col_data /
-// col_scale or bf16 [E, K, N]), the bf16 store and the SwiGLU epilogue of the precision (MX requant /
-// bf16 without the numerics options), 32-bit offsets within reach.
-MI355_HD bool gg_split_applies(const GGParams& p, bool mx, bool b_kn, int epi) {
-  const bool epi_ok = epi == EPI_STORE_BF16 || epi == (mx ? EPI_SWIGLU_MX : EPI_SWIGLU_BF16);
-  return b_kn && epi_ok && gg_offsets_fit(p);
-}
 
 // Tile column j (0..BN-1) -> weight column. SwiGLU: the columns of each wave tile (WN wide) are
 // WN/2 gate columns followed by the matching WN/2 up columns, so a lane holds gate and up of the
@@ -130,12 +104,7 @@ template <class C>
 struct CopyPlan {
   const uint8_t* a[C::A_PER];
   const uint8_t* b[C::B_PER];
-  // OFFS configurations (forward): uniform bases at stage 0 and per-lane offsets instead of a[] / b[]
-  const uint8_t* a_base;
-  const uint8_t* b_base;
-  uint32_t ao[C::A_PER], bo[C::B_PER];
   const uint8_t* s;        // MX: A scale row (waves < AS_WAVES)
-  const uint8_t* s2;       // MX, split roles: the second A scale row of an activation-copying wave
   const uint8_t* bs;       // MX EIO: B scale column pair (waves 0 and 1)
   const uint8_t* bsr;      // MX EOI: B scale row (tile column wave*64 + lane)
   int64_t b_stage_stride;  // bytes to advance B per stage
@@ -149,17 +118,8 @@ struct CopyPlan {
   int64_t as_stage_stride; // grouped-K MX: bytes to advance the A column scales per stage
 };
 
+// Waves 0 and 1 copy the per-stage MX weight scales (EIO layout).
 MI355_HD bool is_bs_wave(int wave) { return wave < 2; }
-// Copy roles (see GGCfg::SPLIT): the index of a wave among the waves that copy activations / weights,
-// whether it copies weights, and whether it copies the per-stage MX weight scales (EIO layout).
-template <class C>
-MI355_HD int a_wave(int wave) { return C::SPLIT ? (wave & 1) : wave; }
-template <class C>
-MI355_HD int b_wave(int wave) { return C::SPLIT ? (wave & 1) : wave; }
-template <class C>
-MI355_HD bool wave_copies_b(int wave) { return !C::SPLIT || wave >= 2; }
-template <class C>
-MI355_HD bool bs_wave(int wave) { return C::SPLIT ? wave >= 2 : wave < 2; }
 // Grouped-K MX: waves 2 and 3 copy the per-stage column scales of A (as waves 0 and 1 do for B).
 MI355_HD bool is_as_wave(int wave) { return wave >= 2; }
 // Grouped-K mode: routed rows (K) per stage - 32 bf16 rows or 64 e4m3 rows of 256 columns.
@@ -191,13 +151,8 @@ template <class C, bool MX, bool GK, class D>
 MI355_HD void issue_a(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
   const uint32_t base = (kt % C::A_SLOTS) * C::A_BYTES;
 #pragma unroll
-  for (int j = 0; j < C::A_PER; ++j) {
-    if constexpr (C::OFFS && !GK)
-      D::template copy_so<16>(cp.a_base + (int64_t)kt * C::KB, cp.ao[j], base + (a_wave<C>(wave) * C::A_PER + j) * 1024,
-                              smem, 1);
-    else
-      D::template copy<16>(a_src<C, GK, MX>(cp, j, kt), base + (a_wave<C>(wave) * C::A_PER + j) * 1024, smem, 1);
-  }
+  for (int j = 0; j < C::A_PER; ++j)
+    D::template copy<16>(a_src<C, GK, MX>(cp, j, kt), base + (wave * C::A_PER + j) * 1024, smem, 1);
   if constexpr (MX && GK)
     if (is_as_wave(wave))
       D::template copy<4>(cp.s + kt * cp.as_stage_stride, C::AS_OFF + (kt % C::A_SLOTS) * C::BS_BYTES + (wave & 1) * 256,
@@ -210,30 +165,18 @@ MI355_HD void issue_b(const CopyPlan<C>& cp, int kt, int wave, uint8_t* smem) {
   if constexpr (!GK) {
     const int64_t boff = (int64_t)kt * cp.b_stage_stride;
 #pragma unroll
-    for (int j = 0; j < C::B_PER; ++j) {
-      if constexpr (C::OFFS)
-        D::template copy_so<16>(cp.b_base + boff, cp.bo[j], base + (b_wave<C>(wave) * C::B_PER + j) * 1024, smem, 1);
-      else
-        D::template copy<16>(cp.b[j] + boff, base + (b_wave<C>(wave) * C::B_PER + j) * 1024, smem, 1);
-    }
+    for (int j = 0; j < C::B_PER; ++j) D::template copy<16>(cp.b[j] + boff, base + (wave * C::B_PER + j) * 1024, smem, 1);
   } else {
 #pragma unroll
     for (int j = 0; j < C::B_INSTR; ++j)
       D::template copy<16>(b_src<C, GK, MX>(cp, j, kt), base + (wave * C::B_INSTR + j) * 1024, smem, 1);
   }
-  if (MX && B_KN && bs_wave<C>(wave))
-    D::template copy<4>(cp.bs + kt * cp.bs_stage_stride, base + C::B_BYTES + (C::SPLIT ? (wave & 1) : wave) * 256, smem,
-                        1);
+  if (MX && B_KN && is_bs_wave(wave)) D::template copy<4>(cp.bs + kt * cp.bs_stage_stride, base + C::B_BYTES + wave * 256, smem, 1);
 }
 // MX: A scale codes of stages 8*grp .. 8*grp+7 (16 bytes per row) into AS slot grp & 1.
 template <class C, class D>
 MI355_HD void issue_as(const CopyPlan<C>& cp, int grp, int wave, uint8_t* smem) {
-  if constexpr (C::SPLIT) {  // an activation-copying wave: its two 64-row scale blocks
-    D::template copy<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 1) * 2048, smem, 1);
-    D::template copy<16>(cp.s2 + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 1) * 2048 + 1024, smem, 1);
-  } else if (wave < C::AS_WAVES) {
-    D::template copy<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + wave * 1024, smem, 1);
-  }
+  if (wave < C::AS_WAVES) D::template copy<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + wave * 1024, smem, 1);
 }
 
 // Work of one pipelined K step of a wave that computes NM 32-row subtiles: MFMAs, LDS fragment
@@ -246,35 +189,26 @@ template <class C, bool MX, int NM, bool GK = false> struct StepShape {
 };
 
 // Copy item it of iteration i (same order as issue_iteration: B copies, B scales, A copies, and in
-// grouped-K MX mode the A column scales). LB: the wave copies weights (always, unless split roles).
-template <class C, bool MX, bool B_KN, bool LA, bool GK, class D, bool LB = true>
+// grouped-K MX mode the A column scales).
+template <class C, bool MX, bool B_KN, bool LA, bool GK, class D>
 MI355_HD void issue_item(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem, int it) {
   constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
   if (it < C::B_PER) {
     const int kt = i + DB;
-    if constexpr (LB && C::OFFS && !GK)
-      D::template copy_so<16>(cp.b_base + (int64_t)kt * cp.b_stage_stride, cp.bo[it],
-                              C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + (b_wave<C>(wave) * C::B_PER + it) * 1024, smem,
-                              kt < nk);
-    else if constexpr (LB)
-      D::template copy<16>(b_src<C, GK, MX>(cp, it, kt),
-                           C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + (b_wave<C>(wave) * C::B_PER + it) * 1024, smem,
-                           kt < nk);
+    D::template copy<16>(b_src<C, GK, MX>(cp, it, kt),
+                         C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + (wave * C::B_PER + it) * 1024, smem, kt < nk);
   } else if (it == C::B_PER) {
     const int kt = i + DB;
-    if constexpr (MX && B_KN && LB)
+    if constexpr (MX && B_KN)
       D::template copy<4>(cp.bs + kt * cp.bs_stage_stride,
                           C::B_OFF + (kt % C::B_SLOTS) * C::B_SLOT + C::B_BYTES + (wave & 1) * 256, smem,
-                          bs_wave<C>(wave) && kt < nk);
+                          is_bs_wave(wave) && kt < nk);
   } else if constexpr (LA) {
     const int j = it - C::B_PER - 1;
     const int kt = i + DA;
-    if (C::OFFS && !GK) {
-      D::template copy_so<16>(cp.a_base + (int64_t)kt * C::KB, cp.ao[j],
-                              (kt % C::A_SLOTS) * C::A_BYTES + (a_wave<C>(wave) * C::A_PER + j) * 1024, smem, kt < nk);
-    } else if (!(MX && GK) || j < C::A_PER) {
+    if (!(MX && GK) || j < C::A_PER) {
       D::template copy<16>(a_src<C, GK, MX>(cp, j, kt),
-                           (kt % C::A_SLOTS) * C::A_BYTES + (a_wave<C>(wave) * C::A_PER + j) * 1024, smem, kt < nk);
+                           (kt % C::A_SLOTS) * C::A_BYTES + (wave * C::A_PER + j) * 1024, smem, kt < nk);
     } else if constexpr (MX && GK) {
       D::template copy<4>(cp.s + kt * cp.as_stage_stride,
                           C::AS_OFF + (kt % C::A_SLOTS) * C::BS_BYTES + (wave & 1) * 256, smem,
@@ -290,10 +224,7 @@ MI355_HD void issue_scales_item(const CopyPlan<C>& cp, int i, int nk, int wave, 
   if constexpr (MX && !GK) {
     const int grp = i / C::AS_GROUP + 1;
     const bool due = (i & (C::AS_GROUP - 1)) == 0 && i + C::AS_GROUP < nk;
-    if constexpr (LA && C::SPLIT) {
-      D::template copy<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 1) * 2048, smem, due);
-      D::template copy<16>(cp.s2 + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 1) * 2048 + 1024, smem, due);
-    } else if constexpr (LA) {
+    if constexpr (LA) {
       D::template copy<16>(cp.s + grp * 16, C::AS_OFF + (grp & 1) * C::AS_SLOT + (wave & 3) * 1024, smem,
                            due && wave < C::AS_WAVES);
     }
@@ -325,10 +256,10 @@ MI355_HD int younger_than(int j, int last, int nk, int la_n, int lb_n) {
   return n;
 }
 
-template <class C, bool MX, bool B_KN, bool LA, bool GK, class D, bool LB = true>
+template <class C, bool MX, bool B_KN, bool LA, bool GK, class D>
 MI355_HD void issue_iteration(const CopyPlan<C>& cp, int i, int nk, int wave, uint8_t* smem) {
   constexpr int DA = C::A_SLOTS, DB = C::B_SLOTS;
-  if (LB && i + DB < nk) issue_b<C, MX, B_KN, GK, D>(cp, i + DB, wave, smem);
+  if (i + DB < nk) issue_b<C, MX, B_KN, GK, D>(cp, i + DB, wave, smem);
   if (LA && i + DA >= 0 && i + DA < nk) {
     if (MX && !GK && i + DA == 0) issue_as<C, D>(cp, 0, wave, smem);
     issue_a<C, MX, GK, D>(cp, i + DA, wave, smem);
@@ -341,7 +272,7 @@ MI355_HD void issue_iteration(const CopyPlan<C>& cp, int i, int nk, int wave, ui
 // issue no A copies (and no A scale copies).
 template <class C>
 MI355_HD bool wave_copies_a(int wave, int rows_valid) {
-  return (!C::SPLIT || wave < 2) && a_wave<C>(wave) * (C::A_PER * 16) < rows_valid;
+  return wave * (C::A_PER * 16) < rows_valid;
 }
 
 // ---- LDS fragment reads and MFMAs ---------------------------------------------------------------

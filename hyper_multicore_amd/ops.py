@@ -414,15 +414,11 @@ def features() -> int:
 # set_gemm_variant (per thread / asyncio context), initially the MI355MOE_GG_VARIANT environment
 # variable, else "default". The library itself keeps no variant state; every call passes its own.
 _GEMM_VARIANT: contextvars.ContextVar[str | None] = contextvars.ContextVar("mi355moe_gemm_variant", default=None)
-_VARIANT_FEATURE = {"dv": _lib.FEATURE_DIRECT_GEMM, "sp": _lib.FEATURE_SPLIT_ROLES, "sp4": _lib.FEATURE_SPLIT_ROLES}
 
 
 def _check_variant(name: str) -> str:
     if name not in _lib.GEMM_VARIANT:
         raise ValueError(f"unknown GEMM variant {name!r}; expected one of {sorted(_lib.GEMM_VARIANT)}")
-    bit = _VARIANT_FEATURE.get(name, 0)
-    if bit and not features() & bit:
-        raise RuntimeError(f"GEMM variant {name!r} is switched off in this library build")
     return name
 
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MI355MOE_ABI_VERSION 6
+#define MI355MOE_ABI_VERSION 7
 
 enum {
   MI355MOE_OK_CODE = 0,
@@ -59,27 +59,22 @@ enum {
   MI355MOE_FEATURE_ROUTE_GRAD = 16,   /* mi355moe_gate_route_grad */
   MI355MOE_FEATURE_MX_WEIGHT_PREP = 32, /* mi355moe_mx_quantize_weight */
   MI355MOE_FEATURE_MX_BACKWARD = 64,  /* mi355moe_moe_backward with precision MXFP8 */
-  MI355MOE_FEATURE_DIRECT_GEMM = 128, /* grouped-GEMM configuration "dv" (MI355MOE_GEMM_DIRECT) */
-  MI355MOE_FEATURE_SPLIT_ROLES = 256, /* grouped-GEMM configurations "sp" / "sp4" (split copy roles) */
+  /* bits 128 and 256 are retired (grouped-GEMM configurations of ABI 6 and earlier) and never set */
 };
 int mi355moe_features(void);
 
 /* Grouped-GEMM configuration of a call (the gemm_variant argument of the grouped GEMMs and of
  * MI355MoeForwardArgs; a measurement control with no counterpart in the reference, whose GEMM tiling
  * is fixed by its tuning tables). The library holds no variant state: every call names its own.
- *   MI355MOE_GEMM_DEFAULT: the 8-wave 256 x 256 configuration where it applies, else the 4-wave one;
- *   MI355MOE_GEMM_PP: the 8-wave configuration where it applies (same as DEFAULT);
- *   MI355MOE_GEMM_W4: the 4-wave 256 x 256 configuration (128 x 128 wave tiles);
- *   MI355MOE_GEMM_B6: the 4-wave configuration with a sixth weight slot;
- *   MI355MOE_GEMM_DIRECT ("dv"): bf16 K-contiguous weights loaded straight into registers,
- *     activations through an 8-slot LDS ring (bf16 EOI GEMMs whose K is a whole number of 8 stages);
- *   MI355MOE_GEMM_SPLIT / _SPLIT_A4 ("sp" / "sp4"): two waves copy the activations and two the
- *     weights, 3 + 6 or 4 + 5 ring slots (MXFP8 GEMMs on EIO weight roots).
- * A GEMM outside a variant's domain runs on the default configuration. An unknown variant, or one
- * whose feature bit is clear, makes the call answer MI355MOE_EUNSUPPORTED. The expert backward
- * always uses the default. */
-enum { MI355MOE_GEMM_DEFAULT = 0, MI355MOE_GEMM_B6 = 1, MI355MOE_GEMM_DIRECT = 2, MI355MOE_GEMM_SPLIT = 3,
-       MI355MOE_GEMM_SPLIT_A4 = 4, MI355MOE_GEMM_PP = 5, MI355MOE_GEMM_W4 = 6 };
+ *   MI355MOE_GEMM_DEFAULT: the 8-wave 256 x 256 configuration where it applies, except that GEMMs
+ *     whose groups average at most 32 rows (decode shapes) run on the 64-row tiles; else the 4-wave
+ *     one;
+ *   MI355MOE_GEMM_PP: the 8-wave configuration where it applies, also for decode shapes (so the MX
+ *     forward keeps the stage-major activation scales there); else the 4-wave one;
+ *   MI355MOE_GEMM_W4: the 4-wave 256 x 256 configuration (128 x 128 wave tiles).
+ * Values 1-4 named configurations of ABI 6 and earlier; they, and any other value, make the call
+ * answer MI355MOE_EUNSUPPORTED. The expert backward always uses the default. */
+enum { MI355MOE_GEMM_DEFAULT = 0, MI355MOE_GEMM_PP = 5, MI355MOE_GEMM_W4 = 6 };
 
 /* ---------------------------------------------------------------------------------------------
  * Router projection: logits[t, e] = sum_h x[t, h] * w[e, h], bf16 inputs, fp32 accumulate and

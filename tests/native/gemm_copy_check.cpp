@@ -35,7 +35,7 @@
 #include <string>
 #include <vector>
 
-#include "../../hyper_multicore_amd/csrc/gemm_direct_plan.h"
+#include "../../hyper_multicore_amd/csrc/gemm_plan.h"
 #include "../../include/mi355moe.h"
 
 // ------------------------------------------------------------------------------------------------
@@ -52,11 +52,8 @@ static std::string g_scenario;
 // the decode tiles switched off): planning and launch both follow it.
 static bool g_force_big = false;
 // The forward tile-configuration variant the scenario passes through the C ABI (gemm_variant
-// argument / MI355MoeForwardArgs::gemm_variant; gemm_var.hip builds the variants).
+// argument / MI355MoeForwardArgs::gemm_variant).
 static int g_variant = 0;
-using GGB6 = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0>;  // gemm_var.hip
-using GGSplit = GGCfg<256, 2, 3, 6, 1024, 1, 2, 0, true>;   // gemm_var.hip (sp)
-using GGSplitA4 = GGCfg<256, 2, 4, 5, 1024, 1, 2, 0, true>; // gemm_var.hip (sp4)
 
 #define CHECK_FAIL(...)                                         \
   do {                                                          \
@@ -362,10 +359,6 @@ struct CheckDma {
     if (!enable) return;
     g_rec->push_back({(const uint8_t*)g, SZ, off, g_iter});
   }
-  template <int SZ>
-  static void copy_so(const uint8_t* base, uint32_t voff, uint32_t off, uint8_t* smem, int enable) {
-    copy<SZ>(base + voff, off, smem, enable);
-  }
 };
 
 // R_ASS: grouped-K MX only - the per-stage column scales of A, A_SLOTS slots of 512 bytes at AS_OFF
@@ -378,7 +371,7 @@ static const char* region_name(int r) {
 // One lane's copy sequence of one work item, replayed in the K loop's order (k_loop in gemm.hip:
 // prologue, the wait for stage 0, then for every pipelined step k the wait for stage k + 1 and the
 // copy items of the step).
-template <class C, bool MX, bool B_KN, bool LA, bool GK, bool LB = true>
+template <class C, bool MX, bool B_KN, bool LA, bool GK>
 static void record_schedule(const CopyPlan<C>& cp, int nk, int wave, std::vector<Rec>& rec, std::vector<Wait>& waits) {
   uint8_t* smem = nullptr;
   g_rec = &rec;
@@ -391,7 +384,7 @@ static void record_schedule(const CopyPlan<C>& cp, int nk, int wave, std::vector
       waits.push_back({rec.size(), k + 1, younger_than<C, LA>(k + 1, k - 1, nk, la_n, lb_n)});
       g_iter = k;
       for (int it = 0; it < StepShape<C, MX, 1, GK>::ITEMS; ++it)
-        issue_item<C, MX, B_KN, LA, GK, D, LB>(cp, k, nk, wave, smem, it);
+        issue_item<C, MX, B_KN, LA, GK, D>(cp, k, nk, wave, smem, it);
       issue_scales_item<C, MX, B_KN, LA, D, GK>(cp, k, nk, wave, smem);
     }
   }
@@ -543,7 +536,7 @@ template <class C, bool MX, bool B_KN, bool SWIGLU, bool GK>
 static void check_lane(const GGParams& p, const Layout& L, ItemCtx& it, int wave, int lane, bool la,
                        const std::vector<Rec>& rec, const std::vector<Wait>& waits) {
   const int slots[R_N] = {C::A_SLOTS, C::B_SLOTS, C::B_SLOTS, 2, 2, C::A_SLOTS};
-  const int per_fill[R_N] = {C::A_PER, C::B_PER, 1, C::SPLIT ? 2 : 1, 1, 1};
+  const int per_fill[R_N] = {C::A_PER, C::B_PER, 1, 1, 1, 1};
   int fills[R_N][8] = {};
   std::vector<Decoded> dec(rec.size());
   for (size_t i = 0; i < rec.size(); ++i) {
@@ -822,23 +815,19 @@ struct FillDma {
     if (!enable) return;
     memcpy(smem + off + (uint32_t)SZ * g_fill_lane, g, SZ);
   }
-  template <int SZ>
-  static void copy_so(const uint8_t* base, uint32_t voff, uint32_t off, uint8_t* smem, int enable) {
-    copy<SZ>(base + voff, off, smem, enable);
-  }
 };
 
-template <class C, bool MX, bool B_KN, bool LA, bool GK, bool LB = true>
+template <class C, bool MX, bool B_KN, bool LA, bool GK>
 static void fill_prologue(const CopyPlan<C>& cp, int nk, int wave, uint8_t* smem) {
   using D = FillDma;
 #include "../../hyper_multicore_amd/csrc/gemm_kloop_prologue.inc"
   (void)la_n;
   (void)lb_n;
 }
-template <class C, bool MX, bool B_KN, bool LA, bool GK, bool LB = true>
+template <class C, bool MX, bool B_KN, bool LA, bool GK>
 static void fill_step(const CopyPlan<C>& cp, int k, int nk, int wave, uint8_t* smem) {
   for (int it = 0; it < StepShape<C, MX, 1, GK>::ITEMS; ++it)
-    issue_item<C, MX, B_KN, LA, GK, FillDma, LB>(cp, k, nk, wave, smem, it);
+    issue_item<C, MX, B_KN, LA, GK, FillDma>(cp, k, nk, wave, smem, it);
   issue_scales_item<C, MX, B_KN, LA, FillDma, GK>(cp, k, nk, wave, smem);
 }
 
@@ -936,11 +925,8 @@ static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la
   for (int w = 0; w < C::WAVES; ++w)
     for (int l = 0; l < 64; ++l) {
       g_fill_lane = l;
-      const bool lb = wave_copies_b<C>(w);
-      if (la[w] && lb) fill_prologue<C, MX, B_KN, true, GK>(cps[w][l], nk, w, smem);
-      else if (la[w]) fill_prologue<C, MX, B_KN, true, GK, false>(cps[w][l], nk, w, smem);
-      else if (lb) fill_prologue<C, MX, B_KN, false, GK>(cps[w][l], nk, w, smem);
-      else fill_prologue<C, MX, B_KN, false, GK, false>(cps[w][l], nk, w, smem);
+      if (la[w]) fill_prologue<C, MX, B_KN, true, GK>(cps[w][l], nk, w, smem);
+      else fill_prologue<C, MX, B_KN, false, GK>(cps[w][l], nk, w, smem);
     }
   for (int w = 0; w < C::WAVES; ++w)
     emu_wave_step<C, MX, B_KN, GK>(tiles[w], nm[w], smem, nk, w / C::WGN, w % C::WGN, -1);
@@ -951,11 +937,8 @@ static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la
       for (int w = 0; w < C::WAVES; ++w)
         for (int l = 0; l < 64; ++l) {
           g_fill_lane = l;
-          const bool lb = wave_copies_b<C>(w);
-          if (la[w] && lb) fill_step<C, MX, B_KN, true, GK>(cps[w][l], k, nk, w, smem);
-          else if (la[w]) fill_step<C, MX, B_KN, true, GK, false>(cps[w][l], k, nk, w, smem);
-          else if (lb) fill_step<C, MX, B_KN, false, GK>(cps[w][l], k, nk, w, smem);
-          else fill_step<C, MX, B_KN, false, GK, false>(cps[w][l], k, nk, w, smem);
+          if (la[w]) fill_step<C, MX, B_KN, true, GK>(cps[w][l], k, nk, w, smem);
+          else fill_step<C, MX, B_KN, false, GK>(cps[w][l], k, nk, w, smem);
         }
   }
   // compare the accumulators with the reference
@@ -1036,7 +1019,6 @@ static int sim_forward(const GGParams& p) {
     for (int wave = 0; wave < C::WAVES; ++wave)
       for (int lane = 0; lane < 64; ++lane) {
         const int L = L_item;
-        const bool copy_role_a = !C::SPLIT || wave < 2, copy_role_b = !C::SPLIT || wave >= 2;
 #include "../../hyper_multicore_amd/csrc/gemm_item_fwd.inc"
         cps[wave][lane] = cp;
         (void)mt;
@@ -1087,14 +1069,11 @@ static int sim_forward(const GGParams& p) {
           }
         }
         const bool la = wave_copies_a<C>(wave, rows_valid);
-        const bool lb = wave_copies_b<C>(wave);
         las[wave] = la;
         rec.clear();
         waits.clear();
-        if (la && lb) record_schedule<C, MX, B_KN, true, false>(cp, nk, wave, rec, waits);
-        else if (la) record_schedule<C, MX, B_KN, true, false, false>(cp, nk, wave, rec, waits);
-        else if (lb) record_schedule<C, MX, B_KN, false, false>(cp, nk, wave, rec, waits);
-        else record_schedule<C, MX, B_KN, false, false, false>(cp, nk, wave, rec, waits);
+        if (la) record_schedule<C, MX, B_KN, true, false>(cp, nk, wave, rec, waits);
+        else record_schedule<C, MX, B_KN, false, false>(cp, nk, wave, rec, waits);
         check_lane<C, MX, B_KN, SWIGLU, false>(p, lay, ctx, wave, lane, la, rec, waits);
       }
     check_coverage<C, MX, B_KN, false>(ctx);
@@ -1237,366 +1216,6 @@ static int sim_wgrad(const GGParams& p) {
   return MI355MOE_OK;
 }
 
-// ------------------------------------------------------------------------------------------------
-// Direct-weight configuration (gemm_direct.hip, variant "dv"): weight fragments loaded into a register
-// ring, activations through an LDS ring. For every work item, wave and lane the issue order of
-// direct_k_loop is replayed through the same plan and issue functions (gemm_direct_plan.h) with a
-// recorder as the memory policy, and checked for: every source inside a live allocation; weight and
-// activation sources equal to the elements the MFMA operand layout and the LDS fragment reads expect
-// (from the C-ABI shapes); each wait (the runtime count and, where the kernel uses it, the
-// compile-time count the kernel uses) covering the loads its step reads; ring slots and scale slots refilled
-// only after their previous stage was consumed. With g_emulate the data path runs too: the loads land
-// in emulated registers and LDS, the kernel's direct_read_a / direct_mfma run through the MFMA model,
-// and the accumulators are compared with the reference GEMM.
-struct DLoad {
-  int kind;   // 0 weight fragment, 1 activation copy, 2 activation-scale group, 3 weight-scale group
-  int index;  // stage (kinds 0, 1) or scale group (kinds 2, 3)
-  int item;   // copy item (kinds 0, 1)
-  int step;   // issuing step (prologue steps negative; scale group 0 before them: -D)
-};
-static std::vector<DLoad>* g_dlist = nullptr;
-static DLoad g_dcur;
-static int g_dlane = 0;
-struct DirectRecMem {
-  static void load(v4i& dst, const uint8_t* base, uint32_t off, int en) {
-    memset(&dst, 0, sizeof(dst));
-    if (!en) CHECK_FAIL("direct: the kernel would load a missing stage (kind %d, %d)", g_dcur.kind, g_dcur.index);
-    ++g_copies;
-    if (!find_alloc(base + off, 16)) CHECK_FAIL("direct: load (kind %d, %d) of lane %d outside every allocation", g_dcur.kind, g_dcur.index, g_dlane);
-    DLoad r = g_dcur;
-    if (r.kind == 2) r.kind = 3;  // a register load of a scale group: the weight scales
-    if (g_dlist) g_dlist->push_back(r);
-  }
-  static void lds(const uint8_t* base, uint32_t off, uint8_t*, uint32_t lds_off, int en) {
-    if (!en) CHECK_FAIL("direct: the kernel would copy a missing stage (kind %d, %d)", g_dcur.kind, g_dcur.index);
-    ++g_copies;
-    if (!find_alloc(base + off, 16)) CHECK_FAIL("direct: LDS copy (kind %d, %d) of lane %d outside every allocation", g_dcur.kind, g_dcur.index, g_dlane);
-    if (lds_off + 16 * 64 > (uint32_t)GGDirect::PREFIX_OFF) CHECK_FAIL("direct: LDS copy at %u past the rings", lds_off);
-    if (g_dlist) g_dlist->push_back(g_dcur);
-  }
-};
-// The emulated data path: loads land at once.
-struct DirectEmuMem {
-  static void load(v4i& dst, const uint8_t* base, uint32_t off, int en) {
-    if (en) memcpy(&dst, base + off, 16);
-  }
-  static void lds(const uint8_t* base, uint32_t off, uint8_t* smem, uint32_t lds_off, int en) {
-    if (en) memcpy(smem + lds_off + 16 * g_dlane, base + off, 16);
-  }
-};
-
-// Replays direct_k_loop's issue order for one lane (M: memory policy); `on_wait(k)` runs at the wait
-// before step k (k = -1: before the prologue's read of stage 0).
-template <bool MX, class M, class W>
-static void direct_schedule(const DirectPlan& d, int nk, int wave, uint8_t* smem, v4i (&ring)[GGDirect::D][GGDirect::B_LOADS],
-                            v4i (&bs)[GGDirect::NI], W on_wait) {
-  using C = GGDirect;
-  if (MX) {
-    g_dcur = {2, 0, 0, -C::D};
-    direct_issue_scales<M>(d, 0, 1, wave, smem, bs);
-  }
-  for (int s = 0; s < C::D - 1; ++s)
-    for (int it = 0; it < C::B_LOADS + C::A_INSTR; ++it) {
-      g_dcur = {it < C::B_LOADS ? 0 : 1, s, it, s - (C::D - 1)};
-      direct_issue<M>(d, s - (C::D - 1), nk, wave, smem, ring[s], it);
-    }
-  on_wait(-1);
-  for (int k = 0; k < nk; ++k) {
-    const int P = k % C::D;
-    const bool last = (k - P) + C::D >= nk;  // the last turn of the ring (the kernel's LAST)
-    on_wait(k);
-    if (MX && P == 0 && !last) {
-      g_dcur = {2, k / 8 + 1, 0, k};
-      direct_issue_scales<M>(d, k / 8 + 1, 1, wave, smem, bs);
-    }
-    if (!last || P == 0)
-      for (int it = 0; it < C::B_LOADS + C::A_INSTR; ++it) {
-        g_dcur = {it < C::B_LOADS ? 0 : 1, k + C::D - 1, it, k};
-        direct_issue<M>(d, k, nk, wave, smem, ring[(P + C::D - 1) % C::D], it);
-      }
-  }
-}
-
-// The kernel's compile-time wait of step k (k = -1: before the prologue's read of stage 0).
-template <bool MX, bool LAST>
-static int direct_fixed_wait_at(int P) {
-  switch (P) {
-    case 0: return direct_wait_fixed<MX, 0, LAST>();
-    case 1: return direct_wait_fixed<MX, 1, LAST>();
-    case 2: return direct_wait_fixed<MX, 2, LAST>();
-    case 3: return direct_wait_fixed<MX, 3, LAST>();
-    case 4: return direct_wait_fixed<MX, 4, LAST>();
-    case 5: return direct_wait_fixed<MX, 5, LAST>();
-    case 6: return direct_wait_fixed<MX, 6, LAST>();
-    default: return direct_wait_fixed<MX, 7, LAST>();
-  }
-}
-template <bool MX>
-static int direct_kernel_wait(int k, int nk) {
-  if (k < 0) return direct_wait_first();
-  const bool last = (k - k % GGDirect::D) + GGDirect::D >= nk;
-  return last ? direct_fixed_wait_at<MX, true>(k % GGDirect::D) : direct_fixed_wait_at<MX, false>(k % GGDirect::D);
-}
-
-template <bool MX, int EPI>
-static int sim_direct(const GGParams& p) {
-  using C = GGDirect;
-  constexpr bool B_KN = false;
-  constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX || EPI == EPI_SWIGLU_BF16_NUM);
-  constexpr int ESIZE = MX ? 1 : 2;
-  ++g_gemms;
-  if (!find_alloc(p.tile_prefix, (size_t)(p.G + 1) * 4)) CHECK_FAIL("tile prefix outside its buffer");
-  const int32_t* prefix = p.tile_prefix;
-  const int splits = 1;
-  const int total = prefix[p.G] * p.n_tiles;
-  const int nk = p.K * ESIZE / C::KB;
-  if (nk % C::D != 0 || nk < C::D) CHECK_FAIL("direct: %d stages, not a multiple of %d", nk, C::D);
-  if (p.a_bytes <= 0 || !find_alloc(p.A, (size_t)p.a_bytes)) CHECK_FAIL("direct: a_bytes %lld does not match A's allocation", (long long)p.a_bytes);
-  Layout lay;
-  if (g_expect.set)
-    lay = {g_expect.A, g_expect.a_row_bytes, p.a_row_index, p.a_row_div, g_expect.a_scale, g_expect.a_scale_ld,
-           g_expect.B, true, p.K, p.Ntot, ESIZE, g_expect.b_scale, g_expect.b_scale_ld};
-  else
-    lay = {p.A, p.lda_bytes, p.a_row_index, p.a_row_div, p.a_scale, p.a_scale_ld, p.B, true, p.K, p.Ntot, ESIZE,
-           p.b_scale, p.b_scale_ld};
-  static DirectPlan plans[C::WAVES][64];
-  for (int L_item = 0; L_item < total; ++L_item) {
-    int item_g = 0, item_nt = 0, item_rows = 0;
-    int64_t item_row0 = 0;
-    for (int wave = 0; wave < C::WAVES; ++wave)
-      for (int lane = 0; lane < 64; ++lane) {
-        const int L = L_item;
-        constexpr bool copy_role_a = true, copy_role_b = true;
-        constexpr int tail_from = INT32_MAX;
-#include "../../hyper_multicore_amd/csrc/gemm_item_fwd.inc"
-        (void)cp;
-        (void)half;
-        (void)mt;
-        (void)split;
-        item_g = g;
-        item_nt = nt;
-        item_rows = rows_valid;
-        item_row0 = tile_row0;
-        plans[wave][lane] = direct_plan(p, g, nt, tile_row0, rows_valid, SWIGLU, MX, wave, lane);
-      }
-    ++g_items;
-    const int g = item_g, nt = item_nt, rows_valid = item_rows;
-    const int64_t tile_row0 = item_row0;
-    if (rows_valid < 1 || rows_valid > C::BM) CHECK_FAIL("item %d: %d valid rows", L_item, rows_valid);
-    // epilogue output range
-    {
-      const int64_t r0 = tile_row0, r1 = tile_row0 + rows_valid - 1;
-      if (EPI == EPI_STORE_BF16) {
-        const int64_t cols = std::min<int64_t>(C::BN, p.N - (int64_t)nt * C::BN);
-        check_range(p.C, (r0 * p.ldc + (int64_t)nt * C::BN) * 2, (r1 * p.ldc + (int64_t)nt * C::BN + cols) * 2, "bf16 epilogue");
-      } else if (EPI == EPI_SWIGLU_MX) {
-        check_range(p.C, r0 * p.ldc + (int64_t)nt * (C::BN / 2), r1 * p.ldc + (int64_t)nt * (C::BN / 2) + C::BN / 2, "MX SwiGLU epilogue");
-        check_range(p.c_scale, r0 * p.c_scale_ld + nt * 4, r1 * p.c_scale_ld + nt * 4 + 4, "MX SwiGLU scales");
-      } else {
-        check_range(p.C, (r0 * p.ldc + (int64_t)nt * (C::BN / 2)) * 2, (r1 * p.ldc + (int64_t)nt * (C::BN / 2) + C::BN / 2) * 2,
-                    "SwiGLU epilogue");
-      }
-    }
-    // issue order, sources and waits
-    for (int wave = 0; wave < C::WAVES; ++wave)
-      for (int lane = 0; lane < 64; ++lane) {
-        const DirectPlan& d = plans[wave][lane];
-        // expected sources (independent of the plan): weight column of subtile q, activation chunk
-        for (int q = 0; q < C::NI; ++q) {
-          int64_t wc;
-          const bool live = tile_weight_col<C>(wave * C::WN + q * 32 + lane % 32, nt, p.N, SWIGLU, p.gate_up_interleaved, &wc);
-          if (!live) continue;
-          for (int s = 0; s < nk; s += std::max(1, nk / 4))
-            for (int h = 0; h < 2; ++h) {
-              const uint8_t* got = d.b_base + (int64_t)s * C::KB + h * 32 + d.b[q];
-              const uint8_t* want = lay.b_at(g, ((int64_t)s * C::KB + h * 32 + 16 * (lane / 32)) / ESIZE, wc);
-              if (got != want) CHECK_FAIL("direct: weight load (q %d, stage %d, half %d) of wave %d lane %d reads the wrong element", q, s, h, wave, lane);
-            }
-          if (MX)
-            for (int grp = 0; grp * 8 < nk; ++grp)
-              if (d.bs_base + grp * 16 + d.bs[q] != lay.bs_row_at(g, wc, grp * 16))
-                CHECK_FAIL("direct: weight scales (q %d, group %d) of wave %d lane %d", q, grp, wave, lane);
-        }
-        for (int j = 0; j < C::A_INSTR; ++j) {
-          const int L16 = (wave * C::A_INSTR + j) * 64 + lane, r = L16 / 4, cs = L16 % 4;
-          if (r >= rows_valid) continue;
-          const int c = cs ^ ((r >> 2) & 3);  // the chunk a_chunk_off places at LDS position cs of row r
-          for (int s = 0; s < nk; s += std::max(1, nk / 4))
-            if (d.a_base + (int64_t)s * C::KB + d.a[j] != lay.a_at(tile_row0 + r, (int64_t)s * C::KB + c * 16))
-              CHECK_FAIL("direct: activation copy %d (stage %d) of wave %d lane %d reads the wrong chunk", j, s, wave, lane);
-        }
-        if (MX && wave * 64 + lane < rows_valid)
-          for (int grp = 0; grp * 8 < nk; ++grp)
-            if (d.as_base + grp * 16 + d.as != lay.as_at(tile_row0 + wave * 64 + lane, grp * 16))
-              CHECK_FAIL("direct: activation scales (group %d) of wave %d lane %d", grp, wave, lane);
-        // the recorded schedule of this lane
-        std::vector<DLoad> list;
-        g_dlist = &list;
-        g_dlane = lane;
-        v4i ring[C::D][C::B_LOADS], bs[C::NI];
-        std::vector<std::pair<int, size_t>> waits;  // (step, loads issued before the wait)
-        direct_schedule<MX, DirectRecMem>(d, nk, wave, nullptr, ring, bs, [&](int k) { waits.push_back({k, list.size()}); });
-        g_dlist = nullptr;
-        if (lane != 0) continue;  // the schedule is the same for every lane of a wave
-        for (const auto& w : waits) {
-          const int k = w.first;
-          const size_t issued = w.second;
-          const int n = direct_kernel_wait<MX>(k, nk);
-          if (n != direct_wait<MX>(k, nk))
-            CHECK_FAIL("direct: the kernel's wait before step %d (position %d) is %d, the schedule's count is %d", k,
-                       k % C::D, n, direct_wait<MX>(k, nk));
-          if (n < 0 || n > 63) CHECK_FAIL("direct: wait count %d of step %d outside vmcnt's range", n, k);
-          for (size_t i = 0; i < issued; ++i) {
-            const DLoad& l = list[i];
-            bool need = false;
-            if (k < 0) need = (l.kind == 1 && l.index == 0) || (l.kind == 2 && l.index == 0);
-            else {
-              need = (l.kind == 0 && l.index == k) || (l.kind == 1 && l.index == k + 1) ||
-                     (l.kind == 2 && l.index == (k + 1) / 8 && k + 1 < nk) || (l.kind == 3 && l.index == k / 8);
-            }
-            if (need && issued - 1 - i < (size_t)n)
-              CHECK_FAIL("direct: the wait before step %d (vmcnt %d after %zu loads) leaves load %zu (kind %d, %d) of wave %d in flight",
-                         k, n, issued, i, l.kind, l.index, wave);
-          }
-          // every stage / group the step reads was issued before the wait
-          if (k >= 0) {
-            int have_b = 0, have_a = 0;
-            for (size_t i = 0; i < issued; ++i) {
-              have_b += list[i].kind == 0 && list[i].index == k;
-              have_a += list[i].kind == 1 && list[i].index == k + 1;
-            }
-            if (have_b != C::B_LOADS || (k + 1 < nk && have_a != C::A_INSTR))
-              CHECK_FAIL("direct: before step %d wave %d has %d weight loads of the stage and %d activation copies of the next", k, wave, have_b, have_a);
-          }
-        }
-        // slot reuse: a ring / LDS slot is refilled only after the stage it held was consumed
-        for (const DLoad& l : list) {
-          if (l.kind == 0 && !(l.step > l.index - C::D && l.step < l.index))
-            CHECK_FAIL("direct: weight stage %d loaded at step %d (ring slot reuse)", l.index, l.step);
-          if (l.kind == 1 && !(l.step > l.index - C::D && l.step < l.index))
-            CHECK_FAIL("direct: activation stage %d copied at step %d (LDS slot reuse)", l.index, l.step);
-          if (l.kind == 2 && l.index > 0 && !(l.step >= 8 * (l.index - 2) + 7 && l.step < 8 * l.index))
-            CHECK_FAIL("direct: scale group %d fetched at step %d (scale slot reuse)", l.index, l.step);
-          if (l.kind == 3 && l.index > 0 && l.step != 8 * (l.index - 1))
-            CHECK_FAIL("direct: weight scale group %d loaded at step %d (register reuse)", l.index, l.step);
-        }
-      }
-    if (g_emulate) {
-      // functional emulation of the work item
-      std::vector<uint8_t> lds(C::TOTAL, 0);
-      uint8_t* smem = lds.data();
-      const int nmi = rows_valid > 128 ? 8 : rows_valid > 64 ? 4 : rows_valid > 32 ? 2 : 1;
-      struct WaveState {
-        v4i ring[64][C::D][C::B_LOADS];
-        v4i bs_cur[64][C::NI], bs_nxt[64][C::NI];
-        DirectFrags<MX> f[64];
-        v16f acc[64][C::MI][C::NI];
-      };
-      auto ws = std::make_unique<WaveState[]>(C::WAVES);
-      for (int w = 0; w < C::WAVES; ++w)
-        for (int l = 0; l < 64; ++l)
-          for (int i = 0; i < C::MI; ++i)
-            for (int j = 0; j < C::NI; ++j)
-              for (int r = 0; r < 16; ++r) ws[w].acc[l][i][j][r] = 0.0f;
-      // prologue
-      for (int w = 0; w < C::WAVES; ++w)
-        for (int l = 0; l < 64; ++l) {
-          g_dlane = l;
-          const DirectPlan& d = plans[w][l];
-          if (MX) direct_issue_scales<DirectEmuMem>(d, 0, 1, w, smem, ws[w].bs_nxt[l]);
-          for (int s = 0; s < C::D - 1; ++s)
-            for (int it = 0; it < C::B_LOADS + C::A_INSTR; ++it)
-              direct_issue<DirectEmuMem>(d, s - (C::D - 1), nk, w, smem, ws[w].ring[l][s], it);
-        }
-      for (int w = 0; w < C::WAVES; ++w)
-        for (int l = 0; l < 64; ++l)
-          for (int mi = 0; mi < nmi; ++mi) direct_read_a<MX, EmuOps>(ws[w].f[l], mi, smem, smem + C::AS_OFF, l);
-      for (int k = 0; k < nk; ++k) {
-        const int P = k % C::D;
-        const int PN = (P + 1) % C::D;
-        const uint8_t* As = smem + PN * C::A_BYTES;
-        const uint8_t* ASs = smem + C::AS_OFF + (((k + 1) / C::AS_GROUP) & 1) * C::AS_SLOT + PN * 2;
-        const bool last = (k - P) + C::D >= nk;
-        if (MX && P == 0)
-          for (int w = 0; w < C::WAVES; ++w)
-            for (int l = 0; l < 64; ++l) {
-              g_dlane = l;
-              for (int q = 0; q < C::NI; ++q) ws[w].bs_cur[l][q] = ws[w].bs_nxt[l][q];
-              if (!last) direct_issue_scales<DirectEmuMem>(plans[w][l], k / 8 + 1, 1, w, smem, ws[w].bs_nxt[l]);
-            }
-        for (int mi = 0; mi < C::MI; ++mi)
-          for (int w = 0; w < C::WAVES; ++w) {
-            if (mi < nmi) {
-              for (int t = 0; t < direct_mfmas<MX>(); ++t) {
-                for (int l = 0; l < 64; ++l) {
-                  g_emu.lane = l;
-                  direct_mfma<MX, EmuOps>(ws[w].f[l], mi, t, ws[w].ring[l][P], ws[w].bs_cur[l], P, l, ws[w].acc[l]);
-                }
-                emu_resolve_mfma(MX);
-              }
-              for (int l = 0; l < 64; ++l) direct_read_a<MX, EmuOps>(ws[w].f[l], mi, As, ASs, l);
-            }
-            if (!last || P == 0)
-              for (int l = 0; l < 64; ++l) {
-                g_dlane = l;
-                direct_issue<DirectEmuMem>(plans[w][l], k, nk, w, smem, ws[w].ring[l][(P + C::D - 1) % C::D], mi);
-              }
-          }
-      }
-      double max_ref = 0.0, max_err = 0.0;
-      int bad_row = -1, bad_col = -1;
-      double bad_got = 0.0, bad_want = 0.0;
-      for (int w = 0; w < C::WAVES; ++w)
-        for (int l = 0; l < 64; ++l)
-          for (int i = 0; i < nmi; ++i)
-            for (int j = 0; j < C::NI; ++j)
-              for (int r = 0; r < 16; ++r) {
-                const int row = i * 32 + 8 * (r / 4) + 4 * (l / 32) + r % 4;
-                const int col = w * C::WN + j * 32 + l % 32;
-                int64_t wc;
-                if (row >= rows_valid || !tile_weight_col<C>(col, nt, p.N, SWIGLU, p.gate_up_interleaved, &wc)) continue;
-                double want = 0.0;
-                for (int64_t kk = 0; kk < p.K; ++kk) {
-                  double av, bv;
-                  if (!MX) {
-                    uint16_t a16, b16;
-                    memcpy(&a16, lay.a_at(tile_row0 + row, 2 * kk), 2);
-                    memcpy(&b16, lay.b_at(g, kk, wc), 2);
-                    av = bf16f(a16);
-                    bv = bf16f(b16);
-                  } else {
-                    av = e4m3f(*lay.a_at(tile_row0 + row, kk)) * e8m0f(*lay.as_at(tile_row0 + row, kk / 32));
-                    bv = e4m3f(*lay.b_at(g, kk, wc)) * e8m0f(*lay.bs_row_at(g, wc, kk / 32));
-                  }
-                  want += av * bv;
-                }
-                const double got = ws[w].acc[l][i][j][r];
-                max_ref = std::max(max_ref, std::fabs(want));
-                const double err = std::fabs(got - want);
-                if (!(err <= max_err)) {
-                  max_err = err;
-                  bad_row = row;
-                  bad_col = col;
-                  bad_got = got;
-                  bad_want = want;
-                }
-              }
-      ++g_emulated_items;
-      if (!(max_err <= 1e-4 * std::max(max_ref, 1e-30)))
-        CHECK_FAIL("direct item: emulated tile differs from the reference GEMM: max |err| %.3g (max |ref| %.3g) at tile "
-                   "(%d, %d): %.6g vs %.6g", max_err, max_ref, bad_row, bad_col, bad_got, bad_want);
-    }
-  }
-  return MI355MOE_OK;
-}
-
-static int sim_direct_dispatch(const GGParams& p, bool mx, bool b_kn, int epi) {
-  if (!direct_supported(p, mx, b_kn, epi)) return MI355MOE_EUNSUPPORTED;
-  if (!mx) return epi == EPI_STORE_BF16 ? sim_direct<false, EPI_STORE_BF16>(p) : sim_direct<false, EPI_SWIGLU_BF16>(p);
-  return epi == EPI_STORE_BF16 ? sim_direct<true, EPI_STORE_BF16>(p) : sim_direct<true, EPI_SWIGLU_MX>(p);
-}
-static long g_direct_gemms = 0;
-static long g_split_gemms = 0;
 
 // The grouped GEMM entry points the host code calls, run on the host
 template <class C>
@@ -1648,28 +1267,6 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   if (epi == EPI_SWIGLU_BF16 && (p.swiglu_limit > 0.0f || p.row_prob != nullptr)) epi = EPI_SWIGLU_BF16_NUM;
   if (g_force_big) small = false;
   if (small) return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
-  if (p.variant == MI355_GG_VARIANT_B6) {
-    const int rc = sim_dispatch<GGB6>(p, mx, b_kn, epi);
-    if (rc != MI355MOE_EUNSUPPORTED) return rc;
-  }
-  if ((p.variant == MI355_GG_VARIANT_SP || p.variant == MI355_GG_VARIANT_SP4) && gg_split_applies(p, mx, b_kn, epi)) {
-    ++g_split_gemms;
-    const bool sp = p.variant == MI355_GG_VARIANT_SP;
-    if (mx && epi == EPI_SWIGLU_MX)
-      return sp ? sim_forward<GGSplit, true, true, EPI_SWIGLU_MX>(p) : sim_forward<GGSplitA4, true, true, EPI_SWIGLU_MX>(p);
-    if (mx) return sp ? sim_forward<GGSplit, true, true, EPI_STORE_BF16>(p) : sim_forward<GGSplitA4, true, true, EPI_STORE_BF16>(p);
-    if (epi == EPI_SWIGLU_BF16)
-      return sp ? sim_forward<GGSplit, false, true, EPI_SWIGLU_BF16>(p)
-                : sim_forward<GGSplitA4, false, true, EPI_SWIGLU_BF16>(p);
-    return sp ? sim_forward<GGSplit, false, true, EPI_STORE_BF16>(p) : sim_forward<GGSplitA4, false, true, EPI_STORE_BF16>(p);
-  }
-  if (p.variant == MI355_GG_VARIANT_DV) {
-    const int rc = sim_direct_dispatch(p, mx, b_kn, epi);
-    if (rc != MI355MOE_EUNSUPPORTED) {
-      ++g_direct_gemms;
-      return rc;
-    }
-  }
   return sim_dispatch<GGBig>(p, mx, b_kn, epi);
 }
 int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t, bool mx) {
@@ -2036,82 +1633,6 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_moe_mx_decode_halves", halves(emu([=] { moe_forward(16, 4, 16, 512, 256, MX, L_EIO, 0.0); }))});
   s.push_back({"emu_moe_bf16_decode_halves", halves(emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EIO, 0.0); }))});
   s.push_back({"emu_moe_mx_gu_decode_halves", halves(emu([=] { moe_forward(16, 4, 16, 512, 256, MX, L_GU, 0.0); }))});
-  auto b6 = [](std::function<void()> f) {
-    return [f] {
-      g_variant = MI355_GG_VARIANT_B6;
-      f();
-      g_variant = 0;
-    };
-  };
-  s.push_back({"emu_b6_bf16_eio", b6(emu([=] { gemm_bf16({70, 0, 129, 300}, 512, 512, L_EIO); }))});
-  s.push_back({"emu_b6_bf16_eoi", b6(emu([=] { gemm_bf16({70, 0, 129, 300}, 512, 512, L_EOI); }))});
-  s.push_back({"emu_b6_mx_eio", b6(emu([=] { gemm_mx({70, 0, 129, 300}, 1024, 256, L_EIO); }))});
-  s.push_back({"b6_moe_bf16", b6([=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
-  s.push_back({"b6_moe_mx_eio", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
-  s.push_back({"b6_moe_mx_gu", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); })});
-  s.push_back({"b6_moe_mx_eoi", b6([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EOI, 0.0); })});
-  // split copy roles (variants sp: 3 activation / 6 weight slots; sp4: 4 / 5), MXFP8 EIO; each scenario
-  // must run them
-  auto sp = [](int v, std::function<void()> f) {
-    return [v, f] {
-      const long before = g_split_gemms;
-      g_variant = v;
-      f();
-      g_variant = 0;
-      if (g_split_gemms == before) CHECK_FAIL("the split-role configuration ran no GEMM");
-    };
-  };
-  const int SP = MI355_GG_VARIANT_SP, SP4 = MI355_GG_VARIANT_SP4;
-  s.push_back({"sp_gemm_mx_eio", sp(SP, [=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EIO); })});
-  s.push_back({"sp_gemm_mx_eio_long_k", sp(SP, [=] { gemm_mx({256, 256}, 2560, 272, L_EIO); })});
-  s.push_back({"sp_gemm_mx_eio_decode_big", big(sp(SP, [=] { gemm_mx(decode_counts(48, 6), 1024, 512, L_EIO); }))});
-  s.push_back({"sp_moe_mx_eio", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
-  s.push_back({"sp_moe_mx_gu", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); })});
-  s.push_back({"sp_moe_mx_eio_decode_big", big(sp(SP, [=] { moe_forward(32, 8, 64, 1024, 512, MX, L_EIO, 0.0); }))});
-  s.push_back({"sp4_gemm_mx_eio", sp(SP4, [=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EIO); })});
-  s.push_back({"sp4_moe_mx_eio", sp(SP4, [=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
-  s.push_back({"emu_sp_mx_eio", sp(SP, emu([=] { gemm_mx({70, 0, 129, 300}, 1024, 256, L_EIO); }))});
-  s.push_back({"emu_sp_mx_eio_decode", big(sp(SP, emu([=] { gemm_mx({5, 0, 17, 64, 1, 33, 0, 8}, 1024, 256, L_EIO); })))});
-  s.push_back({"emu_sp4_mx_eio", sp(SP4, emu([=] { gemm_mx({200, 33}, 1024, 256, L_EIO); }))});
-  s.push_back({"sp_gemm_bf16_eio", sp(SP, [=] { gemm_bf16({100, 0, 300, 1, 129}, 512, 768, L_EIO); })});
-  s.push_back({"sp_gemm_bf16_eio_decode_big", big(sp(SP, [=] { gemm_bf16(decode_counts(48, 6), 512, 512, L_EIO); }))});
-  s.push_back({"sp_moe_bf16_eio", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
-  s.push_back({"sp_moe_bf16_gu", sp(SP, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_GU, 0.0); })});
-  s.push_back({"sp4_moe_bf16_eio", sp(SP4, [=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
-  s.push_back({"emu_sp_bf16_eio", sp(SP, emu([=] { gemm_bf16({70, 0, 129, 300}, 512, 512, L_EIO); }))});
-  s.push_back({"emu_sp_bf16_eio_decode", big(sp(SP, emu([=] { gemm_bf16({5, 0, 17, 64, 1, 33, 0, 8}, 256, 256, L_EIO); })))});
-  s.push_back({"emu_sp4_bf16_eio", sp(SP4, emu([=] { gemm_bf16({200, 33}, 512, 256, L_EIO); }))});
-  // the direct-weight configuration (variant dv): K-contiguous weights only; each scenario must run it
-  auto dv = [](std::function<void()> f) {
-    return [f] {
-      const long before = g_direct_gemms;
-      g_variant = MI355_GG_VARIANT_DV;
-      f();
-      g_variant = 0;
-      if (g_direct_gemms == before) CHECK_FAIL("the direct-weight configuration ran no GEMM");
-    };
-  };
-  s.push_back({"dv_gemm_bf16", dv([=] { gemm_bf16({100, 0, 300, 1, 129}, 1024, 768, L_EOI); })});
-  s.push_back({"dv_gemm_bf16_one_turn", dv([=] { gemm_bf16({100, 0, 300, 1, 129}, 256, 768, L_EOI); })});
-  s.push_back({"dv_gemm_mx", dv([=] { gemm_mx({100, 0, 300, 1, 129}, 1024, 768, L_EOI); })});
-  s.push_back({"dv_gemm_mx_long_k", dv([=] { gemm_mx({256, 256}, 4096, 272, L_EOI); })});
-  s.push_back({"dv_gemm_bf16_decode_big", big(dv([=] { gemm_bf16(decode_counts(64, 5), 1024, 768, L_EOI); }))});
-  s.push_back({"dv_moe_bf16_eoi", dv([=] { moe_forward(640, 2, 4, 512, 512, BF, L_EOI, 0.0); })});
-  s.push_back({"dv_moe_mx_eoi", dv([=] { moe_forward(640, 2, 4, 512, 512, MX, L_EOI, 0.0); })});
-  auto many = [] {
-    std::vector<int> c(1100, 0);
-    for (size_t i = 0; i < c.size(); i += 3) c[i] = 1 + (int)(i % 7);
-    return c;
-  };
-  s.push_back({"dv_gemm_bf16_many_groups", big(dv([=] { gemm_bf16(many(), 256, 256, L_EOI); }))});
-  s.push_back({"dv_gemm_bf16_narrow", dv([=] { gemm_bf16({3, 40, 0, 513, 1}, 256, 200, L_EOI); })});
-  s.push_back({"sp_gemm_mx_many_groups", big(sp(SP, [=] { gemm_mx(many(), 512, 256, L_EIO); }))});
-  s.push_back({"sp_gemm_mx_narrow", sp(SP, [=] { gemm_mx({3, 40, 0, 513, 1}, 512, 272, L_EIO); })});
-  s.push_back({"emu_dv_bf16_narrow", dv(emu([=] { gemm_bf16({3, 40, 0, 300, 1}, 256, 200, L_EOI); }))});
-  s.push_back({"emu_dv_bf16", dv(emu([=] { gemm_bf16({70, 0, 129, 5}, 512, 512, L_EOI); }))});
-  s.push_back({"emu_dv_bf16_one_turn", dv(emu([=] { gemm_bf16({70, 0, 129, 5, 40}, 256, 256, L_EOI); }))});
-  s.push_back({"emu_dv_mx", dv(emu([=] { gemm_mx({70, 0, 129, 5}, 1024, 256, L_EOI); }))});
-  s.push_back({"emu_dv_mx_long_k", dv(emu([=] { gemm_mx({200, 33}, 2048, 256, L_EOI); }))});
   s.push_back({"emu_wgrad_bf16", emu([=] { wgrad_direct({40, 0, 97, 33}, 256, 512, false, EPI_STORE_F32); })});
   s.push_back({"emu_wgrad_mx", emu([=] { wgrad_direct({40, 0, 97, 160}, 256, 256, true, EPI_STORE_F32); })});
   // many groups: the tile prefix comes from global memory past the LDS copy

@@ -160,7 +160,7 @@ def test_gemm_variant_is_per_call():
     import threading
     from hyper_multicore_amd import _lib, ops
     lib = _lib.load()
-    for bad in (-1, 7):
+    for bad in (-1, 1, 2, 3, 4, 7):  # 1-4: configurations retired with ABI 7
         assert lib.mi355moe_grouped_gemm_bf16(None, 4, 64, None, 0, 1, 8, None, None, bad, None, 0, None) \
             == _lib.EUNSUPPORTED
         assert lib.mi355moe_grouped_gemm_mxfp8(None, None, 4, 512, None, None, 0, 1, 16, None, None, bad, None, 0,

@@ -30,27 +30,19 @@ def checker():
 
 
 SCENARIOS = [
-    "gemm_bf16_eio", "gemm_bf16_eoi", "gemm_bf16_eio_narrow", "gemm_bf16_eoi_narrow", "gemm_mx_eio",
-    "gemm_mx_eoi", "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k", "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode",
+    "gemm_bf16_eio", "gemm_bf16_eoi", "gemm_bf16_eio_narrow", "gemm_bf16_eoi_narrow", "gemm_mx_eio", "gemm_mx_eoi",
+    "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k", "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode",
     "gemm_mx_eio_decode", "gemm_mx_eoi_decode", "gemm_bf16_eio_decode_big", "gemm_bf16_eoi_decode_big",
     "gemm_mx_eio_decode_big", "moe_bf16_eio_decode_big", "moe_mx_eio_decode_big", "moe_bf16_gu_decode_big",
     "moe_mx_gu_decode_big", "moe_mx_decode_halves", "moe_mx_gu_decode_halves", "moe_bf16_decode_halves",
     "moe_bf16_gu_decode_halves", "moe_mx_eoi_decode_halves", "emu_bf16_eio", "emu_bf16_eoi", "emu_mx_eio",
     "emu_mx_eoi", "emu_bf16_eio_decode", "emu_bf16_eoi_decode", "emu_mx_eio_decode", "emu_mx_eoi_decode",
-    "emu_moe_mx_decode_halves", "emu_moe_bf16_decode_halves", "emu_moe_mx_gu_decode_halves", "emu_b6_bf16_eio",
-    "emu_b6_bf16_eoi", "emu_b6_mx_eio", "b6_moe_bf16", "b6_moe_mx_eio", "b6_moe_mx_gu", "b6_moe_mx_eoi",
-    "sp_gemm_mx_eio", "sp_gemm_mx_eio_long_k", "sp_gemm_mx_eio_decode_big", "sp_moe_mx_eio", "sp_moe_mx_gu",
-    "sp_moe_mx_eio_decode_big", "sp4_gemm_mx_eio", "sp4_moe_mx_eio", "emu_sp_mx_eio", "emu_sp_mx_eio_decode",
-    "emu_sp4_mx_eio", "sp_gemm_bf16_eio", "sp_gemm_bf16_eio_decode_big", "sp_moe_bf16_eio", "sp_moe_bf16_gu",
-    "sp4_moe_bf16_eio", "emu_sp_bf16_eio", "emu_sp_bf16_eio_decode", "emu_sp4_bf16_eio", "dv_gemm_bf16",
-    "dv_gemm_bf16_one_turn", "dv_gemm_mx", "dv_gemm_mx_long_k", "dv_gemm_bf16_decode_big", "dv_moe_bf16_eoi",
-    "dv_moe_mx_eoi", "dv_gemm_bf16_many_groups", "dv_gemm_bf16_narrow", "sp_gemm_mx_many_groups",
-    "sp_gemm_mx_narrow", "emu_dv_bf16_narrow", "emu_dv_bf16", "emu_dv_bf16_one_turn", "emu_dv_mx",
-    "emu_dv_mx_long_k", "emu_wgrad_bf16", "emu_wgrad_mx", "gemm_bf16_many_groups", "gemm_bf16_noalloc",
-    "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill",
-    "moe_mx_eio_prefill", "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp",
-    "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16",
-    "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill"
+    "emu_moe_mx_decode_halves", "emu_moe_bf16_decode_halves", "emu_moe_mx_gu_decode_halves", "emu_wgrad_bf16",
+    "emu_wgrad_mx", "gemm_bf16_many_groups", "gemm_bf16_noalloc", "moe_bf16_eio", "moe_bf16_eoi",
+    "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
+    "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu",
+    "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32",
+    "bwd_mx_bf16_prefill"
 ]
 
 

@@ -11,7 +11,7 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = ["default", "b6", "dv", "sp", "sp4", "pp", "w4"]
+VARIANTS = ["default", "pp", "w4"]
 
 
 def _blocks_of(w, I):

@@ -4,7 +4,6 @@ Bars: router indices / weights / scores, dispatch metadata, permutation, MX quan
 combine are bit-exact; GEMM outputs are within rel-L2 1e-2 (bf16) / 3e-2 (MXFP8) of the
 fp32-accumulate oracle on the same rounded operands.
 """
-import contextlib
 import zlib
 
 import numpy as np
@@ -416,155 +415,6 @@ def test_moe_forward_mxfp8_eoi_matches_eio(gpu):
     out_eoi = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), e1.view(torch.uint8), e2.view(torch.uint8),
                               w1_scale=t1, w2_scale=t2, layout="EOI", **args).cpu()
     assert torch.equal(out_eio, out_eoi)
-
-
-@contextlib.contextmanager
-def _gemm_variant(name):
-    from hyper_multicore_amd import ops
-    prev = ops.set_gemm_variant(name)
-    try:
-        yield
-    finally:
-        ops.set_gemm_variant(prev)
-
-
-_DIRECT_SKIP = _needs(128, "the direct-weight GEMM configuration")
-
-
-@_DIRECT_SKIP
-@pytest.mark.parametrize("Kd", [256, 2048])
-@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [0, 0, 7], [256] * 4, [3, 40, 0, 513]])
-def test_grouped_gemm_bf16_direct_matches_default(gpu, counts, Kd):
-    """The direct-weight configuration runs the same MFMAs in the same K order as the default one:
-    bit-identical outputs (EOI weights; Kd = 256 is one turn of its 8-stage ring, 2048 eight)."""
-    from hyper_multicore_amd import ops
-    g = _seed(sum(counts) + Kd)
-    G, N = len(counts), 768
-    rows = sum(counts)
-    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
-    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
-    we = w.transpose(1, 2).contiguous().to(gpu)
-    gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
-    out_def = ops.grouped_gemm_bf16(x.to(gpu), we, gl, "EOI").cpu()
-    with _gemm_variant("dv"):
-        out_dv = ops.grouped_gemm_bf16(x.to(gpu), we, gl, "EOI").cpu()
-    assert torch.equal(out_dv, out_def)
-    starts = [0, *gl.cpu().tolist()]
-    ref = torch.cat([x[starts[i]:starts[i + 1]].float() @ w[i].float() for i in range(G)]).to(torch.bfloat16)
-    assert orc.rel_l2(out_dv, ref) < 2e-3
-
-
-@_DIRECT_SKIP
-@_needs(1, "the MXFP8 EOI GEMM path")
-@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2, [3, 40, 0, 513]])
-def test_grouped_gemm_mxfp8_direct_matches_eio(gpu, counts):
-    """MX EOI weights with variant "dv": the library refuses MXFP8 on the direct-weight configuration
-    (its outputs were wrong in every second 32-column block on the GPU), so the call runs on the
-    default configuration and stays bit-identical to the EIO GEMM."""
-    from hyper_multicore_amd import ops
-    g = _seed(sum(counts) + 11)
-    G, Kd, N = len(counts), 1024, 768
-    rows = sum(counts)
-    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
-    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
-    xq, xs = ops.mx_quantize_rows(x.to(gpu))
-    d, s = ops.mx_quantize_cols(w.to(gpu))
-    de, se = ops.mx_weight_to_eoi(d, s)
-    gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
-    out_eio = ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), s, gl).cpu()
-    with _gemm_variant("dv"):
-        out_dv = ops.grouped_gemm_mxfp8(xq, xs, de.view(torch.uint8), se, gl, layout="EOI").cpu()
-    assert torch.equal(out_dv, out_eio)
-
-
-@_DIRECT_SKIP
-def test_moe_forward_bf16_direct_matches_default(gpu):
-    """The MegaMoE forward (EOI bf16) with both expert GEMMs on the direct-weight configuration."""
-    from hyper_multicore_amd import ops
-    T, H, I, E, K = 700, 1024, 512, 16, 4
-    g = _seed(T + E + 5)
-    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
-    w1e, w2e = w1.transpose(1, 2).contiguous().to(gpu), w2.transpose(1, 2).contiguous().to(gpu)
-    args = dict(num_experts=E, intermediate_size=I, layout="EOI")
-    out_def = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1e, w2e, **args).cpu()
-    with _gemm_variant("dv"):
-        out_dv = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), w1e, w2e, **args).cpu()
-    assert torch.equal(out_dv, out_def)
-    ref = orc.expert_forward_reference(x, ids, probs, w1, w2, layout="EIO")
-    assert orc.rel_l2(out_dv, ref) < BF16_REL_L2
-
-
-_SPLIT_SKIP = _needs(256, "the split-role GEMM configurations")
-
-
-@_SPLIT_SKIP
-@pytest.mark.parametrize("variant", ["sp", "sp4"])
-@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2, [3, 40, 0, 513], [5, 0, 17, 1, 33]])
-def test_grouped_gemm_mxfp8_split_roles_match_default(gpu, counts, variant):
-    """Split copy roles change which wave copies what, not the MFMAs or their K order: the MXFP8 EIO
-    grouped GEMM is bit-identical to the default configuration."""
-    from hyper_multicore_amd import ops
-    g = _seed(sum(counts) + 13)
-    G, Kd, N = len(counts), 1024, 768
-    rows = sum(counts)
-    x = torch.randn(rows, Kd, generator=g).to(torch.bfloat16)
-    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16)
-    xq, xs = ops.mx_quantize_rows(x.to(gpu))
-    d, s = ops.mx_quantize_cols(w.to(gpu))
-    gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
-    out_def = ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), s, gl).cpu()
-    with _gemm_variant(variant):
-        out_sp = ops.grouped_gemm_mxfp8(xq, xs, d.view(torch.uint8), s, gl).cpu()
-    assert torch.equal(out_sp, out_def)
-
-
-@_SPLIT_SKIP
-def test_moe_forward_mxfp8_split_roles_match_default(gpu):
-    from hyper_multicore_amd import ops
-    T, H, I, E, K = 700, 1024, 512, 16, 4
-    g = _seed(T + E + 7)
-    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
-    d1, s1 = ops.mx_quantize_cols(w1.to(gpu))
-    d2, s2 = ops.mx_quantize_cols(w2.to(gpu))
-    args = dict(num_experts=E, intermediate_size=I, precision="mxfp8", w1_scale=s1, w2_scale=s2)
-    out_def = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8),
-                              **args).cpu()
-    with _gemm_variant("sp"):
-        out_sp = ops.moe_forward(x.to(gpu), ids.to(gpu), probs.to(gpu), d1.view(torch.uint8), d2.view(torch.uint8),
-                                 **args).cpu()
-    assert torch.equal(out_sp, out_def)
-
-
-@_SPLIT_SKIP
-@pytest.mark.parametrize("variant", ["sp", "sp4"])
-@pytest.mark.parametrize("counts", [[100, 0, 300, 1, 129], [256] * 2, [3, 40, 0, 513], [5, 0, 17, 1, 33]])
-def test_grouped_gemm_bf16_eio_split_roles_match_default(gpu, counts, variant):
-    """The bf16 grouped GEMM on EIO weights [G, K, N] with split copy roles is bit-identical to the
-    default configuration (same MFMAs in the same K order)."""
-    from hyper_multicore_amd import ops
-    g = _seed(sum(counts) + 17)
-    G, Kd, N = len(counts), 1024, 768
-    x = torch.randn(sum(counts), Kd, generator=g).to(torch.bfloat16).to(gpu)
-    w = (torch.randn(G, Kd, N, generator=g) * 0.05).to(torch.bfloat16).to(gpu)
-    gl = torch.tensor(counts).cumsum(0).to(torch.int64).to(gpu)
-    out_def = ops.grouped_gemm_bf16(x, w, gl, "EIO").cpu()
-    with _gemm_variant(variant):
-        out_sp = ops.grouped_gemm_bf16(x, w, gl, "EIO").cpu()
-    assert torch.equal(out_sp, out_def)
-
-
-@_SPLIT_SKIP
-def test_moe_forward_bf16_eio_split_roles_match_default(gpu):
-    from hyper_multicore_amd import ops
-    T, H, I, E, K = 700, 1024, 512, 16, 4
-    g = _seed(T + E + 11)
-    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g)
-    args = dict(num_experts=E, intermediate_size=I, precision="bf16", layout="EIO")
-    ins = [t.to(gpu) for t in (x, ids, probs, w1, w2)]
-    out_def = ops.moe_forward(*ins, **args).cpu()
-    with _gemm_variant("sp"):
-        out_sp = ops.moe_forward(*ins, **args).cpu()
-    assert torch.equal(out_sp, out_def)
 
 
 _NUMERICS_SKIP = _needs(2, "the BF16 numerics options")

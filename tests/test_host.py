@@ -106,9 +106,9 @@ def test_bench_traffic_record(tmp_path):
     import bench
     (tmp_path / "profiles").mkdir()
     rec = {"fetch_kib": 1000.0, "fetch_factor": 0.5, "write_kib": 10.0, "write_factor": 2.0}
-    (tmp_path / "profiles" / "traffic_dsv3_bf16_dv_EOI.json").write_text(json.dumps(rec))
-    assert bench.measured_traffic("dsv3_bf16", "dv", "EOI", root=str(tmp_path)) == (500 + 20) * 1024
-    assert bench.measured_traffic("dsv3_bf16", "dv", "EIO", root=str(tmp_path)) is None
+    (tmp_path / "profiles" / "traffic_dsv3_bf16_w4_EOI.json").write_text(json.dumps(rec))
+    assert bench.measured_traffic("dsv3_bf16", "w4", "EOI", root=str(tmp_path)) == (500 + 20) * 1024
+    assert bench.measured_traffic("dsv3_bf16", "w4", "EIO", root=str(tmp_path)) is None
     assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) is None
     c = bench.CONFIGS["dsv3_bf16"]
     work = {"g1_flops": 1e12, "g1_bytes": 1e10}
