@@ -14,7 +14,6 @@
 #include "common.h"
 #include "gemm.h"
 
-#define MI355_HD __host__ __device__ __forceinline__
 
 // Tile configurations (compile time). Both use 4 waves, tiles of BN = 256 weight columns and
 // 64-byte K stages (32 bf16 or 64 e4m3 per row):

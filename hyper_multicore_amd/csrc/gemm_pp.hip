@@ -1,126 +1,28 @@
-// Persistent grouped GEMM for gfx950 (MI355X), 8-wave ping-pong configuration: bf16 and MXFP8.
+// Persistent grouped GEMM for gfx950 (MI355X), 8-wave ping-pong configuration: bf16 and MXFP8. The
+// tile configurations, work-item decode, copy plan, fragment reads, MFMAs and epilogues are the
+// policy-typed code of gemm_pp_plan.h (replayed on the CPU by the checker under tests/native); this
+// file holds the kernel's stage pipeline and the launch.
 //
-// Work list: as in gemm.hip - every (group, 256-row m-tile, 256-column n-tile) is one work item,
-// decoded on the device from the tile prefix; one workgroup per CU, work item L of round r goes to
-// workgroup 8 * slot + xcd, so each XCD runs a contiguous run of items (m fastest) and the n-tiles
-// that re-read one expert's activation rows run at the same time on one XCD and share its L2.
-//
-// Workgroup: 512 threads = 8 wavefronts, two per SIMD. Tiles are BM x 256 (BM = 320 for bf16, 256
-// for MXFP8). The waves form two groups, 0-3 and 4-7, one wave of each on every SIMD; wave w
-// computes columns 64 * (w % 4) ..+63 of the 32-row blocks 2 mi + w / 4 (mi < BM / 64), 2 x BM / 64
-// blocks of 32 x 32 (bf16 v_mfma_f32_32x32x16_bf16, MXFP8 v_mfma_scale_f32_32x32x64_f8f6f4). The row
-// blocks alternate between the groups and the activation copies between the waves, so a tile that
-// is not full keeps the two groups and the eight waves evenly loaded; bf16 waves skip the MFMAs of
-// row blocks past the item's rows.
-//
-// K stages are 128 bytes per row (64 bf16 or 128 e4m3): whole 128-byte lines per row and stage,
-// which the memory system streams markedly faster than half lines when one operand is re-read from
-// L2 while the other streams from HBM. A stage is 64 KB of operands, so the LDS ring has two slots:
-// the copies of stage q + 1 go out at the start of the interval in which stage q is used, into the
-// slot that stage q - 1 left. A stage is used in two half-steps of 64 bytes of K (one set of
-// operand fragments in registers at a time). Between two barriers the groups alternate on every
-// SIMD: group 0 reads half 0 of stage q while group 1 issues the MFMAs of half 1 of stage q - 1,
-// then group 0 issues half 0's MFMAs while group 1 reads half 0, and so on, so each SIMD's matrix
-// core is fed alternately by its two waves while the other one reads LDS. Before the barrier that
-// ends the interval every wave waits for its own copies (loads of a wave retire in order; every wave
-// issues the same copies per stage). The stages of all work items of a workgroup form one stream,
-// so the next item's first stage is in flight while the current item finishes; copies past the end
-// of the stream re-read the last stage into the free slot, which keeps the counts exact.
-//
-// LDS layouts (16-byte chunks, XOR swizzled against bank conflicts):
-//   K-contiguous rows (activations; EOI weights): row r at r * 128, chunk c at c ^ ((r >> 1) & 7),
-//     read with ds_read_b128;
-//   N-contiguous weights (EIO bf16, MX col_data): K row k of the stage holds 256 columns; bf16
-//     chunk c at c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows),
-//     read with ds_read_b64_tr_b16 / ds_read_b64_tr_b8;
-//   MX scales of a stage: code j (0..3) of tile row r at j * 512 + row0 % 4 + r (from the
-//     stage-major code planes of the activation scales: two 256-byte runs per code from the 4-aligned
-//     address at or below the tile's first row); weight tile column j's two codes of 64-K step s at
-//     s * 512 + j * 2 (the MX root's col_scale pairs).
-//
-// Epilogues: bf16 store, SwiGLU -> bf16 (each 32 x 32 block through a wave-private LDS staging block,
-// so the global stores are 16 bytes per lane) and, for MX inputs, SwiGLU -> fp32 (staged 16 rows at a
-// time, 32-byte stores), which mi355_mx_quant_act then quantises: a requant in this epilogue would
-// run its VALU work while the other wave group waits at the stage barrier. For SwiGLU the 64 weight columns of a wave are 32 gate then
-// the matching 32 up columns, so a lane holds gate and up of the same output element.
+// Pipeline: the stages of all work items of a workgroup form one stream. The copies of stage q + 1
+// go out at the start of the interval in which stage q is used, into the slot that stage q - 1 left;
+// copies past the end of the stream re-read the last stage into the free slot, which keeps the
+// counts exact. A stage is used in two half-steps of 64 bytes of K (one set of operand fragments in
+// registers at a time). Between two barriers the groups alternate on every SIMD: group 0 reads half
+// 0 of stage q while group 1 issues the MFMAs of half 1 of stage q - 1, then group 0 issues half 0's
+// MFMAs while group 1 reads half 0, and so on, so each SIMD's matrix core is fed alternately by its
+// two waves while the other one reads LDS. Before the barrier that ends the interval every wave
+// waits for its own copies (loads of a wave retire in order; every wave issues the same copies per
+// stage), so the next item's first stage is in flight while the current item finishes.
 #include "common.h"
 #include "gemm.h"
+#include "gemm_pp_plan.h"
 #include "../../include/mi355moe.h"
 
 namespace {
 
-constexpr int BN = 256;
-constexpr int KB = 128;  // bytes of K per row and stage
-constexpr int S = 2;     // ring slots
-constexpr int WAVES = 8, THREADS = 64 * WAVES;
-constexpr int WN = 64, NI = WN / 32;
-// MX scales of a stage: 4 activation code planes of 512 bytes (the 256 tile rows from the 4-aligned
-// row at or below the first one), 2 x 256 weight code pairs
-constexpr int AS_PLANE = 512;
-constexpr int B_BYTES = BN * KB, AS_BYTES = 4 * AS_PLANE, BS_BYTES = 2 * BN * 2;
-constexpr int CPW_B = B_BYTES / 1024 / WAVES;  // 1 KB weight copies per wave and stage
-static_assert(CPW_B == 4, "four 1 KB weight copies per wave");
+using namespace pp;
+using O = PpDev;
 
-// Tile height and LDS layout. Tiles are 256 rows, or 320 for bf16 GEMMs whose groups average at most
-// 320 rows (TALL): each m-tile streams its group's weights, whose lines miss L2, and the
-// workgroup's memory requests in flight are what bounds the kernel, so an expert of 257..320 routed
-// rows (DeepSeek-V3 prefill routes 256 on average, with a wide spread) is one m-tile instead of a
-// full one and a short one that streams the weights again. When groups are large multiples of 256
-// rows the fifth row block costs more than the tiles it saves. MX tiles stay 256 rows (no registers
-// left for a fifth row block).
-template <bool MX_, bool TALL>
-struct Cfg {
-  static constexpr bool MX = MX_;
-  static constexpr int BM = (MX || !TALL) ? 256 : 320;
-  static constexpr int WM = BM / 2, MI = WM / 32;  // rows per wave group, 32-row blocks per wave
-  static constexpr int A_BYTES = BM * KB;
-  static constexpr int CPW_A = A_BYTES / 1024 / WAVES;  // 1 KB activation copies per wave and stage
-  static constexpr int B_OFF = A_BYTES, AS_OFF = B_OFF + B_BYTES, BS_OFF = AS_OFF + AS_BYTES;
-  static constexpr int SLOT = MX ? BS_OFF + BS_BYTES : AS_OFF;
-  static constexpr int PREFIX_OFF = S * SLOT;
-  static constexpr int PREFIX_MAX = BM > 256 ? 512 : 1024;  // groups whose tile prefix and row ends are in LDS
-  static constexpr int ROWS_OFF = PREFIX_OFF + (PREFIX_MAX + 1) * 4;
-  // a wave's epilogue staging: 16 rows of a 32-column bf16 block (MX: 16 rows of 32 fp32 columns)
-  static constexpr int EPI_BLOCK = MX ? 2048 : 1024;
-  static constexpr int EPI_OFF = (ROWS_OFF + PREFIX_MAX * 4 + 15) & ~15;
-  static constexpr int TOTAL = EPI_OFF + WAVES * EPI_BLOCK;
-  static_assert(TOTAL <= 160 * 1024, "LDS budget");
-  static_assert(SLOT % 16 == 0, "copy destinations are 16-byte aligned");
-  static_assert(A_BYTES % (1024 * WAVES) == 0, "whole 1 KB activation copies per wave");
-};
-
-// Tile column j (0..255) -> weight column; SwiGLU: wave tile q's 64 columns are gate columns
-// nt * 128 + 32 q .. +31, then the up columns I + the same.
-// With the gate/up interleaved weight layout the projection column goes through gate_up_col.
-__device__ __forceinline__ int tile_col(int j, int nt, int I, bool swiglu, int gu) {
-  if (!swiglu) return nt * BN + j;
-  const int q = j >> 6, jj = j & 63;
-  const int base = nt * (BN / 2) + q * 32;
-  return gate_up_col(jj < 32 ? base + jj : I + base + (jj - 32), I, gu);
-}
-
-__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// Direct global -> LDS copies: lane i writes its 16 (4) bytes at LDS address M0 + 16 i (4 i). Inline
-// assembly, so that the compiler does not treat the copy as an alias of every later LDS read (its
-// builtin makes it wait for all outstanding loads before the next ds_read).
-// The source is a wave-uniform base in scalar registers plus a 32-bit per-lane offset.
-__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
-               : "memory");
-}
-__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
-               : "memory");
-}
-// A pointer known to be wave-uniform, held in scalar registers.
-__device__ __forceinline__ const uint8_t* uni_ptr(const uint8_t* ptr) {
-  const uint64_t v = (uint64_t)(uintptr_t)ptr;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // Workgroup barrier without a memory fence: the copies are ordered by the explicit vmcnt waits.
@@ -130,363 +32,6 @@ __device__ __forceinline__ void barrier() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-}
-
-struct Item {
-  int64_t row0;  // first routed row of the tile
-  int rows;      // valid rows (1..BM)
-  int nt;        // n-tile
-  int g;         // group
-};
-
-#define LDSP(T, p) ((const __attribute__((address_space(3))) T*)(p))
-
-// Work item L from the tile prefix and the groups' row ends, both in LDS (LDS reads only: a global
-// or generic load here would make the wave wait for all of its outstanding copies).
-template <class C>
-__device__ __forceinline__ void decode(const GGParams& p, const uint8_t* smem, int L, Item& it) {
-  constexpr int BM = C::BM;
-  const __attribute__((address_space(3))) int32_t* prefix = LDSP(int32_t, smem + C::PREFIX_OFF);
-  const __attribute__((address_space(3))) int32_t* rows = LDSP(int32_t, smem + C::ROWS_OFF);
-  int lo = 0, hi = p.G - 1;
-  while (lo < hi) {  // largest g with prefix[g] * n_tiles <= L
-    const int mid = (lo + hi + 1) >> 1;
-    if (prefix[mid] * p.n_tiles <= L) lo = mid; else hi = mid - 1;
-  }
-  const int g = uni(lo);
-  const int mtiles = uni(prefix[g + 1] - prefix[g]);
-  const int local = L - uni(prefix[g]) * p.n_tiles;
-  const int nt = local / mtiles;
-  const int mt = local - nt * mtiles;
-  const int64_t row_begin = g == 0 ? 0 : uni(rows[g - 1]);
-  const int64_t row_end = uni(rows[g]);
-  it.g = g;
-  it.nt = nt;
-  it.row0 = row_begin + (int64_t)mt * BM;
-  const int64_t left = row_end - it.row0;
-  it.rows = uni((int)(left < BM ? left : BM));
-}
-
-// Copy sources of one work item: wave-uniform bases of stage 0 (stage k adds k * the stride) and
-// per-lane 32-bit offsets (the activations, one group's weights and the scale arrays are below
-// 4 GiB, which mi355_gg_pp_applies checks).
-// Only the gathered activation offsets are kept per lane; the weight and scale offsets are functions
-// of the lane and the item's n-tile, recomputed for every stage (holding them across the K loop
-// pushed the MX kernels past their registers, and a spill reload between the copies waits for all
-// of them).
-template <int CPW_A>
-struct Plan {
-  const uint8_t* a_base;
-  const uint8_t* b_base;
-  const uint8_t* s_base;   // MX: activation code plane run (every wave)
-  const uint8_t* bs_base;  // MX: the group's weight scales (waves 0-3; waves 4-7 repeat them)
-  uint32_t ao[CPW_A];
-  int a_copies;  // activation copies of this wave (8-row groups past the item's rows are skipped)
-  int nt;        // the item's n-tile
-  int64_t b_stride, s_stride, b_scale_stride;
-};
-
-// Activation and EOI-weight copies: copy i of a stage covers rows 8 i ..+7, lane l row
-// 8 i + l / 8 and LDS position l % 8, which holds chunk (l % 8) ^ ((row >> 1) & 7).
-__device__ __forceinline__ int row_of(int i, int lane) { return i * 8 + (lane >> 3); }
-__device__ __forceinline__ int chunk_of(int r, int lane) { return (lane & 7) ^ ((r >> 1) & 7); }
-
-template <class C, bool B_KN, bool SWIGLU>
-__device__ __forceinline__ void make_plan(const GGParams& p, const Item& it, int wave, int lane,
-                                          Plan<C::CPW_A>& pl) {
-  constexpr bool MX = C::MX;
-  constexpr int ESIZE = MX ? 1 : 2, CPW = C::CPW_A;
-#pragma unroll
-  for (int j = 0; j < CPW; ++j) {
-    const int r = row_of(j * WAVES + wave, lane);
-    const int rr = r < it.rows ? r : it.rows - 1;
-    const int64_t routed = it.row0 + rr;
-    const int64_t src = p.a_row_index ? (int64_t)(p.a_row_index[routed] / p.a_row_div) : routed;
-    pl.ao[j] = (uint32_t)(src * p.lda_bytes + chunk_of(r, lane) * 16);
-  }
-  pl.a_base = uni_ptr(p.A);
-  {
-    // copies of 8-row groups holding rows of the item: the wave's are j * WAVES + wave
-    const int groups = (it.rows + 7) / 8;
-    const int n = (groups - wave + WAVES - 1) / WAVES;
-    pl.a_copies = uni(n < 0 ? 0 : (n > CPW ? CPW : n));
-  }
-  pl.b_base = uni_ptr(p.B + (int64_t)it.g * p.b_group_stride);
-  pl.nt = uni(it.nt);
-  pl.b_stride = B_KN ? (int64_t)(KB / ESIZE) * p.b_row_bytes : KB;
-  pl.s_base = pl.a_base;
-  pl.bs_base = pl.a_base;
-  pl.s_stride = 0;
-  if constexpr (MX) {
-    // code plane wave / 2, bytes 256 (wave % 2) + 4 lane from the 4-aligned row at or below row0
-    // (rows past the item read the next rows or the planes' padding)
-    pl.s_base = uni_ptr(p.a_scale + (wave >> 1) * (p.a_scale_stage_stride >> 2) + (it.row0 & ~(int64_t)3));
-    pl.s_stride = p.a_scale_stage_stride;
-    pl.bs_base = uni_ptr(p.b_scale + (int64_t)it.g * p.b_scale_group_stride);
-    pl.b_scale_stride = (int64_t)p.Ntot * 4;  // two 64-K steps per stage
-  }
-}
-
-template <bool MX, bool B_KN, bool SWIGLU>
-__device__ __forceinline__ uint32_t b_off(const GGParams& p, int nt, int i, int lane) {
-  if constexpr (!B_KN) {  // K-contiguous weights: like the activations, one weight row per tile column
-    const int r = row_of(i, lane);
-    int wc = tile_col(r, nt, p.N, SWIGLU, p.gate_up_interleaved);
-    if (wc >= p.Ntot) wc = p.Ntot - 1;
-    return (uint32_t)wc * (uint32_t)p.b_row_bytes + (uint32_t)(chunk_of(r, lane) * 16);
-  } else if constexpr (MX) {
-    const int L16 = i * 64 + lane;  // K rows of 256 bytes: copy i covers K rows 4 i ..+3
-    const int k = L16 >> 4;
-    const int c = (L16 & 15) ^ (k & 15);
-    int wc = tile_col(c * 16, nt, p.N, SWIGLU, p.gate_up_interleaved);
-    if (wc > p.Ntot - 16) wc = p.Ntot - 16;
-    return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc;
-  } else {
-    const int L16 = i * 64 + lane;  // K rows of 512 bytes: copy i covers K rows 2 i, 2 i + 1
-    const int k = L16 >> 5;
-    const int c = (L16 & 31) ^ ((k & 7) << 1);
-    int wc = tile_col(c * 8, nt, p.N, SWIGLU, p.gate_up_interleaved);
-    if (wc > p.Ntot - 8) wc = p.Ntot - 8;
-    return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc * 2u;
-  }
-}
-
-// `lane` is an opaque copy made per stage, so that the offsets derived from it are recomputed here
-// rather than hoisted out of the K loop into registers.
-template <class C, bool B_KN, bool SWIGLU>
-__device__ __forceinline__ void issue_stage(const GGParams& p, const Plan<C::CPW_A>& pl, int k, uint32_t slot,
-                                            int wave, int lane) {
-  constexpr bool MX = C::MX;
-  constexpr int CPW = C::CPW_A;
-  asm volatile("" : "+v"(lane));
-  const uint8_t* ab = uni_ptr(pl.a_base + (int64_t)k * KB);
-  const uint8_t* bb = uni_ptr(pl.b_base + (int64_t)k * pl.b_stride);
-  // (the waits are for all outstanding copies, so a wave may issue fewer; LDS rows that are not
-  // refilled hold stale data that only feeds accumulator rows the epilogue does not store)
-#pragma unroll
-  for (int j = 0; j < CPW; ++j)
-    if (j < pl.a_copies) dma16(ab, pl.ao[j], uni(slot + (j * WAVES + wave) * 1024));
-#pragma unroll
-  for (int j = 0; j < CPW_B; ++j)
-    dma16(bb, b_off<MX, B_KN, SWIGLU>(p, pl.nt, wave * CPW_B + j, lane),
-          uni(slot + C::B_OFF + (wave * CPW_B + j) * 1024));
-  if constexpr (MX) {
-    // activation code planes: plane wave / 2, bytes 256 (wave % 2) + 4 lane of the item's run;
-    // col_scale [G, K/64, Ntot, 2]: wave w (and w + 4) copies 64-K step (w >> 1) & 1, tile columns
-    // 128 (w & 1) ..+127
-    const uint32_t so = (uint32_t)((wave & 1) * 256 + lane * 4);
-    int wc = tile_col((wave & 1) * 128 + lane * 2, pl.nt, p.N, SWIGLU, p.gate_up_interleaved);
-    if (wc > p.Ntot - 2) wc = p.Ntot - 2;
-    const uint32_t bso = (uint32_t)((((wave >> 1) & 1) * p.Ntot + wc) * 2);
-    dma4(uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), so,
-         uni(slot + C::AS_OFF + (wave >> 1) * AS_PLANE + (wave & 1) * 256));
-    dma4(uni_ptr(pl.bs_base + (int64_t)k * pl.b_scale_stride), bso,
-         uni(slot + C::BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256));
-  }
-}
-
-// LDS offset of 16-byte chunk c of K-contiguous row r
-__device__ __forceinline__ int chunk_off(int r, int c) { return r * KB + ((c ^ ((r >> 1) & 7)) << 4); }
-
-// Operand fragments of one half-step (64 bytes of K).
-template <bool MX, bool B_KN, int MI> struct Frags;
-template <int MI> struct Frags<false, false, MI> { v8bf a[2][MI], b[2][NI]; };
-template <int MI> struct Frags<false, true, MI> { v8bf a[2][MI]; v4s bl[2][NI], bh[2][NI]; };
-template <int MI> struct Frags<true, false, MI> { v4i al[MI], ah[MI], bl[NI], bh[NI]; int sa[MI], sb[NI]; };
-template <int MI> struct Frags<true, true, MI> { v4i al[MI], ah[MI]; v2i bp[NI][4]; int sa[MI], sb[NI]; };
-
-// a_off: the item's first routed row modulo 4 (the offset of the MX activation code planes)
-template <class C, bool B_KN>
-__device__ __forceinline__ void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int h, int grp, int wq,
-                                           int lane, int a_off, int nmi) {
-  constexpr bool MX = C::MX;
-  constexpr int MI = C::MI;
-  // bf16 tiles of five row blocks: the fragment addresses are recomputed per read (held across the
-  // K loop they would take about 28 registers)
-  if constexpr (!MX && MI > 4) asm volatile("" : "+v"(lane));
-  const uint8_t* As = slot;
-  const uint8_t* Bs = slot + C::B_OFF;
-  if constexpr (!MX) {
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const int ks = h * 2 + s2;  // 16-K step of the stage
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi) {
-        if (MI > 4 && mi >= nmi) continue;  // row block without rows of the item
-        const int r = (2 * mi + grp) * 32 + (lane & 31);
-        f.a[s2][mi] = *LDSP(v8bf, As + chunk_off(r, ks * 2 + (lane >> 5)));
-      }
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        if constexpr (!B_KN) {
-          const int n = wq * WN + ni * 32 + (lane & 31);
-          f.b[s2][ni] = *LDSP(v8bf, Bs + chunk_off(n, ks * 2 + (lane >> 5)));
-        } else {
-          const int g16 = lane >> 4, m = lane & 15;
-          const int nb = wq * WN + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
-          const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
-          const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
-          const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
-          f.bl[s2][ni] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) v4s*)LDSP(v4s, Bs + off0));
-          f.bh[s2][ni] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) v4s*)LDSP(v4s, Bs + off1));
-        }
-      }
-    }
-  } else {
-    // one 64-K step h: lane r + 32 g holds K 16 g .. +15 and 32 + 16 g .. +15 of the step
-    const uint8_t* ASs = slot + C::AS_OFF;
-    const uint8_t* BSs = slot + C::BS_OFF;
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      const int r = (2 * mi + grp) * 32 + (lane & 31);
-      const int c0 = h * 4 + (lane >> 5);
-      f.al[mi] = *LDSP(v4i, As + chunk_off(r, c0));
-      f.ah[mi] = *LDSP(v4i, As + chunk_off(r, c0 + 2));
-      f.sa[mi] = *LDSP(uint8_t, ASs + (h * 2 + (lane >> 5)) * AS_PLANE + a_off + r);
-    }
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) {
-      const int n = wq * WN + ni * 32 + (lane & 31);
-      if constexpr (!B_KN) {
-        const int c0 = h * 4 + (lane >> 5);
-        f.bl[ni] = *LDSP(v4i, Bs + chunk_off(n, c0));
-        f.bh[ni] = *LDSP(v4i, Bs + chunk_off(n, c0 + 2));
-      } else {
-        const int g16 = lane >> 4, m = lane & 15;
-        const int nb = wq * WN + ni * 32 + (g16 & 1) * 16;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int k = h * 64 + (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
-          const int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
-          f.bp[ni][q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              (__attribute__((address_space(3))) v2i*)LDSP(v2i, Bs + off));
-        }
-      }
-      f.sb[ni] = *LDSP(uint8_t, BSs + h * 512 + n * 2 + (lane >> 5));
-    }
-  }
-}
-
-// nmi: the wave's row blocks that hold rows of the item (bf16 320-row tiles skip the others, so a
-// tile of up to 256 rows issues the MFMAs a 256-row tile would)
-template <bool MX, bool B_KN, int MI>
-__device__ __forceinline__ void mfmas(const Frags<MX, B_KN, MI>& f, v16f (&acc)[MI][NI], int nmi) {
-  if constexpr (!MX) {
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni) {
-          if (MI > 4 && mi >= nmi) continue;
-          v8bf b;
-          if constexpr (!B_KN) b = f.b[s2][ni];
-          else b = __builtin_bit_cast(v8bf, __builtin_shufflevector(f.bl[s2][ni], f.bh[s2][ni], 0, 1, 2, 3, 4, 5, 6, 7));
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s2][mi], b, acc[mi][ni], 0, 0, 0);
-        }
-  } else {
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      const v8i a = __builtin_shufflevector(f.al[mi], f.ah[mi], 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        v8i b;
-        if constexpr (!B_KN) {
-          b = __builtin_shufflevector(f.bl[ni], f.bh[ni], 0, 1, 2, 3, 4, 5, 6, 7);
-        } else {
-          const v4i b01 = __builtin_shufflevector(f.bp[ni][0], f.bp[ni][1], 0, 1, 2, 3);
-          const v4i b23 = __builtin_shufflevector(f.bp[ni][2], f.bp[ni][3], 0, 1, 2, 3);
-          b = __builtin_shufflevector(b01, b23, 0, 1, 2, 3, 4, 5, 6, 7);
-        }
-        acc[mi][ni] =
-            __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[mi][ni], 0, 0, 0, f.sa[mi], 0, f.sb[ni]);
-      }
-    }
-  }
-}
-
-__device__ __forceinline__ float swiglu_act(float g_acc, float u_acc) {
-  // the gate and up projections are rounded to bf16 (the GMM1 output), SiLU(gate) * up in fp32
-  const float gte = bf16_to_f32(f32_to_bf16(g_acc));
-  const float up = bf16_to_f32(f32_to_bf16(u_acc));
-  return gte / (1.0f + __expf(-gte)) * up;
-}
-
-// Staging offset of element (row, byte column cb) of a 32 x 64-byte block: 16-byte chunks swizzled
-// with (row >> 2) & 3, so the two half-wavefronts (rows r and r + 4) write different banks.
-__device__ __forceinline__ int stage_off(int row, int cb) { return row * 64 + ((((cb >> 4) ^ (row >> 2)) & 3) << 4) + (cb & 15); }
-
-// acc[mi][ni][r] holds row (2 mi + grp) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
-// wq * 64 + ni * 32 + lane % 32 of the tile. Each 32 x 32 output block goes through the wave's LDS
-// staging block 16 rows at a time (LDS operations of a wave complete in order) and is written with
-// 16-byte stores.
-template <class C, int EPI>
-__device__ __forceinline__ void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[C::MI][NI], int grp,
-                                         int wq, int lane_in, uint8_t* stage) {
-  constexpr int MI = C::MI;
-  // the lane index through an empty asm: the staging offsets below are recomputed here instead of
-  // being hoisted out of the K loop (where they would take registers for the whole loop)
-  int lane = lane_in;
-  asm volatile("" : "+v"(lane));
-  __attribute__((address_space(3))) uint8_t* st = (__attribute__((address_space(3))) uint8_t*)stage;
-  constexpr int NB = EPI == EPI_STORE_BF16 ? NI : 1;  // output blocks per 32 rows
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-    const int row_base = (2 * mi + grp) * 32;  // first tile row of the block
-    if (row_base >= it.rows) continue;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      // ---- write the block into the staging area
-      if constexpr (EPI == EPI_SWIGLU_F32) {
-        // Two halves of 16 rows: the fp32 SwiGLU values go through the staging block (16 rows x 128
-        // bytes) and out as 32 bytes per lane (row lane / 4, columns 8 (lane % 4) ..+7).
-        const int cb = it.nt * 4 + wq;  // 32-column block of the output rows
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-          for (int r = 8 * hh; r < 8 * hh + 8; ++r) {
-            const int lrow = 8 * ((r >> 2) & 1) + 4 * (lane >> 5) + (r & 3);  // row within the half
-            const float act = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
-            *(__attribute__((address_space(3))) float*)(st + lrow * 128 + ((((lane & 31) >> 2) ^ (lrow & 7)) << 4) +
-                                                       (lane & 3) * 4) = act;
-          }
-          const int lrow = lane >> 2, part = lane & 3;
-          const v4f v0 = *LDSP(v4f, st + lrow * 128 + (((2 * part) ^ (lrow & 7)) << 4));
-          const v4f v1 = *LDSP(v4f, st + lrow * 128 + (((2 * part + 1) ^ (lrow & 7)) << 4));
-          const int row = hh * 16 + lrow;
-          if (row_base + row < it.rows) {
-            float* dst = (float*)p.C + (it.row0 + row_base + row) * p.ldc + cb * 32 + part * 8;
-            *(v4f*)dst = v0;
-            *(v4f*)(dst + 4) = v1;
-          }
-        }
-      } else {
-        // two halves of 16 rows: bf16 values into the staging block (16 rows x 64 bytes), then
-        // 16 bytes per lane (row lane / 4, columns 8 (lane % 4) ..+7) out
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-          for (int r = 8 * hh; r < 8 * hh + 8; ++r) {
-            const int row = 8 * ((r >> 2) & 1) + 4 * (lane >> 5) + (r & 3);  // row within the half
-            float v;
-            if constexpr (EPI == EPI_STORE_BF16) v = acc[mi][nb][r];
-            else v = swiglu_act(acc[mi][0][r], acc[mi][1][r]);
-            *(__attribute__((address_space(3))) uint16_t*)(st + stage_off(row, (lane & 31) * 2)) = f32_to_bf16(v);
-          }
-          const int row = lane >> 2, c = lane & 3;
-          const v4i v = *LDSP(v4i, st + stage_off(row, c * 16));
-          const int col = EPI == EPI_STORE_BF16 ? it.nt * BN + wq * WN + nb * 32 + c * 8
-                                                : it.nt * (BN / 2) + wq * 32 + c * 8;
-          if (row_base + hh * 16 + row < it.rows && col < p.N) {
-            const int64_t orow = it.row0 + row_base + hh * 16 + row;
-            *(v4i*)((uint16_t*)p.C + orow * p.ldc + col) = v;
-          }
-        }
-      }
-    }
-  }
 }
 
 template <bool MX, bool B_KN, int EPI, bool TALL>
@@ -500,7 +45,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   int32_t* s_rows = (int32_t*)(smem + C::ROWS_OFF);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = uni(tid >> 6);
+  const int wave = O::uni(tid >> 6);
   const int grp = wave >> 2, wq = wave & 3;
 
   // The work list: m-tiles of C::BM rows per group and their exclusive prefix, from group_list (the
@@ -543,28 +88,28 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
     if (tid == THREADS - 1) s_prefix[p.G] = run;
   }
   __syncthreads();
-  const int total = uni(s_prefix[p.G]) * p.n_tiles;
+  const int total = O::uni(s_prefix[p.G]) * p.n_tiles;
   const int nk = p.K * ESIZE / KB;
   const int grid = (int)gridDim.x;
   const int L0 = (int)(blockIdx.x & 7) * (grid >> 3) + (int)(blockIdx.x >> 3);
   if (L0 >= total) return;
   const int n_items = (total - L0 + grid - 1) / grid;
   const int nq = n_items * nk;
-  const uint32_t lds0 = uni((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem);
+  const uint32_t lds0 = O::uni((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem);
 
   // copy cursor: item cL, stage ck
   int cL = L0, ck = 0;
   Item ci;
-  decode<C>(p, smem, cL, ci);
+  decode<C, O>(p, smem, cL, ci);
   Plan<C::CPW_A> pl;
-  make_plan<C, B_KN, SWIGLU>(p, ci, wave, lane, pl);
+  make_plan<C, B_KN, SWIGLU, O>(p, ci, wave, lane, pl);
   auto issue_next = [&](int q) {
-    issue_stage<C, B_KN, SWIGLU>(p, pl, ck, lds0 + (uint32_t)((q % S) * S_SLOT), wave, lane);
+    issue_stage<C, B_KN, SWIGLU, O>(p, pl, ck, lds0 + (uint32_t)((q % S) * S_SLOT), wave, lane);
     if (++ck == nk) {
       if (cL + grid < total) {
         cL += grid;
-        decode<C>(p, smem, cL, ci);
-        make_plan<C, B_KN, SWIGLU>(p, ci, wave, lane, pl);
+        decode<C, O>(p, smem, cL, ci);
+        make_plan<C, B_KN, SWIGLU, O>(p, ci, wave, lane, pl);
         ck = 0;
       } else {
         ck = nk - 1;  // past the end: repeat the last stage into the free slot
@@ -575,11 +120,11 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   // compute cursor: item it, stage kk; `live`: this wave's 128 rows hold rows of the item
   int kL = L0, kk = 0;
   Item it;
-  decode<C>(p, smem, kL, it);
+  decode<C, O>(p, smem, kL, it);
   // row blocks of this wave's group that hold rows of the item; `live`: any
   auto row_blocks = [&]() {
     const int n = ((it.rows + 31) / 32 - grp + 1) / 2;
-    return uni(n < 0 ? 0 : (n > MI ? MI : n));
+    return O::uni(n < 0 ? 0 : (n > MI ? MI : n));
   };
   int nmi = row_blocks();
   bool live = nmi > 0;
@@ -593,7 +138,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
 
   auto finish_stage = [&]() {
     if (++kk == nk) {
-      if (live) epilogue<C, EPI>(p, it, acc, grp, wq, lane, smem + C::EPI_OFF + wave * C::EPI_BLOCK);
+      if (live) epilogue<C, EPI, O>(p, it, acc, grp, wq, lane, smem + C::EPI_OFF + wave * C::EPI_BLOCK);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -603,7 +148,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       kk = 0;
       kL += grid;
       if (kL < total) {
-        decode<C>(p, smem, kL, it);
+        decode<C, O>(p, smem, kL, it);
         nmi = row_blocks();
         live = nmi > 0;
       }
@@ -620,10 +165,10 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       const uint8_t* slot = smem + (q % S) * S_SLOT;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        if (live) read_frags<C, B_KN>(f, slot, h, grp, wq, lane, (int)(it.row0 & 3), nmi);
+        if (live) read_frags<C, B_KN, O>(f, slot, h, grp, wq, lane, (int)(it.row0 & 3), nmi);
         wait_lgkm0();
         __builtin_amdgcn_sched_barrier(0);
-        if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
+        if (live) mfmas<MX, B_KN, MI, O>(f, acc, nmi);
         __builtin_amdgcn_sched_barrier(0);
       }
       finish_stage();
@@ -634,22 +179,22 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
     for (int q = 0; q < nq; ++q) {
       issue_next(q + 1);
       if (q > 0) {  // half 1 of stage q - 1, read before the barrier
-        if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
+        if (live) mfmas<MX, B_KN, MI, O>(f, acc, nmi);
         finish_stage();
       }
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* slot = smem + (q % S) * S_SLOT;
-      if (live) read_frags<C, B_KN>(f, slot, 0, grp, wq, lane, (int)(it.row0 & 3), nmi);
+      if (live) read_frags<C, B_KN, O>(f, slot, 0, grp, wq, lane, (int)(it.row0 & 3), nmi);
       wait_lgkm0();
       __builtin_amdgcn_sched_barrier(0);
-      if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
+      if (live) mfmas<MX, B_KN, MI, O>(f, acc, nmi);
       __builtin_amdgcn_sched_barrier(0);
-      if (live) read_frags<C, B_KN>(f, slot, 1, grp, wq, lane, (int)(it.row0 & 3), nmi);
+      if (live) read_frags<C, B_KN, O>(f, slot, 1, grp, wq, lane, (int)(it.row0 & 3), nmi);
       wait_lgkm0();
       wait_vm0();
       barrier();
     }
-    if (live) mfmas<MX, B_KN, MI>(f, acc, nmi);
+    if (live) mfmas<MX, B_KN, MI, O>(f, acc, nmi);
     finish_stage();
   }
   wait_vm0();  // no copy may still write the LDS when the workgroup ends
@@ -671,17 +216,13 @@ int launch_pp_k(const GGParams& p, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
-// 320-row tiles for bf16 when the caller's row count averages at most 320 per group
-bool pp_tall(const GGParams& p, bool mx) {
-  return !mx && p.rows_hint > 0 && p.rows_hint <= (int64_t)p.G * 320 && p.G <= Cfg<false, true>::PREFIX_MAX;
-}
-
-template <bool MX, bool B_KN, int EPI>
-int launch_pp(const GGParams& p, hipStream_t stream) {
-  if constexpr (!MX)
-    if (pp_tall(p, MX)) return launch_pp_k<MX, B_KN, EPI, true>(p, stream);
-  return launch_pp_k<MX, B_KN, EPI, false>(p, stream);
-}
+struct DevLaunch {
+  hipStream_t stream;
+  template <bool MX, bool B_KN, int EPI, bool TALL>
+  int run(const GGParams& p) {
+    return launch_pp_k<MX, B_KN, EPI, TALL>(p, stream);
+  }
+};
 
 }  // namespace
 
@@ -713,12 +254,6 @@ bool mi355_gg_pp_usable(int variant, bool mx, bool b_kn, int64_t K, int G, int64
 
 int mi355_grouped_gemm_pp(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t stream) {
   if (!mi355_gg_pp_applies(p, mx, b_kn, epi)) return MI355MOE_EUNSUPPORTED;
-  if (!mx) {
-    if (!b_kn) return epi == EPI_STORE_BF16 ? launch_pp<false, false, EPI_STORE_BF16>(p, stream)
-                                            : launch_pp<false, false, EPI_SWIGLU_BF16>(p, stream);
-    return epi == EPI_STORE_BF16 ? launch_pp<false, true, EPI_STORE_BF16>(p, stream)
-                                 : launch_pp<false, true, EPI_SWIGLU_BF16>(p, stream);
-  }
-  return epi == EPI_STORE_BF16 ? launch_pp<true, true, EPI_STORE_BF16>(p, stream)
-                               : launch_pp<true, true, EPI_SWIGLU_F32>(p, stream);
+  DevLaunch L{stream};
+  return pp_select(p, mx, b_kn, epi, L);
 }

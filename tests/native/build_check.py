@@ -22,14 +22,17 @@ HERE = Path(__file__).resolve().parent
 REPO = HERE.parents[1]
 CSRC = REPO / "hyper_multicore_amd" / "csrc"
 OUT = HERE / "_build"
-LIB_SOURCES = ["api.hip", "backward.hip", "dispatch.hip", "quant.hip", "gemm.hip"]
+LIB_SOURCES = ["api.hip", "backward.hip", "dispatch.hip", "quant.hip", "gemm.hip", "gemm_pp.hip"]
 # internal functions defined by the checker instead (made weak in the library objects)
 REPLACED = {
     "gemm.hip": ["mi355_grouped_gemm", "mi355_plan_tiles", "mi355_plan_row_blocks"],
     "dispatch.hip": ["mi355_dispatch_enqueue", "mi355_dispatch_plan_enqueue", "mi355_permute_rows_enqueue", "mi355_unpermute_enqueue",
                      "mi355_zero_enqueue"],
     "quant.hip": ["mi355_mx_quant_rows", "mi355_mx_quant_grouped"],
+    "gemm_pp.hip": ["mi355_grouped_gemm_pp"],
 }
+# internal functions the checker wraps: linked under the name with the suffix `_lib`
+RENAMED = {"gemm_pp.hip": ["mi355_gg_pp_usable"]}
 FLAGS = ["-x", "hip", "--cuda-host-only", "-O1", "-g", "-std=c++17", "-fsanitize=address",
          "-fno-omit-frame-pointer", "-Wno-unused-result", "-Wno-unused-variable",
          f"-I{REPO / 'include'}"]
@@ -41,7 +44,7 @@ def _rocm() -> Path:
 
 def _inputs() -> list[Path]:
     files = [CSRC / f for f in LIB_SOURCES] + sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.inc"))
-    return files + [REPO / "include" / "mi355moe.h", HERE / "gemm_copy_check.cpp", Path(__file__)]
+    return files + [REPO / "include" / "mi355moe.h", HERE / "gemm_copy_check.cpp", HERE / "pp_sim.inc", Path(__file__)]
 
 
 def _digest() -> str:
@@ -86,6 +89,13 @@ def _build_locked() -> Path:
             if len(weak) < len(names):
                 raise RuntimeError(f"{src}: expected symbols {names}, found {weak}")
             _run(["objcopy", *[f"--weaken-symbol={s}" for s in weak], str(obj)])
+        for n in RENAMED.get(src, []):
+            syms = _run(["nm", str(obj)]).split()
+            found = [s for s in syms if re.fullmatch(rf"_Z{len(n)}{n}\w*", s)]
+            if len(found) != 1:
+                raise RuntimeError(f"{src}: expected one symbol {n}, found {found}")
+            new = found[0].replace(f"_Z{len(n)}{n}", f"_Z{len(n) + 4}{n}_lib", 1)
+            _run(["objcopy", f"--redefine-sym={found[0]}={new}", str(obj)])
         objs.append(obj)
     chk = OUT / "gemm_copy_check.o"
     _run([hipcc, *FLAGS, "-c", str(HERE / "gemm_copy_check.cpp"), "-o", str(chk)])

@@ -24,6 +24,7 @@
 // Usage: gemm_copy_check [scenario-name ...]   (no argument: all scenarios). Exit status 0 when
 // every check passed.
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -1256,10 +1257,18 @@ static int sim_dispatch(const GGParams& p, bool mx, bool b_kn, int epi) {
   return MI355MOE_EUNSUPPORTED;
 }
 
-// Library internals replaced by the simulation (same signatures as gemm.h)
-// The checker replays the 4-wave kernels' copy plans: the library's moe_forward is steered onto them
-// (the 8-wave configuration has its own GPU bit-identity tests against them).
-bool mi355_gg_pp_usable(int, bool, bool, int64_t, int, int64_t, int64_t) { return false; }
+// ------------------------------------------------------------------------------------------------
+// The 8-wave configuration (gemm_pp.hip): replayed when a scenario routes GEMMs to it as the library
+// does (g_pp_route); otherwise the library's forward is steered onto the 4-wave and decode kernels.
+static bool g_pp_route = false;
+#include "pp_sim.inc"
+
+// Library internals replaced by the simulation (same signatures as gemm.h). gemm_pp.hip's own
+// mi355_gg_pp_usable is linked under the name below.
+bool mi355_gg_pp_usable_lib(int variant, bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride);
+bool mi355_gg_pp_usable(int variant, bool mx, bool b_kn, int64_t K, int G, int64_t a_bytes, int64_t b_group_stride) {
+  return g_pp_route && mi355_gg_pp_usable_lib(variant, mx, b_kn, K, G, a_bytes, b_group_stride);
+}
 
 int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream_t, bool small) {
   // the dispatcher's choice of the numerics epilogue (gemm.hip, mi355_grouped_gemm)
@@ -1267,6 +1276,12 @@ int mi355_grouped_gemm(const GGParams& p, bool mx, bool b_kn, int epi, hipStream
   if (epi == EPI_SWIGLU_BF16 && (p.swiglu_limit > 0.0f || p.row_prob != nullptr)) epi = EPI_SWIGLU_BF16_NUM;
   if (g_force_big) small = false;
   if (small) return sim_dispatch<GGSmall>(p, mx, b_kn, epi);
+  // the 8-wave configuration first (gemm.hip's order); the 4-wave kernels for what it does not take
+  if (g_pp_route && (p.variant == MI355_GG_VARIANT_DEFAULT || p.variant == MI355_GG_VARIANT_PP)) {
+    const int rc = mi355_grouped_gemm_pp(p, mx, b_kn, epi, nullptr);
+    if (rc != MI355MOE_EUNSUPPORTED) return rc;
+  }
+  if (p.a_scale_stage_stride != 0 || p.c_scale_stage_stride != 0) return MI355MOE_EUNSUPPORTED;
   return sim_dispatch<GGBig>(p, mx, b_kn, epi);
 }
 int mi355_grouped_gemm_wgrad(const GGParams& p, int epi, hipStream_t, bool mx) {
@@ -1407,6 +1422,129 @@ static std::vector<int64_t> route_ids(int64_t T, int K, int E, double skew) {
     }
   }
   return ids;
+}
+
+// The 8-wave configuration on GGParams built here as the forward builds them (api.hip): routed rows
+// gathered from `fanout` slots per token, MX activation scales as stage-major code planes by routed
+// row, SwiGLU on [gate | up] weight columns (optionally gate/up interleaved). With g_emulate the
+// outputs are compared with the reference; for the MX SwiGLU GEMM the fp32 epilogue (the library's)
+// and the MXFP8 epilogue run on the same operands and the latter must equal the MX quantisation of
+// the former, byte for byte.
+static void pp_gemm(std::vector<int> counts, int K, int N, bool mx, bool b_kn, bool swiglu, int gu) {
+  const int G = (int)counts.size(), esize = mx ? 1 : 2;
+  const auto glv = cumsum(counts);
+  const int64_t R = glv.back();
+  const int fanout = 2;
+  const int64_t T = (R + fanout - 1) / fanout;
+  const int Ntot = swiglu ? 2 * N : N;
+  uint8_t* A = mk("pp_A", (size_t)T * K * esize);
+  int32_t* gather = (int32_t*)mk("pp_gather", (size_t)R * 4);
+  {
+    std::vector<int32_t> slots(T * fanout);
+    for (size_t i = 0; i < slots.size(); ++i) slots[i] = (int32_t)i;
+    std::shuffle(slots.begin(), slots.end(), g_rng);
+    for (int64_t r = 0; r < R; ++r) gather[r] = slots[r];
+  }
+  uint8_t* B = mk("pp_B", (size_t)G * K * Ntot * esize);
+  const int64_t planes = (int64_t)(K / 128) * 4 * R + 512;
+  uint8_t* as = mx ? mk("pp_A_scale_planes", (size_t)planes) : nullptr;
+  uint8_t* bs = mx ? mk("pp_col_scale", (size_t)G * (K / 64) * Ntot * 2) : nullptr;
+  int64_t* gl = (int64_t*)mk("pp_group_list", G * 8);
+  memcpy(gl, glv.data(), G * 8);
+  if (g_emulate) {
+    if (mx) {
+      fill_e4m3(A, (size_t)T * K);
+      fill_e4m3(B, (size_t)G * K * Ntot);
+      fill_codes(as, (size_t)planes);
+      fill_codes(bs, (size_t)G * (K / 64) * Ntot * 2);
+    } else {
+      fill_bf16(A, (size_t)T * K);
+      fill_bf16(B, (size_t)G * K * Ntot);
+    }
+  }
+  GGParams p = {};
+  p.A = A;
+  p.lda_bytes = (int64_t)K * esize;
+  p.a_bytes = T * K * esize;
+  p.a_row_index = gather;
+  p.a_row_div = fanout;
+  p.B = B;
+  p.b_group_stride = (int64_t)K * Ntot * esize;
+  p.b_row_bytes = b_kn ? (int64_t)Ntot * esize : (int64_t)K * esize;
+  p.K = K;
+  p.N = N;
+  p.Ntot = Ntot;
+  p.n_tiles = swiglu ? N / 128 : (N + 255) / 256;
+  p.G = G;
+  p.group_list = gl;
+  p.rows_hint = R;
+  p.gate_up_interleaved = gu;
+  p.variant = MI355_GG_VARIANT_DEFAULT;
+  if (mx) {
+    p.a_scale = as;
+    p.a_scale_stage_stride = R * 4;
+    p.a_scale_routed = 1;
+    p.b_scale = bs;
+    p.b_scale_group_stride = (int64_t)(K / 64) * Ntot * 2;
+  }
+  const int epi = !swiglu ? EPI_STORE_BF16 : (mx ? EPI_SWIGLU_F32 : EPI_SWIGLU_BF16);
+  p.C = mk("pp_C", (size_t)R * N * (epi == EPI_SWIGLU_F32 ? 4 : 2));
+  p.ldc = N;
+  expect_rc(mi355_grouped_gemm_pp(p, mx, b_kn, epi, nullptr), 0, "8-wave grouped GEMM");
+  if (!(mx && swiglu)) return;
+  // the MXFP8 SwiGLU epilogue on the same operands
+  GGParams q = p;
+  const int64_t cplanes = (int64_t)(N / 128) * 4 * R + 512;
+  q.C = mk("pp_act_e4m3", (size_t)R * N);
+  q.c_scale = mk("pp_act_planes", (size_t)cplanes);
+  q.c_scale_stage_stride = R * 4;
+  sim_pp<true, true, EPI_SWIGLU_MX, false>(q);
+  if (!g_emulate) return;
+  const float* f = (const float*)p.C;
+  const uint8_t* e = (const uint8_t*)q.C;
+  long bad = 0;
+  for (int64_t r = 0; r < R; ++r)
+    for (int cb = 0; cb < N / 32; ++cb) {
+      float amax = 0.0f;
+      for (int i = 0; i < 32; ++i) amax = std::max(amax, std::fabs(f[r * N + cb * 32 + i]));
+      const uint32_t code = mx_scale_code(amax);
+      const uint8_t got_code = q.c_scale[(cb >> 2) * q.c_scale_stage_stride + (cb & 3) * (q.c_scale_stage_stride >> 2) + r];
+      if (got_code != code && bad++ < 3) CHECK_FAIL("MX SwiGLU epilogue: scale code of row %lld block %d is %d, expected %u", (long long)r, cb, got_code, code);
+      for (int i = 0; i < 32; ++i) {
+        const uint8_t want = (uint8_t)(f32_to_e4m3(mx_apply_inv_scale(f[r * N + cb * 32 + i], code)) & 0xff);
+        if (e[r * N + cb * 32 + i] != want && bad++ < 3)
+          CHECK_FAIL("MX SwiGLU epilogue: element (%lld, %d) is 0x%02x, expected 0x%02x", (long long)r, cb * 32 + i,
+                     e[r * N + cb * 32 + i], want);
+      }
+    }
+  if (bad) CHECK_FAIL("MX SwiGLU epilogue: %ld bytes differ from the quantised fp32 epilogue", bad);
+}
+
+// runs f with replay fault `mutation` switched on: the scenario passes when the checks report it
+static std::function<void()> pp_mutant(int mutation, std::function<void()> f) {
+  return [mutation, f] {
+    const long e0 = g_errors;
+    g_pp_mutation = mutation;
+    g_pp_copy_no = 0;
+    f();
+    g_pp_mutation = 0;
+    const long found = g_errors - e0;
+    g_errors = e0;
+    if (found == 0) CHECK_FAIL("replay fault %d was not reported", mutation);
+    else printf("replay fault %d reported (%ld findings)\n", mutation, found);
+  };
+}
+
+// runs f with the library's GEMMs routed to the 8-wave configuration as the library routes them;
+// the scenario fails when no GEMM ran on it
+static std::function<void()> pp_route(std::function<void()> f) {
+  return [f] {
+    const long before = g_pp_gemms;
+    g_pp_route = true;
+    f();
+    g_pp_route = false;
+    if (g_pp_gemms == before) CHECK_FAIL("no GEMM ran on the 8-wave configuration");
+  };
 }
 
 static void moe_forward(int64_t T, int K, int E, int H, int I, int precision, int layout, double skew,
@@ -1635,6 +1773,43 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_moe_mx_gu_decode_halves", halves(emu([=] { moe_forward(16, 4, 16, 512, 256, MX, L_GU, 0.0); }))});
   s.push_back({"emu_wgrad_bf16", emu([=] { wgrad_direct({40, 0, 97, 33}, 256, 512, false, EPI_STORE_F32); })});
   s.push_back({"emu_wgrad_mx", emu([=] { wgrad_direct({40, 0, 97, 160}, 256, 256, true, EPI_STORE_F32); })});
+  // the 8-wave configuration: through the library (grouped GEMM C-ABI, the MegaMoE forward in both
+  // precisions and layouts, the no-allocation entry point) and directly on GGParams, with emulation
+  s.push_back({"pp_gemm_bf16_eio", pp_route([=] { gemm_bf16({100, 0, 300, 1, 129, 600}, 1024, 768, L_EIO); })});
+  s.push_back({"pp_gemm_bf16_eoi", pp_route([=] { gemm_bf16({100, 0, 300, 1, 129, 600}, 1024, 768, L_EOI); })});
+  s.push_back({"pp_gemm_bf16_eio_narrow", pp_route([=] { gemm_bf16({3, 40, 0, 513}, 128, 200, L_EIO); })});
+  s.push_back({"pp_gemm_bf16_many_items", pp_route([=] {
+                 std::vector<int> c(40, 300);
+                 gemm_bf16(c, 64, 2048, L_EOI);
+               })});
+  s.push_back({"pp_gemm_bf16_noalloc", pp_route([=] {
+                 gemm_bf16({300, 0, 513, 77, 1}, 512, 512, L_EIO, true);
+                 gemm_bf16({5, 400}, 256, 256, L_EOI, true);
+               })});
+  s.push_back({"pp_moe_bf16_eio_prefill", pp_route([=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); })});
+  s.push_back({"pp_moe_bf16_eoi_prefill", pp_route([=] { moe_forward(640, 2, 4, 256, 384, BF, L_EOI, 0.0); })});
+  s.push_back({"pp_moe_bf16_gu_prefill", pp_route([=] { moe_forward(640, 2, 4, 256, 384, BF, L_GU, 0.0); })});
+  s.push_back({"pp_moe_mx_eio_prefill", pp_route([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); })});
+  s.push_back({"pp_moe_mx_gu_prefill", pp_route([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); })});
+  s.push_back({"pp_moe_mx_gu_skewed", pp_route([=] { moe_forward(1500, 4, 12, 512, 256, MX, L_GU, 1.1); })});
+  s.push_back({"pp_moe_bf16_gu_skewed", pp_route([=] { moe_forward(1500, 4, 12, 512, 256, BF, L_GU, 1.1); })});
+  s.push_back({"pp_bf16_kn_store", [=] { pp_gemm({70, 0, 129, 300, 1, 513}, 1024, 768, false, true, false, 0); }});
+  s.push_back({"pp_mx_swiglu_gu", [=] { pp_gemm({70, 0, 129, 300, 1, 513}, 1024, 384, true, true, true, 1); }});
+  s.push_back({"emu_pp_bf16_kn_store", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 512, false, true, false, 0); })});
+  s.push_back({"emu_pp_bf16_nk_store", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 512, false, false, false, 0); })});
+  s.push_back({"emu_pp_bf16_kn_store_256", emu([=] { pp_gemm({700, 33, 300}, 128, 256, false, true, false, 0); })});
+  s.push_back({"emu_pp_bf16_kn_swiglu", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 256, false, true, true, 0); })});
+  s.push_back({"emu_pp_bf16_kn_swiglu_gu", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 256, false, true, true, 1); })});
+  s.push_back({"emu_pp_bf16_nk_swiglu", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 256, false, false, true, 0); })});
+  s.push_back({"emu_pp_mx_store", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 512, true, true, false, 0); })});
+  s.push_back({"emu_pp_mx_swiglu", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 256, true, true, true, 0); })});
+  s.push_back({"emu_pp_mx_swiglu_gu", emu([=] { pp_gemm({70, 0, 257, 1, 511}, 256, 256, true, true, true, 1); })});
+  s.push_back({"mut_pp_copy_offset", pp_mutant(1, emu([=] { pp_gemm({70, 129}, 256, 256, false, true, false, 0); }))});
+  s.push_back({"mut_pp_copy_oob", pp_mutant(2, [=] { pp_gemm({70, 129}, 256, 256, false, true, false, 0); })});
+  s.push_back({"mut_pp_copy_skipped", pp_mutant(3, [=] { pp_gemm({70, 129}, 256, 256, true, true, false, 0); })});
+  s.push_back({"mut_pp_staging", pp_mutant(4, emu([=] { pp_gemm({70, 129}, 256, 256, false, true, true, 0); }))});
+  s.push_back({"mut_pp_shuffle", pp_mutant(5, emu([=] { pp_gemm({70, 129}, 256, 256, true, true, true, 1); }))});
+  s.push_back({"mut_pp_rounding", pp_mutant(6, emu([=] { pp_gemm({70, 129}, 256, 256, true, true, true, 1); }))});
   // many groups: the tile prefix comes from global memory past the LDS copy
   s.push_back({"gemm_bf16_many_groups", [=] {
                  std::vector<int> c(1100, 0);

@@ -4,11 +4,15 @@ Builds tests/native/gemm_copy_check (the library's host code with every optional
 on, linked with host versions of the GEMM launches that replay each kernel's copy schedule) and
 runs its scenarios: the grouped GEMM C-ABI (bf16 / MXFP8, EIO / EOI weights, decode-shaped groups,
 more groups than the LDS tile prefix holds), the MegaMoE forward (both precisions and layouts, the
-numerics options) and the expert backward. For every copy of every work item, wave and lane the
-checker verifies the global source (inside a live allocation and equal to the element the fragment
-reads expect), the LDS destination slot, the vmcnt waits and the ring-slot reuse; the emu_* scenarios
-also run the kernels' fragment reads and MFMAs through an emulation of the lane-crossing instructions
-and compare the accumulators with a reference GEMM. See the header of tests/native/gemm_copy_check.cpp.
+numerics options) and the expert backward, on the 4-wave and decode kernels and (pp_* scenarios) on
+the default 8-wave kernel of gemm_pp.hip. For every copy of every work item, wave and lane the
+checker verifies the global source (inside a live allocation; for the 4-wave kernels also equal to
+the element the fragment reads expect), the LDS destination slot and the slot coverage, and for the
+4-wave kernels the vmcnt waits and the ring-slot reuse; the emu_* scenarios also run the kernels'
+fragment reads, MFMAs and (8-wave) epilogues through an emulation of the lane-crossing instructions
+and compare the results with a reference GEMM, and the 8-wave MXFP8 SwiGLU epilogue with the fp32
+one followed by the MX quantisation; the mut_pp_* scenarios switch on deliberate faults of the
+replay and pass when the checks report them. See tests/native/gemm_copy_check.cpp and pp_sim.inc.
 """
 import shutil
 import subprocess
@@ -38,11 +42,17 @@ SCENARIOS = [
     "moe_bf16_gu_decode_halves", "moe_mx_eoi_decode_halves", "emu_bf16_eio", "emu_bf16_eoi", "emu_mx_eio",
     "emu_mx_eoi", "emu_bf16_eio_decode", "emu_bf16_eoi_decode", "emu_mx_eio_decode", "emu_mx_eoi_decode",
     "emu_moe_mx_decode_halves", "emu_moe_bf16_decode_halves", "emu_moe_mx_gu_decode_halves", "emu_wgrad_bf16",
-    "emu_wgrad_mx", "gemm_bf16_many_groups", "gemm_bf16_noalloc", "moe_bf16_eio", "moe_bf16_eoi",
-    "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
-    "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu",
-    "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32",
-    "bwd_mx_bf16_prefill"
+    "emu_wgrad_mx", "pp_gemm_bf16_eio", "pp_gemm_bf16_eoi", "pp_gemm_bf16_eio_narrow", "pp_gemm_bf16_many_items",
+    "pp_gemm_bf16_noalloc", "pp_moe_bf16_eio_prefill", "pp_moe_bf16_eoi_prefill", "pp_moe_bf16_gu_prefill",
+    "pp_moe_mx_eio_prefill", "pp_moe_mx_gu_prefill", "pp_moe_mx_gu_skewed", "pp_moe_bf16_gu_skewed",
+    "pp_bf16_kn_store", "pp_mx_swiglu_gu", "emu_pp_bf16_kn_store", "emu_pp_bf16_nk_store",
+    "emu_pp_bf16_kn_store_256", "emu_pp_bf16_kn_swiglu", "emu_pp_bf16_kn_swiglu_gu", "emu_pp_bf16_nk_swiglu",
+    "emu_pp_mx_store", "emu_pp_mx_swiglu", "emu_pp_mx_swiglu_gu", "mut_pp_copy_offset", "mut_pp_copy_oob",
+    "mut_pp_copy_skipped", "mut_pp_staging", "mut_pp_shuffle", "mut_pp_rounding", "gemm_bf16_many_groups",
+    "gemm_bf16_noalloc", "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi",
+    "moe_mx_eoi_prefill", "moe_mx_eio_prefill", "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp",
+    "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16",
+    "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill"
 ]
 
 
