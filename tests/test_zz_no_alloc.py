@@ -34,15 +34,19 @@ def _case(counts, K, N, layout, seed, gpu):
     return x, w, gl
 
 
+@pytest.mark.parametrize("variant", ["default", "w4"])
 @pytest.mark.parametrize("layout", ["EIO", "EOI"])
-def test_noalloc_matches_workspace_form_twice(gpu, layout):
+def test_noalloc_matches_workspace_form_twice(gpu, layout, variant):
+    """Both configurations: the default one (8-wave kernel, which builds its work list from group_list)
+    and "w4" (the 4-wave kernel, which reads the tile plan from the static array, so the second,
+    smaller call must not read the first call's longer plan)."""
     from hyper_multicore_amd import ops
-    print(f"[no_alloc] layout {layout}", flush=True)
+    print(f"[no_alloc] layout {layout} variant {variant}", flush=True)
     first = _case([300, 0, 513, 77, 256, 1, 129, 40], 1024, 768, layout, 11, gpu)
     second = _case([5, 260, 0, 31], 512, 256, layout, 12, gpu)  # fewer groups and rows than the first
     for x, w, gl in (first, second):
-        ref = ops.grouped_gemm_bf16(x, w, gl, layout)
-        out = _noalloc(x, w, gl, layout)
+        ref = ops.grouped_gemm_bf16(x, w, gl, layout, gemm_variant=variant)
+        out = _noalloc(x, w, gl, layout, variant)
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16).cpu(), ref.view(torch.int16).cpu())
     # and against the fp32 product of the second case (the bytes compared above are the right ones)
