@@ -3,10 +3,13 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use this module; the
 product package never imports it. Each function cites the reference code it restates.
 
-Pinning (see tests/test_oracle.py): the route against the closed torch forms and the
-DeepSeek-V3 grouped form; route metadata and the permutation against the reference tests'
-known answers (tests/golden/*.json); MX quantisation against torch's own float8_e4m3fn cast and
-the OCP MX invariants; the expert math against the TorchExperts loop and closed forms.
+Pinning (see tests/test_oracle.py and tests/test_oracle_mx_closed_form.py): the route against the
+closed torch forms and the DeepSeek-V3 grouped form; route metadata and the permutation against the
+reference tests' known answers (tests/golden/*.json); MX quantisation against torch's own
+float8_e4m3fn cast, known-answer blocks and an independent brute-force quantiser; the bf16 expert
+math against the TorchExperts loop and closed forms, the MXFP8 expert math against an independent
+single-expert closed form with mutation checks. Parity unpinned: the MX backward's rounding point
+noted at expert_backward_reference_mx.
 """
 from __future__ import annotations
 
