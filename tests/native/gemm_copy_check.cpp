@@ -1793,6 +1793,17 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"pp_moe_mx_gu_prefill", pp_route([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); })});
   s.push_back({"pp_moe_mx_gu_skewed", pp_route([=] { moe_forward(1500, 4, 12, 512, 256, MX, L_GU, 1.1); })});
   s.push_back({"pp_moe_bf16_gu_skewed", pp_route([=] { moe_forward(1500, 4, 12, 512, 256, BF, L_GU, 1.1); })});
+  // variant "pp": the 8-wave kernel also on decode-shaped groups (1-40 rows, many empty)
+  auto variant_pp = [](std::function<void()> f) {
+    return [f] {
+      g_variant = MI355_GG_VARIANT_PP;
+      f();
+      g_variant = 0;
+    };
+  };
+  s.push_back({"pp_moe_mx_gu_decode_variant", pp_route(variant_pp([=] { moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0); }))});
+  s.push_back({"pp_moe_bf16_eio_decode_variant", pp_route(variant_pp([=] { moe_forward(32, 8, 64, 1024, 512, BF, L_EIO, 0.0); }))});
+  s.push_back({"pp_gemm_bf16_decode_variant", pp_route(variant_pp([=] { gemm_bf16(decode_counts(64, 5), 1024, 768, L_EOI); }))});
   s.push_back({"pp_bf16_kn_store", [=] { pp_gemm({70, 0, 129, 300, 1, 513}, 1024, 768, false, true, false, 0); }});
   s.push_back({"pp_mx_swiglu_gu", [=] { pp_gemm({70, 0, 129, 300, 1, 513}, 1024, 384, true, true, true, 1); }});
   s.push_back({"emu_pp_bf16_kn_store", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 512, false, true, false, 0); })});

@@ -45,6 +45,7 @@ SCENARIOS = [
     "emu_wgrad_mx", "pp_gemm_bf16_eio", "pp_gemm_bf16_eoi", "pp_gemm_bf16_eio_narrow", "pp_gemm_bf16_many_items",
     "pp_gemm_bf16_noalloc", "pp_moe_bf16_eio_prefill", "pp_moe_bf16_eoi_prefill", "pp_moe_bf16_gu_prefill",
     "pp_moe_mx_eio_prefill", "pp_moe_mx_gu_prefill", "pp_moe_mx_gu_skewed", "pp_moe_bf16_gu_skewed",
+    "pp_moe_mx_gu_decode_variant", "pp_moe_bf16_eio_decode_variant", "pp_gemm_bf16_decode_variant",
     "pp_bf16_kn_store", "pp_mx_swiglu_gu", "emu_pp_bf16_kn_store", "emu_pp_bf16_nk_store",
     "emu_pp_bf16_kn_store_256", "emu_pp_bf16_kn_swiglu", "emu_pp_bf16_kn_swiglu_gu", "emu_pp_bf16_nk_swiglu",
     "emu_pp_mx_store", "emu_pp_mx_swiglu", "emu_pp_mx_swiglu_gu", "mut_pp_copy_offset", "mut_pp_copy_oob",
