@@ -3,6 +3,7 @@
 // All launches are enqueued on the caller's stream; nothing synchronises the host.
 #include "common.h"
 #include "gemm.h"
+#include "decode_prep.h"
 #include <cmath>
 #include <algorithm>
 #include <mutex>
@@ -412,16 +413,43 @@ extern "C" int mi355moe_moe_forward(const MI355MoeForwardArgs* args, void* works
   int32_t* tile_prefix = (int32_t*)(ws + L.tile_prefix);
   // decode shapes (few routed rows per expert) use the 64-row tiles; the dispatch scan writes their plan
   const bool small = mi355_use_small_tiles(T * K, E, a.gemm_variant);
-  rc = mi355_dispatch_plan_enqueue(a.topk_ids, a.ids_dtype, T, K, E, counts, group_list, mapping, gather, a.error_flag,
-                                   ws + L.dispatch, tile_prefix, mi355_gg_bm(small), st);
-  if (rc) return rc;
   const uint8_t* a1 = (const uint8_t*)a.hidden;
   // MX on the 8-wave GEMM: activation scales stage-major (one 4-byte copy per row and 128-K stage);
   // the 64-row tiles read row-major scales and a tile plan in 64-row units
   const bool pp_mx = mx && !eoi && !small &&
                      mi355_gg_pp_usable(a.gemm_variant, true, true, H, E, T * H, (int64_t)H * 2 * I) &&
                      mi355_gg_pp_usable(a.gemm_variant, true, true, I, E, T * K * I, (int64_t)I * H);
-  if (mx) {
+  // decode: the dispatch and the token quantisation in one launch
+  const bool one_launch = small && mi355_decode_prep_enabled() && dprep::applies(T * K, E);
+  if (one_launch) {
+    dprep::Args d = {};
+    d.ids = a.topk_ids;
+    d.slots = T * K;
+    d.E = E;
+    d.counts = counts;
+    d.group_list = group_list;
+    d.mapping = mapping;
+    d.gather = gather;
+    d.error_flag = a.error_flag;
+    d.tile_prefix = tile_prefix;
+    d.bm = mi355_gg_bm(true);
+    if (mx) {
+      d.x = a.hidden;
+      d.rows = T;
+      d.cols = H;
+      d.q = (uint8_t*)(ws + L.xq);
+      d.scale = (uint8_t*)(ws + L.xs);
+      d.scale_ld = mi355_mx_scale_ld(H);
+    }
+    rc = mi355_decode_prep_enqueue(d, a.ids_dtype, st);
+  } else {
+    rc = mi355_dispatch_plan_enqueue(a.topk_ids, a.ids_dtype, T, K, E, counts, group_list, mapping, gather,
+                                     a.error_flag, ws + L.dispatch, tile_prefix, mi355_gg_bm(small), st);
+  }
+  if (rc) return rc;
+  if (mx && one_launch) {
+    a1 = (const uint8_t*)(ws + L.xq);
+  } else if (mx) {
     // with the 8-wave GEMM the token scales go to each token's routed rows (read in tile order)
     if (pp_mx)
       rc = mi355_mx_quant_tokens_to_planes(a.hidden, T, H, (uint8_t*)(ws + L.xq), (uint8_t*)(ws + L.tok_codes), gather,

@@ -16,6 +16,8 @@
 #pragma clang fp contract(off)
 #include "common.h"
 #include "scan.h"
+#include "decode_prep.h"
+#include "gemm.h"
 #include "../../include/mi355moe.h"
 
 #define DISPATCH_MAX_EXPERTS 4096
@@ -243,6 +245,29 @@ extern "C" int mi355moe_dispatch(const MI355MoeDispatchArgs* args, void* workspa
   return mi355_dispatch_enqueue(a.topk_ids, a.ids_dtype, a.num_tokens, a.top_k, a.num_experts, a.counts,
                                 a.expert_offsets, a.group_list, a.mapping, a.gather_index, a.error_flag,
                                 workspace, (hipStream_t)stream);
+}
+
+// The decode prologue in one launch (decode_prep.h): workgroup 0 the dispatch, the others the MX
+// token quantisation.
+template <bool I64>
+__global__ __launch_bounds__(dprep::THREADS) void decode_prep_kernel(dprep::Args a) {
+  __shared__ dprep::Lds s;
+  dprep::Dev o;
+  dprep::run(o, a, I64, s, (int)blockIdx.x);
+}
+
+int mi355_decode_prep_enqueue(const dprep::Args& a, int dtype, hipStream_t stream) {
+  if (!dprep::applies(a.slots, a.E) || a.mapping == nullptr) return MI355MOE_EINVAL;
+  if (a.rows > 0 && (a.cols <= 0 || a.cols % 32 || a.x == nullptr || a.q == nullptr || a.scale == nullptr ||
+                     a.scale_ld < a.cols / 32))
+    return MI355MOE_EINVAL;
+  const int64_t wg = 1 + (a.rows > 0 ? dprep::quant_workgroups(a.rows, a.cols) : 0);
+  if (wg > INT32_MAX) return MI355MOE_EINVAL;
+  if (dtype == MI355MOE_IDS_INT64)
+    hipLaunchKernelGGL(decode_prep_kernel<true>, dim3((unsigned)wg), dim3(dprep::THREADS), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_prep_kernel<false>, dim3((unsigned)wg), dim3(dprep::THREADS), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? MI355MOE_OK : MI355MOE_ELAUNCH;
 }
 
 // routed[mapping[s]] = x[s / K], 16-byte vectors; one block row per slot.

@@ -1,5 +1,7 @@
 // Feature gates of the optional paths (reported by mi355moe_features).
 #pragma once
+#include <stdlib.h>
+#include <string.h>
 
 // Optional paths. Each was switched on after its GPU parity tests passed; a path switched off answers
 // MI355MOE_EUNSUPPORTED (or the forward keeps the default tiles) and mi355moe_features() clears its
@@ -19,3 +21,11 @@ inline bool mi355_route_grad_enabled() { return true; }
 inline bool mi355_mx_weight_prep_enabled() { return true; }
 // MXFP8 expert backward (needs the MX K-contiguous GEMM path for its data-gradient GEMMs).
 inline bool mi355_mx_backward_enabled() { return true; }
+// The one-launch decode prologue (dispatch + MX token quantisation, decode_prep.h) of the MegaMoE
+// forward on the 64-row tiles. Host-checked; until its GPU parity tests have passed it runs only
+// while MI355MOE_DECODE_PREP=1 is set in the environment (read at each forward call, so a test can
+// compare both prologues in one process).
+inline bool mi355_decode_prep_enabled() {
+  const char* v = getenv("MI355MOE_DECODE_PREP");
+  return v != nullptr && strcmp(v, "1") == 0;
+}

@@ -145,6 +145,10 @@ int mi355_dispatch_enqueue(const void* ids, int dtype, int64_t num_tokens, int t
 int mi355_dispatch_plan_enqueue(const void* ids, int dtype, int64_t num_tokens, int top_k, int E, int32_t* counts,
                                 int64_t* group_list, int32_t* mapping, int32_t* gather_index, int32_t* error_flag,
                                 void* workspace, int32_t* tile_prefix, int bm, hipStream_t stream);
+// The decode prologue (dispatch + MX token quantisation) in one launch (decode_prep.h); dprep::applies
+// must hold.
+namespace dprep { struct Args; }
+int mi355_decode_prep_enqueue(const dprep::Args& a, int dtype, hipStream_t stream);
 int mi355_zero_enqueue(void* p, size_t bytes, hipStream_t st);
 int mi355_permute_rows_enqueue(const uint16_t* x, int64_t slots, int K, int H, const int32_t* mapping,
                                 uint16_t* routed, hipStream_t st);

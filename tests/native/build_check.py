@@ -6,7 +6,10 @@ checker replaces are made weak, and everything is linked with ``gemm_copy_check.
 runtime. Output goes to ``tests/native/_build`` (git-ignored); a build is reused while no input
 changed.
 
-    python tests/native/build_check.py      # builds and prints the binary path
+    python tests/native/build_check.py      # builds and prints the binary paths
+
+``build_prep()`` builds ``prep_check``: the one-launch decode prologue (decode_prep.h) under the host
+emulation of ``prep_sim.inc``, also with AddressSanitizer.
 """
 from __future__ import annotations
 
@@ -27,7 +30,7 @@ LIB_SOURCES = ["api.hip", "backward.hip", "dispatch.hip", "quant.hip", "gemm.hip
 REPLACED = {
     "gemm.hip": ["mi355_grouped_gemm", "mi355_plan_tiles", "mi355_plan_row_blocks"],
     "dispatch.hip": ["mi355_dispatch_enqueue", "mi355_dispatch_plan_enqueue", "mi355_permute_rows_enqueue", "mi355_unpermute_enqueue",
-                     "mi355_zero_enqueue"],
+                     "mi355_zero_enqueue", "mi355_decode_prep_enqueue"],
     "quant.hip": ["mi355_mx_quant_rows", "mi355_mx_quant_grouped"],
     "gemm_pp.hip": ["mi355_grouped_gemm_pp"],
 }
@@ -44,7 +47,8 @@ def _rocm() -> Path:
 
 def _inputs() -> list[Path]:
     files = [CSRC / f for f in LIB_SOURCES] + sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.inc"))
-    return files + [REPO / "include" / "mi355moe.h", HERE / "gemm_copy_check.cpp", HERE / "pp_sim.inc", Path(__file__)]
+    return files + [REPO / "include" / "mi355moe.h", HERE / "gemm_copy_check.cpp", HERE / "pp_sim.inc", HERE / "prep_sim.inc",
+                     Path(__file__)]
 
 
 def _digest() -> str:
@@ -109,11 +113,38 @@ def _build_locked() -> Path:
     stub_o = OUT / "fatbin_stub.o"
     _run(["gcc", "-c", str(stub), "-o", str(stub_o)])
     clangxx = str(_rocm() / "llvm" / "bin" / "clang++")
-    _run([clangxx, "-fsanitize=address", *map(str, objs), str(stub_o), "-o", str(exe)])
+    _run([clangxx, "-fsanitize=address", "-pthread", *map(str, objs), str(stub_o), "-o", str(exe)])
     stamp.write_text(digest)
     return exe
 
 
+PREP_INPUTS = [CSRC / "decode_prep.h", CSRC / "common.h", HERE / "prep_sim.inc", HERE / "prep_check.cpp"]
+
+
+def build_prep() -> Path:
+    """Build tests/native/_build/prep_check once per source digest (same lock as build())."""
+    OUT.mkdir(parents=True, exist_ok=True)
+    with open(OUT / ".lock", "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        exe = OUT / "prep_check"
+        stamp = OUT / "prep_stamp"
+        h = hashlib.sha256()
+        for f in PREP_INPUTS + [Path(__file__)]:
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+        digest = h.hexdigest()[:16]
+        if exe.exists() and stamp.exists() and stamp.read_text() == digest:
+            return exe
+        hipcc = str(_rocm() / "bin" / "hipcc")
+        obj = OUT / "prep_check.o"
+        _run([hipcc, *FLAGS, "-c", str(HERE / "prep_check.cpp"), "-o", str(obj)])
+        clangxx = str(_rocm() / "llvm" / "bin" / "clang++")
+        _run([clangxx, "-fsanitize=address", "-pthread", str(obj), "-o", str(exe)])
+        stamp.write_text(digest)
+        return exe
+
+
 if __name__ == "__main__":
     print(build())
+    print(build_prep())
     sys.exit(0)

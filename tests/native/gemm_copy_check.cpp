@@ -257,6 +257,48 @@ int mi355_dispatch_plan_enqueue(const void* ids, int dtype, int64_t T, int K, in
   if (rc) return rc;
   return mi355_plan_tiles(group_list, E, tile_prefix, st, bm == mi355_gg_bm(true));
 }
+// The one-launch decode prologue: the kernel's own code (decode_prep.h) under the host emulation of
+// prep_sim.inc, checked against the host dispatch above and the host tile plan. Under g_force_big the
+// plan is then rewritten at the 256-row height the GEMM replays assume.
+#include "prep_sim.inc"
+static long g_preps = 0;
+int mi355_decode_prep_enqueue(const dprep::Args& a, int dtype, hipStream_t st) {
+  if (!dprep::applies(a.slots, a.E) || a.mapping == nullptr) return MI355MOE_EINVAL;
+  const bool i64 = dtype == MI355MOE_IDS_INT64;
+  check_span(a.ids, 0, a.slots * (i64 ? 8 : 4), "decode prologue ids");
+  check_span(a.mapping, 0, a.slots * 4, "decode prologue mapping");
+  if (a.gather) check_span(a.gather, 0, a.slots * 4, "decode prologue gather");
+  if (a.counts) check_span(a.counts, 0, (int64_t)a.E * 4, "decode prologue counts");
+  if (a.group_list) check_span(a.group_list, 0, (int64_t)a.E * 8, "decode prologue group_list");
+  if (a.tile_prefix) check_span(a.tile_prefix, 0, (int64_t)(a.E + 1) * 4, "decode prologue tile plan");
+  if (a.rows > 0) {
+    check_span(a.x, 0, a.rows * a.cols * 2, "decode prologue tokens");
+    check_span(a.q, 0, a.rows * a.cols, "decode prologue e4m3 tokens");
+    check_span(a.scale, 0, (a.rows - 1) * a.scale_ld + a.cols / 32, "decode prologue token scales");
+  }
+  if (prep_sim::run(a, i64) != 0) return MI355MOE_EINVAL;
+  ++g_preps;
+  // the host dispatch and plan on copies
+  const int E = a.E;
+  std::vector<int32_t> counts(E), mapping(a.slots), gather(a.slots, -1), prefix(E + 1);
+  std::vector<int64_t> gl(E);
+  const int T = (int)a.slots;  // the host dispatch takes T * K slots: K = 1
+  mi355_dispatch_enqueue(a.ids, dtype, T, 1, E, counts.data(), nullptr, gl.data(), mapping.data(), gather.data(),
+                         nullptr, nullptr, st);
+  for (int e = 0, run = 0; e < E; ++e) {
+    prefix[e] = run;
+    run += (int)((counts[e] + a.bm - 1) / a.bm);
+    prefix[E] = run;
+  }
+  if (memcmp(mapping.data(), a.mapping, a.slots * 4)) CHECK_FAIL("decode prologue: mapping differs");
+  const int64_t routed = gl[E - 1];
+  if (a.gather && memcmp(gather.data(), a.gather, routed * 4)) CHECK_FAIL("decode prologue: gather differs");
+  if (a.counts && memcmp(counts.data(), a.counts, E * 4)) CHECK_FAIL("decode prologue: counts differ");
+  if (a.group_list && memcmp(gl.data(), a.group_list, E * 8)) CHECK_FAIL("decode prologue: group_list differs");
+  if (a.tile_prefix && memcmp(prefix.data(), a.tile_prefix, (E + 1) * 4)) CHECK_FAIL("decode prologue: tile plan differs");
+  if (a.tile_prefix && g_force_big && a.group_list) return mi355_plan_tiles(a.group_list, E, a.tile_prefix, st, false);
+  return MI355MOE_OK;
+}
 int mi355_zero_enqueue(void* p, size_t bytes, hipStream_t) {
   if (bytes && !find_alloc(p, bytes)) {
     CHECK_FAIL("zero fill of %zu bytes outside every allocation", bytes);
@@ -1859,6 +1901,8 @@ static std::vector<Scenario> scenarios() {
 }
 
 int main(int argc, char** argv) {
+  // every optional path on: also the one-launch decode prologue (read once by the library)
+  setenv("MI355MOE_DECODE_PREP", "1", 1);
   const auto all = scenarios();
   if (argc == 2 && std::string(argv[1]) == "--list") {
     for (const auto& sc : all) printf("%s\n", sc.name);
@@ -1870,11 +1914,12 @@ int main(int argc, char** argv) {
     for (int i = 1; i < argc; ++i) pick |= std::string(argv[i]) == sc.name;
     if (!pick) continue;
     g_scenario = sc.name;
-    const long e0 = g_errors, c0 = g_copies, i0 = g_items, m0 = g_gemms, u0 = g_emulated_items;
+    const long e0 = g_errors, c0 = g_copies, i0 = g_items, m0 = g_gemms, u0 = g_emulated_items, p0 = g_preps;
     sc.run();
     free_all();
-    printf("%-32s %s  gemms=%ld items=%ld copies=%ld emulated=%ld\n", sc.name, g_errors == e0 ? "ok" : "FAILED",
-           g_gemms - m0, g_items - i0, g_copies - c0, g_emulated_items - u0);
+    printf("%-32s %s  gemms=%ld items=%ld copies=%ld emulated=%ld preps=%ld\n", sc.name,
+           g_errors == e0 ? "ok" : "FAILED", g_gemms - m0, g_items - i0, g_copies - c0, g_emulated_items - u0,
+           g_preps - p0);
     fflush(stdout);
     ++ran;
   }

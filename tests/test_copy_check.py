@@ -12,7 +12,9 @@ the element the fragment reads expect), the LDS destination slot and the slot co
 fragment reads, MFMAs and (8-wave) epilogues through an emulation of the lane-crossing instructions
 and compare the results with a reference GEMM, and the 8-wave MXFP8 SwiGLU epilogue with the fp32
 one followed by the MX quantisation; the mut_pp_* scenarios switch on deliberate faults of the
-replay and pass when the checks report them. See tests/native/gemm_copy_check.cpp and pp_sim.inc.
+replay and pass when the checks report them. Decode-shaped forwards run the one-launch decode
+prologue's code under a host emulation of its workgroup (prep_sim.inc) and compare its dispatch and
+tile plan with the checker's own. See tests/native/gemm_copy_check.cpp, pp_sim.inc and prep_sim.inc.
 """
 import shutil
 import subprocess
@@ -69,3 +71,6 @@ def test_copy_schedule(checker, name):
     r = subprocess.run([str(checker), name], capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, f"{r.stdout}\n{r.stderr}"
     assert f"{name}" in r.stdout and " ok " in r.stdout
+    if name.startswith(("moe_", "emu_moe_")) and "decode" in name:
+        # decode-shaped forwards take the one-launch prologue (its code under the host emulation)
+        assert "preps=1" in r.stdout, r.stdout
