@@ -187,3 +187,24 @@ def test_mutations_detected(prep, mutation):
     with pytest.raises(AssertionError):
         _check_dispatch(res, ids, 256, 64)
         _check_quant(res, x)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_dispatches(prep, seed):
+    """Seeded random shapes inside the limits: any slot count and expert count, both id types, skewed
+    routing (a few hot experts), a sprinkle of invalid ids, any tile height."""
+    rng = np.random.default_rng(100 + seed)
+    E = int(rng.integers(1, MAX_EXPERTS + 1))
+    slots = int(rng.integers(1, MAX_SLOTS + 1))
+    dtype = np.int64 if seed % 2 else np.int32
+    if seed % 3 == 0:  # hot experts
+        hot = rng.integers(0, E, 3)
+        ids = np.where(rng.random(slots) < 0.7, hot[rng.integers(0, 3, slots)], rng.integers(0, E, slots))
+    else:
+        ids = rng.integers(0, E, slots)
+    ids = ids.astype(dtype)
+    if seed % 4 == 1:
+        bad = rng.choice(slots, max(1, slots // 500), replace=False)
+        ids[bad] = E if dtype == np.int32 else (1 << 33)
+    bm = int(rng.choice([1, 64, 256, 320]))
+    _check_dispatch(prep(ids, E, bm, None), ids, E, bm)
