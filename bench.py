@@ -259,25 +259,34 @@ def measured_traffic(workload: str, variant: str, layout: str, root: str = ROOT)
     """HBM bytes per GMM1 launch from the committed rocprofv3 counter passes of the same workload,
     GEMM variant and weight layout (profiles/traffic_<workload>_<variant>_<layout>.json, written by
     ``--summarize``: FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the factor the same
-    counter reads for a plain copy kernel of known size), or None when no such record exists."""
+    counter reads for a plain copy kernel of known size), and the record's state:
+      "current"  the record's kernel has the same machine code in the library this run loaded
+                 (``code_digest`` of hyper_multicore_amd/codeobj.py);
+      "stale"    the kernel's code changed since the counter runs: no traffic is reported;
+      "none"     no record (no traffic)."""
     path = os.path.join(root, "profiles", f"traffic_{workload}_{variant}_{layout}.json")
     if not os.path.exists(path):
-        return None
+        return None, "none"
     with open(path) as f:
         rec = json.load(f)
-    return round((rec["fetch_kib"] * rec["fetch_factor"] + rec["write_kib"] * rec["write_factor"]) * 1024.0)
+    from hyper_multicore_amd import _lib, codeobj
+    sym, digest = rec.get("symbol"), rec.get("code_digest")
+    if sym is None or digest is None or codeobj.kernel_digests(str(_lib.LIB_PATH)).get(sym) != digest:
+        return None, "stale"
+    return round((rec["fetch_kib"] * rec["fetch_factor"] + rec["write_kib"] * rec["write_factor"]) * 1024.0), "current"
 
 
-def roofline(c: dict, work: dict, gmm1_ms: float, traffic=None) -> dict:
+def roofline(c: dict, work: dict, gmm1_ms: float, traffic=None, traffic_record: str = "none") -> dict:
     """Roofline of the GMM1 kernel (grouped GEMM + SwiGLU epilogue): algorithmic bytes or flops per
     launch over its average launch duration (HIP events around that one kernel on the library's
-    stream). traffic = measured HBM bytes per launch (None without a counter record)."""
+    stream). traffic = measured HBM bytes per launch (None without a current counter record);
+    traffic_record = the record's state (measured_traffic)."""
     mx = c["precision"] == "mxfp8"
     peak_flops = PEAK["mxfp8" if mx else "bf16"]
     t_mfma = work["g1_flops"] / peak_flops
     t_hbm = work["g1_bytes"] / PEAK["hbm"]
     sec = gmm1_ms * 1e-3
-    common = {"traffic": traffic, "algorithmic_bytes": round(work["g1_bytes"]),
+    common = {"traffic": traffic, "traffic_record": traffic_record, "algorithmic_bytes": round(work["g1_bytes"]),
               "traffic_ratio": None if traffic is None else round(traffic / work["g1_bytes"], 3),
               "kernel": "grouped_gemm GMM1+SwiGLU", "launch_ms": round(gmm1_ms, 4)}
     if t_hbm > t_mfma:
@@ -383,8 +392,7 @@ def run_config(name: str, device, steps: int, warmup: int, variant: str = "defau
         "m_tiles": m_tiles(c, counts, variant, bool(layer.ops.features() & layer._lib.FEATURE_DECODE_TILES)),
         "weight_layout": layer.layout,
         "stage_ms": {k: round(v, 4) for k, v in m["stage_ms"].items()},
-        "roofline": roofline(c, work, m["stage_ms"]["gmm1"],
-                             measured_traffic(name, variant, layer.layout)),
+        "roofline": roofline(c, work, m["stage_ms"]["gmm1"], *measured_traffic(name, variant, layer.layout)),
         "graph": measure_graph(layer, steps),
     }
     return res, layer
@@ -511,8 +519,15 @@ def summarize(workload: str, out: str, dest: str = os.path.join(ROOT, "profiles"
     txt = os.path.join(dest, f"grouped_gemm_{workload}.txt")
     with open(txt, "w") as f:
         f.write("\n".join(lines) + "\n")
+    from hyper_multicore_amd import _lib, codeobj
+    # the library this summary runs beside is the one the counter runs loaded (the same tree)
+    found = codeobj.find_kernel(str(_lib.LIB_PATH), g1) if _lib.LIB_PATH.exists() else None
+    if found is None:
+        print(f"[summarize] {g1} is not in {_lib.LIB_PATH}: the record gets no code digest and reads as stale",
+              file=sys.stderr)
+        found = (None, None)
     with open(os.path.join(dest, f"traffic_{workload}_{variant}_{layout}.json"), "w") as f:
-        json.dump({"kernel": g1, "fetch_kib": round(fetch, 1), "fetch_factor": round(fetch_factor, 4),
+        json.dump({"kernel": g1, "symbol": found[0], "code_digest": found[1], "fetch_kib": round(fetch, 1), "fetch_factor": round(fetch_factor, 4),
                    "write_kib": round(write, 1), "write_factor": round(write_factor, 4),
                    "mfma_util_pct": round(mfma, 2), "rocprof_avg_us": round(avg_us, 1),
                    "rocprof_timed_us": round(timed_us, 1),

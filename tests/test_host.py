@@ -1,4 +1,5 @@
 """Host-side logic of the drop-in modules (CPU only; no kernel launches)."""
+import os
 import pytest
 import torch
 
@@ -99,22 +100,72 @@ def test_ops_reject_cpu_tensors():
         ops.mx_quantize_rows(torch.zeros(4, 32, dtype=torch.bfloat16))
 
 
+def _built_kernel():
+    """(mangled symbol, code digest) of the bf16 prefill GMM1 kernel of the built library, or skip."""
+    from hyper_multicore_amd import _lib, codeobj
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("native library not built")
+    found = codeobj.find_kernel(str(_lib.LIB_PATH), PP_BF16_GMM1)
+    assert found is not None
+    return found
+
+
+PP_BF16_GMM1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true>(GGParams)"
+
+
 def test_bench_traffic_record(tmp_path):
     """roofline.traffic comes from a committed counter record of the same workload and GEMM variant:
-    FETCH_SIZE / WRITE_SIZE KiB per dispatch, each times its copy-kernel calibration factor."""
+    FETCH_SIZE / WRITE_SIZE KiB per dispatch, each times its copy-kernel calibration factor, and only
+    while the record's kernel has the same machine code in the library (code digest)."""
     import json
     import bench
+    sym, digest = _built_kernel()
     (tmp_path / "profiles").mkdir()
-    rec = {"fetch_kib": 1000.0, "fetch_factor": 0.5, "write_kib": 10.0, "write_factor": 2.0}
+    rec = {"fetch_kib": 1000.0, "fetch_factor": 0.5, "write_kib": 10.0, "write_factor": 2.0, "symbol": sym,
+           "code_digest": digest}
     (tmp_path / "profiles" / "traffic_dsv3_bf16_w4_EOI.json").write_text(json.dumps(rec))
-    assert bench.measured_traffic("dsv3_bf16", "w4", "EOI", root=str(tmp_path)) == (500 + 20) * 1024
-    assert bench.measured_traffic("dsv3_bf16", "w4", "EIO", root=str(tmp_path)) is None
-    assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) is None
+    assert bench.measured_traffic("dsv3_bf16", "w4", "EOI", root=str(tmp_path)) == ((500 + 20) * 1024, "current")
+    assert bench.measured_traffic("dsv3_bf16", "w4", "EIO", root=str(tmp_path)) == (None, "none")
+    assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) == (None, "none")
+    for bad in ({"code_digest": "0" * 16}, {"symbol": sym + "x"}, {"symbol": None}):
+        (tmp_path / "profiles" / "traffic_dsv3_bf16_w4_EOI.json").write_text(json.dumps({**rec, **bad}))
+        assert bench.measured_traffic("dsv3_bf16", "w4", "EOI", root=str(tmp_path)) == (None, "stale")
     c = bench.CONFIGS["dsv3_bf16"]
     work = {"g1_flops": 1e12, "g1_bytes": 1e10}
-    r = bench.roofline(c, work, 2.0, traffic=2e10)
+    r = bench.roofline(c, work, 2.0, traffic=2e10, traffic_record="current")
     assert r["traffic"] == 2e10 and r["bound"] == "hbm" and r["unit"] == "GB/s"
     assert r["traffic_ratio"] == 2.0 and r["algorithmic_bytes"] == 1e10 and r["achieved"] == 5000.0
+    assert r["traffic_record"] == "current"
+
+
+def test_committed_traffic_records_are_current():
+    """Every committed counter record names a kernel whose machine code in the built library is the
+    code the counters were read from."""
+    import glob
+    import json
+    from hyper_multicore_amd import _lib, codeobj
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("native library not built")
+    digests = codeobj.kernel_digests(str(_lib.LIB_PATH))
+    paths = glob.glob(os.path.join(os.path.dirname(os.path.dirname(__file__)), "profiles", "traffic_*.json"))
+    assert paths
+    for path in paths:
+        rec = json.load(open(path))
+        assert digests.get(rec["symbol"]) == rec["code_digest"], path
+
+
+def test_code_digests_cover_the_kernels():
+    """The code-object reader finds every kernel of the library with a distinct digest per distinct
+    body, and demangles the GEMM kernels' names."""
+    from hyper_multicore_amd import _lib, codeobj
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("native library not built")
+    dig = codeobj.kernel_digests(str(_lib.LIB_PATH))
+    assert len(dig) > 40
+    assert all(len(v) == 16 for v in dig.values())
+    names = codeobj.demangle(sorted(dig))
+    assert PP_BF16_GMM1 in names
+    assert any("decode_prep_kernel" in n for n in names)
 
 
 def _write_csv(path, header, rows):
@@ -159,7 +210,9 @@ def test_bench_profile_summary(tmp_path):
     rec = json.loads((tmp_path / "profiles" / "traffic_dsv3_bf16_default_EOI.json").read_text())
     assert rec["kernel"] == g1 and rec["fetch_kib"] == 1000.0 and rec["fetch_factor"] == 2.0
     assert rec["write_factor"] == 1.0 and rec["rocprof_avg_us"] == 6000.0 and rec["mfma_util_pct"] == 40.0
-    assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) == (2000 + 100) * 1024
+    assert (rec["symbol"], rec["code_digest"]) == _built_kernel()
+    assert bench.measured_traffic("dsv3_bf16", "default", "EOI", root=str(tmp_path)) == ((2000 + 100) * 1024,
+                                                                                           "current")
     text = open(txt).read()
     assert "ratio 1.025" in text and "rocprofv3 --pmc FETCH_SIZE" in text
     assert rec["rocprof_timed_us"] == 6000.0  # no kernel trace: the all-launch average
