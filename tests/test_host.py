@@ -18,6 +18,37 @@ def test_megagate_validation_mirrors_reference():
             hm.MegaGate(**{**kw, **bad})
 
 
+def _small_gate(vision_enabled, initializer_range=0.02):
+    return hm.MegaGate(hidden_size=128, num_experts=16, top_k=6, scoring_func="sqrtsoftplus",
+                       routed_scaling_factor=1.5, vision_enabled=vision_enabled, initializer_range=initializer_range)
+
+
+def test_megagate_parameter_initialization():
+    """As the reference's unit test (tests/ut/modules/mega_gate/test_mega_gate_module.py:45-56): the
+    projection from one Normal(0, initializer_range) draw, zero correction biases, exactly the
+    parameters weight / bias / bias_vl."""
+    from unittest.mock import patch
+    with patch("torch.nn.init.normal_", wraps=torch.nn.init.normal_) as normal:
+        gate = _small_gate(True, initializer_range=0.035)
+    normal.assert_called_once_with(gate.weight, mean=0.0, std=0.035)
+    assert set(gate.state_dict()) == {"weight", "bias", "bias_vl"}
+    assert tuple(gate.weight.shape) == (16, 128)
+    assert torch.isfinite(gate.weight).all() and torch.count_nonzero(gate.weight) > 0
+    assert torch.count_nonzero(gate.bias) == 0 and torch.count_nonzero(gate.bias_vl) == 0
+
+
+def test_megagate_meta_materialization_and_reset():
+    """A module built on the meta device, materialised with to_empty and reset (the reference's
+    test_mega_gate_module.py:58-69)."""
+    with torch.device("meta"):
+        gate = _small_gate(False)
+    gate.to_empty(device="cpu")
+    gate.reset_parameters()
+    assert torch.isfinite(gate.weight).all() and torch.count_nonzero(gate.weight) > 0
+    assert torch.count_nonzero(gate.bias) == 0
+    assert gate.bias_vl is None
+
+
 def test_megagate_keeps_fp32_biases_under_dtype_change():
     gate = hm.MegaGate(hidden_size=16, num_experts=8, top_k=2, scoring_func="sigmoid", routed_scaling_factor=1.0,
                        vision_enabled=True).to(torch.bfloat16)
