@@ -579,6 +579,44 @@ def test_module_autograd_gradients(gpu):
     assert orc.rel_l2(pg.grad.cpu(), rp) < 1e-2
 
 
+@_BACKWARD_SKIP
+@pytest.mark.parametrize("reentrant", [True, False])
+def test_module_activation_checkpoint(gpu, reentrant):
+    """Activation checkpointing replays the forward under no_grad, then again with grad (the
+    reference's test_reentrant_no_grad_then_grad, tests/torch/_test_mega_moe_review_regressions.py:
+    135-165): the checkpointed output equals the ordinary one and the gradients match it (the
+    reference's rtol 2e-2 / atol 2e-3)."""
+    from torch.utils.checkpoint import checkpoint
+    import hyper_multicore_amd as hm
+    T, H, I, E, K = 128, 256, 128, 32, 2
+    g = _seed(91)
+    x, ids, probs, w1, w2 = _expert_inputs(T, H, I, E, K, g, wscale=0.05)
+    ex = hm.MegaMoeExperts(hidden_size=H, intermediate_size=I, num_experts=E, top_k=K)
+    W1 = w1.to(gpu).requires_grad_(True)
+    W2 = w2.to(gpu).requires_grad_(True)
+    idg = ids.to(gpu)
+
+    def run(xx, pp):
+        return ex(xx, idg, pp, expert_weights=(W1, W2))
+
+    xg = x.to(gpu).requires_grad_(True)
+    pg = probs.to(gpu).requires_grad_(True)
+    ordinary = run(xg, pg)
+    ordinary.float().square().mean().backward()
+    expected = [t.detach().clone() for t in (ordinary, xg.grad, pg.grad, W1.grad, W2.grad)]
+    W1.grad, W2.grad = None, None
+    rx = x.to(gpu).requires_grad_(True)
+    rp = probs.to(gpu).requires_grad_(True)
+    out = checkpoint(run, rx, rp, use_reentrant=reentrant)
+    retained = out.detach().clone()
+    out.float().square().mean().backward()
+    assert torch.equal(retained, expected[0])
+    for got, want in zip((out, rx.grad, rp.grad, W1.grad, W2.grad), expected):
+        assert got is not None
+        torch.testing.assert_close(got, want, rtol=2e-2, atol=2e-3)
+    torch.testing.assert_close(out, retained, rtol=0, atol=0)
+
+
 # ------------------------------------------------------------------------------------------------
 # RouteGrad
 # ------------------------------------------------------------------------------------------------
