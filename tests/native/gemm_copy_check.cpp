@@ -956,7 +956,8 @@ static void emu_wave_step(EmuWaveTile<C, MX, B_KN, GK>& w, int nm, uint8_t* smem
 // reference of accumulator tile element (row, col) or NAN where the tile position is not compared.
 template <class C, bool MX, bool B_KN, bool GK>
 static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la)[C::WAVES], const int (&nm)[C::WAVES],
-                         int nk, const std::function<double(int, int)>& value, const char* what) {
+                         int nk, const std::function<double(int, int)>& value, const char* what,
+                         const std::function<void(const EmuWaveTile<C, MX, B_KN, GK>*)>& epilogue = nullptr) {
   std::vector<uint8_t> lds(C::TOTAL, 0);
   uint8_t* smem = lds.data();
   auto tiles = std::make_unique<EmuWaveTile<C, MX, B_KN, GK>[]>(C::WAVES);
@@ -1015,6 +1016,197 @@ static void emulate_item(const CopyPlan<C> (&cps)[C::WAVES][64], const bool (&la
   if (!(max_err <= 1e-4 * std::max(max_ref, 1e-30)))
     CHECK_FAIL("%s: emulated tile differs from the reference GEMM: max |err| %.3g (max |ref| %.3g) at tile "
                "(%d, %d): %.6g vs %.6g", what, max_err, max_ref, bad_row, bad_col, bad_got, bad_want);
+  if (epilogue) epilogue(tiles.get());
+}
+
+// ------------------------------------------------------------------------------------------------
+// The 4-wave kernel's epilogue on the emulated accumulators: the text of gemm_epilogue.inc, run by one
+// host thread per kernel thread, with its workgroup barriers as host barriers (prep_sim.inc) and
+// __expf as the host expf. The outputs it writes are then compared with the reference GEMM (stores)
+// and, for SwiGLU, with the SwiGLU of the kernel's own fp32 accumulators: bf16 exactly, and the fused
+// MX requant byte for byte against an independent quantiser.
+static long g_epilogue_items = 0;
+
+// e4m3 value of a code without its sign (0x7f is NaN)
+static double e4m3_mag(int c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  return e == 0 ? std::ldexp((double)m, -9) : std::ldexp(1.0 + m / 8.0, e - 7);
+}
+
+// Deliberate faults of the epilogue replay (mut_epi_* scenarios; the comparisons must report them):
+// 1 - exp off by 2^-10 relative; 2 - e4m3 conversion rounds toward zero; 3 - scale code one too high.
+static int g_epi_mutation = 0;
+static float epi_expf(float x) { return g_epi_mutation == 1 ? expf(x) * (1.0f + 1.0f / 1024) : expf(x); }
+static uint32_t epi_e4m3(float v) {
+  const uint32_t c = f32_to_e4m3(v);
+  if (g_epi_mutation == 2 && (c & 0x7f) != 0 && e4m3_mag(c & 0x7f) > std::fabs((double)v)) return c - 1;
+  return c;
+}
+static uint32_t epi_scale_code(float amax) { return mx_scale_code(amax) + (g_epi_mutation == 3 ? 1 : 0); }
+
+template <class C, int EPI, class Tile>
+static void epi_thread(const GGParams& p, const Tile* tiles, const ItemCtx& ctx, uint8_t* smem,
+                       prep_sim::Barrier* bar, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int nt = ctx.nt, split = ctx.split, half = ctx.half, rows_valid = ctx.rows_valid;
+  const int64_t tile_row0 = ctx.tile_row0;
+  v16f acc[C::MI][C::NI];
+  for (int i = 0; i < C::MI; ++i)
+    for (int j = 0; j < C::NI; ++j) acc[i][j] = tiles[wave].acc[lane][i][j];
+  (void)tid, (void)split, (void)half, (void)wm, (void)wn;
+#define __syncthreads() bar->wait()
+#define __builtin_amdgcn_sched_barrier(x) ((void)0)
+#define __expf(x) epi_expf(x)
+#define f32_to_e4m3(v) epi_e4m3(v)
+#define mx_scale_code(a) epi_scale_code(a)
+#include "../../hyper_multicore_amd/csrc/gemm_epilogue.inc"
+#undef __syncthreads
+#undef __builtin_amdgcn_sched_barrier
+#undef __expf
+#undef f32_to_e4m3
+#undef mx_scale_code
+}
+
+// One 32-value block: e8m0 code = the smallest e with amax <= 448 * 2^e (searched), each element the
+// nearest e4m3 value of v / 2^e (searched over the codes, ties to the even code).
+static void mx_block_ref(const float* v, uint8_t* q, uint8_t* code) {
+  double amax = 0.0;
+  for (int i = 0; i < 32; ++i) amax = std::max(amax, std::fabs((double)v[i]));
+  int e = -127;
+  if (amax > 0.0)
+    while (e < 127 && amax > 448.0 * std::ldexp(1.0, e)) ++e;
+  *code = (uint8_t)(e + 127);
+  for (int i = 0; i < 32; ++i) {
+    const double s = std::fabs((double)v[i]) / std::ldexp(1.0, e);
+    int best = 0;
+    double bd = INFINITY;
+    for (int c = 0; c < 0x7f; ++c) {
+      const double d = std::fabs(e4m3_mag(c) - s);
+      if (d < bd || (d == bd && (c & 1) == 0)) {
+        bd = d;
+        best = c;
+      }
+    }
+    q[i] = (uint8_t)(best | (std::signbit(v[i]) ? 0x80 : 0));
+  }
+}
+
+template <class C, int EPI, class Tile>
+static void emu_epilogue(const GGParams& p, const Tile* tiles, const ItemCtx& ctx,
+                         const std::function<double(int, int)>& value) {
+  constexpr bool SWIGLU = (EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_MX || EPI == EPI_SWIGLU_BF16_NUM);
+  std::vector<uint8_t> lds(C::TOTAL, 0xa5);  // staging starts with garbage
+  {
+    prep_sim::Barrier bar(C::THREADS);
+    std::vector<std::thread> th;
+    for (int t = 0; t < C::THREADS; ++t)
+      th.emplace_back([&, t] { epi_thread<C, EPI>(p, tiles, ctx, lds.data(), &bar, t); });
+    for (auto& x : th) x.join();
+  }
+  ++g_epilogue_items;
+  // the kernel's fp32 accumulator of tile element (row, col)
+  auto acc_at = [&](int row, int col) -> float {
+    const int wave = (row / C::WM) * C::WGN + col / C::WN;
+    const int i = (row % C::WM) / 32, rr = row % 32, j = (col % C::WN) / 32;
+    const int lane = 32 * ((rr >> 2) & 1) + col % 32, r = 4 * (rr >> 3) + (rr & 3);
+    return tiles[wave].acc[lane][i][j][r];
+  };
+  double max_ref = 0.0;
+  for (int row = 0; row < ctx.rows_valid; ++row)
+    for (int c = 0; c < C::BN; ++c) {
+      const double v = value(row, c);
+      if (!std::isnan(v)) max_ref = std::max(max_ref, std::fabs(v));
+    }
+  long bad = 0;
+  auto fail = [&](const char* what, int row, int col, double got, double want) {
+    if (bad++ < 4)
+      CHECK_FAIL("epilogue (%s) item g%d nt%d rows %lld+%d: (%d, %d) %.6g vs %.6g", what, ctx.g, ctx.nt,
+                 (long long)ctx.tile_row0, ctx.rows_valid, row, col, got, want);
+  };
+  if (EPI == EPI_STORE_F32 || EPI == EPI_STORE_BF16) {
+    for (int row = 0; row < ctx.rows_valid; ++row)
+      for (int c = 0; c < C::BN; ++c) {
+        const double want = value(row, c);
+        if (std::isnan(want)) continue;
+        const int64_t routed = ctx.tile_row0 + row;
+        double got;
+        if (EPI == EPI_STORE_F32) {
+          const int64_t orow = p.c_row_index ? p.c_row_index[routed] : routed;
+          got = ((const float*)p.C)[ctx.split * p.c_split_stride + orow * p.ldc + (int64_t)ctx.nt * C::BN + c];
+          if (got != acc_at(row, c)) fail("fp32 store", row, c, got, acc_at(row, c));
+        } else {
+          got = bf16f(((const uint16_t*)p.C)[routed * p.ldc + (int64_t)ctx.nt * C::BN + c]);
+          if (f32_to_bf16(acc_at(row, c)) != ((const uint16_t*)p.C)[routed * p.ldc + (int64_t)ctx.nt * C::BN + c])
+            fail("bf16 store", row, c, got, acc_at(row, c));
+        }
+        if (!(std::fabs(got - want) <= std::ldexp(std::fabs(want), -8) + 2e-4 * max_ref))
+          fail("store vs reference", row, c, got, want);
+      }
+    return;
+  }
+  if constexpr (SWIGLU) {
+    constexpr int HW = C::WN / 2;
+    const int ncol = C::BN / 2;
+    std::vector<float> act(ncol);
+    for (int row = 0; row < ctx.rows_valid; ++row) {
+      const int64_t routed = ctx.tile_row0 + row;
+      bool live[C::BN / 2];
+      for (int j = 0; j < ncol; ++j) {
+        const int gc = (j / HW) * C::WN + j % HW, uc = gc + HW;
+        const double g_ref = value(row, gc), u_ref = value(row, uc);
+        live[j] = !std::isnan(g_ref) && !std::isnan(u_ref) && (ctx.half < 0 || j / (ncol / 2) == ctx.half);
+        act[j] = 0.0f;
+        if (!live[j]) continue;
+        // the SwiGLU of the kernel's accumulators (gemm_epilogue.inc's arithmetic)
+        float gte = bf16_to_f32(f32_to_bf16(acc_at(row, gc)));
+        float up = bf16_to_f32(f32_to_bf16(acc_at(row, uc)));
+        float a;
+        if (EPI == EPI_SWIGLU_BF16_NUM && p.swiglu_limit > 0.0f) {
+          const float L = p.swiglu_limit;
+          up = fminf(fmaxf(up, -L), L);
+          if (p.swiglu_after_silu) a = fminf(gte / (1.0f + expf(-gte)), L) * up;
+          else {
+            const float gcl = fminf(gte, L);
+            a = gcl / (1.0f + expf(-gcl)) * up;
+          }
+        } else {
+          a = gte / (1.0f + expf(-gte)) * up;
+        }
+        act[j] = a;
+        // and that of the reference GEMM (double), loosely: it pins the column pairing
+        const double gr = bf16f(f32_to_bf16((float)g_ref)), ur = bf16f(f32_to_bf16((float)u_ref));
+        double ar = gr / (1.0 + std::exp(-gr)) * ur;
+        if (EPI == EPI_SWIGLU_BF16_NUM && p.swiglu_limit > 0.0f) {  // MegaMoeNumericsOptions clamp
+          const double L = p.swiglu_limit, uc = std::min(std::max(ur, -L), L);
+          if (p.swiglu_after_silu) ar = std::min(gr / (1.0 + std::exp(-gr)), L) * uc;
+          else ar = std::min(gr, L) / (1.0 + std::exp(-std::min(gr, L))) * uc;
+        }
+        if (!(std::fabs(a - ar) <= 2e-2 * std::fabs(ar) + 1e-3 * max_ref * max_ref)) fail("SwiGLU vs reference", row, j, a, ar);
+      }
+      if (EPI == EPI_SWIGLU_MX) {
+        for (int blk = 0; blk < ncol / 32; ++blk) {
+          if (!live[blk * 32]) continue;
+          uint8_t q[32], code;
+          mx_block_ref(&act[blk * 32], q, &code);
+          const uint8_t* got = (const uint8_t*)p.C + routed * p.ldc + (int64_t)ctx.nt * ncol + blk * 32;
+          const uint8_t gcode = p.c_scale[routed * p.c_scale_ld + ctx.nt * 4 + blk];
+          if (gcode != code) fail("MX scale code", row, blk * 32, gcode, code);
+          for (int i = 0; i < 32; ++i)
+            if (got[i] != q[i]) fail("MX element", row, blk * 32 + i, got[i], q[i]);
+        }
+      } else {
+        const uint16_t* out = (const uint16_t*)p.C + routed * p.ldc + (int64_t)ctx.nt * ncol;
+        for (int j = 0; j < ncol; ++j) {
+          if (!live[j]) continue;
+          float v = act[j];
+          if (EPI == EPI_SWIGLU_BF16_NUM && p.row_prob != nullptr)
+            v = bf16_to_f32(f32_to_bf16(v)) * p.row_prob[p.a_row_index[routed]];
+          if (out[j] != f32_to_bf16(v)) fail("bf16 SwiGLU", row, j, bf16f(out[j]), v);
+        }
+      }
+    }
+  }
 }
 
 // Forward work items that ran as a column half of their tile
@@ -1162,7 +1354,9 @@ static int sim_forward(const GGParams& p) {
         return sum;
       };
       emulate_item<C, MX, B_KN, false>(*reinterpret_cast<const CopyPlan<C>(*)[C::WAVES][64]>(cps.get()), las, nms, nk,
-                                        value, "forward item");
+                                        value, "forward item", [&](const EmuWaveTile<C, MX, B_KN, false>* tiles) {
+                                          emu_epilogue<C, EPI>(p, tiles, ctx, value);
+                                        });
     }
   }
   return MI355MOE_OK;
@@ -1577,6 +1771,20 @@ static std::function<void()> pp_mutant(int mutation, std::function<void()> f) {
   };
 }
 
+// runs f with epilogue replay fault `mutation` switched on: the scenario passes when it is reported
+static std::function<void()> epi_mutant(int mutation, std::function<void()> f) {
+  return [mutation, f] {
+    const long e0 = g_errors;
+    g_epi_mutation = mutation;
+    f();
+    g_epi_mutation = 0;
+    const long found = g_errors - e0;
+    g_errors = e0;
+    if (found == 0) CHECK_FAIL("epilogue fault %d was not reported", mutation);
+    else printf("epilogue fault %d reported (%ld findings)\n", mutation, found);
+  };
+}
+
 // runs f with the library's GEMMs routed to the 8-wave configuration as the library routes them;
 // the scenario fails when no GEMM ran on it
 static std::function<void()> pp_route(std::function<void()> f) {
@@ -1609,6 +1817,25 @@ static void moe_forward(int64_t T, int K, int E, int H, int I, int precision, in
     } else {
       s1 = mk("w1_col_scale", (size_t)E * (H / 64) * 2 * I * 2);
       s2 = mk("w2_col_scale", (size_t)E * (I / 64) * H * 2);
+    }
+  }
+  if (g_emulate) {  // operands of moderate size, so the emulated epilogues compare finite values
+    std::uniform_real_distribution<float> pu(0.05f, 1.0f);
+    for (int64_t i = 0; i < T * K; ++i) wts[i] = pu(g_rng);
+    fill_bf16(hidden, (size_t)T * H);
+    if (mx) {
+      fill_e4m3(w1, (size_t)E * H * 2 * I);
+      fill_e4m3(w2, (size_t)E * I * H);
+      if (eoi) {
+        fill_codes(s1, (size_t)E * 2 * I * mi355moe_mx_weight_scale_ld(H));
+        fill_codes(s2, (size_t)E * H * mi355moe_mx_weight_scale_ld(I));
+      } else {
+        fill_codes(s1, (size_t)E * (H / 64) * 2 * I * 2);
+        fill_codes(s2, (size_t)E * (I / 64) * H * 2);
+      }
+    } else {
+      fill_bf16(w1, (size_t)E * H * 2 * I);
+      fill_bf16(w2, (size_t)E * I * H);
     }
   }
   uint8_t* out = mk("out", (size_t)T * H * 2);
@@ -1857,6 +2084,14 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_pp_mx_store", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 512, true, true, false, 0); })});
   s.push_back({"emu_pp_mx_swiglu", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 256, true, true, true, 0); })});
   s.push_back({"emu_pp_mx_swiglu_gu", emu([=] { pp_gemm({70, 0, 257, 1, 511}, 256, 256, true, true, true, 1); })});
+  s.push_back({"emu_moe_bf16_numerics_clamp", emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EIO, 0.0, 0, 7.0f); })});
+  s.push_back({"emu_moe_bf16_numerics_after_silu",
+               emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EOI, 0.0, MI355MOE_NUMERICS_CLAMP_AFTER_SILU, 7.0f); })});
+  s.push_back({"emu_moe_bf16_probs_before_fc2",
+               emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EIO, 0.0, MI355MOE_NUMERICS_PROBS_BEFORE_FC2); })});
+  s.push_back({"mut_epi_exp", epi_mutant(1, halves(emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EIO, 0.0); })))});
+  s.push_back({"mut_epi_rounding", epi_mutant(2, halves(emu([=] { moe_forward(16, 4, 16, 512, 256, MX, L_EIO, 0.0); })))});
+  s.push_back({"mut_epi_scale", epi_mutant(3, halves(emu([=] { moe_forward(16, 4, 16, 512, 256, MX, L_EIO, 0.0); })))});
   s.push_back({"mut_pp_copy_offset", pp_mutant(1, emu([=] { pp_gemm({70, 129}, 256, 256, false, true, false, 0); }))});
   s.push_back({"mut_pp_copy_oob", pp_mutant(2, [=] { pp_gemm({70, 129}, 256, 256, false, true, false, 0); })});
   s.push_back({"mut_pp_copy_skipped", pp_mutant(3, [=] { pp_gemm({70, 129}, 256, 256, true, true, false, 0); })});
@@ -1914,12 +2149,13 @@ int main(int argc, char** argv) {
     for (int i = 1; i < argc; ++i) pick |= std::string(argv[i]) == sc.name;
     if (!pick) continue;
     g_scenario = sc.name;
-    const long e0 = g_errors, c0 = g_copies, i0 = g_items, m0 = g_gemms, u0 = g_emulated_items, p0 = g_preps;
+    const long e0 = g_errors, c0 = g_copies, i0 = g_items, m0 = g_gemms, u0 = g_emulated_items, p0 = g_preps,
+               q0 = g_epilogue_items;
     sc.run();
     free_all();
-    printf("%-32s %s  gemms=%ld items=%ld copies=%ld emulated=%ld preps=%ld\n", sc.name,
+    printf("%-32s %s  gemms=%ld items=%ld copies=%ld emulated=%ld epilogues=%ld preps=%ld\n", sc.name,
            g_errors == e0 ? "ok" : "FAILED", g_gemms - m0, g_items - i0, g_copies - c0, g_emulated_items - u0,
-           g_preps - p0);
+           g_epilogue_items - q0, g_preps - p0);
     fflush(stdout);
     ++ran;
   }

@@ -11,8 +11,11 @@ the element the fragment reads expect), the LDS destination slot and the slot co
 4-wave kernels the vmcnt waits and the ring-slot reuse; the emu_* scenarios also run the kernels'
 fragment reads, MFMAs and (8-wave) epilogues through an emulation of the lane-crossing instructions
 and compare the results with a reference GEMM, and the 8-wave MXFP8 SwiGLU epilogue with the fp32
-one followed by the MX quantisation; the mut_pp_* scenarios switch on deliberate faults of the
-replay and pass when the checks report them. Decode-shaped forwards run the one-launch decode
+one followed by the MX quantisation; for the 4-wave and decode kernels they also run the text of the
+epilogue (gemm_epilogue.inc, one host thread per kernel thread) on the emulated accumulators and compare
+its stores with the reference GEMM and its fused MX requant byte for byte with an independent
+quantiser; the mut_pp_* and mut_epi_* scenarios switch on deliberate faults of the replay and pass when
+the checks report them. Decode-shaped forwards run the one-launch decode
 prologue's code under a host emulation of its workgroup (prep_sim.inc) and compare its dispatch and
 tile plan with the checker's own. See tests/native/gemm_copy_check.cpp, pp_sim.inc and prep_sim.inc.
 """
@@ -37,25 +40,27 @@ def checker():
 
 SCENARIOS = [
     "gemm_bf16_eio", "gemm_bf16_eoi", "gemm_bf16_eio_narrow", "gemm_bf16_eoi_narrow", "gemm_mx_eio", "gemm_mx_eoi",
-    "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k", "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode",
-    "gemm_mx_eio_decode", "gemm_mx_eoi_decode", "gemm_bf16_eio_decode_big", "gemm_bf16_eoi_decode_big",
-    "gemm_mx_eio_decode_big", "moe_bf16_eio_decode_big", "moe_mx_eio_decode_big", "moe_bf16_gu_decode_big",
-    "moe_mx_gu_decode_big", "moe_mx_decode_halves", "moe_mx_gu_decode_halves", "moe_bf16_decode_halves",
-    "moe_bf16_gu_decode_halves", "moe_mx_eoi_decode_halves", "emu_bf16_eio", "emu_bf16_eoi", "emu_mx_eio",
-    "emu_mx_eoi", "emu_bf16_eio_decode", "emu_bf16_eoi_decode", "emu_mx_eio_decode", "emu_mx_eoi_decode",
-    "emu_moe_mx_decode_halves", "emu_moe_bf16_decode_halves", "emu_moe_mx_gu_decode_halves", "emu_wgrad_bf16",
-    "emu_wgrad_mx", "pp_gemm_bf16_eio", "pp_gemm_bf16_eoi", "pp_gemm_bf16_eio_narrow", "pp_gemm_bf16_many_items",
+    "gemm_mx_eoi_long_k", "gemm_mx_eio_long_k", "gemm_bf16_eio_decode", "gemm_bf16_eoi_decode", "gemm_mx_eio_decode",
+    "gemm_mx_eoi_decode", "gemm_bf16_eio_decode_big", "gemm_bf16_eoi_decode_big", "gemm_mx_eio_decode_big",
+    "moe_bf16_eio_decode_big", "moe_mx_eio_decode_big", "moe_bf16_gu_decode_big", "moe_mx_gu_decode_big",
+    "moe_mx_decode_halves", "moe_mx_gu_decode_halves", "moe_bf16_decode_halves", "moe_bf16_gu_decode_halves",
+    "moe_mx_eoi_decode_halves", "emu_bf16_eio", "emu_bf16_eoi", "emu_mx_eio", "emu_mx_eoi", "emu_bf16_eio_decode",
+    "emu_bf16_eoi_decode", "emu_mx_eio_decode", "emu_mx_eoi_decode", "emu_moe_mx_decode_halves",
+    "emu_moe_bf16_decode_halves", "emu_moe_mx_gu_decode_halves", "emu_wgrad_bf16", "emu_wgrad_mx",
+    "pp_gemm_bf16_eio", "pp_gemm_bf16_eoi", "pp_gemm_bf16_eio_narrow", "pp_gemm_bf16_many_items",
     "pp_gemm_bf16_noalloc", "pp_moe_bf16_eio_prefill", "pp_moe_bf16_eoi_prefill", "pp_moe_bf16_gu_prefill",
     "pp_moe_mx_eio_prefill", "pp_moe_mx_gu_prefill", "pp_moe_mx_gu_skewed", "pp_moe_bf16_gu_skewed",
     "pp_moe_mx_gu_decode_variant", "pp_moe_bf16_eio_decode_variant", "pp_gemm_bf16_decode_variant",
     "pp_bf16_kn_store", "pp_mx_swiglu_gu", "emu_pp_bf16_kn_store", "emu_pp_bf16_nk_store",
     "emu_pp_bf16_kn_store_256", "emu_pp_bf16_kn_swiglu", "emu_pp_bf16_kn_swiglu_gu", "emu_pp_bf16_nk_swiglu",
-    "emu_pp_mx_store", "emu_pp_mx_swiglu", "emu_pp_mx_swiglu_gu", "mut_pp_copy_offset", "mut_pp_copy_oob",
-    "mut_pp_copy_skipped", "mut_pp_staging", "mut_pp_shuffle", "mut_pp_rounding", "gemm_bf16_many_groups",
-    "gemm_bf16_noalloc", "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi",
-    "moe_mx_eoi_prefill", "moe_mx_eio_prefill", "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp",
-    "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16",
-    "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill"
+    "emu_pp_mx_store", "emu_pp_mx_swiglu", "emu_pp_mx_swiglu_gu", "emu_moe_bf16_numerics_clamp",
+    "emu_moe_bf16_numerics_after_silu", "emu_moe_bf16_probs_before_fc2", "mut_epi_exp", "mut_epi_rounding",
+    "mut_epi_scale", "mut_pp_copy_offset", "mut_pp_copy_oob", "mut_pp_copy_skipped", "mut_pp_staging",
+    "mut_pp_shuffle", "mut_pp_rounding", "gemm_bf16_many_groups", "gemm_bf16_noalloc", "moe_bf16_eio",
+    "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
+    "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu",
+    "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32",
+    "bwd_mx_bf16_prefill"
 ]
 
 
