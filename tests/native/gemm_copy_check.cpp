@@ -31,6 +31,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <map>
 #include <memory>
 #include <random>
 #include <string>
@@ -1092,6 +1093,44 @@ static void mx_block_ref(const float* v, uint8_t* q, uint8_t* code) {
   }
 }
 
+// n host threads kept for the epilogue replays (creating a workgroup's threads per item dominated the
+// replay's time): run(f) calls f(t) on thread t = 0..n-1 and returns when all have returned.
+struct EpiPool {
+  explicit EpiPool(int n) : n_(n), start_(n + 1), done_(n + 1) {
+    for (int t = 0; t < n; ++t)
+      th_.emplace_back([this, t] {
+        for (;;) {
+          start_.wait();
+          if (quit_) return;
+          job_(t);
+          done_.wait();
+        }
+      });
+  }
+  void run(const std::function<void(int)>& f) {
+    job_ = f;
+    start_.wait();
+    done_.wait();
+  }
+  ~EpiPool() {
+    quit_ = true;
+    start_.wait();
+    for (auto& x : th_) x.join();
+  }
+  int n_;
+  prep_sim::Barrier start_, done_;
+  std::function<void(int)> job_;
+  bool quit_ = false;
+  std::vector<std::thread> th_;
+};
+
+static EpiPool& epi_pool(int n) {
+  static std::map<int, std::unique_ptr<EpiPool>> pools;
+  auto& p = pools[n];
+  if (!p) p.reset(new EpiPool(n));
+  return *p;
+}
+
 template <class C, int EPI, class Tile>
 static void emu_epilogue(const GGParams& p, const Tile* tiles, const ItemCtx& ctx,
                          const std::function<double(int, int)>& value) {
@@ -1099,10 +1138,7 @@ static void emu_epilogue(const GGParams& p, const Tile* tiles, const ItemCtx& ct
   std::vector<uint8_t> lds(C::TOTAL, 0xa5);  // staging starts with garbage
   {
     prep_sim::Barrier bar(C::THREADS);
-    std::vector<std::thread> th;
-    for (int t = 0; t < C::THREADS; ++t)
-      th.emplace_back([&, t] { epi_thread<C, EPI>(p, tiles, ctx, lds.data(), &bar, t); });
-    for (auto& x : th) x.join();
+    epi_pool(C::THREADS).run([&](int t) { epi_thread<C, EPI>(p, tiles, ctx, lds.data(), &bar, t); });
   }
   ++g_epilogue_items;
   // the kernel's fp32 accumulator of tile element (row, col)
