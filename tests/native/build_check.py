@@ -1,7 +1,7 @@
 """Build the host-side grouped-GEMM copy checker (test infrastructure, CPU only).
 
 The library sources are compiled for the host only (``--cuda-host-only``) with every optional path
-switched on and AddressSanitizer, the internal enqueue functions the
+switched on, AddressSanitizer and UndefinedBehaviorSanitizer, the internal enqueue functions the
 checker replaces are made weak, and everything is linked with ``gemm_copy_check.cpp`` and no HIP
 runtime. Output goes to ``tests/native/_build`` (git-ignored); a build is reused while no input
 changed.
@@ -9,7 +9,7 @@ changed.
     python tests/native/build_check.py      # builds and prints the binary paths
 
 ``build_prep()`` builds ``prep_check``: the one-launch decode prologue (decode_prep.h) under the host
-emulation of ``prep_sim.inc``, also with AddressSanitizer.
+emulation of ``prep_sim.inc``, with the same sanitizers.
 """
 from __future__ import annotations
 
@@ -36,7 +36,11 @@ REPLACED = {
 }
 # internal functions the checker wraps: linked under the name with the suffix `_lib`
 RENAMED = {"gemm_pp.hip": ["mi355_gg_pp_usable"]}
-FLAGS = ["-x", "hip", "--cuda-host-only", "-O1", "-g", "-std=c++17", "-fsanitize=address",
+# AddressSanitizer and UndefinedBehaviorSanitizer (any report ends the run), except the check on
+# pointer arithmetic from a null base: the copy plans of waves that copy no scales hold a null scale
+# pointer, and the kernels form (never dereference) its stage addresses for the predicated-off copies
+SANITIZE = ["-fsanitize=address,undefined", "-fno-sanitize=pointer-overflow", "-fno-sanitize-recover=undefined"]
+FLAGS = ["-x", "hip", "--cuda-host-only", "-O1", "-g", "-std=c++17", *SANITIZE,
          "-fno-omit-frame-pointer", "-Wno-unused-result", "-Wno-unused-variable",
          f"-I{REPO / 'include'}"]
 
@@ -113,7 +117,7 @@ def _build_locked() -> Path:
     stub_o = OUT / "fatbin_stub.o"
     _run(["gcc", "-c", str(stub), "-o", str(stub_o)])
     clangxx = str(_rocm() / "llvm" / "bin" / "clang++")
-    _run([clangxx, "-fsanitize=address", "-pthread", *map(str, objs), str(stub_o), "-o", str(exe)])
+    _run([clangxx, *SANITIZE, "-pthread", *map(str, objs), str(stub_o), "-o", str(exe)])
     stamp.write_text(digest)
     return exe
 
@@ -139,7 +143,7 @@ def build_prep() -> Path:
         obj = OUT / "prep_check.o"
         _run([hipcc, *FLAGS, "-c", str(HERE / "prep_check.cpp"), "-o", str(obj)])
         clangxx = str(_rocm() / "llvm" / "bin" / "clang++")
-        _run([clangxx, "-fsanitize=address", "-pthread", str(obj), "-o", str(exe)])
+        _run([clangxx, *SANITIZE, "-pthread", str(obj), "-o", str(exe)])
         stamp.write_text(digest)
         return exe
 

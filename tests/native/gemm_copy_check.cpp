@@ -19,7 +19,7 @@
 //      every ring slot being refilled only after the stage it held has been read;
 //   5. full coverage of each stage's weight slot (and scale slots) by the four waves.
 // The epilogue's output ranges are checked against the output allocation, and every host-side read
-// of the index arrays runs under AddressSanitizer.
+// of the index arrays runs under AddressSanitizer; UndefinedBehaviorSanitizer ends the run at any report.
 //
 // Usage: gemm_copy_check [scenario-name ...]   (no argument: all scenarios). Exit status 0 when
 // every check passed.

@@ -2,7 +2,7 @@
 
 tests/native/prep_check runs the kernel's code under the host emulation of a workgroup
 (tests/native/prep_sim.inc: 256 threads, the kernel's barriers, ballots and shuffles as lockstep
-points, AddressSanitizer on every buffer). Its outputs are compared with the oracle: counts with
+points, AddressSanitizer on every buffer, UndefinedBehaviorSanitizer). Its outputs are compared with the oracle: counts with
 ``expert_counts`` (route.py:186-211), group_list with the EP=1 ``route_metadata`` (route.py:309-390),
 mapping / gather with ``stable_permutation`` (utilities.asc:176-204), the tile plan with its definition
 (exclusive prefix of ceil(count / bm)), and the token quantisation with ``mx_quantize`` (scale algorithm
