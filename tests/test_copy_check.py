@@ -19,8 +19,10 @@ the checks report them. Decode-shaped forwards run the one-launch decode
 prologue's code under a host emulation of its workgroup (prep_sim.inc) and compare its dispatch and
 tile plan with the checker's own. See tests/native/gemm_copy_check.cpp, pp_sim.inc and prep_sim.inc.
 """
+import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 
 import pytest
 
@@ -71,9 +73,26 @@ def test_scenario_list_matches(checker):
     assert r.stdout.split() == SCENARIOS
 
 
+def _run(checker, name):
+    return subprocess.run([str(checker), name], capture_output=True, text=True, timeout=600)
+
+
+@pytest.fixture(scope="module")
+def runs(checker):
+    """Scenario name -> its run. In a plain pytest process the scenarios run as concurrent checker
+    processes (one per host CPU, at most 8) when the first of them is needed; under pytest-xdist each
+    test runs its own, since the workers already run in parallel."""
+    if os.environ.get("PYTEST_XDIST_WORKER"):
+        return None
+    workers = max(1, min(8, os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        futures = {name: pool.submit(_run, checker, name) for name in SCENARIOS}
+        return {name: f.result() for name, f in futures.items()}
+
+
 @pytest.mark.parametrize("name", SCENARIOS)
-def test_copy_schedule(checker, name):
-    r = subprocess.run([str(checker), name], capture_output=True, text=True, timeout=600)
+def test_copy_schedule(checker, runs, name):
+    r = runs[name] if runs is not None else _run(checker, name)
     assert r.returncode == 0, f"{r.stdout}\n{r.stderr}"
     assert f"{name}" in r.stdout and " ok " in r.stdout
     if name.startswith(("moe_", "emu_moe_")) and "decode" in name:
