@@ -29,3 +29,10 @@ inline bool mi355_decode_prep_enabled() {
   const char* v = getenv("MI355MOE_DECODE_PREP");
   return v != nullptr && strcmp(v, "1") == 0;
 }
+// The skinny 384 x 128 MX tile of the 8-wave GEMM for experts of 257..384 routed rows (one weight
+// pass instead of two). Host-checked; until its GPU tests and an A/B have run it is used only while
+// MI355MOE_PP_SKINNY=1 is set in the environment (read at each GEMM call).
+inline bool mi355_pp_skinny_enabled() {
+  const char* v = getenv("MI355MOE_PP_SKINNY");
+  return v != nullptr && strcmp(v, "1") == 0;
+}

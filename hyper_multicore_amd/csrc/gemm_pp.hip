@@ -34,7 +34,7 @@ __device__ __forceinline__ void barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool MX, bool B_KN, int EPI, bool TALL>
+template <bool MX, bool B_KN, int EPI, bool TALL, int SEL>
 __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   using C = Cfg<MX, TALL>;
   constexpr int MI = C::MI, S_SLOT = C::SLOT;
@@ -46,11 +46,11 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = O::uni(tid >> 6);
-  const int grp = wave >> 2, wq = wave & 3;
+  const int grp = wave >> 2, wq = C::wq_of(wave), rbo = C::rbo_of(wave);
 
-  // The work list: m-tiles of C::BM rows per group and their exclusive prefix, from group_list (the
-  // tile height is this kernel's own, so no host-side plan is read). Thread t takes groups
-  // PER t ..+PER-1; a scan over the threads gives each its first tile.
+  // The work list: m-tiles of C::BM rows per group (of the groups SEL takes) and their exclusive
+  // prefix, from group_list (the tile height is this kernel's own, so no host-side plan is read).
+  // Thread t takes groups PER t ..+PER-1; a scan over the threads gives each its first tile.
   {
     constexpr int PER = (C::PREFIX_MAX + THREADS - 1) / THREADS;
     int cnt[PER];
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       if (g < p.G) {
         const int64_t end = p.group_list[g];
         const int64_t rows = end - (g == 0 ? 0 : p.group_list[g - 1]);
-        cnt[u] = rows > 0 ? (int)((rows + C::BM - 1) / C::BM) : 0;
+        cnt[u] = rows > 0 && sel_takes<SEL>(rows) ? (int)((rows + C::BM - 1) / C::BM) : 0;
         s_rows[g] = (int32_t)end;
       }
       local += cnt[u];
@@ -121,9 +121,9 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   int kL = L0, kk = 0;
   Item it;
   decode<C, O>(p, smem, kL, it);
-  // row blocks of this wave's group that hold rows of the item; `live`: any
+  // row blocks of this wave that hold rows of the item; `live`: any
   auto row_blocks = [&]() {
-    const int n = ((it.rows + 31) / 32 - grp + 1) / 2;
+    const int n = ((it.rows + 31) / 32 - rbo + C::RBS - 1) / C::RBS;
     return O::uni(n < 0 ? 0 : (n > MI ? MI : n));
   };
   int nmi = row_blocks();
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
 
   auto finish_stage = [&]() {
     if (++kk == nk) {
-      if (live) epilogue<C, EPI, O>(p, it, acc, grp, wq, lane, smem + C::EPI_OFF + wave * C::EPI_BLOCK);
+      if (live) epilogue<C, EPI, O>(p, it, acc, rbo, wq, lane, smem + C::EPI_OFF + wave * C::EPI_BLOCK);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       const uint8_t* slot = smem + (q % S) * S_SLOT;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        if (live) read_frags<C, B_KN, O>(f, slot, h, grp, wq, lane, (int)(it.row0 & 3), nmi);
+        if (live) read_frags<C, B_KN, O>(f, slot, h, rbo, wq, lane, (int)(it.row0 & 3), nmi);
         wait_lgkm0();
         __builtin_amdgcn_sched_barrier(0);
         if (live) mfmas<MX, B_KN, MI, O>(f, acc, nmi);
@@ -184,12 +184,12 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* slot = smem + (q % S) * S_SLOT;
-      if (live) read_frags<C, B_KN, O>(f, slot, 0, grp, wq, lane, (int)(it.row0 & 3), nmi);
+      if (live) read_frags<C, B_KN, O>(f, slot, 0, rbo, wq, lane, (int)(it.row0 & 3), nmi);
       wait_lgkm0();
       __builtin_amdgcn_sched_barrier(0);
       if (live) mfmas<MX, B_KN, MI, O>(f, acc, nmi);
       __builtin_amdgcn_sched_barrier(0);
-      if (live) read_frags<C, B_KN, O>(f, slot, 1, grp, wq, lane, (int)(it.row0 & 3), nmi);
+      if (live) read_frags<C, B_KN, O>(f, slot, 1, rbo, wq, lane, (int)(it.row0 & 3), nmi);
       wait_lgkm0();
       wait_vm0();
       barrier();
@@ -200,10 +200,10 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
   wait_vm0();  // no copy may still write the LDS when the workgroup ends
 }
 
-template <bool MX, bool B_KN, int EPI, bool TALL>
+template <bool MX, bool B_KN, int EPI, bool TALL, int SEL>
 int launch_pp_k(const GGParams& p, hipStream_t stream) {
   using C = Cfg<MX, TALL>;
-  auto kern = gg_pp_kernel<MX, B_KN, EPI, TALL>;
+  auto kern = gg_pp_kernel<MX, B_KN, EPI, TALL, SEL>;
   static bool configured = false;
   if (!configured) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::TOTAL) != hipSuccess)
@@ -218,9 +218,9 @@ int launch_pp_k(const GGParams& p, hipStream_t stream) {
 
 struct DevLaunch {
   hipStream_t stream;
-  template <bool MX, bool B_KN, int EPI, bool TALL>
+  template <bool MX, bool B_KN, int EPI, bool TALL, int SEL>
   int run(const GGParams& p) {
-    return launch_pp_k<MX, B_KN, EPI, TALL>(p, stream);
+    return launch_pp_k<MX, B_KN, EPI, TALL, SEL>(p, stream);
   }
 };
 

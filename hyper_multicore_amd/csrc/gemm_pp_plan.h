@@ -51,32 +51,51 @@
 
 namespace pp {
 
-constexpr int BN = 256;
 constexpr int KB = 128;  // bytes of K per row and stage
 constexpr int S = 2;     // ring slots
 constexpr int WAVES = 8, THREADS = 64 * WAVES;
 constexpr int WN = 64, NI = WN / 32;
-// MX scales of a stage: 4 activation code planes of 512 bytes (the 256 tile rows from the 4-aligned
-// row at or below the first one), 2 x 256 weight code pairs
+// MX activation scales of a stage: 4 code planes of 512 bytes (the tile rows from the 4-aligned row
+// at or below the first one; 512 covers tiles of up to 509 rows)
 constexpr int AS_PLANE = 512;
-constexpr int B_BYTES = BN * KB, AS_BYTES = 4 * AS_PLANE, BS_BYTES = 2 * BN * 2;
-constexpr int CPW_B = B_BYTES / 1024 / WAVES;  // 1 KB weight copies per wave and stage
-static_assert(CPW_B == 4, "four 1 KB weight copies per wave");
+constexpr int AS_BYTES = 4 * AS_PLANE;
 
-// Tile height and LDS layout. Tiles are 256 rows, or 320 for bf16 GEMMs whose groups average at most
-// 320 rows (TALL): each m-tile streams its group's weights, whose lines miss L2, and the
+// The skinny tile's groups: those of SKINNY_LO + 1 .. SKINNY_HI rows
+constexpr int SKINNY_LO = 256, SKINNY_HI = 384;
+// Groups a launch takes: SEL_ALL, SEL_NOT_SKINNY (all but the skinny range), SEL_SKINNY (only it)
+enum { SEL_ALL = 0, SEL_NOT_SKINNY = 1, SEL_SKINNY = 2 };
+template <int SEL>
+MI355_HD bool sel_takes(int64_t rows) {
+  if constexpr (SEL == SEL_ALL) return true;
+  const bool skinny = rows > SKINNY_LO && rows <= SKINNY_HI;
+  return SEL == SEL_SKINNY ? skinny : !skinny;
+}
+
+// Tile shape and LDS layout. Tiles are 256 x 256; 320 x 256 for bf16 GEMMs whose groups average at
+// most 320 rows (TALL): each m-tile streams its group's weights, whose lines miss L2, and the
 // workgroup's memory requests in flight are what bounds the kernel, so an expert of 257..320 routed
 // rows (DeepSeek-V3 prefill routes 256 on average, with a wide spread) is one m-tile instead of a
 // full one and a short one that streams the weights again. When groups are large multiples of 256
-// rows the fifth row block costs more than the tiles it saves. MX tiles stay 256 rows (no registers
-// left for a fifth row block).
+// rows the fifth row block costs more than the tiles it saves. MX tiles of 256 rows have no registers
+// left for a fifth row block; for MX, TALL is the skinny 384 x 128 tile instead (same accumulators
+// per workgroup: each wave 3 row blocks x 64 columns, two waves of a group per column range), which
+// streams the weights of an expert of 257..384 rows once.
 template <bool MX_, bool TALL>
 struct Cfg {
   static constexpr bool MX = MX_;
-  static constexpr int BM = (MX || !TALL) ? 256 : 320;
-  static constexpr int WM = BM / 2, MI = WM / 32;  // rows per wave group, 32-row blocks per wave
-  static constexpr int A_BYTES = BM * KB;
+  static constexpr bool SKINNY = MX_ && TALL;
+  static constexpr int BM = SKINNY ? 384 : (MX || !TALL) ? 256 : 320;
+  static constexpr int BN = SKINNY ? 128 : 256;
+  static constexpr int WQN = BN / WN;            // waves of a group across the tile's columns
+  static constexpr int RBS = 2 * (4 / WQN);      // row-block stride of a wave
+  static constexpr int MI = BM / (32 * RBS);     // 32-row blocks per wave
+  static constexpr int A_BYTES = BM * KB, B_BYTES = BN * KB, BS_BYTES = 2 * BN * 2;
   static constexpr int CPW_A = A_BYTES / 1024 / WAVES;  // 1 KB activation copies per wave and stage
+  static constexpr int CPW_B = B_BYTES / 1024 / WAVES;  // 1 KB weight copies per wave and stage
+  static constexpr int B_CH_LOG = SKINNY ? 3 : 4;       // MX weight K rows: BN bytes = 1 << B_CH_LOG chunks
+  // wave w: columns 64 wq_of(w) ..+63, row blocks RBS mi + rbo_of(w); the groups are w / 4
+  MI355_HD static int wq_of(int w) { return w & (WQN - 1); }
+  MI355_HD static int rbo_of(int w) { return (w >> 2) + 2 * ((w & 3) / WQN); }
   static constexpr int B_OFF = A_BYTES, AS_OFF = B_OFF + B_BYTES, BS_OFF = AS_OFF + AS_BYTES;
   static constexpr int SLOT = MX ? BS_OFF + BS_BYTES : AS_OFF;
   static constexpr int PREFIX_OFF = S * SLOT;
@@ -89,6 +108,9 @@ struct Cfg {
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
   static_assert(SLOT % 16 == 0, "copy destinations are 16-byte aligned");
   static_assert(A_BYTES % (1024 * WAVES) == 0, "whole 1 KB activation copies per wave");
+  static_assert(B_BYTES % (1024 * WAVES) == 0 && (BN >> B_CH_LOG) == 16, "whole 1 KB weight copies per wave");
+  static_assert(BM + 3 <= AS_PLANE, "a code plane run covers the tile");
+  static_assert(MI * 32 * RBS == BM && RBS * WQN == 8, "wave geometry");
 };
 
 // The device policy: the gfx950 instructions behind the shared code.
@@ -156,9 +178,10 @@ struct PpDev {
   MI355_DEV static uint32_t e4m3(float v) { return f32_to_e4m3_inrange(v); }
 };
 
-// Tile column j (0..255) -> weight column; SwiGLU: wave tile q's 64 columns are gate columns
-// nt * 128 + 32 q .. +31, then the up columns I + the same.
+// Tile column j (0..BN-1) -> weight column; SwiGLU: wave tile q's 64 columns are gate columns
+// nt * BN / 2 + 32 q .. +31, then the up columns I + the same.
 // With the gate/up interleaved weight layout the projection column goes through gate_up_col.
+template <int BN>
 MI355_HD int tile_col(int j, int nt, int I, bool swiglu, int gu) {
   if (!swiglu) return nt * BN + j;
   const int q = j >> 6, jj = j & 63;
@@ -258,25 +281,27 @@ MI355_HD void make_plan(const GGParams& p, const Item& it, int wave, int lane, P
   }
 }
 
-template <bool MX, bool B_KN, bool SWIGLU>
+template <class C, bool B_KN, bool SWIGLU>
 MI355_HD uint32_t b_off(const GGParams& p, int nt, int i, int lane) {
   if constexpr (!B_KN) {  // K-contiguous weights: like the activations, one weight row per tile column
     const int r = row_of(i, lane);
-    int wc = tile_col(r, nt, p.N, SWIGLU, p.gate_up_interleaved);
+    int wc = tile_col<C::BN>(r, nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc >= p.Ntot) wc = p.Ntot - 1;
     return (uint32_t)wc * (uint32_t)p.b_row_bytes + (uint32_t)(chunk_of(r, lane) * 16);
-  } else if constexpr (MX) {
-    const int L16 = i * 64 + lane;  // K rows of 256 bytes: copy i covers K rows 4 i ..+3
-    const int k = L16 >> 4;
-    const int c = (L16 & 15) ^ (k & 15);
-    int wc = tile_col(c * 16, nt, p.N, SWIGLU, p.gate_up_interleaved);
+  } else if constexpr (C::MX) {
+    // K rows of BN bytes (16 or 8 chunks): copy i covers K rows (4 or 8) i ..
+    constexpr int LG = C::B_CH_LOG, M = (1 << LG) - 1;
+    const int L16 = i * 64 + lane;
+    const int k = L16 >> LG;
+    const int c = (L16 & M) ^ (k & M);
+    int wc = tile_col<C::BN>(c * 16, nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc > p.Ntot - 16) wc = p.Ntot - 16;
     return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc;
   } else {
     const int L16 = i * 64 + lane;  // K rows of 512 bytes: copy i covers K rows 2 i, 2 i + 1
     const int k = L16 >> 5;
     const int c = (L16 & 31) ^ ((k & 7) << 1);
-    int wc = tile_col(c * 8, nt, p.N, SWIGLU, p.gate_up_interleaved);
+    int wc = tile_col<C::BN>(c * 8, nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc > p.Ntot - 8) wc = p.Ntot - 8;
     return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc * 2u;
   }
@@ -298,21 +323,22 @@ MI355_HD void issue_stage(const GGParams& p, const Plan<C::CPW_A>& pl, int k, ui
   for (int j = 0; j < CPW; ++j)
     if (j < pl.a_copies) O::dma16(ab, pl.ao[j], O::uni(slot + (j * WAVES + wave) * 1024));
 #pragma unroll
-  for (int j = 0; j < CPW_B; ++j)
-    O::dma16(bb, b_off<MX, B_KN, SWIGLU>(p, pl.nt, wave * CPW_B + j, lane),
-             O::uni(slot + C::B_OFF + (wave * CPW_B + j) * 1024));
+  for (int j = 0; j < C::CPW_B; ++j)
+    O::dma16(bb, b_off<C, B_KN, SWIGLU>(p, pl.nt, wave * C::CPW_B + j, lane),
+             O::uni(slot + C::B_OFF + (wave * C::CPW_B + j) * 1024));
   if constexpr (MX) {
     // activation code planes: plane wave / 2, bytes 256 (wave % 2) + 4 lane of the item's run;
     // col_scale [G, K/64, Ntot, 2]: wave w (and w + 4) copies 64-K step (w >> 1) & 1, tile columns
-    // 128 (w & 1) ..+127
+    // 128 (w & 1) ..+127 (a 128-column tile: the waves with w & 1 == 0 only), to step * 2 BN
     const uint32_t so = (uint32_t)((wave & 1) * 256 + lane * 4);
-    int wc = tile_col((wave & 1) * 128 + lane * 2, pl.nt, p.N, SWIGLU, p.gate_up_interleaved);
+    int wc = tile_col<C::BN>((wave & 1) * 128 + lane * 2, pl.nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc > p.Ntot - 2) wc = p.Ntot - 2;
     const uint32_t bso = (uint32_t)((((wave >> 1) & 1) * p.Ntot + wc) * 2);
     O::dma4(O::uni_ptr(pl.s_base + (int64_t)k * pl.s_stride), so,
             O::uni(slot + C::AS_OFF + (wave >> 1) * AS_PLANE + (wave & 1) * 256));
-    O::dma4(O::uni_ptr(pl.bs_base + (int64_t)k * pl.b_scale_stride), bso,
-            O::uni(slot + C::BS_OFF + ((wave >> 1) & 1) * 512 + (wave & 1) * 256));
+    if (C::BN == 256 || (wave & 1) == 0)
+      O::dma4(O::uni_ptr(pl.bs_base + (int64_t)k * pl.b_scale_stride), bso,
+              O::uni(slot + C::BS_OFF + ((wave >> 1) & 1) * (2 * C::BN) + (wave & 1) * 256));
   }
 }
 
@@ -328,7 +354,7 @@ template <int MI> struct Frags<true, true, MI> { v4i al[MI], ah[MI]; v2i bp[NI][
 
 // a_off: the item's first routed row modulo 4 (the offset of the MX activation code planes)
 template <class C, bool B_KN, class O>
-MI355_HD void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int h, int grp, int wq, int lane_in,
+MI355_HD void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int h, int rbo, int wq, int lane_in,
                          int a_off, int nmi) {
   constexpr bool MX = C::MX;
   constexpr int MI = C::MI;
@@ -344,7 +370,7 @@ MI355_HD void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int 
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
         if (MI > 4 && mi >= nmi) continue;  // row block without rows of the item
-        const int r = (2 * mi + grp) * 32 + (lane & 31);
+        const int r = (C::RBS * mi + rbo) * 32 + (lane & 31);
         f.a[s2][mi] = O::template lds<v8bf>(As + chunk_off(r, ks * 2 + (lane >> 5)));
       }
 #pragma unroll
@@ -369,7 +395,7 @@ MI355_HD void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int 
     const uint8_t* BSs = slot + C::BS_OFF;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      const int r = (2 * mi + grp) * 32 + (lane & 31);
+      const int r = (C::RBS * mi + rbo) * 32 + (lane & 31);
       const int c0 = h * 4 + (lane >> 5);
       f.al[mi] = O::template lds<v4i>(As + chunk_off(r, c0));
       f.ah[mi] = O::template lds<v4i>(As + chunk_off(r, c0 + 2));
@@ -388,11 +414,12 @@ MI355_HD void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int 
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int k = h * 64 + (q >> 1) * 32 + (g16 >> 1) * 16 + (q & 1) * 8 + (m >> 1);
-          const int off = k * 256 + (((nb >> 4) ^ (k & 15)) << 4) + 8 * (m & 1);
+          constexpr int M = (1 << C::B_CH_LOG) - 1;
+          const int off = k * C::BN + (((nb >> 4) ^ (k & M)) << 4) + 8 * (m & 1);
           f.bp[ni][q] = O::tr8(Bs + off);
         }
       }
-      f.sb[ni] = O::template lds<uint8_t>(BSs + h * 512 + n * 2 + (lane >> 5));
+      f.sb[ni] = O::template lds<uint8_t>(BSs + h * (2 * C::BN) + n * 2 + (lane >> 5));
     }
   }
 }
@@ -446,12 +473,12 @@ MI355_HD float swiglu_act(float g_acc, float u_acc) {
 // with (row >> 2) & 3, so the two half-wavefronts (rows r and r + 4) write different banks.
 MI355_HD int stage_off(int row, int cb) { return row * 64 + ((((cb >> 4) ^ (row >> 2)) & 3) << 4) + (cb & 15); }
 
-// acc[mi][ni][r] holds row (2 mi + grp) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
+// acc[mi][ni][r] holds row (RBS mi + rbo) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4 and column
 // wq * 64 + ni * 32 + lane % 32 of the tile. Each 32 x 32 output block goes through the wave's LDS
 // staging block 16 rows at a time (LDS operations of a wave complete in order) and is written with
 // 16-byte stores (fp32: 32 bytes, MX: 8 e4m3 bytes per lane and the block's scale code).
 template <class C, int EPI, class O>
-MI355_HD void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[C::MI][NI], int grp, int wq, int lane_in,
+MI355_HD void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[C::MI][NI], int rbo, int wq, int lane_in,
                        uint8_t* stage) {
   constexpr int MI = C::MI;
   // the lane index made opaque: the staging offsets are recomputed here instead of being hoisted out
@@ -461,7 +488,7 @@ MI355_HD void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[C::M
   constexpr int NB = EPI == EPI_STORE_BF16 ? NI : 1;  // output blocks per 32 rows
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
-    const int row_base = (2 * mi + grp) * 32;  // first tile row of the block
+    const int row_base = (C::RBS * mi + rbo) * 32;  // first tile row of the block
     if (row_base >= it.rows) continue;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -469,7 +496,7 @@ MI355_HD void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[C::M
         // Two halves of 16 rows: the fp32 SwiGLU values go through the staging block (16 rows x 128
         // bytes); lane l then holds row l / 4, columns 8 (l % 4) ..+7 of the 32-column block cb of the
         // output rows.
-        const int cb = it.nt * 4 + wq;
+        const int cb = it.nt * (C::BN / 64) + wq;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
@@ -527,8 +554,8 @@ MI355_HD void epilogue(const GGParams& p, const Item& it, const v16f (&acc)[C::M
           }
           const int row = lane >> 2, c = lane & 3;
           const v4i v = O::template lds_load<v4i>(st + stage_off(row, c * 16));
-          const int col = EPI == EPI_STORE_BF16 ? it.nt * BN + wq * WN + nb * 32 + c * 8
-                                                : it.nt * (BN / 2) + wq * 32 + c * 8;
+          const int col = EPI == EPI_STORE_BF16 ? it.nt * C::BN + wq * WN + nb * 32 + c * 8
+                                                : it.nt * (C::BN / 2) + wq * 32 + c * 8;
           if (row_base + hh * 16 + row < it.rows && col < p.N) {
             const int64_t orow = it.row0 + row_base + hh * 16 + row;
             O::template store<v4i>((uint16_t*)p.C + orow * p.ldc + col, v);
@@ -545,13 +572,32 @@ inline bool pp_tall(const GGParams& p, bool mx) {
   return !mx && p.rows_hint > 0 && p.rows_hint <= (int64_t)p.G * 320 && p.G <= Cfg<false, true>::PREFIX_MAX;
 }
 
-// The kernel instance of a call that mi355_gg_pp_applies accepted:
-// L.template run<MX, B_KN, EPI, TALL>(p). The library launches it; the host-side checker replays it.
+// MX: the skinny tile for the groups of 257..384 rows, when switched on and the rows average 128..512
+// per group (else few groups fall in the range)
+inline bool pp_skinny(const GGParams& p) {
+  return mi355_pp_skinny_enabled() && p.G <= Cfg<true, true>::PREFIX_MAX && p.rows_hint >= (int64_t)p.G * 128 &&
+         p.rows_hint <= (int64_t)p.G * 512;
+}
+
+// The kernel instances of a call that mi355_gg_pp_applies accepted: L.template run<MX, B_KN, EPI,
+// TALL, SEL>(p), one launch, or two for MX with the skinny tile (the other groups on the 256 x 256
+// tile, then the skinny range on 384 x 128, whose n-tiles are half as wide). The library launches
+// them; the host-side checker replays them.
 template <bool MX, bool B_KN, int EPI, class Launch>
 int pp_select_tall(const GGParams& p, Launch& L) {
-  if constexpr (!MX)
-    if (pp_tall(p, MX)) return L.template run<MX, B_KN, EPI, true>(p);
-  return L.template run<MX, B_KN, EPI, false>(p);
+  if constexpr (!MX) {
+    if (pp_tall(p, MX)) return L.template run<MX, B_KN, EPI, true, SEL_ALL>(p);
+  } else {
+    if (pp_skinny(p)) {
+      const int rc = L.template run<MX, B_KN, EPI, false, SEL_NOT_SKINNY>(p);
+      if (rc) return rc;
+      GGParams q = p;
+      constexpr int cols = EPI == EPI_STORE_BF16 ? Cfg<true, true>::BN : Cfg<true, true>::BN / 2;
+      q.n_tiles = (p.N + cols - 1) / cols;
+      return L.template run<MX, B_KN, EPI, true, SEL_SKINNY>(q);
+    }
+  }
+  return L.template run<MX, B_KN, EPI, false, SEL_ALL>(p);
 }
 template <class Launch>
 int pp_select(const GGParams& p, bool mx, bool b_kn, int epi, Launch& L) {

@@ -1770,7 +1770,7 @@ static void pp_gemm(std::vector<int> counts, int K, int N, bool mx, bool b_kn, b
   q.C = mk("pp_act_e4m3", (size_t)R * N);
   q.c_scale = mk("pp_act_planes", (size_t)cplanes);
   q.c_scale_stage_stride = R * 4;
-  sim_pp<true, true, EPI_SWIGLU_MX, false>(q);
+  sim_pp<true, true, EPI_SWIGLU_MX, false, pp::SEL_ALL>(q);
   if (!g_emulate) return;
   const float* f = (const float*)p.C;
   const uint8_t* e = (const uint8_t*)q.C;
@@ -2120,6 +2120,27 @@ static std::vector<Scenario> scenarios() {
   s.push_back({"emu_pp_mx_store", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 512, true, true, false, 0); })});
   s.push_back({"emu_pp_mx_swiglu", emu([=] { pp_gemm({70, 0, 129, 300, 1}, 256, 256, true, true, true, 0); })});
   s.push_back({"emu_pp_mx_swiglu_gu", emu([=] { pp_gemm({70, 0, 257, 1, 511}, 256, 256, true, true, true, 1); })});
+  // the skinny 384 x 128 MX tile (switched on for the scenario): the groups of 257..384 rows on it,
+  // the others on the 256 x 256 tile, in two launches
+  auto skinny = [](std::function<void()> f) {
+    return [f] {
+      const long before = g_pp_skinny_launches;
+      setenv("MI355MOE_PP_SKINNY", "1", 1);
+      f();
+      unsetenv("MI355MOE_PP_SKINNY");
+      if (g_pp_skinny_launches == before) CHECK_FAIL("no launch ran on the 384 x 128 tile");
+    };
+  };
+  s.push_back({"emu_pp_mx_skinny_store",
+               emu(skinny([=] { pp_gemm({300, 70, 384, 257, 385, 0, 256}, 256, 512, true, true, false, 0); }))});
+  s.push_back({"emu_pp_mx_skinny_swiglu",
+               emu(skinny([=] { pp_gemm({300, 70, 384, 257, 385, 0, 256}, 256, 256, true, true, true, 0); }))});
+  s.push_back({"emu_pp_mx_skinny_swiglu_gu",
+               emu(skinny([=] { pp_gemm({300, 70, 384, 257, 385, 0, 256}, 256, 256, true, true, true, 1); }))});
+  s.push_back({"pp_moe_mx_eio_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); }))});
+  s.push_back({"pp_moe_mx_gu_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); }))});
+  s.push_back({"pp_moe_mx_gu_skinny_skewed",
+               pp_route(skinny([=] { moe_forward(1500, 4, 12, 512, 256, MX, L_GU, 1.1); }))});
   s.push_back({"emu_moe_bf16_numerics_clamp", emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EIO, 0.0, 0, 7.0f); })});
   s.push_back({"emu_moe_bf16_numerics_after_silu",
                emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EOI, 0.0, MI355MOE_NUMERICS_CLAMP_AFTER_SILU, 7.0f); })});

@@ -141,7 +141,7 @@ def _built_kernel():
     return found
 
 
-PP_BF16_GMM1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true>(GGParams)"
+PP_BF16_GMM1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true, 0>(GGParams)"
 
 
 def test_bench_traffic_record(tmp_path):
@@ -220,8 +220,8 @@ def test_bench_profile_summary(tmp_path):
                [["__amd_rocclr_copyBuffer", "FETCH_SIZE", copy_kib / 2], ["other", "FETCH_SIZE", 1.0]])
     _write_csv(out / "copy" / "write" / "pmc_counter_collection.csv", cnt,
                [["__amd_rocclr_copyBuffer", "WRITE_SIZE", copy_kib]])
-    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true>(GGParams)"
-    g2 = "void (anonymous namespace)::gg_pp_kernel<false, false, 0, true>(GGParams)"
+    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true, 0>(GGParams)"
+    g2 = "void (anonymous namespace)::gg_pp_kernel<false, false, 0, true, 0>(GGParams)"
     for name, is_g1 in ((g1, True), (g2, False), ("void grouped_gemm_kernel<GGCfg<64, 1, 3, 3, 256, 2, 2, 2, false>, "
                                                    "true, true, 3>(GGParams)", True),
                         ("void grouped_gemm_kernel<false, false, 1>(GGParams)", False)):
@@ -259,7 +259,7 @@ def test_bench_profile_summary_times_the_timed_launches(tmp_path):
     copy_kib = bench.COPY_BYTES / 1024
     _write_csv(out / "copy" / "fetch" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "FETCH_SIZE", copy_kib]])
     _write_csv(out / "copy" / "write" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "WRITE_SIZE", copy_kib]])
-    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true>(GGParams)"
+    g1 = "void (anonymous namespace)::gg_pp_kernel<false, false, 2, true, 0>(GGParams)"
     d = out / "dsv3_bf16"
     for tag, c in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE"), ("mfma", "MfmaUtil")):
         _write_csv(d / tag / "pmc_counter_collection.csv", cnt, [[g1, c, 1.0]])

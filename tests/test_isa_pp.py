@@ -1,7 +1,8 @@
 """Register budget of the default 8-wave grouped GEMM (CPU only).
 
 gemm_pp.hip runs 8 waves per CU, two per SIMD, so each wave has 256 registers (VGPRs and AGPRs).
-The kernels' design (gemm_pp_plan.h) relies on it: the MXFP8 kernels spill nothing, and the bf16
+The kernels' design (gemm_pp_plan.h) relies on it: the MXFP8 kernels (256 x 256 and 384 x 128)
+spill nothing, and the bf16
 320-row kernels spill one 64-bit value outside the stage loops (a reload inside the loop would wait
 for all outstanding copies). This test compiles gemm_pp.hip for gfx950 to AMD assembly (the code
 built here) and checks, for every kernel, the register count, the spill size and that no scratch
@@ -64,14 +65,17 @@ def asm(tmp_path_factory):
 
 def test_pp_kernels_register_budget(asm):
     bodies, meta = _kernels(asm)
-    assert len(bodies) >= 10 and set(bodies) == set(meta)
+    assert len(bodies) >= 14 and set(bodies) == set(meta)
+    assert any(re.search(r"ILb1ELb1ELi\d+ELb1ELi2E", n) for n in bodies)  # the 384 x 128 MX tile
     for name, lines in bodies.items():
-        mx = "ILb1E" in name  # gg_pp_kernel<MX, B_KN, EPI, TALL>: the first template argument
-        tall = name.endswith("ELb1EEEv8GGParams")
+        # gg_pp_kernel<MX, B_KN, EPI, TALL, SEL>
+        args = re.search(r"gg_pp_kernelILb(\d)ELb(\d)ELi(\d+)ELb(\d)ELi(\d)EEEv8GGParams", name)
+        assert args, name
+        mx, tall = args.group(1) == "1", args.group(4) == "1"  # MX TALL: the 384 x 128 tile
         m = meta[name]
         assert m["vgpr"] <= 256, (name, m)
         if mx or not tall:
-            assert m["private"] == 0, (name, m)  # spill-free
+            assert m["private"] == 0, (name, m)  # spill-free (the MX kernels, the 384 x 128 one included)
         else:
             assert m["private"] <= 16, (name, m)
         assert _scratch_in_loops(lines) == [], name
