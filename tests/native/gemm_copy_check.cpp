@@ -2139,6 +2139,8 @@ static std::vector<Scenario> scenarios() {
                emu(skinny([=] { pp_gemm({300, 70, 384, 257, 385, 0, 256}, 256, 256, true, true, true, 1); }))});
   s.push_back({"pp_moe_mx_eio_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); }))});
   s.push_back({"pp_moe_mx_gu_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); }))});
+  s.push_back({"pp_moe_mx_gu_skinny_none",  // no group in the range: the 384 x 128 launch has no work
+               pp_route(skinny([=] { moe_forward(700, 4, 16, 256, 256, MX, L_GU, 0.0); }))});
   s.push_back({"pp_moe_mx_gu_skinny_skewed",
                pp_route(skinny([=] { moe_forward(1500, 4, 12, 512, 256, MX, L_GU, 1.1); }))});
   s.push_back({"emu_moe_bf16_numerics_clamp", emu([=] { moe_forward(16, 4, 16, 512, 256, BF, L_EIO, 0.0, 0, 7.0f); })});

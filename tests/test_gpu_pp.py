@@ -150,3 +150,39 @@ def test_moe_forward_decode_shape_pp(gpu, variant, precision):
     if precision == "bf16":
         ref = orc.expert_forward_reference(x, ids, probs, w1, w2, layout="EIO")
         assert orc.rel_l2(out_pp, ref) < BF16_REL_L2
+
+
+@pytest.mark.parametrize("T,H,I,E,K,gu", [(640, 1024, 384, 4, 2, False), (640, 1024, 384, 4, 2, True),
+                                          (960, 512, 256, 12, 4, True), (700, 1024, 512, 16, 4, False)])
+def test_moe_forward_mxfp8_skinny_tile_bit_identical(gpu, monkeypatch, T, H, I, E, K, gu):
+    """The 384 x 128 MX tile (MI355MOE_PP_SKINNY=1: experts of 257..384 routed rows on it, one weight
+    pass) runs the same MFMAs in the same K order per output element as the 256 x 256 tile, so the
+    forward is bit-identical with it switched on and off (both GEMMs), and matches the oracle."""
+    from hyper_multicore_amd import ops
+    print(f"[pp] skinny mxfp8 T={T} H={H} I={I} E={E} K={K} gu={gu}", flush=True)
+    g = _seed(T + E + 17)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    probs = torch.rand(T, K, generator=g)
+    probs = probs / probs.sum(1, keepdim=True)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16)
+    d1, s1 = ops.mx_quantize_cols(w1.to(gpu))
+    d2, s2 = ops.mx_quantize_cols(w2.to(gpu))
+    a1, b1 = d1.view(torch.uint8), s1
+    layout = "EIO"
+    if gu:
+        a1, b1 = ops.interleave_gate_up(d1.view(torch.uint8), s1)
+        layout = "EIO_GU"
+    counts = torch.bincount(ids.reshape(-1), minlength=E)
+    assert bool(((counts > 256) & (counts <= 384)).any()) or T == 700
+    args = dict(num_experts=E, intermediate_size=I, precision="mxfp8", layout=layout, w1_scale=b1, w2_scale=s2)
+    ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), a1, d2.view(torch.uint8))
+    monkeypatch.delenv("MI355MOE_PP_SKINNY", raising=False)
+    out = ops.moe_forward(*ins, **args).cpu()
+    monkeypatch.setenv("MI355MOE_PP_SKINNY", "1")
+    out_skinny = ops.moe_forward(*ins, **args).cpu()
+    assert torch.equal(out_skinny, out)
+    ref = orc.expert_forward_reference(x, ids, probs, d1.cpu().view(torch.uint8), d2.cpu().view(torch.uint8),
+                                       precision="mxfp8", w1_scale=s1.cpu(), w2_scale=s2.cpu())
+    assert orc.rel_l2(out_skinny, ref) < 3e-2
