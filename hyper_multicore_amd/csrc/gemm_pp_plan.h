@@ -10,19 +10,21 @@
 // run on a GPU. Policy methods that only the device needs (`opaque`, `uni`) are identities on the
 // host.
 //
-// Work list: every (group, BM-row m-tile, 256-column n-tile) is one work item; the m-tiles of a
-// group come from group_list at the kernel's own tile height (tile prefix and group row ends in
-// LDS). Workgroup b starts at item (b % 8) * (grid / 8) + b / 8 and steps by the grid, so each XCD
+// Work list: every (group, BM-row m-tile, BN-column n-tile) is one work item of the groups the launch
+// takes (all, or either side of the skinny tile's row range); the m-tiles of a group come from
+// group_list at the kernel's own tile height (tile prefix and group row ends in LDS). Workgroup b starts at item (b % 8) * (grid / 8) + b / 8 and steps by the grid, so each XCD
 // runs a contiguous run of items (m fastest) and the n-tiles that re-read one expert's activation
 // rows run at the same time on one XCD and share its L2.
 //
 // Workgroup: 512 threads = 8 wavefronts, two per SIMD. Tiles are BM x 256 (BM = 320 for bf16, 256
-// for MXFP8). The waves form two groups, 0-3 and 4-7, one wave of each on every SIMD; wave w
-// computes columns 64 * (w % 4) ..+63 of the 32-row blocks 2 mi + w / 4 (mi < BM / 64), 2 x BM / 64
-// blocks of 32 x 32 (bf16 v_mfma_f32_32x32x16_bf16, MXFP8 v_mfma_scale_f32_32x32x64_f8f6f4). The row
-// blocks alternate between the groups and the activation copies between the waves, so a tile that
-// is not full keeps the two groups and the eight waves evenly loaded; bf16 waves skip the MFMAs of
-// row blocks past the item's rows.
+// for MXFP8), or 384 x 128 (the MXFP8 skinny tile). The waves form two groups, 0-3 and 4-7, one wave
+// of each on every SIMD; on the 256-column tiles wave w computes columns 64 * (w % 4) ..+63 of the
+// 32-row blocks 2 mi + w / 4 (mi < BM / 64), on the 128-column tile columns 64 * (w % 2) ..+63 of the
+// blocks 4 mi + w / 4 + 2 ((w % 4) / 2) (mi < 3): 2 x MI blocks of 32 x 32 (bf16
+// v_mfma_f32_32x32x16_bf16, MXFP8 v_mfma_scale_f32_32x32x64_f8f6f4). The row blocks alternate between
+// the groups and the activation copies between the waves, so a tile that is not full keeps the two
+// groups and the eight waves evenly loaded; bf16 waves skip the MFMAs of row blocks past the item's
+// rows.
 //
 // K stages are 128 bytes per row (64 bf16 or 128 e4m3): whole 128-byte lines per row and stage. A
 // stage is 64 KB of operands, so the LDS ring has two slots: the copies of stage q + 1 go out at the
@@ -31,13 +33,13 @@
 // LDS layouts (16-byte chunks, XOR swizzled against bank conflicts):
 //   K-contiguous rows (activations; EOI weights): row r at r * 128, chunk c at c ^ ((r >> 1) & 7),
 //     read with ds_read_b128;
-//   N-contiguous weights (EIO bf16, MX col_data): K row k of the stage holds 256 columns; bf16
-//     chunk c at c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows),
-//     read with ds_read_b64_tr_b16 / ds_read_b64_tr_b8;
+//   N-contiguous weights (EIO bf16, MX col_data): K row k of the stage holds the tile's columns; bf16
+//     chunk c at c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows; the
+//     128-column tile: c ^ (k & 7), 128-byte rows), read with ds_read_b64_tr_b16 / ds_read_b64_tr_b8;
 //   MX scales of a stage: code j (0..3) of tile row r at j * 512 + row0 % 4 + r (from the
 //     stage-major code planes of the activation scales: two 256-byte runs per code from the 4-aligned
 //     address at or below the tile's first row); weight tile column j's two codes of 64-K step s at
-//     s * 512 + j * 2 (the MX root's col_scale pairs).
+//     s * 2 BN + j * 2 (the MX root's col_scale pairs).
 //
 // Epilogues: bf16 store, SwiGLU -> bf16 (each 32 x 32 block through a wave-private LDS staging block,
 // so the global stores are 16 bytes per lane), for MX inputs SwiGLU -> fp32 (staged 16 rows at a
