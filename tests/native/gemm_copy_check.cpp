@@ -2139,6 +2139,19 @@ static std::vector<Scenario> scenarios() {
                emu(skinny([=] { pp_gemm({300, 70, 384, 257, 385, 0, 256}, 256, 256, true, true, true, 1); }))});
   s.push_back({"pp_moe_mx_eio_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); }))});
   s.push_back({"pp_moe_mx_gu_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); }))});
+  // the switched-off paths stay off without their environment variables
+  s.push_back({"gate_skinny_off", pp_route([=] {
+                 const long before = g_pp_skinny_launches;
+                 moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0);
+                 if (g_pp_skinny_launches != before) CHECK_FAIL("the 384 x 128 tile ran while switched off");
+               })});
+  s.push_back({"gate_decode_prep_off", [=] {
+                 const long before = g_preps;
+                 unsetenv("MI355MOE_DECODE_PREP");
+                 moe_forward(32, 8, 64, 1024, 512, MX, L_GU, 0.0);
+                 setenv("MI355MOE_DECODE_PREP", "1", 1);
+                 if (g_preps != before) CHECK_FAIL("the one-launch decode prologue ran while switched off");
+               }});
   s.push_back({"pp_moe_mx_gu_skinny_none",  // no group in the range: the 384 x 128 launch has no work
                pp_route(skinny([=] { moe_forward(700, 4, 16, 256, 256, MX, L_GU, 0.0); }))});
   s.push_back({"pp_moe_mx_gu_skinny_skewed",
