@@ -270,8 +270,10 @@ def measured_traffic(workload: str, variant: str, layout: str, root: str = ROOT)
     with open(path) as f:
         rec = json.load(f)
     from hyper_multicore_amd import _lib, codeobj
-    sym, digest = rec.get("symbol"), rec.get("code_digest")
-    if sym is None or digest is None or codeobj.kernel_digests(str(_lib.LIB_PATH)).get(sym) != digest:
+    syms = rec.get("symbols", [rec.get("symbol")])
+    digests = rec.get("code_digests", [rec.get("code_digest")])
+    have = codeobj.kernel_digests(str(_lib.LIB_PATH))
+    if not syms or any(s is None or d is None or have.get(s) != d for s, d in zip(syms, digests)):
         return None, "stale"
     return round((rec["fetch_kib"] * rec["fetch_factor"] + rec["write_kib"] * rec["write_factor"]) * 1024.0), "current"
 
@@ -460,34 +462,41 @@ def summarize(workload: str, out: str, dest: str = os.path.join(ROOT, "profiles"
     gmm1 = [r for r in stats if GMM1_KERNEL.search(r["Name"])]
     if not gmm1:
         raise ValueError("no GMM1 (SwiGLU-epilogue grouped GEMM) kernel in the trace")
-    g1 = gmm1[0]["Name"]
-    is_g1 = lambda name: name == g1  # noqa: E731
+    # GMM1 may be more than one launch per step (the 384 x 128 MX tile beside the 256 x 256 one): the
+    # SwiGLU-epilogue kernels launched as often as the most frequent one, each counted per step
+    calls = max(int(r["Calls"]) for r in gmm1)
+    g1s = [r["Name"] for r in gmm1 if int(r["Calls"]) == calls]
+    g1 = g1s[0]
     copy_kib = COPY_BYTES / 1024.0
     is_copy = lambda name: "copyBuffer" in name  # noqa: E731
     fetch_factor = copy_kib / _counter_mean(os.path.join(out, "copy", "fetch"), "FETCH_SIZE", is_copy)
     write_factor = copy_kib / _counter_mean(os.path.join(out, "copy", "write"), "WRITE_SIZE", is_copy)
-    fetch = _counter_mean(os.path.join(d, "fetch"), "FETCH_SIZE", is_g1)
-    write = _counter_mean(os.path.join(d, "write"), "WRITE_SIZE", is_g1)
-    mfma = _counter_mean(os.path.join(d, "mfma"), "MfmaUtil", is_g1)
+    fetch = sum(_counter_mean(os.path.join(d, "fetch"), "FETCH_SIZE", lambda n, k=k: n == k) for k in g1s)
+    write = sum(_counter_mean(os.path.join(d, "write"), "WRITE_SIZE", lambda n, k=k: n == k) for k in g1s)
     traffic = (fetch * fetch_factor + write * write_factor) * 1024.0
     cfg = line["config"]
     variant, layout = cfg.get("gemm_variant", "default"), cfg.get("weight_layout", "EIO")
     rf = line["roofline"]
-    avg_us = float(gmm1[0]["AverageNs"]) / 1e3
+    avg_of = {r["Name"]: float(r["AverageNs"]) / 1e3 for r in gmm1}
+    avg_us = sum(avg_of[k] for k in g1s)
     # the launches of the timed steps: the run's GMM1 launches in order are the routing-count step,
     # the warm-up steps, the timed steps, then those of the graph-replay measurement (the average
     # above holds them all)
-    timed_us = avg_us
+    timed = dict(avg_of)
     try:
         trace = _csv_rows(os.path.join(d, "kt"), "kernel_trace.csv")
-        durs = [(int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-                for r in trace if r["Kernel_Name"] == g1]
-        durs.sort()
         n, skip = int(line.get("steps", 0)), 1 + int(line.get("warmup", 0))
-        if n > 0 and len(durs) >= skip + n:
-            timed_us = sum(v for _, v in durs[skip:skip + n]) / n
+        for k in g1s:
+            durs = sorted((int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                          for r in trace if r["Kernel_Name"] == k)
+            if n > 0 and len(durs) >= skip + n:
+                timed[k] = sum(v for _, v in durs[skip:skip + n]) / n
     except FileNotFoundError:
         pass
+    timed_us = sum(timed[k] for k in g1s)
+    # MfmaUtil of the launches, weighted by their time
+    mfma = sum(_counter_mean(os.path.join(d, "mfma"), "MfmaUtil", lambda n, k=k: n == k) * timed[k] for k in g1s)
+    mfma /= timed_us
     cmds = profile_commands(workload)
     cal = calibration_commands()
     lines = [f"# rocprofv3 summary: MoE layer forward, workload {workload} (GEMM variant {variant}, {layout} weights)",
@@ -502,7 +511,7 @@ def summarize(workload: str, out: str, dest: str = os.path.join(ROOT, "profiles"
                      f"{float(r['MinNs']) / 1e3:>10.1f} {float(r['MaxNs']) / 1e3:>10.1f} "
                      f"{float(r['TotalDurationNs']) / 1e6:>10.3f}")
     alg = rf.get("algorithmic_bytes")
-    lines += ["", f"GMM1 kernel: {g1}",
+    lines += ["", f"GMM1 kernel: {' + '.join(g1s)}",
               f"  rocprofv3 duration of the timed steps' launches: {timed_us:.1f} us (all {int(gmm1[0]['Calls'])} "
               f"launches, warm-up included: {avg_us:.1f} us); bench HIP-event launch time: "
               f"{rf.get('launch_ms', float('nan')) * 1e3:.1f} us",
@@ -521,13 +530,20 @@ def summarize(workload: str, out: str, dest: str = os.path.join(ROOT, "profiles"
         f.write("\n".join(lines) + "\n")
     from hyper_multicore_amd import _lib, codeobj
     # the library this summary runs beside is the one the counter runs loaded (the same tree)
-    found = codeobj.find_kernel(str(_lib.LIB_PATH), g1) if _lib.LIB_PATH.exists() else None
-    if found is None:
-        print(f"[summarize] {g1} is not in {_lib.LIB_PATH}: the record gets no code digest and reads as stale",
-              file=sys.stderr)
-        found = (None, None)
+    founds = []
+    for k in g1s:
+        found = codeobj.find_kernel(str(_lib.LIB_PATH), k) if _lib.LIB_PATH.exists() else None
+        if found is None:
+            print(f"[summarize] {k} is not in {_lib.LIB_PATH}: the record gets no code digest and reads as stale",
+                  file=sys.stderr)
+            found = (None, None)
+        founds.append(found)
+    found = founds[0]
     with open(os.path.join(dest, f"traffic_{workload}_{variant}_{layout}.json"), "w") as f:
-        json.dump({"kernel": g1, "symbol": found[0], "code_digest": found[1], "fetch_kib": round(fetch, 1), "fetch_factor": round(fetch_factor, 4),
+        json.dump({"kernel": g1, "symbol": found[0], "code_digest": found[1],
+                   **({"kernels": g1s, "symbols": [f[0] for f in founds], "code_digests": [f[1] for f in founds]}
+                      if len(g1s) > 1 else {}),
+                   "fetch_kib": round(fetch, 1), "fetch_factor": round(fetch_factor, 4),
                    "write_kib": round(write, 1), "write_factor": round(write_factor, 4),
                    "mfma_util_pct": round(mfma, 2), "rocprof_avg_us": round(avg_us, 1),
                    "rocprof_timed_us": round(timed_us, 1),

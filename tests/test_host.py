@@ -377,3 +377,43 @@ def test_bench_targets_block():
     assert t["dsv3_decode_mxfp8_gmm1_hbm_frac"] == {"measured": 0.66, "bar": 0.65}
     assert t["dsv3_decode_mxfp8_layer_hbm_frac"]["measured"] == 0.61
     assert bench.targets({"small_bf16": {}}) == {}
+
+
+def test_bench_profile_summary_two_gmm1_launches(tmp_path):
+    """With the 384 x 128 MX tile GMM1 is two launches per step: the summary adds their counters and
+    durations, and the traffic record names both kernels (each must be current for the bench to use it)."""
+    import json
+    import bench
+    from hyper_multicore_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("native library not built")
+    out = tmp_path / "prof"
+    cnt = ["Kernel_Name", "Counter_Name", "Counter_Value"]
+    copy_kib = bench.COPY_BYTES / 1024
+    _write_csv(out / "copy" / "fetch" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "FETCH_SIZE", copy_kib]])
+    _write_csv(out / "copy" / "write" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "WRITE_SIZE", copy_kib]])
+    a = "void (anonymous namespace)::gg_pp_kernel<true, true, 5, false, 1>(GGParams)"
+    b = "void (anonymous namespace)::gg_pp_kernel<true, true, 5, true, 2>(GGParams)"
+    g2 = "void (anonymous namespace)::gg_pp_kernel<true, true, 0, false, 1>(GGParams)"
+    d = out / "dsv3_mxfp8"
+    _write_csv(d / "fetch" / "pmc_counter_collection.csv", cnt, [[a, "FETCH_SIZE", 3000.0], [b, "FETCH_SIZE", 1000.0],
+                                                                 [g2, "FETCH_SIZE", 9.0]])
+    _write_csv(d / "write" / "pmc_counter_collection.csv", cnt, [[a, "WRITE_SIZE", 30.0], [b, "WRITE_SIZE", 10.0]])
+    _write_csv(d / "mfma" / "pmc_counter_collection.csv", cnt, [[a, "MfmaUtil", 30.0], [b, "MfmaUtil", 60.0]])
+    st = ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs"]
+    _write_csv(d / "kt" / "run_kernel_stats.csv", st,
+               [[a, 10, 3e7, 3e6, 50, 3e6, 3e6], [b, 10, 1e7, 1e6, 20, 1e6, 1e6], [g2, 10, 2e7, 2e6, 30, 2e6, 2e6]])
+    line = {"value": 1.0, "ms_per_step": 6.0, "config": {"gemm_variant": "default", "weight_layout": "EIO_GU"},
+            "roofline": {"algorithmic_bytes": 4096 * 1024, "launch_ms": 4.0}}
+    (d / "bench.json").write_text(json.dumps(line) + "\n")
+    txt = bench.summarize("dsv3_mxfp8", str(out), dest=str(tmp_path / "profiles"))
+    rec = json.loads((tmp_path / "profiles" / "traffic_dsv3_mxfp8_default_EIO_GU.json").read_text())
+    assert rec["kernels"] == [a, b] and len(rec["symbols"]) == 2 and None not in rec["code_digests"]
+    assert rec["fetch_kib"] == 4000.0 and rec["write_kib"] == 40.0
+    assert rec["rocprof_avg_us"] == 4000.0 and rec["mfma_util_pct"] == 37.5  # (30 * 3 + 60 * 1) / 4
+    assert bench.measured_traffic("dsv3_mxfp8", "default", "EIO_GU", root=str(tmp_path)) == ((4000 + 40) * 1024,
+                                                                                           "current")
+    assert f"GMM1 kernel: {a} + {b}" in open(txt).read()
+    rec["code_digests"][1] = "0" * 16
+    (tmp_path / "profiles" / "traffic_dsv3_mxfp8_default_EIO_GU.json").write_text(json.dumps(rec))
+    assert bench.measured_traffic("dsv3_mxfp8", "default", "EIO_GU", root=str(tmp_path)) == (None, "stale")
