@@ -179,8 +179,19 @@ def m_tiles(c: dict, counts: torch.Tensor, variant: str = "default", decode_tile
         bm = 320  # the 8-wave configuration's tall bf16 tiles (groups averaging at most 320 rows)
     else:
         bm = 256
-    tiles = int(((counts + bm - 1) // bm).sum())
-    return {"bm": bm, "tiles": tiles, "ideal": -(-R // bm), "padded_row_frac": round(1 - R / (tiles * bm), 4)}
+    active = max(1, int((counts > 0).sum()))
+    # the 384 x 128 MX tile (MI355MOE_PP_SKINNY=1): groups of 257..384 rows in one m-tile of 384 rows
+    skinny = (bm == 256 and c["precision"] == "mxfp8" and variant in ("default", "pp")
+              and os.environ.get("MI355MOE_PP_SKINNY") == "1" and c["E"] * 128 <= R <= c["E"] * 512)
+    in_range = ((counts > 256) & (counts <= 384)) if skinny else torch.zeros_like(counts, dtype=torch.bool)
+    tiles = int(((counts[~in_range] + bm - 1) // bm).sum())
+    n_skinny = int(in_range.sum())
+    res = {"bm": bm, "tiles": tiles, "ideal": -(-R // bm),
+           "padded_row_frac": round(1 - R / (tiles * bm + n_skinny * 384), 4),
+           "weight_passes_per_expert": round((tiles + n_skinny) / active, 3)}
+    if skinny:
+        res["skinny_tiles"] = n_skinny
+    return res
 
 
 def measure(layer: Layer, steps: int, warmup: int) -> dict:

@@ -417,3 +417,18 @@ def test_bench_profile_summary_two_gmm1_launches(tmp_path):
     rec["code_digests"][1] = "0" * 16
     (tmp_path / "profiles" / "traffic_dsv3_mxfp8_default_EIO_GU.json").write_text(json.dumps(rec))
     assert bench.measured_traffic("dsv3_mxfp8", "default", "EIO_GU", root=str(tmp_path)) == (None, "stale")
+
+
+def test_bench_m_tiles_weight_passes(monkeypatch):
+    """m_tiles counts the expert weight passes: an expert of 257..511 rows takes two 256-row m-tiles,
+    or one 384-row tile with MI355MOE_PP_SKINNY=1 when it has at most 384 rows."""
+    import bench
+    c = dict(bench.CONFIGS["dsv3_mxfp8"], T=256, K=4, E=4)  # R = 1024, 256 rows per expert on average
+    counts = torch.tensor([100, 300, 384, 240])
+    monkeypatch.delenv("MI355MOE_PP_SKINNY", raising=False)
+    r = bench.m_tiles(c, counts)
+    assert r["bm"] == 256 and r["tiles"] == 1 + 2 + 2 + 1 and r["weight_passes_per_expert"] == 1.5
+    monkeypatch.setenv("MI355MOE_PP_SKINNY", "1")
+    r = bench.m_tiles(c, counts)
+    assert r["tiles"] == 2 and r["skinny_tiles"] == 2 and r["weight_passes_per_expert"] == 1.0
+    assert r["padded_row_frac"] == round(1 - 1024 / (2 * 256 + 2 * 384), 4)
