@@ -29,10 +29,10 @@ MI355_DEV void lds_dma(const void* g, uint32_t lds_off_uniform, uint8_t* smem, i
   const int en = __builtin_amdgcn_readfirstlane(enable);
   if constexpr (SZ == 16)
     asm volatile("s_cmp_eq_u32 %2, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
-                 "global_load_lds_dwordx4 %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc");
+                 "global_load_lds_dwordx4 %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc", "m0");
   else if constexpr (SZ == 4)
     asm volatile("s_cmp_eq_u32 %2, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
-                 "global_load_lds_dword %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc");
+                 "global_load_lds_dword %0, off\n1:" ::"v"(g), "s"(m0), "s"(en) : "memory", "scc", "m0");
   else static_assert(SZ == 16, "unsupported DMA size");
 }
 // The copy policy of the kernels (see gemm_plan.h).

@@ -135,14 +135,15 @@ struct PpDev {
   // Direct global -> LDS copies: lane i writes its 16 (4) bytes at LDS address M0 + 16 i (4 i).
   // Inline assembly, so that the compiler does not treat the copy as an alias of every later LDS read
   // (its builtin makes it wait for all outstanding loads before the next ds_read). The source is a
-  // wave-uniform base in scalar registers plus a 32-bit per-lane offset; m0 is an LDS address.
+  // wave-uniform base in scalar registers plus a 32-bit per-lane offset; m0 is an LDS address (and
+  // declared clobbered, so the compiler keeps no value of its own in it across a copy).
   MI355_DEV static void dma16(const uint8_t* base, uint32_t off, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
-                 : "memory");
+                 : "memory", "m0");
   }
   MI355_DEV static void dma4(const uint8_t* base, uint32_t off, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
-                 : "memory");
+                 : "memory", "m0");
   }
   template <class T>
   MI355_DEV static T lds(const uint8_t* p) {

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void rc_regs(const u4* __restrict__ p, int64_t
 
 __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
-               : "memory");
+               : "memory", "m0");
 }
 
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
