@@ -36,7 +36,7 @@ __device__ __forceinline__ void barrier() {
 
 template <bool MX, bool B_KN, int EPI, bool TALL, int SEL>
 __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
-  using C = Cfg<MX, TALL>;
+  using C = Cfg<MX, TALL, sel_skinny<SEL>>;
   constexpr int MI = C::MI, S_SLOT = C::SLOT;
   constexpr bool SWIGLU = EPI == EPI_SWIGLU_BF16 || EPI == EPI_SWIGLU_F32;
   constexpr int ESIZE = MX ? 1 : 2;
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
       if (g < p.G) {
         const int64_t end = p.group_list[g];
         const int64_t rows = end - (g == 0 ? 0 : p.group_list[g - 1]);
-        cnt[u] = rows > 0 && sel_takes<SEL>(rows) ? (int)((rows + C::BM - 1) / C::BM) : 0;
+        cnt[u] = rows > 0 && sel_takes<SEL, C::BM>(rows) ? (int)((rows + C::BM - 1) / C::BM) : 0;
         s_rows[g] = (int32_t)end;
       }
       local += cnt[u];
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_pp_kernel(GGParams p) {
 
 template <bool MX, bool B_KN, int EPI, bool TALL, int SEL>
 int launch_pp_k(const GGParams& p, hipStream_t stream) {
-  using C = Cfg<MX, TALL>;
+  using C = Cfg<MX, TALL, sel_skinny<SEL>>;
   auto kern = gg_pp_kernel<MX, B_KN, EPI, TALL, SEL>;
   static bool configured = false;
   if (!configured) {

@@ -62,15 +62,19 @@ constexpr int WN = 64, NI = WN / 32;
 constexpr int AS_PLANE = 512;
 constexpr int AS_BYTES = 4 * AS_PLANE;
 
-// The skinny tile's groups: those of SKINNY_LO + 1 .. SKINNY_HI rows
-constexpr int SKINNY_LO = 256, SKINNY_HI = 384;
-// Groups a launch takes: SEL_ALL, SEL_NOT_SKINNY (all but the skinny range), SEL_SKINNY (only it)
-enum { SEL_ALL = 0, SEL_NOT_SKINNY = 1, SEL_SKINNY = 2 };
+// The skinny tile (384 x 128) takes the groups of more rows than the other launch's tile height and
+// at most SKINNY_HI. Groups a launch takes: SEL_ALL; SEL_NOT_SKINNY (all but those, on a tile of BM
+// rows); SEL_SKINNY_256 / SEL_SKINNY_320 (only those, beside a launch on 256- / 320-row tiles).
+constexpr int SKINNY_HI = 384;
+enum { SEL_ALL = 0, SEL_NOT_SKINNY = 1, SEL_SKINNY_256 = 2, SEL_SKINNY_320 = 3 };
 template <int SEL>
+constexpr bool sel_skinny = SEL >= SEL_SKINNY_256;
+template <int SEL, int BM>
 MI355_HD bool sel_takes(int64_t rows) {
   if constexpr (SEL == SEL_ALL) return true;
-  const bool skinny = rows > SKINNY_LO && rows <= SKINNY_HI;
-  return SEL == SEL_SKINNY ? skinny : !skinny;
+  constexpr int lo = SEL == SEL_SKINNY_256 ? 256 : SEL == SEL_SKINNY_320 ? 320 : BM;
+  const bool skinny = rows > lo && rows <= SKINNY_HI;
+  return sel_skinny<SEL> ? skinny : !skinny;
 }
 
 // Tile shape and LDS layout. Tiles are 256 x 256; 320 x 256 for bf16 GEMMs whose groups average at
@@ -79,13 +83,12 @@ MI355_HD bool sel_takes(int64_t rows) {
 // rows (DeepSeek-V3 prefill routes 256 on average, with a wide spread) is one m-tile instead of a
 // full one and a short one that streams the weights again. When groups are large multiples of 256
 // rows the fifth row block costs more than the tiles it saves. MX tiles of 256 rows have no registers
-// left for a fifth row block; for MX, TALL is the skinny 384 x 128 tile instead (same accumulators
-// per workgroup: each wave 3 row blocks x 64 columns, two waves of a group per column range), which
-// streams the weights of an expert of 257..384 rows once.
-template <bool MX_, bool TALL>
+// left for a fifth row block. SK: the skinny 384 x 128 tile (each wave 3 row blocks x 64 columns, two
+// waves of a group per column range), which streams the weights of an expert of up to 384 rows once.
+template <bool MX_, bool TALL, bool SK = false>
 struct Cfg {
   static constexpr bool MX = MX_;
-  static constexpr bool SKINNY = MX_ && TALL;
+  static constexpr bool SKINNY = SK;
   static constexpr int BM = SKINNY ? 384 : (MX || !TALL) ? 256 : 320;
   static constexpr int BN = SKINNY ? 128 : 256;
   static constexpr int WQN = BN / WN;            // waves of a group across the tile's columns
@@ -575,30 +578,40 @@ inline bool pp_tall(const GGParams& p, bool mx) {
   return !mx && p.rows_hint > 0 && p.rows_hint <= (int64_t)p.G * 320 && p.G <= Cfg<false, true>::PREFIX_MAX;
 }
 
-// MX: the skinny tile for the groups of 257..384 rows, when switched on and the rows average 128..512
-// per group (else few groups fall in the range)
+// The skinny tile for the groups above the other tile's height and up to 384 rows, when switched on
+// and the rows average 128..512 per group (else few groups fall in the range); MX, and bf16 with
+// K-contiguous (EOI) weights
 inline bool pp_skinny(const GGParams& p) {
-  return mi355_pp_skinny_enabled() && p.G <= Cfg<true, true>::PREFIX_MAX && p.rows_hint >= (int64_t)p.G * 128 &&
-         p.rows_hint <= (int64_t)p.G * 512;
+  return mi355_pp_skinny_enabled() && p.G <= Cfg<true, false, true>::PREFIX_MAX &&
+         p.rows_hint >= (int64_t)p.G * 128 && p.rows_hint <= (int64_t)p.G * 512;
+}
+
+// The regular launch over the groups outside the skinny range (tile height from TALL), then the
+// skinny one over the rest, whose n-tiles are half as wide.
+template <bool MX, bool B_KN, int EPI, bool TALL, class Launch>
+int pp_run_skinny(const GGParams& p, Launch& L) {
+  const int rc = L.template run<MX, B_KN, EPI, TALL, SEL_NOT_SKINNY>(p);
+  if (rc) return rc;
+  GGParams q = p;
+  constexpr int cols = EPI == EPI_STORE_BF16 ? Cfg<MX, false, true>::BN : Cfg<MX, false, true>::BN / 2;
+  q.n_tiles = (p.N + cols - 1) / cols;
+  return L.template run<MX, B_KN, EPI, false, Cfg<MX, TALL>::BM == 320 ? SEL_SKINNY_320 : SEL_SKINNY_256>(q);
 }
 
 // The kernel instances of a call that mi355_gg_pp_applies accepted: L.template run<MX, B_KN, EPI,
-// TALL, SEL>(p), one launch, or two for MX with the skinny tile (the other groups on the 256 x 256
-// tile, then the skinny range on 384 x 128, whose n-tiles are half as wide). The library launches
-// them; the host-side checker replays them.
+// TALL, SEL>(p), one launch, or two with the skinny tile. The library launches them; the host-side
+// checker replays them.
 template <bool MX, bool B_KN, int EPI, class Launch>
 int pp_select_tall(const GGParams& p, Launch& L) {
   if constexpr (!MX) {
-    if (pp_tall(p, MX)) return L.template run<MX, B_KN, EPI, true, SEL_ALL>(p);
-  } else {
-    if (pp_skinny(p)) {
-      const int rc = L.template run<MX, B_KN, EPI, false, SEL_NOT_SKINNY>(p);
-      if (rc) return rc;
-      GGParams q = p;
-      constexpr int cols = EPI == EPI_STORE_BF16 ? Cfg<true, true>::BN : Cfg<true, true>::BN / 2;
-      q.n_tiles = (p.N + cols - 1) / cols;
-      return L.template run<MX, B_KN, EPI, true, SEL_SKINNY>(q);
+    const bool tall = pp_tall(p, MX);
+    if constexpr (!B_KN) {
+      if (pp_skinny(p))
+        return tall ? pp_run_skinny<MX, B_KN, EPI, true>(p, L) : pp_run_skinny<MX, B_KN, EPI, false>(p, L);
     }
+    if (tall) return L.template run<MX, B_KN, EPI, true, SEL_ALL>(p);
+  } else {
+    if (pp_skinny(p)) return pp_run_skinny<MX, B_KN, EPI, false>(p, L);
   }
   return L.template run<MX, B_KN, EPI, false, SEL_ALL>(p);
 }

@@ -5,7 +5,8 @@ on, linked with host versions of the GEMM launches that replay each kernel's cop
 runs its scenarios: the grouped GEMM C-ABI (bf16 / MXFP8, EIO / EOI weights, decode-shaped groups,
 more groups than the LDS tile prefix holds), the MegaMoE forward (both precisions and layouts, the
 numerics options) and the expert backward, on the 4-wave and decode kernels and (pp_* scenarios) on
-the default 8-wave kernel of gemm_pp.hip (*_skinny: with its 384 x 128 MX tile switched on). For every copy of every work item, wave and lane the
+the default 8-wave kernel of gemm_pp.hip (*_skinny: with its 384 x 128 tile switched on, MX and bf16; every call's launches must take each
+group once). For every copy of every work item, wave and lane the
 checker verifies the global source (inside a live allocation; for the 4-wave kernels also equal to
 the element the fragment reads expect), the LDS destination slot and the slot coverage, and for the
 4-wave kernels the vmcnt waits and the ring-slot reuse; the emu_* scenarios also run the kernels'
@@ -56,15 +57,17 @@ SCENARIOS = [
     "pp_bf16_kn_store", "pp_mx_swiglu_gu", "emu_pp_bf16_kn_store", "emu_pp_bf16_nk_store",
     "emu_pp_bf16_kn_store_256", "emu_pp_bf16_kn_swiglu", "emu_pp_bf16_kn_swiglu_gu", "emu_pp_bf16_nk_swiglu",
     "emu_pp_mx_store", "emu_pp_mx_swiglu", "emu_pp_mx_swiglu_gu", "emu_pp_mx_skinny_store",
-    "emu_pp_mx_skinny_swiglu", "emu_pp_mx_skinny_swiglu_gu", "pp_moe_mx_eio_skinny", "pp_moe_mx_gu_skinny",
-    "gate_skinny_off", "gate_decode_prep_off", "pp_moe_mx_gu_skinny_none", "pp_moe_mx_gu_skinny_skewed",
-    "emu_moe_bf16_numerics_clamp", "emu_moe_bf16_numerics_after_silu", "emu_moe_bf16_probs_before_fc2",
-    "mut_epi_exp", "mut_epi_rounding", "mut_epi_scale", "mut_pp_copy_offset", "mut_pp_copy_oob",
-    "mut_pp_copy_skipped", "mut_pp_staging", "mut_pp_shuffle", "mut_pp_rounding", "gemm_bf16_many_groups",
-    "gemm_bf16_noalloc", "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi",
-    "moe_mx_eoi_prefill", "moe_mx_eio_prefill", "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp",
-    "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16",
-    "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill"
+    "emu_pp_mx_skinny_swiglu", "emu_pp_mx_skinny_swiglu_gu", "emu_pp_bf16_nk_skinny_store_320",
+    "emu_pp_bf16_nk_skinny_swiglu_320", "emu_pp_bf16_nk_skinny_store_256", "emu_pp_bf16_nk_skinny_swiglu_256",
+    "pp_moe_bf16_eoi_skinny", "pp_moe_mx_eio_skinny", "pp_moe_mx_gu_skinny", "gate_skinny_off",
+    "gate_decode_prep_off", "pp_moe_mx_gu_skinny_none", "pp_moe_mx_gu_skinny_skewed", "emu_moe_bf16_numerics_clamp",
+    "emu_moe_bf16_numerics_after_silu", "emu_moe_bf16_probs_before_fc2", "mut_epi_exp", "mut_epi_rounding",
+    "mut_epi_scale", "mut_pp_copy_offset", "mut_pp_copy_oob", "mut_pp_copy_skipped", "mut_pp_staging",
+    "mut_pp_shuffle", "mut_pp_rounding", "gemm_bf16_many_groups", "gemm_bf16_noalloc", "moe_bf16_eio",
+    "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
+    "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu",
+    "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32",
+    "bwd_mx_bf16_prefill"
 ]
 
 

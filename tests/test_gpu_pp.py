@@ -186,3 +186,29 @@ def test_moe_forward_mxfp8_skinny_tile_bit_identical(gpu, monkeypatch, T, H, I, 
     ref = orc.expert_forward_reference(x, ids, probs, d1.cpu().view(torch.uint8), d2.cpu().view(torch.uint8),
                                        precision="mxfp8", w1_scale=s1.cpu(), w2_scale=s2.cpu())
     assert orc.rel_l2(out_skinny, ref) < 3e-2
+
+
+@pytest.mark.parametrize("T,H,I,E,K", [(704, 1024, 384, 4, 2), (640, 1024, 384, 4, 2), (960, 512, 256, 12, 4)])
+def test_moe_forward_bf16_skinny_tile_bit_identical(gpu, monkeypatch, T, H, I, E, K):
+    """bf16 with K-contiguous (EOI) weights: the 384 x 128 tile for the experts above the other
+    launch's tile height (320 when the rows average at most 320 per expert, else 256) and up to 384
+    rows gives the same forward bit for bit as without it, and matches the oracle."""
+    from hyper_multicore_amd import ops
+    print(f"[pp] skinny bf16 T={T} H={H} I={I} E={E} K={K}", flush=True)
+    g = _seed(T + E + 23)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    probs = torch.rand(T, K, generator=g)
+    probs = probs / probs.sum(1, keepdim=True)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16)
+    ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), w1.transpose(1, 2).contiguous().to(gpu),
+           w2.transpose(1, 2).contiguous().to(gpu))
+    args = dict(num_experts=E, intermediate_size=I, layout="EOI")
+    monkeypatch.delenv("MI355MOE_PP_SKINNY", raising=False)
+    out = ops.moe_forward(*ins, **args).cpu()
+    monkeypatch.setenv("MI355MOE_PP_SKINNY", "1")
+    out_skinny = ops.moe_forward(*ins, **args).cpu()
+    assert torch.equal(out_skinny, out)
+    ref = orc.expert_forward_reference(x, ids, probs, w1, w2)
+    assert orc.rel_l2(out_skinny, ref) < BF16_REL_L2

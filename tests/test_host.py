@@ -393,7 +393,7 @@ def test_bench_profile_summary_two_gmm1_launches(tmp_path):
     _write_csv(out / "copy" / "fetch" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "FETCH_SIZE", copy_kib]])
     _write_csv(out / "copy" / "write" / "pmc_counter_collection.csv", cnt, [["__amd_rocclr_copyBuffer", "WRITE_SIZE", copy_kib]])
     a = "void (anonymous namespace)::gg_pp_kernel<true, true, 5, false, 1>(GGParams)"
-    b = "void (anonymous namespace)::gg_pp_kernel<true, true, 5, true, 2>(GGParams)"
+    b = "void (anonymous namespace)::gg_pp_kernel<true, true, 5, false, 2>(GGParams)"
     g2 = "void (anonymous namespace)::gg_pp_kernel<true, true, 0, false, 1>(GGParams)"
     d = out / "dsv3_mxfp8"
     _write_csv(d / "fetch" / "pmc_counter_collection.csv", cnt, [[a, "FETCH_SIZE", 3000.0], [b, "FETCH_SIZE", 1000.0],
@@ -432,3 +432,16 @@ def test_bench_m_tiles_weight_passes(monkeypatch):
     r = bench.m_tiles(c, counts)
     assert r["tiles"] == 2 and r["skinny_tiles"] == 2 and r["weight_passes_per_expert"] == 1.0
     assert r["padded_row_frac"] == round(1 - 1024 / (2 * 256 + 2 * 384), 4)
+
+
+def test_bench_m_tiles_bf16_skinny(monkeypatch):
+    """bf16 EOI: 320-row tiles when the groups average at most 320 rows; with the 384 x 128 tile the
+    groups of 321..384 rows take one pass (EIO weights keep two)."""
+    import bench
+    c = dict(bench.CONFIGS["dsv3_bf16"], T=256, K=4, E=4)  # 256 rows per expert on average
+    counts = torch.tensor([100, 330, 384, 210])
+    monkeypatch.setenv("MI355MOE_PP_SKINNY", "1")
+    r = bench.m_tiles(c, counts, layout="EOI")
+    assert r["bm"] == 320 and r["tiles"] == 2 and r["skinny_tiles"] == 2 and r["weight_passes_per_expert"] == 1.0
+    r = bench.m_tiles(c, counts, layout="EIO")
+    assert "skinny_tiles" not in r and r["tiles"] == 1 + 2 + 2 + 1

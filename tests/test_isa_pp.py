@@ -66,12 +66,13 @@ def asm(tmp_path_factory):
 def test_pp_kernels_register_budget(asm):
     bodies, meta = _kernels(asm)
     assert len(bodies) >= 14 and set(bodies) == set(meta)
-    assert any(re.search(r"ILb1ELb1ELi\d+ELb1ELi2E", n) for n in bodies)  # the 384 x 128 MX tile
+    assert any(re.search(r"ILb1ELb1ELi\d+ELb0ELi2E", n) for n in bodies)  # the 384 x 128 MX tile
+    assert any(re.search(r"ILb0ELb0ELi\d+ELb0ELi[23]E", n) for n in bodies)  # the 384 x 128 bf16 tile
     for name, lines in bodies.items():
         # gg_pp_kernel<MX, B_KN, EPI, TALL, SEL>
         args = re.search(r"gg_pp_kernelILb(\d)ELb(\d)ELi(\d+)ELb(\d)ELi(\d)EEEv8GGParams", name)
         assert args, name
-        mx, tall = args.group(1) == "1", args.group(4) == "1"  # MX TALL: the 384 x 128 tile
+        mx, tall = args.group(1) == "1", args.group(4) == "1"  # SEL 2 / 3: the 384 x 128 tile
         m = meta[name]
         assert m["vgpr"] <= 256, (name, m)
         if mx or not tall:
