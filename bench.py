@@ -167,8 +167,7 @@ def gmm_work(c: dict, counts: torch.Tensor) -> dict:
                 layer_bytes=layer_bytes)
 
 
-def m_tiles(c: dict, counts: torch.Tensor, variant: str = "default", decode_tiles: bool = True,
-            layout: str = "EIO") -> dict:
+def m_tiles(c: dict, counts: torch.Tensor, variant: str = "default", decode_tiles: bool = True) -> dict:
     """Row tiles the expert GEMMs run (per column block) against the ideal R / BM, and the fraction
     of tile rows that are padding: the M-tail waste of ragged groups. BM is the library's choice: 64
     on the decode tiles (routed rows <= 32 per expert under the default variant), 320 for bf16 when
@@ -181,9 +180,9 @@ def m_tiles(c: dict, counts: torch.Tensor, variant: str = "default", decode_tile
     else:
         bm = 256
     active = max(1, int((counts > 0).sum()))
-    # the 384 x 128 tile (MI355MOE_PP_SKINNY=1; MX, and bf16 with K-contiguous weights): the groups above
-    # the other tile's height and up to 384 rows in one m-tile of 384 rows
-    skinny = (bm in (256, 320) and variant in ("default", "pp") and (c["precision"] == "mxfp8" or layout == "EOI")
+    # the 384 x 128 tile (MI355MOE_PP_SKINNY=1): the groups above the other tile's height and up to 384
+    # rows in one m-tile of 384 rows
+    skinny = (bm in (256, 320) and variant in ("default", "pp")
               and os.environ.get("MI355MOE_PP_SKINNY") == "1" and c["E"] * 128 <= R <= c["E"] * 512)
     in_range = ((counts > bm) & (counts <= 384)) if skinny else torch.zeros_like(counts, dtype=torch.bool)
     tiles = int(((counts[~in_range] + bm - 1) // bm).sum())
@@ -404,8 +403,7 @@ def run_config(name: str, device, steps: int, warmup: int, variant: str = "defau
         "layer_mfma_frac": round(work["layer_flops"] / (ms * 1e-3) / PEAK[c["precision"]], 4),
         "layer_hbm_frac": round(work["layer_bytes"] / (ms * 1e-3) / PEAK["hbm"], 4),
         "active_experts": work["active"],
-        "m_tiles": m_tiles(c, counts, variant, bool(layer.ops.features() & layer._lib.FEATURE_DECODE_TILES),
-                           layer.layout),
+        "m_tiles": m_tiles(c, counts, variant, bool(layer.ops.features() & layer._lib.FEATURE_DECODE_TILES)),
         "weight_layout": layer.layout,
         "stage_ms": {k: round(v, 4) for k, v in m["stage_ms"].items()},
         "roofline": roofline(c, work, m["stage_ms"]["gmm1"], *measured_traffic(name, variant, layer.layout)),

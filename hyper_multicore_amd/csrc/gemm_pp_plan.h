@@ -34,8 +34,9 @@
 //   K-contiguous rows (activations; EOI weights): row r at r * 128, chunk c at c ^ ((r >> 1) & 7),
 //     read with ds_read_b128;
 //   N-contiguous weights (EIO bf16, MX col_data): K row k of the stage holds the tile's columns; bf16
-//     chunk c at c ^ ((k & 7) << 1) (512-byte rows), e4m3 chunk c at c ^ (k & 15) (256-byte rows; the
-//     128-column tile: c ^ (k & 7), 128-byte rows), read with ds_read_b64_tr_b16 / ds_read_b64_tr_b8;
+//     chunk c at c ^ ((k & 7) << 1) (512-byte rows; 256 on the 128-column tile), e4m3 chunk c at
+//     c ^ (k & 15) (256-byte rows; the 128-column tile: c ^ (k & 7), 128-byte rows), read with
+//     ds_read_b64_tr_b16 / ds_read_b64_tr_b8;
 //   MX scales of a stage: code j (0..3) of tile row r at j * 512 + row0 % 4 + r (from the
 //     stage-major code planes of the activation scales: two 256-byte runs per code from the 4-aligned
 //     address at or below the tile's first row); weight tile column j's two codes of 64-K step s at
@@ -304,9 +305,11 @@ MI355_HD uint32_t b_off(const GGParams& p, int nt, int i, int lane) {
     if (wc > p.Ntot - 16) wc = p.Ntot - 16;
     return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc;
   } else {
-    const int L16 = i * 64 + lane;  // K rows of 512 bytes: copy i covers K rows 2 i, 2 i + 1
-    const int k = L16 >> 5;
-    const int c = (L16 & 31) ^ ((k & 7) << 1);
+    // K rows of 2 BN bytes (512: copy i covers K rows 2 i, 2 i + 1; 256 on the 128-column tile)
+    constexpr int LG = C::SKINNY ? 4 : 5, M = (1 << LG) - 1;
+    const int L16 = i * 64 + lane;
+    const int k = L16 >> LG;
+    const int c = (L16 & M) ^ ((k & 7) << 1);
     int wc = tile_col<C::BN>(c * 8, nt, p.N, SWIGLU, p.gate_up_interleaved);
     if (wc > p.Ntot - 8) wc = p.Ntot - 8;
     return (uint32_t)k * (uint32_t)p.b_row_bytes + (uint32_t)wc * 2u;
@@ -388,8 +391,8 @@ MI355_HD void read_frags(Frags<C::MX, B_KN, C::MI>& f, const uint8_t* slot, int 
           const int g16 = lane >> 4, m = lane & 15;
           const int nb = wq * WN + ni * 32 + (g16 & 1) * 16 + 4 * (m & 3);
           const int k0 = ks * 16 + (g16 >> 1) * 8 + (m >> 2), k1 = k0 + 4;
-          const int off0 = k0 * 512 + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
-          const int off1 = k1 * 512 + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
+          const int off0 = k0 * (2 * C::BN) + (((nb >> 3) ^ ((k0 & 7) << 1)) << 4) + (nb & 7) * 2;
+          const int off1 = k1 * (2 * C::BN) + (((nb >> 3) ^ ((k1 & 7) << 1)) << 4) + (nb & 7) * 2;
           f.bl[s2][ni] = O::tr16(Bs + off0);
           f.bh[s2][ni] = O::tr16(Bs + off1);
         }
@@ -579,8 +582,7 @@ inline bool pp_tall(const GGParams& p, bool mx) {
 }
 
 // The skinny tile for the groups above the other tile's height and up to 384 rows, when switched on
-// and the rows average 128..512 per group (else few groups fall in the range); MX, and bf16 with
-// K-contiguous (EOI) weights
+// and the rows average 128..512 per group (else few groups fall in the range)
 inline bool pp_skinny(const GGParams& p) {
   return mi355_pp_skinny_enabled() && p.G <= Cfg<true, false, true>::PREFIX_MAX &&
          p.rows_hint >= (int64_t)p.G * 128 && p.rows_hint <= (int64_t)p.G * 512;
@@ -605,10 +607,8 @@ template <bool MX, bool B_KN, int EPI, class Launch>
 int pp_select_tall(const GGParams& p, Launch& L) {
   if constexpr (!MX) {
     const bool tall = pp_tall(p, MX);
-    if constexpr (!B_KN) {
-      if (pp_skinny(p))
-        return tall ? pp_run_skinny<MX, B_KN, EPI, true>(p, L) : pp_run_skinny<MX, B_KN, EPI, false>(p, L);
-    }
+    if (pp_skinny(p))
+      return tall ? pp_run_skinny<MX, B_KN, EPI, true>(p, L) : pp_run_skinny<MX, B_KN, EPI, false>(p, L);
     if (tall) return L.template run<MX, B_KN, EPI, true, SEL_ALL>(p);
   } else {
     if (pp_skinny(p)) return pp_run_skinny<MX, B_KN, EPI, false>(p, L);

@@ -2147,6 +2147,14 @@ static std::vector<Scenario> scenarios() {
                emu(skinny([=] { pp_gemm({300, 500, 384, 257, 600, 350}, 256, 512, false, false, false, 0); }))});
   s.push_back({"emu_pp_bf16_nk_skinny_swiglu_256",
                emu(skinny([=] { pp_gemm({300, 500, 384, 257, 600, 350}, 256, 256, false, false, true, 0); }))});
+  s.push_back({"emu_pp_bf16_kn_skinny_store_320",
+               emu(skinny([=] { pp_gemm({330, 70, 384, 321, 385, 0, 200, 300}, 256, 512, false, true, false, 0); }))});
+  s.push_back({"emu_pp_bf16_kn_skinny_swiglu_256",
+               emu(skinny([=] { pp_gemm({300, 500, 384, 257, 600, 350}, 256, 256, false, true, true, 0); }))});
+  s.push_back({"emu_pp_bf16_kn_skinny_swiglu_gu_320",
+               emu(skinny([=] { pp_gemm({330, 70, 384, 321, 385, 0, 200, 300}, 256, 256, false, true, true, 1); }))});
+  s.push_back({"pp_moe_bf16_gu_skinny", pp_route(skinny([=] { moe_forward(704, 2, 4, 256, 384, BF, L_GU, 0.0); }))});
+  s.push_back({"pp_moe_bf16_eio_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, BF, L_EIO, 0.0); }))});
   s.push_back({"pp_moe_bf16_eoi_skinny", pp_route(skinny([=] { moe_forward(704, 2, 4, 256, 384, BF, L_EOI, 0.0); }))});
   s.push_back({"pp_moe_mx_eio_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_EIO, 0.0); }))});
   s.push_back({"pp_moe_mx_gu_skinny", pp_route(skinny([=] { moe_forward(640, 2, 4, 256, 384, MX, L_GU, 0.0); }))});

@@ -59,15 +59,16 @@ SCENARIOS = [
     "emu_pp_mx_store", "emu_pp_mx_swiglu", "emu_pp_mx_swiglu_gu", "emu_pp_mx_skinny_store",
     "emu_pp_mx_skinny_swiglu", "emu_pp_mx_skinny_swiglu_gu", "emu_pp_bf16_nk_skinny_store_320",
     "emu_pp_bf16_nk_skinny_swiglu_320", "emu_pp_bf16_nk_skinny_store_256", "emu_pp_bf16_nk_skinny_swiglu_256",
-    "pp_moe_bf16_eoi_skinny", "pp_moe_mx_eio_skinny", "pp_moe_mx_gu_skinny", "gate_skinny_off",
-    "gate_decode_prep_off", "pp_moe_mx_gu_skinny_none", "pp_moe_mx_gu_skinny_skewed", "emu_moe_bf16_numerics_clamp",
-    "emu_moe_bf16_numerics_after_silu", "emu_moe_bf16_probs_before_fc2", "mut_epi_exp", "mut_epi_rounding",
-    "mut_epi_scale", "mut_pp_copy_offset", "mut_pp_copy_oob", "mut_pp_copy_skipped", "mut_pp_staging",
-    "mut_pp_shuffle", "mut_pp_rounding", "gemm_bf16_many_groups", "gemm_bf16_noalloc", "moe_bf16_eio",
-    "moe_bf16_eoi", "moe_bf16_eio_prefill", "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill", "moe_mx_eio_prefill",
-    "moe_mx_gu_prefill", "moe_bf16_gu", "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu",
-    "moe_bf16_probs_before_fc2", "bwd_eio_f32", "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32",
-    "bwd_mx_bf16_prefill"
+    "emu_pp_bf16_kn_skinny_store_320", "emu_pp_bf16_kn_skinny_swiglu_256", "emu_pp_bf16_kn_skinny_swiglu_gu_320",
+    "pp_moe_bf16_gu_skinny", "pp_moe_bf16_eio_skinny", "pp_moe_bf16_eoi_skinny", "pp_moe_mx_eio_skinny",
+    "pp_moe_mx_gu_skinny", "gate_skinny_off", "gate_decode_prep_off", "pp_moe_mx_gu_skinny_none",
+    "pp_moe_mx_gu_skinny_skewed", "emu_moe_bf16_numerics_clamp", "emu_moe_bf16_numerics_after_silu",
+    "emu_moe_bf16_probs_before_fc2", "mut_epi_exp", "mut_epi_rounding", "mut_epi_scale", "mut_pp_copy_offset",
+    "mut_pp_copy_oob", "mut_pp_copy_skipped", "mut_pp_staging", "mut_pp_shuffle", "mut_pp_rounding",
+    "gemm_bf16_many_groups", "gemm_bf16_noalloc", "moe_bf16_eio", "moe_bf16_eoi", "moe_bf16_eio_prefill",
+    "moe_mx_eio", "moe_mx_eoi", "moe_mx_eoi_prefill", "moe_mx_eio_prefill", "moe_mx_gu_prefill", "moe_bf16_gu",
+    "moe_bf16_numerics_clamp", "moe_bf16_numerics_after_silu", "moe_bf16_probs_before_fc2", "bwd_eio_f32",
+    "bwd_eoi_bf16", "bwd_eio_bf16_prefill", "bwd_mx_f32", "bwd_mx_bf16_prefill"
 ]
 
 

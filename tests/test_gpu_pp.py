@@ -188,13 +188,14 @@ def test_moe_forward_mxfp8_skinny_tile_bit_identical(gpu, monkeypatch, T, H, I, 
     assert orc.rel_l2(out_skinny, ref) < 3e-2
 
 
+@pytest.mark.parametrize("layout", ["EOI", "EIO", "EIO_GU"])
 @pytest.mark.parametrize("T,H,I,E,K", [(704, 1024, 384, 4, 2), (640, 1024, 384, 4, 2), (960, 512, 256, 12, 4)])
-def test_moe_forward_bf16_skinny_tile_bit_identical(gpu, monkeypatch, T, H, I, E, K):
-    """bf16 with K-contiguous (EOI) weights: the 384 x 128 tile for the experts above the other
-    launch's tile height (320 when the rows average at most 320 per expert, else 256) and up to 384
-    rows gives the same forward bit for bit as without it, and matches the oracle."""
+def test_moe_forward_bf16_skinny_tile_bit_identical(gpu, monkeypatch, T, H, I, E, K, layout):
+    """bf16: the 384 x 128 tile for the experts above the other launch's tile height (320 when the
+    rows average at most 320 per expert, else 256) and up to 384 rows gives the same forward bit for
+    bit as without it, and matches the oracle."""
     from hyper_multicore_amd import ops
-    print(f"[pp] skinny bf16 T={T} H={H} I={I} E={E} K={K}", flush=True)
+    print(f"[pp] skinny bf16 {layout} T={T} H={H} I={I} E={E} K={K}", flush=True)
     g = _seed(T + E + 23)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16)
     ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
@@ -202,9 +203,14 @@ def test_moe_forward_bf16_skinny_tile_bit_identical(gpu, monkeypatch, T, H, I, E
     probs = probs / probs.sum(1, keepdim=True)
     w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
     w2 = (torch.randn(E, I, H, generator=g) * 0.02).to(torch.bfloat16)
-    ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), w1.transpose(1, 2).contiguous().to(gpu),
-           w2.transpose(1, 2).contiguous().to(gpu))
-    args = dict(num_experts=E, intermediate_size=I, layout="EOI")
+    if layout == "EOI":
+        wa, wb = w1.transpose(1, 2).contiguous().to(gpu), w2.transpose(1, 2).contiguous().to(gpu)
+    else:
+        wa, wb = w1.to(gpu), w2.to(gpu)
+        if layout == "EIO_GU":
+            wa, _ = ops.interleave_gate_up(wa)
+    ins = (x.to(gpu), ids.to(gpu), probs.to(gpu), wa, wb)
+    args = dict(num_experts=E, intermediate_size=I, layout=layout)
     monkeypatch.delenv("MI355MOE_PP_SKINNY", raising=False)
     out = ops.moe_forward(*ins, **args).cpu()
     monkeypatch.setenv("MI355MOE_PP_SKINNY", "1")

@@ -435,13 +435,14 @@ def test_bench_m_tiles_weight_passes(monkeypatch):
 
 
 def test_bench_m_tiles_bf16_skinny(monkeypatch):
-    """bf16 EOI: 320-row tiles when the groups average at most 320 rows; with the 384 x 128 tile the
-    groups of 321..384 rows take one pass (EIO weights keep two)."""
+    """bf16: 320-row tiles when the groups average at most 320 rows; with the 384 x 128 tile the
+    groups of 321..384 rows take one pass."""
     import bench
     c = dict(bench.CONFIGS["dsv3_bf16"], T=256, K=4, E=4)  # 256 rows per expert on average
     counts = torch.tensor([100, 330, 384, 210])
     monkeypatch.setenv("MI355MOE_PP_SKINNY", "1")
-    r = bench.m_tiles(c, counts, layout="EOI")
+    r = bench.m_tiles(c, counts)
     assert r["bm"] == 320 and r["tiles"] == 2 and r["skinny_tiles"] == 2 and r["weight_passes_per_expert"] == 1.0
-    r = bench.m_tiles(c, counts, layout="EIO")
+    monkeypatch.delenv("MI355MOE_PP_SKINNY")
+    r = bench.m_tiles(c, counts)
     assert "skinny_tiles" not in r and r["tiles"] == 1 + 2 + 2 + 1
